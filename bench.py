@@ -1,0 +1,170 @@
+#!/usr/bin/env python3
+"""PPO minibatch step throughput on one MI355X.
+
+One step = one PPO minibatch update of the token-transformer policy:
+forward -> PPO clipped loss fwd+bwd -> backward -> global-norm clip + Adam,
+on B = 512 rows drawn (epoch permutations) from a 16 384-row synthetic
+rollout resident in HBM.  Model: 96 entity tokens (+READOUT), 32 numeric
+token features, card ids in [0, 2048), d 256 / 4 heads / FFN 1024 / 4 pre-LN
+layers, 64 masked options, blind value head, fp32 throughout.
+
+Prints one JSON line (see the keys below), including the GEMM kernel's
+roofline (useful flops over measured kernel time, HIP events on the launch
+stream) and the host-CPU baseline (the oracle: PyTorch CPU restatement of
+the same step, timed on a bounded sample in the same run).
+"""
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "PPO minibatch step obs/sec (fwd+bwd+Adam) @B=512; % MFMA/HBM roofline"
+FP32_MFMA_PEAK_TFLOPS = 157.3      # MI355X dense fp32 matrix peak
+
+TRAIN = dict(learning_rate=3e-4, beta1=0.9, beta2=0.999, eps=1e-8, max_grad_norm=0.5,
+             clip_coef=0.2, vf_clip_coef=0.2, vf_coef=0.5, ent_coef=0.01)
+
+
+def useful_gemm_flops(dm, obs_rows):
+    """Useful (valid-token) GEMM flops of one fwd+bwd over `obs_rows`:
+    token rows count only valid tokens (+READOUT in the trunk); every
+    GEMM's backward is 2x its forward (dX and dW), so fwd+bwd = 3x fwd."""
+    from ptcg_amd.params import OPT_E, SC_H, VAL_H, DEC_H
+    off = dm.offsets()
+    zone = obs_rows[:, off["tok_int"][0]:off["tok_int"][1]].reshape(len(obs_rows), dm.l_tok, dm.tok_int)[:, :, 1]
+    n_valid = (zone > 0).sum(1).astype(np.float64)
+    Lv = n_valid + 1
+    d, ffn, NO, B = dm.d, dm.ffn, dm.n_opt, len(obs_rows)
+    tok_in = 2 * dm.d_c + dm.tok_f + 12
+    fwd = 2.0 * n_valid.sum() * tok_in * d
+    fwd += dm.layers * (Lv.sum() * (8 * d * d + 4 * d * ffn))
+    fwd += 2.0 * B * NO * (dm.d_c * OPT_E + dm.d_a * OPT_E + dm.q_in * d + d * d + dm.score_in * SC_H)
+    fwd += 2.0 * B * (dm.global_f * dm.g + dm.g * dm.g + dm.dec_in * DEC_H + DEC_H * DEC_H
+                      + dm.bcast_in * d + dm.val_in * VAL_H)
+    return 3.0 * fwd, float(Lv.mean())
+
+
+def cpu_baseline(dm, obs, inp, B, budget_s):
+    """Oracle (torch CPU) fwd+bwd+PPO+clip+Adam on B-row minibatches of the
+    same rollout until `budget_s` of CPU work; returns obs/s and the sample."""
+    import torch
+    import oracle.model as om
+    import oracle.adam as oa
+    import oracle.step as ost
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    torch.set_num_threads(threads)
+    ref = om.build(dm, seed=0)
+    opt = oa.OracleAdam([p for _, p in ref.named_blob_params()], lr=TRAIN["learning_rate"])
+    hyp = dict(TRAIN)
+    rng = np.random.default_rng(0)
+    times = []
+    t_start = time.perf_counter()
+    while True:
+        idx = rng.choice(len(obs), B, replace=False)
+        t0 = time.perf_counter()
+        ost.minibatch_step(ref, opt, obs[idx], {k: v[idx] for k, v in inp.items()}, hyp)
+        times.append(time.perf_counter() - t0)
+        if time.perf_counter() - t_start > budget_s or len(times) >= 10:
+            break
+    timed = times[1:] if len(times) > 1 else times
+    med = float(np.median(timed))
+    return dict(value=B / med, unit="obs/s", cores=threads, kind="port",
+                sample=f"{len(timed)} timed (+1 warmup) oracle minibatch steps of {B} rows "
+                       f"(fwd+bwd+PPO+clip+Adam, torch CPU fp32), median {med:.2f} s/step")
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--minibatch", type=int, default=512)
+    ap.add_argument("--rollout", type=int, default=16384)
+    ap.add_argument("--cpu-seconds", type=float, default=20.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
+              "(the data-parallel path is designed but not built)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import __graft_entry__
+    __graft_entry__.load_package()
+    from ptcg_amd import dims, synth, trainer, native
+
+    dm = dims.CORE
+    B, R = args.minibatch, args.rollout
+    obs = synth.make_obs(dm, R, seed=1)
+    inp = synth.make_ppo_inputs(dm, obs, seed=2)
+    pl = trainer.create_pufferl({"dims": dm, "train": dict(TRAIN, minibatch_size=B), "seed": 0})
+    trainer.set_rollout(pl, obs, **inp)
+    n_lists = args.warmup + args.steps
+    lists = synth.minibatch_indices(R, B, n_lists, seed=3)
+    d_lists = [pl.to_device(ix, np.int32) for ix in lists]
+    r = pl.rollout
+
+    for i in range(args.warmup):
+        pl.step(r["obs"], d_lists[i], r)
+    torch.cuda.synchronize()
+    L = native.lib()
+    native.check(L.ptcg_profile_begin(4096))
+    t0 = time.perf_counter()
+    for i in range(args.warmup, n_lists):
+        pl.step(r["obs"], d_lists[i], r)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    ms, launches, exec_flops = ctypes.c_double(), ctypes.c_int(), ctypes.c_double()
+    native.check(L.ptcg_profile_end(ctypes.byref(ms), ctypes.byref(launches), ctypes.byref(exec_flops)))
+    losses = trainer.log(pl)
+    if not np.isfinite(losses["total_loss"]):
+        raise RuntimeError(f"non-finite loss during the benchmark: {losses}")
+
+    K = args.steps
+    sec = t1 - t0
+    useful = 0.0
+    lv = []
+    for ix in lists[args.warmup:]:
+        f, l = useful_gemm_flops(dm, obs[ix])
+        useful += f
+        lv.append(l)
+    gemm_s = ms.value / 1e3
+    achieved = useful / gemm_s / 1e12
+    roof = dict(bound="mfma", kernel="gemm_f32_kernel (all launches: trunk, token, option and head GEMMs)",
+                achieved=round(achieved, 3), peak=FP32_MFMA_PEAK_TFLOPS, unit="TFLOP/s",
+                frac=round(achieved / FP32_MFMA_PEAK_TFLOPS, 4), traffic=None,
+                launches_per_step=launches.value / K,
+                avg_launch_us=round(ms.value * 1e3 / max(launches.value, 1), 3),
+                gemm_ms_per_step=round(ms.value / K, 4),
+                executed_tflops=round(exec_flops.value / gemm_s / 1e12, 3),
+                useful_tflop_per_step=round(useful / K / 1e12, 4),
+                mean_valid_seq=round(float(np.mean(lv)), 2))
+    line = {
+        "metric": METRIC, "value": round(B * K / sec, 2), "unit": "obs/s", "n_gpus": 1,
+        "steps": K, "warmup": args.warmup, "ms_per_step": round(sec * 1e3 / K, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp32",
+        "data": "synthetic",
+        "config": {"workload": "PPO minibatch step (fwd+bwd+PPO loss+grad-norm clip+Adam) on 512 rows of "
+                               "a 16384-row HBM-resident rollout; 96 tokens + READOUT, 32 token features, "
+                               "card ids [0,2048), d256/H4/FFN1024/4 layers, 64 options, blind value head",
+                   "minibatch": B, "rollout_rows": R, "seq_len": dm.l_tok + 1,
+                   "parallelism": "single GPU"},
+        "roofline": roof,
+        "losses": {k: round(v, 5) for k, v in losses.items() if isinstance(v, float)},
+    }
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline(dm, obs, inp, B, args.cpu_seconds)
+        line["gpu_over_cpu"] = round(line["value"] / line["cpu_baseline"]["value"], 1)
+    pl.close()
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

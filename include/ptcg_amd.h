@@ -1,0 +1,175 @@
+/*
+ * ptcg_amd.h — C ABI of the MI355X-native PTCG token-transformer PPO step.
+ *
+ * Plain C types only: device pointers are float* / int32_t* into HIP device
+ * memory, streams are passed as void* (a hipStream_t; NULL = the null stream).
+ * Every function returns 0 on success and a negative code on failure; the
+ * message is available from ptcg_last_error() (the reference aborts or throws
+ * std::runtime_error with the same conditions, see each citation).
+ *
+ * Reference interfaces replaced (paths relative to the reference repo):
+ *   - Encoder vtable of the PTCG model plugin: native/src/models.cu:16-47,
+ *     native/model/ptcg_model4.cu:236-284, installed by native/src/ocean.cu:5-18.
+ *   - PPO loss: ppo_loss_fwd_bwd, native/src/pufferlib.cu:1368-1449.
+ *   - optimizer slot: muon_step, native/src/muon.cu:209 (here: clip + Adam).
+ *   - trainer entry points: create_pufferl / train / debug_forward /
+ *     save_weights / load_weights / save_state / load_state,
+ *     native/src/bindings.cu:184-367,581-757; train_impl pufferlib.cu:1847.
+ */
+#ifndef PTCG_AMD_H
+#define PTCG_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PTCG_OK 0
+#define PTCG_ERR_ARG (-1)      /* bad argument / shape mismatch            */
+#define PTCG_ERR_HIP (-2)      /* HIP runtime error                         */
+#define PTCG_ERR_IO (-3)       /* file open/read/write failure              */
+#define PTCG_ERR_UNSUPPORTED (-4)
+
+/* Runtime sizes (the reference's compile-time PT_* macros,
+ * ptcg_model.cu:14-87, and the obs layout of ptcg/rl/buffers.py:29-55).
+ * tables: 0 = learned card/attack tables, 1 = static-table chain.
+ * critic: 0 = blind value head, 1 = oracle critic.                         */
+typedef struct PtcgDims {
+    int l_tok, tok_int, tok_f, n_opt, opt_int, opt_f, global_f, dec_int, dec_f, oracle_f;
+    int d, heads, ffn, layers, d_c, d_a, g;
+    int n_cards, n_attacks, n_skills, n_zones, n_owners, n_opt_types, n_select_types, n_contexts;
+    int tables, critic;
+} PtcgDims;
+
+/* Hyper-parameters of one minibatch step (the keys of the reference's
+ * build_args train dict, native/train_native.py:251-280, plus Adam's).     */
+typedef struct PtcgHypers {
+    float lr, beta1, beta2, eps;          /* Adam                              */
+    float max_grad_norm;                  /* global-norm clip (muon.cu:216)    */
+    float clip_coef, vf_clip_coef, vf_coef, ent_coef;   /* PPO              */
+    float kl_skip_threshold, vf_skip_threshold;  /* gate; <= 0 disables     */
+} PtcgHypers;
+
+typedef struct PtcgModel PtcgModel;
+typedef struct PtcgTrainer PtcgTrainer;
+
+const char* ptcg_last_error(void);
+int ptcg_abi_version(void);
+
+/* ---- layout (ptcg/rl/buffers.py:212-230; native_weights.py:45-113;
+ *      kernels.cu:433-466 16 B alignment; pufferlib.cu:2366-2390) -------- */
+int ptcg_obs_size(const PtcgDims* dims);
+int ptcg_num_params(const PtcgDims* dims);
+/* i-th tensor of the canonical blob order: name, rows, cols (0 for 1-D).   */
+int ptcg_param_info(const PtcgDims* dims, int i, const char** name, int64_t* rows, int64_t* cols);
+int64_t ptcg_packed_floats(const PtcgDims* dims);
+int64_t ptcg_arena_floats(const PtcgDims* dims);
+int ptcg_packed_to_arena(const PtcgDims* dims, const float* packed, float* arena);   /* host */
+int ptcg_arena_to_packed(const PtcgDims* dims, const float* arena, float* packed);   /* host */
+
+/* ---- model: the Encoder vtable, per entry point ----------------------- */
+/* create_weights (ptcg_model4.cu:238-241)                                  */
+int ptcg_model_create(const PtcgDims* dims, PtcgModel** out);
+/* reg_params + alloc_create (ptcg_model4.cu:243-250): bind caller-owned
+ * params / grads arenas, each ptcg_arena_floats() floats, 16 B aligned.    */
+int ptcg_model_bind(PtcgModel* m, float* params_arena, float* grads_arena);
+/* reg_train (ptcg_model4.cu:260-263): size activations for exactly n rows. */
+int ptcg_model_reg_train(PtcgModel* m, int n);
+/* forward (ptcg_model4.cu:269-275): obs rows -> *out (n, n_opt+1) =
+ * [raw option scores || value], aliasing an internal buffer.
+ * row_idx: optional int32 device array of n row indices into obs (NULL =
+ * rows 0..n-1), replacing the trainer's minibatch copy (pufferlib.cu:2005). */
+int ptcg_model_forward(PtcgModel* m, const float* obs, const int32_t* row_idx, int n,
+                       float** out, void* stream);
+/* backward (ptcg_model4.cu:277-281): grad (n, n_opt+1) = [d scores || d value];
+ * OVERWRITES the grads arena (ptcg_model4.cu:15-21).                       */
+int ptcg_model_backward(PtcgModel* m, const float* grad, void* stream);
+/* free_weights + free_activations (ptcg_model4.cu:283-284).                */
+void ptcg_model_free(PtcgModel* m);
+
+/* ---- PPO loss fwd+bwd (pufferlib.cu:1368-1449; kernels :949-1363) -------
+ * dec_out (n, A+1) fused [scores || value]; mask (n rows at mask_stride,
+ * 0 = illegal -> logit -1e4); per-row inputs gathered through row_idx when
+ * non-NULL.  Writes grad (n, A+1) = [grad_logits || grad_value], ratio (n),
+ * newvalue (n) (either may be NULL), stats[8] = 7 loss statistics + count
+ * ADDED into (pufferlib.cu:1254-1284), and guard[2] = this minibatch's
+ * (approx_kl, v_loss) when non-NULL.  All pointers are device pointers.    */
+int ptcg_ppo_loss_fwd_bwd(const float* dec_out, int n, int A,
+                          const float* mask, int64_t mask_stride, const int32_t* row_idx,
+                          const float* actions, const float* old_logprobs,
+                          const float* advantages, const float* returns,
+                          const float* values, const float* prio,
+                          float clip_coef, float vf_clip_coef, float vf_coef, float ent_coef,
+                          float* grad, float* ratio, float* newvalue,
+                          float* stats, float* guard, void* stream);
+
+/* ---- gate (pufferlib.cu:1292-1302): gate[0] = 1 apply / 0 skip, from
+ * guard[0..1] = (approx_kl, v_loss); skipped[0] += 1 - gate.              */
+int ptcg_kl_gate(const float* guard, float kl_threshold, float vf_threshold,
+                 float* gate, float* skipped, void* stream);
+
+/* ---- optimizer slot (muon_step, muon.cu:209-297 -> clip + Adam) ---------
+ * One fused pass over the flat arenas (n floats, n % 4 == 0, 16 B aligned):
+ * g' = g * min(max_norm / (||g||_2 + 1e-6), 1); Adam moments m, v; weights
+ * updated with bias correction for step t = *step + 1 (torch.optim.Adam
+ * semantics).  step: device int32 count of applied steps, advanced on the
+ * device.  gate: optional device float; when it reads 0 the call changes
+ * nothing (weights, m, v, step untouched).  norm_out: optional device float
+ * receiving ||g||_2 before clipping.  workspace: device buffer of
+ * ptcg_adam_workspace_floats() floats.  grads are read, not modified.      */
+int64_t ptcg_adam_workspace_floats(void);
+int ptcg_adam_step(float* weights, float* grads, float* m, float* v, int64_t n,
+                   float lr, float beta1, float beta2, float eps, float max_grad_norm,
+                   const float* gate, int32_t* step, float* norm_out, float* workspace,
+                   void* stream);
+
+/* ---- trainer (create_pufferl / train / debug_forward / weights IO) ----- */
+int ptcg_trainer_create(const PtcgDims* dims, const PtcgHypers* hyp, int minibatch,
+                        PtcgTrainer** out);
+void ptcg_trainer_free(PtcgTrainer* t);
+int ptcg_trainer_set_hypers(PtcgTrainer* t, const PtcgHypers* hyp);
+/* packed blob <-> live arena (bindings.cu:202-215,339-367), host buffers   */
+int ptcg_trainer_set_weights(PtcgTrainer* t, const float* packed);
+int ptcg_trainer_get_weights(PtcgTrainer* t, float* packed);
+int ptcg_trainer_get_grads(PtcgTrainer* t, float* packed);
+int ptcg_trainer_get_moments(PtcgTrainer* t, float* m_packed, float* v_packed);
+int ptcg_trainer_load_weights(PtcgTrainer* t, const char* path);
+int ptcg_trainer_save_weights(PtcgTrainer* t, const char* path);
+/* full state: "PTCGADM1" header (step count, n) + weights + m + v, packed.  */
+int ptcg_trainer_save_state(PtcgTrainer* t, const char* path);
+int ptcg_trainer_load_state(PtcgTrainer* t, const char* path);
+/* debug_forward (bindings.cu:221-250): host obs (minibatch rows) -> host
+ * out (minibatch, n_opt+1); synchronous.                                  */
+int ptcg_trainer_debug_forward(PtcgTrainer* t, const float* obs_host, int n, float* out_host);
+/* One PPO minibatch step on device data (the body of train_impl's loop,
+ * pufferlib.cu:2039-2105): forward -> loss fwd+bwd -> backward -> gate ->
+ * clip + Adam.  obs rows and the per-row inputs (actions, old log-probs,
+ * advantages, returns, old values) are read through row_idx (device int32,
+ * minibatch entries; NULL = rows 0..minibatch-1).  The action mask is the
+ * obs row's opt_mask section.                                              */
+int ptcg_trainer_step(PtcgTrainer* t, const float* obs, const int32_t* row_idx,
+                      const float* actions, const float* old_logprobs,
+                      const float* advantages, const float* returns, const float* values,
+                      void* stream);
+/* The same step without the optimizer (grads left in the grads arena).    */
+int ptcg_trainer_forward_backward(PtcgTrainer* t, const float* obs, const int32_t* row_idx,
+                                  const float* actions, const float* old_logprobs,
+                                  const float* advantages, const float* returns,
+                                  const float* values, void* stream);
+/* losses (bindings.cu:15-118 "losses"): out[0..6] = pg, vf, ent, total,
+ * old_approx_kl, approx_kl, clipfrac summed over steps; out[7] = count;
+ * out[8] = skipped steps; out[9] = last grad norm.  Synchronous.           */
+int ptcg_trainer_losses(PtcgTrainer* t, float* out10, int reset);
+/* device pointer of the last forward's (minibatch, n_opt+1) output and of
+ * the PPO grad buffer (for tests).                                         */
+int ptcg_trainer_buffers(PtcgTrainer* t, float** dec_out, float** ppo_grad,
+                         float** ratio, float** newvalue);
+int ptcg_trainer_sync(PtcgTrainer* t);
+/* number of applied optimizer steps (device counter), synchronous          */
+int ptcg_trainer_step_count(PtcgTrainer* t, int32_t* out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* PTCG_AMD_H */

@@ -1,0 +1,63 @@
+/*
+ * ptcg_amd_kernels.h — kernel-level C ABI of libptcg_amd.so.
+ *
+ * The building blocks the model driver is made of, exported one by one so a
+ * caller (or a parity test) can run each on device buffers of its own.  All
+ * pointers are device pointers; stream is a hipStream_t (NULL = null stream);
+ * return 0 on success, negative on failure (message: ptcg_last_error()).
+ * Reference counterparts are cited per entry point.
+ */
+#ifndef PTCG_AMD_KERNELS_H
+#define PTCG_AMD_KERNELS_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* C[M,N] = epi(sum_k A(m,k) B(k,n)); A(m,k) = a_t ? A[k*lda+m] : A[m*lda+k],
+ * B(k,n) = b_t ? B[k*ldb+n] : B[n*ldb+k].  epi: 0 store, 1 +bias[n],
+ * 2 +bias then C2 = gelu(C), 3 +bias +R[m*ldr+n], 4 *= gelu'(R[m*ldr+n]),
+ * 5 C += acc.  workspace (may be NULL) enables split-K for long K.
+ * Replaces pt_gemm / pt_linear / pt_linear_bwd (ptcg_kernels.cuh:42-108).  */
+int ptcg_kernel_gemm(int M, int N, int K, const float* A, int64_t lda, int a_t,
+                     const float* B, int64_t ldb, int b_t, float* C, int64_t ldc, int epi,
+                     const float* bias, const float* R, int64_t ldr, float* C2, int64_t ldc2,
+                     float* workspace, int64_t workspace_floats, void* stream);
+
+/* deterministic column sums out[n] = sum_m X[m*ldx+n] (pt_bias_grad,
+ * ptcg_kernels.cuh:87-96); workspace >= ceil(M/256)*N floats.              */
+int ptcg_kernel_colsum(const float* X, int64_t ldx, int M, int N, float* out,
+                       float* workspace, int64_t workspace_floats, void* stream);
+
+/* LayerNorm, eps 1e-5 (pt_ln_fwd / pt_ln_bwd, ptcg_kernels.cuh:132-218).
+ * bwd: dx = LN'(dy) [+ dres]; dw, db overwritten; workspace >=
+ * ceil(rows/32)*2*D floats.                                                 */
+int ptcg_kernel_layernorm_fwd(const float* x, const float* w, const float* b, float* y,
+                              float* mean, float* rstd, int rows, int D, void* stream);
+int ptcg_kernel_layernorm_bwd(const float* dy, const float* x, const float* w,
+                              const float* mean, const float* rstd, const float* dres,
+                              float* dx, float* dw, float* db, int rows, int D,
+                              float* workspace, int64_t workspace_floats, void* stream);
+
+/* Masked MHSA over (N, L, 3D) qkv rows, keep (N, L) key mask (1 keep / 0
+ * masked), fused per (sample, head) (ptcg_model3.cu:18-30, 63-91).
+ * fwd: ctx (N, L, D), lse (N, H, L).  bwd: dqkv (N, L, 3D) from dctx.     */
+int ptcg_kernel_attention_fwd(const float* qkv, const float* keep, float* ctx, float* lse,
+                              int N, int L, int H, int Dh, void* stream);
+int ptcg_kernel_attention_bwd(const float* qkv, const float* keep, const float* ctx,
+                              const float* lse, const float* dctx, float* dqkv,
+                              int N, int L, int H, int Dh, void* stream);
+
+/* Launch timing of the GEMM kernel: between begin and end, every GEMM launch
+ * (up to max_launches) is bracketed by a HIP event pair on its own stream.
+ * end waits for the events and returns the summed kernel time (ms), the
+ * number of launches and their summed 2*M*N*K.                             */
+int ptcg_profile_begin(int max_launches);
+int ptcg_profile_end(double* total_ms, int* launches, double* flops);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* PTCG_AMD_KERNELS_H */

@@ -1,0 +1,532 @@
+// extern "C" surface: errors, layout, PPO / gate / Adam entry points and the
+// trainer (include/ptcg_amd.h documents each entry point and the reference
+// interface it replaces).
+#include "model.h"
+
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <deque>
+#include <mutex>
+#include <string>
+#include <vector>
+
+// ------------------------------------------------------------ errors
+static thread_local char g_err[1024] = "";
+
+void ptcg_set_error(const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof g_err, fmt, ap);
+    va_end(ap);
+}
+
+extern "C" const char* ptcg_last_error(void) { return g_err; }
+extern "C" int ptcg_abi_version(void) { return 1; }
+
+// ------------------------------------------------------------ layout
+ObsOff pt_obs_offsets(const PtcgDims& d) {
+    // ptcg/rl/buffers.py:212-227: sections back to back in this order
+    ObsOff o;
+    int cur = 0;
+    o.tok_int = cur; cur += d.l_tok * d.tok_int;
+    o.tok_float = cur; cur += d.l_tok * d.tok_f;
+    o.opt_int = cur; cur += d.n_opt * d.opt_int;
+    o.opt_float = cur; cur += d.n_opt * d.opt_f;
+    o.opt_mask = cur; cur += d.n_opt;
+    o.global_f = cur; cur += d.global_f;
+    o.dec_int = cur; cur += d.dec_int;
+    o.dec_float = cur; cur += d.dec_f;
+    o.oracle = cur; cur += d.oracle_f;
+    o.size = cur;
+    return o;
+}
+
+DimsX pt_dims_x(const PtcgDims& d) {
+    DimsX x;
+    x.l_seq = d.l_tok + 1;
+    x.dh = d.d / d.heads;
+    x.tok_in = 2 * d.d_c + d.tok_f + PT_ZONE_E + PT_OWNER_E;
+    x.dec_in = PT_SEL_E + PT_CTX_E + 2 * d.d_c + 2 * d.d_a + 2 * d.d_c + d.dec_f;
+    x.bcast_in = d.g + PT_DEC_H;
+    x.q_in = PT_TYPE_E + 2 * d.d + 2 * PT_OPT_E + d.opt_f;
+    x.score_in = 3 * d.d + d.g + PT_DEC_H;
+    x.val_in = d.d + d.g;
+    return x;
+}
+
+static const char* intern(const std::string& s) {
+    static std::mutex mu;
+    static std::deque<std::string> pool;
+    std::lock_guard<std::mutex> lk(mu);
+    for (auto& p : pool)
+        if (p == s) return p.c_str();
+    pool.push_back(s);
+    return pool.back().c_str();
+}
+
+// Canonical blob order: native/tools/native_weights.py:34-92 (PT_PARAMS,
+// ptcg_model.cu:95-126); learned tables replace the 13 static-chain tensors
+// with card_table / attack_table; the blind critic drops the oracle critic
+// and aux tensors.
+int pt_param_table(const PtcgDims& d, ParamDef* out, int cap) {
+    std::vector<ParamDef> v;
+    auto add = [&](const std::string& n, long r, long c) { v.push_back({intern(n), r, c}); };
+    const DimsX x = pt_dims_x(d);
+    const long D = d.d, DC = d.d_c, DA = d.d_a, G = d.g;
+    if (d.tables == 1) {
+        add("card_id_emb.weight", d.n_cards, 64);
+        add("attack_id_emb.weight", d.n_attacks, 48);
+        add("skill_id_emb.weight", d.n_skills, 48);
+        add("attack_mlp.0.weight", DA, 127); add("attack_mlp.0.bias", DA, 0);
+        add("skill_mlp.0.weight", DC, 112); add("skill_mlp.0.bias", DC, 0);
+        add("card_mlp.0.weight", 634, 0); add("card_mlp.0.bias", 634, 0);
+        add("card_mlp.1.weight", 256, 634); add("card_mlp.1.bias", 256, 0);
+        add("card_mlp.3.weight", DC, 256); add("card_mlp.3.bias", DC, 0);
+    } else if (d.tables == 0) {
+        add("card_table", d.n_cards, DC);
+        add("attack_table", d.n_attacks, DA);
+    } else {
+        ptcg_set_error("param table: unknown tables mode %d", d.tables);
+        return PTCG_ERR_ARG;
+    }
+    add("zone_emb.weight", d.n_zones, PT_ZONE_E);
+    add("owner_emb.weight", d.n_owners, PT_OWNER_E);
+    add("token_proj.weight", D, x.tok_in); add("token_proj.bias", D, 0);
+    add("readout", D, 0);
+    add("global_mlp.0.weight", G, d.global_f); add("global_mlp.0.bias", G, 0);
+    add("global_mlp.2.weight", G, G); add("global_mlp.2.bias", G, 0);
+    add("sel_type_emb.weight", d.n_select_types, PT_SEL_E);
+    add("ctx_emb.weight", d.n_contexts, PT_CTX_E);
+    add("dec_mlp.0.weight", PT_DEC_H, x.dec_in); add("dec_mlp.0.bias", PT_DEC_H, 0);
+    add("dec_mlp.2.weight", PT_DEC_H, PT_DEC_H); add("dec_mlp.2.bias", PT_DEC_H, 0);
+    add("bcast.weight", D, x.bcast_in); add("bcast.bias", D, 0);
+    auto block = [&](const std::string& p) {
+        add(p + ".ln1.weight", D, 0); add(p + ".ln1.bias", D, 0);
+        add(p + ".qkv.weight", 3 * D, D); add(p + ".qkv.bias", 3 * D, 0);
+        add(p + ".proj.weight", D, D); add(p + ".proj.bias", D, 0);
+        add(p + ".ln2.weight", D, 0); add(p + ".ln2.bias", D, 0);
+        add(p + ".ffn.0.weight", d.ffn, D); add(p + ".ffn.0.bias", d.ffn, 0);
+        add(p + ".ffn.2.weight", D, d.ffn); add(p + ".ffn.2.bias", D, 0);
+    };
+    for (int i = 0; i < d.layers; ++i) block("blocks." + std::to_string(i));
+    add("ln_f.weight", D, 0); add("ln_f.bias", D, 0);
+    add("opt_type_emb.weight", d.n_opt_types, PT_TYPE_E);
+    add("opt_card.weight", PT_OPT_E, DC); add("opt_card.bias", PT_OPT_E, 0);
+    add("opt_attack.weight", PT_OPT_E, DA); add("opt_attack.bias", PT_OPT_E, 0);
+    add("q_mlp.0.weight", D, x.q_in); add("q_mlp.0.bias", D, 0);
+    add("q_mlp.2.weight", D, D); add("q_mlp.2.bias", D, 0);
+    add("score_mlp.0.weight", PT_SC_H, x.score_in); add("score_mlp.0.bias", PT_SC_H, 0);
+    add("score_mlp.2.weight", 1, PT_SC_H); add("score_mlp.2.bias", 1, 0);
+    add("value_mlp.0.weight", PT_VAL_H, x.val_in); add("value_mlp.0.bias", PT_VAL_H, 0);
+    add("value_mlp.2.weight", 1, PT_VAL_H); add("value_mlp.2.bias", 1, 0);
+    if (d.critic == 1) {
+        add("oracle_proj.weight", D, DC + 6); add("oracle_proj.bias", D, 0);
+        add("critic_readout", D, 0);
+        block("critic_blocks.0");
+        add("oracle_value_mlp.0.weight", PT_VAL_H, x.val_in); add("oracle_value_mlp.0.bias", PT_VAL_H, 0);
+        add("oracle_value_mlp.2.weight", 1, PT_VAL_H); add("oracle_value_mlp.2.bias", 1, 0);
+        add("aux_hand.weight", d.n_cards, x.val_in); add("aux_hand.bias", d.n_cards, 0);
+        add("aux_prize.weight", 1, D); add("aux_prize.bias", 1, 0);
+    }
+    if ((int)v.size() > cap) {
+        ptcg_set_error("param table: %zu entries exceed capacity %d", v.size(), cap);
+        return PTCG_ERR_ARG;
+    }
+    for (size_t i = 0; i < v.size(); ++i) out[i] = v[i];
+    return (int)v.size();
+}
+
+static int table(const PtcgDims* dims, std::vector<ParamDef>& v) {
+    PT_REQUIRE(dims != nullptr, "null dims");
+    v.resize(256);
+    int n = pt_param_table(*dims, v.data(), 256);
+    if (n < 0) return n;
+    v.resize(n);
+    return PTCG_OK;
+}
+
+static inline long numel(const ParamDef& p) { return p.rows * (p.cols > 0 ? p.cols : 1); }
+
+extern "C" int ptcg_obs_size(const PtcgDims* dims) {
+    PT_REQUIRE(dims != nullptr, "null dims");
+    return pt_obs_offsets(*dims).size;
+}
+
+extern "C" int ptcg_num_params(const PtcgDims* dims) {
+    std::vector<ParamDef> v;
+    PT_TRY(table(dims, v));
+    return (int)v.size();
+}
+
+extern "C" int ptcg_param_info(const PtcgDims* dims, int i, const char** name, int64_t* rows, int64_t* cols) {
+    std::vector<ParamDef> v;
+    PT_TRY(table(dims, v));
+    PT_REQUIRE(i >= 0 && i < (int)v.size(), "param_info: index %d out of range", i);
+    if (name) *name = v[i].name;
+    if (rows) *rows = v[i].rows;
+    if (cols) *cols = v[i].cols;
+    return PTCG_OK;
+}
+
+extern "C" int64_t ptcg_packed_floats(const PtcgDims* dims) {
+    std::vector<ParamDef> v;
+    PT_TRY(table(dims, v));
+    int64_t n = 0;
+    for (auto& p : v) n += numel(p);
+    return n;
+}
+
+// kernels.cu:433-466 — each tensor starts at a 16 B (4-float) boundary
+extern "C" int64_t ptcg_arena_floats(const PtcgDims* dims) {
+    std::vector<ParamDef> v;
+    PT_TRY(table(dims, v));
+    int64_t off = 0;
+    for (auto& p : v) off = ((off + 3) & ~3L) + numel(p);
+    return (off + 3) & ~3L;
+}
+
+// pufferlib.cu:2366-2390
+static int packed_arena(const PtcgDims* dims, const float* src, float* dst, bool to_arena) {
+    std::vector<ParamDef> v;
+    PT_TRY(table(dims, v));
+    PT_REQUIRE(src && dst, "packed/arena: null buffer");
+    if (to_arena) memset(dst, 0, sizeof(float) * ptcg_arena_floats(dims));
+    int64_t off = 0, poff = 0;
+    for (auto& p : v) {
+        off = (off + 3) & ~3L;
+        const long ne = numel(p);
+        if (to_arena) memcpy(dst + off, src + poff, ne * sizeof(float));
+        else memcpy(dst + poff, src + off, ne * sizeof(float));
+        off += ne;
+        poff += ne;
+    }
+    return PTCG_OK;
+}
+extern "C" int ptcg_packed_to_arena(const PtcgDims* dims, const float* packed, float* arena) {
+    return packed_arena(dims, packed, arena, true);
+}
+extern "C" int ptcg_arena_to_packed(const PtcgDims* dims, const float* arena, float* packed) {
+    return packed_arena(dims, arena, packed, false);
+}
+
+// ------------------------------------------------------------ PPO / gate / Adam
+extern "C" int ptcg_ppo_loss_fwd_bwd(const float* dec_out, int n, int A, const float* mask,
+                                     int64_t mask_stride, const int32_t* row_idx, const float* actions,
+                                     const float* old_logprobs, const float* advantages,
+                                     const float* returns, const float* values, const float* prio,
+                                     float clip_coef, float vf_clip_coef, float vf_coef, float ent_coef,
+                                     float* grad, float* ratio, float* newvalue, float* stats,
+                                     float* guard, void* stream) {
+    PT_REQUIRE(dec_out && mask && actions && old_logprobs && advantages && returns && values && grad,
+               "ppo_loss: null input");
+    hipStream_t s = (hipStream_t)stream;
+    // per-block partials live in a per-thread scratch sized for the largest n seen
+    static thread_local float* part = nullptr;
+    static thread_local long part_cap = 0;
+    const long need = pt_ppo_partial_floats(n);
+    if (need > part_cap) {
+        if (part) PT_HIP(hipFree(part));
+        part = nullptr;
+        PT_HIP(hipMalloc(&part, need * sizeof(float)));
+        part_cap = need;
+    }
+    return pt_ppo_loss(dec_out, n, A, mask, mask_stride, row_idx, actions, old_logprobs, advantages,
+                       returns, values, prio, clip_coef, vf_clip_coef, vf_coef, ent_coef, grad,
+                       ratio, newvalue, stats, guard, part, s);
+}
+
+extern "C" int ptcg_kl_gate(const float* guard, float kl_threshold, float vf_threshold, float* gate,
+                            float* skipped, void* stream) {
+    PT_REQUIRE(guard && gate, "kl_gate: null buffer");
+    return pt_kl_gate(guard, kl_threshold, vf_threshold, gate, skipped, (hipStream_t)stream);
+}
+
+extern "C" int ptcg_adam_step(float* weights, float* grads, float* m, float* v, int64_t n, float lr,
+                              float beta1, float beta2, float eps, float max_grad_norm,
+                              const float* gate, int32_t* step, float* norm_out, float* workspace,
+                              void* stream) {
+    PT_REQUIRE(weights && grads && m && v && step && workspace, "adam_step: null buffer");
+    return pt_adam_step(weights, grads, m, v, n, lr, beta1, beta2, eps, max_grad_norm, gate, step,
+                        norm_out, workspace, (hipStream_t)stream);
+}
+
+extern "C" int64_t ptcg_adam_workspace_floats(void) { return pt_adam_ws_floats(); }
+
+// ------------------------------------------------------------ trainer
+long pt_model_arena(const PtcgModel* m);
+float* pt_model_out(const PtcgModel* m);
+
+struct PtcgTrainer {
+    PtcgDims dm;
+    PtcgHypers hyp;
+    ObsOff off;
+    int B = 0;
+    long arena = 0, packed = 0;
+    PtcgModel* model = nullptr;
+    char* mem = nullptr;
+    float *P, *Gr, *M, *V;
+    float *grad, *ratio, *newvalue, *stats, *guard, *gate, *ppo_part, *adam_ws, *dbg_obs;
+    int32_t* step;
+};
+
+extern "C" void ptcg_trainer_free(PtcgTrainer* t) {
+    if (!t) return;
+    if (t->model) ptcg_model_free(t->model);
+    if (t->mem) (void)hipFree(t->mem);
+    delete t;
+}
+
+extern "C" int ptcg_trainer_create(const PtcgDims* dims, const PtcgHypers* hyp, int minibatch,
+                                   PtcgTrainer** out) {
+    PT_REQUIRE(dims && hyp && out, "trainer_create: null argument");
+    PT_REQUIRE(minibatch >= 2, "trainer_create: minibatch %d < 2", minibatch);
+    PtcgTrainer* t = new PtcgTrainer();
+    t->dm = *dims;
+    t->hyp = *hyp;
+    t->B = minibatch;
+    t->off = pt_obs_offsets(*dims);
+    int r = ptcg_model_create(dims, &t->model);
+    if (r != PTCG_OK) { delete t; return r; }
+    t->arena = pt_model_arena(t->model);
+    t->packed = ptcg_packed_floats(dims);
+    const long A1 = dims->n_opt + 1;
+    const long B = minibatch;
+    size_t off = 0;
+    auto take = [&](long floats) { off = (off + 255) & ~(size_t)255; size_t o = off; off += floats * 4; return o; };
+    const size_t oP = take(t->arena), oG = take(t->arena), oM = take(t->arena), oV = take(t->arena);
+    const size_t oGrad = take(B * A1), oRatio = take(B), oNv = take(B), oStats = take(16),
+                 oGuard = take(4), oGate = take(4), oPart = take(pt_ppo_partial_floats(minibatch)),
+                 oAdam = take(pt_adam_ws_floats()), oStep = take(4),
+                 oDbg = take(B * t->off.size);
+    hipError_t e = hipMalloc(&t->mem, off);
+    if (e != hipSuccess) {
+        ptcg_set_error("trainer_create: hipMalloc(%zu): %s", off, hipGetErrorString(e));
+        ptcg_trainer_free(t);
+        return PTCG_ERR_HIP;
+    }
+    e = hipMemset(t->mem, 0, off);
+    if (e != hipSuccess) {
+        ptcg_set_error("trainer_create: hipMemset: %s", hipGetErrorString(e));
+        ptcg_trainer_free(t);
+        return PTCG_ERR_HIP;
+    }
+    auto F = [&](size_t o) { return reinterpret_cast<float*>(t->mem + o); };
+    t->P = F(oP); t->Gr = F(oG); t->M = F(oM); t->V = F(oV);
+    t->grad = F(oGrad); t->ratio = F(oRatio); t->newvalue = F(oNv); t->stats = F(oStats);
+    t->guard = F(oGuard); t->gate = F(oGate); t->ppo_part = F(oPart); t->adam_ws = F(oAdam);
+    t->step = reinterpret_cast<int32_t*>(t->mem + oStep);
+    t->dbg_obs = F(oDbg);
+    r = ptcg_model_bind(t->model, t->P, t->Gr);
+    if (r == PTCG_OK) r = ptcg_model_reg_train(t->model, minibatch);
+    if (r != PTCG_OK) { ptcg_trainer_free(t); return r; }
+    *out = t;
+    return PTCG_OK;
+}
+
+extern "C" int ptcg_trainer_set_hypers(PtcgTrainer* t, const PtcgHypers* hyp) {
+    PT_REQUIRE(t && hyp, "set_hypers: null argument");
+    t->hyp = *hyp;
+    return PTCG_OK;
+}
+
+static int arena_copy_in(PtcgTrainer* t, float* dev, const float* packed) {
+    std::vector<float> img(t->arena, 0.f);
+    PT_TRY(ptcg_packed_to_arena(&t->dm, packed, img.data()));
+    PT_HIP(hipMemcpy(dev, img.data(), t->arena * sizeof(float), hipMemcpyHostToDevice));
+    return PTCG_OK;
+}
+static int arena_copy_out(PtcgTrainer* t, const float* dev, float* packed) {
+    std::vector<float> img(t->arena);
+    PT_HIP(hipDeviceSynchronize());
+    PT_HIP(hipMemcpy(img.data(), dev, t->arena * sizeof(float), hipMemcpyDeviceToHost));
+    return ptcg_arena_to_packed(&t->dm, img.data(), packed);
+}
+
+extern "C" int ptcg_trainer_set_weights(PtcgTrainer* t, const float* packed) {
+    PT_REQUIRE(t && packed, "set_weights: null argument");
+    return arena_copy_in(t, t->P, packed);
+}
+extern "C" int ptcg_trainer_get_weights(PtcgTrainer* t, float* packed) {
+    PT_REQUIRE(t && packed, "get_weights: null argument");
+    return arena_copy_out(t, t->P, packed);
+}
+extern "C" int ptcg_trainer_get_grads(PtcgTrainer* t, float* packed) {
+    PT_REQUIRE(t && packed, "get_grads: null argument");
+    return arena_copy_out(t, t->Gr, packed);
+}
+extern "C" int ptcg_trainer_get_moments(PtcgTrainer* t, float* m, float* v) {
+    PT_REQUIRE(t && m && v, "get_moments: null argument");
+    PT_TRY(arena_copy_out(t, t->M, m));
+    return arena_copy_out(t, t->V, v);
+}
+
+// bindings.cu:202-215 (save) / 339-367 (load): packed fp32 blob on disk
+extern "C" int ptcg_trainer_save_weights(PtcgTrainer* t, const char* path) {
+    PT_REQUIRE(t && path, "save_weights: null argument");
+    std::vector<float> packed(t->packed);
+    PT_TRY(ptcg_trainer_get_weights(t, packed.data()));
+    FILE* f = fopen(path, "wb");
+    if (!f) { ptcg_set_error("Failed to open %s for writing", path); return PTCG_ERR_IO; }
+    size_t w = fwrite(packed.data(), sizeof(float), packed.size(), f);
+    fclose(f);
+    if (w != packed.size()) { ptcg_set_error("Failed to write %s", path); return PTCG_ERR_IO; }
+    return PTCG_OK;
+}
+
+extern "C" int ptcg_trainer_load_weights(PtcgTrainer* t, const char* path) {
+    PT_REQUIRE(t && path, "load_weights: null argument");
+    FILE* f = fopen(path, "rb");
+    if (!f) { ptcg_set_error("Failed to open %s for reading", path); return PTCG_ERR_IO; }
+    fseek(f, 0, SEEK_END);
+    long size = ftell(f);
+    fseek(f, 0, SEEK_SET);
+    const long want = t->packed * (long)sizeof(float);
+    if (size != want) {
+        fclose(f);
+        ptcg_set_error("Weight file size mismatch: expected %ld bytes, got %ld", want, size);
+        return PTCG_ERR_IO;
+    }
+    std::vector<float> packed(t->packed);
+    size_t rd = fread(packed.data(), 1, want, f);
+    fclose(f);
+    if ((long)rd != want) { ptcg_set_error("Failed to read weight file %s", path); return PTCG_ERR_IO; }
+    return ptcg_trainer_set_weights(t, packed.data());
+}
+
+// Adam state: "PTCGADM1" | int64 step | int64 n_params | weights | m | v (packed).
+// A separate magic from the reference's Muon state (PTCGSTA1, bindings.cu:257-293).
+struct AdmHeader { char magic[8]; int64_t step; int64_t n_params; };
+
+extern "C" int ptcg_trainer_save_state(PtcgTrainer* t, const char* path) {
+    PT_REQUIRE(t && path, "save_state: null argument");
+    std::vector<float> w(t->packed), m(t->packed), v(t->packed);
+    PT_TRY(arena_copy_out(t, t->P, w.data()));
+    PT_TRY(arena_copy_out(t, t->M, m.data()));
+    PT_TRY(arena_copy_out(t, t->V, v.data()));
+    int32_t step = 0;
+    PT_HIP(hipMemcpy(&step, t->step, sizeof step, hipMemcpyDeviceToHost));
+    AdmHeader h;
+    memcpy(h.magic, "PTCGADM1", 8);
+    h.step = step;
+    h.n_params = t->packed;
+    std::string tmp = std::string(path) + ".tmp";
+    FILE* f = fopen(tmp.c_str(), "wb");
+    if (!f) { ptcg_set_error("Failed to open %s for writing", tmp.c_str()); return PTCG_ERR_IO; }
+    bool ok = fwrite(&h, sizeof h, 1, f) == 1 && fwrite(w.data(), 4, w.size(), f) == w.size() &&
+              fwrite(m.data(), 4, m.size(), f) == m.size() && fwrite(v.data(), 4, v.size(), f) == v.size();
+    ok = ok && fflush(f) == 0;
+    fclose(f);
+    if (!ok || rename(tmp.c_str(), path) != 0) {
+        ptcg_set_error("Failed to write state %s", path);
+        return PTCG_ERR_IO;
+    }
+    return PTCG_OK;
+}
+
+extern "C" int ptcg_trainer_load_state(PtcgTrainer* t, const char* path) {
+    PT_REQUIRE(t && path, "load_state: null argument");
+    FILE* f = fopen(path, "rb");
+    if (!f) { ptcg_set_error("Failed to open %s for reading", path); return PTCG_ERR_IO; }
+    AdmHeader h;
+    if (fread(&h, sizeof h, 1, f) != 1 || memcmp(h.magic, "PTCGADM1", 8) != 0) {
+        fclose(f);
+        ptcg_set_error("%s is not a PTCGADM1 state file", path);
+        return PTCG_ERR_IO;
+    }
+    if (h.n_params != t->packed) {
+        fclose(f);
+        ptcg_set_error("State param count mismatch: file %lld, model %ld", (long long)h.n_params, t->packed);
+        return PTCG_ERR_IO;
+    }
+    std::vector<float> w(t->packed), m(t->packed), v(t->packed);
+    bool ok = fread(w.data(), 4, w.size(), f) == w.size() && fread(m.data(), 4, m.size(), f) == m.size() &&
+              fread(v.data(), 4, v.size(), f) == v.size();
+    fclose(f);
+    if (!ok) { ptcg_set_error("Truncated state file %s", path); return PTCG_ERR_IO; }
+    PT_TRY(arena_copy_in(t, t->P, w.data()));
+    PT_TRY(arena_copy_in(t, t->M, m.data()));
+    PT_TRY(arena_copy_in(t, t->V, v.data()));
+    int32_t step = (int32_t)h.step;
+    PT_HIP(hipMemcpy(t->step, &step, sizeof step, hipMemcpyHostToDevice));
+    return PTCG_OK;
+}
+
+extern "C" int ptcg_trainer_debug_forward(PtcgTrainer* t, const float* obs_host, int n, float* out_host) {
+    PT_REQUIRE(t && obs_host && out_host, "debug_forward: null argument");
+    PT_REQUIRE(n == t->B, "debug_forward: need exactly %ld floats (minibatch %d x obs %d), got %ld",
+               (long)t->B * t->off.size, t->B, t->off.size, (long)n * t->off.size);
+    PT_HIP(hipMemcpy(t->dbg_obs, obs_host, (size_t)n * t->off.size * sizeof(float), hipMemcpyHostToDevice));
+    float* out = nullptr;
+    PT_TRY(ptcg_model_forward(t->model, t->dbg_obs, nullptr, n, &out, nullptr));
+    PT_HIP(hipStreamSynchronize(nullptr));
+    PT_HIP(hipMemcpy(out_host, out, (size_t)n * (t->dm.n_opt + 1) * sizeof(float), hipMemcpyDeviceToHost));
+    return PTCG_OK;
+}
+
+static int fwd_bwd(PtcgTrainer* t, const float* obs, const int32_t* idx, const float* actions,
+                   const float* old_logprobs, const float* advantages, const float* returns,
+                   const float* values, hipStream_t s) {
+    PT_REQUIRE(t && obs && actions && old_logprobs && advantages && returns && values,
+               "trainer_step: null input");
+    float* out = nullptr;
+    PT_TRY(ptcg_model_forward(t->model, obs, idx, t->B, &out, s));
+    const PtcgHypers& h = t->hyp;
+    PT_TRY(pt_ppo_loss(out, t->B, t->dm.n_opt, obs + t->off.opt_mask, t->off.size, idx, actions,
+                       old_logprobs, advantages, returns, values, nullptr, h.clip_coef, h.vf_clip_coef,
+                       h.vf_coef, h.ent_coef, t->grad, t->ratio, t->newvalue, t->stats, t->guard,
+                       t->ppo_part, s));
+    PT_TRY(ptcg_model_backward(t->model, t->grad, s));
+    return PTCG_OK;
+}
+
+extern "C" int ptcg_trainer_forward_backward(PtcgTrainer* t, const float* obs, const int32_t* row_idx,
+                                             const float* actions, const float* old_logprobs,
+                                             const float* advantages, const float* returns,
+                                             const float* values, void* stream) {
+    return fwd_bwd(t, obs, row_idx, actions, old_logprobs, advantages, returns, values, (hipStream_t)stream);
+}
+
+extern "C" int ptcg_trainer_step(PtcgTrainer* t, const float* obs, const int32_t* row_idx,
+                                 const float* actions, const float* old_logprobs, const float* advantages,
+                                 const float* returns, const float* values, void* stream) {
+    hipStream_t s = (hipStream_t)stream;
+    PT_TRY(fwd_bwd(t, obs, row_idx, actions, old_logprobs, advantages, returns, values, s));
+    const PtcgHypers& h = t->hyp;
+    const bool gate_on = h.kl_skip_threshold > 0.f || h.vf_skip_threshold > 0.f;
+    if (gate_on) PT_TRY(pt_kl_gate(t->guard, h.kl_skip_threshold, h.vf_skip_threshold, t->gate, t->stats + 8, s));
+    PT_TRY(pt_adam_step(t->P, t->Gr, t->M, t->V, t->arena, h.lr, h.beta1, h.beta2, h.eps, h.max_grad_norm,
+                        gate_on ? t->gate : nullptr, t->step, t->stats + 9, t->adam_ws, s));
+    return PTCG_OK;
+}
+
+extern "C" int ptcg_trainer_losses(PtcgTrainer* t, float* out10, int reset) {
+    PT_REQUIRE(t && out10, "losses: null argument");
+    PT_HIP(hipDeviceSynchronize());
+    PT_HIP(hipMemcpy(out10, t->stats, 10 * sizeof(float), hipMemcpyDeviceToHost));
+    if (reset) PT_HIP(hipMemset(t->stats, 0, 10 * sizeof(float)));
+    return PTCG_OK;
+}
+
+extern "C" int ptcg_trainer_buffers(PtcgTrainer* t, float** dec_out, float** ppo_grad, float** ratio,
+                                    float** newvalue) {
+    PT_REQUIRE(t, "buffers: null trainer");
+    if (dec_out) *dec_out = pt_model_out(t->model);
+    if (ppo_grad) *ppo_grad = t->grad;
+    if (ratio) *ratio = t->ratio;
+    if (newvalue) *newvalue = t->newvalue;
+    return PTCG_OK;
+}
+
+extern "C" int ptcg_trainer_sync(PtcgTrainer* t) {
+    (void)t;
+    PT_HIP(hipDeviceSynchronize());
+    return PTCG_OK;
+}
+
+extern "C" int ptcg_trainer_step_count(PtcgTrainer* t, int32_t* out) {
+    PT_REQUIRE(t && out, "step_count: null argument");
+    PT_HIP(hipMemcpy(out, t->step, sizeof(int32_t), hipMemcpyDeviceToHost));
+    return PTCG_OK;
+}

@@ -1,0 +1,121 @@
+// Shared helpers for the PTCG HIP kernels (gfx950 / CDNA4, wave64).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <math.h>
+
+#include "../../include/ptcg_amd.h"
+
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+// ---------------------------------------------------------------- errors
+void ptcg_set_error(const char* fmt, ...);
+
+#define PT_HIP(call)                                                        \
+    do {                                                                    \
+        hipError_t _e = (call);                                             \
+        if (_e != hipSuccess) {                                             \
+            ptcg_set_error("%s:%d %s: %s", __FILE__, __LINE__, #call,       \
+                           hipGetErrorString(_e));                          \
+            return PTCG_ERR_HIP;                                            \
+        }                                                                   \
+    } while (0)
+
+#define PT_REQUIRE(cond, ...)                                               \
+    do {                                                                    \
+        if (!(cond)) {                                                      \
+            ptcg_set_error(__VA_ARGS__);                                    \
+            return PTCG_ERR_ARG;                                            \
+        }                                                                   \
+    } while (0)
+
+#define PT_TRY(expr)                                                        \
+    do {                                                                    \
+        int _r = (expr);                                                    \
+        if (_r != PTCG_OK) return _r;                                       \
+    } while (0)
+
+// launch then check the launch status
+#define PT_LAUNCH_CHECK()  PT_HIP(hipGetLastError())
+
+static inline int pt_cdiv(long a, long b) { return (int)((a + b - 1) / b); }
+
+// ---------------------------------------------------------------- device math
+// Exact (erf) GELU, torch nn.GELU() default; the reference's pt_gelu_fwd/bwd
+// (ptcg_kernels.cuh:111-128) computes the same function and derivative.
+__device__ __forceinline__ float pt_gelu(float x) {
+    return 0.5f * x * (1.f + erff(x * 0.70710678118654752f));
+}
+__device__ __forceinline__ float pt_gelu_grad(float x) {
+    float cdf = 0.5f * (1.f + erff(x * 0.70710678118654752f));
+    float pdf = 0.3989422804014327f * expf(-0.5f * x * x);
+    return cdf + x * pdf;
+}
+
+// fp32 id read back from an obs row: C cast truncates toward zero, then clamp
+__device__ __forceinline__ int pt_id_clamp(float v, int hi) {
+    int i = (int)v;
+    return i < 0 ? 0 : (i > hi ? hi : i);
+}
+
+// wave64 reductions (DPP/permute via __shfl_xor)
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
+// row pointer of obs row n, optionally through an int32 row-index list
+__device__ __forceinline__ const float* obs_row(const float* obs, const int32_t* idx,
+                                                long stride, int n) {
+    long r = idx ? (long)idx[n] : (long)n;
+    return obs + r * stride;
+}
+
+// ---------------------------------------------------------------- GEMM API
+// C[M,N] = epi( sum_k A(m,k) B(k,n) ),
+//   A(m,k) = a_t ? A[k*lda+m] : A[m*lda+k];  B(k,n) = b_t ? B[k*ldb+n] : B[n*ldb+k]
+enum PtEpi {
+    EPI_STORE = 0,      // C = acc
+    EPI_BIAS = 1,       // C = acc + bias[n]
+    EPI_BIAS_GELU = 2,  // C = acc + bias[n]; C2 = gelu(C)
+    EPI_BIAS_RESID = 3, // C = acc + bias[n] + R[m*ldr+n]
+    EPI_GELU_BWD = 4,   // C = acc * gelu'(R[m*ldr+n])
+    EPI_ACCUM = 5,      // C += acc
+};
+
+struct GemmArgs {
+    int M, N, K;
+    const float* A; long lda;
+    const float* B; long ldb;
+    float* C; long ldc;
+    const float* bias;
+    const float* R; long ldr;
+    float* C2; long ldc2;
+    int a_t, b_t, epi;
+};
+
+// Launch C = epi(A*B) on `stream`. Requirements: K % 4 == 0 when the operand
+// is k-contiguous, M (N) % 4 == 0 when A (B) is m- (n-) contiguous, leading
+// dims multiples of 4, 16 B-aligned bases.  Weight-gradient shapes
+// (large K, small M*N) are split over K with a deterministic reduction.
+int pt_gemm(const GemmArgs& g, float* splitk_ws, long splitk_ws_floats, hipStream_t s);
+
+// Linear helpers on row-major activations X (rows, in) and W (out, in)
+int pt_linear_fwd(const float* X, const float* W, const float* b, float* Y, int rows,
+                  int in, int out, int epi, const float* R, float* Y2, hipStream_t s);
+// dX = dY W  (epi: EPI_STORE, EPI_ACCUM or EPI_GELU_BWD with R = pre-activation)
+int pt_linear_dx(const float* dY, const float* W, float* dX, int rows, int in, int out,
+                 int epi, const float* R, hipStream_t s);
+// dW = dY^T X (overwrite), db = colsum(dY) (overwrite, may be NULL)
+int pt_linear_dw(const float* dY, const float* X, float* dW, float* db, int rows, int in,
+                 int out, float* ws, long ws_floats, hipStream_t s);
+
+// deterministic column sums: out[n] = sum_m X[m*ldx + n], m < M
+int pt_colsum(const float* X, long ldx, int M, int N, float* out, float* ws, long ws_floats,
+              hipStream_t s);

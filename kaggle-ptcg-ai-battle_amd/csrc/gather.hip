@@ -1,0 +1,536 @@
+// Gathers and scatters around the GEMMs: token concat, decision concat,
+// trunk input assembly, option-scorer inputs, and their backward scatters.
+//
+// Reference counterparts (native/model/ptcg_model.cu, ptcg_model2.cu):
+//   k_tok_cat :289 / k_tok_cat_bwd :36      -> tok_cat_*
+//   k_dec_in :324 / k_dec_in_bwd :66        -> dec_in_*
+//   k_x0 :348 / k_x0_bwd :202               -> x0_*
+//   k_opt_gather :371 / k_opt_gather_bwd :135
+//   k_q_in :390 / k_q_in_bwd :85
+//   k_sc_in :423 / k_sc_in_bwd :115
+//   k_val_in :503 / k_val_in_bwd :191
+// Ids come from fp32 obs columns: (int) truncation toward zero, then clamp
+// to the vocabulary (ptcg_model.cu:299-318).  Forward gathers move 16 B per
+// lane.  Per-sample reductions (the bcast row sum, the pointer scatter into
+// the trunk output, the option sums into r/g/dvec) run one workgroup per
+// sample in a fixed order instead of the reference's atomics; only the
+// scatters into shared embedding tables (card/attack/zone/owner/type/select/
+// context rows shared across samples) use fp32 atomics, as the reference does.
+#include "model.h"
+
+namespace {
+
+constexpr int TB = 256;
+
+__global__ void tok_cat_fwd_kernel(GatherCtx c, const float* __restrict__ card,
+        const float* __restrict__ zemb, const float* __restrict__ oemb, float* __restrict__ out) {
+    const int Lt = c.dm.l_tok, dc = c.dm.d_c, tin = c.dx.tok_in;
+    const int chunks = tin / 4;
+    const long i = (long)blockIdx.x * TB + threadIdx.x;
+    if (i >= (long)c.N * Lt * chunks) return;
+    const int ch = (int)(i % chunks);
+    const long r = i / chunks;
+    const int n = (int)(r / Lt), t = (int)(r % Lt);
+    const float* row = obs_row(c.obs, c.idx, c.stride, n);
+    const float* ti = row + c.off.tok_int + (long)t * c.dm.tok_int;
+    const int col = ch * 4;
+    const int NC = c.dm.n_cards;
+    float4 v;
+    if (col < dc) {
+        const int cid = pt_id_clamp(ti[0], NC - 1);
+        v = *reinterpret_cast<const float4*>(card + (long)cid * dc + col);
+    } else if (col < 2 * dc) {
+        const int e = col - dc;
+        const int t0 = (int)ti[3], t1 = (int)ti[4];
+        float4 a = make_float4(0.f, 0.f, 0.f, 0.f), b = a;
+        if (t0 > 0) a = *reinterpret_cast<const float4*>(card + (long)(t0 >= NC ? NC - 1 : t0) * dc + e);
+        if (t1 > 0) b = *reinterpret_cast<const float4*>(card + (long)(t1 >= NC ? NC - 1 : t1) * dc + e);
+        v = make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
+    } else if (col < 2 * dc + c.dm.tok_f) {
+        v = *reinterpret_cast<const float4*>(row + c.off.tok_float + (long)t * c.dm.tok_f + (col - 2 * dc));
+    } else if (col < 2 * dc + c.dm.tok_f + PT_ZONE_E) {
+        const int z = pt_id_clamp(ti[1], c.dm.n_zones - 1);
+        v = *reinterpret_cast<const float4*>(zemb + z * PT_ZONE_E + (col - 2 * dc - c.dm.tok_f));
+    } else {
+        const int o = pt_id_clamp(ti[2], c.dm.n_owners - 1);
+        v = *reinterpret_cast<const float4*>(oemb + o * PT_OWNER_E + (col - 2 * dc - c.dm.tok_f - PT_ZONE_E));
+    }
+    *reinterpret_cast<float4*>(out + r * tin + col) = v;
+}
+
+__global__ void tok_cat_bwd_kernel(GatherCtx c, const float* __restrict__ d_cat, float* d_card,
+                                   float* d_zemb, float* d_oemb) {
+    const int Lt = c.dm.l_tok, dc = c.dm.d_c, tin = c.dx.tok_in;
+    const long i = (long)blockIdx.x * TB + threadIdx.x;
+    if (i >= (long)c.N * Lt * tin) return;
+    const int col = (int)(i % tin);
+    const long r = i / tin;
+    const float g = d_cat[i];
+    if (g == 0.f) return;
+    const int n = (int)(r / Lt), t = (int)(r % Lt);
+    const float* ti = obs_row(c.obs, c.idx, c.stride, n) + c.off.tok_int + (long)t * c.dm.tok_int;
+    const int NC = c.dm.n_cards;
+    if (col < dc) {
+        atomicAdd(d_card + (long)pt_id_clamp(ti[0], NC - 1) * dc + col, g);
+    } else if (col < 2 * dc) {
+        const int e = col - dc;
+        const int t0 = (int)ti[3], t1 = (int)ti[4];
+        if (t0 > 0) atomicAdd(d_card + (long)(t0 >= NC ? NC - 1 : t0) * dc + e, g);
+        if (t1 > 0) atomicAdd(d_card + (long)(t1 >= NC ? NC - 1 : t1) * dc + e, g);
+    } else if (col < 2 * dc + c.dm.tok_f) {
+        // numeric features are inputs: no gradient
+    } else if (col < 2 * dc + c.dm.tok_f + PT_ZONE_E) {
+        const int z = pt_id_clamp(ti[1], c.dm.n_zones - 1);
+        atomicAdd(d_zemb + z * PT_ZONE_E + (col - 2 * dc - c.dm.tok_f), g);
+    } else {
+        const int o = pt_id_clamp(ti[2], c.dm.n_owners - 1);
+        atomicAdd(d_oemb + o * PT_OWNER_E + (col - 2 * dc - c.dm.tok_f - PT_ZONE_E), g);
+    }
+}
+
+__global__ void glob_in_kernel(GatherCtx c, float* __restrict__ out) {
+    const int G = c.dm.global_f;
+    const long i = (long)blockIdx.x * TB + threadIdx.x;
+    if (i >= (long)c.N * G) return;
+    const int n = (int)(i / G), k = (int)(i % G);
+    out[i] = obs_row(c.obs, c.idx, c.stride, n)[c.off.global_f + k];
+}
+
+// dec concat: [sel8 | ctx32 | cv(eff) | cv(ctx) | av(my) | av(opp) | cv(msup) | cv(osup) | dec_f]
+struct DecSeg { int kind; int slot; int width; };
+__device__ __forceinline__ void dec_locate(const GatherCtx& c, int col, int& kind, int& di, int& e) {
+    const int dc = c.dm.d_c, da = c.dm.d_a;
+    const int b0 = PT_SEL_E, b1 = b0 + PT_CTX_E, b2 = b1 + dc, b3 = b2 + dc, b4 = b3 + da,
+              b5 = b4 + da, b6 = b5 + dc, b7 = b6 + dc;
+    if (col < b0) { kind = 0; di = 0; e = col; }
+    else if (col < b1) { kind = 1; di = 1; e = col - b0; }
+    else if (col < b2) { kind = 2; di = 2; e = col - b1; }
+    else if (col < b3) { kind = 2; di = 3; e = col - b2; }
+    else if (col < b4) { kind = 3; di = 4; e = col - b3; }
+    else if (col < b5) { kind = 3; di = 5; e = col - b4; }
+    else if (col < b6) { kind = 2; di = 6; e = col - b5; }
+    else if (col < b7) { kind = 2; di = 7; e = col - b6; }
+    else { kind = 4; di = 0; e = col - b7; }
+}
+
+__global__ void dec_in_fwd_kernel(GatherCtx c, const float* __restrict__ card,
+        const float* __restrict__ att, const float* __restrict__ semb,
+        const float* __restrict__ cemb, float* __restrict__ out) {
+    const int W = c.dx.dec_in;
+    const long i = (long)blockIdx.x * TB + threadIdx.x;
+    if (i >= (long)c.N * W) return;
+    const int n = (int)(i / W), col = (int)(i % W);
+    const float* row = obs_row(c.obs, c.idx, c.stride, n);
+    const float* di_ = row + c.off.dec_int;
+    int kind, di, e;
+    dec_locate(c, col, kind, di, e);
+    float v;
+    if (kind == 0) v = semb[pt_id_clamp(di_[0], c.dm.n_select_types - 1) * PT_SEL_E + e];
+    else if (kind == 1) v = cemb[pt_id_clamp(di_[1], c.dm.n_contexts - 1) * PT_CTX_E + e];
+    else if (kind == 2) v = card[(long)pt_id_clamp(di_[di], c.dm.n_cards - 1) * c.dm.d_c + e];
+    else if (kind == 3) v = att[(long)pt_id_clamp(di_[di], c.dm.n_attacks - 1) * c.dm.d_a + e];
+    else v = row[c.off.dec_float + e];
+    out[i] = v;
+}
+
+__global__ void dec_in_bwd_kernel(GatherCtx c, const float* __restrict__ d_in, float* d_card,
+                                  float* d_att, float* d_semb, float* d_cemb) {
+    const int W = c.dx.dec_in;
+    const long i = (long)blockIdx.x * TB + threadIdx.x;
+    if (i >= (long)c.N * W) return;
+    const float g = d_in[i];
+    if (g == 0.f) return;
+    const int n = (int)(i / W), col = (int)(i % W);
+    const float* di_ = obs_row(c.obs, c.idx, c.stride, n) + c.off.dec_int;
+    int kind, di, e;
+    dec_locate(c, col, kind, di, e);
+    if (kind == 0) atomicAdd(d_semb + pt_id_clamp(di_[0], c.dm.n_select_types - 1) * PT_SEL_E + e, g);
+    else if (kind == 1) atomicAdd(d_cemb + pt_id_clamp(di_[1], c.dm.n_contexts - 1) * PT_CTX_E + e, g);
+    else if (kind == 2) atomicAdd(d_card + (long)pt_id_clamp(di_[di], c.dm.n_cards - 1) * c.dm.d_c + e, g);
+    else if (kind == 3) atomicAdd(d_att + (long)pt_id_clamp(di_[di], c.dm.n_attacks - 1) * c.dm.d_a + e, g);
+}
+
+// x0[n,0] = readout; x0[n,l] = tokp[n,l-1] + bc[n]; keep[n,l] = l==0 || zone_float > 0
+__global__ void x0_fwd_kernel(GatherCtx c, const float* __restrict__ tokp,
+        const float* __restrict__ bc, const float* __restrict__ readout, float* __restrict__ x0,
+        float* __restrict__ keep) {
+    const int Ls = c.dx.l_seq, D = c.dm.d, ch4 = D / 4;
+    const long i = (long)blockIdx.x * TB + threadIdx.x;
+    if (i >= (long)c.N * Ls * ch4) return;
+    const int col = (int)(i % ch4) * 4;
+    const long nl = i / ch4;
+    const int n = (int)(nl / Ls), l = (int)(nl % Ls);
+    float4 v;
+    if (l == 0) {
+        v = *reinterpret_cast<const float4*>(readout + col);
+    } else {
+        const float4 a = *reinterpret_cast<const float4*>(tokp + ((long)n * c.dm.l_tok + (l - 1)) * D + col);
+        const float4 b = *reinterpret_cast<const float4*>(bc + (long)n * D + col);
+        v = make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
+    }
+    *reinterpret_cast<float4*>(x0 + nl * D + col) = v;
+    if (col == 0) {
+        float kp = 1.f;
+        if (l > 0) {
+            const float z = obs_row(c.obs, c.idx, c.stride, n)[c.off.tok_int + (long)(l - 1) * c.dm.tok_int + 1];
+            kp = z > 0.f ? 1.f : 0.f;
+        }
+        keep[(long)n * Ls + l] = kp;
+    }
+}
+
+// one workgroup per sample: d_tokp[n,t] = d_x0[n,t+1]; d_bc[n] = sum_t d_x0[n,t+1]
+__global__ void x0_bwd_kernel(GatherCtx c, const float* __restrict__ d_x0, float* __restrict__ d_tokp,
+                              float* __restrict__ d_bc) {
+    const int n = blockIdx.x, Ls = c.dx.l_seq, Lt = c.dm.l_tok, D = c.dm.d;
+    for (int col = threadIdx.x; col < D; col += TB) {
+        float acc = 0.f;
+        for (int t = 0; t < Lt; ++t) {
+            const float v = d_x0[((long)n * Ls + t + 1) * D + col];
+            d_tokp[((long)n * Lt + t) * D + col] = v;
+            acc += v;
+        }
+        d_bc[(long)n * D + col] = acc;
+    }
+}
+
+__global__ void opt_gather_fwd_kernel(GatherCtx c, const float* __restrict__ card,
+        const float* __restrict__ att, float* __restrict__ ocard, float* __restrict__ oatt) {
+    const int NO = c.dm.n_opt, dc = c.dm.d_c, da = c.dm.d_a;
+    const int W = dc > da ? dc : da;
+    const long i = (long)blockIdx.x * TB + threadIdx.x;
+    if (i >= (long)c.N * NO * W) return;
+    const int e = (int)(i % W);
+    const long nj = i / W;
+    const int n = (int)(nj / NO), j = (int)(nj % NO);
+    const float* oi = obs_row(c.obs, c.idx, c.stride, n) + c.off.opt_int + (long)j * c.dm.opt_int;
+    if (e < dc) ocard[nj * dc + e] = card[(long)pt_id_clamp(oi[3], c.dm.n_cards - 1) * dc + e];
+    if (e < da) oatt[nj * da + e] = att[(long)pt_id_clamp(oi[4], c.dm.n_attacks - 1) * da + e];
+}
+
+__global__ void opt_gather_bwd_kernel(GatherCtx c, const float* __restrict__ d_ocard,
+        const float* __restrict__ d_oatt, float* d_card, float* d_att) {
+    const int NO = c.dm.n_opt, dc = c.dm.d_c, da = c.dm.d_a;
+    const int W = dc > da ? dc : da;
+    const long i = (long)blockIdx.x * TB + threadIdx.x;
+    if (i >= (long)c.N * NO * W) return;
+    const int e = (int)(i % W);
+    const long nj = i / W;
+    const int n = (int)(nj / NO), j = (int)(nj % NO);
+    const float* oi = obs_row(c.obs, c.idx, c.stride, n) + c.off.opt_int + (long)j * c.dm.opt_int;
+    if (e < dc) {
+        const float g = d_ocard[nj * dc + e];
+        if (g != 0.f) atomicAdd(d_card + (long)pt_id_clamp(oi[3], c.dm.n_cards - 1) * dc + e, g);
+    }
+    if (e < da) {
+        const float g = d_oatt[nj * da + e];
+        if (g != 0.f) atomicAdd(d_att + (long)pt_id_clamp(oi[4], c.dm.n_attacks - 1) * da + e, g);
+    }
+}
+
+// q_in = [temb16 | h(p1) | h(p2) | (opt_card, opt_attack GEMM outputs) | opt_f]
+__global__ void q_in_fwd_kernel(GatherCtx c, const float* __restrict__ h,
+        const float* __restrict__ temb, float* __restrict__ q_in) {
+    const int NO = c.dm.n_opt, D = c.dm.d, W = c.dx.q_in, ch = W / 4;
+    const long i = (long)blockIdx.x * TB + threadIdx.x;
+    if (i >= (long)c.N * NO * ch) return;
+    const int col = (int)(i % ch) * 4;
+    const long nj = i / ch;
+    const int n = (int)(nj / NO), j = (int)(nj % NO);
+    const int oc0 = PT_TYPE_E + 2 * D, of0 = oc0 + 2 * PT_OPT_E;
+    if (col >= oc0 && col < of0) return;      // written by the opt_card / opt_attack GEMMs
+    const float* row = obs_row(c.obs, c.idx, c.stride, n);
+    const float* oi = row + c.off.opt_int + (long)j * c.dm.opt_int;
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (col < PT_TYPE_E) {
+        v = *reinterpret_cast<const float4*>(temb + pt_id_clamp(oi[0], c.dm.n_opt_types - 1) * PT_TYPE_E + col);
+    } else if (col < oc0) {
+        const int which = col < PT_TYPE_E + D ? 1 : 2;
+        const int e = col - PT_TYPE_E - (which - 1) * D;
+        const int p = (int)oi[which];      // 0 = null; else trunk position p (token p-1)
+        if (p > 0 && p <= c.dm.l_tok)
+            v = *reinterpret_cast<const float4*>(h + ((long)n * c.dx.l_seq + p) * D + e);
+    } else {
+        v = *reinterpret_cast<const float4*>(row + c.off.opt_float + (long)j * c.dm.opt_f + (col - of0));
+    }
+    *reinterpret_cast<float4*>(q_in + nj * W + col) = v;
+}
+
+// one workgroup per sample, options in order: d_h[n,p] += d_qin pointer slices
+__global__ void q_in_bwd_kernel(GatherCtx c, const float* __restrict__ d_qin, float* __restrict__ d_h,
+                                float* d_temb) {
+    const int n = blockIdx.x, NO = c.dm.n_opt, D = c.dm.d, W = c.dx.q_in;
+    const float* row = obs_row(c.obs, c.idx, c.stride, n);
+    for (int j = 0; j < NO; ++j) {
+        const float* oi = row + c.off.opt_int + (long)j * c.dm.opt_int;
+        const float* g = d_qin + ((long)n * NO + j) * W;
+        const int p1 = (int)oi[1], p2 = (int)oi[2];
+        const bool v1 = p1 > 0 && p1 <= c.dm.l_tok, v2 = p2 > 0 && p2 <= c.dm.l_tok;
+        for (int col = threadIdx.x; col < D; col += TB) {
+            if (v1) d_h[((long)n * c.dx.l_seq + p1) * D + col] += g[PT_TYPE_E + col];
+        }
+        __syncthreads();
+        for (int col = threadIdx.x; col < D; col += TB) {
+            if (v2) d_h[((long)n * c.dx.l_seq + p2) * D + col] += g[PT_TYPE_E + D + col];
+        }
+        if (threadIdx.x < PT_TYPE_E) {
+            const float gt = g[threadIdx.x];
+            if (gt != 0.f)
+                atomicAdd(d_temb + pt_id_clamp(oi[0], c.dm.n_opt_types - 1) * PT_TYPE_E + threadIdx.x, gt);
+        }
+        __syncthreads();
+    }
+}
+
+// sc_in = [q (GEMM output) | r | g | dvec | q*r],  r = h[n,0], gd = [g | dvec]
+__global__ void sc_in_fwd_kernel(GatherCtx c, const float* __restrict__ h,
+        const float* __restrict__ gd, float* __restrict__ sc) {
+    const int NO = c.dm.n_opt, D = c.dm.d, G = c.dm.g, W = c.dx.score_in;
+    const int cw = W - D, ch = cw / 4;
+    const long i = (long)blockIdx.x * TB + threadIdx.x;
+    if (i >= (long)c.N * NO * ch) return;
+    const int col = D + (int)(i % ch) * 4;
+    const long nj = i / ch;
+    const int n = (int)(nj / NO);
+    const float* r = h + (long)n * c.dx.l_seq * D;
+    float* o = sc + nj * W;
+    float4 v;
+    if (col < 2 * D) v = *reinterpret_cast<const float4*>(r + (col - D));
+    else if (col < 2 * D + G + PT_DEC_H) v = *reinterpret_cast<const float4*>(gd + (long)n * c.dx.bcast_in + (col - 2 * D));
+    else {
+        const int e = col - (2 * D + G + PT_DEC_H);
+        const float4 q = *reinterpret_cast<const float4*>(o + e);
+        const float4 rr = *reinterpret_cast<const float4*>(r + e);
+        v = make_float4(q.x * rr.x, q.y * rr.y, q.z * rr.z, q.w * rr.w);
+    }
+    *reinterpret_cast<float4*>(o + col) = v;
+}
+
+// one workgroup per sample: d_q = dsc[q] + dsc[qr]*r ; d_r, d_g, d_dvec summed over options
+__global__ void sc_in_bwd_kernel(GatherCtx c, const float* __restrict__ d_sc,
+        const float* __restrict__ sc, float* __restrict__ d_q, float* __restrict__ d_h,
+        float* __restrict__ d_gd) {
+    const int n = blockIdx.x, NO = c.dm.n_opt, D = c.dm.d, G = c.dm.g, W = c.dx.score_in;
+    const int o_r = D, o_g = 2 * D, o_dv = 2 * D + G, o_qr = 2 * D + G + PT_DEC_H;
+    for (int col = threadIdx.x; col < D; col += TB) {
+        const float r = sc[(long)n * NO * W + o_r + col];
+        float ar = 0.f, ag = 0.f, adv = 0.f;
+        for (int j = 0; j < NO; ++j) {
+            const long nj = (long)n * NO + j;
+            const float* g = d_sc + nj * W;
+            const float q = sc[nj * W + col];
+            d_q[nj * D + col] = g[col] + g[o_qr + col] * r;
+            ar += g[o_r + col] + g[o_qr + col] * q;
+            if (col < G) ag += g[o_g + col];
+            if (col < PT_DEC_H) adv += g[o_dv + col];
+        }
+        d_h[(long)n * c.dx.l_seq * D + col] += ar;
+        if (col < G) d_gd[(long)n * c.dx.bcast_in + col] += ag;
+        if (col < PT_DEC_H) d_gd[(long)n * c.dx.bcast_in + G + col] += adv;
+    }
+}
+
+__global__ void val_in_fwd_kernel(GatherCtx c, const float* __restrict__ h,
+        const float* __restrict__ gd, float* __restrict__ v) {
+    const int D = c.dm.d, W = c.dx.val_in;
+    const long i = (long)blockIdx.x * TB + threadIdx.x;
+    if (i >= (long)c.N * W) return;
+    const int n = (int)(i / W), col = (int)(i % W);
+    v[i] = col < D ? h[(long)n * c.dx.l_seq * D + col] : gd[(long)n * c.dx.bcast_in + (col - D)];
+}
+
+__global__ void val_in_bwd_kernel(GatherCtx c, const float* __restrict__ dv, float* __restrict__ d_h,
+                                  float* __restrict__ d_gd) {
+    const int D = c.dm.d, W = c.dx.val_in;
+    const long i = (long)blockIdx.x * TB + threadIdx.x;
+    if (i >= (long)c.N * W) return;
+    const int n = (int)(i / W), col = (int)(i % W);
+    if (col < D) d_h[(long)n * c.dx.l_seq * D + col] += dv[i];
+    else d_gd[(long)n * c.dx.bcast_in + (col - D)] += dv[i];
+}
+
+// one wave per row: out = X[r,:] . w + b
+__global__ void head_dot_kernel(const float* __restrict__ X, int rows, int K,
+        const float* __restrict__ w, const float* __restrict__ b, float* __restrict__ out, int per,
+        long ldo, int col0) {
+    const int lane = threadIdx.x & 63;
+    const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (r >= rows) return;
+    const float* x = X + (long)r * K;
+    float s = 0.f;
+    for (int k = lane; k < K; k += 64) s += x[k] * w[k];
+    s = wave_sum(s);
+    if (lane == 0) out[(long)(r / per) * ldo + col0 + (r % per)] = s + b[0];
+}
+
+__global__ void head_dot_bwd_kernel(const float* __restrict__ grad, int per, long ldg, int col0,
+        const float* __restrict__ w, const float* __restrict__ pre, float* __restrict__ dX, int rows,
+        int K) {
+    const long i = (long)blockIdx.x * TB + threadIdx.x;
+    if (i >= (long)rows * K) return;
+    const int r = (int)(i / K), k = (int)(i % K);
+    const float dy = grad[(long)(r / per) * ldg + col0 + (r % per)];
+    dX[i] = dy * w[k] * pt_gelu_grad(pre[i]);
+}
+
+constexpr int HD_ROWS = 256;
+// partial[chunk][0..K) = sum dy*X, partial[chunk][K] = sum dy
+__global__ void head_dot_dw_partial_kernel(const float* __restrict__ grad, int per, long ldg,
+        int col0, const float* __restrict__ X, int rows, int K, float* __restrict__ part) {
+    const int r0 = blockIdx.x * HD_ROWS, r1 = min(rows, r0 + HD_ROWS);
+    for (int k = threadIdx.x; k <= K; k += TB) {
+        float s = 0.f;
+        for (int r = r0; r < r1; ++r) {
+            const float dy = grad[(long)(r / per) * ldg + col0 + (r % per)];
+            s += dy * (k < K ? X[(long)r * K + k] : 1.0f);
+        }
+        part[(long)blockIdx.x * (K + 1) + k] = s;
+    }
+}
+
+__global__ void head_dot_dw_final_kernel(const float* __restrict__ part, int chunks, int K,
+                                         float* __restrict__ dw, float* __restrict__ db) {
+    const int k = blockIdx.x * TB + threadIdx.x;
+    if (k > K) return;
+    float s = 0.f;
+    for (int ch = 0; ch < chunks; ++ch) s += part[(long)ch * (K + 1) + k];
+    if (k < K) dw[k] = s; else db[0] = s;
+}
+
+__global__ void fill_zero_kernel(float4* p, long n4) {
+    const long i = (long)blockIdx.x * TB + threadIdx.x;
+    if (i < n4) p[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+}
+__global__ void fill_zero_tail_kernel(float* p, long n) {
+    const long i = (long)blockIdx.x * TB + threadIdx.x;
+    if (i < n) p[i] = 0.f;
+}
+
+#define PT_GRID(total) dim3(pt_cdiv((long)(total), TB)), dim3(TB), 0, s
+
+}  // namespace
+
+int pt_tok_cat_fwd(const GatherCtx& c, const float* card, const float* zemb, const float* oemb,
+                   float* tok_cat, hipStream_t s) {
+    PT_REQUIRE(c.dm.d_c % 4 == 0 && c.dm.tok_f % 4 == 0 && c.off.tok_float % 4 == 0 && c.stride % 4 == 0,
+               "tok_cat: widths must be multiples of 4");
+    hipLaunchKernelGGL(tok_cat_fwd_kernel, PT_GRID((long)c.N * c.dm.l_tok * (c.dx.tok_in / 4)), c, card, zemb, oemb, tok_cat);
+    PT_LAUNCH_CHECK();
+    return PTCG_OK;
+}
+int pt_tok_cat_bwd(const GatherCtx& c, const float* d_cat, float* d_card, float* d_zemb, float* d_oemb,
+                   hipStream_t s) {
+    hipLaunchKernelGGL(tok_cat_bwd_kernel, PT_GRID((long)c.N * c.dm.l_tok * c.dx.tok_in), c, d_cat, d_card, d_zemb, d_oemb);
+    PT_LAUNCH_CHECK();
+    return PTCG_OK;
+}
+int pt_glob_in(const GatherCtx& c, float* glob_in, hipStream_t s) {
+    hipLaunchKernelGGL(glob_in_kernel, PT_GRID((long)c.N * c.dm.global_f), c, glob_in);
+    PT_LAUNCH_CHECK();
+    return PTCG_OK;
+}
+int pt_dec_in_fwd(const GatherCtx& c, const float* card, const float* att, const float* semb,
+                  const float* cemb, float* dec_in, hipStream_t s) {
+    hipLaunchKernelGGL(dec_in_fwd_kernel, PT_GRID((long)c.N * c.dx.dec_in), c, card, att, semb, cemb, dec_in);
+    PT_LAUNCH_CHECK();
+    return PTCG_OK;
+}
+int pt_dec_in_bwd(const GatherCtx& c, const float* d_in, float* d_card, float* d_att, float* d_semb,
+                  float* d_cemb, hipStream_t s) {
+    hipLaunchKernelGGL(dec_in_bwd_kernel, PT_GRID((long)c.N * c.dx.dec_in), c, d_in, d_card, d_att, d_semb, d_cemb);
+    PT_LAUNCH_CHECK();
+    return PTCG_OK;
+}
+int pt_x0_fwd(const GatherCtx& c, const float* tokp, const float* bc, const float* readout, float* x0,
+              float* keep, hipStream_t s) {
+    hipLaunchKernelGGL(x0_fwd_kernel, PT_GRID((long)c.N * c.dx.l_seq * (c.dm.d / 4)), c, tokp, bc, readout, x0, keep);
+    PT_LAUNCH_CHECK();
+    return PTCG_OK;
+}
+int pt_x0_bwd(const GatherCtx& c, const float* d_x0, float* d_tokp, float* d_bc, hipStream_t s) {
+    hipLaunchKernelGGL(x0_bwd_kernel, dim3(c.N), dim3(TB), 0, s, c, d_x0, d_tokp, d_bc);
+    PT_LAUNCH_CHECK();
+    return PTCG_OK;
+}
+int pt_opt_gather_fwd(const GatherCtx& c, const float* card, const float* att, float* ocard, float* oatt,
+                      hipStream_t s) {
+    const int W = c.dm.d_c > c.dm.d_a ? c.dm.d_c : c.dm.d_a;
+    hipLaunchKernelGGL(opt_gather_fwd_kernel, PT_GRID((long)c.N * c.dm.n_opt * W), c, card, att, ocard, oatt);
+    PT_LAUNCH_CHECK();
+    return PTCG_OK;
+}
+int pt_opt_gather_bwd(const GatherCtx& c, const float* d_ocard, const float* d_oatt, float* d_card,
+                      float* d_att, hipStream_t s) {
+    const int W = c.dm.d_c > c.dm.d_a ? c.dm.d_c : c.dm.d_a;
+    hipLaunchKernelGGL(opt_gather_bwd_kernel, PT_GRID((long)c.N * c.dm.n_opt * W), c, d_ocard, d_oatt, d_card, d_att);
+    PT_LAUNCH_CHECK();
+    return PTCG_OK;
+}
+int pt_q_in_fwd(const GatherCtx& c, const float* h, const float* temb, float* q_in, hipStream_t s) {
+    PT_REQUIRE(c.dx.q_in % 4 == 0 && c.dm.opt_f % 4 == 0 && c.off.opt_float % 4 == 0, "q_in: widths must be multiples of 4");
+    hipLaunchKernelGGL(q_in_fwd_kernel, PT_GRID((long)c.N * c.dm.n_opt * (c.dx.q_in / 4)), c, h, temb, q_in);
+    PT_LAUNCH_CHECK();
+    return PTCG_OK;
+}
+int pt_q_in_bwd(const GatherCtx& c, const float* d_qin, float* d_h, float* d_temb, hipStream_t s) {
+    hipLaunchKernelGGL(q_in_bwd_kernel, dim3(c.N), dim3(TB), 0, s, c, d_qin, d_h, d_temb);
+    PT_LAUNCH_CHECK();
+    return PTCG_OK;
+}
+int pt_sc_in_fwd(const GatherCtx& c, const float* h, const float* gd, float* sc_in, hipStream_t s) {
+    PT_REQUIRE(c.dm.g % 4 == 0, "sc_in: g must be a multiple of 4");
+    hipLaunchKernelGGL(sc_in_fwd_kernel, PT_GRID((long)c.N * c.dm.n_opt * ((c.dx.score_in - c.dm.d) / 4)), c, h, gd, sc_in);
+    PT_LAUNCH_CHECK();
+    return PTCG_OK;
+}
+int pt_sc_in_bwd(const GatherCtx& c, const float* d_sc, const float* sc_in, float* d_q, float* d_h,
+                 float* d_gd, hipStream_t s) {
+    PT_REQUIRE(c.dm.g <= c.dm.d && PT_DEC_H <= c.dm.d, "sc_in bwd: g and the decision width must not exceed d");
+    hipLaunchKernelGGL(sc_in_bwd_kernel, dim3(c.N), dim3(TB), 0, s, c, d_sc, sc_in, d_q, d_h, d_gd);
+    PT_LAUNCH_CHECK();
+    return PTCG_OK;
+}
+int pt_val_in_fwd(const GatherCtx& c, const float* h, const float* gd, float* val_in, hipStream_t s) {
+    hipLaunchKernelGGL(val_in_fwd_kernel, PT_GRID((long)c.N * c.dx.val_in), c, h, gd, val_in);
+    PT_LAUNCH_CHECK();
+    return PTCG_OK;
+}
+int pt_val_in_bwd(const GatherCtx& c, const float* d_val_in, float* d_h, float* d_gd, hipStream_t s) {
+    hipLaunchKernelGGL(val_in_bwd_kernel, PT_GRID((long)c.N * c.dx.val_in), c, d_val_in, d_h, d_gd);
+    PT_LAUNCH_CHECK();
+    return PTCG_OK;
+}
+int pt_head_dot(const float* X, int rows, int K, const float* w, const float* b, float* out, int per,
+                long ldo, int col0, hipStream_t s) {
+    hipLaunchKernelGGL(head_dot_kernel, dim3(pt_cdiv(rows, 4)), dim3(256), 0, s, X, rows, K, w, b, out, per, ldo, col0);
+    PT_LAUNCH_CHECK();
+    return PTCG_OK;
+}
+int pt_head_dot_bwd(const float* grad, int per, long ldg, int col0, const float* w, const float* pre,
+                    float* dX, int rows, int K, hipStream_t s) {
+    hipLaunchKernelGGL(head_dot_bwd_kernel, PT_GRID((long)rows * K), grad, per, ldg, col0, w, pre, dX, rows, K);
+    PT_LAUNCH_CHECK();
+    return PTCG_OK;
+}
+int pt_head_dot_dw(const float* grad, int per, long ldg, int col0, const float* X, int rows, int K,
+                   float* dw, float* db, float* ws, long ws_floats, hipStream_t s) {
+    const int chunks = pt_cdiv(rows, HD_ROWS);
+    PT_REQUIRE(ws && (long)chunks * (K + 1) <= ws_floats, "head dw: workspace too small");
+    hipLaunchKernelGGL(head_dot_dw_partial_kernel, dim3(chunks), dim3(TB), 0, s, grad, per, ldg, col0, X, rows, K, ws);
+    PT_LAUNCH_CHECK();
+    hipLaunchKernelGGL(head_dot_dw_final_kernel, dim3(pt_cdiv(K + 1, TB)), dim3(TB), 0, s, ws, chunks, K, dw, db);
+    PT_LAUNCH_CHECK();
+    return PTCG_OK;
+}
+int pt_fill_zero(float* p, long n, hipStream_t s) {
+    if (n <= 0) return PTCG_OK;
+    if (((uintptr_t)p & 15) == 0) {
+        const long n4 = n / 4;
+        if (n4) hipLaunchKernelGGL(fill_zero_kernel, PT_GRID(n4), (float4*)p, n4);
+        if (n % 4) hipLaunchKernelGGL(fill_zero_tail_kernel, PT_GRID(n % 4), p + n4 * 4, n % 4);
+    } else {
+        hipLaunchKernelGGL(fill_zero_tail_kernel, PT_GRID(n), p, n);
+    }
+    PT_LAUNCH_CHECK();
+    return PTCG_OK;
+}

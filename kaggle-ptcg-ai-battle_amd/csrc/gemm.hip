@@ -1,0 +1,378 @@
+// fp32 GEMM on CDNA4 matrix cores (v_mfma_f32_16x16x4_f32), LDS-staged.
+//
+// Replaces the reference's cuBLAS GemmEx wrappers pt_gemm / pt_linear /
+// pt_linear_bwd / pt_bias_grad (native/model/ptcg_kernels.cuh:42-108) with
+// one templated kernel: 128x128 block tile, BK = 16, 256 threads = 4 waves
+// in a 2x2 grid, each wave a 64x64 sub-tile of 4x4 MFMA 16x16 tiles.  Both
+// operands are staged k-major in LDS (row = k, 4-float pad) so every MFMA
+// operand fetch is one conflict-free ds_read_b32 per lane; global->LDS uses
+// 128-bit loads along whichever dimension is contiguous in memory, double
+// buffered (prefetch of tile t+1 overlaps the MFMAs of tile t).  Epilogues
+// fuse bias, exact GELU (keeping the pre-activation), residual add and the
+// GELU backward multiply.  Weight gradients (K = rows, small M*N) split K
+// across blocks and sum the partials in a fixed order, so results do not
+// depend on scheduling (the reference accumulates with atomics).
+#include "common.h"
+
+#include <vector>
+
+namespace {
+
+constexpr int BM = 128, BN = 128, BK = 16, PAD = 4;
+constexpr int SA = BM + PAD, SB = BN + PAD;
+constexpr int NT = 256;
+
+template <bool AT, bool BT, int EPI, bool PARTIAL>
+__global__ __launch_bounds__(NT) void gemm_f32_kernel(GemmArgs g, int k_chunk, long part_stride) {
+    __shared__ float As[2][BK][SA];
+    __shared__ float Bs[2][BK][SB];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+    const int kbeg = blockIdx.z * k_chunk;
+    const int kend = min(g.K, kbeg + k_chunk);
+    const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
+    const int li = lane & 15, lq = lane >> 4;
+
+    floatx4 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+    float4 ra[2], rb[2];
+    const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
+
+    auto gload = [&](int k0) {
+#pragma unroll
+        for (int it = 0; it < 2; ++it) {
+            const int idx = tid + it * NT;
+            if (!AT) {
+                const int row = idx >> 2, kq = idx & 3;
+                const int gm = m0 + row, gk = k0 + kq * 4;
+                ra[it] = (gm < g.M && gk < kend)
+                             ? *reinterpret_cast<const float4*>(g.A + (long)gm * g.lda + gk) : z4;
+            } else {
+                const int kr = idx >> 5, mq = idx & 31;
+                const int gk = k0 + kr, gm = m0 + mq * 4;
+                ra[it] = (gk < kend && gm < g.M)
+                             ? *reinterpret_cast<const float4*>(g.A + (long)gk * g.lda + gm) : z4;
+            }
+            if (!BT) {
+                const int row = idx >> 2, kq = idx & 3;
+                const int gn = n0 + row, gk = k0 + kq * 4;
+                rb[it] = (gn < g.N && gk < kend)
+                             ? *reinterpret_cast<const float4*>(g.B + (long)gn * g.ldb + gk) : z4;
+            } else {
+                const int kr = idx >> 5, nq = idx & 31;
+                const int gk = k0 + kr, gn = n0 + nq * 4;
+                rb[it] = (gk < kend && gn < g.N)
+                             ? *reinterpret_cast<const float4*>(g.B + (long)gk * g.ldb + gn) : z4;
+            }
+        }
+    };
+    auto sstore = [&](int buf) {
+#pragma unroll
+        for (int it = 0; it < 2; ++it) {
+            const int idx = tid + it * NT;
+            if (!AT) {
+                const int row = idx >> 2, kq = idx & 3;
+                As[buf][kq * 4 + 0][row] = ra[it].x;
+                As[buf][kq * 4 + 1][row] = ra[it].y;
+                As[buf][kq * 4 + 2][row] = ra[it].z;
+                As[buf][kq * 4 + 3][row] = ra[it].w;
+            } else {
+                const int kr = idx >> 5, mq = idx & 31;
+                *reinterpret_cast<float4*>(&As[buf][kr][mq * 4]) = ra[it];
+            }
+            if (!BT) {
+                const int row = idx >> 2, kq = idx & 3;
+                Bs[buf][kq * 4 + 0][row] = rb[it].x;
+                Bs[buf][kq * 4 + 1][row] = rb[it].y;
+                Bs[buf][kq * 4 + 2][row] = rb[it].z;
+                Bs[buf][kq * 4 + 3][row] = rb[it].w;
+            } else {
+                const int kr = idx >> 5, nq = idx & 31;
+                *reinterpret_cast<float4*>(&Bs[buf][kr][nq * 4]) = rb[it];
+            }
+        }
+    };
+
+    if (kbeg < kend) {
+        gload(kbeg);
+        sstore(0);
+        __syncthreads();
+        int buf = 0;
+        for (int k0 = kbeg; k0 < kend; k0 += BK) {
+            const bool more = k0 + BK < kend;
+            if (more) gload(k0 + BK);
+#pragma unroll
+            for (int kk = 0; kk < BK / 4; ++kk) {
+                float a[4], b[4];
+#pragma unroll
+                for (int t = 0; t < 4; ++t) a[t] = As[buf][kk * 4 + lq][wm + t * 16 + li];
+#pragma unroll
+                for (int t = 0; t < 4; ++t) b[t] = Bs[buf][kk * 4 + lq][wn + t * 16 + li];
+#pragma unroll
+                for (int ti = 0; ti < 4; ++ti)
+#pragma unroll
+                    for (int tj = 0; tj < 4; ++tj)
+                        acc[ti][tj] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[ti], b[tj], acc[ti][tj], 0, 0, 0);
+            }
+            if (more) sstore(buf ^ 1);
+            __syncthreads();
+            buf ^= 1;
+        }
+    }
+
+    // epilogue: acc[ti][tj][r] = C[wm + ti*16 + 4*lq + r][wn + tj*16 + li]
+#pragma unroll
+    for (int ti = 0; ti < 4; ++ti)
+#pragma unroll
+        for (int tj = 0; tj < 4; ++tj) {
+            const int n = n0 + wn + tj * 16 + li;
+            if (n >= g.N) continue;
+            float bn = 0.f;
+            if (!PARTIAL && (EPI == EPI_BIAS || EPI == EPI_BIAS_GELU || EPI == EPI_BIAS_RESID))
+                bn = g.bias[n];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int m = m0 + wm + ti * 16 + lq * 4 + r;
+                if (m >= g.M) continue;
+                float v = acc[ti][tj][r];
+                if (PARTIAL) {
+                    g.C[(long)blockIdx.z * part_stride + (long)m * g.ldc + n] = v;
+                } else if (EPI == EPI_STORE) {
+                    g.C[(long)m * g.ldc + n] = v;
+                } else if (EPI == EPI_BIAS) {
+                    g.C[(long)m * g.ldc + n] = v + bn;
+                } else if (EPI == EPI_BIAS_GELU) {
+                    v += bn;
+                    g.C[(long)m * g.ldc + n] = v;
+                    g.C2[(long)m * g.ldc2 + n] = pt_gelu(v);
+                } else if (EPI == EPI_BIAS_RESID) {
+                    g.C[(long)m * g.ldc + n] = v + bn + g.R[(long)m * g.ldr + n];
+                } else if (EPI == EPI_GELU_BWD) {
+                    g.C[(long)m * g.ldc + n] = v * pt_gelu_grad(g.R[(long)m * g.ldr + n]);
+                } else if (EPI == EPI_ACCUM) {
+                    g.C[(long)m * g.ldc + n] += v;
+                }
+            }
+        }
+}
+
+// out[m][n] (=|+=) sum_s part[s][m][n], fixed order over s
+template <bool ACCUM>
+__global__ void splitk_reduce_kernel(float* C, long ldc, const float* part, long part_stride,
+                                     int splits, int M, int N) {
+    long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (long)M * N) return;
+    int m = (int)(i / N), n = (int)(i % N);
+    long o = (long)m * ldc + n;
+    float s = 0.f;
+    for (int k = 0; k < splits; ++k) s += part[(long)k * part_stride + o];
+    if (ACCUM) C[o] += s; else C[o] = s;
+}
+
+// partial column sums: block (64 cols x 4 row groups) over a chunk of rows
+constexpr int CS_ROWS = 256;
+__global__ void colsum_partial_kernel(const float* X, long ldx, int M, int N, float* part) {
+    __shared__ float sh[4][64];
+    int c = blockIdx.x * 64 + (threadIdx.x & 63);
+    int rg = threadIdx.x >> 6;
+    int r0 = blockIdx.y * CS_ROWS, r1 = min(M, r0 + CS_ROWS);
+    float s = 0.f;
+    if (c < N)
+        for (int r = r0 + rg; r < r1; r += 4) s += X[(long)r * ldx + c];
+    sh[rg][threadIdx.x & 63] = s;
+    __syncthreads();
+    if (rg == 0 && c < N)
+        part[(long)blockIdx.y * N + c] = sh[0][threadIdx.x] + sh[1][threadIdx.x] +
+                                         sh[2][threadIdx.x] + sh[3][threadIdx.x];
+}
+
+__global__ void colsum_final_kernel(const float* part, int chunks, int N, float* out) {
+    int c = blockIdx.x * blockDim.x + threadIdx.x;
+    if (c >= N) return;
+    float s = 0.f;
+    for (int k = 0; k < chunks; ++k) s += part[(long)k * N + c];
+    out[c] = s;
+}
+
+// Optional launch timing (ptcg_profile_*): a HIP event pair around every
+// GEMM kernel launch, recorded on the launch's own stream.
+struct GemmProf {
+    bool on = false;
+    int used = 0;
+    std::vector<hipEvent_t> ev;
+    std::vector<double> flops;
+};
+GemmProf g_prof;
+
+template <bool AT, bool BT, int EPI, bool PARTIAL>
+void launch(const GemmArgs& g, dim3 grid, int k_chunk, long part_stride, hipStream_t s) {
+    const bool rec = g_prof.on && g_prof.used * 2 + 1 < (int)g_prof.ev.size();
+    if (rec) (void)hipEventRecord(g_prof.ev[2 * g_prof.used], s);
+    hipLaunchKernelGGL((gemm_f32_kernel<AT, BT, EPI, PARTIAL>), grid, dim3(NT), 0, s, g, k_chunk,
+                       part_stride);
+    if (rec) {
+        (void)hipEventRecord(g_prof.ev[2 * g_prof.used + 1], s);
+        g_prof.flops[g_prof.used] = 2.0 * g.M * (double)g.N * g.K;
+        g_prof.used++;
+    }
+}
+
+}  // namespace
+
+extern "C" int ptcg_profile_begin(int max_launches) {
+    PT_REQUIRE(max_launches > 0, "profile_begin: max_launches must be positive");
+    for (auto e : g_prof.ev) (void)hipEventDestroy(e);
+    g_prof.ev.assign(2 * (size_t)max_launches, nullptr);
+    for (auto& e : g_prof.ev) PT_HIP(hipEventCreate(&e));
+    g_prof.flops.assign(max_launches, 0.0);
+    g_prof.used = 0;
+    g_prof.on = true;
+    return PTCG_OK;
+}
+
+extern "C" int ptcg_profile_end(double* total_ms, int* launches, double* flops) {
+    g_prof.on = false;
+    double ms = 0.0, fl = 0.0;
+    for (int i = 0; i < g_prof.used; ++i) {
+        PT_HIP(hipEventSynchronize(g_prof.ev[2 * i + 1]));
+        float t = 0.f;
+        PT_HIP(hipEventElapsedTime(&t, g_prof.ev[2 * i], g_prof.ev[2 * i + 1]));
+        ms += t;
+        fl += g_prof.flops[i];
+    }
+    if (total_ms) *total_ms = ms;
+    if (launches) *launches = g_prof.used;
+    if (flops) *flops = fl;
+    for (auto e : g_prof.ev) (void)hipEventDestroy(e);
+    g_prof.ev.clear();
+    g_prof.used = 0;
+    return PTCG_OK;
+}
+
+int pt_gemm(const GemmArgs& g, float* ws, long ws_floats, hipStream_t s) {
+    PT_REQUIRE(g.M > 0 && g.N > 0 && g.K > 0, "gemm: empty shape %d x %d x %d", g.M, g.N, g.K);
+    PT_REQUIRE(g.a_t ? (g.M % 4 == 0) : (g.K % 4 == 0), "gemm: A operand not float4-able (M=%d K=%d a_t=%d)", g.M, g.K, g.a_t);
+    PT_REQUIRE(g.b_t ? (g.N % 4 == 0) : (g.K % 4 == 0), "gemm: B operand not float4-able (N=%d K=%d b_t=%d)", g.N, g.K, g.b_t);
+    PT_REQUIRE(g.lda % 4 == 0 && g.ldb % 4 == 0, "gemm: leading dims must be multiples of 4");
+    PT_REQUIRE(((uintptr_t)g.A & 15) == 0 && ((uintptr_t)g.B & 15) == 0, "gemm: operands must be 16 B aligned");
+    const int tm = pt_cdiv(g.M, BM), tn = pt_cdiv(g.N, BN);
+    const int tiles = tm * tn;
+    // split K when the output is too small to fill the chip and K is long
+    int splits = 1;
+    const int target = 512;
+    if (tiles < target && g.K >= 4 * BK * 16) {
+        splits = pt_cdiv(target, tiles);
+        int max_splits = g.K / (BK * 16);
+        if (splits > max_splits) splits = max_splits;
+        if (splits < 1) splits = 1;
+    }
+    if (splits > 1 && !(g.epi == EPI_STORE || g.epi == EPI_ACCUM)) splits = 1;
+    long part_stride = (long)g.M * g.ldc;
+    if (splits > 1 && (ws == nullptr || (long)splits * part_stride > ws_floats)) {
+        long fit = ws ? ws_floats / part_stride : 0;
+        splits = fit > 1 ? (int)fit : 1;
+    }
+    int k_chunk = g.K;
+    if (splits > 1) {
+        k_chunk = pt_cdiv(pt_cdiv(g.K, splits), BK) * BK;
+        splits = pt_cdiv(g.K, k_chunk);
+    }
+    dim3 grid(tn, tm, splits);
+    const int code = (g.a_t ? 1 : 0) * 2 + (g.b_t ? 1 : 0);
+    if (splits > 1) {
+        GemmArgs p = g;
+        p.C = ws;
+        if (code == 3) launch<true, true, EPI_STORE, true>(p, grid, k_chunk, part_stride, s);
+        else if (code == 1) launch<false, true, EPI_STORE, true>(p, grid, k_chunk, part_stride, s);
+        else if (code == 0) launch<false, false, EPI_STORE, true>(p, grid, k_chunk, part_stride, s);
+        else launch<true, false, EPI_STORE, true>(p, grid, k_chunk, part_stride, s);
+        PT_LAUNCH_CHECK();
+        long tot = (long)g.M * g.N;
+        if (g.epi == EPI_ACCUM)
+            hipLaunchKernelGGL(splitk_reduce_kernel<true>, dim3(pt_cdiv(tot, 256)), dim3(256), 0, s,
+                               g.C, g.ldc, ws, part_stride, splits, g.M, g.N);
+        else
+            hipLaunchKernelGGL(splitk_reduce_kernel<false>, dim3(pt_cdiv(tot, 256)), dim3(256), 0, s,
+                               g.C, g.ldc, ws, part_stride, splits, g.M, g.N);
+        PT_LAUNCH_CHECK();
+        return PTCG_OK;
+    }
+#define PT_EPI_CASES(AT, BT)                                                                   \
+    switch (g.epi) {                                                                           \
+        case EPI_STORE: launch<AT, BT, EPI_STORE, false>(g, grid, k_chunk, 0, s); break;       \
+        case EPI_BIAS: launch<AT, BT, EPI_BIAS, false>(g, grid, k_chunk, 0, s); break;         \
+        case EPI_BIAS_GELU: launch<AT, BT, EPI_BIAS_GELU, false>(g, grid, k_chunk, 0, s); break; \
+        case EPI_BIAS_RESID: launch<AT, BT, EPI_BIAS_RESID, false>(g, grid, k_chunk, 0, s); break; \
+        case EPI_GELU_BWD: launch<AT, BT, EPI_GELU_BWD, false>(g, grid, k_chunk, 0, s); break; \
+        case EPI_ACCUM: launch<AT, BT, EPI_ACCUM, false>(g, grid, k_chunk, 0, s); break;       \
+        default: PT_REQUIRE(false, "gemm: bad epilogue %d", g.epi);                            \
+    }
+    if (code == 0) {
+        PT_EPI_CASES(false, false)
+    } else if (code == 1) {
+        PT_EPI_CASES(false, true)
+    } else if (code == 3) {
+        PT_EPI_CASES(true, true)
+    } else {
+        PT_EPI_CASES(true, false)
+    }
+#undef PT_EPI_CASES
+    PT_LAUNCH_CHECK();
+    return PTCG_OK;
+}
+
+int pt_linear_fwd(const float* X, const float* W, const float* b, float* Y, int rows, int in,
+                  int out, int epi, const float* R, float* Y2, hipStream_t s) {
+    GemmArgs g{};
+    g.M = rows; g.N = out; g.K = in;
+    g.A = X; g.lda = in; g.a_t = 0;
+    g.B = W; g.ldb = in; g.b_t = 0;
+    g.C = Y; g.ldc = out;
+    g.bias = b; g.R = R; g.ldr = out; g.C2 = Y2; g.ldc2 = out;
+    g.epi = epi;
+    if ((epi == EPI_BIAS || epi == EPI_BIAS_GELU || epi == EPI_BIAS_RESID) && b == nullptr)
+        g.epi = (epi == EPI_BIAS) ? EPI_STORE : epi;
+    PT_REQUIRE(!(g.epi == EPI_BIAS_GELU || g.epi == EPI_BIAS_RESID) || b != nullptr,
+               "linear_fwd: epilogue %d needs a bias", epi);
+    return pt_gemm(g, nullptr, 0, s);
+}
+
+int pt_linear_dx(const float* dY, const float* W, float* dX, int rows, int in, int out, int epi,
+                 const float* R, hipStream_t s) {
+    GemmArgs g{};
+    g.M = rows; g.N = in; g.K = out;
+    g.A = dY; g.lda = out; g.a_t = 0;
+    g.B = W; g.ldb = in; g.b_t = 1;
+    g.C = dX; g.ldc = in;
+    g.R = R; g.ldr = in;
+    g.epi = epi;
+    return pt_gemm(g, nullptr, 0, s);
+}
+
+int pt_linear_dw(const float* dY, const float* X, float* dW, float* db, int rows, int in, int out,
+                 float* ws, long ws_floats, hipStream_t s) {
+    GemmArgs g{};
+    g.M = out; g.N = in; g.K = rows;
+    g.A = dY; g.lda = out; g.a_t = 1;
+    g.B = X; g.ldb = in; g.b_t = 1;
+    g.C = dW; g.ldc = in;
+    g.epi = EPI_STORE;
+    PT_TRY(pt_gemm(g, ws, ws_floats, s));
+    if (db) PT_TRY(pt_colsum(dY, out, rows, out, db, ws, ws_floats, s));
+    return PTCG_OK;
+}
+
+int pt_colsum(const float* X, long ldx, int M, int N, float* out, float* ws, long ws_floats,
+              hipStream_t s) {
+    int chunks = pt_cdiv(M, CS_ROWS);
+    PT_REQUIRE(ws != nullptr && (long)chunks * N <= ws_floats, "colsum: workspace too small (%d x %d)", chunks, N);
+    hipLaunchKernelGGL(colsum_partial_kernel, dim3(pt_cdiv(N, 64), chunks), dim3(256), 0, s, X, ldx, M, N, ws);
+    PT_LAUNCH_CHECK();
+    hipLaunchKernelGGL(colsum_final_kernel, dim3(pt_cdiv(N, 256)), dim3(256), 0, s, ws, chunks, N, out);
+    PT_LAUNCH_CHECK();
+    return PTCG_OK;
+}

@@ -1,0 +1,57 @@
+// extern "C" wrappers of the individual kernels (include/ptcg_amd_kernels.h).
+#include "model.h"
+#include "../../include/ptcg_amd_kernels.h"
+
+extern "C" int ptcg_kernel_gemm(int M, int N, int K, const float* A, int64_t lda, int a_t,
+                                const float* B, int64_t ldb, int b_t, float* C, int64_t ldc,
+                                int epi, const float* bias, const float* R, int64_t ldr, float* C2,
+                                int64_t ldc2, float* workspace, int64_t workspace_floats,
+                                void* stream) {
+    PT_REQUIRE(A && B && C, "kernel_gemm: null operand");
+    PT_REQUIRE(epi >= EPI_STORE && epi <= EPI_ACCUM, "kernel_gemm: bad epilogue %d", epi);
+    PT_REQUIRE(!((epi == EPI_BIAS || epi == EPI_BIAS_GELU || epi == EPI_BIAS_RESID) && !bias),
+               "kernel_gemm: epilogue %d needs bias", epi);
+    PT_REQUIRE(!((epi == EPI_BIAS_RESID || epi == EPI_GELU_BWD) && !R), "kernel_gemm: epilogue %d needs R", epi);
+    PT_REQUIRE(!(epi == EPI_BIAS_GELU && !C2), "kernel_gemm: epilogue 2 needs C2");
+    GemmArgs g{};
+    g.M = M; g.N = N; g.K = K;
+    g.A = A; g.lda = lda; g.a_t = a_t;
+    g.B = B; g.ldb = ldb; g.b_t = b_t;
+    g.C = C; g.ldc = ldc; g.epi = epi;
+    g.bias = bias; g.R = R; g.ldr = ldr; g.C2 = C2; g.ldc2 = ldc2;
+    return pt_gemm(g, workspace, workspace_floats, (hipStream_t)stream);
+}
+
+extern "C" int ptcg_kernel_colsum(const float* X, int64_t ldx, int M, int N, float* out,
+                                  float* workspace, int64_t workspace_floats, void* stream) {
+    PT_REQUIRE(X && out, "kernel_colsum: null buffer");
+    return pt_colsum(X, ldx, M, N, out, workspace, workspace_floats, (hipStream_t)stream);
+}
+
+extern "C" int ptcg_kernel_layernorm_fwd(const float* x, const float* w, const float* b, float* y,
+                                         float* mean, float* rstd, int rows, int D, void* stream) {
+    PT_REQUIRE(x && w && b && y && mean && rstd, "kernel_layernorm_fwd: null buffer");
+    return pt_ln_fwd(x, D, w, b, y, D, mean, rstd, rows, D, (hipStream_t)stream);
+}
+
+extern "C" int ptcg_kernel_layernorm_bwd(const float* dy, const float* x, const float* w,
+                                         const float* mean, const float* rstd, const float* dres,
+                                         float* dx, float* dw, float* db, int rows, int D,
+                                         float* workspace, int64_t workspace_floats, void* stream) {
+    PT_REQUIRE(dy && x && w && mean && rstd && dx, "kernel_layernorm_bwd: null buffer");
+    return pt_ln_bwd(dy, D, x, D, w, mean, rstd, dres, D, dx, D, dw, db, rows, D, workspace,
+                     workspace_floats, (hipStream_t)stream);
+}
+
+extern "C" int ptcg_kernel_attention_fwd(const float* qkv, const float* keep, float* ctx, float* lse,
+                                         int N, int L, int H, int Dh, void* stream) {
+    PT_REQUIRE(qkv && keep && ctx && lse, "kernel_attention_fwd: null buffer");
+    return pt_attn_fwd(qkv, keep, ctx, lse, N, L, H, Dh, (hipStream_t)stream);
+}
+
+extern "C" int ptcg_kernel_attention_bwd(const float* qkv, const float* keep, const float* ctx,
+                                         const float* lse, const float* dctx, float* dqkv, int N,
+                                         int L, int H, int Dh, void* stream) {
+    PT_REQUIRE(qkv && keep && ctx && lse && dctx && dqkv, "kernel_attention_bwd: null buffer");
+    return pt_attn_bwd(qkv, keep, ctx, lse, dctx, dqkv, N, L, H, Dh, (hipStream_t)stream);
+}

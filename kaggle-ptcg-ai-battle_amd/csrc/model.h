@@ -1,0 +1,89 @@
+// Internal interface between the model driver (model.hip) and its kernels.
+#pragma once
+#include "common.h"
+
+// Section offsets of one obs row (ptcg/rl/buffers.py:212-227).
+struct ObsOff {
+    int tok_int, tok_float, opt_int, opt_float, opt_mask, global_f, dec_int, dec_float, oracle, size;
+};
+ObsOff pt_obs_offsets(const PtcgDims& d);
+
+// Width constants of the reference model (ptcg/rl/model.py:114-175).
+enum {
+    PT_OPT_E = 64, PT_TYPE_E = 16, PT_SC_H = 256, PT_VAL_H = 256, PT_DEC_H = 64,
+    PT_ZONE_E = 8, PT_OWNER_E = 4, PT_SEL_E = 8, PT_CTX_E = 32,
+};
+
+struct DimsX {   // derived widths
+    int l_seq, dh, tok_in, dec_in, bcast_in, q_in, score_in, val_in;
+};
+DimsX pt_dims_x(const PtcgDims& d);
+
+// canonical weight table
+struct ParamDef { const char* name; long rows, cols; };
+int pt_param_table(const PtcgDims& d, ParamDef* out, int cap);   // returns count or <0
+
+// kernels (layernorm.hip, attention.hip, ppo.hip, adam.hip, gather.hip)
+int pt_ln_fwd(const float* x, long ldx, const float* w, const float* b, float* y, long ldy,
+              float* mean, float* rstd, int rows, int D, hipStream_t s);
+int pt_ln_bwd(const float* dy, long lddy, const float* x, long ldx, const float* w,
+              const float* mean, const float* rstd, const float* dres, long ldres, float* dx,
+              long lddx, float* dw, float* db, int rows, int D, float* ws, long ws_floats,
+              hipStream_t s);
+int pt_attn_supported(int L, int DH);
+int pt_attn_fwd(const float* qkv, const float* keep, float* ctx, float* lse, int N, int L, int H,
+                int DH, hipStream_t s);
+int pt_attn_bwd(const float* qkv, const float* keep, const float* ctx, const float* lse,
+                const float* dctx, float* dqkv, int N, int L, int H, int DH, hipStream_t s);
+long pt_ppo_partial_floats(int n);
+int pt_ppo_loss(const float* out, int n, int A, const float* mask, long mask_stride,
+                const int32_t* idx, const float* actions, const float* old_logp,
+                const float* adv, const float* ret, const float* val, const float* prio,
+                float clip, float vf_clip, float vf_coef, float ent_coef, float* grad,
+                float* ratio, float* newvalue, float* stats, float* guard, float* partial,
+                hipStream_t s);
+int pt_kl_gate(const float* guard, float kl_thr, float vf_thr, float* gate, float* skipped,
+               hipStream_t s);
+long pt_adam_ws_floats();
+int pt_adam_step(float* w, float* g, float* m, float* v, long n, float lr, float b1, float b2,
+                 float eps, float max_norm, const float* gate, int32_t* step, float* norm_out,
+                 float* ws, hipStream_t s);
+
+// ---- gathers / scatters of the token, decision and option paths (gather.hip)
+struct GatherCtx {
+    const float* obs; const int32_t* idx; long stride; int N;
+    PtcgDims dm; DimsX dx; ObsOff off;
+};
+int pt_tok_cat_fwd(const GatherCtx& c, const float* card, const float* zemb, const float* oemb,
+                   float* tok_cat, hipStream_t s);
+int pt_tok_cat_bwd(const GatherCtx& c, const float* d_cat, float* d_card, float* d_zemb,
+                   float* d_oemb, hipStream_t s);
+int pt_glob_in(const GatherCtx& c, float* glob_in, hipStream_t s);
+int pt_dec_in_fwd(const GatherCtx& c, const float* card, const float* att, const float* semb,
+                  const float* cemb, float* dec_in, hipStream_t s);
+int pt_dec_in_bwd(const GatherCtx& c, const float* d_in, float* d_card, float* d_att,
+                  float* d_semb, float* d_cemb, hipStream_t s);
+int pt_x0_fwd(const GatherCtx& c, const float* tokp, const float* bc, const float* readout,
+              float* x0, float* keep, hipStream_t s);
+int pt_x0_bwd(const GatherCtx& c, const float* d_x0, float* d_tokp, float* d_bc, hipStream_t s);
+int pt_opt_gather_fwd(const GatherCtx& c, const float* card, const float* att, float* ocard,
+                      float* oatt, hipStream_t s);
+int pt_opt_gather_bwd(const GatherCtx& c, const float* d_ocard, const float* d_oatt,
+                      float* d_card, float* d_att, hipStream_t s);
+int pt_q_in_fwd(const GatherCtx& c, const float* h, const float* temb, float* q_in, hipStream_t s);
+int pt_q_in_bwd(const GatherCtx& c, const float* d_qin, float* d_h, float* d_temb, hipStream_t s);
+int pt_sc_in_fwd(const GatherCtx& c, const float* h, const float* gd, float* sc_in, hipStream_t s);
+int pt_sc_in_bwd(const GatherCtx& c, const float* d_sc, const float* sc_in, float* d_q,
+                 float* d_h, float* d_gd, hipStream_t s);
+int pt_val_in_fwd(const GatherCtx& c, const float* h, const float* gd, float* val_in, hipStream_t s);
+int pt_val_in_bwd(const GatherCtx& c, const float* d_val_in, float* d_h, float* d_gd, hipStream_t s);
+// y[r] = X[r,:] . w + b, written to out[r / per * ldo + col0 + r % per]
+int pt_head_dot(const float* X, int rows, int K, const float* w, const float* b, float* out,
+                int per, long ldo, int col0, hipStream_t s);
+// dX[r,:] = dy[r] * w[:] * gelu'(pre[r,:]),  dy[r] = grad[r / per * ldg + col0 + r % per]
+int pt_head_dot_bwd(const float* grad, int per, long ldg, int col0, const float* w,
+                    const float* pre, float* dX, int rows, int K, hipStream_t s);
+// dw[k] = sum_r dy[r] X[r,k]; db = sum_r dy[r]   (fixed order)
+int pt_head_dot_dw(const float* grad, int per, long ldg, int col0, const float* X, int rows, int K,
+                   float* dw, float* db, float* ws, long ws_floats, hipStream_t s);
+int pt_fill_zero(float* p, long n, hipStream_t s);

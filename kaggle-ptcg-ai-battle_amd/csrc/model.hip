@@ -1,0 +1,432 @@
+// Model driver: weight binding, activation arena, forward and backward.
+//
+// Mirrors the reference's PTCG Encoder plugin (native/model/ptcg_model3.cu
+// ptcg_forward_core :246-369, blk_fwd :12-40, blk_bwd :44-95;
+// ptcg_model4.cu ptcg_backward_core :10-190) for the learned-table /
+// blind-critic model, with a different kernel plan:
+//   * GEMM epilogues carry bias, GELU (pre-activation kept), residual add
+//     and GELU-backward, so there are no separate bias / gelu / add kernels;
+//   * attention is one fused kernel per direction (no (N,H,L,L) tensor);
+//   * concat inputs are written in place by the producing GEMMs (leading
+//     dimension = concat width) — g/dvec into the bcast input, opt_card /
+//     opt_attack into q_in, q into the score input;
+//   * every activation the backward needs is kept (LayerNorm outputs, qkv,
+//     attention context, GELU pre- and post-activations), so the backward
+//     recomputes nothing but the attention probabilities.
+// Grads are overwritten on every backward (ptcg_model4.cu:15-21).
+#include "model.h"
+
+#include <map>
+#include <string>
+#include <vector>
+
+struct BlockP {
+    float *ln1w, *ln1b, *qkvw, *qkvb, *projw, *projb, *ln2w, *ln2b, *f1w, *f1b, *f2w, *f2b;
+};
+struct BlockA {
+    float *ln1, *mu1, *rs1, *qkv, *ctx, *lse, *xmid, *ln2, *mu2, *rs2, *ffp, *ffa;
+};
+
+struct PtcgModel {
+    PtcgDims dm;
+    DimsX dx;
+    ObsOff off;
+    std::vector<ParamDef> defs;
+    std::vector<long> offs;
+    long arena = 0;
+    float* P = nullptr;
+    float* Gr = nullptr;
+    float *card, *att, *zemb, *oemb, *tp_w, *tp_b, *readout, *g1_w, *g1_b, *g2_w, *g2_b, *semb,
+        *cemb, *d1_w, *d1_b, *d2_w, *d2_b, *bc_w, *bc_b;
+    std::vector<BlockP> blk;
+    float *lnf_w, *lnf_b, *temb, *oc_w, *oc_b, *oa_w, *oa_b, *q1_w, *q1_b, *q2_w, *q2_b, *s1_w,
+        *s1_b, *s2_w, *s2_b, *v1_w, *v1_b, *v2_w, *v2_b;
+    // activations
+    int N = 0;
+    char* mem = nullptr;
+    size_t mem_bytes = 0;
+    float *tok_cat, *tokp, *glob_in, *g1, *g1a, *dec_in, *d1, *d1a, *gd, *bc, *keep;
+    std::vector<float*> x;
+    std::vector<BlockA> ba;
+    float *h, *lnf_mu, *lnf_rs;
+    float *ocard, *oatt, *q_in, *q1, *q1a, *sc_in, *s1, *s1a, *val_in, *v1, *v1a, *out;
+    float *dxa, *dxb, *dffn, *dln, *dqkv, *dctx, *dsc, *ds1, *dq, *dq1, *dqin, *docard, *doatt,
+        *dvin, *dv1, *dgd, *dd1, *dg1, *ddec, *dtokp, *dtokcat, *dbc;
+    float* ws = nullptr;
+    long ws_floats = 0;
+    const float* obs = nullptr;
+    const int32_t* idx = nullptr;
+
+    float* G(const float* p) const { return Gr + (p - P); }
+};
+
+// ------------------------------------------------------------ helpers
+static int lin(const float* X, long ldx, const float* W, const float* b, float* Y, long ldy,
+               int rows, int in, int out, int epi, const float* R, long ldr, float* Y2, long ldy2,
+               hipStream_t s) {
+    GemmArgs g{};
+    g.M = rows; g.N = out; g.K = in;
+    g.A = X; g.lda = ldx; g.a_t = 0;
+    g.B = W; g.ldb = in; g.b_t = 0;
+    g.C = Y; g.ldc = ldy;
+    g.bias = b; g.R = R; g.ldr = ldr; g.C2 = Y2; g.ldc2 = ldy2;
+    g.epi = epi;
+    return pt_gemm(g, nullptr, 0, s);
+}
+static int linf(const float* X, const float* W, const float* b, float* Y, int rows, int in,
+                int out, int epi, const float* R, float* Y2, hipStream_t s) {
+    return lin(X, in, W, b, Y, out, rows, in, out, epi, R, out, Y2, out, s);
+}
+// dX = dY W : dY (rows, out) ld lddy ; W (out, in) ; dX (rows, in) ld lddx
+static int ldx_(const float* dY, long lddy, const float* W, float* dX, long lddx, int rows, int in,
+                int out, int epi, const float* R, long ldr, hipStream_t s) {
+    GemmArgs g{};
+    g.M = rows; g.N = in; g.K = out;
+    g.A = dY; g.lda = lddy; g.a_t = 0;
+    g.B = W; g.ldb = in; g.b_t = 1;
+    g.C = dX; g.ldc = lddx;
+    g.R = R; g.ldr = ldr;
+    g.epi = epi;
+    return pt_gemm(g, nullptr, 0, s);
+}
+// dW = dY^T X (overwrite), db = colsum dY
+static int ldw_(PtcgModel* m, const float* dY, long lddy, const float* X, long ldxx, float* dW,
+                float* db, int rows, int in, int out, hipStream_t s) {
+    GemmArgs g{};
+    g.M = out; g.N = in; g.K = rows;
+    g.A = dY; g.lda = lddy; g.a_t = 1;
+    g.B = X; g.ldb = ldxx; g.b_t = 1;
+    g.C = dW; g.ldc = in;
+    g.epi = EPI_STORE;
+    PT_TRY(pt_gemm(g, m->ws, m->ws_floats, s));
+    if (db) PT_TRY(pt_colsum(dY, lddy, rows, out, db, m->ws, m->ws_floats, s));
+    return PTCG_OK;
+}
+
+// ------------------------------------------------------------ lifecycle
+extern "C" int ptcg_model_create(const PtcgDims* dims, PtcgModel** out) {
+    PT_REQUIRE(dims && out, "model_create: null argument");
+    PtcgDims d = *dims;
+    PT_REQUIRE(d.tables == 0 && d.critic == 0,
+               "model_create: only the learned-table / blind-critic model is implemented "
+               "(tables=%d critic=%d)", d.tables, d.critic);
+    PT_REQUIRE(d.d % d.heads == 0, "model_create: d=%d not divisible by heads=%d", d.d, d.heads);
+    PT_REQUIRE(d.n_opt <= 64, "model_create: n_opt=%d > 64 unsupported", d.n_opt);
+    PT_REQUIRE(d.d % 4 == 0 && d.d_c % 4 == 0 && d.d_a % 4 == 0 && d.g % 4 == 0 && d.ffn % 4 == 0 &&
+               d.tok_f % 4 == 0 && d.opt_f % 4 == 0 && d.global_f % 4 == 0,
+               "model_create: widths must be multiples of 4");
+    PT_REQUIRE(pt_attn_supported(d.l_tok + 1, d.d / d.heads),
+               "model_create: attention shape L=%d Dh=%d unsupported", d.l_tok + 1, d.d / d.heads);
+    PT_REQUIRE(d.g <= d.d && PT_DEC_H <= d.d, "model_create: g and decision width must not exceed d");
+    PtcgModel* m = new PtcgModel();
+    m->dm = d;
+    m->dx = pt_dims_x(d);
+    m->off = pt_obs_offsets(d);
+    ParamDef tmp[256];
+    int np = pt_param_table(d, tmp, 256);
+    if (np < 0) { delete m; return PTCG_ERR_ARG; }
+    m->defs.assign(tmp, tmp + np);
+    long off = 0;
+    for (auto& p : m->defs) {
+        off = (off + 3) & ~3L;
+        m->offs.push_back(off);
+        off += p.rows * (p.cols > 0 ? p.cols : 1);
+    }
+    m->arena = (off + 3) & ~3L;
+    *out = m;
+    return PTCG_OK;
+}
+
+long pt_model_arena(const PtcgModel* m) { return m->arena; }
+
+extern "C" int ptcg_model_bind(PtcgModel* m, float* params, float* grads) {
+    PT_REQUIRE(m && params && grads, "model_bind: null argument");
+    PT_REQUIRE(((uintptr_t)params & 15) == 0 && ((uintptr_t)grads & 15) == 0,
+               "model_bind: arenas must be 16 B aligned");
+    m->P = params;
+    m->Gr = grads;
+    std::map<std::string, float*> byname;
+    for (size_t i = 0; i < m->defs.size(); ++i) byname[m->defs[i].name] = params + m->offs[i];
+    auto get = [&](const std::string& n) -> float* {
+        auto it = byname.find(n);
+        return it == byname.end() ? nullptr : it->second;
+    };
+    m->card = get("card_table"); m->att = get("attack_table");
+    m->zemb = get("zone_emb.weight"); m->oemb = get("owner_emb.weight");
+    m->tp_w = get("token_proj.weight"); m->tp_b = get("token_proj.bias");
+    m->readout = get("readout");
+    m->g1_w = get("global_mlp.0.weight"); m->g1_b = get("global_mlp.0.bias");
+    m->g2_w = get("global_mlp.2.weight"); m->g2_b = get("global_mlp.2.bias");
+    m->semb = get("sel_type_emb.weight"); m->cemb = get("ctx_emb.weight");
+    m->d1_w = get("dec_mlp.0.weight"); m->d1_b = get("dec_mlp.0.bias");
+    m->d2_w = get("dec_mlp.2.weight"); m->d2_b = get("dec_mlp.2.bias");
+    m->bc_w = get("bcast.weight"); m->bc_b = get("bcast.bias");
+    m->blk.resize(m->dm.layers);
+    for (int i = 0; i < m->dm.layers; ++i) {
+        std::string p = "blocks." + std::to_string(i) + ".";
+        BlockP& b = m->blk[i];
+        b.ln1w = get(p + "ln1.weight"); b.ln1b = get(p + "ln1.bias");
+        b.qkvw = get(p + "qkv.weight"); b.qkvb = get(p + "qkv.bias");
+        b.projw = get(p + "proj.weight"); b.projb = get(p + "proj.bias");
+        b.ln2w = get(p + "ln2.weight"); b.ln2b = get(p + "ln2.bias");
+        b.f1w = get(p + "ffn.0.weight"); b.f1b = get(p + "ffn.0.bias");
+        b.f2w = get(p + "ffn.2.weight"); b.f2b = get(p + "ffn.2.bias");
+    }
+    m->lnf_w = get("ln_f.weight"); m->lnf_b = get("ln_f.bias");
+    m->temb = get("opt_type_emb.weight");
+    m->oc_w = get("opt_card.weight"); m->oc_b = get("opt_card.bias");
+    m->oa_w = get("opt_attack.weight"); m->oa_b = get("opt_attack.bias");
+    m->q1_w = get("q_mlp.0.weight"); m->q1_b = get("q_mlp.0.bias");
+    m->q2_w = get("q_mlp.2.weight"); m->q2_b = get("q_mlp.2.bias");
+    m->s1_w = get("score_mlp.0.weight"); m->s1_b = get("score_mlp.0.bias");
+    m->s2_w = get("score_mlp.2.weight"); m->s2_b = get("score_mlp.2.bias");
+    m->v1_w = get("value_mlp.0.weight"); m->v1_b = get("value_mlp.0.bias");
+    m->v2_w = get("value_mlp.2.weight"); m->v2_b = get("value_mlp.2.bias");
+    PT_REQUIRE(m->card && m->att && m->v2_b, "model_bind: parameter table incomplete");
+    return PTCG_OK;
+}
+
+struct Carver {
+    char* base; size_t off = 0;
+    float* take(size_t floats) {
+        off = (off + 255) & ~(size_t)255;
+        float* p = base ? reinterpret_cast<float*>(base + off) : nullptr;
+        off += floats * sizeof(float);
+        return p;
+    }
+};
+
+static size_t carve(PtcgModel* m, char* base) {
+    const PtcgDims& d = m->dm;
+    const DimsX& x = m->dx;
+    const long N = m->N, Lt = d.l_tok, Ls = x.l_seq, NL = N * Ls, NO = d.n_opt, D = d.d;
+    Carver c{base};
+    m->tok_cat = c.take(N * Lt * x.tok_in);
+    m->tokp = c.take(N * Lt * D);
+    m->glob_in = c.take(N * d.global_f);
+    m->g1 = c.take(N * d.g); m->g1a = c.take(N * d.g);
+    m->dec_in = c.take(N * x.dec_in);
+    m->d1 = c.take(N * PT_DEC_H); m->d1a = c.take(N * PT_DEC_H);
+    m->gd = c.take(N * x.bcast_in);
+    m->bc = c.take(N * D);
+    m->keep = c.take(NL);
+    m->x.resize(d.layers + 1);
+    for (auto& p : m->x) p = c.take(NL * D);
+    m->ba.resize(d.layers);
+    for (auto& a : m->ba) {
+        a.ln1 = c.take(NL * D); a.mu1 = c.take(NL); a.rs1 = c.take(NL);
+        a.qkv = c.take(NL * 3 * D); a.ctx = c.take(NL * D); a.lse = c.take(NL * d.heads);
+        a.xmid = c.take(NL * D);
+        a.ln2 = c.take(NL * D); a.mu2 = c.take(NL); a.rs2 = c.take(NL);
+        a.ffp = c.take(NL * d.ffn); a.ffa = c.take(NL * d.ffn);
+    }
+    m->h = c.take(NL * D); m->lnf_mu = c.take(NL); m->lnf_rs = c.take(NL);
+    m->ocard = c.take(N * NO * d.d_c); m->oatt = c.take(N * NO * d.d_a);
+    m->q_in = c.take(N * NO * x.q_in);
+    m->q1 = c.take(N * NO * D); m->q1a = c.take(N * NO * D);
+    m->sc_in = c.take(N * NO * x.score_in);
+    m->s1 = c.take(N * NO * PT_SC_H); m->s1a = c.take(N * NO * PT_SC_H);
+    m->val_in = c.take(N * x.val_in);
+    m->v1 = c.take(N * PT_VAL_H); m->v1a = c.take(N * PT_VAL_H);
+    m->out = c.take(N * (NO + 1));
+    // backward scratch
+    m->dxa = c.take(NL * D); m->dxb = c.take(NL * D);
+    m->dffn = c.take(NL * d.ffn); m->dln = c.take(NL * D);
+    m->dqkv = c.take(NL * 3 * D); m->dctx = c.take(NL * D);
+    m->dsc = c.take(N * NO * x.score_in); m->ds1 = c.take(N * NO * PT_SC_H);
+    m->dq = c.take(N * NO * D); m->dq1 = c.take(N * NO * D);
+    m->dqin = c.take(N * NO * x.q_in);
+    m->docard = c.take(N * NO * d.d_c); m->doatt = c.take(N * NO * d.d_a);
+    m->dvin = c.take(N * x.val_in); m->dv1 = c.take(N * PT_VAL_H);
+    m->dgd = c.take(N * x.bcast_in); m->dd1 = c.take(N * PT_DEC_H); m->dg1 = c.take(N * d.g);
+    m->ddec = c.take(N * x.dec_in);
+    m->dtokp = c.take(N * Lt * D); m->dtokcat = c.take(N * Lt * x.tok_in);
+    m->dbc = c.take(N * D);
+    // workspace: split-K partials, column-sum / LayerNorm / head partials
+    m->ws_floats = 16L << 20;
+    long ln_part = (long)pt_cdiv(NL, 32) * 2 * D;
+    if (ln_part > m->ws_floats) m->ws_floats = ln_part;
+    m->ws = c.take(m->ws_floats);
+    return c.off;
+}
+
+extern "C" int ptcg_model_reg_train(PtcgModel* m, int n) {
+    PT_REQUIRE(m && n >= 2, "model_reg_train: need n >= 2 rows");
+    if (m->mem) {
+        PT_HIP(hipFree(m->mem));
+        m->mem = nullptr;
+    }
+    m->N = n;
+    size_t bytes = carve(m, nullptr);
+    PT_HIP(hipMalloc(&m->mem, bytes));
+    m->mem_bytes = bytes;
+    carve(m, m->mem);
+    return PTCG_OK;
+}
+
+extern "C" void ptcg_model_free(PtcgModel* m) {
+    if (!m) return;
+    if (m->mem) (void)hipFree(m->mem);
+    delete m;
+}
+
+size_t pt_model_act_bytes(const PtcgModel* m) { return m->mem_bytes; }
+float* pt_model_out(const PtcgModel* m) { return m->out; }
+float* pt_model_ws(const PtcgModel* m, long* floats) { *floats = m->ws_floats; return m->ws; }
+
+// ------------------------------------------------------------ forward
+static int block_fwd(PtcgModel* m, int i, const float* xin, float* xout, hipStream_t s) {
+    const PtcgDims& d = m->dm;
+    const int NL = m->N * m->dx.l_seq, D = d.d;
+    const BlockP& w = m->blk[i];
+    const BlockA& a = m->ba[i];
+    PT_TRY(pt_ln_fwd(xin, D, w.ln1w, w.ln1b, a.ln1, D, a.mu1, a.rs1, NL, D, s));
+    PT_TRY(linf(a.ln1, w.qkvw, w.qkvb, a.qkv, NL, D, 3 * D, EPI_BIAS, nullptr, nullptr, s));
+    PT_TRY(pt_attn_fwd(a.qkv, m->keep, a.ctx, a.lse, m->N, m->dx.l_seq, d.heads, m->dx.dh, s));
+    PT_TRY(linf(a.ctx, w.projw, w.projb, a.xmid, NL, D, D, EPI_BIAS_RESID, xin, nullptr, s));
+    PT_TRY(pt_ln_fwd(a.xmid, D, w.ln2w, w.ln2b, a.ln2, D, a.mu2, a.rs2, NL, D, s));
+    PT_TRY(linf(a.ln2, w.f1w, w.f1b, a.ffp, NL, D, d.ffn, EPI_BIAS_GELU, nullptr, a.ffa, s));
+    PT_TRY(linf(a.ffa, w.f2w, w.f2b, xout, NL, d.ffn, D, EPI_BIAS_RESID, a.xmid, nullptr, s));
+    return PTCG_OK;
+}
+
+extern "C" int ptcg_model_forward(PtcgModel* m, const float* obs, const int32_t* row_idx, int n,
+                                  float** out, void* stream) {
+    PT_REQUIRE(m && obs && m->P, "model_forward: model not bound");
+    PT_REQUIRE(m->mem, "model_forward: activations not registered (call ptcg_model_reg_train)");
+    PT_REQUIRE(n == m->N, "model_forward: need exactly %d rows (activations are sized at "
+               "registration, bindings.cu:227-233), got %d", m->N, n);
+    hipStream_t s = (hipStream_t)stream;
+    const PtcgDims& d = m->dm;
+    const DimsX& x = m->dx;
+    const int N = m->N, Lt = d.l_tok, NO = d.n_opt, D = d.d, G = d.g;
+    m->obs = obs;
+    m->idx = row_idx;
+    GatherCtx c{obs, row_idx, (long)m->off.size, N, d, x, m->off};
+
+    PT_TRY(pt_tok_cat_fwd(c, m->card, m->zemb, m->oemb, m->tok_cat, s));
+    PT_TRY(linf(m->tok_cat, m->tp_w, m->tp_b, m->tokp, N * Lt, x.tok_in, D, EPI_BIAS, nullptr, nullptr, s));
+    PT_TRY(pt_glob_in(c, m->glob_in, s));
+    PT_TRY(linf(m->glob_in, m->g1_w, m->g1_b, m->g1, N, d.global_f, G, EPI_BIAS_GELU, nullptr, m->g1a, s));
+    PT_TRY(lin(m->g1a, G, m->g2_w, m->g2_b, m->gd, x.bcast_in, N, G, G, EPI_BIAS, nullptr, 0, nullptr, 0, s));
+    PT_TRY(pt_dec_in_fwd(c, m->card, m->att, m->semb, m->cemb, m->dec_in, s));
+    PT_TRY(linf(m->dec_in, m->d1_w, m->d1_b, m->d1, N, x.dec_in, PT_DEC_H, EPI_BIAS_GELU, nullptr, m->d1a, s));
+    PT_TRY(lin(m->d1a, PT_DEC_H, m->d2_w, m->d2_b, m->gd + G, x.bcast_in, N, PT_DEC_H, PT_DEC_H, EPI_BIAS,
+               nullptr, 0, nullptr, 0, s));
+    PT_TRY(lin(m->gd, x.bcast_in, m->bc_w, m->bc_b, m->bc, D, N, x.bcast_in, D, EPI_BIAS, nullptr, 0, nullptr, 0, s));
+    PT_TRY(pt_x0_fwd(c, m->tokp, m->bc, m->readout, m->x[0], m->keep, s));
+    for (int i = 0; i < d.layers; ++i) PT_TRY(block_fwd(m, i, m->x[i], m->x[i + 1], s));
+    const int NL = N * x.l_seq;
+    PT_TRY(pt_ln_fwd(m->x[d.layers], D, m->lnf_w, m->lnf_b, m->h, D, m->lnf_mu, m->lnf_rs, NL, D, s));
+
+    // option scorer
+    const int NJ = N * NO;
+    const int oc0 = PT_TYPE_E + 2 * D, oa0 = oc0 + PT_OPT_E;
+    PT_TRY(pt_opt_gather_fwd(c, m->card, m->att, m->ocard, m->oatt, s));
+    PT_TRY(lin(m->ocard, d.d_c, m->oc_w, m->oc_b, m->q_in + oc0, x.q_in, NJ, d.d_c, PT_OPT_E, EPI_BIAS,
+               nullptr, 0, nullptr, 0, s));
+    PT_TRY(lin(m->oatt, d.d_a, m->oa_w, m->oa_b, m->q_in + oa0, x.q_in, NJ, d.d_a, PT_OPT_E, EPI_BIAS,
+               nullptr, 0, nullptr, 0, s));
+    PT_TRY(pt_q_in_fwd(c, m->h, m->temb, m->q_in, s));
+    PT_TRY(linf(m->q_in, m->q1_w, m->q1_b, m->q1, NJ, x.q_in, D, EPI_BIAS_GELU, nullptr, m->q1a, s));
+    PT_TRY(lin(m->q1a, D, m->q2_w, m->q2_b, m->sc_in, x.score_in, NJ, D, D, EPI_BIAS, nullptr, 0, nullptr, 0, s));
+    PT_TRY(pt_sc_in_fwd(c, m->h, m->gd, m->sc_in, s));
+    PT_TRY(linf(m->sc_in, m->s1_w, m->s1_b, m->s1, NJ, x.score_in, PT_SC_H, EPI_BIAS_GELU, nullptr, m->s1a, s));
+    PT_TRY(pt_head_dot(m->s1a, NJ, PT_SC_H, m->s2_w, m->s2_b, m->out, NO, NO + 1, 0, s));
+    // blind value head
+    PT_TRY(pt_val_in_fwd(c, m->h, m->gd, m->val_in, s));
+    PT_TRY(linf(m->val_in, m->v1_w, m->v1_b, m->v1, N, x.val_in, PT_VAL_H, EPI_BIAS_GELU, nullptr, m->v1a, s));
+    PT_TRY(pt_head_dot(m->v1a, N, PT_VAL_H, m->v2_w, m->v2_b, m->out, 1, NO + 1, NO, s));
+    if (out) *out = m->out;
+    return PTCG_OK;
+}
+
+// ------------------------------------------------------------ backward
+// dA holds d(x_out) on entry and d(x_in) on exit; dC is scratch for d(x_mid)
+static int block_bwd(PtcgModel* m, int i, const float* xin, float* dA, float* dC, hipStream_t s) {
+    const PtcgDims& d = m->dm;
+    const int NL = m->N * m->dx.l_seq, D = d.d;
+    const BlockP& w = m->blk[i];
+    const BlockA& a = m->ba[i];
+    PT_TRY(ldw_(m, dA, D, a.ffa, d.ffn, m->G(w.f2w), m->G(w.f2b), NL, d.ffn, D, s));
+    PT_TRY(ldx_(dA, D, w.f2w, m->dffn, d.ffn, NL, d.ffn, D, EPI_GELU_BWD, a.ffp, d.ffn, s));
+    PT_TRY(ldw_(m, m->dffn, d.ffn, a.ln2, D, m->G(w.f1w), m->G(w.f1b), NL, D, d.ffn, s));
+    PT_TRY(ldx_(m->dffn, d.ffn, w.f1w, m->dln, D, NL, D, d.ffn, EPI_STORE, nullptr, 0, s));
+    PT_TRY(pt_ln_bwd(m->dln, D, a.xmid, D, w.ln2w, a.mu2, a.rs2, dA, D, dC, D, m->G(w.ln2w),
+                     m->G(w.ln2b), NL, D, m->ws, m->ws_floats, s));
+    PT_TRY(ldw_(m, dC, D, a.ctx, D, m->G(w.projw), m->G(w.projb), NL, D, D, s));
+    PT_TRY(ldx_(dC, D, w.projw, m->dctx, D, NL, D, D, EPI_STORE, nullptr, 0, s));
+    PT_TRY(pt_attn_bwd(a.qkv, m->keep, a.ctx, a.lse, m->dctx, m->dqkv, m->N, m->dx.l_seq, d.heads,
+                       m->dx.dh, s));
+    PT_TRY(ldw_(m, m->dqkv, 3 * D, a.ln1, D, m->G(w.qkvw), m->G(w.qkvb), NL, D, 3 * D, s));
+    PT_TRY(ldx_(m->dqkv, 3 * D, w.qkvw, m->dln, D, NL, D, 3 * D, EPI_STORE, nullptr, 0, s));
+    PT_TRY(pt_ln_bwd(m->dln, D, xin, D, w.ln1w, a.mu1, a.rs1, dC, D, dA, D, m->G(w.ln1w),
+                     m->G(w.ln1b), NL, D, m->ws, m->ws_floats, s));
+    return PTCG_OK;
+}
+
+extern "C" int ptcg_model_backward(PtcgModel* m, const float* grad, void* stream) {
+    PT_REQUIRE(m && grad && m->mem && m->obs, "model_backward: run a forward first");
+    hipStream_t s = (hipStream_t)stream;
+    const PtcgDims& d = m->dm;
+    const DimsX& x = m->dx;
+    const int N = m->N, Lt = d.l_tok, NO = d.n_opt, D = d.d, G = d.g, NJ = N * NO;
+    const int NL = N * x.l_seq;
+    GatherCtx c{m->obs, m->idx, (long)m->off.size, N, d, x, m->off};
+
+    PT_TRY(pt_fill_zero(m->Gr, m->arena, s));
+    PT_TRY(pt_fill_zero(m->dxa, (long)NL * D, s));
+    PT_TRY(pt_fill_zero(m->dgd, (long)N * x.bcast_in, s));
+
+    // blind value head: grad[:, NO]
+    PT_TRY(pt_head_dot_dw(grad, 1, NO + 1, NO, m->v1a, N, PT_VAL_H, m->G(m->v2_w), m->G(m->v2_b), m->ws,
+                          m->ws_floats, s));
+    PT_TRY(pt_head_dot_bwd(grad, 1, NO + 1, NO, m->v2_w, m->v1, m->dv1, N, PT_VAL_H, s));
+    PT_TRY(ldw_(m, m->dv1, PT_VAL_H, m->val_in, x.val_in, m->G(m->v1_w), m->G(m->v1_b), N, x.val_in, PT_VAL_H, s));
+    PT_TRY(ldx_(m->dv1, PT_VAL_H, m->v1_w, m->dvin, x.val_in, N, x.val_in, PT_VAL_H, EPI_STORE, nullptr, 0, s));
+    PT_TRY(pt_val_in_bwd(c, m->dvin, m->dxa, m->dgd, s));
+
+    // option scores: grad[:, :NO]
+    PT_TRY(pt_head_dot_dw(grad, NO, NO + 1, 0, m->s1a, NJ, PT_SC_H, m->G(m->s2_w), m->G(m->s2_b), m->ws,
+                          m->ws_floats, s));
+    PT_TRY(pt_head_dot_bwd(grad, NO, NO + 1, 0, m->s2_w, m->s1, m->ds1, NJ, PT_SC_H, s));
+    PT_TRY(ldw_(m, m->ds1, PT_SC_H, m->sc_in, x.score_in, m->G(m->s1_w), m->G(m->s1_b), NJ, x.score_in, PT_SC_H, s));
+    PT_TRY(ldx_(m->ds1, PT_SC_H, m->s1_w, m->dsc, x.score_in, NJ, x.score_in, PT_SC_H, EPI_STORE, nullptr, 0, s));
+    PT_TRY(pt_sc_in_bwd(c, m->dsc, m->sc_in, m->dq, m->dxa, m->dgd, s));
+    PT_TRY(ldw_(m, m->dq, D, m->q1a, D, m->G(m->q2_w), m->G(m->q2_b), NJ, D, D, s));
+    PT_TRY(ldx_(m->dq, D, m->q2_w, m->dq1, D, NJ, D, D, EPI_GELU_BWD, m->q1, D, s));
+    PT_TRY(ldw_(m, m->dq1, D, m->q_in, x.q_in, m->G(m->q1_w), m->G(m->q1_b), NJ, x.q_in, D, s));
+    PT_TRY(ldx_(m->dq1, D, m->q1_w, m->dqin, x.q_in, NJ, x.q_in, D, EPI_STORE, nullptr, 0, s));
+    PT_TRY(pt_q_in_bwd(c, m->dqin, m->dxa, m->G(m->temb), s));
+    const int oc0 = PT_TYPE_E + 2 * D, oa0 = oc0 + PT_OPT_E;
+    PT_TRY(ldw_(m, m->dqin + oc0, x.q_in, m->ocard, d.d_c, m->G(m->oc_w), m->G(m->oc_b), NJ, d.d_c, PT_OPT_E, s));
+    PT_TRY(ldx_(m->dqin + oc0, x.q_in, m->oc_w, m->docard, d.d_c, NJ, d.d_c, PT_OPT_E, EPI_STORE, nullptr, 0, s));
+    PT_TRY(ldw_(m, m->dqin + oa0, x.q_in, m->oatt, d.d_a, m->G(m->oa_w), m->G(m->oa_b), NJ, d.d_a, PT_OPT_E, s));
+    PT_TRY(ldx_(m->dqin + oa0, x.q_in, m->oa_w, m->doatt, d.d_a, NJ, d.d_a, PT_OPT_E, EPI_STORE, nullptr, 0, s));
+    PT_TRY(pt_opt_gather_bwd(c, m->docard, m->doatt, m->G(m->card), m->G(m->att), s));
+
+    // final LayerNorm, then the trunk in reverse (d_x in dxb, scratch dxa)
+    PT_TRY(pt_ln_bwd(m->dxa, D, m->x[d.layers], D, m->lnf_w, m->lnf_mu, m->lnf_rs, nullptr, 0, m->dxb, D,
+                     m->G(m->lnf_w), m->G(m->lnf_b), NL, D, m->ws, m->ws_floats, s));
+    for (int i = d.layers - 1; i >= 0; --i) PT_TRY(block_bwd(m, i, m->x[i], m->dxb, m->dxa, s));
+
+    // trunk input: readout / token projection / broadcast
+    PT_TRY(pt_x0_bwd(c, m->dxb, m->dtokp, m->dbc, s));
+    PT_TRY(pt_colsum(m->dxb, (long)x.l_seq * D, N, D, m->G(m->readout), m->ws, m->ws_floats, s));
+    PT_TRY(ldw_(m, m->dtokp, D, m->tok_cat, x.tok_in, m->G(m->tp_w), m->G(m->tp_b), N * Lt, x.tok_in, D, s));
+    PT_TRY(ldx_(m->dtokp, D, m->tp_w, m->dtokcat, x.tok_in, N * Lt, x.tok_in, D, EPI_STORE, nullptr, 0, s));
+    PT_TRY(pt_tok_cat_bwd(c, m->dtokcat, m->G(m->card), m->G(m->zemb), m->G(m->oemb), s));
+    PT_TRY(ldw_(m, m->dbc, D, m->gd, x.bcast_in, m->G(m->bc_w), m->G(m->bc_b), N, x.bcast_in, D, s));
+    PT_TRY(ldx_(m->dbc, D, m->bc_w, m->dgd, x.bcast_in, N, x.bcast_in, D, EPI_ACCUM, nullptr, 0, s));
+    // decision MLP (d_dvec = dgd[:, G:])
+    PT_TRY(ldw_(m, m->dgd + G, x.bcast_in, m->d1a, PT_DEC_H, m->G(m->d2_w), m->G(m->d2_b), N, PT_DEC_H, PT_DEC_H, s));
+    PT_TRY(ldx_(m->dgd + G, x.bcast_in, m->d2_w, m->dd1, PT_DEC_H, N, PT_DEC_H, PT_DEC_H, EPI_GELU_BWD, m->d1, PT_DEC_H, s));
+    PT_TRY(ldw_(m, m->dd1, PT_DEC_H, m->dec_in, x.dec_in, m->G(m->d1_w), m->G(m->d1_b), N, x.dec_in, PT_DEC_H, s));
+    PT_TRY(ldx_(m->dd1, PT_DEC_H, m->d1_w, m->ddec, x.dec_in, N, x.dec_in, PT_DEC_H, EPI_STORE, nullptr, 0, s));
+    PT_TRY(pt_dec_in_bwd(c, m->ddec, m->G(m->card), m->G(m->att), m->G(m->semb), m->G(m->cemb), s));
+    // global MLP (d_g = dgd[:, :G])
+    PT_TRY(ldw_(m, m->dgd, x.bcast_in, m->g1a, G, m->G(m->g2_w), m->G(m->g2_b), N, G, G, s));
+    PT_TRY(ldx_(m->dgd, x.bcast_in, m->g2_w, m->dg1, G, N, G, G, EPI_GELU_BWD, m->g1, G, s));
+    PT_TRY(ldw_(m, m->dg1, G, m->glob_in, d.global_f, m->G(m->g1_w), m->G(m->g1_b), N, d.global_f, G, s));
+    return PTCG_OK;
+}

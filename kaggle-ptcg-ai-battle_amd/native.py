@@ -1,0 +1,143 @@
+"""ctypes binding of libptcg_amd.so (the C ABI in include/ptcg_amd.h).
+
+The library is the only compute path: if it is missing or fails to load,
+every entry point raises — there is no CPU fallback.
+"""
+import ctypes
+import os
+
+from .dims import CPtcgDims
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libptcg_amd.so")
+
+c_float_p = ctypes.POINTER(ctypes.c_float)
+c_i32_p = ctypes.POINTER(ctypes.c_int32)
+c_void_p = ctypes.c_void_p
+
+
+class CPtcgHypers(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_float) for n in (
+        "lr", "beta1", "beta2", "eps", "max_grad_norm", "clip_coef", "vf_clip_coef",
+        "vf_coef", "ent_coef", "kl_skip_threshold", "vf_skip_threshold")]
+
+
+# name -> (restype, argtypes)
+_SIGS = {
+    "ptcg_last_error": (ctypes.c_char_p, []),
+    "ptcg_abi_version": (ctypes.c_int, []),
+    "ptcg_obs_size": (ctypes.c_int, [ctypes.POINTER(CPtcgDims)]),
+    "ptcg_num_params": (ctypes.c_int, [ctypes.POINTER(CPtcgDims)]),
+    "ptcg_param_info": (ctypes.c_int, [ctypes.POINTER(CPtcgDims), ctypes.c_int,
+                                       ctypes.POINTER(ctypes.c_char_p),
+                                       ctypes.POINTER(ctypes.c_int64),
+                                       ctypes.POINTER(ctypes.c_int64)]),
+    "ptcg_packed_floats": (ctypes.c_int64, [ctypes.POINTER(CPtcgDims)]),
+    "ptcg_arena_floats": (ctypes.c_int64, [ctypes.POINTER(CPtcgDims)]),
+    "ptcg_packed_to_arena": (ctypes.c_int, [ctypes.POINTER(CPtcgDims), c_float_p, c_float_p]),
+    "ptcg_arena_to_packed": (ctypes.c_int, [ctypes.POINTER(CPtcgDims), c_float_p, c_float_p]),
+    "ptcg_model_create": (ctypes.c_int, [ctypes.POINTER(CPtcgDims), ctypes.POINTER(c_void_p)]),
+    "ptcg_model_bind": (ctypes.c_int, [c_void_p, c_void_p, c_void_p]),
+    "ptcg_model_reg_train": (ctypes.c_int, [c_void_p, ctypes.c_int]),
+    "ptcg_model_forward": (ctypes.c_int, [c_void_p, c_void_p, c_void_p, ctypes.c_int,
+                                          ctypes.POINTER(c_void_p), c_void_p]),
+    "ptcg_model_backward": (ctypes.c_int, [c_void_p, c_void_p, c_void_p]),
+    "ptcg_model_free": (None, [c_void_p]),
+    "ptcg_ppo_loss_fwd_bwd": (ctypes.c_int, [
+        c_void_p, ctypes.c_int, ctypes.c_int, c_void_p, ctypes.c_int64, c_void_p,
+        c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+        ctypes.c_float, ctypes.c_float, ctypes.c_float, ctypes.c_float,
+        c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
+    "ptcg_kl_gate": (ctypes.c_int, [c_void_p, ctypes.c_float, ctypes.c_float, c_void_p,
+                                    c_void_p, c_void_p]),
+    "ptcg_adam_workspace_floats": (ctypes.c_int64, []),
+    "ptcg_adam_step": (ctypes.c_int, [
+        c_void_p, c_void_p, c_void_p, c_void_p, ctypes.c_int64,
+        ctypes.c_float, ctypes.c_float, ctypes.c_float, ctypes.c_float, ctypes.c_float,
+        c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
+    "ptcg_trainer_create": (ctypes.c_int, [ctypes.POINTER(CPtcgDims), ctypes.POINTER(CPtcgHypers),
+                                           ctypes.c_int, ctypes.POINTER(c_void_p)]),
+    "ptcg_trainer_free": (None, [c_void_p]),
+    "ptcg_trainer_set_hypers": (ctypes.c_int, [c_void_p, ctypes.POINTER(CPtcgHypers)]),
+    "ptcg_trainer_set_weights": (ctypes.c_int, [c_void_p, c_float_p]),
+    "ptcg_trainer_get_weights": (ctypes.c_int, [c_void_p, c_float_p]),
+    "ptcg_trainer_get_grads": (ctypes.c_int, [c_void_p, c_float_p]),
+    "ptcg_trainer_get_moments": (ctypes.c_int, [c_void_p, c_float_p, c_float_p]),
+    "ptcg_trainer_load_weights": (ctypes.c_int, [c_void_p, ctypes.c_char_p]),
+    "ptcg_trainer_save_weights": (ctypes.c_int, [c_void_p, ctypes.c_char_p]),
+    "ptcg_trainer_save_state": (ctypes.c_int, [c_void_p, ctypes.c_char_p]),
+    "ptcg_trainer_load_state": (ctypes.c_int, [c_void_p, ctypes.c_char_p]),
+    "ptcg_trainer_debug_forward": (ctypes.c_int, [c_void_p, c_float_p, ctypes.c_int, c_float_p]),
+    "ptcg_trainer_step": (ctypes.c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+                                         c_void_p, c_void_p, c_void_p, c_void_p]),
+    "ptcg_trainer_forward_backward": (ctypes.c_int, [c_void_p, c_void_p, c_void_p, c_void_p,
+                                                     c_void_p, c_void_p, c_void_p, c_void_p,
+                                                     c_void_p]),
+    "ptcg_trainer_losses": (ctypes.c_int, [c_void_p, c_float_p, ctypes.c_int]),
+    "ptcg_trainer_buffers": (ctypes.c_int, [c_void_p, ctypes.POINTER(c_void_p),
+                                            ctypes.POINTER(c_void_p), ctypes.POINTER(c_void_p),
+                                            ctypes.POINTER(c_void_p)]),
+    "ptcg_trainer_sync": (ctypes.c_int, [c_void_p]),
+    "ptcg_trainer_step_count": (ctypes.c_int, [c_void_p, c_i32_p]),
+    # include/ptcg_amd_kernels.h
+    "ptcg_profile_begin": (ctypes.c_int, [ctypes.c_int]),
+    "ptcg_profile_end": (ctypes.c_int, [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_int),
+                                        ctypes.POINTER(ctypes.c_double)]),
+    "ptcg_kernel_gemm": (ctypes.c_int, [
+        ctypes.c_int, ctypes.c_int, ctypes.c_int, c_void_p, ctypes.c_int64, ctypes.c_int,
+        c_void_p, ctypes.c_int64, ctypes.c_int, c_void_p, ctypes.c_int64, ctypes.c_int,
+        c_void_p, c_void_p, ctypes.c_int64, c_void_p, ctypes.c_int64, c_void_p,
+        ctypes.c_int64, c_void_p]),
+    "ptcg_kernel_colsum": (ctypes.c_int, [c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_int,
+                                          c_void_p, c_void_p, ctypes.c_int64, c_void_p]),
+    "ptcg_kernel_layernorm_fwd": (ctypes.c_int, [c_void_p, c_void_p, c_void_p, c_void_p,
+                                                 c_void_p, c_void_p, ctypes.c_int, ctypes.c_int,
+                                                 c_void_p]),
+    "ptcg_kernel_layernorm_bwd": (ctypes.c_int, [c_void_p, c_void_p, c_void_p, c_void_p,
+                                                 c_void_p, c_void_p, c_void_p, c_void_p,
+                                                 c_void_p, ctypes.c_int, ctypes.c_int, c_void_p,
+                                                 ctypes.c_int64, c_void_p]),
+    "ptcg_kernel_attention_fwd": (ctypes.c_int, [c_void_p, c_void_p, c_void_p, c_void_p,
+                                                 ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                                 ctypes.c_int, c_void_p]),
+    "ptcg_kernel_attention_bwd": (ctypes.c_int, [c_void_p, c_void_p, c_void_p, c_void_p,
+                                                 c_void_p, c_void_p, ctypes.c_int, ctypes.c_int,
+                                                 ctypes.c_int, ctypes.c_int, c_void_p]),
+}
+
+_lib = None
+
+
+def lib():
+    """Load the library once; raise if it is absent (no fallback exists)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"{LIB_PATH} not built: run __graft_entry__.build() (hipcc, gfx950) first")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in _SIGS.items():
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = L
+    return _lib
+
+
+def exported_symbols():
+    return sorted(_SIGS)
+
+
+class PtcgError(RuntimeError):
+    pass
+
+
+def check(rc):
+    if rc != 0:
+        raise PtcgError(lib().ptcg_last_error().decode(errors="replace"))
+    return rc
+
+
+def fptr(a):
+    """float* of a contiguous float32 numpy array."""
+    return a.ctypes.data_as(c_float_p)

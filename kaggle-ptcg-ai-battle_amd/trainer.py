@@ -1,0 +1,235 @@
+"""Host-side mirror of the reference trainer's Python API for the training
+step (the ``_C`` module of native/src/bindings.cu:675-862 as used by
+native/train_native.py and native/tools/model_parity.py).
+
+Same names, argument meaning and error behaviour (``RuntimeError`` with the
+reference's messages) for the hot-path subset:
+
+    create_pufferl(args) -> PuffeRL         bindings.cu:581-673
+    train(pl) -> dict                       bindings.cu:184-192 / train_impl
+    debug_forward(pl, rows) -> (B, A+1)     bindings.cu:221-250
+    save_weights / load_weights             bindings.cu:202-215, 339-367
+    save_state / load_state                 bindings.cu:257-337 (Adam state)
+    log(pl) -> dict                         bindings.cu:15-118 ("losses")
+    close(pl)
+
+Rollout collection is out of scope: ``set_rollout`` hands the trainer a
+device-resident rollout (obs rows plus per-row actions, old log-probs,
+advantages, returns, old values) in place of the env/vec pipeline.
+Device memory for the rollout is plumbing held in torch tensors; every
+computation runs in libptcg_amd.so.
+"""
+import ctypes
+
+import numpy as np
+
+from . import dims as dims_mod
+from .native import lib, check, fptr, CPtcgHypers, c_void_p, c_i32_p
+
+LOSS_KEYS = ("policy_loss", "value_loss", "entropy", "total_loss",
+             "old_approx_kl", "approx_kl", "clipfrac")
+
+TRAIN_DEFAULTS = {
+    "learning_rate": 3e-4, "beta1": 0.9, "beta2": 0.999, "eps": 1e-8,
+    "max_grad_norm": 0.5, "clip_coef": 0.2, "vf_clip_coef": 0.2,
+    "vf_coef": 0.5, "ent_coef": 0.01, "kl_skip_threshold": 0.0,
+    "vf_skip_threshold": 0.0, "minibatch_size": 512, "update_epochs": 4,
+    "minibatches_per_epoch": 8,
+}
+
+
+def _hypers(train):
+    t = dict(TRAIN_DEFAULTS)
+    t.update(train or {})
+    return CPtcgHypers(t["learning_rate"], t["beta1"], t["beta2"], t["eps"],
+                       t["max_grad_norm"], t["clip_coef"], t["vf_clip_coef"],
+                       t["vf_coef"], t["ent_coef"], t["kl_skip_threshold"],
+                       t["vf_skip_threshold"]), t
+
+
+class PuffeRL:
+    """Handle returned by :func:`create_pufferl` (owns a PtcgTrainer)."""
+
+    def __init__(self, dm, train, seed=0):
+        import torch
+        if not torch.cuda.is_available():
+            raise RuntimeError("CUDA is not available")
+        self._torch = torch
+        self.dims = dm
+        self._cdims = dm.as_ctypes()
+        self._chyp, self.train_cfg = _hypers(train)
+        self.minibatch = int(self.train_cfg["minibatch_size"])
+        self.seed = seed
+        h = c_void_p()
+        check(lib().ptcg_trainer_create(ctypes.byref(self._cdims), ctypes.byref(self._chyp),
+                                        self.minibatch, ctypes.byref(h)))
+        self._h = h
+        self.packed_floats = lib().ptcg_packed_floats(ctypes.byref(self._cdims))
+        self.obs_size = lib().ptcg_obs_size(ctypes.byref(self._cdims))
+        self.rollout = None
+        self.epoch = 0
+
+    # -------------------------------------------------- weights
+    def set_weights(self, packed):
+        packed = np.ascontiguousarray(packed, dtype=np.float32).ravel()
+        if packed.size != self.packed_floats:
+            raise RuntimeError(f"Weight blob size mismatch: expected {self.packed_floats} floats, "
+                               f"got {packed.size}")
+        check(lib().ptcg_trainer_set_weights(self._h, fptr(packed)))
+
+    def get_weights(self):
+        out = np.empty(self.packed_floats, np.float32)
+        check(lib().ptcg_trainer_get_weights(self._h, fptr(out)))
+        return out
+
+    def get_grads(self):
+        out = np.empty(self.packed_floats, np.float32)
+        check(lib().ptcg_trainer_get_grads(self._h, fptr(out)))
+        return out
+
+    def get_moments(self):
+        m = np.empty(self.packed_floats, np.float32)
+        v = np.empty(self.packed_floats, np.float32)
+        check(lib().ptcg_trainer_get_moments(self._h, fptr(m), fptr(v)))
+        return m, v
+
+    def step_count(self):
+        v = ctypes.c_int32()
+        check(lib().ptcg_trainer_step_count(self._h, ctypes.byref(v)))
+        return v.value
+
+    def set_hypers(self, **kw):
+        self.train_cfg.update(kw)
+        self._chyp, self.train_cfg = _hypers(self.train_cfg)
+        check(lib().ptcg_trainer_set_hypers(self._h, ctypes.byref(self._chyp)))
+
+    # -------------------------------------------------- device helpers
+    def to_device(self, a, dtype=np.float32):
+        t = self._torch.from_numpy(np.ascontiguousarray(a, dtype=dtype))
+        return t.to("cuda")
+
+    def buffers(self):
+        p = [c_void_p() for _ in range(4)]
+        check(lib().ptcg_trainer_buffers(self._h, *[ctypes.byref(x) for x in p]))
+        return [x.value for x in p]
+
+    def sync(self):
+        check(lib().ptcg_trainer_sync(self._h))
+
+    def forward_backward(self, obs, idx, inp, stream=None):
+        """One forward + PPO loss + backward on device tensors (no optimizer)."""
+        check(lib().ptcg_trainer_forward_backward(
+            self._h, obs.data_ptr(), idx.data_ptr() if idx is not None else None,
+            inp["actions"].data_ptr(), inp["logprobs"].data_ptr(),
+            inp["advantages"].data_ptr(), inp["returns"].data_ptr(),
+            inp["values"].data_ptr(), stream))
+
+    def step(self, obs, idx, inp, stream=None):
+        """One full minibatch step on device tensors (with the optimizer)."""
+        check(lib().ptcg_trainer_step(
+            self._h, obs.data_ptr(), idx.data_ptr() if idx is not None else None,
+            inp["actions"].data_ptr(), inp["logprobs"].data_ptr(),
+            inp["advantages"].data_ptr(), inp["returns"].data_ptr(),
+            inp["values"].data_ptr(), stream))
+
+    def close(self):
+        if getattr(self, "_h", None) is not None and self._h.value:
+            lib().ptcg_trainer_free(self._h)
+            self._h = c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def create_pufferl(args):
+    """args: {"dims": PtcgDims | dict, "train": {...}, "seed": int,
+    "init_weights": packed blob | None}.  Unknown dims keys raise."""
+    dm = args.get("dims", dims_mod.CORE)
+    if isinstance(dm, dict):
+        dm = dims_mod.PtcgDims(**dm)
+    pl = PuffeRL(dm, args.get("train", {}), args.get("seed", 0))
+    init = args.get("init_weights")
+    if init is None:
+        from .params import init_blob
+        init = init_blob(dm, args.get("seed", 0))
+    pl.set_weights(init)
+    return pl
+
+
+def set_rollout(pl, obs, actions, logprobs, advantages, returns, values):
+    """Upload a rollout (rows = observations) to device memory."""
+    n = obs.shape[0]
+    if obs.shape[1] != pl.obs_size:
+        raise RuntimeError(f"rollout obs width {obs.shape[1]} != obs size {pl.obs_size}")
+    pl.rollout = dict(
+        obs=pl.to_device(obs), actions=pl.to_device(actions), logprobs=pl.to_device(logprobs),
+        advantages=pl.to_device(advantages), returns=pl.to_device(returns),
+        values=pl.to_device(values), n=n)
+
+
+def train(pl, index_lists=None):
+    """One PPO update over the stored rollout: update_epochs epochs, each a
+    fresh seeded permutation cut into minibatches (at most
+    minibatches_per_epoch of them); or the given index lists.  Returns the
+    loss dictionary of :func:`log`."""
+    if pl.rollout is None:
+        raise RuntimeError("train: no rollout set (call set_rollout)")
+    from .synth import minibatch_indices
+    r = pl.rollout
+    B = pl.minibatch
+    if index_lists is None:
+        ep = int(pl.train_cfg["update_epochs"])
+        per = min(int(pl.train_cfg["minibatches_per_epoch"]), r["n"] // B)
+        index_lists = minibatch_indices(r["n"], B, ep * per, pl.seed + pl.epoch, epochs=ep)
+    for idx in index_lists:
+        idx = np.asarray(idx, dtype=np.int32)
+        if idx.size != B:
+            raise RuntimeError(f"minibatch index list has {idx.size} rows, trainer minibatch is {B}")
+        pl.step(r["obs"], pl.to_device(idx, np.int32), r)
+    pl.epoch += 1
+    return log(pl)
+
+
+def debug_forward(pl, rows):
+    rows = np.ascontiguousarray(rows, dtype=np.float32)
+    n = rows.size // pl.obs_size if rows.ndim == 1 else rows.shape[0]
+    if rows.size != pl.minibatch * pl.obs_size:
+        raise RuntimeError(f"debug_forward: need exactly {pl.minibatch * pl.obs_size} floats "
+                           f"(minibatch {pl.minibatch} x obs {pl.obs_size}), got {rows.size}")
+    out = np.empty((n, pl.dims.n_opt + 1), np.float32)
+    check(lib().ptcg_trainer_debug_forward(pl._h, fptr(rows), n, fptr(out)))
+    return out
+
+
+def save_weights(pl, path):
+    check(lib().ptcg_trainer_save_weights(pl._h, str(path).encode()))
+
+
+def load_weights(pl, path):
+    check(lib().ptcg_trainer_load_weights(pl._h, str(path).encode()))
+
+
+def save_state(pl, path):
+    check(lib().ptcg_trainer_save_state(pl._h, str(path).encode()))
+
+
+def load_state(pl, path):
+    check(lib().ptcg_trainer_load_state(pl._h, str(path).encode()))
+
+
+def log(pl, reset=True):
+    out = np.zeros(10, np.float32)
+    check(lib().ptcg_trainer_losses(pl._h, fptr(out), 1 if reset else 0))
+    cnt = max(float(out[7]), 1.0)
+    d = {k: float(out[i]) / cnt for i, k in enumerate(LOSS_KEYS)}
+    d["minibatches"] = int(out[7])
+    d["guard_skipped"] = int(out[8])
+    d["grad_norm"] = float(out[9])
+    return d
+
+
+def close(pl):
+    pl.close()

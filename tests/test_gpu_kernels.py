@@ -1,0 +1,295 @@
+"""Kernel-level parity on the GPU, through the C ABI (include/ptcg_amd_kernels.h
+and the PPO / Adam entry points of include/ptcg_amd.h).
+
+References: float64 torch on the CPU for GEMM / LayerNorm / attention (the
+oracle's attention restatement), the oracle PPO loss and Adam.  Tolerance:
+relative L2 error <= 1e-5 and max error <= 1e-4 of the reference's max for
+fp32 kernels (written per test).
+"""
+import ctypes
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import rel_l2, max_rel
+from ptcg_amd import native
+import oracle.ppo as oppo
+import oracle.adam as oadam
+
+pytestmark = pytest.mark.gpu
+
+
+def dev(a, dtype=torch.float32):
+    return torch.as_tensor(np.ascontiguousarray(a)).to(dtype).to("cuda")
+
+
+def empty(*shape):
+    return torch.zeros(*shape, dtype=torch.float32, device="cuda")
+
+
+def P(t):
+    return None if t is None else t.data_ptr()
+
+
+def gelu(x):
+    return 0.5 * x * (1 + torch.erf(x / math.sqrt(2.0)))
+
+
+def gelu_grad(x):
+    return 0.5 * (1 + torch.erf(x / math.sqrt(2.0))) + x * torch.exp(-0.5 * x * x) / math.sqrt(2 * math.pi)
+
+
+GEMM_CASES = [
+    # M, N, K, a_t, b_t, epi
+    (37, 52, 300, 0, 0, 0), (37, 52, 300, 0, 0, 1), (130, 68, 64, 0, 0, 2),
+    (256, 256, 256, 0, 0, 3), (200, 96, 40, 0, 1, 4), (64, 300, 256, 0, 1, 0),
+    (64, 128, 20000, 1, 1, 0), (768, 256, 4096, 1, 1, 0), (96, 36, 12, 1, 0, 0),
+    (129, 131, 132, 0, 1, 5), (512, 1024, 256, 0, 0, 2),
+]
+
+
+@pytest.mark.parametrize("case", GEMM_CASES, ids=lambda c: "M%d_N%d_K%d_at%d_bt%d_e%d" % c)
+def test_gemm_layouts_and_epilogues(case, cuda):
+    M, N, K, a_t, b_t, epi = case
+    g = torch.Generator().manual_seed(M * 7 + N * 3 + K)
+    A = torch.randn(K, M, generator=g) if a_t else torch.randn(M, K, generator=g)
+    B = torch.randn(K, N, generator=g) if b_t else torch.randn(N, K, generator=g)
+    bias = torch.randn(N, generator=g)
+    R = torch.randn(M, N, generator=g)
+    C0 = torch.randn(M, N, generator=g)
+    Am = (A.T if a_t else A).double()
+    Bm = (B if b_t else B.T).double()
+    acc = Am @ Bm
+    ref2 = None
+    if epi == 0: ref = acc
+    elif epi == 1: ref = acc + bias.double()
+    elif epi == 2:
+        ref = acc + bias.double()
+        ref2 = gelu(ref)
+    elif epi == 3: ref = acc + bias.double() + R.double()
+    elif epi == 4: ref = acc * gelu_grad(R.double())
+    else: ref = C0.double() + acc
+    dA, dB, dbias, dR = dev(A), dev(B), dev(bias), dev(R)
+    dC = dev(C0) if epi == 5 else empty(M, N)
+    dC2 = empty(M, N)
+    ws = empty(32 << 20)
+    L = native.lib()
+    native.check(L.ptcg_kernel_gemm(M, N, K, P(dA), M if a_t else K, a_t, P(dB), N if b_t else K, b_t,
+                                    P(dC), N, epi, P(dbias), P(dR), N, P(dC2), N, P(ws), ws.numel(), None))
+    torch.cuda.synchronize()
+    got = dC.cpu().double()
+    assert rel_l2(got, ref) < 1e-5 and max_rel(got, ref) < 1e-4, (rel_l2(got, ref), max_rel(got, ref))
+    if ref2 is not None:
+        got2 = dC2.cpu().double()
+        assert rel_l2(got2, ref2) < 1e-5
+
+
+def test_gemm_rejects_unaligned_k(cuda):
+    a = empty(8, 6)
+    with pytest.raises(native.PtcgError, match="float4"):
+        native.check(native.lib().ptcg_kernel_gemm(8, 8, 6, P(a), 6, 0, P(a), 6, 0, P(empty(8, 8)), 8, 0,
+                                                   None, None, 0, None, 0, None, 0, None))
+
+
+def test_colsum(cuda):
+    X = torch.randn(1000, 300, generator=torch.Generator().manual_seed(1))
+    out = empty(300)
+    ws = empty(1 << 20)
+    native.check(native.lib().ptcg_kernel_colsum(P(dev(X)), 300, 1000, 300, P(out), P(ws), ws.numel(), None))
+    torch.cuda.synchronize()
+    assert rel_l2(out.cpu(), X.double().sum(0)) < 1e-6
+
+
+@pytest.mark.parametrize("rows,D", [(1000, 256), (37, 64), (130, 1024), (9, 300)])
+def test_layernorm_fwd_bwd(rows, D, cuda):
+    g = torch.Generator().manual_seed(rows + D)
+    x = (torch.randn(rows, D, generator=g) * 3 + 1).double().requires_grad_()
+    w = (torch.randn(D, generator=g)).double().requires_grad_()
+    b = (torch.randn(D, generator=g)).double().requires_grad_()
+    dy = torch.randn(rows, D, generator=g).double()
+    dres = torch.randn(rows, D, generator=g).double()
+    y = torch.nn.functional.layer_norm(x, (D,), w, b, eps=1e-5)
+    y.backward(dy)
+    L = native.lib()
+    dx_, dw_, db_ = dev(x.detach()), dev(w.detach()), dev(b.detach())
+    yy, mu, rs = empty(rows, D), empty(rows), empty(rows)
+    native.check(L.ptcg_kernel_layernorm_fwd(P(dx_), P(dw_), P(db_), P(yy), P(mu), P(rs), rows, D, None))
+    gx, gw, gb = empty(rows, D), empty(D), empty(D)
+    ws = empty(1 << 20)
+    native.check(L.ptcg_kernel_layernorm_bwd(P(dev(dy)), P(dx_), P(dw_), P(mu), P(rs), P(dev(dres)), P(gx),
+                                             P(gw), P(gb), rows, D, P(ws), ws.numel(), None))
+    torch.cuda.synchronize()
+    assert rel_l2(yy.cpu(), y.detach()) < 1e-6
+    assert rel_l2(gx.cpu(), x.grad + dres) < 1e-5
+    assert rel_l2(gw.cpu(), w.grad) < 1e-5
+    assert rel_l2(gb.cpu(), b.grad) < 1e-5
+
+
+def _attn_ref(qkv, keep, H, Dh):
+    """Oracle attention (oracle/model.py Block.attention, fp64) on (N,L,3D)."""
+    N, L, D3 = qkv.shape
+    D = D3 // 3
+    q, k, v = qkv.view(N, L, 3, H, Dh).permute(2, 0, 3, 1, 4).unbind(0)
+    s = (q @ k.transpose(-1, -2)) / math.sqrt(Dh)
+    s = s.masked_fill(~keep[:, None, None, :], -1e30)
+    p = torch.softmax(s, -1)
+    return (p @ v).transpose(1, 2).reshape(N, L, D), torch.logsumexp(s, -1)
+
+
+@pytest.mark.parametrize("N,L,H,Dh", [(6, 97, 4, 64), (5, 25, 2, 32), (3, 100, 2, 64), (4, 64, 8, 32), (2, 1, 4, 64)])
+def test_attention_fwd_bwd(N, L, H, Dh, cuda):
+    g = torch.Generator().manual_seed(N * L + H)
+    D = H * Dh
+    qkv = torch.randn(N, L, 3 * D, generator=g).double().requires_grad_()
+    keep = torch.rand(N, L, generator=g) < 0.7
+    keep[:, 0] = True
+    ctx, lse = _attn_ref(qkv, keep, H, Dh)
+    dctx = torch.randn(N, L, D, generator=g).double()
+    ctx.backward(dctx)
+    L_ = native.lib()
+    dq = dev(qkv.detach())
+    dk = dev(keep.float())
+    c, l = empty(N, L, D), empty(N, H, L)
+    native.check(L_.ptcg_kernel_attention_fwd(P(dq), P(dk), P(c), P(l), N, L, H, Dh, None))
+    gq = empty(N, L, 3 * D)
+    native.check(L_.ptcg_kernel_attention_bwd(P(dq), P(dk), P(c), P(l), P(dev(dctx)), P(gq), N, L, H, Dh, None))
+    torch.cuda.synchronize()
+    assert rel_l2(c.cpu(), ctx.detach()) < 1e-5
+    assert rel_l2(l.cpu(), lse.detach()) < 1e-6
+    assert rel_l2(gq.cpu(), qkv.grad) < 1e-5
+    # masked keys receive no gradient in K and V
+    gk = gq.cpu().view(N, L, 3, D)
+    assert torch.all(gk[:, :, 1:][~keep] == 0)
+
+
+def test_attention_rejects_oversized(cuda):
+    a = empty(4)
+    with pytest.raises(native.PtcgError, match="LDS"):
+        native.check(native.lib().ptcg_kernel_attention_fwd(P(a), P(a), P(a), P(a), 1, 300, 1, 64, None))
+
+
+def _ppo_inputs(n, A, seed):
+    rng = np.random.default_rng(seed)
+    scores = rng.standard_normal((n, A + 1)).astype(np.float32)
+    mask = (rng.random((n, A)) < 0.4).astype(np.float32)
+    mask[np.arange(n), rng.integers(0, A, n)] = 1
+    acts = np.array([rng.choice(np.flatnonzero(m)) for m in mask], np.float32)
+    old = rng.normal(-2, 0.5, n).astype(np.float32)
+    adv = rng.standard_normal(n).astype(np.float32)
+    ret = rng.standard_normal(n).astype(np.float32)
+    val = (ret - adv + rng.normal(0, 0.3, n)).astype(np.float32)
+    return scores, mask, acts, old, adv, ret, val
+
+
+@pytest.mark.parametrize("n,A", [(512, 64), (37, 64), (64, 17), (2048, 64)])
+def test_ppo_loss_matches_oracle(n, A, cuda):
+    scores, mask, acts, old, adv, ret, val = _ppo_inputs(n, A, n + A)
+    kw = dict(clip=0.2, vf_clip=0.2, vf_coef=0.5, ent_coef=0.01)
+    T = lambda a: torch.from_numpy(a).double()
+    ref = oppo.ppo_loss(T(scores), T(mask), T(acts), T(old), T(adv), T(ret), T(val), **kw)
+    grad, ratio, nv = empty(n, A + 1), empty(n), empty(n)
+    stats, guard = empty(8), empty(2)
+    idx = np.random.default_rng(1).permutation(n).astype(np.int32)
+    # rows gathered through row_idx: inputs stored permuted
+    inv = np.argsort(idx)
+    L = native.lib()
+    native.check(L.ptcg_ppo_loss_fwd_bwd(
+        P(dev(scores)), n, A, P(dev(mask)), A, None,
+        P(dev(acts)), P(dev(old)), P(dev(adv)), P(dev(ret)), P(dev(val)), None,
+        0.2, 0.2, 0.5, 0.01, P(grad), P(ratio), P(nv), P(stats), P(guard), None))
+    torch.cuda.synchronize()
+    assert rel_l2(grad.cpu(), ref["grad"]) < 1e-5
+    assert rel_l2(ratio.cpu(), ref["ratio"]) < 1e-6
+    st = stats.cpu().double()
+    assert np.allclose(st[:7], ref["stats"], rtol=1e-5, atol=1e-6)
+    assert st[7] == 1.0
+    assert abs(guard[0].item() - ref["stats"][5].item()) < 1e-5 + 1e-5 * abs(ref["stats"][5].item())
+    # row_idx path: per-row inputs live at permuted rows
+    grad2 = empty(n, A + 1)
+    pm = lambda a: dev(a[inv])    # stored so that row r's data sits at position idx[r]
+    native.check(L.ptcg_ppo_loss_fwd_bwd(
+        P(dev(scores)), n, A, P(pm(mask)), A, P(dev(idx, torch.int32)),
+        P(pm(acts)), P(pm(old)), P(pm(adv)), P(pm(ret)), P(pm(val)), None,
+        0.2, 0.2, 0.5, 0.01, P(grad2), None, None, None, None, None))
+    torch.cuda.synchronize()
+    assert rel_l2(grad2.cpu(), ref["grad"]) < 1e-5
+
+
+def test_kl_gate(cuda):
+    L = native.lib()
+    for kl, vf, kt, vt, want in [(0.01, 0.1, 0.05, 0.5, 1.0), (0.06, 0.1, 0.05, 0.5, 0.0),
+                                 (float("nan"), 0.1, 0.05, 0.5, 0.0), (float("nan"), 0.1, 0.0, 0.5, 1.0),
+                                 (0.01, float("inf"), 0.05, 0.5, 0.0), (0.01, 0.7, 0.05, 0.0, 1.0)]:
+        g, sk = empty(1), empty(1)
+        native.check(L.ptcg_kl_gate(P(dev(np.array([kl, vf], np.float32))), kt, vt, P(g), P(sk), None))
+        torch.cuda.synchronize()
+        assert g.item() == want == oppo.kl_gate(kl, vf, kt, vt)
+        assert sk.item() == 1.0 - want
+
+
+def _adam_case(n, seed):
+    rng = np.random.default_rng(seed)
+    p = rng.standard_normal(n).astype(np.float32)
+    g = (rng.standard_normal(n) * 0.1).astype(np.float32)
+    return p, g
+
+
+@pytest.mark.parametrize("n,max_norm", [(4096, 0.5), (1 << 20, 1e6), (4319216, 0.5)])
+def test_adam_matches_torch(n, max_norm, cuda):
+    p, g = _adam_case(n, n)
+    tp = torch.nn.Parameter(torch.from_numpy(p.copy()))
+    opt = oadam.OracleAdam([tp], lr=3e-4)
+    L = native.lib()
+    dp, dm_, dv = dev(p), empty(n), empty(n)
+    step = torch.zeros(1, dtype=torch.int32, device="cuda")
+    ws = empty(native.lib().ptcg_adam_workspace_floats())
+    norm = empty(1)
+    for it in range(3):
+        gi = g * (1 + it)
+        tp.grad = torch.from_numpy(gi.copy())
+        tnorm = opt.step(max_norm)
+        native.check(L.ptcg_adam_step(P(dp), P(dev(gi)), P(dm_), P(dv), n, 3e-4, 0.9, 0.999, 1e-8,
+                                      max_norm, None, P(step), P(norm), P(ws), None))
+    torch.cuda.synchronize()
+    assert step.item() == 3
+    assert abs(norm.item() - float(tnorm)) <= 1e-5 * float(tnorm)
+    m_ref, v_ref = opt.moments()
+    assert rel_l2(dm_.cpu(), m_ref) < 1e-5
+    assert rel_l2(dv.cpu(), v_ref) < 1e-5
+    upd_gpu = dp.cpu().numpy() - p
+    upd_ref = tp.detach().numpy() - p
+    assert rel_l2(upd_gpu, upd_ref) < 1e-4
+
+
+def test_adam_gate_zero_is_bit_exact_noop(cuda):
+    n = 8192
+    p, g = _adam_case(n, 5)
+    g[7] = np.nan
+    L = native.lib()
+    dp, dm_, dv = dev(p), dev(np.full(n, 0.25, np.float32)), dev(np.full(n, 0.5, np.float32))
+    step = torch.full((1,), 4, dtype=torch.int32, device="cuda")
+    ws = empty(L.ptcg_adam_workspace_floats())
+    gate = dev(np.zeros(1, np.float32))
+    dg = dev(g)
+    native.check(L.ptcg_adam_step(P(dp), P(dg), P(dm_), P(dv), n, 1e-3, 0.9, 0.999, 1e-8, 0.5,
+                                  P(gate), P(step), None, P(ws), None))
+    torch.cuda.synchronize()
+    assert np.array_equal(dp.cpu().numpy().view(np.uint32), p.view(np.uint32))
+    assert torch.all(dm_ == 0.25) and torch.all(dv == 0.5) and step.item() == 4
+    assert np.array_equal(dg.cpu().numpy().view(np.uint32), g.view(np.uint32))
+
+
+def test_adam_first_step_is_lr_sign(cuda):
+    n = 4096
+    p, g = _adam_case(n, 9)
+    L = native.lib()
+    dp = dev(p)
+    step = torch.zeros(1, dtype=torch.int32, device="cuda")
+    ws = empty(L.ptcg_adam_workspace_floats())
+    native.check(L.ptcg_adam_step(P(dp), P(dev(g)), P(empty(n)), P(empty(n)), n, 1e-3, 0.9, 0.999, 1e-8,
+                                  1e6, None, P(step), None, P(ws), None))
+    torch.cuda.synchronize()
+    d = dp.cpu().numpy() - p
+    assert np.allclose(d, -1e-3 * np.sign(g), rtol=1e-3, atol=1e-7)

@@ -45,7 +45,7 @@ typedef struct PtcgDims {
 /* Hyper-parameters of one minibatch step (the keys of the reference's
  * build_args train dict, native/train_native.py:251-280, plus Adam's).     */
 typedef struct PtcgHypers {
-    float lr, beta1, beta2, eps;          /* Adam                              */
+    double lr, beta1, beta2, eps;         /* Adam (double: torch's scalars)    */
     float max_grad_norm;                  /* global-norm clip (muon.cu:216)    */
     float clip_coef, vf_clip_coef, vf_coef, ent_coef;   /* PPO              */
     float kl_skip_threshold, vf_skip_threshold;  /* gate; <= 0 disables     */
@@ -120,7 +120,7 @@ int ptcg_kl_gate(const float* guard, float kl_threshold, float vf_threshold,
  * ptcg_adam_workspace_floats() floats.  grads are read, not modified.      */
 int64_t ptcg_adam_workspace_floats(void);
 int ptcg_adam_step(float* weights, float* grads, float* m, float* v, int64_t n,
-                   float lr, float beta1, float beta2, float eps, float max_grad_norm,
+                   double lr, double beta1, double beta2, double eps, float max_grad_norm,
                    const float* gate, int32_t* step, float* norm_out, float* workspace,
                    void* stream);
 

@@ -52,7 +52,7 @@ __global__ __launch_bounds__(NT) void adam_norm_kernel(const float4* __restrict_
 
 __global__ __launch_bounds__(NT) void adam_update_kernel(float4* __restrict__ p,
         const float4* __restrict__ g, float4* __restrict__ m, float4* __restrict__ v, long n4,
-        int nparts, float lr, float b1, float b2, float eps, float max_norm,
+        int nparts, double lr, double b1, double b2, double eps, float max_norm,
         const float* __restrict__ gate, const float* __restrict__ ws, float* __restrict__ norm_out) {
     if (gate && gate[0] == 0.0f) return;
     __shared__ float red[NT];
@@ -73,18 +73,20 @@ __global__ __launch_bounds__(NT) void adam_update_kernel(float4* __restrict__ p,
     __syncthreads();
     const float coef = sh_coef;
     const int t = reinterpret_cast<const int32_t*>(ws + NPART)[0];
-    const float bc1 = 1.0f - powf(b1, (float)t);
-    const float bc2s = sqrtf(1.0f - powf(b2, (float)t));
-    const float step_size = lr / bc1;
-    const float omb1 = 1.0f - b1, omb2 = 1.0f - b2;
+    // scalars in double, rounded once to fp32 (torch keeps them as Python
+    // floats and hands fp32 kernels the rounded value)
+    const float step_size = (float)(lr / (1.0 - pow(b1, (double)t)));
+    const float bc2s = (float)sqrt(1.0 - pow(b2, (double)t));
+    const float omb1 = (float)(1.0 - b1), omb2 = (float)(1.0 - b2);
+    const float b2f = (float)b2, epsf = (float)eps;
     for (long i = (long)blockIdx.x * NT + threadIdx.x; i < n4; i += (long)gridDim.x * NT) {
         float4 gg = g[i], mm = m[i], vv = v[i], pp = p[i];
 #define PT_ADAM_LANE(c)                                             \
         {                                                           \
             const float gc = gg.c * coef;                           \
             mm.c = mm.c + omb1 * (gc - mm.c);                       \
-            vv.c = vv.c * b2 + omb2 * (gc * gc);                    \
-            const float den = sqrtf(vv.c) / bc2s + eps;             \
+            vv.c = vv.c * b2f + omb2 * gc * gc;                     \
+            const float den = sqrtf(vv.c) / bc2s + epsf;            \
             pp.c = pp.c + (-step_size) * (mm.c / den);              \
         }
         PT_ADAM_LANE(x) PT_ADAM_LANE(y) PT_ADAM_LANE(z) PT_ADAM_LANE(w)
@@ -104,8 +106,8 @@ __global__ void adam_step_commit_kernel(const float* gate, int32_t* step, const 
 
 long pt_adam_ws_floats() { return NPART + 4; }
 
-int pt_adam_step(float* w, float* g, float* m, float* v, long n, float lr, float b1, float b2,
-                 float eps, float max_norm, const float* gate, int32_t* step, float* norm_out,
+int pt_adam_step(float* w, float* g, float* m, float* v, long n, double lr, double b1, double b2,
+                 double eps, float max_norm, const float* gate, int32_t* step, float* norm_out,
                  float* ws, hipStream_t s) {
     PT_REQUIRE(n > 0 && n % 4 == 0, "adam: arena length %ld must be a positive multiple of 4", n);
     PT_REQUIRE(((uintptr_t)w | (uintptr_t)g | (uintptr_t)m | (uintptr_t)v) % 16 == 0,

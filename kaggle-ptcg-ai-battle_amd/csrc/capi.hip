@@ -243,8 +243,8 @@ extern "C" int ptcg_kl_gate(const float* guard, float kl_threshold, float vf_thr
     return pt_kl_gate(guard, kl_threshold, vf_threshold, gate, skipped, (hipStream_t)stream);
 }
 
-extern "C" int ptcg_adam_step(float* weights, float* grads, float* m, float* v, int64_t n, float lr,
-                              float beta1, float beta2, float eps, float max_grad_norm,
+extern "C" int ptcg_adam_step(float* weights, float* grads, float* m, float* v, int64_t n, double lr,
+                              double beta1, double beta2, double eps, float max_grad_norm,
                               const float* gate, int32_t* step, float* norm_out, float* workspace,
                               void* stream) {
     PT_REQUIRE(weights && grads && m && v && step && workspace, "adam_step: null buffer");

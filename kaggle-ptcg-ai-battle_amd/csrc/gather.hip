@@ -312,19 +312,22 @@ __global__ void sc_in_bwd_kernel(GatherCtx c, const float* __restrict__ d_sc,
         float* __restrict__ d_gd) {
     const int n = blockIdx.x, NO = c.dm.n_opt, D = c.dm.d, G = c.dm.g, W = c.dx.score_in;
     const int o_r = D, o_g = 2 * D, o_dv = 2 * D + G, o_qr = 2 * D + G + PT_DEC_H;
-    for (int col = threadIdx.x; col < D; col += TB) {
-        const float r = sc[(long)n * NO * W + o_r + col];
+    const int span = max(D, max(G, (int)PT_DEC_H));
+    for (int col = threadIdx.x; col < span; col += TB) {
+        const float r = col < D ? sc[(long)n * NO * W + o_r + col] : 0.f;
         float ar = 0.f, ag = 0.f, adv = 0.f;
         for (int j = 0; j < NO; ++j) {
             const long nj = (long)n * NO + j;
             const float* g = d_sc + nj * W;
-            const float q = sc[nj * W + col];
-            d_q[nj * D + col] = g[col] + g[o_qr + col] * r;
-            ar += g[o_r + col] + g[o_qr + col] * q;
+            if (col < D) {
+                const float q = sc[nj * W + col];
+                d_q[nj * D + col] = g[col] + g[o_qr + col] * r;
+                ar += g[o_r + col] + g[o_qr + col] * q;
+            }
             if (col < G) ag += g[o_g + col];
             if (col < PT_DEC_H) adv += g[o_dv + col];
         }
-        d_h[(long)n * c.dx.l_seq * D + col] += ar;
+        if (col < D) d_h[(long)n * c.dx.l_seq * D + col] += ar;
         if (col < G) d_gd[(long)n * c.dx.bcast_in + col] += ag;
         if (col < PT_DEC_H) d_gd[(long)n * c.dx.bcast_in + G + col] += adv;
     }
@@ -485,7 +488,6 @@ int pt_sc_in_fwd(const GatherCtx& c, const float* h, const float* gd, float* sc_
 }
 int pt_sc_in_bwd(const GatherCtx& c, const float* d_sc, const float* sc_in, float* d_q, float* d_h,
                  float* d_gd, hipStream_t s) {
-    PT_REQUIRE(c.dm.g <= c.dm.d && PT_DEC_H <= c.dm.d, "sc_in bwd: g and the decision width must not exceed d");
     hipLaunchKernelGGL(sc_in_bwd_kernel, dim3(c.N), dim3(TB), 0, s, c, d_sc, sc_in, d_q, d_h, d_gd);
     PT_LAUNCH_CHECK();
     return PTCG_OK;

@@ -45,8 +45,8 @@ int pt_ppo_loss(const float* out, int n, int A, const float* mask, long mask_str
 int pt_kl_gate(const float* guard, float kl_thr, float vf_thr, float* gate, float* skipped,
                hipStream_t s);
 long pt_adam_ws_floats();
-int pt_adam_step(float* w, float* g, float* m, float* v, long n, float lr, float b1, float b2,
-                 float eps, float max_norm, const float* gate, int32_t* step, float* norm_out,
+int pt_adam_step(float* w, float* g, float* m, float* v, long n, double lr, double b1, double b2,
+                 double eps, float max_norm, const float* gate, int32_t* step, float* norm_out,
                  float* ws, hipStream_t s);
 
 // ---- gathers / scatters of the token, decision and option paths (gather.hip)

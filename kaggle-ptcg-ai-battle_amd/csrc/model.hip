@@ -117,7 +117,6 @@ extern "C" int ptcg_model_create(const PtcgDims* dims, PtcgModel** out) {
                "model_create: widths must be multiples of 4");
     PT_REQUIRE(pt_attn_supported(d.l_tok + 1, d.d / d.heads),
                "model_create: attention shape L=%d Dh=%d unsupported", d.l_tok + 1, d.d / d.heads);
-    PT_REQUIRE(d.g <= d.d && PT_DEC_H <= d.d, "model_create: g and decision width must not exceed d");
     PtcgModel* m = new PtcgModel();
     m->dm = d;
     m->dx = pt_dims_x(d);

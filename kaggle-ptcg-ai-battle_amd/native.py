@@ -17,9 +17,10 @@ c_void_p = ctypes.c_void_p
 
 
 class CPtcgHypers(ctypes.Structure):
-    _fields_ = [(n, ctypes.c_float) for n in (
-        "lr", "beta1", "beta2", "eps", "max_grad_norm", "clip_coef", "vf_clip_coef",
-        "vf_coef", "ent_coef", "kl_skip_threshold", "vf_skip_threshold")]
+    _fields_ = [(n, ctypes.c_double) for n in ("lr", "beta1", "beta2", "eps")] + \
+        [(n, ctypes.c_float) for n in (
+            "max_grad_norm", "clip_coef", "vf_clip_coef", "vf_coef", "ent_coef",
+            "kl_skip_threshold", "vf_skip_threshold")]
 
 
 # name -> (restype, argtypes)
@@ -53,7 +54,7 @@ _SIGS = {
     "ptcg_adam_workspace_floats": (ctypes.c_int64, []),
     "ptcg_adam_step": (ctypes.c_int, [
         c_void_p, c_void_p, c_void_p, c_void_p, ctypes.c_int64,
-        ctypes.c_float, ctypes.c_float, ctypes.c_float, ctypes.c_float, ctypes.c_float,
+        ctypes.c_double, ctypes.c_double, ctypes.c_double, ctypes.c_double, ctypes.c_float,
         c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
     "ptcg_trainer_create": (ctypes.c_int, [ctypes.POINTER(CPtcgDims), ctypes.POINTER(CPtcgHypers),
                                            ctypes.c_int, ctypes.POINTER(c_void_p)]),

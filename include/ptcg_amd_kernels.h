@@ -33,7 +33,7 @@ int ptcg_kernel_colsum(const float* X, int64_t ldx, int M, int N, float* out,
 
 /* LayerNorm, eps 1e-5 (pt_ln_fwd / pt_ln_bwd, ptcg_kernels.cuh:132-218).
  * bwd: dx = LN'(dy) [+ dres]; dw, db overwritten; workspace >=
- * ceil(rows/32)*2*D floats.                                                 */
+ * 2048*D floats.                                                          */
 int ptcg_kernel_layernorm_fwd(const float* x, const float* w, const float* b, float* y,
                               float* mean, float* rstd, int rows, int D, void* stream);
 int ptcg_kernel_layernorm_bwd(const float* dy, const float* x, const float* w,

@@ -119,3 +119,6 @@ int pt_linear_dw(const float* dY, const float* X, float* dW, float* db, int rows
 // deterministic column sums: out[n] = sum_m X[m*ldx + n], m < M
 int pt_colsum(const float* X, long ldx, int M, int N, float* out, float* ws, long ws_floats,
               hipStream_t s);
+// same, columns n < split to out_lo[n], the rest to out_hi[n - split]
+int pt_colsum2(const float* X, long ldx, int M, int N, int split, float* out_lo, float* out_hi,
+               float* ws, long ws_floats, hipStream_t s);

@@ -173,29 +173,26 @@ __global__ void splitk_reduce_kernel(float* C, long ldc, const float* part, long
     if (ACCUM) C[o] += s; else C[o] = s;
 }
 
-// partial column sums: block (64 cols x 4 row groups) over a chunk of rows
-constexpr int CS_ROWS = 256;
-__global__ void colsum_partial_kernel(const float* X, long ldx, int M, int N, float* part) {
+// Deterministic column sums in two levels.  Level 1: block (64 columns x 4
+// row groups) sums one slice of rows; level 2: the same shape sums the
+// slice partials.  Every add happens in a fixed order.
+__global__ void colsum_level_kernel(const float* __restrict__ X, long ldx, int M, int N, int chunk,
+                                    float* __restrict__ out, long ldo, int split, float* __restrict__ out_hi) {
     __shared__ float sh[4][64];
-    int c = blockIdx.x * 64 + (threadIdx.x & 63);
-    int rg = threadIdx.x >> 6;
-    int r0 = blockIdx.y * CS_ROWS, r1 = min(M, r0 + CS_ROWS);
+    const int c = blockIdx.x * 64 + (threadIdx.x & 63);
+    const int rg = threadIdx.x >> 6;
+    const int r0 = blockIdx.y * chunk, r1 = min(M, r0 + chunk);
     float s = 0.f;
     if (c < N)
         for (int r = r0 + rg; r < r1; r += 4) s += X[(long)r * ldx + c];
     sh[rg][threadIdx.x & 63] = s;
     __syncthreads();
-    if (rg == 0 && c < N)
-        part[(long)blockIdx.y * N + c] = sh[0][threadIdx.x] + sh[1][threadIdx.x] +
-                                         sh[2][threadIdx.x] + sh[3][threadIdx.x];
-}
-
-__global__ void colsum_final_kernel(const float* part, int chunks, int N, float* out) {
-    int c = blockIdx.x * blockDim.x + threadIdx.x;
-    if (c >= N) return;
-    float s = 0.f;
-    for (int k = 0; k < chunks; ++k) s += part[(long)k * N + c];
-    out[c] = s;
+    if (rg == 0 && c < N) {
+        const float v = ((sh[0][threadIdx.x] + sh[1][threadIdx.x]) + sh[2][threadIdx.x]) + sh[3][threadIdx.x];
+        if (out_hi == nullptr) out[(long)blockIdx.y * ldo + c] = v;
+        else if (c < split) out[c] = v;
+        else out_hi[c - split] = v;
+    }
 }
 
 // Optional launch timing (ptcg_profile_*): a HIP event pair around every
@@ -366,13 +363,24 @@ int pt_linear_dw(const float* dY, const float* X, float* dW, float* db, int rows
     return PTCG_OK;
 }
 
-int pt_colsum(const float* X, long ldx, int M, int N, float* out, float* ws, long ws_floats,
-              hipStream_t s) {
-    int chunks = pt_cdiv(M, CS_ROWS);
-    PT_REQUIRE(ws != nullptr && (long)chunks * N <= ws_floats, "colsum: workspace too small (%d x %d)", chunks, N);
-    hipLaunchKernelGGL(colsum_partial_kernel, dim3(pt_cdiv(N, 64), chunks), dim3(256), 0, s, X, ldx, M, N, ws);
+int pt_colsum2(const float* X, long ldx, int M, int N, int split, float* out_lo, float* out_hi,
+               float* ws, long ws_floats, hipStream_t s) {
+    PT_REQUIRE(M > 0 && N > 0, "colsum: empty shape %d x %d", M, N);
+    int slices = pt_cdiv(M, 64);
+    if (slices > 256) slices = 256;
+    const int chunk = pt_cdiv(M, slices);
+    slices = pt_cdiv(M, chunk);
+    PT_REQUIRE(ws != nullptr && (long)slices * N <= ws_floats, "colsum: workspace too small (%d x %d)", slices, N);
+    hipLaunchKernelGGL(colsum_level_kernel, dim3(pt_cdiv(N, 64), slices), dim3(256), 0, s, X, ldx, M, N, chunk,
+                       ws, (long)N, 0, nullptr);
     PT_LAUNCH_CHECK();
-    hipLaunchKernelGGL(colsum_final_kernel, dim3(pt_cdiv(N, 256)), dim3(256), 0, s, ws, chunks, N, out);
+    hipLaunchKernelGGL(colsum_level_kernel, dim3(pt_cdiv(N, 64), 1), dim3(256), 0, s, ws, (long)N, slices, N,
+                       slices, out_lo, 0L, out_hi ? split : N, out_hi ? out_hi : out_lo + N);
     PT_LAUNCH_CHECK();
     return PTCG_OK;
+}
+
+int pt_colsum(const float* X, long ldx, int M, int N, float* out, float* ws, long ws_floats,
+              hipStream_t s) {
+    return pt_colsum2(X, ldx, M, N, N, out, nullptr, ws, ws_floats, s);
 }

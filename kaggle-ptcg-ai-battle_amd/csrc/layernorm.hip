@@ -4,14 +4,15 @@
 // one wave64 per row with the row held in registers as float4s (the
 // reference uses one 128-thread block per row), two-pass mean/variance.
 // Backward writes dx (optionally adding a residual gradient in the same
-// pass) and per-block dW/dB partials that a second kernel sums in fixed
-// order — deterministic, where the reference issues one atomicAdd per
-// element per row into 2*D addresses.
+// pass) and per-workgroup dW/dB partials (512 workgroups stride over the
+// rows) that a two-level column sum folds in fixed order — deterministic,
+// where the reference issues one atomicAdd per element per row into 2*D
+// addresses.
 #include "common.h"
 
 namespace {
 
-constexpr int LN_ROWS_PER_BLOCK_BWD = 32;
+constexpr int LN_BWD_BLOCKS = 512;   // partial rows of dW/dB (grid-stride over rows)
 
 template <int VPL>
 __global__ __launch_bounds__(256) void ln_fwd_kernel(const float* __restrict__ x, long ldx,
@@ -82,10 +83,7 @@ __global__ __launch_bounds__(256) void ln_bwd_kernel(const float* __restrict__ d
         const int col = (lane + 64 * c) * 4;
         wv[c] = col < D ? *reinterpret_cast<const float4*>(w + col) : aw[c];
     }
-    const int r0 = blockIdx.x * LN_ROWS_PER_BLOCK_BWD;
-    for (int rr = wave; rr < LN_ROWS_PER_BLOCK_BWD; rr += 4) {
-        const int row = r0 + rr;
-        if (row >= rows) break;
+    for (int row = blockIdx.x * 4 + wave; row < rows; row += gridDim.x * 4) {
         const float mu = mean[row], rs = rstd[row];
         const float* xr = x + (long)row * ldx;
         const float* dyr = dy + (long)row * lddy;
@@ -153,19 +151,6 @@ __global__ __launch_bounds__(256) void ln_bwd_kernel(const float* __restrict__ d
     }
 }
 
-__global__ void ln_part_reduce_kernel(const float* __restrict__ part, int blocks, int D,
-                                      float* __restrict__ dw, float* __restrict__ db) {
-    const int c = blockIdx.x * blockDim.x + threadIdx.x;
-    if (c >= 2 * D) return;
-    float s = 0.f;
-    for (int k = 0; k < blocks; ++k) s += part[(long)k * 2 * D + c];
-    if (c < D) {
-        if (dw) dw[c] = s;
-    } else {
-        if (db) db[c - D] = s;
-    }
-}
-
 }  // namespace
 
 int pt_ln_fwd(const float* x, long ldx, const float* w, const float* b, float* y, long ldy,
@@ -187,8 +172,9 @@ int pt_ln_bwd(const float* dy, long lddy, const float* x, long ldx, const float*
               long lddx, float* dw, float* db, int rows, int D, float* ws, long ws_floats,
               hipStream_t s) {
     PT_REQUIRE(D % 4 == 0 && D <= 1024, "layernorm bwd: D=%d unsupported", D);
-    const int blocks = pt_cdiv(rows, LN_ROWS_PER_BLOCK_BWD);
-    PT_REQUIRE(ws && (long)blocks * 2 * D <= ws_floats, "layernorm bwd: workspace too small");
+    int blocks = pt_cdiv(rows, 4);
+    if (blocks > LN_BWD_BLOCKS) blocks = LN_BWD_BLOCKS;
+    PT_REQUIRE(ws && (long)blocks * 2 * D * 2 <= ws_floats, "layernorm bwd: workspace too small");
     dim3 grid(blocks);
     if (D <= 256)
         hipLaunchKernelGGL(ln_bwd_kernel<1>, grid, dim3(256), 0, s, dy, lddy, x, ldx, w, mean, rstd, dres, ldres, dx, lddx, ws, rows, D);
@@ -197,7 +183,9 @@ int pt_ln_bwd(const float* dy, long lddy, const float* x, long ldx, const float*
     else
         hipLaunchKernelGGL(ln_bwd_kernel<4>, grid, dim3(256), 0, s, dy, lddy, x, ldx, w, mean, rstd, dres, ldres, dx, lddx, ws, rows, D);
     PT_LAUNCH_CHECK();
-    hipLaunchKernelGGL(ln_part_reduce_kernel, dim3(pt_cdiv(2 * D, 256)), dim3(256), 0, s, ws, blocks, D, dw, db);
-    PT_LAUNCH_CHECK();
+    if (dw && db)
+        return pt_colsum2(ws, 2 * D, blocks, 2 * D, D, dw, db, ws + (long)blocks * 2 * D,
+                          ws_floats - (long)blocks * 2 * D, s);
+    PT_REQUIRE(!dw && !db, "layernorm bwd: dw and db must both be given or both be NULL");
     return PTCG_OK;
 }

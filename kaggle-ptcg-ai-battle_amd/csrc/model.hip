@@ -243,7 +243,7 @@ static size_t carve(PtcgModel* m, char* base) {
     m->dbc = c.take(N * D);
     // workspace: split-K partials, column-sum / LayerNorm / head partials
     m->ws_floats = 16L << 20;
-    long ln_part = (long)pt_cdiv(NL, 32) * 2 * D;
+    long ln_part = 2048L * D;   // LayerNorm dW/dB partials (layernorm.hip)
     if (ln_part > m->ws_floats) m->ws_floats = ln_part;
     m->ws = c.take(m->ws_floats);
     return c.off;

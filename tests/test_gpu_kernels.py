@@ -140,7 +140,9 @@ def _attn_ref(qkv, keep, H, Dh):
     return (p @ v).transpose(1, 2).reshape(N, L, D), torch.logsumexp(s, -1)
 
 
-@pytest.mark.parametrize("N,L,H,Dh", [(6, 97, 4, 64), (5, 25, 2, 32), (3, 100, 2, 64), (4, 64, 8, 32), (2, 1, 4, 64)])
+@pytest.mark.parametrize("N,L,H,Dh", [(6, 97, 4, 64), (5, 25, 2, 32), (3, 100, 2, 64), (4, 64, 8, 32), (2, 1, 4, 64),
+                                      (3, 128, 2, 32), (2, 17, 1, 64),
+                                      (2, 140, 2, 32)])   # L=140/Dh=32: beyond the MFMA kernel's LDS budget -> VALU kernel
 def test_attention_fwd_bwd(N, L, H, Dh, cuda):
     g = torch.Generator().manual_seed(N * L + H)
     D = H * Dh

@@ -7,6 +7,13 @@
 #include "../../include/ptcg_amd.h"
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
+// global-address-space views (lets the compiler emit global_load, not flat_load)
+typedef __attribute__((address_space(1))) float gfloat;
+typedef __attribute__((address_space(1))) floatx4 gfloatx4;
+__device__ __forceinline__ float4 ld_g4(const gfloat* p) {
+    const floatx4 v = *(const gfloatx4*)p;
+    return make_float4(v[0], v[1], v[2], v[3]);
+}
 
 // ---------------------------------------------------------------- errors
 void ptcg_set_error(const char* fmt, ...);

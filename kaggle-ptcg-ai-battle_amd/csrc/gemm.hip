@@ -3,11 +3,12 @@
 // Replaces the reference's cuBLAS GemmEx wrappers pt_gemm / pt_linear /
 // pt_linear_bwd / pt_bias_grad (native/model/ptcg_kernels.cuh:42-108) with
 // one templated kernel: 128x128 block tile, BK = 16, 256 threads = 4 waves
-// in a 2x2 grid, each wave a 64x64 sub-tile of 4x4 MFMA 16x16 tiles.  Both
-// operands are staged k-major in LDS (row = k, 4-float pad) so every MFMA
-// operand fetch is one conflict-free ds_read_b32 per lane; global->LDS uses
-// 128-bit loads along whichever dimension is contiguous in memory, double
-// buffered (prefetch of tile t+1 overlaps the MFMAs of tile t).  Epilogues
+// in a 2x2 grid, each wave a 64x64 sub-tile of 4x4 MFMA 16x16 tiles.
+// Global->LDS moves 128-bit vectors along whichever dimension is contiguous
+// in memory, double buffered (the prefetch of tile t+1 overlaps the MFMAs of
+// tile t), and is stored without transposition; the MFMA k order is chosen
+// so a k-contiguous fragment is a single 128-bit LDS read per four MFMA
+// steps.  Tiles are ordered per XCD (L2 reuse of the A rows).  Epilogues
 // fuse bias, exact GELU (keeping the pre-activation), residual add and the
 // GELU backward multiply.  Weight gradients (K = rows, small M*N) split K
 // across blocks and sum the partials in a fixed order, so results do not
@@ -18,16 +19,37 @@
 
 namespace {
 
-constexpr int BM = 128, BN = 128, BK = 16, PAD = 4;
-constexpr int SA = BM + PAD, SB = BN + PAD;
+constexpr int BM = 128, BN = 128, BK = 16;
 constexpr int NT = 256;
+// LDS layouts.  A k-contiguous operand is staged [row][k] (stride BK+4: the
+// 128-bit fragment reads of 8 consecutive rows cover all 32 banks); an
+// m-contiguous operand is staged [k][row] (stride BM+4: rows 4 apart land 16
+// banks apart).  Both use the same k order: lane group lq of an MFMA step kk
+// supplies k = 4*lq + kk, so a [row][k] fragment is one 128-bit read serving
+// four MFMA steps.
+constexpr int SK = BK + 4;      // [row][k] stride
+constexpr int SM = BM + 4;      // [k][row] stride
+template <bool T> struct Stage { static constexpr int floats = T ? BK * SM : BM * SK; };
+
+// XCD-aware tile order: workgroups are dealt round-robin to the 8 XCDs, so
+// hand XCD x a contiguous range of logical tiles (all N-tiles of a run of
+// M-tiles) and the A rows stay in that XCD's L2.
+__device__ __forceinline__ void tile_of(int b, int tiles, int tn, int& tm_i, int& tn_i) {
+    int lb = b;
+    if ((tiles & 7) == 0) lb = (b & 7) * (tiles >> 3) + (b >> 3);
+    tm_i = lb / tn;
+    tn_i = lb % tn;
+}
 
 template <bool AT, bool BT, int EPI, bool PARTIAL>
 __global__ __launch_bounds__(NT) void gemm_f32_kernel(GemmArgs g, int k_chunk, long part_stride) {
-    __shared__ float As[2][BK][SA];
-    __shared__ float Bs[2][BK][SB];
+    __shared__ __align__(16) float As[2][Stage<AT>::floats];
+    __shared__ __align__(16) float Bs[2][Stage<BT>::floats];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+    const int tm = (g.M + BM - 1) / BM, tn = (g.N + BN - 1) / BN;
+    int tmi, tni;
+    tile_of(blockIdx.x, tm * tn, tn, tmi, tni);
+    const int m0 = tmi * BM, n0 = tni * BN;
     const int kbeg = blockIdx.z * k_chunk;
     const int kend = min(g.K, kbeg + k_chunk);
     const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
@@ -39,92 +61,74 @@ __global__ __launch_bounds__(NT) void gemm_f32_kernel(GemmArgs g, int k_chunk, l
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-    float4 ra[2], rb[2];
+    // operands are global memory: say so, or the loads become flat loads that
+    // also count against lgkmcnt and stall the LDS waits on global latency
+    const gfloat* __restrict__ Ag = (const gfloat*)(g.A);
+    const gfloat* __restrict__ Bg = (const gfloat*)(g.B);
     const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
-
-    auto gload = [&](int k0) {
-#pragma unroll
-        for (int it = 0; it < 2; ++it) {
-            const int idx = tid + it * NT;
-            if (!AT) {
-                const int row = idx >> 2, kq = idx & 3;
-                const int gm = m0 + row, gk = k0 + kq * 4;
-                ra[it] = (gm < g.M && gk < kend)
-                             ? *reinterpret_cast<const float4*>(g.A + (long)gm * g.lda + gk) : z4;
-            } else {
-                const int kr = idx >> 5, mq = idx & 31;
-                const int gk = k0 + kr, gm = m0 + mq * 4;
-                ra[it] = (gk < kend && gm < g.M)
-                             ? *reinterpret_cast<const float4*>(g.A + (long)gk * g.lda + gm) : z4;
-            }
-            if (!BT) {
-                const int row = idx >> 2, kq = idx & 3;
-                const int gn = n0 + row, gk = k0 + kq * 4;
-                rb[it] = (gn < g.N && gk < kend)
-                             ? *reinterpret_cast<const float4*>(g.B + (long)gn * g.ldb + gk) : z4;
-            } else {
-                const int kr = idx >> 5, nq = idx & 31;
-                const int gk = k0 + kr, gn = n0 + nq * 4;
-                rb[it] = (gk < kend && gn < g.N)
-                             ? *reinterpret_cast<const float4*>(g.B + (long)gk * g.ldb + gn) : z4;
-            }
-        }
-    };
-    auto sstore = [&](int buf) {
-#pragma unroll
-        for (int it = 0; it < 2; ++it) {
-            const int idx = tid + it * NT;
-            if (!AT) {
-                const int row = idx >> 2, kq = idx & 3;
-                As[buf][kq * 4 + 0][row] = ra[it].x;
-                As[buf][kq * 4 + 1][row] = ra[it].y;
-                As[buf][kq * 4 + 2][row] = ra[it].z;
-                As[buf][kq * 4 + 3][row] = ra[it].w;
-            } else {
-                const int kr = idx >> 5, mq = idx & 31;
-                *reinterpret_cast<float4*>(&As[buf][kr][mq * 4]) = ra[it];
-            }
-            if (!BT) {
-                const int row = idx >> 2, kq = idx & 3;
-                Bs[buf][kq * 4 + 0][row] = rb[it].x;
-                Bs[buf][kq * 4 + 1][row] = rb[it].y;
-                Bs[buf][kq * 4 + 2][row] = rb[it].z;
-                Bs[buf][kq * 4 + 3][row] = rb[it].w;
-            } else {
-                const int kr = idx >> 5, nq = idx & 31;
-                *reinterpret_cast<float4*>(&Bs[buf][kr][nq * 4]) = rb[it];
-            }
-        }
-    };
+    // per-thread staging slots: 128 rows x 16 k = 512 float4 per operand, two per thread
+    // (T == false: row idx>>2, k quarter idx&3; T == true: k row idx>>5, 4-row group idx&31)
+    const int i0 = tid, i1 = tid + NT;
+    const int ra0 = AT ? (i0 & 31) * 4 : (i0 >> 2), rk0 = AT ? (i0 >> 5) : (i0 & 3) * 4;
+    const int ra1 = AT ? (i1 & 31) * 4 : (i1 >> 2), rk1 = AT ? (i1 >> 5) : (i1 & 3) * 4;
+    const int rb0 = BT ? (i0 & 31) * 4 : (i0 >> 2), kb0 = BT ? (i0 >> 5) : (i0 & 3) * 4;
+    const int rb1 = BT ? (i1 & 31) * 4 : (i1 >> 2), kb1 = BT ? (i1 >> 5) : (i1 & 3) * 4;
+    const int sa0 = AT ? rk0 * SM + ra0 : ra0 * SK + rk0, sa1 = AT ? rk1 * SM + ra1 : ra1 * SK + rk1;
+    const int sb0 = BT ? kb0 * SM + rb0 : rb0 * SK + kb0, sb1 = BT ? kb1 * SM + rb1 : rb1 * SK + kb1;
+#define PT_LD(X, ld, lim, r0, T, rr, kk, k0)                                                   \
+    (((r0) + (rr) < (lim) && (k0) + (kk) < kend)                                                \
+         ? ld_g4((X) + ((T) ? (long)((k0) + (kk)) * (ld) + (r0) + (rr)                       \
+                            : (long)((r0) + (rr)) * (ld) + (k0) + (kk)))                        \
+         : z4)
+    float4 va0, va1, vb0, vb1;
+#define PT_GLOAD(k0)                                           \
+    va0 = PT_LD(Ag, g.lda, g.M, m0, AT, ra0, rk0, k0);         \
+    va1 = PT_LD(Ag, g.lda, g.M, m0, AT, ra1, rk1, k0);         \
+    vb0 = PT_LD(Bg, g.ldb, g.N, n0, BT, rb0, kb0, k0);         \
+    vb1 = PT_LD(Bg, g.ldb, g.N, n0, BT, rb1, kb1, k0);
+#define PT_SSTORE(buf)                                         \
+    *reinterpret_cast<float4*>(&As[buf][sa0]) = va0;           \
+    *reinterpret_cast<float4*>(&As[buf][sa1]) = va1;           \
+    *reinterpret_cast<float4*>(&Bs[buf][sb0]) = vb0;           \
+    *reinterpret_cast<float4*>(&Bs[buf][sb1]) = vb1;
 
     if (kbeg < kend) {
-        gload(kbeg);
-        sstore(0);
+        PT_GLOAD(kbeg)
+        PT_SSTORE(0)
         __syncthreads();
         int buf = 0;
         for (int k0 = kbeg; k0 < kend; k0 += BK) {
             const bool more = k0 + BK < kend;
-            if (more) gload(k0 + BK);
+            if (more) { PT_GLOAD(k0 + BK) }
+            const float* Ab = As[buf];
+            const float* Bb = Bs[buf];
+            float4 af[4], bf[4];
 #pragma unroll
-            for (int kk = 0; kk < BK / 4; ++kk) {
-                float a[4], b[4];
-#pragma unroll
-                for (int t = 0; t < 4; ++t) a[t] = As[buf][kk * 4 + lq][wm + t * 16 + li];
-#pragma unroll
-                for (int t = 0; t < 4; ++t) b[t] = Bs[buf][kk * 4 + lq][wn + t * 16 + li];
-#pragma unroll
-                for (int ti = 0; ti < 4; ++ti)
-#pragma unroll
-                    for (int tj = 0; tj < 4; ++tj)
-                        acc[ti][tj] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[ti], b[tj], acc[ti][tj], 0, 0, 0);
+            for (int t = 0; t < 4; ++t) {
+                if (!AT) af[t] = *reinterpret_cast<const float4*>(Ab + (wm + t * 16 + li) * SK + 4 * lq);
+                else af[t] = make_float4(Ab[(4 * lq + 0) * SM + wm + t * 16 + li], Ab[(4 * lq + 1) * SM + wm + t * 16 + li],
+                                         Ab[(4 * lq + 2) * SM + wm + t * 16 + li], Ab[(4 * lq + 3) * SM + wm + t * 16 + li]);
+                if (!BT) bf[t] = *reinterpret_cast<const float4*>(Bb + (wn + t * 16 + li) * SK + 4 * lq);
+                else bf[t] = make_float4(Bb[(4 * lq + 0) * SM + wn + t * 16 + li], Bb[(4 * lq + 1) * SM + wn + t * 16 + li],
+                                         Bb[(4 * lq + 2) * SM + wn + t * 16 + li], Bb[(4 * lq + 3) * SM + wn + t * 16 + li]);
             }
-            if (more) sstore(buf ^ 1);
+#define PT_MFMA_STEP(c)                                                                             \
+            _Pragma("unroll") for (int ti = 0; ti < 4; ++ti)                                        \
+            _Pragma("unroll") for (int tj = 0; tj < 4; ++tj)                                        \
+                acc[ti][tj] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[ti].c, bf[tj].c, acc[ti][tj], 0, 0, 0);
+            PT_MFMA_STEP(x) PT_MFMA_STEP(y) PT_MFMA_STEP(z) PT_MFMA_STEP(w)
+#undef PT_MFMA_STEP
+            if (more) { PT_SSTORE(buf ^ 1) }
             __syncthreads();
             buf ^= 1;
         }
     }
+#undef PT_GLOAD
+#undef PT_SSTORE
+#undef PT_LD
 
     // epilogue: acc[ti][tj][r] = C[wm + ti*16 + 4*lq + r][wn + tj*16 + li]
+    const long zoff = PARTIAL ? (long)blockIdx.z * part_stride : 0;
 #pragma unroll
     for (int ti = 0; ti < 4; ++ti)
 #pragma unroll
@@ -140,7 +144,7 @@ __global__ __launch_bounds__(NT) void gemm_f32_kernel(GemmArgs g, int k_chunk, l
                 if (m >= g.M) continue;
                 float v = acc[ti][tj][r];
                 if (PARTIAL) {
-                    g.C[(long)blockIdx.z * part_stride + (long)m * g.ldc + n] = v;
+                    g.C[zoff + (long)m * g.ldc + n] = v;
                 } else if (EPI == EPI_STORE) {
                     g.C[(long)m * g.ldc + n] = v;
                 } else if (EPI == EPI_BIAS) {
@@ -278,7 +282,7 @@ int pt_gemm(const GemmArgs& g, float* ws, long ws_floats, hipStream_t s) {
         k_chunk = pt_cdiv(pt_cdiv(g.K, splits), BK) * BK;
         splits = pt_cdiv(g.K, k_chunk);
     }
-    dim3 grid(tn, tm, splits);
+    dim3 grid(tn * tm, 1, splits);
     const int code = (g.a_t ? 1 : 0) * 2 + (g.b_t ? 1 : 0);
     if (splits > 1) {
         GemmArgs p = g;

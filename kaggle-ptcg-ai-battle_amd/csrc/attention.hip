@@ -214,9 +214,11 @@ __global__ __launch_bounds__(256) void attn_bwd_kernel(const float* __restrict__
 // key dimension — so P goes from accumulators to the P.V product without
 // touching LDS (B supplies V rows in the same key order).  The padded length
 // Lp = 16 * ceil(L / 16); padded keys score -inf, padded rows are zero.
+// 8 waves per workgroup: one 16-row stripe each (Lp <= 128), two waves per
+// SIMD to overlap LDS reads with MFMAs.
 
 template <int DH, int NT>   // NT = Lp / 16 key (and query) tiles
-__global__ __launch_bounds__(256) void attn_fwd_mfma_kernel(const float* __restrict__ qkv,
+__global__ __launch_bounds__(512) void attn_fwd_mfma_kernel(const float* __restrict__ qkv,
         const float* __restrict__ keep, float* __restrict__ ctx, float* __restrict__ lse,
         int L, int H, float scale) {
     constexpr int LP = NT * 16, SK = DH + 4;
@@ -227,22 +229,22 @@ __global__ __launch_bounds__(256) void attn_fwd_mfma_kernel(const float* __restr
     const int li = lane & 15, lq = lane >> 4;
     const int n = blockIdx.x / H, h = blockIdx.x % H;
     const int D = H * DH;
-    const float* base = qkv + (long)n * L * 3 * D + h * DH;
-    for (int idx = tid; idx < LP * (DH / 4); idx += 256) {
+    const gfloat* base = (const gfloat*)qkv + (long)n * L * 3 * D + h * DH;
+    for (int idx = tid; idx < LP * (DH / 4); idx += 512) {
         const int l = idx / (DH / 4), c4 = (idx % (DH / 4)) * 4;
         float4 k4 = make_float4(0.f, 0.f, 0.f, 0.f), v4 = k4;
         if (l < L) {
-            const float* r = base + (long)l * 3 * D + c4;
-            k4 = *reinterpret_cast<const float4*>(r + D);
-            v4 = *reinterpret_cast<const float4*>(r + 2 * D);
+            const gfloat* r = base + (long)l * 3 * D + c4;
+            k4 = ld_g4(r + D);
+            v4 = ld_g4(r + 2 * D);
         }
         *reinterpret_cast<float4*>(&Ks[l * SK + c4]) = k4;
         *reinterpret_cast<float4*>(&Vs[l * SK + c4]) = v4;
     }
-    for (int l = tid; l < LP; l += 256) kf[l] = l < L ? (keep[(long)n * L + l] != 0.f ? 1.f : 0.f) : -1.f;
+    for (int l = tid; l < LP; l += 512) kf[l] = l < L ? (keep[(long)n * L + l] != 0.f ? 1.f : 0.f) : -1.f;
     __syncthreads();
 
-    for (int st = wave; st < NT; st += 4) {
+    for (int st = wave; st < NT; st += 8) {
         const int q0 = st * 16;
         // Q^T as the B operand: lane (li = query, lq) holds Q[q0+li][4kk+lq]
         float qb[DH / 4];
@@ -301,7 +303,7 @@ __global__ __launch_bounds__(256) void attn_fwd_mfma_kernel(const float* __restr
             const float inv = 1.0f / __shfl(sum, 4 * lq + r, 64);
             const int q = q0 + 4 * lq + r;
             if (q < L) {
-                float* dst = ctx + ((long)n * L + q) * D + h * DH + li;
+                gfloat* dst = (gfloat*)ctx + ((long)n * L + q) * D + h * DH + li;
 #pragma unroll
                 for (int dt = 0; dt < DH / 16; ++dt) dst[16 * dt] = o[dt][r] * inv;
             }
@@ -316,7 +318,7 @@ __global__ __launch_bounds__(256) void attn_fwd_mfma_kernel(const float* __restr
 // (register-r trick again, now over queries), and parks dS*scale in LDS.
 // Pass B walks query stripes: dQ = dS K from LDS.
 template <int DH, int NT>
-__global__ __launch_bounds__(256) void attn_bwd_mfma_kernel(const float* __restrict__ qkv,
+__global__ __launch_bounds__(512) void attn_bwd_mfma_kernel(const float* __restrict__ qkv,
         const float* __restrict__ keep, const float* __restrict__ ctx,
         const float* __restrict__ lse, const float* __restrict__ dctx,
         float* __restrict__ dqkv, int L, int H, float scale) {
@@ -333,29 +335,29 @@ __global__ __launch_bounds__(256) void attn_bwd_mfma_kernel(const float* __restr
     const int li = lane & 15, lq = lane >> 4;
     const int n = blockIdx.x / H, h = blockIdx.x % H;
     const int D = H * DH;
-    const float* base = qkv + (long)n * L * 3 * D + h * DH;
-    const float* ob = ctx + (long)n * L * D + h * DH;
-    const float* dob = dctx + (long)n * L * D + h * DH;
-    float* gb = dqkv + (long)n * L * 3 * D + h * DH;
-    for (int idx = tid; idx < LP * (DH / 4); idx += 256) {
+    const gfloat* base = (const gfloat*)qkv + (long)n * L * 3 * D + h * DH;
+    const gfloat* ob = (const gfloat*)ctx + (long)n * L * D + h * DH;
+    const gfloat* dob = (const gfloat*)dctx + (long)n * L * D + h * DH;
+    gfloat* gb = (gfloat*)dqkv + (long)n * L * 3 * D + h * DH;
+    for (int idx = tid; idx < LP * (DH / 4); idx += 512) {
         const int l = idx / (DH / 4), c4 = (idx % (DH / 4)) * 4;
         float4 q4 = make_float4(0.f, 0.f, 0.f, 0.f), k4 = q4, d4 = q4;
         if (l < L) {
-            const float* r = base + (long)l * 3 * D + c4;
-            q4 = *reinterpret_cast<const float4*>(r);
-            k4 = *reinterpret_cast<const float4*>(r + D);
-            d4 = *reinterpret_cast<const float4*>(dob + (long)l * D + c4);
+            const gfloat* r = base + (long)l * 3 * D + c4;
+            q4 = ld_g4(r);
+            k4 = ld_g4(r + D);
+            d4 = ld_g4(dob + (long)l * D + c4);
         }
         *reinterpret_cast<float4*>(&Qs[l * SQ + c4]) = q4;
         *reinterpret_cast<float4*>(&dOs[l * SQ + c4]) = d4;
         *reinterpret_cast<float4*>(&Ks[l * SKB + c4]) = k4;
     }
-    for (int l = tid; l < LP; l += 256) {
+    for (int l = tid; l < LP; l += 512) {
         kf[l] = l < L ? (keep[(long)n * L + l] != 0.f ? 1.f : 0.f) : 0.f;
         ls[l] = l < L ? lse[((long)n * H + h) * L + l] : INFINITY;
     }
     // Dv[q] = sum_d dO[q][d] O[q][d]   (a wave per row; padded rows 0)
-    for (int q = wave; q < LP; q += 4) {
+    for (int q = wave; q < LP; q += 8) {
         float v = 0.f;
         if (q < L)
             for (int d = lane; d < DH; d += 64) v += dob[(long)q * D + d] * ob[(long)q * D + d];
@@ -365,7 +367,7 @@ __global__ __launch_bounds__(256) void attn_bwd_mfma_kernel(const float* __restr
     __syncthreads();
 
     // ---- pass A: key stripes
-    for (int kb = wave; kb < NT; kb += 4) {
+    for (int kb = wave; kb < NT; kb += 8) {
         const int k0 = kb * 16;
         const bool kv = k0 + li < L;
         float kr[DH / 4], vr[DH / 4];    // B operands: lane (li = key, lq) holds K/V[k0+li][4kk+lq]
@@ -413,7 +415,7 @@ __global__ __launch_bounds__(256) void attn_bwd_mfma_kernel(const float* __restr
         for (int r = 0; r < 4; ++r) {
             const int key = k0 + 4 * lq + r;
             if (key < L) {
-                float* g = gb + (long)key * 3 * D + li;
+                gfloat* g = gb + (long)key * 3 * D + li;
 #pragma unroll
                 for (int dt = 0; dt < DH / 16; ++dt) {
                     g[D + 16 * dt] = dk[dt][r] * scale;
@@ -425,7 +427,7 @@ __global__ __launch_bounds__(256) void attn_bwd_mfma_kernel(const float* __restr
     __syncthreads();
 
     // ---- pass B: query stripes, dQ = (dS*scale) K
-    for (int qt = wave; qt < NT; qt += 4) {
+    for (int qt = wave; qt < NT; qt += 8) {
         floatx4 dq[DH / 16];
 #pragma unroll
         for (int dt = 0; dt < DH / 16; ++dt) dq[dt] = floatx4{0.f, 0.f, 0.f, 0.f};
@@ -440,7 +442,7 @@ __global__ __launch_bounds__(256) void attn_bwd_mfma_kernel(const float* __restr
         for (int r = 0; r < 4; ++r) {
             const int q = 16 * qt + 4 * lq + r;
             if (q < L) {
-                float* g = gb + (long)q * 3 * D + li;
+                gfloat* g = gb + (long)q * 3 * D + li;
 #pragma unroll
                 for (int dt = 0; dt < DH / 16; ++dt) g[16 * dt] = dq[dt][r];
             }
@@ -455,7 +457,7 @@ size_t bwd_mfma_lds_bytes(int LP, int DH) {
 template <int DH, int NT>
 int launch_fwd_mfma(const float* qkv, const float* keep, float* ctx, float* lse, int N, int L, int H,
                     hipStream_t s) {
-    hipLaunchKernelGGL((attn_fwd_mfma_kernel<DH, NT>), dim3(N * H), dim3(256), 0, s, qkv, keep, ctx, lse,
+    hipLaunchKernelGGL((attn_fwd_mfma_kernel<DH, NT>), dim3(N * H), dim3(512), 0, s, qkv, keep, ctx, lse,
                        L, H, 1.0f / sqrtf((float)DH));
     PT_LAUNCH_CHECK();
     return PTCG_OK;
@@ -467,7 +469,7 @@ int launch_bwd_mfma(const float* qkv, const float* keep, const float* ctx, const
     const size_t lds = bwd_mfma_lds_bytes(NT * 16, DH);
     PT_HIP(hipFuncSetAttribute((const void*)attn_bwd_mfma_kernel<DH, NT>,
                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-    hipLaunchKernelGGL((attn_bwd_mfma_kernel<DH, NT>), dim3(N * H), dim3(256), lds, s, qkv, keep, ctx, lse,
+    hipLaunchKernelGGL((attn_bwd_mfma_kernel<DH, NT>), dim3(N * H), dim3(512), lds, s, qkv, keep, ctx, lse,
                        dctx, dqkv, L, H, 1.0f / sqrtf((float)DH));
     PT_LAUNCH_CHECK();
     return PTCG_OK;

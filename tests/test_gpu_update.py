@@ -1,0 +1,61 @@
+"""Full PPO update at the training configuration (GPU vs the CPU oracle).
+
+16 384-row rollout at the CORE dims; 4 epochs x 8 minibatches of 512 rows from
+seeded permutations (the same index lists for both sides); global-norm clip 0.5
+then Adam (lr 3e-4, betas 0.9/0.999, eps 1e-8).  The weight blob after the 32nd
+step must agree at relative L2 1e-4; every element within 2*lr*steps (Adam's
+normalised step near g = 0 is a sign function of rounding noise).  The loss
+statistics summed over the 32 minibatches agree at relative 1e-3 (clipfrac
+counts ratio comparisons at the clip boundary, which rounding can flip).
+
+The oracle takes ~1-2 minutes on 16 host threads, hence the long timeout.
+"""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import rel_l2
+from ptcg_amd import dims, synth, trainer
+import oracle.model as om
+import oracle.adam as oadam
+import oracle.step as ostep
+
+pytestmark = pytest.mark.gpu
+
+HYP = dict(clip_coef=0.2, vf_clip_coef=0.2, vf_coef=0.5, ent_coef=0.01, max_grad_norm=0.5)
+
+
+@pytest.mark.timeout(900)
+def test_full_update_4_epochs_x_8_minibatches(cuda):
+    torch.set_num_threads(min(16, os.cpu_count() or 1))
+    dm, B, R, epochs, per_epoch = dims.CORE, 512, 16384, 4, 8
+    steps = epochs * per_epoch
+    ref = om.build(dm, seed=41)
+    w0 = ref.to_blob()
+    rows = synth.make_obs(dm, R, seed=42)
+    inp = synth.make_ppo_inputs(dm, rows, seed=43)
+    idx_lists = synth.minibatch_indices(R, B, steps, seed=44, epochs=epochs)
+    assert len(idx_lists) == steps
+
+    pl = trainer.create_pufferl({"dims": dm, "init_weights": w0,
+                                 "train": dict(minibatch_size=B, learning_rate=3e-4, **HYP)})
+    trainer.set_rollout(pl, rows, **inp)
+    lg = trainer.train(pl, index_lists=idx_lists)
+    w_gpu = pl.get_weights()
+    assert pl.step_count() == steps and lg["minibatches"] == steps
+    pl.close()
+
+    opt = oadam.OracleAdam([p for _, p in ref.named_blob_params()], lr=3e-4)
+    stats = ostep.run_update(ref, opt, rows, inp, idx_lists, dict(HYP)).double().sum(0)
+    w_ref = ref.to_blob()
+
+    err = rel_l2(w_gpu, w_ref)
+    assert err < 1e-4, err
+    assert np.abs(w_gpu - w_ref).max() <= 2.0 * 3e-4 * steps
+    assert rel_l2(w_gpu - w0, w_ref - w0) < 1e-2
+    names = ("policy_loss", "value_loss", "entropy", "total_loss", "old_approx_kl", "approx_kl")
+    for i, k in enumerate(names):
+        want = float(stats[i]) / steps
+        assert abs(lg[k] - want) <= 1e-3 * max(1.0, abs(want)), (k, lg[k], want)

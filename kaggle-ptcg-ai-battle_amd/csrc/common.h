@@ -105,6 +105,9 @@ struct GemmArgs {
     const float* R; long ldr;
     float* C2; long ldc2;
     int a_t, b_t, epi;
+    // optional, a_t == 1 with the STORE epilogue only: dbias[m] = sum_k A[k][m]
+    // (the bias gradient of a weight-gradient product dW = dY^T X)
+    float* dbias;
 };
 
 // Launch C = epi(A*B) on `stream`. Requirements: K % 4 == 0 when the operand

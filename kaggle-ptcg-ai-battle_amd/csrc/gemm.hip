@@ -41,7 +41,10 @@ __device__ __forceinline__ void tile_of(int b, int tiles, int tn, int& tm_i, int
     tn_i = lb % tn;
 }
 
-template <bool AT, bool BT, int EPI, bool PARTIAL>
+// DB (AT only): blocks of the first N-tile also sum their A tile over k, the
+// bias gradient sum_k dY[k][m]; thread t covers m = t % 128 over k half t / 128.
+// With PARTIAL the per-split sums go to C + splits*part_stride + z*M.
+template <bool AT, bool BT, int EPI, bool PARTIAL, bool DB = false>
 __global__ __launch_bounds__(NT) void gemm_f32_kernel(GemmArgs g, int k_chunk, long part_stride) {
     __shared__ __align__(16) float As[2][Stage<AT>::floats];
     __shared__ __align__(16) float Bs[2][Stage<BT>::floats];
@@ -92,6 +95,8 @@ __global__ __launch_bounds__(NT) void gemm_f32_kernel(GemmArgs g, int k_chunk, l
     *reinterpret_cast<float4*>(&Bs[buf][sb0]) = vb0;           \
     *reinterpret_cast<float4*>(&Bs[buf][sb1]) = vb1;
 
+    const bool do_db = DB && AT && tni == 0;
+    float dbsum = 0.f;
     if (kbeg < kend) {
         PT_GLOAD(kbeg)
         PT_SSTORE(0)
@@ -118,6 +123,11 @@ __global__ __launch_bounds__(NT) void gemm_f32_kernel(GemmArgs g, int k_chunk, l
                 acc[ti][tj] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[ti].c, bf[tj].c, acc[ti][tj], 0, 0, 0);
             PT_MFMA_STEP(x) PT_MFMA_STEP(y) PT_MFMA_STEP(z) PT_MFMA_STEP(w)
 #undef PT_MFMA_STEP
+            if (do_db) {
+                // rows beyond kend / columns beyond M were staged as zeros
+#pragma unroll
+                for (int kk = 0; kk < BK / 2; ++kk) dbsum += Ab[((tid >> 7) * (BK / 2) + kk) * SM + (tid & 127)];
+            }
             if (more) { PT_SSTORE(buf ^ 1) }
             __syncthreads();
             buf ^= 1;
@@ -126,6 +136,19 @@ __global__ __launch_bounds__(NT) void gemm_f32_kernel(GemmArgs g, int k_chunk, l
 #undef PT_GLOAD
 #undef PT_SSTORE
 #undef PT_LD
+
+    if (do_db) {
+        // the loop ended on a barrier, so buffer 0 is free; fixed-order pair sum
+        float* sh = As[0];
+        sh[tid] = dbsum;
+        __syncthreads();
+        const int m = m0 + tid;
+        if (tid < 128 && m < g.M) {
+            const float v = sh[tid] + sh[tid + 128];
+            if (PARTIAL) g.C[(long)gridDim.z * part_stride + (long)blockIdx.z * g.M + m] = v;
+            else g.dbias[m] = v;
+        }
+    }
 
     // epilogue: acc[ti][tj][r] = C[wm + ti*16 + 4*lq + r][wn + tj*16 + li]
     const long zoff = PARTIAL ? (long)blockIdx.z * part_stride : 0;
@@ -165,11 +188,21 @@ __global__ __launch_bounds__(NT) void gemm_f32_kernel(GemmArgs g, int k_chunk, l
 }
 
 // out[m][n] (=|+=) sum_s part[s][m][n], fixed order over s
+// and, when db is set, db[m] = sum_s part[splits*part_stride + s*M + m]
 template <bool ACCUM>
 __global__ void splitk_reduce_kernel(float* C, long ldc, const float* part, long part_stride,
-                                     int splits, int M, int N) {
+                                     int splits, int M, int N, float* db) {
     long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= (long)M * N) return;
+    if (i >= (long)M * N) {
+        const long m = i - (long)M * N;
+        if (db != nullptr && m < M) {
+            const float* bp = part + (long)splits * part_stride + m;
+            float s = 0.f;
+            for (int k = 0; k < splits; ++k) s += bp[(long)k * M];
+            db[m] = s;
+        }
+        return;
+    }
     int m = (int)(i / N), n = (int)(i % N);
     long o = (long)m * ldc + n;
     float s = 0.f;
@@ -209,11 +242,11 @@ struct GemmProf {
 };
 GemmProf g_prof;
 
-template <bool AT, bool BT, int EPI, bool PARTIAL>
+template <bool AT, bool BT, int EPI, bool PARTIAL, bool DB = false>
 void launch(const GemmArgs& g, dim3 grid, int k_chunk, long part_stride, hipStream_t s) {
     const bool rec = g_prof.on && g_prof.used * 2 + 1 < (int)g_prof.ev.size();
     if (rec) (void)hipEventRecord(g_prof.ev[2 * g_prof.used], s);
-    hipLaunchKernelGGL((gemm_f32_kernel<AT, BT, EPI, PARTIAL>), grid, dim3(NT), 0, s, g, k_chunk,
+    hipLaunchKernelGGL((gemm_f32_kernel<AT, BT, EPI, PARTIAL, DB>), grid, dim3(NT), 0, s, g, k_chunk,
                        part_stride);
     if (rec) {
         (void)hipEventRecord(g_prof.ev[2 * g_prof.used + 1], s);
@@ -272,9 +305,12 @@ int pt_gemm(const GemmArgs& g, float* ws, long ws_floats, hipStream_t s) {
         if (splits < 1) splits = 1;
     }
     if (splits > 1 && !(g.epi == EPI_STORE || g.epi == EPI_ACCUM)) splits = 1;
+    const bool db = g.dbias != nullptr;
+    PT_REQUIRE(!db || (g.a_t && g.epi == EPI_STORE), "gemm: dbias needs a_t = 1 and the STORE epilogue");
     long part_stride = (long)g.M * g.ldc;
-    if (splits > 1 && (ws == nullptr || (long)splits * part_stride > ws_floats)) {
-        long fit = ws ? ws_floats / part_stride : 0;
+    const long per_split = part_stride + (db ? g.M : 0);
+    if (splits > 1 && (ws == nullptr || (long)splits * per_split > ws_floats)) {
+        long fit = ws ? ws_floats / per_split : 0;
         splits = fit > 1 ? (int)fit : 1;
     }
     int k_chunk = g.K;
@@ -287,18 +323,20 @@ int pt_gemm(const GemmArgs& g, float* ws, long ws_floats, hipStream_t s) {
     if (splits > 1) {
         GemmArgs p = g;
         p.C = ws;
-        if (code == 3) launch<true, true, EPI_STORE, true>(p, grid, k_chunk, part_stride, s);
+        if (code == 3 && db) launch<true, true, EPI_STORE, true, true>(p, grid, k_chunk, part_stride, s);
+        else if (code == 2 && db) launch<true, false, EPI_STORE, true, true>(p, grid, k_chunk, part_stride, s);
+        else if (code == 3) launch<true, true, EPI_STORE, true>(p, grid, k_chunk, part_stride, s);
         else if (code == 1) launch<false, true, EPI_STORE, true>(p, grid, k_chunk, part_stride, s);
         else if (code == 0) launch<false, false, EPI_STORE, true>(p, grid, k_chunk, part_stride, s);
         else launch<true, false, EPI_STORE, true>(p, grid, k_chunk, part_stride, s);
         PT_LAUNCH_CHECK();
-        long tot = (long)g.M * g.N;
+        long tot = (long)g.M * g.N + (db ? g.M : 0);
         if (g.epi == EPI_ACCUM)
             hipLaunchKernelGGL(splitk_reduce_kernel<true>, dim3(pt_cdiv(tot, 256)), dim3(256), 0, s,
-                               g.C, g.ldc, ws, part_stride, splits, g.M, g.N);
+                               g.C, g.ldc, ws, part_stride, splits, g.M, g.N, g.dbias);
         else
             hipLaunchKernelGGL(splitk_reduce_kernel<false>, dim3(pt_cdiv(tot, 256)), dim3(256), 0, s,
-                               g.C, g.ldc, ws, part_stride, splits, g.M, g.N);
+                               g.C, g.ldc, ws, part_stride, splits, g.M, g.N, g.dbias);
         PT_LAUNCH_CHECK();
         return PTCG_OK;
     }
@@ -312,7 +350,10 @@ int pt_gemm(const GemmArgs& g, float* ws, long ws_floats, hipStream_t s) {
         case EPI_ACCUM: launch<AT, BT, EPI_ACCUM, false>(g, grid, k_chunk, 0, s); break;       \
         default: PT_REQUIRE(false, "gemm: bad epilogue %d", g.epi);                            \
     }
-    if (code == 0) {
+    if (db) {
+        if (code == 3) launch<true, true, EPI_STORE, false, true>(g, grid, k_chunk, 0, s);
+        else launch<true, false, EPI_STORE, false, true>(g, grid, k_chunk, 0, s);
+    } else if (code == 0) {
         PT_EPI_CASES(false, false)
     } else if (code == 1) {
         PT_EPI_CASES(false, true)
@@ -362,9 +403,8 @@ int pt_linear_dw(const float* dY, const float* X, float* dW, float* db, int rows
     g.B = X; g.ldb = in; g.b_t = 1;
     g.C = dW; g.ldc = in;
     g.epi = EPI_STORE;
-    PT_TRY(pt_gemm(g, ws, ws_floats, s));
-    if (db) PT_TRY(pt_colsum(dY, out, rows, out, db, ws, ws_floats, s));
-    return PTCG_OK;
+    g.dbias = db;
+    return pt_gemm(g, ws, ws_floats, s);
 }
 
 int pt_colsum2(const float* X, long ldx, int M, int N, int split, float* out_lo, float* out_hi,

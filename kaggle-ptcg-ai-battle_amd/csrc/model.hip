@@ -98,9 +98,8 @@ static int ldw_(PtcgModel* m, const float* dY, long lddy, const float* X, long l
     g.B = X; g.ldb = ldxx; g.b_t = 1;
     g.C = dW; g.ldc = in;
     g.epi = EPI_STORE;
-    PT_TRY(pt_gemm(g, m->ws, m->ws_floats, s));
-    if (db) PT_TRY(pt_colsum(dY, lddy, rows, out, db, m->ws, m->ws_floats, s));
-    return PTCG_OK;
+    g.dbias = db;
+    return pt_gemm(g, m->ws, m->ws_floats, s);
 }
 
 // ------------------------------------------------------------ lifecycle

@@ -26,6 +26,15 @@ int ptcg_kernel_gemm(int M, int N, int K, const float* A, int64_t lda, int a_t,
                      const float* bias, const float* R, int64_t ldr, float* C2, int64_t ldc2,
                      float* workspace, int64_t workspace_floats, void* stream);
 
+/* weight gradient of a linear layer Y = X W^T + b (pt_linear_bwd's dW / db,
+ * ptcg_kernels.cuh:81-108): dW (out, in) = dY^T X, db (out) = column sums of
+ * dY (optional, NULL to skip), both overwritten and summed in a fixed order.
+ * dY (rows, out) at row stride lddy, X (rows, in) at row stride ldx.
+ * workspace: split-K partials, up to 512 tiles of out*in + out floats.      */
+int ptcg_kernel_gemm_dw(int rows, int in, int out, const float* dY, int64_t lddy,
+                        const float* X, int64_t ldx, float* dW, float* db,
+                        float* workspace, int64_t workspace_floats, void* stream);
+
 /* deterministic column sums out[n] = sum_m X[m*ldx+n] (pt_bias_grad,
  * ptcg_kernels.cuh:87-96); workspace >= ceil(M/256)*N floats.              */
 int ptcg_kernel_colsum(const float* X, int64_t ldx, int M, int N, float* out,
@@ -49,6 +58,11 @@ int ptcg_kernel_attention_fwd(const float* qkv, const float* keep, float* ctx, f
 int ptcg_kernel_attention_bwd(const float* qkv, const float* keep, const float* ctx,
                               const float* lse, const float* dctx, float* dqkv,
                               int N, int L, int H, int Dh, void* stream);
+
+/* which attention kernels a row length takes: bit 0 forward (MFMA), bit 1
+ * backward with the L x L dS tile parked in LDS (Lp <= 128), bit 2 backward
+ * recomputing S and dP per query stripe (longer rows); -1 unsupported.     */
+int ptcg_kernel_attention_path(int L, int Dh);
 
 /* Launch timing of the GEMM kernel: between begin and end, every GEMM launch
  * (up to max_launches) is bracketed by a HIP event pair on its own stream.

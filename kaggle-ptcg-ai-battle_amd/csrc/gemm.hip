@@ -41,10 +41,36 @@ __device__ __forceinline__ void tile_of(int b, int tiles, int tn, int& tm_i, int
     tn_i = lb % tn;
 }
 
+// Operand load of 4 consecutive floats along the contiguous dimension for
+// shapes that break the 128-bit rules (a width or leading dimension not a
+// multiple of 4, as the reference's 127-, 134- and 634-wide inputs do):
+// scalar loads, each bounds-checked.  T: X[k][r..r+3], else X[r][k..k+3].
+template <bool T>
+__device__ __forceinline__ float4 ld_scalar4(const gfloat* X, long ld, int lim, int r, int k, int kend) {
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (T) {
+        if (k < kend) {
+            const gfloat* p = X + (long)k * ld + r;
+            if (r < lim) v.x = p[0];
+            if (r + 1 < lim) v.y = p[1];
+            if (r + 2 < lim) v.z = p[2];
+            if (r + 3 < lim) v.w = p[3];
+        }
+    } else if (r < lim) {
+        const gfloat* p = X + (long)r * ld + k;
+        if (k < kend) v.x = p[0];
+        if (k + 1 < kend) v.y = p[1];
+        if (k + 2 < kend) v.z = p[2];
+        if (k + 3 < kend) v.w = p[3];
+    }
+    return v;
+}
+
 // DB (AT only): blocks of the first N-tile also sum their A tile over k, the
 // bias gradient sum_k dY[k][m]; thread t covers m = t % 128 over k half t / 128.
 // With PARTIAL the per-split sums go to C + splits*part_stride + z*M.
-template <bool AT, bool BT, int EPI, bool PARTIAL, bool DB = false>
+// VEC: operands satisfy the 128-bit load rules (else scalar loads).
+template <bool AT, bool BT, int EPI, bool PARTIAL, bool DB, bool VEC>
 __global__ __launch_bounds__(NT) void gemm_f32_kernel(GemmArgs g, int k_chunk, long part_stride) {
     __shared__ __align__(16) float As[2][Stage<AT>::floats];
     __shared__ __align__(16) float Bs[2][Stage<BT>::floats];
@@ -79,7 +105,8 @@ __global__ __launch_bounds__(NT) void gemm_f32_kernel(GemmArgs g, int k_chunk, l
     const int sa0 = AT ? rk0 * SM + ra0 : ra0 * SK + rk0, sa1 = AT ? rk1 * SM + ra1 : ra1 * SK + rk1;
     const int sb0 = BT ? kb0 * SM + rb0 : rb0 * SK + kb0, sb1 = BT ? kb1 * SM + rb1 : rb1 * SK + kb1;
 #define PT_LD(X, ld, lim, r0, T, rr, kk, k0)                                                   \
-    (((r0) + (rr) < (lim) && (k0) + (kk) < kend)                                                \
+    (!VEC ? ld_scalar4<T>((X), (ld), (lim), (r0) + (rr), (k0) + (kk), kend)                      \
+     : ((r0) + (rr) < (lim) && (k0) + (kk) < kend)                                              \
          ? ld_g4((X) + ((T) ? (long)((k0) + (kk)) * (ld) + (r0) + (rr)                       \
                             : (long)((r0) + (rr)) * (ld) + (k0) + (kk)))                        \
          : z4)
@@ -242,17 +269,57 @@ struct GemmProf {
 };
 GemmProf g_prof;
 
-template <bool AT, bool BT, int EPI, bool PARTIAL, bool DB = false>
+template <bool AT, bool BT, int EPI, bool PARTIAL, bool DB, bool VEC>
 void launch(const GemmArgs& g, dim3 grid, int k_chunk, long part_stride, hipStream_t s) {
     const bool rec = g_prof.on && g_prof.used * 2 + 1 < (int)g_prof.ev.size();
     if (rec) (void)hipEventRecord(g_prof.ev[2 * g_prof.used], s);
-    hipLaunchKernelGGL((gemm_f32_kernel<AT, BT, EPI, PARTIAL, DB>), grid, dim3(NT), 0, s, g, k_chunk,
+    hipLaunchKernelGGL((gemm_f32_kernel<AT, BT, EPI, PARTIAL, DB, VEC>), grid, dim3(NT), 0, s, g, k_chunk,
                        part_stride);
     if (rec) {
         (void)hipEventRecord(g_prof.ev[2 * g_prof.used + 1], s);
         g_prof.flops[g_prof.used] = 2.0 * g.M * (double)g.N * g.K;
         g_prof.used++;
     }
+}
+
+// split-K partial products (STORE into the workspace), optional bias sums
+template <bool VEC>
+void launch_partial(const GemmArgs& p, bool db, dim3 grid, int k_chunk, long part_stride, hipStream_t s) {
+    const int code = (p.a_t ? 1 : 0) * 2 + (p.b_t ? 1 : 0);
+    if (code == 3 && db) launch<true, true, EPI_STORE, true, true, VEC>(p, grid, k_chunk, part_stride, s);
+    else if (code == 2 && db) launch<true, false, EPI_STORE, true, true, VEC>(p, grid, k_chunk, part_stride, s);
+    else if (code == 3) launch<true, true, EPI_STORE, true, false, VEC>(p, grid, k_chunk, part_stride, s);
+    else if (code == 1) launch<false, true, EPI_STORE, true, false, VEC>(p, grid, k_chunk, part_stride, s);
+    else if (code == 0) launch<false, false, EPI_STORE, true, false, VEC>(p, grid, k_chunk, part_stride, s);
+    else launch<true, false, EPI_STORE, true, false, VEC>(p, grid, k_chunk, part_stride, s);
+}
+
+template <bool AT, bool BT, bool VEC>
+int launch_epi(const GemmArgs& g, dim3 grid, int k_chunk, hipStream_t s) {
+    switch (g.epi) {
+        case EPI_STORE: launch<AT, BT, EPI_STORE, false, false, VEC>(g, grid, k_chunk, 0, s); break;
+        case EPI_BIAS: launch<AT, BT, EPI_BIAS, false, false, VEC>(g, grid, k_chunk, 0, s); break;
+        case EPI_BIAS_GELU: launch<AT, BT, EPI_BIAS_GELU, false, false, VEC>(g, grid, k_chunk, 0, s); break;
+        case EPI_BIAS_RESID: launch<AT, BT, EPI_BIAS_RESID, false, false, VEC>(g, grid, k_chunk, 0, s); break;
+        case EPI_GELU_BWD: launch<AT, BT, EPI_GELU_BWD, false, false, VEC>(g, grid, k_chunk, 0, s); break;
+        case EPI_ACCUM: launch<AT, BT, EPI_ACCUM, false, false, VEC>(g, grid, k_chunk, 0, s); break;
+        default: PT_REQUIRE(false, "gemm: bad epilogue %d", g.epi);
+    }
+    return PTCG_OK;
+}
+
+template <bool VEC>
+int launch_full(const GemmArgs& g, bool db, dim3 grid, int k_chunk, hipStream_t s) {
+    const int code = (g.a_t ? 1 : 0) * 2 + (g.b_t ? 1 : 0);
+    if (db) {
+        if (code == 3) launch<true, true, EPI_STORE, false, true, VEC>(g, grid, k_chunk, 0, s);
+        else launch<true, false, EPI_STORE, false, true, VEC>(g, grid, k_chunk, 0, s);
+        return PTCG_OK;
+    }
+    if (code == 0) return launch_epi<false, false, VEC>(g, grid, k_chunk, s);
+    if (code == 1) return launch_epi<false, true, VEC>(g, grid, k_chunk, s);
+    if (code == 3) return launch_epi<true, true, VEC>(g, grid, k_chunk, s);
+    return launch_epi<true, false, VEC>(g, grid, k_chunk, s);
 }
 
 }  // namespace
@@ -289,10 +356,12 @@ extern "C" int ptcg_profile_end(double* total_ms, int* launches, double* flops) 
 
 int pt_gemm(const GemmArgs& g, float* ws, long ws_floats, hipStream_t s) {
     PT_REQUIRE(g.M > 0 && g.N > 0 && g.K > 0, "gemm: empty shape %d x %d x %d", g.M, g.N, g.K);
-    PT_REQUIRE(g.a_t ? (g.M % 4 == 0) : (g.K % 4 == 0), "gemm: A operand not float4-able (M=%d K=%d a_t=%d)", g.M, g.K, g.a_t);
-    PT_REQUIRE(g.b_t ? (g.N % 4 == 0) : (g.K % 4 == 0), "gemm: B operand not float4-able (N=%d K=%d b_t=%d)", g.N, g.K, g.b_t);
-    PT_REQUIRE(g.lda % 4 == 0 && g.ldb % 4 == 0, "gemm: leading dims must be multiples of 4");
-    PT_REQUIRE(((uintptr_t)g.A & 15) == 0 && ((uintptr_t)g.B & 15) == 0, "gemm: operands must be 16 B aligned");
+    PT_REQUIRE(g.A && g.B && g.C, "gemm: null operand");
+    // 128-bit loads need the contiguous extent and the leading dimensions to be
+    // multiples of 4 floats and 16 B aligned operands; otherwise scalar loads
+    const bool vec = (g.a_t ? (g.M % 4 == 0) : (g.K % 4 == 0)) && (g.b_t ? (g.N % 4 == 0) : (g.K % 4 == 0)) &&
+                     g.lda % 4 == 0 && g.ldb % 4 == 0 && ((uintptr_t)g.A & 15) == 0 &&
+                     ((uintptr_t)g.B & 15) == 0;
     const int tm = pt_cdiv(g.M, BM), tn = pt_cdiv(g.N, BN);
     const int tiles = tm * tn;
     // split K when the output is too small to fill the chip and K is long
@@ -319,16 +388,11 @@ int pt_gemm(const GemmArgs& g, float* ws, long ws_floats, hipStream_t s) {
         splits = pt_cdiv(g.K, k_chunk);
     }
     dim3 grid(tn * tm, 1, splits);
-    const int code = (g.a_t ? 1 : 0) * 2 + (g.b_t ? 1 : 0);
     if (splits > 1) {
         GemmArgs p = g;
         p.C = ws;
-        if (code == 3 && db) launch<true, true, EPI_STORE, true, true>(p, grid, k_chunk, part_stride, s);
-        else if (code == 2 && db) launch<true, false, EPI_STORE, true, true>(p, grid, k_chunk, part_stride, s);
-        else if (code == 3) launch<true, true, EPI_STORE, true>(p, grid, k_chunk, part_stride, s);
-        else if (code == 1) launch<false, true, EPI_STORE, true>(p, grid, k_chunk, part_stride, s);
-        else if (code == 0) launch<false, false, EPI_STORE, true>(p, grid, k_chunk, part_stride, s);
-        else launch<true, false, EPI_STORE, true>(p, grid, k_chunk, part_stride, s);
+        if (vec) launch_partial<true>(p, db, grid, k_chunk, part_stride, s);
+        else launch_partial<false>(p, db, grid, k_chunk, part_stride, s);
         PT_LAUNCH_CHECK();
         long tot = (long)g.M * g.N + (db ? g.M : 0);
         if (g.epi == EPI_ACCUM)
@@ -340,29 +404,7 @@ int pt_gemm(const GemmArgs& g, float* ws, long ws_floats, hipStream_t s) {
         PT_LAUNCH_CHECK();
         return PTCG_OK;
     }
-#define PT_EPI_CASES(AT, BT)                                                                   \
-    switch (g.epi) {                                                                           \
-        case EPI_STORE: launch<AT, BT, EPI_STORE, false>(g, grid, k_chunk, 0, s); break;       \
-        case EPI_BIAS: launch<AT, BT, EPI_BIAS, false>(g, grid, k_chunk, 0, s); break;         \
-        case EPI_BIAS_GELU: launch<AT, BT, EPI_BIAS_GELU, false>(g, grid, k_chunk, 0, s); break; \
-        case EPI_BIAS_RESID: launch<AT, BT, EPI_BIAS_RESID, false>(g, grid, k_chunk, 0, s); break; \
-        case EPI_GELU_BWD: launch<AT, BT, EPI_GELU_BWD, false>(g, grid, k_chunk, 0, s); break; \
-        case EPI_ACCUM: launch<AT, BT, EPI_ACCUM, false>(g, grid, k_chunk, 0, s); break;       \
-        default: PT_REQUIRE(false, "gemm: bad epilogue %d", g.epi);                            \
-    }
-    if (db) {
-        if (code == 3) launch<true, true, EPI_STORE, false, true>(g, grid, k_chunk, 0, s);
-        else launch<true, false, EPI_STORE, false, true>(g, grid, k_chunk, 0, s);
-    } else if (code == 0) {
-        PT_EPI_CASES(false, false)
-    } else if (code == 1) {
-        PT_EPI_CASES(false, true)
-    } else if (code == 3) {
-        PT_EPI_CASES(true, true)
-    } else {
-        PT_EPI_CASES(true, false)
-    }
-#undef PT_EPI_CASES
+    PT_TRY(vec ? launch_full<true>(g, db, grid, k_chunk, s) : launch_full<false>(g, db, grid, k_chunk, s));
     PT_LAUNCH_CHECK();
     return PTCG_OK;
 }

@@ -22,6 +22,19 @@ extern "C" int ptcg_kernel_gemm(int M, int N, int K, const float* A, int64_t lda
     return pt_gemm(g, workspace, workspace_floats, (hipStream_t)stream);
 }
 
+extern "C" int ptcg_kernel_gemm_dw(int rows, int in, int out, const float* dY, int64_t lddy,
+                                   const float* X, int64_t ldx, float* dW, float* db,
+                                   float* workspace, int64_t workspace_floats, void* stream) {
+    PT_REQUIRE(dY && X && dW, "kernel_gemm_dw: null operand");
+    GemmArgs g{};
+    g.M = out; g.N = in; g.K = rows;
+    g.A = dY; g.lda = lddy; g.a_t = 1;
+    g.B = X; g.ldb = ldx; g.b_t = 1;
+    g.C = dW; g.ldc = in; g.epi = EPI_STORE;
+    g.dbias = db;
+    return pt_gemm(g, workspace, workspace_floats, (hipStream_t)stream);
+}
+
 extern "C" int ptcg_kernel_colsum(const float* X, int64_t ldx, int M, int N, float* out,
                                   float* workspace, int64_t workspace_floats, void* stream) {
     PT_REQUIRE(X && out, "kernel_colsum: null buffer");
@@ -48,6 +61,9 @@ extern "C" int ptcg_kernel_attention_fwd(const float* qkv, const float* keep, fl
     PT_REQUIRE(qkv && keep && ctx && lse, "kernel_attention_fwd: null buffer");
     return pt_attn_fwd(qkv, keep, ctx, lse, N, L, H, Dh, (hipStream_t)stream);
 }
+
+int pt_attn_path(int L, int DH);
+extern "C" int ptcg_kernel_attention_path(int L, int Dh) { return pt_attn_path(L, Dh); }
 
 extern "C" int ptcg_kernel_attention_bwd(const float* qkv, const float* keep, const float* ctx,
                                          const float* lse, const float* dctx, float* dqkv, int N,

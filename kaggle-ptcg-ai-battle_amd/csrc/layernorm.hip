@@ -151,13 +151,120 @@ __global__ __launch_bounds__(256) void ln_bwd_kernel(const float* __restrict__ d
     }
 }
 
+// Scalar variants for widths that are not multiples of 4 (the reference's
+// 634-wide card LayerNorm): element col = lane + 64c, up to 16 per lane.
+constexpr int LN_SC = 16;
+
+__global__ __launch_bounds__(256) void ln_fwd_scalar_kernel(const float* __restrict__ x, long ldx,
+        const float* __restrict__ w, const float* __restrict__ b, float* __restrict__ y, long ldy,
+        float* __restrict__ mean, float* __restrict__ rstd, int rows, int D) {
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const float* xr = x + (long)row * ldx;
+    float v[LN_SC];
+    float s = 0.f;
+#pragma unroll
+    for (int c = 0; c < LN_SC; ++c) {
+        const int col = lane + 64 * c;
+        v[c] = col < D ? xr[col] : 0.f;
+        s += v[c];
+    }
+    const float mu = wave_sum(s) / (float)D;
+    float q = 0.f;
+#pragma unroll
+    for (int c = 0; c < LN_SC; ++c)
+        if (lane + 64 * c < D) q += (v[c] - mu) * (v[c] - mu);
+    const float rs = 1.0f / sqrtf(wave_sum(q) / (float)D + 1e-5f);
+    if (lane == 0) {
+        mean[row] = mu;
+        rstd[row] = rs;
+    }
+    float* yr = y + (long)row * ldy;
+#pragma unroll
+    for (int c = 0; c < LN_SC; ++c) {
+        const int col = lane + 64 * c;
+        if (col < D) yr[col] = (v[c] - mu) * rs * w[col] + b[col];
+    }
+}
+
+__global__ __launch_bounds__(256) void ln_bwd_scalar_kernel(const float* __restrict__ dy, long lddy,
+        const float* __restrict__ x, long ldx, const float* __restrict__ w,
+        const float* __restrict__ mean, const float* __restrict__ rstd,
+        const float* __restrict__ dres, long ldres, float* __restrict__ dx, long lddx,
+        float* __restrict__ part, int rows, int D) {
+    __shared__ float sh_w[4][LN_SC * 64];
+    __shared__ float sh_b[4][LN_SC * 64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    float aw[LN_SC], ab[LN_SC], wv[LN_SC];
+#pragma unroll
+    for (int c = 0; c < LN_SC; ++c) {
+        aw[c] = 0.f;
+        ab[c] = 0.f;
+        const int col = lane + 64 * c;
+        wv[c] = col < D ? w[col] : 0.f;
+    }
+    for (int row = blockIdx.x * 4 + wave; row < rows; row += gridDim.x * 4) {
+        const float mu = mean[row], rs = rstd[row];
+        const float* xr = x + (long)row * ldx;
+        const float* dyr = dy + (long)row * lddy;
+        float xh[LN_SC], g[LN_SC];
+        float s1 = 0.f, s2 = 0.f;
+#pragma unroll
+        for (int c = 0; c < LN_SC; ++c) {
+            const int col = lane + 64 * c;
+            xh[c] = 0.f;
+            g[c] = 0.f;
+            if (col < D) {
+                const float d = dyr[col];
+                xh[c] = (xr[col] - mu) * rs;
+                g[c] = d * wv[c];
+                s1 += g[c];
+                s2 += g[c] * xh[c];
+                aw[c] += d * xh[c];
+                ab[c] += d;
+            }
+        }
+        const float m1 = wave_sum(s1) / (float)D;
+        const float m2 = wave_sum(s2) / (float)D;
+        float* dxr = dx + (long)row * lddx;
+        const float* dr = dres ? dres + (long)row * ldres : nullptr;
+#pragma unroll
+        for (int c = 0; c < LN_SC; ++c) {
+            const int col = lane + 64 * c;
+            if (col < D) dxr[col] = (g[c] - m1 - xh[c] * m2) * rs + (dr ? dr[col] : 0.f);
+        }
+    }
+#pragma unroll
+    for (int c = 0; c < LN_SC; ++c) {
+        sh_w[wave][lane + 64 * c] = aw[c];
+        sh_b[wave][lane + 64 * c] = ab[c];
+    }
+    __syncthreads();
+    if (wave == 0) {
+        float* pw = part + (long)blockIdx.x * 2 * D;
+#pragma unroll
+        for (int c = 0; c < LN_SC; ++c) {
+            const int col = lane + 64 * c;
+            if (col < D) {
+                pw[col] = ((sh_w[0][col] + sh_w[1][col]) + sh_w[2][col]) + sh_w[3][col];
+                pw[D + col] = ((sh_b[0][col] + sh_b[1][col]) + sh_b[2][col]) + sh_b[3][col];
+            }
+        }
+    }
+}
+
+bool ln_vec_ok(const void* p, long ld, int D) { return D % 4 == 0 && ld % 4 == 0 && ((uintptr_t)p & 15) == 0; }
+
 }  // namespace
 
 int pt_ln_fwd(const float* x, long ldx, const float* w, const float* b, float* y, long ldy,
               float* mean, float* rstd, int rows, int D, hipStream_t s) {
-    PT_REQUIRE(D % 4 == 0 && D <= 1024 && ldx % 4 == 0 && ldy % 4 == 0, "layernorm: D=%d unsupported", D);
+    PT_REQUIRE(D >= 1 && D <= 1024, "layernorm: D=%d unsupported", D);
     dim3 grid(pt_cdiv(rows, 4));
-    if (D <= 256)
+    if (!(ln_vec_ok(x, ldx, D) && ln_vec_ok(y, ldy, D) && ln_vec_ok(w, 0, D) && ln_vec_ok(b, 0, D)))
+        hipLaunchKernelGGL(ln_fwd_scalar_kernel, grid, dim3(256), 0, s, x, ldx, w, b, y, ldy, mean, rstd, rows, D);
+    else if (D <= 256)
         hipLaunchKernelGGL(ln_fwd_kernel<1>, grid, dim3(256), 0, s, x, ldx, w, b, y, ldy, mean, rstd, rows, D);
     else if (D <= 512)
         hipLaunchKernelGGL(ln_fwd_kernel<2>, grid, dim3(256), 0, s, x, ldx, w, b, y, ldy, mean, rstd, rows, D);
@@ -171,12 +278,16 @@ int pt_ln_bwd(const float* dy, long lddy, const float* x, long ldx, const float*
               const float* mean, const float* rstd, const float* dres, long ldres, float* dx,
               long lddx, float* dw, float* db, int rows, int D, float* ws, long ws_floats,
               hipStream_t s) {
-    PT_REQUIRE(D % 4 == 0 && D <= 1024, "layernorm bwd: D=%d unsupported", D);
+    PT_REQUIRE(D >= 1 && D <= 1024, "layernorm bwd: D=%d unsupported", D);
     int blocks = pt_cdiv(rows, 4);
     if (blocks > LN_BWD_BLOCKS) blocks = LN_BWD_BLOCKS;
     PT_REQUIRE(ws && (long)blocks * 2 * D * 2 <= ws_floats, "layernorm bwd: workspace too small");
     dim3 grid(blocks);
-    if (D <= 256)
+    const bool vec = ln_vec_ok(dy, lddy, D) && ln_vec_ok(x, ldx, D) && ln_vec_ok(w, 0, D) &&
+                     ln_vec_ok(dx, lddx, D) && (dres == nullptr || ln_vec_ok(dres, ldres, D));
+    if (!vec)
+        hipLaunchKernelGGL(ln_bwd_scalar_kernel, grid, dim3(256), 0, s, dy, lddy, x, ldx, w, mean, rstd, dres, ldres, dx, lddx, ws, rows, D);
+    else if (D <= 256)
         hipLaunchKernelGGL(ln_bwd_kernel<1>, grid, dim3(256), 0, s, dy, lddy, x, ldx, w, mean, rstd, dres, ldres, dx, lddx, ws, rows, D);
     else if (D <= 512)
         hipLaunchKernelGGL(ln_bwd_kernel<2>, grid, dim3(256), 0, s, dy, lddy, x, ldx, w, mean, rstd, dres, ldres, dx, lddx, ws, rows, D);

@@ -47,6 +47,10 @@ GEMM_CASES = [
     (256, 256, 256, 0, 0, 3), (200, 96, 40, 0, 1, 4), (64, 300, 256, 0, 1, 0),
     (64, 128, 20000, 1, 1, 0), (768, 256, 4096, 1, 1, 0), (96, 36, 12, 1, 0, 0),
     (129, 132, 132, 0, 1, 5), (512, 1024, 256, 0, 0, 2),
+    # widths / leading dimensions that are not multiples of 4 (the reference's
+    # 127-wide attack input, 634-wide card input, 134-wide oracle token input)
+    (1573, 64, 127, 0, 0, 2), (1284, 634, 256, 0, 1, 0), (300, 256, 134, 0, 0, 1),
+    (64, 127, 1573, 1, 1, 0), (45, 33, 17, 1, 0, 5), (256, 634, 20000, 1, 1, 0),
 ]
 
 
@@ -86,11 +90,33 @@ def test_gemm_layouts_and_epilogues(case, cuda):
         assert rel_l2(got2, ref2) < 1e-5
 
 
-def test_gemm_rejects_unaligned_k(cuda):
-    a = empty(8, 6)
-    with pytest.raises(native.PtcgError, match="float4"):
-        native.check(native.lib().ptcg_kernel_gemm(8, 8, 6, P(a), 6, 0, P(a), 6, 0, P(empty(8, 8)), 8, 0,
-                                                   None, None, 0, None, 0, None, 0, None))
+def test_gemm_operand_not_16b_aligned(cuda):
+    # aligned widths, but A starts one float into its buffer: scalar-load path
+    g = torch.Generator().manual_seed(5)
+    A = torch.randn(200 * 64 + 1, generator=g)
+    B = torch.randn(96, 64, generator=g)
+    dA, dB, dC = dev(A), dev(B), empty(200, 96)
+    native.check(native.lib().ptcg_kernel_gemm(200, 96, 64, dA.data_ptr() + 4, 64, 0, P(dB), 64, 0, P(dC), 96, 0,
+                                               None, None, 0, None, 0, None, 0, None))
+    torch.cuda.synchronize()
+    ref = A[1:].view(200, 64).double() @ B.double().T
+    assert rel_l2(dC.cpu().double(), ref) < 1e-5
+
+
+@pytest.mark.parametrize("rows,inp,out", [(6000, 256, 768), (1573, 127, 64), (100, 64, 36), (8192, 1024, 256)])
+def test_gemm_weight_grad_with_bias_sums(rows, inp, out, cuda):
+    g = torch.Generator().manual_seed(rows + inp)
+    dY = torch.randn(rows, out, generator=g)
+    X = torch.randn(rows, inp, generator=g)
+    d_dY, d_X, dW, db = dev(dY), dev(X), empty(out, inp), empty(out)
+    ws = empty(32 << 20)
+    native.check(native.lib().ptcg_kernel_gemm_dw(rows, inp, out, P(d_dY), out, P(d_X), inp, P(dW), P(db),
+                                                  P(ws), ws.numel(), None))
+    torch.cuda.synchronize()
+    refW = dY.double().T @ X.double()
+    refb = dY.double().sum(0)
+    assert rel_l2(dW.cpu().double(), refW) < 1e-5
+    assert rel_l2(db.cpu().double(), refb) < 1e-5
 
 
 def test_colsum(cuda):
@@ -103,7 +129,7 @@ def test_colsum(cuda):
     assert rel_l2(out.cpu(), X.double().sum(0)) < 1e-6
 
 
-@pytest.mark.parametrize("rows,D", [(1000, 256), (37, 64), (130, 1024), (9, 300)])
+@pytest.mark.parametrize("rows,D", [(1000, 256), (37, 64), (130, 1024), (9, 300), (1284, 634), (50, 127)])
 def test_layernorm_fwd_bwd(rows, D, cuda):
     g = torch.Generator().manual_seed(rows + D)
     x = (torch.randn(rows, D, generator=g) * 3 + 1).double().requires_grad_()
@@ -140,10 +166,16 @@ def _attn_ref(qkv, keep, H, Dh):
     return (p @ v).transpose(1, 2).reshape(N, L, D), torch.logsumexp(s, -1)
 
 
-@pytest.mark.parametrize("N,L,H,Dh", [(6, 97, 4, 64), (5, 25, 2, 32), (3, 100, 2, 64), (4, 64, 8, 32), (2, 1, 4, 64),
-                                      (3, 128, 2, 32), (2, 17, 1, 64),
-                                      (2, 140, 2, 32)])   # L=140/Dh=32: beyond the MFMA kernel's LDS budget -> VALU kernel
-def test_attention_fwd_bwd(N, L, H, Dh, cuda):
+# (N, L, H, Dh, path): path bit 1 = backward with dS in LDS, bit 2 = recompute
+ATTN_CASES = [(6, 97, 4, 64, 3), (5, 25, 2, 32, 3), (3, 100, 2, 64, 3), (4, 64, 8, 32, 3), (2, 1, 4, 64, 3),
+              (3, 128, 2, 32, 3), (2, 17, 1, 64, 3),
+              # rows too long for dS in LDS: the reference's trunk (161) and critic (218) at Dh 32
+              (2, 140, 2, 32, 5), (3, 161, 8, 32, 5), (2, 218, 8, 32, 5), (1, 256, 2, 32, 5), (2, 140, 2, 64, 5)]
+
+
+@pytest.mark.parametrize("N,L,H,Dh,path", ATTN_CASES, ids=lambda *a: None)
+def test_attention_fwd_bwd(N, L, H, Dh, path, cuda):
+    assert native.lib().ptcg_kernel_attention_path(L, Dh) == path
     g = torch.Generator().manual_seed(N * L + H)
     D = H * Dh
     qkv = torch.randn(N, L, 3 * D, generator=g).double().requires_grad_()
@@ -173,6 +205,8 @@ def test_attention_rejects_oversized(cuda):
     a = empty(4)
     with pytest.raises(native.PtcgError, match="LDS"):
         native.check(native.lib().ptcg_kernel_attention_fwd(P(a), P(a), P(a), P(a), 1, 300, 1, 64, None))
+    assert native.lib().ptcg_kernel_attention_path(145, 64) == -1
+    assert native.lib().ptcg_kernel_attention_path(257, 32) == -1
 
 
 def _ppo_inputs(n, A, seed):

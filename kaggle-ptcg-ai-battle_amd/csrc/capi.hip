@@ -53,6 +53,12 @@ DimsX pt_dims_x(const PtcgDims& d) {
     x.q_in = PT_TYPE_E + 2 * d.d + 2 * PT_OPT_E + d.opt_f;
     x.score_in = 3 * d.d + d.g + PT_DEC_H;
     x.val_in = d.d + d.g;
+    x.card_in = PT_ID_C + PT_CARD_STATIC + PT_CARD_TEXT + 2 * d.d_a + 2 * d.d_c;
+    x.att_in = PT_ID_A + PT_ATT_STATIC + PT_ATT_TEXT;
+    x.sk_in = PT_ID_A + PT_SKILL_TEXT;
+    x.orc_in = d.d_c + 6;
+    x.n_orc = PT_N_HAND + PT_N_SPLIT + PT_N_PRIZE;
+    x.l_crit = 1 + x.l_seq + x.n_orc;
     return x;
 }
 
@@ -76,14 +82,14 @@ int pt_param_table(const PtcgDims& d, ParamDef* out, int cap) {
     const DimsX x = pt_dims_x(d);
     const long D = d.d, DC = d.d_c, DA = d.d_a, G = d.g;
     if (d.tables == 1) {
-        add("card_id_emb.weight", d.n_cards, 64);
-        add("attack_id_emb.weight", d.n_attacks, 48);
-        add("skill_id_emb.weight", d.n_skills, 48);
-        add("attack_mlp.0.weight", DA, 127); add("attack_mlp.0.bias", DA, 0);
-        add("skill_mlp.0.weight", DC, 112); add("skill_mlp.0.bias", DC, 0);
-        add("card_mlp.0.weight", 634, 0); add("card_mlp.0.bias", 634, 0);
-        add("card_mlp.1.weight", 256, 634); add("card_mlp.1.bias", 256, 0);
-        add("card_mlp.3.weight", DC, 256); add("card_mlp.3.bias", DC, 0);
+        add("card_id_emb.weight", d.n_cards, PT_ID_C);
+        add("attack_id_emb.weight", d.n_attacks, PT_ID_A);
+        add("skill_id_emb.weight", d.n_skills, PT_ID_A);
+        add("attack_mlp.0.weight", DA, x.att_in); add("attack_mlp.0.bias", DA, 0);
+        add("skill_mlp.0.weight", DC, x.sk_in); add("skill_mlp.0.bias", DC, 0);
+        add("card_mlp.0.weight", x.card_in, 0); add("card_mlp.0.bias", x.card_in, 0);
+        add("card_mlp.1.weight", PT_CARD_H, x.card_in); add("card_mlp.1.bias", PT_CARD_H, 0);
+        add("card_mlp.3.weight", DC, PT_CARD_H); add("card_mlp.3.bias", DC, 0);
     } else if (d.tables == 0) {
         add("card_table", d.n_cards, DC);
         add("attack_table", d.n_attacks, DA);
@@ -122,7 +128,7 @@ int pt_param_table(const PtcgDims& d, ParamDef* out, int cap) {
     add("value_mlp.0.weight", PT_VAL_H, x.val_in); add("value_mlp.0.bias", PT_VAL_H, 0);
     add("value_mlp.2.weight", 1, PT_VAL_H); add("value_mlp.2.bias", 1, 0);
     if (d.critic == 1) {
-        add("oracle_proj.weight", D, DC + 6); add("oracle_proj.bias", D, 0);
+        add("oracle_proj.weight", D, x.orc_in); add("oracle_proj.bias", D, 0);
         add("critic_readout", D, 0);
         block("critic_blocks.0");
         add("oracle_value_mlp.0.weight", PT_VAL_H, x.val_in); add("oracle_value_mlp.0.bias", PT_VAL_H, 0);

@@ -13,9 +13,21 @@ enum {
     PT_OPT_E = 64, PT_TYPE_E = 16, PT_SC_H = 256, PT_VAL_H = 256, PT_DEC_H = 64,
     PT_ZONE_E = 8, PT_OWNER_E = 4, PT_SEL_E = 8, PT_CTX_E = 32,
 };
+// Static-table chain (ptcg/rl/model.py:110-127, ptcg_model.cu:38-56): id
+// embedding widths, static / text feature widths, pool fan-ins, CardVec MLP.
+enum {
+    PT_ID_C = 64, PT_ID_A = 48, PT_CARD_STATIC = 58, PT_CARD_TEXT = 128, PT_ATT_STATIC = 15,
+    PT_ATT_TEXT = 64, PT_SKILL_TEXT = 64, PT_K_ATT = 4, PT_K_SK = 2, PT_CARD_H = 256,
+};
+// Oracle block (ptcg/rl/buffers.py:42-45): 24 opp-hand (id, count/4), 24
+// split (id, deck/4, prize/4), 8 my-prize (id, count/4) slots; aux-loss
+// coefficients and the MY_UNSEEN zone (ptcg_model.cu:83-87).
+enum { PT_N_HAND = 24, PT_N_SPLIT = 24, PT_N_PRIZE = 8, PT_ZONE_MY_UNSEEN = 9 };
+constexpr float PT_AUX_VF = 1.0f, PT_AUX_HAND = 0.1f, PT_AUX_PRIZE = 0.1f;
 
 struct DimsX {   // derived widths
     int l_seq, dh, tok_in, dec_in, bcast_in, q_in, score_in, val_in;
+    int card_in, att_in, sk_in, orc_in, n_orc, l_crit;
 };
 DimsX pt_dims_x(const PtcgDims& d);
 

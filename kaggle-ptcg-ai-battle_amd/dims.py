@@ -147,3 +147,11 @@ def tiny(**kw):
                 ffn=128, layers=2, d_c=32, d_a=16, g=32, n_opt=16)
     base.update(kw)
     return replace(CORE, **base)
+
+
+def tiny_frozen(**kw):
+    """A small config of the reference's model variant: static-table chain,
+    oracle critic and aux heads (for parity tests)."""
+    base = dict(tables=TABLES_STATIC, critic=CRITIC_ORACLE, n_skills=21, heads=2)
+    base.update(kw)
+    return tiny(**base)

@@ -21,7 +21,7 @@ DEC_H = 64       # dec_mlp width
 CARD_H = 256     # card_mlp hidden (static tables)
 ATT_IN = 127     # 48 id + 15 static + 64 text  (ptcg_model.cu:42)
 SK_IN = 112      # 48 id + 64 text              (ptcg_model.cu:43)
-CARD_IN = 634    # ptcg_model.cu:53
+CARD_STATIC, CARD_TEXT = 58, 128   # static feature widths (ptcg/rl/cards.py)
 ORC_IN = 134     # d_c + 6                      (ptcg_model.cu:56)
 
 
@@ -36,6 +36,12 @@ def _block(prefix, d, ffn):
     ]
 
 
+def card_in_width(dims):
+    """CardVec MLP input (ptcg_model.cu:53): [id64 | static | text | attack
+    mean/max | skill mean/max] = 634 at d_a 64 / d_c 128."""
+    return 64 + CARD_STATIC + CARD_TEXT + 2 * dims.d_a + 2 * dims.d_c
+
+
 def param_order(dims):
     """(torch_name, shape) in canonical blob order.
 
@@ -48,6 +54,7 @@ def param_order(dims):
     the reference order.
     """
     d, dc, da, G = dims.d, dims.d_c, dims.d_a, dims.g
+    card_in = card_in_width(dims)
     if dims.tables == TABLES_STATIC:
         order = [
             ("card_id_emb.weight", (dims.n_cards, 64)),
@@ -55,8 +62,8 @@ def param_order(dims):
             ("skill_id_emb.weight", (dims.n_skills, 48)),
             ("attack_mlp.0.weight", (da, ATT_IN)), ("attack_mlp.0.bias", (da,)),
             ("skill_mlp.0.weight", (dc, SK_IN)), ("skill_mlp.0.bias", (dc,)),
-            ("card_mlp.0.weight", (CARD_IN,)), ("card_mlp.0.bias", (CARD_IN,)),
-            ("card_mlp.1.weight", (CARD_H, CARD_IN)), ("card_mlp.1.bias", (CARD_H,)),
+            ("card_mlp.0.weight", (card_in,)), ("card_mlp.0.bias", (card_in,)),
+            ("card_mlp.1.weight", (CARD_H, card_in)), ("card_mlp.1.bias", (CARD_H,)),
             ("card_mlp.3.weight", (dc, CARD_H)), ("card_mlp.3.bias", (dc,)),
         ]
     elif dims.tables == TABLES_LEARNED:

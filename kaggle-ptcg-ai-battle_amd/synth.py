@@ -11,7 +11,12 @@ ids are stored as fp32.  Distributions (per row):
   one is legal; a legal slot has type U[1,17), ptr1 = a valid token + 1,
   ptr2 = 0 or a valid token + 1 (p = 1/2 each), card id U[0, n_cards),
   ``opt_f`` features ~ N(0,1); illegal slots are zero; opt_mask = legal.
-* global_f ~ N(0,1); dec_int zero; dec_float ~ N(0,1); oracle block zero.
+* global_f ~ N(0,1); dec_int zero; dec_float ~ N(0,1).
+* oracle block (models with the oracle critic only, else zero): each of the
+  24 opp-hand and 8 my-prize slots holds (id, count/4) and each of the 24
+  split slots (id, deck/4, prize/4), id U[1, n_cards) with p = 0.6 else
+  empty (0), counts U{1..4}; valid tokens of such models carry zone
+  U[1, n_zones) (so MY_UNSEEN = 9 tokens occur) instead of 1.
 
 ``rich=True`` additionally exercises the id paths the default leaves at 0
 (tool ids, attack ids, decision ids, out-of-range and negative ids that the
@@ -38,7 +43,7 @@ def make_obs(dims, n, seed, max_pad=None, rich=False):
         ti = row[off["tok_int"][0]:off["tok_int"][1]].reshape(L, T)
         tf = row[off["tok_float"][0]:off["tok_float"][1]].reshape(L, dims.tok_f)
         ti[:nv, 0] = rng.integers(0, dims.n_cards, size=nv)
-        ti[:nv, 1] = 1
+        ti[:nv, 1] = rng.integers(1, dims.n_zones, size=nv) if dims.critic == 1 else 1
         ti[:nv, 2] = 1
         tf[:nv] = rng.standard_normal((nv, dims.tok_f))
         if rich:
@@ -72,12 +77,52 @@ def make_obs(dims, n, seed, max_pad=None, rich=False):
         row[g0:g1] = rng.standard_normal(g1 - g0)
         f0, f1 = off["dec_float"]
         row[f0:f1] = rng.standard_normal(f1 - f0)
+        if dims.critic == 1:
+            o0, o1 = off["oracle"]
+            row[o0:o1] = _oracle_block(rng, dims, rich)
         if rich:
             d0, d1 = off["dec_int"]
             hi = [dims.n_select_types, dims.n_contexts, dims.n_cards, dims.n_cards,
                   dims.n_attacks, dims.n_attacks, dims.n_cards, dims.n_cards]
             row[d0:d1] = [rng.integers(0, h + 2) for h in hi[:d1 - d0]]
     return obs
+
+
+def _oracle_block(rng, dims, rich):
+    """(24 x (id, c/4)) + (24 x (id, d/4, p/4)) + (8 x (id, c/4))"""
+    def ids(k):
+        v = rng.integers(1, dims.n_cards, size=k)
+        v[rng.random(k) < 0.4] = 0
+        if rich:   # out-of-range, negative and the unknown id (n_cards - 1)
+            r = rng.random(k)
+            v[r < 0.05] = dims.n_cards + 2
+            v[(r >= 0.05) & (r < 0.1)] = -2
+            v[(r >= 0.1) & (r < 0.15)] = dims.n_cards - 1
+        return v.astype(np.float32)
+    cnt = lambda k: rng.integers(0 if rich else 1, 5, size=k).astype(np.float32) / 4
+    hand = np.stack([ids(24), cnt(24)], 1)
+    split = np.stack([ids(24), cnt(24), cnt(24)], 1)
+    prize = np.stack([ids(8), cnt(8)], 1)
+    return np.concatenate([hand.ravel(), split.ravel(), prize.ravel()])
+
+
+def make_static(dims, seed):
+    """Static card / attack / skill features for the static-table model
+    (the engine-derived tables of ptcg/rl/cards.py, synthetic here):
+    features ~ N(0, 0.5^2); each card lists up to 4 attack ids and 2 skill
+    ids (0 = empty slot), occasionally the same id twice."""
+    rng = np.random.Generator(np.random.PCG64(seed))
+    NC, NA, NS = dims.n_cards, dims.n_attacks, dims.n_skills
+    f = lambda *sh: (0.5 * rng.standard_normal(sh)).astype(np.float32)
+    att = rng.integers(1, NA, size=(NC, 4))
+    att[rng.random((NC, 4)) < 0.4] = 0
+    dup = rng.random(NC) < 0.05
+    att[dup, 1] = att[dup, 0]
+    sk = rng.integers(1, NS, size=(NC, 2))
+    sk[rng.random((NC, 2)) < 0.6] = 0
+    return dict(card_static=f(NC, 58), att_static=f(NA, 15), card_text=f(NC, 128),
+                att_text=f(NA, 64), skill_text=f(NS, 64),
+                card_attacks=att.astype(np.int32), card_skills=sk.astype(np.int32))
 
 
 def make_ppo_inputs(dims, obs, seed):

@@ -40,6 +40,7 @@ def blob_order(dm):
     q_in = 16 + 2 * d + 2 * 64 + dm.opt_f
     score_in = 3 * d + dm.g + 64
     val_in = d + dm.g
+    card_in = 64 + 58 + 128 + 2 * dm.d_a + 2 * dm.d_c   # 634 at d_a 64 / d_c 128
 
     def block(p):
         return [(f"{p}.ln1.weight", (d,)), (f"{p}.ln1.bias", (d,)),
@@ -55,8 +56,8 @@ def blob_order(dm):
                  ("skill_id_emb.weight", (dm.n_skills, 48)),
                  ("attack_mlp.0.weight", (dm.d_a, 127)), ("attack_mlp.0.bias", (dm.d_a,)),
                  ("skill_mlp.0.weight", (dm.d_c, 112)), ("skill_mlp.0.bias", (dm.d_c,)),
-                 ("card_mlp.0.weight", (634,)), ("card_mlp.0.bias", (634,)),
-                 ("card_mlp.1.weight", (256, 634)), ("card_mlp.1.bias", (256,)),
+                 ("card_mlp.0.weight", (card_in,)), ("card_mlp.0.bias", (card_in,)),
+                 ("card_mlp.1.weight", (256, card_in)), ("card_mlp.1.bias", (256,)),
                  ("card_mlp.3.weight", (dm.d_c, 256)), ("card_mlp.3.bias", (dm.d_c,))]
     else:
         order = [("card_table", (dm.n_cards, dm.d_c)),

@@ -16,10 +16,24 @@ build replaces):
   which ``Tensor.long()`` + ``clamp`` reproduces.
 
 Output is the decoder contract (N, n_opt + 1) = [raw scores || value]
-(ptcg_model.cu:512-517).  Implemented variant: learned card/attack tables
-and the blind value head (``value_mlp([r || g])``, model.py:317-318) — the
-synthetic workload's model.  The static-table chain and the oracle critic
-(model.py:185-205, 278-308) are not restated yet.
+(ptcg_model.cu:512-517).  Two variants per switch:
+
+* tables: learned (n_cards, d_c) / (n_attacks, d_a) tables (the synthetic
+  workload), or the reference's static-table chain (model.py:185-205,
+  ptcg_model2.cu:422-485) rebuilt every forward from uploaded static
+  features: AttackVec = GELU(Linear([id48 | static15 | text64])), SkillVec
+  likewise, CardVec = MLP(LN([id64 | static58 | text128 | attack mean/max |
+  skill mean/max])).  The max pool follows the native kernel (k_pool,
+  ptcg_model.cu:236-256): masked slots take part as 0 and the gradient goes
+  to the FIRST maximal slot (torch's amax would split it between ties);
+* critic: blind (value = value_mlp([r | g])) or the oracle critic block
+  over [critic readout | h | 56 oracle tokens] (model.py:278-308,
+  ptcg_model.cu:442-509) whose value fills the output column, with the
+  blind value head and the belief aux heads trained by the aux losses the
+  native backward injects (ptcg_model4.cu:26-61, ptcg_model2.cu:219-285):
+  blind-V MSE (coef 1), softplus hand-count MSE (0.1), per-MY_UNSEEN-token
+  prize BCE (0.1).  :func:`aux_loss` states them as one differentiable
+  objective whose autograd gradient is the kernels' gradient.
 """
 import math
 
@@ -28,6 +42,21 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from .layout import offsets, blob_order
+
+# static feature widths and pool fan-ins of the reference tables
+# (ptcg/rl/cards.py:19-82; ptcg_model2.cu:383-396)
+STATIC_SHAPES = dict(card_static=58, att_static=15, card_text=128, att_text=64, skill_text=64)
+K_ATT, K_SK = 4, 2
+# oracle block: 24 opp-hand (id, count/4), 24 split (id, deck/4, prize/4),
+# 8 my-prize (id, count/4) slots (ptcg/rl/buffers.py:42-45)
+N_HAND, N_SPLIT, N_PRIZE = 24, 24, 8
+ZONE_MY_UNSEEN = 9
+AUX_VF_COEF, AUX_HAND_COEF, AUX_PRIZE_COEF = 1.0, 0.1, 0.1   # ptcg_model.cu:85-87
+
+
+def card_in_width(dm):
+    """[id64 | static58 | text128 | a_mean | a_max | s_mean | s_max]"""
+    return 64 + 58 + 128 + 2 * dm.d_a + 2 * dm.d_c
 
 
 class Block(nn.Module):
@@ -57,17 +86,30 @@ class Block(nn.Module):
         return x + self.ffn(self.ln2(x))
 
 
+def first_max_pool(v):
+    """max over dim 1 whose gradient goes to the first maximal slot only."""
+    idx = torch.argmax(v, dim=1, keepdim=True)
+    return v.gather(1, idx).squeeze(1)
+
+
 class OraclePolicy(nn.Module):
     def __init__(self, dm):
         super().__init__()
-        if dm.tables != 0 or dm.critic != 0:
-            raise NotImplementedError(
-                "oracle restates the learned-table / blind-critic model only")
         self.dm = dm
         d, dc, da, G = dm.d, dm.d_c, dm.d_a, dm.g
         self.off, self.obs_size = offsets(dm)
-        self.card_table = nn.Parameter(torch.randn(dm.n_cards, dc))
-        self.attack_table = nn.Parameter(torch.randn(dm.n_attacks, da))
+        if dm.tables == 0:
+            self.card_table = nn.Parameter(torch.randn(dm.n_cards, dc))
+            self.attack_table = nn.Parameter(torch.randn(dm.n_attacks, da))
+        else:
+            self.card_id_emb = nn.Embedding(dm.n_cards, 64)
+            self.attack_id_emb = nn.Embedding(dm.n_attacks, 48)
+            self.skill_id_emb = nn.Embedding(dm.n_skills, 48)
+            self.attack_mlp = nn.Sequential(nn.Linear(48 + 15 + 64, da), nn.GELU())
+            self.skill_mlp = nn.Sequential(nn.Linear(48 + 64, dc), nn.GELU())
+            ci = card_in_width(dm)
+            self.card_mlp = nn.Sequential(nn.LayerNorm(ci), nn.Linear(ci, 256), nn.GELU(), nn.Linear(256, dc))
+            self.static = None
         self.zone_emb = nn.Embedding(dm.n_zones, 8)
         self.owner_emb = nn.Embedding(dm.n_owners, 4)
         self.token_proj = nn.Linear(2 * dc + dm.tok_f + 8 + 4, d)
@@ -88,6 +130,48 @@ class OraclePolicy(nn.Module):
         self.score_mlp = nn.Sequential(nn.Linear(3 * d + G + 64, 256), nn.GELU(), nn.Linear(256, 1))
         nn.init.orthogonal_(self.score_mlp[-1].weight, gain=0.01)
         self.value_mlp = nn.Sequential(nn.Linear(d + G, 256), nn.GELU(), nn.Linear(256, 1))
+        if dm.critic == 1:
+            if dm.oracle_f != 2 * N_HAND + 3 * N_SPLIT + 2 * N_PRIZE:
+                raise ValueError(f"oracle critic needs a {2 * N_HAND + 3 * N_SPLIT + 2 * N_PRIZE}-float oracle block")
+            self.oracle_proj = nn.Linear(dc + 6, d)
+            self.critic_readout = nn.Parameter(torch.randn(d) * 0.02)
+            self.critic_blocks = nn.ModuleList([Block(d, dm.heads, dm.ffn)])
+            self.oracle_value_mlp = nn.Sequential(nn.Linear(d + G, 256), nn.GELU(), nn.Linear(256, 1))
+            self.aux_hand = nn.Linear(d + G, dm.n_cards)
+            self.aux_prize = nn.Linear(d, 1)
+
+    # ---- static tables (pt_static_upload, ptcg_model2.cu:383-419)
+    def set_static(self, st):
+        """st: dict of numpy arrays card_static (n_cards, 58), att_static
+        (n_attacks, 15), card_text (n_cards, 128), att_text (n_attacks, 64),
+        skill_text (n_skills, 64), card_attacks (n_cards, 4) and card_skills
+        (n_cards, 2) integer ids (0 = empty slot)."""
+        dt = next(self.parameters()).dtype
+        self.static = {k: torch.as_tensor(v).to(dt) if k in STATIC_SHAPES else torch.as_tensor(v).long()
+                       for k, v in st.items()}
+        return self
+
+    def tables(self):
+        """(card_vec (n_cards, d_c), attack_vec (n_attacks, d_a))."""
+        if self.dm.tables == 0:
+            return self.card_table, self.attack_table
+        if self.static is None:
+            raise RuntimeError("static tables not set (set_static)")
+        st = self.static
+        att = self.attack_mlp(torch.cat([self.attack_id_emb.weight, st["att_static"], st["att_text"]], -1))
+        sk = self.skill_mlp(torch.cat([self.skill_id_emb.weight, st["skill_text"]], -1))
+
+        def pools(tab, ids):
+            m = (ids > 0).unsqueeze(-1).to(tab.dtype)
+            v = tab[ids] * m                      # masked slots are 0-valued participants
+            mean = v.sum(1) / m.sum(1).clamp(min=1)
+            return mean, first_max_pool(v)
+
+        a_mean, a_max = pools(att, st["card_attacks"])
+        s_mean, s_max = pools(sk, st["card_skills"])
+        cv = self.card_mlp(torch.cat([self.card_id_emb.weight, st["card_static"], st["card_text"],
+                                      a_mean, a_max, s_mean, s_max], -1))
+        return cv, att
 
     # ---- blob IO (native_weights.py:94-113)
     def named_blob_params(self):
@@ -123,7 +207,7 @@ class OraclePolicy(nn.Module):
         dm = self.dm
         B = obs.shape[0]
         L = dm.l_tok
-        cv, av = self.card_table, self.attack_table
+        cv, av = self.tables()
         tok = self._take(obs, "tok_int").reshape(B, L, dm.tok_int)
         ti = tok.long()
         tok_f = self._take(obs, "tok_float").reshape(B, L, dm.tok_f)
@@ -174,18 +258,94 @@ class OraclePolicy(nn.Module):
         gg = g.unsqueeze(1).expand(-1, NO, -1)
         dd = d_vec.unsqueeze(1).expand(-1, NO, -1)
         scores = self.score_mlp(torch.cat([q, rr, gg, dd, q * rr], dim=-1)).squeeze(-1)
-        value = self.value_mlp(torch.cat([r, g], dim=-1))
+        rg = torch.cat([r, g], dim=-1)
+        blind_v = self.value_mlp(rg)
+        parts = dict(h=h, r=r, g=g, d_vec=d_vec, keep=keep, q=q, x0_bc=bc, card_vec=cv, attack_vec=av,
+                     blind_v=blind_v)
+        if dm.critic == 1:
+            value = self._oracle_value(obs, cv, h, keep, g)
+            parts["hand_lin"] = self.aux_hand(rg)
+            parts["prize_logit"] = self.aux_prize(h[:, 1:]).squeeze(-1)
+        else:
+            value = blind_v
         out = torch.cat([scores, value], dim=-1)
         if return_parts:
-            return out, dict(h=h, r=r, g=g, d_vec=d_vec, keep=keep, q=q, x0_bc=bc)
+            return out, parts
         return out
 
+    def _oracle_ids(self, obs):
+        o = self._take(obs, "oracle")
+        H, S, P = N_HAND, N_SPLIT, N_PRIZE
+        hand = o[:, :2 * H].reshape(-1, H, 2)
+        split = o[:, 2 * H:2 * H + 3 * S].reshape(-1, S, 3)
+        prize = o[:, 2 * H + 3 * S:].reshape(-1, P, 2)
+        return hand, split, prize
 
-def build(dm, blob=None, seed=0, dtype=torch.float32):
+    def _oracle_value(self, obs, cv, h, keep, g):
+        """Critic top (model.py:278-308; k_otok_in / k_xc, ptcg_model.cu:441-496)."""
+        dm = self.dm
+        B = obs.shape[0]
+        hand, split, prize = self._oracle_ids(obs)
+        H, S, P = N_HAND, N_SPLIT, N_PRIZE
+        ids = torch.cat([hand[:, :, 0], split[:, :, 0], prize[:, :, 0]], 1).long()
+        feats = torch.zeros(B, H + S + P, 6, dtype=h.dtype)
+        feats[:, :H, 0] = 1.0
+        feats[:, :H, 3] = hand[:, :, 1]
+        feats[:, H:H + S, 1] = 1.0
+        feats[:, H:H + S, 4] = split[:, :, 1]
+        feats[:, H:H + S, 5] = split[:, :, 2]
+        feats[:, H + S:, 2] = 1.0
+        feats[:, H + S:, 3] = prize[:, :, 1]
+        otok = self.oracle_proj(torch.cat([cv[ids.clamp(0, dm.n_cards - 1)], feats], -1))
+        x = torch.cat([self.critic_readout.expand(B, 1, -1), h, otok], 1)
+        kc = torch.cat([torch.ones(B, 1, dtype=torch.bool), keep, ids > 0], 1)
+        for blk in self.critic_blocks:
+            x = blk(x, kc)
+        return self.oracle_value_mlp(torch.cat([x[:, 0], g], -1))
+
+    def aux_loss(self, obs, parts, returns):
+        """The belief / blind-value losses the native backward applies
+        (k_aux_targets, k_hand_grad, k_prize_count/grad, k_blind_grad,
+        ptcg_model2.cu:219-285): their autograd gradient is the injected one."""
+        dm = self.dm
+        B = obs.shape[0]
+        NC = dm.n_cards
+        dt = parts["h"].dtype
+        hand, _, prize = self._oracle_ids(obs)
+        # opp-hand count targets: += 4*count at id, ids in (0, NC) except the unknown id NC-1
+        hid = hand[:, :, 0].long()
+        hcnt = hand[:, :, 1].to(dt) * 4.0
+        ok = (hid > 0) & (hid < NC) & (hid != NC - 1) & (hcnt != 0)
+        tgt = torch.zeros(B, NC, dtype=dt)
+        rows = torch.arange(B).unsqueeze(1).expand_as(hid)
+        tgt.index_put_((rows[ok], hid[ok]), hcnt[ok], accumulate=True)
+        # my-prize indicator
+        pid = prize[:, :, 0].long()
+        pok = (pid > 0) & (pid < NC) & (prize[:, :, 1] > 0)
+        prized = torch.zeros(B, NC, dtype=dt)
+        prows = torch.arange(B).unsqueeze(1).expand_as(pid)
+        prized[prows[pok], pid[pok]] = 1.0
+        l_hand = AUX_HAND_COEF * ((F.softplus(parts["hand_lin"]) - tgt) ** 2).sum() / (B * NC)
+        ret = torch.as_tensor(returns).to(dt).reshape(B, 1)
+        l_blind = AUX_VF_COEF * 0.5 * ((parts["blind_v"] - ret) ** 2).sum() / B
+        ti = self._take(obs, "tok_int").reshape(B, dm.l_tok, dm.tok_int).long()
+        unseen = ti[:, :, 1] == ZONE_MY_UNSEEN
+        cnt = max(int(unseen.sum()), 1)
+        t = prized.gather(1, ti[:, :, 0].clamp(0, NC - 1))
+        bce = F.binary_cross_entropy_with_logits(parts["prize_logit"], t, reduction="none")
+        l_prize = AUX_PRIZE_COEF * (bce * unseen.to(dt)).sum() / cnt
+        return l_blind + l_hand + l_prize
+
+
+def build(dm, blob=None, seed=0, dtype=torch.float32, static=None):
     """Construct the oracle; with ``blob`` load those weights, else a
-    torch-seeded default init (native_weights.py:116-121 analogue)."""
+    torch-seeded default init (native_weights.py:116-121 analogue).  The
+    static-table model takes its static features in ``static``."""
     torch.manual_seed(seed)
     m = OraclePolicy(dm)
     if blob is not None:
         m.load_blob(blob)
-    return m.to(dtype)
+    m = m.to(dtype)
+    if static is not None:
+        m.set_static(static)
+    return m

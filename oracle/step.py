@@ -14,14 +14,19 @@ def minibatch_step(model, opt, obs, inp, hyp):
     m0, m1 = off["opt_mask"]
     mask = obs[:, m0:m1]
     T = lambda k: torch.as_tensor(inp[k])
-    out = model(obs)
+    out, parts = model(obs, return_parts=True)
     res = ppo_loss(out.detach(), mask, T("actions"), T("logprobs"), T("advantages"),
                    T("returns"), T("values"), clip=hyp["clip_coef"],
                    vf_clip=hyp["vf_clip_coef"], vf_coef=hyp["vf_coef"],
                    ent_coef=hyp["ent_coef"])
     for p in model.parameters():
         p.grad = None
-    out.backward(res["grad"])
+    # PPO gradient on [scores || value]; with the oracle critic the aux losses
+    # the native backward injects (ptcg_model4.cu:26-61) join the objective
+    obj = (out * res["grad"].to(out.dtype)).sum()
+    if model.dm.critic == 1:
+        obj = obj + model.aux_loss(obs, parts, inp["returns"])
+    obj.backward()
     gate = kl_gate(float(res["stats"][5]), float(res["stats"][1]),
                    hyp.get("kl_skip_threshold", 0.0), hyp.get("vf_skip_threshold", 0.0))
     norm = opt.step(hyp["max_grad_norm"], gate)

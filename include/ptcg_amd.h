@@ -87,6 +87,21 @@ int ptcg_model_forward(PtcgModel* m, const float* obs, const int32_t* row_idx, i
 int ptcg_model_backward(PtcgModel* m, const float* grad, void* stream);
 /* free_weights + free_activations (ptcg_model4.cu:283-284).                */
 void ptcg_model_free(PtcgModel* m);
+/* pt_static_upload (ptcg_model2.cu:383-419), static-table models
+ * (dims.tables == 1) only: host arrays card_static (n_cards, 58),
+ * att_static (n_attacks, 15), card_text (n_cards, 128), att_text
+ * (n_attacks, 64), skill_text (n_skills, 64), card_attacks (n_cards, 4) ids
+ * in [0, n_attacks), card_skills (n_cards, 2) ids in [0, n_skills); 0 = an
+ * empty slot.  Copied to device memory the model owns; required before the
+ * first forward.                                                          */
+int ptcg_model_set_static(PtcgModel* m, const float* card_static, const float* att_static,
+                          const float* card_text, const float* att_text, const float* skill_text,
+                          const int32_t* card_attacks, const int32_t* card_skills);
+/* ptcg_bind_train_graph (ptcg_model2.cu:323-330), oracle-critic models
+ * (dims.critic == 1): device array of per-row returns the blind-value aux
+ * loss regresses to, indexed like the obs rows of the forward (through its
+ * row_idx when one was given).  Read by ptcg_model_backward.              */
+int ptcg_model_bind_returns(PtcgModel* m, const float* returns);
 
 /* ---- PPO loss fwd+bwd (pufferlib.cu:1368-1449; kernels :949-1363) -------
  * dec_out (n, A+1) fused [scores || value]; mask (n rows at mask_stride,
@@ -142,6 +157,10 @@ int ptcg_trainer_load_state(PtcgTrainer* t, const char* path);
 /* debug_forward (bindings.cu:221-250): host obs (minibatch rows) -> host
  * out (minibatch, n_opt+1); synchronous.                                  */
 int ptcg_trainer_debug_forward(PtcgTrainer* t, const float* obs_host, int n, float* out_host);
+/* ptcg_model_set_static on the trainer's model.                          */
+int ptcg_trainer_set_static(PtcgTrainer* t, const float* card_static, const float* att_static,
+                            const float* card_text, const float* att_text, const float* skill_text,
+                            const int32_t* card_attacks, const int32_t* card_skills);
 /* One PPO minibatch step on device data (the body of train_impl's loop,
  * pufferlib.cu:2039-2105): forward -> loss fwd+bwd -> backward -> gate ->
  * clip + Adam.  obs rows and the per-row inputs (actions, old log-probs,

@@ -483,6 +483,7 @@ static int fwd_bwd(PtcgTrainer* t, const float* obs, const int32_t* idx, const f
                        old_logprobs, advantages, returns, values, nullptr, h.clip_coef, h.vf_clip_coef,
                        h.vf_coef, h.ent_coef, t->grad, t->ratio, t->newvalue, t->stats, t->guard,
                        t->ppo_part, s));
+    PT_TRY(ptcg_model_bind_returns(t->model, returns));
     PT_TRY(ptcg_model_backward(t->model, t->grad, s));
     return PTCG_OK;
 }
@@ -492,6 +493,14 @@ extern "C" int ptcg_trainer_forward_backward(PtcgTrainer* t, const float* obs, c
                                              const float* advantages, const float* returns,
                                              const float* values, void* stream) {
     return fwd_bwd(t, obs, row_idx, actions, old_logprobs, advantages, returns, values, (hipStream_t)stream);
+}
+
+extern "C" int ptcg_trainer_set_static(PtcgTrainer* t, const float* card_static, const float* att_static,
+                                       const float* card_text, const float* att_text, const float* skill_text,
+                                       const int32_t* card_attacks, const int32_t* card_skills) {
+    PT_REQUIRE(t, "trainer_set_static: null trainer");
+    return ptcg_model_set_static(t->model, card_static, att_static, card_text, att_text, skill_text,
+                                 card_attacks, card_skills);
 }
 
 extern "C" int ptcg_trainer_step(PtcgTrainer* t, const float* obs, const int32_t* row_idx,

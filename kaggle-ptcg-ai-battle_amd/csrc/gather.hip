@@ -334,21 +334,21 @@ __global__ void sc_in_bwd_kernel(GatherCtx c, const float* __restrict__ d_sc,
 }
 
 __global__ void val_in_fwd_kernel(GatherCtx c, const float* __restrict__ h,
-        const float* __restrict__ gd, float* __restrict__ v) {
+        const float* __restrict__ gd, float* __restrict__ v, int ls) {
     const int D = c.dm.d, W = c.dx.val_in;
     const long i = (long)blockIdx.x * TB + threadIdx.x;
     if (i >= (long)c.N * W) return;
     const int n = (int)(i / W), col = (int)(i % W);
-    v[i] = col < D ? h[(long)n * c.dx.l_seq * D + col] : gd[(long)n * c.dx.bcast_in + (col - D)];
+    v[i] = col < D ? h[(long)n * ls * D + col] : gd[(long)n * c.dx.bcast_in + (col - D)];
 }
 
 __global__ void val_in_bwd_kernel(GatherCtx c, const float* __restrict__ dv, float* __restrict__ d_h,
-                                  float* __restrict__ d_gd) {
+                                  float* __restrict__ d_gd, int ls) {
     const int D = c.dm.d, W = c.dx.val_in;
     const long i = (long)blockIdx.x * TB + threadIdx.x;
     if (i >= (long)c.N * W) return;
     const int n = (int)(i / W), col = (int)(i % W);
-    if (col < D) d_h[(long)n * c.dx.l_seq * D + col] += dv[i];
+    if (col < D) d_h[(long)n * ls * D + col] += dv[i];
     else d_gd[(long)n * c.dx.bcast_in + (col - D)] += dv[i];
 }
 
@@ -492,13 +492,13 @@ int pt_sc_in_bwd(const GatherCtx& c, const float* d_sc, const float* sc_in, floa
     PT_LAUNCH_CHECK();
     return PTCG_OK;
 }
-int pt_val_in_fwd(const GatherCtx& c, const float* h, const float* gd, float* val_in, hipStream_t s) {
-    hipLaunchKernelGGL(val_in_fwd_kernel, PT_GRID((long)c.N * c.dx.val_in), c, h, gd, val_in);
+int pt_val_in_fwd(const GatherCtx& c, const float* h, const float* gd, float* val_in, hipStream_t s, int ls) {
+    hipLaunchKernelGGL(val_in_fwd_kernel, PT_GRID((long)c.N * c.dx.val_in), c, h, gd, val_in, ls ? ls : c.dx.l_seq);
     PT_LAUNCH_CHECK();
     return PTCG_OK;
 }
-int pt_val_in_bwd(const GatherCtx& c, const float* d_val_in, float* d_h, float* d_gd, hipStream_t s) {
-    hipLaunchKernelGGL(val_in_bwd_kernel, PT_GRID((long)c.N * c.dx.val_in), c, d_val_in, d_h, d_gd);
+int pt_val_in_bwd(const GatherCtx& c, const float* d_val_in, float* d_h, float* d_gd, hipStream_t s, int ls) {
+    hipLaunchKernelGGL(val_in_bwd_kernel, PT_GRID((long)c.N * c.dx.val_in), c, d_val_in, d_h, d_gd, ls ? ls : c.dx.l_seq);
     PT_LAUNCH_CHECK();
     return PTCG_OK;
 }

@@ -87,8 +87,9 @@ int pt_q_in_bwd(const GatherCtx& c, const float* d_qin, float* d_h, float* d_tem
 int pt_sc_in_fwd(const GatherCtx& c, const float* h, const float* gd, float* sc_in, hipStream_t s);
 int pt_sc_in_bwd(const GatherCtx& c, const float* d_sc, const float* sc_in, float* d_q,
                  float* d_h, float* d_gd, hipStream_t s);
-int pt_val_in_fwd(const GatherCtx& c, const float* h, const float* gd, float* val_in, hipStream_t s);
-int pt_val_in_bwd(const GatherCtx& c, const float* d_val_in, float* d_h, float* d_gd, hipStream_t s);
+// [seq[:, 0] | g] over sequences of ls rows (ls = 0: the trunk's l_seq)
+int pt_val_in_fwd(const GatherCtx& c, const float* h, const float* gd, float* val_in, hipStream_t s, int ls = 0);
+int pt_val_in_bwd(const GatherCtx& c, const float* d_val_in, float* d_h, float* d_gd, hipStream_t s, int ls = 0);
 // y[r] = X[r,:] . w + b, written to out[r / per * ldo + col0 + r % per]
 int pt_head_dot(const float* X, int rows, int K, const float* w, const float* b, float* out,
                 int per, long ldo, int col0, hipStream_t s);
@@ -99,3 +100,19 @@ int pt_head_dot_bwd(const float* grad, int per, long ldg, int col0, const float*
 int pt_head_dot_dw(const float* grad, int per, long ldg, int col0, const float* X, int rows, int K,
                    float* dw, float* db, float* ws, long ws_floats, hipStream_t s);
 int pt_fill_zero(float* p, long n, hipStream_t s);
+
+// ---- reference model variant: static tables, oracle critic, aux losses (frozen.hip)
+int pt_copy_cols(float* dst, long ldd, const float* src, long lds, int rows, int cols, hipStream_t s);
+int pt_pool_fwd(const float* tab, int E, const int* ids, int K, int NC, float* out, long ldo, int col_mean,
+                int col_max, int* amax, hipStream_t s);
+int pt_pool_bwd(const float* dsrc, long ld, int col_mean, int col_max, const int* amax, const int* ids, int K,
+                int NC, int E, float* d_tab, hipStream_t s);
+int pt_gelu_bwd(const float* dy, const float* pre, float* dx, long n, hipStream_t s);
+int pt_otok_in(const GatherCtx& c, const float* cv, const float* keep, float* out, float* ckeep, hipStream_t s);
+int pt_otok_bwd(const GatherCtx& c, const float* d_in, float* d_card, hipStream_t s);
+int pt_xc_fwd(const float* cread, const float* h, const float* otok, float* xc, int N, int Ls, int NO, int D,
+              hipStream_t s);
+int pt_xc_bwd(const float* d_xc, float* d_h, float* d_otok, int N, int Ls, int NO, int D, hipStream_t s);
+int pt_aux_grads(const GatherCtx& c, const float* hand_lin, const float* prize_all, const float* blind_v,
+                 const float* ret, int* cnt, float* d_hand, float* d_prize, float* d_blind, hipStream_t s);
+int pt_rank1_add(const float* dy, const float* w, float* dX, int rows, int K, hipStream_t s);

@@ -2,17 +2,22 @@
 //
 // Mirrors the reference's PTCG Encoder plugin (native/model/ptcg_model3.cu
 // ptcg_forward_core :246-369, blk_fwd :12-40, blk_bwd :44-95;
-// ptcg_model4.cu ptcg_backward_core :10-190) for the learned-table /
-// blind-critic model, with a different kernel plan:
+// ptcg_model4.cu ptcg_backward_core :10-190; ptcg_model2.cu tables_fwd /
+// tables_bwd :422-485) with a different kernel plan:
 //   * GEMM epilogues carry bias, GELU (pre-activation kept), residual add
 //     and GELU-backward, so there are no separate bias / gelu / add kernels;
 //   * attention is one fused kernel per direction (no (N,H,L,L) tensor);
 //   * concat inputs are written in place by the producing GEMMs (leading
 //     dimension = concat width) — g/dvec into the bcast input, opt_card /
-//     opt_attack into q_in, q into the score input;
+//     opt_attack into q_in, q into the score input; the static / text
+//     columns of the table-chain inputs are written once at upload;
 //   * every activation the backward needs is kept (LayerNorm outputs, qkv,
 //     attention context, GELU pre- and post-activations), so the backward
 //     recomputes nothing but the attention probabilities.
+// Two switches select the model variant: tables (learned card / attack
+// tables, or the static-table chain rebuilt every forward) and critic (blind
+// value head, or the oracle critic block with the blind value and belief aux
+// heads trained by losses injected in the backward).
 // Grads are overwritten on every backward (ptcg_model4.cu:15-21).
 #include "model.h"
 
@@ -36,11 +41,27 @@ struct PtcgModel {
     long arena = 0;
     float* P = nullptr;
     float* Gr = nullptr;
-    float *card, *att, *zemb, *oemb, *tp_w, *tp_b, *readout, *g1_w, *g1_b, *g2_w, *g2_b, *semb,
-        *cemb, *d1_w, *d1_b, *d2_w, *d2_b, *bc_w, *bc_b;
+    // card / attack vectors the gathers read, and where their gradients go:
+    // the learned tables and their grads, or the table chain's outputs and
+    // scratch gradients that the chain's backward consumes
+    float *card = nullptr, *att = nullptr, *dcard = nullptr, *datt = nullptr;
+    float *zemb, *oemb, *tp_w, *tp_b, *readout, *g1_w, *g1_b, *g2_w, *g2_b, *semb, *cemb, *d1_w, *d1_b,
+        *d2_w, *d2_b, *bc_w, *bc_b;
     std::vector<BlockP> blk;
     float *lnf_w, *lnf_b, *temb, *oc_w, *oc_b, *oa_w, *oa_b, *q1_w, *q1_b, *q2_w, *q2_b, *s1_w,
         *s1_b, *s2_w, *s2_b, *v1_w, *v1_b, *v2_w, *v2_b;
+    // static-table chain weights (tables == 1)
+    float *cid_emb = nullptr, *aid_emb, *sid_emb, *am_w, *am_b, *sm_w, *sm_b, *cln_w, *cln_b, *c1_w, *c1_b,
+        *c3_w, *c3_b;
+    // oracle critic + aux heads (critic == 1)
+    float *op_w = nullptr, *op_b, *cread, *ov1_w, *ov1_b, *ov2_w, *ov2_b, *ah_w, *ah_b, *ap_w, *ap_b;
+    BlockP cblk;
+    // static tables and the chain's batch-independent buffers (own allocation)
+    char* tmem = nullptr;
+    int *card_attacks, *card_skills, *a_amax, *s_amax;
+    float *att_in, *att_lin, *att_tab, *sk_in, *sk_lin, *sk_tab, *card_in, *c_mu, *c_rs, *card_ln, *card_h1,
+        *card_g1, *card_vec;
+    float *d_card_vec, *d_att_tab, *d_sk_tab, *d_card_h, *d_card_ln, *d_card_in, *d_att_lin, *d_sk_lin;
     // activations
     int N = 0;
     char* mem = nullptr;
@@ -52,6 +73,12 @@ struct PtcgModel {
     float *ocard, *oatt, *q_in, *q1, *q1a, *sc_in, *s1, *s1a, *val_in, *v1, *v1a, *out;
     float *dxa, *dxb, *dffn, *dln, *dqkv, *dctx, *dsc, *ds1, *dq, *dq1, *dqin, *docard, *doatt,
         *dvin, *dv1, *dgd, *dd1, *dg1, *ddec, *dtokp, *dtokcat, *dbc;
+    // oracle critic / aux activations and scratch
+    float *otok_in, *otok, *ckeep, *xc, *xco, *ov_in, *ov1, *ov1a, *bv, *hand_lin, *prize_all;
+    BlockA cba;
+    float *d_hand, *d_prize, *d_blind, *dxc, *dxc2, *dotok, *dotok_in, *dov1, *dovin;
+    int* aux_cnt;
+    const float* ret = nullptr;
     float* ws = nullptr;
     long ws_floats = 0;
     const float* obs = nullptr;
@@ -77,19 +104,24 @@ static int linf(const float* X, const float* W, const float* b, float* Y, int ro
                 int out, int epi, const float* R, float* Y2, hipStream_t s) {
     return lin(X, in, W, b, Y, out, rows, in, out, epi, R, out, Y2, out, s);
 }
-// dX = dY W : dY (rows, out) ld lddy ; W (out, in) ; dX (rows, in) ld lddx
-static int ldx_(const float* dY, long lddy, const float* W, float* dX, long lddx, int rows, int in,
-                int out, int epi, const float* R, long ldr, hipStream_t s) {
+// dX = dY W[:, :in] : dY (rows, out) ld lddy ; W (out, ldw) ; dX (rows, in) ld lddx
+static int ldxw_(const float* dY, long lddy, const float* W, long ldw, float* dX, long lddx, int rows, int in,
+                 int out, int epi, const float* R, long ldr, hipStream_t s) {
     GemmArgs g{};
     g.M = rows; g.N = in; g.K = out;
     g.A = dY; g.lda = lddy; g.a_t = 0;
-    g.B = W; g.ldb = in; g.b_t = 1;
+    g.B = W; g.ldb = ldw; g.b_t = 1;
     g.C = dX; g.ldc = lddx;
     g.R = R; g.ldr = ldr;
     g.epi = epi;
     return pt_gemm(g, nullptr, 0, s);
 }
-// dW = dY^T X (overwrite), db = colsum dY
+// dX = dY W : dY (rows, out) ld lddy ; W (out, in) ; dX (rows, in) ld lddx
+static int ldx_(const float* dY, long lddy, const float* W, float* dX, long lddx, int rows, int in,
+                int out, int epi, const float* R, long ldr, hipStream_t s) {
+    return ldxw_(dY, lddy, W, in, dX, lddx, rows, in, out, epi, R, ldr, s);
+}
+// dW = dY^T X (overwrite), db = colsum dY (fused into the product)
 static int ldw_(PtcgModel* m, const float* dY, long lddy, const float* X, long ldxx, float* dW,
                 float* db, int rows, int in, int out, hipStream_t s) {
     GemmArgs g{};
@@ -102,13 +134,22 @@ static int ldw_(PtcgModel* m, const float* dY, long lddy, const float* X, long l
     return pt_gemm(g, m->ws, m->ws_floats, s);
 }
 
+struct Carver {
+    char* base; size_t off = 0;
+    float* take(size_t floats) {
+        off = (off + 255) & ~(size_t)255;
+        float* p = base ? reinterpret_cast<float*>(base + off) : nullptr;
+        off += floats * sizeof(float);
+        return p;
+    }
+};
+
 // ------------------------------------------------------------ lifecycle
 extern "C" int ptcg_model_create(const PtcgDims* dims, PtcgModel** out) {
     PT_REQUIRE(dims && out, "model_create: null argument");
     PtcgDims d = *dims;
-    PT_REQUIRE(d.tables == 0 && d.critic == 0,
-               "model_create: only the learned-table / blind-critic model is implemented "
-               "(tables=%d critic=%d)", d.tables, d.critic);
+    PT_REQUIRE(d.tables == 0 || d.tables == 1, "model_create: unknown tables mode %d", d.tables);
+    PT_REQUIRE(d.critic == 0 || d.critic == 1, "model_create: unknown critic mode %d", d.critic);
     PT_REQUIRE(d.d % d.heads == 0, "model_create: d=%d not divisible by heads=%d", d.d, d.heads);
     PT_REQUIRE(d.n_opt <= 64, "model_create: n_opt=%d > 64 unsupported", d.n_opt);
     PT_REQUIRE(d.d % 4 == 0 && d.d_c % 4 == 0 && d.d_a % 4 == 0 && d.g % 4 == 0 && d.ffn % 4 == 0 &&
@@ -116,6 +157,15 @@ extern "C" int ptcg_model_create(const PtcgDims* dims, PtcgModel** out) {
                "model_create: widths must be multiples of 4");
     PT_REQUIRE(pt_attn_supported(d.l_tok + 1, d.d / d.heads),
                "model_create: attention shape L=%d Dh=%d unsupported", d.l_tok + 1, d.d / d.heads);
+    if (d.critic == 1) {
+        PT_REQUIRE(d.oracle_f == 2 * PT_N_HAND + 3 * PT_N_SPLIT + 2 * PT_N_PRIZE,
+                   "model_create: the oracle critic needs a %d-float oracle block, got %d",
+                   2 * PT_N_HAND + 3 * PT_N_SPLIT + 2 * PT_N_PRIZE, d.oracle_f);
+        const int lc = d.l_tok + 2 + PT_N_HAND + PT_N_SPLIT + PT_N_PRIZE;
+        PT_REQUIRE(pt_attn_supported(lc, d.d / d.heads),
+                   "model_create: critic attention shape L=%d Dh=%d unsupported", lc, d.d / d.heads);
+        PT_REQUIRE(d.n_cards <= 8192, "model_create: n_cards=%d too large for the aux targets", d.n_cards);
+    }
     PtcgModel* m = new PtcgModel();
     m->dm = d;
     m->dx = pt_dims_x(d);
@@ -137,6 +187,19 @@ extern "C" int ptcg_model_create(const PtcgDims* dims, PtcgModel** out) {
 
 long pt_model_arena(const PtcgModel* m) { return m->arena; }
 
+static void bind_block(const std::map<std::string, float*>& byname, const std::string& p, BlockP& b) {
+    auto get = [&](const std::string& n) -> float* {
+        auto it = byname.find(n);
+        return it == byname.end() ? nullptr : it->second;
+    };
+    b.ln1w = get(p + "ln1.weight"); b.ln1b = get(p + "ln1.bias");
+    b.qkvw = get(p + "qkv.weight"); b.qkvb = get(p + "qkv.bias");
+    b.projw = get(p + "proj.weight"); b.projb = get(p + "proj.bias");
+    b.ln2w = get(p + "ln2.weight"); b.ln2b = get(p + "ln2.bias");
+    b.f1w = get(p + "ffn.0.weight"); b.f1b = get(p + "ffn.0.bias");
+    b.f2w = get(p + "ffn.2.weight"); b.f2b = get(p + "ffn.2.bias");
+}
+
 extern "C" int ptcg_model_bind(PtcgModel* m, float* params, float* grads) {
     PT_REQUIRE(m && params && grads, "model_bind: null argument");
     PT_REQUIRE(((uintptr_t)params & 15) == 0 && ((uintptr_t)grads & 15) == 0,
@@ -149,7 +212,20 @@ extern "C" int ptcg_model_bind(PtcgModel* m, float* params, float* grads) {
         auto it = byname.find(n);
         return it == byname.end() ? nullptr : it->second;
     };
-    m->card = get("card_table"); m->att = get("attack_table");
+    if (m->dm.tables == 0) {
+        m->card = get("card_table"); m->att = get("attack_table");
+        PT_REQUIRE(m->card && m->att, "model_bind: parameter table incomplete");
+        m->dcard = m->G(m->card); m->datt = m->G(m->att);
+    } else {
+        m->cid_emb = get("card_id_emb.weight"); m->aid_emb = get("attack_id_emb.weight");
+        m->sid_emb = get("skill_id_emb.weight");
+        m->am_w = get("attack_mlp.0.weight"); m->am_b = get("attack_mlp.0.bias");
+        m->sm_w = get("skill_mlp.0.weight"); m->sm_b = get("skill_mlp.0.bias");
+        m->cln_w = get("card_mlp.0.weight"); m->cln_b = get("card_mlp.0.bias");
+        m->c1_w = get("card_mlp.1.weight"); m->c1_b = get("card_mlp.1.bias");
+        m->c3_w = get("card_mlp.3.weight"); m->c3_b = get("card_mlp.3.bias");
+        PT_REQUIRE(m->cid_emb && m->c3_b, "model_bind: parameter table incomplete");
+    }
     m->zemb = get("zone_emb.weight"); m->oemb = get("owner_emb.weight");
     m->tp_w = get("token_proj.weight"); m->tp_b = get("token_proj.bias");
     m->readout = get("readout");
@@ -160,16 +236,7 @@ extern "C" int ptcg_model_bind(PtcgModel* m, float* params, float* grads) {
     m->d2_w = get("dec_mlp.2.weight"); m->d2_b = get("dec_mlp.2.bias");
     m->bc_w = get("bcast.weight"); m->bc_b = get("bcast.bias");
     m->blk.resize(m->dm.layers);
-    for (int i = 0; i < m->dm.layers; ++i) {
-        std::string p = "blocks." + std::to_string(i) + ".";
-        BlockP& b = m->blk[i];
-        b.ln1w = get(p + "ln1.weight"); b.ln1b = get(p + "ln1.bias");
-        b.qkvw = get(p + "qkv.weight"); b.qkvb = get(p + "qkv.bias");
-        b.projw = get(p + "proj.weight"); b.projb = get(p + "proj.bias");
-        b.ln2w = get(p + "ln2.weight"); b.ln2b = get(p + "ln2.bias");
-        b.f1w = get(p + "ffn.0.weight"); b.f1b = get(p + "ffn.0.bias");
-        b.f2w = get(p + "ffn.2.weight"); b.f2b = get(p + "ffn.2.bias");
-    }
+    for (int i = 0; i < m->dm.layers; ++i) bind_block(byname, "blocks." + std::to_string(i) + ".", m->blk[i]);
     m->lnf_w = get("ln_f.weight"); m->lnf_b = get("ln_f.bias");
     m->temb = get("opt_type_emb.weight");
     m->oc_w = get("opt_card.weight"); m->oc_b = get("opt_card.bias");
@@ -180,24 +247,106 @@ extern "C" int ptcg_model_bind(PtcgModel* m, float* params, float* grads) {
     m->s2_w = get("score_mlp.2.weight"); m->s2_b = get("score_mlp.2.bias");
     m->v1_w = get("value_mlp.0.weight"); m->v1_b = get("value_mlp.0.bias");
     m->v2_w = get("value_mlp.2.weight"); m->v2_b = get("value_mlp.2.bias");
-    PT_REQUIRE(m->card && m->att && m->v2_b, "model_bind: parameter table incomplete");
+    PT_REQUIRE(m->v2_b, "model_bind: parameter table incomplete");
+    if (m->dm.critic == 1) {
+        m->op_w = get("oracle_proj.weight"); m->op_b = get("oracle_proj.bias");
+        m->cread = get("critic_readout");
+        bind_block(byname, "critic_blocks.0.", m->cblk);
+        m->ov1_w = get("oracle_value_mlp.0.weight"); m->ov1_b = get("oracle_value_mlp.0.bias");
+        m->ov2_w = get("oracle_value_mlp.2.weight"); m->ov2_b = get("oracle_value_mlp.2.bias");
+        m->ah_w = get("aux_hand.weight"); m->ah_b = get("aux_hand.bias");
+        m->ap_w = get("aux_prize.weight"); m->ap_b = get("aux_prize.bias");
+        PT_REQUIRE(m->op_w && m->cblk.f2b && m->ap_b, "model_bind: parameter table incomplete");
+    }
     return PTCG_OK;
 }
 
-struct Carver {
-    char* base; size_t off = 0;
-    float* take(size_t floats) {
-        off = (off + 255) & ~(size_t)255;
-        float* p = base ? reinterpret_cast<float*>(base + off) : nullptr;
-        off += floats * sizeof(float);
-        return p;
+// the static-table chain's batch-independent buffers
+static size_t carve_tables(PtcgModel* m, char* base) {
+    const PtcgDims& d = m->dm;
+    const DimsX& x = m->dx;
+    const long NC = d.n_cards, NA = d.n_attacks, NS = d.n_skills;
+    Carver c{base};
+    m->card_attacks = reinterpret_cast<int*>(c.take(NC * PT_K_ATT));
+    m->card_skills = reinterpret_cast<int*>(c.take(NC * PT_K_SK));
+    m->a_amax = reinterpret_cast<int*>(c.take(NC * d.d_a));
+    m->s_amax = reinterpret_cast<int*>(c.take(NC * d.d_c));
+    m->att_in = c.take(NA * x.att_in); m->att_lin = c.take(NA * d.d_a); m->att_tab = c.take(NA * d.d_a);
+    m->sk_in = c.take(NS * x.sk_in); m->sk_lin = c.take(NS * d.d_c); m->sk_tab = c.take(NS * d.d_c);
+    m->card_in = c.take(NC * x.card_in); m->c_mu = c.take(NC); m->c_rs = c.take(NC);
+    m->card_ln = c.take(NC * x.card_in);
+    m->card_h1 = c.take(NC * PT_CARD_H); m->card_g1 = c.take(NC * PT_CARD_H);
+    m->card_vec = c.take(NC * d.d_c);
+    m->d_card_vec = c.take(NC * d.d_c); m->d_att_tab = c.take(NA * d.d_a); m->d_sk_tab = c.take(NS * d.d_c);
+    m->d_card_h = c.take(NC * PT_CARD_H);
+    m->d_card_ln = c.take(NC * x.card_in); m->d_card_in = c.take(NC * x.card_in);
+    m->d_att_lin = c.take(NA * d.d_a); m->d_sk_lin = c.take(NS * d.d_c);
+    return c.off;
+}
+
+extern "C" int ptcg_model_set_static(PtcgModel* m, const float* card_static, const float* att_static,
+                                     const float* card_text, const float* att_text, const float* skill_text,
+                                     const int32_t* card_attacks, const int32_t* card_skills) {
+    PT_REQUIRE(m, "model_set_static: null model");
+    PT_REQUIRE(m->dm.tables == 1, "model_set_static: the model has learned tables (tables=0)");
+    PT_REQUIRE(card_static && att_static && card_text && att_text && skill_text && card_attacks && card_skills,
+               "model_set_static: null table");
+    const PtcgDims& d = m->dm;
+    const DimsX& x = m->dx;
+    const long NC = d.n_cards, NA = d.n_attacks, NS = d.n_skills;
+    for (long i = 0; i < NC * PT_K_ATT; ++i)
+        PT_REQUIRE(card_attacks[i] >= 0 && card_attacks[i] < NA, "model_set_static: card_attacks[%ld]=%d "
+                   "outside [0, %ld)", i, card_attacks[i], NA);
+    for (long i = 0; i < NC * PT_K_SK; ++i)
+        PT_REQUIRE(card_skills[i] >= 0 && card_skills[i] < NS, "model_set_static: card_skills[%ld]=%d "
+                   "outside [0, %ld)", i, card_skills[i], NS);
+    if (!m->tmem) {
+        const size_t bytes = carve_tables(m, nullptr);
+        PT_HIP(hipMalloc(&m->tmem, bytes));
+        PT_HIP(hipMemset(m->tmem, 0, bytes));
+        carve_tables(m, m->tmem);
     }
-};
+    auto put = [&](float* dst, long ld, int col0, const float* src, int w, long rows) -> int {
+        PT_HIP(hipMemcpy2D(dst + col0, ld * sizeof(float), src, w * sizeof(float), w * sizeof(float), rows,
+                           hipMemcpyHostToDevice));
+        return PTCG_OK;
+    };
+    // concat inputs: [id | static | text] (the id columns are refreshed every forward)
+    PT_TRY(put(m->att_in, x.att_in, PT_ID_A, att_static, PT_ATT_STATIC, NA));
+    PT_TRY(put(m->att_in, x.att_in, PT_ID_A + PT_ATT_STATIC, att_text, PT_ATT_TEXT, NA));
+    PT_TRY(put(m->sk_in, x.sk_in, PT_ID_A, skill_text, PT_SKILL_TEXT, NS));
+    PT_TRY(put(m->card_in, x.card_in, PT_ID_C, card_static, PT_CARD_STATIC, NC));
+    PT_TRY(put(m->card_in, x.card_in, PT_ID_C + PT_CARD_STATIC, card_text, PT_CARD_TEXT, NC));
+    PT_HIP(hipMemcpy(m->card_attacks, card_attacks, NC * PT_K_ATT * sizeof(int), hipMemcpyHostToDevice));
+    PT_HIP(hipMemcpy(m->card_skills, card_skills, NC * PT_K_SK * sizeof(int), hipMemcpyHostToDevice));
+    m->card = m->card_vec;
+    m->att = m->att_tab;
+    m->dcard = m->d_card_vec;
+    m->datt = m->d_att_tab;
+    return PTCG_OK;
+}
+
+extern "C" int ptcg_model_bind_returns(PtcgModel* m, const float* returns) {
+    PT_REQUIRE(m, "model_bind_returns: null model");
+    m->ret = returns;
+    return PTCG_OK;
+}
+
+static void carve_block(Carver& c, BlockA& a, long NL, const PtcgDims& d) {
+    const long D = d.d;
+    a.ln1 = c.take(NL * D); a.mu1 = c.take(NL); a.rs1 = c.take(NL);
+    a.qkv = c.take(NL * 3 * D); a.ctx = c.take(NL * D); a.lse = c.take(NL * d.heads);
+    a.xmid = c.take(NL * D);
+    a.ln2 = c.take(NL * D); a.mu2 = c.take(NL); a.rs2 = c.take(NL);
+    a.ffp = c.take(NL * d.ffn); a.ffa = c.take(NL * d.ffn);
+}
 
 static size_t carve(PtcgModel* m, char* base) {
     const PtcgDims& d = m->dm;
     const DimsX& x = m->dx;
     const long N = m->N, Lt = d.l_tok, Ls = x.l_seq, NL = N * Ls, NO = d.n_opt, D = d.d;
+    const bool crit = d.critic == 1;
+    const long NLC = crit ? N * x.l_crit : 0, NLmax = NL > NLC ? NL : NLC, NK = N * x.n_orc;
     Carver c{base};
     m->tok_cat = c.take(N * Lt * x.tok_in);
     m->tokp = c.take(N * Lt * D);
@@ -211,13 +360,7 @@ static size_t carve(PtcgModel* m, char* base) {
     m->x.resize(d.layers + 1);
     for (auto& p : m->x) p = c.take(NL * D);
     m->ba.resize(d.layers);
-    for (auto& a : m->ba) {
-        a.ln1 = c.take(NL * D); a.mu1 = c.take(NL); a.rs1 = c.take(NL);
-        a.qkv = c.take(NL * 3 * D); a.ctx = c.take(NL * D); a.lse = c.take(NL * d.heads);
-        a.xmid = c.take(NL * D);
-        a.ln2 = c.take(NL * D); a.mu2 = c.take(NL); a.rs2 = c.take(NL);
-        a.ffp = c.take(NL * d.ffn); a.ffa = c.take(NL * d.ffn);
-    }
+    for (auto& a : m->ba) carve_block(c, a, NL, d);
     m->h = c.take(NL * D); m->lnf_mu = c.take(NL); m->lnf_rs = c.take(NL);
     m->ocard = c.take(N * NO * d.d_c); m->oatt = c.take(N * NO * d.d_a);
     m->q_in = c.take(N * NO * x.q_in);
@@ -227,10 +370,26 @@ static size_t carve(PtcgModel* m, char* base) {
     m->val_in = c.take(N * x.val_in);
     m->v1 = c.take(N * PT_VAL_H); m->v1a = c.take(N * PT_VAL_H);
     m->out = c.take(N * (NO + 1));
-    // backward scratch
+    if (crit) {
+        m->otok_in = c.take(NK * x.orc_in); m->otok = c.take(NK * D);
+        m->ckeep = c.take(NLC);
+        m->xc = c.take(NLC * D); m->xco = c.take(NLC * D);
+        carve_block(c, m->cba, NLC, d);
+        m->ov_in = c.take(N * x.val_in);
+        m->ov1 = c.take(N * PT_VAL_H); m->ov1a = c.take(N * PT_VAL_H);
+        m->bv = c.take(N);
+        m->hand_lin = c.take(N * d.n_cards);
+        m->prize_all = c.take(NL);
+        m->d_hand = c.take(N * d.n_cards); m->d_prize = c.take(NL); m->d_blind = c.take(N);
+        m->dxc = c.take(NLC * D); m->dxc2 = c.take(NLC * D);
+        m->dotok = c.take(NK * D); m->dotok_in = c.take(NK * x.orc_in);
+        m->dov1 = c.take(N * PT_VAL_H); m->dovin = c.take(N * x.val_in);
+        m->aux_cnt = reinterpret_cast<int*>(c.take(64));
+    }
+    // backward scratch (block scratch sized for the longer of trunk and critic)
     m->dxa = c.take(NL * D); m->dxb = c.take(NL * D);
-    m->dffn = c.take(NL * d.ffn); m->dln = c.take(NL * D);
-    m->dqkv = c.take(NL * 3 * D); m->dctx = c.take(NL * D);
+    m->dffn = c.take(NLmax * d.ffn); m->dln = c.take(NLmax * D);
+    m->dqkv = c.take(NLmax * 3 * D); m->dctx = c.take(NLmax * D);
     m->dsc = c.take(N * NO * x.score_in); m->ds1 = c.take(N * NO * PT_SC_H);
     m->dq = c.take(N * NO * D); m->dq1 = c.take(N * NO * D);
     m->dqin = c.take(N * NO * x.q_in);
@@ -242,7 +401,7 @@ static size_t carve(PtcgModel* m, char* base) {
     m->dbc = c.take(N * D);
     // workspace: split-K partials, column-sum / LayerNorm / head partials
     m->ws_floats = 16L << 20;
-    long ln_part = 2048L * D;   // LayerNorm dW/dB partials (layernorm.hip)
+    long ln_part = 4096L * (D > x.card_in ? D : x.card_in);   // LayerNorm dW/dB partials (layernorm.hip)
     if (ln_part > m->ws_floats) m->ws_floats = ln_part;
     m->ws = c.take(m->ws_floats);
     return c.off;
@@ -265,6 +424,7 @@ extern "C" int ptcg_model_reg_train(PtcgModel* m, int n) {
 extern "C" void ptcg_model_free(PtcgModel* m) {
     if (!m) return;
     if (m->mem) (void)hipFree(m->mem);
+    if (m->tmem) (void)hipFree(m->tmem);
     delete m;
 }
 
@@ -273,18 +433,43 @@ float* pt_model_out(const PtcgModel* m) { return m->out; }
 float* pt_model_ws(const PtcgModel* m, long* floats) { *floats = m->ws_floats; return m->ws; }
 
 // ------------------------------------------------------------ forward
-static int block_fwd(PtcgModel* m, int i, const float* xin, float* xout, hipStream_t s) {
+static int block_fwd(PtcgModel* m, const BlockP& w, const BlockA& a, int L, const float* keep, const float* xin,
+                     float* xout, hipStream_t s) {
     const PtcgDims& d = m->dm;
-    const int NL = m->N * m->dx.l_seq, D = d.d;
-    const BlockP& w = m->blk[i];
-    const BlockA& a = m->ba[i];
+    const int NL = m->N * L, D = d.d;
     PT_TRY(pt_ln_fwd(xin, D, w.ln1w, w.ln1b, a.ln1, D, a.mu1, a.rs1, NL, D, s));
     PT_TRY(linf(a.ln1, w.qkvw, w.qkvb, a.qkv, NL, D, 3 * D, EPI_BIAS, nullptr, nullptr, s));
-    PT_TRY(pt_attn_fwd(a.qkv, m->keep, a.ctx, a.lse, m->N, m->dx.l_seq, d.heads, m->dx.dh, s));
+    PT_TRY(pt_attn_fwd(a.qkv, keep, a.ctx, a.lse, m->N, L, d.heads, m->dx.dh, s));
     PT_TRY(linf(a.ctx, w.projw, w.projb, a.xmid, NL, D, D, EPI_BIAS_RESID, xin, nullptr, s));
     PT_TRY(pt_ln_fwd(a.xmid, D, w.ln2w, w.ln2b, a.ln2, D, a.mu2, a.rs2, NL, D, s));
     PT_TRY(linf(a.ln2, w.f1w, w.f1b, a.ffp, NL, D, d.ffn, EPI_BIAS_GELU, nullptr, a.ffa, s));
     PT_TRY(linf(a.ffa, w.f2w, w.f2b, xout, NL, d.ffn, D, EPI_BIAS_RESID, a.xmid, nullptr, s));
+    return PTCG_OK;
+}
+
+// AttackVec, SkillVec, CardVec rebuilt from the static tables (tables_fwd,
+// ptcg_model2.cu:422-452)
+static int tables_fwd(PtcgModel* m, hipStream_t s) {
+    const PtcgDims& d = m->dm;
+    const DimsX& x = m->dx;
+    const int NC = d.n_cards, NA = d.n_attacks, NS = d.n_skills, DA = d.d_a, DC = d.d_c;
+    const int pa = PT_ID_C + PT_CARD_STATIC + PT_CARD_TEXT;   // first pool column of card_in
+    PT_TRY(pt_copy_cols(m->att_in, x.att_in, m->aid_emb, PT_ID_A, NA, PT_ID_A, s));
+    PT_TRY(lin(m->att_in, x.att_in, m->am_w, m->am_b, m->att_lin, DA, NA, x.att_in, DA, EPI_BIAS_GELU, nullptr, 0,
+               m->att_tab, DA, s));
+    PT_TRY(pt_copy_cols(m->sk_in, x.sk_in, m->sid_emb, PT_ID_A, NS, PT_ID_A, s));
+    PT_TRY(lin(m->sk_in, x.sk_in, m->sm_w, m->sm_b, m->sk_lin, DC, NS, x.sk_in, DC, EPI_BIAS_GELU, nullptr, 0,
+               m->sk_tab, DC, s));
+    PT_TRY(pt_copy_cols(m->card_in, x.card_in, m->cid_emb, PT_ID_C, NC, PT_ID_C, s));
+    PT_TRY(pt_pool_fwd(m->att_tab, DA, m->card_attacks, PT_K_ATT, NC, m->card_in, x.card_in, pa, pa + DA,
+                       m->a_amax, s));
+    PT_TRY(pt_pool_fwd(m->sk_tab, DC, m->card_skills, PT_K_SK, NC, m->card_in, x.card_in, pa + 2 * DA,
+                       pa + 2 * DA + DC, m->s_amax, s));
+    PT_TRY(pt_ln_fwd(m->card_in, x.card_in, m->cln_w, m->cln_b, m->card_ln, x.card_in, m->c_mu, m->c_rs, NC,
+                     x.card_in, s));
+    PT_TRY(lin(m->card_ln, x.card_in, m->c1_w, m->c1_b, m->card_h1, PT_CARD_H, NC, x.card_in, PT_CARD_H,
+               EPI_BIAS_GELU, nullptr, 0, m->card_g1, PT_CARD_H, s));
+    PT_TRY(linf(m->card_g1, m->c3_w, m->c3_b, m->card_vec, NC, PT_CARD_H, DC, EPI_BIAS, nullptr, nullptr, s));
     return PTCG_OK;
 }
 
@@ -294,6 +479,7 @@ extern "C" int ptcg_model_forward(PtcgModel* m, const float* obs, const int32_t*
     PT_REQUIRE(m->mem, "model_forward: activations not registered (call ptcg_model_reg_train)");
     PT_REQUIRE(n == m->N, "model_forward: need exactly %d rows (activations are sized at "
                "registration, bindings.cu:227-233), got %d", m->N, n);
+    PT_REQUIRE(m->dm.tables == 0 || m->tmem, "model_forward: static tables not uploaded (ptcg_model_set_static)");
     hipStream_t s = (hipStream_t)stream;
     const PtcgDims& d = m->dm;
     const DimsX& x = m->dx;
@@ -302,6 +488,7 @@ extern "C" int ptcg_model_forward(PtcgModel* m, const float* obs, const int32_t*
     m->idx = row_idx;
     GatherCtx c{obs, row_idx, (long)m->off.size, N, d, x, m->off};
 
+    if (d.tables == 1) PT_TRY(tables_fwd(m, s));
     PT_TRY(pt_tok_cat_fwd(c, m->card, m->zemb, m->oemb, m->tok_cat, s));
     PT_TRY(linf(m->tok_cat, m->tp_w, m->tp_b, m->tokp, N * Lt, x.tok_in, D, EPI_BIAS, nullptr, nullptr, s));
     PT_TRY(pt_glob_in(c, m->glob_in, s));
@@ -313,7 +500,8 @@ extern "C" int ptcg_model_forward(PtcgModel* m, const float* obs, const int32_t*
                nullptr, 0, nullptr, 0, s));
     PT_TRY(lin(m->gd, x.bcast_in, m->bc_w, m->bc_b, m->bc, D, N, x.bcast_in, D, EPI_BIAS, nullptr, 0, nullptr, 0, s));
     PT_TRY(pt_x0_fwd(c, m->tokp, m->bc, m->readout, m->x[0], m->keep, s));
-    for (int i = 0; i < d.layers; ++i) PT_TRY(block_fwd(m, i, m->x[i], m->x[i + 1], s));
+    for (int i = 0; i < d.layers; ++i)
+        PT_TRY(block_fwd(m, m->blk[i], m->ba[i], x.l_seq, m->keep, m->x[i], m->x[i + 1], s));
     const int NL = N * x.l_seq;
     PT_TRY(pt_ln_fwd(m->x[d.layers], D, m->lnf_w, m->lnf_b, m->h, D, m->lnf_mu, m->lnf_rs, NL, D, s));
 
@@ -331,21 +519,36 @@ extern "C" int ptcg_model_forward(PtcgModel* m, const float* obs, const int32_t*
     PT_TRY(pt_sc_in_fwd(c, m->h, m->gd, m->sc_in, s));
     PT_TRY(linf(m->sc_in, m->s1_w, m->s1_b, m->s1, NJ, x.score_in, PT_SC_H, EPI_BIAS_GELU, nullptr, m->s1a, s));
     PT_TRY(pt_head_dot(m->s1a, NJ, PT_SC_H, m->s2_w, m->s2_b, m->out, NO, NO + 1, 0, s));
-    // blind value head
+    // blind value head: the output value, or (oracle critic) an aux head
     PT_TRY(pt_val_in_fwd(c, m->h, m->gd, m->val_in, s));
     PT_TRY(linf(m->val_in, m->v1_w, m->v1_b, m->v1, N, x.val_in, PT_VAL_H, EPI_BIAS_GELU, nullptr, m->v1a, s));
-    PT_TRY(pt_head_dot(m->v1a, N, PT_VAL_H, m->v2_w, m->v2_b, m->out, 1, NO + 1, NO, s));
+    if (d.critic == 0) {
+        PT_TRY(pt_head_dot(m->v1a, N, PT_VAL_H, m->v2_w, m->v2_b, m->out, 1, NO + 1, NO, s));
+    } else {
+        PT_TRY(pt_head_dot(m->v1a, N, PT_VAL_H, m->v2_w, m->v2_b, m->bv, 1, 1, 0, s));
+        // belief heads: opp-hand counts from [r | g], prize logit per token
+        PT_TRY(linf(m->val_in, m->ah_w, m->ah_b, m->hand_lin, N, x.val_in, d.n_cards, EPI_BIAS, nullptr, nullptr, s));
+        PT_TRY(pt_head_dot(m->h, NL, D, m->ap_w, m->ap_b, m->prize_all, 1, 1, 0, s));
+        // oracle critic top (ptcg_model3.cu:334-351)
+        const int NK = N * x.n_orc;
+        PT_TRY(pt_otok_in(c, m->card, m->keep, m->otok_in, m->ckeep, s));
+        PT_TRY(linf(m->otok_in, m->op_w, m->op_b, m->otok, NK, x.orc_in, D, EPI_BIAS, nullptr, nullptr, s));
+        PT_TRY(pt_xc_fwd(m->cread, m->h, m->otok, m->xc, N, x.l_seq, x.n_orc, D, s));
+        PT_TRY(block_fwd(m, m->cblk, m->cba, x.l_crit, m->ckeep, m->xc, m->xco, s));
+        PT_TRY(pt_val_in_fwd(c, m->xco, m->gd, m->ov_in, s, x.l_crit));
+        PT_TRY(linf(m->ov_in, m->ov1_w, m->ov1_b, m->ov1, N, x.val_in, PT_VAL_H, EPI_BIAS_GELU, nullptr, m->ov1a, s));
+        PT_TRY(pt_head_dot(m->ov1a, N, PT_VAL_H, m->ov2_w, m->ov2_b, m->out, 1, NO + 1, NO, s));
+    }
     if (out) *out = m->out;
     return PTCG_OK;
 }
 
 // ------------------------------------------------------------ backward
 // dA holds d(x_out) on entry and d(x_in) on exit; dC is scratch for d(x_mid)
-static int block_bwd(PtcgModel* m, int i, const float* xin, float* dA, float* dC, hipStream_t s) {
+static int block_bwd(PtcgModel* m, const BlockP& w, const BlockA& a, int L, const float* keep, const float* xin,
+                     float* dA, float* dC, hipStream_t s) {
     const PtcgDims& d = m->dm;
-    const int NL = m->N * m->dx.l_seq, D = d.d;
-    const BlockP& w = m->blk[i];
-    const BlockA& a = m->ba[i];
+    const int NL = m->N * L, D = d.d;
     PT_TRY(ldw_(m, dA, D, a.ffa, d.ffn, m->G(w.f2w), m->G(w.f2b), NL, d.ffn, D, s));
     PT_TRY(ldx_(dA, D, w.f2w, m->dffn, d.ffn, NL, d.ffn, D, EPI_GELU_BWD, a.ffp, d.ffn, s));
     PT_TRY(ldw_(m, m->dffn, d.ffn, a.ln2, D, m->G(w.f1w), m->G(w.f1b), NL, D, d.ffn, s));
@@ -354,12 +557,83 @@ static int block_bwd(PtcgModel* m, int i, const float* xin, float* dA, float* dC
                      m->G(w.ln2b), NL, D, m->ws, m->ws_floats, s));
     PT_TRY(ldw_(m, dC, D, a.ctx, D, m->G(w.projw), m->G(w.projb), NL, D, D, s));
     PT_TRY(ldx_(dC, D, w.projw, m->dctx, D, NL, D, D, EPI_STORE, nullptr, 0, s));
-    PT_TRY(pt_attn_bwd(a.qkv, m->keep, a.ctx, a.lse, m->dctx, m->dqkv, m->N, m->dx.l_seq, d.heads,
-                       m->dx.dh, s));
+    PT_TRY(pt_attn_bwd(a.qkv, keep, a.ctx, a.lse, m->dctx, m->dqkv, m->N, L, d.heads, m->dx.dh, s));
     PT_TRY(ldw_(m, m->dqkv, 3 * D, a.ln1, D, m->G(w.qkvw), m->G(w.qkvb), NL, D, 3 * D, s));
     PT_TRY(ldx_(m->dqkv, 3 * D, w.qkvw, m->dln, D, NL, D, 3 * D, EPI_STORE, nullptr, 0, s));
     PT_TRY(pt_ln_bwd(m->dln, D, xin, D, w.ln1w, a.mu1, a.rs1, dC, D, dA, D, m->G(w.ln1w),
                      m->G(w.ln1b), NL, D, m->ws, m->ws_floats, s));
+    return PTCG_OK;
+}
+
+// the static-table chain from d CardVec / d AttackVec down to the id
+// embeddings (tables_bwd, ptcg_model2.cu:454-485)
+static int tables_bwd(PtcgModel* m, hipStream_t s) {
+    const PtcgDims& d = m->dm;
+    const DimsX& x = m->dx;
+    const int NC = d.n_cards, NA = d.n_attacks, NS = d.n_skills, DA = d.d_a, DC = d.d_c;
+    const int pa = PT_ID_C + PT_CARD_STATIC + PT_CARD_TEXT;
+    PT_TRY(ldw_(m, m->d_card_vec, DC, m->card_g1, PT_CARD_H, m->G(m->c3_w), m->G(m->c3_b), NC, PT_CARD_H, DC, s));
+    PT_TRY(ldx_(m->d_card_vec, DC, m->c3_w, m->d_card_h, PT_CARD_H, NC, PT_CARD_H, DC, EPI_GELU_BWD, m->card_h1,
+                PT_CARD_H, s));
+    PT_TRY(ldw_(m, m->d_card_h, PT_CARD_H, m->card_ln, x.card_in, m->G(m->c1_w), m->G(m->c1_b), NC, x.card_in,
+                PT_CARD_H, s));
+    PT_TRY(ldx_(m->d_card_h, PT_CARD_H, m->c1_w, m->d_card_ln, x.card_in, NC, x.card_in, PT_CARD_H, EPI_STORE,
+                nullptr, 0, s));
+    PT_TRY(pt_ln_bwd(m->d_card_ln, x.card_in, m->card_in, x.card_in, m->cln_w, m->c_mu, m->c_rs, nullptr, 0,
+                     m->d_card_in, x.card_in, m->G(m->cln_w), m->G(m->cln_b), NC, x.card_in, m->ws, m->ws_floats, s));
+    PT_TRY(pt_copy_cols(m->G(m->cid_emb), PT_ID_C, m->d_card_in, x.card_in, NC, PT_ID_C, s));
+    PT_TRY(pt_pool_bwd(m->d_card_in, x.card_in, pa, pa + DA, m->a_amax, m->card_attacks, PT_K_ATT, NC, DA,
+                       m->d_att_tab, s));
+    PT_TRY(pt_pool_bwd(m->d_card_in, x.card_in, pa + 2 * DA, pa + 2 * DA + DC, m->s_amax, m->card_skills, PT_K_SK,
+                       NC, DC, m->d_sk_tab, s));
+    PT_TRY(pt_gelu_bwd(m->d_att_tab, m->att_lin, m->d_att_lin, (long)NA * DA, s));
+    PT_TRY(ldw_(m, m->d_att_lin, DA, m->att_in, x.att_in, m->G(m->am_w), m->G(m->am_b), NA, x.att_in, DA, s));
+    PT_TRY(ldxw_(m->d_att_lin, DA, m->am_w, x.att_in, m->G(m->aid_emb), PT_ID_A, NA, PT_ID_A, DA, EPI_STORE,
+                 nullptr, 0, s));
+    PT_TRY(pt_gelu_bwd(m->d_sk_tab, m->sk_lin, m->d_sk_lin, (long)NS * DC, s));
+    PT_TRY(ldw_(m, m->d_sk_lin, DC, m->sk_in, x.sk_in, m->G(m->sm_w), m->G(m->sm_b), NS, x.sk_in, DC, s));
+    PT_TRY(ldxw_(m->d_sk_lin, DC, m->sm_w, x.sk_in, m->G(m->sid_emb), PT_ID_A, NS, PT_ID_A, DC, EPI_STORE,
+                 nullptr, 0, s));
+    return PTCG_OK;
+}
+
+// oracle critic top + blind value + belief heads: the PPO value gradient
+// (grad[:, NO]) enters at the oracle value; the aux losses at the heads
+// (ptcg_model4.cu:26-101).  Adds into dxa (d h), dgd and dcard.
+static int critic_bwd(PtcgModel* m, const GatherCtx& c, const float* grad, hipStream_t s) {
+    const PtcgDims& d = m->dm;
+    const DimsX& x = m->dx;
+    const int N = m->N, NO = d.n_opt, D = d.d, NL = N * x.l_seq, NK = N * x.n_orc;
+    PT_TRY(pt_aux_grads(c, m->hand_lin, m->prize_all, m->bv, m->ret, m->aux_cnt, m->d_hand, m->d_prize,
+                        m->d_blind, s));
+    // blind value (aux): d_blind -> value_mlp -> d [r | g]
+    PT_TRY(pt_head_dot_dw(m->d_blind, 1, 1, 0, m->v1a, N, PT_VAL_H, m->G(m->v2_w), m->G(m->v2_b), m->ws,
+                          m->ws_floats, s));
+    PT_TRY(pt_head_dot_bwd(m->d_blind, 1, 1, 0, m->v2_w, m->v1, m->dv1, N, PT_VAL_H, s));
+    PT_TRY(ldw_(m, m->dv1, PT_VAL_H, m->val_in, x.val_in, m->G(m->v1_w), m->G(m->v1_b), N, x.val_in, PT_VAL_H, s));
+    PT_TRY(ldx_(m->dv1, PT_VAL_H, m->v1_w, m->dvin, x.val_in, N, x.val_in, PT_VAL_H, EPI_STORE, nullptr, 0, s));
+    // opp-hand counts (shares the [r | g] input)
+    PT_TRY(ldw_(m, m->d_hand, d.n_cards, m->val_in, x.val_in, m->G(m->ah_w), m->G(m->ah_b), N, x.val_in,
+                d.n_cards, s));
+    PT_TRY(ldx_(m->d_hand, d.n_cards, m->ah_w, m->dvin, x.val_in, N, x.val_in, d.n_cards, EPI_ACCUM, nullptr, 0, s));
+    PT_TRY(pt_val_in_bwd(c, m->dvin, m->dxa, m->dgd, s));
+    // prize head over the trunk output rows
+    PT_TRY(pt_head_dot_dw(m->d_prize, 1, 1, 0, m->h, NL, D, m->G(m->ap_w), m->G(m->ap_b), m->ws, m->ws_floats, s));
+    PT_TRY(pt_rank1_add(m->d_prize, m->ap_w, m->dxa, NL, D, s));
+    // oracle value -> critic block -> h / oracle tokens / critic readout
+    PT_TRY(pt_head_dot_dw(grad, 1, NO + 1, NO, m->ov1a, N, PT_VAL_H, m->G(m->ov2_w), m->G(m->ov2_b), m->ws,
+                          m->ws_floats, s));
+    PT_TRY(pt_head_dot_bwd(grad, 1, NO + 1, NO, m->ov2_w, m->ov1, m->dov1, N, PT_VAL_H, s));
+    PT_TRY(ldw_(m, m->dov1, PT_VAL_H, m->ov_in, x.val_in, m->G(m->ov1_w), m->G(m->ov1_b), N, x.val_in, PT_VAL_H, s));
+    PT_TRY(ldx_(m->dov1, PT_VAL_H, m->ov1_w, m->dovin, x.val_in, N, x.val_in, PT_VAL_H, EPI_STORE, nullptr, 0, s));
+    PT_TRY(pt_fill_zero(m->dxc, (long)N * x.l_crit * D, s));
+    PT_TRY(pt_val_in_bwd(c, m->dovin, m->dxc, m->dgd, s, x.l_crit));
+    PT_TRY(block_bwd(m, m->cblk, m->cba, x.l_crit, m->ckeep, m->xc, m->dxc, m->dxc2, s));
+    PT_TRY(pt_colsum(m->dxc, (long)x.l_crit * D, N, D, m->G(m->cread), m->ws, m->ws_floats, s));
+    PT_TRY(pt_xc_bwd(m->dxc, m->dxa, m->dotok, N, x.l_seq, x.n_orc, D, s));
+    PT_TRY(ldw_(m, m->dotok, D, m->otok_in, x.orc_in, m->G(m->op_w), m->G(m->op_b), NK, x.orc_in, D, s));
+    PT_TRY(ldx_(m->dotok, D, m->op_w, m->dotok_in, x.orc_in, NK, x.orc_in, D, EPI_STORE, nullptr, 0, s));
+    PT_TRY(pt_otok_bwd(c, m->dotok_in, m->dcard, s));
     return PTCG_OK;
 }
 
@@ -375,14 +649,23 @@ extern "C" int ptcg_model_backward(PtcgModel* m, const float* grad, void* stream
     PT_TRY(pt_fill_zero(m->Gr, m->arena, s));
     PT_TRY(pt_fill_zero(m->dxa, (long)NL * D, s));
     PT_TRY(pt_fill_zero(m->dgd, (long)N * x.bcast_in, s));
+    if (d.tables == 1) {
+        PT_TRY(pt_fill_zero(m->d_card_vec, (long)d.n_cards * d.d_c, s));
+        PT_TRY(pt_fill_zero(m->d_att_tab, (long)d.n_attacks * d.d_a, s));
+        PT_TRY(pt_fill_zero(m->d_sk_tab, (long)d.n_skills * d.d_c, s));
+    }
 
-    // blind value head: grad[:, NO]
-    PT_TRY(pt_head_dot_dw(grad, 1, NO + 1, NO, m->v1a, N, PT_VAL_H, m->G(m->v2_w), m->G(m->v2_b), m->ws,
-                          m->ws_floats, s));
-    PT_TRY(pt_head_dot_bwd(grad, 1, NO + 1, NO, m->v2_w, m->v1, m->dv1, N, PT_VAL_H, s));
-    PT_TRY(ldw_(m, m->dv1, PT_VAL_H, m->val_in, x.val_in, m->G(m->v1_w), m->G(m->v1_b), N, x.val_in, PT_VAL_H, s));
-    PT_TRY(ldx_(m->dv1, PT_VAL_H, m->v1_w, m->dvin, x.val_in, N, x.val_in, PT_VAL_H, EPI_STORE, nullptr, 0, s));
-    PT_TRY(pt_val_in_bwd(c, m->dvin, m->dxa, m->dgd, s));
+    if (d.critic == 1) {
+        PT_TRY(critic_bwd(m, c, grad, s));
+    } else {
+        // blind value head: grad[:, NO]
+        PT_TRY(pt_head_dot_dw(grad, 1, NO + 1, NO, m->v1a, N, PT_VAL_H, m->G(m->v2_w), m->G(m->v2_b), m->ws,
+                              m->ws_floats, s));
+        PT_TRY(pt_head_dot_bwd(grad, 1, NO + 1, NO, m->v2_w, m->v1, m->dv1, N, PT_VAL_H, s));
+        PT_TRY(ldw_(m, m->dv1, PT_VAL_H, m->val_in, x.val_in, m->G(m->v1_w), m->G(m->v1_b), N, x.val_in, PT_VAL_H, s));
+        PT_TRY(ldx_(m->dv1, PT_VAL_H, m->v1_w, m->dvin, x.val_in, N, x.val_in, PT_VAL_H, EPI_STORE, nullptr, 0, s));
+        PT_TRY(pt_val_in_bwd(c, m->dvin, m->dxa, m->dgd, s));
+    }
 
     // option scores: grad[:, :NO]
     PT_TRY(pt_head_dot_dw(grad, NO, NO + 1, 0, m->s1a, NJ, PT_SC_H, m->G(m->s2_w), m->G(m->s2_b), m->ws,
@@ -401,19 +684,20 @@ extern "C" int ptcg_model_backward(PtcgModel* m, const float* grad, void* stream
     PT_TRY(ldx_(m->dqin + oc0, x.q_in, m->oc_w, m->docard, d.d_c, NJ, d.d_c, PT_OPT_E, EPI_STORE, nullptr, 0, s));
     PT_TRY(ldw_(m, m->dqin + oa0, x.q_in, m->oatt, d.d_a, m->G(m->oa_w), m->G(m->oa_b), NJ, d.d_a, PT_OPT_E, s));
     PT_TRY(ldx_(m->dqin + oa0, x.q_in, m->oa_w, m->doatt, d.d_a, NJ, d.d_a, PT_OPT_E, EPI_STORE, nullptr, 0, s));
-    PT_TRY(pt_opt_gather_bwd(c, m->docard, m->doatt, m->G(m->card), m->G(m->att), s));
+    PT_TRY(pt_opt_gather_bwd(c, m->docard, m->doatt, m->dcard, m->datt, s));
 
     // final LayerNorm, then the trunk in reverse (d_x in dxb, scratch dxa)
     PT_TRY(pt_ln_bwd(m->dxa, D, m->x[d.layers], D, m->lnf_w, m->lnf_mu, m->lnf_rs, nullptr, 0, m->dxb, D,
                      m->G(m->lnf_w), m->G(m->lnf_b), NL, D, m->ws, m->ws_floats, s));
-    for (int i = d.layers - 1; i >= 0; --i) PT_TRY(block_bwd(m, i, m->x[i], m->dxb, m->dxa, s));
+    for (int i = d.layers - 1; i >= 0; --i)
+        PT_TRY(block_bwd(m, m->blk[i], m->ba[i], x.l_seq, m->keep, m->x[i], m->dxb, m->dxa, s));
 
     // trunk input: readout / token projection / broadcast
     PT_TRY(pt_x0_bwd(c, m->dxb, m->dtokp, m->dbc, s));
     PT_TRY(pt_colsum(m->dxb, (long)x.l_seq * D, N, D, m->G(m->readout), m->ws, m->ws_floats, s));
     PT_TRY(ldw_(m, m->dtokp, D, m->tok_cat, x.tok_in, m->G(m->tp_w), m->G(m->tp_b), N * Lt, x.tok_in, D, s));
     PT_TRY(ldx_(m->dtokp, D, m->tp_w, m->dtokcat, x.tok_in, N * Lt, x.tok_in, D, EPI_STORE, nullptr, 0, s));
-    PT_TRY(pt_tok_cat_bwd(c, m->dtokcat, m->G(m->card), m->G(m->zemb), m->G(m->oemb), s));
+    PT_TRY(pt_tok_cat_bwd(c, m->dtokcat, m->dcard, m->G(m->zemb), m->G(m->oemb), s));
     PT_TRY(ldw_(m, m->dbc, D, m->gd, x.bcast_in, m->G(m->bc_w), m->G(m->bc_b), N, x.bcast_in, D, s));
     PT_TRY(ldx_(m->dbc, D, m->bc_w, m->dgd, x.bcast_in, N, x.bcast_in, D, EPI_ACCUM, nullptr, 0, s));
     // decision MLP (d_dvec = dgd[:, G:])
@@ -421,10 +705,11 @@ extern "C" int ptcg_model_backward(PtcgModel* m, const float* grad, void* stream
     PT_TRY(ldx_(m->dgd + G, x.bcast_in, m->d2_w, m->dd1, PT_DEC_H, N, PT_DEC_H, PT_DEC_H, EPI_GELU_BWD, m->d1, PT_DEC_H, s));
     PT_TRY(ldw_(m, m->dd1, PT_DEC_H, m->dec_in, x.dec_in, m->G(m->d1_w), m->G(m->d1_b), N, x.dec_in, PT_DEC_H, s));
     PT_TRY(ldx_(m->dd1, PT_DEC_H, m->d1_w, m->ddec, x.dec_in, N, x.dec_in, PT_DEC_H, EPI_STORE, nullptr, 0, s));
-    PT_TRY(pt_dec_in_bwd(c, m->ddec, m->G(m->card), m->G(m->att), m->G(m->semb), m->G(m->cemb), s));
+    PT_TRY(pt_dec_in_bwd(c, m->ddec, m->dcard, m->datt, m->G(m->semb), m->G(m->cemb), s));
     // global MLP (d_g = dgd[:, :G])
     PT_TRY(ldw_(m, m->dgd, x.bcast_in, m->g1a, G, m->G(m->g2_w), m->G(m->g2_b), N, G, G, s));
     PT_TRY(ldx_(m->dgd, x.bcast_in, m->g2_w, m->dg1, G, N, G, G, EPI_GELU_BWD, m->g1, G, s));
     PT_TRY(ldw_(m, m->dg1, G, m->glob_in, d.global_f, m->G(m->g1_w), m->G(m->g1_b), N, d.global_f, G, s));
+    if (d.tables == 1) PT_TRY(tables_bwd(m, s));
     return PTCG_OK;
 }

@@ -43,6 +43,9 @@ _SIGS = {
     "ptcg_model_forward": (ctypes.c_int, [c_void_p, c_void_p, c_void_p, ctypes.c_int,
                                           ctypes.POINTER(c_void_p), c_void_p]),
     "ptcg_model_backward": (ctypes.c_int, [c_void_p, c_void_p, c_void_p]),
+    "ptcg_model_set_static": (ctypes.c_int, [c_void_p] * 8),
+    "ptcg_model_bind_returns": (ctypes.c_int, [c_void_p, c_void_p]),
+    "ptcg_trainer_set_static": (ctypes.c_int, [c_void_p] * 8),
     "ptcg_model_free": (None, [c_void_p]),
     "ptcg_ppo_loss_fwd_bwd": (ctypes.c_int, [
         c_void_p, ctypes.c_int, ctypes.c_int, c_void_p, ctypes.c_int64, c_void_p,

@@ -22,7 +22,6 @@ CARD_H = 256     # card_mlp hidden (static tables)
 ATT_IN = 127     # 48 id + 15 static + 64 text  (ptcg_model.cu:42)
 SK_IN = 112      # 48 id + 64 text              (ptcg_model.cu:43)
 CARD_STATIC, CARD_TEXT = 58, 128   # static feature widths (ptcg/rl/cards.py)
-ORC_IN = 134     # d_c + 6                      (ptcg_model.cu:56)
 
 
 def _block(prefix, d, ffn):
@@ -102,7 +101,7 @@ def param_order(dims):
     ]
     if dims.critic == CRITIC_ORACLE:
         order += [
-            ("oracle_proj.weight", (d, ORC_IN)), ("oracle_proj.bias", (d,)),
+            ("oracle_proj.weight", (d, dc + 6)), ("oracle_proj.bias", (d,)),
             ("critic_readout", (d,)),
         ]
         order += _block("critic_blocks.0", d, dims.ffn)

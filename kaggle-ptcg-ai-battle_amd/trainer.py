@@ -93,6 +93,26 @@ class PuffeRL:
         check(lib().ptcg_trainer_get_moments(self._h, fptr(m), fptr(v)))
         return m, v
 
+    def set_static(self, st):
+        """Upload the static card / attack / skill tables of a static-table
+        model (pt_static_upload, ptcg_model2.cu:383-419); ``st`` holds the
+        arrays of :func:`synth.make_static`'s layout."""
+        f = {k: np.ascontiguousarray(st[k], dtype=np.float32)
+             for k in ("card_static", "att_static", "card_text", "att_text", "skill_text")}
+        i = {k: np.ascontiguousarray(st[k], dtype=np.int32) for k in ("card_attacks", "card_skills")}
+        dm = self.dims
+        want = dict(card_static=(dm.n_cards, 58), att_static=(dm.n_attacks, 15), card_text=(dm.n_cards, 128),
+                    att_text=(dm.n_attacks, 64), skill_text=(dm.n_skills, 64), card_attacks=(dm.n_cards, 4),
+                    card_skills=(dm.n_cards, 2))
+        for k, shp in want.items():
+            a = f.get(k, i.get(k))
+            if a.shape != shp:
+                raise RuntimeError(f"static table {k}: shape {a.shape}, expected {shp}")
+        check(lib().ptcg_trainer_set_static(self._h, *[fptr(f[k]) for k in ("card_static", "att_static",
+                                                                            "card_text", "att_text", "skill_text")],
+                                            i["card_attacks"].ctypes.data, i["card_skills"].ctypes.data))
+        self._static = (f, i)   # keep the host copies alive for the call's duration
+
     def step_count(self):
         v = ctypes.c_int32()
         check(lib().ptcg_trainer_step_count(self._h, ctypes.byref(v)))
@@ -146,11 +166,14 @@ class PuffeRL:
 
 def create_pufferl(args):
     """args: {"dims": PtcgDims | dict, "train": {...}, "seed": int,
-    "init_weights": packed blob | None}.  Unknown dims keys raise."""
+    "init_weights": packed blob | None, "static": static tables (static-table
+    models)}.  Unknown dims keys raise."""
     dm = args.get("dims", dims_mod.CORE)
     if isinstance(dm, dict):
         dm = dims_mod.PtcgDims(**dm)
     pl = PuffeRL(dm, args.get("train", {}), args.get("seed", 0))
+    if args.get("static") is not None:
+        pl.set_static(args["static"])
     init = args.get("init_weights")
     if init is None:
         from .params import init_blob

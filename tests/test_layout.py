@@ -21,7 +21,8 @@ FROZEN_OFFSETS = {   # docs/model.md "The observation row" table
     "oracle": 10808,
 }
 
-CONFIGS = [dims.FROZEN, dims.CORE, dims.tiny(), dims.tiny(l_tok=7, n_opt=5, heads=4)]
+CONFIGS = [dims.FROZEN, dims.CORE, dims.tiny(), dims.tiny(l_tok=7, n_opt=5, heads=4), dims.tiny_frozen(),
+           dims.tiny_frozen(d_c=8, d_a=4)]
 
 
 def test_frozen_obs_offsets_match_reference_table():

@@ -12,6 +12,12 @@ Prints one JSON line (see the keys below), including the GEMM kernel's
 roofline (useful flops over measured kernel time, HIP events on the launch
 stream) and the host-CPU baseline (the oracle: PyTorch CPU restatement of
 the same step, timed on a bounded sample in the same run).
+
+Secondary workloads (not the headline line): ``--workload rollout`` times
+the rollout step — inference forward of 8192 rows plus one sampled action
+per row; ``--workload frozen`` times the training step of the reference's
+own model variant (frozen layout: 160 tokens, d256/H8/FFN512, static-table
+card vectors, oracle critic over 218 positions, aux losses).
 """
 import argparse
 import ctypes
@@ -89,6 +95,8 @@ def main():
     ap.add_argument("--rollout", type=int, default=16384)
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--workload", choices=("train", "rollout", "frozen"), default="train")
+    ap.add_argument("--rollout-rows", type=int, default=8192)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
@@ -100,11 +108,16 @@ def main():
     __graft_entry__.load_package()
     from ptcg_amd import dims, synth, trainer, native
 
-    dm = dims.CORE
+    if args.workload == "rollout":
+        return bench_rollout(args)
+    dm = dims.FROZEN if args.workload == "frozen" else dims.CORE
     B, R = args.minibatch, args.rollout
+    if args.workload == "frozen":
+        R = min(R, 4096)
     obs = synth.make_obs(dm, R, seed=1)
     inp = synth.make_ppo_inputs(dm, obs, seed=2)
-    pl = trainer.create_pufferl({"dims": dm, "train": dict(TRAIN, minibatch_size=B), "seed": 0})
+    static = synth.make_static(dm, 4) if dm.tables == 1 else None
+    pl = trainer.create_pufferl({"dims": dm, "train": dict(TRAIN, minibatch_size=B), "seed": 0, "static": static})
     trainer.set_rollout(pl, obs, **inp)
     n_lists = args.warmup + args.steps
     lists = synth.minibatch_indices(R, B, n_lists, seed=3)
@@ -129,6 +142,24 @@ def main():
 
     K = args.steps
     sec = t1 - t0
+    if args.workload == "frozen":
+        line = {
+            "metric": "PPO minibatch step obs/sec (fwd+bwd+Adam), reference model variant @B=512",
+            "value": round(B * K / sec, 2), "unit": "obs/s", "n_gpus": 1, "steps": K, "warmup": args.warmup,
+            "ms_per_step": round(sec * 1e3 / K, 4), "higher_is_better": True, "scaling": "weak",
+            "vs_baseline": None, "dtype": "fp32", "data": "synthetic",
+            "config": {"workload": "PPO minibatch step of the reference model variant: 160 tokens + READOUT, "
+                                   "56 token features, d256/H8/FFN512/4 layers, static-table card vectors "
+                                   "(1284 cards, 1573 attacks, 448 skills), oracle critic over 218 positions, "
+                                   "blind-value / hand / prize aux losses",
+                       "minibatch": B, "rollout_rows": R, "seq_len": dm.l_tok + 1, "parallelism": "single GPU"},
+            "gemm": {"launches_per_step": launches.value / K, "gemm_ms_per_step": round(ms.value / K, 4),
+                     "executed_tflops": round(exec_flops.value / (ms.value / 1e3) / 1e12, 3)},
+            "losses": {k: round(v, 5) for k, v in losses.items() if isinstance(v, float)},
+        }
+        pl.close()
+        print(json.dumps(line), flush=True)
+        return
     useful = 0.0
     lv = []
     for ix in lists[args.warmup:]:
@@ -162,6 +193,52 @@ def main():
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(dm, obs, inp, B, args.cpu_seconds)
         line["gpu_over_cpu"] = round(line["value"] / line["cpu_baseline"]["value"], 1)
+    pl.close()
+    print(json.dumps(line), flush=True)
+
+
+def bench_rollout(args):
+    """Rollout step: inference forward of n rows (one block's activations
+    reused across layers) + one sampled action per row (counter RNG)."""
+    import torch
+    from ptcg_amd import dims, synth, trainer, native
+    dm = dims.CORE
+    n = args.rollout_rows
+    obs = synth.make_obs(dm, n, seed=1)
+    pl = trainer.create_pufferl({"dims": dm, "train": dict(TRAIN, minibatch_size=8), "seed": 0})
+    d_obs = pl.to_device(obs)
+    for i in range(args.warmup):
+        pl.rollout_step(d_obs, n, seed=0, step=i)
+    torch.cuda.synchronize()
+    L = native.lib()
+    native.check(L.ptcg_profile_begin(4096))
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        acts, lps, vals = pl.rollout_step(d_obs, n, seed=0, step=args.warmup + i)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    ms, launches, exec_flops = ctypes.c_double(), ctypes.c_int(), ctypes.c_double()
+    native.check(L.ptcg_profile_end(ctypes.byref(ms), ctypes.byref(launches), ctypes.byref(exec_flops)))
+    if not torch.isfinite(lps).all():
+        raise RuntimeError("non-finite log-probabilities in the rollout benchmark")
+    K = args.steps
+    sec = t1 - t0
+    useful, lv = useful_gemm_flops(dm, obs)
+    useful_fwd = useful / 3.0
+    gemm_s = ms.value / 1e3
+    achieved = useful_fwd * K / gemm_s / 1e12
+    line = {
+        "metric": "rollout forward + action sampling obs/sec @8192 rows", "value": round(n * K / sec, 2),
+        "unit": "obs/s", "n_gpus": 1, "steps": K, "warmup": args.warmup, "ms_per_step": round(sec * 1e3 / K, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp32", "data": "synthetic",
+        "config": {"workload": f"inference forward of {n} obs rows (CORE model: 96 tokens + READOUT, d256/H4/"
+                               "FFN1024/4 layers) + one inverse-CDF action sample per row from Philox4x32-10",
+                   "rows": n, "seq_len": dm.l_tok + 1, "parallelism": "single GPU"},
+        "roofline": dict(bound="mfma", kernel="gemm_f32_kernel (forward GEMMs)", achieved=round(achieved, 3),
+                         peak=FP32_MFMA_PEAK_TFLOPS, unit="TFLOP/s", frac=round(achieved / FP32_MFMA_PEAK_TFLOPS, 4),
+                         traffic=None, gemm_ms_per_step=round(ms.value / K, 4),
+                         launches_per_step=launches.value / K, mean_valid_seq=round(lv, 2)),
+    }
     pl.close()
     print(json.dumps(line), flush=True)
 

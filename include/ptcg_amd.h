@@ -76,6 +76,11 @@ int ptcg_model_create(const PtcgDims* dims, PtcgModel** out);
 int ptcg_model_bind(PtcgModel* m, float* params_arena, float* grads_arena);
 /* reg_train (ptcg_model4.cu:260-263): size activations for exactly n rows. */
 int ptcg_model_reg_train(PtcgModel* m, int n);
+/* reg_rollout (ptcg_model4.cu:265-267): inference activations for exactly
+ * n rows — one block's buffers reused by every layer, no backward; the
+ * training-only heads (blind value and belief heads of the oracle-critic
+ * model) are skipped.  ptcg_model_backward then fails.                    */
+int ptcg_model_reg_rollout(PtcgModel* m, int n);
 /* forward (ptcg_model4.cu:269-275): obs rows -> *out (n, n_opt+1) =
  * [raw option scores || value], aliasing an internal buffer.
  * row_idx: optional int32 device array of n row indices into obs (NULL =
@@ -139,6 +144,18 @@ int ptcg_adam_step(float* weights, float* grads, float* m, float* v, int64_t n,
                    const float* gate, int32_t* step, float* norm_out, float* workspace,
                    void* stream);
 
+/* ---- action sampler (sample_logits, pufferlib.cu:584-718) ---------------
+ * One discrete head of A options per row of dec_out (n, A+1) = [scores ||
+ * value]: masked (mask == 0 -> -1e4, rows at mask_stride, gathered through
+ * row_idx when non-NULL) softmax, inverse-CDF draw with
+ * u = Philox4x32-10(counter = (row, step), key = seed) in (0, 1) where the
+ * reference advances a per-row cuRAND state.  Writes actions (option index
+ * as float), logprobs, values (last column; may be NULL) and, when
+ * non-NULL, the uniforms used.                                            */
+int ptcg_sample_actions(const float* dec_out, int n, int A, const float* mask, int64_t mask_stride,
+                        const int32_t* row_idx, uint64_t seed, uint64_t step, float* actions,
+                        float* logprobs, float* values, float* uniforms, void* stream);
+
 /* ---- trainer (create_pufferl / train / debug_forward / weights IO) ----- */
 int ptcg_trainer_create(const PtcgDims* dims, const PtcgHypers* hyp, int minibatch,
                         PtcgTrainer** out);
@@ -157,6 +174,15 @@ int ptcg_trainer_load_state(PtcgTrainer* t, const char* path);
 /* debug_forward (bindings.cu:221-250): host obs (minibatch rows) -> host
  * out (minibatch, n_opt+1); synchronous.                                  */
 int ptcg_trainer_debug_forward(PtcgTrainer* t, const float* obs_host, int n, float* out_host);
+/* Rollout step of the policy (net_callback_wrapper -> policy_forward ->
+ * sample_logits, pufferlib.cu:757-946): forward n obs rows (device, through
+ * row_idx when non-NULL) with inference activations on the trainer's
+ * current weights, then sample one action per row (ptcg_sample_actions,
+ * mask = the rows' opt_mask section).  actions, logprobs, values: device
+ * arrays of n floats.                                                     */
+int ptcg_trainer_rollout(PtcgTrainer* t, const float* obs, const int32_t* row_idx, int n,
+                         uint64_t seed, uint64_t step, float* actions, float* logprobs,
+                         float* values, void* stream);
 /* ptcg_model_set_static on the trainer's model.                          */
 int ptcg_trainer_set_static(PtcgTrainer* t, const float* card_static, const float* att_static,
                             const float* card_text, const float* att_text, const float* skill_text,

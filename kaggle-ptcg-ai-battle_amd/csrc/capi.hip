@@ -275,11 +275,18 @@ struct PtcgTrainer {
     float *P, *Gr, *M, *V;
     float *grad, *ratio, *newvalue, *stats, *guard, *gate, *ppo_part, *adam_ws, *dbg_obs;
     int32_t* step;
+    // rollout policy: a second model on the same weights with inference
+    // activations for `roll_n` rows (reg_rollout), made on first use
+    PtcgModel* roll = nullptr;
+    int roll_n = 0;
+    std::vector<float> st_f[5];
+    std::vector<int32_t> st_i[2];
 };
 
 extern "C" void ptcg_trainer_free(PtcgTrainer* t) {
     if (!t) return;
     if (t->model) ptcg_model_free(t->model);
+    if (t->roll) ptcg_model_free(t->roll);
     if (t->mem) (void)hipFree(t->mem);
     delete t;
 }
@@ -499,8 +506,45 @@ extern "C" int ptcg_trainer_set_static(PtcgTrainer* t, const float* card_static,
                                        const float* card_text, const float* att_text, const float* skill_text,
                                        const int32_t* card_attacks, const int32_t* card_skills) {
     PT_REQUIRE(t, "trainer_set_static: null trainer");
-    return ptcg_model_set_static(t->model, card_static, att_static, card_text, att_text, skill_text,
-                                 card_attacks, card_skills);
+    PT_TRY(ptcg_model_set_static(t->model, card_static, att_static, card_text, att_text, skill_text,
+                                 card_attacks, card_skills));
+    // host copies for the rollout policy's own upload
+    const PtcgDims& d = t->dm;
+    const long NC = d.n_cards, NA = d.n_attacks, NS = d.n_skills;
+    t->st_f[0].assign(card_static, card_static + NC * PT_CARD_STATIC);
+    t->st_f[1].assign(att_static, att_static + NA * PT_ATT_STATIC);
+    t->st_f[2].assign(card_text, card_text + NC * PT_CARD_TEXT);
+    t->st_f[3].assign(att_text, att_text + NA * PT_ATT_TEXT);
+    t->st_f[4].assign(skill_text, skill_text + NS * PT_SKILL_TEXT);
+    t->st_i[0].assign(card_attacks, card_attacks + NC * PT_K_ATT);
+    t->st_i[1].assign(card_skills, card_skills + NC * PT_K_SK);
+    if (t->roll)
+        PT_TRY(ptcg_model_set_static(t->roll, card_static, att_static, card_text, att_text, skill_text,
+                                     card_attacks, card_skills));
+    return PTCG_OK;
+}
+
+extern "C" int ptcg_trainer_rollout(PtcgTrainer* t, const float* obs, const int32_t* row_idx, int n,
+                                    uint64_t seed, uint64_t step, float* actions, float* logprobs,
+                                    float* values, void* stream) {
+    PT_REQUIRE(t && obs && actions && logprobs, "trainer_rollout: null argument");
+    PT_REQUIRE(n >= 1, "trainer_rollout: n=%d", n);
+    if (!t->roll || t->roll_n != n) {
+        if (!t->roll) {
+            PT_TRY(ptcg_model_create(&t->dm, &t->roll));
+            PT_TRY(ptcg_model_bind(t->roll, t->P, t->Gr));
+            if (t->dm.tables == 1 && !t->st_i[0].empty())
+                PT_TRY(ptcg_model_set_static(t->roll, t->st_f[0].data(), t->st_f[1].data(), t->st_f[2].data(),
+                                             t->st_f[3].data(), t->st_f[4].data(), t->st_i[0].data(),
+                                             t->st_i[1].data()));
+        }
+        PT_TRY(ptcg_model_reg_rollout(t->roll, n));
+        t->roll_n = n;
+    }
+    float* out = nullptr;
+    PT_TRY(ptcg_model_forward(t->roll, obs, row_idx, n, &out, stream));
+    return ptcg_sample_actions(out, n, t->dm.n_opt, obs + t->off.opt_mask, t->off.size, row_idx, seed, step, actions,
+                               logprobs, values, nullptr, stream);
 }
 
 extern "C" int ptcg_trainer_step(PtcgTrainer* t, const float* obs, const int32_t* row_idx,

@@ -62,8 +62,10 @@ struct PtcgModel {
     float *att_in, *att_lin, *att_tab, *sk_in, *sk_lin, *sk_tab, *card_in, *c_mu, *c_rs, *card_ln, *card_h1,
         *card_g1, *card_vec;
     float *d_card_vec, *d_att_tab, *d_sk_tab, *d_card_h, *d_card_ln, *d_card_in, *d_att_lin, *d_sk_lin;
-    // activations
+    // activations (train: every layer's kept for the backward; rollout:
+    // one block's worth reused by every layer, no backward buffers)
     int N = 0;
+    bool train = true;
     char* mem = nullptr;
     size_t mem_bytes = 0;
     float *tok_cat, *tokp, *glob_in, *g1, *g1a, *dec_in, *d1, *d1a, *gd, *bc, *keep;
@@ -345,7 +347,7 @@ static size_t carve(PtcgModel* m, char* base) {
     const PtcgDims& d = m->dm;
     const DimsX& x = m->dx;
     const long N = m->N, Lt = d.l_tok, Ls = x.l_seq, NL = N * Ls, NO = d.n_opt, D = d.d;
-    const bool crit = d.critic == 1;
+    const bool crit = d.critic == 1, train = m->train;
     const long NLC = crit ? N * x.l_crit : 0, NLmax = NL > NLC ? NL : NLC, NK = N * x.n_orc;
     Carver c{base};
     m->tok_cat = c.take(N * Lt * x.tok_in);
@@ -357,9 +359,9 @@ static size_t carve(PtcgModel* m, char* base) {
     m->gd = c.take(N * x.bcast_in);
     m->bc = c.take(N * D);
     m->keep = c.take(NL);
-    m->x.resize(d.layers + 1);
+    m->x.resize(train ? d.layers + 1 : 2);
     for (auto& p : m->x) p = c.take(NL * D);
-    m->ba.resize(d.layers);
+    m->ba.resize(train ? d.layers : 1);
     for (auto& a : m->ba) carve_block(c, a, NL, d);
     m->h = c.take(NL * D); m->lnf_mu = c.take(NL); m->lnf_rs = c.take(NL);
     m->ocard = c.take(N * NO * d.d_c); m->oatt = c.take(N * NO * d.d_a);
@@ -377,14 +379,21 @@ static size_t carve(PtcgModel* m, char* base) {
         carve_block(c, m->cba, NLC, d);
         m->ov_in = c.take(N * x.val_in);
         m->ov1 = c.take(N * PT_VAL_H); m->ov1a = c.take(N * PT_VAL_H);
-        m->bv = c.take(N);
-        m->hand_lin = c.take(N * d.n_cards);
-        m->prize_all = c.take(NL);
-        m->d_hand = c.take(N * d.n_cards); m->d_prize = c.take(NL); m->d_blind = c.take(N);
-        m->dxc = c.take(NLC * D); m->dxc2 = c.take(NLC * D);
-        m->dotok = c.take(NK * D); m->dotok_in = c.take(NK * x.orc_in);
-        m->dov1 = c.take(N * PT_VAL_H); m->dovin = c.take(N * x.val_in);
-        m->aux_cnt = reinterpret_cast<int*>(c.take(64));
+        if (train) {
+            m->bv = c.take(N);
+            m->hand_lin = c.take(N * d.n_cards);
+            m->prize_all = c.take(NL);
+            m->d_hand = c.take(N * d.n_cards); m->d_prize = c.take(NL); m->d_blind = c.take(N);
+            m->dxc = c.take(NLC * D); m->dxc2 = c.take(NLC * D);
+            m->dotok = c.take(NK * D); m->dotok_in = c.take(NK * x.orc_in);
+            m->dov1 = c.take(N * PT_VAL_H); m->dovin = c.take(N * x.val_in);
+            m->aux_cnt = reinterpret_cast<int*>(c.take(64));
+        }
+    }
+    if (!train) {   // forward GEMMs and LayerNorms need no workspace
+        m->ws_floats = 0;
+        m->ws = nullptr;
+        return c.off;
     }
     // backward scratch (block scratch sized for the longer of trunk and critic)
     m->dxa = c.take(NL * D); m->dxb = c.take(NL * D);
@@ -407,18 +416,28 @@ static size_t carve(PtcgModel* m, char* base) {
     return c.off;
 }
 
-extern "C" int ptcg_model_reg_train(PtcgModel* m, int n) {
-    PT_REQUIRE(m && n >= 2, "model_reg_train: need n >= 2 rows");
+static int reg(PtcgModel* m, int n, bool train) {
     if (m->mem) {
         PT_HIP(hipFree(m->mem));
         m->mem = nullptr;
     }
     m->N = n;
+    m->train = train;
     size_t bytes = carve(m, nullptr);
     PT_HIP(hipMalloc(&m->mem, bytes));
     m->mem_bytes = bytes;
     carve(m, m->mem);
     return PTCG_OK;
+}
+
+extern "C" int ptcg_model_reg_train(PtcgModel* m, int n) {
+    PT_REQUIRE(m && n >= 2, "model_reg_train: need n >= 2 rows");
+    return reg(m, n, true);
+}
+
+extern "C" int ptcg_model_reg_rollout(PtcgModel* m, int n) {
+    PT_REQUIRE(m && n >= 1, "model_reg_rollout: need n >= 1 rows");
+    return reg(m, n, false);
 }
 
 extern "C" void ptcg_model_free(PtcgModel* m) {
@@ -500,10 +519,13 @@ extern "C" int ptcg_model_forward(PtcgModel* m, const float* obs, const int32_t*
                nullptr, 0, nullptr, 0, s));
     PT_TRY(lin(m->gd, x.bcast_in, m->bc_w, m->bc_b, m->bc, D, N, x.bcast_in, D, EPI_BIAS, nullptr, 0, nullptr, 0, s));
     PT_TRY(pt_x0_fwd(c, m->tokp, m->bc, m->readout, m->x[0], m->keep, s));
+    const bool tr = m->train;
     for (int i = 0; i < d.layers; ++i)
-        PT_TRY(block_fwd(m, m->blk[i], m->ba[i], x.l_seq, m->keep, m->x[i], m->x[i + 1], s));
+        PT_TRY(block_fwd(m, m->blk[i], m->ba[tr ? i : 0], x.l_seq, m->keep, m->x[tr ? i : i % 2],
+                         m->x[tr ? i + 1 : (i + 1) % 2], s));
     const int NL = N * x.l_seq;
-    PT_TRY(pt_ln_fwd(m->x[d.layers], D, m->lnf_w, m->lnf_b, m->h, D, m->lnf_mu, m->lnf_rs, NL, D, s));
+    PT_TRY(pt_ln_fwd(m->x[tr ? d.layers : d.layers % 2], D, m->lnf_w, m->lnf_b, m->h, D, m->lnf_mu, m->lnf_rs,
+                     NL, D, s));
 
     // option scorer
     const int NJ = N * NO;
@@ -525,10 +547,12 @@ extern "C" int ptcg_model_forward(PtcgModel* m, const float* obs, const int32_t*
     if (d.critic == 0) {
         PT_TRY(pt_head_dot(m->v1a, N, PT_VAL_H, m->v2_w, m->v2_b, m->out, 1, NO + 1, NO, s));
     } else {
-        PT_TRY(pt_head_dot(m->v1a, N, PT_VAL_H, m->v2_w, m->v2_b, m->bv, 1, 1, 0, s));
-        // belief heads: opp-hand counts from [r | g], prize logit per token
-        PT_TRY(linf(m->val_in, m->ah_w, m->ah_b, m->hand_lin, N, x.val_in, d.n_cards, EPI_BIAS, nullptr, nullptr, s));
-        PT_TRY(pt_head_dot(m->h, NL, D, m->ap_w, m->ap_b, m->prize_all, 1, 1, 0, s));
+        if (tr) {   // training only (ptcg_model3.cu:353-363): blind value and belief heads
+            PT_TRY(pt_head_dot(m->v1a, N, PT_VAL_H, m->v2_w, m->v2_b, m->bv, 1, 1, 0, s));
+            PT_TRY(linf(m->val_in, m->ah_w, m->ah_b, m->hand_lin, N, x.val_in, d.n_cards, EPI_BIAS, nullptr,
+                        nullptr, s));
+            PT_TRY(pt_head_dot(m->h, NL, D, m->ap_w, m->ap_b, m->prize_all, 1, 1, 0, s));
+        }
         // oracle critic top (ptcg_model3.cu:334-351)
         const int NK = N * x.n_orc;
         PT_TRY(pt_otok_in(c, m->card, m->keep, m->otok_in, m->ckeep, s));
@@ -639,6 +663,7 @@ static int critic_bwd(PtcgModel* m, const GatherCtx& c, const float* grad, hipSt
 
 extern "C" int ptcg_model_backward(PtcgModel* m, const float* grad, void* stream) {
     PT_REQUIRE(m && grad && m->mem && m->obs, "model_backward: run a forward first");
+    PT_REQUIRE(m->train, "model_backward: activations were registered for rollout (ptcg_model_reg_train)");
     hipStream_t s = (hipStream_t)stream;
     const PtcgDims& d = m->dm;
     const DimsX& x = m->dx;

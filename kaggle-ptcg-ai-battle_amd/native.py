@@ -46,6 +46,12 @@ _SIGS = {
     "ptcg_model_set_static": (ctypes.c_int, [c_void_p] * 8),
     "ptcg_model_bind_returns": (ctypes.c_int, [c_void_p, c_void_p]),
     "ptcg_trainer_set_static": (ctypes.c_int, [c_void_p] * 8),
+    "ptcg_model_reg_rollout": (ctypes.c_int, [c_void_p, ctypes.c_int]),
+    "ptcg_sample_actions": (ctypes.c_int, [c_void_p, ctypes.c_int, ctypes.c_int, c_void_p, ctypes.c_int64,
+                                           c_void_p, ctypes.c_uint64, ctypes.c_uint64, c_void_p, c_void_p,
+                                           c_void_p, c_void_p, c_void_p]),
+    "ptcg_trainer_rollout": (ctypes.c_int, [c_void_p, c_void_p, c_void_p, ctypes.c_int, ctypes.c_uint64,
+                                            ctypes.c_uint64, c_void_p, c_void_p, c_void_p, c_void_p]),
     "ptcg_model_free": (None, [c_void_p]),
     "ptcg_ppo_loss_fwd_bwd": (ctypes.c_int, [
         c_void_p, ctypes.c_int, ctypes.c_int, c_void_p, ctypes.c_int64, c_void_p,

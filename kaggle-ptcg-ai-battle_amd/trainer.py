@@ -113,6 +113,16 @@ class PuffeRL:
                                             i["card_attacks"].ctypes.data, i["card_skills"].ctypes.data))
         self._static = (f, i)   # keep the host copies alive for the call's duration
 
+    def rollout_step(self, obs, n, seed, step, idx=None, stream=None):
+        """Forward ``n`` device obs rows with inference activations and sample
+        one action per row; returns device tensors (actions, logprobs, values)."""
+        t = self._torch
+        acts = t.empty(n, dtype=t.float32, device="cuda")
+        lps, vals = t.empty_like(acts), t.empty_like(acts)
+        check(lib().ptcg_trainer_rollout(self._h, obs.data_ptr(), idx.data_ptr() if idx is not None else None,
+                                         n, seed, step, acts.data_ptr(), lps.data_ptr(), vals.data_ptr(), stream))
+        return acts, lps, vals
+
     def step_count(self):
         v = ctypes.c_int32()
         check(lib().ptcg_trainer_step_count(self._h, ctypes.byref(v)))

@@ -17,7 +17,9 @@ Secondary workloads (not the headline line): ``--workload rollout`` times
 the rollout step — inference forward of 8192 rows plus one sampled action
 per row; ``--workload frozen`` times the training step of the reference's
 own model variant (frozen layout: 160 tokens, d256/H8/FFN512, static-table
-card vectors, oracle critic over 218 positions, aux losses).
+card vectors, oracle critic over 218 positions, aux losses);
+``--workload bf16`` times the training step at B = 2048 with bf16 GEMM
+products (fp32 accumulation and everything else fp32).
 """
 import argparse
 import ctypes
@@ -33,6 +35,7 @@ sys.path.insert(0, ROOT)
 
 METRIC = "PPO minibatch step obs/sec (fwd+bwd+Adam) @B=512; % MFMA/HBM roofline"
 FP32_MFMA_PEAK_TFLOPS = 157.3      # MI355X dense fp32 matrix peak
+BF16_MFMA_PEAK_TFLOPS = 2500.0     # MI355X dense bf16 matrix peak
 
 TRAIN = dict(learning_rate=3e-4, beta1=0.9, beta2=0.999, eps=1e-8, max_grad_norm=0.5,
              clip_coef=0.2, vf_clip_coef=0.2, vf_coef=0.5, ent_coef=0.01)
@@ -95,7 +98,7 @@ def main():
     ap.add_argument("--rollout", type=int, default=16384)
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--workload", choices=("train", "rollout", "frozen"), default="train")
+    ap.add_argument("--workload", choices=("train", "rollout", "frozen", "bf16"), default="train")
     ap.add_argument("--rollout-rows", type=int, default=8192)
     args = ap.parse_args()
     if args.gpus != 1:
@@ -112,12 +115,16 @@ def main():
         return bench_rollout(args)
     dm = dims.FROZEN if args.workload == "frozen" else dims.CORE
     B, R = args.minibatch, args.rollout
+    bf16 = args.workload == "bf16"
+    if bf16 and B == 512:
+        B = 2048   # the mixed-precision configuration's minibatch
     if args.workload == "frozen":
         R = min(R, 4096)
     obs = synth.make_obs(dm, R, seed=1)
     inp = synth.make_ppo_inputs(dm, obs, seed=2)
     static = synth.make_static(dm, 4) if dm.tables == 1 else None
-    pl = trainer.create_pufferl({"dims": dm, "train": dict(TRAIN, minibatch_size=B), "seed": 0, "static": static})
+    pl = trainer.create_pufferl({"dims": dm, "train": dict(TRAIN, minibatch_size=B), "seed": 0, "static": static,
+                                 "precision": "bf16" if bf16 else "fp32"})
     trainer.set_rollout(pl, obs, **inp)
     n_lists = args.warmup + args.steps
     lists = synth.minibatch_indices(R, B, n_lists, seed=3)
@@ -168,9 +175,11 @@ def main():
         lv.append(l)
     gemm_s = ms.value / 1e3
     achieved = useful / gemm_s / 1e12
-    roof = dict(bound="mfma", kernel="gemm_f32_kernel (all launches: trunk, token, option and head GEMMs)",
-                achieved=round(achieved, 3), peak=FP32_MFMA_PEAK_TFLOPS, unit="TFLOP/s",
-                frac=round(achieved / FP32_MFMA_PEAK_TFLOPS, 4), traffic=None,
+    peak = BF16_MFMA_PEAK_TFLOPS if bf16 else FP32_MFMA_PEAK_TFLOPS
+    kname = "gemm_bf16_kernel" if bf16 else "gemm_f32_kernel"
+    roof = dict(bound="mfma", kernel=f"{kname} (all launches: trunk, token, option and head GEMMs)",
+                achieved=round(achieved, 3), peak=peak, unit="TFLOP/s",
+                frac=round(achieved / peak, 4), traffic=None,
                 launches_per_step=launches.value / K,
                 avg_launch_us=round(ms.value * 1e3 / max(launches.value, 1), 3),
                 gemm_ms_per_step=round(ms.value / K, 4),
@@ -178,19 +187,22 @@ def main():
                 useful_tflop_per_step=round(useful / K / 1e12, 4),
                 mean_valid_seq=round(float(np.mean(lv)), 2))
     line = {
-        "metric": METRIC, "value": round(B * K / sec, 2), "unit": "obs/s", "n_gpus": 1,
+        "metric": METRIC if not bf16 else "PPO minibatch step obs/sec (fwd+bwd+Adam) @B=2048, bf16 GEMM products",
+        "value": round(B * K / sec, 2), "unit": "obs/s", "n_gpus": 1,
         "steps": K, "warmup": args.warmup, "ms_per_step": round(sec * 1e3 / K, 4),
-        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp32",
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16" if bf16 else "fp32",
         "data": "synthetic",
-        "config": {"workload": "PPO minibatch step (fwd+bwd+PPO loss+grad-norm clip+Adam) on 512 rows of "
+        "config": {"workload": f"PPO minibatch step (fwd+bwd+PPO loss+grad-norm clip+Adam) on {B} rows of "
                                "a 16384-row HBM-resident rollout; 96 tokens + READOUT, 32 token features, "
-                               "card ids [0,2048), d256/H4/FFN1024/4 layers, 64 options, blind value head",
+                               "card ids [0,2048), d256/H4/FFN1024/4 layers, 64 options, blind value head"
+                               + ("; bf16 GEMM operands, fp32 accumulation, LayerNorm, attention, loss, "
+                                  "master weights and Adam state" if bf16 else ""),
                    "minibatch": B, "rollout_rows": R, "seq_len": dm.l_tok + 1,
                    "parallelism": "single GPU"},
         "roofline": roof,
         "losses": {k: round(v, 5) for k, v in losses.items() if isinstance(v, float)},
     }
-    if not args.no_cpu_baseline:
+    if not args.no_cpu_baseline and not bf16:
         line["cpu_baseline"] = cpu_baseline(dm, obs, inp, B, args.cpu_seconds)
         line["gpu_over_cpu"] = round(line["value"] / line["cpu_baseline"]["value"], 1)
     pl.close()

@@ -102,6 +102,11 @@ void ptcg_model_free(PtcgModel* m);
 int ptcg_model_set_static(PtcgModel* m, const float* card_static, const float* att_static,
                           const float* card_text, const float* att_text, const float* skill_text,
                           const int32_t* card_attacks, const int32_t* card_skills);
+/* GEMM product precision (the reference's USE_BF16 switch, compile-time
+ * there): 0 = fp32 (default), 1 = bf16 operands with fp32 accumulation.
+ * LayerNorm, attention, softmax, loss, weights and optimizer state stay
+ * fp32 in both.                                                           */
+int ptcg_model_set_precision(PtcgModel* m, int prec);
 /* ptcg_bind_train_graph (ptcg_model2.cu:323-330), oracle-critic models
  * (dims.critic == 1): device array of per-row returns the blind-value aux
  * loss regresses to, indexed like the obs rows of the forward (through its
@@ -183,6 +188,8 @@ int ptcg_trainer_debug_forward(PtcgTrainer* t, const float* obs_host, int n, flo
 int ptcg_trainer_rollout(PtcgTrainer* t, const float* obs, const int32_t* row_idx, int n,
                          uint64_t seed, uint64_t step, float* actions, float* logprobs,
                          float* values, void* stream);
+/* ptcg_model_set_precision on the trainer's models (train and rollout).  */
+int ptcg_trainer_set_precision(PtcgTrainer* t, int prec);
 /* ptcg_model_set_static on the trainer's model.                          */
 int ptcg_trainer_set_static(PtcgTrainer* t, const float* card_static, const float* att_static,
                             const float* card_text, const float* att_text, const float* skill_text,

@@ -26,6 +26,16 @@ int ptcg_kernel_gemm(int M, int N, int K, const float* A, int64_t lda, int a_t,
                      const float* bias, const float* R, int64_t ldr, float* C2, int64_t ldc2,
                      float* workspace, int64_t workspace_floats, void* stream);
 
+/* ptcg_kernel_gemm with bf16 products: A and B rounded to bf16 (round to
+ * nearest even) on the way into LDS, v_mfma_f32_16x16x32_bf16, fp32
+ * accumulation and epilogue (the reference's USE_BF16 build, pufferlib.cu
+ * precision_t = bf16 with cuBLAS fp32 compute).  Shapes that break the
+ * 128-bit operand rules run the fp32 kernel.                              */
+int ptcg_kernel_gemm_bf16(int M, int N, int K, const float* A, int64_t lda, int a_t,
+                          const float* B, int64_t ldb, int b_t, float* C, int64_t ldc, int epi,
+                          const float* bias, const float* R, int64_t ldr, float* C2, int64_t ldc2,
+                          float* workspace, int64_t workspace_floats, void* stream);
+
 /* weight gradient of a linear layer Y = X W^T + b (pt_linear_bwd's dW / db,
  * ptcg_kernels.cuh:81-108): dW (out, in) = dY^T X, db (out) = column sums of
  * dY (optional, NULL to skip), both overwritten and summed in a fixed order.

@@ -279,6 +279,7 @@ struct PtcgTrainer {
     // activations for `roll_n` rows (reg_rollout), made on first use
     PtcgModel* roll = nullptr;
     int roll_n = 0;
+    int prec = 0;
     std::vector<float> st_f[5];
     std::vector<int32_t> st_i[2];
 };
@@ -524,6 +525,14 @@ extern "C" int ptcg_trainer_set_static(PtcgTrainer* t, const float* card_static,
     return PTCG_OK;
 }
 
+extern "C" int ptcg_trainer_set_precision(PtcgTrainer* t, int prec) {
+    PT_REQUIRE(t, "trainer_set_precision: null trainer");
+    PT_TRY(ptcg_model_set_precision(t->model, prec));
+    if (t->roll) PT_TRY(ptcg_model_set_precision(t->roll, prec));
+    t->prec = prec;
+    return PTCG_OK;
+}
+
 extern "C" int ptcg_trainer_rollout(PtcgTrainer* t, const float* obs, const int32_t* row_idx, int n,
                                     uint64_t seed, uint64_t step, float* actions, float* logprobs,
                                     float* values, void* stream) {
@@ -533,6 +542,7 @@ extern "C" int ptcg_trainer_rollout(PtcgTrainer* t, const float* obs, const int3
         if (!t->roll) {
             PT_TRY(ptcg_model_create(&t->dm, &t->roll));
             PT_TRY(ptcg_model_bind(t->roll, t->P, t->Gr));
+            PT_TRY(ptcg_model_set_precision(t->roll, t->prec));
             if (t->dm.tables == 1 && !t->st_i[0].empty())
                 PT_TRY(ptcg_model_set_static(t->roll, t->st_f[0].data(), t->st_f[1].data(), t->st_f[2].data(),
                                              t->st_f[3].data(), t->st_f[4].data(), t->st_i[0].data(),

@@ -108,6 +108,9 @@ struct GemmArgs {
     // optional, a_t == 1 with the STORE epilogue only: dbias[m] = sum_k A[k][m]
     // (the bias gradient of a weight-gradient product dW = dY^T X)
     float* dbias;
+    // 0: fp32 products (v_mfma_f32_16x16x4_f32); 1: operands rounded to bf16
+    // on the way into LDS, fp32 accumulation (v_mfma_f32_16x16x32_bf16)
+    int prec;
 };
 
 // Launch C = epi(A*B) on `stream`. Requirements: K % 4 == 0 when the operand

@@ -66,6 +66,47 @@ __device__ __forceinline__ float4 ld_scalar4(const gfloat* X, long ld, int lim, 
     return v;
 }
 
+// Epilogue shared by the fp32 and bf16 kernels: acc[ti][tj][r] holds
+// C[wm + ti*16 + 4*lq + r][wn + tj*16 + li] of the block tile at (m0, n0).
+template <int EPI, bool PARTIAL>
+__device__ __forceinline__ void gemm_epilogue(const GemmArgs& g, floatx4 (&acc)[4][4], int m0, int n0, int wm,
+                                              int wn, int li, int lq, long part_stride) {
+    const long zoff = PARTIAL ? (long)blockIdx.z * part_stride : 0;
+#pragma unroll
+    for (int ti = 0; ti < 4; ++ti)
+#pragma unroll
+        for (int tj = 0; tj < 4; ++tj) {
+            const int n = n0 + wn + tj * 16 + li;
+            if (n >= g.N) continue;
+            float bn = 0.f;
+            if (!PARTIAL && (EPI == EPI_BIAS || EPI == EPI_BIAS_GELU || EPI == EPI_BIAS_RESID))
+                bn = g.bias[n];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int m = m0 + wm + ti * 16 + lq * 4 + r;
+                if (m >= g.M) continue;
+                float v = acc[ti][tj][r];
+                if (PARTIAL) {
+                    g.C[zoff + (long)m * g.ldc + n] = v;
+                } else if (EPI == EPI_STORE) {
+                    g.C[(long)m * g.ldc + n] = v;
+                } else if (EPI == EPI_BIAS) {
+                    g.C[(long)m * g.ldc + n] = v + bn;
+                } else if (EPI == EPI_BIAS_GELU) {
+                    v += bn;
+                    g.C[(long)m * g.ldc + n] = v;
+                    g.C2[(long)m * g.ldc2 + n] = pt_gelu(v);
+                } else if (EPI == EPI_BIAS_RESID) {
+                    g.C[(long)m * g.ldc + n] = v + bn + g.R[(long)m * g.ldr + n];
+                } else if (EPI == EPI_GELU_BWD) {
+                    g.C[(long)m * g.ldc + n] = v * pt_gelu_grad(g.R[(long)m * g.ldr + n]);
+                } else if (EPI == EPI_ACCUM) {
+                    g.C[(long)m * g.ldc + n] += v;
+                }
+            }
+        }
+}
+
 // DB (AT only): blocks of the first N-tile also sum their A tile over k, the
 // bias gradient sum_k dY[k][m]; thread t covers m = t % 128 over k half t / 128.
 // With PARTIAL the per-split sums go to C + splits*part_stride + z*M.
@@ -177,41 +218,118 @@ __global__ __launch_bounds__(NT) void gemm_f32_kernel(GemmArgs g, int k_chunk, l
         }
     }
 
-    // epilogue: acc[ti][tj][r] = C[wm + ti*16 + 4*lq + r][wn + tj*16 + li]
-    const long zoff = PARTIAL ? (long)blockIdx.z * part_stride : 0;
+    gemm_epilogue<EPI, PARTIAL>(g, acc, m0, n0, wm, wn, li, lq, part_stride);
+}
+
+// ---------------------------------------------------------------- bf16
+// Mixed precision: fp32 operands from HBM are rounded to bf16 (RNE) on the
+// way into LDS and multiplied on v_mfma_f32_16x16x32_bf16 with fp32
+// accumulation; the epilogue is the fp32 kernel's.  Same 128x128 block,
+// 4 waves x 64x64, XCD tile order; BK = 32 (one MFMA k-step).  Both operands
+// sit in LDS as [row][k] bf16 (row stride 40: 16 B-aligned 128-bit fragment
+// reads, conflict-free across 8 lanes); an m-contiguous operand is
+// transposed in registers (4x4 blocks) before its 64-bit LDS stores.  A
+// lane's fragment is 8 consecutive k of one row; A and B use the same
+// (lane group, element) -> k map, so the product is independent of the
+// hardware's internal k order.
+constexpr int BK2 = 32, SKB2 = BK2 + 8;
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ bf16x4 to_bf16x4(float a, float b, float c, float d) {
+    return bf16x4{(__bf16)a, (__bf16)b, (__bf16)c, (__bf16)d};
+}
+
+// stage one operand's 128 x 32 tile: T (m-contiguous in memory) or not.
+// Thread t covers: !T: row t/2, k 16*(t%2) .. +15 (four 128-bit loads);
+// T: rows 4*(t/8) .. +3, k 4*(t%8) .. +3 (four 128-bit loads along m).
+template <bool T>
+__device__ __forceinline__ void bf_load(const gfloat* X, long ld, int lim, int r0, int k0, int kend, int tid,
+                                        float4 (&v)[4]) {
+    const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (!T) {
+        const int row = r0 + (tid >> 1), kq = k0 + (tid & 1) * 16;
 #pragma unroll
-    for (int ti = 0; ti < 4; ++ti)
+        for (int j = 0; j < 4; ++j)
+            v[j] = (row < lim && kq + 4 * j < kend) ? ld_g4(X + (long)row * ld + kq + 4 * j) : z4;
+    } else {
+        const int mq = r0 + (tid >> 3) * 4, kq = k0 + (tid & 7) * 4;
 #pragma unroll
-        for (int tj = 0; tj < 4; ++tj) {
-            const int n = n0 + wn + tj * 16 + li;
-            if (n >= g.N) continue;
-            float bn = 0.f;
-            if (!PARTIAL && (EPI == EPI_BIAS || EPI == EPI_BIAS_GELU || EPI == EPI_BIAS_RESID))
-                bn = g.bias[n];
+        for (int j = 0; j < 4; ++j)
+            v[j] = (mq < lim && kq + j < kend) ? ld_g4(X + (long)(kq + j) * ld + mq) : z4;
+    }
+}
+
+template <bool T>
+__device__ __forceinline__ void bf_store(__bf16* S, int tid, const float4 (&v)[4]) {
+    if (!T) {
+        const int row = tid >> 1, kq = (tid & 1) * 16;
+        bf16x4* d = reinterpret_cast<bf16x4*>(S + row * SKB2 + kq);
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int m = m0 + wm + ti * 16 + lq * 4 + r;
-                if (m >= g.M) continue;
-                float v = acc[ti][tj][r];
-                if (PARTIAL) {
-                    g.C[zoff + (long)m * g.ldc + n] = v;
-                } else if (EPI == EPI_STORE) {
-                    g.C[(long)m * g.ldc + n] = v;
-                } else if (EPI == EPI_BIAS) {
-                    g.C[(long)m * g.ldc + n] = v + bn;
-                } else if (EPI == EPI_BIAS_GELU) {
-                    v += bn;
-                    g.C[(long)m * g.ldc + n] = v;
-                    g.C2[(long)m * g.ldc2 + n] = pt_gelu(v);
-                } else if (EPI == EPI_BIAS_RESID) {
-                    g.C[(long)m * g.ldc + n] = v + bn + g.R[(long)m * g.ldr + n];
-                } else if (EPI == EPI_GELU_BWD) {
-                    g.C[(long)m * g.ldc + n] = v * pt_gelu_grad(g.R[(long)m * g.ldr + n]);
-                } else if (EPI == EPI_ACCUM) {
-                    g.C[(long)m * g.ldc + n] += v;
-                }
+        for (int j = 0; j < 4; ++j) d[j] = to_bf16x4(v[j].x, v[j].y, v[j].z, v[j].w);
+    } else {
+        const int mq = (tid >> 3) * 4, kq = (tid & 7) * 4;
+        *reinterpret_cast<bf16x4*>(S + (mq + 0) * SKB2 + kq) = to_bf16x4(v[0].x, v[1].x, v[2].x, v[3].x);
+        *reinterpret_cast<bf16x4*>(S + (mq + 1) * SKB2 + kq) = to_bf16x4(v[0].y, v[1].y, v[2].y, v[3].y);
+        *reinterpret_cast<bf16x4*>(S + (mq + 2) * SKB2 + kq) = to_bf16x4(v[0].z, v[1].z, v[2].z, v[3].z);
+        *reinterpret_cast<bf16x4*>(S + (mq + 3) * SKB2 + kq) = to_bf16x4(v[0].w, v[1].w, v[2].w, v[3].w);
+    }
+}
+
+template <bool AT, bool BT, int EPI, bool PARTIAL>
+__global__ __launch_bounds__(NT) void gemm_bf16_kernel(GemmArgs g, int k_chunk, long part_stride) {
+    __shared__ __align__(16) __bf16 As[2][BM * SKB2];
+    __shared__ __align__(16) __bf16 Bs[2][BN * SKB2];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tm = (g.M + BM - 1) / BM, tn = (g.N + BN - 1) / BN;
+    int tmi, tni;
+    tile_of(blockIdx.x, tm * tn, tn, tmi, tni);
+    const int m0 = tmi * BM, n0 = tni * BN;
+    const int kbeg = blockIdx.z * k_chunk;
+    const int kend = min(g.K, kbeg + k_chunk);
+    const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
+    const int li = lane & 15, lq = lane >> 4;
+    floatx4 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+    const gfloat* __restrict__ Ag = (const gfloat*)(g.A);
+    const gfloat* __restrict__ Bg = (const gfloat*)(g.B);
+    float4 va[4], vb[4];
+    if (kbeg < kend) {
+        bf_load<AT>(Ag, g.lda, g.M, m0, kbeg, kend, tid, va);
+        bf_load<BT>(Bg, g.ldb, g.N, n0, kbeg, kend, tid, vb);
+        bf_store<AT>(As[0], tid, va);
+        bf_store<BT>(Bs[0], tid, vb);
+        __syncthreads();
+        int buf = 0;
+        for (int k0 = kbeg; k0 < kend; k0 += BK2) {
+            const bool more = k0 + BK2 < kend;
+            if (more) {
+                bf_load<AT>(Ag, g.lda, g.M, m0, k0 + BK2, kend, tid, va);
+                bf_load<BT>(Bg, g.ldb, g.N, n0, k0 + BK2, kend, tid, vb);
             }
+            bf16x8 af[4], bfr[4];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                af[t] = *reinterpret_cast<const bf16x8*>(&As[buf][(wm + t * 16 + li) * SKB2 + 8 * lq]);
+                bfr[t] = *reinterpret_cast<const bf16x8*>(&Bs[buf][(wn + t * 16 + li) * SKB2 + 8 * lq]);
+            }
+#pragma unroll
+            for (int ti = 0; ti < 4; ++ti)
+#pragma unroll
+                for (int tj = 0; tj < 4; ++tj)
+                    acc[ti][tj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[ti], bfr[tj], acc[ti][tj], 0, 0, 0);
+            if (more) {
+                bf_store<AT>(As[buf ^ 1], tid, va);
+                bf_store<BT>(Bs[buf ^ 1], tid, vb);
+            }
+            __syncthreads();
+            buf ^= 1;
         }
+    }
+    gemm_epilogue<EPI, PARTIAL>(g, acc, m0, n0, wm, wn, li, lq, part_stride);
 }
 
 // out[m][n] (=|+=) sum_s part[s][m][n], fixed order over s
@@ -280,6 +398,44 @@ void launch(const GemmArgs& g, dim3 grid, int k_chunk, long part_stride, hipStre
         g_prof.flops[g_prof.used] = 2.0 * g.M * (double)g.N * g.K;
         g_prof.used++;
     }
+}
+
+template <bool AT, bool BT, int EPI, bool PARTIAL>
+void launch_bf16(const GemmArgs& g, dim3 grid, int k_chunk, long part_stride, hipStream_t s) {
+    const bool rec = g_prof.on && g_prof.used * 2 + 1 < (int)g_prof.ev.size();
+    if (rec) (void)hipEventRecord(g_prof.ev[2 * g_prof.used], s);
+    hipLaunchKernelGGL((gemm_bf16_kernel<AT, BT, EPI, PARTIAL>), grid, dim3(NT), 0, s, g, k_chunk, part_stride);
+    if (rec) {
+        (void)hipEventRecord(g_prof.ev[2 * g_prof.used + 1], s);
+        g_prof.flops[g_prof.used] = 2.0 * g.M * (double)g.N * g.K;
+        g_prof.used++;
+    }
+}
+
+template <bool AT, bool BT>
+int launch_bf16_epi(const GemmArgs& g, dim3 grid, int k_chunk, long part_stride, bool partial, hipStream_t s) {
+    if (partial) {
+        launch_bf16<AT, BT, EPI_STORE, true>(g, grid, k_chunk, part_stride, s);
+        return PTCG_OK;
+    }
+    switch (g.epi) {
+        case EPI_STORE: launch_bf16<AT, BT, EPI_STORE, false>(g, grid, k_chunk, 0, s); break;
+        case EPI_BIAS: launch_bf16<AT, BT, EPI_BIAS, false>(g, grid, k_chunk, 0, s); break;
+        case EPI_BIAS_GELU: launch_bf16<AT, BT, EPI_BIAS_GELU, false>(g, grid, k_chunk, 0, s); break;
+        case EPI_BIAS_RESID: launch_bf16<AT, BT, EPI_BIAS_RESID, false>(g, grid, k_chunk, 0, s); break;
+        case EPI_GELU_BWD: launch_bf16<AT, BT, EPI_GELU_BWD, false>(g, grid, k_chunk, 0, s); break;
+        case EPI_ACCUM: launch_bf16<AT, BT, EPI_ACCUM, false>(g, grid, k_chunk, 0, s); break;
+        default: PT_REQUIRE(false, "gemm: bad epilogue %d", g.epi);
+    }
+    return PTCG_OK;
+}
+
+int launch_bf16_any(const GemmArgs& g, dim3 grid, int k_chunk, long part_stride, bool partial, hipStream_t s) {
+    const int code = (g.a_t ? 1 : 0) * 2 + (g.b_t ? 1 : 0);
+    if (code == 0) return launch_bf16_epi<false, false>(g, grid, k_chunk, part_stride, partial, s);
+    if (code == 1) return launch_bf16_epi<false, true>(g, grid, k_chunk, part_stride, partial, s);
+    if (code == 3) return launch_bf16_epi<true, true>(g, grid, k_chunk, part_stride, partial, s);
+    return launch_bf16_epi<true, false>(g, grid, k_chunk, part_stride, partial, s);
 }
 
 // split-K partial products (STORE into the workspace), optional bias sums
@@ -362,20 +518,24 @@ int pt_gemm(const GemmArgs& g, float* ws, long ws_floats, hipStream_t s) {
     const bool vec = (g.a_t ? (g.M % 4 == 0) : (g.K % 4 == 0)) && (g.b_t ? (g.N % 4 == 0) : (g.K % 4 == 0)) &&
                      g.lda % 4 == 0 && g.ldb % 4 == 0 && ((uintptr_t)g.A & 15) == 0 &&
                      ((uintptr_t)g.B & 15) == 0;
+    // bf16 products need the 128-bit operand path; other shapes stay fp32
+    const bool bf = g.prec == 1 && vec;
+    const int bk = bf ? BK2 : BK;
     const int tm = pt_cdiv(g.M, BM), tn = pt_cdiv(g.N, BN);
     const int tiles = tm * tn;
     // split K when the output is too small to fill the chip and K is long
     int splits = 1;
     const int target = 512;
-    if (tiles < target && g.K >= 4 * BK * 16) {
+    if (tiles < target && g.K >= 4 * bk * 16) {
         splits = pt_cdiv(target, tiles);
-        int max_splits = g.K / (BK * 16);
+        int max_splits = g.K / (bk * 16);
         if (splits > max_splits) splits = max_splits;
         if (splits < 1) splits = 1;
     }
     if (splits > 1 && !(g.epi == EPI_STORE || g.epi == EPI_ACCUM)) splits = 1;
-    const bool db = g.dbias != nullptr;
-    PT_REQUIRE(!db || (g.a_t && g.epi == EPI_STORE), "gemm: dbias needs a_t = 1 and the STORE epilogue");
+    PT_REQUIRE(!(g.dbias && !(g.a_t && g.epi == EPI_STORE)), "gemm: dbias needs a_t = 1 and the STORE epilogue");
+    // the bf16 kernel leaves bias sums to the fp32 column sum (kept in fp32 from the unrounded dY)
+    const bool db = g.dbias != nullptr && !bf;
     long part_stride = (long)g.M * g.ldc;
     const long per_split = part_stride + (db ? g.M : 0);
     if (splits > 1 && (ws == nullptr || (long)splits * per_split > ws_floats)) {
@@ -384,27 +544,33 @@ int pt_gemm(const GemmArgs& g, float* ws, long ws_floats, hipStream_t s) {
     }
     int k_chunk = g.K;
     if (splits > 1) {
-        k_chunk = pt_cdiv(pt_cdiv(g.K, splits), BK) * BK;
+        k_chunk = pt_cdiv(pt_cdiv(g.K, splits), bk) * bk;
         splits = pt_cdiv(g.K, k_chunk);
     }
     dim3 grid(tn * tm, 1, splits);
+    if (bf && g.dbias) {
+        // bias sums first: they read the fp32 dY, which the product does not modify
+        PT_TRY(pt_colsum(g.A, g.lda, g.K, g.M, g.dbias, ws, ws_floats, s));
+    }
     if (splits > 1) {
         GemmArgs p = g;
         p.C = ws;
-        if (vec) launch_partial<true>(p, db, grid, k_chunk, part_stride, s);
+        if (bf) PT_TRY(launch_bf16_any(p, grid, k_chunk, part_stride, true, s));
+        else if (vec) launch_partial<true>(p, db, grid, k_chunk, part_stride, s);
         else launch_partial<false>(p, db, grid, k_chunk, part_stride, s);
         PT_LAUNCH_CHECK();
         long tot = (long)g.M * g.N + (db ? g.M : 0);
         if (g.epi == EPI_ACCUM)
             hipLaunchKernelGGL(splitk_reduce_kernel<true>, dim3(pt_cdiv(tot, 256)), dim3(256), 0, s,
-                               g.C, g.ldc, ws, part_stride, splits, g.M, g.N, g.dbias);
+                               g.C, g.ldc, ws, part_stride, splits, g.M, g.N, db ? g.dbias : nullptr);
         else
             hipLaunchKernelGGL(splitk_reduce_kernel<false>, dim3(pt_cdiv(tot, 256)), dim3(256), 0, s,
-                               g.C, g.ldc, ws, part_stride, splits, g.M, g.N, g.dbias);
+                               g.C, g.ldc, ws, part_stride, splits, g.M, g.N, db ? g.dbias : nullptr);
         PT_LAUNCH_CHECK();
         return PTCG_OK;
     }
-    PT_TRY(vec ? launch_full<true>(g, db, grid, k_chunk, s) : launch_full<false>(g, db, grid, k_chunk, s));
+    if (bf) PT_TRY(launch_bf16_any(g, grid, k_chunk, 0, false, s));
+    else PT_TRY(vec ? launch_full<true>(g, db, grid, k_chunk, s) : launch_full<false>(g, db, grid, k_chunk, s));
     PT_LAUNCH_CHECK();
     return PTCG_OK;
 }

@@ -22,6 +22,23 @@ extern "C" int ptcg_kernel_gemm(int M, int N, int K, const float* A, int64_t lda
     return pt_gemm(g, workspace, workspace_floats, (hipStream_t)stream);
 }
 
+extern "C" int ptcg_kernel_gemm_bf16(int M, int N, int K, const float* A, int64_t lda, int a_t,
+                                     const float* B, int64_t ldb, int b_t, float* C, int64_t ldc,
+                                     int epi, const float* bias, const float* R, int64_t ldr, float* C2,
+                                     int64_t ldc2, float* workspace, int64_t workspace_floats,
+                                     void* stream) {
+    PT_REQUIRE(A && B && C, "kernel_gemm_bf16: null operand");
+    PT_REQUIRE(epi >= EPI_STORE && epi <= EPI_ACCUM, "kernel_gemm_bf16: bad epilogue %d", epi);
+    GemmArgs g{};
+    g.M = M; g.N = N; g.K = K;
+    g.A = A; g.lda = lda; g.a_t = a_t;
+    g.B = B; g.ldb = ldb; g.b_t = b_t;
+    g.C = C; g.ldc = ldc; g.epi = epi;
+    g.bias = bias; g.R = R; g.ldr = ldr; g.C2 = C2; g.ldc2 = ldc2;
+    g.prec = 1;
+    return pt_gemm(g, workspace, workspace_floats, (hipStream_t)stream);
+}
+
 extern "C" int ptcg_kernel_gemm_dw(int rows, int in, int out, const float* dY, int64_t lddy,
                                    const float* X, int64_t ldx, float* dW, float* db,
                                    float* workspace, int64_t workspace_floats, void* stream) {

@@ -66,6 +66,7 @@ struct PtcgModel {
     // one block's worth reused by every layer, no backward buffers)
     int N = 0;
     bool train = true;
+    int prec = 0;   // GEMM products: 0 fp32, 1 bf16 operands with fp32 accumulation
     char* mem = nullptr;
     size_t mem_bytes = 0;
     float *tok_cat, *tokp, *glob_in, *g1, *g1a, *dec_in, *d1, *d1a, *gd, *bc, *keep;
@@ -90,10 +91,11 @@ struct PtcgModel {
 };
 
 // ------------------------------------------------------------ helpers
-static int lin(const float* X, long ldx, const float* W, const float* b, float* Y, long ldy,
+static int lin(const PtcgModel* m, const float* X, long ldx, const float* W, const float* b, float* Y, long ldy,
                int rows, int in, int out, int epi, const float* R, long ldr, float* Y2, long ldy2,
                hipStream_t s) {
     GemmArgs g{};
+    g.prec = m->prec;
     g.M = rows; g.N = out; g.K = in;
     g.A = X; g.lda = ldx; g.a_t = 0;
     g.B = W; g.ldb = in; g.b_t = 0;
@@ -102,14 +104,15 @@ static int lin(const float* X, long ldx, const float* W, const float* b, float* 
     g.epi = epi;
     return pt_gemm(g, nullptr, 0, s);
 }
-static int linf(const float* X, const float* W, const float* b, float* Y, int rows, int in,
+static int linf(const PtcgModel* m, const float* X, const float* W, const float* b, float* Y, int rows, int in,
                 int out, int epi, const float* R, float* Y2, hipStream_t s) {
-    return lin(X, in, W, b, Y, out, rows, in, out, epi, R, out, Y2, out, s);
+    return lin(m, X, in, W, b, Y, out, rows, in, out, epi, R, out, Y2, out, s);
 }
 // dX = dY W[:, :in] : dY (rows, out) ld lddy ; W (out, ldw) ; dX (rows, in) ld lddx
-static int ldxw_(const float* dY, long lddy, const float* W, long ldw, float* dX, long lddx, int rows, int in,
-                 int out, int epi, const float* R, long ldr, hipStream_t s) {
+static int ldxw_(const PtcgModel* m, const float* dY, long lddy, const float* W, long ldw, float* dX, long lddx,
+                 int rows, int in, int out, int epi, const float* R, long ldr, hipStream_t s) {
     GemmArgs g{};
+    g.prec = m->prec;
     g.M = rows; g.N = in; g.K = out;
     g.A = dY; g.lda = lddy; g.a_t = 0;
     g.B = W; g.ldb = ldw; g.b_t = 1;
@@ -119,9 +122,9 @@ static int ldxw_(const float* dY, long lddy, const float* W, long ldw, float* dX
     return pt_gemm(g, nullptr, 0, s);
 }
 // dX = dY W : dY (rows, out) ld lddy ; W (out, in) ; dX (rows, in) ld lddx
-static int ldx_(const float* dY, long lddy, const float* W, float* dX, long lddx, int rows, int in,
-                int out, int epi, const float* R, long ldr, hipStream_t s) {
-    return ldxw_(dY, lddy, W, in, dX, lddx, rows, in, out, epi, R, ldr, s);
+static int ldx_(const PtcgModel* m, const float* dY, long lddy, const float* W, float* dX, long lddx, int rows,
+                int in, int out, int epi, const float* R, long ldr, hipStream_t s) {
+    return ldxw_(m, dY, lddy, W, in, dX, lddx, rows, in, out, epi, R, ldr, s);
 }
 // dW = dY^T X (overwrite), db = colsum dY (fused into the product)
 static int ldw_(PtcgModel* m, const float* dY, long lddy, const float* X, long ldxx, float* dW,
@@ -133,6 +136,7 @@ static int ldw_(PtcgModel* m, const float* dY, long lddy, const float* X, long l
     g.C = dW; g.ldc = in;
     g.epi = EPI_STORE;
     g.dbias = db;
+    g.prec = m->prec;
     return pt_gemm(g, m->ws, m->ws_floats, s);
 }
 
@@ -328,6 +332,12 @@ extern "C" int ptcg_model_set_static(PtcgModel* m, const float* card_static, con
     return PTCG_OK;
 }
 
+extern "C" int ptcg_model_set_precision(PtcgModel* m, int prec) {
+    PT_REQUIRE(m && (prec == 0 || prec == 1), "model_set_precision: precision must be 0 (fp32) or 1 (bf16)");
+    m->prec = prec;
+    return PTCG_OK;
+}
+
 extern "C" int ptcg_model_bind_returns(PtcgModel* m, const float* returns) {
     PT_REQUIRE(m, "model_bind_returns: null model");
     m->ret = returns;
@@ -457,12 +467,12 @@ static int block_fwd(PtcgModel* m, const BlockP& w, const BlockA& a, int L, cons
     const PtcgDims& d = m->dm;
     const int NL = m->N * L, D = d.d;
     PT_TRY(pt_ln_fwd(xin, D, w.ln1w, w.ln1b, a.ln1, D, a.mu1, a.rs1, NL, D, s));
-    PT_TRY(linf(a.ln1, w.qkvw, w.qkvb, a.qkv, NL, D, 3 * D, EPI_BIAS, nullptr, nullptr, s));
+    PT_TRY(linf(m, a.ln1, w.qkvw, w.qkvb, a.qkv, NL, D, 3 * D, EPI_BIAS, nullptr, nullptr, s));
     PT_TRY(pt_attn_fwd(a.qkv, keep, a.ctx, a.lse, m->N, L, d.heads, m->dx.dh, s));
-    PT_TRY(linf(a.ctx, w.projw, w.projb, a.xmid, NL, D, D, EPI_BIAS_RESID, xin, nullptr, s));
+    PT_TRY(linf(m, a.ctx, w.projw, w.projb, a.xmid, NL, D, D, EPI_BIAS_RESID, xin, nullptr, s));
     PT_TRY(pt_ln_fwd(a.xmid, D, w.ln2w, w.ln2b, a.ln2, D, a.mu2, a.rs2, NL, D, s));
-    PT_TRY(linf(a.ln2, w.f1w, w.f1b, a.ffp, NL, D, d.ffn, EPI_BIAS_GELU, nullptr, a.ffa, s));
-    PT_TRY(linf(a.ffa, w.f2w, w.f2b, xout, NL, d.ffn, D, EPI_BIAS_RESID, a.xmid, nullptr, s));
+    PT_TRY(linf(m, a.ln2, w.f1w, w.f1b, a.ffp, NL, D, d.ffn, EPI_BIAS_GELU, nullptr, a.ffa, s));
+    PT_TRY(linf(m, a.ffa, w.f2w, w.f2b, xout, NL, d.ffn, D, EPI_BIAS_RESID, a.xmid, nullptr, s));
     return PTCG_OK;
 }
 
@@ -474,10 +484,10 @@ static int tables_fwd(PtcgModel* m, hipStream_t s) {
     const int NC = d.n_cards, NA = d.n_attacks, NS = d.n_skills, DA = d.d_a, DC = d.d_c;
     const int pa = PT_ID_C + PT_CARD_STATIC + PT_CARD_TEXT;   // first pool column of card_in
     PT_TRY(pt_copy_cols(m->att_in, x.att_in, m->aid_emb, PT_ID_A, NA, PT_ID_A, s));
-    PT_TRY(lin(m->att_in, x.att_in, m->am_w, m->am_b, m->att_lin, DA, NA, x.att_in, DA, EPI_BIAS_GELU, nullptr, 0,
+    PT_TRY(lin(m, m->att_in, x.att_in, m->am_w, m->am_b, m->att_lin, DA, NA, x.att_in, DA, EPI_BIAS_GELU, nullptr, 0,
                m->att_tab, DA, s));
     PT_TRY(pt_copy_cols(m->sk_in, x.sk_in, m->sid_emb, PT_ID_A, NS, PT_ID_A, s));
-    PT_TRY(lin(m->sk_in, x.sk_in, m->sm_w, m->sm_b, m->sk_lin, DC, NS, x.sk_in, DC, EPI_BIAS_GELU, nullptr, 0,
+    PT_TRY(lin(m, m->sk_in, x.sk_in, m->sm_w, m->sm_b, m->sk_lin, DC, NS, x.sk_in, DC, EPI_BIAS_GELU, nullptr, 0,
                m->sk_tab, DC, s));
     PT_TRY(pt_copy_cols(m->card_in, x.card_in, m->cid_emb, PT_ID_C, NC, PT_ID_C, s));
     PT_TRY(pt_pool_fwd(m->att_tab, DA, m->card_attacks, PT_K_ATT, NC, m->card_in, x.card_in, pa, pa + DA,
@@ -486,9 +496,9 @@ static int tables_fwd(PtcgModel* m, hipStream_t s) {
                        pa + 2 * DA + DC, m->s_amax, s));
     PT_TRY(pt_ln_fwd(m->card_in, x.card_in, m->cln_w, m->cln_b, m->card_ln, x.card_in, m->c_mu, m->c_rs, NC,
                      x.card_in, s));
-    PT_TRY(lin(m->card_ln, x.card_in, m->c1_w, m->c1_b, m->card_h1, PT_CARD_H, NC, x.card_in, PT_CARD_H,
+    PT_TRY(lin(m, m->card_ln, x.card_in, m->c1_w, m->c1_b, m->card_h1, PT_CARD_H, NC, x.card_in, PT_CARD_H,
                EPI_BIAS_GELU, nullptr, 0, m->card_g1, PT_CARD_H, s));
-    PT_TRY(linf(m->card_g1, m->c3_w, m->c3_b, m->card_vec, NC, PT_CARD_H, DC, EPI_BIAS, nullptr, nullptr, s));
+    PT_TRY(linf(m, m->card_g1, m->c3_w, m->c3_b, m->card_vec, NC, PT_CARD_H, DC, EPI_BIAS, nullptr, nullptr, s));
     return PTCG_OK;
 }
 
@@ -509,15 +519,15 @@ extern "C" int ptcg_model_forward(PtcgModel* m, const float* obs, const int32_t*
 
     if (d.tables == 1) PT_TRY(tables_fwd(m, s));
     PT_TRY(pt_tok_cat_fwd(c, m->card, m->zemb, m->oemb, m->tok_cat, s));
-    PT_TRY(linf(m->tok_cat, m->tp_w, m->tp_b, m->tokp, N * Lt, x.tok_in, D, EPI_BIAS, nullptr, nullptr, s));
+    PT_TRY(linf(m, m->tok_cat, m->tp_w, m->tp_b, m->tokp, N * Lt, x.tok_in, D, EPI_BIAS, nullptr, nullptr, s));
     PT_TRY(pt_glob_in(c, m->glob_in, s));
-    PT_TRY(linf(m->glob_in, m->g1_w, m->g1_b, m->g1, N, d.global_f, G, EPI_BIAS_GELU, nullptr, m->g1a, s));
-    PT_TRY(lin(m->g1a, G, m->g2_w, m->g2_b, m->gd, x.bcast_in, N, G, G, EPI_BIAS, nullptr, 0, nullptr, 0, s));
+    PT_TRY(linf(m, m->glob_in, m->g1_w, m->g1_b, m->g1, N, d.global_f, G, EPI_BIAS_GELU, nullptr, m->g1a, s));
+    PT_TRY(lin(m, m->g1a, G, m->g2_w, m->g2_b, m->gd, x.bcast_in, N, G, G, EPI_BIAS, nullptr, 0, nullptr, 0, s));
     PT_TRY(pt_dec_in_fwd(c, m->card, m->att, m->semb, m->cemb, m->dec_in, s));
-    PT_TRY(linf(m->dec_in, m->d1_w, m->d1_b, m->d1, N, x.dec_in, PT_DEC_H, EPI_BIAS_GELU, nullptr, m->d1a, s));
-    PT_TRY(lin(m->d1a, PT_DEC_H, m->d2_w, m->d2_b, m->gd + G, x.bcast_in, N, PT_DEC_H, PT_DEC_H, EPI_BIAS,
+    PT_TRY(linf(m, m->dec_in, m->d1_w, m->d1_b, m->d1, N, x.dec_in, PT_DEC_H, EPI_BIAS_GELU, nullptr, m->d1a, s));
+    PT_TRY(lin(m, m->d1a, PT_DEC_H, m->d2_w, m->d2_b, m->gd + G, x.bcast_in, N, PT_DEC_H, PT_DEC_H, EPI_BIAS,
                nullptr, 0, nullptr, 0, s));
-    PT_TRY(lin(m->gd, x.bcast_in, m->bc_w, m->bc_b, m->bc, D, N, x.bcast_in, D, EPI_BIAS, nullptr, 0, nullptr, 0, s));
+    PT_TRY(lin(m, m->gd, x.bcast_in, m->bc_w, m->bc_b, m->bc, D, N, x.bcast_in, D, EPI_BIAS, nullptr, 0, nullptr, 0, s));
     PT_TRY(pt_x0_fwd(c, m->tokp, m->bc, m->readout, m->x[0], m->keep, s));
     const bool tr = m->train;
     for (int i = 0; i < d.layers; ++i)
@@ -531,36 +541,36 @@ extern "C" int ptcg_model_forward(PtcgModel* m, const float* obs, const int32_t*
     const int NJ = N * NO;
     const int oc0 = PT_TYPE_E + 2 * D, oa0 = oc0 + PT_OPT_E;
     PT_TRY(pt_opt_gather_fwd(c, m->card, m->att, m->ocard, m->oatt, s));
-    PT_TRY(lin(m->ocard, d.d_c, m->oc_w, m->oc_b, m->q_in + oc0, x.q_in, NJ, d.d_c, PT_OPT_E, EPI_BIAS,
+    PT_TRY(lin(m, m->ocard, d.d_c, m->oc_w, m->oc_b, m->q_in + oc0, x.q_in, NJ, d.d_c, PT_OPT_E, EPI_BIAS,
                nullptr, 0, nullptr, 0, s));
-    PT_TRY(lin(m->oatt, d.d_a, m->oa_w, m->oa_b, m->q_in + oa0, x.q_in, NJ, d.d_a, PT_OPT_E, EPI_BIAS,
+    PT_TRY(lin(m, m->oatt, d.d_a, m->oa_w, m->oa_b, m->q_in + oa0, x.q_in, NJ, d.d_a, PT_OPT_E, EPI_BIAS,
                nullptr, 0, nullptr, 0, s));
     PT_TRY(pt_q_in_fwd(c, m->h, m->temb, m->q_in, s));
-    PT_TRY(linf(m->q_in, m->q1_w, m->q1_b, m->q1, NJ, x.q_in, D, EPI_BIAS_GELU, nullptr, m->q1a, s));
-    PT_TRY(lin(m->q1a, D, m->q2_w, m->q2_b, m->sc_in, x.score_in, NJ, D, D, EPI_BIAS, nullptr, 0, nullptr, 0, s));
+    PT_TRY(linf(m, m->q_in, m->q1_w, m->q1_b, m->q1, NJ, x.q_in, D, EPI_BIAS_GELU, nullptr, m->q1a, s));
+    PT_TRY(lin(m, m->q1a, D, m->q2_w, m->q2_b, m->sc_in, x.score_in, NJ, D, D, EPI_BIAS, nullptr, 0, nullptr, 0, s));
     PT_TRY(pt_sc_in_fwd(c, m->h, m->gd, m->sc_in, s));
-    PT_TRY(linf(m->sc_in, m->s1_w, m->s1_b, m->s1, NJ, x.score_in, PT_SC_H, EPI_BIAS_GELU, nullptr, m->s1a, s));
+    PT_TRY(linf(m, m->sc_in, m->s1_w, m->s1_b, m->s1, NJ, x.score_in, PT_SC_H, EPI_BIAS_GELU, nullptr, m->s1a, s));
     PT_TRY(pt_head_dot(m->s1a, NJ, PT_SC_H, m->s2_w, m->s2_b, m->out, NO, NO + 1, 0, s));
     // blind value head: the output value, or (oracle critic) an aux head
     PT_TRY(pt_val_in_fwd(c, m->h, m->gd, m->val_in, s));
-    PT_TRY(linf(m->val_in, m->v1_w, m->v1_b, m->v1, N, x.val_in, PT_VAL_H, EPI_BIAS_GELU, nullptr, m->v1a, s));
+    PT_TRY(linf(m, m->val_in, m->v1_w, m->v1_b, m->v1, N, x.val_in, PT_VAL_H, EPI_BIAS_GELU, nullptr, m->v1a, s));
     if (d.critic == 0) {
         PT_TRY(pt_head_dot(m->v1a, N, PT_VAL_H, m->v2_w, m->v2_b, m->out, 1, NO + 1, NO, s));
     } else {
         if (tr) {   // training only (ptcg_model3.cu:353-363): blind value and belief heads
             PT_TRY(pt_head_dot(m->v1a, N, PT_VAL_H, m->v2_w, m->v2_b, m->bv, 1, 1, 0, s));
-            PT_TRY(linf(m->val_in, m->ah_w, m->ah_b, m->hand_lin, N, x.val_in, d.n_cards, EPI_BIAS, nullptr,
+            PT_TRY(linf(m, m->val_in, m->ah_w, m->ah_b, m->hand_lin, N, x.val_in, d.n_cards, EPI_BIAS, nullptr,
                         nullptr, s));
             PT_TRY(pt_head_dot(m->h, NL, D, m->ap_w, m->ap_b, m->prize_all, 1, 1, 0, s));
         }
         // oracle critic top (ptcg_model3.cu:334-351)
         const int NK = N * x.n_orc;
         PT_TRY(pt_otok_in(c, m->card, m->keep, m->otok_in, m->ckeep, s));
-        PT_TRY(linf(m->otok_in, m->op_w, m->op_b, m->otok, NK, x.orc_in, D, EPI_BIAS, nullptr, nullptr, s));
+        PT_TRY(linf(m, m->otok_in, m->op_w, m->op_b, m->otok, NK, x.orc_in, D, EPI_BIAS, nullptr, nullptr, s));
         PT_TRY(pt_xc_fwd(m->cread, m->h, m->otok, m->xc, N, x.l_seq, x.n_orc, D, s));
         PT_TRY(block_fwd(m, m->cblk, m->cba, x.l_crit, m->ckeep, m->xc, m->xco, s));
         PT_TRY(pt_val_in_fwd(c, m->xco, m->gd, m->ov_in, s, x.l_crit));
-        PT_TRY(linf(m->ov_in, m->ov1_w, m->ov1_b, m->ov1, N, x.val_in, PT_VAL_H, EPI_BIAS_GELU, nullptr, m->ov1a, s));
+        PT_TRY(linf(m, m->ov_in, m->ov1_w, m->ov1_b, m->ov1, N, x.val_in, PT_VAL_H, EPI_BIAS_GELU, nullptr, m->ov1a, s));
         PT_TRY(pt_head_dot(m->ov1a, N, PT_VAL_H, m->ov2_w, m->ov2_b, m->out, 1, NO + 1, NO, s));
     }
     if (out) *out = m->out;
@@ -574,16 +584,16 @@ static int block_bwd(PtcgModel* m, const BlockP& w, const BlockA& a, int L, cons
     const PtcgDims& d = m->dm;
     const int NL = m->N * L, D = d.d;
     PT_TRY(ldw_(m, dA, D, a.ffa, d.ffn, m->G(w.f2w), m->G(w.f2b), NL, d.ffn, D, s));
-    PT_TRY(ldx_(dA, D, w.f2w, m->dffn, d.ffn, NL, d.ffn, D, EPI_GELU_BWD, a.ffp, d.ffn, s));
+    PT_TRY(ldx_(m, dA, D, w.f2w, m->dffn, d.ffn, NL, d.ffn, D, EPI_GELU_BWD, a.ffp, d.ffn, s));
     PT_TRY(ldw_(m, m->dffn, d.ffn, a.ln2, D, m->G(w.f1w), m->G(w.f1b), NL, D, d.ffn, s));
-    PT_TRY(ldx_(m->dffn, d.ffn, w.f1w, m->dln, D, NL, D, d.ffn, EPI_STORE, nullptr, 0, s));
+    PT_TRY(ldx_(m, m->dffn, d.ffn, w.f1w, m->dln, D, NL, D, d.ffn, EPI_STORE, nullptr, 0, s));
     PT_TRY(pt_ln_bwd(m->dln, D, a.xmid, D, w.ln2w, a.mu2, a.rs2, dA, D, dC, D, m->G(w.ln2w),
                      m->G(w.ln2b), NL, D, m->ws, m->ws_floats, s));
     PT_TRY(ldw_(m, dC, D, a.ctx, D, m->G(w.projw), m->G(w.projb), NL, D, D, s));
-    PT_TRY(ldx_(dC, D, w.projw, m->dctx, D, NL, D, D, EPI_STORE, nullptr, 0, s));
+    PT_TRY(ldx_(m, dC, D, w.projw, m->dctx, D, NL, D, D, EPI_STORE, nullptr, 0, s));
     PT_TRY(pt_attn_bwd(a.qkv, keep, a.ctx, a.lse, m->dctx, m->dqkv, m->N, L, d.heads, m->dx.dh, s));
     PT_TRY(ldw_(m, m->dqkv, 3 * D, a.ln1, D, m->G(w.qkvw), m->G(w.qkvb), NL, D, 3 * D, s));
-    PT_TRY(ldx_(m->dqkv, 3 * D, w.qkvw, m->dln, D, NL, D, 3 * D, EPI_STORE, nullptr, 0, s));
+    PT_TRY(ldx_(m, m->dqkv, 3 * D, w.qkvw, m->dln, D, NL, D, 3 * D, EPI_STORE, nullptr, 0, s));
     PT_TRY(pt_ln_bwd(m->dln, D, xin, D, w.ln1w, a.mu1, a.rs1, dC, D, dA, D, m->G(w.ln1w),
                      m->G(w.ln1b), NL, D, m->ws, m->ws_floats, s));
     return PTCG_OK;
@@ -597,11 +607,11 @@ static int tables_bwd(PtcgModel* m, hipStream_t s) {
     const int NC = d.n_cards, NA = d.n_attacks, NS = d.n_skills, DA = d.d_a, DC = d.d_c;
     const int pa = PT_ID_C + PT_CARD_STATIC + PT_CARD_TEXT;
     PT_TRY(ldw_(m, m->d_card_vec, DC, m->card_g1, PT_CARD_H, m->G(m->c3_w), m->G(m->c3_b), NC, PT_CARD_H, DC, s));
-    PT_TRY(ldx_(m->d_card_vec, DC, m->c3_w, m->d_card_h, PT_CARD_H, NC, PT_CARD_H, DC, EPI_GELU_BWD, m->card_h1,
+    PT_TRY(ldx_(m, m->d_card_vec, DC, m->c3_w, m->d_card_h, PT_CARD_H, NC, PT_CARD_H, DC, EPI_GELU_BWD, m->card_h1,
                 PT_CARD_H, s));
     PT_TRY(ldw_(m, m->d_card_h, PT_CARD_H, m->card_ln, x.card_in, m->G(m->c1_w), m->G(m->c1_b), NC, x.card_in,
                 PT_CARD_H, s));
-    PT_TRY(ldx_(m->d_card_h, PT_CARD_H, m->c1_w, m->d_card_ln, x.card_in, NC, x.card_in, PT_CARD_H, EPI_STORE,
+    PT_TRY(ldx_(m, m->d_card_h, PT_CARD_H, m->c1_w, m->d_card_ln, x.card_in, NC, x.card_in, PT_CARD_H, EPI_STORE,
                 nullptr, 0, s));
     PT_TRY(pt_ln_bwd(m->d_card_ln, x.card_in, m->card_in, x.card_in, m->cln_w, m->c_mu, m->c_rs, nullptr, 0,
                      m->d_card_in, x.card_in, m->G(m->cln_w), m->G(m->cln_b), NC, x.card_in, m->ws, m->ws_floats, s));
@@ -612,11 +622,11 @@ static int tables_bwd(PtcgModel* m, hipStream_t s) {
                        NC, DC, m->d_sk_tab, s));
     PT_TRY(pt_gelu_bwd(m->d_att_tab, m->att_lin, m->d_att_lin, (long)NA * DA, s));
     PT_TRY(ldw_(m, m->d_att_lin, DA, m->att_in, x.att_in, m->G(m->am_w), m->G(m->am_b), NA, x.att_in, DA, s));
-    PT_TRY(ldxw_(m->d_att_lin, DA, m->am_w, x.att_in, m->G(m->aid_emb), PT_ID_A, NA, PT_ID_A, DA, EPI_STORE,
+    PT_TRY(ldxw_(m, m->d_att_lin, DA, m->am_w, x.att_in, m->G(m->aid_emb), PT_ID_A, NA, PT_ID_A, DA, EPI_STORE,
                  nullptr, 0, s));
     PT_TRY(pt_gelu_bwd(m->d_sk_tab, m->sk_lin, m->d_sk_lin, (long)NS * DC, s));
     PT_TRY(ldw_(m, m->d_sk_lin, DC, m->sk_in, x.sk_in, m->G(m->sm_w), m->G(m->sm_b), NS, x.sk_in, DC, s));
-    PT_TRY(ldxw_(m->d_sk_lin, DC, m->sm_w, x.sk_in, m->G(m->sid_emb), PT_ID_A, NS, PT_ID_A, DC, EPI_STORE,
+    PT_TRY(ldxw_(m, m->d_sk_lin, DC, m->sm_w, x.sk_in, m->G(m->sid_emb), PT_ID_A, NS, PT_ID_A, DC, EPI_STORE,
                  nullptr, 0, s));
     return PTCG_OK;
 }
@@ -635,11 +645,11 @@ static int critic_bwd(PtcgModel* m, const GatherCtx& c, const float* grad, hipSt
                           m->ws_floats, s));
     PT_TRY(pt_head_dot_bwd(m->d_blind, 1, 1, 0, m->v2_w, m->v1, m->dv1, N, PT_VAL_H, s));
     PT_TRY(ldw_(m, m->dv1, PT_VAL_H, m->val_in, x.val_in, m->G(m->v1_w), m->G(m->v1_b), N, x.val_in, PT_VAL_H, s));
-    PT_TRY(ldx_(m->dv1, PT_VAL_H, m->v1_w, m->dvin, x.val_in, N, x.val_in, PT_VAL_H, EPI_STORE, nullptr, 0, s));
+    PT_TRY(ldx_(m, m->dv1, PT_VAL_H, m->v1_w, m->dvin, x.val_in, N, x.val_in, PT_VAL_H, EPI_STORE, nullptr, 0, s));
     // opp-hand counts (shares the [r | g] input)
     PT_TRY(ldw_(m, m->d_hand, d.n_cards, m->val_in, x.val_in, m->G(m->ah_w), m->G(m->ah_b), N, x.val_in,
                 d.n_cards, s));
-    PT_TRY(ldx_(m->d_hand, d.n_cards, m->ah_w, m->dvin, x.val_in, N, x.val_in, d.n_cards, EPI_ACCUM, nullptr, 0, s));
+    PT_TRY(ldx_(m, m->d_hand, d.n_cards, m->ah_w, m->dvin, x.val_in, N, x.val_in, d.n_cards, EPI_ACCUM, nullptr, 0, s));
     PT_TRY(pt_val_in_bwd(c, m->dvin, m->dxa, m->dgd, s));
     // prize head over the trunk output rows
     PT_TRY(pt_head_dot_dw(m->d_prize, 1, 1, 0, m->h, NL, D, m->G(m->ap_w), m->G(m->ap_b), m->ws, m->ws_floats, s));
@@ -649,14 +659,14 @@ static int critic_bwd(PtcgModel* m, const GatherCtx& c, const float* grad, hipSt
                           m->ws_floats, s));
     PT_TRY(pt_head_dot_bwd(grad, 1, NO + 1, NO, m->ov2_w, m->ov1, m->dov1, N, PT_VAL_H, s));
     PT_TRY(ldw_(m, m->dov1, PT_VAL_H, m->ov_in, x.val_in, m->G(m->ov1_w), m->G(m->ov1_b), N, x.val_in, PT_VAL_H, s));
-    PT_TRY(ldx_(m->dov1, PT_VAL_H, m->ov1_w, m->dovin, x.val_in, N, x.val_in, PT_VAL_H, EPI_STORE, nullptr, 0, s));
+    PT_TRY(ldx_(m, m->dov1, PT_VAL_H, m->ov1_w, m->dovin, x.val_in, N, x.val_in, PT_VAL_H, EPI_STORE, nullptr, 0, s));
     PT_TRY(pt_fill_zero(m->dxc, (long)N * x.l_crit * D, s));
     PT_TRY(pt_val_in_bwd(c, m->dovin, m->dxc, m->dgd, s, x.l_crit));
     PT_TRY(block_bwd(m, m->cblk, m->cba, x.l_crit, m->ckeep, m->xc, m->dxc, m->dxc2, s));
     PT_TRY(pt_colsum(m->dxc, (long)x.l_crit * D, N, D, m->G(m->cread), m->ws, m->ws_floats, s));
     PT_TRY(pt_xc_bwd(m->dxc, m->dxa, m->dotok, N, x.l_seq, x.n_orc, D, s));
     PT_TRY(ldw_(m, m->dotok, D, m->otok_in, x.orc_in, m->G(m->op_w), m->G(m->op_b), NK, x.orc_in, D, s));
-    PT_TRY(ldx_(m->dotok, D, m->op_w, m->dotok_in, x.orc_in, NK, x.orc_in, D, EPI_STORE, nullptr, 0, s));
+    PT_TRY(ldx_(m, m->dotok, D, m->op_w, m->dotok_in, x.orc_in, NK, x.orc_in, D, EPI_STORE, nullptr, 0, s));
     PT_TRY(pt_otok_bwd(c, m->dotok_in, m->dcard, s));
     return PTCG_OK;
 }
@@ -688,7 +698,7 @@ extern "C" int ptcg_model_backward(PtcgModel* m, const float* grad, void* stream
                               m->ws_floats, s));
         PT_TRY(pt_head_dot_bwd(grad, 1, NO + 1, NO, m->v2_w, m->v1, m->dv1, N, PT_VAL_H, s));
         PT_TRY(ldw_(m, m->dv1, PT_VAL_H, m->val_in, x.val_in, m->G(m->v1_w), m->G(m->v1_b), N, x.val_in, PT_VAL_H, s));
-        PT_TRY(ldx_(m->dv1, PT_VAL_H, m->v1_w, m->dvin, x.val_in, N, x.val_in, PT_VAL_H, EPI_STORE, nullptr, 0, s));
+        PT_TRY(ldx_(m, m->dv1, PT_VAL_H, m->v1_w, m->dvin, x.val_in, N, x.val_in, PT_VAL_H, EPI_STORE, nullptr, 0, s));
         PT_TRY(pt_val_in_bwd(c, m->dvin, m->dxa, m->dgd, s));
     }
 
@@ -697,18 +707,18 @@ extern "C" int ptcg_model_backward(PtcgModel* m, const float* grad, void* stream
                           m->ws_floats, s));
     PT_TRY(pt_head_dot_bwd(grad, NO, NO + 1, 0, m->s2_w, m->s1, m->ds1, NJ, PT_SC_H, s));
     PT_TRY(ldw_(m, m->ds1, PT_SC_H, m->sc_in, x.score_in, m->G(m->s1_w), m->G(m->s1_b), NJ, x.score_in, PT_SC_H, s));
-    PT_TRY(ldx_(m->ds1, PT_SC_H, m->s1_w, m->dsc, x.score_in, NJ, x.score_in, PT_SC_H, EPI_STORE, nullptr, 0, s));
+    PT_TRY(ldx_(m, m->ds1, PT_SC_H, m->s1_w, m->dsc, x.score_in, NJ, x.score_in, PT_SC_H, EPI_STORE, nullptr, 0, s));
     PT_TRY(pt_sc_in_bwd(c, m->dsc, m->sc_in, m->dq, m->dxa, m->dgd, s));
     PT_TRY(ldw_(m, m->dq, D, m->q1a, D, m->G(m->q2_w), m->G(m->q2_b), NJ, D, D, s));
-    PT_TRY(ldx_(m->dq, D, m->q2_w, m->dq1, D, NJ, D, D, EPI_GELU_BWD, m->q1, D, s));
+    PT_TRY(ldx_(m, m->dq, D, m->q2_w, m->dq1, D, NJ, D, D, EPI_GELU_BWD, m->q1, D, s));
     PT_TRY(ldw_(m, m->dq1, D, m->q_in, x.q_in, m->G(m->q1_w), m->G(m->q1_b), NJ, x.q_in, D, s));
-    PT_TRY(ldx_(m->dq1, D, m->q1_w, m->dqin, x.q_in, NJ, x.q_in, D, EPI_STORE, nullptr, 0, s));
+    PT_TRY(ldx_(m, m->dq1, D, m->q1_w, m->dqin, x.q_in, NJ, x.q_in, D, EPI_STORE, nullptr, 0, s));
     PT_TRY(pt_q_in_bwd(c, m->dqin, m->dxa, m->G(m->temb), s));
     const int oc0 = PT_TYPE_E + 2 * D, oa0 = oc0 + PT_OPT_E;
     PT_TRY(ldw_(m, m->dqin + oc0, x.q_in, m->ocard, d.d_c, m->G(m->oc_w), m->G(m->oc_b), NJ, d.d_c, PT_OPT_E, s));
-    PT_TRY(ldx_(m->dqin + oc0, x.q_in, m->oc_w, m->docard, d.d_c, NJ, d.d_c, PT_OPT_E, EPI_STORE, nullptr, 0, s));
+    PT_TRY(ldx_(m, m->dqin + oc0, x.q_in, m->oc_w, m->docard, d.d_c, NJ, d.d_c, PT_OPT_E, EPI_STORE, nullptr, 0, s));
     PT_TRY(ldw_(m, m->dqin + oa0, x.q_in, m->oatt, d.d_a, m->G(m->oa_w), m->G(m->oa_b), NJ, d.d_a, PT_OPT_E, s));
-    PT_TRY(ldx_(m->dqin + oa0, x.q_in, m->oa_w, m->doatt, d.d_a, NJ, d.d_a, PT_OPT_E, EPI_STORE, nullptr, 0, s));
+    PT_TRY(ldx_(m, m->dqin + oa0, x.q_in, m->oa_w, m->doatt, d.d_a, NJ, d.d_a, PT_OPT_E, EPI_STORE, nullptr, 0, s));
     PT_TRY(pt_opt_gather_bwd(c, m->docard, m->doatt, m->dcard, m->datt, s));
 
     // final LayerNorm, then the trunk in reverse (d_x in dxb, scratch dxa)
@@ -721,19 +731,19 @@ extern "C" int ptcg_model_backward(PtcgModel* m, const float* grad, void* stream
     PT_TRY(pt_x0_bwd(c, m->dxb, m->dtokp, m->dbc, s));
     PT_TRY(pt_colsum(m->dxb, (long)x.l_seq * D, N, D, m->G(m->readout), m->ws, m->ws_floats, s));
     PT_TRY(ldw_(m, m->dtokp, D, m->tok_cat, x.tok_in, m->G(m->tp_w), m->G(m->tp_b), N * Lt, x.tok_in, D, s));
-    PT_TRY(ldx_(m->dtokp, D, m->tp_w, m->dtokcat, x.tok_in, N * Lt, x.tok_in, D, EPI_STORE, nullptr, 0, s));
+    PT_TRY(ldx_(m, m->dtokp, D, m->tp_w, m->dtokcat, x.tok_in, N * Lt, x.tok_in, D, EPI_STORE, nullptr, 0, s));
     PT_TRY(pt_tok_cat_bwd(c, m->dtokcat, m->dcard, m->G(m->zemb), m->G(m->oemb), s));
     PT_TRY(ldw_(m, m->dbc, D, m->gd, x.bcast_in, m->G(m->bc_w), m->G(m->bc_b), N, x.bcast_in, D, s));
-    PT_TRY(ldx_(m->dbc, D, m->bc_w, m->dgd, x.bcast_in, N, x.bcast_in, D, EPI_ACCUM, nullptr, 0, s));
+    PT_TRY(ldx_(m, m->dbc, D, m->bc_w, m->dgd, x.bcast_in, N, x.bcast_in, D, EPI_ACCUM, nullptr, 0, s));
     // decision MLP (d_dvec = dgd[:, G:])
     PT_TRY(ldw_(m, m->dgd + G, x.bcast_in, m->d1a, PT_DEC_H, m->G(m->d2_w), m->G(m->d2_b), N, PT_DEC_H, PT_DEC_H, s));
-    PT_TRY(ldx_(m->dgd + G, x.bcast_in, m->d2_w, m->dd1, PT_DEC_H, N, PT_DEC_H, PT_DEC_H, EPI_GELU_BWD, m->d1, PT_DEC_H, s));
+    PT_TRY(ldx_(m, m->dgd + G, x.bcast_in, m->d2_w, m->dd1, PT_DEC_H, N, PT_DEC_H, PT_DEC_H, EPI_GELU_BWD, m->d1, PT_DEC_H, s));
     PT_TRY(ldw_(m, m->dd1, PT_DEC_H, m->dec_in, x.dec_in, m->G(m->d1_w), m->G(m->d1_b), N, x.dec_in, PT_DEC_H, s));
-    PT_TRY(ldx_(m->dd1, PT_DEC_H, m->d1_w, m->ddec, x.dec_in, N, x.dec_in, PT_DEC_H, EPI_STORE, nullptr, 0, s));
+    PT_TRY(ldx_(m, m->dd1, PT_DEC_H, m->d1_w, m->ddec, x.dec_in, N, x.dec_in, PT_DEC_H, EPI_STORE, nullptr, 0, s));
     PT_TRY(pt_dec_in_bwd(c, m->ddec, m->dcard, m->datt, m->G(m->semb), m->G(m->cemb), s));
     // global MLP (d_g = dgd[:, :G])
     PT_TRY(ldw_(m, m->dgd, x.bcast_in, m->g1a, G, m->G(m->g2_w), m->G(m->g2_b), N, G, G, s));
-    PT_TRY(ldx_(m->dgd, x.bcast_in, m->g2_w, m->dg1, G, N, G, G, EPI_GELU_BWD, m->g1, G, s));
+    PT_TRY(ldx_(m, m->dgd, x.bcast_in, m->g2_w, m->dg1, G, N, G, G, EPI_GELU_BWD, m->g1, G, s));
     PT_TRY(ldw_(m, m->dg1, G, m->glob_in, d.global_f, m->G(m->g1_w), m->G(m->g1_b), N, d.global_f, G, s));
     if (d.tables == 1) PT_TRY(tables_bwd(m, s));
     return PTCG_OK;

@@ -52,6 +52,8 @@ _SIGS = {
                                            c_void_p, c_void_p, c_void_p]),
     "ptcg_trainer_rollout": (ctypes.c_int, [c_void_p, c_void_p, c_void_p, ctypes.c_int, ctypes.c_uint64,
                                             ctypes.c_uint64, c_void_p, c_void_p, c_void_p, c_void_p]),
+    "ptcg_model_set_precision": (ctypes.c_int, [c_void_p, ctypes.c_int]),
+    "ptcg_trainer_set_precision": (ctypes.c_int, [c_void_p, ctypes.c_int]),
     "ptcg_model_free": (None, [c_void_p]),
     "ptcg_ppo_loss_fwd_bwd": (ctypes.c_int, [
         c_void_p, ctypes.c_int, ctypes.c_int, c_void_p, ctypes.c_int64, c_void_p,
@@ -94,6 +96,11 @@ _SIGS = {
     "ptcg_profile_end": (ctypes.c_int, [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_int),
                                         ctypes.POINTER(ctypes.c_double)]),
     "ptcg_kernel_gemm": (ctypes.c_int, [
+        ctypes.c_int, ctypes.c_int, ctypes.c_int, c_void_p, ctypes.c_int64, ctypes.c_int,
+        c_void_p, ctypes.c_int64, ctypes.c_int, c_void_p, ctypes.c_int64, ctypes.c_int,
+        c_void_p, c_void_p, ctypes.c_int64, c_void_p, ctypes.c_int64, c_void_p,
+        ctypes.c_int64, c_void_p]),
+    "ptcg_kernel_gemm_bf16": (ctypes.c_int, [
         ctypes.c_int, ctypes.c_int, ctypes.c_int, c_void_p, ctypes.c_int64, ctypes.c_int,
         c_void_p, ctypes.c_int64, ctypes.c_int, c_void_p, ctypes.c_int64, ctypes.c_int,
         c_void_p, c_void_p, ctypes.c_int64, c_void_p, ctypes.c_int64, c_void_p,

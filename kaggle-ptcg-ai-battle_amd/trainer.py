@@ -177,13 +177,18 @@ class PuffeRL:
 def create_pufferl(args):
     """args: {"dims": PtcgDims | dict, "train": {...}, "seed": int,
     "init_weights": packed blob | None, "static": static tables (static-table
-    models)}.  Unknown dims keys raise."""
+    models), "precision": "fp32" | "bf16" (GEMM products)}.  Unknown dims keys
+    raise."""
     dm = args.get("dims", dims_mod.CORE)
     if isinstance(dm, dict):
         dm = dims_mod.PtcgDims(**dm)
     pl = PuffeRL(dm, args.get("train", {}), args.get("seed", 0))
     if args.get("static") is not None:
         pl.set_static(args["static"])
+    prec = args.get("precision", "fp32")
+    if prec not in ("fp32", "bf16"):
+        raise ValueError(f"precision must be 'fp32' or 'bf16', got {prec!r}")
+    check(lib().ptcg_trainer_set_precision(pl._h, 1 if prec == "bf16" else 0))
     init = args.get("init_weights")
     if init is None:
         from .params import init_blob

@@ -338,3 +338,53 @@ def test_adam_first_step_is_lr_sign(cuda):
     # first Adam step in closed form: m_hat = g, v_hat = g^2
     g64 = g.astype(np.float64)
     assert np.allclose(d, -1e-3 * g64 / (np.abs(g64) + 1e-8), rtol=1e-4, atol=2e-10)
+
+
+def _bf16(t):
+    return t.to(torch.bfloat16).to(torch.float64)
+
+
+BF16_CASES = [(37, 52, 300, 0, 0, 1), (130, 68, 64, 0, 0, 2), (256, 256, 256, 0, 0, 3), (200, 96, 40, 0, 1, 4),
+              (64, 300, 256, 0, 1, 0), (768, 256, 20000, 1, 1, 0), (96, 36, 12, 1, 0, 0), (129, 132, 132, 0, 1, 5),
+              (4096, 1024, 256, 0, 0, 2), (4096, 256, 1024, 0, 1, 0)]
+
+
+@pytest.mark.parametrize("case", BF16_CASES, ids=lambda c: "M%d_N%d_K%d_at%d_bt%d_e%d" % c)
+def test_gemm_bf16_products(case, cuda):
+    """bf16 operands (round to nearest even), fp32 accumulation: equals the
+    fp64 product of the bf16-rounded operands to fp32-accumulation accuracy."""
+    M, N, K, a_t, b_t, epi = case
+    g = torch.Generator().manual_seed(M + N + K)
+    A = torch.randn(K, M, generator=g) if a_t else torch.randn(M, K, generator=g)
+    B = torch.randn(K, N, generator=g) if b_t else torch.randn(N, K, generator=g)
+    bias = torch.randn(N, generator=g)
+    R = torch.randn(M, N, generator=g)
+    C0 = torch.randn(M, N, generator=g)
+    Am = _bf16(A.T if a_t else A)
+    Bm = _bf16(B if b_t else B.T)
+    acc = Am @ Bm
+    ref2 = None
+    if epi == 0: ref = acc
+    elif epi == 1: ref = acc + bias.double()
+    elif epi == 2:
+        ref = acc + bias.double()
+        ref2 = gelu(ref)
+    elif epi == 3: ref = acc + bias.double() + R.double()
+    elif epi == 4: ref = acc * gelu_grad(R.double())
+    else: ref = C0.double() + acc
+    dA, dB, dbias, dR = dev(A), dev(B), dev(bias), dev(R)
+    dC = dev(C0) if epi == 5 else empty(M, N)
+    dC2 = empty(M, N)
+    ws = empty(32 << 20)
+    native.check(native.lib().ptcg_kernel_gemm_bf16(M, N, K, P(dA), M if a_t else K, a_t, P(dB), N if b_t else K, b_t,
+                                                    P(dC), N, epi, P(dbias), P(dR), N, P(dC2), N, P(ws), ws.numel(),
+                                                    None))
+    torch.cuda.synchronize()
+    got = dC.cpu().double()
+    assert rel_l2(got, ref) < 1e-5, rel_l2(got, ref)
+    if ref2 is not None:
+        assert rel_l2(dC2.cpu().double(), ref2) < 1e-5
+    # and it is a bf16 product, not the fp32 one
+    exact = (A.T if a_t else A).double() @ (B if b_t else B.T).double()
+    if epi == 0:
+        assert rel_l2(got, exact) > 1e-4

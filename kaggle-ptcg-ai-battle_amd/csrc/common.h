@@ -111,6 +111,10 @@ struct GemmArgs {
     // 0: fp32 products (v_mfma_f32_16x16x4_f32); 1: operands rounded to bf16
     // on the way into LDS, fp32 accumulation (v_mfma_f32_16x16x32_bf16)
     int prec;
+    // set by pt_gemm: a launch covers logical tiles [tile0, tile0 + ntiles)
+    // (ntiles 0 = all); tail_part: split-K partials of those tiles go to a
+    // tile-local workspace [split][tile][128 x 128]
+    int tile0, ntiles, tail_part;
 };
 
 // Launch C = epi(A*B) on `stream`. Requirements: K % 4 == 0 when the operand

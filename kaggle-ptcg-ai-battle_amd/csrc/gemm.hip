@@ -40,6 +40,35 @@ __device__ __forceinline__ void tile_of(int b, int tiles, int tn, int& tm_i, int
     tm_i = lb / tn;
     tn_i = lb % tn;
 }
+// the launch's logical tile range [g.tile0, g.tile0 + count)
+__device__ __forceinline__ void tile_of_range(const GemmArgs& g, int tm, int tn, int& tm_i, int& tn_i) {
+    const int count = g.ntiles ? g.ntiles : tm * tn;
+    int lb = blockIdx.x;
+    if ((count & 7) == 0) lb = (lb & 7) * (count >> 3) + (lb >> 3);
+    lb += g.tile0;
+    tm_i = lb / tn;
+    tn_i = lb % tn;
+}
+
+// one output element through the epilogue
+template <int EPI>
+__device__ __forceinline__ void epi_store(const GemmArgs& g, int m, int n, float v) {
+    if (EPI == EPI_STORE) {
+        g.C[(long)m * g.ldc + n] = v;
+    } else if (EPI == EPI_BIAS) {
+        g.C[(long)m * g.ldc + n] = v + g.bias[n];
+    } else if (EPI == EPI_BIAS_GELU) {
+        v += g.bias[n];
+        g.C[(long)m * g.ldc + n] = v;
+        g.C2[(long)m * g.ldc2 + n] = pt_gelu(v);
+    } else if (EPI == EPI_BIAS_RESID) {
+        g.C[(long)m * g.ldc + n] = v + g.bias[n] + g.R[(long)m * g.ldr + n];
+    } else if (EPI == EPI_GELU_BWD) {
+        g.C[(long)m * g.ldc + n] = v * pt_gelu_grad(g.R[(long)m * g.ldr + n]);
+    } else if (EPI == EPI_ACCUM) {
+        g.C[(long)m * g.ldc + n] += v;
+    }
+}
 
 // Operand load of 4 consecutive floats along the contiguous dimension for
 // shapes that break the 128-bit rules (a width or leading dimension not a
@@ -71,6 +100,20 @@ __device__ __forceinline__ float4 ld_scalar4(const gfloat* X, long ld, int lim, 
 template <int EPI, bool PARTIAL>
 __device__ __forceinline__ void gemm_epilogue(const GemmArgs& g, floatx4 (&acc)[4][4], int m0, int n0, int wm,
                                               int wn, int li, int lq, long part_stride) {
+    if (PARTIAL && g.tail_part) {
+        // tile-local partial [split][tile - tile0][BM][BN] (no bounds: the reduce masks)
+        const int tn = (g.N + BN - 1) / BN;
+        const long t = (long)(m0 / BM) * tn + n0 / BN - g.tile0;
+        float* P = g.C + ((long)blockIdx.z * g.ntiles + t) * (BM * BN);
+#pragma unroll
+        for (int ti = 0; ti < 4; ++ti)
+#pragma unroll
+            for (int tj = 0; tj < 4; ++tj)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    P[(wm + ti * 16 + lq * 4 + r) * BN + wn + tj * 16 + li] = acc[ti][tj][r];
+        return;
+    }
     const long zoff = PARTIAL ? (long)blockIdx.z * part_stride : 0;
 #pragma unroll
     for (int ti = 0; ti < 4; ++ti)
@@ -78,31 +121,12 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& g, floatx4 (&acc)[
         for (int tj = 0; tj < 4; ++tj) {
             const int n = n0 + wn + tj * 16 + li;
             if (n >= g.N) continue;
-            float bn = 0.f;
-            if (!PARTIAL && (EPI == EPI_BIAS || EPI == EPI_BIAS_GELU || EPI == EPI_BIAS_RESID))
-                bn = g.bias[n];
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int m = m0 + wm + ti * 16 + lq * 4 + r;
                 if (m >= g.M) continue;
-                float v = acc[ti][tj][r];
-                if (PARTIAL) {
-                    g.C[zoff + (long)m * g.ldc + n] = v;
-                } else if (EPI == EPI_STORE) {
-                    g.C[(long)m * g.ldc + n] = v;
-                } else if (EPI == EPI_BIAS) {
-                    g.C[(long)m * g.ldc + n] = v + bn;
-                } else if (EPI == EPI_BIAS_GELU) {
-                    v += bn;
-                    g.C[(long)m * g.ldc + n] = v;
-                    g.C2[(long)m * g.ldc2 + n] = pt_gelu(v);
-                } else if (EPI == EPI_BIAS_RESID) {
-                    g.C[(long)m * g.ldc + n] = v + bn + g.R[(long)m * g.ldr + n];
-                } else if (EPI == EPI_GELU_BWD) {
-                    g.C[(long)m * g.ldc + n] = v * pt_gelu_grad(g.R[(long)m * g.ldr + n]);
-                } else if (EPI == EPI_ACCUM) {
-                    g.C[(long)m * g.ldc + n] += v;
-                }
+                if (PARTIAL) g.C[zoff + (long)m * g.ldc + n] = acc[ti][tj][r];
+                else epi_store<EPI>(g, m, n, acc[ti][tj][r]);
             }
         }
 }
@@ -118,7 +142,7 @@ __global__ __launch_bounds__(NT) void gemm_f32_kernel(GemmArgs g, int k_chunk, l
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int tm = (g.M + BM - 1) / BM, tn = (g.N + BN - 1) / BN;
     int tmi, tni;
-    tile_of(blockIdx.x, tm * tn, tn, tmi, tni);
+    tile_of_range(g, tm, tn, tmi, tni);
     const int m0 = tmi * BM, n0 = tni * BN;
     const int kbeg = blockIdx.z * k_chunk;
     const int kend = min(g.K, kbeg + k_chunk);
@@ -283,7 +307,7 @@ __global__ __launch_bounds__(NT) void gemm_bf16_kernel(GemmArgs g, int k_chunk, 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int tm = (g.M + BM - 1) / BM, tn = (g.N + BN - 1) / BN;
     int tmi, tni;
-    tile_of(blockIdx.x, tm * tn, tn, tmi, tni);
+    tile_of_range(g, tm, tn, tmi, tni);
     const int m0 = tmi * BM, n0 = tni * BN;
     const int kbeg = blockIdx.z * k_chunk;
     const int kend = min(g.K, kbeg + k_chunk);
@@ -353,6 +377,21 @@ __global__ void splitk_reduce_kernel(float* C, long ldc, const float* part, long
     float s = 0.f;
     for (int k = 0; k < splits; ++k) s += part[(long)k * part_stride + o];
     if (ACCUM) C[o] += s; else C[o] = s;
+}
+
+// Tail tiles of a balanced launch: C[tile] = epi(sum_s part[s][tile]), fixed order over s.
+template <int EPI>
+__global__ void tail_reduce_kernel(GemmArgs g, const float* __restrict__ part, int splits) {
+    const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (long)g.ntiles * BM * BN) return;
+    const int t = (int)(i / (BM * BN)), e = (int)(i % (BM * BN));
+    const int tn = (g.N + BN - 1) / BN;
+    const int lt = g.tile0 + t;
+    const int m = (lt / tn) * BM + e / BN, n = (lt % tn) * BN + e % BN;
+    if (m >= g.M || n >= g.N) return;
+    float v = 0.f;
+    for (int z = 0; z < splits; ++z) v += part[((long)z * g.ntiles + t) * (BM * BN) + e];
+    epi_store<EPI>(g, m, n, v);
 }
 
 // Deterministic column sums in two levels.  Level 1: block (64 columns x 4
@@ -510,6 +549,19 @@ extern "C" int ptcg_profile_end(double* total_ms, int* launches, double* flops) 
     return PTCG_OK;
 }
 
+// compute units of the current device (cached per device)
+static int pt_cu_count() {
+    static int cache[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+    if (!cache[dev]) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+        cache[dev] = n;
+    }
+    return cache[dev];
+}
+
 int pt_gemm(const GemmArgs& g, float* ws, long ws_floats, hipStream_t s) {
     PT_REQUIRE(g.M > 0 && g.N > 0 && g.K > 0, "gemm: empty shape %d x %d x %d", g.M, g.N, g.K);
     PT_REQUIRE(g.A && g.B && g.C, "gemm: null operand");
@@ -568,6 +620,53 @@ int pt_gemm(const GemmArgs& g, float* ws, long ws_floats, hipStream_t s) {
                                g.C, g.ldc, ws, part_stride, splits, g.M, g.N, db ? g.dbias : nullptr);
         PT_LAUNCH_CHECK();
         return PTCG_OK;
+    }
+    // Balance the last wave: with T tiles on S CUs, T % S tail tiles would run
+    // as a partial wave (e.g. 776 tiles = 3.03 per CU: the CUs holding 4 set
+    // the time).  Run the first T - T % S tiles whole and split the tail's K
+    // across the idle CUs, then reduce the tail partials in a fixed order.
+    if (!db && ws != nullptr) {
+        const int S = pt_cu_count();
+        const int R = S > 0 ? tiles % S : 0;
+        const int ksteps = pt_cdiv(g.K, bk);
+        int s2 = R ? S / R : 0;
+        if (s2 > ksteps / 2) s2 = ksteps / 2;
+        if (tiles > S && R != 0 && s2 >= 2 && (long)s2 * R * BM * BN <= ws_floats) {
+            const int kc = pt_cdiv(pt_cdiv(g.K, s2), bk) * bk;
+            s2 = pt_cdiv(g.K, kc);
+            GemmArgs a = g;
+            a.tile0 = 0;
+            a.ntiles = tiles - R;
+            const dim3 ga(tiles - R, 1, 1);
+            if (bf) PT_TRY(launch_bf16_any(a, ga, g.K, 0, false, s));
+            else PT_TRY(vec ? launch_full<true>(a, false, ga, g.K, s) : launch_full<false>(a, false, ga, g.K, s));
+            PT_LAUNCH_CHECK();
+            GemmArgs p = g;
+            p.C = ws;
+            p.tile0 = tiles - R;
+            p.ntiles = R;
+            p.tail_part = 1;
+            const dim3 gp(R, 1, s2);
+            if (bf) PT_TRY(launch_bf16_any(p, gp, kc, 0, true, s));
+            else if (vec) launch_partial<true>(p, false, gp, kc, 0, s);
+            else launch_partial<false>(p, false, gp, kc, 0, s);
+            PT_LAUNCH_CHECK();
+            GemmArgs t = g;
+            t.tile0 = tiles - R;
+            t.ntiles = R;
+            const dim3 gr(pt_cdiv((long)R * BM * BN, 256));
+            switch (g.epi) {
+                case EPI_STORE: hipLaunchKernelGGL(tail_reduce_kernel<EPI_STORE>, gr, dim3(256), 0, s, t, ws, s2); break;
+                case EPI_BIAS: hipLaunchKernelGGL(tail_reduce_kernel<EPI_BIAS>, gr, dim3(256), 0, s, t, ws, s2); break;
+                case EPI_BIAS_GELU: hipLaunchKernelGGL(tail_reduce_kernel<EPI_BIAS_GELU>, gr, dim3(256), 0, s, t, ws, s2); break;
+                case EPI_BIAS_RESID: hipLaunchKernelGGL(tail_reduce_kernel<EPI_BIAS_RESID>, gr, dim3(256), 0, s, t, ws, s2); break;
+                case EPI_GELU_BWD: hipLaunchKernelGGL(tail_reduce_kernel<EPI_GELU_BWD>, gr, dim3(256), 0, s, t, ws, s2); break;
+                case EPI_ACCUM: hipLaunchKernelGGL(tail_reduce_kernel<EPI_ACCUM>, gr, dim3(256), 0, s, t, ws, s2); break;
+                default: PT_REQUIRE(false, "gemm: bad epilogue %d", g.epi);
+            }
+            PT_LAUNCH_CHECK();
+            return PTCG_OK;
+        }
     }
     if (bf) PT_TRY(launch_bf16_any(g, grid, k_chunk, 0, false, s));
     else PT_TRY(vec ? launch_full<true>(g, db, grid, k_chunk, s) : launch_full<false>(g, db, grid, k_chunk, s));

@@ -102,7 +102,7 @@ static int lin(const PtcgModel* m, const float* X, long ldx, const float* W, con
     g.C = Y; g.ldc = ldy;
     g.bias = b; g.R = R; g.ldr = ldr; g.C2 = Y2; g.ldc2 = ldy2;
     g.epi = epi;
-    return pt_gemm(g, nullptr, 0, s);
+    return pt_gemm(g, m->ws, m->ws_floats, s);
 }
 static int linf(const PtcgModel* m, const float* X, const float* W, const float* b, float* Y, int rows, int in,
                 int out, int epi, const float* R, float* Y2, hipStream_t s) {
@@ -119,7 +119,7 @@ static int ldxw_(const PtcgModel* m, const float* dY, long lddy, const float* W,
     g.C = dX; g.ldc = lddx;
     g.R = R; g.ldr = ldr;
     g.epi = epi;
-    return pt_gemm(g, nullptr, 0, s);
+    return pt_gemm(g, m->ws, m->ws_floats, s);
 }
 // dX = dY W : dY (rows, out) ld lddy ; W (out, in) ; dX (rows, in) ld lddx
 static int ldx_(const PtcgModel* m, const float* dY, long lddy, const float* W, float* dX, long lddx, int rows,
@@ -400,9 +400,9 @@ static size_t carve(PtcgModel* m, char* base) {
             m->aux_cnt = reinterpret_cast<int*>(c.take(64));
         }
     }
-    if (!train) {   // forward GEMMs and LayerNorms need no workspace
-        m->ws_floats = 0;
-        m->ws = nullptr;
+    if (!train) {   // forward GEMMs use the workspace for balanced tail tiles only
+        m->ws_floats = 4L << 20;
+        m->ws = c.take(m->ws_floats);
         return c.off;
     }
     // backward scratch (block scratch sized for the longer of trunk and critic)

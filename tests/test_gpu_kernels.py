@@ -51,6 +51,10 @@ GEMM_CASES = [
     # 127-wide attack input, 634-wide card input, 134-wide oracle token input)
     (1573, 64, 127, 0, 0, 2), (1284, 634, 256, 0, 1, 0), (300, 256, 134, 0, 0, 1),
     (64, 127, 1573, 1, 1, 0), (45, 33, 17, 1, 0, 5), (256, 634, 20000, 1, 1, 0),
+    # more tiles than compute units with a small remainder: the balanced launch
+    # (whole tiles + a split-K tail reduced through the epilogue)
+    (34000, 256, 256, 0, 0, 2), (33000, 384, 256, 0, 1, 4), (33024, 256, 512, 0, 0, 5),
+    (33100, 256, 256, 0, 0, 3),
 ]
 
 
@@ -346,7 +350,7 @@ def _bf16(t):
 
 BF16_CASES = [(37, 52, 300, 0, 0, 1), (130, 68, 64, 0, 0, 2), (256, 256, 256, 0, 0, 3), (200, 96, 40, 0, 1, 4),
               (64, 300, 256, 0, 1, 0), (768, 256, 20000, 1, 1, 0), (96, 36, 12, 1, 0, 0), (129, 132, 132, 0, 1, 5),
-              (4096, 1024, 256, 0, 0, 2), (4096, 256, 1024, 0, 1, 0)]
+              (4096, 1024, 256, 0, 0, 2), (4096, 256, 1024, 0, 1, 0), (34000, 256, 256, 0, 0, 2)]
 
 
 @pytest.mark.parametrize("case", BF16_CASES, ids=lambda c: "M%d_N%d_K%d_at%d_bt%d_e%d" % c)

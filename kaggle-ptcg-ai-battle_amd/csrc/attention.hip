@@ -33,7 +33,7 @@ namespace {
 template <int DH, int NT>   // NT = Lp / 16 key (and query) tiles
 __global__ __launch_bounds__(512) void attn_fwd_mfma_kernel(const float* __restrict__ qkv,
         const float* __restrict__ keep, float* __restrict__ ctx, float* __restrict__ lse,
-        int L, int H, float scale) {
+        int Lfix, int H, float scale, const int* __restrict__ coff) {
     constexpr int LP = NT * 16, SK = DH + 4;
     extern __shared__ float sm[];
     float* Ks = sm;                 // [LP][SK]
@@ -42,8 +42,11 @@ __global__ __launch_bounds__(512) void attn_fwd_mfma_kernel(const float* __restr
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int li = lane & 15, lq = lane >> 4;
     const int n = blockIdx.x / H, h = blockIdx.x % H;
+    // rows of sample n: [rb, rb + L) (compact layout) or [n*Lfix, (n+1)*Lfix)
+    const long rb = coff ? (long)coff[n] : (long)n * Lfix;
+    const int L = coff ? coff[n + 1] - coff[n] : Lfix;
     const int D = H * DH;
-    const gfloat* base = (const gfloat*)qkv + (long)n * L * 3 * D + h * DH;
+    const gfloat* base = (const gfloat*)qkv + rb * 3 * D + h * DH;
     for (int idx = tid; idx < LP * (DH / 4); idx += 512) {
         const int l = idx / (DH / 4), c4 = (idx % (DH / 4)) * 4;
         float4 k4 = make_float4(0.f, 0.f, 0.f, 0.f), v4 = k4;
@@ -55,7 +58,7 @@ __global__ __launch_bounds__(512) void attn_fwd_mfma_kernel(const float* __restr
         *reinterpret_cast<float4*>(&Ks[l * SK + c4]) = k4;
         *reinterpret_cast<float4*>(&Vs[l * SK + c4]) = v4;
     }
-    for (int l = tid; l < LP; l += 512) kf[l] = l < L ? (keep[(long)n * L + l] != 0.f ? 1.f : 0.f) : -1.f;
+    for (int l = tid; l < LP; l += 512) kf[l] = l < L ? (keep[rb + l] != 0.f ? 1.f : 0.f) : -1.f;
     __syncthreads();
 
     for (int st = wave; st < NT; st += 8) {
@@ -143,12 +146,12 @@ __global__ __launch_bounds__(512) void attn_fwd_mfma_kernel(const float* __restr
             const float inv = 1.0f / __shfl(sum, 4 * lq + r, 64);
             const int q = q0 + 4 * lq + r;
             if (q < L) {
-                gfloat* dst = (gfloat*)ctx + ((long)n * L + q) * D + h * DH + li;
+                gfloat* dst = (gfloat*)ctx + (rb + q) * D + h * DH + li;
 #pragma unroll
                 for (int dt = 0; dt < DH / 16; ++dt) dst[16 * dt] = o[dt][r] * inv;
             }
         }
-        if (lq == 0 && qv) lse[((long)n * H + h) * L + q0 + li] = mx + logf(sum);
+        if (lq == 0 && qv) lse[((long)n * H + h) * Lfix + q0 + li] = mx + logf(sum);
     }
 }
 
@@ -161,7 +164,7 @@ template <int DH, int NT>
 __global__ __launch_bounds__(512) void attn_bwd_mfma_kernel(const float* __restrict__ qkv,
         const float* __restrict__ keep, const float* __restrict__ ctx,
         const float* __restrict__ lse, const float* __restrict__ dctx,
-        float* __restrict__ dqkv, int L, int H, float scale) {
+        float* __restrict__ dqkv, int Lfix, int H, float scale, const int* __restrict__ coff) {
     constexpr int LP = NT * 16, SQ = DH + 4, SKB = DH + 16, SS = LP + 4;
     extern __shared__ float sm[];
     float* Qs = sm;                 // [LP][SQ]
@@ -174,11 +177,14 @@ __global__ __launch_bounds__(512) void attn_bwd_mfma_kernel(const float* __restr
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int li = lane & 15, lq = lane >> 4;
     const int n = blockIdx.x / H, h = blockIdx.x % H;
+    // rows of sample n: [rb, rb + L) (compact layout) or [n*Lfix, (n+1)*Lfix)
+    const long rb = coff ? (long)coff[n] : (long)n * Lfix;
+    const int L = coff ? coff[n + 1] - coff[n] : Lfix;
     const int D = H * DH;
-    const gfloat* base = (const gfloat*)qkv + (long)n * L * 3 * D + h * DH;
-    const gfloat* ob = (const gfloat*)ctx + (long)n * L * D + h * DH;
-    const gfloat* dob = (const gfloat*)dctx + (long)n * L * D + h * DH;
-    gfloat* gb = (gfloat*)dqkv + (long)n * L * 3 * D + h * DH;
+    const gfloat* base = (const gfloat*)qkv + rb * 3 * D + h * DH;
+    const gfloat* ob = (const gfloat*)ctx + rb * D + h * DH;
+    const gfloat* dob = (const gfloat*)dctx + rb * D + h * DH;
+    gfloat* gb = (gfloat*)dqkv + rb * 3 * D + h * DH;
     for (int idx = tid; idx < LP * (DH / 4); idx += 512) {
         const int l = idx / (DH / 4), c4 = (idx % (DH / 4)) * 4;
         float4 q4 = make_float4(0.f, 0.f, 0.f, 0.f), k4 = q4, d4 = q4;
@@ -193,8 +199,8 @@ __global__ __launch_bounds__(512) void attn_bwd_mfma_kernel(const float* __restr
         *reinterpret_cast<float4*>(&Ks[l * SKB + c4]) = k4;
     }
     for (int l = tid; l < LP; l += 512) {
-        kf[l] = l < L ? (keep[(long)n * L + l] != 0.f ? 1.f : 0.f) : 0.f;
-        ls[l] = l < L ? lse[((long)n * H + h) * L + l] : INFINITY;
+        kf[l] = l < L ? (keep[rb + l] != 0.f ? 1.f : 0.f) : 0.f;
+        ls[l] = l < L ? lse[((long)n * H + h) * Lfix + l] : INFINITY;
     }
     // Dv[q] = sum_d dO[q][d] O[q][d]   (a wave per row; padded rows 0)
     for (int q = wave; q < LP; q += 8) {
@@ -300,7 +306,7 @@ template <int DH, int NT>
 __global__ __launch_bounds__(512) void attn_bwd_mfma_rc_kernel(const float* __restrict__ qkv,
         const float* __restrict__ keep, const float* __restrict__ ctx,
         const float* __restrict__ lse, const float* __restrict__ dctx,
-        float* __restrict__ dqkv, int L, int H, float scale) {
+        float* __restrict__ dqkv, int Lfix, int H, float scale, const int* __restrict__ coff) {
     constexpr int LP = NT * 16, SQ = DH + 4;
     extern __shared__ float sm[];
     float* Qs = sm;                 // [LP][SQ]
@@ -313,11 +319,14 @@ __global__ __launch_bounds__(512) void attn_bwd_mfma_rc_kernel(const float* __re
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int li = lane & 15, lq = lane >> 4;
     const int n = blockIdx.x / H, h = blockIdx.x % H;
+    // rows of sample n: [rb, rb + L) (compact layout) or [n*Lfix, (n+1)*Lfix)
+    const long rb = coff ? (long)coff[n] : (long)n * Lfix;
+    const int L = coff ? coff[n + 1] - coff[n] : Lfix;
     const int D = H * DH;
-    const gfloat* base = (const gfloat*)qkv + (long)n * L * 3 * D + h * DH;
-    const gfloat* ob = (const gfloat*)ctx + (long)n * L * D + h * DH;
-    const gfloat* dob = (const gfloat*)dctx + (long)n * L * D + h * DH;
-    gfloat* gb = (gfloat*)dqkv + (long)n * L * 3 * D + h * DH;
+    const gfloat* base = (const gfloat*)qkv + rb * 3 * D + h * DH;
+    const gfloat* ob = (const gfloat*)ctx + rb * D + h * DH;
+    const gfloat* dob = (const gfloat*)dctx + rb * D + h * DH;
+    gfloat* gb = (gfloat*)dqkv + rb * 3 * D + h * DH;
     for (int idx = tid; idx < LP * (DH / 4); idx += 512) {
         const int l = idx / (DH / 4), c4 = (idx % (DH / 4)) * 4;
         float4 q4 = make_float4(0.f, 0.f, 0.f, 0.f), k4 = q4, v4 = q4, d4 = q4;
@@ -334,8 +343,8 @@ __global__ __launch_bounds__(512) void attn_bwd_mfma_rc_kernel(const float* __re
         *reinterpret_cast<float4*>(&Vs[l * SQ + c4]) = v4;
     }
     for (int l = tid; l < LP; l += 512) {
-        kf[l] = l < L ? (keep[(long)n * L + l] != 0.f ? 1.f : 0.f) : 0.f;
-        ls[l] = l < L ? lse[((long)n * H + h) * L + l] : INFINITY;
+        kf[l] = l < L ? (keep[rb + l] != 0.f ? 1.f : 0.f) : 0.f;
+        ls[l] = l < L ? lse[((long)n * H + h) * Lfix + l] : INFINITY;
     }
     for (int q = wave; q < LP; q += 8) {
         float v = 0.f;
@@ -460,36 +469,36 @@ size_t bwd_mfma_lds_bytes(int LP, int DH) {
 
 template <int DH, int NT>
 int launch_fwd_mfma(const float* qkv, const float* keep, float* ctx, float* lse, int N, int L, int H,
-                    hipStream_t s) {
+                    hipStream_t s, const int* coff) {
     const size_t lds = fwd_mfma_lds_bytes(NT * 16, DH);
     PT_HIP(hipFuncSetAttribute((const void*)attn_fwd_mfma_kernel<DH, NT>,
                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
     hipLaunchKernelGGL((attn_fwd_mfma_kernel<DH, NT>), dim3(N * H), dim3(512), lds, s, qkv, keep, ctx, lse,
-                       L, H, 1.0f / sqrtf((float)DH));
+                       L, H, 1.0f / sqrtf((float)DH), coff);
     PT_LAUNCH_CHECK();
     return PTCG_OK;
 }
 
 template <int DH, int NT>
 int launch_bwd_rc(const float* qkv, const float* keep, const float* ctx, const float* lse,
-                  const float* dctx, float* dqkv, int N, int L, int H, hipStream_t s) {
+                  const float* dctx, float* dqkv, int N, int L, int H, hipStream_t s, const int* coff) {
     const size_t lds = bwd_rc_lds_bytes(NT * 16, DH);
     PT_HIP(hipFuncSetAttribute((const void*)attn_bwd_mfma_rc_kernel<DH, NT>,
                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
     hipLaunchKernelGGL((attn_bwd_mfma_rc_kernel<DH, NT>), dim3(N * H), dim3(512), lds, s, qkv, keep, ctx,
-                       lse, dctx, dqkv, L, H, 1.0f / sqrtf((float)DH));
+                       lse, dctx, dqkv, L, H, 1.0f / sqrtf((float)DH), coff);
     PT_LAUNCH_CHECK();
     return PTCG_OK;
 }
 
 template <int DH, int NT>
 int launch_bwd_mfma(const float* qkv, const float* keep, const float* ctx, const float* lse,
-                    const float* dctx, float* dqkv, int N, int L, int H, hipStream_t s) {
+                    const float* dctx, float* dqkv, int N, int L, int H, hipStream_t s, const int* coff) {
     const size_t lds = bwd_mfma_lds_bytes(NT * 16, DH);
     PT_HIP(hipFuncSetAttribute((const void*)attn_bwd_mfma_kernel<DH, NT>,
                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
     hipLaunchKernelGGL((attn_bwd_mfma_kernel<DH, NT>), dim3(N * H), dim3(512), lds, s, qkv, keep, ctx, lse,
-                       dctx, dqkv, L, H, 1.0f / sqrtf((float)DH));
+                       dctx, dqkv, L, H, 1.0f / sqrtf((float)DH), coff);
     PT_LAUNCH_CHECK();
     return PTCG_OK;
 }
@@ -542,34 +551,34 @@ int pt_attn_supported(int L, int DH) {
     }
 
 int pt_attn_fwd(const float* qkv, const float* keep, float* ctx, float* lse, int N, int L, int H,
-                int DH, hipStream_t s) {
+                int DH, hipStream_t s, const int* coff) {
     PT_REQUIRE(pt_attn_supported(L, DH), "attention: L=%d Dh=%d exceeds the fused kernels' LDS budget", L, DH);
     const int nt = fwd_tiles(L, DH);
     if (nt && DH == 64) {
-        PT_NT_SWITCH8(64, nt, launch_fwd_mfma, qkv, keep, ctx, lse, N, L, H, s)
-        if (nt == 9) return launch_fwd_mfma<64, 9>(qkv, keep, ctx, lse, N, L, H, s);
+        PT_NT_SWITCH8(64, nt, launch_fwd_mfma, qkv, keep, ctx, lse, N, L, H, s, coff)
+        if (nt == 9) return launch_fwd_mfma<64, 9>(qkv, keep, ctx, lse, N, L, H, s, coff);
     } else if (nt) {
-        PT_NT_SWITCH8(32, nt, launch_fwd_mfma, qkv, keep, ctx, lse, N, L, H, s)
-        PT_NT_SWITCH_HI(32, nt, launch_fwd_mfma, qkv, keep, ctx, lse, N, L, H, s)
+        PT_NT_SWITCH8(32, nt, launch_fwd_mfma, qkv, keep, ctx, lse, N, L, H, s, coff)
+        PT_NT_SWITCH_HI(32, nt, launch_fwd_mfma, qkv, keep, ctx, lse, N, L, H, s, coff)
     }
     PT_REQUIRE(false, "attention: no kernel for L=%d Dh=%d", L, DH);
 }
 
 int pt_attn_bwd(const float* qkv, const float* keep, const float* ctx, const float* lse,
-                const float* dctx, float* dqkv, int N, int L, int H, int DH, hipStream_t s) {
+                const float* dctx, float* dqkv, int N, int L, int H, int DH, hipStream_t s, const int* coff) {
     PT_REQUIRE(pt_attn_supported(L, DH), "attention bwd: L=%d Dh=%d exceeds the fused kernels' LDS budget", L, DH);
     int nt = bwd_store_tiles(L, DH);
     if (nt) {
-        if (DH == 64) { PT_NT_SWITCH8(64, nt, launch_bwd_mfma, qkv, keep, ctx, lse, dctx, dqkv, N, L, H, s) }
-        else { PT_NT_SWITCH8(32, nt, launch_bwd_mfma, qkv, keep, ctx, lse, dctx, dqkv, N, L, H, s) }
+        if (DH == 64) { PT_NT_SWITCH8(64, nt, launch_bwd_mfma, qkv, keep, ctx, lse, dctx, dqkv, N, L, H, s, coff) }
+        else { PT_NT_SWITCH8(32, nt, launch_bwd_mfma, qkv, keep, ctx, lse, dctx, dqkv, N, L, H, s, coff) }
     }
     nt = bwd_rc_tiles(L, DH);
     if (nt && DH == 64) {
-        PT_NT_SWITCH8(64, nt, launch_bwd_rc, qkv, keep, ctx, lse, dctx, dqkv, N, L, H, s)
-        if (nt == 9) return launch_bwd_rc<64, 9>(qkv, keep, ctx, lse, dctx, dqkv, N, L, H, s);
+        PT_NT_SWITCH8(64, nt, launch_bwd_rc, qkv, keep, ctx, lse, dctx, dqkv, N, L, H, s, coff)
+        if (nt == 9) return launch_bwd_rc<64, 9>(qkv, keep, ctx, lse, dctx, dqkv, N, L, H, s, coff);
     } else if (nt) {
-        PT_NT_SWITCH8(32, nt, launch_bwd_rc, qkv, keep, ctx, lse, dctx, dqkv, N, L, H, s)
-        PT_NT_SWITCH_HI(32, nt, launch_bwd_rc, qkv, keep, ctx, lse, dctx, dqkv, N, L, H, s)
+        PT_NT_SWITCH8(32, nt, launch_bwd_rc, qkv, keep, ctx, lse, dctx, dqkv, N, L, H, s, coff)
+        PT_NT_SWITCH_HI(32, nt, launch_bwd_rc, qkv, keep, ctx, lse, dctx, dqkv, N, L, H, s, coff)
     }
     PT_REQUIRE(false, "attention bwd: no kernel for L=%d Dh=%d", L, DH);
 }

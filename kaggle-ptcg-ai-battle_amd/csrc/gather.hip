@@ -27,10 +27,23 @@ __global__ void tok_cat_fwd_kernel(GatherCtx c, const float* __restrict__ card,
     const int Lt = c.dm.l_tok, dc = c.dm.d_c, tin = c.dx.tok_in;
     const int chunks = tin / 4;
     const long i = (long)blockIdx.x * TB + threadIdx.x;
-    if (i >= (long)c.N * Lt * chunks) return;
+    // rows: (n, token t) full length, or the compact trunk rows (READOUT rows get zeros)
+    const long nrows = c.rowmap ? (long)*c.rows : (long)c.N * Lt;
+    if (i >= nrows * chunks) return;
     const int ch = (int)(i % chunks);
     const long r = i / chunks;
-    const int n = (int)(r / Lt), t = (int)(r % Lt);
+    int n, t;
+    if (c.rowmap) {
+        n = c.rsam[r];
+        t = c.rpos[r] - 1;
+        if (t < 0) {
+            *reinterpret_cast<float4*>(out + r * tin + ch * 4) = make_float4(0.f, 0.f, 0.f, 0.f);
+            return;
+        }
+    } else {
+        n = (int)(r / Lt);
+        t = (int)(r % Lt);
+    }
     const float* row = obs_row(c.obs, c.idx, c.stride, n);
     const float* ti = row + c.off.tok_int + (long)t * c.dm.tok_int;
     const int col = ch * 4;
@@ -62,12 +75,21 @@ __global__ void tok_cat_bwd_kernel(GatherCtx c, const float* __restrict__ d_cat,
                                    float* d_zemb, float* d_oemb) {
     const int Lt = c.dm.l_tok, dc = c.dm.d_c, tin = c.dx.tok_in;
     const long i = (long)blockIdx.x * TB + threadIdx.x;
-    if (i >= (long)c.N * Lt * tin) return;
+    const long nrows = c.rowmap ? (long)*c.rows : (long)c.N * Lt;
+    if (i >= nrows * tin) return;
     const int col = (int)(i % tin);
     const long r = i / tin;
     const float g = d_cat[i];
     if (g == 0.f) return;
-    const int n = (int)(r / Lt), t = (int)(r % Lt);
+    int n, t;
+    if (c.rowmap) {
+        n = c.rsam[r];
+        t = c.rpos[r] - 1;
+        if (t < 0) return;
+    } else {
+        n = (int)(r / Lt);
+        t = (int)(r % Lt);
+    }
     const float* ti = obs_row(c.obs, c.idx, c.stride, n) + c.off.tok_int + (long)t * c.dm.tok_int;
     const int NC = c.dm.n_cards;
     if (col < dc) {
@@ -156,15 +178,18 @@ __global__ void x0_fwd_kernel(GatherCtx c, const float* __restrict__ tokp,
         float* __restrict__ keep) {
     const int Ls = c.dx.l_seq, D = c.dm.d, ch4 = D / 4;
     const long i = (long)blockIdx.x * TB + threadIdx.x;
-    if (i >= (long)c.N * Ls * ch4) return;
+    const long nrows = c.rowmap ? (long)*c.rows : (long)c.N * Ls;
+    if (i >= nrows * ch4) return;
     const int col = (int)(i % ch4) * 4;
     const long nl = i / ch4;
-    const int n = (int)(nl / Ls), l = (int)(nl % Ls);
+    // full length: row (n, l), token projection row (n, l-1); compact: both at row nl
+    const int n = c.rowmap ? c.rsam[nl] : (int)(nl / Ls), l = c.rowmap ? c.rpos[nl] : (int)(nl % Ls);
     float4 v;
     if (l == 0) {
         v = *reinterpret_cast<const float4*>(readout + col);
     } else {
-        const float4 a = *reinterpret_cast<const float4*>(tokp + ((long)n * c.dm.l_tok + (l - 1)) * D + col);
+        const long tr = c.rowmap ? nl : (long)n * c.dm.l_tok + (l - 1);
+        const float4 a = *reinterpret_cast<const float4*>(tokp + tr * D + col);
         const float4 b = *reinterpret_cast<const float4*>(bc + (long)n * D + col);
         v = make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
     }
@@ -175,7 +200,7 @@ __global__ void x0_fwd_kernel(GatherCtx c, const float* __restrict__ tokp,
             const float z = obs_row(c.obs, c.idx, c.stride, n)[c.off.tok_int + (long)(l - 1) * c.dm.tok_int + 1];
             kp = z > 0.f ? 1.f : 0.f;
         }
-        keep[(long)n * Ls + l] = kp;
+        keep[nl] = kp;
     }
 }
 
@@ -183,6 +208,20 @@ __global__ void x0_fwd_kernel(GatherCtx c, const float* __restrict__ tokp,
 __global__ void x0_bwd_kernel(GatherCtx c, const float* __restrict__ d_x0, float* __restrict__ d_tokp,
                               float* __restrict__ d_bc) {
     const int n = blockIdx.x, Ls = c.dx.l_seq, Lt = c.dm.l_tok, D = c.dm.d;
+    if (c.rowmap) {   // compact: the sample's rows after its READOUT row (token rows share the index)
+        const long r0 = c.coff[n], r1 = c.coff[n + 1];
+        for (int col = threadIdx.x; col < D; col += TB) {
+            float acc = 0.f;
+            d_tokp[r0 * D + col] = 0.f;
+            for (long r = r0 + 1; r < r1; ++r) {
+                const float v = d_x0[r * D + col];
+                d_tokp[r * D + col] = v;
+                acc += v;
+            }
+            d_bc[(long)n * D + col] = acc;
+        }
+        return;
+    }
     for (int col = threadIdx.x; col < D; col += TB) {
         float acc = 0.f;
         for (int t = 0; t < Lt; ++t) {
@@ -249,7 +288,7 @@ __global__ void q_in_fwd_kernel(GatherCtx c, const float* __restrict__ h,
         const int e = col - PT_TYPE_E - (which - 1) * D;
         const int p = (int)oi[which];      // 0 = null; else trunk position p (token p-1)
         if (p > 0 && p <= c.dm.l_tok)
-            v = *reinterpret_cast<const float4*>(h + ((long)n * c.dx.l_seq + p) * D + e);
+            v = *reinterpret_cast<const float4*>(h + pt_hrow(c, n, p) * D + e);
     } else {
         v = *reinterpret_cast<const float4*>(row + c.off.opt_float + (long)j * c.dm.opt_f + (col - of0));
     }
@@ -267,11 +306,11 @@ __global__ void q_in_bwd_kernel(GatherCtx c, const float* __restrict__ d_qin, fl
         const int p1 = (int)oi[1], p2 = (int)oi[2];
         const bool v1 = p1 > 0 && p1 <= c.dm.l_tok, v2 = p2 > 0 && p2 <= c.dm.l_tok;
         for (int col = threadIdx.x; col < D; col += TB) {
-            if (v1) d_h[((long)n * c.dx.l_seq + p1) * D + col] += g[PT_TYPE_E + col];
+            if (v1) d_h[pt_hrow(c, n, p1) * D + col] += g[PT_TYPE_E + col];
         }
         __syncthreads();
         for (int col = threadIdx.x; col < D; col += TB) {
-            if (v2) d_h[((long)n * c.dx.l_seq + p2) * D + col] += g[PT_TYPE_E + D + col];
+            if (v2) d_h[pt_hrow(c, n, p2) * D + col] += g[PT_TYPE_E + D + col];
         }
         if (threadIdx.x < PT_TYPE_E) {
             const float gt = g[threadIdx.x];
@@ -292,7 +331,7 @@ __global__ void sc_in_fwd_kernel(GatherCtx c, const float* __restrict__ h,
     const int col = D + (int)(i % ch) * 4;
     const long nj = i / ch;
     const int n = (int)(nj / NO);
-    const float* r = h + (long)n * c.dx.l_seq * D;
+    const float* r = h + pt_hrow(c, n, 0) * D;
     float* o = sc + nj * W;
     float4 v;
     if (col < 2 * D) v = *reinterpret_cast<const float4*>(r + (col - D));
@@ -327,7 +366,7 @@ __global__ void sc_in_bwd_kernel(GatherCtx c, const float* __restrict__ d_sc,
             if (col < G) ag += g[o_g + col];
             if (col < PT_DEC_H) adv += g[o_dv + col];
         }
-        if (col < D) d_h[(long)n * c.dx.l_seq * D + col] += ar;
+        if (col < D) d_h[pt_hrow(c, n, 0) * D + col] += ar;
         if (col < G) d_gd[(long)n * c.dx.bcast_in + col] += ag;
         if (col < PT_DEC_H) d_gd[(long)n * c.dx.bcast_in + G + col] += adv;
     }
@@ -339,7 +378,8 @@ __global__ void val_in_fwd_kernel(GatherCtx c, const float* __restrict__ h,
     const long i = (long)blockIdx.x * TB + threadIdx.x;
     if (i >= (long)c.N * W) return;
     const int n = (int)(i / W), col = (int)(i % W);
-    v[i] = col < D ? h[(long)n * ls * D + col] : gd[(long)n * c.dx.bcast_in + (col - D)];
+    const long hr = ls == c.dx.l_seq ? pt_hrow(c, n, 0) : (long)n * ls;
+    v[i] = col < D ? h[hr * D + col] : gd[(long)n * c.dx.bcast_in + (col - D)];
 }
 
 __global__ void val_in_bwd_kernel(GatherCtx c, const float* __restrict__ dv, float* __restrict__ d_h,
@@ -348,7 +388,8 @@ __global__ void val_in_bwd_kernel(GatherCtx c, const float* __restrict__ dv, flo
     const long i = (long)blockIdx.x * TB + threadIdx.x;
     if (i >= (long)c.N * W) return;
     const int n = (int)(i / W), col = (int)(i % W);
-    if (col < D) d_h[(long)n * ls * D + col] += dv[i];
+    const long hr = ls == c.dx.l_seq ? pt_hrow(c, n, 0) : (long)n * ls;
+    if (col < D) d_h[hr * D + col] += dv[i];
     else d_gd[(long)n * c.dx.bcast_in + (col - D)] += dv[i];
 }
 
@@ -417,13 +458,15 @@ int pt_tok_cat_fwd(const GatherCtx& c, const float* card, const float* zemb, con
                    float* tok_cat, hipStream_t s) {
     PT_REQUIRE(c.dm.d_c % 4 == 0 && c.dm.tok_f % 4 == 0 && c.off.tok_float % 4 == 0 && c.stride % 4 == 0,
                "tok_cat: widths must be multiples of 4");
-    hipLaunchKernelGGL(tok_cat_fwd_kernel, PT_GRID((long)c.N * c.dm.l_tok * (c.dx.tok_in / 4)), c, card, zemb, oemb, tok_cat);
+    const long rows = c.rowmap ? (long)c.N * c.dx.l_seq : (long)c.N * c.dm.l_tok;
+    hipLaunchKernelGGL(tok_cat_fwd_kernel, PT_GRID(rows * (c.dx.tok_in / 4)), c, card, zemb, oemb, tok_cat);
     PT_LAUNCH_CHECK();
     return PTCG_OK;
 }
 int pt_tok_cat_bwd(const GatherCtx& c, const float* d_cat, float* d_card, float* d_zemb, float* d_oemb,
                    hipStream_t s) {
-    hipLaunchKernelGGL(tok_cat_bwd_kernel, PT_GRID((long)c.N * c.dm.l_tok * c.dx.tok_in), c, d_cat, d_card, d_zemb, d_oemb);
+    const long rows = c.rowmap ? (long)c.N * c.dx.l_seq : (long)c.N * c.dm.l_tok;
+    hipLaunchKernelGGL(tok_cat_bwd_kernel, PT_GRID(rows * c.dx.tok_in), c, d_cat, d_card, d_zemb, d_oemb);
     PT_LAUNCH_CHECK();
     return PTCG_OK;
 }

@@ -40,14 +40,20 @@ __device__ __forceinline__ void tile_of(int b, int tiles, int tn, int& tm_i, int
     tm_i = lb / tn;
     tn_i = lb % tn;
 }
-// the launch's logical tile range [g.tile0, g.tile0 + count)
-__device__ __forceinline__ void tile_of_range(const GemmArgs& g, int tm, int tn, int& tm_i, int& tn_i) {
-    const int count = g.ntiles ? g.ntiles : tm * tn;
-    int lb = blockIdx.x;
-    if ((count & 7) == 0) lb = (lb & 7) * (count >> 3) + (lb >> 3);
-    lb += g.tile0;
+// The launch's logical tile range [g.tile0, g.tile0 + count), count taken
+// from the effective (device) row count: blocks are dealt round-robin to the
+// 8 XCDs, so XCD x gets the contiguous logical range starting at
+// x*q + min(x, r) (count = 8q + r) — every XCD gets work and keeps its A rows
+// in its own L2.  Returns false for blocks beyond the count.
+__device__ __forceinline__ bool tile_of_range(const GemmArgs& g, int tn, int& tm_i, int& tn_i) {
+    const int count = g.ntiles ? g.ntiles : ((g.M + BM - 1) / BM) * tn;
+    const int b = blockIdx.x;
+    if (b >= count) return false;
+    const int q = count >> 3, r = count & 7, x = b & 7;
+    const int lb = g.tile0 + x * q + min(x, r) + (b >> 3);
     tm_i = lb / tn;
     tn_i = lb % tn;
+    return true;
 }
 
 // one output element through the epilogue
@@ -67,6 +73,33 @@ __device__ __forceinline__ void epi_store(const GemmArgs& g, int m, int n, float
         g.C[(long)m * g.ldc + n] = v * pt_gelu_grad(g.R[(long)m * g.ldr + n]);
     } else if (EPI == EPI_ACCUM) {
         g.C[(long)m * g.ldc + n] += v;
+    }
+}
+
+// four consecutive outputs C[m][n..n+3] through the epilogue (128-bit
+// accesses: the caller checked alignment and n + 3 < N); same arithmetic
+// order as epi_store
+__device__ __forceinline__ void st_g4(float* p, floatx4 v) { *(gfloatx4*)(gfloat*)p = v; }
+__device__ __forceinline__ floatx4 ld_v4(const float* p) { return *(const gfloatx4*)(const gfloat*)p; }
+
+template <int EPI>
+__device__ __forceinline__ void epi_store4(const GemmArgs& g, int m, int n, floatx4 v) {
+    float* c = g.C + (long)m * g.ldc + n;
+    if (EPI == EPI_STORE) {
+        st_g4(c, v);
+    } else if (EPI == EPI_BIAS) {
+        st_g4(c, v + ld_v4(g.bias + n));
+    } else if (EPI == EPI_BIAS_GELU) {
+        v += ld_v4(g.bias + n);
+        st_g4(c, v);
+        st_g4(g.C2 + (long)m * g.ldc2 + n, floatx4{pt_gelu(v[0]), pt_gelu(v[1]), pt_gelu(v[2]), pt_gelu(v[3])});
+    } else if (EPI == EPI_BIAS_RESID) {
+        st_g4(c, (v + ld_v4(g.bias + n)) + ld_v4(g.R + (long)m * g.ldr + n));
+    } else if (EPI == EPI_GELU_BWD) {
+        const floatx4 x = ld_v4(g.R + (long)m * g.ldr + n);
+        st_g4(c, v * floatx4{pt_gelu_grad(x[0]), pt_gelu_grad(x[1]), pt_gelu_grad(x[2]), pt_gelu_grad(x[3])});
+    } else if (EPI == EPI_ACCUM) {
+        st_g4(c, ld_v4(c) + v);
     }
 }
 
@@ -95,8 +128,11 @@ __device__ __forceinline__ float4 ld_scalar4(const gfloat* X, long ld, int lim, 
     return v;
 }
 
-// Epilogue shared by the fp32 and bf16 kernels: acc[ti][tj][r] holds
-// C[wm + ti*16 + 4*lq + r][wn + tj*16 + li] of the block tile at (m0, n0).
+// Epilogue shared by the fp32 and bf16 kernels.  The MFMAs take the B tile
+// as their first operand, so acc[ti][tj][r] holds the transposed product
+// C[wm + ti*16 + li][wn + tj*16 + 4*lq + r] of the block tile at (m0, n0):
+// four consecutive columns of one row per lane, stored (and the bias /
+// residual / pre-activation read) as one 128-bit access when aligned.
 template <int EPI, bool PARTIAL>
 __device__ __forceinline__ void gemm_epilogue(const GemmArgs& g, floatx4 (&acc)[4][4], int m0, int n0, int wm,
                                               int wn, int li, int lq, long part_stride) {
@@ -108,27 +144,34 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& g, floatx4 (&acc)[
 #pragma unroll
         for (int ti = 0; ti < 4; ++ti)
 #pragma unroll
-            for (int tj = 0; tj < 4; ++tj)
-#pragma unroll
-                for (int r = 0; r < 4; ++r)
-                    P[(wm + ti * 16 + lq * 4 + r) * BN + wn + tj * 16 + li] = acc[ti][tj][r];
+            for (int tj = 0; tj < 4; ++tj) st_g4(P + (wm + ti * 16 + li) * BN + wn + tj * 16 + 4 * lq, acc[ti][tj]);
         return;
     }
     const long zoff = PARTIAL ? (long)blockIdx.z * part_stride : 0;
+    const uintptr_t al = PARTIAL ? (uintptr_t)g.C | (uintptr_t)(g.ldc * 4)
+                                 : (uintptr_t)g.C | (uintptr_t)g.C2 | (uintptr_t)g.R | (uintptr_t)g.bias |
+                                       (uintptr_t)((g.ldc | g.ldc2 | g.ldr) * 4);
+    const bool vo = (al & 15) == 0;
 #pragma unroll
-    for (int ti = 0; ti < 4; ++ti)
+    for (int ti = 0; ti < 4; ++ti) {
+        const int m = m0 + wm + ti * 16 + li;
+        if (m >= g.M) continue;
 #pragma unroll
         for (int tj = 0; tj < 4; ++tj) {
-            const int n = n0 + wn + tj * 16 + li;
-            if (n >= g.N) continue;
+            const int n = n0 + wn + tj * 16 + 4 * lq;
+            if (vo && n + 3 < g.N) {
+                if (PARTIAL) st_g4(g.C + zoff + (long)m * g.ldc + n, acc[ti][tj]);
+                else epi_store4<EPI>(g, m, n, acc[ti][tj]);
+                continue;
+            }
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int m = m0 + wm + ti * 16 + lq * 4 + r;
-                if (m >= g.M) continue;
-                if (PARTIAL) g.C[zoff + (long)m * g.ldc + n] = acc[ti][tj][r];
-                else epi_store<EPI>(g, m, n, acc[ti][tj][r]);
+                if (n + r >= g.N) continue;
+                if (PARTIAL) g.C[zoff + (long)m * g.ldc + n + r] = acc[ti][tj][r];
+                else epi_store<EPI>(g, m, n + r, acc[ti][tj][r]);
             }
         }
+    }
 }
 
 // DB (AT only): blocks of the first N-tile also sum their A tile over k, the
@@ -136,13 +179,13 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& g, floatx4 (&acc)[
 // With PARTIAL the per-split sums go to C + splits*part_stride + z*M.
 // VEC: operands satisfy the 128-bit load rules (else scalar loads).
 template <bool AT, bool BT, int EPI, bool PARTIAL, bool DB, bool VEC>
-__global__ __launch_bounds__(NT) void gemm_f32_kernel(GemmArgs g, int k_chunk, long part_stride) {
+__global__ __launch_bounds__(NT) void gemm_f32_kernel(const GemmArgs g, int k_chunk, long part_stride) {
     __shared__ __align__(16) float As[2][Stage<AT>::floats];
     __shared__ __align__(16) float Bs[2][Stage<BT>::floats];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int tm = (g.M + BM - 1) / BM, tn = (g.N + BN - 1) / BN;
+    const int tn = (g.N + BN - 1) / BN;
     int tmi, tni;
-    tile_of_range(g, tm, tn, tmi, tni);
+    if (!tile_of_range(g, tn, tmi, tni)) return;   // beyond the (device) tile count
     const int m0 = tmi * BM, n0 = tni * BN;
     const int kbeg = blockIdx.z * k_chunk;
     const int kend = min(g.K, kbeg + k_chunk);
@@ -212,7 +255,7 @@ __global__ __launch_bounds__(NT) void gemm_f32_kernel(GemmArgs g, int k_chunk, l
 #define PT_MFMA_STEP(c)                                                                             \
             _Pragma("unroll") for (int ti = 0; ti < 4; ++ti)                                        \
             _Pragma("unroll") for (int tj = 0; tj < 4; ++tj)                                        \
-                acc[ti][tj] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[ti].c, bf[tj].c, acc[ti][tj], 0, 0, 0);
+                acc[ti][tj] = __builtin_amdgcn_mfma_f32_16x16x4f32(bf[tj].c, af[ti].c, acc[ti][tj], 0, 0, 0);
             PT_MFMA_STEP(x) PT_MFMA_STEP(y) PT_MFMA_STEP(z) PT_MFMA_STEP(w)
 #undef PT_MFMA_STEP
             if (do_db) {
@@ -301,13 +344,13 @@ __device__ __forceinline__ void bf_store(__bf16* S, int tid, const float4 (&v)[4
 }
 
 template <bool AT, bool BT, int EPI, bool PARTIAL>
-__global__ __launch_bounds__(NT) void gemm_bf16_kernel(GemmArgs g, int k_chunk, long part_stride) {
+__global__ __launch_bounds__(NT) void gemm_bf16_kernel(const GemmArgs g, int k_chunk, long part_stride) {
     __shared__ __align__(16) __bf16 As[2][BM * SKB2];
     __shared__ __align__(16) __bf16 Bs[2][BN * SKB2];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int tm = (g.M + BM - 1) / BM, tn = (g.N + BN - 1) / BN;
+    const int tn = (g.N + BN - 1) / BN;
     int tmi, tni;
-    tile_of_range(g, tm, tn, tmi, tni);
+    if (!tile_of_range(g, tn, tmi, tni)) return;   // beyond the (device) tile count
     const int m0 = tmi * BM, n0 = tni * BN;
     const int kbeg = blockIdx.z * k_chunk;
     const int kend = min(g.K, kbeg + k_chunk);
@@ -344,7 +387,7 @@ __global__ __launch_bounds__(NT) void gemm_bf16_kernel(GemmArgs g, int k_chunk, 
             for (int ti = 0; ti < 4; ++ti)
 #pragma unroll
                 for (int tj = 0; tj < 4; ++tj)
-                    acc[ti][tj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[ti], bfr[tj], acc[ti][tj], 0, 0, 0);
+                    acc[ti][tj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bfr[tj], af[ti], acc[ti][tj], 0, 0, 0);
             if (more) {
                 bf_store<AT>(As[buf ^ 1], tid, va);
                 bf_store<BT>(Bs[buf ^ 1], tid, vb);
@@ -426,6 +469,15 @@ struct GemmProf {
 };
 GemmProf g_prof;
 
+// products a launch executes: its share of the tiles, over the whole of K
+// (split-K launches cover K across grid.z)
+double launch_flops(const GemmArgs& g) {
+    const double all = 2.0 * g.M * (double)g.N * g.K;
+    if (!g.ntiles) return all;
+    const double tiles = (double)pt_cdiv(g.M, BM) * pt_cdiv(g.N, BN);
+    return all * g.ntiles / tiles;
+}
+
 template <bool AT, bool BT, int EPI, bool PARTIAL, bool DB, bool VEC>
 void launch(const GemmArgs& g, dim3 grid, int k_chunk, long part_stride, hipStream_t s) {
     const bool rec = g_prof.on && g_prof.used * 2 + 1 < (int)g_prof.ev.size();
@@ -434,7 +486,7 @@ void launch(const GemmArgs& g, dim3 grid, int k_chunk, long part_stride, hipStre
                        part_stride);
     if (rec) {
         (void)hipEventRecord(g_prof.ev[2 * g_prof.used + 1], s);
-        g_prof.flops[g_prof.used] = 2.0 * g.M * (double)g.N * g.K;
+        g_prof.flops[g_prof.used] = launch_flops(g);
         g_prof.used++;
     }
 }
@@ -446,7 +498,7 @@ void launch_bf16(const GemmArgs& g, dim3 grid, int k_chunk, long part_stride, hi
     hipLaunchKernelGGL((gemm_bf16_kernel<AT, BT, EPI, PARTIAL>), grid, dim3(NT), 0, s, g, k_chunk, part_stride);
     if (rec) {
         (void)hipEventRecord(g_prof.ev[2 * g_prof.used + 1], s);
-        g_prof.flops[g_prof.used] = 2.0 * g.M * (double)g.N * g.K;
+        g_prof.flops[g_prof.used] = launch_flops(g);
         g_prof.used++;
     }
 }

@@ -43,10 +43,13 @@ int pt_ln_bwd(const float* dy, long lddy, const float* x, long ldx, const float*
               long lddx, float* dw, float* db, int rows, int D, float* ws, long ws_floats,
               hipStream_t s);
 int pt_attn_supported(int L, int DH);
+// coff (nullable): sample n's rows are [coff[n], coff[n+1]) (length <= L);
+// else rows n*L .. n*L+L-1.  lse is laid out (N, H, L) either way.
 int pt_attn_fwd(const float* qkv, const float* keep, float* ctx, float* lse, int N, int L, int H,
-                int DH, hipStream_t s);
+                int DH, hipStream_t s, const int* coff = nullptr);
 int pt_attn_bwd(const float* qkv, const float* keep, const float* ctx, const float* lse,
-                const float* dctx, float* dqkv, int N, int L, int H, int DH, hipStream_t s);
+                const float* dctx, float* dqkv, int N, int L, int H, int DH, hipStream_t s,
+                const int* coff = nullptr);
 long pt_ppo_partial_floats(int n);
 int pt_ppo_loss(const float* out, int n, int A, const float* mask, long mask_stride,
                 const int32_t* idx, const float* actions, const float* old_logp,
@@ -65,7 +68,17 @@ int pt_adam_step(float* w, float* g, float* m, float* v, long n, double lr, doub
 struct GatherCtx {
     const float* obs; const int32_t* idx; long stride; int N;
     PtcgDims dm; DimsX dx; ObsOff off;
+    // compact trunk layout (null = full length, row n*l_seq + pos): sample n
+    // owns rows [coff[n], coff[n+1]) = READOUT then its active positions
+    // (valid tokens and pointer targets) in order; rowmap[n*l_seq + pos] is
+    // the row of an active position (-1 otherwise); rsam / rpos invert it;
+    // *rows = coff[N].
+    const int* coff; const int* rowmap; const int* rsam; const int* rpos; const int* rows;
 };
+// trunk row of (sample n, position pos); pos must be active in the compact layout
+__device__ __forceinline__ long pt_hrow(const GatherCtx& c, int n, int pos) {
+    return c.rowmap ? (long)c.rowmap[(long)n * c.dx.l_seq + pos] : (long)n * c.dx.l_seq + pos;
+}
 int pt_tok_cat_fwd(const GatherCtx& c, const float* card, const float* zemb, const float* oemb,
                    float* tok_cat, hipStream_t s);
 int pt_tok_cat_bwd(const GatherCtx& c, const float* d_cat, float* d_card, float* d_zemb,
@@ -116,3 +129,11 @@ int pt_xc_bwd(const float* d_xc, float* d_h, float* d_otok, int N, int Ls, int N
 int pt_aux_grads(const GatherCtx& c, const float* hand_lin, const float* prize_all, const float* blind_v,
                  const float* ret, int* cnt, float* d_hand, float* d_prize, float* d_blind, hipStream_t s);
 int pt_rank1_add(const float* dy, const float* w, float* dX, int rows, int K, hipStream_t s);
+
+// ---- compact trunk layout (compact.hip)
+// Active positions of each sample (READOUT, valid tokens, pointer targets),
+// row offsets, row maps; act is scratch of N * l_seq ints.
+int pt_compact_map(const GatherCtx& c, int* act, int* cnt, int* coff, int* rowmap, int* rsam, int* rpos,
+                   hipStream_t s);
+// dst[n] = src[coff[n]]  (rows of width D)
+int pt_gather_rows(const float* src, long ld, const int* coff, int N, int D, float* dst, hipStream_t s);

@@ -67,6 +67,16 @@ struct PtcgModel {
     int N = 0;
     bool train = true;
     int prec = 0;   // GEMM products: 0 fp32, 1 bf16 operands with fp32 accumulation
+    // compact trunk layout (blind-critic models): only READOUT, valid tokens
+    // and pointer targets are trunk rows; *Tr = their count (device), read
+    // back once per forward into rows (pinned rows_h) so every GEMM,
+    // LayerNorm and grid is sized for exactly those rows
+    bool compact = false;
+    int *c_act = nullptr, *c_cnt, *c_off, *c_map, *c_rsam, *c_rpos;
+    const int* Tr = nullptr;
+    int* rows_h = nullptr;
+    int rows = 0;
+    float* rd_buf = nullptr;
     char* mem = nullptr;
     size_t mem_bytes = 0;
     float *tok_cat, *tokp, *glob_in, *g1, *g1a, *dec_in, *d1, *d1a, *gd, *bc, *keep;
@@ -360,8 +370,21 @@ static size_t carve(PtcgModel* m, char* base) {
     const bool crit = d.critic == 1, train = m->train;
     const long NLC = crit ? N * x.l_crit : 0, NLmax = NL > NLC ? NL : NLC, NK = N * x.n_orc;
     Carver c{base};
-    m->tok_cat = c.take(N * Lt * x.tok_in);
-    m->tokp = c.take(N * Lt * D);
+    const long tok_rows = m->compact ? NL : N * Lt;   // compact: token rows share the trunk row index
+    m->tok_cat = c.take(tok_rows * x.tok_in);
+    m->tokp = c.take(tok_rows * D);
+    if (m->compact) {
+        m->c_act = reinterpret_cast<int*>(c.take(NL));
+        m->c_cnt = reinterpret_cast<int*>(c.take(N));
+        m->c_off = reinterpret_cast<int*>(c.take(N + 1));
+        m->c_map = reinterpret_cast<int*>(c.take(NL));
+        m->c_rsam = reinterpret_cast<int*>(c.take(NL));
+        m->c_rpos = reinterpret_cast<int*>(c.take(NL));
+        m->rd_buf = c.take(N * D);
+        m->Tr = m->c_off ? m->c_off + N : nullptr;
+    } else {
+        m->Tr = nullptr;
+    }
     m->glob_in = c.take(N * d.global_f);
     m->g1 = c.take(N * d.g); m->g1a = c.take(N * d.g);
     m->dec_in = c.take(N * x.dec_in);
@@ -416,7 +439,7 @@ static size_t carve(PtcgModel* m, char* base) {
     m->dvin = c.take(N * x.val_in); m->dv1 = c.take(N * PT_VAL_H);
     m->dgd = c.take(N * x.bcast_in); m->dd1 = c.take(N * PT_DEC_H); m->dg1 = c.take(N * d.g);
     m->ddec = c.take(N * x.dec_in);
-    m->dtokp = c.take(N * Lt * D); m->dtokcat = c.take(N * Lt * x.tok_in);
+    m->dtokp = c.take(tok_rows * D); m->dtokcat = c.take(tok_rows * x.tok_in);
     m->dbc = c.take(N * D);
     // workspace: split-K partials, column-sum / LayerNorm / head partials
     m->ws_floats = 16L << 20;
@@ -433,6 +456,8 @@ static int reg(PtcgModel* m, int n, bool train) {
     }
     m->N = n;
     m->train = train;
+    m->compact = m->dm.critic == 0;
+    if (m->compact && !m->rows_h) PT_HIP(hipHostMalloc((void**)&m->rows_h, sizeof(int), hipHostMallocDefault));
     size_t bytes = carve(m, nullptr);
     PT_HIP(hipMalloc(&m->mem, bytes));
     m->mem_bytes = bytes;
@@ -454,6 +479,7 @@ extern "C" void ptcg_model_free(PtcgModel* m) {
     if (!m) return;
     if (m->mem) (void)hipFree(m->mem);
     if (m->tmem) (void)hipFree(m->tmem);
+    if (m->rows_h) (void)hipHostFree(m->rows_h);
     delete m;
 }
 
@@ -462,13 +488,15 @@ float* pt_model_out(const PtcgModel* m) { return m->out; }
 float* pt_model_ws(const PtcgModel* m, long* floats) { *floats = m->ws_floats; return m->ws; }
 
 // ------------------------------------------------------------ forward
+// rows / coff: row count and per-sample row offsets of a compact layout
+// (rows 0, coff null: N * L rows)
 static int block_fwd(PtcgModel* m, const BlockP& w, const BlockA& a, int L, const float* keep, const float* xin,
-                     float* xout, hipStream_t s) {
+                     float* xout, hipStream_t s, int rows = 0, const int* coff = nullptr) {
     const PtcgDims& d = m->dm;
-    const int NL = m->N * L, D = d.d;
+    const int NL = rows ? rows : m->N * L, D = d.d;
     PT_TRY(pt_ln_fwd(xin, D, w.ln1w, w.ln1b, a.ln1, D, a.mu1, a.rs1, NL, D, s));
     PT_TRY(linf(m, a.ln1, w.qkvw, w.qkvb, a.qkv, NL, D, 3 * D, EPI_BIAS, nullptr, nullptr, s));
-    PT_TRY(pt_attn_fwd(a.qkv, keep, a.ctx, a.lse, m->N, L, d.heads, m->dx.dh, s));
+    PT_TRY(pt_attn_fwd(a.qkv, keep, a.ctx, a.lse, m->N, L, d.heads, m->dx.dh, s, coff));
     PT_TRY(linf(m, a.ctx, w.projw, w.projb, a.xmid, NL, D, D, EPI_BIAS_RESID, xin, nullptr, s));
     PT_TRY(pt_ln_fwd(a.xmid, D, w.ln2w, w.ln2b, a.ln2, D, a.mu2, a.rs2, NL, D, s));
     PT_TRY(linf(m, a.ln2, w.f1w, w.f1b, a.ffp, NL, D, d.ffn, EPI_BIAS_GELU, nullptr, a.ffa, s));
@@ -516,10 +544,25 @@ extern "C" int ptcg_model_forward(PtcgModel* m, const float* obs, const int32_t*
     m->obs = obs;
     m->idx = row_idx;
     GatherCtx c{obs, row_idx, (long)m->off.size, N, d, x, m->off};
+    const int* Tr = m->Tr;
+    const int* coff = m->compact ? m->c_off : nullptr;
+    m->rows = N * x.l_seq;
+    if (m->compact) {
+        PT_TRY(pt_compact_map(c, m->c_act, m->c_cnt, m->c_off, m->c_map, m->c_rsam, m->c_rpos, s));
+        c.coff = m->c_off; c.rowmap = m->c_map; c.rsam = m->c_rsam; c.rpos = m->c_rpos; c.rows = Tr;
+        // the one host read-back of the step: the trunk row count sizes every
+        // launch that follows
+        PT_HIP(hipMemcpyAsync(m->rows_h, Tr, sizeof(int), hipMemcpyDeviceToHost, s));
+        PT_HIP(hipStreamSynchronize(s));
+        m->rows = *m->rows_h;
+        PT_REQUIRE(m->rows >= N && m->rows <= N * x.l_seq, "model_forward: compact row count %d out of range",
+                   m->rows);
+    }
+    const int tok_rows = m->compact ? m->rows : N * Lt;
 
     if (d.tables == 1) PT_TRY(tables_fwd(m, s));
     PT_TRY(pt_tok_cat_fwd(c, m->card, m->zemb, m->oemb, m->tok_cat, s));
-    PT_TRY(linf(m, m->tok_cat, m->tp_w, m->tp_b, m->tokp, N * Lt, x.tok_in, D, EPI_BIAS, nullptr, nullptr, s));
+    PT_TRY(linf(m, m->tok_cat, m->tp_w, m->tp_b, m->tokp, tok_rows, x.tok_in, D, EPI_BIAS, nullptr, nullptr, s));
     PT_TRY(pt_glob_in(c, m->glob_in, s));
     PT_TRY(linf(m, m->glob_in, m->g1_w, m->g1_b, m->g1, N, d.global_f, G, EPI_BIAS_GELU, nullptr, m->g1a, s));
     PT_TRY(lin(m, m->g1a, G, m->g2_w, m->g2_b, m->gd, x.bcast_in, N, G, G, EPI_BIAS, nullptr, 0, nullptr, 0, s));
@@ -532,10 +575,10 @@ extern "C" int ptcg_model_forward(PtcgModel* m, const float* obs, const int32_t*
     const bool tr = m->train;
     for (int i = 0; i < d.layers; ++i)
         PT_TRY(block_fwd(m, m->blk[i], m->ba[tr ? i : 0], x.l_seq, m->keep, m->x[tr ? i : i % 2],
-                         m->x[tr ? i + 1 : (i + 1) % 2], s));
+                         m->x[tr ? i + 1 : (i + 1) % 2], s, m->rows, coff));
     const int NL = N * x.l_seq;
     PT_TRY(pt_ln_fwd(m->x[tr ? d.layers : d.layers % 2], D, m->lnf_w, m->lnf_b, m->h, D, m->lnf_mu, m->lnf_rs,
-                     NL, D, s));
+                     m->rows, D, s));
 
     // option scorer
     const int NJ = N * NO;
@@ -580,9 +623,9 @@ extern "C" int ptcg_model_forward(PtcgModel* m, const float* obs, const int32_t*
 // ------------------------------------------------------------ backward
 // dA holds d(x_out) on entry and d(x_in) on exit; dC is scratch for d(x_mid)
 static int block_bwd(PtcgModel* m, const BlockP& w, const BlockA& a, int L, const float* keep, const float* xin,
-                     float* dA, float* dC, hipStream_t s) {
+                     float* dA, float* dC, hipStream_t s, int rows = 0, const int* coff = nullptr) {
     const PtcgDims& d = m->dm;
-    const int NL = m->N * L, D = d.d;
+    const int NL = rows ? rows : m->N * L, D = d.d;
     PT_TRY(ldw_(m, dA, D, a.ffa, d.ffn, m->G(w.f2w), m->G(w.f2b), NL, d.ffn, D, s));
     PT_TRY(ldx_(m, dA, D, w.f2w, m->dffn, d.ffn, NL, d.ffn, D, EPI_GELU_BWD, a.ffp, d.ffn, s));
     PT_TRY(ldw_(m, m->dffn, d.ffn, a.ln2, D, m->G(w.f1w), m->G(w.f1b), NL, D, d.ffn, s));
@@ -591,7 +634,7 @@ static int block_bwd(PtcgModel* m, const BlockP& w, const BlockA& a, int L, cons
                      m->G(w.ln2b), NL, D, m->ws, m->ws_floats, s));
     PT_TRY(ldw_(m, dC, D, a.ctx, D, m->G(w.projw), m->G(w.projb), NL, D, D, s));
     PT_TRY(ldx_(m, dC, D, w.projw, m->dctx, D, NL, D, D, EPI_STORE, nullptr, 0, s));
-    PT_TRY(pt_attn_bwd(a.qkv, keep, a.ctx, a.lse, m->dctx, m->dqkv, m->N, L, d.heads, m->dx.dh, s));
+    PT_TRY(pt_attn_bwd(a.qkv, keep, a.ctx, a.lse, m->dctx, m->dqkv, m->N, L, d.heads, m->dx.dh, s, coff));
     PT_TRY(ldw_(m, m->dqkv, 3 * D, a.ln1, D, m->G(w.qkvw), m->G(w.qkvb), NL, D, 3 * D, s));
     PT_TRY(ldx_(m, m->dqkv, 3 * D, w.qkvw, m->dln, D, NL, D, 3 * D, EPI_STORE, nullptr, 0, s));
     PT_TRY(pt_ln_bwd(m->dln, D, xin, D, w.ln1w, a.mu1, a.rs1, dC, D, dA, D, m->G(w.ln1w),
@@ -680,9 +723,16 @@ extern "C" int ptcg_model_backward(PtcgModel* m, const float* grad, void* stream
     const int N = m->N, Lt = d.l_tok, NO = d.n_opt, D = d.d, G = d.g, NJ = N * NO;
     const int NL = N * x.l_seq;
     GatherCtx c{m->obs, m->idx, (long)m->off.size, N, d, x, m->off};
+    const int* Tr = m->Tr;
+    const int* coff = m->compact ? m->c_off : nullptr;
+    if (m->compact) {   // the map of the forward (same rows)
+        c.coff = m->c_off; c.rowmap = m->c_map; c.rsam = m->c_rsam; c.rpos = m->c_rpos; c.rows = Tr;
+    }
+    const int rows = m->rows;   // trunk rows of the forward
+    const int tok_rows = m->compact ? rows : N * Lt;
 
     PT_TRY(pt_fill_zero(m->Gr, m->arena, s));
-    PT_TRY(pt_fill_zero(m->dxa, (long)NL * D, s));
+    PT_TRY(pt_fill_zero(m->dxa, (long)rows * D, s));
     PT_TRY(pt_fill_zero(m->dgd, (long)N * x.bcast_in, s));
     if (d.tables == 1) {
         PT_TRY(pt_fill_zero(m->d_card_vec, (long)d.n_cards * d.d_c, s));
@@ -723,15 +773,20 @@ extern "C" int ptcg_model_backward(PtcgModel* m, const float* grad, void* stream
 
     // final LayerNorm, then the trunk in reverse (d_x in dxb, scratch dxa)
     PT_TRY(pt_ln_bwd(m->dxa, D, m->x[d.layers], D, m->lnf_w, m->lnf_mu, m->lnf_rs, nullptr, 0, m->dxb, D,
-                     m->G(m->lnf_w), m->G(m->lnf_b), NL, D, m->ws, m->ws_floats, s));
+                     m->G(m->lnf_w), m->G(m->lnf_b), rows, D, m->ws, m->ws_floats, s));
     for (int i = d.layers - 1; i >= 0; --i)
-        PT_TRY(block_bwd(m, m->blk[i], m->ba[i], x.l_seq, m->keep, m->x[i], m->dxb, m->dxa, s));
+        PT_TRY(block_bwd(m, m->blk[i], m->ba[i], x.l_seq, m->keep, m->x[i], m->dxb, m->dxa, s, rows, coff));
 
     // trunk input: readout / token projection / broadcast
     PT_TRY(pt_x0_bwd(c, m->dxb, m->dtokp, m->dbc, s));
-    PT_TRY(pt_colsum(m->dxb, (long)x.l_seq * D, N, D, m->G(m->readout), m->ws, m->ws_floats, s));
-    PT_TRY(ldw_(m, m->dtokp, D, m->tok_cat, x.tok_in, m->G(m->tp_w), m->G(m->tp_b), N * Lt, x.tok_in, D, s));
-    PT_TRY(ldx_(m, m->dtokp, D, m->tp_w, m->dtokcat, x.tok_in, N * Lt, x.tok_in, D, EPI_STORE, nullptr, 0, s));
+    if (m->compact) {
+        PT_TRY(pt_gather_rows(m->dxb, D, m->c_off, N, D, m->rd_buf, s));
+        PT_TRY(pt_colsum(m->rd_buf, D, N, D, m->G(m->readout), m->ws, m->ws_floats, s));
+    } else {
+        PT_TRY(pt_colsum(m->dxb, (long)x.l_seq * D, N, D, m->G(m->readout), m->ws, m->ws_floats, s));
+    }
+    PT_TRY(ldw_(m, m->dtokp, D, m->tok_cat, x.tok_in, m->G(m->tp_w), m->G(m->tp_b), tok_rows, x.tok_in, D, s));
+    PT_TRY(ldx_(m, m->dtokp, D, m->tp_w, m->dtokcat, x.tok_in, tok_rows, x.tok_in, D, EPI_STORE, nullptr, 0, s));
     PT_TRY(pt_tok_cat_bwd(c, m->dtokcat, m->dcard, m->G(m->zemb), m->G(m->oemb), s));
     PT_TRY(ldw_(m, m->dbc, D, m->gd, x.bcast_in, m->G(m->bc_w), m->G(m->bc_b), N, x.bcast_in, D, s));
     PT_TRY(ldx_(m, m->dbc, D, m->bc_w, m->dgd, x.bcast_in, N, x.bcast_in, D, EPI_ACCUM, nullptr, 0, s));

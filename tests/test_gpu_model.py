@@ -204,3 +204,40 @@ def test_gate_vetoes_step(cuda):
     m, v = pl.get_moments()
     assert not m.any() and not v.any()
     pl.close()
+
+
+def test_pointers_into_padding_and_no_valid_tokens(cuda):
+    """Option pointers that select padded tokens (whose trunk rows are then
+    computed although they are no keys) and a sample with no valid token at
+    all: the compact trunk layout must give the full-length results."""
+    dm = dims.tiny()
+    B = 8
+    ref, pl = make(dm, B, seed=51)
+    obs = synth.make_obs(dm, B, seed=52, rich=True, max_pad=dm.l_tok // 2)
+    off = dm.offsets()
+    ti = obs[:, off["tok_int"][0]:off["tok_int"][1]].reshape(B, dm.l_tok, dm.tok_int)
+    oi = obs[:, off["opt_int"][0]:off["opt_int"][1]].reshape(B, dm.n_opt, dm.opt_int)
+    tf = obs[:, off["tok_float"][0]:off["tok_float"][1]].reshape(B, dm.l_tok, dm.tok_f)
+    rng = np.random.default_rng(53)
+    for i in range(B):
+        pad = np.flatnonzero(ti[i, :, 1] <= 0)
+        if pad.size:
+            ti[i, pad, 0] = rng.integers(0, dm.n_cards, pad.size)      # padded tokens carry content
+            tf[i, pad] = rng.standard_normal((pad.size, dm.tok_f))
+            oi[i, 0, 1] = pad[0] + 1
+            oi[i, 1, 2] = pad[-1] + 1
+    ti[3, :, 1] = 0                                                     # sample 3: every token padded
+    inp = synth.make_ppo_inputs(dm, obs, seed=54)
+    o = torch.from_numpy(obs)
+    out = ref(o)
+    m0, m1 = off["opt_mask"]
+    T = lambda k: torch.from_numpy(inp[k])
+    res = oppo.ppo_loss(out.detach(), o[:, m0:m1], T("actions"), T("logprobs"), T("advantages"),
+                        T("returns"), T("values"), clip=0.2, vf_clip=0.2, vf_coef=0.5, ent_coef=0.01)
+    out.backward(res["grad"])
+    pl.forward_backward(pl.to_device(obs), None, {k: pl.to_device(v) for k, v in inp.items()})
+    pl.sync()
+    dec, _, _, _ = pl.buffers()
+    fwd_check(d2h(dec, (B, dm.n_opt + 1)), out.detach().numpy())
+    _grads_check(pl, ref, dm, res["grad"].numpy()[:, :dm.n_opt])
+    pl.close()

@@ -13,10 +13,13 @@
 // to the vocabulary (ptcg_model.cu:299-318).  Forward gathers move 16 B per
 // lane.  Per-sample reductions (the bcast row sum, the pointer scatter into
 // the trunk output, the option sums into r/g/dvec) run one workgroup per
-// sample in a fixed order instead of the reference's atomics; only the
-// scatters into shared embedding tables (card/attack/zone/owner/type/select/
-// context rows shared across samples) use fp32 atomics, as the reference does.
+// sample, each element owned by one thread; the scatters into shared
+// embedding tables (card/attack/zone/owner/type/select/context rows shared
+// across samples) use fp32 atomics, as the reference does, after summing
+// rows of equal id in a per-thread id cache (IdCache).
 #include "model.h"
+
+#include <algorithm>
 
 namespace {
 
@@ -71,43 +74,89 @@ __global__ void tok_cat_fwd_kernel(GatherCtx c, const float* __restrict__ card,
     *reinterpret_cast<float4*>(out + r * tin + col) = v;
 }
 
+// Scatter-add of one table column with a per-thread cache of four (id, sum)
+// pairs.  A thread walks its column down a run of rows in order; rows that
+// share an id (padding ids, the few zones / owners / option types, frequent
+// cards) add in registers, and the table sees one atomic per eviction
+// instead of one per row — the reference's per-element atomics serialise on
+// such hot rows.  Zero gradients (masked options, padding) are skipped.
+struct IdCache {
+    int id0 = -1, id1 = -1, id2 = -1, id3 = -1;
+    float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+    int next = 0;
+    __device__ __forceinline__ static void put(float* tab, long ld, int col, int id, float a) {
+        if (id >= 0 && a != 0.f) atomicAdd(tab + (long)id * ld + col, a);
+    }
+    __device__ __forceinline__ void add(float* tab, long ld, int col, int id, float g) {
+        if (g == 0.f) return;
+        if (id == id0) { a0 += g; return; }
+        if (id == id1) { a1 += g; return; }
+        if (id == id2) { a2 += g; return; }
+        if (id == id3) { a3 += g; return; }
+        if (next == 0) { put(tab, ld, col, id0, a0); id0 = id; a0 = g; }
+        else if (next == 1) { put(tab, ld, col, id1, a1); id1 = id; a1 = g; }
+        else if (next == 2) { put(tab, ld, col, id2, a2); id2 = id; a2 = g; }
+        else { put(tab, ld, col, id3, a3); id3 = id; a3 = g; }
+        next = (next + 1) & 3;
+    }
+    __device__ __forceinline__ void flush(float* tab, long ld, int col) {
+        put(tab, ld, col, id0, a0);
+        put(tab, ld, col, id1, a1);
+        put(tab, ld, col, id2, a2);
+        put(tab, ld, col, id3, a3);
+    }
+};
+
+// rows per workgroup of the column-owner scatters
+constexpr int SCATTER_ROWS = 32;
+
+// token concat backward: thread = one gradient-bearing column (card | tool
+// card | zone | owner; the numeric features are inputs), workgroup = a run
+// of SCATTER_ROWS token rows
 __global__ void tok_cat_bwd_kernel(GatherCtx c, const float* __restrict__ d_cat, float* d_card,
                                    float* d_zemb, float* d_oemb) {
     const int Lt = c.dm.l_tok, dc = c.dm.d_c, tin = c.dx.tok_in;
-    const long i = (long)blockIdx.x * TB + threadIdx.x;
+    const int zc = 2 * dc + c.dm.tok_f;   // first zone column of the concat
+    const int q = threadIdx.x;
+    if (q >= 2 * dc + PT_ZONE_E + PT_OWNER_E) return;
+    const int col = q < 2 * dc ? q : zc + (q - 2 * dc);
     const long nrows = c.rowmap ? (long)*c.rows : (long)c.N * Lt;
-    if (i >= nrows * tin) return;
-    const int col = (int)(i % tin);
-    const long r = i / tin;
-    const float g = d_cat[i];
-    if (g == 0.f) return;
-    int n, t;
-    if (c.rowmap) {
-        n = c.rsam[r];
-        t = c.rpos[r] - 1;
-        if (t < 0) return;
-    } else {
-        n = (int)(r / Lt);
-        t = (int)(r % Lt);
-    }
-    const float* ti = obs_row(c.obs, c.idx, c.stride, n) + c.off.tok_int + (long)t * c.dm.tok_int;
+    const long r0 = (long)blockIdx.x * SCATTER_ROWS, r1 = min(nrows, r0 + SCATTER_ROWS);
     const int NC = c.dm.n_cards;
-    if (col < dc) {
-        atomicAdd(d_card + (long)pt_id_clamp(ti[0], NC - 1) * dc + col, g);
-    } else if (col < 2 * dc) {
-        const int e = col - dc;
-        const int t0 = (int)ti[3], t1 = (int)ti[4];
-        if (t0 > 0) atomicAdd(d_card + (long)(t0 >= NC ? NC - 1 : t0) * dc + e, g);
-        if (t1 > 0) atomicAdd(d_card + (long)(t1 >= NC ? NC - 1 : t1) * dc + e, g);
-    } else if (col < 2 * dc + c.dm.tok_f) {
-        // numeric features are inputs: no gradient
-    } else if (col < 2 * dc + c.dm.tok_f + PT_ZONE_E) {
-        const int z = pt_id_clamp(ti[1], c.dm.n_zones - 1);
-        atomicAdd(d_zemb + z * PT_ZONE_E + (col - 2 * dc - c.dm.tok_f), g);
-    } else {
-        const int o = pt_id_clamp(ti[2], c.dm.n_owners - 1);
-        atomicAdd(d_oemb + o * PT_OWNER_E + (col - 2 * dc - c.dm.tok_f - PT_ZONE_E), g);
+    IdCache k0, k1;   // k1: the second tool card
+    float* tab;
+    long ld;
+    int tc;
+    if (q < 2 * dc) { tab = d_card; ld = dc; tc = q < dc ? q : q - dc; }
+    else if (q < 2 * dc + PT_ZONE_E) { tab = d_zemb; ld = PT_ZONE_E; tc = q - 2 * dc; }
+    else { tab = d_oemb; ld = PT_OWNER_E; tc = q - 2 * dc - PT_ZONE_E; }
+    for (long r = r0; r < r1; ++r) {
+        const float g = d_cat[r * tin + col];
+        if (g == 0.f) continue;
+        int n, t;
+        if (c.rowmap) {
+            n = c.rsam[r];
+            t = c.rpos[r] - 1;
+            if (t < 0) continue;
+        } else {
+            n = (int)(r / Lt);
+            t = (int)(r % Lt);
+        }
+        const float* ti = obs_row(c.obs, c.idx, c.stride, n) + c.off.tok_int + (long)t * c.dm.tok_int;
+        if (q < dc) {
+            k0.add(tab, ld, tc, pt_id_clamp(ti[0], NC - 1), g);
+        } else if (q < 2 * dc) {
+            const int t0 = (int)ti[3], t1 = (int)ti[4];
+            if (t0 > 0) k0.add(tab, ld, tc, t0 >= NC ? NC - 1 : t0, g);
+            if (t1 > 0) k1.add(tab, ld, tc, t1 >= NC ? NC - 1 : t1, g);
+        } else if (q < 2 * dc + PT_ZONE_E) {
+            k0.add(tab, ld, tc, pt_id_clamp(ti[1], c.dm.n_zones - 1), g);
+        } else {
+            k0.add(tab, ld, tc, pt_id_clamp(ti[2], c.dm.n_owners - 1), g);
+        }
     }
+    k0.flush(tab, ld, tc);
+    k1.flush(tab, ld, tc);
 }
 
 __global__ void glob_in_kernel(GatherCtx c, float* __restrict__ out) {
@@ -155,21 +204,32 @@ __global__ void dec_in_fwd_kernel(GatherCtx c, const float* __restrict__ card,
     out[i] = v;
 }
 
+// decision concat backward: thread = column, workgroup = (column block, a
+// run of SCATTER_ROWS samples)
 __global__ void dec_in_bwd_kernel(GatherCtx c, const float* __restrict__ d_in, float* d_card,
                                   float* d_att, float* d_semb, float* d_cemb) {
     const int W = c.dx.dec_in;
-    const long i = (long)blockIdx.x * TB + threadIdx.x;
-    if (i >= (long)c.N * W) return;
-    const float g = d_in[i];
-    if (g == 0.f) return;
-    const int n = (int)(i / W), col = (int)(i % W);
-    const float* di_ = obs_row(c.obs, c.idx, c.stride, n) + c.off.dec_int;
+    const int col = blockIdx.x * TB + threadIdx.x;
+    if (col >= W) return;
     int kind, di, e;
     dec_locate(c, col, kind, di, e);
-    if (kind == 0) atomicAdd(d_semb + pt_id_clamp(di_[0], c.dm.n_select_types - 1) * PT_SEL_E + e, g);
-    else if (kind == 1) atomicAdd(d_cemb + pt_id_clamp(di_[1], c.dm.n_contexts - 1) * PT_CTX_E + e, g);
-    else if (kind == 2) atomicAdd(d_card + (long)pt_id_clamp(di_[di], c.dm.n_cards - 1) * c.dm.d_c + e, g);
-    else if (kind == 3) atomicAdd(d_att + (long)pt_id_clamp(di_[di], c.dm.n_attacks - 1) * c.dm.d_a + e, g);
+    if (kind == 4) return;   // numeric features: no gradient
+    float* tab;
+    long ld;
+    int hi;
+    if (kind == 0) { tab = d_semb; ld = PT_SEL_E; hi = c.dm.n_select_types - 1; }
+    else if (kind == 1) { tab = d_cemb; ld = PT_CTX_E; hi = c.dm.n_contexts - 1; }
+    else if (kind == 2) { tab = d_card; ld = c.dm.d_c; hi = c.dm.n_cards - 1; }
+    else { tab = d_att; ld = c.dm.d_a; hi = c.dm.n_attacks - 1; }
+    const int n0 = blockIdx.y * SCATTER_ROWS, n1 = min(c.N, n0 + SCATTER_ROWS);
+    IdCache k;
+    for (int n = n0; n < n1; ++n) {
+        const float g = d_in[(long)n * W + col];
+        if (g == 0.f) continue;
+        const float* di_ = obs_row(c.obs, c.idx, c.stride, n) + c.off.dec_int;
+        k.add(tab, ld, e, pt_id_clamp(di_[di], hi), g);
+    }
+    k.flush(tab, ld, e);
 }
 
 // x0[n,0] = readout; x0[n,l] = tokp[n,l-1] + bc[n]; keep[n,l] = l==0 || zone_float > 0
@@ -247,24 +307,30 @@ __global__ void opt_gather_fwd_kernel(GatherCtx c, const float* __restrict__ car
     if (e < da) oatt[nj * da + e] = att[(long)pt_id_clamp(oi[4], c.dm.n_attacks - 1) * da + e];
 }
 
+// option card / attack backward: thread = column (d_c card columns, then
+// d_a attack columns), workgroup = a run of SCATTER_ROWS options
 __global__ void opt_gather_bwd_kernel(GatherCtx c, const float* __restrict__ d_ocard,
         const float* __restrict__ d_oatt, float* d_card, float* d_att) {
     const int NO = c.dm.n_opt, dc = c.dm.d_c, da = c.dm.d_a;
-    const int W = dc > da ? dc : da;
-    const long i = (long)blockIdx.x * TB + threadIdx.x;
-    if (i >= (long)c.N * NO * W) return;
-    const int e = (int)(i % W);
-    const long nj = i / W;
-    const int n = (int)(nj / NO), j = (int)(nj % NO);
-    const float* oi = obs_row(c.obs, c.idx, c.stride, n) + c.off.opt_int + (long)j * c.dm.opt_int;
-    if (e < dc) {
-        const float g = d_ocard[nj * dc + e];
-        if (g != 0.f) atomicAdd(d_card + (long)pt_id_clamp(oi[3], c.dm.n_cards - 1) * dc + e, g);
+    const int q = threadIdx.x;
+    if (q >= dc + da) return;
+    const bool is_card = q < dc;
+    const int e = is_card ? q : q - dc;
+    const int w = is_card ? dc : da;
+    const float* src = is_card ? d_ocard : d_oatt;
+    float* tab = is_card ? d_card : d_att;
+    const int hi = is_card ? c.dm.n_cards - 1 : c.dm.n_attacks - 1;
+    const int slot = is_card ? 3 : 4;
+    const long nj0 = (long)blockIdx.x * SCATTER_ROWS, nj1 = min((long)c.N * NO, nj0 + SCATTER_ROWS);
+    IdCache k;
+    for (long nj = nj0; nj < nj1; ++nj) {
+        const float g = src[nj * w + e];
+        if (g == 0.f) continue;
+        const int n = (int)(nj / NO), j = (int)(nj % NO);
+        const float* oi = obs_row(c.obs, c.idx, c.stride, n) + c.off.opt_int + (long)j * c.dm.opt_int;
+        k.add(tab, w, e, pt_id_clamp(oi[slot], hi), g);
     }
-    if (e < da) {
-        const float g = d_oatt[nj * da + e];
-        if (g != 0.f) atomicAdd(d_att + (long)pt_id_clamp(oi[4], c.dm.n_attacks - 1) * da + e, g);
-    }
+    k.flush(tab, w, e);
 }
 
 // q_in = [temb16 | h(p1) | h(p2) | (opt_card, opt_attack GEMM outputs) | opt_f]
@@ -295,29 +361,37 @@ __global__ void q_in_fwd_kernel(GatherCtx c, const float* __restrict__ h,
     *reinterpret_cast<float4*>(q_in + nj * W + col) = v;
 }
 
-// one workgroup per sample, options in order: d_h[n,p] += d_qin pointer slices
+// one workgroup per sample: d_h[n,p] += d_qin pointer slices.  A thread
+// owns its columns, so no two threads add to one element; the adds are
+// no-return atomics so successive options do not wait on each other's
+// read-modify-write.  Option types (few, hot) go through an id cache.
 __global__ void q_in_bwd_kernel(GatherCtx c, const float* __restrict__ d_qin, float* __restrict__ d_h,
                                 float* d_temb) {
     const int n = blockIdx.x, NO = c.dm.n_opt, D = c.dm.d, W = c.dx.q_in;
     const float* row = obs_row(c.obs, c.idx, c.stride, n);
-    for (int j = 0; j < NO; ++j) {
-        const float* oi = row + c.off.opt_int + (long)j * c.dm.opt_int;
-        const float* g = d_qin + ((long)n * NO + j) * W;
-        const int p1 = (int)oi[1], p2 = (int)oi[2];
-        const bool v1 = p1 > 0 && p1 <= c.dm.l_tok, v2 = p2 > 0 && p2 <= c.dm.l_tok;
-        for (int col = threadIdx.x; col < D; col += TB) {
-            if (v1) d_h[pt_hrow(c, n, p1) * D + col] += g[PT_TYPE_E + col];
+    for (int col = threadIdx.x; col < D; col += TB) {
+        for (int j = 0; j < NO; ++j) {
+            const float* oi = row + c.off.opt_int + (long)j * c.dm.opt_int;
+            const float* g = d_qin + ((long)n * NO + j) * W;
+            const int p1 = (int)oi[1], p2 = (int)oi[2];
+            if (p1 > 0 && p1 <= c.dm.l_tok) {
+                const float v = g[PT_TYPE_E + col];
+                if (v != 0.f) atomicAdd(d_h + pt_hrow(c, n, p1) * D + col, v);
+            }
+            if (p2 > 0 && p2 <= c.dm.l_tok) {
+                const float v = g[PT_TYPE_E + D + col];
+                if (v != 0.f) atomicAdd(d_h + pt_hrow(c, n, p2) * D + col, v);
+            }
         }
-        __syncthreads();
-        for (int col = threadIdx.x; col < D; col += TB) {
-            if (v2) d_h[pt_hrow(c, n, p2) * D + col] += g[PT_TYPE_E + D + col];
+    }
+    if (threadIdx.x < PT_TYPE_E) {
+        IdCache k;
+        for (int j = 0; j < NO; ++j) {
+            const float* oi = row + c.off.opt_int + (long)j * c.dm.opt_int;
+            k.add(d_temb, PT_TYPE_E, threadIdx.x, pt_id_clamp(oi[0], c.dm.n_opt_types - 1),
+                  d_qin[((long)n * NO + j) * W + threadIdx.x]);
         }
-        if (threadIdx.x < PT_TYPE_E) {
-            const float gt = g[threadIdx.x];
-            if (gt != 0.f)
-                atomicAdd(d_temb + pt_id_clamp(oi[0], c.dm.n_opt_types - 1) * PT_TYPE_E + threadIdx.x, gt);
-        }
-        __syncthreads();
+        k.flush(d_temb, PT_TYPE_E, threadIdx.x);
     }
 }
 
@@ -345,17 +419,23 @@ __global__ void sc_in_fwd_kernel(GatherCtx c, const float* __restrict__ h,
     *reinterpret_cast<float4*>(o + col) = v;
 }
 
-// one workgroup per sample: d_q = dsc[q] + dsc[qr]*r ; d_r, d_g, d_dvec summed over options
-__global__ void sc_in_bwd_kernel(GatherCtx c, const float* __restrict__ d_sc,
+// one workgroup per sample: d_q = dsc[q] + dsc[qr]*r ; d_r, d_g, d_dvec summed
+// over options.  SC_OG option groups of TB threads each sum a contiguous
+// quarter of the options; the group partials add in a fixed order.
+constexpr int SC_OG = 4;
+__global__ __launch_bounds__(TB * SC_OG) void sc_in_bwd_kernel(GatherCtx c, const float* __restrict__ d_sc,
         const float* __restrict__ sc, float* __restrict__ d_q, float* __restrict__ d_h,
         float* __restrict__ d_gd) {
+    extern __shared__ float red[];   // [3][SC_OG][span]
     const int n = blockIdx.x, NO = c.dm.n_opt, D = c.dm.d, G = c.dm.g, W = c.dx.score_in;
     const int o_r = D, o_g = 2 * D, o_dv = 2 * D + G, o_qr = 2 * D + G + PT_DEC_H;
     const int span = max(D, max(G, (int)PT_DEC_H));
-    for (int col = threadIdx.x; col < span; col += TB) {
+    const int og = threadIdx.x / TB, t = threadIdx.x % TB;
+    const int j0 = og * NO / SC_OG, j1 = (og + 1) * NO / SC_OG;
+    for (int col = t; col < span; col += TB) {
         const float r = col < D ? sc[(long)n * NO * W + o_r + col] : 0.f;
         float ar = 0.f, ag = 0.f, adv = 0.f;
-        for (int j = 0; j < NO; ++j) {
+        for (int j = j0; j < j1; ++j) {
             const long nj = (long)n * NO + j;
             const float* g = d_sc + nj * W;
             if (col < D) {
@@ -365,6 +445,19 @@ __global__ void sc_in_bwd_kernel(GatherCtx c, const float* __restrict__ d_sc,
             }
             if (col < G) ag += g[o_g + col];
             if (col < PT_DEC_H) adv += g[o_dv + col];
+        }
+        red[(0 * SC_OG + og) * span + col] = ar;
+        red[(1 * SC_OG + og) * span + col] = ag;
+        red[(2 * SC_OG + og) * span + col] = adv;
+    }
+    __syncthreads();
+    if (og != 0) return;
+    for (int col = t; col < span; col += TB) {
+        float ar = 0.f, ag = 0.f, adv = 0.f;
+        for (int k = 0; k < SC_OG; ++k) {
+            ar += red[(0 * SC_OG + k) * span + col];
+            ag += red[(1 * SC_OG + k) * span + col];
+            adv += red[(2 * SC_OG + k) * span + col];
         }
         if (col < D) d_h[pt_hrow(c, n, 0) * D + col] += ar;
         if (col < G) d_gd[(long)n * c.dx.bcast_in + col] += ag;
@@ -466,7 +559,10 @@ int pt_tok_cat_fwd(const GatherCtx& c, const float* card, const float* zemb, con
 int pt_tok_cat_bwd(const GatherCtx& c, const float* d_cat, float* d_card, float* d_zemb, float* d_oemb,
                    hipStream_t s) {
     const long rows = c.rowmap ? (long)c.N * c.dx.l_seq : (long)c.N * c.dm.l_tok;
-    hipLaunchKernelGGL(tok_cat_bwd_kernel, PT_GRID(rows * c.dx.tok_in), c, d_cat, d_card, d_zemb, d_oemb);
+    const int cols = 2 * c.dm.d_c + PT_ZONE_E + PT_OWNER_E;
+    PT_REQUIRE(cols <= 1024, "tok_cat_bwd: %d gradient columns", cols);
+    hipLaunchKernelGGL(tok_cat_bwd_kernel, dim3(pt_cdiv(rows, SCATTER_ROWS)), dim3(pt_cdiv(cols, 64) * 64), 0, s, c,
+                       d_cat, d_card, d_zemb, d_oemb);
     PT_LAUNCH_CHECK();
     return PTCG_OK;
 }
@@ -483,7 +579,8 @@ int pt_dec_in_fwd(const GatherCtx& c, const float* card, const float* att, const
 }
 int pt_dec_in_bwd(const GatherCtx& c, const float* d_in, float* d_card, float* d_att, float* d_semb,
                   float* d_cemb, hipStream_t s) {
-    hipLaunchKernelGGL(dec_in_bwd_kernel, PT_GRID((long)c.N * c.dx.dec_in), c, d_in, d_card, d_att, d_semb, d_cemb);
+    hipLaunchKernelGGL(dec_in_bwd_kernel, dim3(pt_cdiv(c.dx.dec_in, TB), pt_cdiv(c.N, SCATTER_ROWS)), dim3(TB), 0, s,
+                       c, d_in, d_card, d_att, d_semb, d_cemb);
     PT_LAUNCH_CHECK();
     return PTCG_OK;
 }
@@ -507,8 +604,10 @@ int pt_opt_gather_fwd(const GatherCtx& c, const float* card, const float* att, f
 }
 int pt_opt_gather_bwd(const GatherCtx& c, const float* d_ocard, const float* d_oatt, float* d_card,
                       float* d_att, hipStream_t s) {
-    const int W = c.dm.d_c > c.dm.d_a ? c.dm.d_c : c.dm.d_a;
-    hipLaunchKernelGGL(opt_gather_bwd_kernel, PT_GRID((long)c.N * c.dm.n_opt * W), c, d_ocard, d_oatt, d_card, d_att);
+    const int cols = c.dm.d_c + c.dm.d_a;
+    PT_REQUIRE(cols <= 1024, "opt_gather_bwd: %d columns", cols);
+    hipLaunchKernelGGL(opt_gather_bwd_kernel, dim3(pt_cdiv((long)c.N * c.dm.n_opt, SCATTER_ROWS)),
+                       dim3(pt_cdiv(cols, 64) * 64), 0, s, c, d_ocard, d_oatt, d_card, d_att);
     PT_LAUNCH_CHECK();
     return PTCG_OK;
 }
@@ -531,7 +630,9 @@ int pt_sc_in_fwd(const GatherCtx& c, const float* h, const float* gd, float* sc_
 }
 int pt_sc_in_bwd(const GatherCtx& c, const float* d_sc, const float* sc_in, float* d_q, float* d_h,
                  float* d_gd, hipStream_t s) {
-    hipLaunchKernelGGL(sc_in_bwd_kernel, dim3(c.N), dim3(TB), 0, s, c, d_sc, sc_in, d_q, d_h, d_gd);
+    const int span = std::max(c.dm.d, std::max(c.dm.g, (int)PT_DEC_H));
+    hipLaunchKernelGGL(sc_in_bwd_kernel, dim3(c.N), dim3(TB * SC_OG), 3 * SC_OG * span * sizeof(float), s, c, d_sc,
+                       sc_in, d_q, d_h, d_gd);
     PT_LAUNCH_CHECK();
     return PTCG_OK;
 }

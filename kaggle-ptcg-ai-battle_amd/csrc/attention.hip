@@ -46,8 +46,10 @@ __global__ __launch_bounds__(512) void attn_fwd_mfma_kernel(const float* __restr
     const long rb = coff ? (long)coff[n] : (long)n * Lfix;
     const int L = coff ? coff[n + 1] - coff[n] : Lfix;
     const int D = H * DH;
+    // this sample's tiles (compact rows vary in length; the template covers the longest)
+    const int ntl = min(NT, (L + 15) / 16);
     const gfloat* base = (const gfloat*)qkv + rb * 3 * D + h * DH;
-    for (int idx = tid; idx < LP * (DH / 4); idx += 512) {
+    for (int idx = tid; idx < ntl * 16 * (DH / 4); idx += 512) {
         const int l = idx / (DH / 4), c4 = (idx % (DH / 4)) * 4;
         float4 k4 = make_float4(0.f, 0.f, 0.f, 0.f), v4 = k4;
         if (l < L) {
@@ -61,7 +63,7 @@ __global__ __launch_bounds__(512) void attn_fwd_mfma_kernel(const float* __restr
     for (int l = tid; l < LP; l += 512) kf[l] = l < L ? (keep[rb + l] != 0.f ? 1.f : 0.f) : -1.f;
     __syncthreads();
 
-    for (int st = wave; st < NT; st += 8) {
+    for (int st = wave; st < ntl; st += 8) {
         const int q0 = st * 16;
         // Q^T as the B operand: lane (li = query, lq) holds Q[q0+li][4kk+lq]
         float qb[DH / 4];
@@ -77,12 +79,12 @@ __global__ __launch_bounds__(512) void attn_fwd_mfma_kernel(const float* __restr
         constexpr int CH = NT < 8 ? NT : 8;
         float mx = -INFINITY, sum = 0.f;
 #pragma unroll 1
-        for (int c0 = 0; c0 < NT; c0 += CH) {
+        for (int c0 = 0; c0 < ntl; c0 += CH) {
             floatx4 sc[CH];
 #pragma unroll
             for (int j = 0; j < CH; ++j) {
                 sc[j] = floatx4{0.f, 0.f, 0.f, 0.f};
-                if (c0 + j < NT) {
+                if (c0 + j < ntl) {
 #pragma unroll
                     for (int kk = 0; kk < DH / 4; ++kk)
                         sc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(Ks[(16 * (c0 + j) + li) * SK + 4 * kk + lq], qb[kk],
@@ -95,7 +97,7 @@ __global__ __launch_bounds__(512) void attn_fwd_mfma_kernel(const float* __restr
             for (int j = 0; j < CH; ++j)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    const float f = c0 + j < NT ? kf[16 * (c0 + j) + 4 * lq + r] : -1.f;
+                    const float f = c0 + j < ntl ? kf[16 * (c0 + j) + 4 * lq + r] : -1.f;
                     const float v = f > 0.f ? sc[j][r] * scale : (f == 0.f ? -1e30f : -INFINITY);
                     sc[j][r] = v;
                     cm = fmaxf(cm, v);
@@ -129,7 +131,7 @@ __global__ __launch_bounds__(512) void attn_fwd_mfma_kernel(const float* __restr
             // O += P V over the permuted key order
 #pragma unroll
             for (int j = 0; j < CH; ++j) {
-                if (c0 + j < NT) {
+                if (c0 + j < ntl) {
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
                         const float* vr = &Vs[(16 * (c0 + j) + 4 * lq + r) * SK + li];
@@ -181,11 +183,13 @@ __global__ __launch_bounds__(512) void attn_bwd_mfma_kernel(const float* __restr
     const long rb = coff ? (long)coff[n] : (long)n * Lfix;
     const int L = coff ? coff[n + 1] - coff[n] : Lfix;
     const int D = H * DH;
+    // this sample's tiles (compact rows vary in length; the template covers the longest)
+    const int ntl = min(NT, (L + 15) / 16);
     const gfloat* base = (const gfloat*)qkv + rb * 3 * D + h * DH;
     const gfloat* ob = (const gfloat*)ctx + rb * D + h * DH;
     const gfloat* dob = (const gfloat*)dctx + rb * D + h * DH;
     gfloat* gb = (gfloat*)dqkv + rb * 3 * D + h * DH;
-    for (int idx = tid; idx < LP * (DH / 4); idx += 512) {
+    for (int idx = tid; idx < ntl * 16 * (DH / 4); idx += 512) {
         const int l = idx / (DH / 4), c4 = (idx % (DH / 4)) * 4;
         float4 q4 = make_float4(0.f, 0.f, 0.f, 0.f), k4 = q4, d4 = q4;
         if (l < L) {
@@ -203,7 +207,7 @@ __global__ __launch_bounds__(512) void attn_bwd_mfma_kernel(const float* __restr
         ls[l] = l < L ? lse[((long)n * H + h) * Lfix + l] : INFINITY;
     }
     // Dv[q] = sum_d dO[q][d] O[q][d]   (a wave per row; padded rows 0)
-    for (int q = wave; q < LP; q += 8) {
+    for (int q = wave; q < ntl * 16; q += 8) {
         float v = 0.f;
         if (q < L)
             for (int d = lane; d < DH; d += 64) v += dob[(long)q * D + d] * ob[(long)q * D + d];
@@ -213,7 +217,7 @@ __global__ __launch_bounds__(512) void attn_bwd_mfma_kernel(const float* __restr
     __syncthreads();
 
     // ---- pass A: key stripes
-    for (int kb = wave; kb < NT; kb += 8) {
+    for (int kb = wave; kb < ntl; kb += 8) {
         const int k0 = kb * 16;
         const bool kv = k0 + li < L;
         float kr[DH / 4], vr[DH / 4];    // B operands: lane (li = key, lq) holds K/V[k0+li][4kk+lq]
@@ -229,7 +233,7 @@ __global__ __launch_bounds__(512) void attn_bwd_mfma_kernel(const float* __restr
             dv[dt] = floatx4{0.f, 0.f, 0.f, 0.f};
             dk[dt] = dv[dt];
         }
-        for (int qt = 0; qt < NT; ++qt) {
+        for (int qt = 0; qt < ntl; ++qt) {
             floatx4 s = floatx4{0.f, 0.f, 0.f, 0.f}, dp = s;
 #pragma unroll
             for (int kk = 0; kk < DH / 4; ++kk) {
@@ -273,11 +277,11 @@ __global__ __launch_bounds__(512) void attn_bwd_mfma_kernel(const float* __restr
     __syncthreads();
 
     // ---- pass B: query stripes, dQ = (dS*scale) K
-    for (int qt = wave; qt < NT; qt += 8) {
+    for (int qt = wave; qt < ntl; qt += 8) {
         floatx4 dq[DH / 16];
 #pragma unroll
         for (int dt = 0; dt < DH / 16; ++dt) dq[dt] = floatx4{0.f, 0.f, 0.f, 0.f};
-        for (int kk = 0; kk < NT * 4; ++kk) {
+        for (int kk = 0; kk < ntl * 4; ++kk) {
             const float a = dSs[(16 * qt + li) * SS + 4 * kk + lq];
             const float* kr = &Ks[(4 * kk + lq) * SKB + li];
 #pragma unroll

@@ -128,14 +128,55 @@ __device__ __forceinline__ float4 ld_scalar4(const gfloat* X, long ld, int lim, 
     return v;
 }
 
+// Epilogues with a residual / pre-activation operand or the GELU: the tile
+// goes through LDS in two 64-row halves and a rolled loop applies the
+// epilogue to row-contiguous float4s (one GELU body instead of 64 inlined
+// copies, whose code would not fit the instruction cache; R is read 512 B
+// per row).  Staging layout [64][SST]; half h holds the rows
+// wm + 32h .. wm + 32h + 31 of both wave rows.
+constexpr int SST = BN + 4;
+constexpr int STAGE_FLOATS = 64 * SST;
+template <int EPI> struct EpiStaged {
+    static constexpr bool value = EPI == EPI_BIAS_GELU || EPI == EPI_GELU_BWD || EPI == EPI_BIAS_RESID;
+};
+
+template <int EPI>
+__device__ __forceinline__ void epilogue_staged(const GemmArgs& g, floatx4 (&acc)[4][4], int m0, int n0, int wm,
+                                                int wn, int li, int lq, float* stage, bool vo) {
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        __syncthreads();   // the stage is free (main loop done / previous half consumed)
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+            for (int tj = 0; tj < 4; ++tj)
+                *reinterpret_cast<floatx4*>(stage + ((wm >> 6) * 32 + u * 16 + li) * SST + wn + tj * 16 + 4 * lq) =
+                    acc[2 * h + u][tj];
+        __syncthreads();
+        for (int it = tid; it < 64 * (BN / 4); it += NT) {
+            const int lr = it / (BN / 4), c = (it % (BN / 4)) * 4;
+            const int m = m0 + (lr >> 5) * 64 + 32 * h + (lr & 31), n = n0 + c;
+            if (m >= g.M || n >= g.N) continue;
+            const floatx4 v = *reinterpret_cast<const floatx4*>(stage + lr * SST + c);
+            if (vo && n + 3 < g.N) {
+                epi_store4<EPI>(g, m, n, v);
+            } else {
+                for (int r = 0; r < 4 && n + r < g.N; ++r) epi_store<EPI>(g, m, n + r, v[r]);
+            }
+        }
+    }
+}
+
 // Epilogue shared by the fp32 and bf16 kernels.  The MFMAs take the B tile
 // as their first operand, so acc[ti][tj][r] holds the transposed product
 // C[wm + ti*16 + li][wn + tj*16 + 4*lq + r] of the block tile at (m0, n0):
 // four consecutive columns of one row per lane, stored (and the bias /
 // residual / pre-activation read) as one 128-bit access when aligned.
+// stage: STAGE_FLOATS of LDS the main loop no longer uses.
 template <int EPI, bool PARTIAL>
 __device__ __forceinline__ void gemm_epilogue(const GemmArgs& g, floatx4 (&acc)[4][4], int m0, int n0, int wm,
-                                              int wn, int li, int lq, long part_stride) {
+                                              int wn, int li, int lq, long part_stride, float* stage) {
     if (PARTIAL && g.tail_part) {
         // tile-local partial [split][tile - tile0][BM][BN] (no bounds: the reduce masks)
         const int tn = (g.N + BN - 1) / BN;
@@ -152,6 +193,10 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& g, floatx4 (&acc)[
                                  : (uintptr_t)g.C | (uintptr_t)g.C2 | (uintptr_t)g.R | (uintptr_t)g.bias |
                                        (uintptr_t)((g.ldc | g.ldc2 | g.ldr) * 4);
     const bool vo = (al & 15) == 0;
+    if (!PARTIAL && EpiStaged<EPI>::value) {
+        epilogue_staged<EPI>(g, acc, m0, n0, wm, wn, li, lq, stage, vo);
+        return;
+    }
 #pragma unroll
     for (int ti = 0; ti < 4; ++ti) {
         const int m = m0 + wm + ti * 16 + li;
@@ -180,8 +225,12 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& g, floatx4 (&acc)[
 // VEC: operands satisfy the 128-bit load rules (else scalar loads).
 template <bool AT, bool BT, int EPI, bool PARTIAL, bool DB, bool VEC>
 __global__ __launch_bounds__(NT) void gemm_f32_kernel(const GemmArgs g, int k_chunk, long part_stride) {
-    __shared__ __align__(16) float As[2][Stage<AT>::floats];
-    __shared__ __align__(16) float Bs[2][Stage<BT>::floats];
+    // one LDS array: the operand stages, reused by the staged epilogue
+    constexpr int SMEM = 2 * (Stage<AT>::floats + Stage<BT>::floats);
+    static_assert(SMEM >= STAGE_FLOATS, "epilogue stage does not fit the operand stages");
+    __shared__ __align__(16) float smem[SMEM];
+    float (*As)[Stage<AT>::floats] = reinterpret_cast<float (*)[Stage<AT>::floats]>(smem);
+    float (*Bs)[Stage<BT>::floats] = reinterpret_cast<float (*)[Stage<BT>::floats]>(smem + 2 * Stage<AT>::floats);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int tn = (g.N + BN - 1) / BN;
     int tmi, tni;
@@ -285,7 +334,7 @@ __global__ __launch_bounds__(NT) void gemm_f32_kernel(const GemmArgs g, int k_ch
         }
     }
 
-    gemm_epilogue<EPI, PARTIAL>(g, acc, m0, n0, wm, wn, li, lq, part_stride);
+    gemm_epilogue<EPI, PARTIAL>(g, acc, m0, n0, wm, wn, li, lq, part_stride, smem);
 }
 
 // ---------------------------------------------------------------- bf16
@@ -345,8 +394,11 @@ __device__ __forceinline__ void bf_store(__bf16* S, int tid, const float4 (&v)[4
 
 template <bool AT, bool BT, int EPI, bool PARTIAL>
 __global__ __launch_bounds__(NT) void gemm_bf16_kernel(const GemmArgs g, int k_chunk, long part_stride) {
-    __shared__ __align__(16) __bf16 As[2][BM * SKB2];
-    __shared__ __align__(16) __bf16 Bs[2][BN * SKB2];
+    constexpr int SMEM = 2 * (BM + BN) * SKB2 / 2;   // floats
+    static_assert(SMEM >= STAGE_FLOATS, "epilogue stage does not fit the operand stages");
+    __shared__ __align__(16) float smem[SMEM];
+    __bf16 (*As)[BM * SKB2] = reinterpret_cast<__bf16 (*)[BM * SKB2]>(smem);
+    __bf16 (*Bs)[BN * SKB2] = reinterpret_cast<__bf16 (*)[BN * SKB2]>(smem + BM * SKB2);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int tn = (g.N + BN - 1) / BN;
     int tmi, tni;
@@ -396,7 +448,7 @@ __global__ __launch_bounds__(NT) void gemm_bf16_kernel(const GemmArgs g, int k_c
             buf ^= 1;
         }
     }
-    gemm_epilogue<EPI, PARTIAL>(g, acc, m0, n0, wm, wn, li, lq, part_stride);
+    gemm_epilogue<EPI, PARTIAL>(g, acc, m0, n0, wm, wn, li, lq, part_stride, smem);
 }
 
 // out[m][n] (=|+=) sum_s part[s][m][n], fixed order over s

@@ -189,30 +189,30 @@ __global__ __launch_bounds__(512) void attn_bwd_mfma_kernel(const float* __restr
     const gfloat* ob = (const gfloat*)ctx + rb * D + h * DH;
     const gfloat* dob = (const gfloat*)dctx + rb * D + h * DH;
     gfloat* gb = (gfloat*)dqkv + rb * 3 * D + h * DH;
+    // stage Q, dO, K and form Dv[q] = sum_d dO[q][d] O[q][d]: the DH/4 lanes
+    // holding a row's 4-column partials are adjacent (512 is a multiple of
+    // DH/4), so a butterfly over them gives the row sum (padded rows 0)
     for (int idx = tid; idx < ntl * 16 * (DH / 4); idx += 512) {
         const int l = idx / (DH / 4), c4 = (idx % (DH / 4)) * 4;
-        float4 q4 = make_float4(0.f, 0.f, 0.f, 0.f), k4 = q4, d4 = q4;
+        float4 q4 = make_float4(0.f, 0.f, 0.f, 0.f), k4 = q4, d4 = q4, o4 = q4;
         if (l < L) {
             const gfloat* r = base + (long)l * 3 * D + c4;
             q4 = ld_g4(r);
             k4 = ld_g4(r + D);
             d4 = ld_g4(dob + (long)l * D + c4);
+            o4 = ld_g4(ob + (long)l * D + c4);
         }
         *reinterpret_cast<float4*>(&Qs[l * SQ + c4]) = q4;
         *reinterpret_cast<float4*>(&dOs[l * SQ + c4]) = d4;
         *reinterpret_cast<float4*>(&Ks[l * SKB + c4]) = k4;
+        float part = ((d4.x * o4.x + d4.y * o4.y) + d4.z * o4.z) + d4.w * o4.w;
+#pragma unroll
+        for (int o = 1; o < DH / 4; o <<= 1) part += __shfl_xor(part, o, 64);
+        if (c4 == 0) Dv[l] = part;
     }
     for (int l = tid; l < LP; l += 512) {
         kf[l] = l < L ? (keep[rb + l] != 0.f ? 1.f : 0.f) : 0.f;
         ls[l] = l < L ? lse[((long)n * H + h) * Lfix + l] : INFINITY;
-    }
-    // Dv[q] = sum_d dO[q][d] O[q][d]   (a wave per row; padded rows 0)
-    for (int q = wave; q < ntl * 16; q += 8) {
-        float v = 0.f;
-        if (q < L)
-            for (int d = lane; d < DH; d += 64) v += dob[(long)q * D + d] * ob[(long)q * D + d];
-        v = wave_sum(v);
-        if (lane == 0) Dv[q] = v;
     }
     __syncthreads();
 
@@ -333,29 +333,28 @@ __global__ __launch_bounds__(512) void attn_bwd_mfma_rc_kernel(const float* __re
     gfloat* gb = (gfloat*)dqkv + rb * 3 * D + h * DH;
     for (int idx = tid; idx < LP * (DH / 4); idx += 512) {
         const int l = idx / (DH / 4), c4 = (idx % (DH / 4)) * 4;
-        float4 q4 = make_float4(0.f, 0.f, 0.f, 0.f), k4 = q4, v4 = q4, d4 = q4;
+        float4 q4 = make_float4(0.f, 0.f, 0.f, 0.f), k4 = q4, v4 = q4, d4 = q4, o4 = q4;
         if (l < L) {
             const gfloat* r = base + (long)l * 3 * D + c4;
             q4 = ld_g4(r);
             k4 = ld_g4(r + D);
             v4 = ld_g4(r + 2 * D);
             d4 = ld_g4(dob + (long)l * D + c4);
+            o4 = ld_g4(ob + (long)l * D + c4);
         }
         *reinterpret_cast<float4*>(&Qs[l * SQ + c4]) = q4;
         *reinterpret_cast<float4*>(&dOs[l * SQ + c4]) = d4;
         *reinterpret_cast<float4*>(&Ks[l * SQ + c4]) = k4;
         *reinterpret_cast<float4*>(&Vs[l * SQ + c4]) = v4;
+        // Dv[l] = sum_d dO[l][d] O[l][d]: butterfly over the row's DH/4 adjacent lanes
+        float part = ((d4.x * o4.x + d4.y * o4.y) + d4.z * o4.z) + d4.w * o4.w;
+#pragma unroll
+        for (int o = 1; o < DH / 4; o <<= 1) part += __shfl_xor(part, o, 64);
+        if (c4 == 0) Dv[l] = part;
     }
     for (int l = tid; l < LP; l += 512) {
         kf[l] = l < L ? (keep[rb + l] != 0.f ? 1.f : 0.f) : 0.f;
         ls[l] = l < L ? lse[((long)n * H + h) * Lfix + l] : INFINITY;
-    }
-    for (int q = wave; q < LP; q += 8) {
-        float v = 0.f;
-        if (q < L)
-            for (int d = lane; d < DH; d += 64) v += dob[(long)q * D + d] * ob[(long)q * D + d];
-        v = wave_sum(v);
-        if (lane == 0) Dv[q] = v;
     }
     __syncthreads();
 

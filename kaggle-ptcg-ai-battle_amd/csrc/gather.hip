@@ -510,28 +510,42 @@ __global__ void head_dot_bwd_kernel(const float* __restrict__ grad, int per, lon
     dX[i] = dy * w[k] * pt_gelu_grad(pre[i]);
 }
 
-constexpr int HD_ROWS = 256;
-// partial[chunk][0..K) = sum dy*X, partial[chunk][K] = sum dy
+constexpr int HD_ROWS = 64;
+// partial[chunk][0..K) = sum dy*X, partial[chunk][K] = sum dy (every thread
+// forms the dy sum alongside its column; thread 0 stores it)
 __global__ void head_dot_dw_partial_kernel(const float* __restrict__ grad, int per, long ldg,
         int col0, const float* __restrict__ X, int rows, int K, float* __restrict__ part) {
     const int r0 = blockIdx.x * HD_ROWS, r1 = min(rows, r0 + HD_ROWS);
-    for (int k = threadIdx.x; k <= K; k += TB) {
-        float s = 0.f;
+    for (int k0 = 0; k0 < K; k0 += TB) {
+        const int k = k0 + threadIdx.x;
+        float s = 0.f, sd = 0.f;
         for (int r = r0; r < r1; ++r) {
             const float dy = grad[(long)(r / per) * ldg + col0 + (r % per)];
-            s += dy * (k < K ? X[(long)r * K + k] : 1.0f);
+            sd += dy;
+            if (k < K) s += dy * X[(long)r * K + k];
         }
-        part[(long)blockIdx.x * (K + 1) + k] = s;
+        if (k < K) part[(long)blockIdx.x * (K + 1) + k] = s;
+        if (k0 == 0 && threadIdx.x == 0) part[(long)blockIdx.x * (K + 1) + K] = sd;
     }
 }
 
+// one workgroup per output column: strided chunk sums, then a fixed-order tree
 __global__ void head_dot_dw_final_kernel(const float* __restrict__ part, int chunks, int K,
                                          float* __restrict__ dw, float* __restrict__ db) {
-    const int k = blockIdx.x * TB + threadIdx.x;
-    if (k > K) return;
+    __shared__ float red[TB];
+    const int k = blockIdx.x;
     float s = 0.f;
-    for (int ch = 0; ch < chunks; ++ch) s += part[(long)ch * (K + 1) + k];
-    if (k < K) dw[k] = s; else db[0] = s;
+    for (int ch = threadIdx.x; ch < chunks; ch += TB) s += part[(long)ch * (K + 1) + k];
+    red[threadIdx.x] = s;
+    __syncthreads();
+    for (int w = TB / 2; w > 0; w >>= 1) {
+        if (threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        if (k < K) dw[k] = red[0];
+        else db[0] = red[0];
+    }
 }
 
 __global__ void fill_zero_kernel(float4* p, long n4) {
@@ -664,7 +678,7 @@ int pt_head_dot_dw(const float* grad, int per, long ldg, int col0, const float* 
     PT_REQUIRE(ws && (long)chunks * (K + 1) <= ws_floats, "head dw: workspace too small");
     hipLaunchKernelGGL(head_dot_dw_partial_kernel, dim3(chunks), dim3(TB), 0, s, grad, per, ldg, col0, X, rows, K, ws);
     PT_LAUNCH_CHECK();
-    hipLaunchKernelGGL(head_dot_dw_final_kernel, dim3(pt_cdiv(K + 1, TB)), dim3(TB), 0, s, ws, chunks, K, dw, db);
+    hipLaunchKernelGGL(head_dot_dw_final_kernel, dim3(K + 1), dim3(TB), 0, s, ws, chunks, K, dw, db);
     PT_LAUNCH_CHECK();
     return PTCG_OK;
 }

@@ -453,12 +453,15 @@ __global__ __launch_bounds__(NT) void gemm_bf16_kernel(const GemmArgs g, int k_c
 
 // out[m][n] (=|+=) sum_s part[s][m][n], fixed order over s
 // and, when db is set, db[m] = sum_s part[splits*part_stride + s*M + m]
-template <bool ACCUM>
+// V4: a thread sums 4 consecutive columns (N, ldc multiples of 4, C 16 B aligned)
+template <bool ACCUM, bool V4>
 __global__ void splitk_reduce_kernel(float* C, long ldc, const float* part, long part_stride,
                                      int splits, int M, int N, float* db) {
-    long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= (long)M * N) {
-        const long m = i - (long)M * N;
+    constexpr int W = V4 ? 4 : 1;
+    const long nq = N / W;
+    const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (long)M * nq) {
+        const long m = i - (long)M * nq;
         if (db != nullptr && m < M) {
             const float* bp = part + (long)splits * part_stride + m;
             float s = 0.f;
@@ -467,11 +470,19 @@ __global__ void splitk_reduce_kernel(float* C, long ldc, const float* part, long
         }
         return;
     }
-    int m = (int)(i / N), n = (int)(i % N);
-    long o = (long)m * ldc + n;
-    float s = 0.f;
-    for (int k = 0; k < splits; ++k) s += part[(long)k * part_stride + o];
-    if (ACCUM) C[o] += s; else C[o] = s;
+    const int m = (int)(i / nq), n = (int)(i % nq) * W;
+    const long o = (long)m * ldc + n;
+    if (V4) {
+        floatx4 s = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll 8
+        for (int k = 0; k < splits; ++k) s += ld_v4(part + (long)k * part_stride + o);
+        st_g4(C + o, ACCUM ? ld_v4(C + o) + s : s);
+    } else {
+        float s = 0.f;
+#pragma unroll 8
+        for (int k = 0; k < splits; ++k) s += part[(long)k * part_stride + o];
+        if (ACCUM) C[o] += s; else C[o] = s;
+    }
 }
 
 // Tail tiles of a balanced launch: C[tile] = epi(sum_s part[s][tile]), fixed order over s.
@@ -715,13 +726,22 @@ int pt_gemm(const GemmArgs& g, float* ws, long ws_floats, hipStream_t s) {
         else if (vec) launch_partial<true>(p, db, grid, k_chunk, part_stride, s);
         else launch_partial<false>(p, db, grid, k_chunk, part_stride, s);
         PT_LAUNCH_CHECK();
-        long tot = (long)g.M * g.N + (db ? g.M : 0);
-        if (g.epi == EPI_ACCUM)
-            hipLaunchKernelGGL(splitk_reduce_kernel<true>, dim3(pt_cdiv(tot, 256)), dim3(256), 0, s,
-                               g.C, g.ldc, ws, part_stride, splits, g.M, g.N, db ? g.dbias : nullptr);
+        const bool v4 = g.N % 4 == 0 && g.ldc % 4 == 0 && ((uintptr_t)g.C & 15) == 0;
+        const long tot = (long)g.M * (v4 ? g.N / 4 : g.N) + (db ? g.M : 0);
+        float* dbp = db ? g.dbias : nullptr;
+        const dim3 gr(pt_cdiv(tot, 256));
+        if (g.epi == EPI_ACCUM && v4)
+            hipLaunchKernelGGL((splitk_reduce_kernel<true, true>), gr, dim3(256), 0, s, g.C, g.ldc, ws, part_stride,
+                               splits, g.M, g.N, dbp);
+        else if (g.epi == EPI_ACCUM)
+            hipLaunchKernelGGL((splitk_reduce_kernel<true, false>), gr, dim3(256), 0, s, g.C, g.ldc, ws, part_stride,
+                               splits, g.M, g.N, dbp);
+        else if (v4)
+            hipLaunchKernelGGL((splitk_reduce_kernel<false, true>), gr, dim3(256), 0, s, g.C, g.ldc, ws, part_stride,
+                               splits, g.M, g.N, dbp);
         else
-            hipLaunchKernelGGL(splitk_reduce_kernel<false>, dim3(pt_cdiv(tot, 256)), dim3(256), 0, s,
-                               g.C, g.ldc, ws, part_stride, splits, g.M, g.N, db ? g.dbias : nullptr);
+            hipLaunchKernelGGL((splitk_reduce_kernel<false, false>), gr, dim3(256), 0, s, g.C, g.ldc, ws, part_stride,
+                               splits, g.M, g.N, dbp);
         PT_LAUNCH_CHECK();
         return PTCG_OK;
     }

@@ -176,7 +176,7 @@ def main():
     gemm_s = ms.value / 1e3
     achieved = useful / gemm_s / 1e12
     peak = BF16_MFMA_PEAK_TFLOPS if bf16 else FP32_MFMA_PEAK_TFLOPS
-    kname = "gemm_bf16_kernel" if bf16 else "gemm_f32_kernel"
+    kname = "gemm_bf16_kernel" if bf16 else "gemm_f32_dma_kernel + gemm_f32_kernel"
     roof = dict(bound="mfma", kernel=f"{kname} (all launches: trunk, token, option and head GEMMs)",
                 achieved=round(achieved, 3), peak=peak, unit="TFLOP/s",
                 frac=round(achieved / peak, 4), traffic=None,

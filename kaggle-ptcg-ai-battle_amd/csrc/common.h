@@ -115,6 +115,8 @@ struct GemmArgs {
     // (ntiles 0 = all); tail_part: split-K partials of those tiles go to a
     // tile-local workspace [split][tile][128 x 128]
     int tile0, ntiles, tail_part;
+    // set by pt_gemm: fp32 products through the LDS-DMA kernel
+    int dma;
 };
 
 // Launch C = epi(A*B) on `stream`. Requirements: K % 4 == 0 when the operand

@@ -337,6 +337,160 @@ __global__ __launch_bounds__(NT) void gemm_f32_kernel(const GemmArgs g, int k_ch
     gemm_epilogue<EPI, PARTIAL>(g, acc, m0, n0, wm, wn, li, lq, part_stride, smem);
 }
 
+
+// ---------------------------------------------------------------- fp32, LDS DMA
+// Operand tiles go global -> LDS with buffer_load ... lds (16 B per lane;
+// lane L writes L*16 B past the wave's LDS base), DMA_NS stages deep: no
+// staging registers, and the loads of tile i + DMA_NS - 1 are in flight
+// while tile i is multiplied.  Buffer loads return zero past the operand's
+// last element (num_records = its exact extent), which zeroes the k tail of
+// an m-contiguous operand; a k-contiguous operand needs K % BK == 0 (its row
+// tails would read the next row).  Rows / columns past M / N read what lies
+// there or zero and only reach C rows / columns that are never stored.
+// The DMA is issued from inline assembly so the compiler does not tie LDS
+// reads to the outstanding loads; the loop waits on vmcnt itself.
+constexpr int DMA_NS = 3;
+typedef int int32x4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ int32x4_t buffer_rsrc(const float* p, unsigned bytes) {
+    const unsigned long long a = (unsigned long long)p;
+    int32x4_t r;
+    r.x = (int)(unsigned)(a & 0xffffffffull);
+    r.y = (int)(unsigned)(a >> 32);   // stride 0 (canonical addresses are below 2^48)
+    r.z = (int)bytes;                 // num_records: bytes from the base
+    r.w = 0x00020000;                 // gfx9 raw buffer: 32-bit data format, no swizzle
+    return r;
+}
+__device__ __forceinline__ void dma16(int32x4_t rsrc, const float* lds_base, int voffset_bytes) {
+    const unsigned lds = (unsigned)(uintptr_t)lds_base;   // LDS offset (low bits of the generic address)
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+                 :: "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(voffset_bytes), "s"(rsrc) : "memory", "m0");
+}
+template <int N> __device__ __forceinline__ void wait_vm() {
+    if (N == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    else if (N == 4) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
+    else asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+}
+// row swizzle of the [row][k] layout: conflict-free 128-bit reads of 16 rows
+// (one k group) on 32- and 64-bank LDS, and conflict-free DMA writes
+__device__ __forceinline__ int swz(int r) { return ((r >> 1) ^ (r >> 3)) & 3; }
+// DMA LDS layouts (unpadded, 4-float groups XOR-swizzled):
+//   [row][k] (k-contiguous): element (r, k) at r*BK + 4*((k>>2) ^ swz(r)) + (k&3)
+//   [k][row] (m-contiguous): element (k, r) at k*BM + 4*((r>>2) ^ (k&4)) + (r&3)
+// The [row][k] swizzle keeps the fragment reads (16 rows, one group) on
+// distinct banks; the [k][row] one puts the four k rows of a fragment read
+// (k = 4*lq + c) on alternating bank halves.
+template <bool T> __device__ __forceinline__ int dma_at(int r, int k) {
+    return T ? k * BM + 4 * ((r >> 2) ^ (k & 4)) + (r & 3) : r * BK + 4 * ((k >> 2) ^ swz(r)) + (k & 3);
+}
+// Thread's chunk offset (elements, without the tile's k0) for DMA chunk c of
+// a 128 x 16 operand tile: [row][k] chunk = rows 16c.., [k][row] chunk = k rows 2c, 2c+1
+template <bool T> __device__ __forceinline__ int dma_src(int c, int lane, int r0, long ld) {
+    if (!T) {
+        const int r = 16 * c + (lane >> 2), gq = lane & 3;
+        return (int)((r0 + r) * ld) + 4 * (gq ^ swz(r));
+    }
+    const int k = 2 * c + (lane >> 5), gq = lane & 31;
+    return (int)(k * ld) + r0 + 4 * (gq ^ (k & 4));
+}
+
+template <bool AT, bool BT, int EPI, bool PARTIAL, bool DB>
+__global__ __launch_bounds__(NT) void gemm_f32_dma_kernel(const GemmArgs g, int k_chunk, long part_stride) {
+    constexpr int TILE = BM * BK;   // floats per operand tile (BM == BN)
+    constexpr int SMEM = DMA_NS * 2 * TILE > STAGE_FLOATS ? DMA_NS * 2 * TILE : STAGE_FLOATS;
+    __shared__ __align__(16) float smem[SMEM];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tn = (g.N + BN - 1) / BN;
+    int tmi, tni;
+    if (!tile_of_range(g, tn, tmi, tni)) return;   // beyond the tile count
+    const int m0 = tmi * BM, n0 = tni * BN;
+    const int kbeg = blockIdx.z * k_chunk;
+    const int kend = min(g.K, kbeg + k_chunk);
+    const int nk = kend > kbeg ? (kend - kbeg + BK - 1) / BK : 0;
+    const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
+    const int li = lane & 15, lq = lane >> 4;
+
+    floatx4 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+    // exact operand extents (host checked < 2^31 bytes)
+    const unsigned ea = (unsigned)(AT ? ((long)(g.K - 1) * g.lda + g.M) : ((long)(g.M - 1) * g.lda + g.K)) * 4u;
+    const unsigned eb = (unsigned)(BT ? ((long)(g.K - 1) * g.ldb + g.N) : ((long)(g.N - 1) * g.ldb + g.K)) * 4u;
+    const int32x4_t ra = buffer_rsrc(g.A, ea), rb = buffer_rsrc(g.B, eb);
+    const int sa0 = dma_src<AT>(2 * wave, lane, m0, g.lda), sa1 = dma_src<AT>(2 * wave + 1, lane, m0, g.lda);
+    const int sb0 = dma_src<BT>(2 * wave, lane, n0, g.ldb), sb1 = dma_src<BT>(2 * wave + 1, lane, n0, g.ldb);
+    const int ka = AT ? (int)g.lda : 1, kb = BT ? (int)g.ldb : 1;   // element step per k
+#define PT_ISSUE(tile)                                                                  \
+    {                                                                                   \
+        const int k0_ = kbeg + (tile) * BK;                                             \
+        const float* st_ = smem + ((tile) % DMA_NS) * 2 * TILE;                         \
+        dma16(ra, st_ + (2 * wave) * 256, (sa0 + k0_ * ka) * 4);                        \
+        dma16(ra, st_ + (2 * wave + 1) * 256, (sa1 + k0_ * ka) * 4);                    \
+        dma16(rb, st_ + TILE + (2 * wave) * 256, (sb0 + k0_ * kb) * 4);                 \
+        dma16(rb, st_ + TILE + (2 * wave + 1) * 256, (sb1 + k0_ * kb) * 4);             \
+    }
+    const bool do_db = DB && AT && tni == 0;
+    float dbsum = 0.f;
+    if (nk > 0) {
+#pragma unroll
+        for (int t = 0; t < DMA_NS - 1; ++t)
+            if (t < nk) PT_ISSUE(t)
+        for (int it = 0; it < nk; ++it) {
+            // tile it has landed once at most min(DMA_NS - 2, nk - 1 - it) later
+            // tiles (4 loads each) are still in flight
+            const int later = min(DMA_NS - 2, nk - 1 - it);
+            if (later >= 2) wait_vm<8>();
+            else if (later == 1) wait_vm<4>();
+            else wait_vm<0>();
+            __syncthreads();   // every wave's loads of tile it are in LDS; tile it - 1 is consumed
+            if (it + DMA_NS - 1 < nk) PT_ISSUE(it + DMA_NS - 1)
+            const float* Ab = smem + (it % DMA_NS) * 2 * TILE;
+            const float* Bb = Ab + TILE;
+            float4 af[4], bf[4];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const int ca = wm + t * 16 + li, cb = wn + t * 16 + li;
+                if (!AT) af[t] = *reinterpret_cast<const float4*>(Ab + dma_at<false>(ca, 4 * lq));
+                else af[t] = make_float4(Ab[dma_at<true>(ca, 4 * lq)], Ab[dma_at<true>(ca, 4 * lq + 1)],
+                                         Ab[dma_at<true>(ca, 4 * lq + 2)], Ab[dma_at<true>(ca, 4 * lq + 3)]);
+                if (!BT) bf[t] = *reinterpret_cast<const float4*>(Bb + dma_at<false>(cb, 4 * lq));
+                else bf[t] = make_float4(Bb[dma_at<true>(cb, 4 * lq)], Bb[dma_at<true>(cb, 4 * lq + 1)],
+                                         Bb[dma_at<true>(cb, 4 * lq + 2)], Bb[dma_at<true>(cb, 4 * lq + 3)]);
+            }
+#define PT_MFMA_STEP(c)                                                                             \
+            _Pragma("unroll") for (int ti = 0; ti < 4; ++ti)                                        \
+            _Pragma("unroll") for (int tj = 0; tj < 4; ++tj)                                        \
+                acc[ti][tj] = __builtin_amdgcn_mfma_f32_16x16x4f32(bf[tj].c, af[ti].c, acc[ti][tj], 0, 0, 0);
+            PT_MFMA_STEP(x) PT_MFMA_STEP(y) PT_MFMA_STEP(z) PT_MFMA_STEP(w)
+#undef PT_MFMA_STEP
+            if (do_db) {
+                // k rows past K were loaded as zeros; columns past M are never stored
+#pragma unroll
+                for (int kk = 0; kk < BK / 2; ++kk) dbsum += Ab[dma_at<true>(tid & 127, (tid >> 7) * (BK / 2) + kk)];
+            }
+        }
+    }
+#undef PT_ISSUE
+    __syncthreads();   // the stages are free for the bias sums / staged epilogue
+
+    if (do_db) {
+        float* sh = smem;
+        sh[tid] = dbsum;
+        __syncthreads();
+        const int m = m0 + tid;
+        if (tid < 128 && m < g.M) {
+            const float v = sh[tid] + sh[tid + 128];
+            if (PARTIAL) g.C[(long)gridDim.z * part_stride + (long)blockIdx.z * g.M + m] = v;
+            else g.dbias[m] = v;
+        }
+    }
+
+    gemm_epilogue<EPI, PARTIAL>(g, acc, m0, n0, wm, wn, li, lq, part_stride, smem);
+}
+
 // ---------------------------------------------------------------- bf16
 // Mixed precision: fp32 operands from HBM are rounded to bf16 (RNE) on the
 // way into LDS and multiplied on v_mfma_f32_16x16x32_bf16 with fp32
@@ -545,8 +699,12 @@ template <bool AT, bool BT, int EPI, bool PARTIAL, bool DB, bool VEC>
 void launch(const GemmArgs& g, dim3 grid, int k_chunk, long part_stride, hipStream_t s) {
     const bool rec = g_prof.on && g_prof.used * 2 + 1 < (int)g_prof.ev.size();
     if (rec) (void)hipEventRecord(g_prof.ev[2 * g_prof.used], s);
-    hipLaunchKernelGGL((gemm_f32_kernel<AT, BT, EPI, PARTIAL, DB, VEC>), grid, dim3(NT), 0, s, g, k_chunk,
-                       part_stride);
+    if (VEC && g.dma)
+        hipLaunchKernelGGL((gemm_f32_dma_kernel<AT, BT, EPI, PARTIAL, DB>), grid, dim3(NT), 0, s, g, k_chunk,
+                           part_stride);
+    else
+        hipLaunchKernelGGL((gemm_f32_kernel<AT, BT, EPI, PARTIAL, DB, VEC>), grid, dim3(NT), 0, s, g, k_chunk,
+                           part_stride);
     if (rec) {
         (void)hipEventRecord(g_prof.ev[2 * g_prof.used + 1], s);
         g_prof.flops[g_prof.used] = launch_flops(g);
@@ -677,7 +835,21 @@ static int pt_cu_count() {
     return cache[dev];
 }
 
-int pt_gemm(const GemmArgs& g, float* ws, long ws_floats, hipStream_t s) {
+// LDS-DMA kernel: k-contiguous operands need K % BK == 0, and every byte
+// offset a tile can form (rows / columns up to one tile past the end) must
+// fit the buffer instructions' 32-bit offsets
+static bool dma_fits(int rows, int cols, long ld) {
+    return ((long)rows + 2 * BM) * ld * 4 + ((long)cols + 2 * BM) * 4 < (1L << 31);
+}
+static bool dma_ok(const GemmArgs& g) {
+    if (!g.a_t && g.K % BK != 0) return false;
+    if (!g.b_t && g.K % BK != 0) return false;
+    return dma_fits(g.a_t ? g.K : g.M, g.a_t ? g.M : g.K, g.lda) &&
+           dma_fits(g.b_t ? g.K : g.N, g.b_t ? g.N : g.K, g.ldb);
+}
+
+int pt_gemm(const GemmArgs& g0, float* ws, long ws_floats, hipStream_t s) {
+    GemmArgs g = g0;
     PT_REQUIRE(g.M > 0 && g.N > 0 && g.K > 0, "gemm: empty shape %d x %d x %d", g.M, g.N, g.K);
     PT_REQUIRE(g.A && g.B && g.C, "gemm: null operand");
     // 128-bit loads need the contiguous extent and the leading dimensions to be
@@ -687,6 +859,7 @@ int pt_gemm(const GemmArgs& g, float* ws, long ws_floats, hipStream_t s) {
                      ((uintptr_t)g.B & 15) == 0;
     // bf16 products need the 128-bit operand path; other shapes stay fp32
     const bool bf = g.prec == 1 && vec;
+    g.dma = vec && !bf && dma_ok(g);
     const int bk = bf ? BK2 : BK;
     const int tm = pt_cdiv(g.M, BM), tn = pt_cdiv(g.N, BN);
     const int tiles = tm * tn;

@@ -349,7 +349,7 @@ __global__ __launch_bounds__(NT) void gemm_f32_kernel(const GemmArgs g, int k_ch
 // there or zero and only reach C rows / columns that are never stored.
 // The DMA is issued from inline assembly so the compiler does not tie LDS
 // reads to the outstanding loads; the loop waits on vmcnt itself.
-constexpr int DMA_NS = 3;
+constexpr int DMA_NS = 2;
 typedef int int32x4_t __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ int32x4_t buffer_rsrc(const float* p, unsigned bytes) {
@@ -919,16 +919,17 @@ int pt_gemm(const GemmArgs& g0, float* ws, long ws_floats, hipStream_t s) {
         return PTCG_OK;
     }
     // Balance the last wave: with T tiles on S CUs, T % S tail tiles would run
-    // as a partial wave (e.g. 776 tiles = 3.03 per CU: the CUs holding 4 set
+    // as a partial wave (e.g. 584 tiles = 2.28 per CU: the CUs holding 3 set
     // the time).  Run the first T - T % S tiles whole and split the tail's K
     // across the idle CUs, then reduce the tail partials in a fixed order.
+    // Worth its two extra launches only while a CU holds few tiles (T < 4 S).
     if (!db && ws != nullptr) {
         const int S = pt_cu_count();
         const int R = S > 0 ? tiles % S : 0;
         const int ksteps = pt_cdiv(g.K, bk);
         int s2 = R ? S / R : 0;
         if (s2 > ksteps / 2) s2 = ksteps / 2;
-        if (tiles > S && R != 0 && s2 >= 2 && (long)s2 * R * BM * BN <= ws_floats) {
+        if (tiles > S && tiles < 4 * S && R != 0 && s2 >= 2 && (long)s2 * R * BM * BN <= ws_floats) {
             const int kc = pt_cdiv(pt_cdiv(g.K, s2), bk) * bk;
             s2 = pt_cdiv(g.K, kc);
             GemmArgs a = g;

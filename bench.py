@@ -100,6 +100,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--workload", choices=("train", "rollout", "frozen", "bf16"), default="train")
     ap.add_argument("--rollout-rows", type=int, default=8192)
+    ap.add_argument("--sync-free", action="store_true",
+                    help="compact row count kept on the device (no host read-back per forward)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
@@ -124,7 +126,7 @@ def main():
     inp = synth.make_ppo_inputs(dm, obs, seed=2)
     static = synth.make_static(dm, 4) if dm.tables == 1 else None
     pl = trainer.create_pufferl({"dims": dm, "train": dict(TRAIN, minibatch_size=B), "seed": 0, "static": static,
-                                 "precision": "bf16" if bf16 else "fp32"})
+                                 "precision": "bf16" if bf16 else "fp32", "sync_free": args.sync_free})
     trainer.set_rollout(pl, obs, **inp)
     n_lists = args.warmup + args.steps
     lists = synth.minibatch_indices(R, B, n_lists, seed=3)
@@ -198,7 +200,8 @@ def main():
                                + ("; bf16 GEMM operands, fp32 accumulation, LayerNorm, attention, loss, "
                                   "master weights and Adam state" if bf16 else ""),
                    "minibatch": B, "rollout_rows": R, "seq_len": dm.l_tok + 1,
-                   "parallelism": "single GPU"},
+                   "parallelism": "single GPU",
+                   "compact_rows": "device count, no host read-back" if args.sync_free else "host read-back"},
         "roofline": roof,
         "losses": {k: round(v, 5) for k, v in losses.items() if isinstance(v, float)},
     }
@@ -217,7 +220,8 @@ def bench_rollout(args):
     dm = dims.CORE
     n = args.rollout_rows
     obs = synth.make_obs(dm, n, seed=1)
-    pl = trainer.create_pufferl({"dims": dm, "train": dict(TRAIN, minibatch_size=8), "seed": 0})
+    pl = trainer.create_pufferl({"dims": dm, "train": dict(TRAIN, minibatch_size=8), "seed": 0,
+                                 "sync_free": args.sync_free})
     d_obs = pl.to_device(obs)
     for i in range(args.warmup):
         pl.rollout_step(d_obs, n, seed=0, step=i)

@@ -107,6 +107,14 @@ int ptcg_model_set_static(PtcgModel* m, const float* card_static, const float* a
  * LayerNorm, attention, softmax, loss, weights and optimizer state stay
  * fp32 in both.                                                           */
 int ptcg_model_set_precision(PtcgModel* m, int prec);
+/* Compact-layout row count handling (blind-critic models, whose trunk runs
+ * only READOUT, valid-token and pointer-target rows).  0 (default): the
+ * forward reads the row count back to the host once and sizes every trunk
+ * launch for it.  1: no host read-back — launches are sized for the full
+ * N * l_seq rows and stop at the count on the device, so forward / backward
+ * stay stream-ordered and can be captured in a HIP graph, as the
+ * reference's are (pufferlib.cu:2019-2140).  Results are the same.        */
+int ptcg_model_set_sync_free(PtcgModel* m, int on);
 /* ptcg_bind_train_graph (ptcg_model2.cu:323-330), oracle-critic models
  * (dims.critic == 1): device array of per-row returns the blind-value aux
  * loss regresses to, indexed like the obs rows of the forward (through its
@@ -190,6 +198,8 @@ int ptcg_trainer_rollout(PtcgTrainer* t, const float* obs, const int32_t* row_id
                          float* values, void* stream);
 /* ptcg_model_set_precision on the trainer's models (train and rollout).  */
 int ptcg_trainer_set_precision(PtcgTrainer* t, int prec);
+/* ptcg_model_set_sync_free on the trainer's models (train and rollout).   */
+int ptcg_trainer_set_sync_free(PtcgTrainer* t, int on);
 /* ptcg_model_set_static on the trainer's model.                          */
 int ptcg_trainer_set_static(PtcgTrainer* t, const float* card_static, const float* att_static,
                             const float* card_text, const float* att_text, const float* skill_text,

@@ -280,6 +280,7 @@ struct PtcgTrainer {
     PtcgModel* roll = nullptr;
     int roll_n = 0;
     int prec = 0;
+    int sync_free = 0;
     std::vector<float> st_f[5];
     std::vector<int32_t> st_i[2];
 };
@@ -533,6 +534,14 @@ extern "C" int ptcg_trainer_set_precision(PtcgTrainer* t, int prec) {
     return PTCG_OK;
 }
 
+extern "C" int ptcg_trainer_set_sync_free(PtcgTrainer* t, int on) {
+    PT_REQUIRE(t, "trainer_set_sync_free: null trainer");
+    PT_TRY(ptcg_model_set_sync_free(t->model, on));
+    if (t->roll) PT_TRY(ptcg_model_set_sync_free(t->roll, on));
+    t->sync_free = on;
+    return PTCG_OK;
+}
+
 extern "C" int ptcg_trainer_rollout(PtcgTrainer* t, const float* obs, const int32_t* row_idx, int n,
                                     uint64_t seed, uint64_t step, float* actions, float* logprobs,
                                     float* values, void* stream) {
@@ -543,6 +552,7 @@ extern "C" int ptcg_trainer_rollout(PtcgTrainer* t, const float* obs, const int3
             PT_TRY(ptcg_model_create(&t->dm, &t->roll));
             PT_TRY(ptcg_model_bind(t->roll, t->P, t->Gr));
             PT_TRY(ptcg_model_set_precision(t->roll, t->prec));
+            PT_TRY(ptcg_model_set_sync_free(t->roll, t->sync_free));
             if (t->dm.tables == 1 && !t->st_i[0].empty())
                 PT_TRY(ptcg_model_set_static(t->roll, t->st_f[0].data(), t->st_f[1].data(), t->st_f[2].data(),
                                              t->st_f[3].data(), t->st_f[4].data(), t->st_i[0].data(),

@@ -117,6 +117,11 @@ struct GemmArgs {
     int tile0, ntiles, tail_part;
     // set by pt_gemm: fp32 products through the LDS-DMA kernel
     int dma;
+    // optional device row counts (stream-ordered compact layouts): the
+    // product covers min(*Mdev, M) rows of A / C and min(*Kdev, K) of the
+    // reduction; launches are sized for M and K
+    const int* Mdev;
+    const int* Kdev;
 };
 
 // Launch C = epi(A*B) on `stream`. Requirements: K % 4 == 0 when the operand

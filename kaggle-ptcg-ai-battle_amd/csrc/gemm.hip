@@ -40,6 +40,14 @@ __device__ __forceinline__ void tile_of(int b, int tiles, int tn, int& tm_i, int
     tm_i = lb / tn;
     tn_i = lb % tn;
 }
+// effective shape of a launch: the device row / reduction counts when given
+__device__ __forceinline__ GemmArgs gemm_shape(const GemmArgs& g0) {
+    GemmArgs g = g0;
+    if (g.Mdev) g.M = min(*g.Mdev, g.M);
+    if (g.Kdev) g.K = min(*g.Kdev, g.K);
+    return g;
+}
+
 // The launch's logical tile range [g.tile0, g.tile0 + count), count taken
 // from the effective (device) row count: blocks are dealt round-robin to the
 // 8 XCDs, so XCD x gets the contiguous logical range starting at
@@ -224,7 +232,10 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& g, floatx4 (&acc)[
 // With PARTIAL the per-split sums go to C + splits*part_stride + z*M.
 // VEC: operands satisfy the 128-bit load rules (else scalar loads).
 template <bool AT, bool BT, int EPI, bool PARTIAL, bool DB, bool VEC>
-__global__ __launch_bounds__(NT) void gemm_f32_kernel(const GemmArgs g, int k_chunk, long part_stride) {
+__global__ __launch_bounds__(NT) void gemm_f32_kernel(const GemmArgs g0, int k_chunk0, long part_stride) {
+    const GemmArgs g = gemm_shape(g0);
+    // a device reduction count splits its own K evenly over the launch's splits
+    const int k_chunk = g0.Kdev ? (((g.K + (int)gridDim.z - 1) / (int)gridDim.z + BK - 1) / BK) * BK : k_chunk0;
     // one LDS array: the operand stages, reused by the staged epilogue
     constexpr int SMEM = 2 * (Stage<AT>::floats + Stage<BT>::floats);
     static_assert(SMEM >= STAGE_FLOATS, "epilogue stage does not fit the operand stages");
@@ -395,7 +406,10 @@ template <bool T> __device__ __forceinline__ int dma_src(int c, int lane, int r0
 }
 
 template <bool AT, bool BT, int EPI, bool PARTIAL, bool DB>
-__global__ __launch_bounds__(NT) void gemm_f32_dma_kernel(const GemmArgs g, int k_chunk, long part_stride) {
+__global__ __launch_bounds__(NT) void gemm_f32_dma_kernel(const GemmArgs g0, int k_chunk0, long part_stride) {
+    const GemmArgs g = gemm_shape(g0);
+    // a device reduction count splits its own K evenly over the launch's splits
+    const int k_chunk = g0.Kdev ? (((g.K + (int)gridDim.z - 1) / (int)gridDim.z + BK - 1) / BK) * BK : k_chunk0;
     constexpr int TILE = BM * BK;   // floats per operand tile (BM == BN)
     constexpr int SMEM = DMA_NS * 2 * TILE > STAGE_FLOATS ? DMA_NS * 2 * TILE : STAGE_FLOATS;
     __shared__ __align__(16) float smem[SMEM];
@@ -547,7 +561,10 @@ __device__ __forceinline__ void bf_store(__bf16* S, int tid, const float4 (&v)[4
 }
 
 template <bool AT, bool BT, int EPI, bool PARTIAL>
-__global__ __launch_bounds__(NT) void gemm_bf16_kernel(const GemmArgs g, int k_chunk, long part_stride) {
+__global__ __launch_bounds__(NT) void gemm_bf16_kernel(const GemmArgs g0, int k_chunk0, long part_stride) {
+    const GemmArgs g = gemm_shape(g0);
+    // a device reduction count splits its own K evenly over the launch's splits
+    const int k_chunk = g0.Kdev ? (((g.K + (int)gridDim.z - 1) / (int)gridDim.z + BK2 - 1) / BK2) * BK2 : k_chunk0;
     constexpr int SMEM = 2 * (BM + BN) * SKB2 / 2;   // floats
     static_assert(SMEM >= STAGE_FLOATS, "epilogue stage does not fit the operand stages");
     __shared__ __align__(16) float smem[SMEM];
@@ -873,6 +890,7 @@ int pt_gemm(const GemmArgs& g0, float* ws, long ws_floats, hipStream_t s) {
         if (splits < 1) splits = 1;
     }
     if (splits > 1 && !(g.epi == EPI_STORE || g.epi == EPI_ACCUM)) splits = 1;
+    if (g.Mdev) splits = 1;   // device row counts: one pass (partials are sized by M)
     PT_REQUIRE(!(g.dbias && !(g.a_t && g.epi == EPI_STORE)), "gemm: dbias needs a_t = 1 and the STORE epilogue");
     // the bf16 kernel leaves bias sums to the fp32 column sum (kept in fp32 from the unrounded dY)
     const bool db = g.dbias != nullptr && !bf;
@@ -923,7 +941,7 @@ int pt_gemm(const GemmArgs& g0, float* ws, long ws_floats, hipStream_t s) {
     // the time).  Run the first T - T % S tiles whole and split the tail's K
     // across the idle CUs, then reduce the tail partials in a fixed order.
     // Worth its two extra launches only while a CU holds few tiles (T < 4 S).
-    if (!db && ws != nullptr) {
+    if (!db && !g.Mdev && ws != nullptr) {
         const int S = pt_cu_count();
         const int R = S > 0 ? tiles % S : 0;
         const int ksteps = pt_cdiv(g.K, bk);

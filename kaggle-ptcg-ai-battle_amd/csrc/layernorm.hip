@@ -17,7 +17,9 @@ constexpr int LN_BWD_BLOCKS = 512;   // partial rows of dW/dB (grid-stride over 
 template <int VPL>
 __global__ __launch_bounds__(256) void ln_fwd_kernel(const float* __restrict__ x, long ldx,
         const float* __restrict__ w, const float* __restrict__ b, float* __restrict__ y, long ldy,
-        float* __restrict__ mean, float* __restrict__ rstd, int rows, int D) {
+        float* __restrict__ mean, float* __restrict__ rstd, int rows, int D,
+        const int* __restrict__ rows_dev) {
+    if (rows_dev) rows = min(rows, *rows_dev);   // device row count (compact layouts)
     const int lane = threadIdx.x & 63;
     const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= rows) return;
@@ -70,7 +72,9 @@ __global__ __launch_bounds__(256) void ln_bwd_kernel(const float* __restrict__ d
         const float* __restrict__ x, long ldx, const float* __restrict__ w,
         const float* __restrict__ mean, const float* __restrict__ rstd,
         const float* __restrict__ dres, long ldres, float* __restrict__ dx, long lddx,
-        float* __restrict__ part, int rows, int D) {
+        float* __restrict__ part, int rows, int D,
+        const int* __restrict__ rows_dev) {
+    if (rows_dev) rows = min(rows, *rows_dev);   // device row count (compact layouts)
     __shared__ float4 sh_w[4][VPL * 64];
     __shared__ float4 sh_b[4][VPL * 64];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -157,7 +161,9 @@ constexpr int LN_SC = 16;
 
 __global__ __launch_bounds__(256) void ln_fwd_scalar_kernel(const float* __restrict__ x, long ldx,
         const float* __restrict__ w, const float* __restrict__ b, float* __restrict__ y, long ldy,
-        float* __restrict__ mean, float* __restrict__ rstd, int rows, int D) {
+        float* __restrict__ mean, float* __restrict__ rstd, int rows, int D,
+        const int* __restrict__ rows_dev) {
+    if (rows_dev) rows = min(rows, *rows_dev);   // device row count (compact layouts)
     const int lane = threadIdx.x & 63;
     const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= rows) return;
@@ -192,7 +198,9 @@ __global__ __launch_bounds__(256) void ln_bwd_scalar_kernel(const float* __restr
         const float* __restrict__ x, long ldx, const float* __restrict__ w,
         const float* __restrict__ mean, const float* __restrict__ rstd,
         const float* __restrict__ dres, long ldres, float* __restrict__ dx, long lddx,
-        float* __restrict__ part, int rows, int D) {
+        float* __restrict__ part, int rows, int D,
+        const int* __restrict__ rows_dev) {
+    if (rows_dev) rows = min(rows, *rows_dev);   // device row count (compact layouts)
     __shared__ float sh_w[4][LN_SC * 64];
     __shared__ float sh_b[4][LN_SC * 64];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -259,17 +267,17 @@ bool ln_vec_ok(const void* p, long ld, int D) { return D % 4 == 0 && ld % 4 == 0
 }  // namespace
 
 int pt_ln_fwd(const float* x, long ldx, const float* w, const float* b, float* y, long ldy,
-              float* mean, float* rstd, int rows, int D, hipStream_t s) {
+              float* mean, float* rstd, int rows, int D, hipStream_t s, const int* rows_dev) {
     PT_REQUIRE(D >= 1 && D <= 1024, "layernorm: D=%d unsupported", D);
     dim3 grid(pt_cdiv(rows, 4));
     if (!(ln_vec_ok(x, ldx, D) && ln_vec_ok(y, ldy, D) && ln_vec_ok(w, 0, D) && ln_vec_ok(b, 0, D)))
-        hipLaunchKernelGGL(ln_fwd_scalar_kernel, grid, dim3(256), 0, s, x, ldx, w, b, y, ldy, mean, rstd, rows, D);
+        hipLaunchKernelGGL(ln_fwd_scalar_kernel, grid, dim3(256), 0, s, x, ldx, w, b, y, ldy, mean, rstd, rows, D, rows_dev);
     else if (D <= 256)
-        hipLaunchKernelGGL(ln_fwd_kernel<1>, grid, dim3(256), 0, s, x, ldx, w, b, y, ldy, mean, rstd, rows, D);
+        hipLaunchKernelGGL(ln_fwd_kernel<1>, grid, dim3(256), 0, s, x, ldx, w, b, y, ldy, mean, rstd, rows, D, rows_dev);
     else if (D <= 512)
-        hipLaunchKernelGGL(ln_fwd_kernel<2>, grid, dim3(256), 0, s, x, ldx, w, b, y, ldy, mean, rstd, rows, D);
+        hipLaunchKernelGGL(ln_fwd_kernel<2>, grid, dim3(256), 0, s, x, ldx, w, b, y, ldy, mean, rstd, rows, D, rows_dev);
     else
-        hipLaunchKernelGGL(ln_fwd_kernel<4>, grid, dim3(256), 0, s, x, ldx, w, b, y, ldy, mean, rstd, rows, D);
+        hipLaunchKernelGGL(ln_fwd_kernel<4>, grid, dim3(256), 0, s, x, ldx, w, b, y, ldy, mean, rstd, rows, D, rows_dev);
     PT_LAUNCH_CHECK();
     return PTCG_OK;
 }
@@ -277,7 +285,7 @@ int pt_ln_fwd(const float* x, long ldx, const float* w, const float* b, float* y
 int pt_ln_bwd(const float* dy, long lddy, const float* x, long ldx, const float* w,
               const float* mean, const float* rstd, const float* dres, long ldres, float* dx,
               long lddx, float* dw, float* db, int rows, int D, float* ws, long ws_floats,
-              hipStream_t s) {
+              hipStream_t s, const int* rows_dev) {
     PT_REQUIRE(D >= 1 && D <= 1024, "layernorm bwd: D=%d unsupported", D);
     int blocks = pt_cdiv(rows, 4);
     if (blocks > LN_BWD_BLOCKS) blocks = LN_BWD_BLOCKS;
@@ -286,13 +294,13 @@ int pt_ln_bwd(const float* dy, long lddy, const float* x, long ldx, const float*
     const bool vec = ln_vec_ok(dy, lddy, D) && ln_vec_ok(x, ldx, D) && ln_vec_ok(w, 0, D) &&
                      ln_vec_ok(dx, lddx, D) && (dres == nullptr || ln_vec_ok(dres, ldres, D));
     if (!vec)
-        hipLaunchKernelGGL(ln_bwd_scalar_kernel, grid, dim3(256), 0, s, dy, lddy, x, ldx, w, mean, rstd, dres, ldres, dx, lddx, ws, rows, D);
+        hipLaunchKernelGGL(ln_bwd_scalar_kernel, grid, dim3(256), 0, s, dy, lddy, x, ldx, w, mean, rstd, dres, ldres, dx, lddx, ws, rows, D, rows_dev);
     else if (D <= 256)
-        hipLaunchKernelGGL(ln_bwd_kernel<1>, grid, dim3(256), 0, s, dy, lddy, x, ldx, w, mean, rstd, dres, ldres, dx, lddx, ws, rows, D);
+        hipLaunchKernelGGL(ln_bwd_kernel<1>, grid, dim3(256), 0, s, dy, lddy, x, ldx, w, mean, rstd, dres, ldres, dx, lddx, ws, rows, D, rows_dev);
     else if (D <= 512)
-        hipLaunchKernelGGL(ln_bwd_kernel<2>, grid, dim3(256), 0, s, dy, lddy, x, ldx, w, mean, rstd, dres, ldres, dx, lddx, ws, rows, D);
+        hipLaunchKernelGGL(ln_bwd_kernel<2>, grid, dim3(256), 0, s, dy, lddy, x, ldx, w, mean, rstd, dres, ldres, dx, lddx, ws, rows, D, rows_dev);
     else
-        hipLaunchKernelGGL(ln_bwd_kernel<4>, grid, dim3(256), 0, s, dy, lddy, x, ldx, w, mean, rstd, dres, ldres, dx, lddx, ws, rows, D);
+        hipLaunchKernelGGL(ln_bwd_kernel<4>, grid, dim3(256), 0, s, dy, lddy, x, ldx, w, mean, rstd, dres, ldres, dx, lddx, ws, rows, D, rows_dev);
     PT_LAUNCH_CHECK();
     if (dw && db)
         return pt_colsum2(ws, 2 * D, blocks, 2 * D, D, dw, db, ws + (long)blocks * 2 * D,

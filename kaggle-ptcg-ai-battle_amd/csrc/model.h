@@ -36,12 +36,13 @@ struct ParamDef { const char* name; long rows, cols; };
 int pt_param_table(const PtcgDims& d, ParamDef* out, int cap);   // returns count or <0
 
 // kernels (layernorm.hip, attention.hip, ppo.hip, adam.hip, gather.hip)
+// rows_dev (nullable): device row count <= rows (the launch covers rows)
 int pt_ln_fwd(const float* x, long ldx, const float* w, const float* b, float* y, long ldy,
-              float* mean, float* rstd, int rows, int D, hipStream_t s);
+              float* mean, float* rstd, int rows, int D, hipStream_t s, const int* rows_dev = nullptr);
 int pt_ln_bwd(const float* dy, long lddy, const float* x, long ldx, const float* w,
               const float* mean, const float* rstd, const float* dres, long ldres, float* dx,
               long lddx, float* dw, float* db, int rows, int D, float* ws, long ws_floats,
-              hipStream_t s);
+              hipStream_t s, const int* rows_dev = nullptr);
 int pt_attn_supported(int L, int DH);
 // coff (nullable): sample n's rows are [coff[n], coff[n+1]) (length <= L);
 // else rows n*L .. n*L+L-1.  lse is laid out (N, H, L) either way.

@@ -68,14 +68,19 @@ struct PtcgModel {
     bool train = true;
     int prec = 0;   // GEMM products: 0 fp32, 1 bf16 operands with fp32 accumulation
     // compact trunk layout (blind-critic models): only READOUT, valid tokens
-    // and pointer targets are trunk rows; *Tr = their count (device), read
-    // back once per forward into rows (pinned rows_h) so every GEMM,
-    // LayerNorm and grid is sized for exactly those rows
+    // and pointer targets are trunk rows; *Tr = their count (device).
+    // Default: the count is read back once per forward (pinned rows_h) and
+    // every trunk launch is sized for exactly those rows (rows, Tdev null).
+    // sync_free: no host read-back, so the step stays stream-ordered and can
+    // be captured in a HIP graph; launches are sized for N * l_seq rows and
+    // stop at the device count (rows = N * l_seq, Tdev = Tr).
     bool compact = false;
+    bool sync_free = false;
     int *c_act = nullptr, *c_cnt, *c_off, *c_map, *c_rsam, *c_rpos;
     const int* Tr = nullptr;
     int* rows_h = nullptr;
     int rows = 0;
+    const int* Tdev = nullptr;
     float* rd_buf = nullptr;
     char* mem = nullptr;
     size_t mem_bytes = 0;
@@ -103,9 +108,10 @@ struct PtcgModel {
 // ------------------------------------------------------------ helpers
 static int lin(const PtcgModel* m, const float* X, long ldx, const float* W, const float* b, float* Y, long ldy,
                int rows, int in, int out, int epi, const float* R, long ldr, float* Y2, long ldy2,
-               hipStream_t s) {
+               hipStream_t s, const int* Mdev = nullptr) {
     GemmArgs g{};
     g.prec = m->prec;
+    g.Mdev = Mdev;
     g.M = rows; g.N = out; g.K = in;
     g.A = X; g.lda = ldx; g.a_t = 0;
     g.B = W; g.ldb = in; g.b_t = 0;
@@ -115,14 +121,16 @@ static int lin(const PtcgModel* m, const float* X, long ldx, const float* W, con
     return pt_gemm(g, m->ws, m->ws_floats, s);
 }
 static int linf(const PtcgModel* m, const float* X, const float* W, const float* b, float* Y, int rows, int in,
-                int out, int epi, const float* R, float* Y2, hipStream_t s) {
-    return lin(m, X, in, W, b, Y, out, rows, in, out, epi, R, out, Y2, out, s);
+                int out, int epi, const float* R, float* Y2, hipStream_t s, const int* Mdev = nullptr) {
+    return lin(m, X, in, W, b, Y, out, rows, in, out, epi, R, out, Y2, out, s, Mdev);
 }
 // dX = dY W[:, :in] : dY (rows, out) ld lddy ; W (out, ldw) ; dX (rows, in) ld lddx
 static int ldxw_(const PtcgModel* m, const float* dY, long lddy, const float* W, long ldw, float* dX, long lddx,
-                 int rows, int in, int out, int epi, const float* R, long ldr, hipStream_t s) {
+                 int rows, int in, int out, int epi, const float* R, long ldr, hipStream_t s,
+                 const int* Mdev = nullptr) {
     GemmArgs g{};
     g.prec = m->prec;
+    g.Mdev = Mdev;
     g.M = rows; g.N = in; g.K = out;
     g.A = dY; g.lda = lddy; g.a_t = 0;
     g.B = W; g.ldb = ldw; g.b_t = 1;
@@ -133,13 +141,14 @@ static int ldxw_(const PtcgModel* m, const float* dY, long lddy, const float* W,
 }
 // dX = dY W : dY (rows, out) ld lddy ; W (out, in) ; dX (rows, in) ld lddx
 static int ldx_(const PtcgModel* m, const float* dY, long lddy, const float* W, float* dX, long lddx, int rows,
-                int in, int out, int epi, const float* R, long ldr, hipStream_t s) {
-    return ldxw_(m, dY, lddy, W, in, dX, lddx, rows, in, out, epi, R, ldr, s);
+                int in, int out, int epi, const float* R, long ldr, hipStream_t s, const int* Mdev = nullptr) {
+    return ldxw_(m, dY, lddy, W, in, dX, lddx, rows, in, out, epi, R, ldr, s, Mdev);
 }
 // dW = dY^T X (overwrite), db = colsum dY (fused into the product)
 static int ldw_(PtcgModel* m, const float* dY, long lddy, const float* X, long ldxx, float* dW,
-                float* db, int rows, int in, int out, hipStream_t s) {
+                float* db, int rows, int in, int out, hipStream_t s, const int* Kdev = nullptr) {
     GemmArgs g{};
+    g.Kdev = Kdev;
     g.M = out; g.N = in; g.K = rows;
     g.A = dY; g.lda = lddy; g.a_t = 1;
     g.B = X; g.ldb = ldxx; g.b_t = 1;
@@ -450,6 +459,7 @@ static size_t carve(PtcgModel* m, char* base) {
 }
 
 static int reg(PtcgModel* m, int n, bool train) {
+    if (!m->rows_h) PT_HIP(hipHostMalloc((void**)&m->rows_h, sizeof(int), hipHostMallocDefault));
     if (m->mem) {
         PT_HIP(hipFree(m->mem));
         m->mem = nullptr;
@@ -457,11 +467,16 @@ static int reg(PtcgModel* m, int n, bool train) {
     m->N = n;
     m->train = train;
     m->compact = m->dm.critic == 0;
-    if (m->compact && !m->rows_h) PT_HIP(hipHostMalloc((void**)&m->rows_h, sizeof(int), hipHostMallocDefault));
     size_t bytes = carve(m, nullptr);
     PT_HIP(hipMalloc(&m->mem, bytes));
     m->mem_bytes = bytes;
     carve(m, m->mem);
+    return PTCG_OK;
+}
+
+extern "C" int ptcg_model_set_sync_free(PtcgModel* m, int on) {
+    PT_REQUIRE(m, "model_set_sync_free: null model");
+    m->sync_free = on != 0;
     return PTCG_OK;
 }
 
@@ -488,19 +503,20 @@ float* pt_model_out(const PtcgModel* m) { return m->out; }
 float* pt_model_ws(const PtcgModel* m, long* floats) { *floats = m->ws_floats; return m->ws; }
 
 // ------------------------------------------------------------ forward
-// rows / coff: row count and per-sample row offsets of a compact layout
-// (rows 0, coff null: N * L rows)
+// rows / Tr / coff of a compact layout: launch rows, device row count
+// (nullable) and per-sample row offsets (rows 0, coff null: N * L rows)
 static int block_fwd(PtcgModel* m, const BlockP& w, const BlockA& a, int L, const float* keep, const float* xin,
-                     float* xout, hipStream_t s, int rows = 0, const int* coff = nullptr) {
+                     float* xout, hipStream_t s, int rows = 0, const int* Tr = nullptr,
+                     const int* coff = nullptr) {
     const PtcgDims& d = m->dm;
     const int NL = rows ? rows : m->N * L, D = d.d;
-    PT_TRY(pt_ln_fwd(xin, D, w.ln1w, w.ln1b, a.ln1, D, a.mu1, a.rs1, NL, D, s));
-    PT_TRY(linf(m, a.ln1, w.qkvw, w.qkvb, a.qkv, NL, D, 3 * D, EPI_BIAS, nullptr, nullptr, s));
+    PT_TRY(pt_ln_fwd(xin, D, w.ln1w, w.ln1b, a.ln1, D, a.mu1, a.rs1, NL, D, s, Tr));
+    PT_TRY(linf(m, a.ln1, w.qkvw, w.qkvb, a.qkv, NL, D, 3 * D, EPI_BIAS, nullptr, nullptr, s, Tr));
     PT_TRY(pt_attn_fwd(a.qkv, keep, a.ctx, a.lse, m->N, L, d.heads, m->dx.dh, s, coff));
-    PT_TRY(linf(m, a.ctx, w.projw, w.projb, a.xmid, NL, D, D, EPI_BIAS_RESID, xin, nullptr, s));
-    PT_TRY(pt_ln_fwd(a.xmid, D, w.ln2w, w.ln2b, a.ln2, D, a.mu2, a.rs2, NL, D, s));
-    PT_TRY(linf(m, a.ln2, w.f1w, w.f1b, a.ffp, NL, D, d.ffn, EPI_BIAS_GELU, nullptr, a.ffa, s));
-    PT_TRY(linf(m, a.ffa, w.f2w, w.f2b, xout, NL, d.ffn, D, EPI_BIAS_RESID, a.xmid, nullptr, s));
+    PT_TRY(linf(m, a.ctx, w.projw, w.projb, a.xmid, NL, D, D, EPI_BIAS_RESID, xin, nullptr, s, Tr));
+    PT_TRY(pt_ln_fwd(a.xmid, D, w.ln2w, w.ln2b, a.ln2, D, a.mu2, a.rs2, NL, D, s, Tr));
+    PT_TRY(linf(m, a.ln2, w.f1w, w.f1b, a.ffp, NL, D, d.ffn, EPI_BIAS_GELU, nullptr, a.ffa, s, Tr));
+    PT_TRY(linf(m, a.ffa, w.f2w, w.f2b, xout, NL, d.ffn, D, EPI_BIAS_RESID, a.xmid, nullptr, s, Tr));
     return PTCG_OK;
 }
 
@@ -547,22 +563,28 @@ extern "C" int ptcg_model_forward(PtcgModel* m, const float* obs, const int32_t*
     const int* Tr = m->Tr;
     const int* coff = m->compact ? m->c_off : nullptr;
     m->rows = N * x.l_seq;
+    m->Tdev = nullptr;
     if (m->compact) {
         PT_TRY(pt_compact_map(c, m->c_act, m->c_cnt, m->c_off, m->c_map, m->c_rsam, m->c_rpos, s));
         c.coff = m->c_off; c.rowmap = m->c_map; c.rsam = m->c_rsam; c.rpos = m->c_rpos; c.rows = Tr;
-        // the one host read-back of the step: the trunk row count sizes every
-        // launch that follows
-        PT_HIP(hipMemcpyAsync(m->rows_h, Tr, sizeof(int), hipMemcpyDeviceToHost, s));
-        PT_HIP(hipStreamSynchronize(s));
-        m->rows = *m->rows_h;
-        PT_REQUIRE(m->rows >= N && m->rows <= N * x.l_seq, "model_forward: compact row count %d out of range",
-                   m->rows);
+        if (m->sync_free) {
+            m->Tdev = Tr;
+        } else {
+            // the step's one host read-back: the trunk row count sizes every
+            // launch that follows
+            PT_HIP(hipMemcpyAsync(m->rows_h, Tr, sizeof(int), hipMemcpyDeviceToHost, s));
+            PT_HIP(hipStreamSynchronize(s));
+            m->rows = *m->rows_h;
+            PT_REQUIRE(m->rows >= N && m->rows <= N * x.l_seq, "model_forward: compact row count %d out of range",
+                       m->rows);
+        }
     }
+    const int* Td = m->Tdev;
     const int tok_rows = m->compact ? m->rows : N * Lt;
 
     if (d.tables == 1) PT_TRY(tables_fwd(m, s));
     PT_TRY(pt_tok_cat_fwd(c, m->card, m->zemb, m->oemb, m->tok_cat, s));
-    PT_TRY(linf(m, m->tok_cat, m->tp_w, m->tp_b, m->tokp, tok_rows, x.tok_in, D, EPI_BIAS, nullptr, nullptr, s));
+    PT_TRY(linf(m, m->tok_cat, m->tp_w, m->tp_b, m->tokp, tok_rows, x.tok_in, D, EPI_BIAS, nullptr, nullptr, s, Td));
     PT_TRY(pt_glob_in(c, m->glob_in, s));
     PT_TRY(linf(m, m->glob_in, m->g1_w, m->g1_b, m->g1, N, d.global_f, G, EPI_BIAS_GELU, nullptr, m->g1a, s));
     PT_TRY(lin(m, m->g1a, G, m->g2_w, m->g2_b, m->gd, x.bcast_in, N, G, G, EPI_BIAS, nullptr, 0, nullptr, 0, s));
@@ -575,10 +597,10 @@ extern "C" int ptcg_model_forward(PtcgModel* m, const float* obs, const int32_t*
     const bool tr = m->train;
     for (int i = 0; i < d.layers; ++i)
         PT_TRY(block_fwd(m, m->blk[i], m->ba[tr ? i : 0], x.l_seq, m->keep, m->x[tr ? i : i % 2],
-                         m->x[tr ? i + 1 : (i + 1) % 2], s, m->rows, coff));
+                         m->x[tr ? i + 1 : (i + 1) % 2], s, m->rows, Td, coff));
     const int NL = N * x.l_seq;
     PT_TRY(pt_ln_fwd(m->x[tr ? d.layers : d.layers % 2], D, m->lnf_w, m->lnf_b, m->h, D, m->lnf_mu, m->lnf_rs,
-                     m->rows, D, s));
+                     m->rows, D, s, Td));
 
     // option scorer
     const int NJ = N * NO;
@@ -623,22 +645,23 @@ extern "C" int ptcg_model_forward(PtcgModel* m, const float* obs, const int32_t*
 // ------------------------------------------------------------ backward
 // dA holds d(x_out) on entry and d(x_in) on exit; dC is scratch for d(x_mid)
 static int block_bwd(PtcgModel* m, const BlockP& w, const BlockA& a, int L, const float* keep, const float* xin,
-                     float* dA, float* dC, hipStream_t s, int rows = 0, const int* coff = nullptr) {
+                     float* dA, float* dC, hipStream_t s, int rows = 0, const int* Tr = nullptr,
+                     const int* coff = nullptr) {
     const PtcgDims& d = m->dm;
     const int NL = rows ? rows : m->N * L, D = d.d;
-    PT_TRY(ldw_(m, dA, D, a.ffa, d.ffn, m->G(w.f2w), m->G(w.f2b), NL, d.ffn, D, s));
-    PT_TRY(ldx_(m, dA, D, w.f2w, m->dffn, d.ffn, NL, d.ffn, D, EPI_GELU_BWD, a.ffp, d.ffn, s));
-    PT_TRY(ldw_(m, m->dffn, d.ffn, a.ln2, D, m->G(w.f1w), m->G(w.f1b), NL, D, d.ffn, s));
-    PT_TRY(ldx_(m, m->dffn, d.ffn, w.f1w, m->dln, D, NL, D, d.ffn, EPI_STORE, nullptr, 0, s));
+    PT_TRY(ldw_(m, dA, D, a.ffa, d.ffn, m->G(w.f2w), m->G(w.f2b), NL, d.ffn, D, s, Tr));
+    PT_TRY(ldx_(m, dA, D, w.f2w, m->dffn, d.ffn, NL, d.ffn, D, EPI_GELU_BWD, a.ffp, d.ffn, s, Tr));
+    PT_TRY(ldw_(m, m->dffn, d.ffn, a.ln2, D, m->G(w.f1w), m->G(w.f1b), NL, D, d.ffn, s, Tr));
+    PT_TRY(ldx_(m, m->dffn, d.ffn, w.f1w, m->dln, D, NL, D, d.ffn, EPI_STORE, nullptr, 0, s, Tr));
     PT_TRY(pt_ln_bwd(m->dln, D, a.xmid, D, w.ln2w, a.mu2, a.rs2, dA, D, dC, D, m->G(w.ln2w),
-                     m->G(w.ln2b), NL, D, m->ws, m->ws_floats, s));
-    PT_TRY(ldw_(m, dC, D, a.ctx, D, m->G(w.projw), m->G(w.projb), NL, D, D, s));
-    PT_TRY(ldx_(m, dC, D, w.projw, m->dctx, D, NL, D, D, EPI_STORE, nullptr, 0, s));
+                     m->G(w.ln2b), NL, D, m->ws, m->ws_floats, s, Tr));
+    PT_TRY(ldw_(m, dC, D, a.ctx, D, m->G(w.projw), m->G(w.projb), NL, D, D, s, Tr));
+    PT_TRY(ldx_(m, dC, D, w.projw, m->dctx, D, NL, D, D, EPI_STORE, nullptr, 0, s, Tr));
     PT_TRY(pt_attn_bwd(a.qkv, keep, a.ctx, a.lse, m->dctx, m->dqkv, m->N, L, d.heads, m->dx.dh, s, coff));
-    PT_TRY(ldw_(m, m->dqkv, 3 * D, a.ln1, D, m->G(w.qkvw), m->G(w.qkvb), NL, D, 3 * D, s));
-    PT_TRY(ldx_(m, m->dqkv, 3 * D, w.qkvw, m->dln, D, NL, D, 3 * D, EPI_STORE, nullptr, 0, s));
+    PT_TRY(ldw_(m, m->dqkv, 3 * D, a.ln1, D, m->G(w.qkvw), m->G(w.qkvb), NL, D, 3 * D, s, Tr));
+    PT_TRY(ldx_(m, m->dqkv, 3 * D, w.qkvw, m->dln, D, NL, D, 3 * D, EPI_STORE, nullptr, 0, s, Tr));
     PT_TRY(pt_ln_bwd(m->dln, D, xin, D, w.ln1w, a.mu1, a.rs1, dC, D, dA, D, m->G(w.ln1w),
-                     m->G(w.ln1b), NL, D, m->ws, m->ws_floats, s));
+                     m->G(w.ln1b), NL, D, m->ws, m->ws_floats, s, Tr));
     return PTCG_OK;
 }
 
@@ -728,7 +751,8 @@ extern "C" int ptcg_model_backward(PtcgModel* m, const float* grad, void* stream
     if (m->compact) {   // the map of the forward (same rows)
         c.coff = m->c_off; c.rowmap = m->c_map; c.rsam = m->c_rsam; c.rpos = m->c_rpos; c.rows = Tr;
     }
-    const int rows = m->rows;   // trunk rows of the forward
+    const int rows = m->rows;        // trunk launch rows of the forward
+    const int* Td = m->Tdev;         // and its device row count (sync-free mode)
     const int tok_rows = m->compact ? rows : N * Lt;
 
     PT_TRY(pt_fill_zero(m->Gr, m->arena, s));
@@ -773,9 +797,9 @@ extern "C" int ptcg_model_backward(PtcgModel* m, const float* grad, void* stream
 
     // final LayerNorm, then the trunk in reverse (d_x in dxb, scratch dxa)
     PT_TRY(pt_ln_bwd(m->dxa, D, m->x[d.layers], D, m->lnf_w, m->lnf_mu, m->lnf_rs, nullptr, 0, m->dxb, D,
-                     m->G(m->lnf_w), m->G(m->lnf_b), rows, D, m->ws, m->ws_floats, s));
+                     m->G(m->lnf_w), m->G(m->lnf_b), rows, D, m->ws, m->ws_floats, s, Td));
     for (int i = d.layers - 1; i >= 0; --i)
-        PT_TRY(block_bwd(m, m->blk[i], m->ba[i], x.l_seq, m->keep, m->x[i], m->dxb, m->dxa, s, rows, coff));
+        PT_TRY(block_bwd(m, m->blk[i], m->ba[i], x.l_seq, m->keep, m->x[i], m->dxb, m->dxa, s, rows, Td, coff));
 
     // trunk input: readout / token projection / broadcast
     PT_TRY(pt_x0_bwd(c, m->dxb, m->dtokp, m->dbc, s));
@@ -785,8 +809,8 @@ extern "C" int ptcg_model_backward(PtcgModel* m, const float* grad, void* stream
     } else {
         PT_TRY(pt_colsum(m->dxb, (long)x.l_seq * D, N, D, m->G(m->readout), m->ws, m->ws_floats, s));
     }
-    PT_TRY(ldw_(m, m->dtokp, D, m->tok_cat, x.tok_in, m->G(m->tp_w), m->G(m->tp_b), tok_rows, x.tok_in, D, s));
-    PT_TRY(ldx_(m, m->dtokp, D, m->tp_w, m->dtokcat, x.tok_in, tok_rows, x.tok_in, D, EPI_STORE, nullptr, 0, s));
+    PT_TRY(ldw_(m, m->dtokp, D, m->tok_cat, x.tok_in, m->G(m->tp_w), m->G(m->tp_b), tok_rows, x.tok_in, D, s, Td));
+    PT_TRY(ldx_(m, m->dtokp, D, m->tp_w, m->dtokcat, x.tok_in, tok_rows, x.tok_in, D, EPI_STORE, nullptr, 0, s, Td));
     PT_TRY(pt_tok_cat_bwd(c, m->dtokcat, m->dcard, m->G(m->zemb), m->G(m->oemb), s));
     PT_TRY(ldw_(m, m->dbc, D, m->gd, x.bcast_in, m->G(m->bc_w), m->G(m->bc_b), N, x.bcast_in, D, s));
     PT_TRY(ldx_(m, m->dbc, D, m->bc_w, m->dgd, x.bcast_in, N, x.bcast_in, D, EPI_ACCUM, nullptr, 0, s));

@@ -177,7 +177,9 @@ class PuffeRL:
 def create_pufferl(args):
     """args: {"dims": PtcgDims | dict, "train": {...}, "seed": int,
     "init_weights": packed blob | None, "static": static tables (static-table
-    models), "precision": "fp32" | "bf16" (GEMM products)}.  Unknown dims keys
+    models), "precision": "fp32" | "bf16" (GEMM products), "sync_free": bool
+    (compact row count kept on the device: no host read-back per forward, so
+    the step can be graph-captured)}.  Unknown dims keys
     raise."""
     dm = args.get("dims", dims_mod.CORE)
     if isinstance(dm, dict):
@@ -189,6 +191,8 @@ def create_pufferl(args):
     if prec not in ("fp32", "bf16"):
         raise ValueError(f"precision must be 'fp32' or 'bf16', got {prec!r}")
     check(lib().ptcg_trainer_set_precision(pl._h, 1 if prec == "bf16" else 0))
+    if args.get("sync_free", False):
+        check(lib().ptcg_trainer_set_sync_free(pl._h, 1))
     init = args.get("init_weights")
     if init is None:
         from .params import init_blob

@@ -60,6 +60,58 @@ def useful_gemm_flops(dm, obs_rows):
     return 3.0 * fwd, float(Lv.mean())
 
 
+def _gemm_list(dm, obs_rows):
+    """(rows M, in K, out N, GELU epilogue, residual epilogue) of every
+    linear layer of the forward, on valid rows only."""
+    from ptcg_amd.params import OPT_E, SC_H, VAL_H, DEC_H
+    off = dm.offsets()
+    zone = obs_rows[:, off["tok_int"][0]:off["tok_int"][1]].reshape(len(obs_rows), dm.l_tok, dm.tok_int)[:, :, 1]
+    n_valid = float((zone > 0).sum())
+    R = n_valid + len(obs_rows)
+    d, ffn, B = dm.d, dm.ffn, len(obs_rows)
+    NJ = B * dm.n_opt
+    g = [(n_valid, 2 * dm.d_c + dm.tok_f + 12, d, 0, 0)]
+    for _ in range(dm.layers):
+        g += [(R, d, 3 * d, 0, 0), (R, d, d, 0, 1), (R, d, ffn, 1, 0), (R, ffn, d, 0, 1)]
+    g += [(NJ, dm.d_c, OPT_E, 0, 0), (NJ, dm.d_a, OPT_E, 0, 0), (NJ, dm.q_in, d, 1, 0), (NJ, d, d, 0, 0),
+          (NJ, dm.score_in, SC_H, 1, 0), (B, dm.global_f, dm.g, 1, 0), (B, dm.g, dm.g, 0, 0),
+          (B, dm.dec_in, DEC_H, 1, 0), (B, DEC_H, DEC_H, 0, 0), (B, dm.bcast_in, d, 0, 0),
+          (B, dm.val_in, VAL_H, 1, 0)]
+    return g
+
+
+def algorithmic_gemm_bytes(dm, obs_rows):
+    """HBM bytes of one fwd+bwd's GEMMs with every operand read and every
+    output written once (fp32): forward X, W, Y (+ GELU output, + residual
+    read); backward dX = dY W (+ pre-activation read for a GELU input) and
+    dW = dY^T X."""
+    tot = 0.0
+    for M, K, N, gelu, resid in _gemm_list(dm, obs_rows):
+        fwd = M * K + N * K + M * N * (2 if gelu else 1) + (M * N if resid else 0)
+        dx = M * N + N * K + M * K
+        dw = M * N + M * K + N * K
+        tot += fwd + dx + dw
+    # the GELU backward reads the saved pre-activation in the dX product of
+    # the layer after it (one extra M x N read per GELU layer)
+    tot += sum(M * N for M, K, N, gelu, _ in _gemm_list(dm, obs_rows) if gelu)
+    return 4.0 * tot
+
+
+def measured_gemm_traffic():
+    """HBM bytes per GEMM launch measured with rocprofv3 --pmc (FETCH_SIZE,
+    WRITE_SIZE, copy-kernel calibrated) for this workload, read from the
+    committed profile summary; None when absent."""
+    import re
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                        "ptcg_step_b512_fp32_gemm_hbm_traffic.md")
+    try:
+        txt = open(path).read()
+    except OSError:
+        return None
+    m = re.search(r"traffic_bytes_per_launch\s*\|\s*([0-9.e+]+)", txt)
+    return float(m.group(1)) if m else None
+
+
 def cpu_baseline(dm, obs, inp, B, budget_s):
     """Oracle (torch CPU) fwd+bwd+PPO+clip+Adam on B-row minibatches of the
     same rollout until `budget_s` of CPU work; returns obs/s and the sample."""
@@ -100,6 +152,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--workload", choices=("train", "rollout", "frozen", "bf16"), default="train")
     ap.add_argument("--rollout-rows", type=int, default=8192)
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run three 256 MiB device-to-device copies (the HBM counter calibration)")
     ap.add_argument("--sync-free", action="store_true",
                     help="compact row count kept on the device (no host read-back per forward)")
     args = ap.parse_args()
@@ -109,6 +163,17 @@ def main():
         sys.exit(2)
 
     import torch
+    if args.copy_calibration:
+        # a plain copy of known size: rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE of
+        # this run give the counters' scale (bytes read / written per KiB counted)
+        n = 64 << 20
+        x = torch.ones(n, device="cuda")
+        y = torch.empty(n, device="cuda")
+        for _ in range(3):
+            y.copy_(x)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes": n * 4, "copies": 3}), flush=True)
+        return
     import __graft_entry__
     __graft_entry__.load_package()
     from ptcg_amd import dims, synth, trainer, native
@@ -170,10 +235,12 @@ def main():
         print(json.dumps(line), flush=True)
         return
     useful = 0.0
+    abytes = 0.0
     lv = []
     for ix in lists[args.warmup:]:
         f, l = useful_gemm_flops(dm, obs[ix])
         useful += f
+        abytes += algorithmic_gemm_bytes(dm, obs[ix])
         lv.append(l)
     gemm_s = ms.value / 1e3
     achieved = useful / gemm_s / 1e12
@@ -181,7 +248,9 @@ def main():
     kname = "gemm_bf16_kernel" if bf16 else "gemm_f32_dma_kernel + gemm_f32_kernel"
     roof = dict(bound="mfma", kernel=f"{kname} (all launches: trunk, token, option and head GEMMs)",
                 achieved=round(achieved, 3), peak=peak, unit="TFLOP/s",
-                frac=round(achieved / peak, 4), traffic=None,
+                frac=round(achieved / peak, 4),
+                traffic=None if bf16 else measured_gemm_traffic(),
+                algorithmic_bytes_per_launch=round(abytes / max(launches.value, 1)),
                 launches_per_step=launches.value / K,
                 avg_launch_us=round(ms.value * 1e3 / max(launches.value, 1), 3),
                 gemm_ms_per_step=round(ms.value / K, 4),

@@ -41,20 +41,32 @@ TRAIN = dict(learning_rate=3e-4, beta1=0.9, beta2=0.999, eps=1e-8, max_grad_norm
              clip_coef=0.2, vf_clip_coef=0.2, vf_coef=0.5, ent_coef=0.01)
 
 
+def option_rows(dm, obs_rows):
+    """Option rows the loss can see: each row's legal options (all of them
+    in a row with none legal); a masked option's score reaches the PPO loss
+    only as the constant -1e4."""
+    off = dm.offsets()
+    mask = obs_rows[:, off["opt_mask"][0]:off["opt_mask"][1]] != 0
+    legal = mask.sum(1)
+    return float(np.where(legal > 0, legal, dm.n_opt).sum())
+
+
 def useful_gemm_flops(dm, obs_rows):
-    """Useful (valid-token) GEMM flops of one fwd+bwd over `obs_rows`:
-    token rows count only valid tokens (+READOUT in the trunk); every
-    GEMM's backward is 2x its forward (dX and dW), so fwd+bwd = 3x fwd."""
+    """Useful GEMM flops of one fwd+bwd over `obs_rows`: token rows count
+    only valid tokens (+READOUT in the trunk), option rows only the options
+    the loss can see; every GEMM's backward is 2x its forward (dX and dW),
+    so fwd+bwd = 3x fwd."""
     from ptcg_amd.params import OPT_E, SC_H, VAL_H, DEC_H
     off = dm.offsets()
     zone = obs_rows[:, off["tok_int"][0]:off["tok_int"][1]].reshape(len(obs_rows), dm.l_tok, dm.tok_int)[:, :, 1]
     n_valid = (zone > 0).sum(1).astype(np.float64)
     Lv = n_valid + 1
-    d, ffn, NO, B = dm.d, dm.ffn, dm.n_opt, len(obs_rows)
+    d, ffn, B = dm.d, dm.ffn, len(obs_rows)
+    NJ = option_rows(dm, obs_rows)
     tok_in = 2 * dm.d_c + dm.tok_f + 12
     fwd = 2.0 * n_valid.sum() * tok_in * d
     fwd += dm.layers * (Lv.sum() * (8 * d * d + 4 * d * ffn))
-    fwd += 2.0 * B * NO * (dm.d_c * OPT_E + dm.d_a * OPT_E + dm.q_in * d + d * d + dm.score_in * SC_H)
+    fwd += 2.0 * NJ * (dm.d_c * OPT_E + dm.d_a * OPT_E + dm.q_in * d + d * d + dm.score_in * SC_H)
     fwd += 2.0 * B * (dm.global_f * dm.g + dm.g * dm.g + dm.dec_in * DEC_H + DEC_H * DEC_H
                       + dm.bcast_in * d + dm.val_in * VAL_H)
     return 3.0 * fwd, float(Lv.mean())
@@ -69,7 +81,7 @@ def _gemm_list(dm, obs_rows):
     n_valid = float((zone > 0).sum())
     R = n_valid + len(obs_rows)
     d, ffn, B = dm.d, dm.ffn, len(obs_rows)
-    NJ = B * dm.n_opt
+    NJ = option_rows(dm, obs_rows)
     g = [(n_valid, 2 * dm.d_c + dm.tok_f + 12, d, 0, 0)]
     for _ in range(dm.layers):
         g += [(R, d, 3 * d, 0, 0), (R, d, d, 0, 1), (R, d, ffn, 1, 0), (R, ffn, d, 0, 1)]

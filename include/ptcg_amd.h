@@ -115,6 +115,14 @@ int ptcg_model_set_precision(PtcgModel* m, int prec);
  * stay stream-ordered and can be captured in a HIP graph, as the
  * reference's are (pufferlib.cu:2019-2140).  Results are the same.        */
 int ptcg_model_set_sync_free(PtcgModel* m, int on);
+/* Masked-option skipping, for callers whose loss masks illegal options
+ * (the PPO loss maps opt_mask == 0 to the constant logit -1e4,
+ * pufferlib.cu:949-962, so such a slot's score never reaches the loss and
+ * its gradient is exactly 0 whenever the row has a legal option).  1: the
+ * option scorer runs only each row's legal options (all of them when none is
+ * legal), forward and backward; masked slots of the output read 0.  0
+ * (default): every slot is scored, as the reference's forward does.       */
+int ptcg_model_set_skip_masked_options(PtcgModel* m, int on);
 /* ptcg_bind_train_graph (ptcg_model2.cu:323-330), oracle-critic models
  * (dims.critic == 1): device array of per-row returns the blind-value aux
  * loss regresses to, indexed like the obs rows of the forward (through its
@@ -200,6 +208,10 @@ int ptcg_trainer_rollout(PtcgTrainer* t, const float* obs, const int32_t* row_id
 int ptcg_trainer_set_precision(PtcgTrainer* t, int prec);
 /* ptcg_model_set_sync_free on the trainer's models (train and rollout).   */
 int ptcg_trainer_set_sync_free(PtcgTrainer* t, int on);
+/* Masked-option skipping in the trainer's own steps and rollouts (default
+ * on: its PPO loss and sampler mask those slots); debug_forward always
+ * scores every slot.                                                      */
+int ptcg_trainer_set_skip_masked_options(PtcgTrainer* t, int on);
 /* ptcg_model_set_static on the trainer's model.                          */
 int ptcg_trainer_set_static(PtcgTrainer* t, const float* card_static, const float* att_static,
                             const float* card_text, const float* att_text, const float* skill_text,

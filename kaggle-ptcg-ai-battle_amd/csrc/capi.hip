@@ -281,6 +281,7 @@ struct PtcgTrainer {
     int roll_n = 0;
     int prec = 0;
     int sync_free = 0;
+    int skip_masked = 1;   // the PPO loss and the sampler mask those slots
     std::vector<float> st_f[5];
     std::vector<int32_t> st_i[2];
 };
@@ -304,6 +305,7 @@ extern "C" int ptcg_trainer_create(const PtcgDims* dims, const PtcgHypers* hyp, 
     t->off = pt_obs_offsets(*dims);
     int r = ptcg_model_create(dims, &t->model);
     if (r != PTCG_OK) { delete t; return r; }
+    ptcg_model_set_skip_masked_options(t->model, t->skip_masked);
     t->arena = pt_model_arena(t->model);
     t->packed = ptcg_packed_floats(dims);
     const long A1 = dims->n_opt + 1;
@@ -474,7 +476,11 @@ extern "C" int ptcg_trainer_debug_forward(PtcgTrainer* t, const float* obs_host,
                (long)t->B * t->off.size, t->B, t->off.size, (long)n * t->off.size);
     PT_HIP(hipMemcpy(t->dbg_obs, obs_host, (size_t)n * t->off.size * sizeof(float), hipMemcpyHostToDevice));
     float* out = nullptr;
-    PT_TRY(ptcg_model_forward(t->model, t->dbg_obs, nullptr, n, &out, nullptr));
+    // debug_forward reports every slot's score, as the reference's does
+    PT_TRY(ptcg_model_set_skip_masked_options(t->model, 0));
+    const int rf = ptcg_model_forward(t->model, t->dbg_obs, nullptr, n, &out, nullptr);
+    PT_TRY(ptcg_model_set_skip_masked_options(t->model, t->skip_masked));
+    PT_TRY(rf);
     PT_HIP(hipStreamSynchronize(nullptr));
     PT_HIP(hipMemcpy(out_host, out, (size_t)n * (t->dm.n_opt + 1) * sizeof(float), hipMemcpyDeviceToHost));
     return PTCG_OK;
@@ -534,6 +540,14 @@ extern "C" int ptcg_trainer_set_precision(PtcgTrainer* t, int prec) {
     return PTCG_OK;
 }
 
+extern "C" int ptcg_trainer_set_skip_masked_options(PtcgTrainer* t, int on) {
+    PT_REQUIRE(t, "trainer_set_skip_masked_options: null trainer");
+    PT_TRY(ptcg_model_set_skip_masked_options(t->model, on));
+    if (t->roll) PT_TRY(ptcg_model_set_skip_masked_options(t->roll, on));
+    t->skip_masked = on != 0;
+    return PTCG_OK;
+}
+
 extern "C" int ptcg_trainer_set_sync_free(PtcgTrainer* t, int on) {
     PT_REQUIRE(t, "trainer_set_sync_free: null trainer");
     PT_TRY(ptcg_model_set_sync_free(t->model, on));
@@ -553,6 +567,7 @@ extern "C" int ptcg_trainer_rollout(PtcgTrainer* t, const float* obs, const int3
             PT_TRY(ptcg_model_bind(t->roll, t->P, t->Gr));
             PT_TRY(ptcg_model_set_precision(t->roll, t->prec));
             PT_TRY(ptcg_model_set_sync_free(t->roll, t->sync_free));
+            PT_TRY(ptcg_model_set_skip_masked_options(t->roll, t->skip_masked));
             if (t->dm.tables == 1 && !t->st_i[0].empty())
                 PT_TRY(ptcg_model_set_static(t->roll, t->st_f[0].data(), t->st_f[1].data(), t->st_f[2].data(),
                                              t->st_f[3].data(), t->st_f[4].data(), t->st_i[0].data(),

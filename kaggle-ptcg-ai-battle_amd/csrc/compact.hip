@@ -89,6 +89,37 @@ __global__ void compact_fill_kernel(GatherCtx c, const int* __restrict__ act, co
     }
 }
 
+// One wave per sample: the legal options (mask != 0) of sample n, or all of
+// them when none is legal.  A masked option's score enters the loss only as
+// the constant -1e4 and gets exactly zero gradient whenever some option is
+// legal, so only these rows need the option scorer in training.
+__device__ __forceinline__ bool opt_on(const float* mk, int j, bool none) { return none || mk[j] != 0.f; }
+__global__ void opt_count_kernel(GatherCtx c, int* __restrict__ cnt) {
+    const int n = blockIdx.x, NO = c.dm.n_opt, lane = threadIdx.x;
+    const float* mk = obs_row(c.obs, c.idx, c.stride, n) + c.off.opt_mask;
+    int legal = 0;
+    for (int j0 = 0; j0 < NO; j0 += 64) {
+        const int j = j0 + lane;
+        legal += __popcll(__ballot(j < NO && mk[j] != 0.f));
+    }
+    if (lane == 0) cnt[n] = legal > 0 ? legal : NO;
+}
+__global__ void opt_fill_kernel(GatherCtx c, const int* __restrict__ ooff, int* __restrict__ orow) {
+    const int n = blockIdx.x, NO = c.dm.n_opt, lane = threadIdx.x;
+    const float* mk = obs_row(c.obs, c.idx, c.stride, n) + c.off.opt_mask;
+    int legal = 0;
+    for (int j0 = 0; j0 < NO; j0 += 64) legal += __popcll(__ballot(j0 + lane < NO && mk[j0 + lane] != 0.f));
+    const bool none = legal == 0;
+    int base = ooff[n];
+    for (int j0 = 0; j0 < NO; j0 += 64) {
+        const int j = j0 + lane;
+        const bool on = j < NO && opt_on(mk, j, none);
+        const unsigned long long bal = __ballot(on);
+        if (on) orow[base + __popcll(bal & ((1ull << lane) - 1ull))] = n * NO + j;
+        base += __popcll(bal);
+    }
+}
+
 __global__ void gather_rows_kernel(const float* __restrict__ src, long ld, const int* __restrict__ coff, int N,
                                    int D, float* __restrict__ dst) {
     const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
@@ -107,6 +138,16 @@ int pt_compact_map(const GatherCtx& c, int* act, int* cnt, int* coff, int* rowma
     hipLaunchKernelGGL(compact_scan_kernel, dim3(1), dim3(256), 0, s, cnt, c.N, coff);
     PT_LAUNCH_CHECK();
     hipLaunchKernelGGL(compact_fill_kernel, dim3(c.N), dim3(64), 0, s, c, act, coff, rowmap, rsam, rpos);
+    PT_LAUNCH_CHECK();
+    return PTCG_OK;
+}
+
+int pt_opt_map(const GatherCtx& c, int* cnt, int* ooff, int* orow, hipStream_t s) {
+    hipLaunchKernelGGL(opt_count_kernel, dim3(c.N), dim3(64), 0, s, c, cnt);
+    PT_LAUNCH_CHECK();
+    hipLaunchKernelGGL(compact_scan_kernel, dim3(1), dim3(256), 0, s, cnt, c.N, ooff);
+    PT_LAUNCH_CHECK();
+    hipLaunchKernelGGL(opt_fill_kernel, dim3(c.N), dim3(64), 0, s, c, ooff, orow);
     PT_LAUNCH_CHECK();
     return PTCG_OK;
 }

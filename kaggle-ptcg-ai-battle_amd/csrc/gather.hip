@@ -298,13 +298,13 @@ __global__ void opt_gather_fwd_kernel(GatherCtx c, const float* __restrict__ car
     const int NO = c.dm.n_opt, dc = c.dm.d_c, da = c.dm.d_a;
     const int W = dc > da ? dc : da;
     const long i = (long)blockIdx.x * TB + threadIdx.x;
-    if (i >= (long)c.N * NO * W) return;
+    if (i >= pt_orows(c) * W) return;
     const int e = (int)(i % W);
-    const long nj = i / W;
+    const long row = i / W, nj = pt_onj(c, row);   // option row, option
     const int n = (int)(nj / NO), j = (int)(nj % NO);
     const float* oi = obs_row(c.obs, c.idx, c.stride, n) + c.off.opt_int + (long)j * c.dm.opt_int;
-    if (e < dc) ocard[nj * dc + e] = card[(long)pt_id_clamp(oi[3], c.dm.n_cards - 1) * dc + e];
-    if (e < da) oatt[nj * da + e] = att[(long)pt_id_clamp(oi[4], c.dm.n_attacks - 1) * da + e];
+    if (e < dc) ocard[row * dc + e] = card[(long)pt_id_clamp(oi[3], c.dm.n_cards - 1) * dc + e];
+    if (e < da) oatt[row * da + e] = att[(long)pt_id_clamp(oi[4], c.dm.n_attacks - 1) * da + e];
 }
 
 // option card / attack backward: thread = column (d_c card columns, then
@@ -321,11 +321,12 @@ __global__ void opt_gather_bwd_kernel(GatherCtx c, const float* __restrict__ d_o
     float* tab = is_card ? d_card : d_att;
     const int hi = is_card ? c.dm.n_cards - 1 : c.dm.n_attacks - 1;
     const int slot = is_card ? 3 : 4;
-    const long nj0 = (long)blockIdx.x * SCATTER_ROWS, nj1 = min((long)c.N * NO, nj0 + SCATTER_ROWS);
+    const long r0 = (long)blockIdx.x * SCATTER_ROWS, r1 = min(pt_orows(c), r0 + SCATTER_ROWS);
     IdCache k;
-    for (long nj = nj0; nj < nj1; ++nj) {
-        const float g = src[nj * w + e];
+    for (long row = r0; row < r1; ++row) {
+        const float g = src[row * w + e];
         if (g == 0.f) continue;
+        const long nj = pt_onj(c, row);
         const int n = (int)(nj / NO), j = (int)(nj % NO);
         const float* oi = obs_row(c.obs, c.idx, c.stride, n) + c.off.opt_int + (long)j * c.dm.opt_int;
         k.add(tab, w, e, pt_id_clamp(oi[slot], hi), g);
@@ -338,9 +339,9 @@ __global__ void q_in_fwd_kernel(GatherCtx c, const float* __restrict__ h,
         const float* __restrict__ temb, float* __restrict__ q_in) {
     const int NO = c.dm.n_opt, D = c.dm.d, W = c.dx.q_in, ch = W / 4;
     const long i = (long)blockIdx.x * TB + threadIdx.x;
-    if (i >= (long)c.N * NO * ch) return;
+    if (i >= pt_orows(c) * ch) return;
     const int col = (int)(i % ch) * 4;
-    const long nj = i / ch;
+    const long orow = i / ch, nj = pt_onj(c, orow);   // option row, option
     const int n = (int)(nj / NO), j = (int)(nj % NO);
     const int oc0 = PT_TYPE_E + 2 * D, of0 = oc0 + 2 * PT_OPT_E;
     if (col >= oc0 && col < of0) return;      // written by the opt_card / opt_attack GEMMs
@@ -358,7 +359,7 @@ __global__ void q_in_fwd_kernel(GatherCtx c, const float* __restrict__ h,
     } else {
         v = *reinterpret_cast<const float4*>(row + c.off.opt_float + (long)j * c.dm.opt_f + (col - of0));
     }
-    *reinterpret_cast<float4*>(q_in + nj * W + col) = v;
+    *reinterpret_cast<float4*>(q_in + orow * W + col) = v;
 }
 
 // one workgroup per sample: d_h[n,p] += d_qin pointer slices.  A thread
@@ -369,10 +370,13 @@ __global__ void q_in_bwd_kernel(GatherCtx c, const float* __restrict__ d_qin, fl
                                 float* d_temb) {
     const int n = blockIdx.x, NO = c.dm.n_opt, D = c.dm.d, W = c.dx.q_in;
     const float* row = obs_row(c.obs, c.idx, c.stride, n);
+    // the sample's option rows
+    const long b0 = c.ooff ? c.ooff[n] : (long)n * NO, b1 = c.ooff ? c.ooff[n + 1] : b0 + NO;
     for (int col = threadIdx.x; col < D; col += TB) {
-        for (int j = 0; j < NO; ++j) {
+        for (long q = b0; q < b1; ++q) {
+            const int j = (int)(pt_onj(c, q) % NO);
             const float* oi = row + c.off.opt_int + (long)j * c.dm.opt_int;
-            const float* g = d_qin + ((long)n * NO + j) * W;
+            const float* g = d_qin + q * W;
             const int p1 = (int)oi[1], p2 = (int)oi[2];
             if (p1 > 0 && p1 <= c.dm.l_tok) {
                 const float v = g[PT_TYPE_E + col];
@@ -386,10 +390,10 @@ __global__ void q_in_bwd_kernel(GatherCtx c, const float* __restrict__ d_qin, fl
     }
     if (threadIdx.x < PT_TYPE_E) {
         IdCache k;
-        for (int j = 0; j < NO; ++j) {
+        for (long q = b0; q < b1; ++q) {
+            const int j = (int)(pt_onj(c, q) % NO);
             const float* oi = row + c.off.opt_int + (long)j * c.dm.opt_int;
-            k.add(d_temb, PT_TYPE_E, threadIdx.x, pt_id_clamp(oi[0], c.dm.n_opt_types - 1),
-                  d_qin[((long)n * NO + j) * W + threadIdx.x]);
+            k.add(d_temb, PT_TYPE_E, threadIdx.x, pt_id_clamp(oi[0], c.dm.n_opt_types - 1), d_qin[q * W + threadIdx.x]);
         }
         k.flush(d_temb, PT_TYPE_E, threadIdx.x);
     }
@@ -401,12 +405,12 @@ __global__ void sc_in_fwd_kernel(GatherCtx c, const float* __restrict__ h,
     const int NO = c.dm.n_opt, D = c.dm.d, G = c.dm.g, W = c.dx.score_in;
     const int cw = W - D, ch = cw / 4;
     const long i = (long)blockIdx.x * TB + threadIdx.x;
-    if (i >= (long)c.N * NO * ch) return;
+    if (i >= pt_orows(c) * ch) return;
     const int col = D + (int)(i % ch) * 4;
-    const long nj = i / ch;
-    const int n = (int)(nj / NO);
+    const long row = i / ch;
+    const int n = (int)(pt_onj(c, row) / NO);
     const float* r = h + pt_hrow(c, n, 0) * D;
-    float* o = sc + nj * W;
+    float* o = sc + row * W;
     float4 v;
     if (col < 2 * D) v = *reinterpret_cast<const float4*>(r + (col - D));
     else if (col < 2 * D + G + PT_DEC_H) v = *reinterpret_cast<const float4*>(gd + (long)n * c.dx.bcast_in + (col - 2 * D));
@@ -431,12 +435,15 @@ __global__ __launch_bounds__(TB * SC_OG) void sc_in_bwd_kernel(GatherCtx c, cons
     const int o_r = D, o_g = 2 * D, o_dv = 2 * D + G, o_qr = 2 * D + G + PT_DEC_H;
     const int span = max(D, max(G, (int)PT_DEC_H));
     const int og = threadIdx.x / TB, t = threadIdx.x % TB;
-    const int j0 = og * NO / SC_OG, j1 = (og + 1) * NO / SC_OG;
+    // the sample's option rows [b0, b0 + no), split into SC_OG contiguous groups
+    const long b0 = c.ooff ? c.ooff[n] : (long)n * NO;
+    const int no = c.ooff ? c.ooff[n + 1] - c.ooff[n] : NO;
+    const int j0 = og * no / SC_OG, j1 = (og + 1) * no / SC_OG;
     for (int col = t; col < span; col += TB) {
-        const float r = col < D ? sc[(long)n * NO * W + o_r + col] : 0.f;
+        const float r = col < D ? sc[b0 * W + o_r + col] : 0.f;
         float ar = 0.f, ag = 0.f, adv = 0.f;
         for (int j = j0; j < j1; ++j) {
-            const long nj = (long)n * NO + j;
+            const long nj = b0 + j;
             const float* g = d_sc + nj * W;
             if (col < D) {
                 const float q = sc[nj * W + col];
@@ -487,9 +494,17 @@ __global__ void val_in_bwd_kernel(GatherCtx c, const float* __restrict__ dv, flo
 }
 
 // one wave per row: out = X[r,:] . w + b
+// head rows: rmap (nullable) maps a row to its output / gradient slot q,
+// rows_dev (nullable) bounds the rows on the device
+__device__ __forceinline__ long hd_slot(const int* rmap, int r, int per, long ld, int col0) {
+    const int q = rmap ? rmap[r] : r;
+    return (long)(q / per) * ld + col0 + (q % per);
+}
+
 __global__ void head_dot_kernel(const float* __restrict__ X, int rows, int K,
         const float* __restrict__ w, const float* __restrict__ b, float* __restrict__ out, int per,
-        long ldo, int col0) {
+        long ldo, int col0, const int* __restrict__ rmap, const int* __restrict__ rows_dev) {
+    if (rows_dev) rows = min(rows, *rows_dev);
     const int lane = threadIdx.x & 63;
     const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (r >= rows) return;
@@ -497,16 +512,17 @@ __global__ void head_dot_kernel(const float* __restrict__ X, int rows, int K,
     float s = 0.f;
     for (int k = lane; k < K; k += 64) s += x[k] * w[k];
     s = wave_sum(s);
-    if (lane == 0) out[(long)(r / per) * ldo + col0 + (r % per)] = s + b[0];
+    if (lane == 0) out[hd_slot(rmap, r, per, ldo, col0)] = s + b[0];
 }
 
 __global__ void head_dot_bwd_kernel(const float* __restrict__ grad, int per, long ldg, int col0,
         const float* __restrict__ w, const float* __restrict__ pre, float* __restrict__ dX, int rows,
-        int K) {
+        int K, const int* __restrict__ rmap, const int* __restrict__ rows_dev) {
+    if (rows_dev) rows = min(rows, *rows_dev);
     const long i = (long)blockIdx.x * TB + threadIdx.x;
     if (i >= (long)rows * K) return;
     const int r = (int)(i / K), k = (int)(i % K);
-    const float dy = grad[(long)(r / per) * ldg + col0 + (r % per)];
+    const float dy = grad[hd_slot(rmap, r, per, ldg, col0)];
     dX[i] = dy * w[k] * pt_gelu_grad(pre[i]);
 }
 
@@ -514,13 +530,15 @@ constexpr int HD_ROWS = 64;
 // partial[chunk][0..K) = sum dy*X, partial[chunk][K] = sum dy (every thread
 // forms the dy sum alongside its column; thread 0 stores it)
 __global__ void head_dot_dw_partial_kernel(const float* __restrict__ grad, int per, long ldg,
-        int col0, const float* __restrict__ X, int rows, int K, float* __restrict__ part) {
+        int col0, const float* __restrict__ X, int rows, int K, float* __restrict__ part,
+        const int* __restrict__ rmap, const int* __restrict__ rows_dev) {
+    if (rows_dev) rows = min(rows, *rows_dev);
     const int r0 = blockIdx.x * HD_ROWS, r1 = min(rows, r0 + HD_ROWS);
     for (int k0 = 0; k0 < K; k0 += TB) {
         const int k = k0 + threadIdx.x;
         float s = 0.f, sd = 0.f;
         for (int r = r0; r < r1; ++r) {
-            const float dy = grad[(long)(r / per) * ldg + col0 + (r % per)];
+            const float dy = grad[hd_slot(rmap, r, per, ldg, col0)];
             sd += dy;
             if (k < K) s += dy * X[(long)r * K + k];
         }
@@ -610,7 +628,7 @@ int pt_x0_bwd(const GatherCtx& c, const float* d_x0, float* d_tokp, float* d_bc,
     return PTCG_OK;
 }
 int pt_opt_gather_fwd(const GatherCtx& c, const float* card, const float* att, float* ocard, float* oatt,
-                      hipStream_t s) {
+                      hipStream_t s) {   // grids sized for all N * n_opt option rows
     const int W = c.dm.d_c > c.dm.d_a ? c.dm.d_c : c.dm.d_a;
     hipLaunchKernelGGL(opt_gather_fwd_kernel, PT_GRID((long)c.N * c.dm.n_opt * W), c, card, att, ocard, oatt);
     PT_LAUNCH_CHECK();
@@ -661,22 +679,26 @@ int pt_val_in_bwd(const GatherCtx& c, const float* d_val_in, float* d_h, float* 
     return PTCG_OK;
 }
 int pt_head_dot(const float* X, int rows, int K, const float* w, const float* b, float* out, int per,
-                long ldo, int col0, hipStream_t s) {
-    hipLaunchKernelGGL(head_dot_kernel, dim3(pt_cdiv(rows, 4)), dim3(256), 0, s, X, rows, K, w, b, out, per, ldo, col0);
+                long ldo, int col0, hipStream_t s, const int* rmap, const int* rows_dev) {
+    hipLaunchKernelGGL(head_dot_kernel, dim3(pt_cdiv(rows, 4)), dim3(256), 0, s, X, rows, K, w, b, out, per, ldo, col0,
+                       rmap, rows_dev);
     PT_LAUNCH_CHECK();
     return PTCG_OK;
 }
 int pt_head_dot_bwd(const float* grad, int per, long ldg, int col0, const float* w, const float* pre,
-                    float* dX, int rows, int K, hipStream_t s) {
-    hipLaunchKernelGGL(head_dot_bwd_kernel, PT_GRID((long)rows * K), grad, per, ldg, col0, w, pre, dX, rows, K);
+                    float* dX, int rows, int K, hipStream_t s, const int* rmap, const int* rows_dev) {
+    hipLaunchKernelGGL(head_dot_bwd_kernel, PT_GRID((long)rows * K), grad, per, ldg, col0, w, pre, dX, rows, K, rmap,
+                       rows_dev);
     PT_LAUNCH_CHECK();
     return PTCG_OK;
 }
 int pt_head_dot_dw(const float* grad, int per, long ldg, int col0, const float* X, int rows, int K,
-                   float* dw, float* db, float* ws, long ws_floats, hipStream_t s) {
+                   float* dw, float* db, float* ws, long ws_floats, hipStream_t s, const int* rmap,
+                   const int* rows_dev) {
     const int chunks = pt_cdiv(rows, HD_ROWS);
     PT_REQUIRE(ws && (long)chunks * (K + 1) <= ws_floats, "head dw: workspace too small");
-    hipLaunchKernelGGL(head_dot_dw_partial_kernel, dim3(chunks), dim3(TB), 0, s, grad, per, ldg, col0, X, rows, K, ws);
+    hipLaunchKernelGGL(head_dot_dw_partial_kernel, dim3(chunks), dim3(TB), 0, s, grad, per, ldg, col0, X, rows, K, ws,
+                       rmap, rows_dev);
     PT_LAUNCH_CHECK();
     hipLaunchKernelGGL(head_dot_dw_final_kernel, dim3(K + 1), dim3(TB), 0, s, ws, chunks, K, dw, db);
     PT_LAUNCH_CHECK();

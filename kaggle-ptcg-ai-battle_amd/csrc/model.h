@@ -75,7 +75,18 @@ struct GatherCtx {
     // the row of an active position (-1 otherwise); rsam / rpos invert it;
     // *rows = coff[N].
     const int* coff; const int* rowmap; const int* rsam; const int* rpos; const int* rows;
+    // compact option rows (null = all n_opt options, row n*n_opt + j): sample
+    // n's legal options (every option when it has none legal) are rows
+    // [ooff[n], ooff[n+1]) in slot order; orow[i] = n*n_opt + j of row i;
+    // *orows = ooff[N]
+    const int* orow; const int* ooff; const int* orows;
 };
+// option (n * n_opt + j) of option row i
+__device__ __forceinline__ long pt_onj(const GatherCtx& c, long i) { return c.orow ? (long)c.orow[i] : i; }
+// option rows of the launch: the device count bounds the compact layout
+__device__ __forceinline__ long pt_orows(const GatherCtx& c) {
+    return c.orow ? (long)*c.orows : (long)c.N * c.dm.n_opt;
+}
 // trunk row of (sample n, position pos); pos must be active in the compact layout
 __device__ __forceinline__ long pt_hrow(const GatherCtx& c, int n, int pos) {
     return c.rowmap ? (long)c.rowmap[(long)n * c.dx.l_seq + pos] : (long)n * c.dx.l_seq + pos;
@@ -104,15 +115,19 @@ int pt_sc_in_bwd(const GatherCtx& c, const float* d_sc, const float* sc_in, floa
 // [seq[:, 0] | g] over sequences of ls rows (ls = 0: the trunk's l_seq)
 int pt_val_in_fwd(const GatherCtx& c, const float* h, const float* gd, float* val_in, hipStream_t s, int ls = 0);
 int pt_val_in_bwd(const GatherCtx& c, const float* d_val_in, float* d_h, float* d_gd, hipStream_t s, int ls = 0);
-// y[r] = X[r,:] . w + b, written to out[r / per * ldo + col0 + r % per]
+// y[r] = X[r,:] . w + b, written to out[q / per * ldo + col0 + q % per], q = rmap ? rmap[r] : r;
+// rows_dev (nullable): device row count <= rows
 int pt_head_dot(const float* X, int rows, int K, const float* w, const float* b, float* out,
-                int per, long ldo, int col0, hipStream_t s);
-// dX[r,:] = dy[r] * w[:] * gelu'(pre[r,:]),  dy[r] = grad[r / per * ldg + col0 + r % per]
+                int per, long ldo, int col0, hipStream_t s, const int* rmap = nullptr,
+                const int* rows_dev = nullptr);
+// dX[r,:] = dy[r] * w[:] * gelu'(pre[r,:]),  dy[r] = grad[q / per * ldg + col0 + q % per]
 int pt_head_dot_bwd(const float* grad, int per, long ldg, int col0, const float* w,
-                    const float* pre, float* dX, int rows, int K, hipStream_t s);
+                    const float* pre, float* dX, int rows, int K, hipStream_t s, const int* rmap = nullptr,
+                    const int* rows_dev = nullptr);
 // dw[k] = sum_r dy[r] X[r,k]; db = sum_r dy[r]   (fixed order)
 int pt_head_dot_dw(const float* grad, int per, long ldg, int col0, const float* X, int rows, int K,
-                   float* dw, float* db, float* ws, long ws_floats, hipStream_t s);
+                   float* dw, float* db, float* ws, long ws_floats, hipStream_t s, const int* rmap = nullptr,
+                   const int* rows_dev = nullptr);
 int pt_fill_zero(float* p, long n, hipStream_t s);
 
 // ---- reference model variant: static tables, oracle critic, aux losses (frozen.hip)
@@ -136,5 +151,8 @@ int pt_rank1_add(const float* dy, const float* w, float* dX, int rows, int K, hi
 // row offsets, row maps; act is scratch of N * l_seq ints.
 int pt_compact_map(const GatherCtx& c, int* act, int* cnt, int* coff, int* rowmap, int* rsam, int* rpos,
                    hipStream_t s);
+// Option rows of each sample: its legal options (opt_mask != 0), or all of
+// them when none is legal; per-sample counts, offsets, row -> option map.
+int pt_opt_map(const GatherCtx& c, int* cnt, int* ooff, int* orow, hipStream_t s);
 // dst[n] = src[coff[n]]  (rows of width D)
 int pt_gather_rows(const float* src, long ld, const int* coff, int N, int D, float* dst, hipStream_t s);

@@ -78,9 +78,18 @@ struct PtcgModel {
     bool sync_free = false;
     int *c_act = nullptr, *c_cnt, *c_off, *c_map, *c_rsam, *c_rpos;
     const int* Tr = nullptr;
-    int* rows_h = nullptr;
+    int* rows_h = nullptr;   // pinned: [trunk rows, option rows]
     int rows = 0;
     const int* Tdev = nullptr;
+    // masked-option skipping (a loss that masks them, as the PPO loss does):
+    // the option scorer runs only each sample's legal options (all of them
+    // when none is legal), stored contiguously per sample (o_off, o_row);
+    // masked slots of the output read 0.  orows / Odev: host / device count,
+    // as rows / Tdev above.  skip_fwd: the mode the last forward ran in.
+    bool skip_masked = false, skip_fwd = false;
+    int *o_cnt = nullptr, *o_off = nullptr, *o_row = nullptr;
+    int orows = 0;
+    const int* Odev = nullptr;
     float* rd_buf = nullptr;
     char* mem = nullptr;
     size_t mem_bytes = 0;
@@ -394,6 +403,9 @@ static size_t carve(PtcgModel* m, char* base) {
     } else {
         m->Tr = nullptr;
     }
+    m->o_cnt = reinterpret_cast<int*>(c.take(N));
+    m->o_off = reinterpret_cast<int*>(c.take(N + 1));
+    m->o_row = reinterpret_cast<int*>(c.take(N * NO));
     m->glob_in = c.take(N * d.global_f);
     m->g1 = c.take(N * d.g); m->g1a = c.take(N * d.g);
     m->dec_in = c.take(N * x.dec_in);
@@ -459,7 +471,7 @@ static size_t carve(PtcgModel* m, char* base) {
 }
 
 static int reg(PtcgModel* m, int n, bool train) {
-    if (!m->rows_h) PT_HIP(hipHostMalloc((void**)&m->rows_h, sizeof(int), hipHostMallocDefault));
+    if (!m->rows_h) PT_HIP(hipHostMalloc((void**)&m->rows_h, 2 * sizeof(int), hipHostMallocDefault));
     if (m->mem) {
         PT_HIP(hipFree(m->mem));
         m->mem = nullptr;
@@ -471,6 +483,12 @@ static int reg(PtcgModel* m, int n, bool train) {
     PT_HIP(hipMalloc(&m->mem, bytes));
     m->mem_bytes = bytes;
     carve(m, m->mem);
+    return PTCG_OK;
+}
+
+extern "C" int ptcg_model_set_skip_masked_options(PtcgModel* m, int on) {
+    PT_REQUIRE(m, "model_set_skip_masked_options: null model");
+    m->skip_masked = on != 0;
     return PTCG_OK;
 }
 
@@ -564,19 +582,34 @@ extern "C" int ptcg_model_forward(PtcgModel* m, const float* obs, const int32_t*
     const int* coff = m->compact ? m->c_off : nullptr;
     m->rows = N * x.l_seq;
     m->Tdev = nullptr;
+    m->orows = N * NO;
+    m->Odev = nullptr;
+    const bool skip = m->skip_masked;
+    m->skip_fwd = skip;
     if (m->compact) {
         PT_TRY(pt_compact_map(c, m->c_act, m->c_cnt, m->c_off, m->c_map, m->c_rsam, m->c_rpos, s));
         c.coff = m->c_off; c.rowmap = m->c_map; c.rsam = m->c_rsam; c.rpos = m->c_rpos; c.rows = Tr;
+    }
+    if (skip) {
+        PT_TRY(pt_opt_map(c, m->o_cnt, m->o_off, m->o_row, s));
+        c.orow = m->o_row; c.ooff = m->o_off; c.orows = m->o_off + N;
+    }
+    if (m->compact || skip) {
         if (m->sync_free) {
-            m->Tdev = Tr;
+            m->Tdev = m->compact ? Tr : nullptr;
+            m->Odev = skip ? m->o_off + N : nullptr;
         } else {
-            // the step's one host read-back: the trunk row count sizes every
-            // launch that follows
-            PT_HIP(hipMemcpyAsync(m->rows_h, Tr, sizeof(int), hipMemcpyDeviceToHost, s));
+            // the step's one host read-back: the trunk and option row counts
+            // size every launch that follows
+            if (m->compact) PT_HIP(hipMemcpyAsync(m->rows_h, Tr, sizeof(int), hipMemcpyDeviceToHost, s));
+            if (skip) PT_HIP(hipMemcpyAsync(m->rows_h + 1, m->o_off + N, sizeof(int), hipMemcpyDeviceToHost, s));
             PT_HIP(hipStreamSynchronize(s));
-            m->rows = *m->rows_h;
+            if (m->compact) m->rows = m->rows_h[0];
+            if (skip) m->orows = m->rows_h[1];
             PT_REQUIRE(m->rows >= N && m->rows <= N * x.l_seq, "model_forward: compact row count %d out of range",
                        m->rows);
+            PT_REQUIRE(m->orows >= N && m->orows <= N * NO, "model_forward: option row count %d out of range",
+                       m->orows);
         }
     }
     const int* Td = m->Tdev;
@@ -602,20 +635,24 @@ extern "C" int ptcg_model_forward(PtcgModel* m, const float* obs, const int32_t*
     PT_TRY(pt_ln_fwd(m->x[tr ? d.layers : d.layers % 2], D, m->lnf_w, m->lnf_b, m->h, D, m->lnf_mu, m->lnf_rs,
                      m->rows, D, s, Td));
 
-    // option scorer
-    const int NJ = N * NO;
+    // option scorer over the option rows (all N * n_opt, or the legal ones)
+    const int NJ = m->orows;
+    const int* Od = m->Odev;
     const int oc0 = PT_TYPE_E + 2 * D, oa0 = oc0 + PT_OPT_E;
     PT_TRY(pt_opt_gather_fwd(c, m->card, m->att, m->ocard, m->oatt, s));
     PT_TRY(lin(m, m->ocard, d.d_c, m->oc_w, m->oc_b, m->q_in + oc0, x.q_in, NJ, d.d_c, PT_OPT_E, EPI_BIAS,
-               nullptr, 0, nullptr, 0, s));
+               nullptr, 0, nullptr, 0, s, Od));
     PT_TRY(lin(m, m->oatt, d.d_a, m->oa_w, m->oa_b, m->q_in + oa0, x.q_in, NJ, d.d_a, PT_OPT_E, EPI_BIAS,
-               nullptr, 0, nullptr, 0, s));
+               nullptr, 0, nullptr, 0, s, Od));
     PT_TRY(pt_q_in_fwd(c, m->h, m->temb, m->q_in, s));
-    PT_TRY(linf(m, m->q_in, m->q1_w, m->q1_b, m->q1, NJ, x.q_in, D, EPI_BIAS_GELU, nullptr, m->q1a, s));
-    PT_TRY(lin(m, m->q1a, D, m->q2_w, m->q2_b, m->sc_in, x.score_in, NJ, D, D, EPI_BIAS, nullptr, 0, nullptr, 0, s));
+    PT_TRY(linf(m, m->q_in, m->q1_w, m->q1_b, m->q1, NJ, x.q_in, D, EPI_BIAS_GELU, nullptr, m->q1a, s, Od));
+    PT_TRY(lin(m, m->q1a, D, m->q2_w, m->q2_b, m->sc_in, x.score_in, NJ, D, D, EPI_BIAS, nullptr, 0, nullptr, 0, s,
+               Od));
     PT_TRY(pt_sc_in_fwd(c, m->h, m->gd, m->sc_in, s));
-    PT_TRY(linf(m, m->sc_in, m->s1_w, m->s1_b, m->s1, NJ, x.score_in, PT_SC_H, EPI_BIAS_GELU, nullptr, m->s1a, s));
-    PT_TRY(pt_head_dot(m->s1a, NJ, PT_SC_H, m->s2_w, m->s2_b, m->out, NO, NO + 1, 0, s));
+    PT_TRY(linf(m, m->sc_in, m->s1_w, m->s1_b, m->s1, NJ, x.score_in, PT_SC_H, EPI_BIAS_GELU, nullptr, m->s1a, s,
+                Od));
+    if (skip) PT_TRY(pt_fill_zero(m->out, (long)N * (NO + 1), s));   // masked slots read 0
+    PT_TRY(pt_head_dot(m->s1a, NJ, PT_SC_H, m->s2_w, m->s2_b, m->out, NO, NO + 1, 0, s, skip ? m->o_row : nullptr, Od));
     // blind value head: the output value, or (oracle critic) an aux head
     PT_TRY(pt_val_in_fwd(c, m->h, m->gd, m->val_in, s));
     PT_TRY(linf(m, m->val_in, m->v1_w, m->v1_b, m->v1, N, x.val_in, PT_VAL_H, EPI_BIAS_GELU, nullptr, m->v1a, s));
@@ -743,14 +780,21 @@ extern "C" int ptcg_model_backward(PtcgModel* m, const float* grad, void* stream
     hipStream_t s = (hipStream_t)stream;
     const PtcgDims& d = m->dm;
     const DimsX& x = m->dx;
-    const int N = m->N, Lt = d.l_tok, NO = d.n_opt, D = d.d, G = d.g, NJ = N * NO;
+    const int N = m->N, Lt = d.l_tok, NO = d.n_opt, D = d.d, G = d.g;
     const int NL = N * x.l_seq;
     GatherCtx c{m->obs, m->idx, (long)m->off.size, N, d, x, m->off};
     const int* Tr = m->Tr;
     const int* coff = m->compact ? m->c_off : nullptr;
-    if (m->compact) {   // the map of the forward (same rows)
+    if (m->compact) {   // the maps of the forward (same rows)
         c.coff = m->c_off; c.rowmap = m->c_map; c.rsam = m->c_rsam; c.rpos = m->c_rpos; c.rows = Tr;
     }
+    const bool skip = m->skip_fwd;
+    if (skip) {
+        c.orow = m->o_row; c.ooff = m->o_off; c.orows = m->o_off + N;
+    }
+    const int NJo = m->orows;    // option rows of the forward
+    const int* Od = m->Odev;
+    const int* om = skip ? m->o_row : nullptr;
     const int rows = m->rows;        // trunk launch rows of the forward
     const int* Td = m->Tdev;         // and its device row count (sync-free mode)
     const int tok_rows = m->compact ? rows : N * Lt;
@@ -777,22 +821,28 @@ extern "C" int ptcg_model_backward(PtcgModel* m, const float* grad, void* stream
     }
 
     // option scores: grad[:, :NO]
-    PT_TRY(pt_head_dot_dw(grad, NO, NO + 1, 0, m->s1a, NJ, PT_SC_H, m->G(m->s2_w), m->G(m->s2_b), m->ws,
-                          m->ws_floats, s));
-    PT_TRY(pt_head_dot_bwd(grad, NO, NO + 1, 0, m->s2_w, m->s1, m->ds1, NJ, PT_SC_H, s));
-    PT_TRY(ldw_(m, m->ds1, PT_SC_H, m->sc_in, x.score_in, m->G(m->s1_w), m->G(m->s1_b), NJ, x.score_in, PT_SC_H, s));
-    PT_TRY(ldx_(m, m->ds1, PT_SC_H, m->s1_w, m->dsc, x.score_in, NJ, x.score_in, PT_SC_H, EPI_STORE, nullptr, 0, s));
+    PT_TRY(pt_head_dot_dw(grad, NO, NO + 1, 0, m->s1a, NJo, PT_SC_H, m->G(m->s2_w), m->G(m->s2_b), m->ws,
+                          m->ws_floats, s, om, Od));
+    PT_TRY(pt_head_dot_bwd(grad, NO, NO + 1, 0, m->s2_w, m->s1, m->ds1, NJo, PT_SC_H, s, om, Od));
+    PT_TRY(ldw_(m, m->ds1, PT_SC_H, m->sc_in, x.score_in, m->G(m->s1_w), m->G(m->s1_b), NJo, x.score_in, PT_SC_H, s,
+                Od));
+    PT_TRY(ldx_(m, m->ds1, PT_SC_H, m->s1_w, m->dsc, x.score_in, NJo, x.score_in, PT_SC_H, EPI_STORE, nullptr, 0, s,
+                Od));
     PT_TRY(pt_sc_in_bwd(c, m->dsc, m->sc_in, m->dq, m->dxa, m->dgd, s));
-    PT_TRY(ldw_(m, m->dq, D, m->q1a, D, m->G(m->q2_w), m->G(m->q2_b), NJ, D, D, s));
-    PT_TRY(ldx_(m, m->dq, D, m->q2_w, m->dq1, D, NJ, D, D, EPI_GELU_BWD, m->q1, D, s));
-    PT_TRY(ldw_(m, m->dq1, D, m->q_in, x.q_in, m->G(m->q1_w), m->G(m->q1_b), NJ, x.q_in, D, s));
-    PT_TRY(ldx_(m, m->dq1, D, m->q1_w, m->dqin, x.q_in, NJ, x.q_in, D, EPI_STORE, nullptr, 0, s));
+    PT_TRY(ldw_(m, m->dq, D, m->q1a, D, m->G(m->q2_w), m->G(m->q2_b), NJo, D, D, s, Od));
+    PT_TRY(ldx_(m, m->dq, D, m->q2_w, m->dq1, D, NJo, D, D, EPI_GELU_BWD, m->q1, D, s, Od));
+    PT_TRY(ldw_(m, m->dq1, D, m->q_in, x.q_in, m->G(m->q1_w), m->G(m->q1_b), NJo, x.q_in, D, s, Od));
+    PT_TRY(ldx_(m, m->dq1, D, m->q1_w, m->dqin, x.q_in, NJo, x.q_in, D, EPI_STORE, nullptr, 0, s, Od));
     PT_TRY(pt_q_in_bwd(c, m->dqin, m->dxa, m->G(m->temb), s));
     const int oc0 = PT_TYPE_E + 2 * D, oa0 = oc0 + PT_OPT_E;
-    PT_TRY(ldw_(m, m->dqin + oc0, x.q_in, m->ocard, d.d_c, m->G(m->oc_w), m->G(m->oc_b), NJ, d.d_c, PT_OPT_E, s));
-    PT_TRY(ldx_(m, m->dqin + oc0, x.q_in, m->oc_w, m->docard, d.d_c, NJ, d.d_c, PT_OPT_E, EPI_STORE, nullptr, 0, s));
-    PT_TRY(ldw_(m, m->dqin + oa0, x.q_in, m->oatt, d.d_a, m->G(m->oa_w), m->G(m->oa_b), NJ, d.d_a, PT_OPT_E, s));
-    PT_TRY(ldx_(m, m->dqin + oa0, x.q_in, m->oa_w, m->doatt, d.d_a, NJ, d.d_a, PT_OPT_E, EPI_STORE, nullptr, 0, s));
+    PT_TRY(ldw_(m, m->dqin + oc0, x.q_in, m->ocard, d.d_c, m->G(m->oc_w), m->G(m->oc_b), NJo, d.d_c, PT_OPT_E, s,
+                Od));
+    PT_TRY(ldx_(m, m->dqin + oc0, x.q_in, m->oc_w, m->docard, d.d_c, NJo, d.d_c, PT_OPT_E, EPI_STORE, nullptr, 0, s,
+                Od));
+    PT_TRY(ldw_(m, m->dqin + oa0, x.q_in, m->oatt, d.d_a, m->G(m->oa_w), m->G(m->oa_b), NJo, d.d_a, PT_OPT_E, s,
+                Od));
+    PT_TRY(ldx_(m, m->dqin + oa0, x.q_in, m->oa_w, m->doatt, d.d_a, NJo, d.d_a, PT_OPT_E, EPI_STORE, nullptr, 0, s,
+                Od));
     PT_TRY(pt_opt_gather_bwd(c, m->docard, m->doatt, m->dcard, m->datt, s));
 
     // final LayerNorm, then the trunk in reverse (d_x in dxb, scratch dxa)

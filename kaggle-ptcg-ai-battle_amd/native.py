@@ -56,6 +56,8 @@ _SIGS = {
     "ptcg_trainer_set_precision": (ctypes.c_int, [c_void_p, ctypes.c_int]),
     "ptcg_model_set_sync_free": (ctypes.c_int, [c_void_p, ctypes.c_int]),
     "ptcg_trainer_set_sync_free": (ctypes.c_int, [c_void_p, ctypes.c_int]),
+    "ptcg_model_set_skip_masked_options": (ctypes.c_int, [c_void_p, ctypes.c_int]),
+    "ptcg_trainer_set_skip_masked_options": (ctypes.c_int, [c_void_p, ctypes.c_int]),
     "ptcg_model_free": (None, [c_void_p]),
     "ptcg_ppo_loss_fwd_bwd": (ctypes.c_int, [
         c_void_p, ctypes.c_int, ctypes.c_int, c_void_p, ctypes.c_int64, c_void_p,

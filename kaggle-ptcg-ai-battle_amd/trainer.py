@@ -179,7 +179,8 @@ def create_pufferl(args):
     "init_weights": packed blob | None, "static": static tables (static-table
     models), "precision": "fp32" | "bf16" (GEMM products), "sync_free": bool
     (compact row count kept on the device: no host read-back per forward, so
-    the step can be graph-captured)}.  Unknown dims keys
+    the step can be graph-captured), "skip_masked_options": bool (default True:
+    the option scorer runs only legal options in steps and rollouts)}.  Unknown dims keys
     raise."""
     dm = args.get("dims", dims_mod.CORE)
     if isinstance(dm, dict):
@@ -193,6 +194,8 @@ def create_pufferl(args):
     check(lib().ptcg_trainer_set_precision(pl._h, 1 if prec == "bf16" else 0))
     if args.get("sync_free", False):
         check(lib().ptcg_trainer_set_sync_free(pl._h, 1))
+    if not args.get("skip_masked_options", True):
+        check(lib().ptcg_trainer_set_skip_masked_options(pl._h, 0))
     init = args.get("init_weights")
     if init is None:
         from .params import init_blob

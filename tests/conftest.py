@@ -58,3 +58,16 @@ def d2h(ptr, shape, dtype=np.float32):
     rc = _hip.hipMemcpy(out.ctypes.data, ptr, out.nbytes, 2)   # hipMemcpyDeviceToHost
     assert rc == 0, f"hipMemcpy failed: {rc}"
     return out
+
+
+def masked_slots_zeroed(out, mask):
+    """The trainer's own forward output: it runs the option scorer only on
+    legal options (their masked scores never reach the loss), so masked
+    slots read 0 — except in rows with no legal option, scored in full."""
+    out = np.array(out, dtype=np.float32, copy=True)
+    mask = np.asarray(mask) != 0
+    A = mask.shape[1]
+    rows = mask.any(axis=1)
+    sl = out[:, :A]
+    sl[rows[:, None] & ~mask] = 0.0
+    return out

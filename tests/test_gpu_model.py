@@ -15,7 +15,7 @@ import numpy as np
 import pytest
 import torch
 
-from conftest import rel_l2, max_rel, d2h
+from conftest import rel_l2, max_rel, d2h, masked_slots_zeroed
 from ptcg_amd import dims, params, synth, trainer, native
 import oracle.model as om
 import oracle.adam as oadam
@@ -103,7 +103,7 @@ def test_backward_grads_match_oracle(dm, B, rich, cuda):
     pl.forward_backward(d_obs, None, d_inp)
     pl.sync()
     dec, pgrad, ratio, nv = pl.buffers()
-    fwd_check(d2h(dec, (B, dm.n_opt + 1)), out.detach().numpy())
+    fwd_check(d2h(dec, (B, dm.n_opt + 1)), masked_slots_zeroed(out.detach().numpy(), obs[:, m0:m1]))
     assert rel_l2(d2h(pgrad, (B, dm.n_opt + 1)), res["grad"].numpy()) < 1e-4
     assert rel_l2(d2h(ratio, (B,)), res["ratio"].numpy()) < 1e-4
     _grads_check(pl, ref, dm, res["grad"].numpy()[:, :dm.n_opt])
@@ -238,6 +238,6 @@ def test_pointers_into_padding_and_no_valid_tokens(cuda):
     pl.forward_backward(pl.to_device(obs), None, {k: pl.to_device(v) for k, v in inp.items()})
     pl.sync()
     dec, _, _, _ = pl.buffers()
-    fwd_check(d2h(dec, (B, dm.n_opt + 1)), out.detach().numpy())
+    fwd_check(d2h(dec, (B, dm.n_opt + 1)), masked_slots_zeroed(out.detach().numpy(), obs[:, m0:m1]))
     _grads_check(pl, ref, dm, res["grad"].numpy()[:, :dm.n_opt])
     pl.close()

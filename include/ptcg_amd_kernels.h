@@ -19,7 +19,10 @@ extern "C" {
 /* C[M,N] = epi(sum_k A(m,k) B(k,n)); A(m,k) = a_t ? A[k*lda+m] : A[m*lda+k],
  * B(k,n) = b_t ? B[k*ldb+n] : B[n*ldb+k].  epi: 0 store, 1 +bias[n],
  * 2 +bias then C2 = gelu(C), 3 +bias +R[m*ldr+n], 4 *= gelu'(R[m*ldr+n]),
- * 5 C += acc.  workspace (may be NULL) enables split-K for long K.
+ * 5 C += acc, 6 z = acc + bias[n], C = gelu'(z), C2 = gelu(z),
+ * 7 C = acc * R[m*ldr+n] (6 and 7 are a GELU layer's forward / backward
+ * keeping gelu'(z) instead of z).  workspace (may be NULL) enables split-K
+ * for long K.
  * Replaces pt_gemm / pt_linear / pt_linear_bwd (ptcg_kernels.cuh:42-108).  */
 int ptcg_kernel_gemm(int M, int N, int K, const float* A, int64_t lda, int a_t,
                      const float* B, int64_t ldb, int b_t, float* C, int64_t ldc, int epi,

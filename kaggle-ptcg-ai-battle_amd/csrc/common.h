@@ -58,6 +58,14 @@ __device__ __forceinline__ float pt_gelu_grad(float x) {
     float pdf = 0.3989422804014327f * expf(-0.5f * x * x);
     return cdf + x * pdf;
 }
+// both from one erf, with the same arithmetic as pt_gelu / pt_gelu_grad
+__device__ __forceinline__ void pt_gelu_both(float x, float& g, float& gd) {
+    const float e = erff(x * 0.70710678118654752f);
+    g = 0.5f * x * (1.f + e);
+    const float cdf = 0.5f * (1.f + e);
+    const float pdf = 0.3989422804014327f * expf(-0.5f * x * x);
+    gd = cdf + x * pdf;
+}
 
 // fp32 id read back from an obs row: C cast truncates toward zero, then clamp
 __device__ __forceinline__ int pt_id_clamp(float v, int hi) {
@@ -94,6 +102,11 @@ enum PtEpi {
     EPI_BIAS_RESID = 3, // C = acc + bias[n] + R[m*ldr+n]
     EPI_GELU_BWD = 4,   // C = acc * gelu'(R[m*ldr+n])
     EPI_ACCUM = 5,      // C += acc
+    // the model's form of a GELU layer: the forward keeps gelu'(z) instead
+    // of z (the backward needs nothing else of z), so the backward epilogue
+    // is one multiply
+    EPI_BIAS_GELU_D = 6,  // z = acc + bias[n]; C = gelu'(z); C2 = gelu(z)
+    EPI_MUL = 7,          // C = acc * R[m*ldr+n]
 };
 
 struct GemmArgs {

@@ -78,10 +78,10 @@ __global__ void pool_bwd_kernel(const float* __restrict__ dsrc, long ld, int col
     }
 }
 
-__global__ void gelu_bwd_kernel(const float* __restrict__ dy, const float* __restrict__ pre,
-                                float* __restrict__ dx, long n) {
+__global__ void mul_kernel(const float* __restrict__ dy, const float* __restrict__ gd,
+                           float* __restrict__ dx, long n) {
     const long i = (long)blockIdx.x * TB + threadIdx.x;
-    if (i < n) dx[i] = dy[i] * pt_gelu_grad(pre[i]);
+    if (i < n) dx[i] = dy[i] * gd[i];
 }
 
 // oracle token inputs (N, n_orc, d_c + 6) = [CardVec(id) | kind one-hot 3 |
@@ -276,8 +276,8 @@ int pt_pool_bwd(const float* dsrc, long ld, int col_mean, int col_max, const int
     PT_LAUNCH_CHECK();
     return PTCG_OK;
 }
-int pt_gelu_bwd(const float* dy, const float* pre, float* dx, long n, hipStream_t s) {
-    hipLaunchKernelGGL(gelu_bwd_kernel, FZ_GRID(n), dy, pre, dx, n);
+int pt_mul(const float* dy, const float* gd, float* dx, long n, hipStream_t s) {
+    hipLaunchKernelGGL(mul_kernel, FZ_GRID(n), dy, gd, dx, n);
     PT_LAUNCH_CHECK();
     return PTCG_OK;
 }

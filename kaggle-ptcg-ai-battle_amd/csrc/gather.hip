@@ -516,14 +516,14 @@ __global__ void head_dot_kernel(const float* __restrict__ X, int rows, int K,
 }
 
 __global__ void head_dot_bwd_kernel(const float* __restrict__ grad, int per, long ldg, int col0,
-        const float* __restrict__ w, const float* __restrict__ pre, float* __restrict__ dX, int rows,
+        const float* __restrict__ w, const float* __restrict__ gd, float* __restrict__ dX, int rows,
         int K, const int* __restrict__ rmap, const int* __restrict__ rows_dev) {
     if (rows_dev) rows = min(rows, *rows_dev);
     const long i = (long)blockIdx.x * TB + threadIdx.x;
     if (i >= (long)rows * K) return;
     const int r = (int)(i / K), k = (int)(i % K);
     const float dy = grad[hd_slot(rmap, r, per, ldg, col0)];
-    dX[i] = dy * w[k] * pt_gelu_grad(pre[i]);
+    dX[i] = dy * w[k] * gd[i];
 }
 
 constexpr int HD_ROWS = 64;
@@ -685,9 +685,9 @@ int pt_head_dot(const float* X, int rows, int K, const float* w, const float* b,
     PT_LAUNCH_CHECK();
     return PTCG_OK;
 }
-int pt_head_dot_bwd(const float* grad, int per, long ldg, int col0, const float* w, const float* pre,
+int pt_head_dot_bwd(const float* grad, int per, long ldg, int col0, const float* w, const float* gd,
                     float* dX, int rows, int K, hipStream_t s, const int* rmap, const int* rows_dev) {
-    hipLaunchKernelGGL(head_dot_bwd_kernel, PT_GRID((long)rows * K), grad, per, ldg, col0, w, pre, dX, rows, K, rmap,
+    hipLaunchKernelGGL(head_dot_bwd_kernel, PT_GRID((long)rows * K), grad, per, ldg, col0, w, gd, dX, rows, K, rmap,
                        rows_dev);
     PT_LAUNCH_CHECK();
     return PTCG_OK;

@@ -79,6 +79,13 @@ __device__ __forceinline__ void epi_store(const GemmArgs& g, int m, int n, float
         g.C[(long)m * g.ldc + n] = v + g.bias[n] + g.R[(long)m * g.ldr + n];
     } else if (EPI == EPI_GELU_BWD) {
         g.C[(long)m * g.ldc + n] = v * pt_gelu_grad(g.R[(long)m * g.ldr + n]);
+    } else if (EPI == EPI_BIAS_GELU_D) {
+        float gv, gd;
+        pt_gelu_both(v + g.bias[n], gv, gd);
+        g.C[(long)m * g.ldc + n] = gd;
+        g.C2[(long)m * g.ldc2 + n] = gv;
+    } else if (EPI == EPI_MUL) {
+        g.C[(long)m * g.ldc + n] = v * g.R[(long)m * g.ldr + n];
     } else if (EPI == EPI_ACCUM) {
         g.C[(long)m * g.ldc + n] += v;
     }
@@ -106,6 +113,15 @@ __device__ __forceinline__ void epi_store4(const GemmArgs& g, int m, int n, floa
     } else if (EPI == EPI_GELU_BWD) {
         const floatx4 x = ld_v4(g.R + (long)m * g.ldr + n);
         st_g4(c, v * floatx4{pt_gelu_grad(x[0]), pt_gelu_grad(x[1]), pt_gelu_grad(x[2]), pt_gelu_grad(x[3])});
+    } else if (EPI == EPI_BIAS_GELU_D) {
+        v += ld_v4(g.bias + n);
+        float gv[4], gd[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) pt_gelu_both(v[i], gv[i], gd[i]);
+        st_g4(c, floatx4{gd[0], gd[1], gd[2], gd[3]});
+        st_g4(g.C2 + (long)m * g.ldc2 + n, floatx4{gv[0], gv[1], gv[2], gv[3]});
+    } else if (EPI == EPI_MUL) {
+        st_g4(c, v * ld_v4(g.R + (long)m * g.ldr + n));
     } else if (EPI == EPI_ACCUM) {
         st_g4(c, ld_v4(c) + v);
     }
@@ -145,7 +161,8 @@ __device__ __forceinline__ float4 ld_scalar4(const gfloat* X, long ld, int lim, 
 constexpr int SST = BN + 4;
 constexpr int STAGE_FLOATS = 64 * SST;
 template <int EPI> struct EpiStaged {
-    static constexpr bool value = EPI == EPI_BIAS_GELU || EPI == EPI_GELU_BWD || EPI == EPI_BIAS_RESID;
+    static constexpr bool value = EPI == EPI_BIAS_GELU || EPI == EPI_GELU_BWD || EPI == EPI_BIAS_RESID ||
+                                  EPI == EPI_BIAS_GELU_D || EPI == EPI_MUL;
 };
 
 template <int EPI>
@@ -753,6 +770,8 @@ int launch_bf16_epi(const GemmArgs& g, dim3 grid, int k_chunk, long part_stride,
         case EPI_BIAS_GELU: launch_bf16<AT, BT, EPI_BIAS_GELU, false>(g, grid, k_chunk, 0, s); break;
         case EPI_BIAS_RESID: launch_bf16<AT, BT, EPI_BIAS_RESID, false>(g, grid, k_chunk, 0, s); break;
         case EPI_GELU_BWD: launch_bf16<AT, BT, EPI_GELU_BWD, false>(g, grid, k_chunk, 0, s); break;
+        case EPI_BIAS_GELU_D: launch_bf16<AT, BT, EPI_BIAS_GELU_D, false>(g, grid, k_chunk, 0, s); break;
+        case EPI_MUL: launch_bf16<AT, BT, EPI_MUL, false>(g, grid, k_chunk, 0, s); break;
         case EPI_ACCUM: launch_bf16<AT, BT, EPI_ACCUM, false>(g, grid, k_chunk, 0, s); break;
         default: PT_REQUIRE(false, "gemm: bad epilogue %d", g.epi);
     }
@@ -787,6 +806,8 @@ int launch_epi(const GemmArgs& g, dim3 grid, int k_chunk, hipStream_t s) {
         case EPI_BIAS_GELU: launch<AT, BT, EPI_BIAS_GELU, false, false, VEC>(g, grid, k_chunk, 0, s); break;
         case EPI_BIAS_RESID: launch<AT, BT, EPI_BIAS_RESID, false, false, VEC>(g, grid, k_chunk, 0, s); break;
         case EPI_GELU_BWD: launch<AT, BT, EPI_GELU_BWD, false, false, VEC>(g, grid, k_chunk, 0, s); break;
+        case EPI_BIAS_GELU_D: launch<AT, BT, EPI_BIAS_GELU_D, false, false, VEC>(g, grid, k_chunk, 0, s); break;
+        case EPI_MUL: launch<AT, BT, EPI_MUL, false, false, VEC>(g, grid, k_chunk, 0, s); break;
         case EPI_ACCUM: launch<AT, BT, EPI_ACCUM, false, false, VEC>(g, grid, k_chunk, 0, s); break;
         default: PT_REQUIRE(false, "gemm: bad epilogue %d", g.epi);
     }
@@ -977,6 +998,8 @@ int pt_gemm(const GemmArgs& g0, float* ws, long ws_floats, hipStream_t s) {
                 case EPI_BIAS_GELU: hipLaunchKernelGGL(tail_reduce_kernel<EPI_BIAS_GELU>, gr, dim3(256), 0, s, t, ws, s2); break;
                 case EPI_BIAS_RESID: hipLaunchKernelGGL(tail_reduce_kernel<EPI_BIAS_RESID>, gr, dim3(256), 0, s, t, ws, s2); break;
                 case EPI_GELU_BWD: hipLaunchKernelGGL(tail_reduce_kernel<EPI_GELU_BWD>, gr, dim3(256), 0, s, t, ws, s2); break;
+                case EPI_BIAS_GELU_D: hipLaunchKernelGGL(tail_reduce_kernel<EPI_BIAS_GELU_D>, gr, dim3(256), 0, s, t, ws, s2); break;
+                case EPI_MUL: hipLaunchKernelGGL(tail_reduce_kernel<EPI_MUL>, gr, dim3(256), 0, s, t, ws, s2); break;
                 case EPI_ACCUM: hipLaunchKernelGGL(tail_reduce_kernel<EPI_ACCUM>, gr, dim3(256), 0, s, t, ws, s2); break;
                 default: PT_REQUIRE(false, "gemm: bad epilogue %d", g.epi);
             }
@@ -999,9 +1022,9 @@ int pt_linear_fwd(const float* X, const float* W, const float* b, float* Y, int 
     g.C = Y; g.ldc = out;
     g.bias = b; g.R = R; g.ldr = out; g.C2 = Y2; g.ldc2 = out;
     g.epi = epi;
-    if ((epi == EPI_BIAS || epi == EPI_BIAS_GELU || epi == EPI_BIAS_RESID) && b == nullptr)
+    if ((epi == EPI_BIAS || epi == EPI_BIAS_GELU || epi == EPI_BIAS_RESID || epi == EPI_BIAS_GELU_D) && b == nullptr)
         g.epi = (epi == EPI_BIAS) ? EPI_STORE : epi;
-    PT_REQUIRE(!(g.epi == EPI_BIAS_GELU || g.epi == EPI_BIAS_RESID) || b != nullptr,
+    PT_REQUIRE(!(g.epi == EPI_BIAS_GELU || g.epi == EPI_BIAS_RESID || g.epi == EPI_BIAS_GELU_D) || b != nullptr,
                "linear_fwd: epilogue %d needs a bias", epi);
     return pt_gemm(g, nullptr, 0, s);
 }

@@ -8,11 +8,12 @@ extern "C" int ptcg_kernel_gemm(int M, int N, int K, const float* A, int64_t lda
                                 int64_t ldc2, float* workspace, int64_t workspace_floats,
                                 void* stream) {
     PT_REQUIRE(A && B && C, "kernel_gemm: null operand");
-    PT_REQUIRE(epi >= EPI_STORE && epi <= EPI_ACCUM, "kernel_gemm: bad epilogue %d", epi);
-    PT_REQUIRE(!((epi == EPI_BIAS || epi == EPI_BIAS_GELU || epi == EPI_BIAS_RESID) && !bias),
+    PT_REQUIRE(epi >= EPI_STORE && epi <= EPI_MUL, "kernel_gemm: bad epilogue %d", epi);
+    PT_REQUIRE(!((epi == EPI_BIAS || epi == EPI_BIAS_GELU || epi == EPI_BIAS_RESID || epi == EPI_BIAS_GELU_D) && !bias),
                "kernel_gemm: epilogue %d needs bias", epi);
-    PT_REQUIRE(!((epi == EPI_BIAS_RESID || epi == EPI_GELU_BWD) && !R), "kernel_gemm: epilogue %d needs R", epi);
-    PT_REQUIRE(!(epi == EPI_BIAS_GELU && !C2), "kernel_gemm: epilogue 2 needs C2");
+    PT_REQUIRE(!((epi == EPI_BIAS_RESID || epi == EPI_GELU_BWD || epi == EPI_MUL) && !R),
+               "kernel_gemm: epilogue %d needs R", epi);
+    PT_REQUIRE(!((epi == EPI_BIAS_GELU || epi == EPI_BIAS_GELU_D) && !C2), "kernel_gemm: epilogue %d needs C2", epi);
     GemmArgs g{};
     g.M = M; g.N = N; g.K = K;
     g.A = A; g.lda = lda; g.a_t = a_t;
@@ -28,7 +29,7 @@ extern "C" int ptcg_kernel_gemm_bf16(int M, int N, int K, const float* A, int64_
                                      int64_t ldc2, float* workspace, int64_t workspace_floats,
                                      void* stream) {
     PT_REQUIRE(A && B && C, "kernel_gemm_bf16: null operand");
-    PT_REQUIRE(epi >= EPI_STORE && epi <= EPI_ACCUM, "kernel_gemm_bf16: bad epilogue %d", epi);
+    PT_REQUIRE(epi >= EPI_STORE && epi <= EPI_MUL, "kernel_gemm_bf16: bad epilogue %d", epi);
     GemmArgs g{};
     g.M = M; g.N = N; g.K = K;
     g.A = A; g.lda = lda; g.a_t = a_t;

@@ -120,9 +120,10 @@ int pt_val_in_bwd(const GatherCtx& c, const float* d_val_in, float* d_h, float* 
 int pt_head_dot(const float* X, int rows, int K, const float* w, const float* b, float* out,
                 int per, long ldo, int col0, hipStream_t s, const int* rmap = nullptr,
                 const int* rows_dev = nullptr);
-// dX[r,:] = dy[r] * w[:] * gelu'(pre[r,:]),  dy[r] = grad[q / per * ldg + col0 + q % per]
+// dX[r,:] = dy[r] * w[:] * gd[r,:] (gd = the GELU derivative kept by the forward),
+// dy[r] = grad[q / per * ldg + col0 + q % per]
 int pt_head_dot_bwd(const float* grad, int per, long ldg, int col0, const float* w,
-                    const float* pre, float* dX, int rows, int K, hipStream_t s, const int* rmap = nullptr,
+                    const float* gd, float* dX, int rows, int K, hipStream_t s, const int* rmap = nullptr,
                     const int* rows_dev = nullptr);
 // dw[k] = sum_r dy[r] X[r,k]; db = sum_r dy[r]   (fixed order)
 int pt_head_dot_dw(const float* grad, int per, long ldg, int col0, const float* X, int rows, int K,
@@ -136,7 +137,8 @@ int pt_pool_fwd(const float* tab, int E, const int* ids, int K, int NC, float* o
                 int col_max, int* amax, hipStream_t s);
 int pt_pool_bwd(const float* dsrc, long ld, int col_mean, int col_max, const int* amax, const int* ids, int K,
                 int NC, int E, float* d_tab, hipStream_t s);
-int pt_gelu_bwd(const float* dy, const float* pre, float* dx, long n, hipStream_t s);
+// dx = dy * gd elementwise (gd = the GELU derivative kept by the forward)
+int pt_mul(const float* dy, const float* gd, float* dx, long n, hipStream_t s);
 int pt_otok_in(const GatherCtx& c, const float* cv, const float* keep, float* out, float* ckeep, hipStream_t s);
 int pt_otok_bwd(const GatherCtx& c, const float* d_in, float* d_card, hipStream_t s);
 int pt_xc_fwd(const float* cread, const float* h, const float* otok, float* xc, int N, int Ls, int NO, int D,

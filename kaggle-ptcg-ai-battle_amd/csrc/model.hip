@@ -4,15 +4,18 @@
 // ptcg_forward_core :246-369, blk_fwd :12-40, blk_bwd :44-95;
 // ptcg_model4.cu ptcg_backward_core :10-190; ptcg_model2.cu tables_fwd /
 // tables_bwd :422-485) with a different kernel plan:
-//   * GEMM epilogues carry bias, GELU (pre-activation kept), residual add
-//     and GELU-backward, so there are no separate bias / gelu / add kernels;
+//   * GEMM epilogues carry bias, GELU, residual add and the GELU backward,
+//     so there are no separate bias / gelu / add kernels; a GELU layer's
+//     forward keeps gelu'(z) in place of the pre-activation z (the only
+//     thing the backward needs of z), so its backward is one multiply in
+//     the epilogue of the next layer's dX product;
 //   * attention is one fused kernel per direction (no (N,H,L,L) tensor);
 //   * concat inputs are written in place by the producing GEMMs (leading
 //     dimension = concat width) — g/dvec into the bcast input, opt_card /
 //     opt_attack into q_in, q into the score input; the static / text
 //     columns of the table-chain inputs are written once at upload;
 //   * every activation the backward needs is kept (LayerNorm outputs, qkv,
-//     attention context, GELU pre- and post-activations), so the backward
+//     attention context, GELU derivatives and outputs), so the backward
 //     recomputes nothing but the attention probabilities.
 // Two switches select the model variant: tables (learned card / attack
 // tables, or the static-table chain rebuilt every forward) and critic (blind
@@ -28,6 +31,8 @@
 struct BlockP {
     float *ln1w, *ln1b, *qkvw, *qkvb, *projw, *projb, *ln2w, *ln2b, *f1w, *f1b, *f2w, *f2b;
 };
+// per-layer activations; ffp = gelu'(z) and ffa = gelu(z) of the FFN's
+// first product z (every GELU layer keeps its derivative, not z)
 struct BlockA {
     float *ln1, *mu1, *rs1, *qkv, *ctx, *lse, *xmid, *ln2, *mu2, *rs2, *ffp, *ffa;
 };
@@ -533,7 +538,7 @@ static int block_fwd(PtcgModel* m, const BlockP& w, const BlockA& a, int L, cons
     PT_TRY(pt_attn_fwd(a.qkv, keep, a.ctx, a.lse, m->N, L, d.heads, m->dx.dh, s, coff));
     PT_TRY(linf(m, a.ctx, w.projw, w.projb, a.xmid, NL, D, D, EPI_BIAS_RESID, xin, nullptr, s, Tr));
     PT_TRY(pt_ln_fwd(a.xmid, D, w.ln2w, w.ln2b, a.ln2, D, a.mu2, a.rs2, NL, D, s, Tr));
-    PT_TRY(linf(m, a.ln2, w.f1w, w.f1b, a.ffp, NL, D, d.ffn, EPI_BIAS_GELU, nullptr, a.ffa, s, Tr));
+    PT_TRY(linf(m, a.ln2, w.f1w, w.f1b, a.ffp, NL, D, d.ffn, EPI_BIAS_GELU_D, nullptr, a.ffa, s, Tr));
     PT_TRY(linf(m, a.ffa, w.f2w, w.f2b, xout, NL, d.ffn, D, EPI_BIAS_RESID, a.xmid, nullptr, s, Tr));
     return PTCG_OK;
 }
@@ -546,10 +551,10 @@ static int tables_fwd(PtcgModel* m, hipStream_t s) {
     const int NC = d.n_cards, NA = d.n_attacks, NS = d.n_skills, DA = d.d_a, DC = d.d_c;
     const int pa = PT_ID_C + PT_CARD_STATIC + PT_CARD_TEXT;   // first pool column of card_in
     PT_TRY(pt_copy_cols(m->att_in, x.att_in, m->aid_emb, PT_ID_A, NA, PT_ID_A, s));
-    PT_TRY(lin(m, m->att_in, x.att_in, m->am_w, m->am_b, m->att_lin, DA, NA, x.att_in, DA, EPI_BIAS_GELU, nullptr, 0,
+    PT_TRY(lin(m, m->att_in, x.att_in, m->am_w, m->am_b, m->att_lin, DA, NA, x.att_in, DA, EPI_BIAS_GELU_D, nullptr, 0,
                m->att_tab, DA, s));
     PT_TRY(pt_copy_cols(m->sk_in, x.sk_in, m->sid_emb, PT_ID_A, NS, PT_ID_A, s));
-    PT_TRY(lin(m, m->sk_in, x.sk_in, m->sm_w, m->sm_b, m->sk_lin, DC, NS, x.sk_in, DC, EPI_BIAS_GELU, nullptr, 0,
+    PT_TRY(lin(m, m->sk_in, x.sk_in, m->sm_w, m->sm_b, m->sk_lin, DC, NS, x.sk_in, DC, EPI_BIAS_GELU_D, nullptr, 0,
                m->sk_tab, DC, s));
     PT_TRY(pt_copy_cols(m->card_in, x.card_in, m->cid_emb, PT_ID_C, NC, PT_ID_C, s));
     PT_TRY(pt_pool_fwd(m->att_tab, DA, m->card_attacks, PT_K_ATT, NC, m->card_in, x.card_in, pa, pa + DA,
@@ -559,7 +564,7 @@ static int tables_fwd(PtcgModel* m, hipStream_t s) {
     PT_TRY(pt_ln_fwd(m->card_in, x.card_in, m->cln_w, m->cln_b, m->card_ln, x.card_in, m->c_mu, m->c_rs, NC,
                      x.card_in, s));
     PT_TRY(lin(m, m->card_ln, x.card_in, m->c1_w, m->c1_b, m->card_h1, PT_CARD_H, NC, x.card_in, PT_CARD_H,
-               EPI_BIAS_GELU, nullptr, 0, m->card_g1, PT_CARD_H, s));
+               EPI_BIAS_GELU_D, nullptr, 0, m->card_g1, PT_CARD_H, s));
     PT_TRY(linf(m, m->card_g1, m->c3_w, m->c3_b, m->card_vec, NC, PT_CARD_H, DC, EPI_BIAS, nullptr, nullptr, s));
     return PTCG_OK;
 }
@@ -619,10 +624,10 @@ extern "C" int ptcg_model_forward(PtcgModel* m, const float* obs, const int32_t*
     PT_TRY(pt_tok_cat_fwd(c, m->card, m->zemb, m->oemb, m->tok_cat, s));
     PT_TRY(linf(m, m->tok_cat, m->tp_w, m->tp_b, m->tokp, tok_rows, x.tok_in, D, EPI_BIAS, nullptr, nullptr, s, Td));
     PT_TRY(pt_glob_in(c, m->glob_in, s));
-    PT_TRY(linf(m, m->glob_in, m->g1_w, m->g1_b, m->g1, N, d.global_f, G, EPI_BIAS_GELU, nullptr, m->g1a, s));
+    PT_TRY(linf(m, m->glob_in, m->g1_w, m->g1_b, m->g1, N, d.global_f, G, EPI_BIAS_GELU_D, nullptr, m->g1a, s));
     PT_TRY(lin(m, m->g1a, G, m->g2_w, m->g2_b, m->gd, x.bcast_in, N, G, G, EPI_BIAS, nullptr, 0, nullptr, 0, s));
     PT_TRY(pt_dec_in_fwd(c, m->card, m->att, m->semb, m->cemb, m->dec_in, s));
-    PT_TRY(linf(m, m->dec_in, m->d1_w, m->d1_b, m->d1, N, x.dec_in, PT_DEC_H, EPI_BIAS_GELU, nullptr, m->d1a, s));
+    PT_TRY(linf(m, m->dec_in, m->d1_w, m->d1_b, m->d1, N, x.dec_in, PT_DEC_H, EPI_BIAS_GELU_D, nullptr, m->d1a, s));
     PT_TRY(lin(m, m->d1a, PT_DEC_H, m->d2_w, m->d2_b, m->gd + G, x.bcast_in, N, PT_DEC_H, PT_DEC_H, EPI_BIAS,
                nullptr, 0, nullptr, 0, s));
     PT_TRY(lin(m, m->gd, x.bcast_in, m->bc_w, m->bc_b, m->bc, D, N, x.bcast_in, D, EPI_BIAS, nullptr, 0, nullptr, 0, s));
@@ -645,17 +650,17 @@ extern "C" int ptcg_model_forward(PtcgModel* m, const float* obs, const int32_t*
     PT_TRY(lin(m, m->oatt, d.d_a, m->oa_w, m->oa_b, m->q_in + oa0, x.q_in, NJ, d.d_a, PT_OPT_E, EPI_BIAS,
                nullptr, 0, nullptr, 0, s, Od));
     PT_TRY(pt_q_in_fwd(c, m->h, m->temb, m->q_in, s));
-    PT_TRY(linf(m, m->q_in, m->q1_w, m->q1_b, m->q1, NJ, x.q_in, D, EPI_BIAS_GELU, nullptr, m->q1a, s, Od));
+    PT_TRY(linf(m, m->q_in, m->q1_w, m->q1_b, m->q1, NJ, x.q_in, D, EPI_BIAS_GELU_D, nullptr, m->q1a, s, Od));
     PT_TRY(lin(m, m->q1a, D, m->q2_w, m->q2_b, m->sc_in, x.score_in, NJ, D, D, EPI_BIAS, nullptr, 0, nullptr, 0, s,
                Od));
     PT_TRY(pt_sc_in_fwd(c, m->h, m->gd, m->sc_in, s));
-    PT_TRY(linf(m, m->sc_in, m->s1_w, m->s1_b, m->s1, NJ, x.score_in, PT_SC_H, EPI_BIAS_GELU, nullptr, m->s1a, s,
+    PT_TRY(linf(m, m->sc_in, m->s1_w, m->s1_b, m->s1, NJ, x.score_in, PT_SC_H, EPI_BIAS_GELU_D, nullptr, m->s1a, s,
                 Od));
     if (skip) PT_TRY(pt_fill_zero(m->out, (long)N * (NO + 1), s));   // masked slots read 0
     PT_TRY(pt_head_dot(m->s1a, NJ, PT_SC_H, m->s2_w, m->s2_b, m->out, NO, NO + 1, 0, s, skip ? m->o_row : nullptr, Od));
     // blind value head: the output value, or (oracle critic) an aux head
     PT_TRY(pt_val_in_fwd(c, m->h, m->gd, m->val_in, s));
-    PT_TRY(linf(m, m->val_in, m->v1_w, m->v1_b, m->v1, N, x.val_in, PT_VAL_H, EPI_BIAS_GELU, nullptr, m->v1a, s));
+    PT_TRY(linf(m, m->val_in, m->v1_w, m->v1_b, m->v1, N, x.val_in, PT_VAL_H, EPI_BIAS_GELU_D, nullptr, m->v1a, s));
     if (d.critic == 0) {
         PT_TRY(pt_head_dot(m->v1a, N, PT_VAL_H, m->v2_w, m->v2_b, m->out, 1, NO + 1, NO, s));
     } else {
@@ -672,7 +677,7 @@ extern "C" int ptcg_model_forward(PtcgModel* m, const float* obs, const int32_t*
         PT_TRY(pt_xc_fwd(m->cread, m->h, m->otok, m->xc, N, x.l_seq, x.n_orc, D, s));
         PT_TRY(block_fwd(m, m->cblk, m->cba, x.l_crit, m->ckeep, m->xc, m->xco, s));
         PT_TRY(pt_val_in_fwd(c, m->xco, m->gd, m->ov_in, s, x.l_crit));
-        PT_TRY(linf(m, m->ov_in, m->ov1_w, m->ov1_b, m->ov1, N, x.val_in, PT_VAL_H, EPI_BIAS_GELU, nullptr, m->ov1a, s));
+        PT_TRY(linf(m, m->ov_in, m->ov1_w, m->ov1_b, m->ov1, N, x.val_in, PT_VAL_H, EPI_BIAS_GELU_D, nullptr, m->ov1a, s));
         PT_TRY(pt_head_dot(m->ov1a, N, PT_VAL_H, m->ov2_w, m->ov2_b, m->out, 1, NO + 1, NO, s));
     }
     if (out) *out = m->out;
@@ -687,7 +692,7 @@ static int block_bwd(PtcgModel* m, const BlockP& w, const BlockA& a, int L, cons
     const PtcgDims& d = m->dm;
     const int NL = rows ? rows : m->N * L, D = d.d;
     PT_TRY(ldw_(m, dA, D, a.ffa, d.ffn, m->G(w.f2w), m->G(w.f2b), NL, d.ffn, D, s, Tr));
-    PT_TRY(ldx_(m, dA, D, w.f2w, m->dffn, d.ffn, NL, d.ffn, D, EPI_GELU_BWD, a.ffp, d.ffn, s, Tr));
+    PT_TRY(ldx_(m, dA, D, w.f2w, m->dffn, d.ffn, NL, d.ffn, D, EPI_MUL, a.ffp, d.ffn, s, Tr));
     PT_TRY(ldw_(m, m->dffn, d.ffn, a.ln2, D, m->G(w.f1w), m->G(w.f1b), NL, D, d.ffn, s, Tr));
     PT_TRY(ldx_(m, m->dffn, d.ffn, w.f1w, m->dln, D, NL, D, d.ffn, EPI_STORE, nullptr, 0, s, Tr));
     PT_TRY(pt_ln_bwd(m->dln, D, a.xmid, D, w.ln2w, a.mu2, a.rs2, dA, D, dC, D, m->G(w.ln2w),
@@ -710,7 +715,7 @@ static int tables_bwd(PtcgModel* m, hipStream_t s) {
     const int NC = d.n_cards, NA = d.n_attacks, NS = d.n_skills, DA = d.d_a, DC = d.d_c;
     const int pa = PT_ID_C + PT_CARD_STATIC + PT_CARD_TEXT;
     PT_TRY(ldw_(m, m->d_card_vec, DC, m->card_g1, PT_CARD_H, m->G(m->c3_w), m->G(m->c3_b), NC, PT_CARD_H, DC, s));
-    PT_TRY(ldx_(m, m->d_card_vec, DC, m->c3_w, m->d_card_h, PT_CARD_H, NC, PT_CARD_H, DC, EPI_GELU_BWD, m->card_h1,
+    PT_TRY(ldx_(m, m->d_card_vec, DC, m->c3_w, m->d_card_h, PT_CARD_H, NC, PT_CARD_H, DC, EPI_MUL, m->card_h1,
                 PT_CARD_H, s));
     PT_TRY(ldw_(m, m->d_card_h, PT_CARD_H, m->card_ln, x.card_in, m->G(m->c1_w), m->G(m->c1_b), NC, x.card_in,
                 PT_CARD_H, s));
@@ -723,11 +728,11 @@ static int tables_bwd(PtcgModel* m, hipStream_t s) {
                        m->d_att_tab, s));
     PT_TRY(pt_pool_bwd(m->d_card_in, x.card_in, pa + 2 * DA, pa + 2 * DA + DC, m->s_amax, m->card_skills, PT_K_SK,
                        NC, DC, m->d_sk_tab, s));
-    PT_TRY(pt_gelu_bwd(m->d_att_tab, m->att_lin, m->d_att_lin, (long)NA * DA, s));
+    PT_TRY(pt_mul(m->d_att_tab, m->att_lin, m->d_att_lin, (long)NA * DA, s));
     PT_TRY(ldw_(m, m->d_att_lin, DA, m->att_in, x.att_in, m->G(m->am_w), m->G(m->am_b), NA, x.att_in, DA, s));
     PT_TRY(ldxw_(m, m->d_att_lin, DA, m->am_w, x.att_in, m->G(m->aid_emb), PT_ID_A, NA, PT_ID_A, DA, EPI_STORE,
                  nullptr, 0, s));
-    PT_TRY(pt_gelu_bwd(m->d_sk_tab, m->sk_lin, m->d_sk_lin, (long)NS * DC, s));
+    PT_TRY(pt_mul(m->d_sk_tab, m->sk_lin, m->d_sk_lin, (long)NS * DC, s));
     PT_TRY(ldw_(m, m->d_sk_lin, DC, m->sk_in, x.sk_in, m->G(m->sm_w), m->G(m->sm_b), NS, x.sk_in, DC, s));
     PT_TRY(ldxw_(m, m->d_sk_lin, DC, m->sm_w, x.sk_in, m->G(m->sid_emb), PT_ID_A, NS, PT_ID_A, DC, EPI_STORE,
                  nullptr, 0, s));
@@ -830,7 +835,7 @@ extern "C" int ptcg_model_backward(PtcgModel* m, const float* grad, void* stream
                 Od));
     PT_TRY(pt_sc_in_bwd(c, m->dsc, m->sc_in, m->dq, m->dxa, m->dgd, s));
     PT_TRY(ldw_(m, m->dq, D, m->q1a, D, m->G(m->q2_w), m->G(m->q2_b), NJo, D, D, s, Od));
-    PT_TRY(ldx_(m, m->dq, D, m->q2_w, m->dq1, D, NJo, D, D, EPI_GELU_BWD, m->q1, D, s, Od));
+    PT_TRY(ldx_(m, m->dq, D, m->q2_w, m->dq1, D, NJo, D, D, EPI_MUL, m->q1, D, s, Od));
     PT_TRY(ldw_(m, m->dq1, D, m->q_in, x.q_in, m->G(m->q1_w), m->G(m->q1_b), NJo, x.q_in, D, s, Od));
     PT_TRY(ldx_(m, m->dq1, D, m->q1_w, m->dqin, x.q_in, NJo, x.q_in, D, EPI_STORE, nullptr, 0, s, Od));
     PT_TRY(pt_q_in_bwd(c, m->dqin, m->dxa, m->G(m->temb), s));
@@ -866,13 +871,13 @@ extern "C" int ptcg_model_backward(PtcgModel* m, const float* grad, void* stream
     PT_TRY(ldx_(m, m->dbc, D, m->bc_w, m->dgd, x.bcast_in, N, x.bcast_in, D, EPI_ACCUM, nullptr, 0, s));
     // decision MLP (d_dvec = dgd[:, G:])
     PT_TRY(ldw_(m, m->dgd + G, x.bcast_in, m->d1a, PT_DEC_H, m->G(m->d2_w), m->G(m->d2_b), N, PT_DEC_H, PT_DEC_H, s));
-    PT_TRY(ldx_(m, m->dgd + G, x.bcast_in, m->d2_w, m->dd1, PT_DEC_H, N, PT_DEC_H, PT_DEC_H, EPI_GELU_BWD, m->d1, PT_DEC_H, s));
+    PT_TRY(ldx_(m, m->dgd + G, x.bcast_in, m->d2_w, m->dd1, PT_DEC_H, N, PT_DEC_H, PT_DEC_H, EPI_MUL, m->d1, PT_DEC_H, s));
     PT_TRY(ldw_(m, m->dd1, PT_DEC_H, m->dec_in, x.dec_in, m->G(m->d1_w), m->G(m->d1_b), N, x.dec_in, PT_DEC_H, s));
     PT_TRY(ldx_(m, m->dd1, PT_DEC_H, m->d1_w, m->ddec, x.dec_in, N, x.dec_in, PT_DEC_H, EPI_STORE, nullptr, 0, s));
     PT_TRY(pt_dec_in_bwd(c, m->ddec, m->dcard, m->datt, m->G(m->semb), m->G(m->cemb), s));
     // global MLP (d_g = dgd[:, :G])
     PT_TRY(ldw_(m, m->dgd, x.bcast_in, m->g1a, G, m->G(m->g2_w), m->G(m->g2_b), N, G, G, s));
-    PT_TRY(ldx_(m, m->dgd, x.bcast_in, m->g2_w, m->dg1, G, N, G, G, EPI_GELU_BWD, m->g1, G, s));
+    PT_TRY(ldx_(m, m->dgd, x.bcast_in, m->g2_w, m->dg1, G, N, G, G, EPI_MUL, m->g1, G, s));
     PT_TRY(ldw_(m, m->dg1, G, m->glob_in, d.global_f, m->G(m->g1_w), m->G(m->g1_b), N, d.global_f, G, s));
     if (d.tables == 1) PT_TRY(tables_bwd(m, s));
     return PTCG_OK;

@@ -55,6 +55,10 @@ GEMM_CASES = [
     # (whole tiles + a split-K tail reduced through the epilogue)
     (34000, 256, 256, 0, 0, 2), (33000, 384, 256, 0, 1, 4), (33024, 256, 512, 0, 0, 5),
     (33100, 256, 256, 0, 0, 3),
+    # a GELU layer keeping gelu'(z): forward (6) and the multiply backward (7),
+    # on the LDS-DMA kernel, the register-staged kernel (K = 172) and a balanced launch
+    (512, 1024, 256, 0, 0, 6), (300, 256, 172, 0, 0, 6), (34000, 256, 256, 0, 0, 6),
+    (512, 1024, 256, 0, 1, 7), (200, 96, 40, 0, 1, 7), (33000, 384, 256, 0, 1, 7),
 ]
 
 
@@ -78,6 +82,10 @@ def test_gemm_layouts_and_epilogues(case, cuda):
         ref2 = gelu(ref)
     elif epi == 3: ref = acc + bias.double() + R.double()
     elif epi == 4: ref = acc * gelu_grad(R.double())
+    elif epi == 6:
+        z = acc + bias.double()
+        ref, ref2 = gelu_grad(z), gelu(z)
+    elif epi == 7: ref = acc * R.double()
     else: ref = C0.double() + acc
     dA, dB, dbias, dR = dev(A), dev(B), dev(bias), dev(R)
     dC = dev(C0) if epi == 5 else empty(M, N)
@@ -375,6 +383,10 @@ def test_gemm_bf16_products(case, cuda):
         ref2 = gelu(ref)
     elif epi == 3: ref = acc + bias.double() + R.double()
     elif epi == 4: ref = acc * gelu_grad(R.double())
+    elif epi == 6:
+        z = acc + bias.double()
+        ref, ref2 = gelu_grad(z), gelu(z)
+    elif epi == 7: ref = acc * R.double()
     else: ref = C0.double() + acc
     dA, dB, dbias, dR = dev(A), dev(B), dev(bias), dev(R)
     dC = dev(C0) if epi == 5 else empty(M, N)

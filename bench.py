@@ -36,6 +36,9 @@ sys.path.insert(0, ROOT)
 METRIC = "PPO minibatch step obs/sec (fwd+bwd+Adam) @B=512; % MFMA/HBM roofline"
 FP32_MFMA_PEAK_TFLOPS = 157.3      # MI355X dense fp32 matrix peak
 BF16_MFMA_PEAK_TFLOPS = 2500.0     # MI355X dense bf16 matrix peak
+HBM_PEAK_GBS = 8000.0              # MI355X HBM3E bandwidth
+# launch classes of ptcg_profile_class: (index, name); amounts are HBM bytes
+HBM_CLASSES = ((1, "layernorm_fwd"), (2, "layernorm_bwd"), (3, "adam_norm"), (4, "adam_update"))
 
 TRAIN = dict(learning_rate=3e-4, beta1=0.9, beta2=0.999, eps=1e-8, max_grad_norm=0.5,
              clip_coef=0.2, vf_clip_coef=0.2, vf_coef=0.5, ent_coef=0.01)
@@ -124,6 +127,36 @@ def measured_gemm_traffic():
     return float(m.group(1)) if m else None
 
 
+def hbm_kernels(L, K):
+    """Achieved HBM bandwidth of the memory-bound kernels of the timed steps:
+    algorithmic bytes (each launch's inputs read and outputs written once) over
+    the summed HIP-event durations of their launches."""
+    out = {}
+    tot_ms, tot_b = 0.0, 0.0
+    for cls, name in HBM_CLASSES:
+        ms, n, amt = ctypes.c_double(), ctypes.c_int(), ctypes.c_double()
+        native_check(L.ptcg_profile_class(cls, ctypes.byref(ms), ctypes.byref(n), ctypes.byref(amt)))
+        if n.value == 0 or ms.value <= 0:
+            continue
+        gbs = amt.value / (ms.value / 1e3) / 1e9
+        out[name] = dict(achieved=round(gbs, 1), peak=HBM_PEAK_GBS, unit="GB/s", frac=round(gbs / HBM_PEAK_GBS, 4),
+                         launches_per_step=n.value / K, avg_launch_us=round(ms.value * 1e3 / n.value, 2),
+                         bytes_per_launch=round(amt.value / n.value))
+        if name.startswith("adam"):
+            tot_ms += ms.value
+            tot_b += amt.value
+    if tot_ms > 0:
+        gbs = tot_b / (tot_ms / 1e3) / 1e9
+        out["adam"] = dict(achieved=round(gbs, 1), peak=HBM_PEAK_GBS, unit="GB/s", frac=round(gbs / HBM_PEAK_GBS, 4),
+                           note="norm + update passes, 32 B per parameter")
+    return out
+
+
+def native_check(rc):
+    from ptcg_amd import native
+    native.check(rc)
+
+
 def cpu_baseline(dm, obs, inp, B, budget_s):
     """Oracle (torch CPU) fwd+bwd+PPO+clip+Adam on B-row minibatches of the
     same rollout until `budget_s` of CPU work; returns obs/s and the sample."""
@@ -166,6 +199,8 @@ def main():
     ap.add_argument("--rollout-rows", type=int, default=8192)
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run three 256 MiB device-to-device copies (the HBM counter calibration)")
+    ap.add_argument("--copy-rate", action="store_true",
+                    help="only time device-to-device copies of the memory-bound kernels' sizes (GB/s for scale)")
     ap.add_argument("--sync-free", action="store_true",
                     help="compact row count kept on the device (no host read-back per forward)")
     args = ap.parse_args()
@@ -185,6 +220,28 @@ def main():
             y.copy_(x)
         torch.cuda.synchronize()
         print(json.dumps({"copy_bytes": n * 4, "copies": 3}), flush=True)
+        return
+    if args.copy_rate:
+        # what a plain streaming copy reaches at the step's kernel sizes:
+        # 38 MB (one 37.4k x 256 fp32 activation), 60 MB, 256 MB
+        out = {}
+        for mb in (38.3, 60.5, 256.0):
+            n = int(mb * 1e6) // 4
+            x = torch.ones(n, device="cuda")
+            y = torch.empty(n, device="cuda")
+            for _ in range(5):
+                y.copy_(x)
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            ts = []
+            for _ in range(20):
+                e0.record()
+                y.copy_(x)
+                e1.record()
+                e1.synchronize()
+                ts.append(e0.elapsed_time(e1))
+            ms = sorted(ts)[len(ts) // 2]
+            out[f"{mb:g}MB"] = dict(median_us=round(ms * 1e3, 2), gbs=round(2 * n * 4 / (ms / 1e3) / 1e9, 1))
+        print(json.dumps({"copy_rate": out}), flush=True)
         return
     import __graft_entry__
     __graft_entry__.load_package()
@@ -214,7 +271,7 @@ def main():
         pl.step(r["obs"], d_lists[i], r)
     torch.cuda.synchronize()
     L = native.lib()
-    native.check(L.ptcg_profile_begin(4096))
+    native.check(L.ptcg_profile_begin(256 * args.steps))
     t0 = time.perf_counter()
     for i in range(args.warmup, n_lists):
         pl.step(r["obs"], d_lists[i], r)
@@ -241,6 +298,7 @@ def main():
                        "minibatch": B, "rollout_rows": R, "seq_len": dm.l_tok + 1, "parallelism": "single GPU"},
             "gemm": {"launches_per_step": launches.value / K, "gemm_ms_per_step": round(ms.value / K, 4),
                      "executed_tflops": round(exec_flops.value / (ms.value / 1e3) / 1e12, 3)},
+            "hbm_kernels": hbm_kernels(L, K),
             "losses": {k: round(v, 5) for k, v in losses.items() if isinstance(v, float)},
         }
         pl.close()
@@ -284,6 +342,7 @@ def main():
                    "parallelism": "single GPU",
                    "compact_rows": "device count, no host read-back" if args.sync_free else "host read-back"},
         "roofline": roof,
+        "hbm_kernels": hbm_kernels(L, K),
         "losses": {k: round(v, 5) for k, v in losses.items() if isinstance(v, float)},
     }
     if not args.no_cpu_baseline and not bf16:
@@ -308,7 +367,7 @@ def bench_rollout(args):
         pl.rollout_step(d_obs, n, seed=0, step=i)
     torch.cuda.synchronize()
     L = native.lib()
-    native.check(L.ptcg_profile_begin(4096))
+    native.check(L.ptcg_profile_begin(256 * args.steps))
     t0 = time.perf_counter()
     for i in range(args.steps):
         acts, lps, vals = pl.rollout_step(d_obs, n, seed=0, step=args.warmup + i)

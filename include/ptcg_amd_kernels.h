@@ -77,12 +77,21 @@ int ptcg_kernel_attention_bwd(const float* qkv, const float* keep, const float* 
  * recomputing S and dP per query stripe (longer rows); -1 unsupported.     */
 int ptcg_kernel_attention_path(int L, int Dh);
 
-/* Launch timing of the GEMM kernel: between begin and end, every GEMM launch
- * (up to max_launches) is bracketed by a HIP event pair on its own stream.
- * end waits for the events and returns the summed kernel time (ms), the
- * number of launches and their summed 2*M*N*K.                             */
+/* Launch timing: between begin and end, every GEMM, LayerNorm and Adam
+ * launch (up to max_launches in all) is bracketed by a HIP event pair on its
+ * own stream.  end waits for the events and returns the GEMM launches'
+ * summed kernel time (ms), their number and their summed 2*M*N*K.
+ * No reference counterpart (measurement only).                             */
 int ptcg_profile_begin(int max_launches);
 int ptcg_profile_end(double* total_ms, int* launches, double* flops);
+
+/* Totals of one launch class of the last closed profile: summed kernel time
+ * (ms), launches, and summed algorithmic amount -- flops for class 0, HBM
+ * bytes for the others:
+ *   0 GEMM; 1 LayerNorm forward (8d+8 B per row + weights);
+ *   2 LayerNorm backward (12d+8 B per row, +4d with a residual gradient);
+ *   3 Adam norm pass (4 B per parameter); 4 Adam update (28 B per parameter). */
+int ptcg_profile_class(int cls, double* total_ms, int* launches, double* amount);
 
 #ifdef __cplusplus
 }

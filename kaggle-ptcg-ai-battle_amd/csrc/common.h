@@ -47,6 +47,15 @@ void ptcg_set_error(const char* fmt, ...);
 
 static inline int pt_cdiv(long a, long b) { return (int)((a + b - 1) / b); }
 
+// Launch timing for ptcg_profile_*: pt_prof_open records a start event on the
+// stream and returns a slot (-1 when no profile is open); pt_prof_close
+// records the end event with the launch's class and algorithmic amount
+// (flops for GEMMs, HBM bytes for the others).
+enum PtProfClass { PROF_GEMM = 0, PROF_LN_FWD = 1, PROF_LN_BWD = 2, PROF_ADAM_NORM = 3, PROF_ADAM_UPDATE = 4,
+                   PROF_NCLASS = 5 };
+int pt_prof_open(hipStream_t s);
+void pt_prof_close(int slot, int cls, double amount, hipStream_t s);
+
 // ---------------------------------------------------------------- device math
 // Exact (erf) GELU, torch nn.GELU() default; the reference's pt_gelu_fwd/bwd
 // (ptcg_kernels.cuh:111-128) computes the same function and derivative.

@@ -711,14 +711,18 @@ __global__ void colsum_level_kernel(const float* __restrict__ X, long ldx, int M
 }
 
 // Optional launch timing (ptcg_profile_*): a HIP event pair around every
-// GEMM kernel launch, recorded on the launch's own stream.
-struct GemmProf {
+// timed launch (GEMMs, LayerNorm, Adam), recorded on the launch's own stream,
+// with the launch's class and algorithmic amount (flops or bytes).
+struct LaunchProf {
     bool on = false;
     int used = 0;
     std::vector<hipEvent_t> ev;
-    std::vector<double> flops;
+    std::vector<double> amount;
+    std::vector<int> cls;
+    double sum_ms[PROF_NCLASS] = {}, sum_amount[PROF_NCLASS] = {};
+    int sum_n[PROF_NCLASS] = {};
 };
-GemmProf g_prof;
+LaunchProf g_prof;
 
 // products a launch executes: its share of the tiles, over the whole of K
 // (split-K launches cover K across grid.z)
@@ -731,31 +735,21 @@ double launch_flops(const GemmArgs& g) {
 
 template <bool AT, bool BT, int EPI, bool PARTIAL, bool DB, bool VEC>
 void launch(const GemmArgs& g, dim3 grid, int k_chunk, long part_stride, hipStream_t s) {
-    const bool rec = g_prof.on && g_prof.used * 2 + 1 < (int)g_prof.ev.size();
-    if (rec) (void)hipEventRecord(g_prof.ev[2 * g_prof.used], s);
+    const int slot = pt_prof_open(s);
     if (VEC && g.dma)
         hipLaunchKernelGGL((gemm_f32_dma_kernel<AT, BT, EPI, PARTIAL, DB>), grid, dim3(NT), 0, s, g, k_chunk,
                            part_stride);
     else
         hipLaunchKernelGGL((gemm_f32_kernel<AT, BT, EPI, PARTIAL, DB, VEC>), grid, dim3(NT), 0, s, g, k_chunk,
                            part_stride);
-    if (rec) {
-        (void)hipEventRecord(g_prof.ev[2 * g_prof.used + 1], s);
-        g_prof.flops[g_prof.used] = launch_flops(g);
-        g_prof.used++;
-    }
+    pt_prof_close(slot, PROF_GEMM, launch_flops(g), s);
 }
 
 template <bool AT, bool BT, int EPI, bool PARTIAL>
 void launch_bf16(const GemmArgs& g, dim3 grid, int k_chunk, long part_stride, hipStream_t s) {
-    const bool rec = g_prof.on && g_prof.used * 2 + 1 < (int)g_prof.ev.size();
-    if (rec) (void)hipEventRecord(g_prof.ev[2 * g_prof.used], s);
+    const int slot = pt_prof_open(s);
     hipLaunchKernelGGL((gemm_bf16_kernel<AT, BT, EPI, PARTIAL>), grid, dim3(NT), 0, s, g, k_chunk, part_stride);
-    if (rec) {
-        (void)hipEventRecord(g_prof.ev[2 * g_prof.used + 1], s);
-        g_prof.flops[g_prof.used] = launch_flops(g);
-        g_prof.used++;
-    }
+    pt_prof_close(slot, PROF_GEMM, launch_flops(g), s);
 }
 
 template <bool AT, bool BT>
@@ -830,12 +824,26 @@ int launch_full(const GemmArgs& g, bool db, dim3 grid, int k_chunk, hipStream_t 
 
 }  // namespace
 
+int pt_prof_open(hipStream_t s) {
+    if (!g_prof.on || g_prof.used * 2 + 1 >= (int)g_prof.ev.size()) return -1;
+    (void)hipEventRecord(g_prof.ev[2 * g_prof.used], s);
+    return g_prof.used++;
+}
+
+void pt_prof_close(int slot, int cls, double amount, hipStream_t s) {
+    if (slot < 0) return;
+    (void)hipEventRecord(g_prof.ev[2 * slot + 1], s);
+    g_prof.cls[slot] = cls;
+    g_prof.amount[slot] = amount;
+}
+
 extern "C" int ptcg_profile_begin(int max_launches) {
     PT_REQUIRE(max_launches > 0, "profile_begin: max_launches must be positive");
     for (auto e : g_prof.ev) (void)hipEventDestroy(e);
     g_prof.ev.assign(2 * (size_t)max_launches, nullptr);
     for (auto& e : g_prof.ev) PT_HIP(hipEventCreate(&e));
-    g_prof.flops.assign(max_launches, 0.0);
+    g_prof.amount.assign(max_launches, 0.0);
+    g_prof.cls.assign(max_launches, PROF_GEMM);
     g_prof.used = 0;
     g_prof.on = true;
     return PTCG_OK;
@@ -843,20 +851,34 @@ extern "C" int ptcg_profile_begin(int max_launches) {
 
 extern "C" int ptcg_profile_end(double* total_ms, int* launches, double* flops) {
     g_prof.on = false;
-    double ms = 0.0, fl = 0.0;
+    for (int c = 0; c < PROF_NCLASS; ++c) {
+        g_prof.sum_ms[c] = 0.0;
+        g_prof.sum_amount[c] = 0.0;
+        g_prof.sum_n[c] = 0;
+    }
     for (int i = 0; i < g_prof.used; ++i) {
         PT_HIP(hipEventSynchronize(g_prof.ev[2 * i + 1]));
         float t = 0.f;
         PT_HIP(hipEventElapsedTime(&t, g_prof.ev[2 * i], g_prof.ev[2 * i + 1]));
-        ms += t;
-        fl += g_prof.flops[i];
+        const int c = g_prof.cls[i];
+        g_prof.sum_ms[c] += t;
+        g_prof.sum_amount[c] += g_prof.amount[i];
+        g_prof.sum_n[c]++;
     }
-    if (total_ms) *total_ms = ms;
-    if (launches) *launches = g_prof.used;
-    if (flops) *flops = fl;
+    if (total_ms) *total_ms = g_prof.sum_ms[PROF_GEMM];
+    if (launches) *launches = g_prof.sum_n[PROF_GEMM];
+    if (flops) *flops = g_prof.sum_amount[PROF_GEMM];
     for (auto e : g_prof.ev) (void)hipEventDestroy(e);
     g_prof.ev.clear();
     g_prof.used = 0;
+    return PTCG_OK;
+}
+
+extern "C" int ptcg_profile_class(int cls, double* total_ms, int* launches, double* amount) {
+    PT_REQUIRE(cls >= 0 && cls < PROF_NCLASS, "profile_class: class %d out of range", cls);
+    if (total_ms) *total_ms = g_prof.sum_ms[cls];
+    if (launches) *launches = g_prof.sum_n[cls];
+    if (amount) *amount = g_prof.sum_amount[cls];
     return PTCG_OK;
 }
 

@@ -99,6 +99,8 @@ _SIGS = {
     "ptcg_profile_begin": (ctypes.c_int, [ctypes.c_int]),
     "ptcg_profile_end": (ctypes.c_int, [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_int),
                                         ctypes.POINTER(ctypes.c_double)]),
+    "ptcg_profile_class": (ctypes.c_int, [ctypes.c_int, ctypes.POINTER(ctypes.c_double),
+                                          ctypes.POINTER(ctypes.c_int), ctypes.POINTER(ctypes.c_double)]),
     "ptcg_kernel_gemm": (ctypes.c_int, [
         ctypes.c_int, ctypes.c_int, ctypes.c_int, c_void_p, ctypes.c_int64, ctypes.c_int,
         c_void_p, ctypes.c_int64, ctypes.c_int, c_void_p, ctypes.c_int64, ctypes.c_int,

@@ -141,7 +141,10 @@ def test_colsum(cuda):
     assert rel_l2(out.cpu(), X.double().sum(0)) < 1e-6
 
 
-@pytest.mark.parametrize("rows,D", [(1000, 256), (37, 64), (130, 1024), (9, 300), (1284, 634), (50, 127)])
+# (20001, 256): several row pairs per wave in the backward and an odd tail;
+# (5, 256): fewer rows than one workgroup's waves
+@pytest.mark.parametrize("rows,D", [(1000, 256), (37, 64), (130, 1024), (9, 300), (1284, 634), (50, 127),
+                                    (20001, 256), (5, 256), (33, 512), (700, 1024)])
 def test_layernorm_fwd_bwd(rows, D, cuda):
     g = torch.Generator().manual_seed(rows + D)
     x = (torch.randn(rows, D, generator=g) * 3 + 1).double().requires_grad_()

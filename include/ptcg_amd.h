@@ -177,6 +177,46 @@ int ptcg_sample_actions(const float* dec_out, int n, int A, const float* mask, i
                         const int32_t* row_idx, uint64_t seed, uint64_t step, float* actions,
                         float* logprobs, float* values, float* uniforms, void* stream);
 
+/* ---- rollout-side steps of train_impl (pufferlib.cu:1847-2160) ----------
+ * All buffers are device fp32 (int32 where named) on the caller's stream.
+ *
+ * transpose_102 (kernels.cu:179-188; train_impl :1863-1883): dst[b, a, c] =
+ * src[a, b, c] for shapes [A, B, C] -> [B, A, C]; clamp != 0 also clamps to
+ * [-1, 1] on the way (the rewards' clamp_precision_kernel, :1889-1891).   */
+int ptcg_transpose_102(float* dst, const float* src, int A, int B, int C, int clamp, void* stream);
+/* fill_precision_kernel (:1893-1895; the importance ratios' reset to 1).  */
+int ptcg_fill(float* dst, int64_t n, float value, void* stream);
+/* negamax V-trace/GAE, ptcg_puff_advantage / k_negamax_adv
+ * (ptcg_model2.cu:287-321, after the advantages' puf_zero at :1966): rows
+ * of T steps in (B, T) layout; seat_t = obs[(b*T + t)*obs_stride + seat_col]
+ * (the actor-seat global feature); advantages[:, T-1] = 0.  returns
+ * (optional) = values + advantages, which select_copy forms (:1773).      */
+int ptcg_negamax_advantage(const float* values, const float* rewards, const float* dones,
+                           const float* importance, const float* obs, int64_t obs_stride, int seat_col,
+                           float* advantages, float* returns, float gamma, float lambda, float rho_clip,
+                           float c_clip, int B, int T, void* stream);
+/* prioritized replay, prio_replay_cuda (:1455-1591): per segment
+ * p_b = (sum_t |adv_bt|)^alpha (non-finite -> 0), probs = (p + 1e-6) /
+ * (sum p + 1e-6) (written to probs, B floats), cdf = inclusive scan (B
+ * floats); n_samples draws with replacement u_k = Philox4x32-10(counter =
+ * (offset + k, 0, 1), key = seed) where the reference draws cuRAND
+ * Philox(seed, offset + k); idx_k = first b with cdf_b >= u_k (B-1 if none);
+ * mb_prio_k = (total_agents * probs[idx_k])^-anneal_beta; *rng_offset (device
+ * int64) += n_samples.  Optional outputs for a step that reads rows through
+ * row_idx: row_idx (n_samples * T int32) = idx_k * T + t; row_prio (B * T
+ * floats, rollout rows) gets mb_prio_k at the sampled segments' rows.
+ * B <= ptcg_prio_replay_max_segments().                                    */
+int ptcg_prio_replay_max_segments(void);
+int ptcg_prio_replay(const float* advantages, int B, int T, float prio_alpha, int n_samples,
+                     int total_agents, float anneal_beta, uint64_t seed, int64_t* rng_offset,
+                     float* probs, float* cdf, int32_t* idx, float* mb_prio, int32_t* row_idx,
+                     float* row_prio, void* stream);
+/* index_copy (:1747-1754; the ratio / new-value write-back :2146-2160):
+ * dst row idx[i] <- src row i, rows of row_floats floats; rows whose index
+ * is outside [0, dst_rows) are skipped.                                   */
+int ptcg_index_copy(float* dst, const int32_t* idx, const float* src, int n_idx, int row_floats,
+                    int dst_rows, void* stream);
+
 /* ---- trainer (create_pufferl / train / debug_forward / weights IO) ----- */
 int ptcg_trainer_create(const PtcgDims* dims, const PtcgHypers* hyp, int minibatch,
                         PtcgTrainer** out);
@@ -226,6 +266,11 @@ int ptcg_trainer_step(PtcgTrainer* t, const float* obs, const int32_t* row_idx,
                       const float* actions, const float* old_logprobs,
                       const float* advantages, const float* returns, const float* values,
                       void* stream);
+/* Importance weights of the policy loss (the reference's mb_prio, read per
+ * row as g.prio, pufferlib.cu:1040): a device array read through row_idx
+ * like the other per-row inputs (e.g. ptcg_prio_replay's row_prio), used by
+ * every later step until replaced; NULL = weight 1 (the default).          */
+int ptcg_trainer_set_prio(PtcgTrainer* t, const float* prio);
 /* The same step without the optimizer (grads left in the grads arena).    */
 int ptcg_trainer_forward_backward(PtcgTrainer* t, const float* obs, const int32_t* row_idx,
                                   const float* actions, const float* old_logprobs,

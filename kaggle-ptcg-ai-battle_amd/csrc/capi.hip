@@ -282,6 +282,7 @@ struct PtcgTrainer {
     int prec = 0;
     int sync_free = 0;
     int skip_masked = 1;   // the PPO loss and the sampler mask those slots
+    const float* prio = nullptr;   // policy-loss importance weights per rollout row
     std::vector<float> st_f[5];
     std::vector<int32_t> st_i[2];
 };
@@ -495,11 +496,17 @@ static int fwd_bwd(PtcgTrainer* t, const float* obs, const int32_t* idx, const f
     PT_TRY(ptcg_model_forward(t->model, obs, idx, t->B, &out, s));
     const PtcgHypers& h = t->hyp;
     PT_TRY(pt_ppo_loss(out, t->B, t->dm.n_opt, obs + t->off.opt_mask, t->off.size, idx, actions,
-                       old_logprobs, advantages, returns, values, nullptr, h.clip_coef, h.vf_clip_coef,
+                       old_logprobs, advantages, returns, values, t->prio, h.clip_coef, h.vf_clip_coef,
                        h.vf_coef, h.ent_coef, t->grad, t->ratio, t->newvalue, t->stats, t->guard,
                        t->ppo_part, s));
     PT_TRY(ptcg_model_bind_returns(t->model, returns));
     PT_TRY(ptcg_model_backward(t->model, t->grad, s));
+    return PTCG_OK;
+}
+
+extern "C" int ptcg_trainer_set_prio(PtcgTrainer* t, const float* prio) {
+    PT_REQUIRE(t, "trainer_set_prio: null trainer");
+    t->prio = prio;
     return PTCG_OK;
 }
 

@@ -76,6 +76,28 @@ __device__ __forceinline__ void pt_gelu_both(float x, float& g, float& gd) {
     gd = cdf + x * pdf;
 }
 
+// Philox4x32-10 (Salmon, Moraes, Dror, Shaw, "Parallel random numbers: as
+// easy as 1, 2, 3", SC'11), restated from the paper: 10 rounds of
+// (hi, lo) = mulhilo(M, c), Weyl key bumps.  Counter-based: every (key,
+// counter) pair is its own stream, no state in memory.
+__device__ __forceinline__ uint4 philox4x32_10(uint4 c, uint2 k) {
+    constexpr unsigned M0 = 0xD2511F53u, M1 = 0xCD9E8D57u, W0 = 0x9E3779B9u, W1 = 0xBB67AE85u;
+#pragma unroll
+    for (int r = 0; r < 10; ++r) {
+        const unsigned hi0 = __umulhi(M0, c.x), lo0 = M0 * c.x;
+        const unsigned hi1 = __umulhi(M1, c.z), lo1 = M1 * c.z;
+        c = make_uint4(hi1 ^ c.y ^ k.x, lo1, hi0 ^ c.w ^ k.y, lo0);
+        k.x += W0;
+        k.y += W1;
+    }
+    return c;
+}
+// uniform in (0, 1) from 32 random bits: (2 (x >> 9) + 1) * 2^-24, exactly
+// representable in fp32, in [2^-24, 1 - 2^-24]
+__device__ __forceinline__ float pt_u01(unsigned x) {
+    return ((float)(x >> 9) * 2.0f + 1.0f) * 5.9604644775390625e-08f;
+}
+
 // fp32 id read back from an obs row: C cast truncates toward zero, then clamp
 __device__ __forceinline__ int pt_id_clamp(float v, int hi) {
     int i = (int)v;

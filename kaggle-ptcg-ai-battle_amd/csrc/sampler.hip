@@ -14,19 +14,6 @@
 
 namespace {
 
-__device__ __forceinline__ uint4 philox4x32_10(uint4 c, uint2 k) {
-    constexpr unsigned M0 = 0xD2511F53u, M1 = 0xCD9E8D57u, W0 = 0x9E3779B9u, W1 = 0xBB67AE85u;
-#pragma unroll
-    for (int r = 0; r < 10; ++r) {
-        const unsigned hi0 = __umulhi(M0, c.x), lo0 = M0 * c.x;
-        const unsigned hi1 = __umulhi(M1, c.z), lo1 = M1 * c.z;
-        c = make_uint4(hi1 ^ c.y ^ k.x, lo1, hi0 ^ c.w ^ k.y, lo0);
-        k.x += W0;
-        k.y += W1;
-    }
-    return c;
-}
-
 __device__ __forceinline__ float safe_masked(float l, const float* mk, int a) {
     if (isnan(l)) l = 0.f;
     if (isinf(l)) l = l > 0.f ? 3.4028e+38f : -3.4028e+38f;
@@ -54,7 +41,7 @@ __global__ void sample_kernel(const float* __restrict__ dec, int n, int A, const
     const float lse = mx + logf(se);
     const uint4 r = philox4x32_10(make_uint4((unsigned)i, (unsigned)step, (unsigned)(step >> 32), 0u),
                                   make_uint2((unsigned)seed, (unsigned)(seed >> 32)));
-    const float u = ((float)(r.x >> 9) * 2.0f + 1.0f) * 5.9604644775390625e-08f;   // (2k+1) * 2^-24
+    const float u = pt_u01(r.x);
     float cs = 0.f;
     int act = -1;
     for (int a = 0; a < A; ++a) {

@@ -93,6 +93,14 @@ class PtcgDims:
     def offsets(self):
         return build_offsets(self)[0]
 
+    def seat_col(self):
+        """Obs column of the actor-seat global feature (GlobF.ACTOR_SEAT = 31,
+        ptcg/rl/buffers.py:154,232) that the negamax advantage reads
+        (PT_SEAT_COL_M, native/model/ptcg_model2.cu:288)."""
+        if self.global_f <= 31:
+            raise ValueError(f"global_f={self.global_f} has no actor-seat column (31)")
+        return self.offsets()["global_f"][0] + 31
+
     def as_dict(self):
         return asdict(self)
 

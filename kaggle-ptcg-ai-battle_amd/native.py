@@ -95,6 +95,21 @@ _SIGS = {
                                             ctypes.POINTER(c_void_p)]),
     "ptcg_trainer_sync": (ctypes.c_int, [c_void_p]),
     "ptcg_trainer_step_count": (ctypes.c_int, [c_void_p, c_i32_p]),
+    "ptcg_trainer_set_prio": (ctypes.c_int, [c_void_p, c_void_p]),
+    # rollout-side steps
+    "ptcg_transpose_102": (ctypes.c_int, [c_void_p, c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                          ctypes.c_int, c_void_p]),
+    "ptcg_fill": (ctypes.c_int, [c_void_p, ctypes.c_int64, ctypes.c_float, c_void_p]),
+    "ptcg_negamax_advantage": (ctypes.c_int, [
+        c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, ctypes.c_int64, ctypes.c_int,
+        c_void_p, c_void_p, ctypes.c_float, ctypes.c_float, ctypes.c_float, ctypes.c_float,
+        ctypes.c_int, ctypes.c_int, c_void_p]),
+    "ptcg_prio_replay_max_segments": (ctypes.c_int, []),
+    "ptcg_prio_replay": (ctypes.c_int, [
+        c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_float, ctypes.c_int, ctypes.c_int, ctypes.c_float,
+        ctypes.c_uint64, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
+    "ptcg_index_copy": (ctypes.c_int, [c_void_p, c_void_p, c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                       c_void_p]),
     # include/ptcg_amd_kernels.h
     "ptcg_profile_begin": (ctypes.c_int, [ctypes.c_int]),
     "ptcg_profile_end": (ctypes.c_int, [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_int),

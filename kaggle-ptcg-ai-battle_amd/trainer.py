@@ -7,6 +7,9 @@ reference's messages) for the hot-path subset:
 
     create_pufferl(args) -> PuffeRL         bindings.cu:581-673
     train(pl) -> dict                       bindings.cu:184-192 / train_impl
+                                            (segment rollouts: advantage ->
+                                            prioritized replay -> step ->
+                                            ratio / value write-back)
     debug_forward(pl, rows) -> (B, A+1)     bindings.cu:221-250
     save_weights / load_weights             bindings.cu:202-215, 339-367
     save_state / load_state                 bindings.cu:257-337 (Adam state)
@@ -15,7 +18,11 @@ reference's messages) for the hot-path subset:
 
 Rollout collection is out of scope: ``set_rollout`` hands the trainer a
 device-resident rollout (obs rows plus per-row actions, old log-probs,
-advantages, returns, old values) in place of the env/vec pipeline.
+advantages, returns, old values) in place of the env/vec pipeline, trained
+from index lists; ``set_segment_rollout`` hands it what the reference's
+trainer holds after collection (total_agents segments of horizon steps:
+obs, actions, log-probs, rewards, terminals, values), and ``train`` then runs
+train_impl's minibatch loop (pufferlib.cu:1963-2160) on the device.
 Device memory for the rollout is plumbing held in torch tensors; every
 computation runs in libptcg_amd.so.
 """
@@ -35,6 +42,9 @@ TRAIN_DEFAULTS = {
     "vf_coef": 0.5, "ent_coef": 0.01, "kl_skip_threshold": 0.0,
     "vf_skip_threshold": 0.0, "minibatch_size": 512, "update_epochs": 4,
     "minibatches_per_epoch": 8,
+    # segment rollouts (train_impl; native/train_native.py:250-270 values)
+    "gamma": 1.0, "gae_lambda": 0.95, "vtrace_rho_clip": 1.0, "vtrace_c_clip": 1.0,
+    "prio_alpha": 0.8, "prio_beta0": 0.2, "replay_ratio": 1.0, "total_epochs": 1,
 }
 
 
@@ -215,13 +225,103 @@ def set_rollout(pl, obs, actions, logprobs, advantages, returns, values):
         values=pl.to_device(values), n=n)
 
 
+def set_segment_rollout(pl, obs, actions, logprobs, rewards, dones, values, horizon, layout="BT"):
+    """A rollout as the reference's trainer holds it after collection:
+    total_agents segments of ``horizon`` steps.  layout "TB": arrays in
+    collection order (horizon, total_agents, ...), moved to the train layout
+    (total_agents, horizon, ...) on the device (ptcg_transpose_102,
+    train_impl :1863-1883); "BT": already in the train layout (row b*T + t).
+    Rewards are clamped to [-1, 1] and the importance ratios set to 1, as
+    train_impl does before its minibatch loop (:1889-1895)."""
+    torch = pl._torch
+    L = lib()
+    T = int(horizon)
+    obs = np.ascontiguousarray(obs, dtype=np.float32)
+    n = obs.size // pl.obs_size
+    if obs.size != n * pl.obs_size or n % T:
+        raise RuntimeError(f"segment rollout: {obs.size} obs floats are not whole segments of {T} rows")
+    S = n // T
+    if layout not in ("BT", "TB"):
+        raise ValueError(f"layout must be 'BT' or 'TB', got {layout!r}")
+    if S > L.ptcg_prio_replay_max_segments():
+        raise RuntimeError(f"segment rollout: {S} segments exceed {L.ptcg_prio_replay_max_segments()}")
+    dev = lambda a, dt=torch.float32: torch.empty(a, dtype=dt, device="cuda")
+
+    def train_layout(a, width, clamp=0):
+        a = np.ascontiguousarray(a, dtype=np.float32).reshape(-1)
+        if a.size != n * width:
+            raise RuntimeError(f"segment rollout: array of {a.size} floats, expected {n * width}")
+        src = torch.from_numpy(a).to("cuda")
+        if layout == "BT" and not clamp:
+            return src
+        out = dev(n * width)
+        if layout == "BT":   # a [1, n*width] -> [n*width, 1] transpose is the clamped copy
+            check(L.ptcg_transpose_102(out.data_ptr(), src.data_ptr(), 1, n * width, 1, clamp, None))
+        else:
+            check(L.ptcg_transpose_102(out.data_ptr(), src.data_ptr(), T, S, width, clamp, None))
+        return out
+
+    r = dict(obs=train_layout(obs, pl.obs_size), actions=train_layout(actions, 1),
+             logprobs=train_layout(logprobs, 1), rewards=train_layout(rewards, 1, clamp=1),
+             dones=train_layout(dones, 1), values=train_layout(values, 1).clone(), ratio=dev(n),
+             advantages=dev(n), returns=dev(n), probs=dev(S), cdf=dev(S), row_prio=dev(n),
+             idx=dev(max(S, pl.minibatch // T), torch.int32), mb_prio=dev(max(S, pl.minibatch // T)),
+             row_idx=dev(pl.minibatch, torch.int32),
+             rng_offset=torch.zeros(1, dtype=torch.int64, device="cuda"), n=n, horizon=T, segments=S)
+    check(L.ptcg_fill(r["ratio"].data_ptr(), n, 1.0, None))
+    pl.rollout = r
+
+
+def _train_segments(pl):
+    """train_impl's minibatch loop (pufferlib.cu:1963-2160): per minibatch,
+    the negamax advantage over the whole rollout, a prioritized draw of
+    minibatch / horizon segments, one step on their rows with their
+    importance weights, then the step's ratios and new values written back
+    into the rollout at the drawn segments."""
+    L = lib()
+    r, cfg = pl.rollout, pl.train_cfg
+    T, S, B = r["horizon"], r["segments"], pl.minibatch
+    if B % T:
+        raise RuntimeError(f"minibatch {B} is not a whole number of {T}-step segments")
+    mb_segs = B // T
+    total_mb = int(cfg["replay_ratio"] * S * T / B)
+    alpha, b0 = float(cfg["prio_alpha"]), float(cfg["prio_beta0"])
+    beta = b0 + (1.0 - b0) * alpha * pl.epoch / max(1, int(cfg["total_epochs"]))
+    seat = pl.dims.seat_col()
+    P = lambda k: r[k].data_ptr()
+    _, _, ratio_buf, nv_buf = pl.buffers()
+    try:
+        for _ in range(total_mb):
+            check(L.ptcg_negamax_advantage(P("values"), P("rewards"), P("dones"), P("ratio"), P("obs"),
+                                           pl.obs_size, seat, P("advantages"), P("returns"),
+                                           cfg["gamma"], cfg["gae_lambda"], cfg["vtrace_rho_clip"],
+                                           cfg["vtrace_c_clip"], S, T, None))
+            check(L.ptcg_prio_replay(P("advantages"), S, T, alpha, mb_segs, S, beta, pl.seed & ((1 << 64) - 1),
+                                     P("rng_offset"), P("probs"), P("cdf"), P("idx"), P("mb_prio"),
+                                     P("row_idx"), P("row_prio"), None))
+            check(L.ptcg_trainer_set_prio(pl._h, P("row_prio")))
+            pl.step(r["obs"], r["row_idx"], r)
+            check(L.ptcg_index_copy(P("ratio"), P("idx"), ratio_buf, mb_segs, T, S, None))
+            check(L.ptcg_index_copy(P("values"), P("idx"), nv_buf, mb_segs, T, S, None))
+    finally:
+        check(L.ptcg_trainer_set_prio(pl._h, None))
+    pl.epoch += 1
+    return log(pl)
+
+
 def train(pl, index_lists=None):
-    """One PPO update over the stored rollout: update_epochs epochs, each a
-    fresh seeded permutation cut into minibatches (at most
-    minibatches_per_epoch of them); or the given index lists.  Returns the
+    """One PPO update over the stored rollout.  A segment rollout
+    (:func:`set_segment_rollout`) runs the reference's prioritized minibatch
+    loop; a row rollout (:func:`set_rollout`) runs update_epochs epochs, each
+    a fresh seeded permutation cut into minibatches (at most
+    minibatches_per_epoch of them), or the given index lists.  Returns the
     loss dictionary of :func:`log`."""
     if pl.rollout is None:
         raise RuntimeError("train: no rollout set (call set_rollout)")
+    if "horizon" in pl.rollout:
+        if index_lists is not None:
+            raise RuntimeError("train: index lists apply to row rollouts, not segment rollouts")
+        return _train_segments(pl)
     from .synth import minibatch_indices
     r = pl.rollout
     B = pl.minibatch

@@ -18,7 +18,7 @@ def minibatch_step(model, opt, obs, inp, hyp):
     res = ppo_loss(out.detach(), mask, T("actions"), T("logprobs"), T("advantages"),
                    T("returns"), T("values"), clip=hyp["clip_coef"],
                    vf_clip=hyp["vf_clip_coef"], vf_coef=hyp["vf_coef"],
-                   ent_coef=hyp["ent_coef"])
+                   ent_coef=hyp["ent_coef"], prio=T("prio") if "prio" in inp else None)
     for p in model.parameters():
         p.grad = None
     # PPO gradient on [scores || value]; with the oracle critic the aux losses

@@ -18,6 +18,8 @@ the rollout step — inference forward of 8192 rows plus one sampled action
 per row; ``--workload frozen`` times the training step of the reference's
 own model variant (frozen layout: 160 tokens, d256/H8/FFN512, static-table
 card vectors, oracle critic over 218 positions, aux losses);
+``--workload replay`` times the rollout-side steps around the training step
+(negamax advantage, prioritized replay draw, train-layout transposes);
 ``--workload bf16`` times the training step at B = 2048 with bf16 GEMM
 products (fp32 accumulation and everything else fp32).
 """
@@ -195,7 +197,7 @@ def main():
     ap.add_argument("--rollout", type=int, default=16384)
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--workload", choices=("train", "rollout", "frozen", "bf16"), default="train")
+    ap.add_argument("--workload", choices=("train", "rollout", "frozen", "bf16", "replay"), default="train")
     ap.add_argument("--rollout-rows", type=int, default=8192)
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run three 256 MiB device-to-device copies (the HBM counter calibration)")
@@ -249,6 +251,8 @@ def main():
 
     if args.workload == "rollout":
         return bench_rollout(args)
+    if args.workload == "replay":
+        return bench_replay(args)
     dm = dims.FROZEN if args.workload == "frozen" else dims.CORE
     B, R = args.minibatch, args.rollout
     bf16 = args.workload == "bf16"
@@ -396,6 +400,116 @@ def bench_rollout(args):
                          launches_per_step=launches.value / K, mean_valid_seq=round(lv, 2)),
     }
     pl.close()
+    print(json.dumps(line), flush=True)
+
+
+def bench_replay(args):
+    """Rollout-side steps of train_impl at the reference trainer's defaults
+    (native/train_native.py: total_agents 2048, horizon 64, minibatch 1024):
+    per minibatch the negamax advantage over the whole rollout and one
+    prioritized draw of 16 segments (weights, row indices); per epoch the
+    transposes of the rollout into the train layout (obs rows of the CORE
+    dims and the six per-step arrays).  Synthetic device data."""
+    import torch
+    from ptcg_amd import dims, native
+    import oracle.replay as orp
+    L = native.lib()
+    dm = dims.CORE
+    W, S, T, mb = dm.obs_size, 2048, 64, 1024
+    n, segs, seat = S * T, mb // T, dm.seat_col()
+    g = torch.Generator(device="cuda").manual_seed(5)
+    obs_tb = torch.randn(n * W, device="cuda", generator=g)
+    obs_tb.view(n, W)[:, seat] = torch.randint(0, 2, (n,), device="cuda", generator=g).float()
+    obs = torch.empty_like(obs_tb)
+    small_tb = [torch.randn(n, device="cuda", generator=g) for _ in range(6)]
+    small = [torch.empty(n, device="cuda") for _ in range(6)]
+    values, rewards = torch.randn(n, device="cuda", generator=g), torch.rand(n, device="cuda", generator=g) * 2 - 1
+    dones = (torch.rand(n, device="cuda", generator=g) < 0.02).float()
+    ratio = torch.rand(n, device="cuda", generator=g) + 0.5
+    adv, ret = torch.empty(n, device="cuda"), torch.empty(n, device="cuda")
+    probs, cdf, mbp = torch.empty(S, device="cuda"), torch.empty(S, device="cuda"), torch.empty(segs, device="cuda")
+    idx, rows = torch.empty(segs, dtype=torch.int32, device="cuda"), torch.empty(mb, dtype=torch.int32, device="cuda")
+    rprio, off = torch.empty(n, device="cuda"), torch.zeros(1, dtype=torch.int64, device="cuda")
+    P = lambda t: t.data_ptr()
+
+    def transposes():
+        native.check(L.ptcg_transpose_102(P(obs), P(obs_tb), T, S, W, 0, None))
+        for k in range(6):
+            native.check(L.ptcg_transpose_102(P(small[k]), P(small_tb[k]), T, S, 1, int(k == 1), None))
+
+    def advantage():
+        native.check(L.ptcg_negamax_advantage(P(values), P(rewards), P(dones), P(ratio), P(obs), W, seat, P(adv),
+                                              P(ret), 1.0, 0.95, 1.0, 1.0, S, T, None))
+
+    def replay():
+        native.check(L.ptcg_prio_replay(P(adv), S, T, 0.8, segs, S, 0.2, 7, P(off), P(probs), P(cdf), P(idx),
+                                        P(mbp), P(rows), P(rprio), None))
+
+    def timed(fn, reps):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+        for a, b in ev:
+            a.record()
+            fn()
+            b.record()
+        torch.cuda.synchronize()
+        return sorted(a.elapsed_time(b) for a, b in ev)[reps // 2] * 1e3   # median us
+
+    K = args.steps
+    t_obs = timed(lambda: native.check(L.ptcg_transpose_102(P(obs), P(obs_tb), T, S, W, 0, None)), max(5, K // 4))
+    t_tr = timed(transposes, max(5, K // 4))
+    t_adv = timed(advantage, K)
+    t_rep = timed(replay, K)
+    # whole minibatch prep, back to back (advantage then replay), K times
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(K):
+        advantage()
+        replay()
+    torch.cuda.synchronize()
+    sec = time.perf_counter() - t0
+    obs_bytes = 2.0 * n * W * 4
+    adv_bytes = n * (4 * 4 + 4 + 2 * 4)        # values, rewards, dones, ratio, seat; advantages, returns
+    line = {
+        "metric": "rollout-side minibatch prep (negamax advantage + prioritized replay draw) per second "
+                  "@2048 segments x 64 steps, minibatch 1024",
+        "value": round(K / sec, 2), "unit": "minibatches/s", "n_gpus": 1, "steps": K, "warmup": 3,
+        "ms_per_step": round(sec * 1e3 / K, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "fp32", "data": "synthetic",
+        "config": {"workload": "train_impl's per-minibatch rollout-side work at total_agents 2048, horizon 64, "
+                               "minibatch 1024 (16 segments), CORE obs rows (4736 floats); per-epoch transposes "
+                               "(T, B, ...) -> (B, T, ...)", "segments": S, "horizon": T, "minibatch": mb},
+        # event pairs around each host call: the short kernels' figures include
+        # the host's launch gap (the GPU idles between calls); kernel-only
+        # durations come from a rocprofv3 kernel trace of this workload
+        "per_call_us_host_inclusive": {"negamax_advantage": round(t_adv, 2), "prio_replay": round(t_rep, 2),
+                                       "transpose_obs": round(t_obs, 1), "epoch_transposes": round(t_tr, 1)},
+        "roofline": dict(bound="hbm", kernel="transpose_rows_kernel (obs rows into the train layout, per epoch)",
+                         achieved=round(obs_bytes / (t_obs / 1e6) / 1e9, 1), peak=HBM_PEAK_GBS, unit="GB/s",
+                         frac=round(obs_bytes / (t_obs / 1e6) / 1e9 / HBM_PEAK_GBS, 4), traffic=None,
+                         bytes_per_launch=obs_bytes),
+        "advantage_bytes_per_launch": adv_bytes,
+    }
+    if not args.no_cpu_baseline:
+        # the oracle's numpy restatement on the host: advantage + replay draw
+        v = values.view(S, T).cpu().numpy()
+        rr = rewards.view(S, T).cpu().numpy()
+        dd = dones.view(S, T).cpu().numpy()
+        ii = ratio.view(S, T).cpu().numpy()
+        st = obs.view(n, W)[:, seat].reshape(S, T).cpu().numpy()
+        reps, t0 = 0, time.perf_counter()
+        while True:
+            a, _ = orp.negamax_advantage(v, rr, dd, ii, st, 1.0, 0.95, 1.0, 1.0)
+            orp.prio_replay(a, 0.8, segs, S, 0.2, 7, 0)
+            reps += 1
+            if time.perf_counter() - t0 > min(args.cpu_seconds, 10.0) and reps >= 2:
+                break
+        cs = (time.perf_counter() - t0) / reps
+        line["cpu_baseline"] = dict(value=round(1.0 / cs, 3), unit="minibatches/s", cores=1, kind="port",
+                                    sample=f"{reps} minibatch preps (numpy, vectorized over segments)")
+        line["gpu_over_cpu"] = round(line["value"] / line["cpu_baseline"]["value"], 1)
     print(json.dumps(line), flush=True)
 
 

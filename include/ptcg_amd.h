@@ -165,6 +165,30 @@ int ptcg_adam_step(float* weights, float* grads, float* m, float* v, int64_t n,
                    const float* gate, int32_t* step, float* norm_out, float* workspace,
                    void* stream);
 
+/* ---- Muon, the reference's optimizer (muon.cu:154-297) ------------------
+ * muon_init + muon_post_create: momentum arena (zeroed) and Newton-Schulz
+ * workspaces for the tensor shapes of dims; lr is kept on the device
+ * (the reference's lr_ptr).  momentum = the trainer's beta1 (pufferlib.cu:
+ * 2660), weight_decay applies to >= 2-D tensors (the reference passes 0),
+ * wd_1d to 1-D tensors (muon_wd_1d).                                       */
+typedef struct PtcgMuon PtcgMuon;
+int ptcg_muon_create(const PtcgDims* dims, double lr, double momentum, double weight_decay, double wd_1d,
+                     PtcgMuon** out);
+void ptcg_muon_free(PtcgMuon* m);
+/* the host's learning-rate write (train_impl's cudaMemcpy to lr_ptr, pufferlib.cu:1937); synchronous */
+int ptcg_muon_set_lr(PtcgMuon* m, float lr);
+/* device pointer of the momentum arena (ptcg_arena_floats(dims) floats, params layout) */
+float* ptcg_muon_momentum(PtcgMuon* m);
+/* muon_step (muon.cu:215-297) on the params / grads arenas: global-norm clip
+ * (coefficient min(max_grad_norm / (||g|| + 1e-6), 1)), then per tensor
+ * Nesterov momentum + 5 Newton-Schulz iterations + scaled update (>= 2-D) or
+ * EMA momentum + update (1-D).  grads are read, not modified (the reference
+ * clips and transforms them in place).  gate: optional device float, 0 = the
+ * call changes neither weights nor momentum.  grad_norm_out: optional device
+ * float receiving ||g||_2 before clipping.                                 */
+int ptcg_muon_step(PtcgMuon* m, float* weights, const float* grads, float max_grad_norm, const float* gate,
+                   float* grad_norm_out, void* stream);
+
 /* ---- action sampler (sample_logits, pufferlib.cu:584-718) ---------------
  * One discrete head of A options per row of dec_out (n, A+1) = [scores ||
  * value]: masked (mask == 0 -> -1e4, rows at mask_stride, gathered through
@@ -244,6 +268,15 @@ int ptcg_trainer_debug_forward(PtcgTrainer* t, const float* obs_host, int n, flo
 int ptcg_trainer_rollout(PtcgTrainer* t, const float* obs, const int32_t* row_idx, int n,
                          uint64_t seed, uint64_t step, float* actions, float* logprobs,
                          float* values, void* stream);
+/* Optimizer of the trainer's steps: 0 = clip + Adam (default), 1 = Muon
+ * (ptcg_muon_*, momentum = hyp.beta1, weight decay 0 on >= 2-D tensors,
+ * wd_1d on 1-D tensors, lr = hyp.lr).  save_state / load_state then use the
+ * reference's PTCGSTA1 format (bindings.cu:257-337: header, packed weights,
+ * packed momentum) instead of PTCGADM1.                                    */
+int ptcg_trainer_set_optimizer(PtcgTrainer* t, int kind, double wd_1d);
+/* global_step / epoch carried in PTCGSTA1 headers (bindings.cu:257-262)    */
+int ptcg_trainer_set_counters(PtcgTrainer* t, int64_t global_step, int64_t epoch);
+int ptcg_trainer_get_counters(PtcgTrainer* t, int64_t* global_step, int64_t* epoch);
 /* ptcg_model_set_precision on the trainer's models (train and rollout).  */
 int ptcg_trainer_set_precision(PtcgTrainer* t, int prec);
 /* ptcg_model_set_sync_free on the trainer's models (train and rollout).   */

@@ -29,6 +29,14 @@ int ptcg_kernel_gemm(int M, int N, int K, const float* A, int64_t lda, int a_t,
                      const float* bias, const float* R, int64_t ldr, float* C2, int64_t ldc2,
                      float* workspace, int64_t workspace_floats, void* stream);
 
+/* C = alpha * op(A) op(B) + beta * R (R may not alias C), the alpha / beta
+ * form of cublasGemmExDense / puf_addmm_nn (native/src/kernels.cu:262-310)
+ * that the reference's Muon Newton-Schulz steps use (muon.cu:270-282);
+ * operand conventions as ptcg_kernel_gemm.                                 */
+int ptcg_kernel_gemm_axpby(int M, int N, int K, const float* A, int64_t lda, int a_t,
+                           const float* B, int64_t ldb, int b_t, float* C, int64_t ldc, float alpha,
+                           const float* R, int64_t ldr, float beta, void* stream);
+
 /* ptcg_kernel_gemm with bf16 products: A and B rounded to bf16 (round to
  * nearest even) on the way into LDS, v_mfma_f32_16x16x32_bf16, fp32
  * accumulation and epilogue (the reference's USE_BF16 build, pufferlib.cu

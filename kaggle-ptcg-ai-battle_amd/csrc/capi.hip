@@ -283,6 +283,9 @@ struct PtcgTrainer {
     int sync_free = 0;
     int skip_masked = 1;   // the PPO loss and the sampler mask those slots
     const float* prio = nullptr;   // policy-loss importance weights per rollout row
+    PtcgMuon* muon = nullptr;      // optimizer 1 (Muon); nullptr = Adam
+    double wd_1d = 0.0;
+    int64_t global_step = 0, epoch = 0;
     std::vector<float> st_f[5];
     std::vector<int32_t> st_i[2];
 };
@@ -291,6 +294,7 @@ extern "C" void ptcg_trainer_free(PtcgTrainer* t) {
     if (!t) return;
     if (t->model) ptcg_model_free(t->model);
     if (t->roll) ptcg_model_free(t->roll);
+    if (t->muon) ptcg_muon_free(t->muon);
     if (t->mem) (void)hipFree(t->mem);
     delete t;
 }
@@ -346,6 +350,36 @@ extern "C" int ptcg_trainer_create(const PtcgDims* dims, const PtcgHypers* hyp, 
 extern "C" int ptcg_trainer_set_hypers(PtcgTrainer* t, const PtcgHypers* hyp) {
     PT_REQUIRE(t && hyp, "set_hypers: null argument");
     t->hyp = *hyp;
+    if (t->muon) {
+        PT_TRY(ptcg_muon_set_lr(t->muon, (float)hyp->lr));
+        PT_TRY(pt_muon_set_momentum(t->muon, hyp->beta1));
+    }
+    return PTCG_OK;
+}
+
+extern "C" int ptcg_trainer_set_optimizer(PtcgTrainer* t, int kind, double wd_1d) {
+    PT_REQUIRE(t, "set_optimizer: null trainer");
+    PT_REQUIRE(kind == 0 || kind == 1, "set_optimizer: kind %d (0 Adam, 1 Muon)", kind);
+    if (t->muon) {
+        ptcg_muon_free(t->muon);
+        t->muon = nullptr;
+    }
+    t->wd_1d = wd_1d;
+    if (kind == 1) PT_TRY(ptcg_muon_create(&t->dm, t->hyp.lr, t->hyp.beta1, 0.0, wd_1d, &t->muon));
+    return PTCG_OK;
+}
+
+extern "C" int ptcg_trainer_set_counters(PtcgTrainer* t, int64_t global_step, int64_t epoch) {
+    PT_REQUIRE(t, "set_counters: null trainer");
+    t->global_step = global_step;
+    t->epoch = epoch;
+    return PTCG_OK;
+}
+
+extern "C" int ptcg_trainer_get_counters(PtcgTrainer* t, int64_t* global_step, int64_t* epoch) {
+    PT_REQUIRE(t, "get_counters: null trainer");
+    if (global_step) *global_step = t->global_step;
+    if (epoch) *epoch = t->epoch;
     return PTCG_OK;
 }
 
@@ -416,9 +450,62 @@ extern "C" int ptcg_trainer_load_weights(PtcgTrainer* t, const char* path) {
 // Adam state: "PTCGADM1" | int64 step | int64 n_params | weights | m | v (packed).
 // A separate magic from the reference's Muon state (PTCGSTA1, bindings.cu:257-293).
 struct AdmHeader { char magic[8]; int64_t step; int64_t n_params; };
+// Muon state, the reference's layout (bindings.cu:257-262): magic, global
+// step, epoch, packed count, then packed weights and packed momentum.
+struct StaHeader { char magic[8]; int64_t global_step; int64_t epoch; int64_t n_params; };
+
+static int save_state_muon(PtcgTrainer* t, const char* path) {
+    std::vector<float> w(t->packed), m(t->packed);
+    PT_TRY(arena_copy_out(t, t->P, w.data()));
+    PT_TRY(arena_copy_out(t, ptcg_muon_momentum(t->muon), m.data()));
+    StaHeader h;
+    memcpy(h.magic, "PTCGSTA1", 8);
+    h.global_step = t->global_step;
+    h.epoch = t->epoch;
+    h.n_params = t->packed;
+    std::string tmp = std::string(path) + ".tmp";
+    FILE* f = fopen(tmp.c_str(), "wb");
+    if (!f) { ptcg_set_error("Failed to open %s for writing", tmp.c_str()); return PTCG_ERR_IO; }
+    bool ok = fwrite(&h, sizeof h, 1, f) == 1 && fwrite(w.data(), 4, w.size(), f) == w.size() &&
+              fwrite(m.data(), 4, m.size(), f) == m.size();
+    ok = ok && fflush(f) == 0;
+    fclose(f);
+    if (!ok || rename(tmp.c_str(), path) != 0) {
+        ptcg_set_error("Failed to write state %s", path);
+        return PTCG_ERR_IO;
+    }
+    return PTCG_OK;
+}
+
+static int load_state_muon(PtcgTrainer* t, const char* path) {
+    FILE* f = fopen(path, "rb");
+    if (!f) { ptcg_set_error("Failed to open %s for reading", path); return PTCG_ERR_IO; }
+    StaHeader h;
+    if (fread(&h, sizeof h, 1, f) != 1 || memcmp(h.magic, "PTCGSTA1", 8) != 0) {
+        fclose(f);
+        ptcg_set_error("%s is not a PTCGSTA1 state file", path);
+        return PTCG_ERR_IO;
+    }
+    if (h.n_params != t->packed) {
+        fclose(f);
+        ptcg_set_error("State param count mismatch: file %lld, model %ld", (long long)h.n_params, t->packed);
+        return PTCG_ERR_IO;
+    }
+    std::vector<float> w(t->packed), m(t->packed);
+    const bool ok = fread(w.data(), 4, w.size(), f) == w.size() && fread(m.data(), 4, m.size(), f) == m.size();
+    fclose(f);
+    if (!ok) { ptcg_set_error("Truncated state file %s", path); return PTCG_ERR_IO; }
+    PT_TRY(arena_copy_in(t, t->P, w.data()));
+    PT_TRY(arena_copy_in(t, ptcg_muon_momentum(t->muon), m.data()));
+    PT_HIP(hipDeviceSynchronize());
+    t->global_step = h.global_step;
+    t->epoch = h.epoch;
+    return PTCG_OK;
+}
 
 extern "C" int ptcg_trainer_save_state(PtcgTrainer* t, const char* path) {
     PT_REQUIRE(t && path, "save_state: null argument");
+    if (t->muon) return save_state_muon(t, path);
     std::vector<float> w(t->packed), m(t->packed), v(t->packed);
     PT_TRY(arena_copy_out(t, t->P, w.data()));
     PT_TRY(arena_copy_out(t, t->M, m.data()));
@@ -445,6 +532,7 @@ extern "C" int ptcg_trainer_save_state(PtcgTrainer* t, const char* path) {
 
 extern "C" int ptcg_trainer_load_state(PtcgTrainer* t, const char* path) {
     PT_REQUIRE(t && path, "load_state: null argument");
+    if (t->muon) return load_state_muon(t, path);
     FILE* f = fopen(path, "rb");
     if (!f) { ptcg_set_error("Failed to open %s for reading", path); return PTCG_ERR_IO; }
     AdmHeader h;
@@ -597,8 +685,11 @@ extern "C" int ptcg_trainer_step(PtcgTrainer* t, const float* obs, const int32_t
     const PtcgHypers& h = t->hyp;
     const bool gate_on = h.kl_skip_threshold > 0.f || h.vf_skip_threshold > 0.f;
     if (gate_on) PT_TRY(pt_kl_gate(t->guard, h.kl_skip_threshold, h.vf_skip_threshold, t->gate, t->stats + 8, s));
-    PT_TRY(pt_adam_step(t->P, t->Gr, t->M, t->V, t->arena, h.lr, h.beta1, h.beta2, h.eps, h.max_grad_norm,
-                        gate_on ? t->gate : nullptr, t->step, t->stats + 9, t->adam_ws, s));
+    if (t->muon)
+        PT_TRY(ptcg_muon_step(t->muon, t->P, t->Gr, h.max_grad_norm, gate_on ? t->gate : nullptr, t->stats + 9, s));
+    else
+        PT_TRY(pt_adam_step(t->P, t->Gr, t->M, t->V, t->arena, h.lr, h.beta1, h.beta2, h.eps, h.max_grad_norm,
+                            gate_on ? t->gate : nullptr, t->step, t->stats + 9, t->adam_ws, s));
     return PTCG_OK;
 }
 

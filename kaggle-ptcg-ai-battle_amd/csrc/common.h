@@ -138,6 +138,7 @@ enum PtEpi {
     // is one multiply
     EPI_BIAS_GELU_D = 6,  // z = acc + bias[n]; C = gelu'(z); C2 = gelu(z)
     EPI_MUL = 7,          // C = acc * R[m*ldr+n]
+    EPI_AXPBY = 8,        // C = alpha * acc + beta * R[m*ldr+n] (alpha, beta in GemmArgs)
 };
 
 struct GemmArgs {
@@ -166,6 +167,8 @@ struct GemmArgs {
     // reduction; launches are sized for M and K
     const int* Mdev;
     const int* Kdev;
+    // EPI_AXPBY scalars
+    float alpha, beta;
 };
 
 // Launch C = epi(A*B) on `stream`. Requirements: K % 4 == 0 when the operand

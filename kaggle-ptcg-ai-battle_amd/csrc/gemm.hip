@@ -86,6 +86,8 @@ __device__ __forceinline__ void epi_store(const GemmArgs& g, int m, int n, float
         g.C2[(long)m * g.ldc2 + n] = gv;
     } else if (EPI == EPI_MUL) {
         g.C[(long)m * g.ldc + n] = v * g.R[(long)m * g.ldr + n];
+    } else if (EPI == EPI_AXPBY) {
+        g.C[(long)m * g.ldc + n] = g.alpha * v + g.beta * g.R[(long)m * g.ldr + n];
     } else if (EPI == EPI_ACCUM) {
         g.C[(long)m * g.ldc + n] += v;
     }
@@ -122,6 +124,8 @@ __device__ __forceinline__ void epi_store4(const GemmArgs& g, int m, int n, floa
         st_g4(g.C2 + (long)m * g.ldc2 + n, floatx4{gv[0], gv[1], gv[2], gv[3]});
     } else if (EPI == EPI_MUL) {
         st_g4(c, v * ld_v4(g.R + (long)m * g.ldr + n));
+    } else if (EPI == EPI_AXPBY) {
+        st_g4(c, g.alpha * v + g.beta * ld_v4(g.R + (long)m * g.ldr + n));
     } else if (EPI == EPI_ACCUM) {
         st_g4(c, ld_v4(c) + v);
     }
@@ -162,7 +166,7 @@ constexpr int SST = BN + 4;
 constexpr int STAGE_FLOATS = 64 * SST;
 template <int EPI> struct EpiStaged {
     static constexpr bool value = EPI == EPI_BIAS_GELU || EPI == EPI_GELU_BWD || EPI == EPI_BIAS_RESID ||
-                                  EPI == EPI_BIAS_GELU_D || EPI == EPI_MUL;
+                                  EPI == EPI_BIAS_GELU_D || EPI == EPI_MUL || EPI == EPI_AXPBY;
 };
 
 template <int EPI>
@@ -766,6 +770,7 @@ int launch_bf16_epi(const GemmArgs& g, dim3 grid, int k_chunk, long part_stride,
         case EPI_GELU_BWD: launch_bf16<AT, BT, EPI_GELU_BWD, false>(g, grid, k_chunk, 0, s); break;
         case EPI_BIAS_GELU_D: launch_bf16<AT, BT, EPI_BIAS_GELU_D, false>(g, grid, k_chunk, 0, s); break;
         case EPI_MUL: launch_bf16<AT, BT, EPI_MUL, false>(g, grid, k_chunk, 0, s); break;
+        case EPI_AXPBY: launch_bf16<AT, BT, EPI_AXPBY, false>(g, grid, k_chunk, 0, s); break;
         case EPI_ACCUM: launch_bf16<AT, BT, EPI_ACCUM, false>(g, grid, k_chunk, 0, s); break;
         default: PT_REQUIRE(false, "gemm: bad epilogue %d", g.epi);
     }
@@ -802,6 +807,7 @@ int launch_epi(const GemmArgs& g, dim3 grid, int k_chunk, hipStream_t s) {
         case EPI_GELU_BWD: launch<AT, BT, EPI_GELU_BWD, false, false, VEC>(g, grid, k_chunk, 0, s); break;
         case EPI_BIAS_GELU_D: launch<AT, BT, EPI_BIAS_GELU_D, false, false, VEC>(g, grid, k_chunk, 0, s); break;
         case EPI_MUL: launch<AT, BT, EPI_MUL, false, false, VEC>(g, grid, k_chunk, 0, s); break;
+        case EPI_AXPBY: launch<AT, BT, EPI_AXPBY, false, false, VEC>(g, grid, k_chunk, 0, s); break;
         case EPI_ACCUM: launch<AT, BT, EPI_ACCUM, false, false, VEC>(g, grid, k_chunk, 0, s); break;
         default: PT_REQUIRE(false, "gemm: bad epilogue %d", g.epi);
     }
@@ -1022,6 +1028,7 @@ int pt_gemm(const GemmArgs& g0, float* ws, long ws_floats, hipStream_t s) {
                 case EPI_GELU_BWD: hipLaunchKernelGGL(tail_reduce_kernel<EPI_GELU_BWD>, gr, dim3(256), 0, s, t, ws, s2); break;
                 case EPI_BIAS_GELU_D: hipLaunchKernelGGL(tail_reduce_kernel<EPI_BIAS_GELU_D>, gr, dim3(256), 0, s, t, ws, s2); break;
                 case EPI_MUL: hipLaunchKernelGGL(tail_reduce_kernel<EPI_MUL>, gr, dim3(256), 0, s, t, ws, s2); break;
+                case EPI_AXPBY: hipLaunchKernelGGL(tail_reduce_kernel<EPI_AXPBY>, gr, dim3(256), 0, s, t, ws, s2); break;
                 case EPI_ACCUM: hipLaunchKernelGGL(tail_reduce_kernel<EPI_ACCUM>, gr, dim3(256), 0, s, t, ws, s2); break;
                 default: PT_REQUIRE(false, "gemm: bad epilogue %d", g.epi);
             }

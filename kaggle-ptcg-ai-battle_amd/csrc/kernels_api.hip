@@ -23,6 +23,20 @@ extern "C" int ptcg_kernel_gemm(int M, int N, int K, const float* A, int64_t lda
     return pt_gemm(g, workspace, workspace_floats, (hipStream_t)stream);
 }
 
+extern "C" int ptcg_kernel_gemm_axpby(int M, int N, int K, const float* A, int64_t lda, int a_t,
+                                      const float* B, int64_t ldb, int b_t, float* C, int64_t ldc, float alpha,
+                                      const float* R, int64_t ldr, float beta, void* stream) {
+    PT_REQUIRE(A && B && C && R, "kernel_gemm_axpby: null operand");
+    GemmArgs g{};
+    g.M = M; g.N = N; g.K = K;
+    g.A = A; g.lda = lda; g.a_t = a_t;
+    g.B = B; g.ldb = ldb; g.b_t = b_t;
+    g.C = C; g.ldc = ldc; g.epi = EPI_AXPBY;
+    g.R = R; g.ldr = ldr;
+    g.alpha = alpha; g.beta = beta;
+    return pt_gemm(g, nullptr, 0, (hipStream_t)stream);
+}
+
 extern "C" int ptcg_kernel_gemm_bf16(int M, int N, int K, const float* A, int64_t lda, int a_t,
                                      const float* B, int64_t ldb, int b_t, float* C, int64_t ldc,
                                      int epi, const float* bias, const float* R, int64_t ldr, float* C2,

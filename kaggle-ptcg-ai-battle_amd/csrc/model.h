@@ -60,6 +60,8 @@ int pt_ppo_loss(const float* out, int n, int A, const float* mask, long mask_str
                 hipStream_t s);
 int pt_kl_gate(const float* guard, float kl_thr, float vf_thr, float* gate, float* skipped,
                hipStream_t s);
+struct PtcgMuon;
+int pt_muon_set_momentum(PtcgMuon* m, double momentum);
 long pt_adam_ws_floats();
 int pt_adam_step(float* w, float* g, float* m, float* v, long n, double lr, double b1, double b2,
                  double eps, float max_norm, const float* gate, int32_t* step, float* norm_out,

@@ -96,6 +96,18 @@ _SIGS = {
     "ptcg_trainer_sync": (ctypes.c_int, [c_void_p]),
     "ptcg_trainer_step_count": (ctypes.c_int, [c_void_p, c_i32_p]),
     "ptcg_trainer_set_prio": (ctypes.c_int, [c_void_p, c_void_p]),
+    "ptcg_trainer_set_optimizer": (ctypes.c_int, [c_void_p, ctypes.c_int, ctypes.c_double]),
+    "ptcg_trainer_set_counters": (ctypes.c_int, [c_void_p, ctypes.c_int64, ctypes.c_int64]),
+    "ptcg_trainer_get_counters": (ctypes.c_int, [c_void_p, ctypes.POINTER(ctypes.c_int64),
+                                                 ctypes.POINTER(ctypes.c_int64)]),
+    # Muon
+    "ptcg_muon_create": (ctypes.c_int, [ctypes.POINTER(CPtcgDims), ctypes.c_double, ctypes.c_double,
+                                        ctypes.c_double, ctypes.c_double, ctypes.POINTER(c_void_p)]),
+    "ptcg_muon_free": (None, [c_void_p]),
+    "ptcg_muon_set_lr": (ctypes.c_int, [c_void_p, ctypes.c_float]),
+    "ptcg_muon_momentum": (c_void_p, [c_void_p]),
+    "ptcg_muon_step": (ctypes.c_int, [c_void_p, c_void_p, c_void_p, ctypes.c_float, c_void_p, c_void_p,
+                                      c_void_p]),
     # rollout-side steps
     "ptcg_transpose_102": (ctypes.c_int, [c_void_p, c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                           ctypes.c_int, c_void_p]),
@@ -116,6 +128,10 @@ _SIGS = {
                                         ctypes.POINTER(ctypes.c_double)]),
     "ptcg_profile_class": (ctypes.c_int, [ctypes.c_int, ctypes.POINTER(ctypes.c_double),
                                           ctypes.POINTER(ctypes.c_int), ctypes.POINTER(ctypes.c_double)]),
+    "ptcg_kernel_gemm_axpby": (ctypes.c_int, [
+        ctypes.c_int, ctypes.c_int, ctypes.c_int, c_void_p, ctypes.c_int64, ctypes.c_int,
+        c_void_p, ctypes.c_int64, ctypes.c_int, c_void_p, ctypes.c_int64, ctypes.c_float,
+        c_void_p, ctypes.c_int64, ctypes.c_float, c_void_p]),
     "ptcg_kernel_gemm": (ctypes.c_int, [
         ctypes.c_int, ctypes.c_int, ctypes.c_int, c_void_p, ctypes.c_int64, ctypes.c_int,
         c_void_p, ctypes.c_int64, ctypes.c_int, c_void_p, ctypes.c_int64, ctypes.c_int,

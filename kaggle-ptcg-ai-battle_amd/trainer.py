@@ -45,6 +45,9 @@ TRAIN_DEFAULTS = {
     # segment rollouts (train_impl; native/train_native.py:250-270 values)
     "gamma": 1.0, "gae_lambda": 0.95, "vtrace_rho_clip": 1.0, "vtrace_c_clip": 1.0,
     "prio_alpha": 0.8, "prio_beta0": 0.2, "replay_ratio": 1.0, "total_epochs": 1,
+    # "adam" (clip + Adam) or "muon" (the reference's optimizer: momentum = beta1,
+    # decoupled weight decay muon_wd_1d on 1-D tensors)
+    "optimizer": "adam", "muon_wd_1d": 0.0,
 }
 
 
@@ -206,6 +209,11 @@ def create_pufferl(args):
         check(lib().ptcg_trainer_set_sync_free(pl._h, 1))
     if not args.get("skip_masked_options", True):
         check(lib().ptcg_trainer_set_skip_masked_options(pl._h, 0))
+    opt = pl.train_cfg["optimizer"]
+    if opt not in ("adam", "muon"):
+        raise ValueError(f"optimizer must be 'adam' or 'muon', got {opt!r}")
+    if opt == "muon":
+        check(lib().ptcg_trainer_set_optimizer(pl._h, 1, float(pl.train_cfg["muon_wd_1d"])))
     init = args.get("init_weights")
     if init is None:
         from .params import init_blob
@@ -358,11 +366,19 @@ def load_weights(pl, path):
 
 
 def save_state(pl, path):
+    """Optimizer state: the reference's PTCGSTA1 file (weights + Muon
+    momentum, global step, epoch) with the Muon optimizer, PTCGADM1 (weights,
+    Adam moments, step count) with Adam."""
+    check(lib().ptcg_trainer_set_counters(pl._h, int(getattr(pl, "global_step", 0)), int(pl.epoch)))
     check(lib().ptcg_trainer_save_state(pl._h, str(path).encode()))
 
 
 def load_state(pl, path):
     check(lib().ptcg_trainer_load_state(pl._h, str(path).encode()))
+    gs, ep = ctypes.c_int64(), ctypes.c_int64()
+    check(lib().ptcg_trainer_get_counters(pl._h, ctypes.byref(gs), ctypes.byref(ep)))
+    if pl.train_cfg["optimizer"] == "muon":
+        pl.global_step, pl.epoch = gs.value, ep.value
 
 
 def log(pl, reset=True):

@@ -154,6 +154,21 @@ def hbm_kernels(L, K):
     return out
 
 
+def muon_stats(L, K):
+    """The Muon step of the timed steps: whole-step time (event pair around
+    its launches) and its Newton-Schulz GEMMs' rate."""
+    out = {}
+    for cls, name in ((5, "step"), (6, "ns_gemm")):
+        ms, n, amt = ctypes.c_double(), ctypes.c_int(), ctypes.c_double()
+        native_check(L.ptcg_profile_class(cls, ctypes.byref(ms), ctypes.byref(n), ctypes.byref(amt)))
+        out[name + "_ms_per_step"] = round(ms.value / K, 4)
+        out[name + "_launches_per_step"] = n.value / K
+        if name == "ns_gemm" and ms.value > 0:
+            out["ns_tflops"] = round(amt.value / (ms.value / 1e3) / 1e12, 3)
+            out["ns_tflop_per_step"] = round(amt.value / K / 1e12, 5)
+    return out
+
+
 def native_check(rc):
     from ptcg_amd import native
     native.check(rc)
@@ -203,6 +218,8 @@ def main():
                     help="only run three 256 MiB device-to-device copies (the HBM counter calibration)")
     ap.add_argument("--copy-rate", action="store_true",
                     help="only time device-to-device copies of the memory-bound kernels' sizes (GB/s for scale)")
+    ap.add_argument("--optimizer", choices=("adam", "muon"), default="adam",
+                    help="optimizer of the training step (muon: the reference's, secondary line)")
     ap.add_argument("--sync-free", action="store_true",
                     help="compact row count kept on the device (no host read-back per forward)")
     args = ap.parse_args()
@@ -263,7 +280,10 @@ def main():
     obs = synth.make_obs(dm, R, seed=1)
     inp = synth.make_ppo_inputs(dm, obs, seed=2)
     static = synth.make_static(dm, 4) if dm.tables == 1 else None
-    pl = trainer.create_pufferl({"dims": dm, "train": dict(TRAIN, minibatch_size=B), "seed": 0, "static": static,
+    muon = args.optimizer == "muon"
+    # Muon with the reference trainer's settings (native/train_native.py: momentum = beta1 0.95)
+    tcfg = dict(TRAIN, minibatch_size=B, **(dict(optimizer="muon", beta1=0.95, learning_rate=0.02) if muon else {}))
+    pl = trainer.create_pufferl({"dims": dm, "train": tcfg, "seed": 0, "static": static,
                                  "precision": "bf16" if bf16 else "fp32", "sync_free": args.sync_free})
     trainer.set_rollout(pl, obs, **inp)
     n_lists = args.warmup + args.steps
@@ -332,7 +352,8 @@ def main():
                 useful_tflop_per_step=round(useful / K / 1e12, 4),
                 mean_valid_seq=round(float(np.mean(lv)), 2))
     line = {
-        "metric": METRIC if not bf16 else "PPO minibatch step obs/sec (fwd+bwd+Adam) @B=2048, bf16 GEMM products",
+        "metric": ("PPO minibatch step obs/sec (fwd+bwd+Muon) @B=512" if muon else METRIC) if not bf16
+                  else "PPO minibatch step obs/sec (fwd+bwd+Adam) @B=2048, bf16 GEMM products",
         "value": round(B * K / sec, 2), "unit": "obs/s", "n_gpus": 1,
         "steps": K, "warmup": args.warmup, "ms_per_step": round(sec * 1e3 / K, 4),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16" if bf16 else "fp32",
@@ -349,6 +370,8 @@ def main():
         "hbm_kernels": hbm_kernels(L, K),
         "losses": {k: round(v, 5) for k, v in losses.items() if isinstance(v, float)},
     }
+    if muon:
+        line["muon"] = muon_stats(L, K)
     if not args.no_cpu_baseline and not bf16:
         line["cpu_baseline"] = cpu_baseline(dm, obs, inp, B, args.cpu_seconds)
         line["gpu_over_cpu"] = round(line["value"] / line["cpu_baseline"]["value"], 1)

@@ -98,7 +98,9 @@ int ptcg_profile_end(double* total_ms, int* launches, double* flops);
  * bytes for the others:
  *   0 GEMM; 1 LayerNorm forward (8d+8 B per row + weights);
  *   2 LayerNorm backward (12d+8 B per row, +4d with a residual gradient);
- *   3 Adam norm pass (4 B per parameter); 4 Adam update (28 B per parameter). */
+ *   3 Adam norm pass (4 B per parameter); 4 Adam update (28 B per parameter);
+ *   5 whole Muon step (Newton-Schulz flops); 6 Muon's Newton-Schulz GEMM
+ *   launches (flops; not counted in class 0).                              */
 int ptcg_profile_class(int cls, double* total_ms, int* launches, double* amount);
 
 #ifdef __cplusplus

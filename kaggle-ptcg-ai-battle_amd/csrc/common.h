@@ -52,9 +52,12 @@ static inline int pt_cdiv(long a, long b) { return (int)((a + b - 1) / b); }
 // records the end event with the launch's class and algorithmic amount
 // (flops for GEMMs, HBM bytes for the others).
 enum PtProfClass { PROF_GEMM = 0, PROF_LN_FWD = 1, PROF_LN_BWD = 2, PROF_ADAM_NORM = 3, PROF_ADAM_UPDATE = 4,
-                   PROF_NCLASS = 5 };
+                   PROF_MUON = 5, PROF_MUON_GEMM = 6, PROF_NCLASS = 7 };
 int pt_prof_open(hipStream_t s);
 void pt_prof_close(int slot, int cls, double amount, hipStream_t s);
+// class recorded for GEMM launches (PROF_GEMM unless a caller such as the
+// Muon step files its products separately); returns the previous class
+int pt_prof_gemm_class(int cls);
 
 // ---------------------------------------------------------------- device math
 // Exact (erf) GELU, torch nn.GELU() default; the reference's pt_gelu_fwd/bwd
@@ -176,6 +179,25 @@ struct GemmArgs {
 // dims multiples of 4, 16 B-aligned bases.  Weight-gradient shapes
 // (large K, small M*N) are split over K with a deterministic reduction.
 int pt_gemm(const GemmArgs& g, float* splitk_ws, long splitk_ws_floats, hipStream_t s);
+
+// One product of a grouped launch (pt_gemm_grouped): all products of a
+// launch share the operand layout (a_t, b_t) and epilogue, and must meet the
+// LDS-DMA tile rules (16 B-aligned operands, leading dimensions multiples of
+// 4, K a multiple of 16 for k-contiguous operands).  Split-K products write
+// `splits` partials of M x ldc at g.C (part_stride apart) and
+// pt_grouped_reduce sums them into out.
+struct GroupedGemm {
+    GemmArgs g;
+    int k_chunk, splits, tiles, first;   // first = the product's first work item
+    long part_stride;
+    float* out;
+};
+// items = sum of tiles * splits; item_group[w] = product of work item w
+// flops: the launch's products (2 M N K summed; for launch timing only)
+int pt_gemm_grouped(const GroupedGemm* d_groups, const int* d_item_group, int items, int a_t, int b_t, int epi,
+                    int partial, double flops, hipStream_t s);
+int pt_grouped_reduce(const GroupedGemm* d_groups, const int* d_chunk_group, const int* d_chunk_first, int chunks,
+                      hipStream_t s);
 
 // Linear helpers on row-major activations X (rows, in) and W (out, in)
 int pt_linear_fwd(const float* X, const float* W, const float* b, float* Y, int rows,

@@ -53,9 +53,8 @@ __device__ __forceinline__ GemmArgs gemm_shape(const GemmArgs& g0) {
 // 8 XCDs, so XCD x gets the contiguous logical range starting at
 // x*q + min(x, r) (count = 8q + r) — every XCD gets work and keeps its A rows
 // in its own L2.  Returns false for blocks beyond the count.
-__device__ __forceinline__ bool tile_of_range(const GemmArgs& g, int tn, int& tm_i, int& tn_i) {
+__device__ __forceinline__ bool tile_of_range(const GemmArgs& g, int tn, int& tm_i, int& tn_i, int b) {
     const int count = g.ntiles ? g.ntiles : ((g.M + BM - 1) / BM) * tn;
-    const int b = blockIdx.x;
     if (b >= count) return false;
     const int q = count >> 3, r = count & 7, x = b & 7;
     const int lb = g.tile0 + x * q + min(x, r) + (b >> 3);
@@ -205,19 +204,19 @@ __device__ __forceinline__ void epilogue_staged(const GemmArgs& g, floatx4 (&acc
 // stage: STAGE_FLOATS of LDS the main loop no longer uses.
 template <int EPI, bool PARTIAL>
 __device__ __forceinline__ void gemm_epilogue(const GemmArgs& g, floatx4 (&acc)[4][4], int m0, int n0, int wm,
-                                              int wn, int li, int lq, long part_stride, float* stage) {
+                                              int wn, int li, int lq, long part_stride, float* stage, int bz) {
     if (PARTIAL && g.tail_part) {
         // tile-local partial [split][tile - tile0][BM][BN] (no bounds: the reduce masks)
         const int tn = (g.N + BN - 1) / BN;
         const long t = (long)(m0 / BM) * tn + n0 / BN - g.tile0;
-        float* P = g.C + ((long)blockIdx.z * g.ntiles + t) * (BM * BN);
+        float* P = g.C + ((long)bz * g.ntiles + t) * (BM * BN);
 #pragma unroll
         for (int ti = 0; ti < 4; ++ti)
 #pragma unroll
             for (int tj = 0; tj < 4; ++tj) st_g4(P + (wm + ti * 16 + li) * BN + wn + tj * 16 + 4 * lq, acc[ti][tj]);
         return;
     }
-    const long zoff = PARTIAL ? (long)blockIdx.z * part_stride : 0;
+    const long zoff = PARTIAL ? (long)bz * part_stride : 0;
     const uintptr_t al = PARTIAL ? (uintptr_t)g.C | (uintptr_t)(g.ldc * 4)
                                  : (uintptr_t)g.C | (uintptr_t)g.C2 | (uintptr_t)g.R | (uintptr_t)g.bias |
                                        (uintptr_t)((g.ldc | g.ldc2 | g.ldr) * 4);
@@ -266,7 +265,7 @@ __global__ __launch_bounds__(NT) void gemm_f32_kernel(const GemmArgs g0, int k_c
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int tn = (g.N + BN - 1) / BN;
     int tmi, tni;
-    if (!tile_of_range(g, tn, tmi, tni)) return;   // beyond the (device) tile count
+    if (!tile_of_range(g, tn, tmi, tni, blockIdx.x)) return;   // beyond the (device) tile count
     const int m0 = tmi * BM, n0 = tni * BN;
     const int kbeg = blockIdx.z * k_chunk;
     const int kend = min(g.K, kbeg + k_chunk);
@@ -366,7 +365,7 @@ __global__ __launch_bounds__(NT) void gemm_f32_kernel(const GemmArgs g0, int k_c
         }
     }
 
-    gemm_epilogue<EPI, PARTIAL>(g, acc, m0, n0, wm, wn, li, lq, part_stride, smem);
+    gemm_epilogue<EPI, PARTIAL>(g, acc, m0, n0, wm, wn, li, lq, part_stride, smem, blockIdx.z);
 }
 
 
@@ -386,10 +385,12 @@ typedef int int32x4_t __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ int32x4_t buffer_rsrc(const float* p, unsigned bytes) {
     const unsigned long long a = (unsigned long long)p;
+    // uniform by construction; readfirstlane makes that explicit for operands
+    // loaded from memory (the grouped launch's descriptors)
     int32x4_t r;
-    r.x = (int)(unsigned)(a & 0xffffffffull);
-    r.y = (int)(unsigned)(a >> 32);   // stride 0 (canonical addresses are below 2^48)
-    r.z = (int)bytes;                 // num_records: bytes from the base
+    r.x = __builtin_amdgcn_readfirstlane((int)(unsigned)(a & 0xffffffffull));
+    r.y = __builtin_amdgcn_readfirstlane((int)(unsigned)(a >> 32));   // stride 0 (addresses are below 2^48)
+    r.z = __builtin_amdgcn_readfirstlane((int)bytes);                 // num_records: bytes from the base
     r.w = 0x00020000;                 // gfx9 raw buffer: 32-bit data format, no swizzle
     return r;
 }
@@ -426,20 +427,23 @@ template <bool T> __device__ __forceinline__ int dma_src(int c, int lane, int r0
     return (int)(k * ld) + r0 + 4 * (gq ^ (k & 4));
 }
 
+// One 128 x 128 tile of C (split bz of gz along K) of the logical tile
+// index bx; shared by the per-product launch and the grouped launch.
 template <bool AT, bool BT, int EPI, bool PARTIAL, bool DB>
-__global__ __launch_bounds__(NT) void gemm_f32_dma_kernel(const GemmArgs g0, int k_chunk0, long part_stride) {
+__device__ __forceinline__ void gemm_dma_tile(const GemmArgs& g0, int k_chunk0, long part_stride, int bx, int bz,
+                                              int gz) {
     const GemmArgs g = gemm_shape(g0);
     // a device reduction count splits its own K evenly over the launch's splits
-    const int k_chunk = g0.Kdev ? (((g.K + (int)gridDim.z - 1) / (int)gridDim.z + BK - 1) / BK) * BK : k_chunk0;
+    const int k_chunk = g0.Kdev ? (((g.K + gz - 1) / gz + BK - 1) / BK) * BK : k_chunk0;
     constexpr int TILE = BM * BK;   // floats per operand tile (BM == BN)
     constexpr int SMEM = DMA_NS * 2 * TILE > STAGE_FLOATS ? DMA_NS * 2 * TILE : STAGE_FLOATS;
     __shared__ __align__(16) float smem[SMEM];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int tn = (g.N + BN - 1) / BN;
     int tmi, tni;
-    if (!tile_of_range(g, tn, tmi, tni)) return;   // beyond the tile count
+    if (!tile_of_range(g, tn, tmi, tni, bx)) return;   // beyond the tile count
     const int m0 = tmi * BM, n0 = tni * BN;
-    const int kbeg = blockIdx.z * k_chunk;
+    const int kbeg = bz * k_chunk;
     const int kend = min(g.K, kbeg + k_chunk);
     const int nk = kend > kbeg ? (kend - kbeg + BK - 1) / BK : 0;
     const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
@@ -518,12 +522,56 @@ __global__ __launch_bounds__(NT) void gemm_f32_dma_kernel(const GemmArgs g0, int
         const int m = m0 + tid;
         if (tid < 128 && m < g.M) {
             const float v = sh[tid] + sh[tid + 128];
-            if (PARTIAL) g.C[(long)gridDim.z * part_stride + (long)blockIdx.z * g.M + m] = v;
+            if (PARTIAL) g.C[(long)gz * part_stride + (long)bz * g.M + m] = v;
             else g.dbias[m] = v;
         }
     }
 
-    gemm_epilogue<EPI, PARTIAL>(g, acc, m0, n0, wm, wn, li, lq, part_stride, smem);
+    gemm_epilogue<EPI, PARTIAL>(g, acc, m0, n0, wm, wn, li, lq, part_stride, smem, bz);
+}
+
+template <bool AT, bool BT, int EPI, bool PARTIAL, bool DB>
+__global__ __launch_bounds__(NT) void gemm_f32_dma_kernel(const GemmArgs g0, int k_chunk0, long part_stride) {
+    gemm_dma_tile<AT, BT, EPI, PARTIAL, DB>(g0, k_chunk0, part_stride, blockIdx.x, blockIdx.z, gridDim.z);
+}
+
+// Grouped launch: several independent products (different shapes and
+// operands, one layout and epilogue) in one grid.  Work item w belongs to
+// product item_group[w]; its logical tile and K split follow from the
+// product's first item, tile count and split count.
+template <bool AT, bool BT, int EPI, bool PARTIAL>
+__global__ __launch_bounds__(NT) void gemm_f32_dma_grouped_kernel(const GroupedGemm* __restrict__ gs,
+                                                                  const int* __restrict__ item_group) {
+    const int gi = __builtin_amdgcn_readfirstlane(item_group[blockIdx.x]);
+    const int local = (int)blockIdx.x - gs[gi].first;
+    const int tiles = gs[gi].tiles;
+    gemm_dma_tile<AT, BT, EPI, PARTIAL, false>(gs[gi].g, gs[gi].k_chunk, gs[gi].part_stride, local % tiles,
+                                               local / tiles, gs[gi].splits);
+}
+
+// Fixed-order sums of grouped split-K partials: chunk c covers 1024
+// elements of product chunk_group[c]'s C (row-major M x N at ldc; partial z
+// at g.C + z * part_stride, the sum goes to out).
+__global__ __launch_bounds__(256) void grouped_reduce_kernel(const GroupedGemm* __restrict__ gs,
+                                                             const int* __restrict__ chunk_group,
+                                                             const int* __restrict__ chunk_first) {
+    const int gi = chunk_group[blockIdx.x];
+    const GemmArgs& g = gs[gi].g;
+    float* out = gs[gi].out;
+    const int splits = gs[gi].splits;
+    const long ps = gs[gi].part_stride;
+    const long base = (long)((int)blockIdx.x - chunk_first[gi]) * 1024;
+    const long total = (long)g.M * g.N;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const long e = base + k * 256 + threadIdx.x;
+        if (e >= total) break;
+        const long m = e / g.N, n = e % g.N;
+        const long o = m * g.ldc + n;
+        float v = g.C[o];
+        for (int z = 1; z < splits; ++z) v += g.C[z * ps + o];
+        out[o] = v;
+    }
 }
 
 // ---------------------------------------------------------------- bf16
@@ -594,7 +642,7 @@ __global__ __launch_bounds__(NT) void gemm_bf16_kernel(const GemmArgs g0, int k_
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int tn = (g.N + BN - 1) / BN;
     int tmi, tni;
-    if (!tile_of_range(g, tn, tmi, tni)) return;   // beyond the (device) tile count
+    if (!tile_of_range(g, tn, tmi, tni, blockIdx.x)) return;   // beyond the (device) tile count
     const int m0 = tmi * BM, n0 = tni * BN;
     const int kbeg = blockIdx.z * k_chunk;
     const int kend = min(g.K, kbeg + k_chunk);
@@ -640,7 +688,7 @@ __global__ __launch_bounds__(NT) void gemm_bf16_kernel(const GemmArgs g0, int k_
             buf ^= 1;
         }
     }
-    gemm_epilogue<EPI, PARTIAL>(g, acc, m0, n0, wm, wn, li, lq, part_stride, smem);
+    gemm_epilogue<EPI, PARTIAL>(g, acc, m0, n0, wm, wn, li, lq, part_stride, smem, blockIdx.z);
 }
 
 // out[m][n] (=|+=) sum_s part[s][m][n], fixed order over s
@@ -727,6 +775,7 @@ struct LaunchProf {
     int sum_n[PROF_NCLASS] = {};
 };
 LaunchProf g_prof;
+int g_gemm_class = PROF_GEMM;
 
 // products a launch executes: its share of the tiles, over the whole of K
 // (split-K launches cover K across grid.z)
@@ -746,14 +795,14 @@ void launch(const GemmArgs& g, dim3 grid, int k_chunk, long part_stride, hipStre
     else
         hipLaunchKernelGGL((gemm_f32_kernel<AT, BT, EPI, PARTIAL, DB, VEC>), grid, dim3(NT), 0, s, g, k_chunk,
                            part_stride);
-    pt_prof_close(slot, PROF_GEMM, launch_flops(g), s);
+    pt_prof_close(slot, g_gemm_class, launch_flops(g), s);
 }
 
 template <bool AT, bool BT, int EPI, bool PARTIAL>
 void launch_bf16(const GemmArgs& g, dim3 grid, int k_chunk, long part_stride, hipStream_t s) {
     const int slot = pt_prof_open(s);
     hipLaunchKernelGGL((gemm_bf16_kernel<AT, BT, EPI, PARTIAL>), grid, dim3(NT), 0, s, g, k_chunk, part_stride);
-    pt_prof_close(slot, PROF_GEMM, launch_flops(g), s);
+    pt_prof_close(slot, g_gemm_class, launch_flops(g), s);
 }
 
 template <bool AT, bool BT>
@@ -829,6 +878,12 @@ int launch_full(const GemmArgs& g, bool db, dim3 grid, int k_chunk, hipStream_t 
 }
 
 }  // namespace
+
+int pt_prof_gemm_class(int cls) {
+    const int prev = g_gemm_class;
+    g_gemm_class = cls;
+    return prev;
+}
 
 int pt_prof_open(hipStream_t s) {
     if (!g_prof.on || g_prof.used * 2 + 1 >= (int)g_prof.ev.size()) return -1;
@@ -1038,6 +1093,45 @@ int pt_gemm(const GemmArgs& g0, float* ws, long ws_floats, hipStream_t s) {
     }
     if (bf) PT_TRY(launch_bf16_any(g, grid, k_chunk, 0, false, s));
     else PT_TRY(vec ? launch_full<true>(g, db, grid, k_chunk, s) : launch_full<false>(g, db, grid, k_chunk, s));
+    PT_LAUNCH_CHECK();
+    return PTCG_OK;
+}
+
+namespace {
+template <bool AT, bool BT>
+int launch_grouped(const GroupedGemm* d, const int* ig, int items, int epi, int partial, hipStream_t s) {
+    const dim3 grid(items), blk(NT);
+    if (partial && epi == EPI_STORE)
+        hipLaunchKernelGGL((gemm_f32_dma_grouped_kernel<AT, BT, EPI_STORE, true>), grid, blk, 0, s, d, ig);
+    else if (!partial && epi == EPI_STORE)
+        hipLaunchKernelGGL((gemm_f32_dma_grouped_kernel<AT, BT, EPI_STORE, false>), grid, blk, 0, s, d, ig);
+    else if (!partial && epi == EPI_AXPBY)
+        hipLaunchKernelGGL((gemm_f32_dma_grouped_kernel<AT, BT, EPI_AXPBY, false>), grid, blk, 0, s, d, ig);
+    else
+        PT_REQUIRE(false, "gemm_grouped: epilogue %d (partial %d) not supported", epi, partial);
+    PT_LAUNCH_CHECK();
+    return PTCG_OK;
+}
+}  // namespace
+
+int pt_gemm_grouped(const GroupedGemm* d_groups, const int* d_item_group, int items, int a_t, int b_t, int epi,
+                    int partial, double flops, hipStream_t s) {
+    PT_REQUIRE(d_groups && d_item_group && items > 0, "gemm_grouped: empty launch");
+    const int code = (a_t ? 2 : 0) + (b_t ? 1 : 0);
+    const int slot = pt_prof_open(s);
+    int r;
+    if (code == 0) r = launch_grouped<false, false>(d_groups, d_item_group, items, epi, partial, s);
+    else if (code == 1) r = launch_grouped<false, true>(d_groups, d_item_group, items, epi, partial, s);
+    else if (code == 2) r = launch_grouped<true, false>(d_groups, d_item_group, items, epi, partial, s);
+    else r = launch_grouped<true, true>(d_groups, d_item_group, items, epi, partial, s);
+    pt_prof_close(slot, g_gemm_class, flops, s);
+    return r;
+}
+
+int pt_grouped_reduce(const GroupedGemm* d_groups, const int* d_chunk_group, const int* d_chunk_first, int chunks,
+                      hipStream_t s) {
+    PT_REQUIRE(d_groups && d_chunk_group && d_chunk_first && chunks > 0, "grouped_reduce: empty launch");
+    hipLaunchKernelGGL(grouped_reduce_kernel, dim3(chunks), dim3(256), 0, s, d_groups, d_chunk_group, d_chunk_first);
     PT_LAUNCH_CHECK();
     return PTCG_OK;
 }

@@ -8,6 +8,14 @@ rollout resident in HBM.  Model: 96 entity tokens (+READOUT), 32 numeric
 token features, card ids in [0, 2048), d 256 / 4 heads / FFN 1024 / 4 pre-LN
 layers, 64 masked options, blind value head, fp32 throughout.
 
+The step is captured once in a HIP graph (sync-free compact layout) and
+replayed per minibatch with the minibatch's row indices written into the
+captured index buffer, as the reference's trainer replays its captured train
+graph; `value` is the throughput of those replays.  The same number of
+minibatches then runs launched kernel by kernel with a HIP event pair around
+every GEMM / LayerNorm / Adam launch (`stream_launch`), and the kernels'
+rooflines come from that pass (`--stream` times only the latter).
+
 Prints one JSON line (see the keys below), including the GEMM kernel's
 roofline (useful flops over measured kernel time, HIP events on the launch
 stream) and the host-CPU baseline (the oracle: PyTorch CPU restatement of
@@ -220,6 +228,9 @@ def main():
                     help="only time device-to-device copies of the memory-bound kernels' sizes (GB/s for scale)")
     ap.add_argument("--optimizer", choices=("adam", "muon"), default="adam",
                     help="optimizer of the training step (muon: the reference's, secondary line)")
+    ap.add_argument("--stream", action="store_true",
+                    help="time stream launches only (default for the training step: HIP graph replay for the "
+                         "value, then a stream-launched pass for the kernel rooflines)")
     ap.add_argument("--sync-free", action="store_true",
                     help="compact row count kept on the device (no host read-back per forward)")
     args = ap.parse_args()
@@ -283,8 +294,10 @@ def main():
     muon = args.optimizer == "muon"
     # Muon with the reference trainer's settings (native/train_native.py: momentum = beta1 0.95)
     tcfg = dict(TRAIN, minibatch_size=B, **(dict(optimizer="muon", beta1=0.95, learning_rate=0.02) if muon else {}))
+    # graph replay for the CORE training step (needs the sync-free step)
+    graph = args.workload == "train" and not args.stream
     pl = trainer.create_pufferl({"dims": dm, "train": tcfg, "seed": 0, "static": static,
-                                 "precision": "bf16" if bf16 else "fp32", "sync_free": args.sync_free})
+                                 "precision": "bf16" if bf16 else "fp32", "sync_free": args.sync_free or graph})
     trainer.set_rollout(pl, obs, **inp)
     n_lists = args.warmup + args.steps
     lists = synth.minibatch_indices(R, B, n_lists, seed=3)
@@ -295,6 +308,25 @@ def main():
         pl.step(r["obs"], d_lists[i], r)
     torch.cuda.synchronize()
     L = native.lib()
+    K = args.steps
+    sec_graph = None
+    if graph:
+        # timed region 1 (`value`): the step captured once in a HIP graph over a
+        # fixed index buffer, refreshed and replayed per minibatch -- the
+        # reference trainer's launch mode (pufferlib.cu:2019-2140)
+        idx_buf = torch.empty(B, dtype=torch.int32, device="cuda")
+        idx_buf.copy_(d_lists[0])
+        torch.cuda.synchronize()
+        pl.capture_step(r["obs"], idx_buf, r)
+        t0 = time.perf_counter()
+        for i in range(args.warmup, n_lists):
+            idx_buf.copy_(d_lists[i])
+            pl.replay_step()
+        torch.cuda.synchronize()
+        sec_graph = time.perf_counter() - t0
+    # timed region 2 (the only one with --stream): the same minibatches launched
+    # kernel by kernel, a HIP event pair on the launch stream around every GEMM,
+    # LayerNorm and Adam launch -- the kernels' rooflines
     native.check(L.ptcg_profile_begin(256 * args.steps))
     t0 = time.perf_counter()
     for i in range(args.warmup, n_lists):
@@ -307,8 +339,8 @@ def main():
     if not np.isfinite(losses["total_loss"]):
         raise RuntimeError(f"non-finite loss during the benchmark: {losses}")
 
-    K = args.steps
-    sec = t1 - t0
+    sec_stream = t1 - t0
+    sec = sec_graph if graph else sec_stream
     if args.workload == "frozen":
         line = {
             "metric": "PPO minibatch step obs/sec (fwd+bwd+Adam), reference model variant @B=512",
@@ -365,11 +397,17 @@ def main():
                                   "master weights and Adam state" if bf16 else ""),
                    "minibatch": B, "rollout_rows": R, "seq_len": dm.l_tok + 1,
                    "parallelism": "single GPU",
-                   "compact_rows": "device count, no host read-back" if args.sync_free else "host read-back"},
+                   "compact_rows": "device count, no host read-back" if (args.sync_free or graph)
+                   else "host read-back",
+                   "launch": "HIP graph replay (step captured once)" if graph else "stream"},
         "roofline": roof,
         "hbm_kernels": hbm_kernels(L, K),
         "losses": {k: round(v, 5) for k, v in losses.items() if isinstance(v, float)},
     }
+    if graph:
+        line["stream_launch"] = dict(value=round(B * K / sec_stream, 2), ms_per_step=round(sec_stream * 1e3 / K, 4),
+                                     note="the same minibatches launched kernel by kernel with HIP event pairs; "
+                                          "roofline and hbm_kernels come from this pass")
     if muon:
         line["muon"] = muon_stats(L, K)
     if not args.no_cpu_baseline and not bf16:

@@ -304,6 +304,17 @@ int ptcg_trainer_step(PtcgTrainer* t, const float* obs, const int32_t* row_idx,
  * like the other per-row inputs (e.g. ptcg_prio_replay's row_prio), used by
  * every later step until replaced; NULL = weight 1 (the default).          */
 int ptcg_trainer_set_prio(PtcgTrainer* t, const float* prio);
+/* Graph capture of the training step (the reference's captured train
+ * graph, pufferlib.cu:2019-2140): capture_step records one
+ * ptcg_trainer_step over the given device buffers into a HIP graph (sync-free
+ * mode only: every node is a kernel; nothing runs during capture);
+ * replay_step launches it on `stream`.  The buffers' addresses are baked
+ * in: write each minibatch's indices / inputs into the same buffers before
+ * a replay.  Re-capturing replaces the graph.                              */
+int ptcg_trainer_capture_step(PtcgTrainer* t, const float* obs, const int32_t* row_idx,
+                              const float* actions, const float* old_logprobs,
+                              const float* advantages, const float* returns, const float* values);
+int ptcg_trainer_replay_step(PtcgTrainer* t, void* stream);
 /* The same step without the optimizer (grads left in the grads arena).    */
 int ptcg_trainer_forward_backward(PtcgTrainer* t, const float* obs, const int32_t* row_idx,
                                   const float* actions, const float* old_logprobs,

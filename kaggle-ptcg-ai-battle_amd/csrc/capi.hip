@@ -284,6 +284,10 @@ struct PtcgTrainer {
     int skip_masked = 1;   // the PPO loss and the sampler mask those slots
     const float* prio = nullptr;   // policy-loss importance weights per rollout row
     PtcgMuon* muon = nullptr;      // optimizer 1 (Muon); nullptr = Adam
+    // captured training step (sync-free mode): graph over fixed buffers
+    hipStream_t cap_stream = nullptr;
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t graph_exec = nullptr;
     double wd_1d = 0.0;
     int64_t global_step = 0, epoch = 0;
     std::vector<float> st_f[5];
@@ -295,6 +299,9 @@ extern "C" void ptcg_trainer_free(PtcgTrainer* t) {
     if (t->model) ptcg_model_free(t->model);
     if (t->roll) ptcg_model_free(t->roll);
     if (t->muon) ptcg_muon_free(t->muon);
+    if (t->graph_exec) (void)hipGraphExecDestroy(t->graph_exec);
+    if (t->graph) (void)hipGraphDestroy(t->graph);
+    if (t->cap_stream) (void)hipStreamDestroy(t->cap_stream);
     if (t->mem) (void)hipFree(t->mem);
     delete t;
 }
@@ -690,6 +697,47 @@ extern "C" int ptcg_trainer_step(PtcgTrainer* t, const float* obs, const int32_t
     else
         PT_TRY(pt_adam_step(t->P, t->Gr, t->M, t->V, t->arena, h.lr, h.beta1, h.beta2, h.eps, h.max_grad_norm,
                             gate_on ? t->gate : nullptr, t->step, t->stats + 9, t->adam_ws, s));
+    return PTCG_OK;
+}
+
+// The reference captures its training step in a CUDA graph after warmup and
+// replays it per minibatch over fixed buffers (pufferlib.cu:2019-2140); the
+// same here with a HIP graph over the sync-free step (no host read-back, so
+// every node is a kernel).  Pointers are baked in: the caller rewrites the
+// contents of row_idx (and the per-row arrays) between replays.
+extern "C" int ptcg_trainer_capture_step(PtcgTrainer* t, const float* obs, const int32_t* row_idx,
+                                         const float* actions, const float* old_logprobs,
+                                         const float* advantages, const float* returns, const float* values) {
+    PT_REQUIRE(t, "capture_step: null trainer");
+    PT_REQUIRE(t->sync_free, "capture_step: needs sync-free mode (ptcg_trainer_set_sync_free)");
+    if (t->graph_exec) {
+        PT_HIP(hipGraphExecDestroy(t->graph_exec));
+        t->graph_exec = nullptr;
+    }
+    if (t->graph) {
+        PT_HIP(hipGraphDestroy(t->graph));
+        t->graph = nullptr;
+    }
+    if (!t->cap_stream) PT_HIP(hipStreamCreateWithFlags(&t->cap_stream, hipStreamNonBlocking));
+    PT_HIP(hipDeviceSynchronize());
+    PT_HIP(hipStreamBeginCapture(t->cap_stream, hipStreamCaptureModeThreadLocal));
+    const int r = ptcg_trainer_step(t, obs, row_idx, actions, old_logprobs, advantages, returns, values,
+                                    t->cap_stream);
+    hipGraph_t g = nullptr;
+    const hipError_t e = hipStreamEndCapture(t->cap_stream, &g);
+    if (r != PTCG_OK) {
+        if (g) (void)hipGraphDestroy(g);
+        return r;
+    }
+    PT_HIP(e);
+    t->graph = g;
+    PT_HIP(hipGraphInstantiateWithFlags(&t->graph_exec, t->graph, 0));
+    return PTCG_OK;
+}
+
+extern "C" int ptcg_trainer_replay_step(PtcgTrainer* t, void* stream) {
+    PT_REQUIRE(t && t->graph_exec, "replay_step: no captured step (ptcg_trainer_capture_step)");
+    PT_HIP(hipGraphLaunch(t->graph_exec, (hipStream_t)stream));
     return PTCG_OK;
 }
 

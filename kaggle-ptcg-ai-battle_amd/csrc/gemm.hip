@@ -885,8 +885,15 @@ int pt_prof_gemm_class(int cls) {
     return prev;
 }
 
+// launches being captured into a graph are not timed (an event record would
+// become a capture dependency, not a timestamp)
+static bool prof_capturing(hipStream_t s) {
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    return s != nullptr && hipStreamIsCapturing(s, &st) == hipSuccess && st != hipStreamCaptureStatusNone;
+}
+
 int pt_prof_open(hipStream_t s) {
-    if (!g_prof.on || g_prof.used * 2 + 1 >= (int)g_prof.ev.size()) return -1;
+    if (!g_prof.on || g_prof.used * 2 + 1 >= (int)g_prof.ev.size() || prof_capturing(s)) return -1;
     (void)hipEventRecord(g_prof.ev[2 * g_prof.used], s);
     return g_prof.used++;
 }

@@ -175,6 +175,17 @@ class PuffeRL:
             inp["advantages"].data_ptr(), inp["returns"].data_ptr(),
             inp["values"].data_ptr(), stream))
 
+    def capture_step(self, obs, idx, inp):
+        """Capture one step over these device buffers into a HIP graph
+        (sync-free mode); rewrite the buffers' contents, then replay_step."""
+        check(lib().ptcg_trainer_capture_step(
+            self._h, obs.data_ptr(), idx.data_ptr() if idx is not None else None,
+            inp["actions"].data_ptr(), inp["logprobs"].data_ptr(), inp["advantages"].data_ptr(),
+            inp["returns"].data_ptr(), inp["values"].data_ptr()))
+
+    def replay_step(self, stream=None):
+        check(lib().ptcg_trainer_replay_step(self._h, stream))
+
     def close(self):
         if getattr(self, "_h", None) is not None and self._h.value:
             lib().ptcg_trainer_free(self._h)

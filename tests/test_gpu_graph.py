@@ -1,0 +1,68 @@
+"""The training step captured in a HIP graph (sync-free mode) and replayed
+per minibatch, as the reference replays its captured train graph
+(pufferlib.cu:2019-2140): every replay, with the minibatch's indices
+rewritten into the captured index buffer and eager work and host
+synchronisations in between, must give the weights and loss statistics the
+eager step gives.  Tolerance: embedding-scatter atomics may reorder fp32
+sums (1e-7), and Adam's early steps are lr * sign(g) for elements whose
+gradient is that noise, so weights agree at relative L2 1e-5 with every
+element within 2 lr per step."""
+import numpy as np
+import pytest
+import torch
+
+from conftest import rel_l2
+from ptcg_amd import dims, synth, trainer
+import oracle.model as om
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("opt", ["adam", "muon"])
+@pytest.mark.parametrize("dm", [dims.tiny(), dims.CORE], ids=["tiny", "core"])
+def test_graph_replays_match_eager_steps(dm, opt, cuda):
+    B = 32 if dm.l_tok < 32 else 64
+    blob = om.build(dm, seed=81).to_blob()
+    rows = synth.make_obs(dm, 4 * B, seed=82, rich=dm.l_tok < 32)
+    inp = synth.make_ppo_inputs(dm, rows, seed=83)
+    lists = synth.minibatch_indices(4 * B, B, 5, seed=84, epochs=2)
+    cfg = {"dims": dm, "init_weights": blob, "sync_free": True,
+           "train": dict(minibatch_size=B, learning_rate=1e-3, max_grad_norm=0.5, optimizer=opt)}
+    eager, graph = trainer.create_pufferl(cfg), trainer.create_pufferl(cfg)
+    try:
+        trainer.set_rollout(eager, rows, **inp)
+        trainer.set_rollout(graph, rows, **inp)
+        r = graph.rollout
+        idx_buf = torch.empty(B, dtype=torch.int32, device="cuda")
+        idx_buf.copy_(torch.from_numpy(np.asarray(lists[0], np.int32)))
+        torch.cuda.synchronize()
+        graph.capture_step(r["obs"], idx_buf, r)
+        for i, ix in enumerate(lists):
+            ix = np.asarray(ix, np.int32)
+            idx_buf.copy_(torch.from_numpy(ix).to("cuda"))
+            graph.replay_step()
+            eager.step(eager.rollout["obs"], eager.to_device(ix, np.int32), eager.rollout)
+            torch.cuda.synchronize()
+            # eager work and host synchronisation between replays
+            lg_e, lg_g = trainer.log(eager), trainer.log(graph)
+            for k in ("policy_loss", "value_loss", "entropy", "total_loss"):
+                assert abs(lg_g[k] - lg_e[k]) <= 1e-5 * max(1.0, abs(lg_e[k])), (i, k)
+            w_e, w_g = eager.get_weights(), graph.get_weights()
+            assert rel_l2(w_g, w_e) < 1e-5, i
+            assert np.abs(w_g - w_e).max() <= 2 * 1e-3 * (i + 1) + 1e-6, i
+            assert not np.array_equal(w_g, blob)
+    finally:
+        eager.close()
+        graph.close()
+
+
+def test_capture_needs_sync_free(cuda):
+    dm, B = dims.tiny(), 32
+    pl = trainer.create_pufferl({"dims": dm, "train": dict(minibatch_size=B)})
+    try:
+        rows = synth.make_obs(dm, B, seed=1, rich=True)
+        trainer.set_rollout(pl, rows, **synth.make_ppo_inputs(dm, rows, seed=2))
+        with pytest.raises(RuntimeError, match="sync-free"):
+            pl.capture_step(pl.rollout["obs"], None, pl.rollout)
+    finally:
+        pl.close()

@@ -324,9 +324,14 @@ def main():
             pl.replay_step()
         torch.cuda.synchronize()
         sec_graph = time.perf_counter() - t0
-    # timed region 2 (the only one with --stream): the same minibatches launched
-    # kernel by kernel, a HIP event pair on the launch stream around every GEMM,
-    # LayerNorm and Adam launch -- the kernels' rooflines
+    # timed region 2 (the only one with --stream): the same number of
+    # minibatches launched kernel by kernel, a HIP event pair on the launch
+    # stream around every GEMM, LayerNorm and Adam launch -- the kernels'
+    # rooflines.  Host row counts here, so every launch is sized exactly and
+    # its algorithmic amount is the work it does (a sync-free launch covers
+    # all N * l_seq rows and stops at the device count).
+    if graph and not args.sync_free:
+        native.check(L.ptcg_trainer_set_sync_free(pl._h, 0))
     native.check(L.ptcg_profile_begin(256 * args.steps))
     t0 = time.perf_counter()
     for i in range(args.warmup, n_lists):
@@ -406,8 +411,9 @@ def main():
     }
     if graph:
         line["stream_launch"] = dict(value=round(B * K / sec_stream, 2), ms_per_step=round(sec_stream * 1e3 / K, 4),
-                                     note="the same minibatches launched kernel by kernel with HIP event pairs; "
-                                          "roofline and hbm_kernels come from this pass")
+                                     note="as many minibatches launched kernel by kernel (host row counts, exact "
+                                          "launch sizes) with HIP event pairs; roofline and hbm_kernels come "
+                                          "from this pass")
     if muon:
         line["muon"] = muon_stats(L, K)
     if not args.no_cpu_baseline and not bf16:

@@ -277,6 +277,16 @@ int ptcg_trainer_set_optimizer(PtcgTrainer* t, int kind, double wd_1d);
 /* global_step / epoch carried in PTCGSTA1 headers (bindings.cu:257-262)    */
 int ptcg_trainer_set_counters(PtcgTrainer* t, int64_t global_step, int64_t epoch);
 int ptcg_trainer_get_counters(PtcgTrainer* t, int64_t* global_step, int64_t* epoch);
+/* Graph capture of the rollout step (the reference's per-(t, buf) rollout
+ * graphs, pufferlib.cu:757-946): capture_rollout records, into slot `slot`,
+ * ptcg_trainer_rollout over these device buffers with the draw's step read
+ * from the device counter *step_dev (uint64) and advanced by one at the end
+ * of every replay; replay_rollout launches slot `slot` on `stream`.  Sync-free
+ * mode; every slot uses the same row count n.                              */
+int ptcg_trainer_capture_rollout(PtcgTrainer* t, int slot, const float* obs, const int32_t* row_idx, int n,
+                                 uint64_t seed, uint64_t* step_dev, float* actions, float* logprobs,
+                                 float* values);
+int ptcg_trainer_replay_rollout(PtcgTrainer* t, int slot, void* stream);
 /* ptcg_model_set_precision on the trainer's models (train and rollout).  */
 int ptcg_trainer_set_precision(PtcgTrainer* t, int prec);
 /* ptcg_model_set_sync_free on the trainer's models (train and rollout).   */

@@ -288,6 +288,8 @@ struct PtcgTrainer {
     hipStream_t cap_stream = nullptr;
     hipGraph_t graph = nullptr;
     hipGraphExec_t graph_exec = nullptr;
+    // captured rollout steps, one per slot (the reference's per-(t, buf) graphs)
+    std::vector<hipGraphExec_t> roll_exec;
     double wd_1d = 0.0;
     int64_t global_step = 0, epoch = 0;
     std::vector<float> st_f[5];
@@ -299,6 +301,8 @@ extern "C" void ptcg_trainer_free(PtcgTrainer* t) {
     if (t->model) ptcg_model_free(t->model);
     if (t->roll) ptcg_model_free(t->roll);
     if (t->muon) ptcg_muon_free(t->muon);
+    for (auto x : t->roll_exec)
+        if (x) (void)hipGraphExecDestroy(x);
     if (t->graph_exec) (void)hipGraphExecDestroy(t->graph_exec);
     if (t->graph) (void)hipGraphDestroy(t->graph);
     if (t->cap_stream) (void)hipStreamDestroy(t->cap_stream);
@@ -658,11 +662,7 @@ extern "C" int ptcg_trainer_set_sync_free(PtcgTrainer* t, int on) {
     return PTCG_OK;
 }
 
-extern "C" int ptcg_trainer_rollout(PtcgTrainer* t, const float* obs, const int32_t* row_idx, int n,
-                                    uint64_t seed, uint64_t step, float* actions, float* logprobs,
-                                    float* values, void* stream) {
-    PT_REQUIRE(t && obs && actions && logprobs, "trainer_rollout: null argument");
-    PT_REQUIRE(n >= 1, "trainer_rollout: n=%d", n);
+static int roll_model(PtcgTrainer* t, int n) {
     if (!t->roll || t->roll_n != n) {
         if (!t->roll) {
             PT_TRY(ptcg_model_create(&t->dm, &t->roll));
@@ -675,13 +675,78 @@ extern "C" int ptcg_trainer_rollout(PtcgTrainer* t, const float* obs, const int3
                                              t->st_f[3].data(), t->st_f[4].data(), t->st_i[0].data(),
                                              t->st_i[1].data()));
         }
+        // captured rollout graphs hold the old activation buffers: drop them
+        for (auto& x : t->roll_exec)
+            if (x) {
+                PT_HIP(hipDeviceSynchronize());
+                PT_HIP(hipGraphExecDestroy(x));
+                x = nullptr;
+            }
         PT_TRY(ptcg_model_reg_rollout(t->roll, n));
         t->roll_n = n;
     }
+    return PTCG_OK;
+}
+
+extern "C" int ptcg_trainer_rollout(PtcgTrainer* t, const float* obs, const int32_t* row_idx, int n,
+                                    uint64_t seed, uint64_t step, float* actions, float* logprobs,
+                                    float* values, void* stream) {
+    PT_REQUIRE(t && obs && actions && logprobs, "trainer_rollout: null argument");
+    PT_REQUIRE(n >= 1, "trainer_rollout: n=%d", n);
+    PT_TRY(roll_model(t, n));
     float* out = nullptr;
     PT_TRY(ptcg_model_forward(t->roll, obs, row_idx, n, &out, stream));
     return ptcg_sample_actions(out, n, t->dm.n_opt, obs + t->off.opt_mask, t->off.size, row_idx, seed, step, actions,
                                logprobs, values, nullptr, stream);
+}
+
+// The reference captures one graph per (time step, buffer) of its rollout
+// (net_callback_wrapper, pufferlib.cu:757-946) because each reads and writes
+// different rollout slices; the same here: slot k's graph holds the rollout
+// forward over its own buffers and the draw, with the step read from the
+// device counter step_dev and advanced by one per replay.  Sync-free mode.
+extern "C" int ptcg_trainer_capture_rollout(PtcgTrainer* t, int slot, const float* obs, const int32_t* row_idx,
+                                            int n, uint64_t seed, uint64_t* step_dev, float* actions,
+                                            float* logprobs, float* values) {
+    PT_REQUIRE(t && obs && actions && logprobs && step_dev, "capture_rollout: null argument");
+    PT_REQUIRE(slot >= 0 && slot < 4096, "capture_rollout: slot %d out of range", slot);
+    PT_REQUIRE(n >= 1, "capture_rollout: n=%d", n);
+    PT_REQUIRE(t->sync_free, "capture_rollout: needs sync-free mode (ptcg_trainer_set_sync_free)");
+    PT_TRY(roll_model(t, n));   // allocations happen outside the capture
+    PT_REQUIRE(t->roll_n == n, "capture_rollout: the rollout policy is registered for %d rows", t->roll_n);
+    if ((int)t->roll_exec.size() <= slot) t->roll_exec.resize(slot + 1, nullptr);
+    if (t->roll_exec[slot]) {
+        PT_HIP(hipGraphExecDestroy(t->roll_exec[slot]));
+        t->roll_exec[slot] = nullptr;
+    }
+    if (!t->cap_stream) PT_HIP(hipStreamCreateWithFlags(&t->cap_stream, hipStreamNonBlocking));
+    PT_HIP(hipDeviceSynchronize());
+    PT_HIP(hipStreamBeginCapture(t->cap_stream, hipStreamCaptureModeThreadLocal));
+    float* out = nullptr;
+    int r = ptcg_model_forward(t->roll, obs, row_idx, n, &out, t->cap_stream);
+    if (r == PTCG_OK)
+        r = pt_sample_actions_dev(out, n, t->dm.n_opt, obs + t->off.opt_mask, t->off.size, row_idx, seed, step_dev,
+                                  actions, logprobs, values, t->cap_stream);
+    hipGraph_t g = nullptr;
+    const hipError_t e = hipStreamEndCapture(t->cap_stream, &g);
+    if (r != PTCG_OK) {
+        if (g) (void)hipGraphDestroy(g);
+        return r;
+    }
+    PT_HIP(e);
+    hipGraphExec_t x = nullptr;
+    const hipError_t ei = hipGraphInstantiateWithFlags(&x, g, 0);
+    (void)hipGraphDestroy(g);
+    PT_HIP(ei);
+    t->roll_exec[slot] = x;
+    return PTCG_OK;
+}
+
+extern "C" int ptcg_trainer_replay_rollout(PtcgTrainer* t, int slot, void* stream) {
+    PT_REQUIRE(t && slot >= 0 && slot < (int)t->roll_exec.size() && t->roll_exec[slot],
+               "replay_rollout: slot %d has no captured rollout", slot);
+    PT_HIP(hipGraphLaunch(t->roll_exec[slot], (hipStream_t)stream));
+    return PTCG_OK;
 }
 
 extern "C" int ptcg_trainer_step(PtcgTrainer* t, const float* obs, const int32_t* row_idx,

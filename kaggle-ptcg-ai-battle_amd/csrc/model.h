@@ -60,6 +60,10 @@ int pt_ppo_loss(const float* out, int n, int A, const float* mask, long mask_str
                 hipStream_t s);
 int pt_kl_gate(const float* guard, float kl_thr, float vf_thr, float* gate, float* skipped,
                hipStream_t s);
+// the sampler with its step read from (and advanced in) device memory
+int pt_sample_actions_dev(const float* dec_out, int n, int A, const float* mask, long mask_stride,
+                          const int32_t* row_idx, uint64_t seed, uint64_t* step_dev, float* actions,
+                          float* logprobs, float* values, hipStream_t s);
 struct PtcgMuon;
 int pt_muon_set_momentum(PtcgMuon* m, double momentum);
 long pt_adam_ws_floats();

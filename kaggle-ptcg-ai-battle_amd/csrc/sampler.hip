@@ -23,10 +23,12 @@ __device__ __forceinline__ float safe_masked(float l, const float* mk, int a) {
 
 __global__ void sample_kernel(const float* __restrict__ dec, int n, int A, const float* __restrict__ mask,
                               long mstride, const int32_t* __restrict__ idx, unsigned long long seed,
-                              unsigned long long step, float* __restrict__ actions, float* __restrict__ logprobs,
+                              unsigned long long step, const unsigned long long* __restrict__ step_dev,
+                              float* __restrict__ actions, float* __restrict__ logprobs,
                               float* __restrict__ values, float* __restrict__ uniforms) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n) return;
+    if (step_dev) step = *step_dev;   // a captured rollout reads its step at replay time
     const float* l = dec + (long)i * (A + 1);
     const float* mk = mask ? mask + (idx ? (long)idx[i] : (long)i) * mstride : nullptr;
     float mx = -INFINITY, se = 0.f;
@@ -66,7 +68,24 @@ __global__ void sample_kernel(const float* __restrict__ dec, int n, int A, const
     if (uniforms) uniforms[i] = u;
 }
 
+// advances a captured rollout's step counter after its draws
+__global__ void step_advance_kernel(unsigned long long* step_dev) { step_dev[0] += 1ull; }
+
 }  // namespace
+
+int pt_sample_actions_dev(const float* dec_out, int n, int A, const float* mask, long mask_stride,
+                          const int32_t* row_idx, uint64_t seed, uint64_t* step_dev, float* actions,
+                          float* logprobs, float* values, hipStream_t s) {
+    PT_REQUIRE(dec_out && actions && logprobs && step_dev, "sample_actions: null buffer");
+    PT_REQUIRE(n > 0 && A > 0, "sample_actions: empty shape n=%d A=%d", n, A);
+    hipLaunchKernelGGL(sample_kernel, dim3(pt_cdiv(n, 256)), dim3(256), 0, s, dec_out, n, A, mask, mask_stride,
+                       row_idx, (unsigned long long)seed, 0ull, (const unsigned long long*)step_dev, actions,
+                       logprobs, values, (float*)nullptr);
+    PT_LAUNCH_CHECK();
+    hipLaunchKernelGGL(step_advance_kernel, dim3(1), dim3(1), 0, s, (unsigned long long*)step_dev);
+    PT_LAUNCH_CHECK();
+    return PTCG_OK;
+}
 
 extern "C" int ptcg_sample_actions(const float* dec_out, int n, int A, const float* mask, int64_t mask_stride,
                                    const int32_t* row_idx, uint64_t seed, uint64_t step, float* actions,
@@ -75,8 +94,8 @@ extern "C" int ptcg_sample_actions(const float* dec_out, int n, int A, const flo
     PT_REQUIRE(n > 0 && A > 0, "sample_actions: empty shape n=%d A=%d", n, A);
     hipStream_t s = (hipStream_t)stream;
     hipLaunchKernelGGL(sample_kernel, dim3(pt_cdiv(n, 256)), dim3(256), 0, s, dec_out, n, A, mask, (long)mask_stride,
-                       row_idx, (unsigned long long)seed, (unsigned long long)step, actions, logprobs, values,
-                       uniforms);
+                       row_idx, (unsigned long long)seed, (unsigned long long)step,
+                       (const unsigned long long*)nullptr, actions, logprobs, values, uniforms);
     PT_LAUNCH_CHECK();
     return PTCG_OK;
 }

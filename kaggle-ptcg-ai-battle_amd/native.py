@@ -98,6 +98,9 @@ _SIGS = {
     "ptcg_trainer_set_prio": (ctypes.c_int, [c_void_p, c_void_p]),
     "ptcg_trainer_capture_step": (ctypes.c_int, [c_void_p] * 8),
     "ptcg_trainer_replay_step": (ctypes.c_int, [c_void_p, c_void_p]),
+    "ptcg_trainer_capture_rollout": (ctypes.c_int, [c_void_p, ctypes.c_int, c_void_p, c_void_p, ctypes.c_int,
+                                                    ctypes.c_uint64, c_void_p, c_void_p, c_void_p, c_void_p]),
+    "ptcg_trainer_replay_rollout": (ctypes.c_int, [c_void_p, ctypes.c_int, c_void_p]),
     "ptcg_trainer_set_optimizer": (ctypes.c_int, [c_void_p, ctypes.c_int, ctypes.c_double]),
     "ptcg_trainer_set_counters": (ctypes.c_int, [c_void_p, ctypes.c_int64, ctypes.c_int64]),
     "ptcg_trainer_get_counters": (ctypes.c_int, [c_void_p, ctypes.POINTER(ctypes.c_int64),

@@ -136,6 +136,18 @@ class PuffeRL:
                                          n, seed, step, acts.data_ptr(), lps.data_ptr(), vals.data_ptr(), stream))
         return acts, lps, vals
 
+    def capture_rollout(self, slot, obs, n, seed, step_dev, actions, logprobs, values, idx=None):
+        """Capture slot `slot`: the rollout step over these device buffers,
+        the draw's step read from the device uint64 counter step_dev and
+        advanced by one per replay (sync-free mode)."""
+        check(lib().ptcg_trainer_capture_rollout(self._h, slot, obs.data_ptr(),
+                                                 idx.data_ptr() if idx is not None else None, n, seed,
+                                                 step_dev.data_ptr(), actions.data_ptr(), logprobs.data_ptr(),
+                                                 values.data_ptr()))
+
+    def replay_rollout(self, slot, stream=None):
+        check(lib().ptcg_trainer_replay_rollout(self._h, slot, stream))
+
     def step_count(self):
         v = ctypes.c_int32()
         check(lib().ptcg_trainer_step_count(self._h, ctypes.byref(v)))

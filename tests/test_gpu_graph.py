@@ -66,3 +66,37 @@ def test_capture_needs_sync_free(cuda):
             pl.capture_step(pl.rollout["obs"], None, pl.rollout)
     finally:
         pl.close()
+
+
+def test_rollout_graph_slots_match_eager(cuda):
+    """Two captured rollout slots over their own obs / output buffers (the
+    reference's per-(t, buf) graphs), replayed in turn with the device step
+    counter advancing per replay, give bit for bit what eager rollout calls
+    with the same steps give."""
+    dm, n = dims.CORE, 256
+    blob = om.build(dm, seed=91).to_blob()
+    obs = [synth.make_obs(dm, n, seed=92 + k) for k in range(2)]
+    cfg = {"dims": dm, "init_weights": blob, "sync_free": True, "train": dict(minibatch_size=64)}
+    pl = trainer.create_pufferl(cfg)
+    try:
+        d_obs = [pl.to_device(o) for o in obs]
+        outs = [[torch.empty(n, device="cuda") for _ in range(3)] for _ in range(2)]
+        step = torch.tensor([40], dtype=torch.int64, device="cuda")
+        for k in range(2):
+            pl.capture_rollout(k, d_obs[k], n, 1234, step, *outs[k])
+        expect_step = 40
+        for rep in range(3):
+            for k in range(2):
+                pl.replay_rollout(k)
+                torch.cuda.synchronize()
+                got = [t.cpu().numpy().copy() for t in outs[k]]
+                # eager work between replays: the same draw, launched call by call
+                a, lp, v = pl.rollout_step(d_obs[k], n, seed=1234, step=expect_step)
+                torch.cuda.synchronize()
+                assert np.array_equal(got[0], a.cpu().numpy()), (rep, k)
+                assert np.array_equal(got[1], lp.cpu().numpy()), (rep, k)
+                assert np.array_equal(got[2], v.cpu().numpy()), (rep, k)
+                expect_step += 1
+                assert int(step.item()) == expect_step
+    finally:
+        pl.close()

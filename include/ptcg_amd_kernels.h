@@ -38,10 +38,10 @@ int ptcg_kernel_gemm_axpby(int M, int N, int K, const float* A, int64_t lda, int
                            const float* R, int64_t ldr, float beta, void* stream);
 
 /* ptcg_kernel_gemm with bf16 products: A and B rounded to bf16 (round to
- * nearest even) on the way into LDS, v_mfma_f32_16x16x32_bf16, fp32
- * accumulation and epilogue (the reference's USE_BF16 build, pufferlib.cu
- * precision_t = bf16 with cuBLAS fp32 compute).  Shapes that break the
- * 128-bit operand rules run the fp32 kernel.                              */
+ * nearest even) before v_mfma_f32_16x16x32_bf16, fp32 accumulation and
+ * epilogue (the reference's USE_BF16 build, pufferlib.cu precision_t = bf16
+ * with cuBLAS fp32 compute).  Shapes that break the 128-bit operand rules
+ * run the fp32 kernel.                                                     */
 int ptcg_kernel_gemm_bf16(int M, int N, int K, const float* A, int64_t lda, int a_t,
                           const float* B, int64_t ldb, int b_t, float* C, int64_t ldc, int epi,
                           const float* bias, const float* R, int64_t ldr, float* C2, int64_t ldc2,
@@ -55,6 +55,12 @@ int ptcg_kernel_gemm_bf16(int M, int N, int K, const float* A, int64_t lda, int 
 int ptcg_kernel_gemm_dw(int rows, int in, int out, const float* dY, int64_t lddy,
                         const float* X, int64_t ldx, float* dW, float* db,
                         float* workspace, int64_t workspace_floats, void* stream);
+
+/* ptcg_kernel_gemm_dw with bf16 products (dY and X rounded to bf16 before
+ * the MFMA, fp32 accumulation); db sums the unrounded fp32 dY.            */
+int ptcg_kernel_gemm_dw_bf16(int rows, int in, int out, const float* dY, int64_t lddy,
+                             const float* X, int64_t ldx, float* dW, float* db,
+                             float* workspace, int64_t workspace_floats, void* stream);
 
 /* deterministic column sums out[n] = sum_m X[m*ldx+n] (pt_bias_grad,
  * ptcg_kernels.cuh:87-96); workspace >= ceil(M/256)*N floats.              */

@@ -21,6 +21,13 @@ namespace {
 
 constexpr int BM = 128, BN = 128, BK = 16;
 constexpr int NT = 256;
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+
+// fp32 -> bf16, round to nearest even (v_cvt_pk_bf16_f32)
+__device__ __forceinline__ bf16x4 to_bf16x4(float a, float b, float c, float d) {
+    return bf16x4{(__bf16)a, (__bf16)b, (__bf16)c, (__bf16)d};
+}
 // LDS layouts.  A k-contiguous operand is staged [row][k] (stride BK+4: the
 // 128-bit fragment reads of 8 consecutive rows cover all 32 banks); an
 // m-contiguous operand is staged [k][row] (stride BM+4: rows 4 apart land 16
@@ -400,9 +407,24 @@ __device__ __forceinline__ void dma16(int32x4_t rsrc, const float* lds_base, int
                  :: "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(voffset_bytes), "s"(rsrc) : "memory", "m0");
 }
 template <int N> __device__ __forceinline__ void wait_vm() {
+    static_assert(N % 4 == 0 && N <= 24, "wait_vm: 4 loads per stage, at most 6 later stages");
     if (N == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     else if (N == 4) asm volatile("s_waitcnt vmcnt(4)" ::: "memory");
-    else asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+    else if (N == 8) asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+    else if (N == 12) asm volatile("s_waitcnt vmcnt(12)" ::: "memory");
+    else if (N == 16) asm volatile("s_waitcnt vmcnt(16)" ::: "memory");
+    else if (N == 20) asm volatile("s_waitcnt vmcnt(20)" ::: "memory");
+    else asm volatile("s_waitcnt vmcnt(24)" ::: "memory");
+}
+// wait until at most `later` stages (4 loads each) are still in flight
+template <int NS> __device__ __forceinline__ void wait_stages(int later) {
+    if (NS > 7 && later >= 6) wait_vm<24>();
+    else if (NS > 6 && later == 5) wait_vm<20>();
+    else if (NS > 5 && later == 4) wait_vm<16>();
+    else if (NS > 4 && later == 3) wait_vm<12>();
+    else if (NS > 3 && later == 2) wait_vm<8>();
+    else if (NS > 2 && later == 1) wait_vm<4>();
+    else wait_vm<0>();
 }
 // row swizzle of the [row][k] layout: conflict-free 128-bit reads of 16 rows
 // (one k group) on 32- and 64-bank LDS, and conflict-free DMA writes
@@ -429,14 +451,18 @@ template <bool T> __device__ __forceinline__ int dma_src(int c, int lane, int r0
 
 // One 128 x 128 tile of C (split bz of gz along K) of the logical tile
 // index bx; shared by the per-product launch and the grouped launch.
-template <bool AT, bool BT, int EPI, bool PARTIAL, bool DB>
+// NS: pipeline stages (NS - 1 tiles in flight while one is multiplied).
+// BF: bf16 products — each lane's float4 fragment (k = 4 lq .. 4 lq + 3 of
+// its row, the same k for A and B) is rounded to bf16 (RNE) and one
+// v_mfma_f32_16x16x16_bf16 replaces the four fp32 k-steps.
+template <bool AT, bool BT, int EPI, bool PARTIAL, bool DB, bool BF = false, int NS = DMA_NS>
 __device__ __forceinline__ void gemm_dma_tile(const GemmArgs& g0, int k_chunk0, long part_stride, int bx, int bz,
                                               int gz) {
     const GemmArgs g = gemm_shape(g0);
     // a device reduction count splits its own K evenly over the launch's splits
     const int k_chunk = g0.Kdev ? (((g.K + gz - 1) / gz + BK - 1) / BK) * BK : k_chunk0;
     constexpr int TILE = BM * BK;   // floats per operand tile (BM == BN)
-    constexpr int SMEM = DMA_NS * 2 * TILE > STAGE_FLOATS ? DMA_NS * 2 * TILE : STAGE_FLOATS;
+    constexpr int SMEM = NS * 2 * TILE > STAGE_FLOATS ? NS * 2 * TILE : STAGE_FLOATS;
     __shared__ __align__(16) float smem[SMEM];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int tn = (g.N + BN - 1) / BN;
@@ -465,7 +491,7 @@ __device__ __forceinline__ void gemm_dma_tile(const GemmArgs& g0, int k_chunk0, 
 #define PT_ISSUE(tile)                                                                  \
     {                                                                                   \
         const int k0_ = kbeg + (tile) * BK;                                             \
-        const float* st_ = smem + ((tile) % DMA_NS) * 2 * TILE;                         \
+        const float* st_ = smem + ((tile) % NS) * 2 * TILE;                             \
         dma16(ra, st_ + (2 * wave) * 256, (sa0 + k0_ * ka) * 4);                        \
         dma16(ra, st_ + (2 * wave + 1) * 256, (sa1 + k0_ * ka) * 4);                    \
         dma16(rb, st_ + TILE + (2 * wave) * 256, (sb0 + k0_ * kb) * 4);                 \
@@ -475,18 +501,15 @@ __device__ __forceinline__ void gemm_dma_tile(const GemmArgs& g0, int k_chunk0, 
     float dbsum = 0.f;
     if (nk > 0) {
 #pragma unroll
-        for (int t = 0; t < DMA_NS - 1; ++t)
+        for (int t = 0; t < NS - 1; ++t)
             if (t < nk) PT_ISSUE(t)
         for (int it = 0; it < nk; ++it) {
-            // tile it has landed once at most min(DMA_NS - 2, nk - 1 - it) later
+            // tile it has landed once at most min(NS - 2, nk - 1 - it) later
             // tiles (4 loads each) are still in flight
-            const int later = min(DMA_NS - 2, nk - 1 - it);
-            if (later >= 2) wait_vm<8>();
-            else if (later == 1) wait_vm<4>();
-            else wait_vm<0>();
+            wait_stages<NS>(min(NS - 2, nk - 1 - it));
             __syncthreads();   // every wave's loads of tile it are in LDS; tile it - 1 is consumed
-            if (it + DMA_NS - 1 < nk) PT_ISSUE(it + DMA_NS - 1)
-            const float* Ab = smem + (it % DMA_NS) * 2 * TILE;
+            if (it + NS - 1 < nk) PT_ISSUE(it + NS - 1)
+            const float* Ab = smem + (it % NS) * 2 * TILE;
             const float* Bb = Ab + TILE;
             float4 af[4], bf[4];
 #pragma unroll
@@ -499,12 +522,26 @@ __device__ __forceinline__ void gemm_dma_tile(const GemmArgs& g0, int k_chunk0, 
                 else bf[t] = make_float4(Bb[dma_at<true>(cb, 4 * lq)], Bb[dma_at<true>(cb, 4 * lq + 1)],
                                          Bb[dma_at<true>(cb, 4 * lq + 2)], Bb[dma_at<true>(cb, 4 * lq + 3)]);
             }
+            if constexpr (BF) {
+                bf16x4 ah[4], bh[4];
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    ah[t] = to_bf16x4(af[t].x, af[t].y, af[t].z, af[t].w);
+                    bh[t] = to_bf16x4(bf[t].x, bf[t].y, bf[t].z, bf[t].w);
+                }
+#pragma unroll
+                for (int ti = 0; ti < 4; ++ti)
+#pragma unroll
+                    for (int tj = 0; tj < 4; ++tj)
+                        acc[ti][tj] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(bh[tj], ah[ti], acc[ti][tj], 0, 0, 0);
+            } else {
 #define PT_MFMA_STEP(c)                                                                             \
             _Pragma("unroll") for (int ti = 0; ti < 4; ++ti)                                        \
             _Pragma("unroll") for (int tj = 0; tj < 4; ++tj)                                        \
                 acc[ti][tj] = __builtin_amdgcn_mfma_f32_16x16x4f32(bf[tj].c, af[ti].c, acc[ti][tj], 0, 0, 0);
             PT_MFMA_STEP(x) PT_MFMA_STEP(y) PT_MFMA_STEP(z) PT_MFMA_STEP(w)
 #undef PT_MFMA_STEP
+            }
             if (do_db) {
                 // k rows past K were loaded as zeros; columns past M are never stored
 #pragma unroll
@@ -575,9 +612,10 @@ __global__ __launch_bounds__(256) void grouped_reduce_kernel(const GroupedGemm* 
 }
 
 // ---------------------------------------------------------------- bf16
-// Mixed precision: fp32 operands from HBM are rounded to bf16 (RNE) on the
-// way into LDS and multiplied on v_mfma_f32_16x16x32_bf16 with fp32
-// accumulation; the epilogue is the fp32 kernel's.  Same 128x128 block,
+// Mixed precision, register-staged (shapes off the DMA rules; the DMA ones
+// run gemm_bf16_k16_kernel): fp32 operands from HBM are rounded to bf16
+// (RNE) on the way into LDS and multiplied on v_mfma_f32_16x16x32_bf16 with
+// fp32 accumulation; the epilogue is the fp32 kernel's.  Same 128x128 block,
 // 4 waves x 64x64, XCD tile order; BK = 32 (one MFMA k-step).  Both operands
 // sit in LDS as [row][k] bf16 (row stride 40: 16 B-aligned 128-bit fragment
 // reads, conflict-free across 8 lanes); an m-contiguous operand is
@@ -586,12 +624,6 @@ __global__ __launch_bounds__(256) void grouped_reduce_kernel(const GroupedGemm* 
 // (lane group, element) -> k map, so the product is independent of the
 // hardware's internal k order.
 constexpr int BK2 = 32, SKB2 = BK2 + 8;
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
-
-__device__ __forceinline__ bf16x4 to_bf16x4(float a, float b, float c, float d) {
-    return bf16x4{(__bf16)a, (__bf16)b, (__bf16)c, (__bf16)d};
-}
 
 // stage one operand's 128 x 32 tile: T (m-contiguous in memory) or not.
 // Thread t covers: !T: row t/2, k 16*(t%2) .. +15 (four 128-bit loads);
@@ -689,6 +721,18 @@ __global__ __launch_bounds__(NT) void gemm_bf16_kernel(const GemmArgs g0, int k_
         }
     }
     gemm_epilogue<EPI, PARTIAL>(g, acc, m0, n0, wm, wn, li, lq, part_stride, smem, blockIdx.z);
+}
+
+// ---------------------------------------------------------------- bf16, LDS DMA
+// bf16 products on the fp32 DMA pipeline (16 k per stage, operands rounded
+// as they leave LDS; bias sums of the fp32 tiles as in the fp32 kernel).
+// Three stages: deeper pipelines measured no faster (the loop is bound by
+// the operand fetches, not their latency).
+constexpr int BF_NS = 3;
+template <bool AT, bool BT, int EPI, bool PARTIAL, bool DB>
+__global__ __launch_bounds__(NT) void gemm_bf16_k16_kernel(const GemmArgs g0, int k_chunk0, long part_stride) {
+    gemm_dma_tile<AT, BT, EPI, PARTIAL, DB, true, BF_NS>(g0, k_chunk0, part_stride, blockIdx.x, blockIdx.z,
+                                                         gridDim.z);
 }
 
 // out[m][n] (=|+=) sum_s part[s][m][n], fixed order over s
@@ -798,40 +842,55 @@ void launch(const GemmArgs& g, dim3 grid, int k_chunk, long part_stride, hipStre
     pt_prof_close(slot, g_gemm_class, launch_flops(g), s);
 }
 
-template <bool AT, bool BT, int EPI, bool PARTIAL>
+template <bool AT, bool BT, int EPI, bool PARTIAL, bool DB>
 void launch_bf16(const GemmArgs& g, dim3 grid, int k_chunk, long part_stride, hipStream_t s) {
     const int slot = pt_prof_open(s);
-    hipLaunchKernelGGL((gemm_bf16_kernel<AT, BT, EPI, PARTIAL>), grid, dim3(NT), 0, s, g, k_chunk, part_stride);
+    if (g.dma)
+        hipLaunchKernelGGL((gemm_bf16_k16_kernel<AT, BT, EPI, PARTIAL, DB>), grid, dim3(NT), 0, s, g, k_chunk,
+                           part_stride);
+    else
+        hipLaunchKernelGGL((gemm_bf16_kernel<AT, BT, EPI, PARTIAL>), grid, dim3(NT), 0, s, g, k_chunk, part_stride);
     pt_prof_close(slot, g_gemm_class, launch_flops(g), s);
 }
 
+// db: fused bias sums (A transposed, STORE epilogue, DMA kernel only)
 template <bool AT, bool BT>
-int launch_bf16_epi(const GemmArgs& g, dim3 grid, int k_chunk, long part_stride, bool partial, hipStream_t s) {
+int launch_bf16_epi(const GemmArgs& g, dim3 grid, int k_chunk, long part_stride, bool partial, bool db,
+                    hipStream_t s) {
+    if (db) {
+        PT_REQUIRE(AT && g.dma && g.epi == EPI_STORE, "gemm: bf16 bias sums need A transposed and the DMA kernel");
+        if constexpr (AT) {
+            if (partial) launch_bf16<AT, BT, EPI_STORE, true, true>(g, grid, k_chunk, part_stride, s);
+            else launch_bf16<AT, BT, EPI_STORE, false, true>(g, grid, k_chunk, 0, s);
+        }
+        return PTCG_OK;
+    }
     if (partial) {
-        launch_bf16<AT, BT, EPI_STORE, true>(g, grid, k_chunk, part_stride, s);
+        launch_bf16<AT, BT, EPI_STORE, true, false>(g, grid, k_chunk, part_stride, s);
         return PTCG_OK;
     }
     switch (g.epi) {
-        case EPI_STORE: launch_bf16<AT, BT, EPI_STORE, false>(g, grid, k_chunk, 0, s); break;
-        case EPI_BIAS: launch_bf16<AT, BT, EPI_BIAS, false>(g, grid, k_chunk, 0, s); break;
-        case EPI_BIAS_GELU: launch_bf16<AT, BT, EPI_BIAS_GELU, false>(g, grid, k_chunk, 0, s); break;
-        case EPI_BIAS_RESID: launch_bf16<AT, BT, EPI_BIAS_RESID, false>(g, grid, k_chunk, 0, s); break;
-        case EPI_GELU_BWD: launch_bf16<AT, BT, EPI_GELU_BWD, false>(g, grid, k_chunk, 0, s); break;
-        case EPI_BIAS_GELU_D: launch_bf16<AT, BT, EPI_BIAS_GELU_D, false>(g, grid, k_chunk, 0, s); break;
-        case EPI_MUL: launch_bf16<AT, BT, EPI_MUL, false>(g, grid, k_chunk, 0, s); break;
-        case EPI_AXPBY: launch_bf16<AT, BT, EPI_AXPBY, false>(g, grid, k_chunk, 0, s); break;
-        case EPI_ACCUM: launch_bf16<AT, BT, EPI_ACCUM, false>(g, grid, k_chunk, 0, s); break;
+        case EPI_STORE: launch_bf16<AT, BT, EPI_STORE, false, false>(g, grid, k_chunk, 0, s); break;
+        case EPI_BIAS: launch_bf16<AT, BT, EPI_BIAS, false, false>(g, grid, k_chunk, 0, s); break;
+        case EPI_BIAS_GELU: launch_bf16<AT, BT, EPI_BIAS_GELU, false, false>(g, grid, k_chunk, 0, s); break;
+        case EPI_BIAS_RESID: launch_bf16<AT, BT, EPI_BIAS_RESID, false, false>(g, grid, k_chunk, 0, s); break;
+        case EPI_GELU_BWD: launch_bf16<AT, BT, EPI_GELU_BWD, false, false>(g, grid, k_chunk, 0, s); break;
+        case EPI_BIAS_GELU_D: launch_bf16<AT, BT, EPI_BIAS_GELU_D, false, false>(g, grid, k_chunk, 0, s); break;
+        case EPI_MUL: launch_bf16<AT, BT, EPI_MUL, false, false>(g, grid, k_chunk, 0, s); break;
+        case EPI_AXPBY: launch_bf16<AT, BT, EPI_AXPBY, false, false>(g, grid, k_chunk, 0, s); break;
+        case EPI_ACCUM: launch_bf16<AT, BT, EPI_ACCUM, false, false>(g, grid, k_chunk, 0, s); break;
         default: PT_REQUIRE(false, "gemm: bad epilogue %d", g.epi);
     }
     return PTCG_OK;
 }
 
-int launch_bf16_any(const GemmArgs& g, dim3 grid, int k_chunk, long part_stride, bool partial, hipStream_t s) {
+int launch_bf16_any(const GemmArgs& g, dim3 grid, int k_chunk, long part_stride, bool partial, bool db,
+                    hipStream_t s) {
     const int code = (g.a_t ? 1 : 0) * 2 + (g.b_t ? 1 : 0);
-    if (code == 0) return launch_bf16_epi<false, false>(g, grid, k_chunk, part_stride, partial, s);
-    if (code == 1) return launch_bf16_epi<false, true>(g, grid, k_chunk, part_stride, partial, s);
-    if (code == 3) return launch_bf16_epi<true, true>(g, grid, k_chunk, part_stride, partial, s);
-    return launch_bf16_epi<true, false>(g, grid, k_chunk, part_stride, partial, s);
+    if (code == 0) return launch_bf16_epi<false, false>(g, grid, k_chunk, part_stride, partial, db, s);
+    if (code == 1) return launch_bf16_epi<false, true>(g, grid, k_chunk, part_stride, partial, db, s);
+    if (code == 3) return launch_bf16_epi<true, true>(g, grid, k_chunk, part_stride, partial, db, s);
+    return launch_bf16_epi<true, false>(g, grid, k_chunk, part_stride, partial, db, s);
 }
 
 // split-K partial products (STORE into the workspace), optional bias sums
@@ -963,7 +1022,7 @@ static int pt_cu_count() {
     return cache[dev];
 }
 
-// LDS-DMA kernel: k-contiguous operands need K % BK == 0, and every byte
+// LDS-DMA kernels: k-contiguous operands need K % BK == 0, and every byte
 // offset a tile can form (rows / columns up to one tile past the end) must
 // fit the buffer instructions' 32-bit offsets
 static bool dma_fits(int rows, int cols, long ld) {
@@ -987,8 +1046,8 @@ int pt_gemm(const GemmArgs& g0, float* ws, long ws_floats, hipStream_t s) {
                      ((uintptr_t)g.B & 15) == 0;
     // bf16 products need the 128-bit operand path; other shapes stay fp32
     const bool bf = g.prec == 1 && vec;
-    g.dma = vec && !bf && dma_ok(g);
-    const int bk = bf ? BK2 : BK;
+    g.dma = vec && dma_ok(g);
+    const int bk = bf && !g.dma ? BK2 : BK;
     const int tm = pt_cdiv(g.M, BM), tn = pt_cdiv(g.N, BN);
     const int tiles = tm * tn;
     // split K when the output is too small to fill the chip and K is long
@@ -1003,8 +1062,9 @@ int pt_gemm(const GemmArgs& g0, float* ws, long ws_floats, hipStream_t s) {
     if (splits > 1 && !(g.epi == EPI_STORE || g.epi == EPI_ACCUM)) splits = 1;
     if (g.Mdev) splits = 1;   // device row counts: one pass (partials are sized by M)
     PT_REQUIRE(!(g.dbias && !(g.a_t && g.epi == EPI_STORE)), "gemm: dbias needs a_t = 1 and the STORE epilogue");
-    // the bf16 kernel leaves bias sums to the fp32 column sum (kept in fp32 from the unrounded dY)
-    const bool db = g.dbias != nullptr && !bf;
+    // the register-staged bf16 kernel leaves bias sums to the fp32 column sum
+    // (from the unrounded dY); the DMA kernels sum the fp32 tiles in LDS
+    const bool db = g.dbias != nullptr && (!bf || g.dma);
     long part_stride = (long)g.M * g.ldc;
     const long per_split = part_stride + (db ? g.M : 0);
     if (splits > 1 && (ws == nullptr || (long)splits * per_split > ws_floats)) {
@@ -1017,14 +1077,14 @@ int pt_gemm(const GemmArgs& g0, float* ws, long ws_floats, hipStream_t s) {
         splits = pt_cdiv(g.K, k_chunk);
     }
     dim3 grid(tn * tm, 1, splits);
-    if (bf && g.dbias) {
+    if (bf && g.dbias && !db) {
         // bias sums first: they read the fp32 dY, which the product does not modify
         PT_TRY(pt_colsum(g.A, g.lda, g.K, g.M, g.dbias, ws, ws_floats, s));
     }
     if (splits > 1) {
         GemmArgs p = g;
         p.C = ws;
-        if (bf) PT_TRY(launch_bf16_any(p, grid, k_chunk, part_stride, true, s));
+        if (bf) PT_TRY(launch_bf16_any(p, grid, k_chunk, part_stride, true, db, s));
         else if (vec) launch_partial<true>(p, db, grid, k_chunk, part_stride, s);
         else launch_partial<false>(p, db, grid, k_chunk, part_stride, s);
         PT_LAUNCH_CHECK();
@@ -1065,7 +1125,7 @@ int pt_gemm(const GemmArgs& g0, float* ws, long ws_floats, hipStream_t s) {
             a.tile0 = 0;
             a.ntiles = tiles - R;
             const dim3 ga(tiles - R, 1, 1);
-            if (bf) PT_TRY(launch_bf16_any(a, ga, g.K, 0, false, s));
+            if (bf) PT_TRY(launch_bf16_any(a, ga, g.K, 0, false, false, s));
             else PT_TRY(vec ? launch_full<true>(a, false, ga, g.K, s) : launch_full<false>(a, false, ga, g.K, s));
             PT_LAUNCH_CHECK();
             GemmArgs p = g;
@@ -1074,7 +1134,7 @@ int pt_gemm(const GemmArgs& g0, float* ws, long ws_floats, hipStream_t s) {
             p.ntiles = R;
             p.tail_part = 1;
             const dim3 gp(R, 1, s2);
-            if (bf) PT_TRY(launch_bf16_any(p, gp, kc, 0, true, s));
+            if (bf) PT_TRY(launch_bf16_any(p, gp, kc, 0, true, false, s));
             else if (vec) launch_partial<true>(p, false, gp, kc, 0, s);
             else launch_partial<false>(p, false, gp, kc, 0, s);
             PT_LAUNCH_CHECK();
@@ -1098,7 +1158,7 @@ int pt_gemm(const GemmArgs& g0, float* ws, long ws_floats, hipStream_t s) {
             return PTCG_OK;
         }
     }
-    if (bf) PT_TRY(launch_bf16_any(g, grid, k_chunk, 0, false, s));
+    if (bf) PT_TRY(launch_bf16_any(g, grid, k_chunk, 0, false, db, s));
     else PT_TRY(vec ? launch_full<true>(g, db, grid, k_chunk, s) : launch_full<false>(g, db, grid, k_chunk, s));
     PT_LAUNCH_CHECK();
     return PTCG_OK;

@@ -361,7 +361,8 @@ def _bf16(t):
 
 BF16_CASES = [(37, 52, 300, 0, 0, 1), (130, 68, 64, 0, 0, 2), (256, 256, 256, 0, 0, 3), (200, 96, 40, 0, 1, 4),
               (64, 300, 256, 0, 1, 0), (768, 256, 20000, 1, 1, 0), (96, 36, 12, 1, 0, 0), (129, 132, 132, 0, 1, 5),
-              (4096, 1024, 256, 0, 0, 2), (4096, 256, 1024, 0, 1, 0), (34000, 256, 256, 0, 0, 2)]
+              (4096, 1024, 256, 0, 0, 2), (4096, 256, 1024, 0, 1, 0), (34000, 256, 256, 0, 0, 2),
+              (300, 200, 48, 0, 0, 1), (64, 128, 16, 0, 1, 0), (1000, 136, 80, 1, 0, 7)]
 
 
 @pytest.mark.parametrize("case", BF16_CASES, ids=lambda c: "M%d_N%d_K%d_at%d_bt%d_e%d" % c)
@@ -407,3 +408,23 @@ def test_gemm_bf16_products(case, cuda):
     exact = (A.T if a_t else A).double() @ (B if b_t else B.T).double()
     if epi == 0:
         assert rel_l2(got, exact) > 1e-4
+
+
+@pytest.mark.parametrize("rows,inp,out", [(6000, 256, 768), (1573, 128, 64), (100, 64, 36), (40000, 1024, 256),
+                                          (37, 256, 256)])
+def test_gemm_weight_grad_bf16_with_bias_sums(rows, inp, out, cuda):
+    """bf16 weight gradient: dW equals the fp64 product of the bf16-rounded
+    dY and X; the fused bias sums add the unrounded fp32 dY."""
+    g = torch.Generator().manual_seed(rows + 3 * inp)
+    dY = torch.randn(rows, out, generator=g)
+    X = torch.randn(rows, inp, generator=g)
+    d_dY, d_X, dW, db = dev(dY), dev(X), empty(out, inp), empty(out)
+    ws = empty(32 << 20)
+    native.check(native.lib().ptcg_kernel_gemm_dw_bf16(rows, inp, out, P(d_dY), out, P(d_X), inp, P(dW), P(db),
+                                                       P(ws), ws.numel(), None))
+    torch.cuda.synchronize()
+    refW = _bf16(dY).T @ _bf16(X)
+    refb = dY.double().sum(0)
+    assert rel_l2(dW.cpu().double(), refW) < 1e-5
+    assert rel_l2(db.cpu().double(), refb) < 1e-5
+    assert rel_l2(dW.cpu().double(), dY.double().T @ X.double()) > 1e-4

@@ -455,6 +455,7 @@ def bench_rollout(args):
         sec_graph = time.perf_counter() - t0
         if not torch.isfinite(outs[1]).all():
             raise RuntimeError("non-finite log-probabilities in the rollout benchmark")
+        transport = bench_transport(pl, dm, obs, n, args)
         native.check(L.ptcg_trainer_set_sync_free(pl._h, 0))   # exact launch sizes for the timing pass
     # timed region 2: launched call by call with HIP event pairs (the roofline)
     native.check(L.ptcg_profile_begin(256 * args.steps))
@@ -491,8 +492,51 @@ def bench_rollout(args):
         line["stream_launch"] = dict(value=round(n * K / sec_stream, 2), ms_per_step=round(sec_stream * 1e3 / K, 4),
                                      note="as many steps launched call by call (host row counts); the roofline "
                                           "comes from this pass")
+        line["transport"] = transport
     pl.close()
     print(json.dumps(line), flush=True)
+
+
+def bench_transport(pl, dm, obs, n, args):
+    """PCIe-inclusive rollout rate through the pinned transport (vecenv.h GPU
+    mode): the n agents split into two env buffers; per buffer and step the
+    captured rollout graph on the buffer's stream, D2H of its actions and a
+    stream sync, then the async H2D of its observations, rewards and
+    terminals, which overlaps the other buffer's forward.  Not `value`: the
+    observations cross PCIe here."""
+    import torch
+    from ptcg_amd import transport as tr
+    nbuf = 2
+    x = tr.RolloutTransport(n, nbuf, dm.obs_size)
+    try:
+        x.observations[:] = obs
+        step_dev = torch.zeros(1, dtype=torch.int64, device="cuda")
+        for b in range(nbuf):
+            x.capture_rollout(pl, b, 1 + b, 0, step_dev)   # slots 1, 2
+        for b in range(nbuf):
+            x.upload(b)
+        for _ in range(2):   # warm the slots
+            for b in range(nbuf):
+                x.step(pl, b, 1 + b)
+                x.upload(b)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            for b in range(nbuf):
+                x.step(pl, b, 1 + b)
+                x.upload(b)
+        torch.cuda.synchronize()
+        sec = time.perf_counter() - t0
+        if not np.isfinite(x.actions).all():
+            raise RuntimeError("non-finite actions in the transport benchmark")
+        h2d = x.observations.nbytes + x.rewards.nbytes + x.terminals.nbytes
+        return dict(value=round(n * args.steps / sec, 2), unit="obs/s", buffers=nbuf,
+                    ms_per_step=round(sec * 1e3 / args.steps, 4), h2d_bytes_per_step=int(h2d),
+                    d2h_bytes_per_step=int(x.actions.nbytes),
+                    note="pinned host observations up and actions down per env buffer around the captured "
+                         "rollout graph (PCIe-inclusive; the env step itself is not run)")
+    finally:
+        x.close()
 
 
 def bench_replay(args):

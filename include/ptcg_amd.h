@@ -287,6 +287,45 @@ int ptcg_trainer_capture_rollout(PtcgTrainer* t, int slot, const float* obs, con
                                  uint64_t seed, uint64_t* step_dev, float* actions, float* logprobs,
                                  float* values);
 int ptcg_trainer_replay_rollout(PtcgTrainer* t, int slot, void* stream);
+/* floats per observation row of the trainer's dims (ptcg_obs_size).       */
+int ptcg_trainer_obs_size(PtcgTrainer* t);
+
+/* ---- rollout transport (vecenv.h GPU mode) ------------------------------
+ * Pinned host mirrors of the env-side arrays, their device counterparts and
+ * one stream per env buffer: the reference's cudaHostAlloc(Portable) /
+ * cudaMalloc pairs and per-buffer streams (native/src/vecenv.h:498-545).
+ * total_agents split into num_buffers contiguous slices of
+ * agents_per_buffer agents; per agent: obs_floats observation floats,
+ * num_atns action floats, one reward, one terminal, mask_bytes of action
+ * mask (0: none; this model reads its mask from the observation row), and
+ * on the device only one log-prob and one value (the rollout buffers).    */
+typedef struct PtcgTransport PtcgTransport;
+enum PtcgTransportArray { PTCG_TR_OBS = 0, PTCG_TR_ACTIONS = 1, PTCG_TR_REWARDS = 2, PTCG_TR_TERMINALS = 3,
+                          PTCG_TR_MASK = 4, PTCG_TR_LOGPROBS = 5, PTCG_TR_VALUES = 6, PTCG_TR_COUNT = 7 };
+int ptcg_transport_create(int total_agents, int num_buffers, int64_t obs_floats, int num_atns, int mask_bytes,
+                          PtcgTransport** out);
+int ptcg_transport_free(PtcgTransport* x);
+/* base pointers of an array (host: NULL for log-probs and values)         */
+void* ptcg_transport_host(PtcgTransport* x, int which);
+void* ptcg_transport_device(PtcgTransport* x, int which);
+/* the buffer's stream (hipStream_t)                                       */
+void* ptcg_transport_stream(PtcgTransport* x, int buf);
+int ptcg_transport_agents_per_buffer(PtcgTransport* x);
+/* async H2D of the buffer's observations, rewards, terminals and mask on
+ * its stream (vecenv.h:355-372, after the env step)                       */
+int ptcg_transport_upload(PtcgTransport* x, int buf);
+/* D2H of the buffer's actions on its stream, then a checked stream sync
+ * (vecenv.h:311-337: the env must not step on stale actions)              */
+int ptcg_transport_download(PtcgTransport* x, int buf);
+/* ptcg_trainer_capture_rollout into slot `slot` over the buffer's device
+ * slices (observations in, actions / log-probs / values out; num_atns 1) */
+int ptcg_transport_capture_rollout(PtcgTransport* x, PtcgTrainer* t, int buf, int slot, uint64_t seed,
+                                   uint64_t* step_dev);
+/* one rollout step of a buffer (net_callback + the actions' trip,
+ * vecenv.h:309-337): replay slot `slot` on the buffer's stream, then
+ * ptcg_transport_download                                                 */
+int ptcg_transport_step(PtcgTransport* x, PtcgTrainer* t, int buf, int slot);
+
 /* ptcg_model_set_precision on the trainer's models (train and rollout).  */
 int ptcg_trainer_set_precision(PtcgTrainer* t, int prec);
 /* ptcg_model_set_sync_free on the trainer's models (train and rollout).   */

@@ -688,6 +688,8 @@ static int roll_model(PtcgTrainer* t, int n) {
     return PTCG_OK;
 }
 
+extern "C" int ptcg_trainer_obs_size(PtcgTrainer* t) { return t ? t->off.size : 0; }
+
 extern "C" int ptcg_trainer_rollout(PtcgTrainer* t, const float* obs, const int32_t* row_idx, int n,
                                     uint64_t seed, uint64_t step, float* actions, float* logprobs,
                                     float* values, void* stream) {

@@ -1,0 +1,79 @@
+"""Rollout transport (vecenv.h GPU mode): pinned host observations go up per
+buffer, the buffer's captured rollout graph runs on the buffer's stream and
+the actions come back to pinned host memory.  Checked bit for bit against
+the eager rollout step on the same rows and draw step; rewards / terminals
+must land on the device unchanged."""
+import numpy as np
+import pytest
+import torch
+
+from ptcg_amd import dims, synth, trainer
+from ptcg_amd import transport as tr
+from ptcg_amd.native import check, lib
+import oracle.model as om
+
+pytestmark = pytest.mark.gpu
+
+
+def dev_floats(ptr, n):
+    """n floats at device address ptr, copied to the host (a [1, n] -> [n, 1]
+    transpose is a plain device copy)."""
+    buf = torch.empty(n, dtype=torch.float32, device="cuda")
+    check(lib().ptcg_transpose_102(buf.data_ptr(), ptr, 1, n, 1, 0, None))
+    torch.cuda.synchronize()
+    return buf.cpu().numpy()
+
+
+def test_transport_round_trip_matches_eager(cuda):
+    dm, nbuf, apb = dims.CORE, 2, 96
+    blob = om.build(dm, seed=121).to_blob()
+    pl = trainer.create_pufferl({"dims": dm, "init_weights": blob, "sync_free": True,
+                                 "train": dict(minibatch_size=64)})
+    x = tr.RolloutTransport(nbuf * apb, nbuf, dm.obs_size)
+    try:
+        assert x.agents_per_buffer == apb
+        step = torch.tensor([7], dtype=torch.int64, device="cuda")
+        for b in range(nbuf):
+            x.capture_rollout(pl, b, b, 555, step)
+        expect = 7
+        for t in range(3):
+            for b in range(nbuf):
+                # the env's writes for this buffer, then the upload (vecenv.h:355-372)
+                rows = synth.make_obs(dm, apb, seed=1000 + 10 * t + b)
+                sl = x.slice(b)
+                x.observations[sl] = rows
+                x.rewards[sl] = np.arange(apb, dtype=np.float32) * (t + 1)
+                x.terminals[sl] = (np.arange(apb) % (t + 2) == 0).astype(np.float32)
+                x.upload(b)
+                x.step(pl, b, b)
+                got = x.actions[sl, 0].copy()
+                lp = dev_floats(x.device_ptr(tr.LOGPROBS), nbuf * apb)[sl]
+                vals = dev_floats(x.device_ptr(tr.VALUES), nbuf * apb)[sl]
+                assert np.array_equal(dev_floats(x.device_ptr(tr.REWARDS), nbuf * apb)[sl], x.rewards[sl])
+                assert np.array_equal(dev_floats(x.device_ptr(tr.TERMINALS), nbuf * apb)[sl], x.terminals[sl])
+                d_rows = pl.to_device(rows)
+                a, l, v = pl.rollout_step(d_rows, apb, seed=555, step=expect)
+                torch.cuda.synchronize()
+                assert np.array_equal(got, a.cpu().numpy()), (t, b)
+                assert np.array_equal(lp, l.cpu().numpy()), (t, b)
+                assert np.array_equal(vals, v.cpu().numpy()), (t, b)
+                expect += 1
+                assert int(step.item()) == expect
+    finally:
+        x.close()
+        pl.close()
+
+
+def test_transport_rejects_bad_shapes(cuda):
+    with pytest.raises(Exception, match="do not split"):
+        tr.RolloutTransport(100, 3, 64)
+    dm = dims.tiny()
+    pl = trainer.create_pufferl({"dims": dm, "sync_free": True, "train": dict(minibatch_size=16)})
+    x = tr.RolloutTransport(32, 2, dm.obs_size + 4)
+    try:
+        step = torch.zeros(1, dtype=torch.int64, device="cuda")
+        with pytest.raises(Exception, match="observation rows"):
+            x.capture_rollout(pl, 0, 0, 1, step)
+    finally:
+        x.close()
+        pl.close()

@@ -376,7 +376,7 @@ def main():
     gemm_s = ms.value / 1e3
     achieved = useful / gemm_s / 1e12
     peak = BF16_MFMA_PEAK_TFLOPS if bf16 else FP32_MFMA_PEAK_TFLOPS
-    kname = "gemm_bf16_kernel" if bf16 else "gemm_f32_dma_kernel + gemm_f32_kernel"
+    kname = "gemm_bf16_k16_kernel + gemm_bf16_kernel" if bf16 else "gemm_f32_dma_kernel + gemm_f32_kernel"
     roof = dict(bound="mfma", kernel=f"{kname} (all launches: trunk, token, option and head GEMMs)",
                 achieved=round(achieved, 3), peak=peak, unit="TFLOP/s",
                 frac=round(achieved / peak, 4),
@@ -388,6 +388,17 @@ def main():
                 executed_tflops=round(exec_flops.value / gemm_s / 1e12, 3),
                 useful_tflop_per_step=round(useful / K / 1e12, 4),
                 mean_valid_seq=round(float(np.mean(lv)), 2))
+    if bf16:
+        # The products' arithmetic intensity (useful flops over the fp32
+        # operand / output bytes, ~79 flop/B) is far below the bf16 ridge
+        # point (peak flops / peak bandwidth = 312 flop/B): the bf16 GEMMs are
+        # HBM-bound, so the bound roofline is bytes over time; the MFMA
+        # fraction stays beside it.
+        gbs = abytes / gemm_s / 1e9
+        roof.update(bound="hbm", achieved=round(gbs, 1), peak=HBM_PEAK_GBS, unit="GB/s",
+                    frac=round(gbs / HBM_PEAK_GBS, 4), mfma_tflops=round(achieved, 3), mfma_peak=peak,
+                    mfma_frac=round(achieved / peak, 4), intensity_flop_per_byte=round(useful / abytes, 1),
+                    ridge_flop_per_byte=round(peak * 1e12 / (HBM_PEAK_GBS * 1e9), 1))
     line = {
         "metric": ("PPO minibatch step obs/sec (fwd+bwd+Muon) @B=512" if muon else METRIC) if not bf16
                   else "PPO minibatch step obs/sec (fwd+bwd+Adam) @B=2048, bf16 GEMM products",

@@ -1050,12 +1050,16 @@ int pt_gemm(const GemmArgs& g0, float* ws, long ws_floats, hipStream_t s) {
     const int bk = bf && !g.dma ? BK2 : BK;
     const int tm = pt_cdiv(g.M, BM), tn = pt_cdiv(g.N, BN);
     const int tiles = tm * tn;
-    // split K when the output is too small to fill the chip and K is long
+    // split K when the output is too small to fill the chip: long K in chunks
+    // of >= 16 k-steps; short K (a few hundred rows, e.g. the weight gradients
+    // of the per-sample MLPs at K = B) in chunks of >= 4 k-steps, so a handful
+    // of tiles does not walk its whole K one stage at a time on a few CUs
     int splits = 1;
     const int target = 512;
-    if (tiles < target && g.K >= 4 * bk * 16) {
+    if (tiles < target && g.K >= 2 * bk * 4) {
         splits = pt_cdiv(target, tiles);
-        int max_splits = g.K / (bk * 16);
+        const int min_steps = g.K >= 4 * bk * 16 ? 16 : 4;
+        int max_splits = g.K / (bk * min_steps);
         if (splits > max_splits) splits = max_splits;
         if (splits < 1) splits = 1;
     }

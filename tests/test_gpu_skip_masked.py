@@ -54,8 +54,11 @@ def test_skip_masked_matches_full_scorer(dm, sync_free, cuda):
     l0, w0, f0, a0, p0, v0 = _run(dm, B, blob, rows, inp, lists, False, sync_free)
     l1, w1, f1, a1, p1, v1 = _run(dm, B, blob, rows, inp, lists, True, sync_free)
     # Adam's first steps are lr * sign(g): elements whose gradient is rounding
-    # noise may step the other way (at most 2 * lr per step)
-    assert rel_l2(w1, w0) < 1e-5
+    # noise may step the other way (at most 2 * lr per step).  The two paths
+    # run GEMMs of different row counts (so different split-K sums); one
+    # flipped element alone is ~5e-5 of the weights' L2 norm here, so the L2
+    # bound allows a few and the per-element bound caps each
+    assert rel_l2(w1, w0) < 1e-4
     assert np.abs(w1 - w0).max() <= 2 * 1e-3 * len(lists) + 1e-6
     for k in ("policy_loss", "value_loss", "entropy", "total_loss"):
         assert abs(l1[k] - l0[k]) <= 1e-5 * max(1.0, abs(l0[k])), k

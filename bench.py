@@ -28,8 +28,8 @@ own model variant (frozen layout: 160 tokens, d256/H8/FFN512, static-table
 card vectors, oracle critic over 218 positions, aux losses);
 ``--workload replay`` times the rollout-side steps around the training step
 (negamax advantage, prioritized replay draw, train-layout transposes);
-``--workload bf16`` times the training step at B = 2048 with bf16 GEMM
-products (fp32 accumulation and everything else fp32).
+``--workload bf16`` times the training step at B = 2048 with the GEMMs' and
+attention's products in bf16 (fp32 accumulation; everything else fp32).
 """
 import argparse
 import ctypes
@@ -401,7 +401,7 @@ def main():
                     ridge_flop_per_byte=round(peak * 1e12 / (HBM_PEAK_GBS * 1e9), 1))
     line = {
         "metric": ("PPO minibatch step obs/sec (fwd+bwd+Muon) @B=512" if muon else METRIC) if not bf16
-                  else "PPO minibatch step obs/sec (fwd+bwd+Adam) @B=2048, bf16 GEMM products",
+                  else "PPO minibatch step obs/sec (fwd+bwd+Adam) @B=2048, bf16 GEMM and attention products",
         "value": round(B * K / sec, 2), "unit": "obs/s", "n_gpus": 1,
         "steps": K, "warmup": args.warmup, "ms_per_step": round(sec * 1e3 / K, 4),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16" if bf16 else "fp32",
@@ -409,8 +409,8 @@ def main():
         "config": {"workload": f"PPO minibatch step (fwd+bwd+PPO loss+grad-norm clip+Adam) on {B} rows of "
                                "a 16384-row HBM-resident rollout; 96 tokens + READOUT, 32 token features, "
                                "card ids [0,2048), d256/H4/FFN1024/4 layers, 64 options, blind value head"
-                               + ("; bf16 GEMM operands, fp32 accumulation, LayerNorm, attention, loss, "
-                                  "master weights and Adam state" if bf16 else ""),
+                               + ("; bf16 GEMM and attention operands, fp32 accumulation, LayerNorm, "
+                                  "softmax, loss, master weights and Adam state" if bf16 else ""),
                    "minibatch": B, "rollout_rows": R, "seq_len": dm.l_tok + 1,
                    "parallelism": "single GPU",
                    "compact_rows": "device count, no host read-back" if (args.sync_free or graph)

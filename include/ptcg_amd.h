@@ -102,10 +102,10 @@ void ptcg_model_free(PtcgModel* m);
 int ptcg_model_set_static(PtcgModel* m, const float* card_static, const float* att_static,
                           const float* card_text, const float* att_text, const float* skill_text,
                           const int32_t* card_attacks, const int32_t* card_skills);
-/* GEMM product precision (the reference's USE_BF16 switch, compile-time
- * there): 0 = fp32 (default), 1 = bf16 operands with fp32 accumulation.
- * LayerNorm, attention, softmax, loss, weights and optimizer state stay
- * fp32 in both.                                                           */
+/* Product precision (the reference's USE_BF16 switch, compile-time there):
+ * 0 = fp32 (default), 1 = the GEMMs' and attention's products on bf16 MFMA
+ * (operands rounded to bf16, fp32 accumulation).  LayerNorm, softmax, loss,
+ * weights and optimizer state stay fp32 in both.                          */
 int ptcg_model_set_precision(PtcgModel* m, int prec);
 /* Compact-layout row count handling (blind-critic models, whose trunk runs
  * only READOUT, valid-token and pointer-target rows).  0 (default): the

@@ -85,6 +85,15 @@ int ptcg_kernel_attention_fwd(const float* qkv, const float* keep, float* ctx, f
 int ptcg_kernel_attention_bwd(const float* qkv, const float* keep, const float* ctx,
                               const float* lse, const float* dctx, float* dqkv,
                               int N, int L, int H, int Dh, void* stream);
+/* the same with bf16 products (the reference's USE_BF16 attention, whose
+ * batched products run on precision_t = bf16): S, P.V and the backward's
+ * products on v_mfma_f32_16x16x16_bf16 with operands rounded to bf16 (RNE),
+ * softmax, log-sum-exp and accumulation in fp32.                          */
+int ptcg_kernel_attention_fwd_bf16(const float* qkv, const float* keep, float* ctx, float* lse,
+                                   int N, int L, int H, int Dh, void* stream);
+int ptcg_kernel_attention_bwd_bf16(const float* qkv, const float* keep, const float* ctx,
+                                   const float* lse, const float* dctx, float* dqkv,
+                                   int N, int L, int H, int Dh, void* stream);
 
 /* which attention kernels a row length takes: bit 0 forward (MFMA), bit 1
  * backward with the L x L dS tile parked in LDS (Lp <= 128), bit 2 backward

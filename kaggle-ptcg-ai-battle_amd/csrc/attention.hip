@@ -1,5 +1,5 @@
 // Masked multi-head self-attention over padded entity tokens, fused per
-// (sample, head), fp32.
+// (sample, head); fp32, or bf16 products with fp32 softmax and accumulation.
 //
 // Replaces the reference's chain pt_qkv_split -> batched QK^T GEMM ->
 // pt_attn_softmax_fwd -> batched PV GEMM -> pt_heads_merge and its backward
@@ -30,7 +30,29 @@ namespace {
 // 8 waves per workgroup: one 16-row stripe each (Lp <= 128), two waves per
 // SIMD to overlap LDS reads with MFMAs.
 
-template <int DH, int NT>   // NT = Lp / 16 key (and query) tiles
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+
+// Four fp32 k-steps of one 16x16 product, lane (li, lq) supplying a[e] and
+// b[e] for logical k = 4e + lq of the 16-k group: four
+// v_mfma_f32_16x16x4_f32, or (BF, bf16 products with fp32 accumulation) one
+// v_mfma_f32_16x16x16_bf16 on the same operands rounded to bf16 (RNE).  Its
+// lane group lq, element e is k = 4 lq + e in the hardware's order — the
+// same four k per lane, and A and B use the same map, so both forms sum the
+// same products.
+template <bool BF>
+__device__ __forceinline__ floatx4 mfma4(const float (&a)[4], const float (&b)[4], floatx4 c) {
+    if constexpr (BF) {
+        const bf16x4 ah = {(__bf16)a[0], (__bf16)a[1], (__bf16)a[2], (__bf16)a[3]};
+        const bf16x4 bh = {(__bf16)b[0], (__bf16)b[1], (__bf16)b[2], (__bf16)b[3]};
+        return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(ah, bh, c, 0, 0, 0);
+    } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) c = __builtin_amdgcn_mfma_f32_16x16x4f32(a[e], b[e], c, 0, 0, 0);
+        return c;
+    }
+}
+
+template <int DH, int NT, bool BF>   // NT = Lp / 16 key (and query) tiles
 __global__ __launch_bounds__(512) void attn_fwd_mfma_kernel(const float* __restrict__ qkv,
         const float* __restrict__ keep, float* __restrict__ ctx, float* __restrict__ lse,
         int Lfix, int H, float scale, const int* __restrict__ coff) {
@@ -86,9 +108,15 @@ __global__ __launch_bounds__(512) void attn_fwd_mfma_kernel(const float* __restr
                 sc[j] = floatx4{0.f, 0.f, 0.f, 0.f};
                 if (c0 + j < ntl) {
 #pragma unroll
-                    for (int kk = 0; kk < DH / 4; ++kk)
-                        sc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(Ks[(16 * (c0 + j) + li) * SK + 4 * kk + lq], qb[kk],
-                                                                     sc[j], 0, 0, 0);
+                    for (int kq = 0; kq < DH / 16; ++kq) {
+                        float a[4], b[4];
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            a[e] = Ks[(16 * (c0 + j) + li) * SK + 4 * (4 * kq + e) + lq];
+                            b[e] = qb[4 * kq + e];
+                        }
+                        sc[j] = mfma4<BF>(a, b, sc[j]);
+                    }
                 }
             }
             // sc[j][r] = S^T[key = 16(c0+j) + 4lq + r][query = q0 + li]
@@ -132,12 +160,13 @@ __global__ __launch_bounds__(512) void attn_fwd_mfma_kernel(const float* __restr
 #pragma unroll
             for (int j = 0; j < CH; ++j) {
                 if (c0 + j < ntl) {
+                    const float a[4] = {sc[j][0], sc[j][1], sc[j][2], sc[j][3]};
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        const float* vr = &Vs[(16 * (c0 + j) + 4 * lq + r) * SK + li];
+                    for (int dt = 0; dt < DH / 16; ++dt) {
+                        float b[4];
 #pragma unroll
-                        for (int dt = 0; dt < DH / 16; ++dt)
-                            o[dt] = __builtin_amdgcn_mfma_f32_16x16x4f32(sc[j][r], vr[16 * dt], o[dt], 0, 0, 0);
+                        for (int r = 0; r < 4; ++r) b[r] = Vs[(16 * (c0 + j) + 4 * lq + r) * SK + li + 16 * dt];
+                        o[dt] = mfma4<BF>(a, b, o[dt]);
                     }
                 }
             }
@@ -162,7 +191,7 @@ __global__ __launch_bounds__(512) void attn_fwd_mfma_kernel(const float* __restr
 // dS = P (dP - rowsum(dO o O)), accumulates dV += P^T dO and dK += dS^T Q
 // (register-r trick again, now over queries), and parks dS*scale in LDS.
 // Pass B walks query stripes: dQ = dS K from LDS.
-template <int DH, int NT>
+template <int DH, int NT, bool BF>
 __global__ __launch_bounds__(512) void attn_bwd_mfma_kernel(const float* __restrict__ qkv,
         const float* __restrict__ keep, const float* __restrict__ ctx,
         const float* __restrict__ lse, const float* __restrict__ dctx,
@@ -236,10 +265,18 @@ __global__ __launch_bounds__(512) void attn_bwd_mfma_kernel(const float* __restr
         for (int qt = 0; qt < ntl; ++qt) {
             floatx4 s = floatx4{0.f, 0.f, 0.f, 0.f}, dp = s;
 #pragma unroll
-            for (int kk = 0; kk < DH / 4; ++kk) {
-                const int a_off = (16 * qt + li) * SQ + 4 * kk + lq;
-                s = __builtin_amdgcn_mfma_f32_16x16x4f32(Qs[a_off], kr[kk], s, 0, 0, 0);
-                dp = __builtin_amdgcn_mfma_f32_16x16x4f32(dOs[a_off], vr[kk], dp, 0, 0, 0);
+            for (int kq = 0; kq < DH / 16; ++kq) {
+                float qa[4], da[4], kb4[4], vb4[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int a_off = (16 * qt + li) * SQ + 4 * (4 * kq + e) + lq;
+                    qa[e] = Qs[a_off];
+                    da[e] = dOs[a_off];
+                    kb4[e] = kr[4 * kq + e];
+                    vb4[e] = vr[4 * kq + e];
+                }
+                s = mfma4<BF>(qa, kb4, s);
+                dp = mfma4<BF>(da, vb4, dp);
             }
             // s[r] = S[q = 16qt + 4lq + r][key = k0 + li]
             float p[4], ds[4];
@@ -251,13 +288,16 @@ __global__ __launch_bounds__(512) void attn_bwd_mfma_kernel(const float* __restr
                 dSs[q * SS + k0 + li] = ds[r] * scale;
             }
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int qrow = (16 * qt + 4 * lq + r);
+            for (int dt = 0; dt < DH / 16; ++dt) {
+                float ob[4], qb4[4];
 #pragma unroll
-                for (int dt = 0; dt < DH / 16; ++dt) {
-                    dv[dt] = __builtin_amdgcn_mfma_f32_16x16x4f32(p[r], dOs[qrow * SQ + 16 * dt + li], dv[dt], 0, 0, 0);
-                    dk[dt] = __builtin_amdgcn_mfma_f32_16x16x4f32(ds[r], Qs[qrow * SQ + 16 * dt + li], dk[dt], 0, 0, 0);
+                for (int r = 0; r < 4; ++r) {
+                    const int qrow = 16 * qt + 4 * lq + r;
+                    ob[r] = dOs[qrow * SQ + 16 * dt + li];
+                    qb4[r] = Qs[qrow * SQ + 16 * dt + li];
                 }
+                dv[dt] = mfma4<BF>(p, ob, dv[dt]);
+                dk[dt] = mfma4<BF>(ds, qb4, dk[dt]);
             }
         }
         // dv[dt][r] = dV[k0 + 4lq + r][16dt + li]
@@ -281,12 +321,17 @@ __global__ __launch_bounds__(512) void attn_bwd_mfma_kernel(const float* __restr
         floatx4 dq[DH / 16];
 #pragma unroll
         for (int dt = 0; dt < DH / 16; ++dt) dq[dt] = floatx4{0.f, 0.f, 0.f, 0.f};
-        for (int kk = 0; kk < ntl * 4; ++kk) {
-            const float a = dSs[(16 * qt + li) * SS + 4 * kk + lq];
-            const float* kr = &Ks[(4 * kk + lq) * SKB + li];
+        for (int kq = 0; kq < ntl; ++kq) {
+            float a[4];
 #pragma unroll
-            for (int dt = 0; dt < DH / 16; ++dt)
-                dq[dt] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, kr[16 * dt], dq[dt], 0, 0, 0);
+            for (int e = 0; e < 4; ++e) a[e] = dSs[(16 * qt + li) * SS + 4 * (4 * kq + e) + lq];
+#pragma unroll
+            for (int dt = 0; dt < DH / 16; ++dt) {
+                float b[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) b[e] = Ks[(4 * (4 * kq + e) + lq) * SKB + li + 16 * dt];
+                dq[dt] = mfma4<BF>(a, b, dq[dt]);
+            }
         }
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
@@ -306,7 +351,7 @@ __global__ __launch_bounds__(512) void attn_bwd_mfma_kernel(const float* __restr
 // pass B walks query stripes and recomputes S^T = K Q^T and dP^T = V dO^T
 // per key tile (queries on lanes), then dQ += dS K with the register-r key
 // permutation.  Costs one more S and dP evaluation than the stored variant.
-template <int DH, int NT>
+template <int DH, int NT, bool BF>
 __global__ __launch_bounds__(512) void attn_bwd_mfma_rc_kernel(const float* __restrict__ qkv,
         const float* __restrict__ keep, const float* __restrict__ ctx,
         const float* __restrict__ lse, const float* __restrict__ dctx,
@@ -378,10 +423,18 @@ __global__ __launch_bounds__(512) void attn_bwd_mfma_rc_kernel(const float* __re
         for (int qt = 0; qt < NT; ++qt) {
             floatx4 s = floatx4{0.f, 0.f, 0.f, 0.f}, dp = s;
 #pragma unroll
-            for (int kk = 0; kk < DH / 4; ++kk) {
-                const int a_off = (16 * qt + li) * SQ + 4 * kk + lq;
-                s = __builtin_amdgcn_mfma_f32_16x16x4f32(Qs[a_off], kr[kk], s, 0, 0, 0);
-                dp = __builtin_amdgcn_mfma_f32_16x16x4f32(dOs[a_off], vr[kk], dp, 0, 0, 0);
+            for (int kq = 0; kq < DH / 16; ++kq) {
+                float qa[4], da[4], kb4[4], vb4[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int a_off = (16 * qt + li) * SQ + 4 * (4 * kq + e) + lq;
+                    qa[e] = Qs[a_off];
+                    da[e] = dOs[a_off];
+                    kb4[e] = kr[4 * kq + e];
+                    vb4[e] = vr[4 * kq + e];
+                }
+                s = mfma4<BF>(qa, kb4, s);
+                dp = mfma4<BF>(da, vb4, dp);
             }
             float p[4], ds[4];
 #pragma unroll
@@ -391,13 +444,16 @@ __global__ __launch_bounds__(512) void attn_bwd_mfma_rc_kernel(const float* __re
                 ds[r] = p[r] * (dp[r] - Dv[q]);
             }
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int qrow = 16 * qt + 4 * lq + r;
+            for (int dt = 0; dt < DH / 16; ++dt) {
+                float ob[4], qb4[4];
 #pragma unroll
-                for (int dt = 0; dt < DH / 16; ++dt) {
-                    dv[dt] = __builtin_amdgcn_mfma_f32_16x16x4f32(p[r], dOs[qrow * SQ + 16 * dt + li], dv[dt], 0, 0, 0);
-                    dk[dt] = __builtin_amdgcn_mfma_f32_16x16x4f32(ds[r], Qs[qrow * SQ + 16 * dt + li], dk[dt], 0, 0, 0);
+                for (int r = 0; r < 4; ++r) {
+                    const int qrow = 16 * qt + 4 * lq + r;
+                    ob[r] = dOs[qrow * SQ + 16 * dt + li];
+                    qb4[r] = Qs[qrow * SQ + 16 * dt + li];
                 }
+                dv[dt] = mfma4<BF>(p, ob, dv[dt]);
+                dk[dt] = mfma4<BF>(ds, qb4, dk[dt]);
             }
         }
 #pragma unroll
@@ -430,21 +486,33 @@ __global__ __launch_bounds__(512) void attn_bwd_mfma_rc_kernel(const float* __re
         for (int J = 0; J < NT; ++J) {
             floatx4 st = floatx4{0.f, 0.f, 0.f, 0.f}, dpt = st;
 #pragma unroll
-            for (int kk = 0; kk < DH / 4; ++kk) {
-                const int a_off = (16 * J + li) * SQ + 4 * kk + lq;
-                st = __builtin_amdgcn_mfma_f32_16x16x4f32(Ks[a_off], qb[kk], st, 0, 0, 0);
-                dpt = __builtin_amdgcn_mfma_f32_16x16x4f32(Vs[a_off], db[kk], dpt, 0, 0, 0);
+            for (int kq = 0; kq < DH / 16; ++kq) {
+                float ka[4], va[4], qb4[4], db4[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const int a_off = (16 * J + li) * SQ + 4 * (4 * kq + e) + lq;
+                    ka[e] = Ks[a_off];
+                    va[e] = Vs[a_off];
+                    qb4[e] = qb[4 * kq + e];
+                    db4[e] = db[4 * kq + e];
+                }
+                st = mfma4<BF>(ka, qb4, st);
+                dpt = mfma4<BF>(va, db4, dpt);
             }
             // st[r] = S^T[key = 16J + 4lq + r][query = q0 + li]
+            float dst[4];
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int key = 16 * J + 4 * lq + r;
                 const float pt = kf[key] > 0.f ? expf(st[r] * scale - lsq) : 0.f;
-                const float dst = pt * (dpt[r] - dvq) * scale;
-                const float* kr = &Ks[key * SQ + li];
+                dst[r] = pt * (dpt[r] - dvq) * scale;
+            }
 #pragma unroll
-                for (int dt = 0; dt < DH / 16; ++dt)
-                    dq[dt] = __builtin_amdgcn_mfma_f32_16x16x4f32(dst, kr[16 * dt], dq[dt], 0, 0, 0);
+            for (int dt = 0; dt < DH / 16; ++dt) {
+                float b[4];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) b[r] = Ks[(16 * J + 4 * lq + r) * SQ + li + 16 * dt];
+                dq[dt] = mfma4<BF>(dst, b, dq[dt]);
             }
         }
 #pragma unroll
@@ -470,37 +538,37 @@ size_t bwd_mfma_lds_bytes(int LP, int DH) {
     return sizeof(float) * ((size_t)LP * (DH + 4) * 2 + (size_t)LP * (DH + 16) + (size_t)LP * (LP + 4) + 3 * (size_t)LP);
 }
 
-template <int DH, int NT>
+template <int DH, int NT, bool BF>
 int launch_fwd_mfma(const float* qkv, const float* keep, float* ctx, float* lse, int N, int L, int H,
                     hipStream_t s, const int* coff) {
     const size_t lds = fwd_mfma_lds_bytes(NT * 16, DH);
-    PT_HIP(hipFuncSetAttribute((const void*)attn_fwd_mfma_kernel<DH, NT>,
+    PT_HIP(hipFuncSetAttribute((const void*)attn_fwd_mfma_kernel<DH, NT, BF>,
                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-    hipLaunchKernelGGL((attn_fwd_mfma_kernel<DH, NT>), dim3(N * H), dim3(512), lds, s, qkv, keep, ctx, lse,
+    hipLaunchKernelGGL((attn_fwd_mfma_kernel<DH, NT, BF>), dim3(N * H), dim3(512), lds, s, qkv, keep, ctx, lse,
                        L, H, 1.0f / sqrtf((float)DH), coff);
     PT_LAUNCH_CHECK();
     return PTCG_OK;
 }
 
-template <int DH, int NT>
+template <int DH, int NT, bool BF>
 int launch_bwd_rc(const float* qkv, const float* keep, const float* ctx, const float* lse,
                   const float* dctx, float* dqkv, int N, int L, int H, hipStream_t s, const int* coff) {
     const size_t lds = bwd_rc_lds_bytes(NT * 16, DH);
-    PT_HIP(hipFuncSetAttribute((const void*)attn_bwd_mfma_rc_kernel<DH, NT>,
+    PT_HIP(hipFuncSetAttribute((const void*)attn_bwd_mfma_rc_kernel<DH, NT, BF>,
                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-    hipLaunchKernelGGL((attn_bwd_mfma_rc_kernel<DH, NT>), dim3(N * H), dim3(512), lds, s, qkv, keep, ctx,
+    hipLaunchKernelGGL((attn_bwd_mfma_rc_kernel<DH, NT, BF>), dim3(N * H), dim3(512), lds, s, qkv, keep, ctx,
                        lse, dctx, dqkv, L, H, 1.0f / sqrtf((float)DH), coff);
     PT_LAUNCH_CHECK();
     return PTCG_OK;
 }
 
-template <int DH, int NT>
+template <int DH, int NT, bool BF>
 int launch_bwd_mfma(const float* qkv, const float* keep, const float* ctx, const float* lse,
                     const float* dctx, float* dqkv, int N, int L, int H, hipStream_t s, const int* coff) {
     const size_t lds = bwd_mfma_lds_bytes(NT * 16, DH);
-    PT_HIP(hipFuncSetAttribute((const void*)attn_bwd_mfma_kernel<DH, NT>,
+    PT_HIP(hipFuncSetAttribute((const void*)attn_bwd_mfma_kernel<DH, NT, BF>,
                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-    hipLaunchKernelGGL((attn_bwd_mfma_kernel<DH, NT>), dim3(N * H), dim3(512), lds, s, qkv, keep, ctx, lse,
+    hipLaunchKernelGGL((attn_bwd_mfma_kernel<DH, NT, BF>), dim3(N * H), dim3(512), lds, s, qkv, keep, ctx, lse,
                        dctx, dqkv, L, H, 1.0f / sqrtf((float)DH), coff);
     PT_LAUNCH_CHECK();
     return PTCG_OK;
@@ -535,7 +603,8 @@ int pt_attn_supported(int L, int DH) {
     return (fwd_tiles(L, DH) && (bwd_store_tiles(L, DH) || bwd_rc_tiles(L, DH))) ? 1 : 0;
 }
 
-#define PT_NT_CASE(DH, N, CALL, ...) case N: return CALL<DH, N>(__VA_ARGS__);
+// (used inside the BF-templated dispatchers below)
+#define PT_NT_CASE(DH, N, CALL, ...) case N: return CALL<DH, N, BF>(__VA_ARGS__);
 #define PT_NT_SWITCH8(DH, NT, CALL, ...)                                                              \
     switch (NT) {                                                                                     \
         PT_NT_CASE(DH, 1, CALL, __VA_ARGS__) PT_NT_CASE(DH, 2, CALL, __VA_ARGS__)                     \
@@ -553,13 +622,13 @@ int pt_attn_supported(int L, int DH) {
         default: break;                                                                               \
     }
 
-int pt_attn_fwd(const float* qkv, const float* keep, float* ctx, float* lse, int N, int L, int H,
-                int DH, hipStream_t s, const int* coff) {
-    PT_REQUIRE(pt_attn_supported(L, DH), "attention: L=%d Dh=%d exceeds the fused kernels' LDS budget", L, DH);
+template <bool BF>
+static int attn_fwd_dispatch(const float* qkv, const float* keep, float* ctx, float* lse, int N, int L, int H,
+                             int DH, hipStream_t s, const int* coff) {
     const int nt = fwd_tiles(L, DH);
     if (nt && DH == 64) {
         PT_NT_SWITCH8(64, nt, launch_fwd_mfma, qkv, keep, ctx, lse, N, L, H, s, coff)
-        if (nt == 9) return launch_fwd_mfma<64, 9>(qkv, keep, ctx, lse, N, L, H, s, coff);
+        if (nt == 9) return launch_fwd_mfma<64, 9, BF>(qkv, keep, ctx, lse, N, L, H, s, coff);
     } else if (nt) {
         PT_NT_SWITCH8(32, nt, launch_fwd_mfma, qkv, keep, ctx, lse, N, L, H, s, coff)
         PT_NT_SWITCH_HI(32, nt, launch_fwd_mfma, qkv, keep, ctx, lse, N, L, H, s, coff)
@@ -567,9 +636,10 @@ int pt_attn_fwd(const float* qkv, const float* keep, float* ctx, float* lse, int
     PT_REQUIRE(false, "attention: no kernel for L=%d Dh=%d", L, DH);
 }
 
-int pt_attn_bwd(const float* qkv, const float* keep, const float* ctx, const float* lse,
-                const float* dctx, float* dqkv, int N, int L, int H, int DH, hipStream_t s, const int* coff) {
-    PT_REQUIRE(pt_attn_supported(L, DH), "attention bwd: L=%d Dh=%d exceeds the fused kernels' LDS budget", L, DH);
+template <bool BF>
+static int attn_bwd_dispatch(const float* qkv, const float* keep, const float* ctx, const float* lse,
+                             const float* dctx, float* dqkv, int N, int L, int H, int DH, hipStream_t s,
+                             const int* coff) {
     int nt = bwd_store_tiles(L, DH);
     if (nt) {
         if (DH == 64) { PT_NT_SWITCH8(64, nt, launch_bwd_mfma, qkv, keep, ctx, lse, dctx, dqkv, N, L, H, s, coff) }
@@ -578,12 +648,27 @@ int pt_attn_bwd(const float* qkv, const float* keep, const float* ctx, const flo
     nt = bwd_rc_tiles(L, DH);
     if (nt && DH == 64) {
         PT_NT_SWITCH8(64, nt, launch_bwd_rc, qkv, keep, ctx, lse, dctx, dqkv, N, L, H, s, coff)
-        if (nt == 9) return launch_bwd_rc<64, 9>(qkv, keep, ctx, lse, dctx, dqkv, N, L, H, s, coff);
+        if (nt == 9) return launch_bwd_rc<64, 9, BF>(qkv, keep, ctx, lse, dctx, dqkv, N, L, H, s, coff);
     } else if (nt) {
         PT_NT_SWITCH8(32, nt, launch_bwd_rc, qkv, keep, ctx, lse, dctx, dqkv, N, L, H, s, coff)
         PT_NT_SWITCH_HI(32, nt, launch_bwd_rc, qkv, keep, ctx, lse, dctx, dqkv, N, L, H, s, coff)
     }
     PT_REQUIRE(false, "attention bwd: no kernel for L=%d Dh=%d", L, DH);
+}
+
+int pt_attn_fwd(const float* qkv, const float* keep, float* ctx, float* lse, int N, int L, int H,
+                int DH, hipStream_t s, const int* coff, int prec) {
+    PT_REQUIRE(pt_attn_supported(L, DH), "attention: L=%d Dh=%d exceeds the fused kernels' LDS budget", L, DH);
+    return prec ? attn_fwd_dispatch<true>(qkv, keep, ctx, lse, N, L, H, DH, s, coff)
+                : attn_fwd_dispatch<false>(qkv, keep, ctx, lse, N, L, H, DH, s, coff);
+}
+
+int pt_attn_bwd(const float* qkv, const float* keep, const float* ctx, const float* lse,
+                const float* dctx, float* dqkv, int N, int L, int H, int DH, hipStream_t s, const int* coff,
+                int prec) {
+    PT_REQUIRE(pt_attn_supported(L, DH), "attention bwd: L=%d Dh=%d exceeds the fused kernels' LDS budget", L, DH);
+    return prec ? attn_bwd_dispatch<true>(qkv, keep, ctx, lse, dctx, dqkv, N, L, H, DH, s, coff)
+                : attn_bwd_dispatch<false>(qkv, keep, ctx, lse, dctx, dqkv, N, L, H, DH, s, coff);
 }
 
 // Which kernels a shape takes (for tests): bit 0 forward, bit 1 backward

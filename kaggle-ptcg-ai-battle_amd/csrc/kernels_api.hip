@@ -108,6 +108,19 @@ extern "C" int ptcg_kernel_attention_fwd(const float* qkv, const float* keep, fl
     return pt_attn_fwd(qkv, keep, ctx, lse, N, L, H, Dh, (hipStream_t)stream);
 }
 
+extern "C" int ptcg_kernel_attention_fwd_bf16(const float* qkv, const float* keep, float* ctx, float* lse,
+                                              int N, int L, int H, int Dh, void* stream) {
+    PT_REQUIRE(qkv && keep && ctx && lse, "kernel_attention_fwd_bf16: null buffer");
+    return pt_attn_fwd(qkv, keep, ctx, lse, N, L, H, Dh, (hipStream_t)stream, nullptr, 1);
+}
+
+extern "C" int ptcg_kernel_attention_bwd_bf16(const float* qkv, const float* keep, const float* ctx,
+                                              const float* lse, const float* dctx, float* dqkv, int N,
+                                              int L, int H, int Dh, void* stream) {
+    PT_REQUIRE(qkv && keep && ctx && lse && dctx && dqkv, "kernel_attention_bwd_bf16: null buffer");
+    return pt_attn_bwd(qkv, keep, ctx, lse, dctx, dqkv, N, L, H, Dh, (hipStream_t)stream, nullptr, 1);
+}
+
 int pt_attn_path(int L, int DH);
 extern "C" int ptcg_kernel_attention_path(int L, int Dh) { return pt_attn_path(L, Dh); }
 

@@ -46,11 +46,13 @@ int pt_ln_bwd(const float* dy, long lddy, const float* x, long ldx, const float*
 int pt_attn_supported(int L, int DH);
 // coff (nullable): sample n's rows are [coff[n], coff[n+1]) (length <= L);
 // else rows n*L .. n*L+L-1.  lse is laid out (N, H, L) either way.
+// prec 1: the products (S, P.V and the backward's) on bf16 MFMA with
+// operands rounded to bf16, softmax and accumulation in fp32.
 int pt_attn_fwd(const float* qkv, const float* keep, float* ctx, float* lse, int N, int L, int H,
-                int DH, hipStream_t s, const int* coff = nullptr);
+                int DH, hipStream_t s, const int* coff = nullptr, int prec = 0);
 int pt_attn_bwd(const float* qkv, const float* keep, const float* ctx, const float* lse,
                 const float* dctx, float* dqkv, int N, int L, int H, int DH, hipStream_t s,
-                const int* coff = nullptr);
+                const int* coff = nullptr, int prec = 0);
 long pt_ppo_partial_floats(int n);
 int pt_ppo_loss(const float* out, int n, int A, const float* mask, long mask_stride,
                 const int32_t* idx, const float* actions, const float* old_logp,

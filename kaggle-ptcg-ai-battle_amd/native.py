@@ -182,6 +182,12 @@ _SIGS = {
     "ptcg_kernel_attention_bwd": (ctypes.c_int, [c_void_p, c_void_p, c_void_p, c_void_p,
                                                  c_void_p, c_void_p, ctypes.c_int, ctypes.c_int,
                                                  ctypes.c_int, ctypes.c_int, c_void_p]),
+    "ptcg_kernel_attention_fwd_bf16": (ctypes.c_int, [c_void_p, c_void_p, c_void_p, c_void_p,
+                                                      ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                                      ctypes.c_int, c_void_p]),
+    "ptcg_kernel_attention_bwd_bf16": (ctypes.c_int, [c_void_p, c_void_p, c_void_p, c_void_p,
+                                                      c_void_p, c_void_p, ctypes.c_int, ctypes.c_int,
+                                                      ctypes.c_int, ctypes.c_int, c_void_p]),
 }
 
 _lib = None

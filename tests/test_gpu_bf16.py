@@ -1,4 +1,5 @@
-"""Mixed precision (bf16 GEMM products, fp32 everything else) against the
+"""Mixed precision (bf16 GEMM and attention products, fp32 LayerNorm,
+softmax, loss and accumulation) against the
 fp32 oracle.
 
 Tolerances (written here, per the config's proposal): on legal options the

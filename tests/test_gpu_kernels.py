@@ -216,6 +216,35 @@ def test_attention_fwd_bwd(N, L, H, Dh, path, cuda):
     assert torch.all(gk[:, :, 1:][~keep] == 0)
 
 
+@pytest.mark.parametrize("N,L,H,Dh,path", ATTN_CASES, ids=lambda *a: None)
+def test_attention_bf16_products(N, L, H, Dh, path, cuda):
+    """bf16 products (operands rounded to bf16, fp32 softmax and sums)
+    against the float64 reference: context, log-sum-exp and dqkv within bf16
+    tolerances (8-bit mantissa, ~4e-3 relative per rounded operand), and
+    further from it than the fp32 kernels are (the products really are bf16);
+    masked keys still receive exactly zero K / V gradient."""
+    g = torch.Generator().manual_seed(N * L + H + 7)
+    D = H * Dh
+    qkv = torch.randn(N, L, 3 * D, generator=g).double().requires_grad_()
+    keep = torch.rand(N, L, generator=g) < 0.7
+    keep[:, 0] = True
+    ctx, lse = _attn_ref(qkv, keep, H, Dh)
+    dctx = torch.randn(N, L, D, generator=g).double()
+    ctx.backward(dctx)
+    L_ = native.lib()
+    dq, dk, d_dctx = dev(qkv.detach()), dev(keep.float()), dev(dctx)
+    c, l, gq = empty(N, L, D), empty(N, H, L), empty(N, L, 3 * D)
+    native.check(L_.ptcg_kernel_attention_fwd_bf16(P(dq), P(dk), P(c), P(l), N, L, H, Dh, None))
+    native.check(L_.ptcg_kernel_attention_bwd_bf16(P(dq), P(dk), P(c), P(l), P(d_dctx), P(gq), N, L, H, Dh, None))
+    torch.cuda.synchronize()
+    e_c, e_l, e_g = rel_l2(c.cpu(), ctx.detach()), rel_l2(l.cpu(), lse.detach()), rel_l2(gq.cpu(), qkv.grad)
+    assert e_c < 1e-2 and e_l < 1e-2 and e_g < 3e-2, (e_c, e_l, e_g)
+    if L > 1:
+        assert e_c > 1e-4 and e_g > 1e-4
+    gk = gq.cpu().view(N, L, 3, D)
+    assert torch.all(gk[:, :, 1:][~keep] == 0)
+
+
 def test_attention_rejects_oversized(cuda):
     a = empty(4)
     with pytest.raises(native.PtcgError, match="LDS"):

@@ -66,3 +66,38 @@ def test_sync_free_forward_matches_oracle(cuda):
         pl.close()
     want = ref(torch.from_numpy(rows)).detach().numpy()
     assert np.abs(out - want).max() <= 1e-4 * max(1.0, float(np.abs(want).max()))
+
+
+def _grads(B, blob, rows, inp, sync_free):
+    dm = dims.CORE
+    pl = trainer.create_pufferl({"dims": dm, "init_weights": blob, "sync_free": sync_free,
+                                 "train": dict(minibatch_size=B)})
+    try:
+        d_obs = pl.to_device(rows)
+        d_inp = {k: pl.to_device(v) for k, v in inp.items()}
+        pl.forward_backward(d_obs, None, d_inp)
+        pl.sync()
+        dec = pl.buffers()[0]
+        out = torch.empty(B * (dm.n_opt + 1), device="cuda")
+        from ptcg_amd.native import check, lib
+        check(lib().ptcg_transpose_102(out.data_ptr(), dec, 1, out.numel(), 1, 0, None))
+        torch.cuda.synchronize()
+        return pl.get_grads(), out.cpu().numpy()
+    finally:
+        pl.close()
+
+
+def test_sync_free_matches_default_mode_at_full_batch(cuda):
+    """At B = 512 the trunk's 256-wide products have between one and four
+    tiles per CU: with host row counts their last wave is balanced (the tail
+    tiles split K and reduce through the epilogue); sync-free launches cover
+    every tile in one pass.  One forward + backward in each mode: the outputs
+    and every gradient agree to fp32 accumulation-order accuracy."""
+    dm, B = dims.CORE, 512
+    blob = om.build(dm, seed=15).to_blob()
+    rows = synth.make_obs(dm, B, seed=16)
+    inp = synth.make_ppo_inputs(dm, rows, seed=17)
+    g0, o0 = _grads(B, blob, rows, inp, False)
+    g1, o1 = _grads(B, blob, rows, inp, True)
+    assert np.abs(o1 - o0).max() <= 1e-5 * max(1.0, float(np.abs(o0).max()))
+    assert rel_l2(g1, g0) < 1e-5

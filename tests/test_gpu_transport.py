@@ -77,3 +77,29 @@ def test_transport_rejects_bad_shapes(cuda):
     finally:
         x.close()
         pl.close()
+
+
+def test_transport_mask_round_trip(cuda):
+    """An env-side action mask (MY_ACTION_MASK bytes per agent) goes up with
+    its buffer's observations and lands byte for byte; other buffers' slices
+    are untouched."""
+    x = tr.RolloutTransport(64, 4, 8, num_atns=1, mask_bytes=24)
+    try:
+        rng = np.random.default_rng(5)
+        x.action_mask[:] = rng.integers(0, 256, size=x.action_mask.shape, dtype=np.uint8)
+        x.observations[:] = rng.standard_normal(x.observations.shape).astype(np.float32)
+        x.upload(2)
+        torch.cuda.synchronize()
+        dm = torch.empty(64 * 24, dtype=torch.uint8, device="cuda")
+        check(lib().ptcg_transpose_102(dm.data_ptr(), x.device_ptr(tr.MASK), 1, 64 * 24 // 4, 1, 0, None))
+        dob = dev_floats(x.device_ptr(tr.OBS), 64 * 8).reshape(64, 8)
+        torch.cuda.synchronize()
+        got = dm.cpu().numpy().reshape(64, 24)
+        sl = x.slice(2)
+        assert np.array_equal(got[sl], x.action_mask[sl])
+        assert np.array_equal(dob[sl], x.observations[sl])
+        others = np.ones(64, bool)
+        others[sl] = False
+        assert np.all(got[others] == 0) and np.all(dob[others] == 0)
+    finally:
+        x.close()

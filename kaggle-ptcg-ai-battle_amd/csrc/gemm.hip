@@ -382,8 +382,9 @@ __global__ __launch_bounds__(NT) void gemm_f32_kernel(const GemmArgs g0, int k_c
 // staging registers, and the loads of tile i + DMA_NS - 1 are in flight
 // while tile i is multiplied.  Buffer loads return zero past the operand's
 // last element (num_records = its exact extent), which zeroes the k tail of
-// an m-contiguous operand; a k-contiguous operand needs K % BK == 0 (its row
-// tails would read the next row).  Rows / columns past M / N read what lies
+// an m-contiguous operand; a k-contiguous operand's row tails (K % BK != 0)
+// read the next row and are zeroed in LDS before the last tile's products.
+// Rows / columns past M / N read what lies
 // there or zero and only reach C rows / columns that are never stored.
 // The DMA is issued from inline assembly so the compiler does not tie LDS
 // reads to the outstanding loads; the loop waits on vmcnt itself.
@@ -508,6 +509,24 @@ __device__ __forceinline__ void gemm_dma_tile(const GemmArgs& g0, int k_chunk0, 
             // tiles (4 loads each) are still in flight
             wait_stages<NS>(min(NS - 2, nk - 1 - it));
             __syncthreads();   // every wave's loads of tile it are in LDS; tile it - 1 is consumed
+            if (!(AT && BT)) {
+                // the product's last tile may end inside the stage (K % 16 != 0):
+                // a k-contiguous operand's DMA also brought the floats past each
+                // row's end (the next row, or zeros past the extent) — zero those
+                // k columns before the products
+                const int kv = kend - (kbeg + it * BK);
+                if (kv < BK) {
+                    float* st = smem + (it % NS) * 2 * TILE;
+                    for (int idx = tid; idx < BM * BK; idx += NT) {
+                        const int r = idx / BK, k = idx % BK;
+                        if (k >= kv) {
+                            if (!AT) st[dma_at<false>(r, k)] = 0.f;
+                            if (!BT) st[TILE + dma_at<false>(r, k)] = 0.f;
+                        }
+                    }
+                    __syncthreads();
+                }
+            }
             if (it + NS - 1 < nk) PT_ISSUE(it + NS - 1)
             const float* Ab = smem + (it % NS) * 2 * TILE;
             const float* Bb = Ab + TILE;
@@ -1022,15 +1041,12 @@ static int pt_cu_count() {
     return cache[dev];
 }
 
-// LDS-DMA kernels: k-contiguous operands need K % BK == 0, and every byte
-// offset a tile can form (rows / columns up to one tile past the end) must
-// fit the buffer instructions' 32-bit offsets
+// LDS-DMA kernels: every byte offset a tile can form (rows / columns up to
+// one tile past the end) must fit the buffer instructions' 32-bit offsets
 static bool dma_fits(int rows, int cols, long ld) {
     return ((long)rows + 2 * BM) * ld * 4 + ((long)cols + 2 * BM) * 4 < (1L << 31);
 }
 static bool dma_ok(const GemmArgs& g) {
-    if (!g.a_t && g.K % BK != 0) return false;
-    if (!g.b_t && g.K % BK != 0) return false;
     return dma_fits(g.a_t ? g.K : g.M, g.a_t ? g.M : g.K, g.lda) &&
            dma_fits(g.b_t ? g.K : g.N, g.b_t ? g.N : g.K, g.ldb);
 }

@@ -56,9 +56,13 @@ GEMM_CASES = [
     (34000, 256, 256, 0, 0, 2), (33000, 384, 256, 0, 1, 4), (33024, 256, 512, 0, 0, 5),
     (33100, 256, 256, 0, 0, 3),
     # a GELU layer keeping gelu'(z): forward (6) and the multiply backward (7),
-    # on the LDS-DMA kernel, the register-staged kernel (K = 172) and a balanced launch
+    # on the LDS-DMA kernel (K = 172: a last k-tile ending inside the stage) and
+    # a balanced launch
     (512, 1024, 256, 0, 0, 6), (300, 256, 172, 0, 0, 6), (34000, 256, 256, 0, 0, 6),
     (512, 1024, 256, 0, 1, 7), (200, 96, 40, 0, 1, 7), (33000, 384, 256, 0, 1, 7),
+    # k-contiguous K % 16 != 0 at the model's sizes (option query 664 wide,
+    # token concat 300 wide with a balanced tail) and split K ending mid-stage
+    (13000, 256, 664, 0, 0, 6), (37000, 256, 300, 0, 0, 1), (64, 64, 4100, 0, 0, 0), (96, 64, 2052, 0, 1, 5),
 ]
 
 

@@ -222,6 +222,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--workload", choices=("train", "rollout", "frozen", "bf16", "replay"), default="train")
     ap.add_argument("--rollout-rows", type=int, default=8192)
+    ap.add_argument("--rollout-precision", choices=("fp32", "bf16"), default="fp32",
+                    help="--workload rollout: fp32 or bf16 GEMM and attention products")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run three 256 MiB device-to-device copies (the HBM counter calibration)")
     ap.add_argument("--copy-rate", action="store_true",
@@ -443,8 +445,9 @@ def bench_rollout(args):
     n = args.rollout_rows
     obs = synth.make_obs(dm, n, seed=1)
     graph = not args.stream
+    bf = args.rollout_precision == "bf16"
     pl = trainer.create_pufferl({"dims": dm, "train": dict(TRAIN, minibatch_size=8), "seed": 0,
-                                 "sync_free": args.sync_free or graph})
+                                 "sync_free": args.sync_free or graph, "precision": args.rollout_precision})
     d_obs = pl.to_device(obs)
     for i in range(args.warmup):
         pl.rollout_step(d_obs, n, seed=0, step=i)
@@ -486,16 +489,18 @@ def bench_rollout(args):
     gemm_s = ms.value / 1e3
     achieved = useful_fwd * K / gemm_s / 1e12
     line = {
-        "metric": "rollout forward + action sampling obs/sec @8192 rows", "value": round(n * K / sec, 2),
+        "metric": "rollout forward + action sampling obs/sec @8192 rows" + (", bf16 products" if bf else ""),
+        "value": round(n * K / sec, 2),
         "unit": "obs/s", "n_gpus": 1, "steps": K, "warmup": args.warmup, "ms_per_step": round(sec * 1e3 / K, 4),
-        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp32", "data": "synthetic",
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16" if bf else "fp32", "data": "synthetic",
         "config": {"workload": f"inference forward of {n} obs rows (CORE model: 96 tokens + READOUT, d256/H4/"
                                "FFN1024/4 layers) + one inverse-CDF action sample per row from Philox4x32-10",
                    "rows": n, "seq_len": dm.l_tok + 1, "parallelism": "single GPU",
                    "launch": "HIP graph replay (step captured once)" if graph else "stream"},
-        "roofline": dict(bound="mfma", kernel="gemm_f32_dma_kernel + gemm_f32_kernel (forward GEMMs)",
-                         achieved=round(achieved, 3), peak=FP32_MFMA_PEAK_TFLOPS, unit="TFLOP/s",
-                         frac=round(achieved / FP32_MFMA_PEAK_TFLOPS, 4),
+        "roofline": dict(bound="mfma", kernel=("gemm_bf16_k16_kernel" if bf else "gemm_f32_dma_kernel + gemm_f32_kernel")
+                         + " (forward GEMMs)", achieved=round(achieved, 3),
+                         peak=BF16_MFMA_PEAK_TFLOPS if bf else FP32_MFMA_PEAK_TFLOPS, unit="TFLOP/s",
+                         frac=round(achieved / (BF16_MFMA_PEAK_TFLOPS if bf else FP32_MFMA_PEAK_TFLOPS), 4),
                          traffic=None, gemm_ms_per_step=round(ms.value / K, 4),
                          launches_per_step=launches.value / K, mean_valid_seq=round(lv, 2)),
     }

@@ -94,3 +94,31 @@ def test_bf16_gradients_and_steps(cuda):
     trainer.train(pl, index_lists=idx)
     assert rel_l2(pl.get_weights(), ref.to_blob()) <= 1e-3
     pl.close()
+
+
+def test_bf16_rollout_tracks_fp32(cuda):
+    """Config 5's bf16 rollout: the same rows and uniforms through bf16 GEMM
+    and attention products draw the fp32 rollout's actions except where a
+    draw sits within the logits' bf16 error of a CDF boundary; values and the
+    log-probabilities of agreeing draws within bf16 tolerance."""
+    dm, n = dims.CORE, 512
+    blob = om.build(dm, seed=81).to_blob()
+    rows = synth.make_obs(dm, n, seed=82)
+    res = {}
+    for prec in ("fp32", "bf16"):
+        pl = trainer.create_pufferl({"dims": dm, "init_weights": blob, "precision": prec,
+                                     "train": dict(minibatch_size=64)})
+        try:
+            d = pl.to_device(rows)
+            a, lp, v = pl.rollout_step(d, n, seed=5, step=9)
+            torch.cuda.synchronize()
+            res[prec] = (a.cpu().numpy(), lp.cpu().numpy(), v.cpu().numpy())
+        finally:
+            pl.close()
+    a0, l0, v0 = res["fp32"]
+    a1, l1, v1 = res["bf16"]
+    same = a1 == a0
+    assert same.mean() >= 0.97, same.mean()
+    assert np.abs(l1[same] - l0[same]).max() <= 5e-2
+    assert rel_l2(v1, v0) <= 2e-2
+    assert not np.array_equal(v1, v0)     # the products really ran in bf16

@@ -25,22 +25,27 @@ namespace {
 
 constexpr int TB = 256;
 
+// TOK_LPR lanes per row (256 / TOK_LPR rows per workgroup): a row's metadata
+// (sample, position, obs row, token ids) is loaded once per lane group — the
+// same address in its lanes — and the group walks the row's 16-byte chunks;
+// 64 / TOK_LPR rows per wave keep that many dependent lookup chains in flight.
+constexpr int TOK_LPR = 8;
 __global__ void tok_cat_fwd_kernel(GatherCtx c, const float* __restrict__ card,
         const float* __restrict__ zemb, const float* __restrict__ oemb, float* __restrict__ out) {
     const int Lt = c.dm.l_tok, dc = c.dm.d_c, tin = c.dx.tok_in;
     const int chunks = tin / 4;
-    const long i = (long)blockIdx.x * TB + threadIdx.x;
+    const int lane = threadIdx.x % TOK_LPR;
+    const long r = (long)blockIdx.x * (TB / TOK_LPR) + threadIdx.x / TOK_LPR;
     // rows: (n, token t) full length, or the compact trunk rows (READOUT rows get zeros)
     const long nrows = c.rowmap ? (long)*c.rows : (long)c.N * Lt;
-    if (i >= nrows * chunks) return;
-    const int ch = (int)(i % chunks);
-    const long r = i / chunks;
+    if (r >= nrows) return;
     int n, t;
     if (c.rowmap) {
         n = c.rsam[r];
         t = c.rpos[r] - 1;
         if (t < 0) {
-            *reinterpret_cast<float4*>(out + r * tin + ch * 4) = make_float4(0.f, 0.f, 0.f, 0.f);
+            for (int ch = lane; ch < chunks; ch += TOK_LPR)
+                *reinterpret_cast<float4*>(out + r * tin + ch * 4) = make_float4(0.f, 0.f, 0.f, 0.f);
             return;
         }
     } else {
@@ -49,29 +54,31 @@ __global__ void tok_cat_fwd_kernel(GatherCtx c, const float* __restrict__ card,
     }
     const float* row = obs_row(c.obs, c.idx, c.stride, n);
     const float* ti = row + c.off.tok_int + (long)t * c.dm.tok_int;
-    const int col = ch * 4;
     const int NC = c.dm.n_cards;
-    float4 v;
-    if (col < dc) {
-        const int cid = pt_id_clamp(ti[0], NC - 1);
-        v = *reinterpret_cast<const float4*>(card + (long)cid * dc + col);
-    } else if (col < 2 * dc) {
-        const int e = col - dc;
-        const int t0 = (int)ti[3], t1 = (int)ti[4];
-        float4 a = make_float4(0.f, 0.f, 0.f, 0.f), b = a;
-        if (t0 > 0) a = *reinterpret_cast<const float4*>(card + (long)(t0 >= NC ? NC - 1 : t0) * dc + e);
-        if (t1 > 0) b = *reinterpret_cast<const float4*>(card + (long)(t1 >= NC ? NC - 1 : t1) * dc + e);
-        v = make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
-    } else if (col < 2 * dc + c.dm.tok_f) {
-        v = *reinterpret_cast<const float4*>(row + c.off.tok_float + (long)t * c.dm.tok_f + (col - 2 * dc));
-    } else if (col < 2 * dc + c.dm.tok_f + PT_ZONE_E) {
-        const int z = pt_id_clamp(ti[1], c.dm.n_zones - 1);
-        v = *reinterpret_cast<const float4*>(zemb + z * PT_ZONE_E + (col - 2 * dc - c.dm.tok_f));
-    } else {
-        const int o = pt_id_clamp(ti[2], c.dm.n_owners - 1);
-        v = *reinterpret_cast<const float4*>(oemb + o * PT_OWNER_E + (col - 2 * dc - c.dm.tok_f - PT_ZONE_E));
+    const int cid = pt_id_clamp(ti[0], NC - 1);
+    const int t0 = (int)ti[3], t1 = (int)ti[4];
+    const int z = pt_id_clamp(ti[1], c.dm.n_zones - 1);
+    const int o = pt_id_clamp(ti[2], c.dm.n_owners - 1);
+    for (int ch = lane; ch < chunks; ch += TOK_LPR) {
+        const int col = ch * 4;
+        float4 v;
+        if (col < dc) {
+            v = *reinterpret_cast<const float4*>(card + (long)cid * dc + col);
+        } else if (col < 2 * dc) {
+            const int e = col - dc;
+            float4 a = make_float4(0.f, 0.f, 0.f, 0.f), b = a;
+            if (t0 > 0) a = *reinterpret_cast<const float4*>(card + (long)(t0 >= NC ? NC - 1 : t0) * dc + e);
+            if (t1 > 0) b = *reinterpret_cast<const float4*>(card + (long)(t1 >= NC ? NC - 1 : t1) * dc + e);
+            v = make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
+        } else if (col < 2 * dc + c.dm.tok_f) {
+            v = *reinterpret_cast<const float4*>(row + c.off.tok_float + (long)t * c.dm.tok_f + (col - 2 * dc));
+        } else if (col < 2 * dc + c.dm.tok_f + PT_ZONE_E) {
+            v = *reinterpret_cast<const float4*>(zemb + z * PT_ZONE_E + (col - 2 * dc - c.dm.tok_f));
+        } else {
+            v = *reinterpret_cast<const float4*>(oemb + o * PT_OWNER_E + (col - 2 * dc - c.dm.tok_f - PT_ZONE_E));
+        }
+        *reinterpret_cast<float4*>(out + r * tin + col) = v;
     }
-    *reinterpret_cast<float4*>(out + r * tin + col) = v;
 }
 
 // Scatter-add of one table column with a per-thread cache of four (id, sum)
@@ -580,12 +587,18 @@ __global__ void fill_zero_tail_kernel(float* p, long n) {
 }  // namespace
 
 int pt_tok_cat_fwd(const GatherCtx& c, const float* card, const float* zemb, const float* oemb,
-                   float* tok_cat, hipStream_t s) {
+                   float* tok_cat, hipStream_t s, long rows_done) {
     PT_REQUIRE(c.dm.d_c % 4 == 0 && c.dm.tok_f % 4 == 0 && c.off.tok_float % 4 == 0 && c.stride % 4 == 0,
                "tok_cat: widths must be multiples of 4");
     const long rows = c.rowmap ? (long)c.N * c.dx.l_seq : (long)c.N * c.dm.l_tok;
-    hipLaunchKernelGGL(tok_cat_fwd_kernel, PT_GRID(rows * (c.dx.tok_in / 4)), c, card, zemb, oemb, tok_cat);
+    const int slot = pt_prof_open(s);
+    hipLaunchKernelGGL(tok_cat_fwd_kernel, dim3(pt_cdiv(rows, TB / TOK_LPR)), dim3(TB), 0, s, c, card, zemb, oemb,
+                       tok_cat);
     PT_LAUNCH_CHECK();
+    // HBM bytes: each row written, its token's obs floats read (the embedding
+    // tables, ~1 MB, stay in L2)
+    pt_prof_close(slot, PROF_GATHER, (double)(rows_done > 0 ? rows_done : rows) * 4.0 *
+                  (c.dx.tok_in + c.dm.tok_f + c.dm.tok_int), s);
     return PTCG_OK;
 }
 int pt_tok_cat_bwd(const GatherCtx& c, const float* d_cat, float* d_card, float* d_zemb, float* d_oemb,

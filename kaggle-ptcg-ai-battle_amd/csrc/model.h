@@ -100,7 +100,8 @@ __device__ __forceinline__ long pt_hrow(const GatherCtx& c, int n, int pos) {
     return c.rowmap ? (long)c.rowmap[(long)n * c.dx.l_seq + pos] : (long)n * c.dx.l_seq + pos;
 }
 int pt_tok_cat_fwd(const GatherCtx& c, const float* card, const float* zemb, const float* oemb,
-                   float* tok_cat, hipStream_t s);
+                   float* tok_cat, hipStream_t s,
+                   long rows_done = 0);
 int pt_tok_cat_bwd(const GatherCtx& c, const float* d_cat, float* d_card, float* d_zemb,
                    float* d_oemb, hipStream_t s);
 int pt_glob_in(const GatherCtx& c, float* glob_in, hipStream_t s);

@@ -621,7 +621,7 @@ extern "C" int ptcg_model_forward(PtcgModel* m, const float* obs, const int32_t*
     const int tok_rows = m->compact ? m->rows : N * Lt;
 
     if (d.tables == 1) PT_TRY(tables_fwd(m, s));
-    PT_TRY(pt_tok_cat_fwd(c, m->card, m->zemb, m->oemb, m->tok_cat, s));
+    PT_TRY(pt_tok_cat_fwd(c, m->card, m->zemb, m->oemb, m->tok_cat, s, tok_rows));
     PT_TRY(linf(m, m->tok_cat, m->tp_w, m->tp_b, m->tokp, tok_rows, x.tok_in, D, EPI_BIAS, nullptr, nullptr, s, Td));
     PT_TRY(pt_glob_in(c, m->glob_in, s));
     PT_TRY(linf(m, m->glob_in, m->g1_w, m->g1_b, m->g1, N, d.global_f, G, EPI_BIAS_GELU_D, nullptr, m->g1a, s));

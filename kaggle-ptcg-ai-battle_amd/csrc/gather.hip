@@ -24,6 +24,7 @@
 namespace {
 
 constexpr int TB = 256;
+constexpr int PT_MAX_OPT = 256;   // options per sample the q_in backward stages in LDS
 
 // TOK_LPR lanes per row (256 / TOK_LPR rows per workgroup): a row's metadata
 // (sample, position, obs row, token ids) is loaded once per lane group — the
@@ -373,35 +374,45 @@ __global__ void q_in_fwd_kernel(GatherCtx c, const float* __restrict__ h,
 // owns its columns, so no two threads add to one element; the adds are
 // no-return atomics so successive options do not wait on each other's
 // read-modify-write.  Option types (few, hot) go through an id cache.
+// One workgroup per sample.  The sample's option rows' lookups (option slot
+// -> option ids -> trunk rows of the two pointer targets) are resolved once
+// into LDS; each thread then walks the options in order for its column, so
+// a column's atomics keep their order (deterministic sums) while the
+// gradient loads of successive options no longer wait on a lookup chain.
 __global__ void q_in_bwd_kernel(GatherCtx c, const float* __restrict__ d_qin, float* __restrict__ d_h,
                                 float* d_temb) {
+    __shared__ long s_h1[PT_MAX_OPT], s_h2[PT_MAX_OPT];
+    __shared__ int s_ty[PT_MAX_OPT];
     const int n = blockIdx.x, NO = c.dm.n_opt, D = c.dm.d, W = c.dx.q_in;
     const float* row = obs_row(c.obs, c.idx, c.stride, n);
-    // the sample's option rows
+    // the sample's option rows (at most n_opt of them)
     const long b0 = c.ooff ? c.ooff[n] : (long)n * NO, b1 = c.ooff ? c.ooff[n + 1] : b0 + NO;
+    const int nq = (int)(b1 - b0);
+    for (int i = threadIdx.x; i < nq; i += TB) {
+        const int j = (int)(pt_onj(c, b0 + i) % NO);
+        const float* oi = row + c.off.opt_int + (long)j * c.dm.opt_int;
+        const int p1 = (int)oi[1], p2 = (int)oi[2];
+        s_h1[i] = (p1 > 0 && p1 <= c.dm.l_tok) ? pt_hrow(c, n, p1) : -1;
+        s_h2[i] = (p2 > 0 && p2 <= c.dm.l_tok) ? pt_hrow(c, n, p2) : -1;
+        s_ty[i] = pt_id_clamp(oi[0], c.dm.n_opt_types - 1);
+    }
+    __syncthreads();
     for (int col = threadIdx.x; col < D; col += TB) {
-        for (long q = b0; q < b1; ++q) {
-            const int j = (int)(pt_onj(c, q) % NO);
-            const float* oi = row + c.off.opt_int + (long)j * c.dm.opt_int;
-            const float* g = d_qin + q * W;
-            const int p1 = (int)oi[1], p2 = (int)oi[2];
-            if (p1 > 0 && p1 <= c.dm.l_tok) {
+        for (int i = 0; i < nq; ++i) {
+            const float* g = d_qin + (b0 + i) * W;
+            if (s_h1[i] >= 0) {
                 const float v = g[PT_TYPE_E + col];
-                if (v != 0.f) atomicAdd(d_h + pt_hrow(c, n, p1) * D + col, v);
+                if (v != 0.f) atomicAdd(d_h + s_h1[i] * D + col, v);
             }
-            if (p2 > 0 && p2 <= c.dm.l_tok) {
+            if (s_h2[i] >= 0) {
                 const float v = g[PT_TYPE_E + D + col];
-                if (v != 0.f) atomicAdd(d_h + pt_hrow(c, n, p2) * D + col, v);
+                if (v != 0.f) atomicAdd(d_h + s_h2[i] * D + col, v);
             }
         }
     }
     if (threadIdx.x < PT_TYPE_E) {
         IdCache k;
-        for (long q = b0; q < b1; ++q) {
-            const int j = (int)(pt_onj(c, q) % NO);
-            const float* oi = row + c.off.opt_int + (long)j * c.dm.opt_int;
-            k.add(d_temb, PT_TYPE_E, threadIdx.x, pt_id_clamp(oi[0], c.dm.n_opt_types - 1), d_qin[q * W + threadIdx.x]);
-        }
+        for (int i = 0; i < nq; ++i) k.add(d_temb, PT_TYPE_E, threadIdx.x, s_ty[i], d_qin[(b0 + i) * W + threadIdx.x]);
         k.flush(d_temb, PT_TYPE_E, threadIdx.x);
     }
 }
@@ -663,6 +674,7 @@ int pt_q_in_fwd(const GatherCtx& c, const float* h, const float* temb, float* q_
     return PTCG_OK;
 }
 int pt_q_in_bwd(const GatherCtx& c, const float* d_qin, float* d_h, float* d_temb, hipStream_t s) {
+    PT_REQUIRE(c.dm.n_opt <= PT_MAX_OPT, "q_in backward: %d options per sample exceed %d", c.dm.n_opt, PT_MAX_OPT);
     hipLaunchKernelGGL(q_in_bwd_kernel, dim3(c.N), dim3(TB), 0, s, c, d_qin, d_h, d_temb);
     PT_LAUNCH_CHECK();
     return PTCG_OK;

@@ -130,6 +130,8 @@ int ptcg_model_set_skip_masked_options(PtcgModel* m, int on);
 int ptcg_model_bind_returns(PtcgModel* m, const float* returns);
 
 /* ---- PPO loss fwd+bwd (pufferlib.cu:1368-1449; kernels :949-1363) -------
+ * ent_coef is a device float read by the kernel, as the reference's is
+ * (pufferlib.cu:199,1063: "by-value args get baked into the cuda graph").
  * dec_out (n, A+1) fused [scores || value]; mask (n rows at mask_stride,
  * 0 = illegal -> logit -1e4); per-row inputs gathered through row_idx when
  * non-NULL.  Writes grad (n, A+1) = [grad_logits || grad_value], ratio (n),
@@ -141,7 +143,7 @@ int ptcg_ppo_loss_fwd_bwd(const float* dec_out, int n, int A,
                           const float* actions, const float* old_logprobs,
                           const float* advantages, const float* returns,
                           const float* values, const float* prio,
-                          float clip_coef, float vf_clip_coef, float vf_coef, float ent_coef,
+                          float clip_coef, float vf_clip_coef, float vf_coef, const float* ent_coef,
                           float* grad, float* ratio, float* newvalue,
                           float* stats, float* guard, void* stream);
 
@@ -154,14 +156,15 @@ int ptcg_kl_gate(const float* guard, float kl_threshold, float vf_threshold,
  * One fused pass over the flat arenas (n floats, n % 4 == 0, 16 B aligned):
  * g' = g * min(max_norm / (||g||_2 + 1e-6), 1); Adam moments m, v; weights
  * updated with bias correction for step t = *step + 1 (torch.optim.Adam
- * semantics).  step: device int32 count of applied steps, advanced on the
- * device.  gate: optional device float; when it reads 0 the call changes
+ * semantics).  lr: device double read by the kernel (the reference's
+ * lr_ptr, muon.cu:92-100), so a captured step follows the host's writes.
+ * step: device int32 count of applied steps, advanced on the device.  gate: optional device float; when it reads 0 the call changes
  * nothing (weights, m, v, step untouched).  norm_out: optional device float
  * receiving ||g||_2 before clipping.  workspace: device buffer of
  * ptcg_adam_workspace_floats() floats.  grads are read, not modified.      */
 int64_t ptcg_adam_workspace_floats(void);
 int ptcg_adam_step(float* weights, float* grads, float* m, float* v, int64_t n,
-                   double lr, double beta1, double beta2, double eps, float max_grad_norm,
+                   const double* lr, double beta1, double beta2, double eps, float max_grad_norm,
                    const float* gate, int32_t* step, float* norm_out, float* workspace,
                    void* stream);
 
@@ -245,7 +248,15 @@ int ptcg_index_copy(float* dst, const int32_t* idx, const float* src, int n_idx,
 int ptcg_trainer_create(const PtcgDims* dims, const PtcgHypers* hyp, int minibatch,
                         PtcgTrainer** out);
 void ptcg_trainer_free(PtcgTrainer* t);
+/* New hyper-parameters.  lr and ent_coef go to device scalars read by the
+ * step's kernels (train_impl's per-call cudaMemcpy to lr_ptr and
+ * ppo_bufs.ent_coef, pufferlib.cu:1912-1948), so a captured step follows
+ * them.  A change of any other field drops the captured step (it is a launch
+ * argument there); replay_step then fails until capture_step runs again.   */
 int ptcg_trainer_set_hypers(PtcgTrainer* t, const PtcgHypers* hyp);
+/* Device addresses of those two scalars (a double and a float), for callers
+ * that write the schedule on a stream of their own.                      */
+int ptcg_trainer_hyper_ptrs(PtcgTrainer* t, double** lr, float** ent_coef);
 /* packed blob <-> live arena (bindings.cu:202-215,339-367), host buffers   */
 int ptcg_trainer_set_weights(PtcgTrainer* t, const float* packed);
 int ptcg_trainer_get_weights(PtcgTrainer* t, float* packed);
@@ -359,7 +370,9 @@ int ptcg_trainer_set_prio(PtcgTrainer* t, const float* prio);
  * mode only: every node is a kernel; nothing runs during capture);
  * replay_step launches it on `stream`.  The buffers' addresses are baked
  * in: write each minibatch's indices / inputs into the same buffers before
- * a replay.  Re-capturing replaces the graph.                              */
+ * a replay.  Re-capturing replaces the graph.  set_optimizer, set_precision,
+ * set_sync_free, set_skip_masked_options, a new prio pointer and a change of
+ * a by-value hyper-parameter (set_hypers) drop it.                          */
 int ptcg_trainer_capture_step(PtcgTrainer* t, const float* obs, const int32_t* row_idx,
                               const float* actions, const float* old_logprobs,
                               const float* advantages, const float* returns, const float* values);

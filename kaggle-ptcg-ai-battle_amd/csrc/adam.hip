@@ -14,6 +14,8 @@
 //      p  = p - (lr / (1 - b1^t)) m / (sqrt(v) / sqrt(1 - b2^t) + eps)
 //      (torch.optim.Adam's single-tensor arithmetic: lerp_, mul_/addcmul_,
 //      addcdiv_).  Thread 0 of workgroup 0 commits the step counter.
+// The learning rate is read from a device double (the reference's lr_ptr,
+// muon.cu:92-100), so a captured step follows the host's schedule writes.
 // A device gate (the trainer's KL/value guard, pufferlib.cu:1292-1302) that
 // reads 0 makes both launches return before touching memory, and the step
 // counter does not advance: a vetoed step is a bit-exact no-op.
@@ -63,7 +65,7 @@ __global__ __launch_bounds__(NT_NORM) void adam_norm_kernel(const float4* __rest
 template <int U>
 __global__ __launch_bounds__(NT) void adam_update_kernel(float4* __restrict__ p,
         const float4* __restrict__ g, float4* __restrict__ m, float4* __restrict__ v, long n4,
-        int nparts, double lr, double b1, double b2, double eps, float max_norm,
+        int nparts, const double* __restrict__ lr_dev, double b1, double b2, double eps, float max_norm,
         const float* __restrict__ gate, const float* __restrict__ ws, float* __restrict__ norm_out,
         int32_t* __restrict__ step) {
     if (gate && gate[0] == 0.0f) return;
@@ -94,6 +96,7 @@ __global__ __launch_bounds__(NT) void adam_update_kernel(float4* __restrict__ p,
     }
     // scalars in double, rounded once to fp32 (torch keeps them as Python
     // floats and hands fp32 kernels the rounded value)
+    const double lr = lr_dev[0];
     const float step_size = (float)(lr / (1.0 - pow(b1, (double)t)));
     const float bc2s = (float)sqrt(1.0 - pow(b2, (double)t));
     const float omb1 = (float)(1.0 - b1), omb2 = (float)(1.0 - b2);
@@ -123,9 +126,10 @@ __global__ __launch_bounds__(NT) void adam_update_kernel(float4* __restrict__ p,
 
 long pt_adam_ws_floats() { return NPART + 4; }
 
-int pt_adam_step(float* w, float* g, float* m, float* v, long n, double lr, double b1, double b2,
+int pt_adam_step(float* w, float* g, float* m, float* v, long n, const double* lr, double b1, double b2,
                  double eps, float max_norm, const float* gate, int32_t* step, float* norm_out,
                  float* ws, hipStream_t s) {
+    PT_REQUIRE(lr != nullptr, "adam: the learning rate must be a device scalar");
     PT_REQUIRE(n > 0 && n % 4 == 0, "adam: arena length %ld must be a positive multiple of 4", n);
     PT_REQUIRE(((uintptr_t)w | (uintptr_t)g | (uintptr_t)m | (uintptr_t)v) % 16 == 0,
                "adam: arenas must be 16 B aligned");

@@ -222,10 +222,10 @@ extern "C" int ptcg_ppo_loss_fwd_bwd(const float* dec_out, int n, int A, const f
                                      int64_t mask_stride, const int32_t* row_idx, const float* actions,
                                      const float* old_logprobs, const float* advantages,
                                      const float* returns, const float* values, const float* prio,
-                                     float clip_coef, float vf_clip_coef, float vf_coef, float ent_coef,
+                                     float clip_coef, float vf_clip_coef, float vf_coef, const float* ent_coef,
                                      float* grad, float* ratio, float* newvalue, float* stats,
                                      float* guard, void* stream) {
-    PT_REQUIRE(dec_out && mask && actions && old_logprobs && advantages && returns && values && grad,
+    PT_REQUIRE(dec_out && mask && actions && old_logprobs && advantages && returns && values && grad && ent_coef,
                "ppo_loss: null input");
     hipStream_t s = (hipStream_t)stream;
     // per-block partials live in a per-thread scratch sized for the largest n seen
@@ -249,11 +249,11 @@ extern "C" int ptcg_kl_gate(const float* guard, float kl_threshold, float vf_thr
     return pt_kl_gate(guard, kl_threshold, vf_threshold, gate, skipped, (hipStream_t)stream);
 }
 
-extern "C" int ptcg_adam_step(float* weights, float* grads, float* m, float* v, int64_t n, double lr,
+extern "C" int ptcg_adam_step(float* weights, float* grads, float* m, float* v, int64_t n, const double* lr,
                               double beta1, double beta2, double eps, float max_grad_norm,
                               const float* gate, int32_t* step, float* norm_out, float* workspace,
                               void* stream) {
-    PT_REQUIRE(weights && grads && m && v && step && workspace, "adam_step: null buffer");
+    PT_REQUIRE(weights && grads && m && v && lr && step && workspace, "adam_step: null buffer");
     return pt_adam_step(weights, grads, m, v, n, lr, beta1, beta2, eps, max_grad_norm, gate, step,
                         norm_out, workspace, (hipStream_t)stream);
 }
@@ -275,6 +275,11 @@ struct PtcgTrainer {
     float *P, *Gr, *M, *V;
     float *grad, *ratio, *newvalue, *stats, *guard, *gate, *ppo_part, *adam_ws, *dbg_obs;
     int32_t* step;
+    // device scalars read inside the step (a captured step follows their
+    // writes): Adam's learning rate and the loss's entropy coefficient
+    // (the reference's lr_ptr and ppo_bufs.ent_coef, pufferlib.cu:1912-1948)
+    double* lr_dev;
+    float* ent_dev;
     // rollout policy: a second model on the same weights with inference
     // activations for `roll_n` rows (reg_rollout), made on first use
     PtcgModel* roll = nullptr;
@@ -310,6 +315,42 @@ extern "C" void ptcg_trainer_free(PtcgTrainer* t) {
     delete t;
 }
 
+// lr and ent_coef into their device scalars (the reference's per-train
+// cudaMemcpy to lr_ptr / ppo_bufs.ent_coef, pufferlib.cu:1933,1947)
+static int write_schedule(PtcgTrainer* t, double lr, float ent_coef) {
+    double v[2];
+    memcpy(&v[0], &lr, sizeof lr);
+    float e[2] = {ent_coef, 0.f};
+    memcpy(&v[1], e, sizeof e);
+    PT_HIP(hipMemcpy(t->lr_dev, v, sizeof v, hipMemcpyHostToDevice));
+    return PTCG_OK;
+}
+
+// A captured step holds every by-value argument of its launches and every
+// buffer address.  Whatever changes one of them drops the graph, so that
+// replay_step fails ("no captured step") instead of replaying stale values.
+static int drop_step_graph(PtcgTrainer* t) {
+    if (t->graph_exec) {
+        PT_HIP(hipDeviceSynchronize());
+        PT_HIP(hipGraphExecDestroy(t->graph_exec));
+        t->graph_exec = nullptr;
+    }
+    if (t->graph) {
+        PT_HIP(hipGraphDestroy(t->graph));
+        t->graph = nullptr;
+    }
+    return PTCG_OK;
+}
+static int drop_rollout_graphs(PtcgTrainer* t) {
+    for (auto& x : t->roll_exec)
+        if (x) {
+            PT_HIP(hipDeviceSynchronize());
+            PT_HIP(hipGraphExecDestroy(x));
+            x = nullptr;
+        }
+    return PTCG_OK;
+}
+
 extern "C" int ptcg_trainer_create(const PtcgDims* dims, const PtcgHypers* hyp, int minibatch,
                                    PtcgTrainer** out) {
     PT_REQUIRE(dims && hyp && out, "trainer_create: null argument");
@@ -331,7 +372,7 @@ extern "C" int ptcg_trainer_create(const PtcgDims* dims, const PtcgHypers* hyp, 
     const size_t oP = take(t->arena), oG = take(t->arena), oM = take(t->arena), oV = take(t->arena);
     const size_t oGrad = take(B * A1), oRatio = take(B), oNv = take(B), oStats = take(16),
                  oGuard = take(4), oGate = take(4), oPart = take(pt_ppo_partial_floats(minibatch)),
-                 oAdam = take(pt_adam_ws_floats()), oStep = take(4),
+                 oAdam = take(pt_adam_ws_floats()), oStep = take(4), oHyp = take(4),
                  oDbg = take(B * t->off.size);
     hipError_t e = hipMalloc(&t->mem, off);
     if (e != hipSuccess) {
@@ -350,9 +391,12 @@ extern "C" int ptcg_trainer_create(const PtcgDims* dims, const PtcgHypers* hyp, 
     t->grad = F(oGrad); t->ratio = F(oRatio); t->newvalue = F(oNv); t->stats = F(oStats);
     t->guard = F(oGuard); t->gate = F(oGate); t->ppo_part = F(oPart); t->adam_ws = F(oAdam);
     t->step = reinterpret_cast<int32_t*>(t->mem + oStep);
+    t->lr_dev = reinterpret_cast<double*>(t->mem + oHyp);
+    t->ent_dev = F(oHyp) + 2;
     t->dbg_obs = F(oDbg);
     r = ptcg_model_bind(t->model, t->P, t->Gr);
     if (r == PTCG_OK) r = ptcg_model_reg_train(t->model, minibatch);
+    if (r == PTCG_OK) r = write_schedule(t, hyp->lr, hyp->ent_coef);
     if (r != PTCG_OK) { ptcg_trainer_free(t); return r; }
     *out = t;
     return PTCG_OK;
@@ -360,6 +404,16 @@ extern "C" int ptcg_trainer_create(const PtcgDims* dims, const PtcgHypers* hyp, 
 
 extern "C" int ptcg_trainer_set_hypers(PtcgTrainer* t, const PtcgHypers* hyp) {
     PT_REQUIRE(t && hyp, "set_hypers: null argument");
+    const PtcgHypers& o = t->hyp;
+    // lr and ent_coef live in device scalars; every other field is a launch
+    // argument of the captured step (and Muon's momentum of its kernels)
+    const bool baked = o.beta1 != hyp->beta1 || o.beta2 != hyp->beta2 || o.eps != hyp->eps ||
+                       o.max_grad_norm != hyp->max_grad_norm || o.clip_coef != hyp->clip_coef ||
+                       o.vf_clip_coef != hyp->vf_clip_coef || o.vf_coef != hyp->vf_coef ||
+                       o.kl_skip_threshold != hyp->kl_skip_threshold ||
+                       o.vf_skip_threshold != hyp->vf_skip_threshold;
+    if (baked) PT_TRY(drop_step_graph(t));
+    PT_TRY(write_schedule(t, hyp->lr, hyp->ent_coef));
     t->hyp = *hyp;
     if (t->muon) {
         PT_TRY(ptcg_muon_set_lr(t->muon, (float)hyp->lr));
@@ -368,9 +422,17 @@ extern "C" int ptcg_trainer_set_hypers(PtcgTrainer* t, const PtcgHypers* hyp) {
     return PTCG_OK;
 }
 
+extern "C" int ptcg_trainer_hyper_ptrs(PtcgTrainer* t, double** lr, float** ent_coef) {
+    PT_REQUIRE(t, "hyper_ptrs: null trainer");
+    if (lr) *lr = t->lr_dev;
+    if (ent_coef) *ent_coef = t->ent_dev;
+    return PTCG_OK;
+}
+
 extern "C" int ptcg_trainer_set_optimizer(PtcgTrainer* t, int kind, double wd_1d) {
     PT_REQUIRE(t, "set_optimizer: null trainer");
     PT_REQUIRE(kind == 0 || kind == 1, "set_optimizer: kind %d (0 Adam, 1 Muon)", kind);
+    PT_TRY(drop_step_graph(t));   // the graph points into the old optimizer's memory
     if (t->muon) {
         ptcg_muon_free(t->muon);
         t->muon = nullptr;
@@ -596,7 +658,7 @@ static int fwd_bwd(PtcgTrainer* t, const float* obs, const int32_t* idx, const f
     const PtcgHypers& h = t->hyp;
     PT_TRY(pt_ppo_loss(out, t->B, t->dm.n_opt, obs + t->off.opt_mask, t->off.size, idx, actions,
                        old_logprobs, advantages, returns, values, t->prio, h.clip_coef, h.vf_clip_coef,
-                       h.vf_coef, h.ent_coef, t->grad, t->ratio, t->newvalue, t->stats, t->guard,
+                       h.vf_coef, t->ent_dev, t->grad, t->ratio, t->newvalue, t->stats, t->guard,
                        t->ppo_part, s));
     PT_TRY(ptcg_model_bind_returns(t->model, returns));
     PT_TRY(ptcg_model_backward(t->model, t->grad, s));
@@ -605,6 +667,7 @@ static int fwd_bwd(PtcgTrainer* t, const float* obs, const int32_t* idx, const f
 
 extern "C" int ptcg_trainer_set_prio(PtcgTrainer* t, const float* prio) {
     PT_REQUIRE(t, "trainer_set_prio: null trainer");
+    if (prio != t->prio) PT_TRY(drop_step_graph(t));
     t->prio = prio;
     return PTCG_OK;
 }
@@ -640,6 +703,8 @@ extern "C" int ptcg_trainer_set_static(PtcgTrainer* t, const float* card_static,
 
 extern "C" int ptcg_trainer_set_precision(PtcgTrainer* t, int prec) {
     PT_REQUIRE(t, "trainer_set_precision: null trainer");
+    PT_TRY(drop_step_graph(t));
+    PT_TRY(drop_rollout_graphs(t));
     PT_TRY(ptcg_model_set_precision(t->model, prec));
     if (t->roll) PT_TRY(ptcg_model_set_precision(t->roll, prec));
     t->prec = prec;
@@ -648,6 +713,8 @@ extern "C" int ptcg_trainer_set_precision(PtcgTrainer* t, int prec) {
 
 extern "C" int ptcg_trainer_set_skip_masked_options(PtcgTrainer* t, int on) {
     PT_REQUIRE(t, "trainer_set_skip_masked_options: null trainer");
+    PT_TRY(drop_step_graph(t));
+    PT_TRY(drop_rollout_graphs(t));
     PT_TRY(ptcg_model_set_skip_masked_options(t->model, on));
     if (t->roll) PT_TRY(ptcg_model_set_skip_masked_options(t->roll, on));
     t->skip_masked = on != 0;
@@ -656,6 +723,8 @@ extern "C" int ptcg_trainer_set_skip_masked_options(PtcgTrainer* t, int on) {
 
 extern "C" int ptcg_trainer_set_sync_free(PtcgTrainer* t, int on) {
     PT_REQUIRE(t, "trainer_set_sync_free: null trainer");
+    PT_TRY(drop_step_graph(t));
+    PT_TRY(drop_rollout_graphs(t));
     PT_TRY(ptcg_model_set_sync_free(t->model, on));
     if (t->roll) PT_TRY(ptcg_model_set_sync_free(t->roll, on));
     t->sync_free = on;
@@ -676,12 +745,7 @@ static int roll_model(PtcgTrainer* t, int n) {
                                              t->st_i[1].data()));
         }
         // captured rollout graphs hold the old activation buffers: drop them
-        for (auto& x : t->roll_exec)
-            if (x) {
-                PT_HIP(hipDeviceSynchronize());
-                PT_HIP(hipGraphExecDestroy(x));
-                x = nullptr;
-            }
+        PT_TRY(drop_rollout_graphs(t));
         PT_TRY(ptcg_model_reg_rollout(t->roll, n));
         t->roll_n = n;
     }
@@ -762,7 +826,7 @@ extern "C" int ptcg_trainer_step(PtcgTrainer* t, const float* obs, const int32_t
     if (t->muon)
         PT_TRY(ptcg_muon_step(t->muon, t->P, t->Gr, h.max_grad_norm, gate_on ? t->gate : nullptr, t->stats + 9, s));
     else
-        PT_TRY(pt_adam_step(t->P, t->Gr, t->M, t->V, t->arena, h.lr, h.beta1, h.beta2, h.eps, h.max_grad_norm,
+        PT_TRY(pt_adam_step(t->P, t->Gr, t->M, t->V, t->arena, t->lr_dev, h.beta1, h.beta2, h.eps, h.max_grad_norm,
                             gate_on ? t->gate : nullptr, t->step, t->stats + 9, t->adam_ws, s));
     return PTCG_OK;
 }
@@ -777,14 +841,7 @@ extern "C" int ptcg_trainer_capture_step(PtcgTrainer* t, const float* obs, const
                                          const float* advantages, const float* returns, const float* values) {
     PT_REQUIRE(t, "capture_step: null trainer");
     PT_REQUIRE(t->sync_free, "capture_step: needs sync-free mode (ptcg_trainer_set_sync_free)");
-    if (t->graph_exec) {
-        PT_HIP(hipGraphExecDestroy(t->graph_exec));
-        t->graph_exec = nullptr;
-    }
-    if (t->graph) {
-        PT_HIP(hipGraphDestroy(t->graph));
-        t->graph = nullptr;
-    }
+    PT_TRY(drop_step_graph(t));
     if (!t->cap_stream) PT_HIP(hipStreamCreateWithFlags(&t->cap_stream, hipStreamNonBlocking));
     PT_HIP(hipDeviceSynchronize());
     PT_HIP(hipStreamBeginCapture(t->cap_stream, hipStreamCaptureModeThreadLocal));
@@ -803,7 +860,8 @@ extern "C" int ptcg_trainer_capture_step(PtcgTrainer* t, const float* obs, const
 }
 
 extern "C" int ptcg_trainer_replay_step(PtcgTrainer* t, void* stream) {
-    PT_REQUIRE(t && t->graph_exec, "replay_step: no captured step (ptcg_trainer_capture_step)");
+    PT_REQUIRE(t && t->graph_exec, "replay_step: no captured step (ptcg_trainer_capture_step; a change of "
+               "optimizer, mode, gate or a by-value hyper-parameter drops the captured graph)");
     PT_HIP(hipGraphLaunch(t->graph_exec, (hipStream_t)stream));
     return PTCG_OK;
 }

@@ -57,7 +57,7 @@ long pt_ppo_partial_floats(int n);
 int pt_ppo_loss(const float* out, int n, int A, const float* mask, long mask_stride,
                 const int32_t* idx, const float* actions, const float* old_logp,
                 const float* adv, const float* ret, const float* val, const float* prio,
-                float clip, float vf_clip, float vf_coef, float ent_coef, float* grad,
+                float clip, float vf_clip, float vf_coef, const float* ent_coef, float* grad,
                 float* ratio, float* newvalue, float* stats, float* guard, float* partial,
                 hipStream_t s);
 int pt_kl_gate(const float* guard, float kl_thr, float vf_thr, float* gate, float* skipped,
@@ -69,7 +69,7 @@ int pt_sample_actions_dev(const float* dec_out, int n, int A, const float* mask,
 struct PtcgMuon;
 int pt_muon_set_momentum(PtcgMuon* m, double momentum);
 long pt_adam_ws_floats();
-int pt_adam_step(float* w, float* g, float* m, float* v, long n, double lr, double b1, double b2,
+int pt_adam_step(float* w, float* g, float* m, float* v, long n, const double* lr, double b1, double b2,
                  double eps, float max_norm, const float* gate, int32_t* step, float* norm_out,
                  float* ws, hipStream_t s);
 

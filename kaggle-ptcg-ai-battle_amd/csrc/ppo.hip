@@ -22,7 +22,8 @@ struct PPOArgs {
     const float* mask; long mask_stride;
     const int32_t* idx;
     const float *actions, *old_logp, *adv, *ret, *val, *prio;
-    float clip, vf_clip, vf_coef, ent_coef;
+    float clip, vf_clip, vf_coef;
+    const float* ent_coef;   // device scalar (the reference's *a.ent_coef, pufferlib.cu:1063)
     float *grad, *ratio, *newvalue, *partial;
 };
 
@@ -86,7 +87,8 @@ __global__ __launch_bounds__(256) void ppo_loss_kernel(PPOArgs a) {
         const float vpred = lg[A];
         const float adv_n = (adv - mean) / (adv_std + 1e-8f);
 
-        const float d_ent_term = inv * (-a.ent_coef);
+        const float ent_coef = a.ent_coef[0];
+        const float d_ent_term = inv * (-ent_coef);
         // value loss + gradient (pufferlib.cu:1068-1085)
         const float v_err = vpred - vold;
         const float v_clipped = vold + fmaxf(-a.vf_clip, fminf(a.vf_clip, v_err));
@@ -123,7 +125,7 @@ __global__ __launch_bounds__(256) void ppo_loss_kernel(PPOArgs a) {
         st_v[0] = pg * inv;
         st_v[1] = v_loss * inv;
         st_v[2] = ent * inv;
-        st_v[3] = (pg + a.vf_coef * v_loss - a.ent_coef * ent) * inv;
+        st_v[3] = (pg + a.vf_coef * v_loss - ent_coef * ent) * inv;
         st_v[4] = -logratio * inv;
         st_v[5] = ((ratio - 1.0f) - logratio) * inv;
         st_v[6] = (fabsf(ratio - 1.0f) > a.clip ? 1.0f : 0.0f) * inv;
@@ -172,9 +174,10 @@ long pt_ppo_partial_floats(int n) { return (long)pt_cdiv(n, 4) * NSTAT; }
 int pt_ppo_loss(const float* out, int n, int A, const float* mask, long mask_stride,
                 const int32_t* idx, const float* actions, const float* old_logp,
                 const float* adv, const float* ret, const float* val, const float* prio,
-                float clip, float vf_clip, float vf_coef, float ent_coef, float* grad,
+                float clip, float vf_clip, float vf_coef, const float* ent_coef, float* grad,
                 float* ratio, float* newvalue, float* stats, float* guard, float* partial,
                 hipStream_t s) {
+    PT_REQUIRE(ent_coef != nullptr, "ppo loss: ent_coef must be a device scalar");
     PT_REQUIRE(n >= 2, "ppo loss: need at least 2 rows for the unbiased advantage variance (n=%d)", n);
     PT_REQUIRE(A >= 1 && A <= 64, "ppo loss: A=%d options unsupported (1..64)", A);
     PPOArgs a{out, n, A, mask, mask_stride, idx, actions, old_logp, adv, ret, val, prio,

@@ -62,19 +62,20 @@ _SIGS = {
     "ptcg_ppo_loss_fwd_bwd": (ctypes.c_int, [
         c_void_p, ctypes.c_int, ctypes.c_int, c_void_p, ctypes.c_int64, c_void_p,
         c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
-        ctypes.c_float, ctypes.c_float, ctypes.c_float, ctypes.c_float,
+        ctypes.c_float, ctypes.c_float, ctypes.c_float, c_void_p,
         c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
     "ptcg_kl_gate": (ctypes.c_int, [c_void_p, ctypes.c_float, ctypes.c_float, c_void_p,
                                     c_void_p, c_void_p]),
     "ptcg_adam_workspace_floats": (ctypes.c_int64, []),
     "ptcg_adam_step": (ctypes.c_int, [
         c_void_p, c_void_p, c_void_p, c_void_p, ctypes.c_int64,
-        ctypes.c_double, ctypes.c_double, ctypes.c_double, ctypes.c_double, ctypes.c_float,
+        c_void_p, ctypes.c_double, ctypes.c_double, ctypes.c_double, ctypes.c_float,
         c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
     "ptcg_trainer_create": (ctypes.c_int, [ctypes.POINTER(CPtcgDims), ctypes.POINTER(CPtcgHypers),
                                            ctypes.c_int, ctypes.POINTER(c_void_p)]),
     "ptcg_trainer_free": (None, [c_void_p]),
     "ptcg_trainer_set_hypers": (ctypes.c_int, [c_void_p, ctypes.POINTER(CPtcgHypers)]),
+    "ptcg_trainer_hyper_ptrs": (ctypes.c_int, [c_void_p, c_void_p, c_void_p]),
     "ptcg_trainer_set_weights": (ctypes.c_int, [c_void_p, c_float_p]),
     "ptcg_trainer_get_weights": (ctypes.c_int, [c_void_p, c_float_p]),
     "ptcg_trainer_get_grads": (ctypes.c_int, [c_void_p, c_float_p]),

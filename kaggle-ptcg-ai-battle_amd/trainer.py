@@ -48,7 +48,47 @@ TRAIN_DEFAULTS = {
     # "adam" (clip + Adam) or "muon" (the reference's optimizer: momentum = beta1,
     # decoupled weight decay muon_wd_1d on 1-D tensors)
     "optimizer": "adam", "muon_wd_1d": 0.0,
+    # per-epoch schedules of train_impl (pufferlib.cu:1912-1948; train_native.py
+    # build_args keys).  Off by default: the benchmark configs train at a fixed lr.
+    "anneal_lr": 0, "min_lr_ratio": 0.0, "lr_warmup_epochs": 0, "start_epoch": 0,
+    "lr_anneal_from_epoch": 0, "anneal_ent_coef": 0, "min_ent_coef_ratio": 0.1,
 }
+
+
+def _f32(x):
+    return float(np.float32(x))
+
+
+def cosine_annealing(base, lo, t, T):
+    """pufferlib.cu:1828-1833: lo + (base - lo)(1 + cos(pi t/T))/2, fp32 result."""
+    if T == 0:
+        return _f32(base)
+    ratio = min(1.0, max(0.0, _f32(t / T)))
+    return _f32(_f32(lo) + 0.5 * _f32(_f32(base) - _f32(lo)) * (1.0 + np.cos(np.pi * ratio)))
+
+
+def epoch_schedule(cfg, epoch):
+    """(lr, ent_coef) of train_impl's epoch ``epoch`` (pufferlib.cu:1912-1948):
+    cosine-annealed lr anchored at lr_anneal_from_epoch, times a linear warmup
+    over lr_warmup_epochs counted from start_epoch; cosine-annealed entropy
+    coefficient.  Both fp32 like the reference's.  With neither schedule on,
+    the configured values come back unchanged."""
+    lr, ent = cfg["learning_rate"], cfg["ent_coef"]
+    total = max(1, int(cfg["total_epochs"]))
+    if cfg["anneal_lr"] or cfg["lr_warmup_epochs"] > 0:
+        lr = _f32(lr)
+        if cfg["anneal_lr"]:
+            lr_min = _f32(_f32(cfg["min_lr_ratio"]) * lr)
+            t = max(0, epoch - int(cfg["lr_anneal_from_epoch"]))
+            T = max(1, total - int(cfg["lr_anneal_from_epoch"]))
+            lr = cosine_annealing(lr, lr_min, t, T)
+        if cfg["lr_warmup_epochs"] > 0:
+            ramp = epoch - int(cfg["start_epoch"])
+            lr = _f32(lr * min(1.0, _f32(_f32(ramp + 1) / _f32(cfg["lr_warmup_epochs"]))))
+    if cfg["anneal_ent_coef"]:
+        ent_min = _f32(_f32(cfg["min_ent_coef_ratio"]) * _f32(ent))
+        ent = cosine_annealing(ent, ent_min, epoch, total)
+    return lr, ent
 
 
 def _hypers(train):
@@ -154,9 +194,25 @@ class PuffeRL:
         return v.value
 
     def set_hypers(self, **kw):
+        """New hyper-parameters.  learning_rate and ent_coef reach the step
+        through device scalars (a captured step follows them); a change of
+        any other one drops the captured step (capture again)."""
         self.train_cfg.update(kw)
         self._chyp, self.train_cfg = _hypers(self.train_cfg)
         check(lib().ptcg_trainer_set_hypers(self._h, ctypes.byref(self._chyp)))
+
+    def write_schedule(self, lr, ent_coef):
+        """This epoch's lr and entropy coefficient into the device scalars
+        (train_impl's cudaMemcpy to lr_ptr / ppo_bufs.ent_coef,
+        pufferlib.cu:1933,1947); the configured base values stay."""
+        h, _ = _hypers(dict(self.train_cfg, learning_rate=lr, ent_coef=ent_coef))
+        check(lib().ptcg_trainer_set_hypers(self._h, ctypes.byref(h)))
+
+    def hyper_ptrs(self):
+        """Device addresses of the lr (double) and ent_coef (float) scalars."""
+        lr, ent = c_void_p(), c_void_p()
+        check(lib().ptcg_trainer_hyper_ptrs(self._h, ctypes.byref(lr), ctypes.byref(ent)))
+        return lr.value, ent.value
 
     # -------------------------------------------------- device helpers
     def to_device(self, a, dtype=np.float32):
@@ -321,6 +377,7 @@ def _train_segments(pl):
     seat = pl.dims.seat_col()
     P = lambda k: r[k].data_ptr()
     _, _, ratio_buf, nv_buf = pl.buffers()
+    pl.write_schedule(*epoch_schedule(cfg, pl.epoch))
     try:
         for _ in range(total_mb):
             check(L.ptcg_negamax_advantage(P("values"), P("rewards"), P("dones"), P("ratio"), P("obs"),
@@ -356,6 +413,7 @@ def train(pl, index_lists=None):
     from .synth import minibatch_indices
     r = pl.rollout
     B = pl.minibatch
+    pl.write_schedule(*epoch_schedule(pl.train_cfg, pl.epoch))
     if index_lists is None:
         ep = int(pl.train_cfg["update_epochs"])
         per = min(int(pl.train_cfg["minibatches_per_epoch"]), r["n"] // B)

@@ -100,3 +100,86 @@ def test_rollout_graph_slots_match_eager(cuda):
                 assert int(step.item()) == expect_step
     finally:
         pl.close()
+
+
+@pytest.mark.parametrize("opt", ["adam", "muon"])
+def test_captured_step_follows_lr_and_ent_coef(opt, cuda):
+    """lr and ent_coef are device scalars (the reference's lr_ptr and
+    ppo_bufs.ent_coef): after set_hypers / write_schedule, replays of the
+    graph captured before the change train at the new values, as eager
+    steps at those values do; the loss statistics show the new entropy
+    coefficient in total_loss."""
+    dm, B = dims.tiny(), 32
+    blob = om.build(dm, seed=61).to_blob()
+    rows = synth.make_obs(dm, 3 * B, seed=62, rich=True)
+    inp = synth.make_ppo_inputs(dm, rows, seed=63)
+    lists = synth.minibatch_indices(3 * B, B, 4, seed=64)
+    cfg = {"dims": dm, "init_weights": blob, "sync_free": True,
+           "train": dict(minibatch_size=B, learning_rate=1e-3, ent_coef=0.01, optimizer=opt)}
+    eager, graph = trainer.create_pufferl(cfg), trainer.create_pufferl(cfg)
+    try:
+        trainer.set_rollout(eager, rows, **inp)
+        trainer.set_rollout(graph, rows, **inp)
+        idx_buf = torch.from_numpy(np.asarray(lists[0], np.int32)).to("cuda")
+        torch.cuda.synchronize()
+        graph.capture_step(graph.rollout["obs"], idx_buf, graph.rollout)
+        sched = [(1e-3, 0.01), (3e-4, 0.05), (5e-5, 0.0), (2e-3, 0.02)]
+        for i, (ix, (lr, ent)) in enumerate(zip(lists, sched)):
+            graph.write_schedule(lr, ent)
+            eager.set_hypers(learning_rate=lr, ent_coef=ent)
+            idx_buf.copy_(torch.from_numpy(np.asarray(ix, np.int32)).to("cuda"))
+            graph.replay_step()
+            eager.step(eager.rollout["obs"], eager.to_device(np.asarray(ix, np.int32), np.int32), eager.rollout)
+            torch.cuda.synchronize()
+            lg_e, lg_g = trainer.log(eager), trainer.log(graph)
+            for k in ("entropy", "total_loss"):
+                assert abs(lg_g[k] - lg_e[k]) <= 1e-5 * max(1.0, abs(lg_e[k])), (i, k)
+            w_e, w_g = eager.get_weights(), graph.get_weights()
+            assert rel_l2(w_g, w_e) < 1e-5, i
+        # a run that kept the capture-time lr would have moved elsewhere
+        frozen = trainer.create_pufferl(cfg)
+        trainer.set_rollout(frozen, rows, **inp)
+        for ix in lists:
+            frozen.step(frozen.rollout["obs"], frozen.to_device(np.asarray(ix, np.int32), np.int32), frozen.rollout)
+        assert rel_l2(frozen.get_weights() - blob, graph.get_weights() - blob) > 0.1
+        frozen.close()
+    finally:
+        eager.close()
+        graph.close()
+
+
+def test_mode_and_hyper_changes_drop_the_captured_step(cuda):
+    """A change that a captured graph cannot follow (optimizer, precision,
+    sync-free / skip-masked modes, a by-value hyper-parameter, a new
+    importance-weight pointer) drops it: replay_step fails until the step is
+    captured again.  lr / ent_coef changes keep it."""
+    dm, B = dims.tiny(), 32
+    rows = synth.make_obs(dm, B, seed=71, rich=True)
+    pl = trainer.create_pufferl({"dims": dm, "sync_free": True, "train": dict(minibatch_size=B)})
+    try:
+        trainer.set_rollout(pl, rows, **synth.make_ppo_inputs(dm, rows, seed=72))
+        r = pl.rollout
+        from ptcg_amd.native import lib, check
+        prio = torch.ones(B, device="cuda")
+        changes = [
+            lambda: pl.set_hypers(clip_coef=0.3),
+            lambda: pl.set_hypers(max_grad_norm=0.7),
+            lambda: pl.set_hypers(kl_skip_threshold=0.05),
+            lambda: check(lib().ptcg_trainer_set_optimizer(pl._h, 1, 0.0)),
+            lambda: check(lib().ptcg_trainer_set_optimizer(pl._h, 0, 0.0)),
+            lambda: check(lib().ptcg_trainer_set_precision(pl._h, 1)),
+            lambda: check(lib().ptcg_trainer_set_skip_masked_options(pl._h, 0)),
+            lambda: check(lib().ptcg_trainer_set_prio(pl._h, prio.data_ptr())),
+            lambda: check(lib().ptcg_trainer_set_sync_free(pl._h, 1)),
+        ]
+        for k, change in enumerate(changes):
+            pl.capture_step(r["obs"], None, r)
+            pl.replay_step()
+            pl.write_schedule(1e-4, 0.02)          # device scalars: the graph stays
+            pl.replay_step()
+            change()
+            with pytest.raises(RuntimeError, match="no captured step"):
+                pl.replay_step()
+        torch.cuda.synchronize()
+    finally:
+        pl.close()

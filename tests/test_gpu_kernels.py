@@ -283,9 +283,10 @@ def test_ppo_loss_matches_oracle(n, A, cuda):
     inv = np.argsort(idx)
     L = native.lib()
     keep = [dev(a) for a in (scores, mask, acts, old, adv, ret, val)]   # hold device buffers
+    ent = dev(np.array([0.01], np.float32))   # device scalar, as in a captured step
     native.check(L.ptcg_ppo_loss_fwd_bwd(
         P(keep[0]), n, A, P(keep[1]), A, None, *[P(t) for t in keep[2:]], None,
-        0.2, 0.2, 0.5, 0.01, P(grad), P(ratio), P(nv), P(stats), P(guard), None))
+        0.2, 0.2, 0.5, P(ent), P(grad), P(ratio), P(nv), P(stats), P(guard), None))
     torch.cuda.synchronize()
     assert rel_l2(grad.cpu(), ref["grad"]) < 1e-5
     assert rel_l2(ratio.cpu(), ref["ratio"]) < 1e-6
@@ -299,7 +300,7 @@ def test_ppo_loss_matches_oracle(n, A, cuda):
     keep2 = [dev(a[inv]) for a in (mask, acts, old, adv, ret, val)] + [dev(idx, torch.int32)]
     native.check(L.ptcg_ppo_loss_fwd_bwd(
         P(keep[0]), n, A, P(keep2[0]), A, P(keep2[6]), *[P(t) for t in keep2[1:6]], None,
-        0.2, 0.2, 0.5, 0.01, P(grad2), None, None, None, None, None))
+        0.2, 0.2, 0.5, P(ent), P(grad2), None, None, None, None, None))
     torch.cuda.synchronize()
     assert rel_l2(grad2.cpu(), ref["grad"]) < 1e-5
 
@@ -315,6 +316,11 @@ def test_kl_gate(cuda):
         torch.cuda.synchronize()
         assert g.item() == want == oppo.kl_gate(kl, vf, kt, vt)
         assert sk.item() == 1.0 - want
+
+
+def lr_dev(lr):
+    """Adam's learning rate as the device double the kernel reads."""
+    return torch.tensor([lr], dtype=torch.float64, device="cuda")
 
 
 def _adam_case(n, seed):
@@ -334,12 +340,13 @@ def test_adam_matches_torch(n, max_norm, cuda):
     step = torch.zeros(1, dtype=torch.int32, device="cuda")
     ws = empty(native.lib().ptcg_adam_workspace_floats())
     norm = empty(1)
+    lr = lr_dev(3e-4)
     for it in range(3):
         gi = g * (1 + it)
         tp.grad = torch.from_numpy(gi.copy())
         tnorm = opt.step(max_norm)
         dg = dev(gi)
-        native.check(L.ptcg_adam_step(P(dp), P(dg), P(dm_), P(dv), n, 3e-4, 0.9, 0.999, 1e-8,
+        native.check(L.ptcg_adam_step(P(dp), P(dg), P(dm_), P(dv), n, P(lr), 0.9, 0.999, 1e-8,
                                       max_norm, None, P(step), P(norm), P(ws), None))
         torch.cuda.synchronize()
     torch.cuda.synchronize()
@@ -363,7 +370,8 @@ def test_adam_gate_zero_is_bit_exact_noop(cuda):
     ws = empty(L.ptcg_adam_workspace_floats())
     gate = dev(np.zeros(1, np.float32))
     dg = dev(g)
-    native.check(L.ptcg_adam_step(P(dp), P(dg), P(dm_), P(dv), n, 1e-3, 0.9, 0.999, 1e-8, 0.5,
+    lr = lr_dev(1e-3)
+    native.check(L.ptcg_adam_step(P(dp), P(dg), P(dm_), P(dv), n, P(lr), 0.9, 0.999, 1e-8, 0.5,
                                   P(gate), P(step), None, P(ws), None))
     torch.cuda.synchronize()
     assert np.array_equal(dp.cpu().numpy().view(np.uint32), p.view(np.uint32))
@@ -379,7 +387,8 @@ def test_adam_first_step_is_lr_sign(cuda):
     step = torch.zeros(1, dtype=torch.int32, device="cuda")
     ws = empty(L.ptcg_adam_workspace_floats())
     dg, dm_, dv = dev(g), empty(n), empty(n)
-    native.check(L.ptcg_adam_step(P(dp), P(dg), P(dm_), P(dv), n, 1e-3, 0.9, 0.999, 1e-8,
+    lr = lr_dev(1e-3)
+    native.check(L.ptcg_adam_step(P(dp), P(dg), P(dm_), P(dv), n, P(lr), 0.9, 0.999, 1e-8,
                                   1e6, None, P(step), None, P(ws), None))
     torch.cuda.synchronize()
     d = dp.cpu().numpy().astype(np.float64) - p

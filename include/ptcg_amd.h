@@ -147,6 +147,24 @@ int ptcg_ppo_loss_fwd_bwd(const float* dec_out, int n, int A,
                           float* grad, float* ratio, float* newvalue,
                           float* stats, float* guard, void* stream);
 
+/* ---- the PPO loss without allocation.  No counterpart in the reference:
+ * for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  Same
+ * arguments and results as ptcg_ppo_loss_fwd_bwd, which allocates its
+ * per-block partials on first use; this one keeps them in a static device
+ * array of the library (one per GPU, held until the process ends) and calls
+ * no allocator.  n <= PT_PPO_NOALLOC_MAX_ROWS, else PTCG_ERR_ARG.  All calls
+ * on one GPU share the array: calls that overlap on one GPU race.          */
+#define PT_PPO_NOALLOC_MAX_ROWS 65536
+int ptcg_ppo_loss_fwd_bwd_noalloc(const float* dec_out, int n, int A,
+                                  const float* mask, int64_t mask_stride, const int32_t* row_idx,
+                                  const float* actions, const float* old_logprobs,
+                                  const float* advantages, const float* returns,
+                                  const float* values, const float* prio,
+                                  float clip_coef, float vf_clip_coef, float vf_coef, const float* ent_coef,
+                                  float* grad, float* ratio, float* newvalue,
+                                  float* stats, float* guard, void* stream);
+
 /* ---- gate (pufferlib.cu:1292-1302): gate[0] = 1 apply / 0 skip, from
  * guard[0..1] = (approx_kl, v_loss); skipped[0] += 1 - gate.              */
 int ptcg_kl_gate(const float* guard, float kl_threshold, float vf_threshold,

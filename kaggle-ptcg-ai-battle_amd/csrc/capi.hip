@@ -243,6 +243,59 @@ extern "C" int ptcg_ppo_loss_fwd_bwd(const float* dec_out, int n, int A, const f
                        ratio, newvalue, stats, guard, part, s);
 }
 
+// ---- the PPO loss without allocation, for callers that cannot allocate
+// device memory (code under graph capture, serving loops, harnesses that
+// forbid hipMalloc).  Its per-block partials live in `scratch`, a
+// file-scope device array of PT_PPO_NOALLOC_MAX_ROWS rows' worth.  The
+// kernels write every partial they later read, so nothing needs clearing.
+// Each GPU has its own copy; all calls on one GPU share it, so calls that
+// overlap on one GPU (other streams, other threads) race.
+static __device__ __align__(256) float scratch[(PT_PPO_NOALLOC_MAX_ROWS / 4) * 7];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+float* g_scratch_ptr[kMaxDevices] = {};   // device address of `scratch`, per device
+}  // namespace
+
+// Device address of this device's `scratch`, looked up once per device with
+// that device current (the array's host-side name is not a device address).
+static int scratch_ptr(float** out) {
+    int dev = -1;
+    PT_HIP(hipGetDevice(&dev));
+    PT_REQUIRE(dev >= 0 && dev < kMaxDevices, "ppo_loss_noalloc: device %d out of range", dev);
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        PT_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        PT_REQUIRE(p != nullptr, "ppo_loss_noalloc: no device address for the scratch array");
+        g_scratch_ptr[dev] = static_cast<float*>(p);
+    }
+    *out = g_scratch_ptr[dev];
+    return PTCG_OK;
+}
+
+extern "C" int ptcg_ppo_loss_fwd_bwd_noalloc(const float* dec_out, int n, int A, const float* mask,
+                                             int64_t mask_stride, const int32_t* row_idx, const float* actions,
+                                             const float* old_logprobs, const float* advantages,
+                                             const float* returns, const float* values, const float* prio,
+                                             float clip_coef, float vf_clip_coef, float vf_coef,
+                                             const float* ent_coef, float* grad, float* ratio, float* newvalue,
+                                             float* stats, float* guard, void* stream) {
+    PT_REQUIRE(dec_out && mask && actions && old_logprobs && advantages && returns && values && grad && ent_coef,
+               "ppo_loss_noalloc: null input");
+    PT_REQUIRE(n >= 2 && n <= PT_PPO_NOALLOC_MAX_ROWS,
+               "ppo_loss_noalloc: n=%d rows outside [2, %d] (the scratch array's limit)", n,
+               PT_PPO_NOALLOC_MAX_ROWS);
+    PT_REQUIRE(pt_ppo_partial_floats(n) <= (long)(sizeof(scratch) / sizeof(float)),
+               "ppo_loss_noalloc: %ld partials exceed the scratch array", pt_ppo_partial_floats(n));
+    float* part = nullptr;
+    PT_TRY(scratch_ptr(&part));
+    return pt_ppo_loss(dec_out, n, A, mask, mask_stride, row_idx, actions, old_logprobs, advantages, returns,
+                       values, prio, clip_coef, vf_clip_coef, vf_coef, ent_coef, grad, ratio, newvalue, stats,
+                       guard, part, (hipStream_t)stream);
+}
+
 extern "C" int ptcg_kl_gate(const float* guard, float kl_threshold, float vf_threshold, float* gate,
                             float* skipped, void* stream) {
     PT_REQUIRE(guard && gate, "kl_gate: null buffer");

@@ -64,6 +64,11 @@ _SIGS = {
         c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
         ctypes.c_float, ctypes.c_float, ctypes.c_float, c_void_p,
         c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
+    "ptcg_ppo_loss_fwd_bwd_noalloc": (ctypes.c_int, [
+        c_void_p, ctypes.c_int, ctypes.c_int, c_void_p, ctypes.c_int64, c_void_p,
+        c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+        ctypes.c_float, ctypes.c_float, ctypes.c_float, c_void_p,
+        c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
     "ptcg_kl_gate": (ctypes.c_int, [c_void_p, ctypes.c_float, ctypes.c_float, c_void_p,
                                     c_void_p, c_void_p]),
     "ptcg_adam_workspace_floats": (ctypes.c_int64, []),

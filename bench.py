@@ -225,6 +225,9 @@ def main():
     ap.add_argument("--rollout-rows", type=int, default=8192)
     ap.add_argument("--rollout-precision", choices=("fp32", "bf16"), default="fp32",
                     help="--workload rollout: fp32 or bf16 GEMM and attention products")
+    ap.add_argument("--sampler", choices=("inverse_cdf", "gumbel"), default="gumbel",
+                    help="--workload rollout: the action draw (Gumbel-max from counter-based noise, "
+                         "or the reference's inverse CDF)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run three 256 MiB device-to-device copies (the HBM counter calibration)")
     ap.add_argument("--copy-rate", action="store_true",
@@ -448,7 +451,8 @@ def bench_rollout(args):
     graph = not args.stream
     bf = args.rollout_precision == "bf16"
     pl = trainer.create_pufferl({"dims": dm, "train": dict(TRAIN, minibatch_size=8), "seed": 0,
-                                 "sync_free": args.sync_free or graph, "precision": args.rollout_precision})
+                                 "sync_free": args.sync_free or graph, "precision": args.rollout_precision,
+                                 "sampler": args.sampler})
     d_obs = pl.to_device(obs)
     for i in range(args.warmup):
         pl.rollout_step(d_obs, n, seed=0, step=i)
@@ -495,7 +499,10 @@ def bench_rollout(args):
         "unit": "obs/s", "n_gpus": 1, "steps": K, "warmup": args.warmup, "ms_per_step": round(sec * 1e3 / K, 4),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16" if bf else "fp32", "data": "synthetic",
         "config": {"workload": f"inference forward of {n} obs rows (CORE model: 96 tokens + READOUT, d256/H4/"
-                               "FFN1024/4 layers) + one inverse-CDF action sample per row from Philox4x32-10",
+                               "FFN1024/4 layers) + one action per row, "
+                               + ("Gumbel-max over 64 options with Philox4x32-10 noise keyed (seed, step, row, option)"
+                                  if args.sampler == "gumbel" else "inverse-CDF draw from Philox4x32-10"),
+                   "sampler": args.sampler,
                    "rows": n, "seq_len": dm.l_tok + 1, "parallelism": "single GPU",
                    "launch": "HIP graph replay (step captured once)" if graph else "stream"},
         "roofline": dict(bound="mfma", kernel=("gemm_bf16_k16_kernel" if bf else "gemm_f32_dma_kernel + gemm_f32_kernel")

@@ -222,6 +222,21 @@ int ptcg_sample_actions(const float* dec_out, int n, int A, const float* mask, i
                         const int32_t* row_idx, uint64_t seed, uint64_t step, float* actions,
                         float* logprobs, float* values, float* uniforms, void* stream);
 
+/* ---- Gumbel-max sampler.  No counterpart in the reference (its rollout
+ * draws by inverse CDF, above); for callers that need draws reproducible
+ * bit for bit from (seed, step, row, option) or from given noise.
+ * action = argmax_j (l_j + g_j), ties to the lowest j, over the same safe,
+ * masked logits (mask == 0 -> -1e4); g_j = -log(-log u_j) with
+ * u_j = Philox4x32-10(counter = (row, step lo, step hi, 1 + j/4), key = seed),
+ * word j % 4, mapped to (0, 1) as above, and log evaluated by a fixed
+ * sequence of correctly rounded fp32 operations (so a CPU restatement
+ * reproduces every g_j).  noise: optional device (n, A) array of g_j to use
+ * instead (NULL = generate).  logprobs = l_a - logsumexp(l) (fp32), values
+ * = the last column.  noise_out: optional (n, A), the g_j used.  A <= 64.  */
+int ptcg_sample_actions_gumbel(const float* dec_out, int n, int A, const float* mask, int64_t mask_stride,
+                               const int32_t* row_idx, const float* noise, uint64_t seed, uint64_t step,
+                               float* actions, float* logprobs, float* values, float* noise_out, void* stream);
+
 /* ---- rollout-side steps of train_impl (pufferlib.cu:1847-2160) ----------
  * All buffers are device fp32 (int32 where named) on the caller's stream.
  *
@@ -316,6 +331,13 @@ int ptcg_trainer_capture_rollout(PtcgTrainer* t, int slot, const float* obs, con
                                  uint64_t seed, uint64_t* step_dev, float* actions, float* logprobs,
                                  float* values);
 int ptcg_trainer_replay_rollout(PtcgTrainer* t, int slot, void* stream);
+/* The rollout's draw (ptcg_trainer_rollout, capture_rollout): 0 = inverse
+ * CDF (default, the reference's sample_logits), 1 = Gumbel-max
+ * (ptcg_sample_actions_gumbel).  A change drops captured rollout slots.   */
+int ptcg_trainer_set_sampler(PtcgTrainer* t, int kind);
+/* device pointer of the rollout policy's (roll_n, n_opt+1) output of the
+ * last rollout call (for tests)                                           */
+int ptcg_trainer_rollout_output(PtcgTrainer* t, float** dec_out);
 /* floats per observation row of the trainer's dims (ptcg_obs_size).       */
 int ptcg_trainer_obs_size(PtcgTrainer* t);
 

@@ -340,6 +340,7 @@ struct PtcgTrainer {
     int prec = 0;
     int sync_free = 0;
     int skip_masked = 1;   // the PPO loss and the sampler mask those slots
+    int sampler = 0;       // rollout draws: 0 = inverse CDF (the reference's), 1 = Gumbel-max
     const float* prio = nullptr;   // policy-loss importance weights per rollout row
     PtcgMuon* muon = nullptr;      // optimizer 1 (Muon); nullptr = Adam
     // captured training step (sync-free mode): graph over fixed buffers
@@ -815,8 +816,26 @@ extern "C" int ptcg_trainer_rollout(PtcgTrainer* t, const float* obs, const int3
     PT_TRY(roll_model(t, n));
     float* out = nullptr;
     PT_TRY(ptcg_model_forward(t->roll, obs, row_idx, n, &out, stream));
+    if (t->sampler == 1)
+        return pt_sample_gumbel(out, n, t->dm.n_opt, obs + t->off.opt_mask, t->off.size, row_idx, nullptr, seed, step,
+                                nullptr, actions, logprobs, values, nullptr, (hipStream_t)stream);
     return ptcg_sample_actions(out, n, t->dm.n_opt, obs + t->off.opt_mask, t->off.size, row_idx, seed, step, actions,
                                logprobs, values, nullptr, stream);
+}
+
+extern "C" int ptcg_trainer_rollout_output(PtcgTrainer* t, float** dec_out) {
+    PT_REQUIRE(t && dec_out, "rollout_output: null argument");
+    PT_REQUIRE(t->roll, "rollout_output: no rollout has run");
+    *dec_out = pt_model_out(t->roll);
+    return PTCG_OK;
+}
+
+extern "C" int ptcg_trainer_set_sampler(PtcgTrainer* t, int kind) {
+    PT_REQUIRE(t, "set_sampler: null trainer");
+    PT_REQUIRE(kind == 0 || kind == 1, "set_sampler: kind %d (0 inverse CDF, 1 Gumbel-max)", kind);
+    if (kind != t->sampler) PT_TRY(drop_rollout_graphs(t));
+    t->sampler = kind;
+    return PTCG_OK;
 }
 
 // The reference captures one graph per (time step, buffer) of its rollout
@@ -843,7 +862,10 @@ extern "C" int ptcg_trainer_capture_rollout(PtcgTrainer* t, int slot, const floa
     PT_HIP(hipStreamBeginCapture(t->cap_stream, hipStreamCaptureModeThreadLocal));
     float* out = nullptr;
     int r = ptcg_model_forward(t->roll, obs, row_idx, n, &out, t->cap_stream);
-    if (r == PTCG_OK)
+    if (r == PTCG_OK && t->sampler == 1)
+        r = pt_sample_gumbel(out, n, t->dm.n_opt, obs + t->off.opt_mask, t->off.size, row_idx, nullptr, seed, 0,
+                             step_dev, actions, logprobs, values, nullptr, t->cap_stream);
+    else if (r == PTCG_OK)
         r = pt_sample_actions_dev(out, n, t->dm.n_opt, obs + t->off.opt_mask, t->off.size, row_idx, seed, step_dev,
                                   actions, logprobs, values, t->cap_stream);
     hipGraph_t g = nullptr;

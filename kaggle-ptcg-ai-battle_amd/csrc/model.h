@@ -66,6 +66,12 @@ int pt_kl_gate(const float* guard, float kl_thr, float vf_thr, float* gate, floa
 int pt_sample_actions_dev(const float* dec_out, int n, int A, const float* mask, long mask_stride,
                           const int32_t* row_idx, uint64_t seed, uint64_t* step_dev, float* actions,
                           float* logprobs, float* values, hipStream_t s);
+// Gumbel-max sampler; noise (n, A) optional (NULL = Philox noise for
+// (seed, step or *step_dev, row, option)); step_dev advanced by one when given
+int pt_sample_gumbel(const float* dec_out, int n, int A, const float* mask, long mask_stride,
+                     const int32_t* row_idx, const float* noise, uint64_t seed, uint64_t step,
+                     uint64_t* step_dev, float* actions, float* logprobs, float* values, float* noise_out,
+                     hipStream_t s);
 struct PtcgMuon;
 int pt_muon_set_momentum(PtcgMuon* m, double momentum);
 long pt_adam_ws_floats();

@@ -69,6 +69,11 @@ _SIGS = {
         c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
         ctypes.c_float, ctypes.c_float, ctypes.c_float, c_void_p,
         c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
+    "ptcg_sample_actions_gumbel": (ctypes.c_int, [
+        c_void_p, ctypes.c_int, ctypes.c_int, c_void_p, ctypes.c_int64, c_void_p, c_void_p,
+        ctypes.c_uint64, ctypes.c_uint64, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
+    "ptcg_trainer_set_sampler": (ctypes.c_int, [c_void_p, ctypes.c_int]),
+    "ptcg_trainer_rollout_output": (ctypes.c_int, [c_void_p, c_void_p]),
     "ptcg_kl_gate": (ctypes.c_int, [c_void_p, ctypes.c_float, ctypes.c_float, c_void_p,
                                     c_void_p, c_void_p]),
     "ptcg_adam_workspace_floats": (ctypes.c_int64, []),

@@ -185,6 +185,12 @@ class PuffeRL:
                                                  step_dev.data_ptr(), actions.data_ptr(), logprobs.data_ptr(),
                                                  values.data_ptr()))
 
+    def rollout_output(self):
+        """Device pointer of the last rollout call's (n, n_opt+1) output."""
+        p = c_void_p()
+        check(lib().ptcg_trainer_rollout_output(self._h, ctypes.byref(p)))
+        return p.value
+
     def replay_rollout(self, slot, stream=None):
         check(lib().ptcg_trainer_replay_rollout(self._h, slot, stream))
 
@@ -272,7 +278,9 @@ def create_pufferl(args):
     models), "precision": "fp32" | "bf16" (GEMM products), "sync_free": bool
     (compact row count kept on the device: no host read-back per forward, so
     the step can be graph-captured), "skip_masked_options": bool (default True:
-    the option scorer runs only legal options in steps and rollouts)}.  Unknown dims keys
+    the option scorer runs only legal options in steps and rollouts),
+    "sampler": "inverse_cdf" (default, the reference's rollout draw) | "gumbel"
+    (Gumbel-max from counter-based noise)}.  Unknown dims keys
     raise."""
     dm = args.get("dims", dims_mod.CORE)
     if isinstance(dm, dict):
@@ -288,6 +296,10 @@ def create_pufferl(args):
         check(lib().ptcg_trainer_set_sync_free(pl._h, 1))
     if not args.get("skip_masked_options", True):
         check(lib().ptcg_trainer_set_skip_masked_options(pl._h, 0))
+    sampler = args.get("sampler", "inverse_cdf")
+    if sampler not in ("inverse_cdf", "gumbel"):
+        raise ValueError(f"sampler must be 'inverse_cdf' or 'gumbel', got {sampler!r}")
+    check(lib().ptcg_trainer_set_sampler(pl._h, 1 if sampler == "gumbel" else 0))
     opt = pl.train_cfg["optimizer"]
     if opt not in ("adam", "muon"):
         raise ValueError(f"optimizer must be 'adam' or 'muon', got {opt!r}")

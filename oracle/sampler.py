@@ -17,6 +17,14 @@
   exp(l - logsumexp), fallback to the last legal option when rounding leaves
   the CDF below u; logprob = l[a] - logsumexp; value = the fused last column.
   Restated in float32 arithmetic in the same order.
+* Gumbel-max (no counterpart in the reference): a = argmax_j (l_j + g_j),
+  ties to the lowest j, g_j = -log(-log u_j), u_j from Philox4x32-10 with
+  counter (row, step lo, step hi, 1 + j/4), word j % 4.  ``log_rep`` is the
+  product's logarithm: argument reduction to m in [sqrt(1/2), sqrt(2)) and
+  the atanh series log m = 2 s (1 + z/3 + ... + z^5/11), s = (m-1)/(m+1),
+  z = s^2 (Abramowitz & Stegun 4.1.27), evaluated here with numpy float32
+  operations in the kernel's order, each correctly rounded, so the noise
+  and the draws agree bit for bit.
 """
 import numpy as np
 
@@ -109,3 +117,63 @@ def boundary_margin(dec_out, mask, u):
         cdf = np.cumsum(p / p.sum())
         out[i] = np.abs(cdf - float(u[i])).min()
     return out
+
+
+# ---- Gumbel-max
+_F = np.float32
+LOG_C = [_F(1 / 11), _F(1 / 9), _F(1 / 7), _F(1 / 5), _F(1 / 3)]
+LN2_HI = _F(0.693145751953125)                  # 0x3f317200: e * LN2_HI is exact
+LN2_LO = _F(np.log(2.0) - 0.693145751953125)    # 0x35bfbe8e
+
+
+def log_rep(x):
+    """log of positive normal float32 values, in the kernel's exact fp32 order."""
+    x = np.asarray(x, dtype=np.float32)
+    b = x.view(np.uint32).astype(np.int64)
+    e = (b >> 23) - 127
+    mb = (b & 0x007FFFFF) | 0x3F800000
+    big = mb > 0x3FB504F3
+    mb = np.where(big, mb - 0x00800000, mb)
+    e = np.where(big, e + 1, e)
+    m = mb.astype(np.uint32).view(np.float32)
+    s = (m - _F(1)) / (m + _F(1))
+    z = s * s
+    p = np.full_like(z, LOG_C[0])
+    for c in LOG_C[1:]:
+        p = c + z * p
+    p = _F(1) + z * p
+    lm = (s + s) * p
+    ef = e.astype(np.float32)
+    return ef * LN2_HI + (lm + ef * LN2_LO)
+
+
+def gumbel_uniforms(seed, step, n, A):
+    """u (n, A): Philox4x32-10 counter (row, step lo, step hi, 1 + j/4), word j % 4."""
+    groups = (A + 3) // 4
+    rows = np.repeat(np.arange(n, dtype=np.uint64), groups)
+    grp = np.tile(np.arange(groups, dtype=np.uint64), n) + np.uint64(1)
+    m = rows.size
+    ctr = np.stack([rows, np.full(m, step & 0xFFFFFFFF, np.uint64),
+                    np.full(m, (step >> 32) & 0xFFFFFFFF, np.uint64), grp], -1)
+    key = np.broadcast_to(np.array([seed & 0xFFFFFFFF, (seed >> 32) & 0xFFFFFFFF], np.uint64), (m, 2))
+    x = philox4x32_10(ctr, key).reshape(n, groups * 4)[:, :A]
+    return ((x >> np.uint32(9)).astype(np.float32) * np.float32(2) + np.float32(1)) * np.float32(2.0 ** -24)
+
+
+def gumbel_noise(seed, step, n, A):
+    return -log_rep(-log_rep(gumbel_uniforms(seed, step, n, A)))
+
+
+def sample_gumbel(dec_out, mask, noise):
+    """dec_out (n, A+1), mask (n, A), noise (n, A) -> actions (n,) int,
+    logprobs (n,) (float64 log-softmax of the draw), values (n,)."""
+    dec_out = np.asarray(dec_out, dtype=np.float32)
+    n, A1 = dec_out.shape
+    A = A1 - 1
+    l = np.stack([safe_masked(dec_out[i, :A], mask[i]) for i in range(n)])
+    v = l + np.asarray(noise, dtype=np.float32)          # fp32 adds
+    acts = np.argmax(v, axis=1)                           # first maximum
+    l64 = l.astype(np.float64)
+    lse = l64.max(1) + np.log(np.exp(l64 - l64.max(1, keepdims=True)).sum(1))
+    lps = l64[np.arange(n), acts] - lse
+    return acts, lps, dec_out[:, A].copy()

@@ -68,15 +68,17 @@ def test_capture_needs_sync_free(cuda):
         pl.close()
 
 
-def test_rollout_graph_slots_match_eager(cuda):
+@pytest.mark.parametrize("sampler", ["inverse_cdf", "gumbel"])
+def test_rollout_graph_slots_match_eager(sampler, cuda):
     """Two captured rollout slots over their own obs / output buffers (the
     reference's per-(t, buf) graphs), replayed in turn with the device step
     counter advancing per replay, give bit for bit what eager rollout calls
-    with the same steps give."""
+    with the same steps give, with either sampler."""
     dm, n = dims.CORE, 256
     blob = om.build(dm, seed=91).to_blob()
     obs = [synth.make_obs(dm, n, seed=92 + k) for k in range(2)]
-    cfg = {"dims": dm, "init_weights": blob, "sync_free": True, "train": dict(minibatch_size=64)}
+    cfg = {"dims": dm, "init_weights": blob, "sync_free": True, "sampler": sampler,
+           "train": dict(minibatch_size=64)}
     pl = trainer.create_pufferl(cfg)
     try:
         d_obs = [pl.to_device(o) for o in obs]

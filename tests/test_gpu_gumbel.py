@@ -1,0 +1,159 @@
+"""Config 5: rollout-inference over 8 192 observations with Gumbel-max
+sampling from a counter-based RNG (no counterpart in the reference, whose
+rollout draws by inverse CDF), fp32 and bf16.
+
+Bar:
+* noise: the kernel's g_j = -log(-log u_j) equal to the oracle's bit for
+  bit (same Philox words, same fp32 operation sequence of the logarithm);
+* actions: bit-exact (np.array_equal) against the oracle's argmax given the
+  same logits and the same noise — with generated noise and with noise
+  passed in;
+* the forward feeding the sampler: legal logits and values against the
+  oracle model at relative L2 1e-5 (fp32), and within the stated bf16
+  tolerance for the bf16 products (legal logits |d| <= 2e-2 max(1, |ref|),
+  value relative L2 <= 2e-2, mean masked-softmax KL <= 1e-3);
+* draws from the oracle's own logits: they may differ from the GPU's only
+  on rows whose top-two perturbed logits lie within the logits' error
+  (fp32: 1e-4, bf16: 2e-2 x scale) of each other; log-probabilities of the
+  draw within 1e-5 (fp32) / 5e-2 (bf16).
+"""
+import numpy as np
+import pytest
+import torch
+
+from conftest import rel_l2, d2h
+from ptcg_amd import dims, synth, trainer, native
+import oracle.model as om
+import oracle.sampler as osamp
+
+pytestmark = pytest.mark.gpu
+
+
+def _gumbel(dec, mask, seed, step, noise=None):
+    n, A1 = dec.shape
+    A = A1 - 1
+    d_dec = torch.from_numpy(np.ascontiguousarray(dec)).cuda()
+    d_mask = torch.from_numpy(np.ascontiguousarray(mask)).cuda()
+    d_noise = None if noise is None else torch.from_numpy(np.ascontiguousarray(noise, np.float32)).cuda()
+    acts = torch.empty(n, device="cuda")
+    lps, vals = torch.empty_like(acts), torch.empty_like(acts)
+    nout = torch.empty(n * A, device="cuda")
+    native.check(native.lib().ptcg_sample_actions_gumbel(
+        d_dec.data_ptr(), n, A, d_mask.data_ptr(), mask.shape[1], None,
+        None if d_noise is None else d_noise.data_ptr(), seed, step, acts.data_ptr(), lps.data_ptr(),
+        vals.data_ptr(), nout.data_ptr(), None))
+    torch.cuda.synchronize()
+    return (acts.cpu().numpy().astype(np.int64), lps.cpu().numpy(), vals.cpu().numpy(),
+            nout.cpu().numpy().reshape(n, A))
+
+
+@pytest.mark.parametrize("seed,step", [(0, 0), (987654321, 41), (2 ** 40 + 5, 2 ** 33 + 2)])
+def test_gumbel_kernel_bit_exact(seed, step, cuda):
+    rng = np.random.default_rng(seed % 997)
+    n, A = 8192, 64
+    dec = (rng.standard_normal((n, A + 1)) * 2).astype(np.float32)
+    mask = (rng.random((n, A)) < 0.4).astype(np.float32)
+    mask[np.arange(n), rng.integers(0, A, n)] = 1
+    dec[0, 3], dec[1, 4], dec[2, 5] = np.nan, np.inf, -np.inf
+    mask[1, 4] = 1
+    acts, lps, vals, noise = _gumbel(dec, mask, seed, step)
+    r_noise = osamp.gumbel_noise(seed, step, n, A)
+    assert np.array_equal(noise.view(np.uint32), r_noise.view(np.uint32))
+    r_acts, r_lps, r_vals = osamp.sample_gumbel(dec, mask, r_noise)
+    assert np.array_equal(acts, r_acts)
+    assert np.array_equal(vals, r_vals)
+    assert np.abs(lps - r_lps).max() < 1e-5
+    assert acts[1] == 4
+    assert np.all(mask[np.arange(n), acts] != 0)
+    # the same draws from the noise passed in; other noise, other draws
+    a2 = _gumbel(dec, mask, seed, step, noise=r_noise)[0]
+    assert np.array_equal(a2, acts)
+    other = osamp.gumbel_noise(seed, step + 1, n, A)
+    a3 = _gumbel(dec, mask, seed, step, noise=other)[0]
+    assert np.array_equal(a3, osamp.sample_gumbel(dec, mask, other)[0])
+    assert (a3 != acts).mean() > 0.3
+
+
+def test_gumbel_ties_and_small_heads(cuda):
+    n, A = 64, 5
+    dec = np.zeros((n, A + 1), np.float32)
+    mask = np.ones((n, A), np.float32)
+    noise = np.zeros((n, A), np.float32)          # every option ties: lowest index
+    assert np.array_equal(_gumbel(dec, mask, 1, 1, noise)[0], np.zeros(n))
+    mask[:, 0] = 0                                  # masked first option: next one
+    assert np.array_equal(_gumbel(dec, mask, 1, 1, noise)[0], np.ones(n))
+
+
+def test_gumbel_distribution(cuda):
+    A = 12
+    logits = np.linspace(-2, 2, A).astype(np.float32)
+    mask = np.ones(A, np.float32)
+    mask[[3, 7]] = 0
+    n = 60000
+    dec = np.tile(np.append(logits, 0.0).astype(np.float32), (n, 1))
+    acts = _gumbel(dec, np.tile(mask, (n, 1)), 99, 1)[0]
+    l = np.where(mask == 0, -1e4, logits).astype(np.float64)
+    p = np.exp(l - l.max())
+    p /= p.sum()
+    cnt = np.bincount(acts, minlength=A)
+    assert cnt[3] == 0 and cnt[7] == 0
+    k = p > 1e-9
+    chi2 = ((cnt[k] - n * p[k]) ** 2 / (n * p[k])).sum()
+    assert chi2 < 29.6   # 9 dof, p = 0.0005
+
+
+@pytest.mark.parametrize("prec", ["fp32", "bf16"])
+def test_config5_rollout_8192(prec, cuda):
+    dm, n, seed, step = dims.CORE, 8192, 31, 17
+    ref = om.build(dm, seed=51)
+    rows = synth.make_obs(dm, n, seed=52)
+    pl = trainer.create_pufferl({"dims": dm, "init_weights": ref.to_blob(), "precision": prec,
+                                 "sampler": "gumbel", "train": dict(minibatch_size=64)})
+    try:
+        acts, lps, vals = pl.rollout_step(pl.to_device(rows), n, seed=seed, step=step)
+        torch.cuda.synchronize()
+        dec = d2h(pl.rollout_output(), (n, dm.n_opt + 1))
+        acts = acts.cpu().numpy().astype(np.int64)
+        lps, vals = lps.cpu().numpy(), vals.cpu().numpy()
+    finally:
+        pl.close()
+    m0, m1 = dm.offsets()["opt_mask"]
+    mask = rows[:, m0:m1]
+    legal = mask != 0
+    noise = osamp.gumbel_noise(seed, step, n, dm.n_opt)
+    # the sampler: bit-exact given the GPU's logits and the same noise
+    g_acts, g_lps, g_vals = osamp.sample_gumbel(dec, mask, noise)
+    assert np.array_equal(acts, g_acts)
+    assert np.array_equal(vals, dec[:, -1])
+    # the forward against the oracle model
+    with torch.no_grad():
+        want = torch.cat([ref(torch.from_numpy(rows[i:i + 1024])) for i in range(0, n, 1024)]).numpy()
+    A = dm.n_opt
+    if prec == "fp32":
+        assert rel_l2(dec[:, :A][legal], want[:, :A][legal]) <= 1e-5
+        assert rel_l2(dec[:, A], want[:, A]) <= 1e-5
+        tol, lp_tol = 1e-4, 1e-5
+    else:
+        assert np.all(np.abs(dec[:, :A] - want[:, :A])[legal] <= 2e-2 * np.maximum(1.0, np.abs(want[:, :A][legal])))
+        assert rel_l2(dec[:, A], want[:, A]) <= 2e-2
+        lw = np.where(legal, want[:, :A], -1e4).astype(np.float64)
+        lg = np.where(legal, dec[:, :A], -1e4).astype(np.float64)
+        pw = np.exp(lw - lw.max(1, keepdims=True))
+        pw /= pw.sum(1, keepdims=True)
+        lsw = np.log(pw + 1e-300)
+        lsg = lg - lg.max(1, keepdims=True)
+        lsg = lsg - np.log(np.exp(lsg).sum(1, keepdims=True))
+        kl = (pw * (lsw - lsg)).sum(1).mean()
+        assert kl <= 1e-3, kl
+        tol, lp_tol = 2e-2 * max(1.0, float(np.abs(want[:, :A][legal]).max())), 5e-2
+    # draws from the oracle's own logits: flips only at near-ties
+    o_acts, o_lps, _ = osamp.sample_gumbel(want, mask, noise)
+    diff = o_acts != acts
+    if diff.any():
+        v = np.where(legal, want[:, :A], -1e4).astype(np.float64) + noise
+        top2 = np.sort(v, axis=1)[:, -2:]
+        margin = top2[:, 1] - top2[:, 0]
+        assert np.all(margin[diff] <= 2 * tol), margin[diff].max()
+    assert diff.mean() <= (1e-3 if prec == "fp32" else 5e-2), diff.mean()
+    same = ~diff
+    assert np.abs(lps[same] - o_lps[same]).max() <= lp_tol

@@ -63,3 +63,68 @@ def test_sampling_distribution_matches_softmax():
 def test_safe_logits():
     l = S.safe_masked(np.array([np.nan, np.inf, -np.inf, 1.0], np.float32), np.array([1, 1, 1, 0]))
     assert l[0] == 0 and l[1] == np.float32(3.4028e38) and l[2] == np.float32(-3.4028e38) and l[3] == np.float32(-1e4)
+
+
+# ---- Gumbel-max sampler of the oracle: pinned by float64 math and closed forms
+
+def test_log_rep_against_float64_log():
+    """log_rep within 3 ulp of the float64 logarithm over every binade the
+    Gumbel transform meets (and well beyond), exact at 1."""
+    rng = np.random.default_rng(0)
+    x = np.concatenate([
+        (rng.random(400000) * np.float32(2.0) ** rng.integers(-30, 30, 400000)).astype(np.float32),
+        np.float32(2.0) ** np.arange(-126, 127, dtype=np.float32),
+        np.array([1.0, np.nextafter(np.float32(1), np.float32(2)), np.nextafter(np.float32(1), np.float32(0)),
+                  1.41421354, 1.41421366, 0.70710677], np.float32)])
+    x = x[(x > 0) & np.isfinite(x) & (x >= np.finfo(np.float32).tiny)]
+    got = S.log_rep(x).astype(np.float64)
+    want = np.log(x.astype(np.float64))
+    ulp = np.spacing(np.abs(want).astype(np.float32)).astype(np.float64)
+    ok = want != 0
+    assert np.max(np.abs(got - want)[ok] / ulp[ok]) <= 3.0
+    assert S.log_rep(np.float32(1.0)) == 0.0
+
+
+def test_gumbel_noise_distribution_and_layout():
+    """g = -log(-log u): mean = Euler's gamma, variance = pi^2 / 6, CDF
+    exp(-exp(-g)) (Kolmogorov-Smirnov); the uniforms are the Philox words of
+    counter (row, step lo, step hi, 1 + j/4), word j % 4."""
+    n, A = 4096, 64
+    g = S.gumbel_noise(11, 5, n, A).astype(np.float64).ravel()
+    assert abs(g.mean() - 0.5772156649) < 5e-3
+    assert abs(g.var() - np.pi ** 2 / 6) < 2e-2
+    gs = np.sort(g)
+    cdf = np.exp(-np.exp(-gs))
+    emp = np.arange(1, gs.size + 1) / gs.size
+    assert np.abs(cdf - emp).max() < 1.63 / np.sqrt(gs.size) * 1.5
+    u = S.gumbel_uniforms(3, 2 ** 33 + 9, 3, 8)
+    w = S.philox4x32_10(np.array([[2, 9, 2, 2]], np.uint64), np.array([[3, 0]], np.uint64))[0]
+    want = ((w >> np.uint32(9)).astype(np.float32) * np.float32(2) + np.float32(1)) * np.float32(2.0 ** -24)
+    assert np.array_equal(u[2, 4:8], want)
+
+
+def test_gumbel_max_samples_the_masked_softmax():
+    A, n = 10, 200000
+    logits = np.linspace(-1.5, 2.0, A).astype(np.float32)
+    mask = np.ones(A, np.float32)
+    mask[[0, 6]] = 0
+    dec = np.tile(np.append(logits, 0).astype(np.float32), (n, 1))
+    acts, lps, _ = S.sample_gumbel(dec, np.tile(mask, (n, 1)), S.gumbel_noise(4, 0, n, A))
+    l = np.where(mask == 0, -1e4, logits).astype(np.float64)
+    p = np.exp(l - l.max())
+    p /= p.sum()
+    cnt = np.bincount(acts, minlength=A)
+    assert cnt[0] == 0 and cnt[6] == 0
+    k = p > 1e-9
+    assert ((cnt[k] - n * p[k]) ** 2 / (n * p[k])).sum() < 26.1   # 7 dof, p = 0.0005
+    assert np.allclose(lps, np.log(p[acts]), atol=1e-12)
+
+
+def test_gumbel_ties_and_single_legal():
+    dec = np.zeros((3, 5), np.float32)
+    mask = np.ones((3, 4), np.float32)
+    mask[1, :2] = 0
+    mask[2] = [0, 0, 1, 0]
+    acts, lps, _ = S.sample_gumbel(dec, mask, np.zeros((3, 4), np.float32))
+    assert list(acts) == [0, 2, 2]
+    assert lps[2] == 0.0

@@ -4,7 +4,9 @@
 seeded permutations (the same index lists for both sides); global-norm clip 0.5
 then Adam (lr 3e-4, betas 0.9/0.999, eps 1e-8).  The weight blob after the 32nd
 step must agree at relative L2 1e-4; every element within 2*lr*steps (Adam's
-normalised step near g = 0 is a sign function of rounding noise).  The loss
+normalised step near g = 0 is a sign function of rounding noise).  The update
+(weights after minus before): at most 2 % of its elements outside relative
+1e-4 and 0.5 % outside 1e-3 (each + 1e-3 lr absolute), relative L2 <= 5e-3.  The loss
 statistics summed over the 32 minibatches agree at relative 1e-3 (clipfrac
 counts ratio comparisons at the clip boundary, which rounding can flip).
 
@@ -54,7 +56,18 @@ def test_full_update_4_epochs_x_8_minibatches(cuda):
     err = rel_l2(w_gpu, w_ref)
     assert err < 1e-4, err
     assert np.abs(w_gpu - w_ref).max() <= 2.0 * 3e-4 * steps
-    assert rel_l2(w_gpu - w0, w_ref - w0) < 1e-2
+    # the update itself, element by element: outside relative 1e-4 (plus
+    # 1e-3 lr absolute) only where Adam's normalised step follows rounding
+    # noise of a near-zero gradient; measured 0.9 % of elements (0.2 %
+    # outside 1e-3), update relative L2 1.7e-3
+    du_g, du_r = (w_gpu - w0).astype(np.float64), (w_ref - w0).astype(np.float64)
+    e = np.abs(du_g - du_r)
+    out4 = (e > 1e-4 * np.abs(du_r) + 1e-3 * 3e-4).mean()
+    out3 = (e > 1e-3 * np.abs(du_r) + 1e-3 * 3e-4).mean()
+    print(f"update: {out4:.2e} of elements outside rel 1e-4, {out3:.2e} outside 1e-3, "
+          f"relative L2 {rel_l2(du_g, du_r):.2e}", flush=True)
+    assert out4 <= 0.02 and out3 <= 0.005, (out4, out3)
+    assert rel_l2(du_g, du_r) < 5e-3
     names = ("policy_loss", "value_loss", "entropy", "total_loss", "old_approx_kl", "approx_kl")
     for i, k in enumerate(names):
         want = float(stats[i]) / steps

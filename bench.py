@@ -123,19 +123,33 @@ def algorithmic_gemm_bytes(dm, obs_rows):
     return 4.0 * tot
 
 
+def gemm_source_sha():
+    """sha256 (first 16 hex) of the GEMM kernel source the library was built from."""
+    import hashlib
+    with open(os.path.join(ROOT, "kaggle-ptcg-ai-battle_amd", "csrc", "gemm.hip"), "rb") as f:
+        return hashlib.sha256(f.read()).hexdigest()[:16]
+
+
 def measured_gemm_traffic():
     """HBM bytes per GEMM launch measured with rocprofv3 --pmc (FETCH_SIZE,
     WRITE_SIZE, copy-kernel calibrated) for this workload, read from the
-    committed profile summary; None when absent."""
+    committed profile summary, which records the sha256 of the gemm.hip it
+    was measured on.  Returns (bytes or None, provenance note): None when the
+    summary is absent or was measured on another gemm.hip (stale)."""
     import re
-    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
-                        "ptcg_step_b512_fp32_gemm_hbm_traffic.md")
+    rel = os.path.join("profiles", "ptcg_step_b512_fp32_gemm_hbm_traffic.md")
     try:
-        txt = open(path).read()
+        txt = open(os.path.join(ROOT, rel)).read()
     except OSError:
-        return None
+        return None, f"{rel} absent"
     m = re.search(r"traffic_bytes_per_launch\s*\|\s*([0-9.e+]+)", txt)
-    return float(m.group(1)) if m else None
+    h = re.search(r"gemm_hip_sha256_16\s*\|\s*([0-9a-f]+)", txt)
+    cur = gemm_source_sha()
+    if not m or not h:
+        return None, f"{rel} has no traffic figure with its gemm.hip sha"
+    if h.group(1) != cur:
+        return None, f"stale: {rel} was measured on gemm.hip {h.group(1)}, this build is {cur}"
+    return float(m.group(1)), f"rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, {rel} (gemm.hip {cur})"
 
 
 def hbm_kernels(L, K):
@@ -183,33 +197,38 @@ def native_check(rc):
     native.check(rc)
 
 
-def cpu_baseline(dm, obs, inp, B, budget_s):
-    """Oracle (torch CPU) fwd+bwd+PPO+clip+Adam on B-row minibatches of the
-    same rollout until `budget_s` of CPU work; returns obs/s and the sample."""
+def cpu_baseline(dm, obs, inp, B, budget_s, warmup=3, timed=10):
+    """Oracle (torch CPU, fp32) fwd+bwd+PPO+clip+Adam on B-row minibatches of
+    the same rollout: `warmup` untimed steps, then the median of `timed`
+    steps (more while under `budget_s` of timed CPU work).  Threads: the
+    host's os.cpu_count(), unless OMP_NUM_THREADS sets the process's share
+    (both are reported)."""
     import torch
     import oracle.model as om
     import oracle.adam as oa
     import oracle.step as ost
-    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    host = os.cpu_count() or 1
+    omp = os.environ.get("OMP_NUM_THREADS")
+    threads = int(omp) if omp else host
     torch.set_num_threads(threads)
     ref = om.build(dm, seed=0)
     opt = oa.OracleAdam([p for _, p in ref.named_blob_params()], lr=TRAIN["learning_rate"])
     hyp = dict(TRAIN)
     rng = np.random.default_rng(0)
     times = []
-    t_start = time.perf_counter()
-    while True:
+    for k in range(warmup + 10 ** 6):
         idx = rng.choice(len(obs), B, replace=False)
         t0 = time.perf_counter()
-        ost.minibatch_step(ref, opt, obs[idx], {k: v[idx] for k, v in inp.items()}, hyp)
-        times.append(time.perf_counter() - t0)
-        if time.perf_counter() - t_start > budget_s or len(times) >= 10:
+        ost.minibatch_step(ref, opt, obs[idx], {k2: v[idx] for k2, v in inp.items()}, hyp)
+        if k >= warmup:
+            times.append(time.perf_counter() - t0)
+        if len(times) >= timed and sum(times) > budget_s or len(times) >= 4 * timed:
             break
-    timed = times[1:] if len(times) > 1 else times
-    med = float(np.median(timed))
-    return dict(value=B / med, unit="obs/s", cores=threads, kind="port",
-                sample=f"{len(timed)} timed (+1 warmup) oracle minibatch steps of {B} rows "
-                       f"(fwd+bwd+PPO+clip+Adam, torch CPU fp32), median {med:.2f} s/step")
+    med = float(np.median(times))
+    return dict(value=B / med, unit="obs/s", cores=threads, kind="port", host_cpu_count=host,
+                omp_num_threads=int(omp) if omp else None,
+                sample=f"median of {len(times)} timed oracle minibatch steps of {B} rows after {warmup} warmup "
+                       f"(fwd+bwd+PPO+clip+Adam, torch CPU fp32, {threads} threads), {med:.2f} s/step")
 
 
 def main():
@@ -219,7 +238,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--minibatch", type=int, default=512)
     ap.add_argument("--rollout", type=int, default=16384)
-    ap.add_argument("--cpu-seconds", type=float, default=20.0)
+    ap.add_argument("--cpu-seconds", type=float, default=20.0,
+                    help="CPU baseline: keep timing past 10 steps while under this many seconds")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--workload", choices=("train", "rollout", "frozen", "bf16", "replay"), default="train")
     ap.add_argument("--rollout-rows", type=int, default=8192)
@@ -382,11 +402,12 @@ def main():
     gemm_s = ms.value / 1e3
     achieved = useful / gemm_s / 1e12
     peak = BF16_MFMA_PEAK_TFLOPS if bf16 else FP32_MFMA_PEAK_TFLOPS
+    traffic = measured_gemm_traffic()
     kname = "gemm_bf16_k16_kernel + gemm_bf16_kernel" if bf16 else "gemm_f32_dma_kernel + gemm_f32_kernel"
     roof = dict(bound="mfma", kernel=f"{kname} (all launches: trunk, token, option and head GEMMs)",
                 achieved=round(achieved, 3), peak=peak, unit="TFLOP/s",
                 frac=round(achieved / peak, 4),
-                traffic=None if bf16 else measured_gemm_traffic(),
+                traffic=None if bf16 else traffic[0], traffic_source=None if bf16 else traffic[1],
                 algorithmic_bytes_per_launch=round(abytes / max(launches.value, 1)),
                 launches_per_step=launches.value / K,
                 avg_launch_us=round(ms.value * 1e3 / max(launches.value, 1), 3),

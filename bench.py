@@ -544,32 +544,37 @@ def bench_rollout(args):
 
 def bench_transport(pl, dm, obs, n, args):
     """PCIe-inclusive rollout rate through the pinned transport (vecenv.h GPU
-    mode): the n agents split into two env buffers; per buffer and step the
-    captured rollout graph on the buffer's stream, D2H of its actions and a
-    stream sync, then the async H2D of its observations, rewards and
-    terminals, which overlaps the other buffer's forward.  Not `value`: the
-    observations cross PCIe here."""
+    mode): the n agents split into two env buffers, each on its own rollout
+    policy (activations), stream and draw-step counter; per step both
+    buffers' captured rollout graphs and action downloads are launched, then
+    each buffer's checked stream sync is followed by the async H2D of its
+    observations, rewards and terminals, which overlaps the other buffer's
+    work.  Not `value`: the observations cross PCIe here."""
     import torch
     from ptcg_amd import transport as tr
     nbuf = 2
     x = tr.RolloutTransport(n, nbuf, dm.obs_size)
     try:
         x.observations[:] = obs
-        step_dev = torch.zeros(1, dtype=torch.int64, device="cuda")
+        step_dev = [torch.zeros(1, dtype=torch.int64, device="cuda") for _ in range(nbuf)]
         for b in range(nbuf):
-            x.capture_rollout(pl, b, 1 + b, 0, step_dev)   # slots 1, 2
+            x.capture_rollout(pl, b, 1 + b, 0, step_dev[b])   # slots 1, 2
         for b in range(nbuf):
             x.upload(b)
-        for _ in range(2):   # warm the slots
+
+        def step():
             for b in range(nbuf):
-                x.step(pl, b, 1 + b)
+                x.launch(pl, b, 1 + b)
+            for b in range(nbuf):
+                x.wait(b)
                 x.upload(b)
+
+        for _ in range(2):   # warm the slots
+            step()
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         for _ in range(args.steps):
-            for b in range(nbuf):
-                x.step(pl, b, 1 + b)
-                x.upload(b)
+            step()
         torch.cuda.synchronize()
         sec = time.perf_counter() - t0
         if not np.isfinite(x.actions).all():
@@ -579,7 +584,8 @@ def bench_transport(pl, dm, obs, n, args):
                     ms_per_step=round(sec * 1e3 / args.steps, 4), h2d_bytes_per_step=int(h2d),
                     d2h_bytes_per_step=int(x.actions.nbytes),
                     note="pinned host observations up and actions down per env buffer around the captured "
-                         "rollout graph (PCIe-inclusive; the env step itself is not run)")
+                         "rollout graphs, buffers' forwards in flight together (PCIe-inclusive; the env step "
+                         "itself is not run)")
     finally:
         x.close()
 

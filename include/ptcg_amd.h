@@ -312,6 +312,14 @@ int ptcg_trainer_debug_forward(PtcgTrainer* t, const float* obs_host, int n, flo
 int ptcg_trainer_rollout(PtcgTrainer* t, const float* obs, const int32_t* row_idx, int n,
                          uint64_t seed, uint64_t step, float* actions, float* logprobs,
                          float* values, void* stream);
+/* The same on rollout policy `buf` (0 <= buf < 64): each policy has its own
+ * inference activations (registered for the n of its calls), so calls on
+ * different policies may run concurrently on different streams — the
+ * reference's per-buffer rollout threads and streams (pufferlib.cu:502-509,
+ * vecenv.h:259-384).  ptcg_trainer_rollout is policy 0.                   */
+int ptcg_trainer_rollout_on(PtcgTrainer* t, int buf, const float* obs, const int32_t* row_idx, int n,
+                            uint64_t seed, uint64_t step, float* actions, float* logprobs,
+                            float* values, void* stream);
 /* Optimizer of the trainer's steps: 0 = clip + Adam (default), 1 = Muon
  * (ptcg_muon_*, momentum = hyp.beta1, weight decay 0 on >= 2-D tensors,
  * wd_1d on 1-D tensors, lr = hyp.lr).  save_state / load_state then use the
@@ -331,6 +339,11 @@ int ptcg_trainer_capture_rollout(PtcgTrainer* t, int slot, const float* obs, con
                                  uint64_t seed, uint64_t* step_dev, float* actions, float* logprobs,
                                  float* values);
 int ptcg_trainer_replay_rollout(PtcgTrainer* t, int slot, void* stream);
+/* capture_rollout on rollout policy `buf` (see ptcg_trainer_rollout_on):
+ * slots captured on different policies may replay concurrently.           */
+int ptcg_trainer_capture_rollout_on(PtcgTrainer* t, int buf, int slot, const float* obs, const int32_t* row_idx,
+                                    int n, uint64_t seed, uint64_t* step_dev, float* actions, float* logprobs,
+                                    float* values);
 /* The rollout's draw (ptcg_trainer_rollout, capture_rollout): 0 = inverse
  * CDF (default, the reference's sample_logits), 1 = Gumbel-max
  * (ptcg_sample_actions_gumbel).  A change drops captured rollout slots.   */
@@ -368,14 +381,21 @@ int ptcg_transport_upload(PtcgTransport* x, int buf);
 /* D2H of the buffer's actions on its stream, then a checked stream sync
  * (vecenv.h:311-337: the env must not step on stale actions)              */
 int ptcg_transport_download(PtcgTransport* x, int buf);
-/* ptcg_trainer_capture_rollout into slot `slot` over the buffer's device
- * slices (observations in, actions / log-probs / values out; num_atns 1) */
+/* ptcg_trainer_capture_rollout_on(t, buf, slot, ...) over the buffer's
+ * device slices (observations in, actions / log-probs / values out;
+ * num_atns 1): buffer b runs on rollout policy b, so buffers' steps may
+ * overlap                                                                 */
 int ptcg_transport_capture_rollout(PtcgTransport* x, PtcgTrainer* t, int buf, int slot, uint64_t seed,
                                    uint64_t* step_dev);
 /* one rollout step of a buffer (net_callback + the actions' trip,
  * vecenv.h:309-337): replay slot `slot` on the buffer's stream, then
  * ptcg_transport_download                                                 */
 int ptcg_transport_step(PtcgTransport* x, PtcgTrainer* t, int buf, int slot);
+/* the same split in two, so that one host thread can keep several buffers'
+ * forwards in flight: launch = replay + async D2H of the actions (returns at
+ * once); wait = the buffer's checked stream sync                          */
+int ptcg_transport_launch(PtcgTransport* x, PtcgTrainer* t, int buf, int slot);
+int ptcg_transport_wait(PtcgTransport* x, int buf);
 
 /* ptcg_model_set_precision on the trainer's models (train and rollout).  */
 int ptcg_trainer_set_precision(PtcgTrainer* t, int prec);

@@ -333,10 +333,12 @@ struct PtcgTrainer {
     // (the reference's lr_ptr and ppo_bufs.ent_coef, pufferlib.cu:1912-1948)
     double* lr_dev;
     float* ent_dev;
-    // rollout policy: a second model on the same weights with inference
-    // activations for `roll_n` rows (reg_rollout), made on first use
-    PtcgModel* roll = nullptr;
-    int roll_n = 0;
+    // rollout policies: models on the same weights with inference
+    // activations (reg_rollout), one per env buffer so that buffers' forwards
+    // may overlap on their own streams (the reference's per-buffer threads,
+    // pufferlib.cu:502-509); made on first use, rolls[b] for roll_n[b] rows
+    std::vector<PtcgModel*> rolls;
+    std::vector<int> roll_n;
     int prec = 0;
     int sync_free = 0;
     int skip_masked = 1;   // the PPO loss and the sampler mask those slots
@@ -347,8 +349,10 @@ struct PtcgTrainer {
     hipStream_t cap_stream = nullptr;
     hipGraph_t graph = nullptr;
     hipGraphExec_t graph_exec = nullptr;
-    // captured rollout steps, one per slot (the reference's per-(t, buf) graphs)
+    // captured rollout steps, one per slot (the reference's per-(t, buf)
+    // graphs), and the rollout policy each was captured on
     std::vector<hipGraphExec_t> roll_exec;
+    std::vector<int> roll_exec_buf;
     double wd_1d = 0.0;
     int64_t global_step = 0, epoch = 0;
     std::vector<float> st_f[5];
@@ -358,7 +362,8 @@ struct PtcgTrainer {
 extern "C" void ptcg_trainer_free(PtcgTrainer* t) {
     if (!t) return;
     if (t->model) ptcg_model_free(t->model);
-    if (t->roll) ptcg_model_free(t->roll);
+    for (auto r : t->rolls)
+        if (r) ptcg_model_free(r);
     if (t->muon) ptcg_muon_free(t->muon);
     for (auto x : t->roll_exec)
         if (x) (void)hipGraphExecDestroy(x);
@@ -395,12 +400,13 @@ static int drop_step_graph(PtcgTrainer* t) {
     }
     return PTCG_OK;
 }
-static int drop_rollout_graphs(PtcgTrainer* t) {
-    for (auto& x : t->roll_exec)
-        if (x) {
+// buf < 0: every slot; else the slots captured on rollout policy buf
+static int drop_rollout_graphs(PtcgTrainer* t, int buf = -1) {
+    for (size_t i = 0; i < t->roll_exec.size(); ++i)
+        if (t->roll_exec[i] && (buf < 0 || t->roll_exec_buf[i] == buf)) {
             PT_HIP(hipDeviceSynchronize());
-            PT_HIP(hipGraphExecDestroy(x));
-            x = nullptr;
+            PT_HIP(hipGraphExecDestroy(t->roll_exec[i]));
+            t->roll_exec[i] = nullptr;
         }
     return PTCG_OK;
 }
@@ -749,9 +755,9 @@ extern "C" int ptcg_trainer_set_static(PtcgTrainer* t, const float* card_static,
     t->st_f[4].assign(skill_text, skill_text + NS * PT_SKILL_TEXT);
     t->st_i[0].assign(card_attacks, card_attacks + NC * PT_K_ATT);
     t->st_i[1].assign(card_skills, card_skills + NC * PT_K_SK);
-    if (t->roll)
-        PT_TRY(ptcg_model_set_static(t->roll, card_static, att_static, card_text, att_text, skill_text,
-                                     card_attacks, card_skills));
+    for (auto r : t->rolls)
+        if (r) PT_TRY(ptcg_model_set_static(r, card_static, att_static, card_text, att_text, skill_text,
+                                            card_attacks, card_skills));
     return PTCG_OK;
 }
 
@@ -760,7 +766,8 @@ extern "C" int ptcg_trainer_set_precision(PtcgTrainer* t, int prec) {
     PT_TRY(drop_step_graph(t));
     PT_TRY(drop_rollout_graphs(t));
     PT_TRY(ptcg_model_set_precision(t->model, prec));
-    if (t->roll) PT_TRY(ptcg_model_set_precision(t->roll, prec));
+    for (auto r : t->rolls)
+        if (r) PT_TRY(ptcg_model_set_precision(r, prec));
     t->prec = prec;
     return PTCG_OK;
 }
@@ -770,7 +777,8 @@ extern "C" int ptcg_trainer_set_skip_masked_options(PtcgTrainer* t, int on) {
     PT_TRY(drop_step_graph(t));
     PT_TRY(drop_rollout_graphs(t));
     PT_TRY(ptcg_model_set_skip_masked_options(t->model, on));
-    if (t->roll) PT_TRY(ptcg_model_set_skip_masked_options(t->roll, on));
+    for (auto r : t->rolls)
+        if (r) PT_TRY(ptcg_model_set_skip_masked_options(r, on));
     t->skip_masked = on != 0;
     return PTCG_OK;
 }
@@ -780,53 +788,79 @@ extern "C" int ptcg_trainer_set_sync_free(PtcgTrainer* t, int on) {
     PT_TRY(drop_step_graph(t));
     PT_TRY(drop_rollout_graphs(t));
     PT_TRY(ptcg_model_set_sync_free(t->model, on));
-    if (t->roll) PT_TRY(ptcg_model_set_sync_free(t->roll, on));
+    for (auto r : t->rolls)
+        if (r) PT_TRY(ptcg_model_set_sync_free(r, on));
     t->sync_free = on;
     return PTCG_OK;
 }
 
-static int roll_model(PtcgTrainer* t, int n) {
-    if (!t->roll || t->roll_n != n) {
-        if (!t->roll) {
-            PT_TRY(ptcg_model_create(&t->dm, &t->roll));
-            PT_TRY(ptcg_model_bind(t->roll, t->P, t->Gr));
-            PT_TRY(ptcg_model_set_precision(t->roll, t->prec));
-            PT_TRY(ptcg_model_set_sync_free(t->roll, t->sync_free));
-            PT_TRY(ptcg_model_set_skip_masked_options(t->roll, t->skip_masked));
+constexpr int PT_MAX_ROLL_BUFS = 64;
+
+// rollout policy `buf`, registered for n rows (allocations happen here,
+// never inside a capture)
+static int roll_model(PtcgTrainer* t, int buf, int n) {
+    PT_REQUIRE(buf >= 0 && buf < PT_MAX_ROLL_BUFS, "rollout: buffer %d outside [0, %d)", buf, PT_MAX_ROLL_BUFS);
+    if ((int)t->rolls.size() <= buf) {
+        t->rolls.resize(buf + 1, nullptr);
+        t->roll_n.resize(buf + 1, 0);
+    }
+    PtcgModel*& m = t->rolls[buf];
+    if (!m || t->roll_n[buf] != n) {
+        if (!m) {
+            PT_TRY(ptcg_model_create(&t->dm, &m));
+            PT_TRY(ptcg_model_bind(m, t->P, t->Gr));
+            PT_TRY(ptcg_model_set_precision(m, t->prec));
+            PT_TRY(ptcg_model_set_sync_free(m, t->sync_free));
+            PT_TRY(ptcg_model_set_skip_masked_options(m, t->skip_masked));
             if (t->dm.tables == 1 && !t->st_i[0].empty())
-                PT_TRY(ptcg_model_set_static(t->roll, t->st_f[0].data(), t->st_f[1].data(), t->st_f[2].data(),
+                PT_TRY(ptcg_model_set_static(m, t->st_f[0].data(), t->st_f[1].data(), t->st_f[2].data(),
                                              t->st_f[3].data(), t->st_f[4].data(), t->st_i[0].data(),
                                              t->st_i[1].data()));
         }
-        // captured rollout graphs hold the old activation buffers: drop them
-        PT_TRY(drop_rollout_graphs(t));
-        PT_TRY(ptcg_model_reg_rollout(t->roll, n));
-        t->roll_n = n;
+        // captured rollout graphs of this policy hold its old activation buffers: drop them
+        PT_TRY(drop_rollout_graphs(t, buf));
+        PT_TRY(ptcg_model_reg_rollout(m, n));
+        t->roll_n[buf] = n;
     }
     return PTCG_OK;
 }
 
 extern "C" int ptcg_trainer_obs_size(PtcgTrainer* t) { return t ? t->off.size : 0; }
 
+static int draw(PtcgTrainer* t, const float* out, const float* obs, const int32_t* row_idx, int n, uint64_t seed,
+                uint64_t step, uint64_t* step_dev, float* actions, float* logprobs, float* values, hipStream_t s) {
+    const float* mask = obs + t->off.opt_mask;
+    if (t->sampler == 1)
+        return pt_sample_gumbel(out, n, t->dm.n_opt, mask, t->off.size, row_idx, nullptr, seed, step, step_dev,
+                                actions, logprobs, values, nullptr, s);
+    if (step_dev)
+        return pt_sample_actions_dev(out, n, t->dm.n_opt, mask, t->off.size, row_idx, seed, step_dev, actions,
+                                     logprobs, values, s);
+    return ptcg_sample_actions(out, n, t->dm.n_opt, mask, t->off.size, row_idx, seed, step, actions, logprobs,
+                               values, nullptr, s);
+}
+
+extern "C" int ptcg_trainer_rollout_on(PtcgTrainer* t, int buf, const float* obs, const int32_t* row_idx, int n,
+                                       uint64_t seed, uint64_t step, float* actions, float* logprobs, float* values,
+                                       void* stream) {
+    PT_REQUIRE(t && obs && actions && logprobs, "trainer_rollout: null argument");
+    PT_REQUIRE(n >= 1, "trainer_rollout: n=%d", n);
+    PT_TRY(roll_model(t, buf, n));
+    float* out = nullptr;
+    PT_TRY(ptcg_model_forward(t->rolls[buf], obs, row_idx, n, &out, stream));
+    return draw(t, out, obs, row_idx, n, seed, step, nullptr, actions, logprobs, values, (hipStream_t)stream);
+}
+
 extern "C" int ptcg_trainer_rollout(PtcgTrainer* t, const float* obs, const int32_t* row_idx, int n,
                                     uint64_t seed, uint64_t step, float* actions, float* logprobs,
                                     float* values, void* stream) {
-    PT_REQUIRE(t && obs && actions && logprobs, "trainer_rollout: null argument");
-    PT_REQUIRE(n >= 1, "trainer_rollout: n=%d", n);
-    PT_TRY(roll_model(t, n));
-    float* out = nullptr;
-    PT_TRY(ptcg_model_forward(t->roll, obs, row_idx, n, &out, stream));
-    if (t->sampler == 1)
-        return pt_sample_gumbel(out, n, t->dm.n_opt, obs + t->off.opt_mask, t->off.size, row_idx, nullptr, seed, step,
-                                nullptr, actions, logprobs, values, nullptr, (hipStream_t)stream);
-    return ptcg_sample_actions(out, n, t->dm.n_opt, obs + t->off.opt_mask, t->off.size, row_idx, seed, step, actions,
-                               logprobs, values, nullptr, stream);
+    return ptcg_trainer_rollout_on(t, 0, obs, row_idx, n, seed, step, actions, logprobs, values, stream);
 }
 
 extern "C" int ptcg_trainer_rollout_output(PtcgTrainer* t, float** dec_out) {
     PT_REQUIRE(t && dec_out, "rollout_output: null argument");
-    PT_REQUIRE(t->roll, "rollout_output: no rollout has run");
-    *dec_out = pt_model_out(t->roll);
+    PT_REQUIRE(!t->rolls.empty() && t->rolls[0], "rollout_output: no rollout has run");
+    *dec_out = pt_model_out(t->rolls[0]);
     return PTCG_OK;
 }
 
@@ -841,19 +875,24 @@ extern "C" int ptcg_trainer_set_sampler(PtcgTrainer* t, int kind) {
 // The reference captures one graph per (time step, buffer) of its rollout
 // (net_callback_wrapper, pufferlib.cu:757-946) because each reads and writes
 // different rollout slices; the same here: slot k's graph holds the rollout
-// forward over its own buffers and the draw, with the step read from the
-// device counter step_dev and advanced by one per replay.  Sync-free mode.
-extern "C" int ptcg_trainer_capture_rollout(PtcgTrainer* t, int slot, const float* obs, const int32_t* row_idx,
-                                            int n, uint64_t seed, uint64_t* step_dev, float* actions,
-                                            float* logprobs, float* values) {
+// forward over its own buffers on rollout policy buf's activations and the
+// draw, with the step read from the device counter step_dev and advanced by
+// one per replay.  Slots on different policies may replay concurrently on
+// different streams.  Sync-free mode.
+extern "C" int ptcg_trainer_capture_rollout_on(PtcgTrainer* t, int buf, int slot, const float* obs,
+                                               const int32_t* row_idx, int n, uint64_t seed, uint64_t* step_dev,
+                                               float* actions, float* logprobs, float* values) {
     PT_REQUIRE(t && obs && actions && logprobs && step_dev, "capture_rollout: null argument");
     PT_REQUIRE(slot >= 0 && slot < 4096, "capture_rollout: slot %d out of range", slot);
     PT_REQUIRE(n >= 1, "capture_rollout: n=%d", n);
     PT_REQUIRE(t->sync_free, "capture_rollout: needs sync-free mode (ptcg_trainer_set_sync_free)");
-    PT_TRY(roll_model(t, n));   // allocations happen outside the capture
-    PT_REQUIRE(t->roll_n == n, "capture_rollout: the rollout policy is registered for %d rows", t->roll_n);
-    if ((int)t->roll_exec.size() <= slot) t->roll_exec.resize(slot + 1, nullptr);
+    PT_TRY(roll_model(t, buf, n));   // allocations happen outside the capture
+    if ((int)t->roll_exec.size() <= slot) {
+        t->roll_exec.resize(slot + 1, nullptr);
+        t->roll_exec_buf.resize(slot + 1, -1);
+    }
     if (t->roll_exec[slot]) {
+        PT_HIP(hipDeviceSynchronize());
         PT_HIP(hipGraphExecDestroy(t->roll_exec[slot]));
         t->roll_exec[slot] = nullptr;
     }
@@ -861,13 +900,9 @@ extern "C" int ptcg_trainer_capture_rollout(PtcgTrainer* t, int slot, const floa
     PT_HIP(hipDeviceSynchronize());
     PT_HIP(hipStreamBeginCapture(t->cap_stream, hipStreamCaptureModeThreadLocal));
     float* out = nullptr;
-    int r = ptcg_model_forward(t->roll, obs, row_idx, n, &out, t->cap_stream);
-    if (r == PTCG_OK && t->sampler == 1)
-        r = pt_sample_gumbel(out, n, t->dm.n_opt, obs + t->off.opt_mask, t->off.size, row_idx, nullptr, seed, 0,
-                             step_dev, actions, logprobs, values, nullptr, t->cap_stream);
-    else if (r == PTCG_OK)
-        r = pt_sample_actions_dev(out, n, t->dm.n_opt, obs + t->off.opt_mask, t->off.size, row_idx, seed, step_dev,
-                                  actions, logprobs, values, t->cap_stream);
+    int r = ptcg_model_forward(t->rolls[buf], obs, row_idx, n, &out, t->cap_stream);
+    if (r == PTCG_OK)
+        r = draw(t, out, obs, row_idx, n, seed, 0, step_dev, actions, logprobs, values, t->cap_stream);
     hipGraph_t g = nullptr;
     const hipError_t e = hipStreamEndCapture(t->cap_stream, &g);
     if (r != PTCG_OK) {
@@ -880,7 +915,14 @@ extern "C" int ptcg_trainer_capture_rollout(PtcgTrainer* t, int slot, const floa
     (void)hipGraphDestroy(g);
     PT_HIP(ei);
     t->roll_exec[slot] = x;
+    t->roll_exec_buf[slot] = buf;
     return PTCG_OK;
+}
+
+extern "C" int ptcg_trainer_capture_rollout(PtcgTrainer* t, int slot, const float* obs, const int32_t* row_idx,
+                                            int n, uint64_t seed, uint64_t* step_dev, float* actions,
+                                            float* logprobs, float* values) {
+    return ptcg_trainer_capture_rollout_on(t, 0, slot, obs, row_idx, n, seed, step_dev, actions, logprobs, values);
 }
 
 extern "C" int ptcg_trainer_replay_rollout(PtcgTrainer* t, int slot, void* stream) {

@@ -9,11 +9,12 @@
 // forward is ordered after them on the same stream.  Here:
 // ptcg_transport_step (captured rollout graph replay + download) and
 // ptcg_transport_upload.  Buffers are contiguous agent slices
-// [buf * apb, (buf + 1) * apb) of every array.  Every buffer's rollout graph
-// runs on the trainer's one set of rollout activations, so steps of
-// different buffers must not overlap: ptcg_transport_step ends in a stream
-// sync, and steps issued from one host thread run one after another (the
-// uploads, which touch only their own slices, may overlap anything).
+// [buf * apb, (buf + 1) * apb) of every array.  Buffer b's rollout graph runs
+// on the trainer's rollout policy b (its own activations), so the buffers'
+// forwards may overlap on their streams, as the reference's per-buffer
+// threads do: ptcg_transport_launch queues a buffer's forward, draw and
+// action download without waiting, ptcg_transport_wait ends in its checked
+// stream sync, and ptcg_transport_step is the two in a row.
 #include <string.h>
 #include <vector>
 
@@ -168,13 +169,28 @@ extern "C" int ptcg_transport_capture_rollout(PtcgTransport* x, PtcgTrainer* t, 
     PT_REQUIRE(row == x->obs_floats, "transport_capture_rollout: observation rows of %lld floats, trainer expects %lld",
                (long long)x->obs_floats, (long long)row);
     const size_t a0 = (size_t)buf * x->apb;
-    return ptcg_trainer_capture_rollout(t, slot, (const float*)x->devp[PTCG_TR_OBS] + a0 * x->obs_floats, nullptr,
-                                        x->apb, seed, step_dev, (float*)x->devp[PTCG_TR_ACTIONS] + a0,
-                                        (float*)x->devp[PTCG_TR_LOGPROBS] + a0, (float*)x->devp[PTCG_TR_VALUES] + a0);
+    return ptcg_trainer_capture_rollout_on(t, buf, slot, (const float*)x->devp[PTCG_TR_OBS] + a0 * x->obs_floats,
+                                           nullptr, x->apb, seed, step_dev, (float*)x->devp[PTCG_TR_ACTIONS] + a0,
+                                           (float*)x->devp[PTCG_TR_LOGPROBS] + a0,
+                                           (float*)x->devp[PTCG_TR_VALUES] + a0);
+}
+
+extern "C" int ptcg_transport_launch(PtcgTransport* x, PtcgTrainer* t, int buf, int slot) {
+    PT_REQUIRE(x && t && buf >= 0 && buf < x->nbuf, "transport_launch: buffer %d out of range", buf);
+    PT_TRY(ptcg_trainer_replay_rollout(t, slot, x->streams[buf]));
+    return copy_slice(x, PTCG_TR_ACTIONS, buf, hipMemcpyDeviceToHost);
+}
+
+extern "C" int ptcg_transport_wait(PtcgTransport* x, int buf) {
+    PT_REQUIRE(x && buf >= 0 && buf < x->nbuf, "transport_wait: buffer %d out of range", buf);
+    // a failed sync leaves the env stepping on stale actions: report it
+    const hipError_t e = hipStreamSynchronize(x->streams[buf]);
+    if (e != hipSuccess) return PT_FAIL(PTCG_ERR_HIP, "transport_wait: buffer %d stream sync: %s", buf,
+                                        hipGetErrorString(e));
+    return PTCG_OK;
 }
 
 extern "C" int ptcg_transport_step(PtcgTransport* x, PtcgTrainer* t, int buf, int slot) {
-    PT_REQUIRE(x && t && buf >= 0 && buf < x->nbuf, "transport_step: buffer %d out of range", buf);
-    PT_TRY(ptcg_trainer_replay_rollout(t, slot, x->streams[buf]));
-    return ptcg_transport_download(x, buf);
+    PT_TRY(ptcg_transport_launch(x, t, buf, slot));
+    return ptcg_transport_wait(x, buf);
 }

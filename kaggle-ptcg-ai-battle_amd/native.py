@@ -112,6 +112,12 @@ _SIGS = {
     "ptcg_trainer_capture_rollout": (ctypes.c_int, [c_void_p, ctypes.c_int, c_void_p, c_void_p, ctypes.c_int,
                                                     ctypes.c_uint64, c_void_p, c_void_p, c_void_p, c_void_p]),
     "ptcg_trainer_replay_rollout": (ctypes.c_int, [c_void_p, ctypes.c_int, c_void_p]),
+    "ptcg_trainer_capture_rollout_on": (ctypes.c_int, [c_void_p, ctypes.c_int, ctypes.c_int, c_void_p, c_void_p,
+                                                       ctypes.c_int, ctypes.c_uint64, c_void_p, c_void_p, c_void_p,
+                                                       c_void_p]),
+    "ptcg_trainer_rollout_on": (ctypes.c_int, [c_void_p, ctypes.c_int, c_void_p, c_void_p, ctypes.c_int,
+                                               ctypes.c_uint64, ctypes.c_uint64, c_void_p, c_void_p, c_void_p,
+                                               c_void_p]),
     "ptcg_trainer_obs_size": (ctypes.c_int, [c_void_p]),
     "ptcg_transport_create": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, ctypes.c_int64, ctypes.c_int, ctypes.c_int,
                                              ctypes.POINTER(c_void_p)]),
@@ -125,6 +131,8 @@ _SIGS = {
     "ptcg_transport_capture_rollout": (ctypes.c_int, [c_void_p, c_void_p, ctypes.c_int, ctypes.c_int,
                                                       ctypes.c_uint64, c_void_p]),
     "ptcg_transport_step": (ctypes.c_int, [c_void_p, c_void_p, ctypes.c_int, ctypes.c_int]),
+    "ptcg_transport_launch": (ctypes.c_int, [c_void_p, c_void_p, ctypes.c_int, ctypes.c_int]),
+    "ptcg_transport_wait": (ctypes.c_int, [c_void_p, ctypes.c_int]),
     "ptcg_trainer_set_optimizer": (ctypes.c_int, [c_void_p, ctypes.c_int, ctypes.c_double]),
     "ptcg_trainer_set_counters": (ctypes.c_int, [c_void_p, ctypes.c_int64, ctypes.c_int64]),
     "ptcg_trainer_get_counters": (ctypes.c_int, [c_void_p, ctypes.POINTER(ctypes.c_int64),

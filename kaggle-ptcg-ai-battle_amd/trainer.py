@@ -166,14 +166,16 @@ class PuffeRL:
                                             i["card_attacks"].ctypes.data, i["card_skills"].ctypes.data))
         self._static = (f, i)   # keep the host copies alive for the call's duration
 
-    def rollout_step(self, obs, n, seed, step, idx=None, stream=None):
-        """Forward ``n`` device obs rows with inference activations and sample
-        one action per row; returns device tensors (actions, logprobs, values)."""
+    def rollout_step(self, obs, n, seed, step, idx=None, stream=None, buf=0):
+        """Forward ``n`` device obs rows with inference activations (rollout
+        policy ``buf``: its own activations, so policies may run on different
+        streams at once) and sample one action per row; returns device tensors
+        (actions, logprobs, values)."""
         t = self._torch
         acts = t.empty(n, dtype=t.float32, device="cuda")
         lps, vals = t.empty_like(acts), t.empty_like(acts)
-        check(lib().ptcg_trainer_rollout(self._h, obs.data_ptr(), idx.data_ptr() if idx is not None else None,
-                                         n, seed, step, acts.data_ptr(), lps.data_ptr(), vals.data_ptr(), stream))
+        check(lib().ptcg_trainer_rollout_on(self._h, buf, obs.data_ptr(), idx.data_ptr() if idx is not None else None,
+                                            n, seed, step, acts.data_ptr(), lps.data_ptr(), vals.data_ptr(), stream))
         return acts, lps, vals
 
     def capture_rollout(self, slot, obs, n, seed, step_dev, actions, logprobs, values, idx=None):

@@ -9,7 +9,10 @@ they are invalid after ``close()``.  Per (buffer, step):
 ``step(trainer, buf, slot)`` replays the buffer's captured rollout graph on
 its stream and brings the actions back (checked stream sync); after the env
 step, ``upload(buf)`` queues the new observations, rewards and terminals on
-the same stream, ahead of the buffer's next forward.
+the same stream, ahead of the buffer's next forward.  Buffer b's graph runs
+on the trainer's rollout policy b (its own activations), so ``launch`` (the
+replay and the actions' download, without waiting) of several buffers keeps
+their forwards in flight together, and ``wait(buf)`` is the checked sync.
 """
 import ctypes
 
@@ -64,6 +67,12 @@ class RolloutTransport:
 
     def step(self, pl, buf, slot):
         check(lib().ptcg_transport_step(self._h, pl._h, buf, slot))
+
+    def launch(self, pl, buf, slot):
+        check(lib().ptcg_transport_launch(self._h, pl._h, buf, slot))
+
+    def wait(self, buf):
+        check(lib().ptcg_transport_wait(self._h, buf))
 
     def close(self):
         if getattr(self, "_h", None) is not None and self._h.value:

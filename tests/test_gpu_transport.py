@@ -103,3 +103,42 @@ def test_transport_mask_round_trip(cuda):
         assert np.all(got[others] == 0) and np.all(dob[others] == 0)
     finally:
         x.close()
+
+
+def test_transport_buffers_overlap(cuda):
+    """Four env buffers, each on its own rollout policy (activations) and
+    stream: all four forwards are launched before any is waited on, so they
+    may run at once, and each buffer's actions, log-probabilities and values
+    equal the eager rollout step's on its rows, bit for bit, at every step."""
+    dm, nbuf, apb = dims.CORE, 4, 128
+    blob = om.build(dm, seed=131).to_blob()
+    pl = trainer.create_pufferl({"dims": dm, "init_weights": blob, "sync_free": True, "sampler": "gumbel",
+                                 "train": dict(minibatch_size=64)})
+    x = tr.RolloutTransport(nbuf * apb, nbuf, dm.obs_size)
+    try:
+        steps = [torch.tensor([20 + b], dtype=torch.int64, device="cuda") for b in range(nbuf)]
+        for b in range(nbuf):
+            x.capture_rollout(pl, b, b, 777, steps[b])
+        for t in range(3):
+            rows = {}
+            for b in range(nbuf):
+                rows[b] = synth.make_obs(dm, apb, seed=2000 + 10 * t + b)
+                x.observations[x.slice(b)] = rows[b]
+                x.upload(b)
+            for b in range(nbuf):
+                x.launch(pl, b, b)
+            for b in range(nbuf):
+                x.wait(b)
+            lp_all = dev_floats(x.device_ptr(tr.LOGPROBS), nbuf * apb)
+            v_all = dev_floats(x.device_ptr(tr.VALUES), nbuf * apb)
+            for b in range(nbuf):
+                sl = x.slice(b)
+                a, l, v = pl.rollout_step(pl.to_device(rows[b]), apb, seed=777, step=20 + b + t, buf=nbuf)
+                torch.cuda.synchronize()
+                assert np.array_equal(x.actions[sl, 0], a.cpu().numpy()), (t, b)
+                assert np.array_equal(lp_all[sl], l.cpu().numpy()), (t, b)
+                assert np.array_equal(v_all[sl], v.cpu().numpy()), (t, b)
+                assert int(steps[b].item()) == 20 + b + t + 1
+    finally:
+        x.close()
+        pl.close()

@@ -14,8 +14,9 @@
 //   k_prize_head / k_prize_head_bwd (ptcg_model3.cu:411-438) -> head_dot +
 //       rank1_add
 // Shared-table scatters (card rows referenced by several cards / tokens /
-// options) use fp32 atomics as the reference does; per-sample work runs one
-// workgroup per sample with the targets built in LDS.
+// options), where the reference uses fp32 atomics, add in 64-bit fixed point
+// (detsum.hip), so their sums do not depend on the order the adds land in;
+// per-sample work runs one workgroup per sample with the targets built in LDS.
 #include "model.h"
 
 namespace {
@@ -61,7 +62,7 @@ __global__ void pool_fwd_kernel(const float* __restrict__ tab, int E, const int*
 
 __global__ void pool_bwd_kernel(const float* __restrict__ dsrc, long ld, int col_mean, int col_max,
                                 const int* __restrict__ amax, const int* __restrict__ ids, int K, int NC,
-                                int E, float* d_tab) {
+                                int E, DetSink d_tab) {
     const long i = (long)blockIdx.x * TB + threadIdx.x;
     if (i >= (long)NC * E) return;
     const int n = (int)(i / E), e = (int)(i % E);
@@ -70,11 +71,11 @@ __global__ void pool_bwd_kernel(const float* __restrict__ dsrc, long ld, int col
     const float dm = dsrc[(long)n * ld + col_mean + e] / (float)(cnt > 0 ? cnt : 1);
     const float dx = dsrc[(long)n * ld + col_max + e];
     const int am = amax[i];
+    const double sc = *d_tab.scale;
     for (int k = 0; k < K; ++k) {
         const int id = ids[n * K + k];
         if (id <= 0) continue;
-        const float g = dm + (k == am ? dx : 0.f);
-        if (g != 0.f) atomicAdd(&d_tab[(long)id * E + e], g);
+        pt_det_add(d_tab, sc, (long)id * E + e, dm + (k == am ? dx : 0.f));
     }
 }
 
@@ -126,7 +127,7 @@ __global__ void otok_in_kernel(GatherCtx c, const float* __restrict__ cv, const 
     }
 }
 
-__global__ void otok_bwd_kernel(GatherCtx c, const float* __restrict__ d_in, float* d_card) {
+__global__ void otok_bwd_kernel(GatherCtx c, const float* __restrict__ d_in, DetSink d_card) {
     const int DC = c.dm.d_c, W = c.dx.orc_in, NO = c.dx.n_orc;
     const long i = (long)blockIdx.x * TB + threadIdx.x;
     if (i >= (long)c.N * NO * DC) return;
@@ -139,7 +140,7 @@ __global__ void otok_bwd_kernel(GatherCtx c, const float* __restrict__ d_in, flo
     const int id = k < PT_N_HAND ? obs_id(o[2 * k])
                  : k < PT_N_HAND + PT_N_SPLIT ? obs_id(o[2 * PT_N_HAND + 3 * (k - PT_N_HAND)])
                  : obs_id(o[2 * PT_N_HAND + 3 * PT_N_SPLIT + 2 * (k - PT_N_HAND - PT_N_SPLIT)]);
-    atomicAdd(&d_card[(long)clamp_id(id, c.dm.n_cards) * DC + col], g);
+    pt_det_add(d_card, *d_card.scale, (long)clamp_id(id, c.dm.n_cards) * DC + col, g);
 }
 
 // critic sequence (N, l_crit, D) = [critic readout | h (l_seq rows) | otok]
@@ -271,7 +272,7 @@ int pt_pool_fwd(const float* tab, int E, const int* ids, int K, int NC, float* o
     return PTCG_OK;
 }
 int pt_pool_bwd(const float* dsrc, long ld, int col_mean, int col_max, const int* amax, const int* ids, int K,
-                int NC, int E, float* d_tab, hipStream_t s) {
+                int NC, int E, const DetSink& d_tab, hipStream_t s) {
     hipLaunchKernelGGL(pool_bwd_kernel, FZ_GRID((long)NC * E), dsrc, ld, col_mean, col_max, amax, ids, K, NC, E, d_tab);
     PT_LAUNCH_CHECK();
     return PTCG_OK;
@@ -286,7 +287,7 @@ int pt_otok_in(const GatherCtx& c, const float* cv, const float* keep, float* ou
     PT_LAUNCH_CHECK();
     return PTCG_OK;
 }
-int pt_otok_bwd(const GatherCtx& c, const float* d_in, float* d_card, hipStream_t s) {
+int pt_otok_bwd(const GatherCtx& c, const float* d_in, const DetSink& d_card, hipStream_t s) {
     hipLaunchKernelGGL(otok_bwd_kernel, FZ_GRID((long)c.N * c.dx.n_orc * c.dm.d_c), c, d_in, d_card);
     PT_LAUNCH_CHECK();
     return PTCG_OK;

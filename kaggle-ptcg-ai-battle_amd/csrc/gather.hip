@@ -15,8 +15,10 @@
 // the trunk output, the option sums into r/g/dvec) run one workgroup per
 // sample, each element owned by one thread; the scatters into shared
 // embedding tables (card/attack/zone/owner/type/select/context rows shared
-// across samples) use fp32 atomics, as the reference does, after summing
-// rows of equal id in a per-thread id cache (IdCache).
+// across samples), where the reference uses fp32 atomics, sum rows of equal
+// id in a per-thread id cache (IdCache) and add the partial sums in 64-bit
+// fixed point (detsum.hip), so the tables' gradients do not depend on the
+// order the adds land in.
 #include "model.h"
 
 #include <algorithm>
@@ -85,33 +87,38 @@ __global__ void tok_cat_fwd_kernel(GatherCtx c, const float* __restrict__ card,
 // Scatter-add of one table column with a per-thread cache of four (id, sum)
 // pairs.  A thread walks its column down a run of rows in order; rows that
 // share an id (padding ids, the few zones / owners / option types, frequent
-// cards) add in registers, and the table sees one atomic per eviction
-// instead of one per row — the reference's per-element atomics serialise on
-// such hot rows.  Zero gradients (masked options, padding) are skipped.
+// cards) add in registers, and the table sees one fixed-point add (pt_det_add)
+// per eviction instead of one per row — the reference's per-element atomics
+// serialise on such hot rows.  Zero gradients (masked options, padding) are
+// skipped.
 struct IdCache {
     int id0 = -1, id1 = -1, id2 = -1, id3 = -1;
     float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
     int next = 0;
-    __device__ __forceinline__ static void put(float* tab, long ld, int col, int id, float a) {
-        if (id >= 0 && a != 0.f) atomicAdd(tab + (long)id * ld + col, a);
+    DetSink k;
+    double sc;
+    int col;
+    __device__ IdCache(const DetSink& sink, int col_) : k(sink), sc(*sink.scale), col(col_) {}
+    __device__ __forceinline__ void put(int id, float a) {
+        if (id >= 0) pt_det_add(k, sc, (long)id * k.ld + col, a);
     }
-    __device__ __forceinline__ void add(float* tab, long ld, int col, int id, float g) {
+    __device__ __forceinline__ void add(int id, float g) {
         if (g == 0.f) return;
         if (id == id0) { a0 += g; return; }
         if (id == id1) { a1 += g; return; }
         if (id == id2) { a2 += g; return; }
         if (id == id3) { a3 += g; return; }
-        if (next == 0) { put(tab, ld, col, id0, a0); id0 = id; a0 = g; }
-        else if (next == 1) { put(tab, ld, col, id1, a1); id1 = id; a1 = g; }
-        else if (next == 2) { put(tab, ld, col, id2, a2); id2 = id; a2 = g; }
-        else { put(tab, ld, col, id3, a3); id3 = id; a3 = g; }
+        if (next == 0) { put(id0, a0); id0 = id; a0 = g; }
+        else if (next == 1) { put(id1, a1); id1 = id; a1 = g; }
+        else if (next == 2) { put(id2, a2); id2 = id; a2 = g; }
+        else { put(id3, a3); id3 = id; a3 = g; }
         next = (next + 1) & 3;
     }
-    __device__ __forceinline__ void flush(float* tab, long ld, int col) {
-        put(tab, ld, col, id0, a0);
-        put(tab, ld, col, id1, a1);
-        put(tab, ld, col, id2, a2);
-        put(tab, ld, col, id3, a3);
+    __device__ __forceinline__ void flush() {
+        put(id0, a0);
+        put(id1, a1);
+        put(id2, a2);
+        put(id3, a3);
     }
 };
 
@@ -121,8 +128,8 @@ constexpr int SCATTER_ROWS = 32;
 // token concat backward: thread = one gradient-bearing column (card | tool
 // card | zone | owner; the numeric features are inputs), workgroup = a run
 // of SCATTER_ROWS token rows
-__global__ void tok_cat_bwd_kernel(GatherCtx c, const float* __restrict__ d_cat, float* d_card,
-                                   float* d_zemb, float* d_oemb) {
+__global__ void tok_cat_bwd_kernel(GatherCtx c, const float* __restrict__ d_cat, DetSink d_card, DetSink d_zemb,
+                                   DetSink d_oemb) {
     const int Lt = c.dm.l_tok, dc = c.dm.d_c, tin = c.dx.tok_in;
     const int zc = 2 * dc + c.dm.tok_f;   // first zone column of the concat
     const int q = threadIdx.x;
@@ -131,13 +138,9 @@ __global__ void tok_cat_bwd_kernel(GatherCtx c, const float* __restrict__ d_cat,
     const long nrows = c.rowmap ? (long)*c.rows : (long)c.N * Lt;
     const long r0 = (long)blockIdx.x * SCATTER_ROWS, r1 = min(nrows, r0 + SCATTER_ROWS);
     const int NC = c.dm.n_cards;
-    IdCache k0, k1;   // k1: the second tool card
-    float* tab;
-    long ld;
-    int tc;
-    if (q < 2 * dc) { tab = d_card; ld = dc; tc = q < dc ? q : q - dc; }
-    else if (q < 2 * dc + PT_ZONE_E) { tab = d_zemb; ld = PT_ZONE_E; tc = q - 2 * dc; }
-    else { tab = d_oemb; ld = PT_OWNER_E; tc = q - 2 * dc - PT_ZONE_E; }
+    const int tc = q < dc ? q : (q < 2 * dc ? q - dc : (q < 2 * dc + PT_ZONE_E ? q - 2 * dc : q - 2 * dc - PT_ZONE_E));
+    const DetSink& sk = q < 2 * dc ? d_card : (q < 2 * dc + PT_ZONE_E ? d_zemb : d_oemb);
+    IdCache k0(sk, tc), k1(sk, tc);   // k1: the second tool card
     for (long r = r0; r < r1; ++r) {
         const float g = d_cat[r * tin + col];
         if (g == 0.f) continue;
@@ -152,19 +155,19 @@ __global__ void tok_cat_bwd_kernel(GatherCtx c, const float* __restrict__ d_cat,
         }
         const float* ti = obs_row(c.obs, c.idx, c.stride, n) + c.off.tok_int + (long)t * c.dm.tok_int;
         if (q < dc) {
-            k0.add(tab, ld, tc, pt_id_clamp(ti[0], NC - 1), g);
+            k0.add(pt_id_clamp(ti[0], NC - 1), g);
         } else if (q < 2 * dc) {
             const int t0 = (int)ti[3], t1 = (int)ti[4];
-            if (t0 > 0) k0.add(tab, ld, tc, t0 >= NC ? NC - 1 : t0, g);
-            if (t1 > 0) k1.add(tab, ld, tc, t1 >= NC ? NC - 1 : t1, g);
+            if (t0 > 0) k0.add(t0 >= NC ? NC - 1 : t0, g);
+            if (t1 > 0) k1.add(t1 >= NC ? NC - 1 : t1, g);
         } else if (q < 2 * dc + PT_ZONE_E) {
-            k0.add(tab, ld, tc, pt_id_clamp(ti[1], c.dm.n_zones - 1), g);
+            k0.add(pt_id_clamp(ti[1], c.dm.n_zones - 1), g);
         } else {
-            k0.add(tab, ld, tc, pt_id_clamp(ti[2], c.dm.n_owners - 1), g);
+            k0.add(pt_id_clamp(ti[2], c.dm.n_owners - 1), g);
         }
     }
-    k0.flush(tab, ld, tc);
-    k1.flush(tab, ld, tc);
+    k0.flush();
+    k1.flush();
 }
 
 __global__ void glob_in_kernel(GatherCtx c, float* __restrict__ out) {
@@ -214,30 +217,26 @@ __global__ void dec_in_fwd_kernel(GatherCtx c, const float* __restrict__ card,
 
 // decision concat backward: thread = column, workgroup = (column block, a
 // run of SCATTER_ROWS samples)
-__global__ void dec_in_bwd_kernel(GatherCtx c, const float* __restrict__ d_in, float* d_card,
-                                  float* d_att, float* d_semb, float* d_cemb) {
+__global__ void dec_in_bwd_kernel(GatherCtx c, const float* __restrict__ d_in, DetSink d_card, DetSink d_att,
+                                  DetSink d_semb, DetSink d_cemb) {
     const int W = c.dx.dec_in;
     const int col = blockIdx.x * TB + threadIdx.x;
     if (col >= W) return;
     int kind, di, e;
     dec_locate(c, col, kind, di, e);
     if (kind == 4) return;   // numeric features: no gradient
-    float* tab;
-    long ld;
-    int hi;
-    if (kind == 0) { tab = d_semb; ld = PT_SEL_E; hi = c.dm.n_select_types - 1; }
-    else if (kind == 1) { tab = d_cemb; ld = PT_CTX_E; hi = c.dm.n_contexts - 1; }
-    else if (kind == 2) { tab = d_card; ld = c.dm.d_c; hi = c.dm.n_cards - 1; }
-    else { tab = d_att; ld = c.dm.d_a; hi = c.dm.n_attacks - 1; }
+    const DetSink& sk = kind == 0 ? d_semb : (kind == 1 ? d_cemb : (kind == 2 ? d_card : d_att));
+    const int hi = kind == 0 ? c.dm.n_select_types - 1
+                 : (kind == 1 ? c.dm.n_contexts - 1 : (kind == 2 ? c.dm.n_cards - 1 : c.dm.n_attacks - 1));
     const int n0 = blockIdx.y * SCATTER_ROWS, n1 = min(c.N, n0 + SCATTER_ROWS);
-    IdCache k;
+    IdCache k(sk, e);
     for (int n = n0; n < n1; ++n) {
         const float g = d_in[(long)n * W + col];
         if (g == 0.f) continue;
         const float* di_ = obs_row(c.obs, c.idx, c.stride, n) + c.off.dec_int;
-        k.add(tab, ld, e, pt_id_clamp(di_[di], hi), g);
+        k.add(pt_id_clamp(di_[di], hi), g);
     }
-    k.flush(tab, ld, e);
+    k.flush();
 }
 
 // x0[n,0] = readout; x0[n,l] = tokp[n,l-1] + bc[n]; keep[n,l] = l==0 || zone_float > 0
@@ -318,7 +317,7 @@ __global__ void opt_gather_fwd_kernel(GatherCtx c, const float* __restrict__ car
 // option card / attack backward: thread = column (d_c card columns, then
 // d_a attack columns), workgroup = a run of SCATTER_ROWS options
 __global__ void opt_gather_bwd_kernel(GatherCtx c, const float* __restrict__ d_ocard,
-        const float* __restrict__ d_oatt, float* d_card, float* d_att) {
+        const float* __restrict__ d_oatt, DetSink d_card, DetSink d_att) {
     const int NO = c.dm.n_opt, dc = c.dm.d_c, da = c.dm.d_a;
     const int q = threadIdx.x;
     if (q >= dc + da) return;
@@ -326,20 +325,19 @@ __global__ void opt_gather_bwd_kernel(GatherCtx c, const float* __restrict__ d_o
     const int e = is_card ? q : q - dc;
     const int w = is_card ? dc : da;
     const float* src = is_card ? d_ocard : d_oatt;
-    float* tab = is_card ? d_card : d_att;
     const int hi = is_card ? c.dm.n_cards - 1 : c.dm.n_attacks - 1;
     const int slot = is_card ? 3 : 4;
     const long r0 = (long)blockIdx.x * SCATTER_ROWS, r1 = min(pt_orows(c), r0 + SCATTER_ROWS);
-    IdCache k;
+    IdCache k(is_card ? d_card : d_att, e);
     for (long row = r0; row < r1; ++row) {
         const float g = src[row * w + e];
         if (g == 0.f) continue;
         const long nj = pt_onj(c, row);
         const int n = (int)(nj / NO), j = (int)(nj % NO);
         const float* oi = obs_row(c.obs, c.idx, c.stride, n) + c.off.opt_int + (long)j * c.dm.opt_int;
-        k.add(tab, w, e, pt_id_clamp(oi[slot], hi), g);
+        k.add(pt_id_clamp(oi[slot], hi), g);
     }
-    k.flush(tab, w, e);
+    k.flush();
 }
 
 // q_in = [temb16 | h(p1) | h(p2) | (opt_card, opt_attack GEMM outputs) | opt_f]
@@ -380,7 +378,7 @@ __global__ void q_in_fwd_kernel(GatherCtx c, const float* __restrict__ h,
 // a column's atomics keep their order (deterministic sums) while the
 // gradient loads of successive options no longer wait on a lookup chain.
 __global__ void q_in_bwd_kernel(GatherCtx c, const float* __restrict__ d_qin, float* __restrict__ d_h,
-                                float* d_temb) {
+                                DetSink d_temb) {
     __shared__ long s_h1[PT_MAX_OPT], s_h2[PT_MAX_OPT];
     __shared__ int s_ty[PT_MAX_OPT];
     const int n = blockIdx.x, NO = c.dm.n_opt, D = c.dm.d, W = c.dx.q_in;
@@ -411,9 +409,9 @@ __global__ void q_in_bwd_kernel(GatherCtx c, const float* __restrict__ d_qin, fl
         }
     }
     if (threadIdx.x < PT_TYPE_E) {
-        IdCache k;
-        for (int i = 0; i < nq; ++i) k.add(d_temb, PT_TYPE_E, threadIdx.x, s_ty[i], d_qin[(b0 + i) * W + threadIdx.x]);
-        k.flush(d_temb, PT_TYPE_E, threadIdx.x);
+        IdCache k(d_temb, threadIdx.x);
+        for (int i = 0; i < nq; ++i) k.add(s_ty[i], d_qin[(b0 + i) * W + threadIdx.x]);
+        k.flush();
     }
 }
 
@@ -612,8 +610,8 @@ int pt_tok_cat_fwd(const GatherCtx& c, const float* card, const float* zemb, con
                   (c.dx.tok_in + c.dm.tok_f + c.dm.tok_int), s);
     return PTCG_OK;
 }
-int pt_tok_cat_bwd(const GatherCtx& c, const float* d_cat, float* d_card, float* d_zemb, float* d_oemb,
-                   hipStream_t s) {
+int pt_tok_cat_bwd(const GatherCtx& c, const float* d_cat, const DetSink& d_card, const DetSink& d_zemb,
+                   const DetSink& d_oemb, hipStream_t s) {
     const long rows = c.rowmap ? (long)c.N * c.dx.l_seq : (long)c.N * c.dm.l_tok;
     const int cols = 2 * c.dm.d_c + PT_ZONE_E + PT_OWNER_E;
     PT_REQUIRE(cols <= 1024, "tok_cat_bwd: %d gradient columns", cols);
@@ -633,8 +631,8 @@ int pt_dec_in_fwd(const GatherCtx& c, const float* card, const float* att, const
     PT_LAUNCH_CHECK();
     return PTCG_OK;
 }
-int pt_dec_in_bwd(const GatherCtx& c, const float* d_in, float* d_card, float* d_att, float* d_semb,
-                  float* d_cemb, hipStream_t s) {
+int pt_dec_in_bwd(const GatherCtx& c, const float* d_in, const DetSink& d_card, const DetSink& d_att,
+                  const DetSink& d_semb, const DetSink& d_cemb, hipStream_t s) {
     hipLaunchKernelGGL(dec_in_bwd_kernel, dim3(pt_cdiv(c.dx.dec_in, TB), pt_cdiv(c.N, SCATTER_ROWS)), dim3(TB), 0, s,
                        c, d_in, d_card, d_att, d_semb, d_cemb);
     PT_LAUNCH_CHECK();
@@ -658,8 +656,8 @@ int pt_opt_gather_fwd(const GatherCtx& c, const float* card, const float* att, f
     PT_LAUNCH_CHECK();
     return PTCG_OK;
 }
-int pt_opt_gather_bwd(const GatherCtx& c, const float* d_ocard, const float* d_oatt, float* d_card,
-                      float* d_att, hipStream_t s) {
+int pt_opt_gather_bwd(const GatherCtx& c, const float* d_ocard, const float* d_oatt, const DetSink& d_card,
+                      const DetSink& d_att, hipStream_t s) {
     const int cols = c.dm.d_c + c.dm.d_a;
     PT_REQUIRE(cols <= 1024, "opt_gather_bwd: %d columns", cols);
     hipLaunchKernelGGL(opt_gather_bwd_kernel, dim3(pt_cdiv((long)c.N * c.dm.n_opt, SCATTER_ROWS)),
@@ -673,7 +671,7 @@ int pt_q_in_fwd(const GatherCtx& c, const float* h, const float* temb, float* q_
     PT_LAUNCH_CHECK();
     return PTCG_OK;
 }
-int pt_q_in_bwd(const GatherCtx& c, const float* d_qin, float* d_h, float* d_temb, hipStream_t s) {
+int pt_q_in_bwd(const GatherCtx& c, const float* d_qin, float* d_h, const DetSink& d_temb, hipStream_t s) {
     PT_REQUIRE(c.dm.n_opt <= PT_MAX_OPT, "q_in backward: %d options per sample exceed %d", c.dm.n_opt, PT_MAX_OPT);
     hipLaunchKernelGGL(q_in_bwd_kernel, dim3(c.N), dim3(TB), 0, s, c, d_qin, d_h, d_temb);
     PT_LAUNCH_CHECK();

@@ -79,6 +79,45 @@ int pt_adam_step(float* w, float* g, float* m, float* v, long n, const double* l
                  double eps, float max_norm, const float* gate, int32_t* step, float* norm_out,
                  float* ws, hipStream_t s);
 
+// ---- order-independent table scatters (detsum.hip)
+// A site: the tables one point of the backward scatters into and the
+// gradient slices it scatters from (sources; source i feeds table stab[i]).
+constexpr int DET_MAX_TAB = 8, DET_MAX_SRC = 8, DET_PART = 64;
+struct DetSite {
+    int ntab = 0;
+    float* tab[DET_MAX_TAB] = {};       // float tables (the grads), += at finish
+    long tab_n[DET_MAX_TAB] = {};       // floats per table
+    long acc_off[DET_MAX_TAB] = {};     // their accumulators in DetCtx::acc
+    double count[DET_MAX_TAB] = {};     // contributions one element can receive (bound)
+    int nsrc = 0;
+    const float* sp[DET_MAX_SRC] = {};  // source rows: sp + r * sld + scol, swidth floats,
+    long sld[DET_MAX_SRC] = {};         // r < min(srows, *srows_dev)
+    int scol[DET_MAX_SRC] = {}, swidth[DET_MAX_SRC] = {}, stab[DET_MAX_SRC] = {};
+    long srows[DET_MAX_SRC] = {};
+    const int* srows_dev[DET_MAX_SRC] = {};
+    int add_table(float* t, long n, long off, double cnt) {
+        tab[ntab] = t; tab_n[ntab] = n; acc_off[ntab] = off; count[ntab] = cnt < 1.0 ? 1.0 : cnt;
+        return ntab++;
+    }
+    void add_source(int t, const float* p, long ld, int col, int width, long rows, const int* rows_dev = nullptr) {
+        sp[nsrc] = p; sld[nsrc] = ld; scol[nsrc] = col; swidth[nsrc] = width; srows[nsrc] = rows;
+        srows_dev[nsrc] = rows_dev; stab[nsrc] = t; ++nsrc;
+    }
+};
+// the model's accumulator memory (zero between sites), per-block maxima, scales
+struct DetCtx { unsigned long long* acc; long acc_len; float* part; double* scale; };
+// where a scatter kernel adds table t's contributions: row-major, ld floats per id
+struct DetSink { unsigned long long* acc; const double* scale; long ld; };
+int pt_det_prepare(const DetCtx& d, const DetSite& S, hipStream_t s);   // absmax + scales
+int pt_det_finish(const DetCtx& d, const DetSite& S, hipStream_t s);    // tables += acc, acc = 0
+DetSink pt_det_sink(const DetCtx& d, const DetSite& S, int t, long ld);
+// fixed-point add of an fp32 partial sum into element e of a sink (scale read
+// by the caller once per thread; scale < 0 marks a non-finite table)
+__device__ __forceinline__ void pt_det_add(const DetSink& k, double scale, long e, float a) {
+    if (a != 0.f && scale > 0.0 && isfinite(a))
+        atomicAdd(k.acc + e, (unsigned long long)(long long)rint((double)a * scale));
+}
+
 // ---- gathers / scatters of the token, decision and option paths (gather.hip)
 struct GatherCtx {
     const float* obs; const int32_t* idx; long stride; int N;
@@ -108,22 +147,22 @@ __device__ __forceinline__ long pt_hrow(const GatherCtx& c, int n, int pos) {
 int pt_tok_cat_fwd(const GatherCtx& c, const float* card, const float* zemb, const float* oemb,
                    float* tok_cat, hipStream_t s,
                    long rows_done = 0);
-int pt_tok_cat_bwd(const GatherCtx& c, const float* d_cat, float* d_card, float* d_zemb,
-                   float* d_oemb, hipStream_t s);
+int pt_tok_cat_bwd(const GatherCtx& c, const float* d_cat, const DetSink& d_card, const DetSink& d_zemb,
+                   const DetSink& d_oemb, hipStream_t s);
 int pt_glob_in(const GatherCtx& c, float* glob_in, hipStream_t s);
 int pt_dec_in_fwd(const GatherCtx& c, const float* card, const float* att, const float* semb,
                   const float* cemb, float* dec_in, hipStream_t s);
-int pt_dec_in_bwd(const GatherCtx& c, const float* d_in, float* d_card, float* d_att,
-                  float* d_semb, float* d_cemb, hipStream_t s);
+int pt_dec_in_bwd(const GatherCtx& c, const float* d_in, const DetSink& d_card, const DetSink& d_att,
+                  const DetSink& d_semb, const DetSink& d_cemb, hipStream_t s);
 int pt_x0_fwd(const GatherCtx& c, const float* tokp, const float* bc, const float* readout,
               float* x0, float* keep, hipStream_t s);
 int pt_x0_bwd(const GatherCtx& c, const float* d_x0, float* d_tokp, float* d_bc, hipStream_t s);
 int pt_opt_gather_fwd(const GatherCtx& c, const float* card, const float* att, float* ocard,
                       float* oatt, hipStream_t s);
 int pt_opt_gather_bwd(const GatherCtx& c, const float* d_ocard, const float* d_oatt,
-                      float* d_card, float* d_att, hipStream_t s);
+                      const DetSink& d_card, const DetSink& d_att, hipStream_t s);
 int pt_q_in_fwd(const GatherCtx& c, const float* h, const float* temb, float* q_in, hipStream_t s);
-int pt_q_in_bwd(const GatherCtx& c, const float* d_qin, float* d_h, float* d_temb, hipStream_t s);
+int pt_q_in_bwd(const GatherCtx& c, const float* d_qin, float* d_h, const DetSink& d_temb, hipStream_t s);
 int pt_sc_in_fwd(const GatherCtx& c, const float* h, const float* gd, float* sc_in, hipStream_t s);
 int pt_sc_in_bwd(const GatherCtx& c, const float* d_sc, const float* sc_in, float* d_q,
                  float* d_h, float* d_gd, hipStream_t s);
@@ -151,11 +190,11 @@ int pt_copy_cols(float* dst, long ldd, const float* src, long lds, int rows, int
 int pt_pool_fwd(const float* tab, int E, const int* ids, int K, int NC, float* out, long ldo, int col_mean,
                 int col_max, int* amax, hipStream_t s);
 int pt_pool_bwd(const float* dsrc, long ld, int col_mean, int col_max, const int* amax, const int* ids, int K,
-                int NC, int E, float* d_tab, hipStream_t s);
+                int NC, int E, const DetSink& d_tab, hipStream_t s);
 // dx = dy * gd elementwise (gd = the GELU derivative kept by the forward)
 int pt_mul(const float* dy, const float* gd, float* dx, long n, hipStream_t s);
 int pt_otok_in(const GatherCtx& c, const float* cv, const float* keep, float* out, float* ckeep, hipStream_t s);
-int pt_otok_bwd(const GatherCtx& c, const float* d_in, float* d_card, hipStream_t s);
+int pt_otok_bwd(const GatherCtx& c, const float* d_in, const DetSink& d_card, hipStream_t s);
 int pt_xc_fwd(const float* cread, const float* h, const float* otok, float* xc, int N, int Ls, int NO, int D,
               hipStream_t s);
 int pt_xc_bwd(const float* d_xc, float* d_h, float* d_otok, int N, int Ls, int NO, int D, hipStream_t s);

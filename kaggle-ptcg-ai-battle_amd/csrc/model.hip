@@ -110,6 +110,9 @@ struct PtcgModel {
     BlockA cba;
     float *d_hand, *d_prize, *d_blind, *dxc, *dxc2, *dotok, *dotok_in, *dov1, *dovin;
     int* aux_cnt;
+    // order-independent table scatters: fixed-point accumulators (zero
+    // between sites), per-block maxima, per-table scales
+    DetCtx det{};
     const float* ret = nullptr;
     float* ws = nullptr;
     long ws_floats = 0;
@@ -467,6 +470,12 @@ static size_t carve(PtcgModel* m, char* base) {
     m->ddec = c.take(N * x.dec_in);
     m->dtokp = c.take(tok_rows * D); m->dtokcat = c.take(tok_rows * x.tok_in);
     m->dbc = c.take(N * D);
+    // table-scatter accumulators: the card, attack and skill tables plus the
+    // small ones (zone, owner, option type, select type, context) of one site
+    m->det.acc_len = (long)d.n_cards * d.d_c + (long)d.n_attacks * d.d_a + (long)d.n_skills * d.d_c + 4096;
+    m->det.acc = reinterpret_cast<unsigned long long*>(c.take(2 * m->det.acc_len));
+    m->det.part = c.take(DET_MAX_SRC * DET_PART);
+    m->det.scale = reinterpret_cast<double*>(c.take(2 * DET_MAX_TAB));
     // workspace: split-K partials, column-sum / LayerNorm / head partials
     m->ws_floats = 16L << 20;
     long ln_part = 4096L * (D > x.card_in ? D : x.card_in);   // LayerNorm dW/dB partials (layernorm.hip)
@@ -484,10 +493,13 @@ static int reg(PtcgModel* m, int n, bool train) {
     m->N = n;
     m->train = train;
     m->compact = m->dm.critic == 0;
+    m->det = DetCtx{};
     size_t bytes = carve(m, nullptr);
     PT_HIP(hipMalloc(&m->mem, bytes));
     m->mem_bytes = bytes;
     carve(m, m->mem);
+    // the table-scatter accumulators start at zero (each site's finish re-zeroes them)
+    if (m->det.acc) PT_HIP(hipMemset(m->det.acc, 0, m->det.acc_len * sizeof(unsigned long long)));
     return PTCG_OK;
 }
 
@@ -724,10 +736,18 @@ static int tables_bwd(PtcgModel* m, hipStream_t s) {
     PT_TRY(pt_ln_bwd(m->d_card_ln, x.card_in, m->card_in, x.card_in, m->cln_w, m->c_mu, m->c_rs, nullptr, 0,
                      m->d_card_in, x.card_in, m->G(m->cln_w), m->G(m->cln_b), NC, x.card_in, m->ws, m->ws_floats, s));
     PT_TRY(pt_copy_cols(m->G(m->cid_emb), PT_ID_C, m->d_card_in, x.card_in, NC, PT_ID_C, s));
+    // pool backward into the attack and skill tables (each (card, slot) adds mean + max parts)
+    DetSite P;
+    const int ta = P.add_table(m->d_att_tab, (long)NA * DA, 0, 2.0 * NC * PT_K_ATT);
+    const int tk = P.add_table(m->d_sk_tab, (long)NS * DC, (long)NA * DA, 2.0 * NC * PT_K_SK);
+    P.add_source(ta, m->d_card_in, x.card_in, pa, 2 * DA, NC);
+    P.add_source(tk, m->d_card_in, x.card_in, pa + 2 * DA, 2 * DC, NC);
+    PT_TRY(pt_det_prepare(m->det, P, s));
     PT_TRY(pt_pool_bwd(m->d_card_in, x.card_in, pa, pa + DA, m->a_amax, m->card_attacks, PT_K_ATT, NC, DA,
-                       m->d_att_tab, s));
+                       pt_det_sink(m->det, P, ta, DA), s));
     PT_TRY(pt_pool_bwd(m->d_card_in, x.card_in, pa + 2 * DA, pa + 2 * DA + DC, m->s_amax, m->card_skills, PT_K_SK,
-                       NC, DC, m->d_sk_tab, s));
+                       NC, DC, pt_det_sink(m->det, P, tk, DC), s));
+    PT_TRY(pt_det_finish(m->det, P, s));
     PT_TRY(pt_mul(m->d_att_tab, m->att_lin, m->d_att_lin, (long)NA * DA, s));
     PT_TRY(ldw_(m, m->d_att_lin, DA, m->att_in, x.att_in, m->G(m->am_w), m->G(m->am_b), NA, x.att_in, DA, s));
     PT_TRY(ldxw_(m, m->d_att_lin, DA, m->am_w, x.att_in, m->G(m->aid_emb), PT_ID_A, NA, PT_ID_A, DA, EPI_STORE,
@@ -775,7 +795,12 @@ static int critic_bwd(PtcgModel* m, const GatherCtx& c, const float* grad, hipSt
     PT_TRY(pt_xc_bwd(m->dxc, m->dxa, m->dotok, N, x.l_seq, x.n_orc, D, s));
     PT_TRY(ldw_(m, m->dotok, D, m->otok_in, x.orc_in, m->G(m->op_w), m->G(m->op_b), NK, x.orc_in, D, s));
     PT_TRY(ldx_(m, m->dotok, D, m->op_w, m->dotok_in, x.orc_in, NK, x.orc_in, D, EPI_STORE, nullptr, 0, s));
-    PT_TRY(pt_otok_bwd(c, m->dotok_in, m->dcard, s));
+    DetSite O;
+    const int tc = O.add_table(m->dcard, (long)d.n_cards * d.d_c, 0, (double)NK);
+    O.add_source(tc, m->dotok_in, x.orc_in, 0, d.d_c, NK);
+    PT_TRY(pt_det_prepare(m->det, O, s));
+    PT_TRY(pt_otok_bwd(c, m->dotok_in, pt_det_sink(m->det, O, tc, d.d_c), s));
+    PT_TRY(pt_det_finish(m->det, O, s));
     return PTCG_OK;
 }
 
@@ -838,7 +863,6 @@ extern "C" int ptcg_model_backward(PtcgModel* m, const float* grad, void* stream
     PT_TRY(ldx_(m, m->dq, D, m->q2_w, m->dq1, D, NJo, D, D, EPI_MUL, m->q1, D, s, Od));
     PT_TRY(ldw_(m, m->dq1, D, m->q_in, x.q_in, m->G(m->q1_w), m->G(m->q1_b), NJo, x.q_in, D, s, Od));
     PT_TRY(ldx_(m, m->dq1, D, m->q1_w, m->dqin, x.q_in, NJo, x.q_in, D, EPI_STORE, nullptr, 0, s, Od));
-    PT_TRY(pt_q_in_bwd(c, m->dqin, m->dxa, m->G(m->temb), s));
     const int oc0 = PT_TYPE_E + 2 * D, oa0 = oc0 + PT_OPT_E;
     PT_TRY(ldw_(m, m->dqin + oc0, x.q_in, m->ocard, d.d_c, m->G(m->oc_w), m->G(m->oc_b), NJo, d.d_c, PT_OPT_E, s,
                 Od));
@@ -848,7 +872,23 @@ extern "C" int ptcg_model_backward(PtcgModel* m, const float* grad, void* stream
                 Od));
     PT_TRY(ldx_(m, m->dqin + oa0, x.q_in, m->oa_w, m->doatt, d.d_a, NJo, d.d_a, PT_OPT_E, EPI_STORE, nullptr, 0, s,
                 Od));
-    PT_TRY(pt_opt_gather_bwd(c, m->docard, m->doatt, m->dcard, m->datt, s));
+    // option-type, card and attack table rows of the option rows, then the
+    // pointer gradients into the trunk rows (q_in_bwd)
+    {
+        DetSite S;
+        const long nca = (long)d.n_cards * d.d_c, nat = (long)d.n_attacks * d.d_a;
+        const int tc = S.add_table(m->dcard, nca, 0, (double)NJo);
+        const int ta = S.add_table(m->datt, nat, nca, (double)NJo);
+        const int tt = S.add_table(m->G(m->temb), (long)d.n_opt_types * PT_TYPE_E, nca + nat, (double)NJo);
+        S.add_source(tc, m->docard, d.d_c, 0, d.d_c, NJo, Od);
+        S.add_source(ta, m->doatt, d.d_a, 0, d.d_a, NJo, Od);
+        S.add_source(tt, m->dqin, x.q_in, 0, PT_TYPE_E, NJo, Od);
+        PT_TRY(pt_det_prepare(m->det, S, s));
+        PT_TRY(pt_q_in_bwd(c, m->dqin, m->dxa, pt_det_sink(m->det, S, tt, PT_TYPE_E), s));
+        PT_TRY(pt_opt_gather_bwd(c, m->docard, m->doatt, pt_det_sink(m->det, S, tc, d.d_c),
+                                 pt_det_sink(m->det, S, ta, d.d_a), s));
+        PT_TRY(pt_det_finish(m->det, S, s));
+    }
 
     // final LayerNorm, then the trunk in reverse (d_x in dxb, scratch dxa)
     PT_TRY(pt_ln_bwd(m->dxa, D, m->x[d.layers], D, m->lnf_w, m->lnf_mu, m->lnf_rs, nullptr, 0, m->dxb, D,
@@ -866,7 +906,6 @@ extern "C" int ptcg_model_backward(PtcgModel* m, const float* grad, void* stream
     }
     PT_TRY(ldw_(m, m->dtokp, D, m->tok_cat, x.tok_in, m->G(m->tp_w), m->G(m->tp_b), tok_rows, x.tok_in, D, s, Td));
     PT_TRY(ldx_(m, m->dtokp, D, m->tp_w, m->dtokcat, x.tok_in, tok_rows, x.tok_in, D, EPI_STORE, nullptr, 0, s, Td));
-    PT_TRY(pt_tok_cat_bwd(c, m->dtokcat, m->dcard, m->G(m->zemb), m->G(m->oemb), s));
     PT_TRY(ldw_(m, m->dbc, D, m->gd, x.bcast_in, m->G(m->bc_w), m->G(m->bc_b), N, x.bcast_in, D, s));
     PT_TRY(ldx_(m, m->dbc, D, m->bc_w, m->dgd, x.bcast_in, N, x.bcast_in, D, EPI_ACCUM, nullptr, 0, s));
     // decision MLP (d_dvec = dgd[:, G:])
@@ -874,7 +913,39 @@ extern "C" int ptcg_model_backward(PtcgModel* m, const float* grad, void* stream
     PT_TRY(ldx_(m, m->dgd + G, x.bcast_in, m->d2_w, m->dd1, PT_DEC_H, N, PT_DEC_H, PT_DEC_H, EPI_MUL, m->d1, PT_DEC_H, s));
     PT_TRY(ldw_(m, m->dd1, PT_DEC_H, m->dec_in, x.dec_in, m->G(m->d1_w), m->G(m->d1_b), N, x.dec_in, PT_DEC_H, s));
     PT_TRY(ldx_(m, m->dd1, PT_DEC_H, m->d1_w, m->ddec, x.dec_in, N, x.dec_in, PT_DEC_H, EPI_STORE, nullptr, 0, s));
-    PT_TRY(pt_dec_in_bwd(c, m->ddec, m->dcard, m->datt, m->G(m->semb), m->G(m->cemb), s));
+    // token rows (card, tool cards, zone, owner) and decision slots (select
+    // type, context, card, attack) into their tables
+    {
+        DetSite S;
+        const long nca = (long)d.n_cards * d.d_c, nat = (long)d.n_attacks * d.d_a;
+        const long nz = (long)d.n_zones * PT_ZONE_E, no = (long)d.n_owners * PT_OWNER_E;
+        const long nsl = (long)d.n_select_types * PT_SEL_E;
+        const int tc = S.add_table(m->dcard, nca, 0, 3.0 * tok_rows + 4.0 * N);
+        const int ta = S.add_table(m->datt, nat, nca, 2.0 * N);
+        const int tz = S.add_table(m->G(m->zemb), nz, nca + nat, (double)tok_rows);
+        const int to = S.add_table(m->G(m->oemb), no, nca + nat + nz, (double)tok_rows);
+        const int tsl = S.add_table(m->G(m->semb), nsl, nca + nat + nz + no, (double)N);
+        const int tcx = S.add_table(m->G(m->cemb), (long)d.n_contexts * PT_CTX_E, nca + nat + nz + no + nsl,
+                                    (double)N);
+        const int* td = m->compact ? Tr : nullptr;
+        const int zc = 2 * d.d_c + d.tok_f;   // zone columns of the token concat, then owner
+        S.add_source(tc, m->dtokcat, x.tok_in, 0, 2 * d.d_c, tok_rows, td);
+        S.add_source(tz, m->dtokcat, x.tok_in, zc, PT_ZONE_E, tok_rows, td);
+        S.add_source(to, m->dtokcat, x.tok_in, zc + PT_ZONE_E, PT_OWNER_E, tok_rows, td);
+        // decision concat [sel | ctx | 2 card | 2 attack | 2 card | dec_f]
+        const int c0 = PT_SEL_E + PT_CTX_E;
+        S.add_source(tsl, m->ddec, x.dec_in, 0, PT_SEL_E, N);
+        S.add_source(tcx, m->ddec, x.dec_in, PT_SEL_E, PT_CTX_E, N);
+        S.add_source(tc, m->ddec, x.dec_in, c0, 2 * d.d_c, N);
+        S.add_source(ta, m->ddec, x.dec_in, c0 + 2 * d.d_c, 2 * d.d_a, N);
+        S.add_source(tc, m->ddec, x.dec_in, c0 + 2 * d.d_c + 2 * d.d_a, 2 * d.d_c, N);
+        PT_TRY(pt_det_prepare(m->det, S, s));
+        PT_TRY(pt_tok_cat_bwd(c, m->dtokcat, pt_det_sink(m->det, S, tc, d.d_c), pt_det_sink(m->det, S, tz, PT_ZONE_E),
+                              pt_det_sink(m->det, S, to, PT_OWNER_E), s));
+        PT_TRY(pt_dec_in_bwd(c, m->ddec, pt_det_sink(m->det, S, tc, d.d_c), pt_det_sink(m->det, S, ta, d.d_a),
+                             pt_det_sink(m->det, S, tsl, PT_SEL_E), pt_det_sink(m->det, S, tcx, PT_CTX_E), s));
+        PT_TRY(pt_det_finish(m->det, S, s));
+    }
     // global MLP (d_g = dgd[:, :G])
     PT_TRY(ldw_(m, m->dgd, x.bcast_in, m->g1a, G, m->G(m->g2_w), m->G(m->g2_b), N, G, G, s));
     PT_TRY(ldx_(m, m->dgd, x.bcast_in, m->g2_w, m->dg1, G, N, G, G, EPI_MUL, m->g1, G, s));

@@ -5,8 +5,9 @@ dims.critic = 1), against the CPU oracle on identical seeded inputs.
 Tolerances as for the learned-table model (test_gpu_model.py): forward
 relative L2 <= 1e-5; every gradient tensor relative L2 <= 1e-4; weights after
 Adam steps relative L2 <= 1e-4.  The static-table chain's scatters (pool
-backward, CardVec rows shared by tokens / options / oracle tokens) use fp32
-atomics, so the order of those sums varies at the 1e-7 level.
+backward, CardVec rows shared by tokens / options / oracle tokens) add in
+order-independent fixed point, so repeated calls agree bit for bit
+(test_gpu_determinism.py).
 """
 import numpy as np
 import pytest

@@ -62,6 +62,24 @@ int ptcg_kernel_gemm_dw_bf16(int rows, int in, int out, const float* dY, int64_t
                              const float* X, int64_t ldx, float* dW, float* db,
                              float* workspace, int64_t workspace_floats, void* stream);
 
+/* Products on operands STORED in bf16 (the mixed-precision variant's
+ * activations, pufferlib.cu precision_t = bf16; uint16 bit patterns),
+ * v_mfma_f32_16x16x32_bf16 with fp32 accumulation.
+ * ptcg_kernel_gemm_bs: C (M, N) = epi(A B^T), A (M, K) at row stride lda,
+ * B (N, K) at row stride ldb, K, lda, ldb multiples of 8, A and B 16 B
+ * aligned; epilogues STORE (fp32 or bf16 C), BIAS (bf16 C), BIAS_RESID
+ * (fp32 C and R), BIAS_GELU_D (bf16 C = gelu'(z), C2 = gelu(z)), MUL (bf16 C
+ * and R); out_bf16 selects the output type; bias fp32.
+ * ptcg_kernel_gemm_dw_bs: dW (out, in) = dY^T X and db = column sums of dY
+ * (optional), fp32, dY (rows, out) and X (rows, in) bf16; out, in, lddy,
+ * ldx multiples of 8; workspace as ptcg_kernel_gemm_dw.                    */
+int ptcg_kernel_gemm_bs(int M, int N, int K, const void* A, int64_t lda, const void* B, int64_t ldb,
+                        void* C, int64_t ldc, int epi, int out_bf16, const float* bias, const void* R,
+                        int64_t ldr, void* C2, int64_t ldc2, void* stream);
+int ptcg_kernel_gemm_dw_bs(int rows, int in, int out, const void* dY, int64_t lddy, const void* X,
+                           int64_t ldx, float* dW, float* db, float* workspace, int64_t workspace_floats,
+                           void* stream);
+
 /* deterministic column sums out[n] = sum_m X[m*ldx+n] (pt_bias_grad,
  * ptcg_kernels.cuh:87-96); workspace >= ceil(M/256)*N floats.              */
 int ptcg_kernel_colsum(const float* X, int64_t ldx, int M, int N, float* out,

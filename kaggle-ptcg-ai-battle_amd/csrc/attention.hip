@@ -16,6 +16,8 @@
 // is always kept, so no row is fully masked.  dS = P o (dP - rowsum(dO o O)).
 #include "common.h"
 
+#include <type_traits>
+
 namespace {
 
 // ======================================================= MFMA (fp32) path
@@ -52,9 +54,21 @@ __device__ __forceinline__ floatx4 mfma4(const float (&a)[4], const float (&b)[4
     }
 }
 
-template <int DH, int NT, bool BF>   // NT = Lp / 16 key (and query) tiles
-__global__ __launch_bounds__(512) void attn_fwd_mfma_kernel(const float* __restrict__ qkv,
-        const float* __restrict__ keep, float* __restrict__ ctx, float* __restrict__ lse,
+// Element type T of qkv, ctx, dctx and dqkv: float, or __bf16 (the
+// mixed-precision variant's activations, read and written in bf16; the
+// products round their operands to bf16 anyway, so only the stored outputs
+// and rowsum(dO o O) see the narrower type).
+__device__ __forceinline__ float4 ld4(const float* p) { return *reinterpret_cast<const float4*>(p); }
+__device__ __forceinline__ float4 ld4(const __bf16* p) {
+    const bf16x4 b = *reinterpret_cast<const bf16x4*>(p);
+    return make_float4((float)b[0], (float)b[1], (float)b[2], (float)b[3]);
+}
+__device__ __forceinline__ float tof(float v) { return v; }
+__device__ __forceinline__ float tof(__bf16 v) { return (float)v; }
+
+template <int DH, int NT, bool BF, typename T>   // NT = Lp / 16 key (and query) tiles
+__global__ __launch_bounds__(512) void attn_fwd_mfma_kernel(const T* __restrict__ qkv,
+        const float* __restrict__ keep, T* __restrict__ ctx, float* __restrict__ lse,
         int Lfix, int H, float scale, const int* __restrict__ coff) {
     constexpr int LP = NT * 16, SK = DH + 4;
     extern __shared__ float sm[];
@@ -70,14 +84,14 @@ __global__ __launch_bounds__(512) void attn_fwd_mfma_kernel(const float* __restr
     const int D = H * DH;
     // this sample's tiles (compact rows vary in length; the template covers the longest)
     const int ntl = min(NT, (L + 15) / 16);
-    const gfloat* base = (const gfloat*)qkv + rb * 3 * D + h * DH;
+    const T* base = qkv + rb * 3 * D + h * DH;
     for (int idx = tid; idx < ntl * 16 * (DH / 4); idx += 512) {
         const int l = idx / (DH / 4), c4 = (idx % (DH / 4)) * 4;
         float4 k4 = make_float4(0.f, 0.f, 0.f, 0.f), v4 = k4;
         if (l < L) {
-            const gfloat* r = base + (long)l * 3 * D + c4;
-            k4 = ld_g4(r + D);
-            v4 = ld_g4(r + 2 * D);
+            const T* r = base + (long)l * 3 * D + c4;
+            k4 = ld4(r + D);
+            v4 = ld4(r + 2 * D);
         }
         *reinterpret_cast<float4*>(&Ks[l * SK + c4]) = k4;
         *reinterpret_cast<float4*>(&Vs[l * SK + c4]) = v4;
@@ -92,7 +106,7 @@ __global__ __launch_bounds__(512) void attn_fwd_mfma_kernel(const float* __restr
         const bool qv = q0 + li < L;
 #pragma unroll
         for (int kk = 0; kk < DH / 4; ++kk)
-            qb[kk] = qv ? base[(long)(q0 + li) * 3 * D + 4 * kk + lq] : 0.f;
+            qb[kk] = qv ? tof(base[(long)(q0 + li) * 3 * D + 4 * kk + lq]) : 0.f;
         floatx4 o[DH / 16];
 #pragma unroll
         for (int dt = 0; dt < DH / 16; ++dt) o[dt] = floatx4{0.f, 0.f, 0.f, 0.f};
@@ -177,9 +191,9 @@ __global__ __launch_bounds__(512) void attn_fwd_mfma_kernel(const float* __restr
             const float inv = 1.0f / __shfl(sum, 4 * lq + r, 64);
             const int q = q0 + 4 * lq + r;
             if (q < L) {
-                gfloat* dst = (gfloat*)ctx + (rb + q) * D + h * DH + li;
+                T* dst = ctx + (rb + q) * D + h * DH + li;
 #pragma unroll
-                for (int dt = 0; dt < DH / 16; ++dt) dst[16 * dt] = o[dt][r] * inv;
+                for (int dt = 0; dt < DH / 16; ++dt) dst[16 * dt] = (T)(o[dt][r] * inv);
             }
         }
         if (lq == 0 && qv) lse[((long)n * H + h) * Lfix + q0 + li] = mx + logf(sum);
@@ -191,11 +205,11 @@ __global__ __launch_bounds__(512) void attn_fwd_mfma_kernel(const float* __restr
 // dS = P (dP - rowsum(dO o O)), accumulates dV += P^T dO and dK += dS^T Q
 // (register-r trick again, now over queries), and parks dS*scale in LDS.
 // Pass B walks query stripes: dQ = dS K from LDS.
-template <int DH, int NT, bool BF>
-__global__ __launch_bounds__(512) void attn_bwd_mfma_kernel(const float* __restrict__ qkv,
-        const float* __restrict__ keep, const float* __restrict__ ctx,
-        const float* __restrict__ lse, const float* __restrict__ dctx,
-        float* __restrict__ dqkv, int Lfix, int H, float scale, const int* __restrict__ coff) {
+template <int DH, int NT, bool BF, typename T>
+__global__ __launch_bounds__(512) void attn_bwd_mfma_kernel(const T* __restrict__ qkv,
+        const float* __restrict__ keep, const T* __restrict__ ctx,
+        const float* __restrict__ lse, const T* __restrict__ dctx,
+        T* __restrict__ dqkv, int Lfix, int H, float scale, const int* __restrict__ coff) {
     constexpr int LP = NT * 16, SQ = DH + 4, SKB = DH + 16, SS = LP + 4;
     extern __shared__ float sm[];
     float* Qs = sm;                 // [LP][SQ]
@@ -214,10 +228,10 @@ __global__ __launch_bounds__(512) void attn_bwd_mfma_kernel(const float* __restr
     const int D = H * DH;
     // this sample's tiles (compact rows vary in length; the template covers the longest)
     const int ntl = min(NT, (L + 15) / 16);
-    const gfloat* base = (const gfloat*)qkv + rb * 3 * D + h * DH;
-    const gfloat* ob = (const gfloat*)ctx + rb * D + h * DH;
-    const gfloat* dob = (const gfloat*)dctx + rb * D + h * DH;
-    gfloat* gb = (gfloat*)dqkv + rb * 3 * D + h * DH;
+    const T* base = qkv + rb * 3 * D + h * DH;
+    const T* ob = ctx + rb * D + h * DH;
+    const T* dob = dctx + rb * D + h * DH;
+    T* gb = dqkv + rb * 3 * D + h * DH;
     // stage Q, dO, K and form Dv[q] = sum_d dO[q][d] O[q][d]: the DH/4 lanes
     // holding a row's 4-column partials are adjacent (512 is a multiple of
     // DH/4), so a butterfly over them gives the row sum (padded rows 0)
@@ -225,11 +239,11 @@ __global__ __launch_bounds__(512) void attn_bwd_mfma_kernel(const float* __restr
         const int l = idx / (DH / 4), c4 = (idx % (DH / 4)) * 4;
         float4 q4 = make_float4(0.f, 0.f, 0.f, 0.f), k4 = q4, d4 = q4, o4 = q4;
         if (l < L) {
-            const gfloat* r = base + (long)l * 3 * D + c4;
-            q4 = ld_g4(r);
-            k4 = ld_g4(r + D);
-            d4 = ld_g4(dob + (long)l * D + c4);
-            o4 = ld_g4(ob + (long)l * D + c4);
+            const T* r = base + (long)l * 3 * D + c4;
+            q4 = ld4(r);
+            k4 = ld4(r + D);
+            d4 = ld4(dob + (long)l * D + c4);
+            o4 = ld4(ob + (long)l * D + c4);
         }
         *reinterpret_cast<float4*>(&Qs[l * SQ + c4]) = q4;
         *reinterpret_cast<float4*>(&dOs[l * SQ + c4]) = d4;
@@ -252,8 +266,8 @@ __global__ __launch_bounds__(512) void attn_bwd_mfma_kernel(const float* __restr
         float kr[DH / 4], vr[DH / 4];    // B operands: lane (li = key, lq) holds K/V[k0+li][4kk+lq]
 #pragma unroll
         for (int kk = 0; kk < DH / 4; ++kk) {
-            kr[kk] = kv ? base[(long)(k0 + li) * 3 * D + D + 4 * kk + lq] : 0.f;
-            vr[kk] = kv ? base[(long)(k0 + li) * 3 * D + 2 * D + 4 * kk + lq] : 0.f;
+            kr[kk] = kv ? tof(base[(long)(k0 + li) * 3 * D + D + 4 * kk + lq]) : 0.f;
+            vr[kk] = kv ? tof(base[(long)(k0 + li) * 3 * D + 2 * D + 4 * kk + lq]) : 0.f;
         }
         const float kfl = kf[k0 + li];
         floatx4 dv[DH / 16], dk[DH / 16];
@@ -305,11 +319,11 @@ __global__ __launch_bounds__(512) void attn_bwd_mfma_kernel(const float* __restr
         for (int r = 0; r < 4; ++r) {
             const int key = k0 + 4 * lq + r;
             if (key < L) {
-                gfloat* g = gb + (long)key * 3 * D + li;
+                T* g = gb + (long)key * 3 * D + li;
 #pragma unroll
                 for (int dt = 0; dt < DH / 16; ++dt) {
-                    g[D + 16 * dt] = dk[dt][r] * scale;
-                    g[2 * D + 16 * dt] = dv[dt][r];
+                    g[D + 16 * dt] = (T)(dk[dt][r] * scale);
+                    g[2 * D + 16 * dt] = (T)dv[dt][r];
                 }
             }
         }
@@ -337,9 +351,9 @@ __global__ __launch_bounds__(512) void attn_bwd_mfma_kernel(const float* __restr
         for (int r = 0; r < 4; ++r) {
             const int q = 16 * qt + 4 * lq + r;
             if (q < L) {
-                gfloat* g = gb + (long)q * 3 * D + li;
+                T* g = gb + (long)q * 3 * D + li;
 #pragma unroll
-                for (int dt = 0; dt < DH / 16; ++dt) g[16 * dt] = dq[dt][r];
+                for (int dt = 0; dt < DH / 16; ++dt) g[16 * dt] = (T)dq[dt][r];
             }
         }
     }
@@ -351,11 +365,11 @@ __global__ __launch_bounds__(512) void attn_bwd_mfma_kernel(const float* __restr
 // pass B walks query stripes and recomputes S^T = K Q^T and dP^T = V dO^T
 // per key tile (queries on lanes), then dQ += dS K with the register-r key
 // permutation.  Costs one more S and dP evaluation than the stored variant.
-template <int DH, int NT, bool BF>
-__global__ __launch_bounds__(512) void attn_bwd_mfma_rc_kernel(const float* __restrict__ qkv,
-        const float* __restrict__ keep, const float* __restrict__ ctx,
-        const float* __restrict__ lse, const float* __restrict__ dctx,
-        float* __restrict__ dqkv, int Lfix, int H, float scale, const int* __restrict__ coff) {
+template <int DH, int NT, bool BF, typename T>
+__global__ __launch_bounds__(512) void attn_bwd_mfma_rc_kernel(const T* __restrict__ qkv,
+        const float* __restrict__ keep, const T* __restrict__ ctx,
+        const float* __restrict__ lse, const T* __restrict__ dctx,
+        T* __restrict__ dqkv, int Lfix, int H, float scale, const int* __restrict__ coff) {
     constexpr int LP = NT * 16, SQ = DH + 4;
     extern __shared__ float sm[];
     float* Qs = sm;                 // [LP][SQ]
@@ -372,20 +386,20 @@ __global__ __launch_bounds__(512) void attn_bwd_mfma_rc_kernel(const float* __re
     const long rb = coff ? (long)coff[n] : (long)n * Lfix;
     const int L = coff ? coff[n + 1] - coff[n] : Lfix;
     const int D = H * DH;
-    const gfloat* base = (const gfloat*)qkv + rb * 3 * D + h * DH;
-    const gfloat* ob = (const gfloat*)ctx + rb * D + h * DH;
-    const gfloat* dob = (const gfloat*)dctx + rb * D + h * DH;
-    gfloat* gb = (gfloat*)dqkv + rb * 3 * D + h * DH;
+    const T* base = qkv + rb * 3 * D + h * DH;
+    const T* ob = ctx + rb * D + h * DH;
+    const T* dob = dctx + rb * D + h * DH;
+    T* gb = dqkv + rb * 3 * D + h * DH;
     for (int idx = tid; idx < LP * (DH / 4); idx += 512) {
         const int l = idx / (DH / 4), c4 = (idx % (DH / 4)) * 4;
         float4 q4 = make_float4(0.f, 0.f, 0.f, 0.f), k4 = q4, v4 = q4, d4 = q4, o4 = q4;
         if (l < L) {
-            const gfloat* r = base + (long)l * 3 * D + c4;
-            q4 = ld_g4(r);
-            k4 = ld_g4(r + D);
-            v4 = ld_g4(r + 2 * D);
-            d4 = ld_g4(dob + (long)l * D + c4);
-            o4 = ld_g4(ob + (long)l * D + c4);
+            const T* r = base + (long)l * 3 * D + c4;
+            q4 = ld4(r);
+            k4 = ld4(r + D);
+            v4 = ld4(r + 2 * D);
+            d4 = ld4(dob + (long)l * D + c4);
+            o4 = ld4(ob + (long)l * D + c4);
         }
         *reinterpret_cast<float4*>(&Qs[l * SQ + c4]) = q4;
         *reinterpret_cast<float4*>(&dOs[l * SQ + c4]) = d4;
@@ -410,8 +424,8 @@ __global__ __launch_bounds__(512) void attn_bwd_mfma_rc_kernel(const float* __re
         float kr[DH / 4], vr[DH / 4];
 #pragma unroll
         for (int kk = 0; kk < DH / 4; ++kk) {
-            kr[kk] = kv ? base[(long)(k0 + li) * 3 * D + D + 4 * kk + lq] : 0.f;
-            vr[kk] = kv ? base[(long)(k0 + li) * 3 * D + 2 * D + 4 * kk + lq] : 0.f;
+            kr[kk] = kv ? tof(base[(long)(k0 + li) * 3 * D + D + 4 * kk + lq]) : 0.f;
+            vr[kk] = kv ? tof(base[(long)(k0 + li) * 3 * D + 2 * D + 4 * kk + lq]) : 0.f;
         }
         const float kfl = kf[k0 + li];
         floatx4 dv[DH / 16], dk[DH / 16];
@@ -460,11 +474,11 @@ __global__ __launch_bounds__(512) void attn_bwd_mfma_rc_kernel(const float* __re
         for (int r = 0; r < 4; ++r) {
             const int key = k0 + 4 * lq + r;
             if (key < L) {
-                gfloat* g = gb + (long)key * 3 * D + li;
+                T* g = gb + (long)key * 3 * D + li;
 #pragma unroll
                 for (int dt = 0; dt < DH / 16; ++dt) {
-                    g[D + 16 * dt] = dk[dt][r] * scale;
-                    g[2 * D + 16 * dt] = dv[dt][r];
+                    g[D + 16 * dt] = (T)(dk[dt][r] * scale);
+                    g[2 * D + 16 * dt] = (T)dv[dt][r];
                 }
             }
         }
@@ -519,9 +533,9 @@ __global__ __launch_bounds__(512) void attn_bwd_mfma_rc_kernel(const float* __re
         for (int r = 0; r < 4; ++r) {
             const int q = q0 + 4 * lq + r;
             if (q < L) {
-                gfloat* g = gb + (long)q * 3 * D + li;
+                T* g = gb + (long)q * 3 * D + li;
 #pragma unroll
-                for (int dt = 0; dt < DH / 16; ++dt) g[16 * dt] = dq[dt][r];
+                for (int dt = 0; dt < DH / 16; ++dt) g[16 * dt] = (T)dq[dt][r];
             }
         }
     }
@@ -538,38 +552,47 @@ size_t bwd_mfma_lds_bytes(int LP, int DH) {
     return sizeof(float) * ((size_t)LP * (DH + 4) * 2 + (size_t)LP * (DH + 16) + (size_t)LP * (LP + 4) + 3 * (size_t)LP);
 }
 
-template <int DH, int NT, bool BF>
+// BF: bf16 products; IO16 (with BF): qkv / ctx / dctx / dqkv stored in bf16
+template <int DH, int NT, bool BF, bool IO16>
 int launch_fwd_mfma(const float* qkv, const float* keep, float* ctx, float* lse, int N, int L, int H,
                     hipStream_t s, const int* coff) {
+    typedef typename std::conditional<IO16, __bf16, float>::type T;
     const size_t lds = fwd_mfma_lds_bytes(NT * 16, DH);
-    PT_HIP(hipFuncSetAttribute((const void*)attn_fwd_mfma_kernel<DH, NT, BF>,
+    PT_HIP(hipFuncSetAttribute((const void*)attn_fwd_mfma_kernel<DH, NT, BF, T>,
                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-    hipLaunchKernelGGL((attn_fwd_mfma_kernel<DH, NT, BF>), dim3(N * H), dim3(512), lds, s, qkv, keep, ctx, lse,
-                       L, H, 1.0f / sqrtf((float)DH), coff);
+    hipLaunchKernelGGL((attn_fwd_mfma_kernel<DH, NT, BF, T>), dim3(N * H), dim3(512), lds, s,
+                       reinterpret_cast<const T*>(qkv), keep, reinterpret_cast<T*>(ctx), lse, L, H,
+                       1.0f / sqrtf((float)DH), coff);
     PT_LAUNCH_CHECK();
     return PTCG_OK;
 }
 
-template <int DH, int NT, bool BF>
+template <int DH, int NT, bool BF, bool IO16>
 int launch_bwd_rc(const float* qkv, const float* keep, const float* ctx, const float* lse,
                   const float* dctx, float* dqkv, int N, int L, int H, hipStream_t s, const int* coff) {
+    typedef typename std::conditional<IO16, __bf16, float>::type T;
     const size_t lds = bwd_rc_lds_bytes(NT * 16, DH);
-    PT_HIP(hipFuncSetAttribute((const void*)attn_bwd_mfma_rc_kernel<DH, NT, BF>,
+    PT_HIP(hipFuncSetAttribute((const void*)attn_bwd_mfma_rc_kernel<DH, NT, BF, T>,
                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-    hipLaunchKernelGGL((attn_bwd_mfma_rc_kernel<DH, NT, BF>), dim3(N * H), dim3(512), lds, s, qkv, keep, ctx,
-                       lse, dctx, dqkv, L, H, 1.0f / sqrtf((float)DH), coff);
+    hipLaunchKernelGGL((attn_bwd_mfma_rc_kernel<DH, NT, BF, T>), dim3(N * H), dim3(512), lds, s,
+                       reinterpret_cast<const T*>(qkv), keep, reinterpret_cast<const T*>(ctx), lse,
+                       reinterpret_cast<const T*>(dctx), reinterpret_cast<T*>(dqkv), L, H,
+                       1.0f / sqrtf((float)DH), coff);
     PT_LAUNCH_CHECK();
     return PTCG_OK;
 }
 
-template <int DH, int NT, bool BF>
+template <int DH, int NT, bool BF, bool IO16>
 int launch_bwd_mfma(const float* qkv, const float* keep, const float* ctx, const float* lse,
                     const float* dctx, float* dqkv, int N, int L, int H, hipStream_t s, const int* coff) {
+    typedef typename std::conditional<IO16, __bf16, float>::type T;
     const size_t lds = bwd_mfma_lds_bytes(NT * 16, DH);
-    PT_HIP(hipFuncSetAttribute((const void*)attn_bwd_mfma_kernel<DH, NT, BF>,
+    PT_HIP(hipFuncSetAttribute((const void*)attn_bwd_mfma_kernel<DH, NT, BF, T>,
                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-    hipLaunchKernelGGL((attn_bwd_mfma_kernel<DH, NT, BF>), dim3(N * H), dim3(512), lds, s, qkv, keep, ctx, lse,
-                       dctx, dqkv, L, H, 1.0f / sqrtf((float)DH), coff);
+    hipLaunchKernelGGL((attn_bwd_mfma_kernel<DH, NT, BF, T>), dim3(N * H), dim3(512), lds, s,
+                       reinterpret_cast<const T*>(qkv), keep, reinterpret_cast<const T*>(ctx), lse,
+                       reinterpret_cast<const T*>(dctx), reinterpret_cast<T*>(dqkv), L, H,
+                       1.0f / sqrtf((float)DH), coff);
     PT_LAUNCH_CHECK();
     return PTCG_OK;
 }
@@ -603,8 +626,8 @@ int pt_attn_supported(int L, int DH) {
     return (fwd_tiles(L, DH) && (bwd_store_tiles(L, DH) || bwd_rc_tiles(L, DH))) ? 1 : 0;
 }
 
-// (used inside the BF-templated dispatchers below)
-#define PT_NT_CASE(DH, N, CALL, ...) case N: return CALL<DH, N, BF>(__VA_ARGS__);
+// (used inside the BF / IO16-templated dispatchers below)
+#define PT_NT_CASE(DH, N, CALL, ...) case N: return CALL<DH, N, BF, IO16>(__VA_ARGS__);
 #define PT_NT_SWITCH8(DH, NT, CALL, ...)                                                              \
     switch (NT) {                                                                                     \
         PT_NT_CASE(DH, 1, CALL, __VA_ARGS__) PT_NT_CASE(DH, 2, CALL, __VA_ARGS__)                     \
@@ -622,13 +645,13 @@ int pt_attn_supported(int L, int DH) {
         default: break;                                                                               \
     }
 
-template <bool BF>
+template <bool BF, bool IO16>
 static int attn_fwd_dispatch(const float* qkv, const float* keep, float* ctx, float* lse, int N, int L, int H,
                              int DH, hipStream_t s, const int* coff) {
     const int nt = fwd_tiles(L, DH);
     if (nt && DH == 64) {
         PT_NT_SWITCH8(64, nt, launch_fwd_mfma, qkv, keep, ctx, lse, N, L, H, s, coff)
-        if (nt == 9) return launch_fwd_mfma<64, 9, BF>(qkv, keep, ctx, lse, N, L, H, s, coff);
+        if (nt == 9) return launch_fwd_mfma<64, 9, BF, IO16>(qkv, keep, ctx, lse, N, L, H, s, coff);
     } else if (nt) {
         PT_NT_SWITCH8(32, nt, launch_fwd_mfma, qkv, keep, ctx, lse, N, L, H, s, coff)
         PT_NT_SWITCH_HI(32, nt, launch_fwd_mfma, qkv, keep, ctx, lse, N, L, H, s, coff)
@@ -636,7 +659,7 @@ static int attn_fwd_dispatch(const float* qkv, const float* keep, float* ctx, fl
     PT_REQUIRE(false, "attention: no kernel for L=%d Dh=%d", L, DH);
 }
 
-template <bool BF>
+template <bool BF, bool IO16>
 static int attn_bwd_dispatch(const float* qkv, const float* keep, const float* ctx, const float* lse,
                              const float* dctx, float* dqkv, int N, int L, int H, int DH, hipStream_t s,
                              const int* coff) {
@@ -648,7 +671,7 @@ static int attn_bwd_dispatch(const float* qkv, const float* keep, const float* c
     nt = bwd_rc_tiles(L, DH);
     if (nt && DH == 64) {
         PT_NT_SWITCH8(64, nt, launch_bwd_rc, qkv, keep, ctx, lse, dctx, dqkv, N, L, H, s, coff)
-        if (nt == 9) return launch_bwd_rc<64, 9, BF>(qkv, keep, ctx, lse, dctx, dqkv, N, L, H, s, coff);
+        if (nt == 9) return launch_bwd_rc<64, 9, BF, IO16>(qkv, keep, ctx, lse, dctx, dqkv, N, L, H, s, coff);
     } else if (nt) {
         PT_NT_SWITCH8(32, nt, launch_bwd_rc, qkv, keep, ctx, lse, dctx, dqkv, N, L, H, s, coff)
         PT_NT_SWITCH_HI(32, nt, launch_bwd_rc, qkv, keep, ctx, lse, dctx, dqkv, N, L, H, s, coff)
@@ -659,16 +682,18 @@ static int attn_bwd_dispatch(const float* qkv, const float* keep, const float* c
 int pt_attn_fwd(const float* qkv, const float* keep, float* ctx, float* lse, int N, int L, int H,
                 int DH, hipStream_t s, const int* coff, int prec) {
     PT_REQUIRE(pt_attn_supported(L, DH), "attention: L=%d Dh=%d exceeds the fused kernels' LDS budget", L, DH);
-    return prec ? attn_fwd_dispatch<true>(qkv, keep, ctx, lse, N, L, H, DH, s, coff)
-                : attn_fwd_dispatch<false>(qkv, keep, ctx, lse, N, L, H, DH, s, coff);
+    if (prec == 2) return attn_fwd_dispatch<true, true>(qkv, keep, ctx, lse, N, L, H, DH, s, coff);
+    return prec ? attn_fwd_dispatch<true, false>(qkv, keep, ctx, lse, N, L, H, DH, s, coff)
+                : attn_fwd_dispatch<false, false>(qkv, keep, ctx, lse, N, L, H, DH, s, coff);
 }
 
 int pt_attn_bwd(const float* qkv, const float* keep, const float* ctx, const float* lse,
                 const float* dctx, float* dqkv, int N, int L, int H, int DH, hipStream_t s, const int* coff,
                 int prec) {
     PT_REQUIRE(pt_attn_supported(L, DH), "attention bwd: L=%d Dh=%d exceeds the fused kernels' LDS budget", L, DH);
-    return prec ? attn_bwd_dispatch<true>(qkv, keep, ctx, lse, dctx, dqkv, N, L, H, DH, s, coff)
-                : attn_bwd_dispatch<false>(qkv, keep, ctx, lse, dctx, dqkv, N, L, H, DH, s, coff);
+    if (prec == 2) return attn_bwd_dispatch<true, true>(qkv, keep, ctx, lse, dctx, dqkv, N, L, H, DH, s, coff);
+    return prec ? attn_bwd_dispatch<true, false>(qkv, keep, ctx, lse, dctx, dqkv, N, L, H, DH, s, coff)
+                : attn_bwd_dispatch<false, false>(qkv, keep, ctx, lse, dctx, dqkv, N, L, H, DH, s, coff);
 }
 
 // Which kernels a shape takes (for tests): bit 0 forward, bit 1 backward

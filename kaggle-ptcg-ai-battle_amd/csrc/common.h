@@ -159,6 +159,11 @@ struct GemmArgs {
     // 0: fp32 products (v_mfma_f32_16x16x4_f32); 1: operands rounded to bf16
     // on the way into LDS, fp32 accumulation (v_mfma_f32_16x16x32_bf16)
     int prec;
+    // bf16 storage: bs = A and B hold bf16 (k-contiguous both: C = epi(A B^T),
+    // K, lda, ldb multiples of 8; or both transposed: the weight gradient
+    // dW = A^T B, M, N, lda, ldb multiples of 8); obf = C (and C2) hold bf16,
+    // as does R for EPI_MUL.  Pointers stay float* and are reinterpreted.
+    int bs, obf;
     // set by pt_gemm: a launch covers logical tiles [tile0, tile0 + ntiles)
     // (ntiles 0 = all); tail_part: split-K partials of those tiles go to a
     // tile-local workspace [split][tile][128 x 128]

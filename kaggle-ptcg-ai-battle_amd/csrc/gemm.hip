@@ -70,10 +70,48 @@ __device__ __forceinline__ bool tile_of_range(const GemmArgs& g, int tn, int& tm
     return true;
 }
 
-// one output element through the epilogue
+// bf16 activations (OB): C and C2 hold bf16 (round to nearest even), and so
+// does R for EPI_MUL (the GELU derivative the forward stored in bf16); the
+// residual R of EPI_BIAS_RESID and the bias stay fp32
+typedef __attribute__((address_space(1))) __bf16 gbf16;
+typedef __attribute__((address_space(1))) bf16x4 gbf16x4;
+__device__ __forceinline__ __bf16* bfp(float* p) { return reinterpret_cast<__bf16*>(p); }
+__device__ __forceinline__ const __bf16* bfp(const float* p) { return reinterpret_cast<const __bf16*>(p); }
+__device__ __forceinline__ void st_b1(float* base, long i, float v) { *(gbf16*)(bfp(base) + i) = (__bf16)v; }
+__device__ __forceinline__ float ld_b1(const float* base, long i) { return (float)*(const gbf16*)(bfp(base) + i); }
+__device__ __forceinline__ void st_b4(float* base, long i, floatx4 v) {
+    *(gbf16x4*)(bfp(base) + i) = to_bf16x4(v[0], v[1], v[2], v[3]);
+}
+__device__ __forceinline__ floatx4 ld_b4(const float* base, long i) {
+    const bf16x4 b = *(const gbf16x4*)(bfp(base) + i);
+    return floatx4{(float)b[0], (float)b[1], (float)b[2], (float)b[3]};
+}
+
 template <int EPI>
-__device__ __forceinline__ void epi_store(const GemmArgs& g, int m, int n, float v) {
+__device__ __forceinline__ void epi_store_bf(const GemmArgs& g, int m, int n, float v) {
+    const long c = (long)m * g.ldc + n;
     if (EPI == EPI_STORE) {
+        st_b1(g.C, c, v);
+    } else if (EPI == EPI_BIAS) {
+        st_b1(g.C, c, v + g.bias[n]);
+    } else if (EPI == EPI_BIAS_GELU_D) {
+        float gv, gd;
+        pt_gelu_both(v + g.bias[n], gv, gd);
+        st_b1(g.C, c, gd);
+        st_b1(g.C2, (long)m * g.ldc2 + n, gv);
+    } else if (EPI == EPI_MUL) {
+        st_b1(g.C, c, v * ld_b1(g.R, (long)m * g.ldr + n));
+    } else if (EPI == EPI_BIAS_RESID) {
+        st_b1(g.C, c, v + g.bias[n] + g.R[(long)m * g.ldr + n]);
+    }
+}
+
+// one output element through the epilogue
+template <int EPI, bool OB = false>
+__device__ __forceinline__ void epi_store(const GemmArgs& g, int m, int n, float v) {
+    if (OB) {
+        epi_store_bf<EPI>(g, m, n, v);
+    } else if (EPI == EPI_STORE) {
         g.C[(long)m * g.ldc + n] = v;
     } else if (EPI == EPI_BIAS) {
         g.C[(long)m * g.ldc + n] = v + g.bias[n];
@@ -106,7 +144,32 @@ __device__ __forceinline__ void st_g4(float* p, floatx4 v) { *(gfloatx4*)(gfloat
 __device__ __forceinline__ floatx4 ld_v4(const float* p) { return *(const gfloatx4*)(const gfloat*)p; }
 
 template <int EPI>
+__device__ __forceinline__ void epi_store4_bf(const GemmArgs& g, int m, int n, floatx4 v) {
+    const long c = (long)m * g.ldc + n;
+    if (EPI == EPI_STORE) {
+        st_b4(g.C, c, v);
+    } else if (EPI == EPI_BIAS) {
+        st_b4(g.C, c, v + ld_v4(g.bias + n));
+    } else if (EPI == EPI_BIAS_GELU_D) {
+        v += ld_v4(g.bias + n);
+        float gv[4], gd[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) pt_gelu_both(v[i], gv[i], gd[i]);
+        st_b4(g.C, c, floatx4{gd[0], gd[1], gd[2], gd[3]});
+        st_b4(g.C2, (long)m * g.ldc2 + n, floatx4{gv[0], gv[1], gv[2], gv[3]});
+    } else if (EPI == EPI_MUL) {
+        st_b4(g.C, c, v * ld_b4(g.R, (long)m * g.ldr + n));
+    } else if (EPI == EPI_BIAS_RESID) {
+        st_b4(g.C, c, (v + ld_v4(g.bias + n)) + ld_v4(g.R + (long)m * g.ldr + n));
+    }
+}
+
+template <int EPI, bool OB = false>
 __device__ __forceinline__ void epi_store4(const GemmArgs& g, int m, int n, floatx4 v) {
+    if (OB) {
+        epi_store4_bf<EPI>(g, m, n, v);
+        return;
+    }
     float* c = g.C + (long)m * g.ldc + n;
     if (EPI == EPI_STORE) {
         st_g4(c, v);
@@ -175,7 +238,7 @@ template <int EPI> struct EpiStaged {
                                   EPI == EPI_BIAS_GELU_D || EPI == EPI_MUL || EPI == EPI_AXPBY;
 };
 
-template <int EPI>
+template <int EPI, bool OB = false>
 __device__ __forceinline__ void epilogue_staged(const GemmArgs& g, floatx4 (&acc)[4][4], int m0, int n0, int wm,
                                                 int wn, int li, int lq, float* stage, bool vo) {
     const int tid = threadIdx.x;
@@ -195,9 +258,9 @@ __device__ __forceinline__ void epilogue_staged(const GemmArgs& g, floatx4 (&acc
             if (m >= g.M || n >= g.N) continue;
             const floatx4 v = *reinterpret_cast<const floatx4*>(stage + lr * SST + c);
             if (vo && n + 3 < g.N) {
-                epi_store4<EPI>(g, m, n, v);
+                epi_store4<EPI, OB>(g, m, n, v);
             } else {
-                for (int r = 0; r < 4 && n + r < g.N; ++r) epi_store<EPI>(g, m, n + r, v[r]);
+                for (int r = 0; r < 4 && n + r < g.N; ++r) epi_store<EPI, OB>(g, m, n + r, v[r]);
             }
         }
     }
@@ -209,7 +272,7 @@ __device__ __forceinline__ void epilogue_staged(const GemmArgs& g, floatx4 (&acc
 // four consecutive columns of one row per lane, stored (and the bias /
 // residual / pre-activation read) as one 128-bit access when aligned.
 // stage: STAGE_FLOATS of LDS the main loop no longer uses.
-template <int EPI, bool PARTIAL>
+template <int EPI, bool PARTIAL, bool OB = false>
 __device__ __forceinline__ void gemm_epilogue(const GemmArgs& g, floatx4 (&acc)[4][4], int m0, int n0, int wm,
                                               int wn, int li, int lq, long part_stride, float* stage, int bz) {
     if (PARTIAL && g.tail_part) {
@@ -228,8 +291,10 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& g, floatx4 (&acc)[
                                  : (uintptr_t)g.C | (uintptr_t)g.C2 | (uintptr_t)g.R | (uintptr_t)g.bias |
                                        (uintptr_t)((g.ldc | g.ldc2 | g.ldr) * 4);
     const bool vo = (al & 15) == 0;
-    if (!PARTIAL && EpiStaged<EPI>::value) {
-        epilogue_staged<EPI>(g, acc, m0, n0, wm, wn, li, lq, stage, vo);
+    // bf16 outputs always go through the stage: a lane's own four columns
+    // are only 8 B, the staged rows are 256 B contiguous
+    if (!PARTIAL && (EpiStaged<EPI>::value || OB)) {
+        epilogue_staged<EPI, OB>(g, acc, m0, n0, wm, wn, li, lq, stage, vo);
         return;
     }
 #pragma unroll
@@ -241,14 +306,14 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& g, floatx4 (&acc)[
             const int n = n0 + wn + tj * 16 + 4 * lq;
             if (vo && n + 3 < g.N) {
                 if (PARTIAL) st_g4(g.C + zoff + (long)m * g.ldc + n, acc[ti][tj]);
-                else epi_store4<EPI>(g, m, n, acc[ti][tj]);
+                else epi_store4<EPI, OB>(g, m, n, acc[ti][tj]);
                 continue;
             }
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 if (n + r >= g.N) continue;
                 if (PARTIAL) g.C[zoff + (long)m * g.ldc + n + r] = acc[ti][tj][r];
-                else epi_store<EPI>(g, m, n + r, acc[ti][tj][r]);
+                else epi_store<EPI, OB>(g, m, n + r, acc[ti][tj][r]);
             }
         }
     }
@@ -456,9 +521,16 @@ template <bool T> __device__ __forceinline__ int dma_src(int c, int lane, int r0
 // BF: bf16 products — each lane's float4 fragment (k = 4 lq .. 4 lq + 3 of
 // its row, the same k for A and B) is rounded to bf16 (RNE) and one
 // v_mfma_f32_16x16x16_bf16 replaces the four fp32 k-steps.
-template <bool AT, bool BT, int EPI, bool PARTIAL, bool DB, bool BF = false, int NS = DMA_NS>
+// BS: bf16 operands in memory (both k-contiguous).  The caller passes the
+// shapes in float units (K / 2, lda / 2, ldb / 2): the DMA moves bytes, so a
+// 16-float stage row is 32 bf16 k and a 4-float group is 8 — exactly one
+// lane's fragment of v_mfma_f32_16x16x32_bf16 (row li, k = 8 lq .. 8 lq + 7,
+// the same k for A and B).  OB: the epilogue writes bf16 (epi_store_bf).
+template <bool AT, bool BT, int EPI, bool PARTIAL, bool DB, bool BF = false, int NS = DMA_NS, bool BS = false,
+          bool OB = false>
 __device__ __forceinline__ void gemm_dma_tile(const GemmArgs& g0, int k_chunk0, long part_stride, int bx, int bz,
                                               int gz) {
+    static_assert(!BS || (!AT && !BT && !DB && !BF), "bf16 operands: k-contiguous A and B only");
     const GemmArgs g = gemm_shape(g0);
     // a device reduction count splits its own K evenly over the launch's splits
     const int k_chunk = g0.Kdev ? (((g.K + gz - 1) / gz + BK - 1) / BK) * BK : k_chunk0;
@@ -530,6 +602,20 @@ __device__ __forceinline__ void gemm_dma_tile(const GemmArgs& g0, int k_chunk0, 
             if (it + NS - 1 < nk) PT_ISSUE(it + NS - 1)
             const float* Ab = smem + (it % NS) * 2 * TILE;
             const float* Bb = Ab + TILE;
+            if constexpr (BS) {
+                bf16x8 ah[4], bh[4];
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    ah[t] = *reinterpret_cast<const bf16x8*>(Ab + dma_at<false>(wm + t * 16 + li, 4 * lq));
+                    bh[t] = *reinterpret_cast<const bf16x8*>(Bb + dma_at<false>(wn + t * 16 + li, 4 * lq));
+                }
+#pragma unroll
+                for (int ti = 0; ti < 4; ++ti)
+#pragma unroll
+                    for (int tj = 0; tj < 4; ++tj)
+                        acc[ti][tj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bh[tj], ah[ti], acc[ti][tj], 0, 0, 0);
+                continue;
+            }
             float4 af[4], bf[4];
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
@@ -583,7 +669,7 @@ __device__ __forceinline__ void gemm_dma_tile(const GemmArgs& g0, int k_chunk0, 
         }
     }
 
-    gemm_epilogue<EPI, PARTIAL>(g, acc, m0, n0, wm, wn, li, lq, part_stride, smem, bz);
+    gemm_epilogue<EPI, PARTIAL, OB>(g, acc, m0, n0, wm, wn, li, lq, part_stride, smem, bz);
 }
 
 template <bool AT, bool BT, int EPI, bool PARTIAL, bool DB>
@@ -752,6 +838,153 @@ template <bool AT, bool BT, int EPI, bool PARTIAL, bool DB>
 __global__ __launch_bounds__(NT) void gemm_bf16_k16_kernel(const GemmArgs g0, int k_chunk0, long part_stride) {
     gemm_dma_tile<AT, BT, EPI, PARTIAL, DB, true, BF_NS>(g0, k_chunk0, part_stride, blockIdx.x, blockIdx.z,
                                                          gridDim.z);
+}
+
+// ---------------------------------------------------------------- bf16 activations
+// Products whose operands are stored in bf16 (the mixed-precision variant's
+// activations and bf16 copies of the weights), fp32 accumulation.
+//
+// gemm_bs_kernel: C = epi(A B^T), A (M, K) and B (N, K) k-contiguous, on the
+// LDS-DMA pipeline (BS: a 16-float stage row is 32 bf16 k; one
+// v_mfma_f32_16x16x32_bf16 per 16 x 16 tile and stage).  Shapes arrive in
+// float units.  NS stages: a bf16 stage feeds 8x the MFMA work of an fp32
+// one (its 16 KB of DMA per 32 k against 16 k), so more of them are kept in
+// flight.
+template <int EPI, bool OB, int NS>
+__global__ __launch_bounds__(NT) void gemm_bs_kernel(const GemmArgs g0) {
+    gemm_dma_tile<false, false, EPI, false, false, false, NS, true, OB>(g0, g0.K, 0, blockIdx.x, 0, 1);
+}
+
+// gemm_bs_dw_kernel: weight gradients dW (M, N) = sum_k A[k][m] B[k][n] with
+// A = dY (K rows, ld lda) and B = X (K rows, ld ldb) in bf16, K = the rows
+// (split across grid.z in chunks of k_chunk rows, multiples of BKW).  Both
+// operands are m- (n-) contiguous, so a lane's MFMA fragment (8 consecutive
+// k of one column) is strided in memory.  Each thread stages one 8 x 8 block
+// per stage: 8 rows of one 16 B column chunk (16 lanes cover a 256 B row
+// segment), transposed in registers (two 16-bit halves per dword), then
+// written as 8 rows of 16 B into a [column][k] LDS tile; fragment reads are
+// then single 128-bit reads.  LDS tile: row r (a column of the operand),
+// 16 B group q at r * 64 + 8 * (q ^ f(r)), f(r) = (r ^ (r >> 3)) & 7: the
+// 8 lanes of a fragment read (rows r0..r0+7, one group) and of a staging
+// write (rows 8c + i for 8 consecutive c) land on 8 distinct groups.
+// Register double buffering: the global loads of stage it + 1 are in flight
+// while stage it is multiplied.  DB: bias sums sum_k A[k][m] from the staged
+// registers (fixed order: rows within a block, stages, then the 8 blocks).
+constexpr int BKW = 64;
+__device__ __forceinline__ int tw_at(int r, int q) { return r * BKW + 8 * (q ^ ((r ^ (r >> 3)) & 7)); }
+typedef unsigned uintx4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(1))) uintx4 guintx4;
+
+template <bool DB, bool PARTIAL>
+__global__ __launch_bounds__(NT) void gemm_bs_dw_kernel(const GemmArgs g0, int k_chunk0, long part_stride) {
+    const GemmArgs g = gemm_shape(g0);
+    const int gz = gridDim.z, bz = blockIdx.z;
+    const int k_chunk = g0.Kdev ? (((g.K + gz - 1) / gz + BKW - 1) / BKW) * BKW : k_chunk0;
+    __shared__ __align__(16) __bf16 sm[2][2][BM * BKW];   // [buffer][operand][row * 64 + k]
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tn = (g.N + BN - 1) / BN;
+    int tmi, tni;
+    if (!tile_of_range(g, tn, tmi, tni, blockIdx.x)) return;
+    const int m0 = tmi * BM, n0 = tni * BN;
+    const int kbeg = bz * k_chunk;
+    const int kend = min(g.K, kbeg + k_chunk);
+    const int nk = kend > kbeg ? (kend - kbeg + BKW - 1) / BKW : 0;
+    const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
+    const int li = lane & 15, lq = lane >> 4;
+    // staging role: operand op (0: A, 1: B), 8-column chunk cb, 8-row block kb
+    const int op = tid >> 7, cb = tid & 15, kb = (tid >> 4) & 7;
+    const __bf16* src = bfp(op == 0 ? g.A : g.B);
+    const long ld = op == 0 ? g.lda : g.ldb;
+    const int c0 = (op == 0 ? m0 : n0) + 8 * cb;
+    const bool cvalid = c0 < (op == 0 ? g.M : g.N);   // M, N multiples of 8 (host)
+    const bool db_blk = DB && tni == 0;               // uniform over the block
+    floatx4 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+    float dbs[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) dbs[i] = 0.f;
+    unsigned w[8][4];
+    auto load = [&](int it) {
+        const int kr = kbeg + it * BKW + 8 * kb;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            uintx4 v = uintx4{0u, 0u, 0u, 0u};
+            if (cvalid && kr + j < kend) v = *(const guintx4*)(src + (long)(kr + j) * ld + c0);
+            w[j][0] = v[0]; w[j][1] = v[1]; w[j][2] = v[2]; w[j][3] = v[3];
+        }
+    };
+    auto store = [&](int buf) {
+        __bf16* S = &sm[buf][op][0];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            uint4 lo, hi;   // columns 2q (low halves) and 2q + 1 (high halves), rows 0..7
+            lo.x = (w[0][q] & 0xffffu) | (w[1][q] << 16);
+            lo.y = (w[2][q] & 0xffffu) | (w[3][q] << 16);
+            lo.z = (w[4][q] & 0xffffu) | (w[5][q] << 16);
+            lo.w = (w[6][q] & 0xffffu) | (w[7][q] << 16);
+            hi.x = (w[0][q] >> 16) | (w[1][q] & 0xffff0000u);
+            hi.y = (w[2][q] >> 16) | (w[3][q] & 0xffff0000u);
+            hi.z = (w[4][q] >> 16) | (w[5][q] & 0xffff0000u);
+            hi.w = (w[6][q] >> 16) | (w[7][q] & 0xffff0000u);
+            *reinterpret_cast<uint4*>(S + tw_at(8 * cb + 2 * q, kb)) = lo;
+            *reinterpret_cast<uint4*>(S + tw_at(8 * cb + 2 * q + 1, kb)) = hi;
+            if (db_blk && op == 0) {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    dbs[2 * q] += __uint_as_float(w[j][q] << 16);
+                    dbs[2 * q + 1] += __uint_as_float(w[j][q] & 0xffff0000u);
+                }
+            }
+        }
+    };
+    if (nk > 0) {
+        load(0);
+        store(0);
+        __syncthreads();
+        for (int it = 0; it < nk; ++it) {
+            if (it + 1 < nk) load(it + 1);
+            const __bf16* As = &sm[it & 1][0][0];
+            const __bf16* Bs = &sm[it & 1][1][0];
+#pragma unroll
+            for (int kk = 0; kk < BKW / 32; ++kk) {
+                bf16x8 ah[4], bh[4];
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    ah[t] = *reinterpret_cast<const bf16x8*>(As + tw_at(wm + t * 16 + li, 4 * kk + lq));
+                    bh[t] = *reinterpret_cast<const bf16x8*>(Bs + tw_at(wn + t * 16 + li, 4 * kk + lq));
+                }
+#pragma unroll
+                for (int ti = 0; ti < 4; ++ti)
+#pragma unroll
+                    for (int tj = 0; tj < 4; ++tj)
+                        acc[ti][tj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bh[tj], ah[ti], acc[ti][tj], 0, 0, 0);
+            }
+            if (it + 1 < nk) store((it + 1) & 1);
+            __syncthreads();
+        }
+    }
+    if (db_blk) {
+        float* red = reinterpret_cast<float*>(&sm[0][0][0]);   // [8][128]
+        if (op == 0) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) red[kb * BM + 8 * cb + i] = dbs[i];
+        }
+        __syncthreads();
+        if (tid < BM) {
+            float v = 0.f;
+#pragma unroll
+            for (int b = 0; b < 8; ++b) v += red[b * BM + tid];
+            const int m = m0 + tid;
+            if (m < g.M) {
+                if (PARTIAL) g.C[(long)gz * part_stride + (long)bz * g.M + m] = v;
+                else g.dbias[m] = v;
+            }
+        }
+    }
+    gemm_epilogue<EPI_STORE, PARTIAL>(g, acc, m0, n0, wm, wn, li, lq, part_stride, nullptr, bz);
 }
 
 // out[m][n] (=|+=) sum_s part[s][m][n], fixed order over s
@@ -1051,10 +1284,108 @@ static bool dma_ok(const GemmArgs& g) {
            dma_fits(g.b_t ? g.K : g.N, g.b_t ? g.N : g.K, g.ldb);
 }
 
+// ---- bf16 storage (GemmArgs::bs)
+constexpr int BS_NS = 3;
+static bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+template <int EPI, bool OB>
+static void launch_bs(const GemmArgs& f, dim3 grid, hipStream_t s) {
+    hipLaunchKernelGGL((gemm_bs_kernel<EPI, OB, BS_NS>), grid, dim3(NT), 0, s, f);
+}
+
+static int gemm_bs_nt(const GemmArgs& g, hipStream_t s) {
+    PT_REQUIRE(g.K % 8 == 0 && g.lda % 8 == 0 && g.ldb % 8 == 0 && al16(g.A) && al16(g.B),
+               "gemm (bf16 operands): K=%d, lda=%ld, ldb=%ld must be multiples of 8 and A, B 16 B aligned", g.K,
+               g.lda, g.ldb);
+    PT_REQUIRE(g.ldc % 4 == 0 && al16(g.C) && (!g.C2 || (g.ldc2 % 4 == 0 && al16(g.C2))),
+               "gemm (bf16 operands): output leading dimensions must be multiples of 4, 16 B aligned");
+    PT_REQUIRE(!g.Kdev && !g.dbias, "gemm (bf16 operands): no device K or bias sums in C = A B^T");
+    GemmArgs f = g;   // float units for the DMA tile: 2 bf16 per float
+    f.K = g.K / 2;
+    f.lda = g.lda / 2;
+    f.ldb = g.ldb / 2;
+    f.dma = 1;
+    f.tile0 = f.ntiles = f.tail_part = 0;
+    PT_REQUIRE(dma_ok(f), "gemm (bf16 operands): operands exceed 2^31 bytes");
+    const dim3 grid(pt_cdiv(g.M, BM) * pt_cdiv(g.N, BN));
+    const int slot = pt_prof_open(s);
+    const int code = g.epi * 2 + (g.obf ? 1 : 0);
+    switch (code) {
+        case EPI_STORE * 2: launch_bs<EPI_STORE, false>(f, grid, s); break;
+        case EPI_STORE * 2 + 1: launch_bs<EPI_STORE, true>(f, grid, s); break;
+        case EPI_BIAS * 2 + 1: launch_bs<EPI_BIAS, true>(f, grid, s); break;
+        case EPI_BIAS_RESID * 2: launch_bs<EPI_BIAS_RESID, false>(f, grid, s); break;
+        case EPI_BIAS_GELU_D * 2 + 1: launch_bs<EPI_BIAS_GELU_D, true>(f, grid, s); break;
+        case EPI_MUL * 2 + 1: launch_bs<EPI_MUL, true>(f, grid, s); break;
+        default:
+            PT_REQUIRE(false, "gemm (bf16 operands): epilogue %d with %s output not built", g.epi,
+                       g.obf ? "bf16" : "fp32");
+    }
+    pt_prof_close(slot, g_gemm_class, 2.0 * g.M * (double)g.N * g.K, s);
+    PT_LAUNCH_CHECK();
+    return PTCG_OK;
+}
+
+static int gemm_bs_dw(const GemmArgs& g, float* ws, long ws_floats, hipStream_t s) {
+    PT_REQUIRE(g.M % 8 == 0 && g.N % 8 == 0 && g.lda % 8 == 0 && g.ldb % 8 == 0 && al16(g.A) && al16(g.B),
+               "gemm (bf16 weight gradient): M=%d, N=%d, lda=%ld, ldb=%ld must be multiples of 8, A and B 16 B "
+               "aligned", g.M, g.N, g.lda, g.ldb);
+    PT_REQUIRE(g.epi == EPI_STORE && !g.obf && !g.Mdev && g.ldc % 4 == 0 && al16(g.C),
+               "gemm (bf16 weight gradient): fp32 STORE output with ldc a multiple of 4");
+    const int tiles = pt_cdiv(g.M, BM) * pt_cdiv(g.N, BN);
+    const bool db = g.dbias != nullptr;
+    // split the rows so the launch has ~512 blocks, each >= 4 stages of 64 rows
+    int splits = 1;
+    if (tiles < 512 && g.K >= 8 * BKW) {
+        splits = pt_cdiv(512, tiles);
+        const int max_splits = g.K / (4 * BKW);
+        if (splits > max_splits) splits = max_splits;
+        if (splits < 1) splits = 1;
+    }
+    const long part_stride = (long)g.M * g.ldc;
+    const long per_split = part_stride + (db ? g.M : 0);
+    if (splits > 1 && (ws == nullptr || (long)splits * per_split > ws_floats)) {
+        const long fit = ws ? ws_floats / per_split : 0;
+        splits = fit > 1 ? (int)fit : 1;
+    }
+    int k_chunk = g.K;
+    if (splits > 1) {
+        k_chunk = pt_cdiv(pt_cdiv(g.K, splits), BKW) * BKW;
+        splits = pt_cdiv(g.K, k_chunk);
+    }
+    GemmArgs f = g;
+    f.tile0 = f.ntiles = f.tail_part = 0;
+    const dim3 grid(tiles, 1, splits);
+    const int slot = pt_prof_open(s);
+    if (splits > 1) {
+        f.C = ws;
+        if (db) hipLaunchKernelGGL((gemm_bs_dw_kernel<true, true>), grid, dim3(NT), 0, s, f, k_chunk, part_stride);
+        else hipLaunchKernelGGL((gemm_bs_dw_kernel<false, true>), grid, dim3(NT), 0, s, f, k_chunk, part_stride);
+    } else {
+        if (db) hipLaunchKernelGGL((gemm_bs_dw_kernel<true, false>), grid, dim3(NT), 0, s, f, k_chunk, 0L);
+        else hipLaunchKernelGGL((gemm_bs_dw_kernel<false, false>), grid, dim3(NT), 0, s, f, k_chunk, 0L);
+    }
+    pt_prof_close(slot, g_gemm_class, 2.0 * g.M * (double)g.N * g.K, s);
+    PT_LAUNCH_CHECK();
+    if (splits > 1) {
+        const long tot = (long)g.M * (g.N / 4) + (db ? g.M : 0);
+        hipLaunchKernelGGL((splitk_reduce_kernel<false, true>), dim3(pt_cdiv(tot, 256)), dim3(256), 0, s, g.C, g.ldc,
+                           (const float*)ws, part_stride, splits, g.M, g.N, db ? g.dbias : nullptr);
+        PT_LAUNCH_CHECK();
+    }
+    return PTCG_OK;
+}
+
 int pt_gemm(const GemmArgs& g0, float* ws, long ws_floats, hipStream_t s) {
     GemmArgs g = g0;
     PT_REQUIRE(g.M > 0 && g.N > 0 && g.K > 0, "gemm: empty shape %d x %d x %d", g.M, g.N, g.K);
     PT_REQUIRE(g.A && g.B && g.C, "gemm: null operand");
+    if (g.bs) {
+        PT_REQUIRE((!g.a_t && !g.b_t) || (g.a_t && g.b_t),
+                   "gemm (bf16 operands): A and B both k-contiguous or both transposed");
+        return g.a_t ? gemm_bs_dw(g, ws, ws_floats, s) : gemm_bs_nt(g, s);
+    }
+    PT_REQUIRE(!g.obf, "gemm: bf16 output needs bf16 operands");
     // 128-bit loads need the contiguous extent and the leading dimensions to be
     // multiples of 4 floats and 16 B aligned operands; otherwise scalar loads
     const bool vec = (g.a_t ? (g.M % 4 == 0) : (g.K % 4 == 0)) && (g.b_t ? (g.N % 4 == 0) : (g.K % 4 == 0)) &&

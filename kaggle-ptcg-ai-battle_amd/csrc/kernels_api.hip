@@ -81,6 +81,38 @@ extern "C" int ptcg_kernel_gemm_dw_bf16(int rows, int in, int out, const float* 
     return pt_gemm(g, workspace, workspace_floats, (hipStream_t)stream);
 }
 
+extern "C" int ptcg_kernel_gemm_bs(int M, int N, int K, const void* A, int64_t lda, const void* B, int64_t ldb,
+                                   void* C, int64_t ldc, int epi, int out_bf16, const float* bias, const void* R,
+                                   int64_t ldr, void* C2, int64_t ldc2, void* stream) {
+    PT_REQUIRE(A && B && C, "kernel_gemm_bs: null operand");
+    PT_REQUIRE(!((epi == EPI_BIAS || epi == EPI_BIAS_RESID || epi == EPI_BIAS_GELU_D) && !bias),
+               "kernel_gemm_bs: epilogue %d needs bias", epi);
+    PT_REQUIRE(!((epi == EPI_BIAS_RESID || epi == EPI_MUL) && !R), "kernel_gemm_bs: epilogue %d needs R", epi);
+    PT_REQUIRE(!(epi == EPI_BIAS_GELU_D && !C2), "kernel_gemm_bs: epilogue %d needs C2", epi);
+    GemmArgs g{};
+    g.M = M; g.N = N; g.K = K;
+    g.A = (const float*)A; g.lda = lda;
+    g.B = (const float*)B; g.ldb = ldb;
+    g.C = (float*)C; g.ldc = ldc; g.epi = epi;
+    g.bias = bias; g.R = (const float*)R; g.ldr = ldr; g.C2 = (float*)C2; g.ldc2 = ldc2;
+    g.prec = 1; g.bs = 1; g.obf = out_bf16 != 0;
+    return pt_gemm(g, nullptr, 0, (hipStream_t)stream);
+}
+
+extern "C" int ptcg_kernel_gemm_dw_bs(int rows, int in, int out, const void* dY, int64_t lddy, const void* X,
+                                      int64_t ldx, float* dW, float* db, float* workspace, int64_t workspace_floats,
+                                      void* stream) {
+    PT_REQUIRE(dY && X && dW, "kernel_gemm_dw_bs: null operand");
+    GemmArgs g{};
+    g.M = out; g.N = in; g.K = rows;
+    g.A = (const float*)dY; g.lda = lddy; g.a_t = 1;
+    g.B = (const float*)X; g.ldb = ldx; g.b_t = 1;
+    g.C = dW; g.ldc = in; g.epi = EPI_STORE;
+    g.dbias = db;
+    g.prec = 1; g.bs = 1;
+    return pt_gemm(g, workspace, workspace_floats, (hipStream_t)stream);
+}
+
 extern "C" int ptcg_kernel_colsum(const float* X, int64_t ldx, int M, int N, float* out,
                                   float* workspace, int64_t workspace_floats, void* stream) {
     PT_REQUIRE(X && out, "kernel_colsum: null buffer");

@@ -22,8 +22,16 @@ constexpr int LN_FWD_RPW = 1;        // forward rows per wave, loaded together
 constexpr int LN_BWD_WPB = 8;        // backward waves per workgroup (rows of d <= 256)
 constexpr int LN_BWD_RPI = 1;        // backward rows per wave per iteration, loaded together
 
+typedef __bf16 lnbf16x4 __attribute__((ext_vector_type(4)));
+// four floats to bf16 (round to nearest even) at element i of a bf16 array
+__device__ __forceinline__ void st_bf16x4(float* base, long i, float4 o) {
+    *reinterpret_cast<lnbf16x4*>(reinterpret_cast<__bf16*>(base) + i) =
+        lnbf16x4{(__bf16)o.x, (__bf16)o.y, (__bf16)o.z, (__bf16)o.w};
+}
+
 // rows blockIdx.x * 4 * RPW + wave + 4 r, r < RPW
-template <int VPL, int RPW>
+// YB: y is stored in bf16 (the mixed-precision variant's GEMM operand)
+template <int VPL, int RPW, bool YB = false>
 __global__ __launch_bounds__(256) void ln_fwd_kernel(const float* __restrict__ x, long ldx,
         const float* __restrict__ w, const float* __restrict__ b, float* __restrict__ y, long ldy,
         float* __restrict__ mean, float* __restrict__ rstd, int rows, int D,
@@ -67,7 +75,6 @@ __global__ __launch_bounds__(256) void ln_fwd_kernel(const float* __restrict__ x
             mean[row] = mu;
             rstd[row] = rs;
         }
-        float* yr = y + (long)row * ldy;
 #pragma unroll
         for (int c = 0; c < VPL; ++c) {
             const int col = (lane + 64 * c) * 4;
@@ -79,7 +86,8 @@ __global__ __launch_bounds__(256) void ln_fwd_kernel(const float* __restrict__ x
                 o.y = (v[r][c].y - mu) * rs * ww.y + bb.y;
                 o.z = (v[r][c].z - mu) * rs * ww.z + bb.z;
                 o.w = (v[r][c].w - mu) * rs * ww.w + bb.w;
-                *reinterpret_cast<float4*>(yr + col) = o;
+                if (YB) st_bf16x4(y, (long)row * ldy + col, o);
+                else *reinterpret_cast<float4*>(y + (long)row * ldy + col) = o;
             }
         }
     }
@@ -87,6 +95,8 @@ __global__ __launch_bounds__(256) void ln_fwd_kernel(const float* __restrict__ x
 
 // dx = rs*(g - mean(g) - xh*mean(g*xh)) [+ dres], g = dy*w, xh = (x-mu)*rs.
 // part[blk][0..D) = sum dy*xh, part[blk][D..2D) = sum dy over the block's rows.
+// dxh (nullable): a bf16 copy of dx at the same leading dimension (the next
+// products' operand in the mixed-precision variant).
 // Wave w of workgroup b takes rows b*WPB + w + k*S (S = gridDim.x*WPB), RPI
 // consecutive k at a time.
 template <int VPL, int WPB, int RPI>
@@ -95,7 +105,7 @@ __global__ __launch_bounds__(64 * WPB) void ln_bwd_kernel(const float* __restric
         const float* __restrict__ mean, const float* __restrict__ rstd,
         const float* __restrict__ dres, long ldres, float* __restrict__ dx, long lddx,
         float* __restrict__ part, int rows, int D,
-        const int* __restrict__ rows_dev) {
+        const int* __restrict__ rows_dev, float* __restrict__ dxh) {
     if (rows_dev) rows = min(rows, *rows_dev);   // device row count (compact layouts)
     __shared__ float4 sh_w[WPB][VPL * 64];
     __shared__ float4 sh_b[WPB][VPL * 64];
@@ -169,6 +179,7 @@ __global__ __launch_bounds__(64 * WPB) void ln_bwd_kernel(const float* __restric
                         o.x += rv.x; o.y += rv.y; o.z += rv.z; o.w += rv.w;
                     }
                     *reinterpret_cast<float4*>(dxr + col) = o;
+                    if (dxh) st_bf16x4(dxh, (long)row * lddx + col, o);
                 }
             }
         }
@@ -311,10 +322,20 @@ bool ln_vec_ok(const void* p, long ld, int D) { return D % 4 == 0 && ld % 4 == 0
 }  // namespace
 
 int pt_ln_fwd(const float* x, long ldx, const float* w, const float* b, float* y, long ldy,
-              float* mean, float* rstd, int rows, int D, hipStream_t s, const int* rows_dev) {
+              float* mean, float* rstd, int rows, int D, hipStream_t s, const int* rows_dev, int ybf) {
     PT_REQUIRE(D >= 1 && D <= 1024, "layernorm: D=%d unsupported", D);
+    const bool vec = ln_vec_ok(x, ldx, D) && ln_vec_ok(y, ldy, D) && ln_vec_ok(w, 0, D) && ln_vec_ok(b, 0, D);
+    if (ybf) {
+        PT_REQUIRE(vec && D <= 256, "layernorm: bf16 output needs D <= 256, multiples of 4, 16 B aligned rows");
+        const int slot = pt_prof_open(s);
+        hipLaunchKernelGGL((ln_fwd_kernel<1, LN_FWD_RPW, true>), dim3(pt_cdiv(rows, 4 * LN_FWD_RPW)), dim3(256), 0,
+                           s, x, ldx, w, b, y, ldy, mean, rstd, rows, D, rows_dev);
+        PT_LAUNCH_CHECK();
+        pt_prof_close(slot, PROF_LN_FWD, (double)rows * (6.0 * D + 8.0) + 8.0 * D, s);
+        return PTCG_OK;
+    }
     const int slot = pt_prof_open(s);
-    if (!(ln_vec_ok(x, ldx, D) && ln_vec_ok(y, ldy, D) && ln_vec_ok(w, 0, D) && ln_vec_ok(b, 0, D))) {
+    if (!vec) {
         hipLaunchKernelGGL(ln_fwd_scalar_kernel, dim3(pt_cdiv(rows, 4)), dim3(256), 0, s, x, ldx, w, b, y, ldy,
                            mean, rstd, rows, D, rows_dev);
     } else {
@@ -338,10 +359,11 @@ int pt_ln_fwd(const float* x, long ldx, const float* w, const float* b, float* y
 int pt_ln_bwd(const float* dy, long lddy, const float* x, long ldx, const float* w,
               const float* mean, const float* rstd, const float* dres, long ldres, float* dx,
               long lddx, float* dw, float* db, int rows, int D, float* ws, long ws_floats,
-              hipStream_t s, const int* rows_dev) {
+              hipStream_t s, const int* rows_dev, float* dxh) {
     PT_REQUIRE(D >= 1 && D <= 1024, "layernorm bwd: D=%d unsupported", D);
     const bool vec = ln_vec_ok(dy, lddy, D) && ln_vec_ok(x, ldx, D) && ln_vec_ok(w, 0, D) &&
                      ln_vec_ok(dx, lddx, D) && (dres == nullptr || ln_vec_ok(dres, ldres, D));
+    PT_REQUIRE(!dxh || (vec && ((uintptr_t)dxh & 15) == 0), "layernorm bwd: bf16 copy needs the vector layout");
     // 8-wave workgroups for the d <= 256 rows (16 KB of fold buffers);
     // 4-wave ones for wider rows and the scalar kernel
     const int wpb = (vec && D <= 256) ? LN_BWD_WPB : 4;
@@ -356,16 +378,17 @@ int pt_ln_bwd(const float* dy, long lddy, const float* x, long ldx, const float*
                            lddx, ws, rows, D, rows_dev);
     else if (D <= 256)
         hipLaunchKernelGGL((ln_bwd_kernel<1, LN_BWD_WPB, LN_BWD_RPI>), grid, blk, 0, s, dy, lddy, x, ldx, w, mean,
-                           rstd, dres, ldres, dx, lddx, ws, rows, D, rows_dev);
+                           rstd, dres, ldres, dx, lddx, ws, rows, D, rows_dev, dxh);
     else if (D <= 512)
         hipLaunchKernelGGL((ln_bwd_kernel<2, 4, LN_BWD_RPI>), grid, blk, 0, s, dy, lddy, x, ldx, w, mean, rstd, dres,
-                           ldres, dx, lddx, ws, rows, D, rows_dev);
+                           ldres, dx, lddx, ws, rows, D, rows_dev, dxh);
     else
         hipLaunchKernelGGL((ln_bwd_kernel<4, 4, LN_BWD_RPI>), grid, blk, 0, s, dy, lddy, x, ldx, w, mean, rstd, dres,
-                           ldres, dx, lddx, ws, rows, D, rows_dev);
+                           ldres, dx, lddx, ws, rows, D, rows_dev, dxh);
     PT_LAUNCH_CHECK();
-    // read dy, x, mean, rstd (and dres), write dx; read w, write dW, dB
-    pt_prof_close(slot, PROF_LN_BWD, (double)rows * (12.0 * D + 8.0 + (dres ? 4.0 * D : 0.0)) + 12.0 * D, s);
+    // read dy, x, mean, rstd (and dres), write dx (and its bf16 copy); read w, write dW, dB
+    pt_prof_close(slot, PROF_LN_BWD,
+                  (double)rows * (12.0 * D + 8.0 + (dres ? 4.0 * D : 0.0) + (dxh ? 2.0 * D : 0.0)) + 12.0 * D, s);
     if (dw && db)
         return pt_colsum2(ws, 2 * D, blocks, 2 * D, D, dw, db, ws + (long)blocks * 2 * D,
                           ws_floats - (long)blocks * 2 * D, s);

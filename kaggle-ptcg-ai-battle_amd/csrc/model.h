@@ -37,17 +37,20 @@ int pt_param_table(const PtcgDims& d, ParamDef* out, int cap);   // returns coun
 
 // kernels (layernorm.hip, attention.hip, ppo.hip, adam.hip, gather.hip)
 // rows_dev (nullable): device row count <= rows (the launch covers rows)
+// ybf: y stored in bf16 (ldy in bf16 elements); dxh (nullable): a bf16 copy of dx
 int pt_ln_fwd(const float* x, long ldx, const float* w, const float* b, float* y, long ldy,
-              float* mean, float* rstd, int rows, int D, hipStream_t s, const int* rows_dev = nullptr);
+              float* mean, float* rstd, int rows, int D, hipStream_t s, const int* rows_dev = nullptr,
+              int ybf = 0);
 int pt_ln_bwd(const float* dy, long lddy, const float* x, long ldx, const float* w,
               const float* mean, const float* rstd, const float* dres, long ldres, float* dx,
               long lddx, float* dw, float* db, int rows, int D, float* ws, long ws_floats,
-              hipStream_t s, const int* rows_dev = nullptr);
+              hipStream_t s, const int* rows_dev = nullptr, float* dxh = nullptr);
 int pt_attn_supported(int L, int DH);
 // coff (nullable): sample n's rows are [coff[n], coff[n+1]) (length <= L);
 // else rows n*L .. n*L+L-1.  lse is laid out (N, H, L) either way.
 // prec 1: the products (S, P.V and the backward's) on bf16 MFMA with
-// operands rounded to bf16, softmax and accumulation in fp32.
+// operands rounded to bf16, softmax and accumulation in fp32; prec 2: the
+// same with qkv, ctx, dctx and dqkv stored in bf16 (pointers reinterpreted).
 int pt_attn_fwd(const float* qkv, const float* keep, float* ctx, float* lse, int N, int L, int H,
                 int DH, hipStream_t s, const int* coff = nullptr, int prec = 0);
 int pt_attn_bwd(const float* qkv, const float* keep, const float* ctx, const float* lse,
@@ -78,6 +81,16 @@ long pt_adam_ws_floats();
 int pt_adam_step(float* w, float* g, float* m, float* v, long n, const double* lr, double b1, double b2,
                  double eps, float max_norm, const float* gate, int32_t* step, float* norm_out,
                  float* ws, hipStream_t s);
+
+// ---- bf16 copies (bf16copy.hip)
+// One weight matrix W (rows = out, cols = in): dst = bf16 W, dstT = bf16 W^T
+// (cols x rows).  tile0 is set by pt_bf16_weights.
+struct BfWeight { const float* src; __bf16* dst; __bf16* dstT; int rows, cols, tile0; };
+constexpr int BF_MAX_W = 24;
+struct BfWeightSet { int n = 0; BfWeight m[BF_MAX_W]; };
+int pt_bf16_weights(BfWeightSet& ws, hipStream_t s);
+// n floats of src to bf16 at dst (reinterpreted as __bf16)
+int pt_to_bf16(const float* src, float* dst, long n, hipStream_t s);
 
 // ---- order-independent table scatters (detsum.hip)
 // A site: the tables one point of the backward scatters into and the

@@ -36,6 +36,11 @@ struct BlockP {
 struct BlockA {
     float *ln1, *mu1, *rs1, *qkv, *ctx, *lse, *xmid, *ln2, *mu2, *rs2, *ffp, *ffa;
 };
+// bf16 variant: bf16 copies of a block's weight matrices, W (out, in) for the
+// forward products and W^T (in, out) for the backward's dX
+struct BlockW {
+    __bf16 *qkv, *qkvT, *proj, *projT, *f1, *f1T, *f2, *f2T;
+};
 
 struct PtcgModel {
     PtcgDims dm;
@@ -108,6 +113,14 @@ struct PtcgModel {
     // oracle critic / aux activations and scratch
     float *otok_in, *otok, *ckeep, *xc, *xco, *ov_in, *ov1, *ov1a, *bv, *hand_lin, *prize_all;
     BlockA cba;
+    // bf16 variant (prec 1): the blocks keep ln1 / qkv / ctx / ln2 / ffp / ffa
+    // and the backward's dffn / dctx / dqkv in bf16 (the residual stream, the
+    // LayerNorm statistics and the parameter gradients stay fp32); weight
+    // copies refreshed every forward; dAh / dCh: bf16 copies of the residual
+    // gradients dA / dC (written by the LayerNorm backward that produces them)
+    std::vector<BlockW> bw;
+    BlockW cbw{};
+    float *dAh = nullptr, *dCh = nullptr;
     float *d_hand, *d_prize, *d_blind, *dxc, *dxc2, *dotok, *dotok_in, *dov1, *dovin;
     int* aux_cnt;
     // order-independent table scatters: fixed-point accumulators (zero
@@ -176,6 +189,59 @@ static int ldw_(PtcgModel* m, const float* dY, long lddy, const float* X, long l
     return pt_gemm(g, m->ws, m->ws_floats, s);
 }
 
+// bf16-operand products (GemmArgs::bs) of the bf16 variant's blocks:
+// Y = epi(X Wb^T), X (rows, in) and Wb (out, in) bf16; obf: Y (and Y2) bf16;
+// R at leading dimension out (bf16 for EPI_MUL, fp32 for EPI_BIAS_RESID).
+// The backward's dX = dY W is the same product with Wb = W^T (in, out).
+static int blin(const PtcgModel* m, const float* X, int in, const __bf16* Wb, const float* b, float* Y, int out,
+                int rows, int epi, bool obf, const float* R, float* Y2, hipStream_t s, const int* Mdev) {
+    GemmArgs g{};
+    g.prec = 1; g.bs = 1; g.obf = obf ? 1 : 0;
+    g.Mdev = Mdev;
+    g.M = rows; g.N = out; g.K = in;
+    g.A = X; g.lda = in;
+    g.B = reinterpret_cast<const float*>(Wb); g.ldb = in;
+    g.C = Y; g.ldc = out;
+    g.bias = b; g.R = R; g.ldr = out; g.C2 = Y2; g.ldc2 = out;
+    g.epi = epi;
+    return pt_gemm(g, m->ws, m->ws_floats, s);
+}
+// dW (out, in) = dY^T X, db = column sums of dY, with dY (rows, out) and X (rows, in) bf16
+static int bldw(PtcgModel* m, const float* dY, int out, const float* X, int in, float* dW, float* db, int rows,
+                hipStream_t s, const int* Kdev) {
+    GemmArgs g{};
+    g.prec = 1; g.bs = 1;
+    g.Kdev = Kdev;
+    g.M = out; g.N = in; g.K = rows;
+    g.A = dY; g.lda = out; g.a_t = 1;
+    g.B = X; g.ldb = in; g.b_t = 1;
+    g.C = dW; g.ldc = in; g.epi = EPI_STORE;
+    g.dbias = db;
+    return pt_gemm(g, m->ws, m->ws_floats, s);
+}
+
+// refresh the blocks' bf16 weight copies from the fp32 masters
+static int bf16_refresh(PtcgModel* m, hipStream_t s) {
+    BfWeightSet ws;
+    const int D = m->dm.d, F = m->dm.ffn, nl = (int)m->blk.size();
+    const int nb = nl + (m->dm.critic == 1 ? 1 : 0);
+    for (int i = 0; i < nb; ++i) {
+        const BlockP& p = i < nl ? m->blk[i] : m->cblk;
+        const BlockW& w = i < nl ? m->bw[i] : m->cbw;
+        const BfWeight mats[4] = {{p.qkvw, w.qkv, w.qkvT, 3 * D, D, 0}, {p.projw, w.proj, w.projT, D, D, 0},
+                                  {p.f1w, w.f1, w.f1T, F, D, 0}, {p.f2w, w.f2, w.f2T, D, F, 0}};
+        for (const BfWeight& bwm : mats) {
+            if (ws.n == BF_MAX_W) {
+                PT_TRY(pt_bf16_weights(ws, s));
+                ws.n = 0;
+            }
+            ws.m[ws.n++] = bwm;
+        }
+    }
+    if (ws.n) PT_TRY(pt_bf16_weights(ws, s));
+    return PTCG_OK;
+}
+
 struct Carver {
     char* base; size_t off = 0;
     float* take(size_t floats) {
@@ -184,6 +250,7 @@ struct Carver {
         off += floats * sizeof(float);
         return p;
     }
+    __bf16* take_bf(size_t n) { return reinterpret_cast<__bf16*>(take((n + 1) / 2)); }
 };
 
 // ------------------------------------------------------------ lifecycle
@@ -370,6 +437,9 @@ extern "C" int ptcg_model_set_static(PtcgModel* m, const float* card_static, con
 
 extern "C" int ptcg_model_set_precision(PtcgModel* m, int prec) {
     PT_REQUIRE(m && (prec == 0 || prec == 1), "model_set_precision: precision must be 0 (fp32) or 1 (bf16)");
+    PT_REQUIRE(prec == 0 || (m->dm.d % 8 == 0 && m->dm.ffn % 8 == 0 && m->dm.d <= 256),
+               "model_set_precision: bf16 activations need d and ffn multiples of 8 and d <= 256 (d=%d, ffn=%d)",
+               m->dm.d, m->dm.ffn);
     m->prec = prec;
     return PTCG_OK;
 }
@@ -387,6 +457,14 @@ static void carve_block(Carver& c, BlockA& a, long NL, const PtcgDims& d) {
     a.xmid = c.take(NL * D);
     a.ln2 = c.take(NL * D); a.mu2 = c.take(NL); a.rs2 = c.take(NL);
     a.ffp = c.take(NL * d.ffn); a.ffa = c.take(NL * d.ffn);
+}
+
+static void carve_bw(Carver& c, BlockW& w, const PtcgDims& d) {
+    const long D = d.d, F = d.ffn;
+    w.qkv = c.take_bf(3 * D * D); w.qkvT = c.take_bf(3 * D * D);
+    w.proj = c.take_bf(D * D); w.projT = c.take_bf(D * D);
+    w.f1 = c.take_bf(F * D); w.f1T = c.take_bf(F * D);
+    w.f2 = c.take_bf(D * F); w.f2T = c.take_bf(D * F);
 }
 
 static size_t carve(PtcgModel* m, char* base) {
@@ -452,6 +530,9 @@ static size_t carve(PtcgModel* m, char* base) {
             m->aux_cnt = reinterpret_cast<int*>(c.take(64));
         }
     }
+    m->bw.resize(d.layers);
+    for (auto& w : m->bw) carve_bw(c, w, d);
+    if (crit) carve_bw(c, m->cbw, d);
     if (!train) {   // forward GEMMs use the workspace for balanced tail tiles only
         m->ws_floats = 4L << 20;
         m->ws = c.take(m->ws_floats);
@@ -470,6 +551,8 @@ static size_t carve(PtcgModel* m, char* base) {
     m->ddec = c.take(N * x.dec_in);
     m->dtokp = c.take(tok_rows * D); m->dtokcat = c.take(tok_rows * x.tok_in);
     m->dbc = c.take(N * D);
+    m->dAh = reinterpret_cast<float*>(c.take_bf(NLmax * D));
+    m->dCh = reinterpret_cast<float*>(c.take_bf(NLmax * D));
     // table-scatter accumulators: the card, attack and skill tables plus the
     // small ones (zone, owner, option type, select type, context) of one site
     m->det.acc_len = (long)d.n_cards * d.d_c + (long)d.n_attacks * d.d_a + (long)d.n_skills * d.d_c + 4096;
@@ -540,11 +623,23 @@ float* pt_model_ws(const PtcgModel* m, long* floats) { *floats = m->ws_floats; r
 // ------------------------------------------------------------ forward
 // rows / Tr / coff of a compact layout: launch rows, device row count
 // (nullable) and per-sample row offsets (rows 0, coff null: N * L rows)
+// bw (bf16 variant): the block's bf16 weight copies; the block's activations
+// are then stored in bf16 (the residual stream xin / xmid / xout stays fp32)
 static int block_fwd(PtcgModel* m, const BlockP& w, const BlockA& a, int L, const float* keep, const float* xin,
                      float* xout, hipStream_t s, int rows = 0, const int* Tr = nullptr,
-                     const int* coff = nullptr) {
+                     const int* coff = nullptr, const BlockW* bw = nullptr) {
     const PtcgDims& d = m->dm;
     const int NL = rows ? rows : m->N * L, D = d.d;
+    if (bw) {
+        PT_TRY(pt_ln_fwd(xin, D, w.ln1w, w.ln1b, a.ln1, D, a.mu1, a.rs1, NL, D, s, Tr, 1));
+        PT_TRY(blin(m, a.ln1, D, bw->qkv, w.qkvb, a.qkv, 3 * D, NL, EPI_BIAS, true, nullptr, nullptr, s, Tr));
+        PT_TRY(pt_attn_fwd(a.qkv, keep, a.ctx, a.lse, m->N, L, d.heads, m->dx.dh, s, coff, 2));
+        PT_TRY(blin(m, a.ctx, D, bw->proj, w.projb, a.xmid, D, NL, EPI_BIAS_RESID, false, xin, nullptr, s, Tr));
+        PT_TRY(pt_ln_fwd(a.xmid, D, w.ln2w, w.ln2b, a.ln2, D, a.mu2, a.rs2, NL, D, s, Tr, 1));
+        PT_TRY(blin(m, a.ln2, D, bw->f1, w.f1b, a.ffp, d.ffn, NL, EPI_BIAS_GELU_D, true, nullptr, a.ffa, s, Tr));
+        PT_TRY(blin(m, a.ffa, d.ffn, bw->f2, w.f2b, xout, D, NL, EPI_BIAS_RESID, false, a.xmid, nullptr, s, Tr));
+        return PTCG_OK;
+    }
     PT_TRY(pt_ln_fwd(xin, D, w.ln1w, w.ln1b, a.ln1, D, a.mu1, a.rs1, NL, D, s, Tr));
     PT_TRY(linf(m, a.ln1, w.qkvw, w.qkvb, a.qkv, NL, D, 3 * D, EPI_BIAS, nullptr, nullptr, s, Tr));
     PT_TRY(pt_attn_fwd(a.qkv, keep, a.ctx, a.lse, m->N, L, d.heads, m->dx.dh, s, coff, m->prec));
@@ -645,9 +740,11 @@ extern "C" int ptcg_model_forward(PtcgModel* m, const float* obs, const int32_t*
     PT_TRY(lin(m, m->gd, x.bcast_in, m->bc_w, m->bc_b, m->bc, D, N, x.bcast_in, D, EPI_BIAS, nullptr, 0, nullptr, 0, s));
     PT_TRY(pt_x0_fwd(c, m->tokp, m->bc, m->readout, m->x[0], m->keep, s));
     const bool tr = m->train;
+    const bool b16 = m->prec == 1;
+    if (b16) PT_TRY(bf16_refresh(m, s));
     for (int i = 0; i < d.layers; ++i)
         PT_TRY(block_fwd(m, m->blk[i], m->ba[tr ? i : 0], x.l_seq, m->keep, m->x[tr ? i : i % 2],
-                         m->x[tr ? i + 1 : (i + 1) % 2], s, m->rows, Td, coff));
+                         m->x[tr ? i + 1 : (i + 1) % 2], s, m->rows, Td, coff, b16 ? &m->bw[i] : nullptr));
     const int NL = N * x.l_seq;
     PT_TRY(pt_ln_fwd(m->x[tr ? d.layers : d.layers % 2], D, m->lnf_w, m->lnf_b, m->h, D, m->lnf_mu, m->lnf_rs,
                      m->rows, D, s, Td));
@@ -687,7 +784,8 @@ extern "C" int ptcg_model_forward(PtcgModel* m, const float* obs, const int32_t*
         PT_TRY(pt_otok_in(c, m->card, m->keep, m->otok_in, m->ckeep, s));
         PT_TRY(linf(m, m->otok_in, m->op_w, m->op_b, m->otok, NK, x.orc_in, D, EPI_BIAS, nullptr, nullptr, s));
         PT_TRY(pt_xc_fwd(m->cread, m->h, m->otok, m->xc, N, x.l_seq, x.n_orc, D, s));
-        PT_TRY(block_fwd(m, m->cblk, m->cba, x.l_crit, m->ckeep, m->xc, m->xco, s));
+        PT_TRY(block_fwd(m, m->cblk, m->cba, x.l_crit, m->ckeep, m->xc, m->xco, s, 0, nullptr, nullptr,
+                         b16 ? &m->cbw : nullptr));
         PT_TRY(pt_val_in_fwd(c, m->xco, m->gd, m->ov_in, s, x.l_crit));
         PT_TRY(linf(m, m->ov_in, m->ov1_w, m->ov1_b, m->ov1, N, x.val_in, PT_VAL_H, EPI_BIAS_GELU_D, nullptr, m->ov1a, s));
         PT_TRY(pt_head_dot(m->ov1a, N, PT_VAL_H, m->ov2_w, m->ov2_b, m->out, 1, NO + 1, NO, s));
@@ -698,11 +796,30 @@ extern "C" int ptcg_model_forward(PtcgModel* m, const float* obs, const int32_t*
 
 // ------------------------------------------------------------ backward
 // dA holds d(x_out) on entry and d(x_in) on exit; dC is scratch for d(x_mid)
+// bw (bf16 variant): m->dAh holds dA in bf16 on entry and holds the new dA in
+// bf16 on exit (m->dCh likewise for dC)
 static int block_bwd(PtcgModel* m, const BlockP& w, const BlockA& a, int L, const float* keep, const float* xin,
                      float* dA, float* dC, hipStream_t s, int rows = 0, const int* Tr = nullptr,
-                     const int* coff = nullptr) {
+                     const int* coff = nullptr, const BlockW* bw = nullptr) {
     const PtcgDims& d = m->dm;
     const int NL = rows ? rows : m->N * L, D = d.d;
+    if (bw) {
+        PT_TRY(bldw(m, m->dAh, D, a.ffa, d.ffn, m->G(w.f2w), m->G(w.f2b), NL, s, Tr));
+        PT_TRY(blin(m, m->dAh, D, bw->f2T, nullptr, m->dffn, d.ffn, NL, EPI_MUL, true, a.ffp, nullptr, s, Tr));
+        PT_TRY(bldw(m, m->dffn, d.ffn, a.ln2, D, m->G(w.f1w), m->G(w.f1b), NL, s, Tr));
+        PT_TRY(blin(m, m->dffn, d.ffn, bw->f1T, nullptr, m->dln, D, NL, EPI_STORE, false, nullptr, nullptr, s, Tr));
+        PT_TRY(pt_ln_bwd(m->dln, D, a.xmid, D, w.ln2w, a.mu2, a.rs2, dA, D, dC, D, m->G(w.ln2w),
+                         m->G(w.ln2b), NL, D, m->ws, m->ws_floats, s, Tr, m->dCh));
+        PT_TRY(bldw(m, m->dCh, D, a.ctx, D, m->G(w.projw), m->G(w.projb), NL, s, Tr));
+        PT_TRY(blin(m, m->dCh, D, bw->projT, nullptr, m->dctx, D, NL, EPI_STORE, true, nullptr, nullptr, s, Tr));
+        PT_TRY(pt_attn_bwd(a.qkv, keep, a.ctx, a.lse, m->dctx, m->dqkv, m->N, L, d.heads, m->dx.dh, s, coff, 2));
+        PT_TRY(bldw(m, m->dqkv, 3 * D, a.ln1, D, m->G(w.qkvw), m->G(w.qkvb), NL, s, Tr));
+        PT_TRY(blin(m, m->dqkv, 3 * D, bw->qkvT, nullptr, m->dln, D, NL, EPI_STORE, false, nullptr, nullptr, s,
+                    Tr));
+        PT_TRY(pt_ln_bwd(m->dln, D, xin, D, w.ln1w, a.mu1, a.rs1, dC, D, dA, D, m->G(w.ln1w),
+                         m->G(w.ln1b), NL, D, m->ws, m->ws_floats, s, Tr, m->dAh));
+        return PTCG_OK;
+    }
     PT_TRY(ldw_(m, dA, D, a.ffa, d.ffn, m->G(w.f2w), m->G(w.f2b), NL, d.ffn, D, s, Tr));
     PT_TRY(ldx_(m, dA, D, w.f2w, m->dffn, d.ffn, NL, d.ffn, D, EPI_MUL, a.ffp, d.ffn, s, Tr));
     PT_TRY(ldw_(m, m->dffn, d.ffn, a.ln2, D, m->G(w.f1w), m->G(w.f1b), NL, D, d.ffn, s, Tr));
@@ -790,7 +907,10 @@ static int critic_bwd(PtcgModel* m, const GatherCtx& c, const float* grad, hipSt
     PT_TRY(ldx_(m, m->dov1, PT_VAL_H, m->ov1_w, m->dovin, x.val_in, N, x.val_in, PT_VAL_H, EPI_STORE, nullptr, 0, s));
     PT_TRY(pt_fill_zero(m->dxc, (long)N * x.l_crit * D, s));
     PT_TRY(pt_val_in_bwd(c, m->dovin, m->dxc, m->dgd, s, x.l_crit));
-    PT_TRY(block_bwd(m, m->cblk, m->cba, x.l_crit, m->ckeep, m->xc, m->dxc, m->dxc2, s));
+    const bool b16 = m->prec == 1;
+    if (b16) PT_TRY(pt_to_bf16(m->dxc, m->dAh, (long)N * x.l_crit * D, s));
+    PT_TRY(block_bwd(m, m->cblk, m->cba, x.l_crit, m->ckeep, m->xc, m->dxc, m->dxc2, s, 0, nullptr, nullptr,
+                     b16 ? &m->cbw : nullptr));
     PT_TRY(pt_colsum(m->dxc, (long)x.l_crit * D, N, D, m->G(m->cread), m->ws, m->ws_floats, s));
     PT_TRY(pt_xc_bwd(m->dxc, m->dxa, m->dotok, N, x.l_seq, x.n_orc, D, s));
     PT_TRY(ldw_(m, m->dotok, D, m->otok_in, x.orc_in, m->G(m->op_w), m->G(m->op_b), NK, x.orc_in, D, s));
@@ -891,10 +1011,12 @@ extern "C" int ptcg_model_backward(PtcgModel* m, const float* grad, void* stream
     }
 
     // final LayerNorm, then the trunk in reverse (d_x in dxb, scratch dxa)
+    const bool b16 = m->prec == 1;   // bf16 variant: the LayerNorm also writes dx's bf16 copy (dAh)
     PT_TRY(pt_ln_bwd(m->dxa, D, m->x[d.layers], D, m->lnf_w, m->lnf_mu, m->lnf_rs, nullptr, 0, m->dxb, D,
-                     m->G(m->lnf_w), m->G(m->lnf_b), rows, D, m->ws, m->ws_floats, s, Td));
+                     m->G(m->lnf_w), m->G(m->lnf_b), rows, D, m->ws, m->ws_floats, s, Td, b16 ? m->dAh : nullptr));
     for (int i = d.layers - 1; i >= 0; --i)
-        PT_TRY(block_bwd(m, m->blk[i], m->ba[i], x.l_seq, m->keep, m->x[i], m->dxb, m->dxa, s, rows, Td, coff));
+        PT_TRY(block_bwd(m, m->blk[i], m->ba[i], x.l_seq, m->keep, m->x[i], m->dxb, m->dxa, s, rows, Td, coff,
+                         b16 ? &m->bw[i] : nullptr));
 
     // trunk input: readout / token projection / broadcast
     PT_TRY(pt_x0_bwd(c, m->dxb, m->dtokp, m->dbc, s));

@@ -185,6 +185,13 @@ _SIGS = {
     "ptcg_kernel_gemm_dw_bf16": (ctypes.c_int, [
         ctypes.c_int, ctypes.c_int, ctypes.c_int, c_void_p, ctypes.c_int64, c_void_p, ctypes.c_int64,
         c_void_p, c_void_p, c_void_p, ctypes.c_int64, c_void_p]),
+    "ptcg_kernel_gemm_bs": (ctypes.c_int, [
+        ctypes.c_int, ctypes.c_int, ctypes.c_int, c_void_p, ctypes.c_int64, c_void_p, ctypes.c_int64,
+        c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_int, c_void_p, c_void_p, ctypes.c_int64, c_void_p,
+        ctypes.c_int64, c_void_p]),
+    "ptcg_kernel_gemm_dw_bs": (ctypes.c_int, [
+        ctypes.c_int, ctypes.c_int, ctypes.c_int, c_void_p, ctypes.c_int64, c_void_p, ctypes.c_int64,
+        c_void_p, c_void_p, c_void_p, ctypes.c_int64, c_void_p]),
     "ptcg_kernel_attention_path": (ctypes.c_int, [ctypes.c_int, ctypes.c_int]),
     "ptcg_kernel_colsum": (ctypes.c_int, [c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_int,
                                           c_void_p, c_void_p, ctypes.c_int64, c_void_p]),

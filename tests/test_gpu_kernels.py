@@ -470,3 +470,97 @@ def test_gemm_weight_grad_bf16_with_bias_sums(rows, inp, out, cuda):
     assert rel_l2(dW.cpu().double(), refW) < 1e-5
     assert rel_l2(db.cpu().double(), refb) < 1e-5
     assert rel_l2(dW.cpu().double(), dY.double().T @ X.double()) > 1e-4
+
+
+# ---- products on bf16-stored operands (the mixed-precision variant's activations)
+BS_CASES = [
+    # M, N, K, epi, out_bf16
+    (37, 52, 256, 0, 0), (300, 200, 64, 1, 1), (256, 256, 256, 3, 0), (130, 1024, 256, 6, 1),
+    (4096, 256, 1024, 7, 1), (1000, 768, 256, 1, 1), (33000, 256, 256, 3, 0), (512, 256, 768, 0, 1),
+    (129, 136, 40, 0, 0), (200, 96, 1032, 7, 1),
+]
+
+
+def _bf16_bits(t):
+    """torch tensor -> (device bf16 tensor, its float64 value)."""
+    b = t.to(torch.bfloat16)
+    return b.to("cuda"), b.to(torch.float64)
+
+
+@pytest.mark.parametrize("case", BS_CASES, ids=lambda c: "M%d_N%d_K%d_e%d_ob%d" % c)
+def test_gemm_bf16_operands(case, cuda):
+    """C = epi(A B^T) with A, B stored in bf16: fp32 outputs within relative L2
+    1e-5 of the fp64 product of the same bf16 values; bf16 outputs within one
+    bf16 rounding (2^-8 relative) of the fp64 result elementwise, plus 2^-20 of
+    the output's largest magnitude (the fp32 accumulation error, which decides
+    the rounding where acc + bias cancels to near zero)."""
+    M, N, K, epi, ob = case
+    g = torch.Generator().manual_seed(7 * M + N + K)
+    dA, A = _bf16_bits(torch.randn(M, K, generator=g))
+    dB, B = _bf16_bits(torch.randn(N, K, generator=g))
+    bias = torch.randn(N, generator=g)
+    Rf = torch.randn(M, N, generator=g)
+    acc = A @ B.T
+    ref2 = None
+    dR = None
+    if epi == 0: ref = acc
+    elif epi == 1: ref = acc + bias.double()
+    elif epi == 3:
+        ref = acc + bias.double() + Rf.double()
+        dR = dev(Rf)
+    elif epi == 6:
+        z = acc + bias.double()
+        ref, ref2 = gelu_grad(z), gelu(z)
+    elif epi == 7:
+        dR, Rb = _bf16_bits(Rf)
+        ref = acc * Rb
+    odt = torch.bfloat16 if ob else torch.float32
+    dC = torch.zeros(M, N, dtype=odt, device="cuda")
+    dC2 = torch.zeros(M, N, dtype=odt, device="cuda")
+    native.check(native.lib().ptcg_kernel_gemm_bs(M, N, K, P(dA), K, P(dB), K, P(dC), N, epi, ob, P(dev(bias)),
+                                                  P(dR), N, P(dC2), N, None))
+    torch.cuda.synchronize()
+    outs = [(dC, ref)] + ([(dC2, ref2)] if ref2 is not None else [])
+    for d, r in outs:
+        got = d.cpu().double()
+        if ob:
+            # one bf16 rounding of the fp32 result; fp32 accumulation error is far smaller
+            tol = 2.0 ** -8 * r.abs() + 2.0 ** -20 * float(r.abs().max())
+            assert torch.all((got - r).abs() <= tol), ((got - r).abs() - tol).max()
+            assert rel_l2(got, r) < 4e-3
+        else:
+            assert rel_l2(got, r) < 1e-5, rel_l2(got, r)
+
+
+def test_gemm_bf16_operands_rejects_bad_shapes(cuda):
+    a = torch.zeros(64, 36, dtype=torch.bfloat16, device="cuda")
+    c = torch.zeros(64, 64, device="cuda")
+    with pytest.raises(RuntimeError, match="multiples of 8"):
+        native.check(native.lib().ptcg_kernel_gemm_bs(64, 64, 36, P(a), 36, P(a), 36, P(c), 64, 0, 0, None, None,
+                                                      0, None, 0, None))
+    with pytest.raises(RuntimeError, match="not built"):
+        b = torch.zeros(64, 64, dtype=torch.bfloat16, device="cuda")
+        native.check(native.lib().ptcg_kernel_gemm_bs(64, 64, 64, P(b), 64, P(b), 64, P(c), 64, 1, 0, P(c), None,
+                                                      0, None, 0, None))
+
+
+@pytest.mark.parametrize("rows,inp,out", [(6000, 256, 768), (1576, 128, 64), (104, 64, 40), (150000, 256, 1024),
+                                          (37, 256, 256), (40000, 1024, 256), (1, 8, 8)])
+def test_gemm_weight_grad_bf16_operands(rows, inp, out, cuda):
+    """dW = dY^T X and db = column sums of dY with dY, X stored in bf16: both
+    within relative L2 1e-5 of the fp64 values of the same bf16 inputs, and
+    bit-identical on a second call (fixed-order split sums)."""
+    g = torch.Generator().manual_seed(rows + 5 * inp + out)
+    d_dY, dY = _bf16_bits(torch.randn(rows, out, generator=g))
+    d_X, X = _bf16_bits(torch.randn(rows, inp, generator=g))
+    ws = empty(32 << 20)
+    res = []
+    for _ in range(2):
+        dW, db = empty(out, inp), empty(out)
+        native.check(native.lib().ptcg_kernel_gemm_dw_bs(rows, inp, out, P(d_dY), out, P(d_X), inp, P(dW), P(db),
+                                                         P(ws), ws.numel(), None))
+        torch.cuda.synchronize()
+        res.append((dW.cpu(), db.cpu()))
+    assert rel_l2(res[0][0].double(), dY.T @ X) < 1e-5
+    assert rel_l2(res[0][1].double(), dY.sum(0)) < 1e-5
+    assert torch.equal(res[0][0], res[1][0]) and torch.equal(res[0][1], res[1][1])

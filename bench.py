@@ -87,8 +87,9 @@ def useful_gemm_flops(dm, obs_rows):
 
 
 def _gemm_list(dm, obs_rows):
-    """(rows M, in K, out N, GELU epilogue, residual epilogue) of every
-    linear layer of the forward, on valid rows only."""
+    """(rows M, in K, out N, GELU epilogue, residual epilogue, trunk block
+    product: 0 none, 1 QKV, 2 out-projection, 3 FFN1, 4 FFN2) of every linear
+    layer of the forward, on valid rows only."""
     from ptcg_amd.params import OPT_E, SC_H, VAL_H, DEC_H
     off = dm.offsets()
     zone = obs_rows[:, off["tok_int"][0]:off["tok_int"][1]].reshape(len(obs_rows), dm.l_tok, dm.tok_int)[:, :, 1]
@@ -96,31 +97,42 @@ def _gemm_list(dm, obs_rows):
     R = n_valid + len(obs_rows)
     d, ffn, B = dm.d, dm.ffn, len(obs_rows)
     NJ = option_rows(dm, obs_rows)
-    g = [(n_valid, 2 * dm.d_c + dm.tok_f + 12, d, 0, 0)]
+    g = [(n_valid, 2 * dm.d_c + dm.tok_f + 12, d, 0, 0, 0)]
     for _ in range(dm.layers):
-        g += [(R, d, 3 * d, 0, 0), (R, d, d, 0, 1), (R, d, ffn, 1, 0), (R, ffn, d, 0, 1)]
-    g += [(NJ, dm.d_c, OPT_E, 0, 0), (NJ, dm.d_a, OPT_E, 0, 0), (NJ, dm.q_in, d, 1, 0), (NJ, d, d, 0, 0),
-          (NJ, dm.score_in, SC_H, 1, 0), (B, dm.global_f, dm.g, 1, 0), (B, dm.g, dm.g, 0, 0),
-          (B, dm.dec_in, DEC_H, 1, 0), (B, DEC_H, DEC_H, 0, 0), (B, dm.bcast_in, d, 0, 0),
-          (B, dm.val_in, VAL_H, 1, 0)]
+        g += [(R, d, 3 * d, 0, 0, 1), (R, d, d, 0, 1, 2), (R, d, ffn, 1, 0, 3), (R, ffn, d, 0, 1, 4)]
+    g += [(NJ, dm.d_c, OPT_E, 0, 0, 0), (NJ, dm.d_a, OPT_E, 0, 0, 0), (NJ, dm.q_in, d, 1, 0, 0),
+          (NJ, d, d, 0, 0, 0), (NJ, dm.score_in, SC_H, 1, 0, 0), (B, dm.global_f, dm.g, 1, 0, 0),
+          (B, dm.g, dm.g, 0, 0, 0), (B, dm.dec_in, DEC_H, 1, 0, 0), (B, DEC_H, DEC_H, 0, 0, 0),
+          (B, dm.bcast_in, d, 0, 0, 0), (B, dm.val_in, VAL_H, 1, 0, 0)]
     return g
 
 
-def algorithmic_gemm_bytes(dm, obs_rows):
+def algorithmic_gemm_bytes(dm, obs_rows, bf16_blocks=False):
     """HBM bytes of one fwd+bwd's GEMMs with every operand read and every
-    output written once (fp32): forward X, W, Y (+ GELU output, + residual
-    read); backward dX = dY W (+ pre-activation read for a GELU input) and
-    dW = dY^T X."""
+    output written once: forward X, W, Y (+ GELU output, + residual read);
+    backward dX = dY W (+ pre-activation read for a GELU input) and
+    dW = dY^T X.  fp32 throughout, or (bf16_blocks) the bf16 variant's trunk
+    blocks: bf16 activations, weight copies and backward operands, fp32
+    residual stream (the residual epilogues' R and C), fp32 dX where a
+    LayerNorm backward reads it (QKV and FFN1 dX) and fp32 weight gradients."""
     tot = 0.0
-    for M, K, N, gelu, resid in _gemm_list(dm, obs_rows):
-        fwd = M * K + N * K + M * N * (2 if gelu else 1) + (M * N if resid else 0)
-        dx = M * N + N * K + M * K
-        dw = M * N + M * K + N * K
-        tot += fwd + dx + dw
-    # the GELU backward reads the saved pre-activation in the dX product of
-    # the layer after it (one extra M x N read per GELU layer)
-    tot += sum(M * N for M, K, N, gelu, _ in _gemm_list(dm, obs_rows) if gelu)
-    return 4.0 * tot
+    for M, K, N, gelu, resid, trunk in _gemm_list(dm, obs_rows):
+        if bf16_blocks and trunk:
+            fwd = 2 * M * K + 2 * N * K + (8 * M * N if resid else (4 if gelu else 2) * M * N)
+            # dX = dY W: dY bf16; output fp32 for the LayerNorm backward
+            # (QKV, FFN1), bf16 for the attention backward (out-projection)
+            # and for the GELU layer (FFN2, + the bf16 gelu'(z) read)
+            dx = 2 * M * N + 2 * N * K + {1: 4, 2: 2, 3: 4, 4: 4}[trunk] * M * K
+            dw = 2 * M * N + 2 * M * K + 4 * N * K
+            tot += fwd + dx + dw
+        else:
+            fwd = M * K + N * K + M * N * (2 if gelu else 1) + (M * N if resid else 0)
+            dx = M * N + N * K + M * K
+            dw = M * N + M * K + N * K
+            # the GELU backward reads the saved pre-activation in the dX
+            # product of the layer after it (one extra M x N read per GELU layer)
+            tot += 4.0 * (fwd + dx + dw + (M * N if gelu else 0))
+    return tot
 
 
 def gemm_source_sha():
@@ -397,13 +409,14 @@ def main():
     for ix in lists[args.warmup:]:
         f, l = useful_gemm_flops(dm, obs[ix])
         useful += f
-        abytes += algorithmic_gemm_bytes(dm, obs[ix])
+        abytes += algorithmic_gemm_bytes(dm, obs[ix], bf16_blocks=bf16)
         lv.append(l)
     gemm_s = ms.value / 1e3
     achieved = useful / gemm_s / 1e12
     peak = BF16_MFMA_PEAK_TFLOPS if bf16 else FP32_MFMA_PEAK_TFLOPS
     traffic = measured_gemm_traffic()
-    kname = "gemm_bf16_k16_kernel + gemm_bf16_kernel" if bf16 else "gemm_f32_dma_kernel + gemm_f32_kernel"
+    kname = ("gemm_bs_kernel + gemm_bs_dw_kernel (trunk blocks, bf16 operands) + gemm_bf16_k16_kernel"
+             if bf16 else "gemm_f32_dma_kernel + gemm_f32_kernel")
     roof = dict(bound="mfma", kernel=f"{kname} (all launches: trunk, token, option and head GEMMs)",
                 achieved=round(achieved, 3), peak=peak, unit="TFLOP/s",
                 frac=round(achieved / peak, 4),
@@ -416,11 +429,11 @@ def main():
                 useful_tflop_per_step=round(useful / K / 1e12, 4),
                 mean_valid_seq=round(float(np.mean(lv)), 2))
     if bf16:
-        # The products' arithmetic intensity (useful flops over the fp32
-        # operand / output bytes, ~79 flop/B) is far below the bf16 ridge
-        # point (peak flops / peak bandwidth = 312 flop/B): the bf16 GEMMs are
-        # HBM-bound, so the bound roofline is bytes over time; the MFMA
-        # fraction stays beside it.
+        # The products' arithmetic intensity (useful flops over the operand /
+        # output bytes: bf16 in the trunk blocks, fp32 residual stream and
+        # elsewhere) is below the bf16 ridge point (peak flops / peak
+        # bandwidth = 312 flop/B): the bf16 GEMMs are HBM-bound, so the
+        # bound roofline is bytes over time; the MFMA fraction stays beside it.
         gbs = abytes / gemm_s / 1e9
         roof.update(bound="hbm", achieved=round(gbs, 1), peak=HBM_PEAK_GBS, unit="GB/s",
                     frac=round(gbs / HBM_PEAK_GBS, 4), mfma_tflops=round(achieved, 3), mfma_peak=peak,

@@ -360,13 +360,21 @@ __global__ __launch_bounds__(512) void attn_bwd_mfma_kernel(const T* __restrict_
 }
 
 // Backward for rows too long to park dS (L x L) in LDS (the reference's
-// 161-token trunk and 218-token critic at Dh 32).  Q, dO, K and V for the
-// (sample, head) sit in LDS.  Pass A is the pass above without the dS store;
-// pass B walks query stripes and recomputes S^T = K Q^T and dP^T = V dO^T
-// per key tile (queries on lanes), then dQ += dS K with the register-r key
-// permutation.  Costs one more S and dP evaluation than the stored variant.
+// 161-token trunk and 218-token critic at Dh 32), in two launches so two
+// workgroups fit a CU (each stages two L x Dh operands, <= 80 KB):
+// attn_bwd_kv_kernel stages Q and dO and runs pass A (per key stripe: S, dP
+// recomputed, P, dS; dV += P^T dO, dK += dS^T Q) as above without parking
+// dS; attn_bwd_q_kernel stages K and V and recomputes per query stripe S^T
+// = K Q^T and dP^T = V dO^T (queries on lanes), then dQ += dS K with the
+// register-r key permutation; its stripe's Q, dO and O rows are read
+// straight into registers and rowsum(dO o O) is a butterfly over the four
+// lanes holding a row.  Costs one more S and dP evaluation than the stored
+// variant; both walk only the sample's own tiles.  Measured against one
+// fused kernel holding Q, dO, K and V (four operands, one workgroup per
+// CU): 623 vs 809 us at 512 x 161 rows x 8 heads, 973 vs 1266 us at 218
+// rows; at 97 rows x Dh 64 the stored variant stays faster (286 vs 335 us).
 template <int DH, int NT, bool BF, typename T>
-__global__ __launch_bounds__(512) void attn_bwd_mfma_rc_kernel(const T* __restrict__ qkv,
+__global__ __launch_bounds__(512) void attn_bwd_kv_kernel(const T* __restrict__ qkv,
         const float* __restrict__ keep, const T* __restrict__ ctx,
         const float* __restrict__ lse, const T* __restrict__ dctx,
         T* __restrict__ dqkv, int Lfix, int H, float scale, const int* __restrict__ coff) {
@@ -374,38 +382,30 @@ __global__ __launch_bounds__(512) void attn_bwd_mfma_rc_kernel(const T* __restri
     extern __shared__ float sm[];
     float* Qs = sm;                 // [LP][SQ]
     float* dOs = Qs + LP * SQ;      // [LP][SQ]
-    float* Ks = dOs + LP * SQ;      // [LP][SQ]
-    float* Vs = Ks + LP * SQ;       // [LP][SQ]
-    float* ls = Vs + LP * SQ;       // [LP]
+    float* ls = dOs + LP * SQ;      // [LP]
     float* Dv = ls + LP;            // [LP]
     float* kf = Dv + LP;            // [LP]
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int li = lane & 15, lq = lane >> 4;
     const int n = blockIdx.x / H, h = blockIdx.x % H;
-    // rows of sample n: [rb, rb + L) (compact layout) or [n*Lfix, (n+1)*Lfix)
     const long rb = coff ? (long)coff[n] : (long)n * Lfix;
     const int L = coff ? coff[n + 1] - coff[n] : Lfix;
     const int D = H * DH;
+    const int ntl = min(NT, (L + 15) / 16);
     const T* base = qkv + rb * 3 * D + h * DH;
     const T* ob = ctx + rb * D + h * DH;
     const T* dob = dctx + rb * D + h * DH;
     T* gb = dqkv + rb * 3 * D + h * DH;
-    for (int idx = tid; idx < LP * (DH / 4); idx += 512) {
+    for (int idx = tid; idx < ntl * 16 * (DH / 4); idx += 512) {
         const int l = idx / (DH / 4), c4 = (idx % (DH / 4)) * 4;
-        float4 q4 = make_float4(0.f, 0.f, 0.f, 0.f), k4 = q4, v4 = q4, d4 = q4, o4 = q4;
+        float4 q4 = make_float4(0.f, 0.f, 0.f, 0.f), d4 = q4, o4 = q4;
         if (l < L) {
-            const T* r = base + (long)l * 3 * D + c4;
-            q4 = ld4(r);
-            k4 = ld4(r + D);
-            v4 = ld4(r + 2 * D);
+            q4 = ld4(base + (long)l * 3 * D + c4);
             d4 = ld4(dob + (long)l * D + c4);
             o4 = ld4(ob + (long)l * D + c4);
         }
         *reinterpret_cast<float4*>(&Qs[l * SQ + c4]) = q4;
         *reinterpret_cast<float4*>(&dOs[l * SQ + c4]) = d4;
-        *reinterpret_cast<float4*>(&Ks[l * SQ + c4]) = k4;
-        *reinterpret_cast<float4*>(&Vs[l * SQ + c4]) = v4;
-        // Dv[l] = sum_d dO[l][d] O[l][d]: butterfly over the row's DH/4 adjacent lanes
         float part = ((d4.x * o4.x + d4.y * o4.y) + d4.z * o4.z) + d4.w * o4.w;
 #pragma unroll
         for (int o = 1; o < DH / 4; o <<= 1) part += __shfl_xor(part, o, 64);
@@ -416,12 +416,10 @@ __global__ __launch_bounds__(512) void attn_bwd_mfma_rc_kernel(const T* __restri
         ls[l] = l < L ? lse[((long)n * H + h) * Lfix + l] : INFINITY;
     }
     __syncthreads();
-
-    // ---- pass A: key stripes -> dK, dV
-    for (int kb = wave; kb < NT; kb += 8) {
+    for (int kb = wave; kb < ntl; kb += 8) {
         const int k0 = kb * 16;
         const bool kv = k0 + li < L;
-        float kr[DH / 4], vr[DH / 4];
+        float kr[DH / 4], vr[DH / 4];   // B operands: lane (li = key, lq) holds K/V[k0+li][4kk+lq]
 #pragma unroll
         for (int kk = 0; kk < DH / 4; ++kk) {
             kr[kk] = kv ? tof(base[(long)(k0 + li) * 3 * D + D + 4 * kk + lq]) : 0.f;
@@ -434,8 +432,8 @@ __global__ __launch_bounds__(512) void attn_bwd_mfma_rc_kernel(const T* __restri
             dv[dt] = floatx4{0.f, 0.f, 0.f, 0.f};
             dk[dt] = dv[dt];
         }
-        for (int qt = 0; qt < NT; ++qt) {
-            floatx4 s = floatx4{0.f, 0.f, 0.f, 0.f}, dp = s;
+        for (int qt = 0; qt < ntl; ++qt) {
+            floatx4 sc = floatx4{0.f, 0.f, 0.f, 0.f}, dp = sc;
 #pragma unroll
             for (int kq = 0; kq < DH / 16; ++kq) {
                 float qa[4], da[4], kb4[4], vb4[4];
@@ -447,29 +445,31 @@ __global__ __launch_bounds__(512) void attn_bwd_mfma_rc_kernel(const T* __restri
                     kb4[e] = kr[4 * kq + e];
                     vb4[e] = vr[4 * kq + e];
                 }
-                s = mfma4<BF>(qa, kb4, s);
+                sc = mfma4<BF>(qa, kb4, sc);
                 dp = mfma4<BF>(da, vb4, dp);
             }
+            // sc[r] = S[q = 16qt + 4lq + r][key = k0 + li]
             float p[4], ds[4];
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int q = 16 * qt + 4 * lq + r;
-                p[r] = kfl > 0.f ? expf(s[r] * scale - ls[q]) : 0.f;
+                p[r] = kfl > 0.f ? expf(sc[r] * scale - ls[q]) : 0.f;
                 ds[r] = p[r] * (dp[r] - Dv[q]);
             }
 #pragma unroll
             for (int dt = 0; dt < DH / 16; ++dt) {
-                float ob[4], qb4[4];
+                float obr[4], qb4[4];
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     const int qrow = 16 * qt + 4 * lq + r;
-                    ob[r] = dOs[qrow * SQ + 16 * dt + li];
+                    obr[r] = dOs[qrow * SQ + 16 * dt + li];
                     qb4[r] = Qs[qrow * SQ + 16 * dt + li];
                 }
-                dv[dt] = mfma4<BF>(p, ob, dv[dt]);
+                dv[dt] = mfma4<BF>(p, obr, dv[dt]);
                 dk[dt] = mfma4<BF>(ds, qb4, dk[dt]);
             }
         }
+        // dv[dt][r] = dV[k0 + 4lq + r][16dt + li]
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const int key = k0 + 4 * lq + r;
@@ -483,21 +483,62 @@ __global__ __launch_bounds__(512) void attn_bwd_mfma_rc_kernel(const T* __restri
             }
         }
     }
+}
 
-    // ---- pass B: query stripes -> dQ (no barrier needed: LDS is read-only here)
-    for (int qt = wave; qt < NT; qt += 8) {
+template <int DH, int NT, bool BF, typename T>
+__global__ __launch_bounds__(512) void attn_bwd_q_kernel(const T* __restrict__ qkv,
+        const float* __restrict__ keep, const T* __restrict__ ctx,
+        const float* __restrict__ lse, const T* __restrict__ dctx,
+        T* __restrict__ dqkv, int Lfix, int H, float scale, const int* __restrict__ coff) {
+    constexpr int LP = NT * 16, SQ = DH + 4;
+    extern __shared__ float sm[];
+    float* Ks = sm;                 // [LP][SQ]
+    float* Vs = Ks + LP * SQ;       // [LP][SQ]
+    float* kf = Vs + LP * SQ;       // [LP]
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int li = lane & 15, lq = lane >> 4;
+    const int n = blockIdx.x / H, h = blockIdx.x % H;
+    const long rb = coff ? (long)coff[n] : (long)n * Lfix;
+    const int L = coff ? coff[n + 1] - coff[n] : Lfix;
+    const int D = H * DH;
+    const int ntl = min(NT, (L + 15) / 16);
+    const T* base = qkv + rb * 3 * D + h * DH;
+    const T* ob = ctx + rb * D + h * DH;
+    const T* dob = dctx + rb * D + h * DH;
+    T* gb = dqkv + rb * 3 * D + h * DH;
+    for (int idx = tid; idx < ntl * 16 * (DH / 4); idx += 512) {
+        const int l = idx / (DH / 4), c4 = (idx % (DH / 4)) * 4;
+        float4 k4 = make_float4(0.f, 0.f, 0.f, 0.f), v4 = k4;
+        if (l < L) {
+            const T* r = base + (long)l * 3 * D + c4;
+            k4 = ld4(r + D);
+            v4 = ld4(r + 2 * D);
+        }
+        *reinterpret_cast<float4*>(&Ks[l * SQ + c4]) = k4;
+        *reinterpret_cast<float4*>(&Vs[l * SQ + c4]) = v4;
+    }
+    for (int l = tid; l < LP; l += 512) kf[l] = l < L ? (keep[rb + l] != 0.f ? 1.f : 0.f) : 0.f;
+    __syncthreads();
+    for (int qt = wave; qt < ntl; qt += 8) {
         const int q0 = qt * 16;
-        float qb[DH / 4], db[DH / 4];    // B operands: lane (li = query, lq) holds Q/dO[q0+li][4kk+lq]
+        const bool qv = q0 + li < L;
+        float qb[DH / 4], db[DH / 4];   // B operands: lane (li = query, lq) holds Q/dO[q0+li][4kk+lq]
+        float dvq = 0.f;
 #pragma unroll
         for (int kk = 0; kk < DH / 4; ++kk) {
-            qb[kk] = Qs[(q0 + li) * SQ + 4 * kk + lq];
-            db[kk] = dOs[(q0 + li) * SQ + 4 * kk + lq];
+            const long qr = (long)(q0 + li);
+            qb[kk] = qv ? tof(base[qr * 3 * D + 4 * kk + lq]) : 0.f;
+            db[kk] = qv ? tof(dob[qr * D + 4 * kk + lq]) : 0.f;
+            dvq += db[kk] * (qv ? tof(ob[qr * D + 4 * kk + lq]) : 0.f);
         }
-        const float lsq = ls[q0 + li], dvq = Dv[q0 + li];
+        // rowsum(dO o O) of query q0 + li: its four lane groups
+        dvq += __shfl_xor(dvq, 16, 64);
+        dvq += __shfl_xor(dvq, 32, 64);
+        const float lsq = qv ? lse[((long)n * H + h) * Lfix + q0 + li] : INFINITY;
         floatx4 dq[DH / 16];
 #pragma unroll
         for (int dt = 0; dt < DH / 16; ++dt) dq[dt] = floatx4{0.f, 0.f, 0.f, 0.f};
-        for (int J = 0; J < NT; ++J) {
+        for (int J = 0; J < ntl; ++J) {
             floatx4 st = floatx4{0.f, 0.f, 0.f, 0.f}, dpt = st;
 #pragma unroll
             for (int kq = 0; kq < DH / 16; ++kq) {
@@ -541,9 +582,29 @@ __global__ __launch_bounds__(512) void attn_bwd_mfma_rc_kernel(const T* __restri
     }
 }
 
-size_t bwd_rc_lds_bytes(int LP, int DH) {
-    return sizeof(float) * ((size_t)LP * (DH + 4) * 4 + 3 * (size_t)LP);
+size_t bwd_split_lds_bytes(int LP, int DH) { return sizeof(float) * ((size_t)LP * (DH + 4) * 2 + 3 * (size_t)LP); }
+
+template <int DH, int NT, bool BF, bool IO16>
+int launch_bwd_split(const float* qkv, const float* keep, const float* ctx, const float* lse,
+                     const float* dctx, float* dqkv, int N, int L, int H, hipStream_t s, const int* coff) {
+    typedef typename std::conditional<IO16, __bf16, float>::type T;
+    const size_t lds = bwd_split_lds_bytes(NT * 16, DH);
+    PT_HIP(hipFuncSetAttribute((const void*)attn_bwd_kv_kernel<DH, NT, BF, T>,
+                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+    PT_HIP(hipFuncSetAttribute((const void*)attn_bwd_q_kernel<DH, NT, BF, T>,
+                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+    const float sc = 1.0f / sqrtf((float)DH);
+    hipLaunchKernelGGL((attn_bwd_kv_kernel<DH, NT, BF, T>), dim3(N * H), dim3(512), lds, s,
+                       reinterpret_cast<const T*>(qkv), keep, reinterpret_cast<const T*>(ctx), lse,
+                       reinterpret_cast<const T*>(dctx), reinterpret_cast<T*>(dqkv), L, H, sc, coff);
+    PT_LAUNCH_CHECK();
+    hipLaunchKernelGGL((attn_bwd_q_kernel<DH, NT, BF, T>), dim3(N * H), dim3(512), lds, s,
+                       reinterpret_cast<const T*>(qkv), keep, reinterpret_cast<const T*>(ctx), lse,
+                       reinterpret_cast<const T*>(dctx), reinterpret_cast<T*>(dqkv), L, H, sc, coff);
+    PT_LAUNCH_CHECK();
+    return PTCG_OK;
 }
+
 size_t fwd_mfma_lds_bytes(int LP, int DH) {
     return sizeof(float) * ((size_t)LP * (DH + 4) * 2 + (size_t)LP);
 }
@@ -562,21 +623,6 @@ int launch_fwd_mfma(const float* qkv, const float* keep, float* ctx, float* lse,
                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
     hipLaunchKernelGGL((attn_fwd_mfma_kernel<DH, NT, BF, T>), dim3(N * H), dim3(512), lds, s,
                        reinterpret_cast<const T*>(qkv), keep, reinterpret_cast<T*>(ctx), lse, L, H,
-                       1.0f / sqrtf((float)DH), coff);
-    PT_LAUNCH_CHECK();
-    return PTCG_OK;
-}
-
-template <int DH, int NT, bool BF, bool IO16>
-int launch_bwd_rc(const float* qkv, const float* keep, const float* ctx, const float* lse,
-                  const float* dctx, float* dqkv, int N, int L, int H, hipStream_t s, const int* coff) {
-    typedef typename std::conditional<IO16, __bf16, float>::type T;
-    const size_t lds = bwd_rc_lds_bytes(NT * 16, DH);
-    PT_HIP(hipFuncSetAttribute((const void*)attn_bwd_mfma_rc_kernel<DH, NT, BF, T>,
-                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-    hipLaunchKernelGGL((attn_bwd_mfma_rc_kernel<DH, NT, BF, T>), dim3(N * H), dim3(512), lds, s,
-                       reinterpret_cast<const T*>(qkv), keep, reinterpret_cast<const T*>(ctx), lse,
-                       reinterpret_cast<const T*>(dctx), reinterpret_cast<T*>(dqkv), L, H,
                        1.0f / sqrtf((float)DH), coff);
     PT_LAUNCH_CHECK();
     return PTCG_OK;
@@ -604,7 +650,7 @@ static const size_t PT_LDS_MAX = 160 * 1024;
 
 // Kernel choice per (L, Dh), Lp = 16 * ceil(L / 16) = 16 * nt, nt <= 16
 // (Dh 32) / 9 (Dh 64): forward MFMA; backward MFMA with dS parked in LDS
-// when it fits (nt <= 8), else the MFMA recompute kernel.
+// when it fits (nt <= 8), else the split recompute pair.
 static const int PT_NT_MAX32 = 16, PT_NT_MAX64 = 9;
 static int nt_max(int DH) { return DH == 32 ? PT_NT_MAX32 : (DH == 64 ? PT_NT_MAX64 : 0); }
 static int fwd_tiles(int L, int DH) {
@@ -616,14 +662,14 @@ static int bwd_store_tiles(int L, int DH) {
     if (!(DH == 32 || DH == 64) || nt > 8) return 0;
     return bwd_mfma_lds_bytes(nt * 16, DH) <= PT_LDS_MAX ? nt : 0;
 }
-static int bwd_rc_tiles(int L, int DH) {
+static int bwd_split_tiles(int L, int DH) {
     const int nt = pt_cdiv(L, 16);
-    return (nt <= nt_max(DH) && bwd_rc_lds_bytes(nt * 16, DH) <= PT_LDS_MAX) ? nt : 0;
+    return (nt <= nt_max(DH) && bwd_split_lds_bytes(nt * 16, DH) <= PT_LDS_MAX) ? nt : 0;
 }
 
 int pt_attn_supported(int L, int DH) {
     if (!(DH == 32 || DH == 64) || L > 256 || L < 1) return 0;
-    return (fwd_tiles(L, DH) && (bwd_store_tiles(L, DH) || bwd_rc_tiles(L, DH))) ? 1 : 0;
+    return (fwd_tiles(L, DH) && (bwd_store_tiles(L, DH) || bwd_split_tiles(L, DH))) ? 1 : 0;
 }
 
 // (used inside the BF / IO16-templated dispatchers below)
@@ -668,13 +714,13 @@ static int attn_bwd_dispatch(const float* qkv, const float* keep, const float* c
         if (DH == 64) { PT_NT_SWITCH8(64, nt, launch_bwd_mfma, qkv, keep, ctx, lse, dctx, dqkv, N, L, H, s, coff) }
         else { PT_NT_SWITCH8(32, nt, launch_bwd_mfma, qkv, keep, ctx, lse, dctx, dqkv, N, L, H, s, coff) }
     }
-    nt = bwd_rc_tiles(L, DH);
+    nt = bwd_split_tiles(L, DH);
     if (nt && DH == 64) {
-        PT_NT_SWITCH8(64, nt, launch_bwd_rc, qkv, keep, ctx, lse, dctx, dqkv, N, L, H, s, coff)
-        if (nt == 9) return launch_bwd_rc<64, 9, BF, IO16>(qkv, keep, ctx, lse, dctx, dqkv, N, L, H, s, coff);
+        PT_NT_SWITCH8(64, nt, launch_bwd_split, qkv, keep, ctx, lse, dctx, dqkv, N, L, H, s, coff)
+        if (nt == 9) return launch_bwd_split<64, 9, BF, IO16>(qkv, keep, ctx, lse, dctx, dqkv, N, L, H, s, coff);
     } else if (nt) {
-        PT_NT_SWITCH8(32, nt, launch_bwd_rc, qkv, keep, ctx, lse, dctx, dqkv, N, L, H, s, coff)
-        PT_NT_SWITCH_HI(32, nt, launch_bwd_rc, qkv, keep, ctx, lse, dctx, dqkv, N, L, H, s, coff)
+        PT_NT_SWITCH8(32, nt, launch_bwd_split, qkv, keep, ctx, lse, dctx, dqkv, N, L, H, s, coff)
+        PT_NT_SWITCH_HI(32, nt, launch_bwd_split, qkv, keep, ctx, lse, dctx, dqkv, N, L, H, s, coff)
     }
     PT_REQUIRE(false, "attention bwd: no kernel for L=%d Dh=%d", L, DH);
 }
@@ -702,6 +748,6 @@ int pt_attn_path(int L, int DH) {
     if (!pt_attn_supported(L, DH)) return -1;
     int f = fwd_tiles(L, DH) ? 1 : 0;
     if (bwd_store_tiles(L, DH)) f |= 2;
-    else if (bwd_rc_tiles(L, DH)) f |= 4;
+    else if (bwd_split_tiles(L, DH)) f |= 4;
     return f;
 }

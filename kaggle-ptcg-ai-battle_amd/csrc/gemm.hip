@@ -847,9 +847,7 @@ __global__ __launch_bounds__(NT) void gemm_bf16_k16_kernel(const GemmArgs g0, in
 // gemm_bs_kernel: C = epi(A B^T), A (M, K) and B (N, K) k-contiguous, on the
 // LDS-DMA pipeline (BS: a 16-float stage row is 32 bf16 k; one
 // v_mfma_f32_16x16x32_bf16 per 16 x 16 tile and stage).  Shapes arrive in
-// float units.  NS stages: a bf16 stage feeds 8x the MFMA work of an fp32
-// one (its 16 KB of DMA per 32 k against 16 k), so more of them are kept in
-// flight.
+// float units.  NS stages (BS_NS).
 template <int EPI, bool OB, int NS>
 __global__ __launch_bounds__(NT) void gemm_bs_kernel(const GemmArgs g0) {
     gemm_dma_tile<false, false, EPI, false, false, false, NS, true, OB>(g0, g0.K, 0, blockIdx.x, 0, 1);
@@ -1285,7 +1283,11 @@ static bool dma_ok(const GemmArgs& g) {
 }
 
 // ---- bf16 storage (GemmArgs::bs)
-constexpr int BS_NS = 3;
+// two DMA stages: measured faster than three or four at the trunk shapes
+// (149 504 x {256, 768, 1024} x {256, 1024}): the smaller LDS footprint
+// keeps more workgroups per CU, which hides the operand fetches better than
+// a deeper pipeline per workgroup
+constexpr int BS_NS = 2;
 static bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
 template <int EPI, bool OB>

@@ -11,7 +11,8 @@
 //
 // Per site:
 //   1. det_absmax_kernel: max |g| over each source slice (the gradient
-//      columns the site scatters), per-block partial maxima (no atomics);
+//      columns the site scatters), DET_PART per-block partial maxima per
+//      source (no atomics), 128-bit loads where the slice is aligned;
 //   2. det_scale_kernel: per table t, scale_t = 2^(61 - e) with
 //      2^e > count_t * max|g| (count_t bounds how many contributions one
 //      table element can receive), so no partial sum can overflow 2^62;
@@ -29,44 +30,58 @@ namespace {
 
 constexpr int DT_TB = 256;
 
+__device__ __forceinline__ unsigned abits(float v) { return __float_as_uint(v) & 0x7fffffffu; }
+
+// grid (DET_PART, nsrc): block b of source si takes elements b, b + DET_PART * DT_TB, ...
+// of the source's rows x width slice; 128-bit loads where the slice allows
+// (vec[si]: 16 B aligned rows, width and column a multiple of 4)
 __global__ __launch_bounds__(DT_TB) void det_absmax_kernel(DetSite S, float* __restrict__ part) {
     const int si = blockIdx.y;
     const long rows = S.srows_dev[si] ? min((long)*S.srows_dev[si], S.srows[si]) : S.srows[si];
     const int w = S.swidth[si];
-    const long total = rows * w;
+    const float* base = S.sp[si] + S.scol[si];
+    const long ld = S.sld[si];
     unsigned mb = 0u;   // |v| as bits: integer order = float order, NaN above inf
-    for (long i = (long)blockIdx.x * DT_TB + threadIdx.x; i < total; i += (long)gridDim.x * DT_TB) {
-        const long r = i / w;
-        const int c = (int)(i % w);
-        const unsigned b = __float_as_uint(S.sp[si][r * S.sld[si] + S.scol[si] + c]) & 0x7fffffffu;
-        mb = b > mb ? b : mb;
+    if (S.svec[si]) {
+        const unsigned w4 = (unsigned)w >> 2;
+        const unsigned total = (unsigned)rows * w4;   // host: rows * width < 2^31
+        for (unsigned i = blockIdx.x * DT_TB + threadIdx.x; i < total; i += DET_PART * DT_TB) {
+            const unsigned r = i / w4, c = i - r * w4;
+            const float4 v = *reinterpret_cast<const float4*>(base + (long)r * ld + 4 * c);
+            mb = max(mb, max(max(abits(v.x), abits(v.y)), max(abits(v.z), abits(v.w))));
+        }
+    } else {
+        const unsigned total = (unsigned)rows * (unsigned)w;
+        for (unsigned i = blockIdx.x * DT_TB + threadIdx.x; i < total; i += DET_PART * DT_TB) {
+            const unsigned r = i / (unsigned)w, c = i - r * (unsigned)w;
+            mb = max(mb, abits(base[(long)r * ld + c]));
+        }
     }
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-        const unsigned x = (unsigned)__shfl_xor((int)mb, o, 64);
-        mb = x > mb ? x : mb;
-    }
+    for (int o = 32; o > 0; o >>= 1) mb = max(mb, (unsigned)__shfl_xor((int)mb, o, 64));
     __shared__ unsigned red[DT_TB / 64];
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mb;
     __syncthreads();
     if (threadIdx.x == 0) {
         unsigned m = red[0];
-        for (int k = 1; k < DT_TB / 64; ++k) m = red[k] > m ? red[k] : m;
+        for (int k = 1; k < DT_TB / 64; ++k) m = max(m, red[k]);
         part[si * DET_PART + blockIdx.x] = __uint_as_float(m);
     }
 }
 
-__global__ void det_scale_kernel(DetSite S, const float* __restrict__ part, double* __restrict__ scale) {
-    const int t = threadIdx.x;
+// one wave per table: max over its sources' partials, then the scale
+__global__ __launch_bounds__(64 * DET_MAX_TAB) void det_scale_kernel(DetSite S, const float* __restrict__ part,
+                                                                    double* __restrict__ scale) {
+    const int t = threadIdx.x >> 6, lane = threadIdx.x & 63;
     if (t >= S.ntab) return;
     unsigned mb = 0u;
     for (int si = 0; si < S.nsrc; ++si) {
         if (S.stab[si] != t) continue;
-        for (int k = 0; k < DET_PART; ++k) {
-            const unsigned b = __float_as_uint(part[si * DET_PART + k]);
-            mb = b > mb ? b : mb;
-        }
+        for (int k = lane; k < DET_PART; k += 64) mb = max(mb, __float_as_uint(part[si * DET_PART + k]));
     }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) mb = max(mb, (unsigned)__shfl_xor((int)mb, o, 64));
+    if (lane != 0) return;
     double sc;
     if (mb >= 0x7f800000u) {
         sc = -1.0;   // non-finite gradient: the table becomes NaN
@@ -104,11 +119,17 @@ int pt_det_prepare(const DetCtx& d, const DetSite& S, hipStream_t s) {
         PT_REQUIRE(S.acc_off[t] >= 0 && S.acc_off[t] + S.tab_n[t] <= d.acc_len,
                    "det: table %d needs accumulator [%ld, %ld) of %ld", t, S.acc_off[t], S.acc_off[t] + S.tab_n[t],
                    d.acc_len);
-    for (int i = 0; i < S.nsrc; ++i)
+    DetSite V = S;
+    for (int i = 0; i < S.nsrc; ++i) {
         PT_REQUIRE(S.stab[i] >= 0 && S.stab[i] < S.ntab, "det: source %d maps to table %d", i, S.stab[i]);
-    hipLaunchKernelGGL(det_absmax_kernel, dim3(DET_PART, S.nsrc), dim3(DT_TB), 0, s, S, d.part);
+        PT_REQUIRE(S.srows[i] * S.swidth[i] < (1L << 31), "det: source %d of %ld x %d elements", i, S.srows[i],
+                   S.swidth[i]);
+        V.svec[i] = (((uintptr_t)S.sp[i] & 15) == 0 && S.sld[i] % 4 == 0 && S.scol[i] % 4 == 0 &&
+                     S.swidth[i] % 4 == 0) ? 1 : 0;
+    }
+    hipLaunchKernelGGL(det_absmax_kernel, dim3(DET_PART, V.nsrc), dim3(DT_TB), 0, s, V, d.part);
     PT_LAUNCH_CHECK();
-    hipLaunchKernelGGL(det_scale_kernel, dim3(1), dim3(64), 0, s, S, (const float*)d.part, d.scale);
+    hipLaunchKernelGGL(det_scale_kernel, dim3(1), dim3(64 * DET_MAX_TAB), 0, s, V, (const float*)d.part, d.scale);
     PT_LAUNCH_CHECK();
     return PTCG_OK;
 }

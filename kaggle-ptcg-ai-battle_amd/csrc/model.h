@@ -95,7 +95,7 @@ int pt_to_bf16(const float* src, float* dst, long n, hipStream_t s);
 // ---- order-independent table scatters (detsum.hip)
 // A site: the tables one point of the backward scatters into and the
 // gradient slices it scatters from (sources; source i feeds table stab[i]).
-constexpr int DET_MAX_TAB = 8, DET_MAX_SRC = 8, DET_PART = 64;
+constexpr int DET_MAX_TAB = 8, DET_MAX_SRC = 8, DET_PART = 256;
 struct DetSite {
     int ntab = 0;
     float* tab[DET_MAX_TAB] = {};       // float tables (the grads), += at finish
@@ -106,6 +106,7 @@ struct DetSite {
     const float* sp[DET_MAX_SRC] = {};  // source rows: sp + r * sld + scol, swidth floats,
     long sld[DET_MAX_SRC] = {};         // r < min(srows, *srows_dev)
     int scol[DET_MAX_SRC] = {}, swidth[DET_MAX_SRC] = {}, stab[DET_MAX_SRC] = {};
+    int svec[DET_MAX_SRC] = {};         // set by pt_det_prepare: 128-bit loads allowed
     long srows[DET_MAX_SRC] = {};
     const int* srows_dev[DET_MAX_SRC] = {};
     int add_table(float* t, long n, long off, double cnt) {

@@ -415,7 +415,7 @@ def main():
     achieved = useful / gemm_s / 1e12
     peak = BF16_MFMA_PEAK_TFLOPS if bf16 else FP32_MFMA_PEAK_TFLOPS
     traffic = measured_gemm_traffic()
-    kname = ("gemm_bs_kernel + gemm_bs_dw_kernel (trunk blocks, bf16 operands) + gemm_bf16_k16_kernel"
+    kname = ("gemm_bs32_kernel + gemm_bs_dw_kernel (trunk blocks, bf16 operands) + gemm_bf16_k16_kernel"
              if bf16 else "gemm_f32_dma_kernel + gemm_f32_kernel")
     roof = dict(bound="mfma", kernel=f"{kname} (all launches: trunk, token, option and head GEMMs)",
                 achieved=round(achieved, 3), peak=peak, unit="TFLOP/s",

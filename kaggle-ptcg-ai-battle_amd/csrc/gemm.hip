@@ -238,7 +238,7 @@ template <int EPI> struct EpiStaged {
                                   EPI == EPI_BIAS_GELU_D || EPI == EPI_MUL || EPI == EPI_AXPBY;
 };
 
-template <int EPI, bool OB = false>
+template <int EPI>
 __device__ __forceinline__ void epilogue_staged(const GemmArgs& g, floatx4 (&acc)[4][4], int m0, int n0, int wm,
                                                 int wn, int li, int lq, float* stage, bool vo) {
     const int tid = threadIdx.x;
@@ -258,9 +258,9 @@ __device__ __forceinline__ void epilogue_staged(const GemmArgs& g, floatx4 (&acc
             if (m >= g.M || n >= g.N) continue;
             const floatx4 v = *reinterpret_cast<const floatx4*>(stage + lr * SST + c);
             if (vo && n + 3 < g.N) {
-                epi_store4<EPI, OB>(g, m, n, v);
+                epi_store4<EPI>(g, m, n, v);
             } else {
-                for (int r = 0; r < 4 && n + r < g.N; ++r) epi_store<EPI, OB>(g, m, n + r, v[r]);
+                for (int r = 0; r < 4 && n + r < g.N; ++r) epi_store<EPI>(g, m, n + r, v[r]);
             }
         }
     }
@@ -272,7 +272,7 @@ __device__ __forceinline__ void epilogue_staged(const GemmArgs& g, floatx4 (&acc
 // four consecutive columns of one row per lane, stored (and the bias /
 // residual / pre-activation read) as one 128-bit access when aligned.
 // stage: STAGE_FLOATS of LDS the main loop no longer uses.
-template <int EPI, bool PARTIAL, bool OB = false>
+template <int EPI, bool PARTIAL>
 __device__ __forceinline__ void gemm_epilogue(const GemmArgs& g, floatx4 (&acc)[4][4], int m0, int n0, int wm,
                                               int wn, int li, int lq, long part_stride, float* stage, int bz) {
     if (PARTIAL && g.tail_part) {
@@ -291,10 +291,8 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& g, floatx4 (&acc)[
                                  : (uintptr_t)g.C | (uintptr_t)g.C2 | (uintptr_t)g.R | (uintptr_t)g.bias |
                                        (uintptr_t)((g.ldc | g.ldc2 | g.ldr) * 4);
     const bool vo = (al & 15) == 0;
-    // bf16 outputs always go through the stage: a lane's own four columns
-    // are only 8 B, the staged rows are 256 B contiguous
-    if (!PARTIAL && (EpiStaged<EPI>::value || OB)) {
-        epilogue_staged<EPI, OB>(g, acc, m0, n0, wm, wn, li, lq, stage, vo);
+    if (!PARTIAL && EpiStaged<EPI>::value) {
+        epilogue_staged<EPI>(g, acc, m0, n0, wm, wn, li, lq, stage, vo);
         return;
     }
 #pragma unroll
@@ -306,14 +304,14 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& g, floatx4 (&acc)[
             const int n = n0 + wn + tj * 16 + 4 * lq;
             if (vo && n + 3 < g.N) {
                 if (PARTIAL) st_g4(g.C + zoff + (long)m * g.ldc + n, acc[ti][tj]);
-                else epi_store4<EPI, OB>(g, m, n, acc[ti][tj]);
+                else epi_store4<EPI>(g, m, n, acc[ti][tj]);
                 continue;
             }
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 if (n + r >= g.N) continue;
                 if (PARTIAL) g.C[zoff + (long)m * g.ldc + n + r] = acc[ti][tj][r];
-                else epi_store<EPI, OB>(g, m, n + r, acc[ti][tj][r]);
+                else epi_store<EPI>(g, m, n + r, acc[ti][tj][r]);
             }
         }
     }
@@ -521,16 +519,9 @@ template <bool T> __device__ __forceinline__ int dma_src(int c, int lane, int r0
 // BF: bf16 products — each lane's float4 fragment (k = 4 lq .. 4 lq + 3 of
 // its row, the same k for A and B) is rounded to bf16 (RNE) and one
 // v_mfma_f32_16x16x16_bf16 replaces the four fp32 k-steps.
-// BS: bf16 operands in memory (both k-contiguous).  The caller passes the
-// shapes in float units (K / 2, lda / 2, ldb / 2): the DMA moves bytes, so a
-// 16-float stage row is 32 bf16 k and a 4-float group is 8 — exactly one
-// lane's fragment of v_mfma_f32_16x16x32_bf16 (row li, k = 8 lq .. 8 lq + 7,
-// the same k for A and B).  OB: the epilogue writes bf16 (epi_store_bf).
-template <bool AT, bool BT, int EPI, bool PARTIAL, bool DB, bool BF = false, int NS = DMA_NS, bool BS = false,
-          bool OB = false>
+template <bool AT, bool BT, int EPI, bool PARTIAL, bool DB, bool BF = false, int NS = DMA_NS>
 __device__ __forceinline__ void gemm_dma_tile(const GemmArgs& g0, int k_chunk0, long part_stride, int bx, int bz,
                                               int gz) {
-    static_assert(!BS || (!AT && !BT && !DB && !BF), "bf16 operands: k-contiguous A and B only");
     const GemmArgs g = gemm_shape(g0);
     // a device reduction count splits its own K evenly over the launch's splits
     const int k_chunk = g0.Kdev ? (((g.K + gz - 1) / gz + BK - 1) / BK) * BK : k_chunk0;
@@ -602,20 +593,6 @@ __device__ __forceinline__ void gemm_dma_tile(const GemmArgs& g0, int k_chunk0, 
             if (it + NS - 1 < nk) PT_ISSUE(it + NS - 1)
             const float* Ab = smem + (it % NS) * 2 * TILE;
             const float* Bb = Ab + TILE;
-            if constexpr (BS) {
-                bf16x8 ah[4], bh[4];
-#pragma unroll
-                for (int t = 0; t < 4; ++t) {
-                    ah[t] = *reinterpret_cast<const bf16x8*>(Ab + dma_at<false>(wm + t * 16 + li, 4 * lq));
-                    bh[t] = *reinterpret_cast<const bf16x8*>(Bb + dma_at<false>(wn + t * 16 + li, 4 * lq));
-                }
-#pragma unroll
-                for (int ti = 0; ti < 4; ++ti)
-#pragma unroll
-                    for (int tj = 0; tj < 4; ++tj)
-                        acc[ti][tj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bh[tj], ah[ti], acc[ti][tj], 0, 0, 0);
-                continue;
-            }
             float4 af[4], bf[4];
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
@@ -669,7 +646,7 @@ __device__ __forceinline__ void gemm_dma_tile(const GemmArgs& g0, int k_chunk0, 
         }
     }
 
-    gemm_epilogue<EPI, PARTIAL, OB>(g, acc, m0, n0, wm, wn, li, lq, part_stride, smem, bz);
+    gemm_epilogue<EPI, PARTIAL>(g, acc, m0, n0, wm, wn, li, lq, part_stride, smem, bz);
 }
 
 template <bool AT, bool BT, int EPI, bool PARTIAL, bool DB>
@@ -844,13 +821,127 @@ __global__ __launch_bounds__(NT) void gemm_bf16_k16_kernel(const GemmArgs g0, in
 // Products whose operands are stored in bf16 (the mixed-precision variant's
 // activations and bf16 copies of the weights), fp32 accumulation.
 //
-// gemm_bs_kernel: C = epi(A B^T), A (M, K) and B (N, K) k-contiguous, on the
-// LDS-DMA pipeline (BS: a 16-float stage row is 32 bf16 k; one
-// v_mfma_f32_16x16x32_bf16 per 16 x 16 tile and stage).  Shapes arrive in
-// float units.  NS stages (BS_NS).
+// gemm_bs32_kernel: C = epi(A B^T), A (M, K) and B (N, K) bf16, both
+// k-contiguous, shapes in float units: the fp32 kernel's LDS-DMA stages and
+// layouts with the bytes reinterpreted (a 16-float stage row is 32 bf16 k,
+// a 4-float group 8 of them), multiplied on v_mfma_f32_32x32x16_bf16 (1.7x
+// the rate of the 16 x 16 form on this GPU; measured 1-4% faster than a
+// 16 x 16 x 32 version of this kernel, whose loop waits on its operand
+// fetches rather than on the matrix pipe).  A wave's 64 x 64 tile is 2 x 2
+// MFMA tiles of 32 x 32, two 16-k steps per 32-k stage.  Lane (l32 = lane % 32, lh = lane / 32) supplies row
+// l32 of its 32-row slice and k = 8 lh .. 8 lh + 7 of the step — the 16 B
+// group 2 s + lh of the stage row — for both A and B.  With B as the first
+// operand, accumulator register r of lane (l32, lh) holds
+// C[wm + 32 ti + l32][wn + 32 tj + 8 (r / 4) + 4 lh + r % 4]: four runs of
+// four consecutive columns of one row, staged through LDS as the 16 x 16
+// kernels' epilogue does (half h = rows wm + 32 h .. + 31 of both wave rows).
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+template <int EPI, bool OB>
+__device__ __forceinline__ void epilogue_staged32(const GemmArgs& g, floatx16 (&acc)[2][2], int m0, int n0, int wm,
+                                                  int wn, int l32, int lh, float* stage, bool vo) {
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        __syncthreads();   // the stage is free (main loop done / previous half consumed)
+#pragma unroll
+        for (int tj = 0; tj < 2; ++tj)
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                *reinterpret_cast<floatx4*>(stage + ((wm >> 6) * 32 + l32) * SST + wn + 32 * tj + 8 * q + 4 * lh) =
+                    floatx4{acc[h][tj][4 * q], acc[h][tj][4 * q + 1], acc[h][tj][4 * q + 2], acc[h][tj][4 * q + 3]};
+        __syncthreads();
+        for (int it = tid; it < 64 * (BN / 4); it += NT) {
+            const int lr = it / (BN / 4), c = (it % (BN / 4)) * 4;
+            const int m = m0 + (lr >> 5) * 64 + 32 * h + (lr & 31), n = n0 + c;
+            if (m >= g.M || n >= g.N) continue;
+            const floatx4 v = *reinterpret_cast<const floatx4*>(stage + lr * SST + c);
+            if (vo && n + 3 < g.N) {
+                epi_store4<EPI, OB>(g, m, n, v);
+            } else {
+                for (int r = 0; r < 4 && n + r < g.N; ++r) epi_store<EPI, OB>(g, m, n + r, v[r]);
+            }
+        }
+    }
+}
+
 template <int EPI, bool OB, int NS>
-__global__ __launch_bounds__(NT) void gemm_bs_kernel(const GemmArgs g0) {
-    gemm_dma_tile<false, false, EPI, false, false, false, NS, true, OB>(g0, g0.K, 0, blockIdx.x, 0, 1);
+__global__ __launch_bounds__(NT) void gemm_bs32_kernel(const GemmArgs g0) {
+    const GemmArgs g = gemm_shape(g0);
+    constexpr int TILE = BM * BK;   // floats per operand stage (BM == BN)
+    constexpr int SMEM = NS * 2 * TILE > STAGE_FLOATS ? NS * 2 * TILE : STAGE_FLOATS;
+    __shared__ __align__(16) float smem[SMEM];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tn = (g.N + BN - 1) / BN;
+    int tmi, tni;
+    if (!tile_of_range(g, tn, tmi, tni, blockIdx.x)) return;
+    const int m0 = tmi * BM, n0 = tni * BN;
+    const int nk = (g.K + BK - 1) / BK;
+    const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
+    const int l32 = lane & 31, lh = lane >> 5;
+    floatx16 acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+    const unsigned ea = (unsigned)((long)(g.M - 1) * g.lda + g.K) * 4u;
+    const unsigned eb = (unsigned)((long)(g.N - 1) * g.ldb + g.K) * 4u;
+    const int32x4_t ra = buffer_rsrc(g.A, ea), rb = buffer_rsrc(g.B, eb);
+    const int sa0 = dma_src<false>(2 * wave, lane, m0, g.lda), sa1 = dma_src<false>(2 * wave + 1, lane, m0, g.lda);
+    const int sb0 = dma_src<false>(2 * wave, lane, n0, g.ldb), sb1 = dma_src<false>(2 * wave + 1, lane, n0, g.ldb);
+#define PT_ISSUE32(tile)                                                                \
+    {                                                                                   \
+        const int k0_ = (tile) * BK;                                                    \
+        const float* st_ = smem + ((tile) % NS) * 2 * TILE;                             \
+        dma16(ra, st_ + (2 * wave) * 256, (sa0 + k0_) * 4);                             \
+        dma16(ra, st_ + (2 * wave + 1) * 256, (sa1 + k0_) * 4);                         \
+        dma16(rb, st_ + TILE + (2 * wave) * 256, (sb0 + k0_) * 4);                      \
+        dma16(rb, st_ + TILE + (2 * wave + 1) * 256, (sb1 + k0_) * 4);                  \
+    }
+    if (nk > 0) {
+#pragma unroll
+        for (int t = 0; t < NS - 1; ++t)
+            if (t < nk) PT_ISSUE32(t)
+        for (int it = 0; it < nk; ++it) {
+            wait_stages<NS>(min(NS - 2, nk - 1 - it));
+            __syncthreads();   // every wave's loads of stage it are in LDS; stage it - 1 is consumed
+            const int kv = g.K - it * BK;   // floats of this stage inside K
+            if (kv < BK) {
+                float* st = smem + (it % NS) * 2 * TILE;
+                for (int idx = tid; idx < BM * BK; idx += NT) {
+                    const int r = idx / BK, k = idx % BK;
+                    if (k >= kv) {
+                        st[dma_at<false>(r, k)] = 0.f;
+                        st[TILE + dma_at<false>(r, k)] = 0.f;
+                    }
+                }
+                __syncthreads();
+            }
+            if (it + NS - 1 < nk) PT_ISSUE32(it + NS - 1)
+            const float* Ab = smem + (it % NS) * 2 * TILE;
+            const float* Bb = Ab + TILE;
+#pragma unroll
+            for (int st = 0; st < 2; ++st) {
+                bf16x8 ah[2], bh[2];
+#pragma unroll
+                for (int t = 0; t < 2; ++t) {
+                    ah[t] = *reinterpret_cast<const bf16x8*>(Ab + dma_at<false>(wm + 32 * t + l32, 4 * (2 * st + lh)));
+                    bh[t] = *reinterpret_cast<const bf16x8*>(Bb + dma_at<false>(wn + 32 * t + l32, 4 * (2 * st + lh)));
+                }
+#pragma unroll
+                for (int ti = 0; ti < 2; ++ti)
+#pragma unroll
+                    for (int tj = 0; tj < 2; ++tj)
+                        acc[ti][tj] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bh[tj], ah[ti], acc[ti][tj], 0, 0, 0);
+            }
+        }
+    }
+#undef PT_ISSUE32
+    const uintptr_t al = (uintptr_t)g.C | (uintptr_t)g.C2 | (uintptr_t)g.R | (uintptr_t)g.bias |
+                         (uintptr_t)((g.ldc | g.ldc2 | g.ldr) * 4);
+    epilogue_staged32<EPI, OB>(g, acc, m0, n0, wm, wn, l32, lh, smem, (al & 15) == 0);
 }
 
 // gemm_bs_dw_kernel: weight gradients dW (M, N) = sum_k A[k][m] B[k][n] with
@@ -1292,7 +1383,7 @@ static bool al16(const void* p) { return ((uintptr_t)p & 15) == 0; }
 
 template <int EPI, bool OB>
 static void launch_bs(const GemmArgs& f, dim3 grid, hipStream_t s) {
-    hipLaunchKernelGGL((gemm_bs_kernel<EPI, OB, BS_NS>), grid, dim3(NT), 0, s, f);
+    hipLaunchKernelGGL((gemm_bs32_kernel<EPI, OB, BS_NS>), grid, dim3(NT), 0, s, f);
 }
 
 static int gemm_bs_nt(const GemmArgs& g, hipStream_t s) {

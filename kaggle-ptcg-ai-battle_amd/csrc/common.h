@@ -79,6 +79,26 @@ __device__ __forceinline__ void pt_gelu_both(float x, float& g, float& gd) {
     gd = cdf + x * pdf;
 }
 
+// GELU and its derivative for bf16 outputs (the mixed-precision variant's
+// stored activations), branch-free: erf by Abramowitz & Stegun, Handbook of
+// Mathematical Functions, formula 7.1.26 (|error| <= 1.5e-7 on [0, inf)),
+// 1 - erf(x) = t (a1 + t (a2 + t (a3 + t (a4 + t a5)))) e^(-x^2),
+// t = 1 / (1 + p x), x = |z| / sqrt 2, whose e^(-x^2) = e^(-z^2/2) is also the
+// normal density's exponential in gelu'(z) = Phi(z) + z phi(z).  The error is
+// far below the 2^-9 rounding of the stored bf16 value; the fp32 path keeps
+// pt_gelu_both (libm erf).
+__device__ __forceinline__ void pt_gelu_both_bf(float z, float& g, float& gd) {
+    const float x = fabsf(z) * 0.70710678118654752f;
+    const float t = 1.0f / (1.0f + 0.3275911f * x);
+    const float poly =
+        t * (0.254829592f + t * (-0.284496736f + t * (1.421413741f + t * (-1.453152027f + t * 1.061405429f))));
+    const float e = __expf(-x * x);
+    const float q = poly * e;   // 1 - erf(|z| / sqrt 2)
+    const float cdf = z >= 0.f ? 1.0f - 0.5f * q : 0.5f * q;
+    g = z * cdf;
+    gd = cdf + z * (0.3989422804014327f * e);
+}
+
 // Philox4x32-10 (Salmon, Moraes, Dror, Shaw, "Parallel random numbers: as
 // easy as 1, 2, 3", SC'11), restated from the paper: 10 rounds of
 // (hi, lo) = mulhilo(M, c), Weyl key bumps.  Counter-based: every (key,

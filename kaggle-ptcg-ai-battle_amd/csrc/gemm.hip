@@ -96,7 +96,7 @@ __device__ __forceinline__ void epi_store_bf(const GemmArgs& g, int m, int n, fl
         st_b1(g.C, c, v + g.bias[n]);
     } else if (EPI == EPI_BIAS_GELU_D) {
         float gv, gd;
-        pt_gelu_both(v + g.bias[n], gv, gd);
+        pt_gelu_both_bf(v + g.bias[n], gv, gd);
         st_b1(g.C, c, gd);
         st_b1(g.C2, (long)m * g.ldc2 + n, gv);
     } else if (EPI == EPI_MUL) {
@@ -154,13 +154,49 @@ __device__ __forceinline__ void epi_store4_bf(const GemmArgs& g, int m, int n, f
         v += ld_v4(g.bias + n);
         float gv[4], gd[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) pt_gelu_both(v[i], gv[i], gd[i]);
+        for (int i = 0; i < 4; ++i) pt_gelu_both_bf(v[i], gv[i], gd[i]);
         st_b4(g.C, c, floatx4{gd[0], gd[1], gd[2], gd[3]});
         st_b4(g.C2, (long)m * g.ldc2 + n, floatx4{gv[0], gv[1], gv[2], gv[3]});
     } else if (EPI == EPI_MUL) {
         st_b4(g.C, c, v * ld_b4(g.R, (long)m * g.ldr + n));
     } else if (EPI == EPI_BIAS_RESID) {
         st_b4(g.C, c, (v + ld_v4(g.bias + n)) + ld_v4(g.R + (long)m * g.ldr + n));
+    }
+}
+
+// eight consecutive outputs C[m][n..n+7] (16 B bf16 stores; caller checked
+// alignment and n + 7 < N); same arithmetic as epi_store4_bf
+typedef __bf16 bf16x8s __attribute__((ext_vector_type(8)));
+typedef __attribute__((address_space(1))) bf16x8s gbf16x8;
+__device__ __forceinline__ void st_b8(float* base, long i, floatx4 a, floatx4 b) {
+    *(gbf16x8*)(bfp(base) + i) = bf16x8s{(__bf16)a[0], (__bf16)a[1], (__bf16)a[2], (__bf16)a[3],
+                                         (__bf16)b[0], (__bf16)b[1], (__bf16)b[2], (__bf16)b[3]};
+}
+template <int EPI>
+__device__ __forceinline__ void epi_store8_bf(const GemmArgs& g, int m, int n, floatx4 v0, floatx4 v1) {
+    const long c = (long)m * g.ldc + n;
+    if (EPI == EPI_STORE) {
+        st_b8(g.C, c, v0, v1);
+    } else if (EPI == EPI_BIAS) {
+        st_b8(g.C, c, v0 + ld_v4(g.bias + n), v1 + ld_v4(g.bias + n + 4));
+    } else if (EPI == EPI_BIAS_GELU_D) {
+        v0 += ld_v4(g.bias + n);
+        v1 += ld_v4(g.bias + n + 4);
+        float gv[8], gd[8];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            pt_gelu_both_bf(v0[i], gv[i], gd[i]);
+            pt_gelu_both_bf(v1[i], gv[4 + i], gd[4 + i]);
+        }
+        st_b8(g.C, c, floatx4{gd[0], gd[1], gd[2], gd[3]}, floatx4{gd[4], gd[5], gd[6], gd[7]});
+        st_b8(g.C2, (long)m * g.ldc2 + n, floatx4{gv[0], gv[1], gv[2], gv[3]}, floatx4{gv[4], gv[5], gv[6], gv[7]});
+    } else if (EPI == EPI_MUL) {
+        const bf16x8s r = *(const gbf16x8*)(bfp(g.R) + (long)m * g.ldr + n);
+        st_b8(g.C, c, v0 * floatx4{(float)r[0], (float)r[1], (float)r[2], (float)r[3]},
+              v1 * floatx4{(float)r[4], (float)r[5], (float)r[6], (float)r[7]});
+    } else if (EPI == EPI_BIAS_RESID) {
+        st_b8(g.C, c, (v0 + ld_v4(g.bias + n)) + ld_v4(g.R + (long)m * g.ldr + n),
+              (v1 + ld_v4(g.bias + n + 4)) + ld_v4(g.R + (long)m * g.ldr + n + 4));
     }
 }
 
@@ -837,9 +873,11 @@ __global__ __launch_bounds__(NT) void gemm_bf16_k16_kernel(const GemmArgs g0, in
 // kernels' epilogue does (half h = rows wm + 32 h .. + 31 of both wave rows).
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
+// bf16 outputs (OB) are written eight columns per thread (16 B stores) when
+// vo8: bases 16 B aligned and leading dimensions multiples of 8
 template <int EPI, bool OB>
 __device__ __forceinline__ void epilogue_staged32(const GemmArgs& g, floatx16 (&acc)[2][2], int m0, int n0, int wm,
-                                                  int wn, int l32, int lh, float* stage, bool vo) {
+                                                  int wn, int l32, int lh, float* stage, bool vo, bool vo8) {
     const int tid = threadIdx.x;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
@@ -851,6 +889,22 @@ __device__ __forceinline__ void epilogue_staged32(const GemmArgs& g, floatx16 (&
                 *reinterpret_cast<floatx4*>(stage + ((wm >> 6) * 32 + l32) * SST + wn + 32 * tj + 8 * q + 4 * lh) =
                     floatx4{acc[h][tj][4 * q], acc[h][tj][4 * q + 1], acc[h][tj][4 * q + 2], acc[h][tj][4 * q + 3]};
         __syncthreads();
+        if (OB && vo8) {
+            for (int it = tid; it < 64 * (BN / 8); it += NT) {
+                const int lr = it / (BN / 8), c = (it % (BN / 8)) * 8;
+                const int m = m0 + (lr >> 5) * 64 + 32 * h + (lr & 31), n = n0 + c;
+                if (m >= g.M || n >= g.N) continue;
+                const floatx4 v0 = *reinterpret_cast<const floatx4*>(stage + lr * SST + c);
+                const floatx4 v1 = *reinterpret_cast<const floatx4*>(stage + lr * SST + c + 4);
+                if (n + 7 < g.N) {
+                    epi_store8_bf<EPI>(g, m, n, v0, v1);
+                } else {
+                    for (int r = 0; r < 4 && n + r < g.N; ++r) epi_store<EPI, OB>(g, m, n + r, v0[r]);
+                    for (int r = 0; r < 4 && n + 4 + r < g.N; ++r) epi_store<EPI, OB>(g, m, n + 4 + r, v1[r]);
+                }
+            }
+            continue;
+        }
         for (int it = tid; it < 64 * (BN / 4); it += NT) {
             const int lr = it / (BN / 4), c = (it % (BN / 4)) * 4;
             const int m = m0 + (lr >> 5) * 64 + 32 * h + (lr & 31), n = n0 + c;
@@ -941,7 +995,9 @@ __global__ __launch_bounds__(NT) void gemm_bs32_kernel(const GemmArgs g0) {
 #undef PT_ISSUE32
     const uintptr_t al = (uintptr_t)g.C | (uintptr_t)g.C2 | (uintptr_t)g.R | (uintptr_t)g.bias |
                          (uintptr_t)((g.ldc | g.ldc2 | g.ldr) * 4);
-    epilogue_staged32<EPI, OB>(g, acc, m0, n0, wm, wn, l32, lh, smem, (al & 15) == 0);
+    // 16 B bf16 stores: bf16 rows of a multiple of 8 elements (R of EPI_MUL is bf16 too)
+    const uintptr_t al8 = (uintptr_t)g.C | (uintptr_t)g.C2 | (uintptr_t)g.R | (uintptr_t)((g.ldc | g.ldc2 | g.ldr) * 2);
+    epilogue_staged32<EPI, OB>(g, acc, m0, n0, wm, wn, l32, lh, smem, (al & 15) == 0, (al & 15) == 0 && (al8 & 15) == 0);
 }
 
 // gemm_bs_dw_kernel: weight gradients dW (M, N) = sum_k A[k][m] B[k][n] with

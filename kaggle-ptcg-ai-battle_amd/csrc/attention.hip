@@ -65,16 +65,24 @@ __device__ __forceinline__ float4 ld4(const __bf16* p) {
 }
 __device__ __forceinline__ float tof(float v) { return v; }
 __device__ __forceinline__ float tof(__bf16 v) { return (float)v; }
+// LDS operand stores: fp32, or (bf16 products) bf16 — every LDS operand of
+// the bf16 kernels feeds an MFMA that rounds it to bf16 anyway, so storing
+// it rounded gives the same products with half the LDS
+__device__ __forceinline__ void st_lds4(float* p, float4 v) { *reinterpret_cast<float4*>(p) = v; }
+__device__ __forceinline__ void st_lds4(__bf16* p, float4 v) {
+    *reinterpret_cast<bf16x4*>(p) = bf16x4{(__bf16)v.x, (__bf16)v.y, (__bf16)v.z, (__bf16)v.w};
+}
 
 template <int DH, int NT, bool BF, typename T>   // NT = Lp / 16 key (and query) tiles
 __global__ __launch_bounds__(512) void attn_fwd_mfma_kernel(const T* __restrict__ qkv,
         const float* __restrict__ keep, T* __restrict__ ctx, float* __restrict__ lse,
         int Lfix, int H, float scale, const int* __restrict__ coff) {
     constexpr int LP = NT * 16, SK = DH + 4;
+    typedef typename std::conditional<BF, __bf16, float>::type LT;   // LDS operand type
     extern __shared__ float sm[];
-    float* Ks = sm;                 // [LP][SK]
-    float* Vs = Ks + LP * SK;       // [LP][SK]
-    float* kf = Vs + LP * SK;       // [LP]
+    LT* Ks = reinterpret_cast<LT*>(sm);   // [LP][SK]
+    LT* Vs = Ks + LP * SK;                // [LP][SK]
+    float* kf = reinterpret_cast<float*>(Vs + LP * SK);   // [LP]
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int li = lane & 15, lq = lane >> 4;
     const int n = blockIdx.x / H, h = blockIdx.x % H;
@@ -93,8 +101,8 @@ __global__ __launch_bounds__(512) void attn_fwd_mfma_kernel(const T* __restrict_
             k4 = ld4(r + D);
             v4 = ld4(r + 2 * D);
         }
-        *reinterpret_cast<float4*>(&Ks[l * SK + c4]) = k4;
-        *reinterpret_cast<float4*>(&Vs[l * SK + c4]) = v4;
+        st_lds4(&Ks[l * SK + c4], k4);
+        st_lds4(&Vs[l * SK + c4], v4);
     }
     for (int l = tid; l < LP; l += 512) kf[l] = l < L ? (keep[rb + l] != 0.f ? 1.f : 0.f) : -1.f;
     __syncthreads();
@@ -126,7 +134,7 @@ __global__ __launch_bounds__(512) void attn_fwd_mfma_kernel(const T* __restrict_
                         float a[4], b[4];
 #pragma unroll
                         for (int e = 0; e < 4; ++e) {
-                            a[e] = Ks[(16 * (c0 + j) + li) * SK + 4 * (4 * kq + e) + lq];
+                            a[e] = (float)Ks[(16 * (c0 + j) + li) * SK + 4 * (4 * kq + e) + lq];
                             b[e] = qb[4 * kq + e];
                         }
                         sc[j] = mfma4<BF>(a, b, sc[j]);
@@ -179,7 +187,7 @@ __global__ __launch_bounds__(512) void attn_fwd_mfma_kernel(const T* __restrict_
                     for (int dt = 0; dt < DH / 16; ++dt) {
                         float b[4];
 #pragma unroll
-                        for (int r = 0; r < 4; ++r) b[r] = Vs[(16 * (c0 + j) + 4 * lq + r) * SK + li + 16 * dt];
+                        for (int r = 0; r < 4; ++r) b[r] = (float)Vs[(16 * (c0 + j) + 4 * lq + r) * SK + li + 16 * dt];
                         o[dt] = mfma4<BF>(a, b, o[dt]);
                     }
                 }
@@ -211,12 +219,13 @@ __global__ __launch_bounds__(512) void attn_bwd_mfma_kernel(const T* __restrict_
         const float* __restrict__ lse, const T* __restrict__ dctx,
         T* __restrict__ dqkv, int Lfix, int H, float scale, const int* __restrict__ coff) {
     constexpr int LP = NT * 16, SQ = DH + 4, SKB = DH + 16, SS = LP + 4;
+    typedef typename std::conditional<BF, __bf16, float>::type LT;   // LDS operand type
     extern __shared__ float sm[];
-    float* Qs = sm;                 // [LP][SQ]
-    float* dOs = Qs + LP * SQ;      // [LP][SQ]
-    float* Ks = dOs + LP * SQ;      // [LP][SKB]
-    float* dSs = Ks + LP * SKB;     // [LP][SS]  (query-major)
-    float* ls = dSs + LP * SS;      // [LP]
+    LT* Qs = reinterpret_cast<LT*>(sm);   // [LP][SQ]
+    LT* dOs = Qs + LP * SQ;               // [LP][SQ]
+    LT* Ks = dOs + LP * SQ;               // [LP][SKB]
+    LT* dSs = Ks + LP * SKB;              // [LP][SS]  (query-major)
+    float* ls = reinterpret_cast<float*>(dSs + LP * SS);   // [LP]
     float* Dv = ls + LP;            // [LP]
     float* kf = Dv + LP;            // [LP]
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -245,9 +254,9 @@ __global__ __launch_bounds__(512) void attn_bwd_mfma_kernel(const T* __restrict_
             d4 = ld4(dob + (long)l * D + c4);
             o4 = ld4(ob + (long)l * D + c4);
         }
-        *reinterpret_cast<float4*>(&Qs[l * SQ + c4]) = q4;
-        *reinterpret_cast<float4*>(&dOs[l * SQ + c4]) = d4;
-        *reinterpret_cast<float4*>(&Ks[l * SKB + c4]) = k4;
+        st_lds4(&Qs[l * SQ + c4], q4);
+        st_lds4(&dOs[l * SQ + c4], d4);
+        st_lds4(&Ks[l * SKB + c4], k4);
         float part = ((d4.x * o4.x + d4.y * o4.y) + d4.z * o4.z) + d4.w * o4.w;
 #pragma unroll
         for (int o = 1; o < DH / 4; o <<= 1) part += __shfl_xor(part, o, 64);
@@ -284,8 +293,8 @@ __global__ __launch_bounds__(512) void attn_bwd_mfma_kernel(const T* __restrict_
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     const int a_off = (16 * qt + li) * SQ + 4 * (4 * kq + e) + lq;
-                    qa[e] = Qs[a_off];
-                    da[e] = dOs[a_off];
+                    qa[e] = (float)Qs[a_off];
+                    da[e] = (float)dOs[a_off];
                     kb4[e] = kr[4 * kq + e];
                     vb4[e] = vr[4 * kq + e];
                 }
@@ -299,7 +308,7 @@ __global__ __launch_bounds__(512) void attn_bwd_mfma_kernel(const T* __restrict_
                 const int q = 16 * qt + 4 * lq + r;
                 p[r] = kfl > 0.f ? expf(s[r] * scale - ls[q]) : 0.f;
                 ds[r] = p[r] * (dp[r] - Dv[q]);
-                dSs[q * SS + k0 + li] = ds[r] * scale;
+                dSs[q * SS + k0 + li] = (LT)(ds[r] * scale);
             }
 #pragma unroll
             for (int dt = 0; dt < DH / 16; ++dt) {
@@ -307,8 +316,8 @@ __global__ __launch_bounds__(512) void attn_bwd_mfma_kernel(const T* __restrict_
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     const int qrow = 16 * qt + 4 * lq + r;
-                    ob[r] = dOs[qrow * SQ + 16 * dt + li];
-                    qb4[r] = Qs[qrow * SQ + 16 * dt + li];
+                    ob[r] = (float)dOs[qrow * SQ + 16 * dt + li];
+                    qb4[r] = (float)Qs[qrow * SQ + 16 * dt + li];
                 }
                 dv[dt] = mfma4<BF>(p, ob, dv[dt]);
                 dk[dt] = mfma4<BF>(ds, qb4, dk[dt]);
@@ -338,12 +347,12 @@ __global__ __launch_bounds__(512) void attn_bwd_mfma_kernel(const T* __restrict_
         for (int kq = 0; kq < ntl; ++kq) {
             float a[4];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) a[e] = dSs[(16 * qt + li) * SS + 4 * (4 * kq + e) + lq];
+            for (int e = 0; e < 4; ++e) a[e] = (float)dSs[(16 * qt + li) * SS + 4 * (4 * kq + e) + lq];
 #pragma unroll
             for (int dt = 0; dt < DH / 16; ++dt) {
                 float b[4];
 #pragma unroll
-                for (int e = 0; e < 4; ++e) b[e] = Ks[(4 * (4 * kq + e) + lq) * SKB + li + 16 * dt];
+                for (int e = 0; e < 4; ++e) b[e] = (float)Ks[(4 * (4 * kq + e) + lq) * SKB + li + 16 * dt];
                 dq[dt] = mfma4<BF>(a, b, dq[dt]);
             }
         }
@@ -605,12 +614,14 @@ int launch_bwd_split(const float* qkv, const float* keep, const float* ctx, cons
     return PTCG_OK;
 }
 
-size_t fwd_mfma_lds_bytes(int LP, int DH) {
-    return sizeof(float) * ((size_t)LP * (DH + 4) * 2 + (size_t)LP);
+// es: bytes per LDS operand element (4, or 2 for the bf16-product kernels)
+size_t fwd_mfma_lds_bytes(int LP, int DH, size_t es = 4) {
+    return es * (size_t)LP * (DH + 4) * 2 + sizeof(float) * (size_t)LP;
 }
 
-size_t bwd_mfma_lds_bytes(int LP, int DH) {
-    return sizeof(float) * ((size_t)LP * (DH + 4) * 2 + (size_t)LP * (DH + 16) + (size_t)LP * (LP + 4) + 3 * (size_t)LP);
+size_t bwd_mfma_lds_bytes(int LP, int DH, size_t es = 4) {
+    return es * ((size_t)LP * (DH + 4) * 2 + (size_t)LP * (DH + 16) + (size_t)LP * (LP + 4)) +
+           sizeof(float) * 3 * (size_t)LP;
 }
 
 // BF: bf16 products; IO16 (with BF): qkv / ctx / dctx / dqkv stored in bf16
@@ -618,7 +629,7 @@ template <int DH, int NT, bool BF, bool IO16>
 int launch_fwd_mfma(const float* qkv, const float* keep, float* ctx, float* lse, int N, int L, int H,
                     hipStream_t s, const int* coff) {
     typedef typename std::conditional<IO16, __bf16, float>::type T;
-    const size_t lds = fwd_mfma_lds_bytes(NT * 16, DH);
+    const size_t lds = fwd_mfma_lds_bytes(NT * 16, DH, BF ? 2 : 4);
     PT_HIP(hipFuncSetAttribute((const void*)attn_fwd_mfma_kernel<DH, NT, BF, T>,
                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
     hipLaunchKernelGGL((attn_fwd_mfma_kernel<DH, NT, BF, T>), dim3(N * H), dim3(512), lds, s,
@@ -632,7 +643,7 @@ template <int DH, int NT, bool BF, bool IO16>
 int launch_bwd_mfma(const float* qkv, const float* keep, const float* ctx, const float* lse,
                     const float* dctx, float* dqkv, int N, int L, int H, hipStream_t s, const int* coff) {
     typedef typename std::conditional<IO16, __bf16, float>::type T;
-    const size_t lds = bwd_mfma_lds_bytes(NT * 16, DH);
+    const size_t lds = bwd_mfma_lds_bytes(NT * 16, DH, BF ? 2 : 4);
     PT_HIP(hipFuncSetAttribute((const void*)attn_bwd_mfma_kernel<DH, NT, BF, T>,
                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
     hipLaunchKernelGGL((attn_bwd_mfma_kernel<DH, NT, BF, T>), dim3(N * H), dim3(512), lds, s,

@@ -22,22 +22,26 @@ pytestmark = pytest.mark.gpu
 HYP = dict(clip_coef=0.2, vf_clip_coef=0.2, vf_coef=0.5, ent_coef=0.01, max_grad_norm=0.5)
 
 
-def _make(dm, B, seed, static):
+def _make(dm, B, seed, static, precision="fp32"):
     st = synth.make_static(dm, seed + 1000) if static else None
     ref = om.build(dm, seed=seed, static=st)
-    cfg = {"dims": dm, "init_weights": ref.to_blob(), "train": dict(minibatch_size=B, **HYP)}
+    cfg = {"dims": dm, "init_weights": ref.to_blob(), "precision": precision,
+           "train": dict(minibatch_size=B, **HYP)}
     if static:
         cfg["static"] = st
     return trainer.create_pufferl(cfg)
 
 
-CASES = [(dims.tiny(), 32, False), (dims.CORE, 64, False), (dims.tiny_frozen(), 24, True),
-         (dims.FROZEN, 8, True)]
+CASES = [(dims.tiny(), 32, False, "fp32"), (dims.CORE, 64, False, "fp32"), (dims.tiny_frozen(), 24, True, "fp32"),
+         (dims.FROZEN, 8, True, "fp32"), (dims.CORE, 64, False, "bf16"), (dims.tiny_frozen(), 24, True, "bf16")]
 
 
-@pytest.mark.parametrize("dm,B,static", CASES, ids=["tiny", "core", "tiny_frozen", "frozen"])
-def test_backward_bitwise_repeatable(dm, B, static, cuda):
-    pl = _make(dm, B, seed=71, static=static)
+@pytest.mark.parametrize("dm,B,static,precision", CASES,
+                         ids=["tiny", "core", "tiny_frozen", "frozen", "core_bf16", "tiny_frozen_bf16"])
+def test_backward_bitwise_repeatable(dm, B, static, precision, cuda):
+    """fp32, and the bf16 variant (bf16 activations, split-K weight gradients
+    with fixed-order sums, the same fixed-point table sums)."""
+    pl = _make(dm, B, seed=71, static=static, precision=precision)
     try:
         R = 3 * B
         rows = synth.make_obs(dm, R, seed=72, rich=True)

@@ -54,6 +54,39 @@ def test_graph_replays_match_eager_steps(dm, opt, cuda):
         graph.close()
 
 
+def test_graph_replays_match_eager_bf16(cuda):
+    """The bf16 variant captured and replayed: the bf16 weight copies are
+    refreshed inside the captured forward, so every replay trains on the
+    weights the previous step wrote and equals the eager bf16 step bit for
+    bit."""
+    dm, B = dims.CORE, 64
+    blob = om.build(dm, seed=91).to_blob()
+    rows = synth.make_obs(dm, 4 * B, seed=92)
+    inp = synth.make_ppo_inputs(dm, rows, seed=93)
+    lists = synth.minibatch_indices(4 * B, B, 4, seed=94, epochs=1)
+    cfg = {"dims": dm, "init_weights": blob, "sync_free": True, "precision": "bf16",
+           "train": dict(minibatch_size=B, learning_rate=1e-3, max_grad_norm=0.5)}
+    eager, graph = trainer.create_pufferl(cfg), trainer.create_pufferl(cfg)
+    try:
+        trainer.set_rollout(eager, rows, **inp)
+        trainer.set_rollout(graph, rows, **inp)
+        idx_buf = torch.from_numpy(np.asarray(lists[0], np.int32)).to("cuda")
+        torch.cuda.synchronize()
+        graph.capture_step(graph.rollout["obs"], idx_buf, graph.rollout)
+        for i, ix in enumerate(lists):
+            ix = np.asarray(ix, np.int32)
+            idx_buf.copy_(torch.from_numpy(ix).to("cuda"))
+            graph.replay_step()
+            eager.step(eager.rollout["obs"], eager.to_device(ix, np.int32), eager.rollout)
+            torch.cuda.synchronize()
+            w_e, w_g = eager.get_weights(), graph.get_weights()
+            assert np.array_equal(w_g, w_e), (i, rel_l2(w_g, w_e))
+            assert not np.array_equal(w_g, blob)
+    finally:
+        eager.close()
+        graph.close()
+
+
 def test_capture_needs_sync_free(cuda):
     dm, B = dims.tiny(), 32
     pl = trainer.create_pufferl({"dims": dm, "train": dict(minibatch_size=B)})

@@ -121,6 +121,17 @@ struct PtcgModel {
     std::vector<BlockW> bw;
     BlockW cbw{};
     float *dAh = nullptr, *dCh = nullptr;
+    // the blocks' weight gradients run on a side stream (wg_s) concurrently
+    // with the backward's critical path (dX, LayerNorm, attention); wg_ev[0]
+    // forks the side stream off the main one, wg_ev[1..4] mark the side
+    // stream's FFN2 / FFN1 / out-projection / QKV weight gradient of the
+    // latest block done (wg_rec: recorded in this backward); ws2 is the side
+    // stream's split-K workspace
+    hipStream_t wg_s = nullptr;
+    hipEvent_t wg_ev[5] = {};
+    bool wg_rec[5] = {};
+    float* ws2 = nullptr;
+    long ws2_floats = 0;
     float *d_hand, *d_prize, *d_blind, *dxc, *dxc2, *dotok, *dotok_in, *dov1, *dovin;
     int* aux_cnt;
     // order-independent table scatters: fixed-point accumulators (zero
@@ -175,8 +186,9 @@ static int ldx_(const PtcgModel* m, const float* dY, long lddy, const float* W, 
     return ldxw_(m, dY, lddy, W, in, dX, lddx, rows, in, out, epi, R, ldr, s, Mdev);
 }
 // dW = dY^T X (overwrite), db = colsum dY (fused into the product)
+// (side = true: on the side stream's workspace)
 static int ldw_(PtcgModel* m, const float* dY, long lddy, const float* X, long ldxx, float* dW,
-                float* db, int rows, int in, int out, hipStream_t s, const int* Kdev = nullptr) {
+                float* db, int rows, int in, int out, hipStream_t s, const int* Kdev = nullptr, bool side = false) {
     GemmArgs g{};
     g.Kdev = Kdev;
     g.M = out; g.N = in; g.K = rows;
@@ -186,7 +198,7 @@ static int ldw_(PtcgModel* m, const float* dY, long lddy, const float* X, long l
     g.epi = EPI_STORE;
     g.dbias = db;
     g.prec = m->prec;
-    return pt_gemm(g, m->ws, m->ws_floats, s);
+    return pt_gemm(g, side ? m->ws2 : m->ws, side ? m->ws2_floats : m->ws_floats, s);
 }
 
 // bf16-operand products (GemmArgs::bs) of the bf16 variant's blocks:
@@ -207,6 +219,7 @@ static int blin(const PtcgModel* m, const float* X, int in, const __bf16* Wb, co
     return pt_gemm(g, m->ws, m->ws_floats, s);
 }
 // dW (out, in) = dY^T X, db = column sums of dY, with dY (rows, out) and X (rows, in) bf16
+// (on the side stream's workspace)
 static int bldw(PtcgModel* m, const float* dY, int out, const float* X, int in, float* dW, float* db, int rows,
                 hipStream_t s, const int* Kdev) {
     GemmArgs g{};
@@ -217,7 +230,25 @@ static int bldw(PtcgModel* m, const float* dY, int out, const float* X, int in, 
     g.B = X; g.ldb = in; g.b_t = 1;
     g.C = dW; g.ldc = in; g.epi = EPI_STORE;
     g.dbias = db;
-    return pt_gemm(g, m->ws, m->ws_floats, s);
+    return pt_gemm(g, m->ws2, m->ws2_floats, s);
+}
+
+// side-stream ordering: fork = the side stream waits for the main stream's
+// work so far; done(e) = mark the side stream's work so far as event e;
+// after(e) = the main stream waits for event e (if this backward recorded it)
+static int wg_fork(PtcgModel* m, hipStream_t s) {
+    PT_HIP(hipEventRecord(m->wg_ev[0], s));
+    PT_HIP(hipStreamWaitEvent(m->wg_s, m->wg_ev[0], 0));
+    return PTCG_OK;
+}
+static int wg_done(PtcgModel* m, int e) {
+    PT_HIP(hipEventRecord(m->wg_ev[e], m->wg_s));
+    m->wg_rec[e] = true;
+    return PTCG_OK;
+}
+static int wg_after(PtcgModel* m, int e, hipStream_t s) {
+    if (m->wg_rec[e]) PT_HIP(hipStreamWaitEvent(s, m->wg_ev[e], 0));
+    return PTCG_OK;
 }
 
 // refresh the blocks' bf16 weight copies from the fp32 masters
@@ -564,6 +595,8 @@ static size_t carve(PtcgModel* m, char* base) {
     long ln_part = 4096L * (D > x.card_in ? D : x.card_in);   // LayerNorm dW/dB partials (layernorm.hip)
     if (ln_part > m->ws_floats) m->ws_floats = ln_part;
     m->ws = c.take(m->ws_floats);
+    m->ws2_floats = 16L << 20;   // the side stream's weight-gradient split-K partials
+    m->ws2 = c.take(m->ws2_floats);
     return c.off;
 }
 
@@ -577,6 +610,10 @@ static int reg(PtcgModel* m, int n, bool train) {
     m->train = train;
     m->compact = m->dm.critic == 0;
     m->det = DetCtx{};
+    if (train && !m->wg_s) {
+        PT_HIP(hipStreamCreateWithFlags(&m->wg_s, hipStreamNonBlocking));
+        for (auto& e : m->wg_ev) PT_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
+    }
     size_t bytes = carve(m, nullptr);
     PT_HIP(hipMalloc(&m->mem, bytes));
     m->mem_bytes = bytes;
@@ -610,6 +647,12 @@ extern "C" int ptcg_model_reg_rollout(PtcgModel* m, int n) {
 
 extern "C" void ptcg_model_free(PtcgModel* m) {
     if (!m) return;
+    if (m->wg_s) {
+        (void)hipStreamSynchronize(m->wg_s);
+        for (auto e : m->wg_ev)
+            if (e) (void)hipEventDestroy(e);
+        (void)hipStreamDestroy(m->wg_s);
+    }
     if (m->mem) (void)hipFree(m->mem);
     if (m->tmem) (void)hipFree(m->tmem);
     if (m->rows_h) (void)hipHostFree(m->rows_h);
@@ -803,34 +846,64 @@ static int block_bwd(PtcgModel* m, const BlockP& w, const BlockA& a, int L, cons
                      const int* coff = nullptr, const BlockW* bw = nullptr) {
     const PtcgDims& d = m->dm;
     const int NL = rows ? rows : m->N * L, D = d.d;
+    // Weight gradients on the side stream (m->wg_s), each forked once its dY
+    // is written; the main stream waits for the side stream only before it
+    // overwrites a buffer a pending weight gradient reads: dffn (the previous
+    // block's FFN1 dW), dC (its out-projection dW), dqkv (its QKV dW) and dA
+    // (this block's FFN2 dW).
+    hipStream_t s2 = m->wg_s;
     if (bw) {
-        PT_TRY(bldw(m, m->dAh, D, a.ffa, d.ffn, m->G(w.f2w), m->G(w.f2b), NL, s, Tr));
+        PT_TRY(wg_fork(m, s));
+        PT_TRY(bldw(m, m->dAh, D, a.ffa, d.ffn, m->G(w.f2w), m->G(w.f2b), NL, s2, Tr));
+        PT_TRY(wg_done(m, 1));
+        PT_TRY(wg_after(m, 2, s));
         PT_TRY(blin(m, m->dAh, D, bw->f2T, nullptr, m->dffn, d.ffn, NL, EPI_MUL, true, a.ffp, nullptr, s, Tr));
-        PT_TRY(bldw(m, m->dffn, d.ffn, a.ln2, D, m->G(w.f1w), m->G(w.f1b), NL, s, Tr));
+        PT_TRY(wg_fork(m, s));
+        PT_TRY(bldw(m, m->dffn, d.ffn, a.ln2, D, m->G(w.f1w), m->G(w.f1b), NL, s2, Tr));
+        PT_TRY(wg_done(m, 2));
         PT_TRY(blin(m, m->dffn, d.ffn, bw->f1T, nullptr, m->dln, D, NL, EPI_STORE, false, nullptr, nullptr, s, Tr));
+        PT_TRY(wg_after(m, 3, s));
         PT_TRY(pt_ln_bwd(m->dln, D, a.xmid, D, w.ln2w, a.mu2, a.rs2, dA, D, dC, D, m->G(w.ln2w),
                          m->G(w.ln2b), NL, D, m->ws, m->ws_floats, s, Tr, m->dCh));
-        PT_TRY(bldw(m, m->dCh, D, a.ctx, D, m->G(w.projw), m->G(w.projb), NL, s, Tr));
+        PT_TRY(wg_fork(m, s));
+        PT_TRY(bldw(m, m->dCh, D, a.ctx, D, m->G(w.projw), m->G(w.projb), NL, s2, Tr));
+        PT_TRY(wg_done(m, 3));
         PT_TRY(blin(m, m->dCh, D, bw->projT, nullptr, m->dctx, D, NL, EPI_STORE, true, nullptr, nullptr, s, Tr));
+        PT_TRY(wg_after(m, 4, s));
         PT_TRY(pt_attn_bwd(a.qkv, keep, a.ctx, a.lse, m->dctx, m->dqkv, m->N, L, d.heads, m->dx.dh, s, coff, 2));
-        PT_TRY(bldw(m, m->dqkv, 3 * D, a.ln1, D, m->G(w.qkvw), m->G(w.qkvb), NL, s, Tr));
+        PT_TRY(wg_fork(m, s));
+        PT_TRY(bldw(m, m->dqkv, 3 * D, a.ln1, D, m->G(w.qkvw), m->G(w.qkvb), NL, s2, Tr));
+        PT_TRY(wg_done(m, 4));
         PT_TRY(blin(m, m->dqkv, 3 * D, bw->qkvT, nullptr, m->dln, D, NL, EPI_STORE, false, nullptr, nullptr, s,
                     Tr));
+        PT_TRY(wg_after(m, 1, s));
         PT_TRY(pt_ln_bwd(m->dln, D, xin, D, w.ln1w, a.mu1, a.rs1, dC, D, dA, D, m->G(w.ln1w),
                          m->G(w.ln1b), NL, D, m->ws, m->ws_floats, s, Tr, m->dAh));
         return PTCG_OK;
     }
-    PT_TRY(ldw_(m, dA, D, a.ffa, d.ffn, m->G(w.f2w), m->G(w.f2b), NL, d.ffn, D, s, Tr));
+    PT_TRY(wg_fork(m, s));
+    PT_TRY(ldw_(m, dA, D, a.ffa, d.ffn, m->G(w.f2w), m->G(w.f2b), NL, d.ffn, D, s2, Tr, true));
+    PT_TRY(wg_done(m, 1));
+    PT_TRY(wg_after(m, 2, s));
     PT_TRY(ldx_(m, dA, D, w.f2w, m->dffn, d.ffn, NL, d.ffn, D, EPI_MUL, a.ffp, d.ffn, s, Tr));
-    PT_TRY(ldw_(m, m->dffn, d.ffn, a.ln2, D, m->G(w.f1w), m->G(w.f1b), NL, D, d.ffn, s, Tr));
+    PT_TRY(wg_fork(m, s));
+    PT_TRY(ldw_(m, m->dffn, d.ffn, a.ln2, D, m->G(w.f1w), m->G(w.f1b), NL, D, d.ffn, s2, Tr, true));
+    PT_TRY(wg_done(m, 2));
     PT_TRY(ldx_(m, m->dffn, d.ffn, w.f1w, m->dln, D, NL, D, d.ffn, EPI_STORE, nullptr, 0, s, Tr));
+    PT_TRY(wg_after(m, 3, s));
     PT_TRY(pt_ln_bwd(m->dln, D, a.xmid, D, w.ln2w, a.mu2, a.rs2, dA, D, dC, D, m->G(w.ln2w),
                      m->G(w.ln2b), NL, D, m->ws, m->ws_floats, s, Tr));
-    PT_TRY(ldw_(m, dC, D, a.ctx, D, m->G(w.projw), m->G(w.projb), NL, D, D, s, Tr));
+    PT_TRY(wg_fork(m, s));
+    PT_TRY(ldw_(m, dC, D, a.ctx, D, m->G(w.projw), m->G(w.projb), NL, D, D, s2, Tr, true));
+    PT_TRY(wg_done(m, 3));
     PT_TRY(ldx_(m, dC, D, w.projw, m->dctx, D, NL, D, D, EPI_STORE, nullptr, 0, s, Tr));
+    PT_TRY(wg_after(m, 4, s));
     PT_TRY(pt_attn_bwd(a.qkv, keep, a.ctx, a.lse, m->dctx, m->dqkv, m->N, L, d.heads, m->dx.dh, s, coff, m->prec));
-    PT_TRY(ldw_(m, m->dqkv, 3 * D, a.ln1, D, m->G(w.qkvw), m->G(w.qkvb), NL, D, 3 * D, s, Tr));
+    PT_TRY(wg_fork(m, s));
+    PT_TRY(ldw_(m, m->dqkv, 3 * D, a.ln1, D, m->G(w.qkvw), m->G(w.qkvb), NL, D, 3 * D, s2, Tr, true));
+    PT_TRY(wg_done(m, 4));
     PT_TRY(ldx_(m, m->dqkv, 3 * D, w.qkvw, m->dln, D, NL, D, 3 * D, EPI_STORE, nullptr, 0, s, Tr));
+    PT_TRY(wg_after(m, 1, s));
     PT_TRY(pt_ln_bwd(m->dln, D, xin, D, w.ln1w, a.mu1, a.rs1, dC, D, dA, D, m->G(w.ln1w),
                      m->G(w.ln1b), NL, D, m->ws, m->ws_floats, s, Tr));
     return PTCG_OK;
@@ -911,6 +984,7 @@ static int critic_bwd(PtcgModel* m, const GatherCtx& c, const float* grad, hipSt
     if (b16) PT_TRY(pt_to_bf16(m->dxc, m->dAh, (long)N * x.l_crit * D, s));
     PT_TRY(block_bwd(m, m->cblk, m->cba, x.l_crit, m->ckeep, m->xc, m->dxc, m->dxc2, s, 0, nullptr, nullptr,
                      b16 ? &m->cbw : nullptr));
+    PT_TRY(wg_after(m, 4, s));   // the critic block's weight gradients are done
     PT_TRY(pt_colsum(m->dxc, (long)x.l_crit * D, N, D, m->G(m->cread), m->ws, m->ws_floats, s));
     PT_TRY(pt_xc_bwd(m->dxc, m->dxa, m->dotok, N, x.l_seq, x.n_orc, D, s));
     PT_TRY(ldw_(m, m->dotok, D, m->otok_in, x.orc_in, m->G(m->op_w), m->G(m->op_b), NK, x.orc_in, D, s));
@@ -928,6 +1002,7 @@ extern "C" int ptcg_model_backward(PtcgModel* m, const float* grad, void* stream
     PT_REQUIRE(m && grad && m->mem && m->obs, "model_backward: run a forward first");
     PT_REQUIRE(m->train, "model_backward: activations were registered for rollout (ptcg_model_reg_train)");
     hipStream_t s = (hipStream_t)stream;
+    for (bool& r : m->wg_rec) r = false;   // side-stream events of an earlier backward are not waited for
     const PtcgDims& d = m->dm;
     const DimsX& x = m->dx;
     const int N = m->N, Lt = d.l_tok, NO = d.n_opt, D = d.d, G = d.g;
@@ -1017,6 +1092,7 @@ extern "C" int ptcg_model_backward(PtcgModel* m, const float* grad, void* stream
     for (int i = d.layers - 1; i >= 0; --i)
         PT_TRY(block_bwd(m, m->blk[i], m->ba[i], x.l_seq, m->keep, m->x[i], m->dxb, m->dxa, s, rows, Td, coff,
                          b16 ? &m->bw[i] : nullptr));
+    PT_TRY(wg_after(m, 4, s));   // join: every block's weight gradients are done
 
     // trunk input: readout / token projection / broadcast
     PT_TRY(pt_x0_bwd(c, m->dxb, m->dtokp, m->dbc, s));

@@ -365,7 +365,9 @@ def main():
     # timed region 2 (the only one with --stream): the same number of
     # minibatches launched kernel by kernel, a HIP event pair on the launch
     # stream around every GEMM, LayerNorm and Adam launch -- the kernels'
-    # rooflines.  Host row counts here, so every launch is sized exactly and
+    # rooflines.  While the profile is open the blocks' weight gradients stay
+    # on the launch stream (no side stream), so no timed launch shares the
+    # GPU with another.  Host row counts here, so every launch is sized exactly and
     # its algorithmic amount is the work it does (a sync-free launch covers
     # all N * l_seq rows and stops at the device count).
     if graph and not args.sync_free:
@@ -463,8 +465,9 @@ def main():
     if graph:
         line["stream_launch"] = dict(value=round(B * K / sec_stream, 2), ms_per_step=round(sec_stream * 1e3 / K, 4),
                                      note="as many minibatches launched kernel by kernel (host row counts, exact "
-                                          "launch sizes) with HIP event pairs; roofline and hbm_kernels come "
-                                          "from this pass")
+                                          "launch sizes) with HIP event pairs, the blocks' weight gradients on "
+                                          "the launch stream so that every timed launch runs alone; roofline "
+                                          "and hbm_kernels come from this pass")
     if muon:
         line["muon"] = muon_stats(L, K)
     if not args.no_cpu_baseline and not bf16:

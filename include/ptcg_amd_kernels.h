@@ -113,6 +113,18 @@ int ptcg_kernel_attention_bwd_bf16(const float* qkv, const float* keep, const fl
                                    const float* lse, const float* dctx, float* dqkv,
                                    int N, int L, int H, int Dh, void* stream);
 
+/* the backward with its L x L dS tiles in a global scratch instead of LDS
+ * (Lp <= 128): LDS holds only Q and dO, so two workgroups share a CU.  The
+ * scratch takes ptcg_kernel_attention_bwd_ws_bytes(N, L, H, Dh, bf16) bytes
+ * (0: the shape takes the recompute pair, which needs none); bf16 selects
+ * the bf16-product kernels of ptcg_kernel_attention_bwd_bf16.  The model's
+ * training backward runs this form.                                      */
+int64_t ptcg_kernel_attention_bwd_ws_bytes(int N, int L, int H, int Dh, int bf16);
+int ptcg_kernel_attention_bwd_ws(const float* qkv, const float* keep, const float* ctx,
+                                 const float* lse, const float* dctx, float* dqkv,
+                                 int N, int L, int H, int Dh, int bf16, void* workspace,
+                                 int64_t workspace_bytes, void* stream);
+
 /* which attention kernels a row length takes: bit 0 forward (MFMA), bit 1
  * backward with the L x L dS tile parked in LDS (Lp <= 128), bit 2 backward
  * recomputing S and dP per query stripe (longer rows); -1 unsupported.     */

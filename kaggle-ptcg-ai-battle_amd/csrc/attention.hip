@@ -211,21 +211,34 @@ __global__ __launch_bounds__(512) void attn_fwd_mfma_kernel(const T* __restrict_
 // Backward.  Pass A walks key stripes: per query tile it recomputes
 // S = Q K^T and dP = dO V^T with keys on lanes, forms P and
 // dS = P (dP - rowsum(dO o O)), accumulates dV += P^T dO and dK += dS^T Q
-// (register-r trick again, now over queries), and parks dS*scale in LDS.
-// Pass B walks query stripes: dQ = dS K from LDS.
-template <int DH, int NT, bool BF, typename T>
+// (register-r trick again, now over queries), and parks dS*scale.
+// Pass B walks query stripes: dQ = dS K.
+// GDS = false: dS is parked in LDS beside Q, dO and K (one workgroup per CU
+// at Lp = 112, Dh 64).  GDS = true: dS goes to this workgroup's own slice of
+// a global scratch (dsg + blockIdx * Lp * Lp, row-major, L2-resident between
+// the passes: the writes and reads of one workgroup run on one CU, ordered
+// by the barrier), and K is staged after pass A into the space Q and dO
+// leave free, so the workgroup holds only Q and dO in LDS (two workgroups
+// per CU: one's staging overlaps the other's products).  Pass B then reads
+// dS rows as 128-bit loads, taking key 16 kq + 4 lq + e for lane group lq,
+// element e (the K operand uses the same key order, SKB = Dh + 4 keeps those
+// LDS reads conflict-free).
+template <int DH, int NT, bool BF, typename T, bool GDS = false>
 __global__ __launch_bounds__(512) void attn_bwd_mfma_kernel(const T* __restrict__ qkv,
         const float* __restrict__ keep, const T* __restrict__ ctx,
         const float* __restrict__ lse, const T* __restrict__ dctx,
-        T* __restrict__ dqkv, int Lfix, int H, float scale, const int* __restrict__ coff) {
-    constexpr int LP = NT * 16, SQ = DH + 4, SKB = DH + 16, SS = LP + 4;
+        T* __restrict__ dqkv, int Lfix, int H, float scale, const int* __restrict__ coff,
+        typename std::conditional<BF, __bf16, float>::type* __restrict__ dsg = nullptr) {
+    constexpr int LP = NT * 16, SQ = DH + 4, SKB = GDS ? DH + 4 : DH + 16, SS = GDS ? LP : LP + 4;
     typedef typename std::conditional<BF, __bf16, float>::type LT;   // LDS operand type
     extern __shared__ float sm[];
     LT* Qs = reinterpret_cast<LT*>(sm);   // [LP][SQ]
     LT* dOs = Qs + LP * SQ;               // [LP][SQ]
-    LT* Ks = dOs + LP * SQ;               // [LP][SKB]
-    LT* dSs = Ks + LP * SKB;              // [LP][SS]  (query-major)
-    float* ls = reinterpret_cast<float*>(dSs + LP * SS);   // [LP]
+    // K [LP][SKB]: after Q and dO (GDS: in Q's space once pass A is done)
+    LT* Ks = GDS ? Qs : dOs + LP * SQ;
+    // dS [LP][SS] (query-major): in LDS after K, or this workgroup's global slice
+    LT* dSs = GDS ? dsg + (size_t)blockIdx.x * (LP * LP) : Ks + LP * SKB;
+    float* ls = reinterpret_cast<float*>(GDS ? dOs + LP * SQ : Ks + LP * SKB + LP * SS);   // [LP]
     float* Dv = ls + LP;            // [LP]
     float* kf = Dv + LP;            // [LP]
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -256,7 +269,7 @@ __global__ __launch_bounds__(512) void attn_bwd_mfma_kernel(const T* __restrict_
         }
         st_lds4(&Qs[l * SQ + c4], q4);
         st_lds4(&dOs[l * SQ + c4], d4);
-        st_lds4(&Ks[l * SKB + c4], k4);
+        if (!GDS) st_lds4(&Ks[l * SKB + c4], k4);
         float part = ((d4.x * o4.x + d4.y * o4.y) + d4.z * o4.z) + d4.w * o4.w;
 #pragma unroll
         for (int o = 1; o < DH / 4; o <<= 1) part += __shfl_xor(part, o, 64);
@@ -338,6 +351,17 @@ __global__ __launch_bounds__(512) void attn_bwd_mfma_kernel(const T* __restrict_
         }
     }
     __syncthreads();
+    if (GDS) {
+        // Q and dO are consumed: stage K into their space (its rows were just
+        // read by pass A, so they come from L2)
+        for (int idx = tid; idx < ntl * 16 * (DH / 4); idx += 512) {
+            const int l = idx / (DH / 4), c4 = (idx % (DH / 4)) * 4;
+            float4 k4 = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (l < L) k4 = ld4(base + (long)l * 3 * D + D + c4);
+            st_lds4(&Ks[l * SKB + c4], k4);
+        }
+        __syncthreads();
+    }
 
     // ---- pass B: query stripes, dQ = (dS*scale) K
     for (int qt = wave; qt < ntl; qt += 8) {
@@ -346,13 +370,22 @@ __global__ __launch_bounds__(512) void attn_bwd_mfma_kernel(const T* __restrict_
         for (int dt = 0; dt < DH / 16; ++dt) dq[dt] = floatx4{0.f, 0.f, 0.f, 0.f};
         for (int kq = 0; kq < ntl; ++kq) {
             float a[4];
+            if constexpr (GDS) {
+                // keys 16 kq + 4 lq + e: one 128-bit (bf16: 64-bit) load of the dS row
+                const float4 a4 = ld4(dSs + (16 * qt + li) * SS + 16 * kq + 4 * lq);
+                a[0] = a4.x; a[1] = a4.y; a[2] = a4.z; a[3] = a4.w;
+            } else {
 #pragma unroll
-            for (int e = 0; e < 4; ++e) a[e] = (float)dSs[(16 * qt + li) * SS + 4 * (4 * kq + e) + lq];
+                for (int e = 0; e < 4; ++e) a[e] = (float)dSs[(16 * qt + li) * SS + 4 * (4 * kq + e) + lq];
+            }
 #pragma unroll
             for (int dt = 0; dt < DH / 16; ++dt) {
                 float b[4];
 #pragma unroll
-                for (int e = 0; e < 4; ++e) b[e] = (float)Ks[(4 * (4 * kq + e) + lq) * SKB + li + 16 * dt];
+                for (int e = 0; e < 4; ++e) {
+                    const int key = GDS ? 16 * kq + 4 * lq + e : 4 * (4 * kq + e) + lq;
+                    b[e] = (float)Ks[key * SKB + li + 16 * dt];
+                }
                 dq[dt] = mfma4<BF>(a, b, dq[dt]);
             }
         }
@@ -639,17 +672,38 @@ int launch_fwd_mfma(const float* qkv, const float* keep, float* ctx, float* lse,
     return PTCG_OK;
 }
 
+// dS in global scratch: LDS holds Q and dO (K later in Q's space)
+size_t bwd_gds_lds_bytes(int LP, int DH, size_t es = 4) {
+    return es * (size_t)LP * (DH + 4) * 2 + sizeof(float) * 3 * (size_t)LP;
+}
+
+// dsg: the global dS scratch (N * H * Lp * Lp operand elements) or null for
+// the variant that parks dS in LDS
 template <int DH, int NT, bool BF, bool IO16>
 int launch_bwd_mfma(const float* qkv, const float* keep, const float* ctx, const float* lse,
-                    const float* dctx, float* dqkv, int N, int L, int H, hipStream_t s, const int* coff) {
+                    const float* dctx, float* dqkv, int N, int L, int H, hipStream_t s, const int* coff,
+                    void* dsg) {
     typedef typename std::conditional<IO16, __bf16, float>::type T;
+    typedef typename std::conditional<BF, __bf16, float>::type LT;
+    const float sc = 1.0f / sqrtf((float)DH);
+    if (dsg) {
+        const size_t lds = bwd_gds_lds_bytes(NT * 16, DH, BF ? 2 : 4);
+        PT_HIP(hipFuncSetAttribute((const void*)attn_bwd_mfma_kernel<DH, NT, BF, T, true>,
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+        hipLaunchKernelGGL((attn_bwd_mfma_kernel<DH, NT, BF, T, true>), dim3(N * H), dim3(512), lds, s,
+                           reinterpret_cast<const T*>(qkv), keep, reinterpret_cast<const T*>(ctx), lse,
+                           reinterpret_cast<const T*>(dctx), reinterpret_cast<T*>(dqkv), L, H, sc, coff,
+                           reinterpret_cast<LT*>(dsg));
+        PT_LAUNCH_CHECK();
+        return PTCG_OK;
+    }
     const size_t lds = bwd_mfma_lds_bytes(NT * 16, DH, BF ? 2 : 4);
     PT_HIP(hipFuncSetAttribute((const void*)attn_bwd_mfma_kernel<DH, NT, BF, T>,
                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
     hipLaunchKernelGGL((attn_bwd_mfma_kernel<DH, NT, BF, T>), dim3(N * H), dim3(512), lds, s,
                        reinterpret_cast<const T*>(qkv), keep, reinterpret_cast<const T*>(ctx), lse,
-                       reinterpret_cast<const T*>(dctx), reinterpret_cast<T*>(dqkv), L, H,
-                       1.0f / sqrtf((float)DH), coff);
+                       reinterpret_cast<const T*>(dctx), reinterpret_cast<T*>(dqkv), L, H, sc, coff,
+                       nullptr);
     PT_LAUNCH_CHECK();
     return PTCG_OK;
 }
@@ -719,11 +773,11 @@ static int attn_fwd_dispatch(const float* qkv, const float* keep, float* ctx, fl
 template <bool BF, bool IO16>
 static int attn_bwd_dispatch(const float* qkv, const float* keep, const float* ctx, const float* lse,
                              const float* dctx, float* dqkv, int N, int L, int H, int DH, hipStream_t s,
-                             const int* coff) {
+                             const int* coff, void* dsg) {
     int nt = bwd_store_tiles(L, DH);
     if (nt) {
-        if (DH == 64) { PT_NT_SWITCH8(64, nt, launch_bwd_mfma, qkv, keep, ctx, lse, dctx, dqkv, N, L, H, s, coff) }
-        else { PT_NT_SWITCH8(32, nt, launch_bwd_mfma, qkv, keep, ctx, lse, dctx, dqkv, N, L, H, s, coff) }
+        if (DH == 64) { PT_NT_SWITCH8(64, nt, launch_bwd_mfma, qkv, keep, ctx, lse, dctx, dqkv, N, L, H, s, coff, dsg) }
+        else { PT_NT_SWITCH8(32, nt, launch_bwd_mfma, qkv, keep, ctx, lse, dctx, dqkv, N, L, H, s, coff, dsg) }
     }
     nt = bwd_split_tiles(L, DH);
     if (nt && DH == 64) {
@@ -744,13 +798,22 @@ int pt_attn_fwd(const float* qkv, const float* keep, float* ctx, float* lse, int
                 : attn_fwd_dispatch<false, false>(qkv, keep, ctx, lse, N, L, H, DH, s, coff);
 }
 
+size_t pt_attn_bwd_ws_bytes(int N, int L, int H, int DH, int prec) {
+    if (!pt_attn_supported(L, DH)) return 0;
+    const int nt = bwd_store_tiles(L, DH);
+    if (!nt) return 0;   // the split pair keeps nothing between its launches
+    return (size_t)N * H * (size_t)(nt * 16) * (nt * 16) * (prec ? 2 : 4);
+}
+
 int pt_attn_bwd(const float* qkv, const float* keep, const float* ctx, const float* lse,
                 const float* dctx, float* dqkv, int N, int L, int H, int DH, hipStream_t s, const int* coff,
-                int prec) {
+                int prec, void* ws, size_t ws_bytes) {
     PT_REQUIRE(pt_attn_supported(L, DH), "attention bwd: L=%d Dh=%d exceeds the fused kernels' LDS budget", L, DH);
-    if (prec == 2) return attn_bwd_dispatch<true, true>(qkv, keep, ctx, lse, dctx, dqkv, N, L, H, DH, s, coff);
-    return prec ? attn_bwd_dispatch<true, false>(qkv, keep, ctx, lse, dctx, dqkv, N, L, H, DH, s, coff)
-                : attn_bwd_dispatch<false, false>(qkv, keep, ctx, lse, dctx, dqkv, N, L, H, DH, s, coff);
+    const size_t need = pt_attn_bwd_ws_bytes(N, L, H, DH, prec);
+    void* dsg = (ws != nullptr && need > 0 && ws_bytes >= need) ? ws : nullptr;
+    if (prec == 2) return attn_bwd_dispatch<true, true>(qkv, keep, ctx, lse, dctx, dqkv, N, L, H, DH, s, coff, dsg);
+    return prec ? attn_bwd_dispatch<true, false>(qkv, keep, ctx, lse, dctx, dqkv, N, L, H, DH, s, coff, dsg)
+                : attn_bwd_dispatch<false, false>(qkv, keep, ctx, lse, dctx, dqkv, N, L, H, DH, s, coff, dsg);
 }
 
 // Which kernels a shape takes (for tests): bit 0 forward, bit 1 backward

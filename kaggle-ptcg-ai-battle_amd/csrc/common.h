@@ -58,6 +58,10 @@ void pt_prof_close(int slot, int cls, double amount, hipStream_t s);
 // class recorded for GEMM launches (PROF_GEMM unless a caller such as the
 // Muon step files its products separately); returns the previous class
 int pt_prof_gemm_class(int cls);
+// true while a launch profile is open: concurrent streams would overlap the
+// timed launches, so callers that fork work onto a second stream keep it on
+// the launch stream instead
+bool pt_prof_active();
 
 // ---------------------------------------------------------------- device math
 // Exact (erf) GELU, torch nn.GELU() default; the reference's pt_gelu_fwd/bwd

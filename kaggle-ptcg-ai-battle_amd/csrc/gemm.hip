@@ -1335,6 +1335,8 @@ int launch_full(const GemmArgs& g, bool db, dim3 grid, int k_chunk, hipStream_t 
 
 }  // namespace
 
+bool pt_prof_active() { return g_prof.on; }
+
 int pt_prof_gemm_class(int cls) {
     const int prev = g_gemm_class;
     g_gemm_class = cls;

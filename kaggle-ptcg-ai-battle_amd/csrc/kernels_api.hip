@@ -153,6 +153,23 @@ extern "C" int ptcg_kernel_attention_bwd_bf16(const float* qkv, const float* kee
     return pt_attn_bwd(qkv, keep, ctx, lse, dctx, dqkv, N, L, H, Dh, (hipStream_t)stream, nullptr, 1);
 }
 
+extern "C" int64_t ptcg_kernel_attention_bwd_ws_bytes(int N, int L, int H, int Dh, int bf16) {
+    return (int64_t)pt_attn_bwd_ws_bytes(N, L, H, Dh, bf16 ? 1 : 0);
+}
+
+extern "C" int ptcg_kernel_attention_bwd_ws(const float* qkv, const float* keep, const float* ctx,
+                                            const float* lse, const float* dctx, float* dqkv, int N, int L,
+                                            int H, int Dh, int bf16, void* workspace, int64_t workspace_bytes,
+                                            void* stream) {
+    PT_REQUIRE(qkv && keep && ctx && lse && dctx && dqkv, "kernel_attention_bwd_ws: null buffer");
+    const size_t need = pt_attn_bwd_ws_bytes(N, L, H, Dh, bf16 ? 1 : 0);
+    PT_REQUIRE(need > 0, "kernel_attention_bwd_ws: L=%d Dh=%d takes the recompute pair (no dS scratch)", L, Dh);
+    PT_REQUIRE(workspace && workspace_bytes >= (int64_t)need,
+               "kernel_attention_bwd_ws: workspace of %lld bytes, need %zu", (long long)workspace_bytes, need);
+    return pt_attn_bwd(qkv, keep, ctx, lse, dctx, dqkv, N, L, H, Dh, (hipStream_t)stream, nullptr, bf16 ? 1 : 0,
+                       workspace, (size_t)workspace_bytes);
+}
+
 int pt_attn_path(int L, int DH);
 extern "C" int ptcg_kernel_attention_path(int L, int Dh) { return pt_attn_path(L, Dh); }
 

@@ -53,9 +53,12 @@ int pt_attn_supported(int L, int DH);
 // same with qkv, ctx, dctx and dqkv stored in bf16 (pointers reinterpreted).
 int pt_attn_fwd(const float* qkv, const float* keep, float* ctx, float* lse, int N, int L, int H,
                 int DH, hipStream_t s, const int* coff = nullptr, int prec = 0);
+// ws (optional, at least pt_attn_bwd_ws_bytes): global scratch for the
+// backward's dS, so that two workgroups fit a CU; without it dS stays in LDS
 int pt_attn_bwd(const float* qkv, const float* keep, const float* ctx, const float* lse,
                 const float* dctx, float* dqkv, int N, int L, int H, int DH, hipStream_t s,
-                const int* coff = nullptr, int prec = 0);
+                const int* coff = nullptr, int prec = 0, void* ws = nullptr, size_t ws_bytes = 0);
+size_t pt_attn_bwd_ws_bytes(int N, int L, int H, int DH, int prec);
 long pt_ppo_partial_floats(int n);
 int pt_ppo_loss(const float* out, int n, int A, const float* mask, long mask_stride,
                 const int32_t* idx, const float* actions, const float* old_logp,

@@ -126,12 +126,18 @@ struct PtcgModel {
     // forks the side stream off the main one, wg_ev[1..4] mark the side
     // stream's FFN2 / FFN1 / out-projection / QKV weight gradient of the
     // latest block done (wg_rec: recorded in this backward); ws2 is the side
-    // stream's split-K workspace
+    // stream's split-K workspace; wg_serial (set per backward while a launch
+    // profile is open) keeps them on the main stream, so that every timed
+    // launch runs alone
     hipStream_t wg_s = nullptr;
+    bool wg_serial = false;
     hipEvent_t wg_ev[5] = {};
     bool wg_rec[5] = {};
     float* ws2 = nullptr;
     long ws2_floats = 0;
+    // the trunk attention backward's dS scratch (training only)
+    void* attn_ws = nullptr;
+    size_t attn_ws_bytes = 0;
     float *d_hand, *d_prize, *d_blind, *dxc, *dxc2, *dotok, *dotok_in, *dov1, *dovin;
     int* aux_cnt;
     // order-independent table scatters: fixed-point accumulators (zero
@@ -237,11 +243,13 @@ static int bldw(PtcgModel* m, const float* dY, int out, const float* X, int in, 
 // work so far; done(e) = mark the side stream's work so far as event e;
 // after(e) = the main stream waits for event e (if this backward recorded it)
 static int wg_fork(PtcgModel* m, hipStream_t s) {
+    if (m->wg_serial) return PTCG_OK;
     PT_HIP(hipEventRecord(m->wg_ev[0], s));
     PT_HIP(hipStreamWaitEvent(m->wg_s, m->wg_ev[0], 0));
     return PTCG_OK;
 }
 static int wg_done(PtcgModel* m, int e) {
+    if (m->wg_serial) return PTCG_OK;
     PT_HIP(hipEventRecord(m->wg_ev[e], m->wg_s));
     m->wg_rec[e] = true;
     return PTCG_OK;
@@ -597,6 +605,9 @@ static size_t carve(PtcgModel* m, char* base) {
     m->ws = c.take(m->ws_floats);
     m->ws2_floats = 16L << 20;   // the side stream's weight-gradient split-K partials
     m->ws2 = c.take(m->ws2_floats);
+    // the trunk attention backward parks dS here (fp32 size covers both precisions)
+    m->attn_ws_bytes = m->train ? pt_attn_bwd_ws_bytes(N, x.l_seq, d.heads, x.dh, 0) : 0;
+    m->attn_ws = m->attn_ws_bytes ? c.take((m->attn_ws_bytes + 3) / 4) : nullptr;
     return c.off;
 }
 
@@ -851,7 +862,7 @@ static int block_bwd(PtcgModel* m, const BlockP& w, const BlockA& a, int L, cons
     // overwrites a buffer a pending weight gradient reads: dffn (the previous
     // block's FFN1 dW), dC (its out-projection dW), dqkv (its QKV dW) and dA
     // (this block's FFN2 dW).
-    hipStream_t s2 = m->wg_s;
+    hipStream_t s2 = m->wg_serial ? s : m->wg_s;
     if (bw) {
         PT_TRY(wg_fork(m, s));
         PT_TRY(bldw(m, m->dAh, D, a.ffa, d.ffn, m->G(w.f2w), m->G(w.f2b), NL, s2, Tr));
@@ -870,7 +881,8 @@ static int block_bwd(PtcgModel* m, const BlockP& w, const BlockA& a, int L, cons
         PT_TRY(wg_done(m, 3));
         PT_TRY(blin(m, m->dCh, D, bw->projT, nullptr, m->dctx, D, NL, EPI_STORE, true, nullptr, nullptr, s, Tr));
         PT_TRY(wg_after(m, 4, s));
-        PT_TRY(pt_attn_bwd(a.qkv, keep, a.ctx, a.lse, m->dctx, m->dqkv, m->N, L, d.heads, m->dx.dh, s, coff, 2));
+        PT_TRY(pt_attn_bwd(a.qkv, keep, a.ctx, a.lse, m->dctx, m->dqkv, m->N, L, d.heads, m->dx.dh, s, coff, 2,
+                           m->attn_ws, m->attn_ws_bytes));
         PT_TRY(wg_fork(m, s));
         PT_TRY(bldw(m, m->dqkv, 3 * D, a.ln1, D, m->G(w.qkvw), m->G(w.qkvb), NL, s2, Tr));
         PT_TRY(wg_done(m, 4));
@@ -898,7 +910,8 @@ static int block_bwd(PtcgModel* m, const BlockP& w, const BlockA& a, int L, cons
     PT_TRY(wg_done(m, 3));
     PT_TRY(ldx_(m, dC, D, w.projw, m->dctx, D, NL, D, D, EPI_STORE, nullptr, 0, s, Tr));
     PT_TRY(wg_after(m, 4, s));
-    PT_TRY(pt_attn_bwd(a.qkv, keep, a.ctx, a.lse, m->dctx, m->dqkv, m->N, L, d.heads, m->dx.dh, s, coff, m->prec));
+    PT_TRY(pt_attn_bwd(a.qkv, keep, a.ctx, a.lse, m->dctx, m->dqkv, m->N, L, d.heads, m->dx.dh, s, coff, m->prec,
+                       m->attn_ws, m->attn_ws_bytes));
     PT_TRY(wg_fork(m, s));
     PT_TRY(ldw_(m, m->dqkv, 3 * D, a.ln1, D, m->G(w.qkvw), m->G(w.qkvb), NL, D, 3 * D, s2, Tr, true));
     PT_TRY(wg_done(m, 4));
@@ -1003,6 +1016,7 @@ extern "C" int ptcg_model_backward(PtcgModel* m, const float* grad, void* stream
     PT_REQUIRE(m->train, "model_backward: activations were registered for rollout (ptcg_model_reg_train)");
     hipStream_t s = (hipStream_t)stream;
     for (bool& r : m->wg_rec) r = false;   // side-stream events of an earlier backward are not waited for
+    m->wg_serial = pt_prof_active();
     const PtcgDims& d = m->dm;
     const DimsX& x = m->dx;
     const int N = m->N, Lt = d.l_tok, NO = d.n_opt, D = d.d, G = d.g;

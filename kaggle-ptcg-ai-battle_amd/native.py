@@ -214,6 +214,12 @@ _SIGS = {
     "ptcg_kernel_attention_bwd_bf16": (ctypes.c_int, [c_void_p, c_void_p, c_void_p, c_void_p,
                                                       c_void_p, c_void_p, ctypes.c_int, ctypes.c_int,
                                                       ctypes.c_int, ctypes.c_int, c_void_p]),
+    "ptcg_kernel_attention_bwd_ws_bytes": (ctypes.c_int64, [ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                                            ctypes.c_int, ctypes.c_int]),
+    "ptcg_kernel_attention_bwd_ws": (ctypes.c_int, [c_void_p, c_void_p, c_void_p, c_void_p,
+                                                    c_void_p, c_void_p, ctypes.c_int, ctypes.c_int,
+                                                    ctypes.c_int, ctypes.c_int, ctypes.c_int, c_void_p,
+                                                    ctypes.c_int64, c_void_p]),
 }
 
 _lib = None

@@ -249,6 +249,52 @@ def test_attention_bf16_products(N, L, H, Dh, path, cuda):
     assert torch.all(gk[:, :, 1:][~keep] == 0)
 
 
+@pytest.mark.parametrize("N,L,H,Dh,path", [c for c in ATTN_CASES if c[4] & 2], ids=lambda *a: None)
+@pytest.mark.parametrize("bf16", [0, 1])
+def test_attention_bwd_global_ds(N, L, H, Dh, path, bf16, cuda):
+    """The backward with dS parked in a global scratch (the model's training
+    form: LDS holds only Q and dO) against float64 at the same bars as the
+    LDS form, and beside that form's own result; the scratch is filled with
+    NaN first, so a dS entry read before it is written would show."""
+    g = torch.Generator().manual_seed(N * L + H + 11 * bf16)
+    D = H * Dh
+    qkv = torch.randn(N, L, 3 * D, generator=g).double().requires_grad_()
+    keep = torch.rand(N, L, generator=g) < 0.7
+    keep[:, 0] = True
+    ctx, lse = _attn_ref(qkv, keep, H, Dh)
+    dctx = torch.randn(N, L, D, generator=g).double()
+    ctx.backward(dctx)
+    L_ = native.lib()
+    nbytes = L_.ptcg_kernel_attention_bwd_ws_bytes(N, L, H, Dh, bf16)
+    lp = 16 * ((L + 15) // 16)
+    assert nbytes == N * H * lp * lp * (2 if bf16 else 4)
+    ws = torch.full((nbytes // 4,), float("nan"), device="cuda")
+    dq, dk, d_dctx = dev(qkv.detach()), dev(keep.float()), dev(dctx)
+    c, l, g_lds, g_ws = empty(N, L, D), empty(N, H, L), empty(N, L, 3 * D), empty(N, L, 3 * D)
+    fwd = L_.ptcg_kernel_attention_fwd_bf16 if bf16 else L_.ptcg_kernel_attention_fwd
+    bwd = L_.ptcg_kernel_attention_bwd_bf16 if bf16 else L_.ptcg_kernel_attention_bwd
+    native.check(fwd(P(dq), P(dk), P(c), P(l), N, L, H, Dh, None))
+    native.check(bwd(P(dq), P(dk), P(c), P(l), P(d_dctx), P(g_lds), N, L, H, Dh, None))
+    native.check(L_.ptcg_kernel_attention_bwd_ws(P(dq), P(dk), P(c), P(l), P(d_dctx), P(g_ws), N, L, H, Dh, bf16,
+                                                 P(ws), nbytes, None))
+    torch.cuda.synchronize()
+    e_ws, e_lds = rel_l2(g_ws.cpu(), qkv.grad), rel_l2(g_lds.cpu(), qkv.grad)
+    if bf16:
+        assert e_ws < 3e-2, e_ws
+        assert rel_l2(g_ws.cpu(), g_lds.cpu()) < 1e-2
+    else:
+        assert e_ws < 1e-5, (e_ws, e_lds)
+        assert rel_l2(g_ws.cpu(), g_lds.cpu()) < 2e-6
+    # dK and dV are produced by pass A in both forms: identical bits
+    gw, gl = g_ws.cpu().view(N, L, 3, D), g_lds.cpu().view(N, L, 3, D)
+    assert torch.equal(gw[:, :, 1:], gl[:, :, 1:])
+    assert torch.all(gw[:, :, 1:][~keep] == 0)
+    # a scratch one byte short is refused
+    with pytest.raises(native.PtcgError, match="workspace"):
+        native.check(L_.ptcg_kernel_attention_bwd_ws(P(dq), P(dk), P(c), P(l), P(d_dctx), P(g_ws), N, L, H, Dh,
+                                                     bf16, P(ws), nbytes - 1, None))
+
+
 def test_attention_rejects_oversized(cuda):
     a = empty(4)
     with pytest.raises(native.PtcgError, match="LDS"):

@@ -30,7 +30,13 @@ namespace {
 // touching LDS (B supplies V rows in the same key order).  The padded length
 // Lp = 16 * ceil(L / 16); padded keys score -inf, padded rows are zero.
 // 8 waves per workgroup: one 16-row stripe each (Lp <= 128), two waves per
-// SIMD to overlap LDS reads with MFMAs.
+// SIMD to overlap LDS reads with MFMAs.  In the forward and the stored-dS
+// backward, products over the head dimension give lane group lq the dims
+// 16kq + 4lq + e (e = 0..3) of both operands, and products with an output
+// over the head dimension give lane li the output columns W li .. W li + W - 1
+// (W = Dh / 16, one accumulator each): both are permutations applied to both
+// operands alike, so every operand fragment is a row segment read as one
+// vector and every output row segment is one vector store.
 
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 
@@ -72,12 +78,43 @@ __device__ __forceinline__ void st_lds4(float* p, float4 v) { *reinterpret_cast<
 __device__ __forceinline__ void st_lds4(__bf16* p, float4 v) {
     *reinterpret_cast<bf16x4*>(p) = bf16x4{(__bf16)v.x, (__bf16)v.y, (__bf16)v.z, (__bf16)v.w};
 }
+// W (= Dh / 16) consecutive elements of a row as one 128- / 64-bit (bf16:
+// 64- / 32-bit) access, in LDS or global memory
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+template <int W> __device__ __forceinline__ void ldw(const float* p, float (&o)[W]) {
+    if constexpr (W == 4) {
+        const float4 v = *reinterpret_cast<const float4*>(p);
+        o[0] = v.x; o[1] = v.y; o[2] = v.z; o[3] = v.w;
+    } else {
+        static_assert(W == 2, "W is Dh / 16: 2 or 4");
+        const float2 v = *reinterpret_cast<const float2*>(p);
+        o[0] = v.x; o[1] = v.y;
+    }
+}
+template <int W> __device__ __forceinline__ void ldw(const __bf16* p, float (&o)[W]) {
+    if constexpr (W == 4) {
+        const bf16x4 v = *reinterpret_cast<const bf16x4*>(p);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o[i] = (float)v[i];
+    } else {
+        const bf16x2 v = *reinterpret_cast<const bf16x2*>(p);
+        o[0] = (float)v[0]; o[1] = (float)v[1];
+    }
+}
+template <int W> __device__ __forceinline__ void stw(float* p, const float (&v)[W]) {
+    if constexpr (W == 4) *reinterpret_cast<float4*>(p) = make_float4(v[0], v[1], v[2], v[3]);
+    else *reinterpret_cast<float2*>(p) = make_float2(v[0], v[1]);
+}
+template <int W> __device__ __forceinline__ void stw(__bf16* p, const float (&v)[W]) {
+    if constexpr (W == 4) *reinterpret_cast<bf16x4*>(p) = bf16x4{(__bf16)v[0], (__bf16)v[1], (__bf16)v[2], (__bf16)v[3]};
+    else *reinterpret_cast<bf16x2*>(p) = bf16x2{(__bf16)v[0], (__bf16)v[1]};
+}
 
 template <int DH, int NT, bool BF, typename T>   // NT = Lp / 16 key (and query) tiles
 __global__ __launch_bounds__(512) void attn_fwd_mfma_kernel(const T* __restrict__ qkv,
         const float* __restrict__ keep, T* __restrict__ ctx, float* __restrict__ lse,
         int Lfix, int H, float scale, const int* __restrict__ coff) {
-    constexpr int LP = NT * 16, SK = DH + 4;
+    constexpr int LP = NT * 16, SK = DH + 4, W = DH / 16;
     typedef typename std::conditional<BF, __bf16, float>::type LT;   // LDS operand type
     extern __shared__ float sm[];
     LT* Ks = reinterpret_cast<LT*>(sm);   // [LP][SK]
@@ -109,12 +146,16 @@ __global__ __launch_bounds__(512) void attn_fwd_mfma_kernel(const T* __restrict_
 
     for (int st = wave; st < ntl; st += 8) {
         const int q0 = st * 16;
-        // Q^T as the B operand: lane (li = query, lq) holds Q[q0+li][4kk+lq]
+        // Q^T as the B operand: lane (li = query, lq) holds Q[q0+li][16kq+4lq+e]
+        // at qb[4kq+e] (head dims 4lq..4lq+3 of each 16-group: one vector load)
         float qb[DH / 4];
         const bool qv = q0 + li < L;
 #pragma unroll
-        for (int kk = 0; kk < DH / 4; ++kk)
-            qb[kk] = qv ? tof(base[(long)(q0 + li) * 3 * D + 4 * kk + lq]) : 0.f;
+        for (int kq = 0; kq < DH / 16; ++kq) {
+            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (qv) v = ld4(base + (long)(q0 + li) * 3 * D + 16 * kq + 4 * lq);
+            qb[4 * kq] = v.x; qb[4 * kq + 1] = v.y; qb[4 * kq + 2] = v.z; qb[4 * kq + 3] = v.w;
+        }
         floatx4 o[DH / 16];
 #pragma unroll
         for (int dt = 0; dt < DH / 16; ++dt) o[dt] = floatx4{0.f, 0.f, 0.f, 0.f};
@@ -132,11 +173,9 @@ __global__ __launch_bounds__(512) void attn_fwd_mfma_kernel(const T* __restrict_
 #pragma unroll
                     for (int kq = 0; kq < DH / 16; ++kq) {
                         float a[4], b[4];
+                        ldw<4>(Ks + (16 * (c0 + j) + li) * SK + 16 * kq + 4 * lq, a);
 #pragma unroll
-                        for (int e = 0; e < 4; ++e) {
-                            a[e] = (float)Ks[(16 * (c0 + j) + li) * SK + 4 * (4 * kq + e) + lq];
-                            b[e] = qb[4 * kq + e];
-                        }
+                        for (int e = 0; e < 4; ++e) b[e] = qb[4 * kq + e];
                         sc[j] = mfma4<BF>(a, b, sc[j]);
                     }
                 }
@@ -178,30 +217,34 @@ __global__ __launch_bounds__(512) void attn_fwd_mfma_kernel(const T* __restrict_
                     for (int dt = 0; dt < DH / 16; ++dt) o[dt][r] *= a;
                 }
             }
-            // O += P V over the permuted key order
+            // O += P V over the permuted key order; output column W li + dt
+            // of o[dt] (W = Dh / 16), so a lane's V operands of one key are W
+            // consecutive columns (one vector LDS read)
 #pragma unroll
             for (int j = 0; j < CH; ++j) {
                 if (c0 + j < ntl) {
                     const float a[4] = {sc[j][0], sc[j][1], sc[j][2], sc[j][3]};
+                    float vv[4][W];
 #pragma unroll
-                    for (int dt = 0; dt < DH / 16; ++dt) {
-                        float b[4];
+                    for (int r = 0; r < 4; ++r) ldw<W>(Vs + (16 * (c0 + j) + 4 * lq + r) * SK + W * li, vv[r]);
 #pragma unroll
-                        for (int r = 0; r < 4; ++r) b[r] = (float)Vs[(16 * (c0 + j) + 4 * lq + r) * SK + li + 16 * dt];
+                    for (int dt = 0; dt < W; ++dt) {
+                        const float b[4] = {vv[0][dt], vv[1][dt], vv[2][dt], vv[3][dt]};
                         o[dt] = mfma4<BF>(a, b, o[dt]);
                     }
                 }
             }
         }
-        // o[dt][r] = O[q0 + 4lq + r][16dt + li] * sum(query); normalise
+        // o[dt][r] = O[q0 + 4lq + r][W li + dt] * sum(query); normalise
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const float inv = 1.0f / __shfl(sum, 4 * lq + r, 64);
             const int q = q0 + 4 * lq + r;
             if (q < L) {
-                T* dst = ctx + (rb + q) * D + h * DH + li;
+                float v[W];
 #pragma unroll
-                for (int dt = 0; dt < DH / 16; ++dt) dst[16 * dt] = (T)(o[dt][r] * inv);
+                for (int dt = 0; dt < W; ++dt) v[dt] = o[dt][r] * inv;
+                stw<W>(ctx + (rb + q) * D + h * DH + W * li, v);
             }
         }
         if (lq == 0 && qv) lse[((long)n * H + h) * Lfix + q0 + li] = mx + logf(sum);
@@ -229,7 +272,7 @@ __global__ __launch_bounds__(512) void attn_bwd_mfma_kernel(const T* __restrict_
         const float* __restrict__ lse, const T* __restrict__ dctx,
         T* __restrict__ dqkv, int Lfix, int H, float scale, const int* __restrict__ coff,
         typename std::conditional<BF, __bf16, float>::type* __restrict__ dsg = nullptr) {
-    constexpr int LP = NT * 16, SQ = DH + 4, SKB = GDS ? DH + 4 : DH + 16, SS = GDS ? LP : LP + 4;
+    constexpr int LP = NT * 16, SQ = DH + 4, SKB = GDS ? DH + 4 : DH + 16, SS = GDS ? LP : LP + 4, W = DH / 16;
     typedef typename std::conditional<BF, __bf16, float>::type LT;   // LDS operand type
     extern __shared__ float sm[];
     LT* Qs = reinterpret_cast<LT*>(sm);   // [LP][SQ]
@@ -285,11 +328,18 @@ __global__ __launch_bounds__(512) void attn_bwd_mfma_kernel(const T* __restrict_
     for (int kb = wave; kb < ntl; kb += 8) {
         const int k0 = kb * 16;
         const bool kv = k0 + li < L;
-        float kr[DH / 4], vr[DH / 4];    // B operands: lane (li = key, lq) holds K/V[k0+li][4kk+lq]
+        // B operands: lane (li = key, lq) holds K/V[k0+li][16kq+4lq+e] at [4kq+e]
+        // (the head-dim order of the Q / dO operands below: one vector load each)
+        float kr[DH / 4], vr[DH / 4];
 #pragma unroll
-        for (int kk = 0; kk < DH / 4; ++kk) {
-            kr[kk] = kv ? tof(base[(long)(k0 + li) * 3 * D + D + 4 * kk + lq]) : 0.f;
-            vr[kk] = kv ? tof(base[(long)(k0 + li) * 3 * D + 2 * D + 4 * kk + lq]) : 0.f;
+        for (int kq = 0; kq < DH / 16; ++kq) {
+            float4 k4 = make_float4(0.f, 0.f, 0.f, 0.f), v4 = k4;
+            if (kv) {
+                k4 = ld4(base + (long)(k0 + li) * 3 * D + D + 16 * kq + 4 * lq);
+                v4 = ld4(base + (long)(k0 + li) * 3 * D + 2 * D + 16 * kq + 4 * lq);
+            }
+            kr[4 * kq] = k4.x; kr[4 * kq + 1] = k4.y; kr[4 * kq + 2] = k4.z; kr[4 * kq + 3] = k4.w;
+            vr[4 * kq] = v4.x; vr[4 * kq + 1] = v4.y; vr[4 * kq + 2] = v4.z; vr[4 * kq + 3] = v4.w;
         }
         const float kfl = kf[k0 + li];
         floatx4 dv[DH / 16], dk[DH / 16];
@@ -303,11 +353,11 @@ __global__ __launch_bounds__(512) void attn_bwd_mfma_kernel(const T* __restrict_
 #pragma unroll
             for (int kq = 0; kq < DH / 16; ++kq) {
                 float qa[4], da[4], kb4[4], vb4[4];
+                const int a_off = (16 * qt + li) * SQ + 16 * kq + 4 * lq;
+                ldw<4>(Qs + a_off, qa);
+                ldw<4>(dOs + a_off, da);
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    const int a_off = (16 * qt + li) * SQ + 4 * (4 * kq + e) + lq;
-                    qa[e] = (float)Qs[a_off];
-                    da[e] = (float)dOs[a_off];
                     kb4[e] = kr[4 * kq + e];
                     vb4[e] = vr[4 * kq + e];
                 }
@@ -323,30 +373,37 @@ __global__ __launch_bounds__(512) void attn_bwd_mfma_kernel(const T* __restrict_
                 ds[r] = p[r] * (dp[r] - Dv[q]);
                 dSs[q * SS + k0 + li] = (LT)(ds[r] * scale);
             }
+            // dV / dK output column W li + dt of dv[dt] / dk[dt]: a lane's dO / Q
+            // operands of one query row are W consecutive columns
+            float ow[4][W], qw[4][W];
 #pragma unroll
-            for (int dt = 0; dt < DH / 16; ++dt) {
-                float ob[4], qb4[4];
+            for (int r = 0; r < 4; ++r) {
+                const int qrow = 16 * qt + 4 * lq + r;
+                ldw<W>(dOs + qrow * SQ + W * li, ow[r]);
+                ldw<W>(Qs + qrow * SQ + W * li, qw[r]);
+            }
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const int qrow = 16 * qt + 4 * lq + r;
-                    ob[r] = (float)dOs[qrow * SQ + 16 * dt + li];
-                    qb4[r] = (float)Qs[qrow * SQ + 16 * dt + li];
-                }
+            for (int dt = 0; dt < W; ++dt) {
+                const float ob[4] = {ow[0][dt], ow[1][dt], ow[2][dt], ow[3][dt]};
+                const float qb4[4] = {qw[0][dt], qw[1][dt], qw[2][dt], qw[3][dt]};
                 dv[dt] = mfma4<BF>(p, ob, dv[dt]);
                 dk[dt] = mfma4<BF>(ds, qb4, dk[dt]);
             }
         }
-        // dv[dt][r] = dV[k0 + 4lq + r][16dt + li]
+        // dv[dt][r] = dV[k0 + 4lq + r][W li + dt]
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const int key = k0 + 4 * lq + r;
             if (key < L) {
-                T* g = gb + (long)key * 3 * D + li;
+                T* g = gb + (long)key * 3 * D + W * li;
+                float kw[W], vw[W];
 #pragma unroll
-                for (int dt = 0; dt < DH / 16; ++dt) {
-                    g[D + 16 * dt] = (T)(dk[dt][r] * scale);
-                    g[2 * D + 16 * dt] = (T)dv[dt][r];
+                for (int dt = 0; dt < W; ++dt) {
+                    kw[dt] = dk[dt][r] * scale;
+                    vw[dt] = dv[dt][r];
                 }
+                stw<W>(g + D, kw);
+                stw<W>(g + 2 * D, vw);
             }
         }
     }
@@ -378,14 +435,17 @@ __global__ __launch_bounds__(512) void attn_bwd_mfma_kernel(const T* __restrict_
 #pragma unroll
                 for (int e = 0; e < 4; ++e) a[e] = (float)dSs[(16 * qt + li) * SS + 4 * (4 * kq + e) + lq];
             }
+            // dQ output column W li + dt of dq[dt]: a lane's K operands of one
+            // key are W consecutive columns
+            float kw[4][W];
 #pragma unroll
-            for (int dt = 0; dt < DH / 16; ++dt) {
-                float b[4];
+            for (int e = 0; e < 4; ++e) {
+                const int key = GDS ? 16 * kq + 4 * lq + e : 4 * (4 * kq + e) + lq;
+                ldw<W>(Ks + key * SKB + W * li, kw[e]);
+            }
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const int key = GDS ? 16 * kq + 4 * lq + e : 4 * (4 * kq + e) + lq;
-                    b[e] = (float)Ks[key * SKB + li + 16 * dt];
-                }
+            for (int dt = 0; dt < W; ++dt) {
+                const float b[4] = {kw[0][dt], kw[1][dt], kw[2][dt], kw[3][dt]};
                 dq[dt] = mfma4<BF>(a, b, dq[dt]);
             }
         }
@@ -393,9 +453,10 @@ __global__ __launch_bounds__(512) void attn_bwd_mfma_kernel(const T* __restrict_
         for (int r = 0; r < 4; ++r) {
             const int q = 16 * qt + 4 * lq + r;
             if (q < L) {
-                T* g = gb + (long)q * 3 * D + li;
+                float qv[W];
 #pragma unroll
-                for (int dt = 0; dt < DH / 16; ++dt) g[16 * dt] = (T)dq[dt][r];
+                for (int dt = 0; dt < W; ++dt) qv[dt] = dq[dt][r];
+                stw<W>(gb + (long)q * 3 * D + W * li, qv);
             }
         }
     }

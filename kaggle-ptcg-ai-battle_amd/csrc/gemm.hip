@@ -1132,6 +1132,23 @@ __global__ __launch_bounds__(NT) void gemm_bs_dw_kernel(const GemmArgs g0, int k
     gemm_epilogue<EPI_STORE, PARTIAL>(g, acc, m0, n0, wm, wn, li, lq, part_stride, nullptr, bz);
 }
 
+// sum_k bp[k * M] for k < splits in order: loads issued 16 at a time ahead of
+// the adds (a bias partial of every split would otherwise cost one memory
+// round trip each)
+__device__ __forceinline__ float sum_split_column(const float* bp, int splits, int M) {
+    float s = 0.f;
+    int k = 0;
+    for (; k + 16 <= splits; k += 16) {
+        float v[16];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) v[j] = bp[(long)(k + j) * M];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) s += v[j];
+    }
+    for (; k < splits; ++k) s += bp[(long)k * M];
+    return s;
+}
+
 // out[m][n] (=|+=) sum_s part[s][m][n], fixed order over s
 // and, when db is set, db[m] = sum_s part[splits*part_stride + s*M + m]
 // V4: a thread sums 4 consecutive columns (N, ldc multiples of 4, C 16 B aligned)
@@ -1143,12 +1160,7 @@ __global__ void splitk_reduce_kernel(float* C, long ldc, const float* part, long
     const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= (long)M * nq) {
         const long m = i - (long)M * nq;
-        if (db != nullptr && m < M) {
-            const float* bp = part + (long)splits * part_stride + m;
-            float s = 0.f;
-            for (int k = 0; k < splits; ++k) s += bp[(long)k * M];
-            db[m] = s;
-        }
+        if (db != nullptr && m < M) db[m] = sum_split_column(part + (long)splits * part_stride + m, splits, M);
         return;
     }
     const int m = (int)(i / nq), n = (int)(i % nq) * W;
@@ -1164,6 +1176,77 @@ __global__ void splitk_reduce_kernel(float* C, long ldc, const float* part, long
         for (int k = 0; k < splits; ++k) s += part[(long)k * part_stride + o];
         if (ACCUM) C[o] += s; else C[o] = s;
     }
+}
+
+// The same sum for many splits (N, ldc multiples of 4, C 16 B aligned),
+// parallel over split groups: block b covers 256 / G float4 outputs, group g
+// of its threads sums splits [g S / G, (g + 1) S / G) in order, and the G
+// group sums are added in group order through LDS -- a fixed order, so the
+// result does not depend on scheduling.  Blocks past the outputs sum the
+// bias partials (db) as splitk_reduce_kernel does.
+template <bool ACCUM, int G>
+__global__ __launch_bounds__(256) void splitk_reduce_grp_kernel(float* C, long ldc, const float* part,
+                                                                long part_stride, int splits, int M, int N,
+                                                                float* db, int out_blocks) {
+    constexpr int CPB = 256 / G;
+    __shared__ floatx4 sh[G][CPB];
+    const int t = threadIdx.x;
+    if ((int)blockIdx.x >= out_blocks) {
+        const int m = ((int)blockIdx.x - out_blocks) * 256 + t;
+        if (db != nullptr && m < M) db[m] = sum_split_column(part + (long)splits * part_stride + m, splits, M);
+        return;
+    }
+    const int nq = N / 4;
+    const int g = t / CPB, c = t % CPB;
+    const long i = (long)blockIdx.x * CPB + c;
+    const bool live = i < (long)M * nq;
+    const int m = live ? (int)(i / nq) : 0, n = live ? (int)(i % nq) * 4 : 0;
+    const long o = (long)m * ldc + n;
+    floatx4 sum = floatx4{0.f, 0.f, 0.f, 0.f};
+    if (live) {
+        const int zb = (int)(((long)splits * g) / G), ze = (int)(((long)splits * (g + 1)) / G);
+#pragma unroll 4
+        for (int z = zb; z < ze; ++z) sum += ld_v4(part + (long)z * part_stride + o);
+    }
+    sh[g][c] = sum;
+    __syncthreads();
+    if (g == 0 && live) {
+        floatx4 v = sh[0][c];
+#pragma unroll
+        for (int k = 1; k < G; ++k) v += sh[k][c];
+        st_g4(C + o, ACCUM ? ld_v4(C + o) + v : v);
+    }
+}
+
+// split-K partial sums into C (and the bias partials into db): the grouped
+// form for many splits with 128-bit columns, else one thread per output
+template <bool ACCUM>
+void launch_splitk_reduce(float* C, long ldc, const float* part, long part_stride, int splits, int M, int N,
+                          float* db, bool v4, hipStream_t s) {
+    const int G = !v4 ? 1 : splits >= 64 ? 8 : splits >= 24 ? 4 : splits >= 12 ? 2 : 1;
+    if (G > 1) {
+        const long outs = (long)M * (N / 4);
+        const int ob = pt_cdiv(outs, 256 / G), dbb = db ? pt_cdiv(M, 256) : 0;
+        const dim3 gr(ob + dbb);
+        if (G == 8)
+            hipLaunchKernelGGL((splitk_reduce_grp_kernel<ACCUM, 8>), gr, dim3(256), 0, s, C, ldc, part, part_stride,
+                               splits, M, N, db, ob);
+        else if (G == 4)
+            hipLaunchKernelGGL((splitk_reduce_grp_kernel<ACCUM, 4>), gr, dim3(256), 0, s, C, ldc, part, part_stride,
+                               splits, M, N, db, ob);
+        else
+            hipLaunchKernelGGL((splitk_reduce_grp_kernel<ACCUM, 2>), gr, dim3(256), 0, s, C, ldc, part, part_stride,
+                               splits, M, N, db, ob);
+        return;
+    }
+    const long tot = (long)M * (v4 ? N / 4 : N) + (db ? M : 0);
+    const dim3 gr(pt_cdiv(tot, 256));
+    if (v4)
+        hipLaunchKernelGGL((splitk_reduce_kernel<ACCUM, true>), gr, dim3(256), 0, s, C, ldc, part, part_stride,
+                           splits, M, N, db);
+    else
+        hipLaunchKernelGGL((splitk_reduce_kernel<ACCUM, false>), gr, dim3(256), 0, s, C, ldc, part, part_stride,
+                           splits, M, N, db);
 }
 
 // Tail tiles of a balanced launch: C[tile] = epi(sum_s part[s][tile]), fixed order over s.
@@ -1519,9 +1602,7 @@ static int gemm_bs_dw(const GemmArgs& g, float* ws, long ws_floats, hipStream_t 
     pt_prof_close(slot, g_gemm_class, 2.0 * g.M * (double)g.N * g.K, s);
     PT_LAUNCH_CHECK();
     if (splits > 1) {
-        const long tot = (long)g.M * (g.N / 4) + (db ? g.M : 0);
-        hipLaunchKernelGGL((splitk_reduce_kernel<false, true>), dim3(pt_cdiv(tot, 256)), dim3(256), 0, s, g.C, g.ldc,
-                           (const float*)ws, part_stride, splits, g.M, g.N, db ? g.dbias : nullptr);
+        launch_splitk_reduce<false>(g.C, g.ldc, ws, part_stride, splits, g.M, g.N, db ? g.dbias : nullptr, true, s);
         PT_LAUNCH_CHECK();
     }
     return PTCG_OK;
@@ -1591,21 +1672,9 @@ int pt_gemm(const GemmArgs& g0, float* ws, long ws_floats, hipStream_t s) {
         else launch_partial<false>(p, db, grid, k_chunk, part_stride, s);
         PT_LAUNCH_CHECK();
         const bool v4 = g.N % 4 == 0 && g.ldc % 4 == 0 && ((uintptr_t)g.C & 15) == 0;
-        const long tot = (long)g.M * (v4 ? g.N / 4 : g.N) + (db ? g.M : 0);
         float* dbp = db ? g.dbias : nullptr;
-        const dim3 gr(pt_cdiv(tot, 256));
-        if (g.epi == EPI_ACCUM && v4)
-            hipLaunchKernelGGL((splitk_reduce_kernel<true, true>), gr, dim3(256), 0, s, g.C, g.ldc, ws, part_stride,
-                               splits, g.M, g.N, dbp);
-        else if (g.epi == EPI_ACCUM)
-            hipLaunchKernelGGL((splitk_reduce_kernel<true, false>), gr, dim3(256), 0, s, g.C, g.ldc, ws, part_stride,
-                               splits, g.M, g.N, dbp);
-        else if (v4)
-            hipLaunchKernelGGL((splitk_reduce_kernel<false, true>), gr, dim3(256), 0, s, g.C, g.ldc, ws, part_stride,
-                               splits, g.M, g.N, dbp);
-        else
-            hipLaunchKernelGGL((splitk_reduce_kernel<false, false>), gr, dim3(256), 0, s, g.C, g.ldc, ws, part_stride,
-                               splits, g.M, g.N, dbp);
+        if (g.epi == EPI_ACCUM) launch_splitk_reduce<true>(g.C, g.ldc, ws, part_stride, splits, g.M, g.N, dbp, v4, s);
+        else launch_splitk_reduce<false>(g.C, g.ldc, ws, part_stride, splits, g.M, g.N, dbp, v4, s);
         PT_LAUNCH_CHECK();
         return PTCG_OK;
     }

@@ -63,6 +63,8 @@ GEMM_CASES = [
     # k-contiguous K % 16 != 0 at the model's sizes (option query 664 wide,
     # token concat 300 wide with a balanced tail) and split K ending mid-stage
     (13000, 256, 664, 0, 0, 6), (37000, 256, 300, 0, 0, 1), (64, 64, 4100, 0, 0, 0), (96, 64, 2052, 0, 1, 5),
+    # many K splits: partial sums reduced by split groups (accumulate and store)
+    (64, 128, 20000, 0, 1, 5), (256, 256, 20000, 1, 1, 0), (200, 260, 9000, 1, 1, 0),
 ]
 
 

@@ -1306,6 +1306,48 @@ __global__ __launch_bounds__(256) void splitk_reduce_grp_kernel(float* C, long l
     }
 }
 
+// Split-K for a product whose epilogue needs the whole sum (bias, GELU,
+// residual, multiply): C = epi(sum_s part[s]) in split order, one thread per
+// four columns (v4: C, C2, R, bias and leading dimensions 16 B aligned and
+// N a multiple of 4) or per element.
+template <int EPI, bool V4>
+__global__ void splitk_epi_reduce_kernel(GemmArgs g, const float* __restrict__ part, long part_stride,
+                                         int splits) {
+    constexpr int W = V4 ? 4 : 1;
+    const long nq = g.N / W;
+    const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (long)g.M * nq) return;
+    const int m = (int)(i / nq), n = (int)(i % nq) * W;
+    const long o = (long)m * g.ldc + n;
+    if (V4) {
+        floatx4 sum = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll 8
+        for (int z = 0; z < splits; ++z) sum += ld_v4(part + (long)z * part_stride + o);
+        epi_store4<EPI>(g, m, n, sum);
+    } else {
+        float sum = 0.f;
+#pragma unroll 8
+        for (int z = 0; z < splits; ++z) sum += part[(long)z * part_stride + o];
+        epi_store<EPI>(g, m, n, sum);
+    }
+}
+
+template <bool V4>
+int launch_splitk_epi_reduce(const GemmArgs& g, const float* part, long part_stride, int splits, hipStream_t s) {
+    const dim3 gr(pt_cdiv((long)g.M * (g.N / (V4 ? 4 : 1)), 256));
+    switch (g.epi) {
+        case EPI_BIAS: hipLaunchKernelGGL((splitk_epi_reduce_kernel<EPI_BIAS, V4>), gr, dim3(256), 0, s, g, part, part_stride, splits); break;
+        case EPI_BIAS_GELU: hipLaunchKernelGGL((splitk_epi_reduce_kernel<EPI_BIAS_GELU, V4>), gr, dim3(256), 0, s, g, part, part_stride, splits); break;
+        case EPI_BIAS_RESID: hipLaunchKernelGGL((splitk_epi_reduce_kernel<EPI_BIAS_RESID, V4>), gr, dim3(256), 0, s, g, part, part_stride, splits); break;
+        case EPI_GELU_BWD: hipLaunchKernelGGL((splitk_epi_reduce_kernel<EPI_GELU_BWD, V4>), gr, dim3(256), 0, s, g, part, part_stride, splits); break;
+        case EPI_BIAS_GELU_D: hipLaunchKernelGGL((splitk_epi_reduce_kernel<EPI_BIAS_GELU_D, V4>), gr, dim3(256), 0, s, g, part, part_stride, splits); break;
+        case EPI_MUL: hipLaunchKernelGGL((splitk_epi_reduce_kernel<EPI_MUL, V4>), gr, dim3(256), 0, s, g, part, part_stride, splits); break;
+        case EPI_AXPBY: hipLaunchKernelGGL((splitk_epi_reduce_kernel<EPI_AXPBY, V4>), gr, dim3(256), 0, s, g, part, part_stride, splits); break;
+        default: PT_REQUIRE(false, "gemm: split-K epilogue %d not supported", g.epi);
+    }
+    return PTCG_OK;
+}
+
 // split-K partial sums into C (and the bias partials into db): the grouped
 // form for many splits with 128-bit columns, else one thread per output
 template <bool ACCUM>
@@ -1730,8 +1772,9 @@ int pt_gemm(const GemmArgs& g0, float* ws, long ws_floats, hipStream_t s) {
         if (splits > max_splits) splits = max_splits;
         if (splits < 1) splits = 1;
     }
-    if (splits > 1 && !(g.epi == EPI_STORE || g.epi == EPI_ACCUM)) splits = 1;
     if (g.Mdev) splits = 1;   // device row counts: one pass (partials are sized by M)
+    // bf16 output products (GemmArgs::obf) never reach this path; every fp32
+    // epilogue is applied by the reduce when K is split
     PT_REQUIRE(!(g.dbias && !(g.a_t && g.epi == EPI_STORE)), "gemm: dbias needs a_t = 1 and the STORE epilogue");
     // the register-staged bf16 kernel leaves bias sums to the fp32 column sum
     // (from the unrounded dY); the DMA kernels sum the fp32 tiles in LDS
@@ -1761,8 +1804,16 @@ int pt_gemm(const GemmArgs& g0, float* ws, long ws_floats, hipStream_t s) {
         PT_LAUNCH_CHECK();
         const bool v4 = g.N % 4 == 0 && g.ldc % 4 == 0 && ((uintptr_t)g.C & 15) == 0;
         float* dbp = db ? g.dbias : nullptr;
-        if (g.epi == EPI_ACCUM) launch_splitk_reduce<true>(g.C, g.ldc, ws, part_stride, splits, g.M, g.N, dbp, v4, s);
-        else launch_splitk_reduce<false>(g.C, g.ldc, ws, part_stride, splits, g.M, g.N, dbp, v4, s);
+        if (g.epi == EPI_ACCUM) {
+            launch_splitk_reduce<true>(g.C, g.ldc, ws, part_stride, splits, g.M, g.N, dbp, v4, s);
+        } else if (g.epi == EPI_STORE) {
+            launch_splitk_reduce<false>(g.C, g.ldc, ws, part_stride, splits, g.M, g.N, dbp, v4, s);
+        } else {
+            const uintptr_t al = (uintptr_t)g.C | (uintptr_t)g.C2 | (uintptr_t)g.R | (uintptr_t)g.bias |
+                                 (uintptr_t)((g.ldc | g.ldc2 | g.ldr) * 4);
+            if (g.N % 4 == 0 && (al & 15) == 0) PT_TRY(launch_splitk_epi_reduce<true>(g, ws, part_stride, splits, s));
+            else PT_TRY(launch_splitk_epi_reduce<false>(g, ws, part_stride, splits, s));
+        }
         PT_LAUNCH_CHECK();
         return PTCG_OK;
     }

@@ -170,6 +170,10 @@ __global__ void tok_cat_bwd_kernel(GatherCtx c, const float* __restrict__ d_cat,
     k1.flush();
 }
 
+// rows (or samples, options) whose loads are issued together before their
+// ordered adds, in the scatters bound by a chain of dependent loads per row
+constexpr int PF = 16;
+
 __global__ void glob_in_kernel(GatherCtx c, float* __restrict__ out) {
     const int G = c.dm.global_f;
     const long i = (long)blockIdx.x * TB + threadIdx.x;
@@ -280,10 +284,16 @@ __global__ void x0_bwd_kernel(GatherCtx c, const float* __restrict__ d_x0, float
         for (int col = threadIdx.x; col < D; col += TB) {
             float acc = 0.f;
             d_tokp[r0 * D + col] = 0.f;
-            for (long r = r0 + 1; r < r1; ++r) {
-                const float v = d_x0[r * D + col];
-                d_tokp[r * D + col] = v;
-                acc += v;
+            for (long rb = r0 + 1; rb < r1; rb += PF) {   // PF rows' loads together, sums in row order
+                float v[PF];
+#pragma unroll
+                for (int u = 0; u < PF; ++u) v[u] = rb + u < r1 ? d_x0[(rb + u) * D + col] : 0.f;
+#pragma unroll
+                for (int u = 0; u < PF; ++u) {
+                    if (rb + u >= r1) break;
+                    d_tokp[(rb + u) * D + col] = v[u];
+                    acc += v[u];
+                }
             }
             d_bc[(long)n * D + col] = acc;
         }
@@ -395,16 +405,25 @@ __global__ void q_in_bwd_kernel(GatherCtx c, const float* __restrict__ d_qin, fl
         s_ty[i] = pt_id_clamp(oi[0], c.dm.n_opt_types - 1);
     }
     __syncthreads();
+    constexpr int QB = 8;   // options whose gradient loads are issued together
     for (int col = threadIdx.x; col < D; col += TB) {
-        for (int i = 0; i < nq; ++i) {
-            const float* g = d_qin + (b0 + i) * W;
-            if (s_h1[i] >= 0) {
-                const float v = g[PT_TYPE_E + col];
-                if (v != 0.f) atomicAdd(d_h + s_h1[i] * D + col, v);
+        for (int ib = 0; ib < nq; ib += QB) {
+            float v1[QB], v2[QB];
+#pragma unroll
+            for (int u = 0; u < QB; ++u) {
+                const int i = ib + u;
+                v1[u] = v2[u] = 0.f;
+                if (i >= nq) continue;
+                const float* g = d_qin + (b0 + i) * W;
+                if (s_h1[i] >= 0) v1[u] = g[PT_TYPE_E + col];
+                if (s_h2[i] >= 0) v2[u] = g[PT_TYPE_E + D + col];
             }
-            if (s_h2[i] >= 0) {
-                const float v = g[PT_TYPE_E + D + col];
-                if (v != 0.f) atomicAdd(d_h + s_h2[i] * D + col, v);
+#pragma unroll
+            for (int u = 0; u < QB; ++u) {
+                const int i = ib + u;
+                if (i >= nq) break;
+                if (v1[u] != 0.f) atomicAdd(d_h + s_h1[i] * D + col, v1[u]);
+                if (v2[u] != 0.f) atomicAdd(d_h + s_h2[i] * D + col, v2[u]);
             }
         }
     }
@@ -553,10 +572,20 @@ __global__ void head_dot_dw_partial_kernel(const float* __restrict__ grad, int p
     for (int k0 = 0; k0 < K; k0 += TB) {
         const int k = k0 + threadIdx.x;
         float s = 0.f, sd = 0.f;
-        for (int r = r0; r < r1; ++r) {
-            const float dy = grad[hd_slot(rmap, r, per, ldg, col0)];
-            sd += dy;
-            if (k < K) s += dy * X[(long)r * K + k];
+        for (int rb = r0; rb < r1; rb += PF) {   // PF rows' loads together, sums in row order
+            float dy[PF], xv[PF];
+#pragma unroll
+            for (int u = 0; u < PF; ++u) {
+                const int r = rb + u;
+                dy[u] = r < r1 ? grad[hd_slot(rmap, r, per, ldg, col0)] : 0.f;
+                xv[u] = (r < r1 && k < K) ? X[(long)r * K + k] : 0.f;
+            }
+#pragma unroll
+            for (int u = 0; u < PF; ++u) {
+                if (rb + u >= r1) break;
+                sd += dy[u];
+                if (k < K) s += dy[u] * xv[u];
+            }
         }
         if (k < K) part[(long)blockIdx.x * (K + 1) + k] = s;
         if (k0 == 0 && threadIdx.x == 0) part[(long)blockIdx.x * (K + 1) + K] = sd;

@@ -130,6 +130,21 @@ __global__ __launch_bounds__(512) void attn_fwd_mfma_kernel(const T* __restrict_
     // this sample's tiles (compact rows vary in length; the template covers the longest)
     const int ntl = min(NT, (L + 15) / 16);
     const T* base = qkv + rb * 3 * D + h * DH;
+    // Q^T as the B operand: lane (li = query, lq) holds Q[q0+li][16kq+4lq+e]
+    // at qb[4kq+e] (head dims 4lq..4lq+3 of each 16-group: one vector load);
+    // the wave's first stripe is loaded before the K / V staging, so its
+    // latency overlaps the staging's
+    float qb[DH / 4];
+    auto load_q = [&](int q0) {
+        const bool qv = q0 + li < L;
+#pragma unroll
+        for (int kq = 0; kq < DH / 16; ++kq) {
+            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (qv) v = ld4(base + (long)(q0 + li) * 3 * D + 16 * kq + 4 * lq);
+            qb[4 * kq] = v.x; qb[4 * kq + 1] = v.y; qb[4 * kq + 2] = v.z; qb[4 * kq + 3] = v.w;
+        }
+    };
+    if (wave < ntl) load_q(wave * 16);
     for (int idx = tid; idx < ntl * 16 * (DH / 4); idx += 512) {
         const int l = idx / (DH / 4), c4 = (idx % (DH / 4)) * 4;
         float4 k4 = make_float4(0.f, 0.f, 0.f, 0.f), v4 = k4;
@@ -146,16 +161,8 @@ __global__ __launch_bounds__(512) void attn_fwd_mfma_kernel(const T* __restrict_
 
     for (int st = wave; st < ntl; st += 8) {
         const int q0 = st * 16;
-        // Q^T as the B operand: lane (li = query, lq) holds Q[q0+li][16kq+4lq+e]
-        // at qb[4kq+e] (head dims 4lq..4lq+3 of each 16-group: one vector load)
-        float qb[DH / 4];
+        if (st != wave) load_q(q0);
         const bool qv = q0 + li < L;
-#pragma unroll
-        for (int kq = 0; kq < DH / 16; ++kq) {
-            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (qv) v = ld4(base + (long)(q0 + li) * 3 * D + 16 * kq + 4 * lq);
-            qb[4 * kq] = v.x; qb[4 * kq + 1] = v.y; qb[4 * kq + 2] = v.z; qb[4 * kq + 3] = v.w;
-        }
         floatx4 o[DH / 16];
 #pragma unroll
         for (int dt = 0; dt < DH / 16; ++dt) o[dt] = floatx4{0.f, 0.f, 0.f, 0.f};
@@ -297,6 +304,24 @@ __global__ __launch_bounds__(512) void attn_bwd_mfma_kernel(const T* __restrict_
     const T* ob = ctx + rb * D + h * DH;
     const T* dob = dctx + rb * D + h * DH;
     T* gb = dqkv + rb * 3 * D + h * DH;
+    // pass A's B operands, loaded before the staging so their latency overlaps
+    // it: lane (li = key, lq) holds K/V[k0+li][16kq+4lq+e] at [4kq+e] (the
+    // head-dim order of the Q / dO operands below: one vector load each).
+    // Wave w owns key stripe w (at most 8 stripes).
+    static_assert(NT <= 8, "one key stripe per wave");
+    const int kb = wave, k0 = kb * 16;
+    const bool kv = k0 + li < L;
+    float kr[DH / 4], vr[DH / 4];
+#pragma unroll
+    for (int kq = 0; kq < DH / 16; ++kq) {
+        float4 k4 = make_float4(0.f, 0.f, 0.f, 0.f), v4 = k4;
+        if (kb < ntl && kv) {
+            k4 = ld4(base + (long)(k0 + li) * 3 * D + D + 16 * kq + 4 * lq);
+            v4 = ld4(base + (long)(k0 + li) * 3 * D + 2 * D + 16 * kq + 4 * lq);
+        }
+        kr[4 * kq] = k4.x; kr[4 * kq + 1] = k4.y; kr[4 * kq + 2] = k4.z; kr[4 * kq + 3] = k4.w;
+        vr[4 * kq] = v4.x; vr[4 * kq + 1] = v4.y; vr[4 * kq + 2] = v4.z; vr[4 * kq + 3] = v4.w;
+    }
     // stage Q, dO, K and form Dv[q] = sum_d dO[q][d] O[q][d]: the DH/4 lanes
     // holding a row's 4-column partials are adjacent (512 is a multiple of
     // DH/4), so a butterfly over them gives the row sum (padded rows 0)
@@ -324,23 +349,8 @@ __global__ __launch_bounds__(512) void attn_bwd_mfma_kernel(const T* __restrict_
     }
     __syncthreads();
 
-    // ---- pass A: key stripes
-    for (int kb = wave; kb < ntl; kb += 8) {
-        const int k0 = kb * 16;
-        const bool kv = k0 + li < L;
-        // B operands: lane (li = key, lq) holds K/V[k0+li][16kq+4lq+e] at [4kq+e]
-        // (the head-dim order of the Q / dO operands below: one vector load each)
-        float kr[DH / 4], vr[DH / 4];
-#pragma unroll
-        for (int kq = 0; kq < DH / 16; ++kq) {
-            float4 k4 = make_float4(0.f, 0.f, 0.f, 0.f), v4 = k4;
-            if (kv) {
-                k4 = ld4(base + (long)(k0 + li) * 3 * D + D + 16 * kq + 4 * lq);
-                v4 = ld4(base + (long)(k0 + li) * 3 * D + 2 * D + 16 * kq + 4 * lq);
-            }
-            kr[4 * kq] = k4.x; kr[4 * kq + 1] = k4.y; kr[4 * kq + 2] = k4.z; kr[4 * kq + 3] = k4.w;
-            vr[4 * kq] = v4.x; vr[4 * kq + 1] = v4.y; vr[4 * kq + 2] = v4.z; vr[4 * kq + 3] = v4.w;
-        }
+    // ---- pass A: key stripes (wave kb's)
+    if (kb < ntl) {
         const float kfl = kf[k0 + li];
         floatx4 dv[DH / 16], dk[DH / 16];
 #pragma unroll
@@ -425,12 +435,21 @@ __global__ __launch_bounds__(512) void attn_bwd_mfma_kernel(const T* __restrict_
         floatx4 dq[DH / 16];
 #pragma unroll
         for (int dt = 0; dt < DH / 16; ++dt) dq[dt] = floatx4{0.f, 0.f, 0.f, 0.f};
-        for (int kq = 0; kq < ntl; ++kq) {
+        // GDS: the stripe's dS row segments (keys 16 kq + 4 lq + e: one 128-bit,
+        // bf16 64-bit, load per key tile), all issued before the products
+        float4 dsr[NT];
+        if constexpr (GDS) {
+#pragma unroll
+            for (int kq = 0; kq < NT; ++kq)
+                dsr[kq] = kq < ntl ? ld4(dSs + (16 * qt + li) * SS + 16 * kq + 4 * lq)
+                                   : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+#pragma unroll
+        for (int kq = 0; kq < NT; ++kq) {
+            if (kq >= ntl) break;
             float a[4];
             if constexpr (GDS) {
-                // keys 16 kq + 4 lq + e: one 128-bit (bf16: 64-bit) load of the dS row
-                const float4 a4 = ld4(dSs + (16 * qt + li) * SS + 16 * kq + 4 * lq);
-                a[0] = a4.x; a[1] = a4.y; a[2] = a4.z; a[3] = a4.w;
+                a[0] = dsr[kq].x; a[1] = dsr[kq].y; a[2] = dsr[kq].z; a[3] = dsr[kq].w;
             } else {
 #pragma unroll
                 for (int e = 0; e < 4; ++e) a[e] = (float)dSs[(16 * qt + li) * SS + 4 * (4 * kq + e) + lq];

@@ -814,8 +814,35 @@ __device__ __forceinline__ void gemm_dma_tile(const GemmArgs& g0, int k_chunk0, 
         const uintptr_t al = PARTIAL ? (uintptr_t)ge.C | (uintptr_t)(g.ldc * 4)
                                      : (uintptr_t)g.C | (uintptr_t)g.C2 | (uintptr_t)g.R | (uintptr_t)g.bias |
                                            (uintptr_t)((g.ldc | g.ldc2 | g.ldr) * 4);
-        epilogue_staged32<PARTIAL ? EPI_STORE : EPI, false>(ge, acc32, m0, n0, wm, wn, l32, lh, smem, (al & 15) == 0,
-                                                            false);
+        const bool vo = (al & 15) == 0;
+        if (PARTIAL || !EpiStaged<EPI>::value) {
+            // plain, bias and accumulate outputs straight from the accumulators:
+            // a store instruction covers 32 rows x 32 B, and the wave's four
+            // stores of a run (8 q + 4 lh) fill each row's 128 B segment
+            constexpr int E = PARTIAL ? EPI_STORE : EPI;
+#pragma unroll
+            for (int ti = 0; ti < 2; ++ti) {
+                const int m = m0 + wm + 32 * ti + l32;
+                if (m >= g.M) continue;
+#pragma unroll
+                for (int tj = 0; tj < 2; ++tj)
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const int n = n0 + wn + 32 * tj + 8 * q + 4 * lh;
+                        const floatx4 v = floatx4{acc32[ti][tj][4 * q], acc32[ti][tj][4 * q + 1],
+                                                  acc32[ti][tj][4 * q + 2], acc32[ti][tj][4 * q + 3]};
+                        if (vo && n + 3 < g.N) {
+                            epi_store4<E>(ge, m, n, v);
+                        } else {
+#pragma unroll
+                            for (int r = 0; r < 4; ++r)
+                                if (n + r < g.N) epi_store<E>(ge, m, n + r, v[r]);
+                        }
+                    }
+            }
+            return;
+        }
+        epilogue_staged32<EPI, false>(ge, acc32, m0, n0, wm, wn, l32, lh, smem, vo, false);
         return;
     }
     gemm_epilogue<EPI, PARTIAL>(g, acc, m0, n0, wm, wn, li, lq, part_stride, smem, bz);

@@ -6,9 +6,11 @@
 //   1. sum-of-squares partials of the grad arena (128-bit loads, four in
 //      flight per thread); block 0 also publishes the step number this call
 //      will use;
-//   2. every thread issues the loads of its p, g, m, v float4s first, then its
+//   2. persistent workgroups stride over chunks of the arena; every thread
+//      issues the loads of its first chunk's p, g, m, v float4s, then its
 //      workgroup folds the partials in the same fixed order (so all agree bit
-//      for bit on ||g||) while those loads are in flight, then:
+//      for bit on ||g||) while those loads are in flight, and each chunk's
+//      loads are issued before the previous chunk's stores; per element:
 //      g' = g * min(max_norm / (||g|| + 1e-6), 1)
 //      m  = m + (1 - b1) (g' - m);  v = v b2 + (1 - b2) g'^2
 //      p  = p - (lr / (1 - b1^t)) m / (sqrt(v) / sqrt(1 - b2^t) + eps)
@@ -29,7 +31,8 @@ namespace {
 constexpr int NPART = 512;    // pass-1 workgroups (upper bound) = norm partials
 constexpr int NT_NORM = 512;
 constexpr int NT = 256;
-constexpr int UPD_U = 4;      // float4s per thread in pass 2, loaded together
+constexpr int UPD_U = 2;      // float4s per thread and chunk in pass 2, loaded together
+constexpr int UPD_BLOCKS = 512;   // pass-2 workgroups (persistent, striding over the chunks)
 
 __device__ __forceinline__ float sq4(float4 v) { return (v.x * v.x + v.y * v.y) + (v.z * v.z + v.w * v.w); }
 
@@ -69,7 +72,11 @@ __global__ __launch_bounds__(NT) void adam_update_kernel(float4* __restrict__ p,
         const float* __restrict__ gate, const float* __restrict__ ws, float* __restrict__ norm_out,
         int32_t* __restrict__ step) {
     if (gate && gate[0] == 0.0f) return;
-    const long base = (long)blockIdx.x * (NT * U) + threadIdx.x;
+    // persistent: workgroup b takes chunks b, b + G, ... (G = gridDim.x) of
+    // NT * U float4s; a chunk's loads are issued before the previous chunk's
+    // stores, so reads and writes stream together
+    const long stride = (long)gridDim.x * (NT * U);
+    long base = (long)blockIdx.x * (NT * U) + threadIdx.x;
     float4 gg[U], mm[U], vv[U], pp[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
@@ -101,23 +108,41 @@ __global__ __launch_bounds__(NT) void adam_update_kernel(float4* __restrict__ p,
     const float bc2s = (float)sqrt(1.0 - pow(b2, (double)t));
     const float omb1 = (float)(1.0 - b1), omb2 = (float)(1.0 - b2);
     const float b2f = (float)b2, epsf = (float)eps;
+    for (; base < n4; base += stride) {
+        float4 g2[U], m2[U], v2[U], p2[U];
+        const long nb = base + stride;
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-        const long i = base + (long)u * NT;
-        if (i < n4) {
-#define PT_ADAM_LANE(c)                                             \
-            {                                                       \
-                const float gc = gg[u].c * coef;                    \
-                mm[u].c = mm[u].c + omb1 * (gc - mm[u].c);          \
-                vv[u].c = vv[u].c * b2f + omb2 * gc * gc;           \
-                const float den = sqrtf(vv[u].c) / bc2s + epsf;     \
-                pp[u].c = pp[u].c + (-step_size) * (mm[u].c / den); \
+        for (int u = 0; u < U; ++u) {
+            const long i = nb + (long)u * NT;
+            if (i < n4) {
+                g2[u] = g[i];
+                m2[u] = m[i];
+                v2[u] = v[i];
+                p2[u] = p[i];
             }
-            PT_ADAM_LANE(x) PT_ADAM_LANE(y) PT_ADAM_LANE(z) PT_ADAM_LANE(w)
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const long i = base + (long)u * NT;
+            if (i < n4) {
+#define PT_ADAM_LANE(c)                                             \
+                {                                                   \
+                    const float gc = gg[u].c * coef;                \
+                    mm[u].c = mm[u].c + omb1 * (gc - mm[u].c);      \
+                    vv[u].c = vv[u].c * b2f + omb2 * gc * gc;       \
+                    const float den = sqrtf(vv[u].c) / bc2s + epsf; \
+                    pp[u].c = pp[u].c + (-step_size) * (mm[u].c / den); \
+                }
+                PT_ADAM_LANE(x) PT_ADAM_LANE(y) PT_ADAM_LANE(z) PT_ADAM_LANE(w)
 #undef PT_ADAM_LANE
-            m[i] = mm[u];
-            v[i] = vv[u];
-            p[i] = pp[u];
+                m[i] = mm[u];
+                v[i] = vv[u];
+                p[i] = pp[u];
+            }
+            gg[u] = g2[u];
+            mm[u] = m2[u];
+            vv[u] = v2[u];
+            pp[u] = p2[u];
         }
     }
 }
@@ -142,8 +167,8 @@ int pt_adam_step(float* w, float* g, float* m, float* v, long n, const double* l
     hipLaunchKernelGGL(adam_norm_kernel, dim3(parts), dim3(NT_NORM), 0, s, (const float4*)g, n4, gate, step, ws);
     PT_LAUNCH_CHECK();
     pt_prof_close(slot, PROF_ADAM_NORM, 4.0 * n, s);
-    const long ublocks = (n4 + NT * UPD_U - 1) / (NT * UPD_U);
-    PT_REQUIRE(ublocks <= 0x7fffffffL, "adam: arena of %ld floats too large", n);
+    long ublocks = (n4 + NT * UPD_U - 1) / (NT * UPD_U);
+    if (ublocks > UPD_BLOCKS) ublocks = UPD_BLOCKS;
     slot = pt_prof_open(s);
     hipLaunchKernelGGL(adam_update_kernel<UPD_U>, dim3((unsigned)ublocks), dim3(NT), 0, s, (float4*)w, (const float4*)g,
                        (float4*)m, (float4*)v, n4, parts, lr, b1, b2, eps, max_norm, gate, ws, norm_out, step);

@@ -89,11 +89,13 @@ __device__ __forceinline__ void pt_gelu_both(float x, float& g, float& gd) {
 // 1 - erf(x) = t (a1 + t (a2 + t (a3 + t (a4 + t a5)))) e^(-x^2),
 // t = 1 / (1 + p x), x = |z| / sqrt 2, whose e^(-x^2) = e^(-z^2/2) is also the
 // normal density's exponential in gelu'(z) = Phi(z) + z phi(z).  The error is
-// far below the 2^-9 rounding of the stored bf16 value; the fp32 path keeps
+// far below the 2^-9 rounding of the stored bf16 value, as is that of t from
+// v_rcp_f32 (1 ulp) in place of an IEEE division (ten instructions per
+// element in an epilogue bound by its VALU work); the fp32 path keeps
 // pt_gelu_both (libm erf).
 __device__ __forceinline__ void pt_gelu_both_bf(float z, float& g, float& gd) {
     const float x = fabsf(z) * 0.70710678118654752f;
-    const float t = 1.0f / (1.0f + 0.3275911f * x);
+    const float t = __builtin_amdgcn_rcpf(1.0f + 0.3275911f * x);
     const float poly =
         t * (0.254829592f + t * (-0.284496736f + t * (1.421413741f + t * (-1.453152027f + t * 1.061405429f))));
     const float e = __expf(-x * x);

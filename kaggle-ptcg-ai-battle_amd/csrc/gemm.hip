@@ -1060,6 +1060,25 @@ __global__ __launch_bounds__(NT) void gemm_bs32_kernel(const GemmArgs g0) {
     const int32x4_t ra = buffer_rsrc(g.A, ea), rb = buffer_rsrc(g.B, eb);
     const int sa0 = dma_src<false>(2 * wave, lane, m0, g.lda), sa1 = dma_src<false>(2 * wave + 1, lane, m0, g.lda);
     const int sb0 = dma_src<false>(2 * wave, lane, n0, g.ldb), sb1 = dma_src<false>(2 * wave + 1, lane, n0, g.ldb);
+    // multiply epilogue on bf16 (the GELU derivative): the first half's R
+    // segments load before the main loop, the second half's after it, so the
+    // epilogue does not wait on them
+    constexpr bool RPF = EPI == EPI_MUL && OB;
+    const uintptr_t al8 = (uintptr_t)g.C | (uintptr_t)g.C2 | (uintptr_t)g.R | (uintptr_t)((g.ldc | g.ldc2 | g.ldr) * 2);
+    const uintptr_t al = (uintptr_t)g.C | (uintptr_t)g.C2 | (uintptr_t)g.R | (uintptr_t)g.bias |
+                         (uintptr_t)((g.ldc | g.ldc2 | g.ldr) * 4);
+    const bool vo8 = (al & 15) == 0 && (al8 & 15) == 0;
+    bf16x8 rpf[2][4];
+    auto load_r = [&](int h) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int it = tid + j * NT, lr = it / (BN / 8), c = (it % (BN / 8)) * 8;
+            const int m = m0 + (lr >> 5) * 64 + 32 * h + (lr & 31), n = n0 + c;
+            if (m < g.M && n + 7 < g.N)
+                rpf[h][j] = *reinterpret_cast<const bf16x8*>(bfp(g.R) + (long)m * g.ldr + n);
+        }
+    };
+    if (RPF && vo8) load_r(0);
 #define PT_ISSUE32(tile)                                                                \
     {                                                                                   \
         const int k0_ = (tile) * BK;                                                    \
@@ -1108,11 +1127,46 @@ __global__ __launch_bounds__(NT) void gemm_bs32_kernel(const GemmArgs g0) {
         }
     }
 #undef PT_ISSUE32
-    const uintptr_t al = (uintptr_t)g.C | (uintptr_t)g.C2 | (uintptr_t)g.R | (uintptr_t)g.bias |
-                         (uintptr_t)((g.ldc | g.ldc2 | g.ldr) * 4);
+    if constexpr (RPF) {
+        if (vo8) {
+            load_r(1);
+            // 16 B bf16 stores of C = acc * R with the prefetched R (same
+            // staging and arithmetic as epilogue_staged32's EPI_MUL path)
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                __syncthreads();
+#pragma unroll
+                for (int tj = 0; tj < 2; ++tj)
+#pragma unroll
+                    for (int q = 0; q < 4; ++q)
+                        *reinterpret_cast<floatx4*>(smem + ((wm >> 6) * 32 + l32) * SST + wn + 32 * tj + 8 * q +
+                                                    4 * lh) =
+                            floatx4{acc[h][tj][4 * q], acc[h][tj][4 * q + 1], acc[h][tj][4 * q + 2],
+                                    acc[h][tj][4 * q + 3]};
+                __syncthreads();
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int it = tid + j * NT, lr = it / (BN / 8), c = (it % (BN / 8)) * 8;
+                    const int m = m0 + (lr >> 5) * 64 + 32 * h + (lr & 31), n = n0 + c;
+                    if (m >= g.M || n >= g.N) continue;
+                    const floatx4 v0 = *reinterpret_cast<const floatx4*>(smem + lr * SST + c);
+                    const floatx4 v1 = *reinterpret_cast<const floatx4*>(smem + lr * SST + c + 4);
+                    if (n + 7 < g.N) {
+                        const bf16x8 r = rpf[h][j];
+                        st_b8(g.C, (long)m * g.ldc + n,
+                              v0 * floatx4{(float)r[0], (float)r[1], (float)r[2], (float)r[3]},
+                              v1 * floatx4{(float)r[4], (float)r[5], (float)r[6], (float)r[7]});
+                    } else {
+                        for (int e = 0; e < 4 && n + e < g.N; ++e) epi_store<EPI, OB>(g, m, n + e, v0[e]);
+                        for (int e = 0; e < 4 && n + 4 + e < g.N; ++e) epi_store<EPI, OB>(g, m, n + 4 + e, v1[e]);
+                    }
+                }
+            }
+            return;
+        }
+    }
     // 16 B bf16 stores: bf16 rows of a multiple of 8 elements (R of EPI_MUL is bf16 too)
-    const uintptr_t al8 = (uintptr_t)g.C | (uintptr_t)g.C2 | (uintptr_t)g.R | (uintptr_t)((g.ldc | g.ldc2 | g.ldr) * 2);
-    epilogue_staged32<EPI, OB>(g, acc, m0, n0, wm, wn, l32, lh, smem, (al & 15) == 0, (al & 15) == 0 && (al8 & 15) == 0);
+    epilogue_staged32<EPI, OB>(g, acc, m0, n0, wm, wn, l32, lh, smem, (al & 15) == 0, vo8);
 }
 
 // gemm_bs_dw_kernel: weight gradients dW (M, N) = sum_k A[k][m] B[k][n] with

@@ -236,6 +236,17 @@ __device__ __forceinline__ void epi_store4(const GemmArgs& g, int m, int n, floa
     }
 }
 
+// fp32 store of an R-reading epilogue whose R segment r is already loaded.
+template <int EPI>
+__device__ __forceinline__ void epi_store4_r(const GemmArgs& g, int m, int n, floatx4 v, floatx4 r) {
+    float* c = g.C + (long)m * g.ldc + n;
+    if (EPI == EPI_BIAS_RESID) st_g4(c, (v + ld_v4(g.bias + n)) + r);
+    else if (EPI == EPI_GELU_BWD)
+        st_g4(c, v * floatx4{pt_gelu_grad(r[0]), pt_gelu_grad(r[1]), pt_gelu_grad(r[2]), pt_gelu_grad(r[3])});
+    else if (EPI == EPI_MUL) st_g4(c, v * r);
+    else if (EPI == EPI_AXPBY) st_g4(c, g.alpha * v + g.beta * r);
+}
+
 // Operand load of 4 consecutive floats along the contiguous dimension for
 // shapes that break the 128-bit rules (a width or leading dimension not a
 // multiple of 4, as the reference's 127-, 134- and 634-wide inputs do):
@@ -317,8 +328,27 @@ template <int EPI, bool OB>
 __device__ __forceinline__ void epilogue_staged32(const GemmArgs& g, floatx16 (&acc)[2][2], int m0, int n0, int wm,
                                                   int wn, int l32, int lh, float* stage, bool vo, bool vo8) {
     const int tid = threadIdx.x;
+    // fp32 epilogues that read R load half of each row half's R segments
+    // before that half's staging barriers and the rest right after them, so
+    // the loads overlap the LDS round (all of them up front would cost a
+    // fourth of the occupancy in registers).  The loads are branch-free: a
+    // segment outside C reads R's first 4 floats and is not used.
+    constexpr bool RPF = !OB && (EPI == EPI_BIAS_RESID || EPI == EPI_GELU_BWD || EPI == EPI_MUL || EPI == EPI_AXPBY);
+    constexpr int RI = 64 * (BN / 4) / NT, RH = RI / 2;
+    static_assert(64 * (BN / 4) % NT == 0, "epilogue segments must tile the threads");
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
+        floatx4 rv[RPF ? RI : 1];
+        auto load_r = [&](int j) {
+            const int it = tid + j * NT, lr = it / (BN / 4), c = (it % (BN / 4)) * 4;
+            const int m = m0 + (lr >> 5) * 64 + 32 * h + (lr & 31), n = n0 + c;
+            const bool ok = m < g.M && n + 3 < g.N;
+            rv[j] = ld_v4(g.R + (ok ? (long)m * g.ldr + n : 0L));
+        };
+        if (RPF && vo) {
+#pragma unroll
+            for (int j = 0; j < RH; ++j) load_r(j);
+        }
         __syncthreads();   // the stage is free (main loop done / previous half consumed)
 #pragma unroll
         for (int tj = 0; tj < 2; ++tj)
@@ -340,6 +370,21 @@ __device__ __forceinline__ void epilogue_staged32(const GemmArgs& g, floatx16 (&
                     for (int r = 0; r < 4 && n + r < g.N; ++r) epi_store<EPI, OB>(g, m, n + r, v0[r]);
                     for (int r = 0; r < 4 && n + 4 + r < g.N; ++r) epi_store<EPI, OB>(g, m, n + 4 + r, v1[r]);
                 }
+            }
+            continue;
+        }
+        if (RPF && vo) {
+#pragma unroll
+            for (int j = RH; j < RI; ++j) load_r(j);
+#pragma unroll
+            for (int j = 0; j < RI; ++j) {
+                const int it = tid + j * NT, lr = it / (BN / 4), c = (it % (BN / 4)) * 4;
+                const int m = m0 + (lr >> 5) * 64 + 32 * h + (lr & 31), n = n0 + c;
+                if (m >= g.M || n >= g.N) continue;
+                const floatx4 v = *reinterpret_cast<const floatx4*>(stage + lr * SST + c);
+                if (n + 3 < g.N) epi_store4_r<EPI>(g, m, n, v, rv[j]);
+                else
+                    for (int r = 0; r < 4 && n + r < g.N; ++r) epi_store<EPI, OB>(g, m, n + r, v[r]);
             }
             continue;
         }

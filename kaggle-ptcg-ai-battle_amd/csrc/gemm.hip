@@ -1290,11 +1290,14 @@ __global__ __launch_bounds__(NT) void gemm_bs_dw_kernel(const GemmArgs g0, int k
     const int c0 = (op == 0 ? m0 : n0) + 8 * cb;
     const bool cvalid = c0 < (op == 0 ? g.M : g.N);   // M, N multiples of 8 (host)
     const bool db_blk = DB && tni == 0;               // uniform over the block
-    floatx4 acc[4][4];
+    const int l32 = lane & 31, lh = lane >> 5;
+    floatx16 acc[2][2];   // the wave's 64 x 64 as 2 x 2 tiles of v_mfma_f32_32x32x16_bf16
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
     float dbs[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) dbs[i] = 0.f;
@@ -1332,22 +1335,24 @@ __global__ __launch_bounds__(NT) void gemm_bs_dw_kernel(const GemmArgs g0, int k
             }
         }
     };
+    // k step st (16 k): lane (l32, lh) supplies row l32 of its 32-row slice
+    // at k = 16 st + 8 lh .. + 7 (16 B group 2 st + lh) for both A and B
     auto compute = [&](int buf) {
         const __bf16* As = &sm[buf][0][0];
         const __bf16* Bs = &sm[buf][1][0];
 #pragma unroll
-        for (int kk = 0; kk < BKW / 32; ++kk) {
-            bf16x8 ah[4], bh[4];
+        for (int st = 0; st < BKW / 16; ++st) {
+            bf16x8 ah[2], bh[2];
 #pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                ah[t] = *reinterpret_cast<const bf16x8*>(As + tw_at(wm + t * 16 + li, 4 * kk + lq));
-                bh[t] = *reinterpret_cast<const bf16x8*>(Bs + tw_at(wn + t * 16 + li, 4 * kk + lq));
+            for (int t = 0; t < 2; ++t) {
+                ah[t] = *reinterpret_cast<const bf16x8*>(As + tw_at(wm + 32 * t + l32, 2 * st + lh));
+                bh[t] = *reinterpret_cast<const bf16x8*>(Bs + tw_at(wn + 32 * t + l32, 2 * st + lh));
             }
 #pragma unroll
-            for (int ti = 0; ti < 4; ++ti)
+            for (int ti = 0; ti < 2; ++ti)
 #pragma unroll
-                for (int tj = 0; tj < 4; ++tj)
-                    acc[ti][tj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bh[tj], ah[ti], acc[ti][tj], 0, 0, 0);
+                for (int tj = 0; tj < 2; ++tj)
+                    acc[ti][tj] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bh[tj], ah[ti], acc[ti][tj], 0, 0, 0);
         }
     };
     if (nk > 0) {
@@ -1389,7 +1394,31 @@ __global__ __launch_bounds__(NT) void gemm_bs_dw_kernel(const GemmArgs g0, int k
             }
         }
     }
-    gemm_epilogue<EPI_STORE, PARTIAL>(g, acc, m0, n0, wm, wn, li, lq, part_stride, nullptr, bz);
+    // register r of lane (l32, lh) of acc[ti][tj] holds
+    // C[wm + 32 ti + l32][wn + 32 tj + 8 (r / 4) + 4 lh + r % 4]: four runs of
+    // four columns of one row, stored straight from the accumulators
+    float* C = PARTIAL ? g.C + (long)bz * part_stride : g.C;
+    const bool vo = (((uintptr_t)C | (uintptr_t)(g.ldc * 4)) & 15) == 0;
+#pragma unroll
+    for (int ti = 0; ti < 2; ++ti) {
+        const int m = m0 + wm + 32 * ti + l32;
+        if (m >= g.M) continue;
+#pragma unroll
+        for (int tj = 0; tj < 2; ++tj)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int n = n0 + wn + 32 * tj + 8 * q + 4 * lh;
+                const floatx4 v = floatx4{acc[ti][tj][4 * q], acc[ti][tj][4 * q + 1], acc[ti][tj][4 * q + 2],
+                                          acc[ti][tj][4 * q + 3]};
+                if (vo && n + 3 < g.N) {
+                    st_g4(C + (long)m * g.ldc + n, v);
+                } else {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        if (n + r < g.N) C[(long)m * g.ldc + n + r] = v[r];
+                }
+            }
+    }
 }
 
 // sum_k bp[k * M] for k < splits in order: loads issued 16 at a time ahead of

@@ -70,23 +70,6 @@ __device__ __forceinline__ bool tile_of_range(const GemmArgs& g, int tn, int& tm
     return true;
 }
 
-// Split-K launches (grid tiles x 1 x splits): in linear order (x fastest) a
-// split's tiles would be dealt over every XCD, and each XCD's L2 would fetch
-// that split's A and B row chunks again.  Remap the linear workgroup id so
-// XCD x takes a contiguous run of (split, tile) items: a split's tiles run
-// side by side on one XCD and read its row chunks through one L2.  A
-// bijection of the grid, so every (split, tile) is computed exactly once
-// (the partial of split bz still covers the same K range).  Used by the bf16
-// kernels (bf16 step at B = 2048: 164.3k -> 166.1k obs/s).
-__device__ __forceinline__ void splitk_item(int& bx, int& bz) {
-    const int gx = gridDim.x, total = gx * gridDim.z;
-    const int lin = blockIdx.x + gx * blockIdx.z;
-    const int q = total >> 3, r = total & 7, x = lin & 7;
-    const int w = x * q + min(x, r) + (lin >> 3);
-    bz = w / gx;
-    bx = w % gx;
-}
-
 // bf16 activations (OB): C and C2 hold bf16 (round to nearest even), and so
 // does R for EPI_MUL (the GELU derivative the forward stored in bf16); the
 // residual R of EPI_BIAS_RESID and the bias stay fp32
@@ -912,9 +895,6 @@ __device__ __forceinline__ void gemm_dma_tile(const GemmArgs& g0, int k_chunk0, 
 
 template <bool AT, bool BT, int EPI, bool PARTIAL, bool DB>
 __global__ __launch_bounds__(NT) void gemm_f32_dma_kernel(const GemmArgs g0, int k_chunk0, long part_stride) {
-    // linear split-K order here: with splitk_item the fp32 weight gradients
-    // fetched 2.3x fewer bytes past L2 but ran 4% slower (83 -> 87 us per
-    // launch at 37.4k rows; the re-reads were served by the last-level cache)
     gemm_dma_tile<AT, BT, EPI, PARTIAL, DB>(g0, k_chunk0, part_stride, blockIdx.x, blockIdx.z, gridDim.z);
 }
 
@@ -1077,9 +1057,8 @@ __global__ __launch_bounds__(NT) void gemm_bf16_kernel(const GemmArgs g0, int k_
 constexpr int BF_NS = 3;
 template <bool AT, bool BT, int EPI, bool PARTIAL, bool DB>
 __global__ __launch_bounds__(NT) void gemm_bf16_k16_kernel(const GemmArgs g0, int k_chunk0, long part_stride) {
-    int bx = blockIdx.x, bz = blockIdx.z;
-    if (gridDim.z > 1) splitk_item(bx, bz);
-    gemm_dma_tile<AT, BT, EPI, PARTIAL, DB, true, BF_NS>(g0, k_chunk0, part_stride, bx, bz, gridDim.z);
+    gemm_dma_tile<AT, BT, EPI, PARTIAL, DB, true, BF_NS>(g0, k_chunk0, part_stride, blockIdx.x, blockIdx.z,
+                                                         gridDim.z);
 }
 
 // ---------------------------------------------------------------- bf16 activations
@@ -1247,36 +1226,24 @@ __global__ __launch_bounds__(NT) void gemm_bs32_kernel(const GemmArgs g0) {
 // 16 B group q at r * 64 + 8 * (q ^ f(r)), f(r) = (r ^ (r >> 3)) & 7: the
 // 8 lanes of a fragment read (rows r0..r0+7, one group) and of a staging
 // write (rows 8c + i for 8 consecutive c) land on 8 distinct groups.
-// Register prefetch ring of PF stages (stage s lives in register set s % PF;
-// the loop is unrolled by PF so every set index is a constant): stage it + 1
-// is stored to LDS right after stage it is multiplied and the loads of stage
-// it + 1 + PF go out before the barrier, so a stage's loads are in flight
-// across a barrier and a multiply.  The bounds-checked loads are branches, so
-// the compiler drains every outstanding load before a stage's register store;
-// a branch-free form (buffer loads with out-of-range offsets, PF stages truly
-// in flight) measured slower run alone (GEMM launches 89 -> 94 us on average
-// in the bf16 step), as did PF = 3 or 4.  PF = 2: bf16 step at B = 2048
-// 166.3k -> 167.9k obs/s against loads issued one stage ahead.  DB: bias sums
-// sum_k A[k][m] from the staged registers (fixed order: rows within a block,
-// stages, then the 8 blocks).
+// Register double buffering: the global loads of stage it + 1 are in flight
+// while stage it is multiplied.  DB: bias sums sum_k A[k][m] from the staged
+// registers (fixed order: rows within a block, stages, then the 8 blocks).
 constexpr int BKW = 64;
-constexpr int BSDW_PF = 2;
 __device__ __forceinline__ int tw_at(int r, int q) { return r * BKW + 8 * (q ^ ((r ^ (r >> 3)) & 7)); }
 typedef unsigned uintx4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(1))) uintx4 guintx4;
 
-template <bool DB, bool PARTIAL, int PF = BSDW_PF>
+template <bool DB, bool PARTIAL>
 __global__ __launch_bounds__(NT) void gemm_bs_dw_kernel(const GemmArgs g0, int k_chunk0, long part_stride) {
     const GemmArgs g = gemm_shape(g0);
-    const int gz = gridDim.z;
-    int bxi = blockIdx.x, bz = blockIdx.z;
-    if (gz > 1) splitk_item(bxi, bz);
+    const int gz = gridDim.z, bz = blockIdx.z;
     const int k_chunk = g0.Kdev ? (((g.K + gz - 1) / gz + BKW - 1) / BKW) * BKW : k_chunk0;
     __shared__ __align__(16) __bf16 sm[2][2][BM * BKW];   // [buffer][operand][row * 64 + k]
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int tn = (g.N + BN - 1) / BN;
     int tmi, tni;
-    if (!tile_of_range(g, tn, tmi, tni, bxi)) return;
+    if (!tile_of_range(g, tn, tmi, tni, blockIdx.x)) return;
     const int m0 = tmi * BM, n0 = tni * BN;
     const int kbeg = bz * k_chunk;
     const int kend = min(g.K, kbeg + k_chunk);
@@ -1290,90 +1257,72 @@ __global__ __launch_bounds__(NT) void gemm_bs_dw_kernel(const GemmArgs g0, int k
     const int c0 = (op == 0 ? m0 : n0) + 8 * cb;
     const bool cvalid = c0 < (op == 0 ? g.M : g.N);   // M, N multiples of 8 (host)
     const bool db_blk = DB && tni == 0;               // uniform over the block
-    const int l32 = lane & 31, lh = lane >> 5;
-    floatx16 acc[2][2];   // the wave's 64 x 64 as 2 x 2 tiles of v_mfma_f32_32x32x16_bf16
+    floatx4 acc[4][4];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-            for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+        for (int j = 0; j < 4; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
     float dbs[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) dbs[i] = 0.f;
-    unsigned w[PF][8][4];
-    auto load = [&](int it, unsigned (&r)[8][4]) {
+    unsigned w[8][4];
+    auto load = [&](int it) {
         const int kr = kbeg + it * BKW + 8 * kb;
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             uintx4 v = uintx4{0u, 0u, 0u, 0u};
             if (cvalid && kr + j < kend) v = *(const guintx4*)(src + (long)(kr + j) * ld + c0);
-            r[j][0] = v[0]; r[j][1] = v[1]; r[j][2] = v[2]; r[j][3] = v[3];
+            w[j][0] = v[0]; w[j][1] = v[1]; w[j][2] = v[2]; w[j][3] = v[3];
         }
     };
-    auto store = [&](int buf, const unsigned (&r)[8][4]) {
+    auto store = [&](int buf) {
         __bf16* S = &sm[buf][op][0];
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
             uint4 lo, hi;   // columns 2q (low halves) and 2q + 1 (high halves), rows 0..7
-            lo.x = (r[0][q] & 0xffffu) | (r[1][q] << 16);
-            lo.y = (r[2][q] & 0xffffu) | (r[3][q] << 16);
-            lo.z = (r[4][q] & 0xffffu) | (r[5][q] << 16);
-            lo.w = (r[6][q] & 0xffffu) | (r[7][q] << 16);
-            hi.x = (r[0][q] >> 16) | (r[1][q] & 0xffff0000u);
-            hi.y = (r[2][q] >> 16) | (r[3][q] & 0xffff0000u);
-            hi.z = (r[4][q] >> 16) | (r[5][q] & 0xffff0000u);
-            hi.w = (r[6][q] >> 16) | (r[7][q] & 0xffff0000u);
+            lo.x = (w[0][q] & 0xffffu) | (w[1][q] << 16);
+            lo.y = (w[2][q] & 0xffffu) | (w[3][q] << 16);
+            lo.z = (w[4][q] & 0xffffu) | (w[5][q] << 16);
+            lo.w = (w[6][q] & 0xffffu) | (w[7][q] << 16);
+            hi.x = (w[0][q] >> 16) | (w[1][q] & 0xffff0000u);
+            hi.y = (w[2][q] >> 16) | (w[3][q] & 0xffff0000u);
+            hi.z = (w[4][q] >> 16) | (w[5][q] & 0xffff0000u);
+            hi.w = (w[6][q] >> 16) | (w[7][q] & 0xffff0000u);
             *reinterpret_cast<uint4*>(S + tw_at(8 * cb + 2 * q, kb)) = lo;
             *reinterpret_cast<uint4*>(S + tw_at(8 * cb + 2 * q + 1, kb)) = hi;
             if (db_blk && op == 0) {
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
-                    dbs[2 * q] += __uint_as_float(r[j][q] << 16);
-                    dbs[2 * q + 1] += __uint_as_float(r[j][q] & 0xffff0000u);
+                    dbs[2 * q] += __uint_as_float(w[j][q] << 16);
+                    dbs[2 * q + 1] += __uint_as_float(w[j][q] & 0xffff0000u);
                 }
             }
-        }
-    };
-    // k step st (16 k): lane (l32, lh) supplies row l32 of its 32-row slice
-    // at k = 16 st + 8 lh .. + 7 (16 B group 2 st + lh) for both A and B
-    auto compute = [&](int buf) {
-        const __bf16* As = &sm[buf][0][0];
-        const __bf16* Bs = &sm[buf][1][0];
-#pragma unroll
-        for (int st = 0; st < BKW / 16; ++st) {
-            bf16x8 ah[2], bh[2];
-#pragma unroll
-            for (int t = 0; t < 2; ++t) {
-                ah[t] = *reinterpret_cast<const bf16x8*>(As + tw_at(wm + 32 * t + l32, 2 * st + lh));
-                bh[t] = *reinterpret_cast<const bf16x8*>(Bs + tw_at(wn + 32 * t + l32, 2 * st + lh));
-            }
-#pragma unroll
-            for (int ti = 0; ti < 2; ++ti)
-#pragma unroll
-                for (int tj = 0; tj < 2; ++tj)
-                    acc[ti][tj] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bh[tj], ah[ti], acc[ti][tj], 0, 0, 0);
         }
     };
     if (nk > 0) {
-        // stage s in register set s % PF; stages 1 .. PF in flight at the loop's start
-        load(0, w[0]);
-        store(0, w[0]);
-#pragma unroll
-        for (int p = 1; p <= PF; ++p)
-            if (p < nk) load(p, w[p % PF]);
+        load(0);
+        store(0);
         __syncthreads();
-        for (int it0 = 0; it0 < nk; it0 += PF) {
+        for (int it = 0; it < nk; ++it) {
+            if (it + 1 < nk) load(it + 1);
+            const __bf16* As = &sm[it & 1][0][0];
+            const __bf16* Bs = &sm[it & 1][1][0];
 #pragma unroll
-            for (int u = 0; u < PF; ++u) {
-                const int it = it0 + u;   // it % PF == u
-                if (it < nk) {
-                    compute(it & 1);
-                    if (it + 1 < nk) store((it + 1) & 1, w[(u + 1) % PF]);
-                    if (it + 1 + PF < nk) load(it + 1 + PF, w[(u + 1) % PF]);
-                    __syncthreads();
+            for (int kk = 0; kk < BKW / 32; ++kk) {
+                bf16x8 ah[4], bh[4];
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    ah[t] = *reinterpret_cast<const bf16x8*>(As + tw_at(wm + t * 16 + li, 4 * kk + lq));
+                    bh[t] = *reinterpret_cast<const bf16x8*>(Bs + tw_at(wn + t * 16 + li, 4 * kk + lq));
                 }
+#pragma unroll
+                for (int ti = 0; ti < 4; ++ti)
+#pragma unroll
+                    for (int tj = 0; tj < 4; ++tj)
+                        acc[ti][tj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bh[tj], ah[ti], acc[ti][tj], 0, 0, 0);
             }
+            if (it + 1 < nk) store((it + 1) & 1);
+            __syncthreads();
         }
     }
     if (db_blk) {
@@ -1394,31 +1343,7 @@ __global__ __launch_bounds__(NT) void gemm_bs_dw_kernel(const GemmArgs g0, int k
             }
         }
     }
-    // register r of lane (l32, lh) of acc[ti][tj] holds
-    // C[wm + 32 ti + l32][wn + 32 tj + 8 (r / 4) + 4 lh + r % 4]: four runs of
-    // four columns of one row, stored straight from the accumulators
-    float* C = PARTIAL ? g.C + (long)bz * part_stride : g.C;
-    const bool vo = (((uintptr_t)C | (uintptr_t)(g.ldc * 4)) & 15) == 0;
-#pragma unroll
-    for (int ti = 0; ti < 2; ++ti) {
-        const int m = m0 + wm + 32 * ti + l32;
-        if (m >= g.M) continue;
-#pragma unroll
-        for (int tj = 0; tj < 2; ++tj)
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const int n = n0 + wn + 32 * tj + 8 * q + 4 * lh;
-                const floatx4 v = floatx4{acc[ti][tj][4 * q], acc[ti][tj][4 * q + 1], acc[ti][tj][4 * q + 2],
-                                          acc[ti][tj][4 * q + 3]};
-                if (vo && n + 3 < g.N) {
-                    st_g4(C + (long)m * g.ldc + n, v);
-                } else {
-#pragma unroll
-                    for (int r = 0; r < 4; ++r)
-                        if (n + r < g.N) C[(long)m * g.ldc + n + r] = v[r];
-                }
-            }
-    }
+    gemm_epilogue<EPI_STORE, PARTIAL>(g, acc, m0, n0, wm, wn, li, lq, part_stride, nullptr, bz);
 }
 
 // sum_k bp[k * M] for k < splits in order: loads issued 16 at a time ahead of

@@ -34,6 +34,17 @@ constexpr int NT = 256;
 constexpr int UPD_U = 2;      // float4s per thread and chunk in pass 2, loaded together
 constexpr int UPD_BLOCKS = 512;   // pass-2 workgroups (persistent, striding over the chunks)
 
+// streaming loads / stores of the update (nontemporal: none of p, g, m, v is
+// read again in this launch; 26.7 -> 25.9 us per update by launch events)
+typedef float ntfx4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ float4 ntl(const float4* p) {
+    const ntfx4 v = __builtin_nontemporal_load(reinterpret_cast<const ntfx4*>(p));
+    return make_float4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ void nts(float4 v, float4* p) {
+    const ntfx4 x = {v.x, v.y, v.z, v.w};
+    __builtin_nontemporal_store(x, reinterpret_cast<ntfx4*>(p));
+}
 __device__ __forceinline__ float sq4(float4 v) { return (v.x * v.x + v.y * v.y) + (v.z * v.z + v.w * v.w); }
 
 __global__ __launch_bounds__(NT_NORM) void adam_norm_kernel(const float4* __restrict__ g, long n4,
@@ -82,10 +93,10 @@ __global__ __launch_bounds__(NT) void adam_update_kernel(float4* __restrict__ p,
     for (int u = 0; u < U; ++u) {
         const long i = base + (long)u * NT;
         if (i < n4) {
-            gg[u] = g[i];
-            mm[u] = m[i];
-            vv[u] = v[i];
-            pp[u] = p[i];
+            gg[u] = ntl(g + i);
+            mm[u] = ntl(m + i);
+            vv[u] = ntl(v + i);
+            pp[u] = ntl(p + i);
         }
     }
     __shared__ float red[NT / 64];
@@ -115,10 +126,10 @@ __global__ __launch_bounds__(NT) void adam_update_kernel(float4* __restrict__ p,
         for (int u = 0; u < U; ++u) {
             const long i = nb + (long)u * NT;
             if (i < n4) {
-                g2[u] = g[i];
-                m2[u] = m[i];
-                v2[u] = v[i];
-                p2[u] = p[i];
+                g2[u] = ntl(g + i);
+                m2[u] = ntl(m + i);
+                v2[u] = ntl(v + i);
+                p2[u] = ntl(p + i);
             }
         }
 #pragma unroll
@@ -135,9 +146,9 @@ __global__ __launch_bounds__(NT) void adam_update_kernel(float4* __restrict__ p,
                 }
                 PT_ADAM_LANE(x) PT_ADAM_LANE(y) PT_ADAM_LANE(z) PT_ADAM_LANE(w)
 #undef PT_ADAM_LANE
-                m[i] = mm[u];
-                v[i] = vv[u];
-                p[i] = pp[u];
+                nts(mm[u], m + i);
+                nts(vv[u], v + i);
+                nts(pp[u], p + i);
             }
             gg[u] = g2[u];
             mm[u] = m2[u];

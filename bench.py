@@ -135,8 +135,11 @@ def algorithmic_gemm_bytes(dm, obs_rows, bf16_blocks=False):
             dx = M * N + N * K + M * K
             dw = M * N + M * K + N * K
             # the GELU backward reads the saved pre-activation in the dX
-            # product of the layer after it (one extra M x N read per GELU layer)
-            tot += 4.0 * (fwd + dx + dw + (M * N if gelu else 0))
+            # product of the layer after it (one extra M x N read per GELU layer);
+            # a residual product at d = 256 also writes the LayerNorm of its
+            # output (y, mean, rstd) in the same launch
+            ln = M * N + 2 * M if resid and N == 256 else 0
+            tot += 4.0 * (fwd + dx + dw + (M * N if gelu else 0) + ln)
     return tot
 
 
@@ -435,7 +438,7 @@ def main():
     peak = BF16_MFMA_PEAK_TFLOPS if bf16 else FP32_MFMA_PEAK_TFLOPS
     traffic = measured_gemm_traffic()
     kname = ("gemm_bs32_kernel + gemm_bs_dw_kernel (trunk blocks, bf16 operands) + gemm_bf16_k16_kernel"
-             if bf16 else "gemm_f32_dma_kernel + gemm_f32_kernel")
+             if bf16 else "gemm_f32_dma_kernel + gemm_f32_kernel + gemm_resid_ln_kernel")
     roof = dict(bound="mfma", kernel=f"{kname} (all launches: trunk, token, option and head GEMMs)",
                 achieved=round(achieved, 3), peak=peak, unit="TFLOP/s",
                 frac=round(achieved / peak, 4),
@@ -447,6 +450,10 @@ def main():
                 executed_tflops=round(exec_flops.value / gemm_s / 1e12, 3),
                 useful_tflop_per_step=round(useful / K / 1e12, 4),
                 mean_valid_seq=round(float(np.mean(lv)), 2))
+    if not bf16 and dm.d == 256:
+        roof["fused_layernorm"] = ("the blocks' residual products (out-projection, FFN2) run the LayerNorm that "
+                                   "reads their output in the same launch (gemm_resid_ln_kernel): its time and "
+                                   "its output bytes are inside these figures")
     if bf16:
         # The products' arithmetic intensity (useful flops over the operand /
         # output bytes: bf16 in the trunk blocks, fp32 residual stream and

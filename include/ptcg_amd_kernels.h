@@ -90,6 +90,17 @@ int ptcg_kernel_colsum(const float* X, int64_t ldx, int M, int N, float* out,
  * 2048*D floats.                                                          */
 int ptcg_kernel_layernorm_fwd(const float* x, const float* w, const float* b, float* y,
                               float* mean, float* rstd, int rows, int D, void* stream);
+/* A pre-LN block's residual product fused with the LayerNorm that reads its
+ * output: C (rows, 256) = A (rows, K) W^T + bias + R, then y = LN(C) lnw +
+ * lnb with mean / rstd (eps 1e-5), in one launch.  W (256, K) and A at row
+ * stride K; R, C, y at row stride 256; K a multiple of 16; 16 B aligned.
+ * rows_dev (nullable): a device row count, rows <= it are processed.
+ * Replaces the residual add + LayerNorm pair of the block forward
+ * (ptcg_model.cu's pt_linear with residual then pt_ln_fwd,
+ * ptcg_kernels.cuh:42-108,132-175).                                       */
+int ptcg_kernel_gemm_resid_ln(int rows, int K, const float* A, const float* W, const float* bias,
+                              const float* R, float* C, const float* lnw, const float* lnb, float* y,
+                              float* mean, float* rstd, const int* rows_dev, void* stream);
 int ptcg_kernel_layernorm_bwd(const float* dy, const float* x, const float* w,
                               const float* mean, const float* rstd, const float* dres,
                               float* dx, float* dw, float* db, int rows, int D,

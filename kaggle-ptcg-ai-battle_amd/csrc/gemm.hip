@@ -898,6 +898,131 @@ __global__ __launch_bounds__(NT) void gemm_f32_dma_kernel(const GemmArgs g0, int
     gemm_dma_tile<AT, BT, EPI, PARTIAL, DB>(g0, k_chunk0, part_stride, blockIdx.x, blockIdx.z, gridDim.z);
 }
 
+// ---------------------------------------------------------------- residual + LayerNorm
+// C = A W^T + bias + R (a pre-LN block's residual add, EPI_BIAS_RESID) at
+// N = 256, followed in the same launch by the LayerNorm of C's rows that the
+// next stage reads: Y = LN(C) lnw + lnb with its mean and rstd.  The unfused
+// pair is the DMA kernel's EPI_BIAS_RESID then ln_fwd_kernel, which reads C
+// back from HBM.  A workgroup owns 64 full rows: a 64 x 256 tile, the four
+// waves side by side, each a 64 x 64 sub-tile of 2 x 2
+// v_mfma_f32_32x32x2_f32 tiles with the DMA kernel's operand order, so every
+// output accumulates the same products in the same order.  Per 16-k stage
+// the A rows (one 16-row chunk) and W rows (four chunks) go global -> LDS by
+// DMA, two stages deep.  The tile leaves through LDS in two 32-row halves; a
+// wave then takes eight rows, one float4 per lane, adds bias and residual in
+// epi_store4_r's order and normalises in ln_fwd_kernel's order (two-pass
+// mean / variance by wave sums, eps 1e-5), so C, Y, mean and rstd equal the
+// unfused pair's bit for bit.  K % 16 == 0, N = 256 (host checked).
+constexpr int RL_BM = 64, RL_N = 256, RL_SST = RL_N + 4;
+__global__ __launch_bounds__(NT) void gemm_resid_ln_kernel(const GemmArgs g0, const float* __restrict__ lnw,
+        const float* __restrict__ lnb, float* __restrict__ Y, long ldy, float* __restrict__ mean,
+        float* __restrict__ rstd) {
+    const GemmArgs g = gemm_shape(g0);
+    const int m0 = blockIdx.x * RL_BM;
+    if (m0 >= g.M) return;   // beyond the (device) row count
+    constexpr int TA = RL_BM * BK, TB = RL_N * BK, STAGE = TA + TB;
+    constexpr int SMEM = 2 * STAGE > 32 * RL_SST ? 2 * STAGE : 32 * RL_SST;
+    __shared__ __align__(16) float smem[SMEM];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int l32 = lane & 31, lh = lane >> 5;
+    const int wn = 64 * wave;
+    floatx16 acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+    // exact operand extents (host checked < 2^31 bytes): rows past M read zeros
+    const unsigned ea = (unsigned)(((long)(g.M - 1) * g.lda + g.K) * 4);
+    const unsigned eb = (unsigned)(((long)(RL_N - 1) * g.ldb + g.K) * 4);
+    const int32x4_t ra = buffer_rsrc(g.A, ea), rb = buffer_rsrc(g.B, eb);
+    const int sa = dma_src<false>(wave, lane, m0, g.lda);
+    int sb[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) sb[j] = dma_src<false>(4 * wave + j, lane, 0, g.ldb);
+    auto issue = [&](int tile) {
+        const int k0 = tile * BK;
+        const float* st = smem + (tile & 1) * STAGE;
+        dma16(ra, st + wave * 256, (sa + k0) * 4);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) dma16(rb, st + TA + (4 * wave + j) * 256, (sb[j] + k0) * 4);
+    };
+    const int nk = g.K / BK;
+    issue(0);
+    for (int it = 0; it < nk; ++it) {
+        wait_vm<0>();      // this wave's loads of tile it have landed
+        __syncthreads();   // every wave's have; tile it - 1 is consumed
+        if (it + 1 < nk) issue(it + 1);
+        const float* Ab = smem + (it & 1) * STAGE;
+        const float* Bb = Ab + TA;
+        float a8[2][8], b8[2][8];
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const int k0 = 8 * lh + 4 * h;
+                const float4 va = *reinterpret_cast<const float4*>(Ab + dma_at<false>(32 * t + l32, k0));
+                const float4 vb = *reinterpret_cast<const float4*>(Bb + dma_at<false>(wn + 32 * t + l32, k0));
+                a8[t][4 * h] = va.x; a8[t][4 * h + 1] = va.y; a8[t][4 * h + 2] = va.z; a8[t][4 * h + 3] = va.w;
+                b8[t][4 * h] = vb.x; b8[t][4 * h + 1] = vb.y; b8[t][4 * h + 2] = vb.z; b8[t][4 * h + 3] = vb.w;
+            }
+#pragma unroll
+        for (int st = 0; st < 8; ++st)
+#pragma unroll
+            for (int ti = 0; ti < 2; ++ti)
+#pragma unroll
+                for (int tj = 0; tj < 2; ++tj)
+                    acc[ti][tj] = __builtin_amdgcn_mfma_f32_32x32x2f32(b8[tj][st], a8[ti][st], acc[ti][tj], 0, 0, 0);
+    }
+    // register r of lane (l32, lh) of acc[ti][tj] holds
+    // C[32 ti + l32][wn + 32 tj + 8 (r / 4) + 4 lh + r % 4]; half h = rows 32 h ..
+    const floatx4 bv = ld_v4(g.bias + 4 * lane);
+    const float4 ww = *reinterpret_cast<const float4*>(lnw + 4 * lane);
+    const float4 wb = *reinterpret_cast<const float4*>(lnb + 4 * lane);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        // this wave's eight rows of the half: residual segments loaded
+        // before the staging barriers (rows past M read R's first row)
+        floatx4 rv[8];
+#pragma unroll
+        for (int r = 0; r < 8; ++r) {
+            const int m = m0 + 32 * h + 8 * wave + r;
+            rv[r] = ld_v4(g.R + (m < g.M ? (long)m * g.ldr + 4 * lane : 0L));
+        }
+        __syncthreads();   // the stages are free (main loop done / previous half consumed)
+#pragma unroll
+        for (int tj = 0; tj < 2; ++tj)
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                *reinterpret_cast<floatx4*>(smem + l32 * RL_SST + wn + 32 * tj + 8 * q + 4 * lh) =
+                    floatx4{acc[h][tj][4 * q], acc[h][tj][4 * q + 1], acc[h][tj][4 * q + 2], acc[h][tj][4 * q + 3]};
+        __syncthreads();
+#pragma unroll
+        for (int r = 0; r < 8; ++r) {
+            const int lr = 8 * wave + r, m = m0 + 32 * h + lr;
+            if (m >= g.M) break;   // uniform over the wave; later rows are past M too
+            const floatx4 v = *reinterpret_cast<const floatx4*>(smem + lr * RL_SST + 4 * lane);
+            const floatx4 x = (v + bv) + rv[r];
+            st_g4(g.C + (long)m * g.ldc + 4 * lane, x);
+            const float mu = wave_sum((x[0] + x[1]) + (x[2] + x[3])) / (float)RL_N;
+            const float a = x[0] - mu, b = x[1] - mu, c = x[2] - mu, d = x[3] - mu;
+            const float var = wave_sum((a * a + b * b) + (c * c + d * d)) / (float)RL_N;
+            const float rs = 1.0f / sqrtf(var + 1e-5f);
+            if (lane == 0) {
+                mean[m] = mu;
+                rstd[m] = rs;
+            }
+            float4 o;
+            o.x = (x[0] - mu) * rs * ww.x + wb.x;
+            o.y = (x[1] - mu) * rs * ww.y + wb.y;
+            o.z = (x[2] - mu) * rs * ww.z + wb.z;
+            o.w = (x[3] - mu) * rs * ww.w + wb.w;
+            *reinterpret_cast<float4*>(Y + (long)m * ldy + 4 * lane) = o;
+        }
+    }
+}
+
 // Grouped launch: several independent products (different shapes and
 // operands, one layout and epilogue) in one grid.  Work item w belongs to
 // product item_group[w]; its logical tile and K split follow from the
@@ -1861,6 +1986,32 @@ static int gemm_bs_dw(const GemmArgs& g, float* ws, long ws_floats, hipStream_t 
         launch_splitk_reduce<false>(g.C, g.ldc, ws, part_stride, splits, g.M, g.N, db ? g.dbias : nullptr, true, s);
         PT_LAUNCH_CHECK();
     }
+    return PTCG_OK;
+}
+
+// The residual product of a pre-LN block fused with the LayerNorm that reads
+// its output (gemm_resid_ln_kernel).  g: EPI_BIAS_RESID with k-contiguous A
+// (rows x K) and W (256 x K); fp32.  Returns PTCG_ERR_* when the shape or
+// layout does not fit (the caller then runs the unfused pair).
+bool pt_gemm_resid_ln_fits(const GemmArgs& g) {
+    const uintptr_t al = (uintptr_t)g.A | (uintptr_t)g.B | (uintptr_t)g.C | (uintptr_t)g.R | (uintptr_t)g.bias |
+                         (uintptr_t)((g.lda | g.ldb | g.ldc | g.ldr) * 4);
+    return g.N == RL_N && g.K % BK == 0 && g.M > 0 && !g.a_t && !g.b_t && g.epi == EPI_BIAS_RESID && !g.bs &&
+           !g.obf && g.prec == 0 && g.bias && g.R && (al & 15) == 0 && !g.Kdev && dma_ok(g);
+}
+int pt_gemm_resid_ln(const GemmArgs& g, const float* lnw, const float* lnb, float* y, long ldy, float* mean,
+                     float* rstd, hipStream_t s) {
+    PT_REQUIRE(g.A && g.B && g.C && lnw && lnb && y && mean && rstd, "gemm + layernorm: null operand");
+    PT_REQUIRE(pt_gemm_resid_ln_fits(g),
+               "gemm + layernorm: needs fp32 bias + residual with N = 256, K %% 16 == 0, k-contiguous operands, "
+               "16 B aligned (M=%d, N=%d, K=%d)", g.M, g.N, g.K);
+    PT_REQUIRE((((uintptr_t)lnw | (uintptr_t)lnb | (uintptr_t)y | (uintptr_t)(ldy * 4)) & 15) == 0,
+               "gemm + layernorm: LayerNorm parameters and output need 16 B alignment");
+    const int slot = pt_prof_open(s);
+    hipLaunchKernelGGL(gemm_resid_ln_kernel, dim3(pt_cdiv(g.M, RL_BM)), dim3(NT), 0, s, g, lnw, lnb, y, ldy, mean,
+                       rstd);
+    PT_LAUNCH_CHECK();
+    pt_prof_close(slot, g_gemm_class, 2.0 * g.M * (double)g.N * g.K, s);
     return PTCG_OK;
 }
 

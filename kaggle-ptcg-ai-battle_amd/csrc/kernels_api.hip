@@ -125,6 +125,21 @@ extern "C" int ptcg_kernel_layernorm_fwd(const float* x, const float* w, const f
     return pt_ln_fwd(x, D, w, b, y, D, mean, rstd, rows, D, (hipStream_t)stream);
 }
 
+extern "C" int ptcg_kernel_gemm_resid_ln(int rows, int K, const float* A, const float* W, const float* bias,
+                                         const float* R, float* C, const float* lnw, const float* lnb, float* y,
+                                         float* mean, float* rstd, const int* rows_dev, void* stream) {
+    PT_REQUIRE(rows > 0 && K > 0, "kernel_gemm_resid_ln: empty shape %d x %d", rows, K);
+    GemmArgs g{};
+    g.M = rows; g.N = 256; g.K = K;
+    g.A = A; g.lda = K;
+    g.B = W; g.ldb = K;
+    g.C = C; g.ldc = 256;
+    g.bias = bias; g.R = R; g.ldr = 256;
+    g.epi = EPI_BIAS_RESID;
+    g.Mdev = rows_dev;
+    return pt_gemm_resid_ln(g, lnw, lnb, y, 256, mean, rstd, (hipStream_t)stream);
+}
+
 extern "C" int ptcg_kernel_layernorm_bwd(const float* dy, const float* x, const float* w,
                                          const float* mean, const float* rstd, const float* dres,
                                          float* dx, float* dw, float* db, int rows, int D,

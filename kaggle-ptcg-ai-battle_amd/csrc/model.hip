@@ -171,6 +171,28 @@ static int linf(const PtcgModel* m, const float* X, const float* W, const float*
                 int out, int epi, const float* R, float* Y2, hipStream_t s, const int* Mdev = nullptr) {
     return lin(m, X, in, W, b, Y, out, rows, in, out, epi, R, out, Y2, out, s, Mdev);
 }
+// A LayerNorm that reads a residual product's output: weights, output and
+// statistics (eps 1e-5, rows of d)
+struct LnOut {
+    const float* w; const float* b; float* y; float* mu; float* rs;
+};
+// Y = X W^T + b + R (rows x out, out = d), then ln(Y): one fused launch when
+// the shape fits it (fp32, d = 256), else the product and pt_ln_fwd
+static int lin_resid_ln(const PtcgModel* m, const float* X, const float* W, const float* b, float* Y, int rows,
+                        int in, int out, const float* R, const LnOut& ln, hipStream_t s, const int* Mdev) {
+    GemmArgs g{};
+    g.prec = m->prec;
+    g.Mdev = Mdev;
+    g.M = rows; g.N = out; g.K = in;
+    g.A = X; g.lda = in;
+    g.B = W; g.ldb = in;
+    g.C = Y; g.ldc = out;
+    g.bias = b; g.R = R; g.ldr = out;
+    g.epi = EPI_BIAS_RESID;
+    if (pt_gemm_resid_ln_fits(g)) return pt_gemm_resid_ln(g, ln.w, ln.b, ln.y, out, ln.mu, ln.rs, s);
+    PT_TRY(pt_gemm(g, m->ws, m->ws_floats, s));
+    return pt_ln_fwd(Y, out, ln.w, ln.b, ln.y, out, ln.mu, ln.rs, rows, out, s, Mdev);
+}
 // dX = dY W[:, :in] : dY (rows, out) ld lddy ; W (out, ldw) ; dX (rows, in) ld lddx
 static int ldxw_(const PtcgModel* m, const float* dY, long lddy, const float* W, long ldw, float* dX, long lddx,
                  int rows, int in, int out, int epi, const float* R, long ldr, hipStream_t s,
@@ -679,9 +701,14 @@ float* pt_model_ws(const PtcgModel* m, long* floats) { *floats = m->ws_floats; r
 // (nullable) and per-sample row offsets (rows 0, coff null: N * L rows)
 // bw (bf16 variant): the block's bf16 weight copies; the block's activations
 // are then stored in bf16 (the residual stream xin / xmid / xout stays fp32)
+// fp32 blocks: ln1_done = the previous block's FFN2 launch already wrote this
+// block's LayerNorm 1 (a.ln1, mu1, rs1); next (nullable) = the LayerNorm that
+// reads xout (the next block's LayerNorm 1 or the trunk's final one), run with
+// the FFN2 residual product
 static int block_fwd(PtcgModel* m, const BlockP& w, const BlockA& a, int L, const float* keep, const float* xin,
                      float* xout, hipStream_t s, int rows = 0, const int* Tr = nullptr,
-                     const int* coff = nullptr, const BlockW* bw = nullptr) {
+                     const int* coff = nullptr, const BlockW* bw = nullptr, bool ln1_done = false,
+                     const LnOut* next = nullptr) {
     const PtcgDims& d = m->dm;
     const int NL = rows ? rows : m->N * L, D = d.d;
     if (bw) {
@@ -694,12 +721,13 @@ static int block_fwd(PtcgModel* m, const BlockP& w, const BlockA& a, int L, cons
         PT_TRY(blin(m, a.ffa, d.ffn, bw->f2, w.f2b, xout, D, NL, EPI_BIAS_RESID, false, a.xmid, nullptr, s, Tr));
         return PTCG_OK;
     }
-    PT_TRY(pt_ln_fwd(xin, D, w.ln1w, w.ln1b, a.ln1, D, a.mu1, a.rs1, NL, D, s, Tr));
+    if (!ln1_done) PT_TRY(pt_ln_fwd(xin, D, w.ln1w, w.ln1b, a.ln1, D, a.mu1, a.rs1, NL, D, s, Tr));
     PT_TRY(linf(m, a.ln1, w.qkvw, w.qkvb, a.qkv, NL, D, 3 * D, EPI_BIAS, nullptr, nullptr, s, Tr));
     PT_TRY(pt_attn_fwd(a.qkv, keep, a.ctx, a.lse, m->N, L, d.heads, m->dx.dh, s, coff, m->prec));
-    PT_TRY(linf(m, a.ctx, w.projw, w.projb, a.xmid, NL, D, D, EPI_BIAS_RESID, xin, nullptr, s, Tr));
-    PT_TRY(pt_ln_fwd(a.xmid, D, w.ln2w, w.ln2b, a.ln2, D, a.mu2, a.rs2, NL, D, s, Tr));
+    PT_TRY(lin_resid_ln(m, a.ctx, w.projw, w.projb, a.xmid, NL, D, D, xin, LnOut{w.ln2w, w.ln2b, a.ln2, a.mu2, a.rs2},
+                        s, Tr));
     PT_TRY(linf(m, a.ln2, w.f1w, w.f1b, a.ffp, NL, D, d.ffn, EPI_BIAS_GELU_D, nullptr, a.ffa, s, Tr));
+    if (next) return lin_resid_ln(m, a.ffa, w.f2w, w.f2b, xout, NL, d.ffn, D, a.xmid, *next, s, Tr);
     PT_TRY(linf(m, a.ffa, w.f2w, w.f2b, xout, NL, d.ffn, D, EPI_BIAS_RESID, a.xmid, nullptr, s, Tr));
     return PTCG_OK;
 }
@@ -796,12 +824,23 @@ extern "C" int ptcg_model_forward(PtcgModel* m, const float* obs, const int32_t*
     const bool tr = m->train;
     const bool b16 = m->prec == 1;
     if (b16) PT_TRY(bf16_refresh(m, s));
-    for (int i = 0; i < d.layers; ++i)
+    // fp32: each block's FFN2 residual product also runs the LayerNorm that
+    // reads its output (the next block's LayerNorm 1, or the final one)
+    for (int i = 0; i < d.layers; ++i) {
+        LnOut nx{m->lnf_w, m->lnf_b, m->h, m->lnf_mu, m->lnf_rs};
+        if (i + 1 < d.layers) {
+            const BlockP& wn = m->blk[i + 1];
+            const BlockA& an = m->ba[tr ? i + 1 : 0];
+            nx = LnOut{wn.ln1w, wn.ln1b, an.ln1, an.mu1, an.rs1};
+        }
         PT_TRY(block_fwd(m, m->blk[i], m->ba[tr ? i : 0], x.l_seq, m->keep, m->x[tr ? i : i % 2],
-                         m->x[tr ? i + 1 : (i + 1) % 2], s, m->rows, Td, coff, b16 ? &m->bw[i] : nullptr));
+                         m->x[tr ? i + 1 : (i + 1) % 2], s, m->rows, Td, coff, b16 ? &m->bw[i] : nullptr,
+                         !b16 && i > 0, b16 ? nullptr : &nx));
+    }
     const int NL = N * x.l_seq;
-    PT_TRY(pt_ln_fwd(m->x[tr ? d.layers : d.layers % 2], D, m->lnf_w, m->lnf_b, m->h, D, m->lnf_mu, m->lnf_rs,
-                     m->rows, D, s, Td));
+    if (b16)
+        PT_TRY(pt_ln_fwd(m->x[tr ? d.layers : d.layers % 2], D, m->lnf_w, m->lnf_b, m->h, D, m->lnf_mu, m->lnf_rs,
+                         m->rows, D, s, Td));
 
     // option scorer over the option rows (all N * n_opt, or the legal ones)
     const int NJ = m->orows;

@@ -147,6 +147,66 @@ def test_colsum(cuda):
     assert rel_l2(out.cpu(), X.double().sum(0)) < 1e-6
 
 
+# rows: one row, a partial 64-row tile, whole tiles, the trunk's 37.4k rows
+@pytest.mark.parametrize("rows,K", [(1, 256), (63, 256), (200, 1024), (1024, 256), (37417, 256), (3001, 1024)])
+def test_gemm_resid_ln(rows, K, cuda):
+    """The residual product fused with the LayerNorm that reads it: C, y,
+    mean and rstd against float64 (C = A W^T + bias + R; y = LN(C) w + b),
+    bit-equal to the unfused pair (the plain product, no split, then the
+    LayerNorm kernel), and a device row count leaves the later rows alone."""
+    N = 256
+    g = torch.Generator().manual_seed(rows + K)
+    A = torch.randn(rows, K, generator=g) / math.sqrt(K)
+    W = torch.randn(N, K, generator=g)
+    bias = torch.randn(N, generator=g) * 0.1
+    R = torch.randn(rows, N, generator=g) * 2 + 0.5
+    lw = torch.randn(N, generator=g)
+    lb = torch.randn(N, generator=g)
+    C64 = A.double() @ W.double().T + bias.double() + R.double()
+    y64 = torch.nn.functional.layer_norm(C64, (N,), lw.double(), lb.double(), eps=1e-5)
+    mu64 = C64.mean(1)
+    rs64 = 1.0 / torch.sqrt(C64.var(1, unbiased=False) + 1e-5)
+    L = native.lib()
+    dA, dW, db, dR, dlw, dlb = dev(A), dev(W), dev(bias), dev(R), dev(lw), dev(lb)
+    C, y, mu, rs = empty(rows, N), empty(rows, N), empty(rows), empty(rows)
+    native.check(L.ptcg_kernel_gemm_resid_ln(rows, K, P(dA), P(dW), P(db), P(dR), P(C), P(dlw), P(dlb), P(y),
+                                             P(mu), P(rs), None, None))
+    # the unfused pair: EPI_BIAS_RESID (3) without a workspace (no split-K, no tail), then LayerNorm
+    C2, y2, mu2, rs2 = empty(rows, N), empty(rows, N), empty(rows), empty(rows)
+    native.check(L.ptcg_kernel_gemm(rows, N, K, P(dA), K, 0, P(dW), K, 0, P(C2), N, 3, P(db), P(dR), N,
+                                    None, 0, None, 0, None))
+    native.check(L.ptcg_kernel_layernorm_fwd(P(C2), P(dlw), P(dlb), P(y2), P(mu2), P(rs2), rows, N, None))
+    torch.cuda.synchronize()
+    assert rel_l2(C.cpu(), C64) < 1e-6 and max_rel(C.cpu(), C64) < 1e-5
+    assert rel_l2(y.cpu(), y64) < 1e-5 and max_rel(y.cpu(), y64) < 1e-4
+    assert rel_l2(mu.cpu(), mu64) < 1e-5 and rel_l2(rs.cpu(), rs64) < 1e-5
+    for a, b in ((C, C2), (y, y2), (mu, mu2), (rs, rs2)):
+        assert torch.equal(a, b)
+    if rows > 64:
+        # device row count: rows past it keep their contents
+        cut = rows // 2 + 5
+        nd = torch.tensor([cut], dtype=torch.int32, device="cuda")
+        C3 = torch.full((rows, N), 7.0, device="cuda")
+        y3 = torch.full((rows, N), 7.0, device="cuda")
+        mu3, rs3 = torch.full((rows,), 7.0, device="cuda"), torch.full((rows,), 7.0, device="cuda")
+        native.check(L.ptcg_kernel_gemm_resid_ln(rows, K, P(dA), P(dW), P(db), P(dR), P(C3), P(dlw), P(dlb),
+                                                 P(y3), P(mu3), P(rs3), P(nd), None))
+        torch.cuda.synchronize()
+        assert torch.equal(C3[:cut], C[:cut]) and torch.equal(y3[:cut], y[:cut])
+        assert torch.equal(mu3[:cut], mu[:cut]) and torch.equal(rs3[:cut], rs[:cut])
+        assert bool((C3[cut:] == 7.0).all()) and bool((y3[cut:] == 7.0).all())
+        assert bool((mu3[cut:] == 7.0).all()) and bool((rs3[cut:] == 7.0).all())
+
+
+def test_gemm_resid_ln_rejects_other_shapes(cuda):
+    L = native.lib()
+    a, w, b, r = empty(8, 100), empty(256, 100), empty(256), empty(8, 256)
+    out = [empty(8, 256), empty(256), empty(256), empty(8, 256), empty(8), empty(8)]
+    with pytest.raises(RuntimeError, match="gemm \\+ layernorm"):
+        native.check(L.ptcg_kernel_gemm_resid_ln(8, 100, P(a), P(w), P(b), P(r), P(out[0]), P(out[1]), P(out[2]),
+                                                 P(out[3]), P(out[4]), P(out[5]), None, None))
+
+
 # (20001, 256): several row pairs per wave in the backward and an odd tail;
 # (5, 256): fewer rows than one workgroup's waves
 @pytest.mark.parametrize("rows,D", [(1000, 256), (37, 64), (130, 1024), (9, 300), (1284, 634), (50, 127),

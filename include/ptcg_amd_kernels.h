@@ -94,13 +94,15 @@ int ptcg_kernel_layernorm_fwd(const float* x, const float* w, const float* b, fl
  * output: C (rows, 256) = A (rows, K) W^T + bias + R, then y = LN(C) lnw +
  * lnb with mean / rstd (eps 1e-5), in one launch.  W (256, K) and A at row
  * stride K; R, C, y at row stride 256; K a multiple of 16; 16 B aligned.
- * rows_dev (nullable): a device row count, rows <= it are processed.
+ * bf16 = 1: A, W and y hold bf16 (bf16 products, fp32 accumulation, C, R,
+ * statistics fp32; K a multiple of 32).  rows_dev (nullable): a device row
+ * count, rows < it are processed.
  * Replaces the residual add + LayerNorm pair of the block forward
  * (ptcg_model.cu's pt_linear with residual then pt_ln_fwd,
  * ptcg_kernels.cuh:42-108,132-175).                                       */
-int ptcg_kernel_gemm_resid_ln(int rows, int K, const float* A, const float* W, const float* bias,
-                              const float* R, float* C, const float* lnw, const float* lnb, float* y,
-                              float* mean, float* rstd, const int* rows_dev, void* stream);
+int ptcg_kernel_gemm_resid_ln(int rows, int K, const void* A, const void* W, const float* bias,
+                              const float* R, float* C, const float* lnw, const float* lnb, void* y,
+                              float* mean, float* rstd, int bf16, const int* rows_dev, void* stream);
 int ptcg_kernel_layernorm_bwd(const float* dy, const float* x, const float* w,
                               const float* mean, const float* rstd, const float* dres,
                               float* dx, float* dw, float* db, int rows, int D,

@@ -210,11 +210,12 @@ struct GemmArgs {
 // dims multiples of 4, 16 B-aligned bases.  Weight-gradient shapes
 // (large K, small M*N) are split over K with a deterministic reduction.
 int pt_gemm(const GemmArgs& g, float* splitk_ws, long splitk_ws_floats, hipStream_t s);
-// C = A W^T + bias + R (N = 256) and, in the same launch, y = LayerNorm(C)
-// with its mean / rstd (eps 1e-5); pt_gemm_resid_ln_fits says whether g fits
+// C = A W^T + bias + R (N = 256; fp32 or, with g.bs, bf16 operands) and, in
+// the same launch, y = LayerNorm(C) with its mean / rstd (eps 1e-5; ybf: y in
+// bf16); pt_gemm_resid_ln_fits says whether g fits
 bool pt_gemm_resid_ln_fits(const GemmArgs& g);
 int pt_gemm_resid_ln(const GemmArgs& g, const float* lnw, const float* lnb, float* y, long ldy, float* mean,
-                     float* rstd, hipStream_t s);
+                     float* rstd, hipStream_t s, int ybf = 0);
 
 // One product of a grouped launch (pt_gemm_grouped): all products of a
 // launch share the operand layout (a_t, b_t) and epilogue, and must meet the

@@ -913,7 +913,12 @@ __global__ __launch_bounds__(NT) void gemm_f32_dma_kernel(const GemmArgs g0, int
 // epi_store4_r's order and normalises in ln_fwd_kernel's order (two-pass
 // mean / variance by wave sums, eps 1e-5), so C, Y, mean and rstd equal the
 // unfused pair's bit for bit.  K % 16 == 0, N = 256 (host checked).
+// BF: A and W hold bf16 (the mixed-precision variant's activations and weight
+// copies; K, lda, ldb in float units, 2 bf16 per float) and the products run
+// on v_mfma_f32_32x32x16_bf16 in gemm_bs32_kernel's fragment order; YB: Y is
+// stored in bf16 (round to nearest even), ldy in bf16 elements.
 constexpr int RL_BM = 64, RL_N = 256, RL_SST = RL_N + 4;
+template <bool BF, bool YB>
 __global__ __launch_bounds__(NT) void gemm_resid_ln_kernel(const GemmArgs g0, const float* __restrict__ lnw,
         const float* __restrict__ lnb, float* __restrict__ Y, long ldy, float* __restrict__ mean,
         float* __restrict__ rstd) {
@@ -956,6 +961,23 @@ __global__ __launch_bounds__(NT) void gemm_resid_ln_kernel(const GemmArgs g0, co
         if (it + 1 < nk) issue(it + 1);
         const float* Ab = smem + (it & 1) * STAGE;
         const float* Bb = Ab + TA;
+        if constexpr (BF) {
+#pragma unroll
+            for (int st = 0; st < 2; ++st) {
+                bf16x8 ah[2], bh[2];
+#pragma unroll
+                for (int t = 0; t < 2; ++t) {
+                    ah[t] = *reinterpret_cast<const bf16x8*>(Ab + dma_at<false>(32 * t + l32, 4 * (2 * st + lh)));
+                    bh[t] = *reinterpret_cast<const bf16x8*>(Bb + dma_at<false>(wn + 32 * t + l32, 4 * (2 * st + lh)));
+                }
+#pragma unroll
+                for (int ti = 0; ti < 2; ++ti)
+#pragma unroll
+                    for (int tj = 0; tj < 2; ++tj)
+                        acc[ti][tj] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bh[tj], ah[ti], acc[ti][tj], 0, 0, 0);
+            }
+            continue;
+        }
         float a8[2][8], b8[2][8];
 #pragma unroll
         for (int t = 0; t < 2; ++t)
@@ -1018,7 +1040,11 @@ __global__ __launch_bounds__(NT) void gemm_resid_ln_kernel(const GemmArgs g0, co
             o.y = (x[1] - mu) * rs * ww.y + wb.y;
             o.z = (x[2] - mu) * rs * ww.z + wb.z;
             o.w = (x[3] - mu) * rs * ww.w + wb.w;
-            *reinterpret_cast<float4*>(Y + (long)m * ldy + 4 * lane) = o;
+            if constexpr (YB)
+                *reinterpret_cast<bf16x4*>(reinterpret_cast<__bf16*>(Y) + (long)m * ldy + 4 * lane) =
+                    bf16x4{(__bf16)o.x, (__bf16)o.y, (__bf16)o.z, (__bf16)o.w};
+            else
+                *reinterpret_cast<float4*>(Y + (long)m * ldy + 4 * lane) = o;
         }
     }
 }
@@ -1991,25 +2017,41 @@ static int gemm_bs_dw(const GemmArgs& g, float* ws, long ws_floats, hipStream_t 
 
 // The residual product of a pre-LN block fused with the LayerNorm that reads
 // its output (gemm_resid_ln_kernel).  g: EPI_BIAS_RESID with k-contiguous A
-// (rows x K) and W (256 x K); fp32.  Returns PTCG_ERR_* when the shape or
-// layout does not fit (the caller then runs the unfused pair).
+// (rows x K) and W (256 x K), fp32 output; fp32 operands, or bf16 ones (g.bs,
+// K a multiple of 32).  pt_gemm_resid_ln_fits says whether g fits (the caller
+// otherwise runs the product and the LayerNorm apart).  ybf: y in bf16.
+static GemmArgs resid_ln_float_units(const GemmArgs& g) {
+    GemmArgs f = g;
+    if (g.bs) {   // 2 bf16 per float: the DMA tile's units
+        f.K = g.K / 2;
+        f.lda = g.lda / 2;
+        f.ldb = g.ldb / 2;
+    }
+    return f;
+}
 bool pt_gemm_resid_ln_fits(const GemmArgs& g) {
     const uintptr_t al = (uintptr_t)g.A | (uintptr_t)g.B | (uintptr_t)g.C | (uintptr_t)g.R | (uintptr_t)g.bias |
-                         (uintptr_t)((g.lda | g.ldb | g.ldc | g.ldr) * 4);
-    return g.N == RL_N && g.K % BK == 0 && g.M > 0 && !g.a_t && !g.b_t && g.epi == EPI_BIAS_RESID && !g.bs &&
-           !g.obf && g.prec == 0 && g.bias && g.R && (al & 15) == 0 && !g.Kdev && dma_ok(g);
+                         (uintptr_t)(g.ldc * 4) | (uintptr_t)(g.ldr * 4) |
+                         (uintptr_t)((g.lda | g.ldb) * (g.bs ? 2 : 4));
+    const bool prec_ok = g.bs ? (g.K % 32 == 0 && g.lda % 8 == 0 && g.ldb % 8 == 0) : (g.prec == 0 && g.K % BK == 0);
+    return g.N == RL_N && g.M > 0 && prec_ok && !g.a_t && !g.b_t && g.epi == EPI_BIAS_RESID && !g.obf && g.bias &&
+           g.R && (al & 15) == 0 && !g.Kdev && dma_ok(resid_ln_float_units(g));
 }
 int pt_gemm_resid_ln(const GemmArgs& g, const float* lnw, const float* lnb, float* y, long ldy, float* mean,
-                     float* rstd, hipStream_t s) {
+                     float* rstd, hipStream_t s, int ybf) {
     PT_REQUIRE(g.A && g.B && g.C && lnw && lnb && y && mean && rstd, "gemm + layernorm: null operand");
     PT_REQUIRE(pt_gemm_resid_ln_fits(g),
-               "gemm + layernorm: needs fp32 bias + residual with N = 256, K %% 16 == 0, k-contiguous operands, "
-               "16 B aligned (M=%d, N=%d, K=%d)", g.M, g.N, g.K);
-    PT_REQUIRE((((uintptr_t)lnw | (uintptr_t)lnb | (uintptr_t)y | (uintptr_t)(ldy * 4)) & 15) == 0,
+               "gemm + layernorm: needs bias + residual with N = 256, K %% 16 == 0 (bf16 operands: %% 32), "
+               "k-contiguous operands, 16 B aligned (M=%d, N=%d, K=%d)", g.M, g.N, g.K);
+    PT_REQUIRE((((uintptr_t)lnw | (uintptr_t)lnb | (uintptr_t)y | (uintptr_t)(ldy * (ybf ? 2 : 4))) & 15) == 0,
                "gemm + layernorm: LayerNorm parameters and output need 16 B alignment");
+    const GemmArgs f = resid_ln_float_units(g);
+    const dim3 grid(pt_cdiv(g.M, RL_BM)), blk(NT);
     const int slot = pt_prof_open(s);
-    hipLaunchKernelGGL(gemm_resid_ln_kernel, dim3(pt_cdiv(g.M, RL_BM)), dim3(NT), 0, s, g, lnw, lnb, y, ldy, mean,
-                       rstd);
+    if (g.bs && ybf) hipLaunchKernelGGL((gemm_resid_ln_kernel<true, true>), grid, blk, 0, s, f, lnw, lnb, y, ldy, mean, rstd);
+    else if (g.bs) hipLaunchKernelGGL((gemm_resid_ln_kernel<true, false>), grid, blk, 0, s, f, lnw, lnb, y, ldy, mean, rstd);
+    else if (ybf) hipLaunchKernelGGL((gemm_resid_ln_kernel<false, true>), grid, blk, 0, s, f, lnw, lnb, y, ldy, mean, rstd);
+    else hipLaunchKernelGGL((gemm_resid_ln_kernel<false, false>), grid, blk, 0, s, f, lnw, lnb, y, ldy, mean, rstd);
     PT_LAUNCH_CHECK();
     pt_prof_close(slot, g_gemm_class, 2.0 * g.M * (double)g.N * g.K, s);
     return PTCG_OK;

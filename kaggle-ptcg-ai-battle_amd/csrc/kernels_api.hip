@@ -125,19 +125,20 @@ extern "C" int ptcg_kernel_layernorm_fwd(const float* x, const float* w, const f
     return pt_ln_fwd(x, D, w, b, y, D, mean, rstd, rows, D, (hipStream_t)stream);
 }
 
-extern "C" int ptcg_kernel_gemm_resid_ln(int rows, int K, const float* A, const float* W, const float* bias,
-                                         const float* R, float* C, const float* lnw, const float* lnb, float* y,
-                                         float* mean, float* rstd, const int* rows_dev, void* stream) {
+extern "C" int ptcg_kernel_gemm_resid_ln(int rows, int K, const void* A, const void* W, const float* bias,
+                                         const float* R, float* C, const float* lnw, const float* lnb, void* y,
+                                         float* mean, float* rstd, int bf16, const int* rows_dev, void* stream) {
     PT_REQUIRE(rows > 0 && K > 0, "kernel_gemm_resid_ln: empty shape %d x %d", rows, K);
     GemmArgs g{};
     g.M = rows; g.N = 256; g.K = K;
-    g.A = A; g.lda = K;
-    g.B = W; g.ldb = K;
+    g.prec = bf16 ? 1 : 0; g.bs = bf16 ? 1 : 0;
+    g.A = static_cast<const float*>(A); g.lda = K;
+    g.B = static_cast<const float*>(W); g.ldb = K;
     g.C = C; g.ldc = 256;
     g.bias = bias; g.R = R; g.ldr = 256;
     g.epi = EPI_BIAS_RESID;
     g.Mdev = rows_dev;
-    return pt_gemm_resid_ln(g, lnw, lnb, y, 256, mean, rstd, (hipStream_t)stream);
+    return pt_gemm_resid_ln(g, lnw, lnb, static_cast<float*>(y), 256, mean, rstd, (hipStream_t)stream, bf16);
 }
 
 extern "C" int ptcg_kernel_layernorm_bwd(const float* dy, const float* x, const float* w,

@@ -175,6 +175,7 @@ static int linf(const PtcgModel* m, const float* X, const float* W, const float*
 // statistics (eps 1e-5, rows of d)
 struct LnOut {
     const float* w; const float* b; float* y; float* mu; float* rs;
+    int ybf = 0;   // y stored in bf16 (the mixed-precision blocks' LayerNorm outputs)
 };
 // Y = X W^T + b + R (rows x out, out = d), then ln(Y): one fused launch when
 // the shape fits it (fp32, d = 256), else the product and pt_ln_fwd
@@ -189,9 +190,9 @@ static int lin_resid_ln(const PtcgModel* m, const float* X, const float* W, cons
     g.C = Y; g.ldc = out;
     g.bias = b; g.R = R; g.ldr = out;
     g.epi = EPI_BIAS_RESID;
-    if (pt_gemm_resid_ln_fits(g)) return pt_gemm_resid_ln(g, ln.w, ln.b, ln.y, out, ln.mu, ln.rs, s);
+    if (pt_gemm_resid_ln_fits(g)) return pt_gemm_resid_ln(g, ln.w, ln.b, ln.y, out, ln.mu, ln.rs, s, ln.ybf);
     PT_TRY(pt_gemm(g, m->ws, m->ws_floats, s));
-    return pt_ln_fwd(Y, out, ln.w, ln.b, ln.y, out, ln.mu, ln.rs, rows, out, s, Mdev);
+    return pt_ln_fwd(Y, out, ln.w, ln.b, ln.y, out, ln.mu, ln.rs, rows, out, s, Mdev, ln.ybf);
 }
 // dX = dY W[:, :in] : dY (rows, out) ld lddy ; W (out, ldw) ; dX (rows, in) ld lddx
 static int ldxw_(const PtcgModel* m, const float* dY, long lddy, const float* W, long ldw, float* dX, long lddx,
@@ -248,6 +249,24 @@ static int blin(const PtcgModel* m, const float* X, int in, const __bf16* Wb, co
 }
 // dW (out, in) = dY^T X, db = column sums of dY, with dY (rows, out) and X (rows, in) bf16
 // (on the side stream's workspace)
+// blin's residual product (bf16 X and weight copy, fp32 Y and R) followed by
+// ln(Y): one fused launch when the shape fits it, else the product and the
+// LayerNorm
+static int blin_resid_ln(const PtcgModel* m, const float* X, int in, const __bf16* Wb, const float* b, float* Y,
+                         int out, int rows, const float* R, const LnOut& ln, hipStream_t s, const int* Mdev) {
+    GemmArgs g{};
+    g.prec = 1; g.bs = 1;
+    g.Mdev = Mdev;
+    g.M = rows; g.N = out; g.K = in;
+    g.A = X; g.lda = in;
+    g.B = reinterpret_cast<const float*>(Wb); g.ldb = in;
+    g.C = Y; g.ldc = out;
+    g.bias = b; g.R = R; g.ldr = out;
+    g.epi = EPI_BIAS_RESID;
+    if (pt_gemm_resid_ln_fits(g)) return pt_gemm_resid_ln(g, ln.w, ln.b, ln.y, out, ln.mu, ln.rs, s, ln.ybf);
+    PT_TRY(pt_gemm(g, m->ws, m->ws_floats, s));
+    return pt_ln_fwd(Y, out, ln.w, ln.b, ln.y, out, ln.mu, ln.rs, rows, out, s, Mdev, ln.ybf);
+}
 static int bldw(PtcgModel* m, const float* dY, int out, const float* X, int in, float* dW, float* db, int rows,
                 hipStream_t s, const int* Kdev) {
     GemmArgs g{};
@@ -712,12 +731,13 @@ static int block_fwd(PtcgModel* m, const BlockP& w, const BlockA& a, int L, cons
     const PtcgDims& d = m->dm;
     const int NL = rows ? rows : m->N * L, D = d.d;
     if (bw) {
-        PT_TRY(pt_ln_fwd(xin, D, w.ln1w, w.ln1b, a.ln1, D, a.mu1, a.rs1, NL, D, s, Tr, 1));
+        if (!ln1_done) PT_TRY(pt_ln_fwd(xin, D, w.ln1w, w.ln1b, a.ln1, D, a.mu1, a.rs1, NL, D, s, Tr, 1));
         PT_TRY(blin(m, a.ln1, D, bw->qkv, w.qkvb, a.qkv, 3 * D, NL, EPI_BIAS, true, nullptr, nullptr, s, Tr));
         PT_TRY(pt_attn_fwd(a.qkv, keep, a.ctx, a.lse, m->N, L, d.heads, m->dx.dh, s, coff, 2));
-        PT_TRY(blin(m, a.ctx, D, bw->proj, w.projb, a.xmid, D, NL, EPI_BIAS_RESID, false, xin, nullptr, s, Tr));
-        PT_TRY(pt_ln_fwd(a.xmid, D, w.ln2w, w.ln2b, a.ln2, D, a.mu2, a.rs2, NL, D, s, Tr, 1));
+        PT_TRY(blin_resid_ln(m, a.ctx, D, bw->proj, w.projb, a.xmid, D, NL, xin,
+                             LnOut{w.ln2w, w.ln2b, a.ln2, a.mu2, a.rs2, 1}, s, Tr));
         PT_TRY(blin(m, a.ln2, D, bw->f1, w.f1b, a.ffp, d.ffn, NL, EPI_BIAS_GELU_D, true, nullptr, a.ffa, s, Tr));
+        if (next) return blin_resid_ln(m, a.ffa, d.ffn, bw->f2, w.f2b, xout, D, NL, a.xmid, *next, s, Tr);
         PT_TRY(blin(m, a.ffa, d.ffn, bw->f2, w.f2b, xout, D, NL, EPI_BIAS_RESID, false, a.xmid, nullptr, s, Tr));
         return PTCG_OK;
     }
@@ -824,23 +844,21 @@ extern "C" int ptcg_model_forward(PtcgModel* m, const float* obs, const int32_t*
     const bool tr = m->train;
     const bool b16 = m->prec == 1;
     if (b16) PT_TRY(bf16_refresh(m, s));
-    // fp32: each block's FFN2 residual product also runs the LayerNorm that
-    // reads its output (the next block's LayerNorm 1, or the final one)
+    // each block's FFN2 residual product also runs the LayerNorm that reads
+    // its output: the next block's LayerNorm 1 (bf16 output in the
+    // mixed-precision blocks) or the final one (fp32)
     for (int i = 0; i < d.layers; ++i) {
-        LnOut nx{m->lnf_w, m->lnf_b, m->h, m->lnf_mu, m->lnf_rs};
+        LnOut nx{m->lnf_w, m->lnf_b, m->h, m->lnf_mu, m->lnf_rs, 0};
         if (i + 1 < d.layers) {
             const BlockP& wn = m->blk[i + 1];
             const BlockA& an = m->ba[tr ? i + 1 : 0];
-            nx = LnOut{wn.ln1w, wn.ln1b, an.ln1, an.mu1, an.rs1};
+            nx = LnOut{wn.ln1w, wn.ln1b, an.ln1, an.mu1, an.rs1, b16 ? 1 : 0};
         }
         PT_TRY(block_fwd(m, m->blk[i], m->ba[tr ? i : 0], x.l_seq, m->keep, m->x[tr ? i : i % 2],
-                         m->x[tr ? i + 1 : (i + 1) % 2], s, m->rows, Td, coff, b16 ? &m->bw[i] : nullptr,
-                         !b16 && i > 0, b16 ? nullptr : &nx));
+                         m->x[tr ? i + 1 : (i + 1) % 2], s, m->rows, Td, coff, b16 ? &m->bw[i] : nullptr, i > 0,
+                         &nx));
     }
     const int NL = N * x.l_seq;
-    if (b16)
-        PT_TRY(pt_ln_fwd(m->x[tr ? d.layers : d.layers % 2], D, m->lnf_w, m->lnf_b, m->h, D, m->lnf_mu, m->lnf_rs,
-                         m->rows, D, s, Td));
 
     // option scorer over the option rows (all N * n_opt, or the legal ones)
     const int NJ = m->orows;

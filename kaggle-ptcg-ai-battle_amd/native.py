@@ -195,7 +195,8 @@ _SIGS = {
     "ptcg_kernel_attention_path": (ctypes.c_int, [ctypes.c_int, ctypes.c_int]),
     "ptcg_kernel_colsum": (ctypes.c_int, [c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_int,
                                           c_void_p, c_void_p, ctypes.c_int64, c_void_p]),
-    "ptcg_kernel_gemm_resid_ln": (ctypes.c_int, [ctypes.c_int, ctypes.c_int] + [c_void_p] * 12),
+    "ptcg_kernel_gemm_resid_ln": (ctypes.c_int, [ctypes.c_int, ctypes.c_int] + [c_void_p] * 10 + [ctypes.c_int]
+                                  + [c_void_p] * 2),
     "ptcg_kernel_layernorm_fwd": (ctypes.c_int, [c_void_p, c_void_p, c_void_p, c_void_p,
                                                  c_void_p, c_void_p, ctypes.c_int, ctypes.c_int,
                                                  c_void_p]),

@@ -147,17 +147,24 @@ def test_colsum(cuda):
     assert rel_l2(out.cpu(), X.double().sum(0)) < 1e-6
 
 
-# rows: one row, a partial 64-row tile, whole tiles, the trunk's 37.4k rows
-@pytest.mark.parametrize("rows,K", [(1, 256), (63, 256), (200, 1024), (1024, 256), (37417, 256), (3001, 1024)])
-def test_gemm_resid_ln(rows, K, cuda):
+# rows: one row, a partial 64-row tile, whole tiles, the trunk's 37.4k rows;
+# bf16: bf16 operands and LayerNorm output (the mixed-precision blocks)
+@pytest.mark.parametrize("rows,K,bf16", [(1, 256, 0), (63, 256, 0), (200, 1024, 0), (1024, 256, 0),
+                                         (37417, 256, 0), (3001, 1024, 0), (1, 256, 1), (200, 1024, 1),
+                                         (37417, 256, 1), (3001, 1024, 1)])
+def test_gemm_resid_ln(rows, K, bf16, cuda):
     """The residual product fused with the LayerNorm that reads it: C, y,
     mean and rstd against float64 (C = A W^T + bias + R; y = LN(C) w + b),
     bit-equal to the unfused pair (the plain product, no split, then the
-    LayerNorm kernel), and a device row count leaves the later rows alone."""
+    LayerNorm kernel; bf16: the bf16-operand product, and y rounded to bf16
+    by round to nearest even), and a device row count leaves the later rows
+    alone."""
     N = 256
-    g = torch.Generator().manual_seed(rows + K)
+    g = torch.Generator().manual_seed(rows + K + bf16)
     A = torch.randn(rows, K, generator=g) / math.sqrt(K)
     W = torch.randn(N, K, generator=g)
+    if bf16:   # the products see bf16-rounded operands
+        A, W = A.bfloat16().float(), W.bfloat16().float()
     bias = torch.randn(N, generator=g) * 0.1
     R = torch.randn(rows, N, generator=g) * 2 + 0.5
     lw = torch.randn(N, generator=g)
@@ -167,30 +174,40 @@ def test_gemm_resid_ln(rows, K, cuda):
     mu64 = C64.mean(1)
     rs64 = 1.0 / torch.sqrt(C64.var(1, unbiased=False) + 1e-5)
     L = native.lib()
-    dA, dW, db, dR, dlw, dlb = dev(A), dev(W), dev(bias), dev(R), dev(lw), dev(lb)
-    C, y, mu, rs = empty(rows, N), empty(rows, N), empty(rows), empty(rows)
+    ot = torch.bfloat16 if bf16 else torch.float32
+    dA, dW = dev(A, ot), dev(W, ot)
+    db, dR, dlw, dlb = dev(bias), dev(R), dev(lw), dev(lb)
+    C, mu, rs = empty(rows, N), empty(rows), empty(rows)
+    y = torch.zeros(rows, N, dtype=ot, device="cuda")
     native.check(L.ptcg_kernel_gemm_resid_ln(rows, K, P(dA), P(dW), P(db), P(dR), P(C), P(dlw), P(dlb), P(y),
-                                             P(mu), P(rs), None, None))
+                                             P(mu), P(rs), bf16, None, None))
     # the unfused pair: EPI_BIAS_RESID (3) without a workspace (no split-K, no tail), then LayerNorm
     C2, y2, mu2, rs2 = empty(rows, N), empty(rows, N), empty(rows), empty(rows)
-    native.check(L.ptcg_kernel_gemm(rows, N, K, P(dA), K, 0, P(dW), K, 0, P(C2), N, 3, P(db), P(dR), N,
-                                    None, 0, None, 0, None))
+    if bf16:
+        native.check(L.ptcg_kernel_gemm_bs(rows, N, K, P(dA), K, P(dW), K, P(C2), N, 3, 0, P(db), P(dR), N,
+                                           None, 0, None))
+    else:
+        native.check(L.ptcg_kernel_gemm(rows, N, K, P(dA), K, 0, P(dW), K, 0, P(C2), N, 3, P(db), P(dR), N,
+                                        None, 0, None, 0, None))
     native.check(L.ptcg_kernel_layernorm_fwd(P(C2), P(dlw), P(dlb), P(y2), P(mu2), P(rs2), rows, N, None))
     torch.cuda.synchronize()
     assert rel_l2(C.cpu(), C64) < 1e-6 and max_rel(C.cpu(), C64) < 1e-5
-    assert rel_l2(y.cpu(), y64) < 1e-5 and max_rel(y.cpu(), y64) < 1e-4
+    if bf16:   # y rounded to bf16: half an ulp of 2^-8 relative
+        assert rel_l2(y.float().cpu(), y64) < 4e-3
+    else:
+        assert rel_l2(y.cpu(), y64) < 1e-5 and max_rel(y.cpu(), y64) < 1e-4
     assert rel_l2(mu.cpu(), mu64) < 1e-5 and rel_l2(rs.cpu(), rs64) < 1e-5
-    for a, b in ((C, C2), (y, y2), (mu, mu2), (rs, rs2)):
+    for a, b in ((C, C2), (y, y2.to(ot)), (mu, mu2), (rs, rs2)):
         assert torch.equal(a, b)
     if rows > 64:
         # device row count: rows past it keep their contents
         cut = rows // 2 + 5
         nd = torch.tensor([cut], dtype=torch.int32, device="cuda")
         C3 = torch.full((rows, N), 7.0, device="cuda")
-        y3 = torch.full((rows, N), 7.0, device="cuda")
+        y3 = torch.full((rows, N), 7.0, dtype=ot, device="cuda")
         mu3, rs3 = torch.full((rows,), 7.0, device="cuda"), torch.full((rows,), 7.0, device="cuda")
         native.check(L.ptcg_kernel_gemm_resid_ln(rows, K, P(dA), P(dW), P(db), P(dR), P(C3), P(dlw), P(dlb),
-                                                 P(y3), P(mu3), P(rs3), P(nd), None))
+                                                 P(y3), P(mu3), P(rs3), bf16, P(nd), None))
         torch.cuda.synchronize()
         assert torch.equal(C3[:cut], C[:cut]) and torch.equal(y3[:cut], y[:cut])
         assert torch.equal(mu3[:cut], mu[:cut]) and torch.equal(rs3[:cut], rs[:cut])
@@ -204,7 +221,7 @@ def test_gemm_resid_ln_rejects_other_shapes(cuda):
     out = [empty(8, 256), empty(256), empty(256), empty(8, 256), empty(8), empty(8)]
     with pytest.raises(RuntimeError, match="gemm \\+ layernorm"):
         native.check(L.ptcg_kernel_gemm_resid_ln(8, 100, P(a), P(w), P(b), P(r), P(out[0]), P(out[1]), P(out[2]),
-                                                 P(out[3]), P(out[4]), P(out[5]), None, None))
+                                                 P(out[3]), P(out[4]), P(out[5]), 0, None, None))
 
 
 # (20001, 256): several row pairs per wave in the backward and an odd tail;

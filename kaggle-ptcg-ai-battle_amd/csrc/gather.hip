@@ -244,9 +244,13 @@ __global__ void dec_in_bwd_kernel(GatherCtx c, const float* __restrict__ d_in, D
 }
 
 // x0[n,0] = readout; x0[n,l] = tokp[n,l-1] + bc[n]; keep[n,l] = l==0 || zone_float > 0
+// lny (nullable, d = 256): also the first block's LayerNorm 1 of the row, in
+// ln_fwd_kernel's arithmetic (a wave holds one row, one float4 per lane), into
+// lny (bf16 when lnybf) with its mean / rstd
 __global__ void x0_fwd_kernel(GatherCtx c, const float* __restrict__ tokp,
         const float* __restrict__ bc, const float* __restrict__ readout, float* __restrict__ x0,
-        float* __restrict__ keep) {
+        float* __restrict__ keep, const float* __restrict__ lnw, const float* __restrict__ lnb,
+        float* __restrict__ lny, float* __restrict__ lnmu, float* __restrict__ lnrs, int lnybf) {
     const int Ls = c.dx.l_seq, D = c.dm.d, ch4 = D / 4;
     const long i = (long)blockIdx.x * TB + threadIdx.x;
     const long nrows = c.rowmap ? (long)*c.rows : (long)c.N * Ls;
@@ -265,6 +269,30 @@ __global__ void x0_fwd_kernel(GatherCtx c, const float* __restrict__ tokp,
         v = make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
     }
     *reinterpret_cast<float4*>(x0 + nl * D + col) = v;
+    if (lny) {
+        const float mu = wave_sum((v.x + v.y) + (v.z + v.w)) / (float)D;
+        const float a = v.x - mu, b = v.y - mu, cc = v.z - mu, dd = v.w - mu;
+        const float var = wave_sum((a * a + b * b) + (cc * cc + dd * dd)) / (float)D;
+        const float rs = 1.0f / sqrtf(var + 1e-5f);
+        if (col == 0) {
+            lnmu[nl] = mu;
+            lnrs[nl] = rs;
+        }
+        const float4 ww = *reinterpret_cast<const float4*>(lnw + col);
+        const float4 wb = *reinterpret_cast<const float4*>(lnb + col);
+        float4 o;
+        o.x = (v.x - mu) * rs * ww.x + wb.x;
+        o.y = (v.y - mu) * rs * ww.y + wb.y;
+        o.z = (v.z - mu) * rs * ww.z + wb.z;
+        o.w = (v.w - mu) * rs * ww.w + wb.w;
+        if (lnybf) {
+            typedef __bf16 x0bf16x4 __attribute__((ext_vector_type(4)));
+            *reinterpret_cast<x0bf16x4*>(reinterpret_cast<__bf16*>(lny) + nl * D + col) =
+                x0bf16x4{(__bf16)o.x, (__bf16)o.y, (__bf16)o.z, (__bf16)o.w};
+        } else {
+            *reinterpret_cast<float4*>(lny + nl * D + col) = o;
+        }
+    }
     if (col == 0) {
         float kp = 1.f;
         if (l > 0) {
@@ -668,8 +696,12 @@ int pt_dec_in_bwd(const GatherCtx& c, const float* d_in, const DetSink& d_card, 
     return PTCG_OK;
 }
 int pt_x0_fwd(const GatherCtx& c, const float* tokp, const float* bc, const float* readout, float* x0,
-              float* keep, hipStream_t s) {
-    hipLaunchKernelGGL(x0_fwd_kernel, PT_GRID((long)c.N * c.dx.l_seq * (c.dm.d / 4)), c, tokp, bc, readout, x0, keep);
+              float* keep, hipStream_t s, const float* lnw, const float* lnb, float* lny, float* lnmu, float* lnrs,
+              int lnybf) {
+    // one row per wave when the LayerNorm rides along (64 float4s per row, TB a multiple of 64)
+    PT_REQUIRE(!lny || (c.dm.d == 256 && lnw && lnb && lnmu && lnrs), "x0 + layernorm: needs d = 256 and all buffers");
+    hipLaunchKernelGGL(x0_fwd_kernel, PT_GRID((long)c.N * c.dx.l_seq * (c.dm.d / 4)), c, tokp, bc, readout, x0, keep,
+                       lnw, lnb, lny, lnmu, lnrs, lnybf);
     PT_LAUNCH_CHECK();
     return PTCG_OK;
 }

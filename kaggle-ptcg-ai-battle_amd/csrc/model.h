@@ -171,8 +171,11 @@ int pt_dec_in_fwd(const GatherCtx& c, const float* card, const float* att, const
                   const float* cemb, float* dec_in, hipStream_t s);
 int pt_dec_in_bwd(const GatherCtx& c, const float* d_in, const DetSink& d_card, const DetSink& d_att,
                   const DetSink& d_semb, const DetSink& d_cemb, hipStream_t s);
+// lny (nullable, d = 256): the first block's LayerNorm 1 of x0 in the same
+// launch (lnybf: bf16 output), with its mean / rstd
 int pt_x0_fwd(const GatherCtx& c, const float* tokp, const float* bc, const float* readout,
-              float* x0, float* keep, hipStream_t s);
+              float* x0, float* keep, hipStream_t s, const float* lnw = nullptr, const float* lnb = nullptr,
+              float* lny = nullptr, float* lnmu = nullptr, float* lnrs = nullptr, int lnybf = 0);
 int pt_x0_bwd(const GatherCtx& c, const float* d_x0, float* d_tokp, float* d_bc, hipStream_t s);
 int pt_opt_gather_fwd(const GatherCtx& c, const float* card, const float* att, float* ocard,
                       float* oatt, hipStream_t s);

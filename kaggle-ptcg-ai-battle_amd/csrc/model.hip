@@ -840,9 +840,16 @@ extern "C" int ptcg_model_forward(PtcgModel* m, const float* obs, const int32_t*
     PT_TRY(lin(m, m->d1a, PT_DEC_H, m->d2_w, m->d2_b, m->gd + G, x.bcast_in, N, PT_DEC_H, PT_DEC_H, EPI_BIAS,
                nullptr, 0, nullptr, 0, s));
     PT_TRY(lin(m, m->gd, x.bcast_in, m->bc_w, m->bc_b, m->bc, D, N, x.bcast_in, D, EPI_BIAS, nullptr, 0, nullptr, 0, s));
-    PT_TRY(pt_x0_fwd(c, m->tokp, m->bc, m->readout, m->x[0], m->keep, s));
     const bool tr = m->train;
     const bool b16 = m->prec == 1;
+    // at d = 256 the first block's LayerNorm 1 runs inside the trunk-input assembly
+    const bool ln0 = D == 256;
+    const BlockA& a0 = m->ba[0];
+    if (ln0)
+        PT_TRY(pt_x0_fwd(c, m->tokp, m->bc, m->readout, m->x[0], m->keep, s, m->blk[0].ln1w, m->blk[0].ln1b,
+                         a0.ln1, a0.mu1, a0.rs1, b16 ? 1 : 0));
+    else
+        PT_TRY(pt_x0_fwd(c, m->tokp, m->bc, m->readout, m->x[0], m->keep, s));
     if (b16) PT_TRY(bf16_refresh(m, s));
     // each block's FFN2 residual product also runs the LayerNorm that reads
     // its output: the next block's LayerNorm 1 (bf16 output in the
@@ -855,8 +862,8 @@ extern "C" int ptcg_model_forward(PtcgModel* m, const float* obs, const int32_t*
             nx = LnOut{wn.ln1w, wn.ln1b, an.ln1, an.mu1, an.rs1, b16 ? 1 : 0};
         }
         PT_TRY(block_fwd(m, m->blk[i], m->ba[tr ? i : 0], x.l_seq, m->keep, m->x[tr ? i : i % 2],
-                         m->x[tr ? i + 1 : (i + 1) % 2], s, m->rows, Td, coff, b16 ? &m->bw[i] : nullptr, i > 0,
-                         &nx));
+                         m->x[tr ? i + 1 : (i + 1) % 2], s, m->rows, Td, coff, b16 ? &m->bw[i] : nullptr,
+                         i > 0 || ln0, &nx));
     }
     const int NL = N * x.l_seq;
 

@@ -903,12 +903,12 @@ __global__ __launch_bounds__(NT) void gemm_f32_dma_kernel(const GemmArgs g0, int
 // N = 256, followed in the same launch by the LayerNorm of C's rows that the
 // next stage reads: Y = LN(C) lnw + lnb with its mean and rstd.  The unfused
 // pair is the DMA kernel's EPI_BIAS_RESID then ln_fwd_kernel, which reads C
-// back from HBM.  A workgroup owns 64 full rows: a 64 x 256 tile, the four
-// waves side by side, each a 64 x 64 sub-tile of 2 x 2
-// v_mfma_f32_32x32x2_f32 tiles with the DMA kernel's operand order, so every
-// output accumulates the same products in the same order.  Per 16-k stage
+// back from HBM.  A workgroup owns BMR (64 or 32) full rows: a BMR x 256
+// tile, the four waves side by side, each a BMR x 64 sub-tile of
+// v_mfma_f32_32x32x2_f32 tiles (2 x 2 or 1 x 2) with the DMA kernel's operand
+// order, so every output accumulates the same products in the same order.  Per 16-k stage
 // the A rows (one 16-row chunk) and W rows (four chunks) go global -> LDS by
-// DMA, two stages deep.  The tile leaves through LDS in two 32-row halves; a
+// DMA, two stages deep.  The tile leaves through LDS in 32-row halves; a
 // wave then takes eight rows, one float4 per lane, adds bias and residual in
 // epi_store4_r's order and normalises in ln_fwd_kernel's order (two-pass
 // mean / variance by wave sums, eps 1e-5), so C, Y, mean and rstd equal the
@@ -918,22 +918,24 @@ __global__ __launch_bounds__(NT) void gemm_f32_dma_kernel(const GemmArgs g0, int
 // on v_mfma_f32_32x32x16_bf16 in gemm_bs32_kernel's fragment order; YB: Y is
 // stored in bf16 (round to nearest even), ldy in bf16 elements.
 constexpr int RL_BM = 64, RL_N = 256, RL_SST = RL_N + 4;
-template <bool BF, bool YB>
+template <bool BF, bool YB, int BMR = RL_BM>
 __global__ __launch_bounds__(NT) void gemm_resid_ln_kernel(const GemmArgs g0, const float* __restrict__ lnw,
         const float* __restrict__ lnb, float* __restrict__ Y, long ldy, float* __restrict__ mean,
         float* __restrict__ rstd) {
     const GemmArgs g = gemm_shape(g0);
-    const int m0 = blockIdx.x * RL_BM;
+    static_assert(BMR == 64 || BMR == 32, "64- or 32-row tiles");
+    constexpr int TM = BMR / 32;   // 32-row MFMA tiles per wave
+    const int m0 = blockIdx.x * BMR;
     if (m0 >= g.M) return;   // beyond the (device) row count
-    constexpr int TA = RL_BM * BK, TB = RL_N * BK, STAGE = TA + TB;
+    constexpr int TA = BMR * BK, TB = RL_N * BK, STAGE = TA + TB;
     constexpr int SMEM = 2 * STAGE > 32 * RL_SST ? 2 * STAGE : 32 * RL_SST;
     __shared__ __align__(16) float smem[SMEM];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int l32 = lane & 31, lh = lane >> 5;
     const int wn = 64 * wave;
-    floatx16 acc[2][2];
+    floatx16 acc[TM][2];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int j = 0; j < 2; ++j)
 #pragma unroll
@@ -949,7 +951,7 @@ __global__ __launch_bounds__(NT) void gemm_resid_ln_kernel(const GemmArgs g0, co
     auto issue = [&](int tile) {
         const int k0 = tile * BK;
         const float* st = smem + (tile & 1) * STAGE;
-        dma16(ra, st + wave * 256, (sa + k0) * 4);
+        if (wave < BMR / 16) dma16(ra, st + wave * 256, (sa + k0) * 4);
 #pragma unroll
         for (int j = 0; j < 4; ++j) dma16(rb, st + TA + (4 * wave + j) * 256, (sb[j] + k0) * 4);
     };
@@ -964,35 +966,38 @@ __global__ __launch_bounds__(NT) void gemm_resid_ln_kernel(const GemmArgs g0, co
         if constexpr (BF) {
 #pragma unroll
             for (int st = 0; st < 2; ++st) {
-                bf16x8 ah[2], bh[2];
+                bf16x8 ah[TM], bh[2];
 #pragma unroll
-                for (int t = 0; t < 2; ++t) {
+                for (int t = 0; t < TM; ++t)
                     ah[t] = *reinterpret_cast<const bf16x8*>(Ab + dma_at<false>(32 * t + l32, 4 * (2 * st + lh)));
-                    bh[t] = *reinterpret_cast<const bf16x8*>(Bb + dma_at<false>(wn + 32 * t + l32, 4 * (2 * st + lh)));
-                }
 #pragma unroll
-                for (int ti = 0; ti < 2; ++ti)
+                for (int t = 0; t < 2; ++t)
+                    bh[t] = *reinterpret_cast<const bf16x8*>(Bb + dma_at<false>(wn + 32 * t + l32, 4 * (2 * st + lh)));
+#pragma unroll
+                for (int ti = 0; ti < TM; ++ti)
 #pragma unroll
                     for (int tj = 0; tj < 2; ++tj)
                         acc[ti][tj] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bh[tj], ah[ti], acc[ti][tj], 0, 0, 0);
             }
             continue;
         }
-        float a8[2][8], b8[2][8];
+        float a8[TM][8], b8[2][8];
 #pragma unroll
         for (int t = 0; t < 2; ++t)
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
                 const int k0 = 8 * lh + 4 * h;
-                const float4 va = *reinterpret_cast<const float4*>(Ab + dma_at<false>(32 * t + l32, k0));
+                if (t < TM) {
+                    const float4 va = *reinterpret_cast<const float4*>(Ab + dma_at<false>(32 * t + l32, k0));
+                    a8[t][4 * h] = va.x; a8[t][4 * h + 1] = va.y; a8[t][4 * h + 2] = va.z; a8[t][4 * h + 3] = va.w;
+                }
                 const float4 vb = *reinterpret_cast<const float4*>(Bb + dma_at<false>(wn + 32 * t + l32, k0));
-                a8[t][4 * h] = va.x; a8[t][4 * h + 1] = va.y; a8[t][4 * h + 2] = va.z; a8[t][4 * h + 3] = va.w;
                 b8[t][4 * h] = vb.x; b8[t][4 * h + 1] = vb.y; b8[t][4 * h + 2] = vb.z; b8[t][4 * h + 3] = vb.w;
             }
 #pragma unroll
         for (int st = 0; st < 8; ++st)
 #pragma unroll
-            for (int ti = 0; ti < 2; ++ti)
+            for (int ti = 0; ti < TM; ++ti)
 #pragma unroll
                 for (int tj = 0; tj < 2; ++tj)
                     acc[ti][tj] = __builtin_amdgcn_mfma_f32_32x32x2f32(b8[tj][st], a8[ti][st], acc[ti][tj], 0, 0, 0);
@@ -1003,7 +1008,7 @@ __global__ __launch_bounds__(NT) void gemm_resid_ln_kernel(const GemmArgs g0, co
     const float4 ww = *reinterpret_cast<const float4*>(lnw + 4 * lane);
     const float4 wb = *reinterpret_cast<const float4*>(lnb + 4 * lane);
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
+    for (int h = 0; h < TM; ++h) {
         // this wave's eight rows of the half: residual segments loaded
         // before the staging barriers (rows past M read R's first row)
         floatx4 rv[8];
@@ -2046,12 +2051,21 @@ int pt_gemm_resid_ln(const GemmArgs& g, const float* lnw, const float* lnb, floa
     PT_REQUIRE((((uintptr_t)lnw | (uintptr_t)lnb | (uintptr_t)y | (uintptr_t)(ldy * (ybf ? 2 : 4))) & 15) == 0,
                "gemm + layernorm: LayerNorm parameters and output need 16 B alignment");
     const GemmArgs f = resid_ln_float_units(g);
-    const dim3 grid(pt_cdiv(g.M, RL_BM)), blk(NT);
+    // row tiles: 32 for fp32 operands (about 4.6 tiles per CU at 37.4k rows
+    // instead of 2.3, so the last partial wave costs less: headline +0.4% on
+    // one box), 64 for bf16 ones (32-row tiles were 2.8% slower on the bf16
+    // step at B = 2048, whose 149.5k rows fill the chip anyway)
+    const dim3 blk(NT);
     const int slot = pt_prof_open(s);
-    if (g.bs && ybf) hipLaunchKernelGGL((gemm_resid_ln_kernel<true, true>), grid, blk, 0, s, f, lnw, lnb, y, ldy, mean, rstd);
-    else if (g.bs) hipLaunchKernelGGL((gemm_resid_ln_kernel<true, false>), grid, blk, 0, s, f, lnw, lnb, y, ldy, mean, rstd);
-    else if (ybf) hipLaunchKernelGGL((gemm_resid_ln_kernel<false, true>), grid, blk, 0, s, f, lnw, lnb, y, ldy, mean, rstd);
-    else hipLaunchKernelGGL((gemm_resid_ln_kernel<false, false>), grid, blk, 0, s, f, lnw, lnb, y, ldy, mean, rstd);
+    if (g.bs) {
+        const dim3 grid(pt_cdiv(g.M, 64));
+        if (ybf) hipLaunchKernelGGL((gemm_resid_ln_kernel<true, true, 64>), grid, blk, 0, s, f, lnw, lnb, y, ldy, mean, rstd);
+        else hipLaunchKernelGGL((gemm_resid_ln_kernel<true, false, 64>), grid, blk, 0, s, f, lnw, lnb, y, ldy, mean, rstd);
+    } else {
+        const dim3 grid(pt_cdiv(g.M, 32));
+        if (ybf) hipLaunchKernelGGL((gemm_resid_ln_kernel<false, true, 32>), grid, blk, 0, s, f, lnw, lnb, y, ldy, mean, rstd);
+        else hipLaunchKernelGGL((gemm_resid_ln_kernel<false, false, 32>), grid, blk, 0, s, f, lnw, lnb, y, ldy, mean, rstd);
+    }
     PT_LAUNCH_CHECK();
     pt_prof_close(slot, g_gemm_class, 2.0 * g.M * (double)g.N * g.K, s);
     return PTCG_OK;

@@ -107,6 +107,20 @@ int ptcg_kernel_layernorm_bwd(const float* dy, const float* x, const float* w,
                               const float* mean, const float* rstd, const float* dres,
                               float* dx, float* dw, float* db, int rows, int D,
                               float* workspace, int64_t workspace_floats, void* stream);
+/* A bf16 block's dX product fused with the LayerNorm backward that reads
+ * it: dy (rows, 256) = dY (rows, K) WT^T with dY and the weight copy WT
+ * (256, K) bf16 at row stride K (K a multiple of 32, 16 B aligned), then
+ * dx = LN'(dy) [+ dres] at row stride 256, its bf16 copy dxh (nullable),
+ * dw / db overwritten; workspace >= 2048*ceil(rows/64) floats.  rows_dev
+ * (nullable): a device row count, rows < it are processed (dw / db over
+ * those rows only).  Replaces the QKV / FFN1 dX product and the LayerNorm
+ * backward after it (ptcg_model.cu's dX pt_linear then pt_ln_bwd,
+ * ptcg_kernels.cuh:176-218).                                              */
+int ptcg_kernel_gemm_dx_layernorm_bwd(int rows, int K, const void* dY, const void* WT, const float* x,
+                                      const float* w, const float* mean, const float* rstd,
+                                      const float* dres, float* dx, void* dxh, float* dw, float* db,
+                                      float* workspace, int64_t workspace_floats, const int* rows_dev,
+                                      void* stream);
 
 /* Masked MHSA over (N, L, 3D) qkv rows, keep (N, L) key mask (1 keep / 0
  * masked), fused per (sample, head) (ptcg_model3.cu:18-30, 63-91).

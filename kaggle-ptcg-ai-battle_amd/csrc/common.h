@@ -216,6 +216,14 @@ int pt_gemm(const GemmArgs& g, float* splitk_ws, long splitk_ws_floats, hipStrea
 bool pt_gemm_resid_ln_fits(const GemmArgs& g);
 int pt_gemm_resid_ln(const GemmArgs& g, const float* lnw, const float* lnb, float* y, long ldy, float* mean,
                      float* rstd, hipStream_t s, int ybf = 0);
+// the bf16 dX product dy = dY W (N = 256, W^T copy k-contiguous) with the
+// LayerNorm backward of dy in the same launch: dx = LN'(dy) (+ dres), its
+// bf16 copy dxh (nullable), dw / db overwritten; pt_dx_lnbwd_fits says
+// whether g fits
+bool pt_dx_lnbwd_fits(const GemmArgs& g);
+int pt_dx_lnbwd(const GemmArgs& g, const float* x, const float* w, const float* mean, const float* rstd,
+                const float* dres, float* dx, float* dxh, float* dw, float* db, float* ws, long ws_floats,
+                hipStream_t s);
 
 // One product of a grouped launch (pt_gemm_grouped): all products of a
 // launch share the operand layout (a_t, b_t) and epilogue, and must meet the

@@ -1054,6 +1054,134 @@ __global__ __launch_bounds__(NT) void gemm_resid_ln_kernel(const GemmArgs g0, co
     }
 }
 
+// The LayerNorm backward fused into the bf16 dX product that feeds it (the
+// bf16 blocks' QKV and FFN1 dX): dy = dY W (dY rows x K bf16, W^T copy 256 x
+// K bf16, k-contiguous both) never leaves the chip.  The main loop is
+// gemm_resid_ln_kernel's bf16 one on 64 x 256 tiles; the epilogue stages dy
+// in 32-row halves and a wave takes eight rows, one float4 per lane, in
+// ln_bwd_kernel's arithmetic: dx = rs (g - mean(g) - xh mean(g xh)) + dres
+// with g = dy w, xh = (x - mu) rs, written fp32 and as a bf16 copy.  The
+// LayerNorm parameter gradients' per-row terms dy xh and dy are summed per
+// lane over the wave's rows, then over the four waves in order, into one
+// partial row of 512 floats per workgroup (part); workgroups past the device
+// row count write zeros there, so the column sum over every workgroup's row
+// is complete.
+struct LnBwdArgs {
+    const float* x; const float* mean; const float* rstd; const float* w; const float* dres;
+    float* dx; __bf16* dxh; float* part;
+};
+__global__ __launch_bounds__(NT) void gemm_dx_lnbwd_kernel(const GemmArgs g0, const LnBwdArgs a) {
+    const GemmArgs g = gemm_shape(g0);
+    constexpr int BMR = 64, TM = 2;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int m0 = blockIdx.x * BMR;
+    if (m0 >= g.M) {   // beyond the (device) row count: a zero partial row
+        for (int c = tid; c < 2 * RL_N; c += NT) a.part[(long)blockIdx.x * 2 * RL_N + c] = 0.f;
+        return;
+    }
+    constexpr int TA = BMR * BK, TB = RL_N * BK, STAGE = TA + TB;
+    constexpr int SMEM = 2 * STAGE > 32 * RL_SST ? 2 * STAGE : 32 * RL_SST;
+    __shared__ __align__(16) float smem[SMEM];
+    const int l32 = lane & 31, lh = lane >> 5;
+    const int wn = 64 * wave;
+    floatx16 acc[TM][2];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+    const unsigned ea = (unsigned)(((long)(g.M - 1) * g.lda + g.K) * 4);
+    const unsigned eb = (unsigned)(((long)(RL_N - 1) * g.ldb + g.K) * 4);
+    const int32x4_t ra = buffer_rsrc(g.A, ea), rb = buffer_rsrc(g.B, eb);
+    const int sa = dma_src<false>(wave, lane, m0, g.lda);
+    int sb[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) sb[j] = dma_src<false>(4 * wave + j, lane, 0, g.ldb);
+    auto issue = [&](int tile) {
+        const int k0 = tile * BK;
+        const float* st = smem + (tile & 1) * STAGE;
+        dma16(ra, st + wave * 256, (sa + k0) * 4);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) dma16(rb, st + TA + (4 * wave + j) * 256, (sb[j] + k0) * 4);
+    };
+    const int nk = g.K / BK;
+    issue(0);
+    for (int it = 0; it < nk; ++it) {
+        wait_vm<0>();
+        __syncthreads();
+        if (it + 1 < nk) issue(it + 1);
+        const float* Ab = smem + (it & 1) * STAGE;
+        const float* Bb = Ab + TA;
+#pragma unroll
+        for (int st = 0; st < 2; ++st) {
+            bf16x8 ah[TM], bh[2];
+#pragma unroll
+            for (int t = 0; t < TM; ++t)
+                ah[t] = *reinterpret_cast<const bf16x8*>(Ab + dma_at<false>(32 * t + l32, 4 * (2 * st + lh)));
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+                bh[t] = *reinterpret_cast<const bf16x8*>(Bb + dma_at<false>(wn + 32 * t + l32, 4 * (2 * st + lh)));
+#pragma unroll
+            for (int ti = 0; ti < TM; ++ti)
+#pragma unroll
+                for (int tj = 0; tj < 2; ++tj)
+                    acc[ti][tj] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bh[tj], ah[ti], acc[ti][tj], 0, 0, 0);
+        }
+    }
+    const float4 wv = *reinterpret_cast<const float4*>(a.w + 4 * lane);
+    float4 aw = make_float4(0.f, 0.f, 0.f, 0.f), ab = aw;
+#pragma unroll
+    for (int h = 0; h < TM; ++h) {
+        __syncthreads();   // the stages are free (main loop done / previous half consumed)
+#pragma unroll
+        for (int tj = 0; tj < 2; ++tj)
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                *reinterpret_cast<floatx4*>(smem + l32 * RL_SST + wn + 32 * tj + 8 * q + 4 * lh) =
+                    floatx4{acc[h][tj][4 * q], acc[h][tj][4 * q + 1], acc[h][tj][4 * q + 2], acc[h][tj][4 * q + 3]};
+        __syncthreads();
+#pragma unroll 2
+        for (int r = 0; r < 8; ++r) {
+            const int lr = 8 * wave + r, m = m0 + 32 * h + lr;
+            if (m >= g.M) break;   // uniform over the wave; later rows are past M too
+            const float4 dd = *reinterpret_cast<const float4*>(smem + lr * RL_SST + 4 * lane);
+            const float4 xv = *reinterpret_cast<const float4*>(a.x + (long)m * RL_N + 4 * lane);
+            const float mu = a.mean[m], rs = a.rstd[m];
+            const float4 xh = make_float4((xv.x - mu) * rs, (xv.y - mu) * rs, (xv.z - mu) * rs, (xv.w - mu) * rs);
+            const float4 gv = make_float4(dd.x * wv.x, dd.y * wv.y, dd.z * wv.z, dd.w * wv.w);
+            const float s1 = (gv.x + gv.y) + (gv.z + gv.w);
+            const float s2 = (gv.x * xh.x + gv.y * xh.y) + (gv.z * xh.z + gv.w * xh.w);
+            aw.x += dd.x * xh.x; aw.y += dd.y * xh.y; aw.z += dd.z * xh.z; aw.w += dd.w * xh.w;
+            ab.x += dd.x; ab.y += dd.y; ab.z += dd.z; ab.w += dd.w;
+            const float m1 = wave_sum(s1) / (float)RL_N;
+            const float m2 = wave_sum(s2) / (float)RL_N;
+            float4 o;
+            o.x = (gv.x - m1 - xh.x * m2) * rs;
+            o.y = (gv.y - m1 - xh.y * m2) * rs;
+            o.z = (gv.z - m1 - xh.z * m2) * rs;
+            o.w = (gv.w - m1 - xh.w * m2) * rs;
+            if (a.dres) {
+                const float4 rv = *reinterpret_cast<const float4*>(a.dres + (long)m * RL_N + 4 * lane);
+                o.x += rv.x; o.y += rv.y; o.z += rv.z; o.w += rv.w;
+            }
+            *reinterpret_cast<float4*>(a.dx + (long)m * RL_N + 4 * lane) = o;
+            if (a.dxh)
+                *reinterpret_cast<bf16x4*>(a.dxh + (long)m * RL_N + 4 * lane) =
+                    bf16x4{(__bf16)o.x, (__bf16)o.y, (__bf16)o.z, (__bf16)o.w};
+        }
+    }
+    // the workgroup's partial row: [sum dy xh (256) | sum dy (256)], waves in order
+    __syncthreads();   // the stage is free
+    float* red = smem;   // [4 waves][512]
+    *reinterpret_cast<float4*>(red + wave * 2 * RL_N + 4 * lane) = aw;
+    *reinterpret_cast<float4*>(red + wave * 2 * RL_N + RL_N + 4 * lane) = ab;
+    __syncthreads();
+    for (int c = tid; c < 2 * RL_N; c += NT)
+        a.part[(long)blockIdx.x * 2 * RL_N + c] =
+            ((red[c] + red[2 * RL_N + c]) + red[4 * RL_N + c]) + red[6 * RL_N + c];
+}
+
 // Grouped launch: several independent products (different shapes and
 // operands, one layout and epilogue) in one grid.  Work item w belongs to
 // product item_group[w]; its logical tile and K split follow from the
@@ -2069,6 +2197,34 @@ int pt_gemm_resid_ln(const GemmArgs& g, const float* lnw, const float* lnb, floa
     PT_LAUNCH_CHECK();
     pt_prof_close(slot, g_gemm_class, 2.0 * g.M * (double)g.N * g.K, s);
     return PTCG_OK;
+}
+
+// The bf16 dX product dy = dY W (dY rows x K, W^T copy 256 x K, both bf16)
+// fused with the LayerNorm backward that reads dy (gemm_dx_lnbwd_kernel): dx
+// (+ dres) fp32 and its bf16 copy dxh, dw / db from the per-workgroup partial
+// rows by the fixed-order column sum.  x, dres, dx rows of 256 fp32.
+bool pt_dx_lnbwd_fits(const GemmArgs& g) {
+    return g.bs && g.N == RL_N && g.M > 0 && g.K % 32 == 0 && g.lda % 8 == 0 && g.ldb % 8 == 0 && !g.a_t &&
+           !g.b_t && (((uintptr_t)g.A | (uintptr_t)g.B) & 15) == 0 && !g.Kdev && dma_ok(resid_ln_float_units(g));
+}
+int pt_dx_lnbwd(const GemmArgs& g, const float* x, const float* w, const float* mean, const float* rstd,
+                const float* dres, float* dx, float* dxh, float* dw, float* db, float* ws, long ws_floats,
+                hipStream_t s) {
+    PT_REQUIRE(pt_dx_lnbwd_fits(g), "dX + layernorm bwd: needs bf16 operands, N = 256, K %% 32 == 0 (M=%d, K=%d)",
+               g.M, g.K);
+    PT_REQUIRE(x && w && mean && rstd && dx && dw && db && ws, "dX + layernorm bwd: null buffer");
+    PT_REQUIRE((((uintptr_t)x | (uintptr_t)w | (uintptr_t)dx | (uintptr_t)dres | (uintptr_t)dxh) & 15) == 0,
+               "dX + layernorm bwd: 16 B aligned rows needed");
+    const int blocks = pt_cdiv(g.M, 64);
+    PT_REQUIRE((long)blocks * 2 * RL_N * 2 <= ws_floats, "dX + layernorm bwd: workspace too small");
+    LnBwdArgs a{x, mean, rstd, w, dres, dx, reinterpret_cast<__bf16*>(dxh), ws};
+    const GemmArgs f = resid_ln_float_units(g);
+    const int slot = pt_prof_open(s);
+    hipLaunchKernelGGL(gemm_dx_lnbwd_kernel, dim3(blocks), dim3(NT), 0, s, f, a);
+    PT_LAUNCH_CHECK();
+    pt_prof_close(slot, g_gemm_class, 2.0 * g.M * (double)g.N * g.K, s);
+    return pt_colsum2(ws, 2 * RL_N, blocks, 2 * RL_N, RL_N, dw, db, ws + (long)blocks * 2 * RL_N,
+                      ws_floats - (long)blocks * 2 * RL_N, s);
 }
 
 int pt_gemm(const GemmArgs& g0, float* ws, long ws_floats, hipStream_t s) {

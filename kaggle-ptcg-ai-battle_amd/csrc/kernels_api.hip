@@ -141,6 +141,23 @@ extern "C" int ptcg_kernel_gemm_resid_ln(int rows, int K, const void* A, const v
     return pt_gemm_resid_ln(g, lnw, lnb, static_cast<float*>(y), 256, mean, rstd, (hipStream_t)stream, bf16);
 }
 
+extern "C" int ptcg_kernel_gemm_dx_layernorm_bwd(int rows, int K, const void* dY, const void* WT, const float* x,
+                                                const float* w, const float* mean, const float* rstd,
+                                                const float* dres, float* dx, void* dxh, float* dw, float* db,
+                                                float* workspace, int64_t workspace_floats, const int* rows_dev,
+                                                void* stream) {
+    PT_REQUIRE(rows > 0 && K > 0, "kernel_gemm_dx_layernorm_bwd: empty shape %d x %d", rows, K);
+    GemmArgs g{};
+    g.M = rows; g.N = 256; g.K = K;
+    g.prec = 1; g.bs = 1;
+    g.A = static_cast<const float*>(dY); g.lda = K;
+    g.B = static_cast<const float*>(WT); g.ldb = K;
+    g.epi = EPI_STORE;
+    g.Mdev = rows_dev;
+    return pt_dx_lnbwd(g, x, w, mean, rstd, dres, dx, static_cast<float*>(dxh), dw, db, workspace,
+                       workspace_floats, (hipStream_t)stream);
+}
+
 extern "C" int ptcg_kernel_layernorm_bwd(const float* dy, const float* x, const float* w,
                                          const float* mean, const float* rstd, const float* dres,
                                          float* dx, float* dw, float* db, int rows, int D,

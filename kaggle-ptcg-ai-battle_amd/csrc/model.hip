@@ -267,6 +267,25 @@ static int blin_resid_ln(const PtcgModel* m, const float* X, int in, const __bf1
     PT_TRY(pt_gemm(g, m->ws, m->ws_floats, s));
     return pt_ln_fwd(Y, out, ln.w, ln.b, ln.y, out, ln.mu, ln.rs, rows, out, s, Mdev, ln.ybf);
 }
+// blin's dX product dln = dY W (dY bf16 (rows, in), weight copy W^T (D, in))
+// followed by the LayerNorm backward of dln: one fused launch when the shape
+// fits it, else the product and pt_ln_bwd
+static int blin_dx_lnbwd(PtcgModel* m, const float* dY, int in, const __bf16* WT, int rows, const float* x,
+                         const float* lnw, const float* mu, const float* rs, const float* dres, float* dx,
+                         float* dw, float* db, float* dxh, hipStream_t s, const int* Mdev) {
+    const int D = m->dm.d;
+    GemmArgs g{};
+    g.prec = 1; g.bs = 1;
+    g.Mdev = Mdev;
+    g.M = rows; g.N = D; g.K = in;
+    g.A = dY; g.lda = in;
+    g.B = reinterpret_cast<const float*>(WT); g.ldb = in;
+    g.epi = EPI_STORE;
+    if (pt_dx_lnbwd_fits(g)) return pt_dx_lnbwd(g, x, lnw, mu, rs, dres, dx, dxh, dw, db, m->ws, m->ws_floats, s);
+    PT_TRY(blin(m, dY, in, WT, nullptr, m->dln, D, rows, EPI_STORE, false, nullptr, nullptr, s, Mdev));
+    return pt_ln_bwd(m->dln, D, x, D, lnw, mu, rs, dres, D, dx, D, dw, db, rows, D, m->ws, m->ws_floats, s, Mdev,
+                     dxh);
+}
 static int bldw(PtcgModel* m, const float* dY, int out, const float* X, int in, float* dW, float* db, int rows,
                 hipStream_t s, const int* Kdev) {
     GemmArgs g{};
@@ -936,10 +955,9 @@ static int block_bwd(PtcgModel* m, const BlockP& w, const BlockA& a, int L, cons
         PT_TRY(wg_fork(m, s));
         PT_TRY(bldw(m, m->dffn, d.ffn, a.ln2, D, m->G(w.f1w), m->G(w.f1b), NL, s2, Tr));
         PT_TRY(wg_done(m, 2));
-        PT_TRY(blin(m, m->dffn, d.ffn, bw->f1T, nullptr, m->dln, D, NL, EPI_STORE, false, nullptr, nullptr, s, Tr));
-        PT_TRY(wg_after(m, 3, s));
-        PT_TRY(pt_ln_bwd(m->dln, D, a.xmid, D, w.ln2w, a.mu2, a.rs2, dA, D, dC, D, m->G(w.ln2w),
-                         m->G(w.ln2b), NL, D, m->ws, m->ws_floats, s, Tr, m->dCh));
+        PT_TRY(wg_after(m, 3, s));   // dC (the LayerNorm's dx) is read by the previous block's dW
+        PT_TRY(blin_dx_lnbwd(m, m->dffn, d.ffn, bw->f1T, NL, a.xmid, w.ln2w, a.mu2, a.rs2, dA, dC, m->G(w.ln2w),
+                             m->G(w.ln2b), m->dCh, s, Tr));
         PT_TRY(wg_fork(m, s));
         PT_TRY(bldw(m, m->dCh, D, a.ctx, D, m->G(w.projw), m->G(w.projb), NL, s2, Tr));
         PT_TRY(wg_done(m, 3));
@@ -950,11 +968,9 @@ static int block_bwd(PtcgModel* m, const BlockP& w, const BlockA& a, int L, cons
         PT_TRY(wg_fork(m, s));
         PT_TRY(bldw(m, m->dqkv, 3 * D, a.ln1, D, m->G(w.qkvw), m->G(w.qkvb), NL, s2, Tr));
         PT_TRY(wg_done(m, 4));
-        PT_TRY(blin(m, m->dqkv, 3 * D, bw->qkvT, nullptr, m->dln, D, NL, EPI_STORE, false, nullptr, nullptr, s,
-                    Tr));
-        PT_TRY(wg_after(m, 1, s));
-        PT_TRY(pt_ln_bwd(m->dln, D, xin, D, w.ln1w, a.mu1, a.rs1, dC, D, dA, D, m->G(w.ln1w),
-                         m->G(w.ln1b), NL, D, m->ws, m->ws_floats, s, Tr, m->dAh));
+        PT_TRY(wg_after(m, 1, s));   // dA and dAh are read by this block's FFN2 dW
+        PT_TRY(blin_dx_lnbwd(m, m->dqkv, 3 * D, bw->qkvT, NL, xin, w.ln1w, a.mu1, a.rs1, dC, dA, m->G(w.ln1w),
+                             m->G(w.ln1b), m->dAh, s, Tr));
         return PTCG_OK;
     }
     PT_TRY(wg_fork(m, s));

@@ -200,6 +200,8 @@ _SIGS = {
     "ptcg_kernel_layernorm_fwd": (ctypes.c_int, [c_void_p, c_void_p, c_void_p, c_void_p,
                                                  c_void_p, c_void_p, ctypes.c_int, ctypes.c_int,
                                                  c_void_p]),
+    "ptcg_kernel_gemm_dx_layernorm_bwd": (ctypes.c_int, [ctypes.c_int, ctypes.c_int] + [c_void_p] * 12
+                                          + [ctypes.c_int64] + [c_void_p] * 2),
     "ptcg_kernel_layernorm_bwd": (ctypes.c_int, [c_void_p, c_void_p, c_void_p, c_void_p,
                                                  c_void_p, c_void_p, c_void_p, c_void_p,
                                                  c_void_p, ctypes.c_int, ctypes.c_int, c_void_p,

@@ -215,6 +215,88 @@ def test_gemm_resid_ln(rows, K, bf16, cuda):
         assert bool((mu3[cut:] == 7.0).all()) and bool((rs3[cut:] == 7.0).all())
 
 
+# rows: one row, a partial 64-row tile, whole tiles, the trunk's 37.4k rows;
+# K: the FFN1 (1024) and QKV (768) dX products of a bf16 block
+@pytest.mark.parametrize("rows,K,res", [(1, 1024, 1), (63, 768, 0), (200, 1024, 1), (1024, 768, 1),
+                                        (3001, 1024, 0), (37417, 1024, 1), (37417, 768, 1)])
+def test_gemm_dx_layernorm_bwd(rows, K, res, cuda):
+    """The bf16 dX product fused with the LayerNorm backward that reads it:
+    dx, dw, db against float64 (dy = dY WT^T; dx = rs (g - mean g - xh
+    mean(g xh)) + dres with g = dy w, xh = (x - mu) rs; dw = sum dy xh, db =
+    sum dy), against the unfused pair (the bf16 product, then the LayerNorm
+    backward kernel), the bf16 copy of dx rounded to nearest even, and a
+    device row count that leaves the later rows alone and sums dw / db over
+    the rows before it."""
+    N = 256
+    g = torch.Generator().manual_seed(rows + K + res)
+    dY = (torch.randn(rows, K, generator=g) / math.sqrt(K)).bfloat16().float()
+    WT = torch.randn(N, K, generator=g).bfloat16().float()
+    x = torch.randn(rows, N, generator=g) * 1.5 + 0.3
+    w = torch.randn(N, generator=g)
+    mu = x.double().mean(1)
+    rs = 1.0 / torch.sqrt(x.double().var(1, unbiased=False) + 1e-5)
+    mu, rs = mu.float(), rs.float()
+    dres = torch.randn(rows, N, generator=g) if res else None
+
+    def ref(n):
+        dy = dY[:n].double() @ WT.double().T
+        xh = (x[:n].double() - mu[:n, None].double()) * rs[:n, None].double()
+        gg = dy * w.double()
+        dx = rs[:n, None].double() * (gg - gg.mean(1, keepdim=True) - xh * (gg * xh).mean(1, keepdim=True))
+        if res:
+            dx = dx + dres[:n].double()
+        return dy, dx, (dy * xh).sum(0), dy.sum(0)
+
+    dy64, dx64, dw64, db64 = ref(rows)
+    L = native.lib()
+    d_dY, d_WT = dev(dY, torch.bfloat16), dev(WT, torch.bfloat16)
+    dx_, dw_, dmu, drs = dev(x), dev(w), dev(mu), dev(rs)
+    d_dres = dev(dres) if res else None
+    ws = empty(1 << 21)
+    gx, gxh, gw, gb = empty(rows, N), torch.zeros(rows, N, dtype=torch.bfloat16, device="cuda"), empty(N), empty(N)
+    native.check(L.ptcg_kernel_gemm_dx_layernorm_bwd(rows, K, P(d_dY), P(d_WT), P(dx_), P(dw_), P(dmu), P(drs),
+                                                     P(d_dres), P(gx), P(gxh), P(gw), P(gb), P(ws), ws.numel(),
+                                                     None, None))
+    # the unfused pair: the bf16 product (EPI_STORE, no workspace), then the LayerNorm backward
+    dy2, gx2, gw2, gb2 = empty(rows, N), empty(rows, N), empty(N), empty(N)
+    native.check(L.ptcg_kernel_gemm_bs(rows, N, K, P(d_dY), K, P(d_WT), K, P(dy2), N, 0, 0, None, None, 0,
+                                       None, 0, None))
+    native.check(L.ptcg_kernel_layernorm_bwd(P(dy2), P(dx_), P(dw_), P(dmu), P(drs), P(d_dres), P(gx2),
+                                             P(gw2), P(gb2), rows, N, P(ws), ws.numel(), None))
+    torch.cuda.synchronize()
+    assert rel_l2(dy2.cpu(), dy64) < 1e-6
+    assert rel_l2(gx.cpu(), dx64) < 1e-5 and rel_l2(gx.cpu(), gx2.cpu()) < 1e-6
+    assert rel_l2(gw.cpu(), dw64) < 1e-5 and rel_l2(gw.cpu(), gw2.cpu()) < 1e-6
+    assert rel_l2(gb.cpu(), db64) < 1e-5 and rel_l2(gb.cpu(), gb2.cpu()) < 1e-6
+    assert torch.equal(gxh, gx.bfloat16())
+    if rows > 64:
+        # device row count: rows past it keep their contents, dw / db cover the rows before it
+        cut = rows // 2 + 5
+        nd = torch.tensor([cut], dtype=torch.int32, device="cuda")
+        gx3 = torch.full((rows, N), 7.0, device="cuda")
+        gxh3 = torch.full((rows, N), 7.0, dtype=torch.bfloat16, device="cuda")
+        gw3, gb3 = empty(N), empty(N)
+        native.check(L.ptcg_kernel_gemm_dx_layernorm_bwd(rows, K, P(d_dY), P(d_WT), P(dx_), P(dw_), P(dmu),
+                                                         P(drs), P(d_dres), P(gx3), P(gxh3), P(gw3), P(gb3),
+                                                         P(ws), ws.numel(), P(nd), None))
+        torch.cuda.synchronize()
+        assert torch.equal(gx3[:cut], gx[:cut]) and torch.equal(gxh3[:cut], gxh[:cut])
+        assert bool((gx3[cut:] == 7.0).all()) and bool((gxh3[cut:] == 7.0).all())
+        _, _, dw_c, db_c = ref(cut)
+        assert rel_l2(gw3.cpu(), dw_c) < 1e-5 and rel_l2(gb3.cpu(), db_c) < 1e-5
+
+
+def test_gemm_dx_layernorm_bwd_rejects_other_shapes(cuda):
+    L = native.lib()
+    a, wt = torch.zeros(8, 100, dtype=torch.bfloat16, device="cuda"), torch.zeros(256, 100, dtype=torch.bfloat16,
+                                                                                  device="cuda")
+    x, gx, v, st = empty(8, 256), empty(8, 256), empty(256), empty(8)
+    ws = empty(1 << 16)
+    with pytest.raises(RuntimeError, match="layernorm bwd"):
+        native.check(L.ptcg_kernel_gemm_dx_layernorm_bwd(8, 100, P(a), P(wt), P(x), P(v), P(st), P(st), None,
+                                                         P(gx), None, P(v), P(v), P(ws), ws.numel(), None, None))
+
+
 def test_gemm_resid_ln_rejects_other_shapes(cuda):
     L = native.lib()
     a, w, b, r = empty(8, 100), empty(256, 100), empty(256), empty(8, 256)

@@ -437,7 +437,8 @@ def main():
     achieved = useful / gemm_s / 1e12
     peak = BF16_MFMA_PEAK_TFLOPS if bf16 else FP32_MFMA_PEAK_TFLOPS
     traffic = measured_gemm_traffic()
-    kname = ("gemm_bs32_kernel + gemm_bs_dw_kernel (trunk blocks, bf16 operands) + gemm_bf16_k16_kernel"
+    kname = ("gemm_bs32_kernel + gemm_bs_dw_kernel + gemm_resid_ln_kernel + gemm_dx_lnbwd_kernel (trunk blocks, "
+             "bf16 operands) + gemm_bf16_k16_kernel"
              if bf16 else "gemm_f32_dma_kernel + gemm_f32_kernel + gemm_resid_ln_kernel")
     roof = dict(bound="mfma", kernel=f"{kname} (all launches: trunk, token, option and head GEMMs)",
                 achieved=round(achieved, 3), peak=peak, unit="TFLOP/s",
@@ -454,6 +455,11 @@ def main():
         roof["fused_layernorm"] = ("the blocks' residual products (out-projection, FFN2) run the LayerNorm that "
                                    "reads their output in the same launch (gemm_resid_ln_kernel): its time and "
                                    "its output bytes are inside these figures")
+    if bf16 and dm.d == 256:
+        roof["fused_layernorm"] = ("the bf16 blocks' residual products run the LayerNorm forward that reads their "
+                                   "output (gemm_resid_ln_kernel), and their QKV / FFN1 dX products the LayerNorm "
+                                   "backward that reads theirs (gemm_dx_lnbwd_kernel), in the same launch: those "
+                                   "LayerNorms' time is inside these figures, their flops are not counted")
     if bf16:
         # The products' arithmetic intensity (useful flops over the operand /
         # output bytes: bf16 in the trunk blocks, fp32 residual stream and

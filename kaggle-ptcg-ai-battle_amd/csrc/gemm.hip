@@ -1130,9 +1130,23 @@ __global__ __launch_bounds__(NT) void gemm_dx_lnbwd_kernel(const GemmArgs g0, co
         }
     }
     const float4 wv = *reinterpret_cast<const float4*>(a.w + 4 * lane);
-    float4 aw = make_float4(0.f, 0.f, 0.f, 0.f), ab = aw;
+    const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
+    float4 aw = z4, ab = z4;
+    const int mlast = g.M - 1;
+    // a row's x, residual gradient and statistics are loaded one row ahead
+    // (row indices clamped to the last row, so every load is in bounds)
+    auto ld_row = [&](int m, float4& xv, float4& rv, float& mu, float& rs) {
+        xv = *reinterpret_cast<const float4*>(a.x + (long)m * RL_N + 4 * lane);
+        rv = a.dres ? *reinterpret_cast<const float4*>(a.dres + (long)m * RL_N + 4 * lane) : z4;
+        mu = a.mean[m];
+        rs = a.rstd[m];
+    };
 #pragma unroll
     for (int h = 0; h < TM; ++h) {
+        const int mb = m0 + 32 * h + 8 * wave;
+        float4 xv, rv;
+        float mu, rs;
+        ld_row(mb < mlast ? mb : mlast, xv, rv, mu, rs);
         __syncthreads();   // the stages are free (main loop done / previous half consumed)
 #pragma unroll
         for (int tj = 0; tj < 2; ++tj)
@@ -1141,13 +1155,14 @@ __global__ __launch_bounds__(NT) void gemm_dx_lnbwd_kernel(const GemmArgs g0, co
                 *reinterpret_cast<floatx4*>(smem + l32 * RL_SST + wn + 32 * tj + 8 * q + 4 * lh) =
                     floatx4{acc[h][tj][4 * q], acc[h][tj][4 * q + 1], acc[h][tj][4 * q + 2], acc[h][tj][4 * q + 3]};
         __syncthreads();
-#pragma unroll 2
+#pragma unroll
         for (int r = 0; r < 8; ++r) {
-            const int lr = 8 * wave + r, m = m0 + 32 * h + lr;
+            const int lr = 8 * wave + r, m = mb + r;
             if (m >= g.M) break;   // uniform over the wave; later rows are past M too
+            float4 xn, rn;
+            float mun, rsn;
+            ld_row(m < mlast ? m + 1 : mlast, xn, rn, mun, rsn);
             const float4 dd = *reinterpret_cast<const float4*>(smem + lr * RL_SST + 4 * lane);
-            const float4 xv = *reinterpret_cast<const float4*>(a.x + (long)m * RL_N + 4 * lane);
-            const float mu = a.mean[m], rs = a.rstd[m];
             const float4 xh = make_float4((xv.x - mu) * rs, (xv.y - mu) * rs, (xv.z - mu) * rs, (xv.w - mu) * rs);
             const float4 gv = make_float4(dd.x * wv.x, dd.y * wv.y, dd.z * wv.z, dd.w * wv.w);
             const float s1 = (gv.x + gv.y) + (gv.z + gv.w);
@@ -1162,13 +1177,13 @@ __global__ __launch_bounds__(NT) void gemm_dx_lnbwd_kernel(const GemmArgs g0, co
             o.z = (gv.z - m1 - xh.z * m2) * rs;
             o.w = (gv.w - m1 - xh.w * m2) * rs;
             if (a.dres) {
-                const float4 rv = *reinterpret_cast<const float4*>(a.dres + (long)m * RL_N + 4 * lane);
                 o.x += rv.x; o.y += rv.y; o.z += rv.z; o.w += rv.w;
             }
             *reinterpret_cast<float4*>(a.dx + (long)m * RL_N + 4 * lane) = o;
             if (a.dxh)
                 *reinterpret_cast<bf16x4*>(a.dxh + (long)m * RL_N + 4 * lane) =
                     bf16x4{(__bf16)o.x, (__bf16)o.y, (__bf16)o.z, (__bf16)o.w};
+            xv = xn; rv = rn; mu = mun; rs = rsn;
         }
     }
     // the workgroup's partial row: [sum dy xh (256) | sum dy (256)], waves in order

@@ -399,7 +399,7 @@ def main():
     ms, launches, exec_flops = ctypes.c_double(), ctypes.c_int(), ctypes.c_double()
     native.check(L.ptcg_profile_end(ctypes.byref(ms), ctypes.byref(launches), ctypes.byref(exec_flops)))
     losses = trainer.log(pl)
-    if not np.isfinite(losses["total_loss"]):
+    if not np.isfinite(losses["loss"].get("total", np.nan)):
         raise RuntimeError(f"non-finite loss during the benchmark: {losses}")
 
     sec_stream = t1 - t0

@@ -57,6 +57,19 @@ typedef struct PtcgTrainer PtcgTrainer;
 const char* ptcg_last_error(void);
 int ptcg_abi_version(void);
 
+/* ---- device memory (the trainer owns memory like the reference's
+ * Allocator / alloc_create, native/src/kernels.cu:412-474; these give a
+ * host driver its rollout buffers without another GPU runtime) ----------
+ * alloc: zero-filled device bytes (bytes = 0 gives NULL).  memcpy dir: 0
+ * host -> device, 1 device -> host (both synchronous: they wait for
+ * `stream` first and return with the bytes in place), 2 device -> device
+ * (ordered on `stream`).                                                   */
+int ptcg_device_count(int* n);
+int ptcg_device_alloc(int64_t bytes, void** out);
+int ptcg_device_free(void* p);
+int ptcg_memcpy(void* dst, const void* src, int64_t bytes, int dir, void* stream);
+int ptcg_device_synchronize(void);
+
 /* ---- layout (ptcg/rl/buffers.py:212-230; native_weights.py:45-113;
  *      kernels.cu:433-466 16 B alignment; pufferlib.cu:2366-2390) -------- */
 int ptcg_obs_size(const PtcgDims* dims);
@@ -165,8 +178,11 @@ int ptcg_ppo_loss_fwd_bwd_noalloc(const float* dec_out, int n, int A,
                                   float* grad, float* ratio, float* newvalue,
                                   float* stats, float* guard, void* stream);
 
-/* ---- gate (pufferlib.cu:1292-1302): gate[0] = 1 apply / 0 skip, from
- * guard[0..1] = (approx_kl, v_loss); skipped[0] += 1 - gate.              */
+/* ---- gate (kl_gate_kernel, pufferlib.cu:1292-1302): gate[0] = 1 apply /
+ * 0 skip, from guard[0..1] = (approx_kl, v_loss).  skipped: null or two
+ * adjacent device floats, the reference's KL_GUARD_SKIPPED and
+ * KL_GUARD_SKIPPED_VF (pufferlib.cu:37-38): skipped[0] += 1 - gate (every
+ * veto), skipped[1] += 1 when the value test failed.                      */
 int ptcg_kl_gate(const float* guard, float kl_threshold, float vf_threshold,
                  float* gate, float* skipped, void* stream);
 
@@ -185,6 +201,15 @@ int ptcg_adam_step(float* weights, float* grads, float* m, float* v, int64_t n,
                    const double* lr, double beta1, double beta2, double eps, float max_grad_norm,
                    const float* gate, int32_t* step, float* norm_out, float* workspace,
                    void* stream);
+/* The same step with the learning rate read from a device float: the type
+ * of the reference trainer's own lr_ptr (muon.cu:96-99, written by
+ * train_impl at pufferlib.cu:1933), so that a reference-side caller binds
+ * its lr_ptr directly.  The float is widened to double before Adam's
+ * scalar arithmetic; everything else is ptcg_adam_step.                   */
+int ptcg_adam_step_lrf(float* weights, float* grads, float* m, float* v, int64_t n,
+                       const float* lr, double beta1, double beta2, double eps, float max_grad_norm,
+                       const float* gate, int32_t* step, float* norm_out, float* workspace,
+                       void* stream);
 
 /* ---- Muon, the reference's optimizer (muon.cu:154-297) ------------------
  * muon_init + muon_post_create: momentum arena (zeroed) and Newton-Schulz
@@ -442,10 +467,55 @@ int ptcg_trainer_forward_backward(PtcgTrainer* t, const float* obs, const int32_
                                   const float* actions, const float* old_logprobs,
                                   const float* advantages, const float* returns,
                                   const float* values, void* stream);
-/* losses (bindings.cu:15-118 "losses"): out[0..6] = pg, vf, ent, total,
- * old_approx_kl, approx_kl, clipfrac summed over steps; out[7] = count;
- * out[8] = skipped steps; out[9] = last grad norm.  Synchronous.           */
-int ptcg_trainer_losses(PtcgTrainer* t, float* out10, int reset);
+/* ---- log (_C.log, bindings.cu:15-118) ----------------------------------
+ * Phases of PtcgLog.perf_s: the reference's PROF_NAMES (pufferlib.cu:43-57)
+ * in its order, then this build's split of train_forward into the step's
+ * four parts.                                                             */
+#define PTCG_PERF_ROLLOUT 0
+#define PTCG_PERF_EVAL_GPU 1
+#define PTCG_PERF_EVAL_ENV 2
+#define PTCG_PERF_TRAIN_MISC 3
+#define PTCG_PERF_TRAIN_FORWARD 4
+#define PTCG_PERF_FORWARD 5      /* model forward                          */
+#define PTCG_PERF_LOSS 6         /* PPO loss fwd + bwd                     */
+#define PTCG_PERF_BACKWARD 7     /* model backward                         */
+#define PTCG_PERF_OPTIMIZER 8    /* gate + clip + Adam (or Muon)           */
+#define PTCG_PERF_N 9
+typedef struct PtcgLog {
+    /* sums since the last reset (losses_puf, pufferlib.cu:1254-1284):
+     * policy, value, entropy, total, old_kl, kl, clipfrac                  */
+    float loss[7];
+    float n;               /* minibatches in those sums (LOSS_N)            */
+    float kl_skipped;      /* gate vetoes since the last reset              */
+    float vf_skipped;      /* ... of which the value test failed           */
+    float gate;            /* the gate's last decision (kept over resets)   */
+    float grad_norm;       /* last step's global grad norm before the clip  */
+    float lr;              /* the APPLIED lr, read back from the device     */
+    float ent_coef;        /* the applied entropy coefficient (device)      */
+    float gpu_percent;     /* amdgpu gpu_busy_percent of this device, or -1 */
+    float pad_;
+    double perf_s[PTCG_PERF_N];   /* seconds per phase since the last reset */
+    double vram_used_gb, vram_total_gb;   /* hipMemGetInfo                 */
+    int64_t global_step, epoch;          /* ptcg_trainer_set_counters       */
+} PtcgLog;
+/* Synchronous.  reset != 0 zeroes the loss sums, the two skip counters and
+ * perf_s afterwards (the reference zeroes losses, SKIPPED / SKIPPED_VF and
+ * its profile; the gate keeps its value).                                  */
+int ptcg_trainer_log(PtcgTrainer* t, PtcgLog* out, int reset);
+/* Phase timing (the reference's profile.events, pufferlib.cu:1851-2185).
+ * mark 0 / 1: start / end of train's pre-loop setup; mark 2: start of a
+ * minibatch's misc work (advantage, replay draw, index upload).  An eager
+ * ptcg_trainer_step on a stream that is not capturing records the end of
+ * the misc work and the ends of its forward, loss, backward and optimizer.
+ * perf_commit (synchronous) adds the pre-loop span once and the last
+ * minibatch's spans times `minibatches` (the reference's accounting,
+ * pufferlib.cu:2174-2185); spans whose marks were not recorded add 0.      */
+int ptcg_trainer_perf_mark(PtcgTrainer* t, int mark, void* stream);
+int ptcg_trainer_perf_commit(PtcgTrainer* t, int minibatches);
+/* host seconds spent outside the trainer's streams (rollouts, eval), added
+ * to phase `phase` as the reference adds its rollout wall time
+ * (bindings.cu:170-177)                                                    */
+int ptcg_trainer_perf_add(PtcgTrainer* t, int phase, double seconds);
 /* device pointer of the last forward's (minibatch, n_opt+1) output and of
  * the PPO grad buffer (for tests).                                         */
 int ptcg_trainer_buffers(PtcgTrainer* t, float** dec_out, float** ppo_grad,

@@ -81,10 +81,12 @@ __global__ __launch_bounds__(NT_NORM) void adam_norm_kernel(const float4* __rest
     }
 }
 
-template <int U>
+// LR: the learning rate's device type (double: the trainer's scalar; float:
+// the reference trainer's lr_ptr), widened to double before use
+template <int U, typename LR>
 __global__ __launch_bounds__(NT) void adam_update_kernel(float4* __restrict__ p,
         const float4* __restrict__ g, float4* __restrict__ m, float4* __restrict__ v, long n4,
-        int nparts, const double* __restrict__ lr_dev, double b1, double b2, double eps, float max_norm,
+        int nparts, const LR* __restrict__ lr_dev, double b1, double b2, double eps, float max_norm,
         const float* __restrict__ gate, const float* __restrict__ ws, float* __restrict__ norm_out,
         int32_t* __restrict__ step) {
     if (gate && gate[0] == 0.0f) return;
@@ -119,7 +121,7 @@ __global__ __launch_bounds__(NT) void adam_update_kernel(float4* __restrict__ p,
     }
     // scalars in double, rounded once to fp32 (torch keeps them as Python
     // floats and hands fp32 kernels the rounded value)
-    const double lr = lr_dev[0];
+    const double lr = (double)lr_dev[0];
     const float step_size = (float)(lr / (1.0 - pow(b1, (double)t)));
     const float bc2s = (float)sqrt(1.0 - pow(b2, (double)t));
     const float omb1 = (float)(1.0 - b1), omb2 = (float)(1.0 - b2);
@@ -167,9 +169,10 @@ __global__ __launch_bounds__(NT) void adam_update_kernel(float4* __restrict__ p,
 
 long pt_adam_ws_floats() { return NPART + 4; }
 
-int pt_adam_step(float* w, float* g, float* m, float* v, long n, const double* lr, double b1, double b2,
-                 double eps, float max_norm, const float* gate, int32_t* step, float* norm_out,
-                 float* ws, hipStream_t s) {
+template <typename LR>
+static int adam_step(float* w, float* g, float* m, float* v, long n, const LR* lr, double b1, double b2,
+                     double eps, float max_norm, const float* gate, int32_t* step, float* norm_out,
+                     float* ws, hipStream_t s) {
     PT_REQUIRE(lr != nullptr, "adam: the learning rate must be a device scalar");
     PT_REQUIRE(n > 0 && n % 4 == 0, "adam: arena length %ld must be a positive multiple of 4", n);
     PT_REQUIRE(((uintptr_t)w | (uintptr_t)g | (uintptr_t)m | (uintptr_t)v) % 16 == 0,
@@ -186,9 +189,22 @@ int pt_adam_step(float* w, float* g, float* m, float* v, long n, const double* l
     long ublocks = (n4 + NT * UPD_U - 1) / (NT * UPD_U);
     if (ublocks > UPD_BLOCKS) ublocks = UPD_BLOCKS;
     slot = pt_prof_open(s);
-    hipLaunchKernelGGL(adam_update_kernel<UPD_U>, dim3((unsigned)ublocks), dim3(NT), 0, s, (float4*)w, (const float4*)g,
-                       (float4*)m, (float4*)v, n4, parts, lr, b1, b2, eps, max_norm, gate, ws, norm_out, step);
+    hipLaunchKernelGGL((adam_update_kernel<UPD_U, LR>), dim3((unsigned)ublocks), dim3(NT), 0, s, (float4*)w,
+                       (const float4*)g, (float4*)m, (float4*)v, n4, parts, lr, b1, b2, eps, max_norm, gate, ws,
+                       norm_out, step);
     PT_LAUNCH_CHECK();
     pt_prof_close(slot, PROF_ADAM_UPDATE, 28.0 * n, s);
     return PTCG_OK;
+}
+
+int pt_adam_step(float* w, float* g, float* m, float* v, long n, const double* lr, double b1, double b2,
+                 double eps, float max_norm, const float* gate, int32_t* step, float* norm_out,
+                 float* ws, hipStream_t s) {
+    return adam_step(w, g, m, v, n, lr, b1, b2, eps, max_norm, gate, step, norm_out, ws, s);
+}
+
+int pt_adam_step(float* w, float* g, float* m, float* v, long n, const float* lr, double b1, double b2,
+                 double eps, float max_norm, const float* gate, int32_t* step, float* norm_out,
+                 float* ws, hipStream_t s) {
+    return adam_step(w, g, m, v, n, lr, b1, b2, eps, max_norm, gate, step, norm_out, ws, s);
 }

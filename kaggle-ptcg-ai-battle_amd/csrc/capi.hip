@@ -3,6 +3,7 @@
 // interface it replaces).
 #include "model.h"
 
+#include <ctype.h>
 #include <stdarg.h>
 #include <stdio.h>
 #include <string.h>
@@ -217,6 +218,63 @@ extern "C" int ptcg_arena_to_packed(const PtcgDims* dims, const float* arena, fl
     return packed_arena(dims, arena, packed, false);
 }
 
+// ------------------------------------------------------------ device memory
+// The trainer owns its device memory as the reference's does (Allocator /
+// alloc_create, kernels.cu:412-474); these let a host-side driver hold the
+// rollout's device buffers and move bytes without another runtime.
+extern "C" int ptcg_device_count(int* n) {
+    PT_REQUIRE(n, "device_count: null argument");
+    *n = 0;
+    const hipError_t e = hipGetDeviceCount(n);
+    if (e != hipSuccess) *n = 0;
+    return PTCG_OK;
+}
+
+extern "C" int ptcg_device_alloc(int64_t bytes, void** out) {
+    PT_REQUIRE(out && bytes >= 0, "device_alloc: bad arguments");
+    *out = nullptr;
+    if (bytes == 0) return PTCG_OK;
+    PT_HIP(hipMalloc(out, (size_t)bytes));
+    const hipError_t e = hipMemset(*out, 0, (size_t)bytes);
+    if (e != hipSuccess) {
+        (void)hipFree(*out);
+        *out = nullptr;
+        ptcg_set_error("device_alloc: hipMemset: %s", hipGetErrorString(e));
+        return PTCG_ERR_HIP;
+    }
+    return PTCG_OK;
+}
+
+// waits for the device first: work launched on any stream may still read p
+extern "C" int ptcg_device_free(void* p) {
+    if (!p) return PTCG_OK;
+    PT_HIP(hipDeviceSynchronize());
+    PT_HIP(hipFree(p));
+    return PTCG_OK;
+}
+
+// dir: 0 host -> device, 1 device -> host, 2 device -> device.  Host <->
+// device copies are synchronous (they return with the bytes in place);
+// device -> device is ordered on `stream`.
+extern "C" int ptcg_memcpy(void* dst, const void* src, int64_t bytes, int dir, void* stream) {
+    PT_REQUIRE(bytes >= 0 && dir >= 0 && dir <= 2, "memcpy: bad arguments (bytes %lld, dir %d)",
+               (long long)bytes, dir);
+    if (bytes == 0) return PTCG_OK;
+    PT_REQUIRE(dst && src, "memcpy: null pointer");
+    if (dir == 2) {
+        PT_HIP(hipMemcpyAsync(dst, src, (size_t)bytes, hipMemcpyDeviceToDevice, (hipStream_t)stream));
+        return PTCG_OK;
+    }
+    PT_HIP(hipStreamSynchronize((hipStream_t)stream));
+    PT_HIP(hipMemcpy(dst, src, (size_t)bytes, dir == 0 ? hipMemcpyHostToDevice : hipMemcpyDeviceToHost));
+    return PTCG_OK;
+}
+
+extern "C" int ptcg_device_synchronize(void) {
+    PT_HIP(hipDeviceSynchronize());
+    return PTCG_OK;
+}
+
 // ------------------------------------------------------------ PPO / gate / Adam
 extern "C" int ptcg_ppo_loss_fwd_bwd(const float* dec_out, int n, int A, const float* mask,
                                      int64_t mask_stride, const int32_t* row_idx, const float* actions,
@@ -311,10 +369,25 @@ extern "C" int ptcg_adam_step(float* weights, float* grads, float* m, float* v, 
                         norm_out, workspace, (hipStream_t)stream);
 }
 
+extern "C" int ptcg_adam_step_lrf(float* weights, float* grads, float* m, float* v, int64_t n, const float* lr,
+                                  double beta1, double beta2, double eps, float max_grad_norm,
+                                  const float* gate, int32_t* step, float* norm_out, float* workspace,
+                                  void* stream) {
+    PT_REQUIRE(weights && grads && m && v && lr && step && workspace, "adam_step_lrf: null buffer");
+    return pt_adam_step(weights, grads, m, v, n, lr, beta1, beta2, eps, max_grad_norm, gate, step,
+                        norm_out, workspace, (hipStream_t)stream);
+}
+
 extern "C" int64_t ptcg_adam_workspace_floats(void) { return pt_adam_ws_floats(); }
 
 // ------------------------------------------------------------ trainer
 long pt_model_arena(const PtcgModel* m);
+// phase marks: 0 / 1 pre-loop start / end, 2 misc start, 3 step start (misc
+// end), 4 forward end, 5 loss end, 6 backward end, 7 optimizer end
+constexpr int PT_NMARK = 8;
+// trainer stats floats: [0..6] loss sums, [7] minibatches, [8] / [9] the
+// gate's two skip counters (adjacent, as the reference's), [10] grad norm
+constexpr int PT_ST_SKIP = 8, PT_ST_NORM = 10, PT_ST_FLOATS = 11;
 float* pt_model_out(const PtcgModel* m);
 
 struct PtcgTrainer {
@@ -355,6 +428,13 @@ struct PtcgTrainer {
     std::vector<int> roll_exec_buf;
     double wd_1d = 0.0;
     int64_t global_step = 0, epoch = 0;
+    // phase timing (the reference's profile.events, pufferlib.cu:1851-2185):
+    // pev[k] is mark k (ptcg_trainer_perf_mark, ptcg_trainer_step),
+    // pev_rec[k] whether it was recorded since the last commit; perf_s holds
+    // seconds per phase since the last log reset
+    hipEvent_t pev[PT_NMARK] = {};
+    bool pev_rec[PT_NMARK] = {};
+    double perf_s[PTCG_PERF_N] = {};
     std::vector<float> st_f[5];
     std::vector<int32_t> st_i[2];
 };
@@ -370,6 +450,8 @@ extern "C" void ptcg_trainer_free(PtcgTrainer* t) {
     if (t->graph_exec) (void)hipGraphExecDestroy(t->graph_exec);
     if (t->graph) (void)hipGraphDestroy(t->graph);
     if (t->cap_stream) (void)hipStreamDestroy(t->cap_stream);
+    for (auto e : t->pev)
+        if (e) (void)hipEventDestroy(e);
     if (t->mem) (void)hipFree(t->mem);
     delete t;
 }
@@ -454,6 +536,22 @@ extern "C" int ptcg_trainer_create(const PtcgDims* dims, const PtcgHypers* hyp, 
     t->lr_dev = reinterpret_cast<double*>(t->mem + oHyp);
     t->ent_dev = F(oHyp) + 2;
     t->dbg_obs = F(oDbg);
+    for (auto& ev : t->pev) {
+        e = hipEventCreate(&ev);
+        if (e != hipSuccess) {
+            ptcg_set_error("trainer_create: hipEventCreate: %s", hipGetErrorString(e));
+            ptcg_trainer_free(t);
+            return PTCG_ERR_HIP;
+        }
+    }
+    // the gate starts open, as the reference's (pufferlib.cu:2732-2734)
+    const float one = 1.0f;
+    e = hipMemcpy(t->gate, &one, sizeof one, hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        ptcg_set_error("trainer_create: gate init: %s", hipGetErrorString(e));
+        ptcg_trainer_free(t);
+        return PTCG_ERR_HIP;
+    }
     r = ptcg_model_bind(t->model, t->P, t->Gr);
     if (r == PTCG_OK) r = ptcg_model_reg_train(t->model, minibatch);
     if (r == PTCG_OK) r = write_schedule(t, hyp->lr, hyp->ent_coef);
@@ -708,20 +806,46 @@ extern "C" int ptcg_trainer_debug_forward(PtcgTrainer* t, const float* obs_host,
     return PTCG_OK;
 }
 
-static int fwd_bwd(PtcgTrainer* t, const float* obs, const int32_t* idx, const float* actions,
-                   const float* old_logprobs, const float* advantages, const float* returns,
-                   const float* values, hipStream_t s) {
+// record phase mark k on stream s (timed: an eager step on a stream that is
+// not being captured)
+static int perf_rec(PtcgTrainer* t, int k, hipStream_t s, bool timed) {
+    if (!timed) return PTCG_OK;
+    PT_HIP(hipEventRecord(t->pev[k], s));
+    t->pev_rec[k] = true;
+    return PTCG_OK;
+}
+
+// forward -> PPO loss -> backward (-> gate -> optimizer), the reference's
+// minibatch order (pufferlib.cu:2039-2105)
+static int step_impl(PtcgTrainer* t, const float* obs, const int32_t* row_idx, const float* actions,
+                     const float* old_logprobs, const float* advantages, const float* returns, const float* values,
+                     hipStream_t s, bool timed, bool optimizer = true) {
     PT_REQUIRE(t && obs && actions && old_logprobs && advantages && returns && values,
                "trainer_step: null input");
+    PT_TRY(perf_rec(t, 3, s, timed));
     float* out = nullptr;
-    PT_TRY(ptcg_model_forward(t->model, obs, idx, t->B, &out, s));
+    PT_TRY(ptcg_model_forward(t->model, obs, row_idx, t->B, &out, s));
+    PT_TRY(perf_rec(t, 4, s, timed));
     const PtcgHypers& h = t->hyp;
-    PT_TRY(pt_ppo_loss(out, t->B, t->dm.n_opt, obs + t->off.opt_mask, t->off.size, idx, actions,
+    PT_TRY(pt_ppo_loss(out, t->B, t->dm.n_opt, obs + t->off.opt_mask, t->off.size, row_idx, actions,
                        old_logprobs, advantages, returns, values, t->prio, h.clip_coef, h.vf_clip_coef,
                        h.vf_coef, t->ent_dev, t->grad, t->ratio, t->newvalue, t->stats, t->guard,
                        t->ppo_part, s));
+    PT_TRY(perf_rec(t, 5, s, timed));
     PT_TRY(ptcg_model_bind_returns(t->model, returns));
     PT_TRY(ptcg_model_backward(t->model, t->grad, s));
+    PT_TRY(perf_rec(t, 6, s, timed));
+    if (!optimizer) return PTCG_OK;
+    const bool gate_on = h.kl_skip_threshold > 0.f || h.vf_skip_threshold > 0.f;
+    if (gate_on)
+        PT_TRY(pt_kl_gate(t->guard, h.kl_skip_threshold, h.vf_skip_threshold, t->gate, t->stats + PT_ST_SKIP, s));
+    if (t->muon)
+        PT_TRY(ptcg_muon_step(t->muon, t->P, t->Gr, h.max_grad_norm, gate_on ? t->gate : nullptr,
+                              t->stats + PT_ST_NORM, s));
+    else
+        PT_TRY(pt_adam_step(t->P, t->Gr, t->M, t->V, t->arena, t->lr_dev, h.beta1, h.beta2, h.eps, h.max_grad_norm,
+                            gate_on ? t->gate : nullptr, t->step, t->stats + PT_ST_NORM, t->adam_ws, s));
+    PT_TRY(perf_rec(t, 7, s, timed));
     return PTCG_OK;
 }
 
@@ -736,7 +860,9 @@ extern "C" int ptcg_trainer_forward_backward(PtcgTrainer* t, const float* obs, c
                                              const float* actions, const float* old_logprobs,
                                              const float* advantages, const float* returns,
                                              const float* values, void* stream) {
-    return fwd_bwd(t, obs, row_idx, actions, old_logprobs, advantages, returns, values, (hipStream_t)stream);
+    PT_REQUIRE(t, "trainer_forward_backward: null trainer");
+    return step_impl(t, obs, row_idx, actions, old_logprobs, advantages, returns, values, (hipStream_t)stream,
+                     false, false);
 }
 
 extern "C" int ptcg_trainer_set_static(PtcgTrainer* t, const float* card_static, const float* att_static,
@@ -935,16 +1061,59 @@ extern "C" int ptcg_trainer_replay_rollout(PtcgTrainer* t, int slot, void* strea
 extern "C" int ptcg_trainer_step(PtcgTrainer* t, const float* obs, const int32_t* row_idx,
                                  const float* actions, const float* old_logprobs, const float* advantages,
                                  const float* returns, const float* values, void* stream) {
+    PT_REQUIRE(t, "trainer_step: null trainer");
     hipStream_t s = (hipStream_t)stream;
-    PT_TRY(fwd_bwd(t, obs, row_idx, actions, old_logprobs, advantages, returns, values, s));
-    const PtcgHypers& h = t->hyp;
-    const bool gate_on = h.kl_skip_threshold > 0.f || h.vf_skip_threshold > 0.f;
-    if (gate_on) PT_TRY(pt_kl_gate(t->guard, h.kl_skip_threshold, h.vf_skip_threshold, t->gate, t->stats + 8, s));
-    if (t->muon)
-        PT_TRY(ptcg_muon_step(t->muon, t->P, t->Gr, h.max_grad_norm, gate_on ? t->gate : nullptr, t->stats + 9, s));
-    else
-        PT_TRY(pt_adam_step(t->P, t->Gr, t->M, t->V, t->arena, t->lr_dev, h.beta1, h.beta2, h.eps, h.max_grad_norm,
-                            gate_on ? t->gate : nullptr, t->step, t->stats + 9, t->adam_ws, s));
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    PT_HIP(hipStreamIsCapturing(s, &cs));
+    return step_impl(t, obs, row_idx, actions, old_logprobs, advantages, returns, values, s,
+                     cs == hipStreamCaptureStatusNone);
+}
+
+extern "C" int ptcg_trainer_perf_mark(PtcgTrainer* t, int mark, void* stream) {
+    PT_REQUIRE(t, "perf_mark: null trainer");
+    PT_REQUIRE(mark >= 0 && mark <= 2, "perf_mark: mark %d outside [0, 2] (3..7 are the step's own)", mark);
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    PT_HIP(hipStreamIsCapturing((hipStream_t)stream, &cs));
+    return perf_rec(t, mark, (hipStream_t)stream, cs == hipStreamCaptureStatusNone);
+}
+
+// elapsed seconds between marks a and b, 0 unless both were recorded
+static int perf_span(PtcgTrainer* t, int a, int b, double* sec) {
+    *sec = 0.0;
+    if (!t->pev_rec[a] || !t->pev_rec[b]) return PTCG_OK;
+    float ms = 0.f;
+    PT_HIP(hipEventElapsedTime(&ms, t->pev[a], t->pev[b]));
+    *sec = ms > 0.f ? ms * 1e-3 : 0.0;
+    return PTCG_OK;
+}
+
+extern "C" int ptcg_trainer_perf_commit(PtcgTrainer* t, int minibatches) {
+    PT_REQUIRE(t, "perf_commit: null trainer");
+    PT_REQUIRE(minibatches >= 0, "perf_commit: minibatches %d < 0", minibatches);
+    for (int k = 0; k < PT_NMARK; ++k)
+        if (t->pev_rec[k]) PT_HIP(hipEventSynchronize(t->pev[k]));
+    double pre, misc, fwd, loss, bwd, opt;
+    PT_TRY(perf_span(t, 0, 1, &pre));
+    PT_TRY(perf_span(t, 2, 3, &misc));
+    PT_TRY(perf_span(t, 3, 4, &fwd));
+    PT_TRY(perf_span(t, 4, 5, &loss));
+    PT_TRY(perf_span(t, 5, 6, &bwd));
+    PT_TRY(perf_span(t, 6, 7, &opt));
+    const double mb = (double)minibatches;
+    t->perf_s[PTCG_PERF_TRAIN_MISC] += pre + misc * mb;
+    t->perf_s[PTCG_PERF_TRAIN_FORWARD] += (fwd + loss + bwd + opt) * mb;
+    t->perf_s[PTCG_PERF_FORWARD] += fwd * mb;
+    t->perf_s[PTCG_PERF_LOSS] += loss * mb;
+    t->perf_s[PTCG_PERF_BACKWARD] += bwd * mb;
+    t->perf_s[PTCG_PERF_OPTIMIZER] += opt * mb;
+    for (bool& r : t->pev_rec) r = false;
+    return PTCG_OK;
+}
+
+extern "C" int ptcg_trainer_perf_add(PtcgTrainer* t, int phase, double seconds) {
+    PT_REQUIRE(t, "perf_add: null trainer");
+    PT_REQUIRE(phase >= 0 && phase < PTCG_PERF_N, "perf_add: phase %d outside [0, %d)", phase, PTCG_PERF_N);
+    t->perf_s[phase] += seconds;
     return PTCG_OK;
 }
 
@@ -962,8 +1131,8 @@ extern "C" int ptcg_trainer_capture_step(PtcgTrainer* t, const float* obs, const
     if (!t->cap_stream) PT_HIP(hipStreamCreateWithFlags(&t->cap_stream, hipStreamNonBlocking));
     PT_HIP(hipDeviceSynchronize());
     PT_HIP(hipStreamBeginCapture(t->cap_stream, hipStreamCaptureModeThreadLocal));
-    const int r = ptcg_trainer_step(t, obs, row_idx, actions, old_logprobs, advantages, returns, values,
-                                    t->cap_stream);
+    const int r = step_impl(t, obs, row_idx, actions, old_logprobs, advantages, returns, values, t->cap_stream,
+                            false);
     hipGraph_t g = nullptr;
     const hipError_t e = hipStreamEndCapture(t->cap_stream, &g);
     if (r != PTCG_OK) {
@@ -983,11 +1152,65 @@ extern "C" int ptcg_trainer_replay_step(PtcgTrainer* t, void* stream) {
     return PTCG_OK;
 }
 
-extern "C" int ptcg_trainer_losses(PtcgTrainer* t, float* out10, int reset) {
-    PT_REQUIRE(t && out10, "losses: null argument");
+// amdgpu's busy percentage of the current device from sysfs (the
+// reference reads NVML's utilisation, bindings.cu:92-94); -1 if unreadable
+static float gpu_busy_percent() {
+    int dev = 0;
+    char bus[64] = {0};
+    if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetPCIBusId(bus, sizeof bus, dev) != hipSuccess) return -1.f;
+    for (char* c = bus; *c; ++c) *c = (char)tolower((unsigned char)*c);
+    char path[160];
+    snprintf(path, sizeof path, "/sys/bus/pci/devices/%s/gpu_busy_percent", bus);
+    FILE* f = fopen(path, "r");
+    if (!f) return -1.f;
+    int v = -1;
+    if (fscanf(f, "%d", &v) != 1) v = -1;
+    fclose(f);
+    return (float)v;
+}
+
+extern "C" int ptcg_trainer_log(PtcgTrainer* t, PtcgLog* out, int reset) {
+    PT_REQUIRE(t && out, "trainer_log: null argument");
     PT_HIP(hipDeviceSynchronize());
-    PT_HIP(hipMemcpy(out10, t->stats, 10 * sizeof(float), hipMemcpyDeviceToHost));
-    if (reset) PT_HIP(hipMemset(t->stats, 0, 10 * sizeof(float)));
+    float st[PT_ST_FLOATS];
+    PT_HIP(hipMemcpy(st, t->stats, sizeof st, hipMemcpyDeviceToHost));
+    double lr = 0.0;
+    float ent = 0.f, gate = 1.f;
+    // the applied learning rate: the scalar the optimizer's kernels read
+    if (t->muon) {
+        float lf = 0.f;
+        PT_TRY(pt_muon_lr(t->muon, &lf));
+        lr = lf;
+    } else {
+        PT_HIP(hipMemcpy(&lr, t->lr_dev, sizeof lr, hipMemcpyDeviceToHost));
+    }
+    PT_HIP(hipMemcpy(&ent, t->ent_dev, sizeof ent, hipMemcpyDeviceToHost));
+    PT_HIP(hipMemcpy(&gate, t->gate, sizeof gate, hipMemcpyDeviceToHost));
+    PtcgLog& o = *out;
+    memset(&o, 0, sizeof o);
+    for (int i = 0; i < 7; ++i) o.loss[i] = st[i];
+    o.n = st[7];
+    o.kl_skipped = st[PT_ST_SKIP];
+    o.vf_skipped = st[PT_ST_SKIP + 1];
+    o.grad_norm = st[PT_ST_NORM];
+    o.gate = gate;
+    o.lr = (float)lr;
+    o.ent_coef = ent;
+    o.gpu_percent = gpu_busy_percent();
+    for (int i = 0; i < PTCG_PERF_N; ++i) o.perf_s[i] = t->perf_s[i];
+    size_t fr = 0, tot = 0;
+    PT_HIP(hipMemGetInfo(&fr, &tot));
+    const double gib = 1024.0 * 1024.0 * 1024.0;
+    o.vram_used_gb = (double)(tot - fr) / gib;
+    o.vram_total_gb = (double)tot / gib;
+    o.global_step = t->global_step;
+    o.epoch = t->epoch;
+    if (reset) {
+        // the loss sums and both skip counters; the grad norm is overwritten
+        // by every step and the gate keeps its last decision
+        PT_HIP(hipMemset(t->stats, 0, (PT_ST_SKIP + 2) * sizeof(float)));
+        for (double& p : t->perf_s) p = 0.0;
+    }
     return PTCG_OK;
 }
 

@@ -2227,7 +2227,7 @@ int pt_dx_lnbwd(const GemmArgs& g, const float* x, const float* w, const float* 
                 hipStream_t s) {
     PT_REQUIRE(pt_dx_lnbwd_fits(g), "dX + layernorm bwd: needs bf16 operands, N = 256, K %% 32 == 0 (M=%d, K=%d)",
                g.M, g.K);
-    PT_REQUIRE(x && w && mean && rstd && dx && dw && db && ws, "dX + layernorm bwd: null buffer");
+    PT_REQUIRE(g.A && g.B && x && w && mean && rstd && dx && dw && db && ws, "dX + layernorm bwd: null buffer");
     PT_REQUIRE((((uintptr_t)x | (uintptr_t)w | (uintptr_t)dx | (uintptr_t)dres | (uintptr_t)dxh) & 15) == 0,
                "dX + layernorm bwd: 16 B aligned rows needed");
     const int blocks = pt_cdiv(g.M, 64);

@@ -80,8 +80,12 @@ int pt_sample_gumbel(const float* dec_out, int n, int A, const float* mask, long
                      hipStream_t s);
 struct PtcgMuon;
 int pt_muon_set_momentum(PtcgMuon* m, double momentum);
+int pt_muon_lr(PtcgMuon* m, float* lr);
 long pt_adam_ws_floats();
 int pt_adam_step(float* w, float* g, float* m, float* v, long n, const double* lr, double b1, double b2,
+                 double eps, float max_norm, const float* gate, int32_t* step, float* norm_out,
+                 float* ws, hipStream_t s);
+int pt_adam_step(float* w, float* g, float* m, float* v, long n, const float* lr, double b1, double b2,
                  double eps, float max_norm, const float* gate, int32_t* step, float* norm_out,
                  float* ws, hipStream_t s);
 

@@ -497,6 +497,13 @@ extern "C" int ptcg_muon_set_lr(PtcgMuon* m, float lr) {
     return PTCG_OK;
 }
 
+// the learning rate the update kernels read (device float), synchronous
+int pt_muon_lr(PtcgMuon* m, float* lr) {
+    PT_REQUIRE(m && lr, "muon_lr: null argument");
+    PT_HIP(hipMemcpy(lr, m->lr, 4, hipMemcpyDeviceToHost));
+    return PTCG_OK;
+}
+
 extern "C" float* ptcg_muon_momentum(PtcgMuon* m) { return m ? m->mom : nullptr; }
 
 int pt_muon_set_momentum(PtcgMuon* m, double momentum) {

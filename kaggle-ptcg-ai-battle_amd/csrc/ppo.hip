@@ -156,7 +156,9 @@ __global__ void ppo_reduce_kernel(const float* part, int blocks, float* stats, f
     }
 }
 
-// pufferlib.cu:1292-1302
+// pufferlib.cu:1292-1302: a threshold <= 0 disables its test, a non-finite
+// value fails it; skipped[0] counts every veto, skipped[1] the vetoes whose
+// value test failed (KL_GUARD_SKIPPED / KL_GUARD_SKIPPED_VF)
 __global__ void kl_gate_kernel(const float* guard, float kl_thr, float vf_thr, float* gate,
                                float* skipped) {
     const float kl = guard[0], vf = guard[1];
@@ -164,7 +166,10 @@ __global__ void kl_gate_kernel(const float* guard, float kl_thr, float vf_thr, f
     const bool vf_ok = (vf_thr <= 0.0f) || (isfinite(vf) && vf <= vf_thr);
     const float pass = (kl_ok && vf_ok) ? 1.0f : 0.0f;
     gate[0] = pass;
-    if (skipped) skipped[0] += 1.0f - pass;
+    if (skipped) {
+        skipped[0] += 1.0f - pass;
+        skipped[1] += vf_ok ? 0.0f : 1.0f;
+    }
 }
 
 }  // namespace

@@ -23,6 +23,18 @@ class CPtcgHypers(ctypes.Structure):
             "kl_skip_threshold", "vf_skip_threshold")]
 
 
+PERF_N = 9   # PTCG_PERF_N
+
+
+class CPtcgLog(ctypes.Structure):
+    """struct PtcgLog of include/ptcg_amd.h (ptcg_trainer_log)."""
+    _fields_ = [("loss", ctypes.c_float * 7)] + \
+        [(n, ctypes.c_float) for n in ("n", "kl_skipped", "vf_skipped", "gate", "grad_norm", "lr", "ent_coef",
+                                       "gpu_percent", "pad_")] + \
+        [("perf_s", ctypes.c_double * PERF_N), ("vram_used_gb", ctypes.c_double),
+         ("vram_total_gb", ctypes.c_double), ("global_step", ctypes.c_int64), ("epoch", ctypes.c_int64)]
+
+
 # name -> (restype, argtypes)
 _SIGS = {
     "ptcg_last_error": (ctypes.c_char_p, []),
@@ -77,10 +89,21 @@ _SIGS = {
     "ptcg_kl_gate": (ctypes.c_int, [c_void_p, ctypes.c_float, ctypes.c_float, c_void_p,
                                     c_void_p, c_void_p]),
     "ptcg_adam_workspace_floats": (ctypes.c_int64, []),
+    # lr is a device pointer: a double here, a float in the _lrf variant
     "ptcg_adam_step": (ctypes.c_int, [
         c_void_p, c_void_p, c_void_p, c_void_p, ctypes.c_int64,
         c_void_p, ctypes.c_double, ctypes.c_double, ctypes.c_double, ctypes.c_float,
         c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
+    "ptcg_adam_step_lrf": (ctypes.c_int, [
+        c_void_p, c_void_p, c_void_p, c_void_p, ctypes.c_int64,
+        c_void_p, ctypes.c_double, ctypes.c_double, ctypes.c_double, ctypes.c_float,
+        c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
+    # device memory
+    "ptcg_device_count": (ctypes.c_int, [ctypes.POINTER(ctypes.c_int)]),
+    "ptcg_device_alloc": (ctypes.c_int, [ctypes.c_int64, ctypes.POINTER(c_void_p)]),
+    "ptcg_device_free": (ctypes.c_int, [c_void_p]),
+    "ptcg_memcpy": (ctypes.c_int, [c_void_p, c_void_p, ctypes.c_int64, ctypes.c_int, c_void_p]),
+    "ptcg_device_synchronize": (ctypes.c_int, []),
     "ptcg_trainer_create": (ctypes.c_int, [ctypes.POINTER(CPtcgDims), ctypes.POINTER(CPtcgHypers),
                                            ctypes.c_int, ctypes.POINTER(c_void_p)]),
     "ptcg_trainer_free": (None, [c_void_p]),
@@ -100,7 +123,10 @@ _SIGS = {
     "ptcg_trainer_forward_backward": (ctypes.c_int, [c_void_p, c_void_p, c_void_p, c_void_p,
                                                      c_void_p, c_void_p, c_void_p, c_void_p,
                                                      c_void_p]),
-    "ptcg_trainer_losses": (ctypes.c_int, [c_void_p, c_float_p, ctypes.c_int]),
+    "ptcg_trainer_log": (ctypes.c_int, [c_void_p, ctypes.POINTER(CPtcgLog), ctypes.c_int]),
+    "ptcg_trainer_perf_mark": (ctypes.c_int, [c_void_p, ctypes.c_int, c_void_p]),
+    "ptcg_trainer_perf_commit": (ctypes.c_int, [c_void_p, ctypes.c_int]),
+    "ptcg_trainer_perf_add": (ctypes.c_int, [c_void_p, ctypes.c_int, ctypes.c_double]),
     "ptcg_trainer_buffers": (ctypes.c_int, [c_void_p, ctypes.POINTER(c_void_p),
                                             ctypes.POINTER(c_void_p), ctypes.POINTER(c_void_p),
                                             ctypes.POINTER(c_void_p)]),

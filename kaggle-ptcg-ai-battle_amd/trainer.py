@@ -23,18 +23,35 @@ from index lists; ``set_segment_rollout`` hands it what the reference's
 trainer holds after collection (total_agents segments of horizon steps:
 obs, actions, log-probs, rewards, terminals, values), and ``train`` then runs
 train_impl's minibatch loop (pufferlib.cu:1963-2160) on the device.
-Device memory for the rollout is plumbing held in torch tensors; every
-computation runs in libptcg_amd.so.
+The rollout's device buffers are allocated and owned through the library's
+C ABI (:mod:`devmem`), and every computation runs in libptcg_amd.so.
 """
 import ctypes
+import time
 
 import numpy as np
 
 from . import dims as dims_mod
-from .native import lib, check, fptr, CPtcgHypers, c_void_p, c_i32_p
+from . import devmem
+from .devmem import DeviceArray
+from .native import lib, check, fptr, CPtcgHypers, CPtcgLog, c_void_p, c_i32_p
 
-LOSS_KEYS = ("policy_loss", "value_loss", "entropy", "total_loss",
-             "old_approx_kl", "approx_kl", "clipfrac")
+# the loss sums of _C.log()["loss"] (bindings.cu:60-66), in the trainer's order
+LOSS_KEYS = ("policy", "value", "entropy", "total", "old_kl", "kl", "clipfrac")
+# _C.log()["perf"] phases: the reference's PROF_NAMES (pufferlib.cu:51-57),
+# then the four parts of train_forward (model forward, PPO loss, model
+# backward, gate + optimizer)
+PERF_NAMES = ("rollout", "eval_gpu", "eval_env", "train_misc", "train_forward",
+              "train_model_forward", "train_loss", "train_backward", "train_optimizer")
+
+
+def _ptr(x):
+    """Device address of a DeviceArray (or any object with data_ptr()), an
+    int address, or None."""
+    if x is None:
+        return None
+    return x if isinstance(x, int) else x.data_ptr()
+
 
 TRAIN_DEFAULTS = {
     "learning_rate": 3e-4, "beta1": 0.9, "beta2": 0.999, "eps": 1e-8,
@@ -104,10 +121,8 @@ class PuffeRL:
     """Handle returned by :func:`create_pufferl` (owns a PtcgTrainer)."""
 
     def __init__(self, dm, train, seed=0):
-        import torch
-        if not torch.cuda.is_available():
-            raise RuntimeError("CUDA is not available")
-        self._torch = torch
+        if devmem.device_count() < 1:
+            raise RuntimeError("no GPU device is available")
         self.dims = dm
         self._cdims = dm.as_ctypes()
         self._chyp, self.train_cfg = _hypers(train)
@@ -121,6 +136,9 @@ class PuffeRL:
         self.obs_size = lib().ptcg_obs_size(ctypes.byref(self._cdims))
         self.rollout = None
         self.epoch = 0
+        self.global_step = 0     # agent steps trained (the reference's global_step)
+        self._start_time = self._last_log_time = time.time()
+        self._last_log_step = 0
 
     # -------------------------------------------------- weights
     def set_weights(self, packed):
@@ -169,23 +187,19 @@ class PuffeRL:
     def rollout_step(self, obs, n, seed, step, idx=None, stream=None, buf=0):
         """Forward ``n`` device obs rows with inference activations (rollout
         policy ``buf``: its own activations, so policies may run on different
-        streams at once) and sample one action per row; returns device tensors
+        streams at once) and sample one action per row; returns device arrays
         (actions, logprobs, values)."""
-        t = self._torch
-        acts = t.empty(n, dtype=t.float32, device="cuda")
-        lps, vals = t.empty_like(acts), t.empty_like(acts)
-        check(lib().ptcg_trainer_rollout_on(self._h, buf, obs.data_ptr(), idx.data_ptr() if idx is not None else None,
-                                            n, seed, step, acts.data_ptr(), lps.data_ptr(), vals.data_ptr(), stream))
+        acts, lps, vals = DeviceArray(n), DeviceArray(n), DeviceArray(n)
+        check(lib().ptcg_trainer_rollout_on(self._h, buf, _ptr(obs), _ptr(idx), n, seed, step, acts.data_ptr(),
+                                            lps.data_ptr(), vals.data_ptr(), stream))
         return acts, lps, vals
 
     def capture_rollout(self, slot, obs, n, seed, step_dev, actions, logprobs, values, idx=None):
         """Capture slot `slot`: the rollout step over these device buffers,
         the draw's step read from the device uint64 counter step_dev and
         advanced by one per replay (sync-free mode)."""
-        check(lib().ptcg_trainer_capture_rollout(self._h, slot, obs.data_ptr(),
-                                                 idx.data_ptr() if idx is not None else None, n, seed,
-                                                 step_dev.data_ptr(), actions.data_ptr(), logprobs.data_ptr(),
-                                                 values.data_ptr()))
+        check(lib().ptcg_trainer_capture_rollout(self._h, slot, _ptr(obs), _ptr(idx), n, seed, _ptr(step_dev),
+                                                 _ptr(actions), _ptr(logprobs), _ptr(values)))
 
     def rollout_output(self):
         """Device pointer of the last rollout call's (n, n_opt+1) output."""
@@ -224,8 +238,8 @@ class PuffeRL:
 
     # -------------------------------------------------- device helpers
     def to_device(self, a, dtype=np.float32):
-        t = self._torch.from_numpy(np.ascontiguousarray(a, dtype=dtype))
-        return t.to("cuda")
+        """Host array -> DeviceArray (synchronous upload)."""
+        return DeviceArray.from_numpy(np.ascontiguousarray(a, dtype=dtype))
 
     def buffers(self):
         p = [c_void_p() for _ in range(4)]
@@ -235,29 +249,23 @@ class PuffeRL:
     def sync(self):
         check(lib().ptcg_trainer_sync(self._h))
 
+    @staticmethod
+    def _inputs(inp):
+        return [_ptr(inp[k]) for k in ("actions", "logprobs", "advantages", "returns", "values")]
+
     def forward_backward(self, obs, idx, inp, stream=None):
-        """One forward + PPO loss + backward on device tensors (no optimizer)."""
-        check(lib().ptcg_trainer_forward_backward(
-            self._h, obs.data_ptr(), idx.data_ptr() if idx is not None else None,
-            inp["actions"].data_ptr(), inp["logprobs"].data_ptr(),
-            inp["advantages"].data_ptr(), inp["returns"].data_ptr(),
-            inp["values"].data_ptr(), stream))
+        """One forward + PPO loss + backward on device arrays (no optimizer)."""
+        check(lib().ptcg_trainer_forward_backward(self._h, _ptr(obs), _ptr(idx), *self._inputs(inp), stream))
 
     def step(self, obs, idx, inp, stream=None):
-        """One full minibatch step on device tensors (with the optimizer)."""
-        check(lib().ptcg_trainer_step(
-            self._h, obs.data_ptr(), idx.data_ptr() if idx is not None else None,
-            inp["actions"].data_ptr(), inp["logprobs"].data_ptr(),
-            inp["advantages"].data_ptr(), inp["returns"].data_ptr(),
-            inp["values"].data_ptr(), stream))
+        """One full minibatch step on device arrays (with the optimizer).
+        ``idx`` is a device int32 array, an int device address, or None."""
+        check(lib().ptcg_trainer_step(self._h, _ptr(obs), _ptr(idx), *self._inputs(inp), stream))
 
     def capture_step(self, obs, idx, inp):
         """Capture one step over these device buffers into a HIP graph
         (sync-free mode); rewrite the buffers' contents, then replay_step."""
-        check(lib().ptcg_trainer_capture_step(
-            self._h, obs.data_ptr(), idx.data_ptr() if idx is not None else None,
-            inp["actions"].data_ptr(), inp["logprobs"].data_ptr(), inp["advantages"].data_ptr(),
-            inp["returns"].data_ptr(), inp["values"].data_ptr()))
+        check(lib().ptcg_trainer_capture_step(self._h, _ptr(obs), _ptr(idx), *self._inputs(inp)))
 
     def replay_step(self, stream=None):
         check(lib().ptcg_trainer_replay_step(self._h, stream))
@@ -334,7 +342,6 @@ def set_segment_rollout(pl, obs, actions, logprobs, rewards, dones, values, hori
     train_impl :1863-1883); "BT": already in the train layout (row b*T + t).
     Rewards are clamped to [-1, 1] and the importance ratios set to 1, as
     train_impl does before its minibatch loop (:1889-1895)."""
-    torch = pl._torch
     L = lib()
     T = int(horizon)
     obs = np.ascontiguousarray(obs, dtype=np.float32)
@@ -346,13 +353,13 @@ def set_segment_rollout(pl, obs, actions, logprobs, rewards, dones, values, hori
         raise ValueError(f"layout must be 'BT' or 'TB', got {layout!r}")
     if S > L.ptcg_prio_replay_max_segments():
         raise RuntimeError(f"segment rollout: {S} segments exceed {L.ptcg_prio_replay_max_segments()}")
-    dev = lambda a, dt=torch.float32: torch.empty(a, dtype=dt, device="cuda")
+    dev = lambda a, dt=np.float32: DeviceArray(a, dt)
 
     def train_layout(a, width, clamp=0):
         a = np.ascontiguousarray(a, dtype=np.float32).reshape(-1)
         if a.size != n * width:
             raise RuntimeError(f"segment rollout: array of {a.size} floats, expected {n * width}")
-        src = torch.from_numpy(a).to("cuda")
+        src = DeviceArray.from_numpy(a)
         if layout == "BT" and not clamp:
             return src
         out = dev(n * width)
@@ -366,9 +373,8 @@ def set_segment_rollout(pl, obs, actions, logprobs, rewards, dones, values, hori
              logprobs=train_layout(logprobs, 1), rewards=train_layout(rewards, 1, clamp=1),
              dones=train_layout(dones, 1), values=train_layout(values, 1).clone(), ratio=dev(n),
              advantages=dev(n), returns=dev(n), probs=dev(S), cdf=dev(S), row_prio=dev(n),
-             idx=dev(max(S, pl.minibatch // T), torch.int32), mb_prio=dev(max(S, pl.minibatch // T)),
-             row_idx=dev(pl.minibatch, torch.int32),
-             rng_offset=torch.zeros(1, dtype=torch.int64, device="cuda"), n=n, horizon=T, segments=S)
+             idx=dev(max(S, pl.minibatch // T), np.int32), mb_prio=dev(max(S, pl.minibatch // T)),
+             row_idx=dev(pl.minibatch, np.int32), rng_offset=dev(1, np.int64), n=n, horizon=T, segments=S)
     check(L.ptcg_fill(r["ratio"].data_ptr(), n, 1.0, None))
     pl.rollout = r
 
@@ -391,9 +397,12 @@ def _train_segments(pl):
     seat = pl.dims.seat_col()
     P = lambda k: r[k].data_ptr()
     _, _, ratio_buf, nv_buf = pl.buffers()
+    check(L.ptcg_trainer_perf_mark(pl._h, 0, None))
     pl.write_schedule(*epoch_schedule(cfg, pl.epoch))
+    check(L.ptcg_trainer_perf_mark(pl._h, 1, None))
     try:
         for _ in range(total_mb):
+            check(L.ptcg_trainer_perf_mark(pl._h, 2, None))
             check(L.ptcg_negamax_advantage(P("values"), P("rewards"), P("dones"), P("ratio"), P("obs"),
                                            pl.obs_size, seat, P("advantages"), P("returns"),
                                            cfg["gamma"], cfg["gae_lambda"], cfg["vtrace_rho_clip"],
@@ -407,8 +416,10 @@ def _train_segments(pl):
             check(L.ptcg_index_copy(P("values"), P("idx"), nv_buf, mb_segs, T, S, None))
     finally:
         check(L.ptcg_trainer_set_prio(pl._h, None))
+    check(L.ptcg_trainer_perf_commit(pl._h, total_mb))
     pl.epoch += 1
-    return log(pl)
+    pl.global_step += r["n"]
+    return {}
 
 
 def train(pl, index_lists=None):
@@ -416,8 +427,9 @@ def train(pl, index_lists=None):
     (:func:`set_segment_rollout`) runs the reference's prioritized minibatch
     loop; a row rollout (:func:`set_rollout`) runs update_epochs epochs, each
     a fresh seeded permutation cut into minibatches (at most
-    minibatches_per_epoch of them), or the given index lists.  Returns the
-    loss dictionary of :func:`log`."""
+    minibatches_per_epoch of them), or the given index lists.  Returns an
+    empty dict, as the reference's ``_C.train`` (bindings.cu:184-192): the
+    losses accumulate on the device until :func:`log` reads them."""
     if pl.rollout is None:
         raise RuntimeError("train: no rollout set (call set_rollout)")
     if "horizon" in pl.rollout:
@@ -425,20 +437,30 @@ def train(pl, index_lists=None):
             raise RuntimeError("train: index lists apply to row rollouts, not segment rollouts")
         return _train_segments(pl)
     from .synth import minibatch_indices
+    L = lib()
     r = pl.rollout
     B = pl.minibatch
+    check(L.ptcg_trainer_perf_mark(pl._h, 0, None))
     pl.write_schedule(*epoch_schedule(pl.train_cfg, pl.epoch))
     if index_lists is None:
         ep = int(pl.train_cfg["update_epochs"])
         per = min(int(pl.train_cfg["minibatches_per_epoch"]), r["n"] // B)
         index_lists = minibatch_indices(r["n"], B, ep * per, pl.seed + pl.epoch, epochs=ep)
-    for idx in index_lists:
-        idx = np.asarray(idx, dtype=np.int32)
-        if idx.size != B:
-            raise RuntimeError(f"minibatch index list has {idx.size} rows, trainer minibatch is {B}")
-        pl.step(r["obs"], pl.to_device(idx, np.int32), r)
+    lists = [np.asarray(ix, dtype=np.int32) for ix in index_lists]
+    for ix in lists:
+        if ix.size != B:
+            raise RuntimeError(f"minibatch index list has {ix.size} rows, trainer minibatch is {B}")
+    # every minibatch's indices in one upload; step i reads slice i
+    d_idx = DeviceArray.from_numpy(np.concatenate(lists)) if lists else None
+    check(L.ptcg_trainer_perf_mark(pl._h, 1, None))
+    for i in range(len(lists)):
+        check(L.ptcg_trainer_perf_mark(pl._h, 2, None))
+        pl.step(r["obs"], d_idx.data_ptr() + i * B * 4, r)
+    check(L.ptcg_trainer_perf_commit(pl._h, len(lists)))   # synchronous: the steps are done
+    del d_idx
     pl.epoch += 1
-    return log(pl)
+    pl.global_step += r["n"]
+    return {}
 
 
 def debug_forward(pl, rows):
@@ -476,15 +498,69 @@ def load_state(pl, path):
         pl.global_step, pl.epoch = gs.value, ep.value
 
 
+def _rss_gb():
+    """Resident set size of this process in GiB (/proc/self/status VmRSS,
+    as bindings.cu:104-113 reads it), 0 where unavailable."""
+    try:
+        with open("/proc/self/status") as f:
+            for line in f:
+                if line.startswith("VmRSS:"):
+                    return float(line.split()[1]) / (1024.0 * 1024.0)
+    except OSError:
+        pass
+    return 0.0
+
+
 def log(pl, reset=True):
-    out = np.zeros(10, np.float32)
-    check(lib().ptcg_trainer_losses(pl._h, fptr(out), 1 if reset else 0))
-    cnt = max(float(out[7]), 1.0)
-    d = {k: float(out[i]) / cnt for i, k in enumerate(LOSS_KEYS)}
-    d["minibatches"] = int(out[7])
-    d["guard_skipped"] = int(out[8])
-    d["grad_norm"] = float(out[9])
-    return d
+    """The reference's ``_C.log(pl)`` (bindings.cu:15-118): SPS and
+    agent_steps over the agent steps trained since the last log, uptime,
+    epoch, the APPLIED learning rate read back from the device scalar the
+    optimizer reads, ``env`` (empty: the environment is not part of this
+    path), ``loss`` (the means of policy / value / entropy / total / old_kl /
+    kl / clipfrac over the minibatches since the last log, and the gate's
+    kl_skipped / vf_skipped counters; empty when no minibatch ran), ``perf``
+    (seconds per phase from HIP events, the reference's keys plus the step's
+    four parts; ``train`` = train_misc + train_forward) and ``util`` (GPU
+    busy percent from amdgpu's sysfs, device memory in use, host RSS).
+    Beyond the reference's keys: ``minibatches``, ``grad_norm`` (last step's
+    norm before the clip), ``gate`` and ``ent_coef``.  ``reset`` clears the
+    loss sums, the skip counters and the phase times, as the reference's
+    log does."""
+    st = CPtcgLog()
+    check(lib().ptcg_trainer_set_counters(pl._h, int(pl.global_step), int(pl.epoch)))
+    check(lib().ptcg_trainer_log(pl._h, ctypes.byref(st), 1 if reset else 0))
+    return log_dict(pl, st, time.time(), reset)
+
+
+def log_dict(pl, st, now, reset=True):
+    """:func:`log`'s dictionary from a filled PtcgLog ``st`` (host-only)."""
+    dt = now - pl._last_log_time
+    sps = int((pl.global_step - pl._last_log_step) / dt) if dt > 0 else 0
+    if reset:
+        pl._last_log_time, pl._last_log_step = now, pl.global_step
+    out = {"SPS": sps, "agent_steps": int(pl.global_step), "uptime": now - pl._start_time,
+           "epoch": int(pl.epoch), "lr": float(st.lr), "env": {}}
+    loss = {}
+    n = float(st.n)
+    if n > 0:
+        inv = np.float32(1.0) / np.float32(n)      # the reference scales by 1/n in fp32
+        for i, k in enumerate(LOSS_KEYS):
+            loss[k] = float(np.float32(st.loss[i]) * inv)
+        loss["kl_skipped"] = float(st.kl_skipped)
+        loss["vf_skipped"] = float(st.vf_skipped)
+    out["loss"] = loss
+    perf = {k: float(st.perf_s[i]) for i, k in enumerate(PERF_NAMES)}
+    perf["train"] = perf["train_misc"] + perf["train_forward"]
+    out["perf"] = perf
+    tot = float(st.vram_total_gb)
+    out["util"] = {"gpu_percent": float(st.gpu_percent),
+                   "gpu_mem": 100.0 * float(st.vram_used_gb) / tot if tot > 0 else 0.0,
+                   "vram_used_gb": float(st.vram_used_gb), "vram_total_gb": tot, "cpu_mem_gb": _rss_gb()}
+    out["minibatches"] = int(n)
+    out["grad_norm"] = float(st.grad_norm)
+    out["gate"] = float(st.gate)
+    out["ent_coef"] = float(st.ent_coef)
+    return out
 
 
 def close(pl):

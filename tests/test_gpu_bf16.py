@@ -112,7 +112,7 @@ def test_bf16_rollout_tracks_fp32(cuda):
             d = pl.to_device(rows)
             a, lp, v = pl.rollout_step(d, n, seed=5, step=9)
             torch.cuda.synchronize()
-            res[prec] = (a.cpu().numpy(), lp.cpu().numpy(), v.cpu().numpy())
+            res[prec] = (a.numpy(), lp.numpy(), v.numpy())
         finally:
             pl.close()
     a0, l0, v0 = res["fp32"]

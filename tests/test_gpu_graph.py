@@ -43,8 +43,8 @@ def test_graph_replays_match_eager_steps(dm, opt, cuda):
             eager.step(eager.rollout["obs"], eager.to_device(ix, np.int32), eager.rollout)
             torch.cuda.synchronize()
             # eager work and host synchronisation between replays
-            lg_e, lg_g = trainer.log(eager), trainer.log(graph)
-            for k in ("policy_loss", "value_loss", "entropy", "total_loss"):
+            lg_e, lg_g = trainer.log(eager)["loss"], trainer.log(graph)["loss"]
+            for k in ("policy", "value", "entropy", "total"):
                 assert lg_g[k] == lg_e[k], (i, k, lg_g[k], lg_e[k])
             w_e, w_g = eager.get_weights(), graph.get_weights()
             assert np.array_equal(w_g, w_e), (i, rel_l2(w_g, w_e))
@@ -126,9 +126,9 @@ def test_rollout_graph_slots_match_eager(sampler, cuda):
                 # eager work between replays: the same draw, launched call by call
                 a, lp, v = pl.rollout_step(d_obs[k], n, seed=1234, step=expect_step)
                 torch.cuda.synchronize()
-                assert np.array_equal(got[0], a.cpu().numpy()), (rep, k)
-                assert np.array_equal(got[1], lp.cpu().numpy()), (rep, k)
-                assert np.array_equal(got[2], v.cpu().numpy()), (rep, k)
+                assert np.array_equal(got[0], a.numpy()), (rep, k)
+                assert np.array_equal(got[1], lp.numpy()), (rep, k)
+                assert np.array_equal(got[2], v.numpy()), (rep, k)
                 expect_step += 1
                 assert int(step.item()) == expect_step
     finally:
@@ -164,8 +164,8 @@ def test_captured_step_follows_lr_and_ent_coef(opt, cuda):
             graph.replay_step()
             eager.step(eager.rollout["obs"], eager.to_device(np.asarray(ix, np.int32), np.int32), eager.rollout)
             torch.cuda.synchronize()
-            lg_e, lg_g = trainer.log(eager), trainer.log(graph)
-            for k in ("entropy", "total_loss"):
+            lg_e, lg_g = trainer.log(eager)["loss"], trainer.log(graph)["loss"]
+            for k in ("entropy", "total"):
                 assert lg_g[k] == lg_e[k], (i, k, lg_g[k], lg_e[k])
             w_e, w_g = eager.get_weights(), graph.get_weights()
             assert np.array_equal(w_g, w_e), (i, rel_l2(w_g, w_e))

@@ -113,8 +113,8 @@ def test_config5_rollout_8192(prec, cuda):
         acts, lps, vals = pl.rollout_step(pl.to_device(rows), n, seed=seed, step=step)
         torch.cuda.synchronize()
         dec = d2h(pl.rollout_output(), (n, dm.n_opt + 1))
-        acts = acts.cpu().numpy().astype(np.int64)
-        lps, vals = lps.cpu().numpy(), vals.cpu().numpy()
+        acts = acts.numpy().astype(np.int64)
+        lps, vals = lps.numpy(), vals.numpy()
     finally:
         pl.close()
     m0, m1 = dm.offsets()["opt_mask"]

@@ -295,6 +295,13 @@ def test_gemm_dx_layernorm_bwd_rejects_other_shapes(cuda):
     with pytest.raises(RuntimeError, match="layernorm bwd"):
         native.check(L.ptcg_kernel_gemm_dx_layernorm_bwd(8, 100, P(a), P(wt), P(x), P(v), P(st), P(st), None,
                                                          P(gx), None, P(v), P(v), P(ws), ws.numel(), None, None))
+    # a shape that fits, with a null dY or a null W^T: rejected on the host
+    a2, wt2 = torch.zeros(8, 128, dtype=torch.bfloat16, device="cuda"), torch.zeros(256, 128, dtype=torch.bfloat16,
+                                                                                    device="cuda")
+    for pa, pw in ((None, P(wt2)), (P(a2), None)):
+        with pytest.raises(RuntimeError, match="null buffer"):
+            native.check(L.ptcg_kernel_gemm_dx_layernorm_bwd(8, 128, pa, pw, P(x), P(v), P(st), P(st), None,
+                                                             P(gx), None, P(v), P(v), P(ws), ws.numel(), None, None))
 
 
 def test_gemm_resid_ln_rejects_other_shapes(cuda):
@@ -517,12 +524,14 @@ def test_kl_gate(cuda):
     for kl, vf, kt, vt, want in [(0.01, 0.1, 0.05, 0.5, 1.0), (0.06, 0.1, 0.05, 0.5, 0.0),
                                  (float("nan"), 0.1, 0.05, 0.5, 0.0), (float("nan"), 0.1, 0.0, 0.5, 1.0),
                                  (0.01, float("inf"), 0.05, 0.5, 0.0), (0.01, 0.7, 0.05, 0.0, 1.0)]:
-        g, sk = empty(1), empty(1)
+        g, sk = empty(1), empty(2)
         gd = dev(np.array([kl, vf], np.float32))
         native.check(L.ptcg_kl_gate(P(gd), kt, vt, P(g), P(sk), None))
         torch.cuda.synchronize()
         assert g.item() == want == oppo.kl_gate(kl, vf, kt, vt)
-        assert sk.item() == 1.0 - want
+        # every veto, then the vetoes whose value test failed (KL test off)
+        assert sk[0].item() == 1.0 - want
+        assert sk[1].item() == 1.0 - oppo.kl_gate(kl, vf, 0.0, vt)
 
 
 def lr_dev(lr):

@@ -141,8 +141,16 @@ def test_adam_steps_match_oracle(dm, B, steps, cuda):
     opt = oadam.OracleAdam([p for _, p in ref.named_blob_params()], lr=3e-4)
     ostep.run_update(ref, opt, rows, inp, idx_lists, dict(HYP))
     trainer.set_rollout(pl, rows, **inp)
-    lg = trainer.train(pl, index_lists=idx_lists)
+    assert trainer.train(pl, index_lists=idx_lists) == {}      # _C.train returns an empty dict
+    lg = trainer.log(pl)
     assert lg["minibatches"] == steps and pl.step_count() == steps
+    assert lg["agent_steps"] == R and lg["epoch"] == 1
+    assert abs(lg["lr"] - 3e-4) <= 3e-4 * 1e-6      # read back from the device scalar
+    assert lg["perf"]["train_forward"] > 0 and lg["perf"]["train"] >= lg["perf"]["train_forward"]
+    parts = sum(lg["perf"][k] for k in ("train_model_forward", "train_loss", "train_backward", "train_optimizer"))
+    assert abs(parts - lg["perf"]["train_forward"]) <= 1e-6 + 1e-4 * lg["perf"]["train_forward"]
+    assert lg["util"]["vram_used_gb"] > 0 and lg["loss"]["kl_skipped"] == lg["loss"]["vf_skipped"] == 0
+    assert trainer.log(pl)["loss"] == {}     # the sums were reset by the previous log
     w_gpu, w_ref = pl.get_weights(), ref.to_blob()
     assert rel_l2(w_gpu, w_ref) < 1e-4, rel_l2(w_gpu, w_ref)
     upd_err = rel_l2(w_gpu - w0, w_ref - w0)
@@ -198,11 +206,26 @@ def test_gate_vetoes_step(cuda):
     # synthetic old log-probs are far from the policy's -> approx KL >> 1e-6
     pl.set_hypers(kl_skip_threshold=1e-6)
     trainer.set_rollout(pl, rows, **inp)
-    lg = trainer.train(pl, index_lists=[np.arange(B, dtype=np.int32)])
-    assert lg["guard_skipped"] == 1 and pl.step_count() == 0
+    trainer.train(pl, index_lists=[np.arange(B, dtype=np.int32)])
+    lg = trainer.log(pl)
+    # a KL veto: kl_skipped counts it, vf_skipped does not (pufferlib.cu:1300-1301)
+    assert lg["loss"]["kl_skipped"] == 1 and lg["loss"]["vf_skipped"] == 0 and pl.step_count() == 0
+    assert lg["gate"] == 0.0
     assert np.array_equal(pl.get_weights().view(np.uint32), w0.view(np.uint32))
     m, v = pl.get_moments()
     assert not m.any() and not v.any()
+    # a value-loss veto (KL test off): both counters count it; the counters
+    # were reset by the log above, the gate keeps its last value until a step
+    pl.set_hypers(kl_skip_threshold=0.0, vf_skip_threshold=1e-9)
+    trainer.train(pl, index_lists=[np.arange(B, dtype=np.int32)] * 2)
+    lg = trainer.log(pl)
+    assert lg["loss"]["kl_skipped"] == 2 and lg["loss"]["vf_skipped"] == 2 and pl.step_count() == 0
+    # both tests pass: the step applies and no counter moves
+    pl.set_hypers(kl_skip_threshold=1e9, vf_skip_threshold=1e9)
+    trainer.train(pl, index_lists=[np.arange(B, dtype=np.int32)])
+    lg = trainer.log(pl)
+    assert lg["loss"]["kl_skipped"] == 0 and lg["loss"]["vf_skipped"] == 0 and pl.step_count() == 1
+    assert lg["gate"] == 1.0
     pl.close()
 
 

@@ -177,11 +177,12 @@ def test_segment_training_loop_matches_oracle(layout, cuda):
             return np.swapaxes(a, 0, 1).copy() if layout == "TB" else a
         trainer.set_segment_rollout(pl, lay(obs), lay(inp["actions"]), lay(inp["logprobs"]), lay(rewards),
                                     lay(dones), lay(inp["values"]), T, layout=layout)
-        lg = trainer.train(pl)
+        trainer.train(pl)
+        lg = trainer.log(pl)
         w_gpu = pl.get_weights()
         r = pl.rollout
-        vals, ratio, off = r["values"].cpu().numpy(), r["ratio"].cpu().numpy(), int(r["rng_offset"].item())
-        last_idx = r["idx"].cpu().numpy()[:B // T]
+        vals, ratio, off = r["values"].numpy(), r["ratio"].numpy(), int(r["rng_offset"].item())
+        last_idx = r["idx"].numpy()[:B // T]
     finally:
         pl.close()
 
@@ -190,7 +191,8 @@ def test_segment_training_loop_matches_oracle(layout, cuda):
                              dict(HYP), seed, n_minibatches=4, seat_col=dm.seat_col())
     assert off == res["offset"] == 4 * (B // T)
     assert np.array_equal(last_idx, res["draws"][-1]["idx"])
-    assert lg["minibatches"] == 4
+    assert lg["minibatches"] == 4 and lg["agent_steps"] == n and lg["epoch"] == 1
+    assert lg["perf"]["train_misc"] > 0 and lg["perf"]["train_forward"] > 0
     assert rel_l2(w_gpu, ref.to_blob()) < 1e-4
     assert np.abs(vals - res["values"].reshape(-1)).max() <= 1e-4 * max(1.0, float(np.abs(res["values"]).max()))
     assert np.abs(ratio - res["ratio"].reshape(-1)).max() <= 1e-4

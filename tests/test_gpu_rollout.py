@@ -105,11 +105,11 @@ def test_rollout_forward_and_sampling(dm, B, cuda):
     acts, lps, vals = pl.rollout_step(d_rows, B, seed=4, step=11)
     torch.cuda.synchronize()
     out = ref(torch.from_numpy(rows)).detach().numpy()
-    assert rel_l2(vals.cpu().numpy(), out[:, -1]) < 1e-5
+    assert rel_l2(vals.numpy(), out[:, -1]) < 1e-5
     m0, m1 = dm.offsets()["opt_mask"]
     mask = rows[:, m0:m1]
     r_acts, r_lps, _, r_us = osamp.sample(out, mask, 4, 11)
-    diff = acts.cpu().numpy().astype(np.int64) != r_acts
+    diff = acts.numpy().astype(np.int64) != r_acts
     if diff.any():   # GPU logits differ from the oracle's at 1e-6: only boundary rows may flip
         assert np.all(osamp.boundary_margin(out, mask, r_us)[diff] < 1e-4)
     assert diff.sum() <= 1
@@ -117,7 +117,7 @@ def test_rollout_forward_and_sampling(dm, B, cuda):
     perm = np.random.default_rng(1).permutation(B).astype(np.int32)
     acts2, _, vals2 = pl.rollout_step(d_rows, B, seed=4, step=11, idx=pl.to_device(perm, np.int32))
     torch.cuda.synchronize()
-    assert rel_l2(vals2.cpu().numpy(), out[perm, -1]) < 1e-5
+    assert rel_l2(vals2.numpy(), out[perm, -1]) < 1e-5
     # training still works after a rollout on the same weights
     inp = synth.make_ppo_inputs(dm, rows[:8], seed=23)
     trainer.set_rollout(pl, rows[:8], **inp)

@@ -35,11 +35,11 @@ def _run(dm, B, blob, rows, inp, lists, skip, sync_free=False):
         # rollout and debug forward on the initial weights, then the update
         fwd = trainer.debug_forward(pl, rows[:B])
         acts, lps, vals = pl.rollout_step(pl.to_device(rows), rows.shape[0], seed=91, step=5)
-        torch.cuda.synchronize()
         trainer.set_rollout(pl, rows, **inp)
-        losses = trainer.train(pl, index_lists=lists)
+        trainer.train(pl, index_lists=lists)
+        losses = trainer.log(pl)["loss"]
         w = pl.get_weights()
-        return losses, w, fwd, acts.cpu().numpy(), lps.cpu().numpy(), vals.cpu().numpy()
+        return losses, w, fwd, acts.numpy(), lps.numpy(), vals.numpy()
     finally:
         pl.close()
 
@@ -60,7 +60,7 @@ def test_skip_masked_matches_full_scorer(dm, sync_free, cuda):
     # bound allows a few and the per-element bound caps each
     assert rel_l2(w1, w0) < 1e-4
     assert np.abs(w1 - w0).max() <= 2 * 1e-3 * len(lists) + 1e-6
-    for k in ("policy_loss", "value_loss", "entropy", "total_loss"):
+    for k in ("policy", "value", "entropy", "total"):
         assert abs(l1[k] - l0[k]) <= 1e-5 * max(1.0, abs(l0[k])), k
     # debug_forward scores every slot in both modes
     assert np.abs(f1 - f0).max() <= 1e-5 * max(1.0, float(np.abs(f0).max()))

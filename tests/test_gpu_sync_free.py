@@ -29,7 +29,7 @@ def _run(dm, B, blob, rows, inp, lists, sync_free):
         obs = pl.to_device(rows)
         acts, lps, vals = pl.rollout_step(obs, rows.shape[0], seed=77, step=3)
         torch.cuda.synchronize()
-        return fwd0, w, acts.cpu().numpy(), lps.cpu().numpy(), vals.cpu().numpy()
+        return fwd0, w, acts.numpy(), lps.numpy(), vals.numpy()
     finally:
         pl.close()
 

@@ -54,9 +54,9 @@ def test_transport_round_trip_matches_eager(cuda):
                 d_rows = pl.to_device(rows)
                 a, l, v = pl.rollout_step(d_rows, apb, seed=555, step=expect)
                 torch.cuda.synchronize()
-                assert np.array_equal(got, a.cpu().numpy()), (t, b)
-                assert np.array_equal(lp, l.cpu().numpy()), (t, b)
-                assert np.array_equal(vals, v.cpu().numpy()), (t, b)
+                assert np.array_equal(got, a.numpy()), (t, b)
+                assert np.array_equal(lp, l.numpy()), (t, b)
+                assert np.array_equal(vals, v.numpy()), (t, b)
                 expect += 1
                 assert int(step.item()) == expect
     finally:
@@ -135,9 +135,9 @@ def test_transport_buffers_overlap(cuda):
                 sl = x.slice(b)
                 a, l, v = pl.rollout_step(pl.to_device(rows[b]), apb, seed=777, step=20 + b + t, buf=nbuf)
                 torch.cuda.synchronize()
-                assert np.array_equal(x.actions[sl, 0], a.cpu().numpy()), (t, b)
-                assert np.array_equal(lp_all[sl], l.cpu().numpy()), (t, b)
-                assert np.array_equal(v_all[sl], v.cpu().numpy()), (t, b)
+                assert np.array_equal(x.actions[sl, 0], a.numpy()), (t, b)
+                assert np.array_equal(lp_all[sl], l.numpy()), (t, b)
+                assert np.array_equal(v_all[sl], v.numpy()), (t, b)
                 assert int(steps[b].item()) == 20 + b + t + 1
     finally:
         x.close()

@@ -285,16 +285,19 @@ def main():
               "(the data-parallel path is designed but not built)", file=sys.stderr)
         sys.exit(2)
 
-    import torch
+    import __graft_entry__
+    __graft_entry__.load_package()
+    from ptcg_amd import dims, synth, trainer, native, devmem
     if args.copy_calibration:
         # a plain copy of known size: rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE of
         # this run give the counters' scale (bytes read / written per KiB counted)
         n = 64 << 20
-        x = torch.ones(n, device="cuda")
-        y = torch.empty(n, device="cuda")
+        x = devmem.DeviceArray(n)
+        native.check(native.lib().ptcg_fill(x.data_ptr(), n, 1.0, None))
+        y = devmem.DeviceArray(n)
         for _ in range(3):
             y.copy_(x)
-        torch.cuda.synchronize()
+        devmem.synchronize()
         print(json.dumps({"copy_bytes": n * 4, "copies": 3}), flush=True)
         return
     if args.copy_rate:
@@ -303,25 +306,22 @@ def main():
         out = {}
         for mb in (38.3, 60.5, 256.0):
             n = int(mb * 1e6) // 4
-            x = torch.ones(n, device="cuda")
-            y = torch.empty(n, device="cuda")
+            x = devmem.DeviceArray(n)
+            native.check(native.lib().ptcg_fill(x.data_ptr(), n, 1.0, None))
+            y = devmem.DeviceArray(n)
             for _ in range(5):
                 y.copy_(x)
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0, e1 = devmem.Event(), devmem.Event()
             ts = []
             for _ in range(20):
                 e0.record()
                 y.copy_(x)
                 e1.record()
-                e1.synchronize()
-                ts.append(e0.elapsed_time(e1))
+                ts.append(e0.elapsed_ms(e1))
             ms = sorted(ts)[len(ts) // 2]
             out[f"{mb:g}MB"] = dict(median_us=round(ms * 1e3, 2), gbs=round(2 * n * 4 / (ms / 1e3) / 1e9, 1))
         print(json.dumps({"copy_rate": out}), flush=True)
         return
-    import __graft_entry__
-    __graft_entry__.load_package()
-    from ptcg_amd import dims, synth, trainer, native
 
     if args.workload == "rollout":
         return bench_rollout(args)
@@ -352,7 +352,7 @@ def main():
 
     for i in range(args.warmup):
         pl.step(r["obs"], d_lists[i], r)
-    torch.cuda.synchronize()
+    devmem.synchronize()
     L = native.lib()
     K = args.steps
     sec_graph = None
@@ -360,15 +360,15 @@ def main():
         # timed region 1 (`value`): the step captured once in a HIP graph over a
         # fixed index buffer, refreshed and replayed per minibatch -- the
         # reference trainer's launch mode (pufferlib.cu:2019-2140)
-        idx_buf = torch.empty(B, dtype=torch.int32, device="cuda")
+        idx_buf = devmem.DeviceArray(B, np.int32)
         idx_buf.copy_(d_lists[0])
-        torch.cuda.synchronize()
+        devmem.synchronize()
         pl.capture_step(r["obs"], idx_buf, r)
         t0 = time.perf_counter()
         for i in range(args.warmup, n_lists):
             idx_buf.copy_(d_lists[i])
             pl.replay_step()
-        torch.cuda.synchronize()
+        devmem.synchronize()
         sec_graph = time.perf_counter() - t0
     # timed region 2 (the only one with --stream): the same number of
     # minibatches launched kernel by kernel, a HIP event pair on the launch
@@ -388,13 +388,13 @@ def main():
         t0 = time.perf_counter()
         for i in range(args.warmup, n_lists):
             pl.step(r["obs"], d_lists[i], r)
-        torch.cuda.synchronize()
+        devmem.synchronize()
         sec_plain = time.perf_counter() - t0
     native.check(L.ptcg_profile_begin(256 * args.steps))
     t0 = time.perf_counter()
     for i in range(args.warmup, n_lists):
         pl.step(r["obs"], d_lists[i], r)
-    torch.cuda.synchronize()
+    devmem.synchronize()
     t1 = time.perf_counter()
     ms, launches, exec_flops = ctypes.c_double(), ctypes.c_int(), ctypes.c_double()
     native.check(L.ptcg_profile_end(ctypes.byref(ms), ctypes.byref(launches), ctypes.byref(exec_flops)))
@@ -513,8 +513,7 @@ def main():
 def bench_rollout(args):
     """Rollout step: inference forward of n rows (one block's activations
     reused across layers) + one sampled action per row (counter RNG)."""
-    import torch
-    from ptcg_amd import dims, synth, trainer, native
+    from ptcg_amd import dims, synth, trainer, native, devmem
     dm = dims.CORE
     n = args.rollout_rows
     obs = synth.make_obs(dm, n, seed=1)
@@ -526,7 +525,7 @@ def bench_rollout(args):
     d_obs = pl.to_device(obs)
     for i in range(args.warmup):
         pl.rollout_step(d_obs, n, seed=0, step=i)
-    torch.cuda.synchronize()
+    devmem.synchronize()
     L = native.lib()
     K = args.steps
     sec_graph = None
@@ -534,15 +533,15 @@ def bench_rollout(args):
         # timed region 1 (`value`): the rollout step captured once (a slot of
         # the reference's per-(t, buf) graphs) and replayed, the draw's step
         # advancing in a device counter
-        outs = [torch.empty(n, device="cuda") for _ in range(3)]
-        step_dev = torch.tensor([args.warmup], dtype=torch.int64, device="cuda")
+        outs = [devmem.DeviceArray(n) for _ in range(3)]
+        step_dev = devmem.DeviceArray.from_numpy(np.array([args.warmup], np.int64))
         pl.capture_rollout(0, d_obs, n, 0, step_dev, *outs)
         t0 = time.perf_counter()
         for i in range(args.steps):
             pl.replay_rollout(0)
-        torch.cuda.synchronize()
+        devmem.synchronize()
         sec_graph = time.perf_counter() - t0
-        if not torch.isfinite(outs[1]).all():
+        if not np.isfinite(outs[1].numpy()).all():
             raise RuntimeError("non-finite log-probabilities in the rollout benchmark")
         transport = bench_transport(pl, dm, obs, n, args)
         native.check(L.ptcg_trainer_set_sync_free(pl._h, 0))   # exact launch sizes for the timing pass
@@ -551,11 +550,11 @@ def bench_rollout(args):
     t0 = time.perf_counter()
     for i in range(args.steps):
         acts, lps, vals = pl.rollout_step(d_obs, n, seed=0, step=args.warmup + i)
-    torch.cuda.synchronize()
+    devmem.synchronize()
     t1 = time.perf_counter()
     ms, launches, exec_flops = ctypes.c_double(), ctypes.c_int(), ctypes.c_double()
     native.check(L.ptcg_profile_end(ctypes.byref(ms), ctypes.byref(launches), ctypes.byref(exec_flops)))
-    if not torch.isfinite(lps).all():
+    if not np.isfinite(lps.numpy()).all():
         raise RuntimeError("non-finite log-probabilities in the rollout benchmark")
     sec_stream = t1 - t0
     sec = sec_graph if graph else sec_stream
@@ -599,13 +598,12 @@ def bench_transport(pl, dm, obs, n, args):
     each buffer's checked stream sync is followed by the async H2D of its
     observations, rewards and terminals, which overlaps the other buffer's
     work.  Not `value`: the observations cross PCIe here."""
-    import torch
-    from ptcg_amd import transport as tr
+    from ptcg_amd import transport as tr, devmem
     nbuf = 2
     x = tr.RolloutTransport(n, nbuf, dm.obs_size)
     try:
         x.observations[:] = obs
-        step_dev = [torch.zeros(1, dtype=torch.int64, device="cuda") for _ in range(nbuf)]
+        step_dev = [devmem.DeviceArray(1, np.int64) for _ in range(nbuf)]
         for b in range(nbuf):
             x.capture_rollout(pl, b, 1 + b, 0, step_dev[b])   # slots 1, 2
         for b in range(nbuf):
@@ -620,11 +618,11 @@ def bench_transport(pl, dm, obs, n, args):
 
         for _ in range(2):   # warm the slots
             step()
-        torch.cuda.synchronize()
+        devmem.synchronize()
         t0 = time.perf_counter()
         for _ in range(args.steps):
             step()
-        torch.cuda.synchronize()
+        devmem.synchronize()
         sec = time.perf_counter() - t0
         if not np.isfinite(x.actions).all():
             raise RuntimeError("non-finite actions in the transport benchmark")
@@ -646,26 +644,33 @@ def bench_replay(args):
     prioritized draw of 16 segments (weights, row indices); per epoch the
     transposes of the rollout into the train layout (obs rows of the CORE
     dims and the six per-step arrays).  Synthetic device data."""
-    import torch
-    from ptcg_amd import dims, native
+    from ptcg_amd import dims, native, devmem
     import oracle.replay as orp
     L = native.lib()
     dm = dims.CORE
     W, S, T, mb = dm.obs_size, 2048, 64, 1024
     n, segs, seat = S * T, mb // T, dm.seat_col()
-    g = torch.Generator(device="cuda").manual_seed(5)
-    obs_tb = torch.randn(n * W, device="cuda", generator=g)
-    obs_tb.view(n, W)[:, seat] = torch.randint(0, 2, (n,), device="cuda", generator=g).float()
-    obs = torch.empty_like(obs_tb)
-    small_tb = [torch.randn(n, device="cuda", generator=g) for _ in range(6)]
-    small = [torch.empty(n, device="cuda") for _ in range(6)]
-    values, rewards = torch.randn(n, device="cuda", generator=g), torch.rand(n, device="cuda", generator=g) * 2 - 1
-    dones = (torch.rand(n, device="cuda", generator=g) < 0.02).float()
-    ratio = torch.rand(n, device="cuda", generator=g) + 0.5
-    adv, ret = torch.empty(n, device="cuda"), torch.empty(n, device="cuda")
-    probs, cdf, mbp = torch.empty(S, device="cuda"), torch.empty(S, device="cuda"), torch.empty(segs, device="cuda")
-    idx, rows = torch.empty(segs, dtype=torch.int32, device="cuda"), torch.empty(mb, dtype=torch.int32, device="cuda")
-    rprio, off = torch.empty(n, device="cuda"), torch.zeros(1, dtype=torch.int64, device="cuda")
+    rng = np.random.default_rng(5)
+    # obs rows: only the seat column is read by the advantage (the transposes
+    # move whatever bytes are there), so the rest stays zero
+    seat_col = rng.integers(0, 2, n).astype(np.float32)
+    obs_host = np.zeros((n, W), np.float32)
+    obs_host[:, seat] = seat_col
+    obs_tb = devmem.DeviceArray.from_numpy(obs_host)
+    del obs_host
+    obs = devmem.DeviceArray(n * W)
+    D = devmem.DeviceArray.from_numpy
+    small_tb = [D(rng.standard_normal(n).astype(np.float32)) for _ in range(6)]
+    small = [devmem.DeviceArray(n) for _ in range(6)]
+    values_h = rng.standard_normal(n).astype(np.float32)
+    rewards_h = (rng.random(n) * 2 - 1).astype(np.float32)
+    dones_h = (rng.random(n) < 0.02).astype(np.float32)
+    ratio_h = (rng.random(n) + 0.5).astype(np.float32)
+    values, rewards, dones, ratio = D(values_h), D(rewards_h), D(dones_h), D(ratio_h)
+    adv, ret = devmem.DeviceArray(n), devmem.DeviceArray(n)
+    probs, cdf, mbp = devmem.DeviceArray(S), devmem.DeviceArray(S), devmem.DeviceArray(segs)
+    idx, rows = devmem.DeviceArray(segs, np.int32), devmem.DeviceArray(mb, np.int32)
+    rprio, off = devmem.DeviceArray(n), devmem.DeviceArray(1, np.int64)
     P = lambda t: t.data_ptr()
 
     def transposes():
@@ -684,14 +689,14 @@ def bench_replay(args):
     def timed(fn, reps):
         for _ in range(3):
             fn()
-        torch.cuda.synchronize()
-        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+        devmem.synchronize()
+        ev = [(devmem.Event(), devmem.Event()) for _ in range(reps)]
         for a, b in ev:
             a.record()
             fn()
             b.record()
-        torch.cuda.synchronize()
-        return sorted(a.elapsed_time(b) for a, b in ev)[reps // 2] * 1e3   # median us
+        devmem.synchronize()
+        return sorted(a.elapsed_ms(b) for a, b in ev)[reps // 2] * 1e3   # median us
 
     K = args.steps
     t_obs = timed(lambda: native.check(L.ptcg_transpose_102(P(obs), P(obs_tb), T, S, W, 0, None)), max(5, K // 4))
@@ -699,12 +704,12 @@ def bench_replay(args):
     t_adv = timed(advantage, K)
     t_rep = timed(replay, K)
     # whole minibatch prep, back to back (advantage then replay), K times
-    torch.cuda.synchronize()
+    devmem.synchronize()
     t0 = time.perf_counter()
     for _ in range(K):
         advantage()
         replay()
-    torch.cuda.synchronize()
+    devmem.synchronize()
     sec = time.perf_counter() - t0
     obs_bytes = 2.0 * n * W * 4
     adv_bytes = n * (4 * 4 + 4 + 2 * 4)        # values, rewards, dones, ratio, seat; advantages, returns
@@ -730,11 +735,9 @@ def bench_replay(args):
     }
     if not args.no_cpu_baseline:
         # the oracle's numpy restatement on the host: advantage + replay draw
-        v = values.view(S, T).cpu().numpy()
-        rr = rewards.view(S, T).cpu().numpy()
-        dd = dones.view(S, T).cpu().numpy()
-        ii = ratio.view(S, T).cpu().numpy()
-        st = obs.view(n, W)[:, seat].reshape(S, T).cpu().numpy()
+        # the same arrays, in the train layout the advantage reads
+        v, rr, dd, ii = (a.reshape(S, T) for a in (values_h, rewards_h, dones_h, ratio_h))
+        st = seat_col.reshape(T, S).T.copy()    # obs rows after the (T, S) -> (S, T) transpose
         reps, t0 = 0, time.perf_counter()
         while True:
             a, _ = orp.negamax_advantage(v, rr, dd, ii, st, 1.0, 0.95, 1.0, 1.0)

@@ -69,6 +69,11 @@ int ptcg_device_alloc(int64_t bytes, void** out);
 int ptcg_device_free(void* p);
 int ptcg_memcpy(void* dst, const void* src, int64_t bytes, int dir, void* stream);
 int ptcg_device_synchronize(void);
+/* timing events (a hipEvent_t behind void*): elapsed_ms waits for b      */
+int ptcg_event_create(void** ev);
+int ptcg_event_record(void* ev, void* stream);
+int ptcg_event_elapsed_ms(void* a, void* b, float* ms);
+int ptcg_event_destroy(void* ev);
 
 /* ---- layout (ptcg/rl/buffers.py:212-230; native_weights.py:45-113;
  *      kernels.cu:433-466 16 B alignment; pufferlib.cu:2366-2390) -------- */

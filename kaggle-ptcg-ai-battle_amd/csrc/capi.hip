@@ -275,6 +275,34 @@ extern "C" int ptcg_device_synchronize(void) {
     return PTCG_OK;
 }
 
+// timing events for host drivers (hipEvent_t behind void*)
+extern "C" int ptcg_event_create(void** ev) {
+    PT_REQUIRE(ev, "event_create: null argument");
+    hipEvent_t e = nullptr;
+    PT_HIP(hipEventCreate(&e));
+    *ev = e;
+    return PTCG_OK;
+}
+
+extern "C" int ptcg_event_record(void* ev, void* stream) {
+    PT_REQUIRE(ev, "event_record: null event");
+    PT_HIP(hipEventRecord((hipEvent_t)ev, (hipStream_t)stream));
+    return PTCG_OK;
+}
+
+// milliseconds from a to b; waits for b
+extern "C" int ptcg_event_elapsed_ms(void* a, void* b, float* ms) {
+    PT_REQUIRE(a && b && ms, "event_elapsed_ms: null argument");
+    PT_HIP(hipEventSynchronize((hipEvent_t)b));
+    PT_HIP(hipEventElapsedTime(ms, (hipEvent_t)a, (hipEvent_t)b));
+    return PTCG_OK;
+}
+
+extern "C" int ptcg_event_destroy(void* ev) {
+    if (ev) PT_HIP(hipEventDestroy((hipEvent_t)ev));
+    return PTCG_OK;
+}
+
 // ------------------------------------------------------------ PPO / gate / Adam
 extern "C" int ptcg_ppo_loss_fwd_bwd(const float* dec_out, int n, int A, const float* mask,
                                      int64_t mask_stride, const int32_t* row_idx, const float* actions,

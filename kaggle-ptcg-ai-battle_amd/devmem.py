@@ -104,3 +104,28 @@ def device_count():
 
 def synchronize():
     check(lib().ptcg_device_synchronize())
+
+
+class Event:
+    """A timing event on the library's device (hipEvent_t)."""
+
+    def __init__(self):
+        self._e = c_void_p()
+        check(lib().ptcg_event_create(ctypes.byref(self._e)))
+
+    def record(self, stream=None):
+        check(lib().ptcg_event_record(self._e, stream))
+
+    def elapsed_ms(self, end):
+        """Milliseconds from this event to ``end`` (waits for ``end``)."""
+        ms = ctypes.c_float()
+        check(lib().ptcg_event_elapsed_ms(self._e, end._e, ctypes.byref(ms)))
+        return ms.value
+
+    def __del__(self):
+        try:
+            if self._e.value:
+                check(lib().ptcg_event_destroy(self._e))
+                self._e = c_void_p()
+        except Exception:
+            pass

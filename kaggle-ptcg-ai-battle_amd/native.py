@@ -104,6 +104,10 @@ _SIGS = {
     "ptcg_device_free": (ctypes.c_int, [c_void_p]),
     "ptcg_memcpy": (ctypes.c_int, [c_void_p, c_void_p, ctypes.c_int64, ctypes.c_int, c_void_p]),
     "ptcg_device_synchronize": (ctypes.c_int, []),
+    "ptcg_event_create": (ctypes.c_int, [ctypes.POINTER(c_void_p)]),
+    "ptcg_event_record": (ctypes.c_int, [c_void_p, c_void_p]),
+    "ptcg_event_elapsed_ms": (ctypes.c_int, [c_void_p, c_void_p, ctypes.POINTER(ctypes.c_float)]),
+    "ptcg_event_destroy": (ctypes.c_int, [c_void_p]),
     "ptcg_trainer_create": (ctypes.c_int, [ctypes.POINTER(CPtcgDims), ctypes.POINTER(CPtcgHypers),
                                            ctypes.c_int, ctypes.POINTER(c_void_p)]),
     "ptcg_trainer_free": (None, [c_void_p]),

@@ -794,9 +794,14 @@ int launch_bwd_mfma(const float* qkv, const float* keep, const float* ctx, const
 static const size_t PT_LDS_MAX = 160 * 1024;
 
 // Kernel choice per (L, Dh), Lp = 16 * ceil(L / 16) = 16 * nt, nt <= 16
-// (Dh 32) / 9 (Dh 64): forward MFMA; backward MFMA with dS parked in LDS
-// when it fits (nt <= 8), else the split recompute pair.
-static const int PT_NT_MAX32 = 16, PT_NT_MAX64 = 9;
+// (L <= 256) at Dh 32 and 64: forward MFMA; backward MFMA with dS parked in
+// LDS when it fits (nt <= 8), else the split recompute pair.  At Dh 64 the
+// split pair stages up to 80 KB per workgroup through nt = 9 (two
+// workgroups per CU) and up to 139 KB at nt = 16 (one per CU): the
+// reference variant's 161-position trunk and 218-position critic with
+// 4 heads of 64 (native/model/ptcg_model.cu:19-21 sizes the trunk by
+// d_model / heads).
+static const int PT_NT_MAX32 = 16, PT_NT_MAX64 = 16;
 static int nt_max(int DH) { return DH == 32 ? PT_NT_MAX32 : (DH == 64 ? PT_NT_MAX64 : 0); }
 static int fwd_tiles(int L, int DH) {
     const int nt = pt_cdiv(L, 16);
@@ -842,7 +847,7 @@ static int attn_fwd_dispatch(const float* qkv, const float* keep, float* ctx, fl
     const int nt = fwd_tiles(L, DH);
     if (nt && DH == 64) {
         PT_NT_SWITCH8(64, nt, launch_fwd_mfma, qkv, keep, ctx, lse, N, L, H, s, coff)
-        if (nt == 9) return launch_fwd_mfma<64, 9, BF, IO16>(qkv, keep, ctx, lse, N, L, H, s, coff);
+        PT_NT_SWITCH_HI(64, nt, launch_fwd_mfma, qkv, keep, ctx, lse, N, L, H, s, coff)
     } else if (nt) {
         PT_NT_SWITCH8(32, nt, launch_fwd_mfma, qkv, keep, ctx, lse, N, L, H, s, coff)
         PT_NT_SWITCH_HI(32, nt, launch_fwd_mfma, qkv, keep, ctx, lse, N, L, H, s, coff)
@@ -862,7 +867,7 @@ static int attn_bwd_dispatch(const float* qkv, const float* keep, const float* c
     nt = bwd_split_tiles(L, DH);
     if (nt && DH == 64) {
         PT_NT_SWITCH8(64, nt, launch_bwd_split, qkv, keep, ctx, lse, dctx, dqkv, N, L, H, s, coff)
-        if (nt == 9) return launch_bwd_split<64, 9, BF, IO16>(qkv, keep, ctx, lse, dctx, dqkv, N, L, H, s, coff);
+        PT_NT_SWITCH_HI(64, nt, launch_bwd_split, qkv, keep, ctx, lse, dctx, dqkv, N, L, H, s, coff)
     } else if (nt) {
         PT_NT_SWITCH8(32, nt, launch_bwd_split, qkv, keep, ctx, lse, dctx, dqkv, N, L, H, s, coff)
         PT_NT_SWITCH_HI(32, nt, launch_bwd_split, qkv, keep, ctx, lse, dctx, dqkv, N, L, H, s, coff)

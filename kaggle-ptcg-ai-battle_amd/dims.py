@@ -142,6 +142,11 @@ def build_offsets(dims):
 # native_weights.py:24-26, ptcg_model.cu:22-43).
 FROZEN = PtcgDims()
 
+# The reference's other documented trunk size, on the same layout and
+# variant: d128 / 4 heads / FFN 256 (ptcg_model.cu:19, "A d128/h4 trunk is
+# PT_D 128 / PT_H 4 / PT_FFN 256"; head width 32 at both sizes).
+FROZEN_D128 = replace(FROZEN, d=128, heads=4, ffn=256)
+
 # The synthetic workload of the benchmark configs: 96 entity tokens, 32
 # numeric features per token, card ids in [0, 2048), d256 / 4 heads /
 # FFN 1024 / 4 pre-LN layers, 64 options, blind value head, learned tables.

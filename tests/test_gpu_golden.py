@@ -20,6 +20,7 @@ norm; tensors the decoder gradient does not reach (value / aux heads) within
 1e-5 of the aux gradient's norm.
 """
 import ctypes
+import dataclasses
 
 import numpy as np
 import pytest
@@ -79,11 +80,9 @@ class Model:
         lib().ptcg_model_free(self.h)
 
 
-# The second fixture runs a 4-head trunk (head width 64) on the frozen
-# layout's 161-position trunk and 218-position critic; the attention kernels
-# take head width 64 up to 144 positions, so model_create rejects that shape
-# (checked below) and the fixture pins the oracle only (test_golden_reference).
-GPU_CASES = ("frozen",)
+# The second fixture runs a 4-head trunk (head width 64, FFN 1024, 2 layers)
+# on the frozen layout's 161-position trunk and 218-position critic.
+GPU_CASES = ("frozen", "h4ffn1024")
 
 
 @pytest.fixture(scope="module", params=GPU_CASES)
@@ -92,10 +91,12 @@ def fx(request):
 
 
 def test_unsupported_attention_shape_is_rejected(cuda):
+    """A head width the fused attention kernels do not take (128) is refused
+    at creation with a clear message."""
     f = load("h4ffn1024")
+    dm = dataclasses.replace(f.dm, heads=f.dm.d // 128)
     with pytest.raises(RuntimeError, match="attention shape"):
-        trainer.create_pufferl({"dims": f.dm, "init_weights": f.blob, "static": f.static,
-                                "train": dict(minibatch_size=f.obs.shape[0])})
+        trainer.create_pufferl({"dims": dm, "static": f.static, "train": dict(minibatch_size=f.obs.shape[0])})
 
 
 def _check_forward(fx, out):

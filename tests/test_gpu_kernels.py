@@ -357,7 +357,10 @@ def _attn_ref(qkv, keep, H, Dh):
 ATTN_CASES = [(6, 97, 4, 64, 3), (5, 25, 2, 32, 3), (3, 100, 2, 64, 3), (4, 64, 8, 32, 3), (2, 1, 4, 64, 3),
               (3, 128, 2, 32, 3), (2, 17, 1, 64, 3),
               # rows too long for dS in LDS: the reference's trunk (161) and critic (218) at Dh 32
-              (2, 140, 2, 32, 5), (3, 161, 8, 32, 5), (2, 218, 8, 32, 5), (1, 256, 2, 32, 5), (2, 140, 2, 64, 5)]
+              (2, 140, 2, 32, 5), (3, 161, 8, 32, 5), (2, 218, 8, 32, 5), (1, 256, 2, 32, 5), (2, 140, 2, 64, 5),
+              # head width 64 beyond 144 positions (one split-pair workgroup per CU): the
+              # reference variant's trunk and critic with 4 heads, and the longest row
+              (3, 161, 4, 64, 5), (2, 218, 4, 64, 5), (1, 256, 2, 64, 5), (2, 150, 1, 64, 5)]
 
 
 @pytest.mark.parametrize("N,L,H,Dh,path", ATTN_CASES, ids=lambda *a: None)
@@ -467,8 +470,9 @@ def test_attention_rejects_oversized(cuda):
     a = empty(4)
     with pytest.raises(native.PtcgError, match="LDS"):
         native.check(native.lib().ptcg_kernel_attention_fwd(P(a), P(a), P(a), P(a), 1, 300, 1, 64, None))
-    assert native.lib().ptcg_kernel_attention_path(145, 64) == -1
+    assert native.lib().ptcg_kernel_attention_path(257, 64) == -1
     assert native.lib().ptcg_kernel_attention_path(257, 32) == -1
+    assert native.lib().ptcg_kernel_attention_path(97, 48) == -1
 
 
 def _ppo_inputs(n, A, seed):

@@ -39,7 +39,8 @@ def test_variant_shapes_and_blob():
     assert dm.obs_size == 10944
 
 
-@pytest.mark.parametrize("dm,B", [(dims.tiny_frozen(), 8), (dims.FROZEN, 4)], ids=["tiny", "frozen"])
+@pytest.mark.parametrize("dm,B", [(dims.tiny_frozen(), 8), (dims.FROZEN, 4), (dims.FROZEN_D128, 4)],
+                         ids=["tiny", "frozen", "frozen_d128"])
 def test_variant_forward_matches_oracle(dm, B, cuda):
     ref, pl = make(dm, B, seed=3)
     obs = synth.make_obs(dm, B, seed=4, rich=True)
@@ -76,7 +77,11 @@ def _oracle_fwd_bwd(ref, dm, obs, inp):
     return out.detach().numpy(), res
 
 
-@pytest.mark.parametrize("dm,B", [(dims.tiny_frozen(), 12), (dims.FROZEN, 6)], ids=["tiny", "frozen"])
+# frozen_d128: the reference's d128 / h4 / FFN 256 trunk (ptcg_model.cu:19), whose
+# d = 128 blocks take the unfused residual / LayerNorm launches (the fused
+# kernels own d = 256 rows)
+@pytest.mark.parametrize("dm,B", [(dims.tiny_frozen(), 12), (dims.FROZEN, 6), (dims.FROZEN_D128, 6)],
+                         ids=["tiny", "frozen", "frozen_d128"])
 def test_variant_backward_grads_match_oracle(dm, B, cuda):
     ref, pl = make(dm, B, seed=5)
     obs = synth.make_obs(dm, B, seed=6, rich=True)

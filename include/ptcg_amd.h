@@ -105,6 +105,16 @@ int ptcg_model_reg_rollout(PtcgModel* m, int n);
  * rows 0..n-1), replacing the trainer's minibatch copy (pufferlib.cu:2005). */
 int ptcg_model_forward(PtcgModel* m, const float* obs, const int32_t* row_idx, int n,
                        float** out, void* stream);
+/* Stage dumps for parity bisection (the reference's PTCG_DUMP_DIR,
+ * ptcg_model3.cu:222-231,371-400, read by native/tools/stage_parity.py):
+ * every named stage of the last forward as raw fp32 <dir>/<name>.bin —
+ * card_vec, att_tab, tok_cat, tokp (N, l_tok, .), dec_in, g_out, d_out,
+ * bc_out, keep, x0 (and x1..x_layers after a training forward), h
+ * (N, l_seq, .), q_in, q_vec, sc_in (N, n_opt, .), out — rows the compact
+ * trunk or the masked-option skip did not compute written as 0.  Set
+ * PTCG_DUMP_DIR and every forward that is not being captured dumps at its
+ * end.  Debug only: synchronous.                                          */
+int ptcg_model_dump_stages(PtcgModel* m, const char* dir, void* stream);
 /* backward (ptcg_model4.cu:277-281): grad (n, n_opt+1) = [d scores || d value];
  * OVERWRITES the grads arena (ptcg_model4.cu:15-21).                       */
 int ptcg_model_backward(PtcgModel* m, const float* grad, void* stream);

@@ -24,6 +24,10 @@
 // Grads are overwritten on every backward (ptcg_model4.cu:15-21).
 #include "model.h"
 
+#include <stdio.h>
+#include <stdlib.h>
+
+#include <algorithm>
 #include <map>
 #include <string>
 #include <vector>
@@ -928,6 +932,118 @@ extern "C" int ptcg_model_forward(PtcgModel* m, const float* obs, const int32_t*
         PT_TRY(pt_head_dot(m->ov1a, N, PT_VAL_H, m->ov2_w, m->ov2_b, m->out, 1, NO + 1, NO, s));
     }
     if (out) *out = m->out;
+    // stage dumps for parity bisection (the reference's PTCG_DUMP_DIR,
+    // ptcg_model3.cu:371-400); never inside a capture
+    const char* dump_dir = getenv("PTCG_DUMP_DIR");
+    if (dump_dir && dump_dir[0]) {
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        PT_HIP(hipStreamIsCapturing(s, &cs));
+        if (cs == hipStreamCaptureStatusNone) PT_TRY(ptcg_model_dump_stages(m, dump_dir, s));
+    }
+    return PTCG_OK;
+}
+
+// Every named stage of the last forward as raw fp32 files <dir>/<name>.bin
+// in the full layout the reference dumps (ptcg_model3.cu:222-231,371-400):
+// per-sample stages (N, ...), token stages (N, l_tok, ...), trunk stages
+// (N, l_seq, d), option stages (N, n_opt, ...).  Rows the compact trunk or
+// the masked-option skip did not compute are written as 0.  Debug only:
+// synchronises the stream and copies through the host.
+extern "C" int ptcg_model_dump_stages(PtcgModel* m, const char* dir, void* stream) {
+    PT_REQUIRE(m && dir && m->obs, "model_dump_stages: run a forward first");
+    hipStream_t s = (hipStream_t)stream;
+    PT_HIP(hipStreamSynchronize(s));
+    const PtcgDims& d = m->dm;
+    const DimsX& x = m->dx;
+    const long N = m->N, Lt = d.l_tok, Ls = x.l_seq, NO = d.n_opt, D = d.d;
+    auto d2h = [&](const void* src, long n, std::vector<float>& out) -> int {
+        out.resize(n);
+        if (n) PT_HIP(hipMemcpy(out.data(), src, n * sizeof(float), hipMemcpyDeviceToHost));
+        return PTCG_OK;
+    };
+    auto write = [&](const char* name, const std::vector<float>& v) -> int {
+        const std::string path = std::string(dir) + "/" + name + ".bin";
+        FILE* f = fopen(path.c_str(), "wb");
+        PT_REQUIRE(f, "model_dump_stages: cannot open %s", path.c_str());
+        const size_t w = fwrite(v.data(), sizeof(float), v.size(), f);
+        fclose(f);
+        PT_REQUIRE(w == v.size(), "model_dump_stages: short write to %s", path.c_str());
+        return PTCG_OK;
+    };
+    // columns [c0, c0 + w) of n rows of leading dimension ld
+    auto cols = [&](const char* name, const float* src, long n, long ld, long c0, long w) -> int {
+        std::vector<float> a, o((size_t)n * w);
+        PT_TRY(d2h(src, n * ld, a));
+        for (long r = 0; r < n; ++r)
+            for (long k = 0; k < w; ++k) o[r * w + k] = a[r * ld + c0 + k];
+        return write(name, o);
+    };
+    // compact trunk rows: row r holds (sample rsam[r], position rpos[r])
+    int rows = (int)(N * Ls);
+    std::vector<int> rsam, rpos;
+    if (m->compact) {
+        PT_HIP(hipMemcpy(&rows, m->Tr, sizeof(int), hipMemcpyDeviceToHost));
+        PT_REQUIRE(rows >= 0 && rows <= N * Ls, "model_dump_stages: row count %d", rows);
+        rsam.resize(rows);
+        rpos.resize(rows);
+        if (rows) {
+            PT_HIP(hipMemcpy(rsam.data(), m->c_rsam, rows * sizeof(int), hipMemcpyDeviceToHost));
+            PT_HIP(hipMemcpy(rpos.data(), m->c_rpos, rows * sizeof(int), hipMemcpyDeviceToHost));
+        }
+    }
+    // a trunk-row buffer (tokens: pos_off = 1 drops READOUT) to (N, L, w)
+    auto trunk = [&](const char* name, const float* src, long w, long L, int pos_off) -> int {
+        std::vector<float> a, o((size_t)N * L * w, 0.f);
+        const long nr = m->compact ? rows : N * L;
+        PT_TRY(d2h(src, nr * w, a));
+        for (long r = 0; r < nr; ++r) {
+            const long n = m->compact ? rsam[r] : r / L;
+            const long p = m->compact ? rpos[r] - pos_off : r % L;
+            if (n < 0 || n >= N || p < 0 || p >= L) continue;
+            std::copy(a.begin() + r * w, a.begin() + (r + 1) * w, o.begin() + (n * L + p) * w);
+        }
+        return write(name, o);
+    };
+    // option rows (all N * n_opt, or the legal ones through o_row) to (N, n_opt, w)
+    int orows = (int)(N * NO);
+    std::vector<int> orow;
+    if (m->skip_fwd) {
+        PT_HIP(hipMemcpy(&orows, m->o_off + N, sizeof(int), hipMemcpyDeviceToHost));
+        PT_REQUIRE(orows >= 0 && orows <= N * NO, "model_dump_stages: option row count %d", orows);
+        orow.resize(orows);
+        if (orows) PT_HIP(hipMemcpy(orow.data(), m->o_row, orows * sizeof(int), hipMemcpyDeviceToHost));
+    }
+    auto opts = [&](const char* name, const float* src, long ld, long c0, long w) -> int {
+        std::vector<float> a, o((size_t)N * NO * w, 0.f);
+        PT_TRY(d2h(src, (long)orows * ld, a));
+        for (long j = 0; j < orows; ++j) {
+            const long dst = m->skip_fwd ? orow[j] : j;
+            if (dst < 0 || dst >= N * NO) continue;
+            for (long k = 0; k < w; ++k) o[dst * w + k] = a[j * ld + c0 + k];
+        }
+        return write(name, o);
+    };
+    PT_TRY(cols("card_vec", m->card, d.n_cards, d.d_c, 0, d.d_c));
+    PT_TRY(cols("att_tab", m->att, d.n_attacks, d.d_a, 0, d.d_a));
+    const int tok_pos_off = m->compact ? 1 : 0;
+    PT_TRY(trunk("tok_cat", m->tok_cat, x.tok_in, Lt, tok_pos_off));
+    PT_TRY(trunk("tokp", m->tokp, D, Lt, tok_pos_off));
+    PT_TRY(cols("dec_in", m->dec_in, N, x.dec_in, 0, x.dec_in));
+    PT_TRY(cols("g_out", m->gd, N, x.bcast_in, 0, d.g));
+    PT_TRY(cols("d_out", m->gd, N, x.bcast_in, d.g, x.bcast_in - d.g));
+    PT_TRY(cols("bc_out", m->bc, N, D, 0, D));
+    PT_TRY(trunk("keep", m->keep, 1, Ls, 0));
+    PT_TRY(trunk("x0", m->x[0], D, Ls, 0));
+    if (m->train)
+        for (int i = 1; i <= d.layers; ++i) {
+            const std::string nm = "x" + std::to_string(i);
+            PT_TRY(trunk(nm.c_str(), m->x[i], D, Ls, 0));
+        }
+    PT_TRY(trunk("h", m->h, D, Ls, 0));
+    PT_TRY(opts("q_in", m->q_in, x.q_in, 0, x.q_in));
+    PT_TRY(opts("q_vec", m->sc_in, x.score_in, 0, D));
+    PT_TRY(opts("sc_in", m->sc_in, x.score_in, 0, x.score_in));
+    PT_TRY(cols("out", m->out, N, NO + 1, 0, NO + 1));
     return PTCG_OK;
 }
 

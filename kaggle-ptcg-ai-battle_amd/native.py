@@ -55,6 +55,7 @@ _SIGS = {
     "ptcg_model_forward": (ctypes.c_int, [c_void_p, c_void_p, c_void_p, ctypes.c_int,
                                           ctypes.POINTER(c_void_p), c_void_p]),
     "ptcg_model_backward": (ctypes.c_int, [c_void_p, c_void_p, c_void_p]),
+    "ptcg_model_dump_stages": (ctypes.c_int, [c_void_p, ctypes.c_char_p, c_void_p]),
     "ptcg_model_set_static": (ctypes.c_int, [c_void_p] * 8),
     "ptcg_model_bind_returns": (ctypes.c_int, [c_void_p, c_void_p]),
     "ptcg_trainer_set_static": (ctypes.c_int, [c_void_p] * 8),

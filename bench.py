@@ -49,7 +49,7 @@ BF16_MFMA_PEAK_TFLOPS = 2500.0     # MI355X dense bf16 matrix peak
 HBM_PEAK_GBS = 8000.0              # MI355X HBM3E bandwidth
 # launch classes of ptcg_profile_class: (index, name); amounts are HBM bytes
 HBM_CLASSES = ((1, "layernorm_fwd"), (2, "layernorm_bwd"), (3, "adam_norm"), (4, "adam_update"),
-               (7, "embedding_gather"))
+               (7, "embedding_gather"), (8, "ppo_loss_softmax"))
 
 TRAIN = dict(learning_rate=3e-4, beta1=0.9, beta2=0.999, eps=1e-8, max_grad_norm=0.5,
              clip_coef=0.2, vf_clip_coef=0.2, vf_coef=0.5, ent_coef=0.01)

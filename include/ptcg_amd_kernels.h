@@ -172,7 +172,10 @@ int ptcg_profile_end(double* total_ms, int* launches, double* flops);
  *   2 LayerNorm backward (12d+8 B per row, +4d with a residual gradient);
  *   3 Adam norm pass (4 B per parameter); 4 Adam update (28 B per parameter);
  *   5 whole Muon step (Newton-Schulz flops); 6 Muon's Newton-Schulz GEMM
- *   launches (flops; not counted in class 0).                              */
+ *   launches (flops; not counted in class 0); 7 token-concat gather (the
+ *   rows written and the obs floats read); 8 PPO loss with its masked
+ *   softmax (the (A+1) outputs, A mask floats and per-row inputs read, the
+ *   (A+1) gradient and ratio / new value written).                        */
 int ptcg_profile_class(int cls, double* total_ms, int* launches, double* amount);
 
 #ifdef __cplusplus

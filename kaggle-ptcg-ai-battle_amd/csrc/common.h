@@ -52,7 +52,7 @@ static inline int pt_cdiv(long a, long b) { return (int)((a + b - 1) / b); }
 // records the end event with the launch's class and algorithmic amount
 // (flops for GEMMs, HBM bytes for the others).
 enum PtProfClass { PROF_GEMM = 0, PROF_LN_FWD = 1, PROF_LN_BWD = 2, PROF_ADAM_NORM = 3, PROF_ADAM_UPDATE = 4,
-                   PROF_MUON = 5, PROF_MUON_GEMM = 6, PROF_GATHER = 7, PROF_NCLASS = 8 };
+                   PROF_MUON = 5, PROF_MUON_GEMM = 6, PROF_GATHER = 7, PROF_PPO = 8, PROF_NCLASS = 9 };
 int pt_prof_open(hipStream_t s);
 void pt_prof_close(int slot, int cls, double amount, hipStream_t s);
 // class recorded for GEMM launches (PROF_GEMM unless a caller such as the

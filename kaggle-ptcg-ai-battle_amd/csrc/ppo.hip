@@ -188,10 +188,16 @@ int pt_ppo_loss(const float* out, int n, int A, const float* mask, long mask_str
     PPOArgs a{out, n, A, mask, mask_stride, idx, actions, old_logp, adv, ret, val, prio,
               clip, vf_clip, vf_coef, ent_coef, grad, ratio, newvalue, partial};
     const int blocks = pt_cdiv(n, 4);
+    const int slot = pt_prof_open(s);
     hipLaunchKernelGGL(ppo_loss_kernel, dim3(blocks), dim3(256), 0, s, a);
     PT_LAUNCH_CHECK();
     hipLaunchKernelGGL(ppo_reduce_kernel, dim3(1), dim3(64), 0, s, partial, blocks, stats, guard);
     PT_LAUNCH_CHECK();
+    // algorithmic bytes per row: the (A+1) outputs and A mask floats read,
+    // five per-row inputs (+ the importance weight), the (A+1) gradient and
+    // ratio / new value written
+    const double row_bytes = 4.0 * ((A + 1) + A + 5 + (prio ? 1 : 0) + (A + 1) + (ratio ? 1 : 0) + (newvalue ? 1 : 0));
+    pt_prof_close(slot, PROF_PPO, n * row_bytes, s);
     return PTCG_OK;
 }
 

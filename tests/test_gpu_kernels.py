@@ -580,6 +580,29 @@ def test_adam_matches_torch(n, max_norm, cuda):
     assert rel_l2(upd_gpu, upd_ref) < 1e-4
 
 
+def test_adam_float_lr_entry_matches_double(cuda):
+    """ptcg_adam_step_lrf reads the learning rate from a device float (the
+    reference's lr_ptr); with an lr exact in both types the two entry points
+    give the same bits."""
+    n = 300000
+    p, g = _adam_case(n, 17)
+    L = native.lib()
+    out = []
+    for fn, lr in ((L.ptcg_adam_step, lr_dev(2.0 ** -12)),
+                   (L.ptcg_adam_step_lrf, torch.tensor([2.0 ** -12], dtype=torch.float32, device="cuda"))):
+        dp, dm_, dv, dg = dev(p), empty(n), empty(n), dev(g)
+        step = torch.zeros(1, dtype=torch.int32, device="cuda")
+        ws = empty(L.ptcg_adam_workspace_floats())
+        for _ in range(2):
+            native.check(fn(P(dp), P(dg), P(dm_), P(dv), n, P(lr), 0.9, 0.999, 1e-8, 0.5, None, P(step), None,
+                            P(ws), None))
+        torch.cuda.synchronize()
+        out.append((dp.cpu().numpy(), dm_.cpu().numpy(), dv.cpu().numpy(), step.item()))
+    for a, b in zip(out[0][:3], out[1][:3]):
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    assert out[0][3] == out[1][3] == 2
+
+
 def test_adam_gate_zero_is_bit_exact_noop(cuda):
     n = 8192
     p, g = _adam_case(n, 5)

@@ -923,7 +923,8 @@ __global__ __launch_bounds__(NT) void gemm_resid_ln_kernel(const GemmArgs g0, co
         const float* __restrict__ lnb, float* __restrict__ Y, long ldy, float* __restrict__ mean,
         float* __restrict__ rstd) {
     const GemmArgs g = gemm_shape(g0);
-    static_assert(BMR == 64 || BMR == 32, "64- or 32-row tiles");
+    static_assert(BMR == 128 || BMR == 64 || BMR == 32, "128-, 64- or 32-row tiles");
+    static_assert(BF || BMR <= 64, "fp32 operands: 64- or 32-row tiles");
     constexpr int TM = BMR / 32;   // 32-row MFMA tiles per wave
     const int m0 = blockIdx.x * BMR;
     if (m0 >= g.M) return;   // beyond the (device) row count
@@ -944,7 +945,8 @@ __global__ __launch_bounds__(NT) void gemm_resid_ln_kernel(const GemmArgs g0, co
     const unsigned ea = (unsigned)(((long)(g.M - 1) * g.lda + g.K) * 4);
     const unsigned eb = (unsigned)(((long)(RL_N - 1) * g.ldb + g.K) * 4);
     const int32x4_t ra = buffer_rsrc(g.A, ea), rb = buffer_rsrc(g.B, eb);
-    const int sa = dma_src<false>(wave, lane, m0, g.lda);
+    // A's 16-row chunks: chunk wave (and wave + 4 for 128-row tiles)
+    const int sa = dma_src<false>(wave, lane, m0, g.lda), sa2 = dma_src<false>(wave + 4, lane, m0, g.lda);
     int sb[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) sb[j] = dma_src<false>(4 * wave + j, lane, 0, g.ldb);
@@ -952,6 +954,7 @@ __global__ __launch_bounds__(NT) void gemm_resid_ln_kernel(const GemmArgs g0, co
         const int k0 = tile * BK;
         const float* st = smem + (tile & 1) * STAGE;
         if (wave < BMR / 16) dma16(ra, st + wave * 256, (sa + k0) * 4);
+        if (BMR == 128) dma16(ra, st + (wave + 4) * 256, (sa2 + k0) * 4);
 #pragma unroll
         for (int j = 0; j < 4; ++j) dma16(rb, st + TA + (4 * wave + j) * 256, (sb[j] + k0) * 4);
     };
@@ -1057,7 +1060,7 @@ __global__ __launch_bounds__(NT) void gemm_resid_ln_kernel(const GemmArgs g0, co
 // The LayerNorm backward fused into the bf16 dX product that feeds it (the
 // bf16 blocks' QKV and FFN1 dX): dy = dY W (dY rows x K bf16, W^T copy 256 x
 // K bf16, k-contiguous both) never leaves the chip.  The main loop is
-// gemm_resid_ln_kernel's bf16 one on 64 x 256 tiles; the epilogue stages dy
+// gemm_resid_ln_kernel's bf16 one on 128 x 256 tiles; the epilogue stages dy
 // in 32-row halves and a wave takes eight rows, one float4 per lane, in
 // ln_bwd_kernel's arithmetic: dx = rs (g - mean(g) - xh mean(g xh)) + dres
 // with g = dy w, xh = (x - mu) rs, written fp32 and as a bf16 copy.  The
@@ -1070,9 +1073,11 @@ struct LnBwdArgs {
     const float* x; const float* mean; const float* rstd; const float* w; const float* dres;
     float* dx; __bf16* dxh; float* part;
 };
+template <int BMR>
 __global__ __launch_bounds__(NT) void gemm_dx_lnbwd_kernel(const GemmArgs g0, const LnBwdArgs a) {
     const GemmArgs g = gemm_shape(g0);
-    constexpr int BMR = 64, TM = 2;
+    static_assert(BMR == 64 || BMR == 128, "64- or 128-row tiles");
+    constexpr int TM = BMR / 32;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int m0 = blockIdx.x * BMR;
     if (m0 >= g.M) {   // beyond the (device) row count: a zero partial row
@@ -1094,7 +1099,8 @@ __global__ __launch_bounds__(NT) void gemm_dx_lnbwd_kernel(const GemmArgs g0, co
     const unsigned ea = (unsigned)(((long)(g.M - 1) * g.lda + g.K) * 4);
     const unsigned eb = (unsigned)(((long)(RL_N - 1) * g.ldb + g.K) * 4);
     const int32x4_t ra = buffer_rsrc(g.A, ea), rb = buffer_rsrc(g.B, eb);
-    const int sa = dma_src<false>(wave, lane, m0, g.lda);
+    // A's 16-row chunks: chunk wave (and wave + 4 for 128-row tiles)
+    const int sa = dma_src<false>(wave, lane, m0, g.lda), sa2 = dma_src<false>(wave + 4, lane, m0, g.lda);
     int sb[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) sb[j] = dma_src<false>(4 * wave + j, lane, 0, g.ldb);
@@ -1102,6 +1108,7 @@ __global__ __launch_bounds__(NT) void gemm_dx_lnbwd_kernel(const GemmArgs g0, co
         const int k0 = tile * BK;
         const float* st = smem + (tile & 1) * STAGE;
         dma16(ra, st + wave * 256, (sa + k0) * 4);
+        if (BMR == 128) dma16(ra, st + (wave + 4) * 256, (sa2 + k0) * 4);
 #pragma unroll
         for (int j = 0; j < 4; ++j) dma16(rb, st + TA + (4 * wave + j) * 256, (sb[j] + k0) * 4);
     };
@@ -2196,14 +2203,17 @@ int pt_gemm_resid_ln(const GemmArgs& g, const float* lnw, const float* lnb, floa
     const GemmArgs f = resid_ln_float_units(g);
     // row tiles: 32 for fp32 operands (about 4.6 tiles per CU at 37.4k rows
     // instead of 2.3, so the last partial wave costs less: headline +0.4% on
-    // one box), 64 for bf16 ones (32-row tiles were 2.8% slower on the bf16
-    // step at B = 2048, whose 149.5k rows fill the chip anyway)
+    // one box), 128 for bf16 ones (every tile re-reads all of W from L2, so
+    // larger row tiles halve that traffic: with the dX + LayerNorm backward
+    // also on 128-row tiles the bf16 step at B = 2048 ran 1.2% faster than
+    // on 64-row ones, two A/B pairs on one box; 32-row tiles were 2.8% slower
+    // than 64-row ones)
     const dim3 blk(NT);
     const int slot = pt_prof_open(s);
     if (g.bs) {
-        const dim3 grid(pt_cdiv(g.M, 64));
-        if (ybf) hipLaunchKernelGGL((gemm_resid_ln_kernel<true, true, 64>), grid, blk, 0, s, f, lnw, lnb, y, ldy, mean, rstd);
-        else hipLaunchKernelGGL((gemm_resid_ln_kernel<true, false, 64>), grid, blk, 0, s, f, lnw, lnb, y, ldy, mean, rstd);
+        const dim3 grid(pt_cdiv(g.M, 128));
+        if (ybf) hipLaunchKernelGGL((gemm_resid_ln_kernel<true, true, 128>), grid, blk, 0, s, f, lnw, lnb, y, ldy, mean, rstd);
+        else hipLaunchKernelGGL((gemm_resid_ln_kernel<true, false, 128>), grid, blk, 0, s, f, lnw, lnb, y, ldy, mean, rstd);
     } else {
         const dim3 grid(pt_cdiv(g.M, 32));
         if (ybf) hipLaunchKernelGGL((gemm_resid_ln_kernel<false, true, 32>), grid, blk, 0, s, f, lnw, lnb, y, ldy, mean, rstd);
@@ -2230,12 +2240,13 @@ int pt_dx_lnbwd(const GemmArgs& g, const float* x, const float* w, const float* 
     PT_REQUIRE(g.A && g.B && x && w && mean && rstd && dx && dw && db && ws, "dX + layernorm bwd: null buffer");
     PT_REQUIRE((((uintptr_t)x | (uintptr_t)w | (uintptr_t)dx | (uintptr_t)dres | (uintptr_t)dxh) & 15) == 0,
                "dX + layernorm bwd: 16 B aligned rows needed");
-    const int blocks = pt_cdiv(g.M, 64);
+    // 128-row tiles: W (256 x K bf16) is re-read from L2 once per tile
+    const int blocks = pt_cdiv(g.M, 128);
     PT_REQUIRE((long)blocks * 2 * RL_N * 2 <= ws_floats, "dX + layernorm bwd: workspace too small");
     LnBwdArgs a{x, mean, rstd, w, dres, dx, reinterpret_cast<__bf16*>(dxh), ws};
     const GemmArgs f = resid_ln_float_units(g);
     const int slot = pt_prof_open(s);
-    hipLaunchKernelGGL(gemm_dx_lnbwd_kernel, dim3(blocks), dim3(NT), 0, s, f, a);
+    hipLaunchKernelGGL(gemm_dx_lnbwd_kernel<128>, dim3(blocks), dim3(NT), 0, s, f, a);
     PT_LAUNCH_CHECK();
     pt_prof_close(slot, g_gemm_class, 2.0 * g.M * (double)g.N * g.K, s);
     return pt_colsum2(ws, 2 * RL_N, blocks, 2 * RL_N, RL_N, dw, db, ws + (long)blocks * 2 * RL_N,

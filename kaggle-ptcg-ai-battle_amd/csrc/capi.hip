@@ -336,7 +336,7 @@ extern "C" int ptcg_ppo_loss_fwd_bwd(const float* dec_out, int n, int A, const f
 // kernels write every partial they later read, so nothing needs clearing.
 // Each GPU has its own copy; all calls on one GPU share it, so calls that
 // overlap on one GPU (other streams, other threads) race.
-static __device__ __align__(256) float scratch[(PT_PPO_NOALLOC_MAX_ROWS / 4) * 7];
+static __device__ __align__(256) float scratch[(PT_PPO_NOALLOC_MAX_ROWS / 16) * 7];   // 16 rows a partial
 
 namespace {
 constexpr int kMaxDevices = 64;

@@ -2277,11 +2277,23 @@ int pt_gemm(const GemmArgs& g0, float* ws, long ws_floats, hipStream_t s) {
     // split K when the output is too small to fill the chip: long K in chunks
     // of >= 16 k-steps; short K (a few hundred rows, e.g. the weight gradients
     // of the per-sample MLPs at K = B) in chunks of >= 4 k-steps, so a handful
-    // of tiles does not walk its whole K one stage at a time on a few CUs
+    // of tiles does not walk its whole K one stage at a time on a few CUs.
+    // Products with a transposed A (the weight gradients, reduced over the
+    // rows K) aim at K / 128 workgroups (256 .. 1024, at most that many):
+    // they run on the step's side stream beside the dX chain, and fewer,
+    // longer splits leave it more of the chip.  Against 512 workgroups for
+    // every product: the CORE step at B = 512 (K = 37.4k rows) +2.0%, the
+    // reference variant's step (82.4k rows) even, two A/B pairs each on one
+    // box; 384, 448, 640 and 768 for all of them, or K / 64 .. K / 112, were
+    // up to 2% slower on one or the other.
     int splits = 1;
-    const int target = 512;
+    int target = 512;
+    if (g.a_t) {
+        target = g.K / 128;
+        target = target < 256 ? 256 : target > 1024 ? 1024 : target;
+    }
     if (tiles < target && g.K >= 2 * bk * 4) {
-        splits = pt_cdiv(target, tiles);
+        splits = g.a_t ? target / tiles : pt_cdiv(target, tiles);
         const int min_steps = g.K >= 4 * bk * 16 ? 16 : 4;
         int max_splits = g.K / (bk * min_steps);
         if (splits > max_splits) splits = max_splits;

@@ -2130,10 +2130,14 @@ static int gemm_bs_dw(const GemmArgs& g, float* ws, long ws_floats, hipStream_t 
                "gemm (bf16 weight gradient): fp32 STORE output with ldc a multiple of 4");
     const int tiles = pt_cdiv(g.M, BM) * pt_cdiv(g.N, BN);
     const bool db = g.dbias != nullptr;
-    // split the rows so the launch has ~512 blocks, each >= 4 stages of 64 rows
+    // split the rows so the launch has ~256 blocks, each >= 4 stages of 64
+    // rows: the blocks' weight gradients run on the step's side stream beside
+    // the dX chain, and fewer, longer splits leave it more of the chip (the
+    // bf16 step at B = 2048: 256 blocks +0.9%, 384 +0.7% against 512, two A/B
+    // pairs on one box; 768 and 149.5k rows / 128 .. 256 no better)
     int splits = 1;
-    if (tiles < 512 && g.K >= 8 * BKW) {
-        splits = pt_cdiv(512, tiles);
+    if (tiles < 256 && g.K >= 8 * BKW) {
+        splits = pt_cdiv(256, tiles);
         const int max_splits = g.K / (4 * BKW);
         if (splits > max_splits) splits = max_splits;
         if (splits < 1) splits = 1;
@@ -2279,18 +2283,24 @@ int pt_gemm(const GemmArgs& g0, float* ws, long ws_floats, hipStream_t s) {
     // of the per-sample MLPs at K = B) in chunks of >= 4 k-steps, so a handful
     // of tiles does not walk its whole K one stage at a time on a few CUs.
     // Products with a transposed A (the weight gradients, reduced over the
-    // rows K) aim at K / 128 workgroups (256 .. 1024, at most that many):
-    // they run on the step's side stream beside the dX chain, and fewer,
-    // longer splits leave it more of the chip.  Against 512 workgroups for
-    // every product: the CORE step at B = 512 (K = 37.4k rows) +2.0%, the
-    // reference variant's step (82.4k rows) even, two A/B pairs each on one
-    // box; 384, 448, 640 and 768 for all of them, or K / 64 .. K / 112, were
-    // up to 2% slower on one or the other.
+    // rows K) run on the step's side stream beside the dX chain: they aim at
+    // a whole number of workgroups per CU, K / 128 rounded to the nearest
+    // multiple of the CU count (1 .. 4 per CU), and take at most that many
+    // (splits = target / tiles), so a launch alone has no partial last wave
+    // and beside the dX chain leaves it the rest of the chip.  Measured
+    // against 512 workgroups for every product (A/B pairs on one box each):
+    // the CORE step at B = 512 (37.4k rows: 256 workgroups) +2.0% on one box
+    // and even on another, the reference variant's step (82.4k rows: 768)
+    // +0.6% and +0.5%; K / 128 unrounded (288 workgroups at 37.4k rows) was
+    // as fast in the step but 60% slower alone, and 256 workgroups at 82.4k
+    // rows 2.4% slower than 768.
     int splits = 1;
     int target = 512;
     if (g.a_t) {
-        target = g.K / 128;
-        target = target < 256 ? 256 : target > 1024 ? 1024 : target;
+        const int cu = pt_cu_count() > 0 ? pt_cu_count() : 256;
+        int per_cu = (g.K / 128 + cu / 2) / cu;
+        per_cu = per_cu < 1 ? 1 : per_cu > 4 ? 4 : per_cu;
+        target = per_cu * cu;
     }
     if (tiles < target && g.K >= 2 * bk * 4) {
         splits = g.a_t ? target / tiles : pt_cdiv(target, tiles);

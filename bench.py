@@ -12,9 +12,11 @@ The step is captured once in a HIP graph (sync-free compact layout) and
 replayed per minibatch with the minibatch's row indices written into the
 captured index buffer, as the reference's trainer replays its captured train
 graph; `value` is the throughput of those replays.  The same number of
-minibatches then runs launched kernel by kernel with a HIP event pair around
-every GEMM / LayerNorm / Adam launch (`stream_launch`), and the kernels'
-rooflines come from that pass (`--stream` times only the latter).
+minibatches then runs launched kernel by kernel, once with no launch profile
+open (`stream_launch`: host row counts, weight gradients on a side stream)
+and once with a HIP event pair around every GEMM / LayerNorm / Adam launch
+(`profiled_pass`); the kernels' rooflines come from the latter (`--stream`
+times only the stream-launched passes).
 
 Prints one JSON line (see the keys below), including the GEMM kernel's
 roofline (useful flops over measured kernel time, HIP events on the launch
@@ -381,10 +383,14 @@ def main():
     if graph and not args.sync_free:
         native.check(L.ptcg_trainer_set_sync_free(pl._h, 0))
     sec_plain = None
-    if not graph:
-        # the value of a stream-launched workload: the minibatches launched
-        # kernel by kernel with no launch profile open (the blocks' weight
-        # gradients on their side stream); the profiled pass below repeats them
+    if not graph or args.workload == "train":
+        # the value of a stream-launched workload (beside the graph replay's
+        # for the CORE step): the minibatches launched kernel by kernel with
+        # no launch profile open (the blocks' weight gradients on their side
+        # stream); the profiled pass below repeats them
+        if graph:   # one untimed step in host-row-count mode first
+            pl.step(r["obs"], d_lists[0], r)
+            devmem.synchronize()
         t0 = time.perf_counter()
         for i in range(args.warmup, n_lists):
             pl.step(r["obs"], d_lists[i], r)
@@ -496,7 +502,13 @@ def main():
         line["profiled_pass"] = dict(value=round(B * K / sec_stream, 2), ms_per_step=round(sec_stream * 1e3 / K, 4),
                                      note=PROFILED_NOTE)
     if graph:
-        line["stream_launch"] = dict(value=round(B * K / sec_stream, 2), ms_per_step=round(sec_stream * 1e3 / K, 4),
+        line["stream_launch"] = dict(value=round(B * K / sec_plain, 2), ms_per_step=round(sec_plain * 1e3 / K, 4),
+                                     note="as many minibatches launched kernel by kernel (host row counts read "
+                                          "back per minibatch, exact launch sizes, no launch profile open), the "
+                                          "blocks' weight gradients on their side stream beside the dX chain; "
+                                          "a captured step's replay runs its nodes one after another on this "
+                                          "ROCm build, so only stream launch overlaps the two")
+        line["profiled_pass"] = dict(value=round(B * K / sec_stream, 2), ms_per_step=round(sec_stream * 1e3 / K, 4),
                                      note="as many minibatches launched kernel by kernel (host row counts, exact "
                                           "launch sizes) with HIP event pairs, the blocks' weight gradients on "
                                           "the launch stream so that every timed launch runs alone; roofline "

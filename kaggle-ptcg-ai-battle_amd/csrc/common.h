@@ -66,34 +66,17 @@ bool pt_prof_active();
 // ---------------------------------------------------------------- device math
 // Exact (erf) GELU, torch nn.GELU() default; the reference's pt_gelu_fwd/bwd
 // (ptcg_kernels.cuh:111-128) computes the same function and derivative.
-__device__ __forceinline__ float pt_gelu(float x) {
-    return 0.5f * x * (1.f + erff(x * 0.70710678118654752f));
-}
-__device__ __forceinline__ float pt_gelu_grad(float x) {
-    float cdf = 0.5f * (1.f + erff(x * 0.70710678118654752f));
-    float pdf = 0.3989422804014327f * expf(-0.5f * x * x);
-    return cdf + x * pdf;
-}
-// both from one erf, with the same arithmetic as pt_gelu / pt_gelu_grad
-__device__ __forceinline__ void pt_gelu_both(float x, float& g, float& gd) {
-    const float e = erff(x * 0.70710678118654752f);
-    g = 0.5f * x * (1.f + e);
-    const float cdf = 0.5f * (1.f + e);
-    const float pdf = 0.3989422804014327f * expf(-0.5f * x * x);
-    gd = cdf + x * pdf;
-}
-
-// GELU and its derivative for bf16 outputs (the mixed-precision variant's
-// stored activations), branch-free: erf by Abramowitz & Stegun, Handbook of
-// Mathematical Functions, formula 7.1.26 (|error| <= 1.5e-7 on [0, inf)),
-// 1 - erf(x) = t (a1 + t (a2 + t (a3 + t (a4 + t a5)))) e^(-x^2),
-// t = 1 / (1 + p x), x = |z| / sqrt 2, whose e^(-x^2) = e^(-z^2/2) is also the
-// normal density's exponential in gelu'(z) = Phi(z) + z phi(z).  The error is
-// far below the 2^-9 rounding of the stored bf16 value, as is that of t from
-// v_rcp_f32 (1 ulp) in place of an IEEE division (ten instructions per
-// element in an epilogue bound by its VALU work); the fp32 path keeps
-// pt_gelu_both (libm erf).
-__device__ __forceinline__ void pt_gelu_both_bf(float z, float& g, float& gd) {
+// GELU and its derivative from one branch-free erf: Abramowitz & Stegun,
+// Handbook of Mathematical Functions, formula 7.1.26 (|error| <= 1.5e-7 on
+// [0, inf)), 1 - erf(x) = t (a1 + t (a2 + t (a3 + t (a4 + t a5)))) e^(-x^2),
+// t = 1 / (1 + p x), x = |z| / sqrt 2, whose e^(-x^2) = e^(-z^2/2) is also
+// the normal density's exponential in gelu'(z) = Phi(z) + z phi(z).  t comes
+// from v_rcp_f32 (1 ulp) in place of an IEEE division.  The GEMM epilogues
+// that apply it run after the products and are bound by their VALU work:
+// libm's erf (branches over |x| ranges) and a separate expf for the density
+// cost the fp32 FFN1 product with this epilogue 30 us per launch more than
+// the same-shape FFN2 dX product with a multiply epilogue.
+__device__ __forceinline__ void pt_gelu_both(float z, float& g, float& gd) {
     const float x = fabsf(z) * 0.70710678118654752f;
     const float t = __builtin_amdgcn_rcpf(1.0f + 0.3275911f * x);
     const float poly =
@@ -104,6 +87,19 @@ __device__ __forceinline__ void pt_gelu_both_bf(float z, float& g, float& gd) {
     g = z * cdf;
     gd = cdf + z * (0.3989422804014327f * e);
 }
+__device__ __forceinline__ float pt_gelu(float x) {
+    float g, gd;
+    pt_gelu_both(x, g, gd);
+    return g;
+}
+__device__ __forceinline__ float pt_gelu_grad(float x) {
+    float g, gd;
+    pt_gelu_both(x, g, gd);
+    return gd;
+}
+// the mixed-precision variant's stored activations (bf16 outputs): the same
+// function (its error is far below the 2^-9 rounding of the stored value)
+__device__ __forceinline__ void pt_gelu_both_bf(float z, float& g, float& gd) { pt_gelu_both(z, g, gd); }
 
 // Philox4x32-10 (Salmon, Moraes, Dror, Shaw, "Parallel random numbers: as
 // easy as 1, 2, 3", SC'11), restated from the paper: 10 rounds of

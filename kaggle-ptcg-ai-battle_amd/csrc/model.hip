@@ -182,7 +182,14 @@ struct LnOut {
     int ybf = 0;   // y stored in bf16 (the mixed-precision blocks' LayerNorm outputs)
 };
 // Y = X W^T + b + R (rows x out, out = d), then ln(Y): one fused launch when
-// the shape fits it (fp32, d = 256), else the product and pt_ln_fwd
+// the shape fits it (fp32, d = 256) and K < 1024, else the product and
+// pt_ln_fwd.  The fused kernel's 32-row tiles each re-read all of W, so its
+// cost grows with K faster than the 128 x 128-tile product's: measured alone
+// (fused vs product + LayerNorm), 37.4k rows x K 256: 67 vs ~89 us, K 512:
+// 119 vs ~133, K 1024: 231 vs ~213.  In the CORE step (FFN2 at K 1024
+// unfused) +0.4% replayed, +0.8% stream-launched; the reference variant's
+// FFN2 at K 512 x 82.4k rows (280 vs ~258 alone) ran 0.3% slower unfused in
+// its step, so it stays fused.  Both give the same bits.
 static int lin_resid_ln(const PtcgModel* m, const float* X, const float* W, const float* b, float* Y, int rows,
                         int in, int out, const float* R, const LnOut& ln, hipStream_t s, const int* Mdev) {
     GemmArgs g{};
@@ -194,7 +201,8 @@ static int lin_resid_ln(const PtcgModel* m, const float* X, const float* W, cons
     g.C = Y; g.ldc = out;
     g.bias = b; g.R = R; g.ldr = out;
     g.epi = EPI_BIAS_RESID;
-    if (pt_gemm_resid_ln_fits(g)) return pt_gemm_resid_ln(g, ln.w, ln.b, ln.y, out, ln.mu, ln.rs, s, ln.ybf);
+    if (pt_gemm_resid_ln_fits(g) && in < 1024)
+        return pt_gemm_resid_ln(g, ln.w, ln.b, ln.y, out, ln.mu, ln.rs, s, ln.ybf);
     PT_TRY(pt_gemm(g, m->ws, m->ws_floats, s));
     return pt_ln_fwd(Y, out, ln.w, ln.b, ln.y, out, ln.mu, ln.rs, rows, out, s, Mdev, ln.ybf);
 }

@@ -1965,6 +1965,38 @@ __global__ void tail_reduce_kernel(GemmArgs g, const float* __restrict__ part, i
 // Deterministic column sums in two levels.  Level 1: block (64 columns x 4
 // row groups) sums one slice of rows; level 2: the same shape sums the
 // slice partials.  Every add happens in a fixed order.
+// column sums of X (M x N) in one launch: row group g (16 of them) of a
+// column sums rows g, g + 16, ... in four interleaved accumulators, then the
+// sixteen group sums add in order; columns below split go to out, the rest
+// to out_hi
+__global__ __launch_bounds__(1024) void colsum_one_kernel(const float* __restrict__ X, long ldx, int M, int N,
+                                                          float* __restrict__ out, int split,
+                                                          float* __restrict__ out_hi) {
+    __shared__ float sh[16][64];
+    const int c = blockIdx.x * 64 + (threadIdx.x & 63);
+    const int rg = threadIdx.x >> 6;
+    float s0 = 0.f, s1 = 0.f, s2 = 0.f, s3 = 0.f;
+    if (c < N) {
+        int r = rg;
+        for (; r + 48 < M; r += 64) {
+            s0 += X[(long)r * ldx + c];
+            s1 += X[(long)(r + 16) * ldx + c];
+            s2 += X[(long)(r + 32) * ldx + c];
+            s3 += X[(long)(r + 48) * ldx + c];
+        }
+        for (; r < M; r += 16) s0 += X[(long)r * ldx + c];
+    }
+    sh[rg][threadIdx.x & 63] = (s0 + s1) + (s2 + s3);
+    __syncthreads();
+    if (rg == 0 && c < N) {
+        float v = 0.f;
+#pragma unroll
+        for (int g = 0; g < 16; ++g) v += sh[g][threadIdx.x];
+        if (c < split) out[c] = v;
+        else out_hi[c - split] = v;
+    }
+}
+
 __global__ void colsum_level_kernel(const float* __restrict__ X, long ldx, int M, int N, int chunk,
                                     float* __restrict__ out, long ldo, int split, float* __restrict__ out_hi) {
     __shared__ float sh[4][64];
@@ -2687,6 +2719,16 @@ int pt_linear_dw(const float* dY, const float* X, float* dW, float* db, int rows
 int pt_colsum2(const float* X, long ldx, int M, int N, int split, float* out_lo, float* out_hi,
                float* ws, long ws_floats, hipStream_t s) {
     PT_REQUIRE(M > 0 && N > 0, "colsum: empty shape %d x %d", M, N);
+    if (M <= 4096) {
+        // one launch: a workgroup per 64 columns, sixteen row groups of a
+        // column summed in a fixed order (the per-block partial rows of the
+        // LayerNorm backward and the small bias sums: two launches of a few
+        // rows each were bound by their launch latency)
+        hipLaunchKernelGGL(colsum_one_kernel, dim3(pt_cdiv(N, 64)), dim3(1024), 0, s, X, ldx, M, N, out_lo,
+                           out_hi ? split : N, out_hi ? out_hi : out_lo + N);
+        PT_LAUNCH_CHECK();
+        return PTCG_OK;
+    }
     int slices = pt_cdiv(M, 64);
     if (slices > 256) slices = 256;
     const int chunk = pt_cdiv(M, slices);

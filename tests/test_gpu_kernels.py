@@ -137,12 +137,15 @@ def test_gemm_weight_grad_with_bias_sums(rows, inp, out, cuda):
     assert rel_l2(db.cpu().double(), refb) < 1e-5
 
 
-def test_colsum(cuda):
-    X = torch.randn(1000, 300, generator=torch.Generator().manual_seed(1))
-    out = empty(300)
+# one launch up to 4 096 rows (1 row, fewer rows than row groups, a tail
+# past the four interleaved accumulators), two levels past it
+@pytest.mark.parametrize("M,N", [(1000, 300), (1, 70), (13, 64), (4096, 512), (4097, 100), (20000, 300)])
+def test_colsum(M, N, cuda):
+    X = torch.randn(M, N, generator=torch.Generator().manual_seed(M + N))
+    out = empty(N)
     ws = empty(1 << 20)
     dX = dev(X)
-    native.check(native.lib().ptcg_kernel_colsum(P(dX), 300, 1000, 300, P(out), P(ws), ws.numel(), None))
+    native.check(native.lib().ptcg_kernel_colsum(P(dX), N, M, N, P(out), P(ws), ws.numel(), None))
     torch.cuda.synchronize()
     assert rel_l2(out.cpu(), X.double().sum(0)) < 1e-6
 

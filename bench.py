@@ -505,9 +505,7 @@ def main():
         line["stream_launch"] = dict(value=round(B * K / sec_plain, 2), ms_per_step=round(sec_plain * 1e3 / K, 4),
                                      note="as many minibatches launched kernel by kernel (host row counts read "
                                           "back per minibatch, exact launch sizes, no launch profile open), the "
-                                          "blocks' weight gradients on their side stream beside the dX chain; "
-                                          "a captured step's replay runs its nodes one after another on this "
-                                          "ROCm build, so only stream launch overlaps the two")
+                                          "blocks' weight gradients on their side stream beside the dX chain")
         line["profiled_pass"] = dict(value=round(B * K / sec_stream, 2), ms_per_step=round(sec_stream * 1e3 / K, 4),
                                      note="as many minibatches launched kernel by kernel (host row counts, exact "
                                           "launch sizes) with HIP event pairs, the blocks' weight gradients on "

@@ -29,6 +29,16 @@ int ptcg_kernel_gemm(int M, int N, int K, const float* A, int64_t lda, int a_t,
                      const float* bias, const float* R, int64_t ldr, float* C2, int64_t ldc2,
                      float* workspace, int64_t workspace_floats, void* stream);
 
+/* ptcg_kernel_gemm with a device row count, as the sync-free model's
+ * launches run: M is the host's row bound, *rows_dev (device int, <= M) the
+ * rows computed; rows past it are left alone.  A row-major A (a_t = 0) only;
+ * one pass over K per tile (no split-K, no balanced last wave).
+ * No reference counterpart: the sync-free layout's own launch form.        */
+int ptcg_kernel_gemm_rows_dev(int M, int N, int K, const float* A, int64_t lda, const float* B,
+                              int64_t ldb, int b_t, float* C, int64_t ldc, int epi, const float* bias,
+                              const float* R, int64_t ldr, float* C2, int64_t ldc2, const int* rows_dev,
+                              float* workspace, int64_t workspace_floats, void* stream);
+
 /* C = alpha * op(A) op(B) + beta * R (R may not alias C), the alpha / beta
  * form of cublasGemmExDense / puf_addmm_nn (native/src/kernels.cu:262-310)
  * that the reference's Muon Newton-Schulz steps use (muon.cu:270-282);

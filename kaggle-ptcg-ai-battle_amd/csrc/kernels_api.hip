@@ -23,6 +23,30 @@ extern "C" int ptcg_kernel_gemm(int M, int N, int K, const float* A, int64_t lda
     return pt_gemm(g, workspace, workspace_floats, (hipStream_t)stream);
 }
 
+extern "C" int ptcg_kernel_gemm_rows_dev(int M, int N, int K, const float* A, int64_t lda, const float* B,
+                                         int64_t ldb, int b_t, float* C, int64_t ldc, int epi, const float* bias,
+                                         const float* R, int64_t ldr, float* C2, int64_t ldc2,
+                                         const int* rows_dev, float* workspace, int64_t workspace_floats,
+                                         void* stream) {
+    PT_REQUIRE(rows_dev, "kernel_gemm_rows_dev: null device row count");
+    PT_REQUIRE(A && B && C, "kernel_gemm_rows_dev: null operand");
+    PT_REQUIRE(epi >= EPI_STORE && epi <= EPI_MUL, "kernel_gemm_rows_dev: bad epilogue %d", epi);
+    PT_REQUIRE(!((epi == EPI_BIAS || epi == EPI_BIAS_GELU || epi == EPI_BIAS_RESID || epi == EPI_BIAS_GELU_D) && !bias),
+               "kernel_gemm_rows_dev: epilogue %d needs bias", epi);
+    PT_REQUIRE(!((epi == EPI_BIAS_RESID || epi == EPI_GELU_BWD || epi == EPI_MUL) && !R),
+               "kernel_gemm_rows_dev: epilogue %d needs R", epi);
+    PT_REQUIRE(!((epi == EPI_BIAS_GELU || epi == EPI_BIAS_GELU_D) && !C2),
+               "kernel_gemm_rows_dev: epilogue %d needs C2", epi);
+    GemmArgs g{};
+    g.M = M; g.N = N; g.K = K;
+    g.A = A; g.lda = lda; g.a_t = 0;
+    g.B = B; g.ldb = ldb; g.b_t = b_t;
+    g.C = C; g.ldc = ldc; g.epi = epi;
+    g.bias = bias; g.R = R; g.ldr = ldr; g.C2 = C2; g.ldc2 = ldc2;
+    g.Mdev = rows_dev;
+    return pt_gemm(g, workspace, workspace_floats, (hipStream_t)stream);
+}
+
 extern "C" int ptcg_kernel_gemm_axpby(int M, int N, int K, const float* A, int64_t lda, int a_t,
                                       const float* B, int64_t ldb, int b_t, float* C, int64_t ldc, float alpha,
                                       const float* R, int64_t ldr, float beta, void* stream) {

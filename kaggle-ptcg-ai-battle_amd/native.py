@@ -205,6 +205,10 @@ _SIGS = {
         c_void_p, ctypes.c_int64, ctypes.c_int, c_void_p, ctypes.c_int64, ctypes.c_int,
         c_void_p, c_void_p, ctypes.c_int64, c_void_p, ctypes.c_int64, c_void_p,
         ctypes.c_int64, c_void_p]),
+    "ptcg_kernel_gemm_rows_dev": (ctypes.c_int, [
+        ctypes.c_int, ctypes.c_int, ctypes.c_int, c_void_p, ctypes.c_int64, c_void_p, ctypes.c_int64,
+        ctypes.c_int, c_void_p, ctypes.c_int64, ctypes.c_int, c_void_p, c_void_p, ctypes.c_int64, c_void_p,
+        ctypes.c_int64, c_void_p, c_void_p, ctypes.c_int64, c_void_p]),
     "ptcg_kernel_gemm_bf16": (ctypes.c_int, [
         ctypes.c_int, ctypes.c_int, ctypes.c_int, c_void_p, ctypes.c_int64, ctypes.c_int,
         c_void_p, ctypes.c_int64, ctypes.c_int, c_void_p, ctypes.c_int64, ctypes.c_int,

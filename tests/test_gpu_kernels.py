@@ -108,6 +108,63 @@ def test_gemm_layouts_and_epilogues(case, cuda):
         assert rel_l2(got2, ref2) < 1e-5
 
 
+DEV_ROWS_CASES = [
+    # rows computed, N, K, B transposed, epilogue: the sync-free model's 256-wide
+    # products (dX: B transposed, STORE / MUL; forward: BIAS / BIAS_RESID /
+    # BIAS_GELU_D) with between one and four tiles per CU, K with a partial
+    # last k-tile (300), fewer tiles than CUs, more than four per CU
+    (37400, 256, 1024, 1, 0), (37400, 256, 768, 1, 7), (33333, 256, 256, 1, 0),
+    (40000, 256, 1024, 0, 3), (34567, 256, 300, 0, 1), (36000, 256, 256, 0, 6),
+    (900, 256, 256, 1, 0), (70000, 256, 256, 0, 1),
+]
+
+
+@pytest.mark.parametrize("rows,N,K,b_t,epi", DEV_ROWS_CASES)
+def test_gemm_device_rows(rows, N, K, b_t, epi, cuda):
+    """A launch sized for a row bound that computes the device count's rows
+    (the sync-free model's form: every tile in one pass over K) against
+    float64, and against the host-count launch of the same rows to fp32
+    accumulation-order accuracy (that one balances its last wave with a
+    split-K tail); rows past the count keep their contents."""
+    bound = rows + 3000
+    g = torch.Generator().manual_seed(rows + K + epi)
+    A = torch.randn(bound, K, generator=g)
+    B = torch.randn(K, N, generator=g) if b_t else torch.randn(N, K, generator=g)
+    bias = torch.randn(N, generator=g)
+    R = torch.randn(bound, N, generator=g)
+    acc = A[:rows].double() @ (B.double() if b_t else B.double().T)
+    ref2 = None
+    if epi == 0: ref = acc
+    elif epi == 1: ref = acc + bias.double()
+    elif epi == 3: ref = acc + bias.double() + R[:rows].double()
+    elif epi == 6:
+        z = acc + bias.double()
+        ref, ref2 = gelu_grad(z), gelu(z)
+    else: ref = acc * R[:rows].double()
+    dA, dB, dbias, dR = dev(A), dev(B), dev(bias), dev(R)
+    ldb = N if b_t else K
+    ws = empty(32 << 20)
+    L = native.lib()
+    sentinel = 7.0
+    dC, dC2 = torch.full((bound, N), sentinel, device="cuda"), torch.full((bound, N), sentinel, device="cuda")
+    rows_dev = torch.tensor([rows], dtype=torch.int32, device="cuda")
+    native.check(L.ptcg_kernel_gemm_rows_dev(bound, N, K, P(dA), K, P(dB), ldb, b_t, P(dC), N, epi, P(dbias),
+                                             P(dR), N, P(dC2), N, P(rows_dev), P(ws), ws.numel(), None))
+    hC, hC2 = empty(rows, N), empty(rows, N)
+    native.check(L.ptcg_kernel_gemm(rows, N, K, P(dA), K, 0, P(dB), ldb, b_t, P(hC), N, epi, P(dbias), P(dR), N,
+                                    P(hC2), N, P(ws), ws.numel(), None))
+    torch.cuda.synchronize()
+    got = dC[:rows].cpu().double()
+    assert rel_l2(got, ref) < 1e-5 and max_rel(got, ref) < 1e-4, (rel_l2(got, ref), max_rel(got, ref))
+    assert bool((dC[rows:] == sentinel).all())
+    if ref2 is not None:
+        assert rel_l2(dC2[:rows].cpu().double(), ref2) < 1e-5
+        assert bool((dC2[rows:] == sentinel).all())
+    assert rel_l2(got, hC.cpu().double()) < 5e-6
+    if ref2 is not None:
+        assert rel_l2(dC2[:rows].cpu().double(), hC2.cpu().double()) < 5e-6
+
+
 def test_gemm_operand_not_16b_aligned(cuda):
     # aligned widths, but A starts one float into its buffer: scalar-load path
     g = torch.Generator().manual_seed(5)

@@ -66,6 +66,16 @@ int ptcg_kernel_gemm_dw(int rows, int in, int out, const float* dY, int64_t lddy
                         const float* X, int64_t ldx, float* dW, float* db,
                         float* workspace, int64_t workspace_floats, void* stream);
 
+/* ptcg_kernel_gemm_dw over a device row count, as the sync-free model's
+ * weight gradients run: rows is the host's bound, *rows_dev (device int,
+ * <= rows) the rows summed.  The launch is sized for the bound's K splits;
+ * the split count actually used is the same rule applied to the device
+ * count (at most the launched count).
+ * No reference counterpart: the sync-free layout's own launch form.        */
+int ptcg_kernel_gemm_dw_rows_dev(int rows, int in, int out, const float* dY, int64_t lddy,
+                                 const float* X, int64_t ldx, float* dW, float* db, const int* rows_dev,
+                                 float* workspace, int64_t workspace_floats, void* stream);
+
 /* ptcg_kernel_gemm_dw with bf16 products (dY and X rounded to bf16 before
  * the MFMA, fp32 accumulation); db sums the unrounded fp32 dY.            */
 int ptcg_kernel_gemm_dw_bf16(int rows, int in, int out, const float* dY, int64_t lddy,

@@ -199,7 +199,44 @@ struct GemmArgs {
     const int* Kdev;
     // EPI_AXPBY scalars
     float alpha, beta;
+    // set by pt_gemm for a weight gradient (A transposed) with a device
+    // reduction count on the fp32 LDS-DMA kernel: the CU count, and the
+    // launch's K splits follow pt_wgrad_splits of the device count (capped
+    // at the launched splits; later splits return), which workgroup (0, 0, 0)
+    // writes as an int after the partials for the reduce (0 = splits fixed
+    // by the host)
+    int wsplit;
 };
+
+// K splits of a weight gradient (A transposed, reduction over K rows) of
+// `tiles` output tiles on `cu` CUs at k-step bk: a whole number of workgroups
+// per CU, K / 128 rounded to the nearest multiple of the CU count (down: the
+// multiple below; 1 .. 4 per CU), with chunks of at least 16 k-steps (4 below
+// K = 64 bk).  Host and device share it, so a device reduction count splits
+// as the same count given on the host would.
+__host__ __device__ inline int pt_wgrad_splits(int K, int tiles, int cu, int bk, bool down = false) {
+    if (K <= 0 || tiles <= 0) return 1;
+    int per_cu = (K / 128 + (down ? 0 : cu / 2)) / cu;
+    per_cu = per_cu < 1 ? 1 : per_cu > 4 ? 4 : per_cu;
+    const int target = per_cu * cu;
+    int splits = 1;
+    if (tiles < target && K >= 2 * bk * 4) {
+        splits = target / tiles;
+        const int min_steps = K >= 4 * bk * 16 ? 16 : 4;
+        const int max_splits = K / (bk * min_steps);
+        if (splits > max_splits) splits = max_splits;
+        if (splits < 1) splits = 1;
+    }
+    return splits;
+}
+// a split count's chunk of K, rounded up to the k-step, and the count that
+// chunk gives (<= splits; every split but the last a full chunk)
+__host__ __device__ inline int pt_split_chunks(int K, int splits, int bk, int* kc) {
+    *kc = K > 0 ? K : bk;
+    if (splits <= 1 || K <= 0) return 1;
+    *kc = ((K + splits - 1) / splits + bk - 1) / bk * bk;
+    return (K + *kc - 1) / *kc;
+}
 
 // Launch C = epi(A*B) on `stream`. Requirements: K % 4 == 0 when the operand
 // is k-contiguous, M (N) % 4 == 0 when A (B) is m- (n-) contiguous, leading

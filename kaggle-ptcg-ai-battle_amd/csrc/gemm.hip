@@ -668,8 +668,20 @@ __device__ __forceinline__ void gemm_dma_tile(const GemmArgs& g0, int k_chunk0, 
                                               int gz) {
     constexpr bool W32 = !BF;
     const GemmArgs g = gemm_shape(g0);
-    // a device reduction count splits its own K evenly over the launch's splits
-    const int k_chunk = g0.Kdev ? (((g.K + gz - 1) / gz + BK - 1) / BK) * BK : k_chunk0;
+    // a device reduction count splits its own K evenly over the launch's
+    // splits, or (wsplit) as many ways as the weight-gradient rule gives for
+    // that count: the later splits return, and workgroup (0, 0, 0) leaves the
+    // count after the partials (and bias partials) for the reduce
+    int k_chunk = g0.Kdev ? (((g.K + gz - 1) / gz + BK - 1) / BK) * BK : k_chunk0;
+    if constexpr (PARTIAL) {
+        if (g0.Kdev && g0.wsplit) {
+            const int tiles = ((g.M + BM - 1) / BM) * ((g.N + BN - 1) / BN);
+            const int sp = pt_split_chunks(g.K, min(pt_wgrad_splits(g.K, tiles, g0.wsplit, BK), gz), BK, &k_chunk);
+            if (bx == 0 && bz == 0 && threadIdx.x == 0)
+                *reinterpret_cast<int*>(g0.C + (long)gz * (part_stride + (DB ? g0.M : 0))) = sp;
+            if (bz >= sp) return;
+        }
+    }
     constexpr int TILE = BM * BK;   // floats per operand tile (BM == BN)
     constexpr int SMEM = NS * 2 * TILE > STAGE_FLOATS ? NS * 2 * TILE : STAGE_FLOATS;
     __shared__ __align__(16) float smem[SMEM];
@@ -1808,15 +1820,18 @@ __global__ __launch_bounds__(512) void gemm_bs_dw256_kernel(const GemmArgs g0, i
     }
 }
 
+// sdev (optional): the number of partials to sum, written on the device by
+// the product (at most splits, which places the bias partials)
 template <bool ACCUM, bool V4>
 __global__ void splitk_reduce_kernel(float* C, long ldc, const float* part, long part_stride,
-                                     int splits, int M, int N, float* db) {
+                                     int splits, int M, int N, float* db, const int* sdev) {
     constexpr int W = V4 ? 4 : 1;
     const long nq = N / W;
     const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    const int ns = sdev ? *sdev : splits;
     if (i >= (long)M * nq) {
         const long m = i - (long)M * nq;
-        if (db != nullptr && m < M) db[m] = sum_split_column(part + (long)splits * part_stride + m, splits, M);
+        if (db != nullptr && m < M) db[m] = sum_split_column(part + (long)splits * part_stride + m, ns, M);
         return;
     }
     const int m = (int)(i / nq), n = (int)(i % nq) * W;
@@ -1824,12 +1839,12 @@ __global__ void splitk_reduce_kernel(float* C, long ldc, const float* part, long
     if (V4) {
         floatx4 s = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll 8
-        for (int k = 0; k < splits; ++k) s += ld_v4(part + (long)k * part_stride + o);
+        for (int k = 0; k < ns; ++k) s += ld_v4(part + (long)k * part_stride + o);
         st_g4(C + o, ACCUM ? ld_v4(C + o) + s : s);
     } else {
         float s = 0.f;
 #pragma unroll 8
-        for (int k = 0; k < splits; ++k) s += part[(long)k * part_stride + o];
+        for (int k = 0; k < ns; ++k) s += part[(long)k * part_stride + o];
         if (ACCUM) C[o] += s; else C[o] = s;
     }
 }
@@ -1843,13 +1858,14 @@ __global__ void splitk_reduce_kernel(float* C, long ldc, const float* part, long
 template <bool ACCUM, int G>
 __global__ __launch_bounds__(256) void splitk_reduce_grp_kernel(float* C, long ldc, const float* part,
                                                                 long part_stride, int splits, int M, int N,
-                                                                float* db, int out_blocks) {
+                                                                float* db, int out_blocks, const int* sdev) {
     constexpr int CPB = 256 / G;
     __shared__ floatx4 sh[G][CPB];
     const int t = threadIdx.x;
+    const int ns = sdev ? *sdev : splits;
     if ((int)blockIdx.x >= out_blocks) {
         const int m = ((int)blockIdx.x - out_blocks) * 256 + t;
-        if (db != nullptr && m < M) db[m] = sum_split_column(part + (long)splits * part_stride + m, splits, M);
+        if (db != nullptr && m < M) db[m] = sum_split_column(part + (long)splits * part_stride + m, ns, M);
         return;
     }
     const int nq = N / 4;
@@ -1860,7 +1876,7 @@ __global__ __launch_bounds__(256) void splitk_reduce_grp_kernel(float* C, long l
     const long o = (long)m * ldc + n;
     floatx4 sum = floatx4{0.f, 0.f, 0.f, 0.f};
     if (live) {
-        const int zb = (int)(((long)splits * g) / G), ze = (int)(((long)splits * (g + 1)) / G);
+        const int zb = (int)(((long)ns * g) / G), ze = (int)(((long)ns * (g + 1)) / G);
 #pragma unroll 4
         for (int z = zb; z < ze; ++z) sum += ld_v4(part + (long)z * part_stride + o);
     }
@@ -1920,7 +1936,7 @@ int launch_splitk_epi_reduce(const GemmArgs& g, const float* part, long part_str
 // form for many splits with 128-bit columns, else one thread per output
 template <bool ACCUM>
 void launch_splitk_reduce(float* C, long ldc, const float* part, long part_stride, int splits, int M, int N,
-                          float* db, bool v4, hipStream_t s) {
+                          float* db, bool v4, hipStream_t s, const int* sdev = nullptr) {
     const int G = !v4 ? 1 : splits >= 64 ? 8 : splits >= 24 ? 4 : splits >= 12 ? 2 : 1;
     if (G > 1) {
         const long outs = (long)M * (N / 4);
@@ -1928,23 +1944,23 @@ void launch_splitk_reduce(float* C, long ldc, const float* part, long part_strid
         const dim3 gr(ob + dbb);
         if (G == 8)
             hipLaunchKernelGGL((splitk_reduce_grp_kernel<ACCUM, 8>), gr, dim3(256), 0, s, C, ldc, part, part_stride,
-                               splits, M, N, db, ob);
+                               splits, M, N, db, ob, sdev);
         else if (G == 4)
             hipLaunchKernelGGL((splitk_reduce_grp_kernel<ACCUM, 4>), gr, dim3(256), 0, s, C, ldc, part, part_stride,
-                               splits, M, N, db, ob);
+                               splits, M, N, db, ob, sdev);
         else
             hipLaunchKernelGGL((splitk_reduce_grp_kernel<ACCUM, 2>), gr, dim3(256), 0, s, C, ldc, part, part_stride,
-                               splits, M, N, db, ob);
+                               splits, M, N, db, ob, sdev);
         return;
     }
     const long tot = (long)M * (v4 ? N / 4 : N) + (db ? M : 0);
     const dim3 gr(pt_cdiv(tot, 256));
     if (v4)
         hipLaunchKernelGGL((splitk_reduce_kernel<ACCUM, true>), gr, dim3(256), 0, s, C, ldc, part, part_stride,
-                           splits, M, N, db);
+                           splits, M, N, db, sdev);
     else
         hipLaunchKernelGGL((splitk_reduce_kernel<ACCUM, false>), gr, dim3(256), 0, s, C, ldc, part, part_stride,
-                           splits, M, N, db);
+                           splits, M, N, db, sdev);
 }
 
 // Tail tiles of a balanced launch: C[tile] = epi(sum_s part[s][tile]), fixed order over s.
@@ -2520,16 +2536,21 @@ int pt_gemm(const GemmArgs& g0, float* ws, long ws_floats, hipStream_t s) {
     // +0.6% and +0.5%; K / 128 unrounded (288 workgroups at 37.4k rows) was
     // as fast in the step but 60% slower alone, and 256 workgroups at 82.4k
     // rows 2.4% slower than 768.
+    const int cu = pt_cu_count() > 0 ? pt_cu_count() : 256;
+    // a weight gradient over a device row count (K here its host bound) on
+    // the DMA kernel splits the device count as the rule gives for it (the
+    // launch's splits cap it; later splits return): the launch takes the
+    // rule's per-CU count rounded down on the bound, so that a device count
+    // below the bound leaves few or no splits idle -- idle workgroups at the
+    // end of a weight gradient running beside the dX chain delayed it (a
+    // 256 x 256 weight gradient at 37.4k of 49.7k rows: 150 us with 500
+    // workgroups of which 256 worked, 61 us with the 256 alone)
+    const bool wsplit_ok = g.a_t && g.Kdev && !bf && vec && g.dma && (g.epi == EPI_STORE || g.epi == EPI_ACCUM);
     int splits = 1;
-    int target = 512;
     if (g.a_t) {
-        const int cu = pt_cu_count() > 0 ? pt_cu_count() : 256;
-        int per_cu = (g.K / 128 + cu / 2) / cu;
-        per_cu = per_cu < 1 ? 1 : per_cu > 4 ? 4 : per_cu;
-        target = per_cu * cu;
-    }
-    if (tiles < target && g.K >= 2 * bk * 4) {
-        splits = g.a_t ? target / tiles : pt_cdiv(target, tiles);
+        splits = pt_wgrad_splits(g.K, tiles, cu, bk, wsplit_ok);
+    } else if (tiles < 512 && g.K >= 2 * bk * 4) {
+        splits = pt_cdiv(512, tiles);
         const int min_steps = g.K >= 4 * bk * 16 ? 16 : 4;
         int max_splits = g.K / (bk * min_steps);
         if (splits > max_splits) splits = max_splits;
@@ -2549,9 +2570,13 @@ int pt_gemm(const GemmArgs& g0, float* ws, long ws_floats, hipStream_t s) {
         splits = fit > 1 ? (int)fit : 1;
     }
     int k_chunk = g.K;
-    if (splits > 1) {
-        k_chunk = pt_cdiv(pt_cdiv(g.K, splits), bk) * bk;
-        splits = pt_cdiv(g.K, k_chunk);
+    if (splits > 1) splits = pt_split_chunks(g.K, splits, bk, &k_chunk);
+    // the device-derived split count goes to the reduce as an int after the
+    // partials (and bias partials)
+    const int* sdev = nullptr;
+    if (wsplit_ok && splits > 1 && (long)splits * per_split + 1 <= ws_floats) {
+        g.wsplit = cu;
+        sdev = reinterpret_cast<const int*>(ws + (long)splits * per_split);
     }
     dim3 grid(tn * tm, 1, splits);
     if (bf && g.dbias && !db) {
@@ -2568,9 +2593,9 @@ int pt_gemm(const GemmArgs& g0, float* ws, long ws_floats, hipStream_t s) {
         const bool v4 = g.N % 4 == 0 && g.ldc % 4 == 0 && ((uintptr_t)g.C & 15) == 0;
         float* dbp = db ? g.dbias : nullptr;
         if (g.epi == EPI_ACCUM) {
-            launch_splitk_reduce<true>(g.C, g.ldc, ws, part_stride, splits, g.M, g.N, dbp, v4, s);
+            launch_splitk_reduce<true>(g.C, g.ldc, ws, part_stride, splits, g.M, g.N, dbp, v4, s, sdev);
         } else if (g.epi == EPI_STORE) {
-            launch_splitk_reduce<false>(g.C, g.ldc, ws, part_stride, splits, g.M, g.N, dbp, v4, s);
+            launch_splitk_reduce<false>(g.C, g.ldc, ws, part_stride, splits, g.M, g.N, dbp, v4, s, sdev);
         } else {
             const uintptr_t al = (uintptr_t)g.C | (uintptr_t)g.C2 | (uintptr_t)g.R | (uintptr_t)g.bias |
                                  (uintptr_t)((g.ldc | g.ldc2 | g.ldr) * 4);

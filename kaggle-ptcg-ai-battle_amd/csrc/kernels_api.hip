@@ -91,6 +91,21 @@ extern "C" int ptcg_kernel_gemm_dw(int rows, int in, int out, const float* dY, i
     return pt_gemm(g, workspace, workspace_floats, (hipStream_t)stream);
 }
 
+extern "C" int ptcg_kernel_gemm_dw_rows_dev(int rows, int in, int out, const float* dY, int64_t lddy,
+                                            const float* X, int64_t ldx, float* dW, float* db,
+                                            const int* rows_dev, float* workspace, int64_t workspace_floats,
+                                            void* stream) {
+    PT_REQUIRE(dY && X && dW && rows_dev, "kernel_gemm_dw_rows_dev: null operand");
+    GemmArgs g{};
+    g.M = out; g.N = in; g.K = rows;
+    g.A = dY; g.lda = lddy; g.a_t = 1;
+    g.B = X; g.ldb = ldx; g.b_t = 1;
+    g.C = dW; g.ldc = in; g.epi = EPI_STORE;
+    g.dbias = db;
+    g.Kdev = rows_dev;
+    return pt_gemm(g, workspace, workspace_floats, (hipStream_t)stream);
+}
+
 extern "C" int ptcg_kernel_gemm_dw_bf16(int rows, int in, int out, const float* dY, int64_t lddy,
                                         const float* X, int64_t ldx, float* dW, float* db,
                                         float* workspace, int64_t workspace_floats, void* stream) {

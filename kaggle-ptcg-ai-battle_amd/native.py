@@ -217,6 +217,9 @@ _SIGS = {
     "ptcg_kernel_gemm_dw": (ctypes.c_int, [
         ctypes.c_int, ctypes.c_int, ctypes.c_int, c_void_p, ctypes.c_int64, c_void_p, ctypes.c_int64,
         c_void_p, c_void_p, c_void_p, ctypes.c_int64, c_void_p]),
+    "ptcg_kernel_gemm_dw_rows_dev": (ctypes.c_int, [
+        ctypes.c_int, ctypes.c_int, ctypes.c_int, c_void_p, ctypes.c_int64, c_void_p, ctypes.c_int64,
+        c_void_p, c_void_p, c_void_p, c_void_p, ctypes.c_int64, c_void_p]),
     "ptcg_kernel_gemm_dw_bf16": (ctypes.c_int, [
         ctypes.c_int, ctypes.c_int, ctypes.c_int, c_void_p, ctypes.c_int64, c_void_p, ctypes.c_int64,
         c_void_p, c_void_p, c_void_p, ctypes.c_int64, c_void_p]),

@@ -194,6 +194,44 @@ def test_gemm_weight_grad_with_bias_sums(rows, inp, out, cuda):
     assert rel_l2(db.cpu().double(), refb) < 1e-5
 
 
+# (row bound, device rows, in, out): the sync-free trunk's weight gradients at
+# B = 512 (49 664-row bound, 37.4k rows: the bound's split rule gives two
+# workgroups per CU, the device count one), a count below 1 024 rows under a
+# bound above it (the rule's chunk floor changes there), a small product, and
+# no rows at all
+@pytest.mark.parametrize("bound,rows,inp,out", [(49664, 37400, 256, 1024), (49664, 37400, 1024, 256),
+                                                (49664, 37400, 256, 768), (2000, 900, 256, 256),
+                                                (1500, 1100, 64, 36), (49664, 0, 256, 256)])
+def test_gemm_weight_grad_device_rows(bound, rows, inp, out, cuda):
+    """dW = dY^T X and db = column sums of dY over a device row count below
+    the launch's bound: against float64 over those rows, and against the
+    host-count launch of the same rows to fp32 accumulation-order accuracy
+    (both split the rows by the same rule)."""
+    g = torch.Generator().manual_seed(bound + rows + inp)
+    dY = torch.randn(bound, out, generator=g)
+    X = torch.randn(bound, inp, generator=g)
+    d_dY, d_X, dW, db = dev(dY), dev(X), empty(out, inp), empty(out)
+    rows_dev = torch.tensor([rows], dtype=torch.int32, device="cuda")
+    ws = empty(32 << 20)
+    L = native.lib()
+    native.check(L.ptcg_kernel_gemm_dw_rows_dev(bound, inp, out, P(d_dY), out, P(d_X), inp, P(dW), P(db),
+                                                P(rows_dev), P(ws), ws.numel(), None))
+    torch.cuda.synchronize()
+    if rows == 0:
+        assert not bool(dW.any()) and not bool(db.any())
+        return
+    refW = dY[:rows].double().T @ X[:rows].double()
+    refb = dY[:rows].double().sum(0)
+    assert rel_l2(dW.cpu().double(), refW) < 1e-5
+    assert rel_l2(db.cpu().double(), refb) < 1e-5
+    hW, hb = empty(out, inp), empty(out)
+    native.check(L.ptcg_kernel_gemm_dw(rows, inp, out, P(d_dY), out, P(d_X), inp, P(hW), P(hb), P(ws), ws.numel(),
+                                       None))
+    torch.cuda.synchronize()
+    assert rel_l2(dW.cpu().double(), hW.cpu().double()) < 5e-6
+    assert rel_l2(db.cpu().double(), hb.cpu().double()) < 5e-6
+
+
 # one launch up to 4 096 rows (1 row, fewer rows than row groups, a tail
 # past the four interleaved accumulators), two levels past it
 @pytest.mark.parametrize("M,N", [(1000, 300), (1, 70), (13, 64), (4096, 512), (4097, 100), (20000, 300)])

@@ -32,7 +32,9 @@ int ptcg_kernel_gemm(int M, int N, int K, const float* A, int64_t lda, int a_t,
 /* ptcg_kernel_gemm with a device row count, as the sync-free model's
  * launches run: M is the host's row bound, *rows_dev (device int, <= M) the
  * rows computed; rows past it are left alone.  A row-major A (a_t = 0) only;
- * one pass over K per tile (no split-K, no balanced last wave).
+ * no split-K; with B not transposed, a bound of S to 8 S tiles on S CUs
+ * balances the last wave from the device count (the host-count launch's
+ * tiles, K splits and partial sums).
  * No reference counterpart: the sync-free layout's own launch form.        */
 int ptcg_kernel_gemm_rows_dev(int M, int N, int K, const float* A, int64_t lda, const float* B,
                               int64_t ldb, int b_t, float* C, int64_t ldc, int epi, const float* bias,

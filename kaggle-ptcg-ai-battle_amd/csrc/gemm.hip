@@ -663,9 +663,15 @@ template <bool T> __device__ __forceinline__ int dma_src(int c, int lane, int r0
 // BF: bf16 products on 16 x 16 tiles — each lane's float4 fragment
 // (k = 4 lq .. 4 lq + 3 of its row, the same k for A and B) is rounded to
 // bf16 (RNE) and one v_mfma_f32_16x16x16_bf16 replaces four fp32 k-steps.
+// LDS floats of an NS-stage DMA tile (operand stages, or the staged epilogue)
+template <int NS> constexpr int dma_smem_floats() {
+    return NS * 2 * BM * BK > STAGE_FLOATS ? NS * 2 * BM * BK : STAGE_FLOATS;
+}
+// smem: the calling kernel's LDS array of dma_smem_floats<NS>() floats (one
+// array, so a kernel calling several forms of the tile holds it once)
 template <bool AT, bool BT, int EPI, bool PARTIAL, bool DB, bool BF = false, int NS = DMA_NS>
 __device__ __forceinline__ void gemm_dma_tile(const GemmArgs& g0, int k_chunk0, long part_stride, int bx, int bz,
-                                              int gz) {
+                                              int gz, float* smem) {
     constexpr bool W32 = !BF;
     const GemmArgs g = gemm_shape(g0);
     // a device reduction count splits its own K evenly over the launch's
@@ -683,8 +689,6 @@ __device__ __forceinline__ void gemm_dma_tile(const GemmArgs& g0, int k_chunk0, 
         }
     }
     constexpr int TILE = BM * BK;   // floats per operand tile (BM == BN)
-    constexpr int SMEM = NS * 2 * TILE > STAGE_FLOATS ? NS * 2 * TILE : STAGE_FLOATS;
-    __shared__ __align__(16) float smem[SMEM];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int tn = (g.N + BN - 1) / BN;
     int tmi, tni;
@@ -907,7 +911,99 @@ __device__ __forceinline__ void gemm_dma_tile(const GemmArgs& g0, int k_chunk0, 
 
 template <bool AT, bool BT, int EPI, bool PARTIAL, bool DB>
 __global__ __launch_bounds__(NT) void gemm_f32_dma_kernel(const GemmArgs g0, int k_chunk0, long part_stride) {
-    gemm_dma_tile<AT, BT, EPI, PARTIAL, DB>(g0, k_chunk0, part_stride, blockIdx.x, blockIdx.z, gridDim.z);
+    __shared__ __align__(16) float smem[dma_smem_floats<DMA_NS>()];
+    gemm_dma_tile<AT, BT, EPI, PARTIAL, DB>(g0, k_chunk0, part_stride, blockIdx.x, blockIdx.z, gridDim.z, smem);
+}
+
+// The balanced last wave of pt_gemm's host-count launches, decided from a
+// device row count: with T tiles on S CUs and R = T % S tail tiles (when
+// S < T < 4 S and at least two k-splits fit per tail tile), tiles [0, T - R)
+// run whole and the R tail tiles split K s2 = S / R ways (chunks of kc,
+// rounded to the k-step), their partials tile-local in the workspace.  The
+// same arithmetic as the host's, so the same tiles, splits and sums.
+struct DTail {
+    int full, R, s2, kc;
+};
+__device__ __forceinline__ DTail dtail_plan(const GemmArgs& g, int S) {
+    const int count = ((g.M + BM - 1) / BM) * ((g.N + BN - 1) / BN);
+    const int ksteps = (g.K + BK - 1) / BK;
+    DTail p{count, 0, 1, g.K};
+    const int R = count % S;
+    int s2 = R ? S / R : 0;
+    if (s2 > ksteps / 2) s2 = ksteps / 2;
+    if (count > S && count < 4 * S && R != 0 && s2 >= 2) {
+        p.kc = (((g.K + s2 - 1) / s2 + BK - 1) / BK) * BK;
+        p.s2 = (g.K + p.kc - 1) / p.kc;
+        p.R = R;
+        p.full = count - R;
+    }
+    return p;
+}
+
+// A device-row-count product with its last wave balanced: workgroups
+// [0, full) take whole tiles (epilogue applied), the next R s2 take split
+// u / R of tail tile u % R (partials into part); the rest of the launch
+// (sized for the host's row bound plus one workgroup per CU) returns.
+// dtail_reduce_kernel sums the partials after it: the kernel boundary makes
+// them visible to every XCD, where a reduction by the last split to arrive
+// would need an agent-scope release per tail workgroup (an L2 write-back on
+// this GPU, measured slower than the unbalanced wave).
+template <bool AT, bool BT, int EPI>
+__global__ __launch_bounds__(NT) void gemm_f32_dma_dtail_kernel(const GemmArgs g0, float* __restrict__ part,
+                                                               int S) {
+    __shared__ __align__(16) float smem[dma_smem_floats<DMA_NS>()];
+    const DTail p = dtail_plan(gemm_shape(g0), S);
+    const int b = blockIdx.x;
+    if (b < p.full) {
+        GemmArgs f = g0;
+        f.tile0 = 0;
+        f.ntiles = p.full;
+        gemm_dma_tile<AT, BT, EPI, false, false>(f, g0.K, 0, b, 0, 1, smem);
+        return;
+    }
+    const int u = b - p.full;
+    if (u >= p.R * p.s2) return;
+    GemmArgs q = g0;
+    q.C = part;
+    q.tile0 = p.full;
+    q.ntiles = p.R;
+    q.tail_part = 1;
+    gemm_dma_tile<AT, BT, EPI, true, false>(q, p.kc, 0, u % p.R, u / p.R, p.s2, smem);
+}
+
+// The tail tiles of gemm_f32_dma_dtail_kernel: 16 workgroups per tail tile
+// (tile-major, so the launch's S * 16 workgroups past R * 16 return), each
+// thread one float4 of tile t: its s2 partials summed in split order through
+// the epilogue (tail_reduce_kernel's arithmetic, the plan taken from the
+// device row count).
+constexpr int DTAIL_RED_WG = BM * BN / 4 / 256;
+template <int EPI>
+__global__ __launch_bounds__(256) void dtail_reduce_kernel(const GemmArgs g0, const float* __restrict__ part,
+                                                           int S) {
+    const GemmArgs g = gemm_shape(g0);
+    const DTail p = dtail_plan(g, S);
+    const int t = blockIdx.x / DTAIL_RED_WG;
+    if (t >= p.R) return;
+    const int tn = (g.N + BN - 1) / BN, lt = p.full + t;
+    const int m0 = (lt / tn) * BM, n0 = (lt % tn) * BN;
+    {
+        const int e = 4 * ((blockIdx.x % DTAIL_RED_WG) * 256 + threadIdx.x);
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int z = 0; z < p.s2; ++z) {
+            const float4 w = *reinterpret_cast<const float4*>(part + ((long)z * p.R + t) * (BM * BN) + e);
+            v.x += w.x;
+            v.y += w.y;
+            v.z += w.z;
+            v.w += w.w;
+        }
+        const int m = m0 + e / BN, n = n0 + e % BN;
+        if (m < g.M) {
+            if (n < g.N) epi_store<EPI>(g, m, n, v.x);
+            if (n + 1 < g.N) epi_store<EPI>(g, m, n + 1, v.y);
+            if (n + 2 < g.N) epi_store<EPI>(g, m, n + 2, v.z);
+            if (n + 3 < g.N) epi_store<EPI>(g, m, n + 3, v.w);
+        }
+    }
 }
 
 // ---------------------------------------------------------------- residual + LayerNorm
@@ -1223,11 +1319,12 @@ __global__ __launch_bounds__(NT) void gemm_dx_lnbwd_kernel(const GemmArgs g0, co
 template <bool AT, bool BT, int EPI, bool PARTIAL>
 __global__ __launch_bounds__(NT) void gemm_f32_dma_grouped_kernel(const GroupedGemm* __restrict__ gs,
                                                                   const int* __restrict__ item_group) {
+    __shared__ __align__(16) float smem[dma_smem_floats<DMA_NS>()];
     const int gi = __builtin_amdgcn_readfirstlane(item_group[blockIdx.x]);
     const int local = (int)blockIdx.x - gs[gi].first;
     const int tiles = gs[gi].tiles;
     gemm_dma_tile<AT, BT, EPI, PARTIAL, false>(gs[gi].g, gs[gi].k_chunk, gs[gi].part_stride, local % tiles,
-                                               local / tiles, gs[gi].splits);
+                                               local / tiles, gs[gi].splits, smem);
 }
 
 // Fixed-order sums of grouped split-K partials: chunk c covers 1024
@@ -1375,8 +1472,9 @@ __global__ __launch_bounds__(NT) void gemm_bf16_kernel(const GemmArgs g0, int k_
 constexpr int BF_NS = 3;
 template <bool AT, bool BT, int EPI, bool PARTIAL, bool DB>
 __global__ __launch_bounds__(NT) void gemm_bf16_k16_kernel(const GemmArgs g0, int k_chunk0, long part_stride) {
+    __shared__ __align__(16) float smem[dma_smem_floats<BF_NS>()];
     gemm_dma_tile<AT, BT, EPI, PARTIAL, DB, true, BF_NS>(g0, k_chunk0, part_stride, blockIdx.x, blockIdx.z,
-                                                         gridDim.z);
+                                                         gridDim.z, smem);
 }
 
 // ---------------------------------------------------------------- bf16 activations
@@ -2499,6 +2597,29 @@ int pt_dx_lnbwd(const GemmArgs& g, const float* x, const float* w, const float* 
                       ws_floats - (long)blocks * 2 * RL_N, s);
 }
 
+// the device-decided balanced last wave: gemm_f32_dma_dtail_kernel, then
+// dtail_reduce_kernel over its tail partials in ws
+template <bool AT, bool BT, int EPI>
+static void launch_dtail(const GemmArgs& g, int tiles, int S, float* ws, hipStream_t s) {
+    const int slot = pt_prof_open(s);
+    hipLaunchKernelGGL((gemm_f32_dma_dtail_kernel<AT, BT, EPI>), dim3(tiles + S), dim3(NT), 0, s, g, ws, S);
+    pt_prof_close(slot, g_gemm_class, launch_flops(g), s);
+    hipLaunchKernelGGL(dtail_reduce_kernel<EPI>, dim3(S * DTAIL_RED_WG), dim3(256), 0, s, g, (const float*)ws, S);
+}
+// the forward products (B not transposed) of the device-row-count layouts:
+// in the backward the weight gradients on the side stream fill the CUs an
+// unbalanced dX wave leaves idle (balancing them too measured no faster);
+// false: not this product, nothing launched
+static bool try_dtail(const GemmArgs& g, int tiles, int S, float* ws, hipStream_t s) {
+    if (g.a_t || g.b_t) return false;
+    switch (g.epi) {
+        case EPI_BIAS: launch_dtail<false, false, EPI_BIAS>(g, tiles, S, ws, s); return true;
+        case EPI_BIAS_RESID: launch_dtail<false, false, EPI_BIAS_RESID>(g, tiles, S, ws, s); return true;
+        case EPI_BIAS_GELU_D: launch_dtail<false, false, EPI_BIAS_GELU_D>(g, tiles, S, ws, s); return true;
+        default: return false;
+    }
+}
+
 int pt_gemm(const GemmArgs& g0, float* ws, long ws_floats, hipStream_t s) {
     GemmArgs g = g0;
     PT_REQUIRE(g.M > 0 && g.N > 0 && g.K > 0, "gemm: empty shape %d x %d x %d", g.M, g.N, g.K);
@@ -2604,6 +2725,17 @@ int pt_gemm(const GemmArgs& g0, float* ws, long ws_floats, hipStream_t s) {
         }
         PT_LAUNCH_CHECK();
         return PTCG_OK;
+    }
+    // A device row count: the same balancing decided in the launches from the
+    // count (whole tiles and tail partials, then the partials' fixed-order
+    // sums through the epilogue), where the host's row bound allows a tail
+    // (S < T) and leaves fewer than 8 tiles per CU
+    if (g.Mdev && !g.Kdev && !db && !bf && g.dma && vec && ws != nullptr) {
+        const int S = pt_cu_count();
+        if (S > 0 && tiles > S && tiles < 8 * S && (long)S * BM * BN <= ws_floats && try_dtail(g, tiles, S, ws, s)) {
+            PT_LAUNCH_CHECK();
+            return PTCG_OK;
+        }
     }
     // Balance the last wave: with T tiles on S CUs, T % S tail tiles would run
     // as a partial wave (e.g. 584 tiles = 2.28 per CU: the CUs holding 3 set

@@ -122,10 +122,12 @@ DEV_ROWS_CASES = [
 @pytest.mark.parametrize("rows,N,K,b_t,epi", DEV_ROWS_CASES)
 def test_gemm_device_rows(rows, N, K, b_t, epi, cuda):
     """A launch sized for a row bound that computes the device count's rows
-    (the sync-free model's form: every tile in one pass over K) against
-    float64, and against the host-count launch of the same rows to fp32
-    accumulation-order accuracy (that one balances its last wave with a
-    split-K tail); rows past the count keep their contents."""
+    (the sync-free model's form) against float64; rows past the count keep
+    their contents.  With B not transposed it balances its last wave from
+    the device count as the host-count launch does (same tiles, K splits and
+    partial-sum order): the same bits where the host count runs unsplit (at
+    least 512 tiles); otherwise (dX layouts: one pass over K per tile) fp32
+    accumulation-order agreement with the host-count launch."""
     bound = rows + 3000
     g = torch.Generator().manual_seed(rows + K + epi)
     A = torch.randn(bound, K, generator=g)
@@ -163,6 +165,10 @@ def test_gemm_device_rows(rows, N, K, b_t, epi, cuda):
     assert rel_l2(got, hC.cpu().double()) < 5e-6
     if ref2 is not None:
         assert rel_l2(dC2[:rows].cpu().double(), hC2.cpu().double()) < 5e-6
+    if not b_t and ((rows + 127) // 128) * ((N + 127) // 128) >= 512:
+        assert torch.equal(dC[:rows], hC)
+        if ref2 is not None:
+            assert torch.equal(dC2[:rows], hC2)
 
 
 def test_gemm_operand_not_16b_aligned(cuda):

@@ -132,11 +132,12 @@ struct PtcgModel {
     // latest block done (wg_rec: recorded in this backward); ws2 is the side
     // stream's split-K workspace; wg_serial (set per backward while a launch
     // profile is open) keeps them on the main stream, so that every timed
-    // launch runs alone
+    // launch runs alone.  The heads' and trunk input's weight gradients go to
+    // the side stream too (ldw_side), wg_ev[5] marking the latest of them.
     hipStream_t wg_s = nullptr;
     bool wg_serial = false;
-    hipEvent_t wg_ev[5] = {};
-    bool wg_rec[5] = {};
+    hipEvent_t wg_ev[6] = {};
+    bool wg_rec[6] = {};
     float* ws2 = nullptr;
     long ws2_floats = 0;
     // the trunk attention backward's dS scratch (training only)
@@ -329,6 +330,18 @@ static int wg_done(PtcgModel* m, int e) {
 static int wg_after(PtcgModel* m, int e, hipStream_t s) {
     if (m->wg_rec[e]) PT_HIP(hipStreamWaitEvent(s, m->wg_ev[e], 0));
     return PTCG_OK;
+}
+
+// A weight gradient of the heads or the trunk input on the side stream,
+// forked once its dY is written (the main stream goes on with the dX
+// product and what follows it); its dY and X are not rewritten later in the
+// backward, and the backward joins wg_ev[5] before it returns
+static int ldw_side(PtcgModel* m, const float* dY, long lddy, const float* X, long ldxx, float* dW, float* db,
+                    int rows, int in, int out, hipStream_t s, const int* Kdev = nullptr) {
+    if (m->wg_serial) return ldw_(m, dY, lddy, X, ldxx, dW, db, rows, in, out, s, Kdev);
+    PT_TRY(wg_fork(m, s));
+    PT_TRY(ldw_(m, dY, lddy, X, ldxx, dW, db, rows, in, out, m->wg_s, Kdev, true));
+    return wg_done(m, 5);
 }
 
 // refresh the blocks' bf16 weight copies from the fp32 masters
@@ -1258,7 +1271,7 @@ extern "C" int ptcg_model_backward(PtcgModel* m, const float* grad, void* stream
         PT_TRY(pt_head_dot_dw(grad, 1, NO + 1, NO, m->v1a, N, PT_VAL_H, m->G(m->v2_w), m->G(m->v2_b), m->ws,
                               m->ws_floats, s));
         PT_TRY(pt_head_dot_bwd(grad, 1, NO + 1, NO, m->v2_w, m->v1, m->dv1, N, PT_VAL_H, s));
-        PT_TRY(ldw_(m, m->dv1, PT_VAL_H, m->val_in, x.val_in, m->G(m->v1_w), m->G(m->v1_b), N, x.val_in, PT_VAL_H, s));
+        PT_TRY(ldw_side(m, m->dv1, PT_VAL_H, m->val_in, x.val_in, m->G(m->v1_w), m->G(m->v1_b), N, x.val_in, PT_VAL_H, s));
         PT_TRY(ldx_(m, m->dv1, PT_VAL_H, m->v1_w, m->dvin, x.val_in, N, x.val_in, PT_VAL_H, EPI_STORE, nullptr, 0, s));
         PT_TRY(pt_val_in_bwd(c, m->dvin, m->dxa, m->dgd, s));
     }
@@ -1267,21 +1280,21 @@ extern "C" int ptcg_model_backward(PtcgModel* m, const float* grad, void* stream
     PT_TRY(pt_head_dot_dw(grad, NO, NO + 1, 0, m->s1a, NJo, PT_SC_H, m->G(m->s2_w), m->G(m->s2_b), m->ws,
                           m->ws_floats, s, om, Od));
     PT_TRY(pt_head_dot_bwd(grad, NO, NO + 1, 0, m->s2_w, m->s1, m->ds1, NJo, PT_SC_H, s, om, Od));
-    PT_TRY(ldw_(m, m->ds1, PT_SC_H, m->sc_in, x.score_in, m->G(m->s1_w), m->G(m->s1_b), NJo, x.score_in, PT_SC_H, s,
+    PT_TRY(ldw_side(m, m->ds1, PT_SC_H, m->sc_in, x.score_in, m->G(m->s1_w), m->G(m->s1_b), NJo, x.score_in, PT_SC_H, s,
                 Od));
     PT_TRY(ldx_(m, m->ds1, PT_SC_H, m->s1_w, m->dsc, x.score_in, NJo, x.score_in, PT_SC_H, EPI_STORE, nullptr, 0, s,
                 Od));
     PT_TRY(pt_sc_in_bwd(c, m->dsc, m->sc_in, m->dq, m->dxa, m->dgd, s));
-    PT_TRY(ldw_(m, m->dq, D, m->q1a, D, m->G(m->q2_w), m->G(m->q2_b), NJo, D, D, s, Od));
+    PT_TRY(ldw_side(m, m->dq, D, m->q1a, D, m->G(m->q2_w), m->G(m->q2_b), NJo, D, D, s, Od));
     PT_TRY(ldx_(m, m->dq, D, m->q2_w, m->dq1, D, NJo, D, D, EPI_MUL, m->q1, D, s, Od));
-    PT_TRY(ldw_(m, m->dq1, D, m->q_in, x.q_in, m->G(m->q1_w), m->G(m->q1_b), NJo, x.q_in, D, s, Od));
+    PT_TRY(ldw_side(m, m->dq1, D, m->q_in, x.q_in, m->G(m->q1_w), m->G(m->q1_b), NJo, x.q_in, D, s, Od));
     PT_TRY(ldx_(m, m->dq1, D, m->q1_w, m->dqin, x.q_in, NJo, x.q_in, D, EPI_STORE, nullptr, 0, s, Od));
     const int oc0 = PT_TYPE_E + 2 * D, oa0 = oc0 + PT_OPT_E;
-    PT_TRY(ldw_(m, m->dqin + oc0, x.q_in, m->ocard, d.d_c, m->G(m->oc_w), m->G(m->oc_b), NJo, d.d_c, PT_OPT_E, s,
+    PT_TRY(ldw_side(m, m->dqin + oc0, x.q_in, m->ocard, d.d_c, m->G(m->oc_w), m->G(m->oc_b), NJo, d.d_c, PT_OPT_E, s,
                 Od));
     PT_TRY(ldx_(m, m->dqin + oc0, x.q_in, m->oc_w, m->docard, d.d_c, NJo, d.d_c, PT_OPT_E, EPI_STORE, nullptr, 0, s,
                 Od));
-    PT_TRY(ldw_(m, m->dqin + oa0, x.q_in, m->oatt, d.d_a, m->G(m->oa_w), m->G(m->oa_b), NJo, d.d_a, PT_OPT_E, s,
+    PT_TRY(ldw_side(m, m->dqin + oa0, x.q_in, m->oatt, d.d_a, m->G(m->oa_w), m->G(m->oa_b), NJo, d.d_a, PT_OPT_E, s,
                 Od));
     PT_TRY(ldx_(m, m->dqin + oa0, x.q_in, m->oa_w, m->doatt, d.d_a, NJo, d.d_a, PT_OPT_E, EPI_STORE, nullptr, 0, s,
                 Od));
@@ -1320,14 +1333,14 @@ extern "C" int ptcg_model_backward(PtcgModel* m, const float* grad, void* stream
     } else {
         PT_TRY(pt_colsum(m->dxb, (long)x.l_seq * D, N, D, m->G(m->readout), m->ws, m->ws_floats, s));
     }
-    PT_TRY(ldw_(m, m->dtokp, D, m->tok_cat, x.tok_in, m->G(m->tp_w), m->G(m->tp_b), tok_rows, x.tok_in, D, s, Td));
+    PT_TRY(ldw_side(m, m->dtokp, D, m->tok_cat, x.tok_in, m->G(m->tp_w), m->G(m->tp_b), tok_rows, x.tok_in, D, s, Td));
     PT_TRY(ldx_(m, m->dtokp, D, m->tp_w, m->dtokcat, x.tok_in, tok_rows, x.tok_in, D, EPI_STORE, nullptr, 0, s, Td));
-    PT_TRY(ldw_(m, m->dbc, D, m->gd, x.bcast_in, m->G(m->bc_w), m->G(m->bc_b), N, x.bcast_in, D, s));
+    PT_TRY(ldw_side(m, m->dbc, D, m->gd, x.bcast_in, m->G(m->bc_w), m->G(m->bc_b), N, x.bcast_in, D, s));
     PT_TRY(ldx_(m, m->dbc, D, m->bc_w, m->dgd, x.bcast_in, N, x.bcast_in, D, EPI_ACCUM, nullptr, 0, s));
     // decision MLP (d_dvec = dgd[:, G:])
-    PT_TRY(ldw_(m, m->dgd + G, x.bcast_in, m->d1a, PT_DEC_H, m->G(m->d2_w), m->G(m->d2_b), N, PT_DEC_H, PT_DEC_H, s));
+    PT_TRY(ldw_side(m, m->dgd + G, x.bcast_in, m->d1a, PT_DEC_H, m->G(m->d2_w), m->G(m->d2_b), N, PT_DEC_H, PT_DEC_H, s));
     PT_TRY(ldx_(m, m->dgd + G, x.bcast_in, m->d2_w, m->dd1, PT_DEC_H, N, PT_DEC_H, PT_DEC_H, EPI_MUL, m->d1, PT_DEC_H, s));
-    PT_TRY(ldw_(m, m->dd1, PT_DEC_H, m->dec_in, x.dec_in, m->G(m->d1_w), m->G(m->d1_b), N, x.dec_in, PT_DEC_H, s));
+    PT_TRY(ldw_side(m, m->dd1, PT_DEC_H, m->dec_in, x.dec_in, m->G(m->d1_w), m->G(m->d1_b), N, x.dec_in, PT_DEC_H, s));
     PT_TRY(ldx_(m, m->dd1, PT_DEC_H, m->d1_w, m->ddec, x.dec_in, N, x.dec_in, PT_DEC_H, EPI_STORE, nullptr, 0, s));
     // token rows (card, tool cards, zone, owner) and decision slots (select
     // type, context, card, attack) into their tables
@@ -1363,9 +1376,9 @@ extern "C" int ptcg_model_backward(PtcgModel* m, const float* grad, void* stream
         PT_TRY(pt_det_finish(m->det, S, s));
     }
     // global MLP (d_g = dgd[:, :G])
-    PT_TRY(ldw_(m, m->dgd, x.bcast_in, m->g1a, G, m->G(m->g2_w), m->G(m->g2_b), N, G, G, s));
+    PT_TRY(ldw_side(m, m->dgd, x.bcast_in, m->g1a, G, m->G(m->g2_w), m->G(m->g2_b), N, G, G, s));
     PT_TRY(ldx_(m, m->dgd, x.bcast_in, m->g2_w, m->dg1, G, N, G, G, EPI_MUL, m->g1, G, s));
-    PT_TRY(ldw_(m, m->dg1, G, m->glob_in, d.global_f, m->G(m->g1_w), m->G(m->g1_b), N, d.global_f, G, s));
+    PT_TRY(ldw_side(m, m->dg1, G, m->glob_in, d.global_f, m->G(m->g1_w), m->G(m->g1_b), N, d.global_f, G, s));
     if (d.tables == 1) PT_TRY(tables_bwd(m, s));
-    return PTCG_OK;
+    return wg_after(m, 5, s);   // join: the heads' and trunk input's weight gradients are done
 }

@@ -312,12 +312,22 @@ static int bldw(PtcgModel* m, const float* dY, int out, const float* X, int in, 
     return pt_gemm(g, m->ws2, m->ws2_floats, s);
 }
 
-// side-stream ordering: fork = the side stream waits for the main stream's
-// work so far; done(e) = mark the side stream's work so far as event e;
-// after(e) = the main stream waits for event e (if this backward recorded it)
-static int wg_fork(PtcgModel* m, hipStream_t s) {
+// side-stream ordering: mark = record the main stream's work so far;
+// take = the side stream waits for the last mark; done(e) = mark the side
+// stream's work so far as event e; after(e) = the main stream waits for
+// event e (if this backward recorded it).  A weight gradient is marked once
+// its dY exists, and taken after the main stream's next product is enqueued:
+// the same dependencies, but in a captured step the dX product is the first
+// child of the node before it, which is the one graph replay keeps on that
+// node's queue (captured the other way round, the replays ran the dX product
+// after the weight gradient on one queue)
+static int wg_mark(PtcgModel* m, hipStream_t s) {
     if (m->wg_serial) return PTCG_OK;
     PT_HIP(hipEventRecord(m->wg_ev[0], s));
+    return PTCG_OK;
+}
+static int wg_take(PtcgModel* m) {
+    if (m->wg_serial) return PTCG_OK;
     PT_HIP(hipStreamWaitEvent(m->wg_s, m->wg_ev[0], 0));
     return PTCG_OK;
 }
@@ -333,13 +343,13 @@ static int wg_after(PtcgModel* m, int e, hipStream_t s) {
 }
 
 // A weight gradient of the heads or the trunk input on the side stream,
-// forked once its dY is written (the main stream goes on with the dX
-// product and what follows it); its dY and X are not rewritten later in the
-// backward, and the backward joins wg_ev[5] before it returns
+// after the last wg_mark (placed once its dY is written; the main stream's
+// dX product is enqueued between the two); its dY and X are not rewritten
+// later in the backward, and the backward joins wg_ev[5] before it returns
 static int ldw_side(PtcgModel* m, const float* dY, long lddy, const float* X, long ldxx, float* dW, float* db,
                     int rows, int in, int out, hipStream_t s, const int* Kdev = nullptr) {
     if (m->wg_serial) return ldw_(m, dY, lddy, X, ldxx, dW, db, rows, in, out, s, Kdev);
-    PT_TRY(wg_fork(m, s));
+    PT_TRY(wg_take(m));
     PT_TRY(ldw_(m, dY, lddy, X, ldxx, dW, db, rows, in, out, m->wg_s, Kdev, true));
     return wg_done(m, 5);
 }
@@ -1083,56 +1093,66 @@ static int block_bwd(PtcgModel* m, const BlockP& w, const BlockA& a, int L, cons
     // block's FFN1 dW), dC (its out-projection dW), dqkv (its QKV dW) and dA
     // (this block's FFN2 dW).
     hipStream_t s2 = m->wg_serial ? s : m->wg_s;
+    // each weight gradient: marked where its dY is complete, taken after the
+    // main stream's next product (see wg_mark)
     if (bw) {
-        PT_TRY(wg_fork(m, s));
-        PT_TRY(bldw(m, m->dAh, D, a.ffa, d.ffn, m->G(w.f2w), m->G(w.f2b), NL, s2, Tr));
-        PT_TRY(wg_done(m, 1));
+        PT_TRY(wg_mark(m, s));
         PT_TRY(wg_after(m, 2, s));
         PT_TRY(blin(m, m->dAh, D, bw->f2T, nullptr, m->dffn, d.ffn, NL, EPI_MUL, true, a.ffp, nullptr, s, Tr));
-        PT_TRY(wg_fork(m, s));
-        PT_TRY(bldw(m, m->dffn, d.ffn, a.ln2, D, m->G(w.f1w), m->G(w.f1b), NL, s2, Tr));
-        PT_TRY(wg_done(m, 2));
+        PT_TRY(wg_take(m));
+        PT_TRY(bldw(m, m->dAh, D, a.ffa, d.ffn, m->G(w.f2w), m->G(w.f2b), NL, s2, Tr));
+        PT_TRY(wg_done(m, 1));
+        PT_TRY(wg_mark(m, s));
         PT_TRY(wg_after(m, 3, s));   // dC (the LayerNorm's dx) is read by the previous block's dW
         PT_TRY(blin_dx_lnbwd(m, m->dffn, d.ffn, bw->f1T, NL, a.xmid, w.ln2w, a.mu2, a.rs2, dA, dC, m->G(w.ln2w),
                              m->G(w.ln2b), m->dCh, s, Tr));
-        PT_TRY(wg_fork(m, s));
+        PT_TRY(wg_take(m));
+        PT_TRY(bldw(m, m->dffn, d.ffn, a.ln2, D, m->G(w.f1w), m->G(w.f1b), NL, s2, Tr));
+        PT_TRY(wg_done(m, 2));
+        PT_TRY(wg_mark(m, s));
+        PT_TRY(blin(m, m->dCh, D, bw->projT, nullptr, m->dctx, D, NL, EPI_STORE, true, nullptr, nullptr, s, Tr));
+        PT_TRY(wg_take(m));
         PT_TRY(bldw(m, m->dCh, D, a.ctx, D, m->G(w.projw), m->G(w.projb), NL, s2, Tr));
         PT_TRY(wg_done(m, 3));
-        PT_TRY(blin(m, m->dCh, D, bw->projT, nullptr, m->dctx, D, NL, EPI_STORE, true, nullptr, nullptr, s, Tr));
         PT_TRY(wg_after(m, 4, s));
         PT_TRY(pt_attn_bwd(a.qkv, keep, a.ctx, a.lse, m->dctx, m->dqkv, m->N, L, d.heads, m->dx.dh, s, coff, 2,
                            m->attn_ws, m->attn_ws_bytes));
-        PT_TRY(wg_fork(m, s));
-        PT_TRY(bldw(m, m->dqkv, 3 * D, a.ln1, D, m->G(w.qkvw), m->G(w.qkvb), NL, s2, Tr));
-        PT_TRY(wg_done(m, 4));
+        PT_TRY(wg_mark(m, s));
         PT_TRY(wg_after(m, 1, s));   // dA and dAh are read by this block's FFN2 dW
         PT_TRY(blin_dx_lnbwd(m, m->dqkv, 3 * D, bw->qkvT, NL, xin, w.ln1w, a.mu1, a.rs1, dC, dA, m->G(w.ln1w),
                              m->G(w.ln1b), m->dAh, s, Tr));
+        PT_TRY(wg_take(m));
+        PT_TRY(bldw(m, m->dqkv, 3 * D, a.ln1, D, m->G(w.qkvw), m->G(w.qkvb), NL, s2, Tr));
+        PT_TRY(wg_done(m, 4));
         return PTCG_OK;
     }
-    PT_TRY(wg_fork(m, s));
-    PT_TRY(ldw_(m, dA, D, a.ffa, d.ffn, m->G(w.f2w), m->G(w.f2b), NL, d.ffn, D, s2, Tr, true));
-    PT_TRY(wg_done(m, 1));
+    PT_TRY(wg_mark(m, s));
     PT_TRY(wg_after(m, 2, s));
     PT_TRY(ldx_(m, dA, D, w.f2w, m->dffn, d.ffn, NL, d.ffn, D, EPI_MUL, a.ffp, d.ffn, s, Tr));
-    PT_TRY(wg_fork(m, s));
+    PT_TRY(wg_take(m));
+    PT_TRY(ldw_(m, dA, D, a.ffa, d.ffn, m->G(w.f2w), m->G(w.f2b), NL, d.ffn, D, s2, Tr, true));
+    PT_TRY(wg_done(m, 1));
+    PT_TRY(wg_mark(m, s));
+    PT_TRY(ldx_(m, m->dffn, d.ffn, w.f1w, m->dln, D, NL, D, d.ffn, EPI_STORE, nullptr, 0, s, Tr));
+    PT_TRY(wg_take(m));
     PT_TRY(ldw_(m, m->dffn, d.ffn, a.ln2, D, m->G(w.f1w), m->G(w.f1b), NL, D, d.ffn, s2, Tr, true));
     PT_TRY(wg_done(m, 2));
-    PT_TRY(ldx_(m, m->dffn, d.ffn, w.f1w, m->dln, D, NL, D, d.ffn, EPI_STORE, nullptr, 0, s, Tr));
     PT_TRY(wg_after(m, 3, s));
     PT_TRY(pt_ln_bwd(m->dln, D, a.xmid, D, w.ln2w, a.mu2, a.rs2, dA, D, dC, D, m->G(w.ln2w),
                      m->G(w.ln2b), NL, D, m->ws, m->ws_floats, s, Tr));
-    PT_TRY(wg_fork(m, s));
+    PT_TRY(wg_mark(m, s));
+    PT_TRY(ldx_(m, dC, D, w.projw, m->dctx, D, NL, D, D, EPI_STORE, nullptr, 0, s, Tr));
+    PT_TRY(wg_take(m));
     PT_TRY(ldw_(m, dC, D, a.ctx, D, m->G(w.projw), m->G(w.projb), NL, D, D, s2, Tr, true));
     PT_TRY(wg_done(m, 3));
-    PT_TRY(ldx_(m, dC, D, w.projw, m->dctx, D, NL, D, D, EPI_STORE, nullptr, 0, s, Tr));
     PT_TRY(wg_after(m, 4, s));
     PT_TRY(pt_attn_bwd(a.qkv, keep, a.ctx, a.lse, m->dctx, m->dqkv, m->N, L, d.heads, m->dx.dh, s, coff, m->prec,
                        m->attn_ws, m->attn_ws_bytes));
-    PT_TRY(wg_fork(m, s));
+    PT_TRY(wg_mark(m, s));
+    PT_TRY(ldx_(m, m->dqkv, 3 * D, w.qkvw, m->dln, D, NL, D, 3 * D, EPI_STORE, nullptr, 0, s, Tr));
+    PT_TRY(wg_take(m));
     PT_TRY(ldw_(m, m->dqkv, 3 * D, a.ln1, D, m->G(w.qkvw), m->G(w.qkvb), NL, D, 3 * D, s2, Tr, true));
     PT_TRY(wg_done(m, 4));
-    PT_TRY(ldx_(m, m->dqkv, 3 * D, w.qkvw, m->dln, D, NL, D, 3 * D, EPI_STORE, nullptr, 0, s, Tr));
     PT_TRY(wg_after(m, 1, s));
     PT_TRY(pt_ln_bwd(m->dln, D, xin, D, w.ln1w, a.mu1, a.rs1, dC, D, dA, D, m->G(w.ln1w),
                      m->G(w.ln1b), NL, D, m->ws, m->ws_floats, s, Tr));
@@ -1271,8 +1291,9 @@ extern "C" int ptcg_model_backward(PtcgModel* m, const float* grad, void* stream
         PT_TRY(pt_head_dot_dw(grad, 1, NO + 1, NO, m->v1a, N, PT_VAL_H, m->G(m->v2_w), m->G(m->v2_b), m->ws,
                               m->ws_floats, s));
         PT_TRY(pt_head_dot_bwd(grad, 1, NO + 1, NO, m->v2_w, m->v1, m->dv1, N, PT_VAL_H, s));
-        PT_TRY(ldw_side(m, m->dv1, PT_VAL_H, m->val_in, x.val_in, m->G(m->v1_w), m->G(m->v1_b), N, x.val_in, PT_VAL_H, s));
+        PT_TRY(wg_mark(m, s));
         PT_TRY(ldx_(m, m->dv1, PT_VAL_H, m->v1_w, m->dvin, x.val_in, N, x.val_in, PT_VAL_H, EPI_STORE, nullptr, 0, s));
+        PT_TRY(ldw_side(m, m->dv1, PT_VAL_H, m->val_in, x.val_in, m->G(m->v1_w), m->G(m->v1_b), N, x.val_in, PT_VAL_H, s));
         PT_TRY(pt_val_in_bwd(c, m->dvin, m->dxa, m->dgd, s));
     }
 
@@ -1280,23 +1301,28 @@ extern "C" int ptcg_model_backward(PtcgModel* m, const float* grad, void* stream
     PT_TRY(pt_head_dot_dw(grad, NO, NO + 1, 0, m->s1a, NJo, PT_SC_H, m->G(m->s2_w), m->G(m->s2_b), m->ws,
                           m->ws_floats, s, om, Od));
     PT_TRY(pt_head_dot_bwd(grad, NO, NO + 1, 0, m->s2_w, m->s1, m->ds1, NJo, PT_SC_H, s, om, Od));
-    PT_TRY(ldw_side(m, m->ds1, PT_SC_H, m->sc_in, x.score_in, m->G(m->s1_w), m->G(m->s1_b), NJo, x.score_in, PT_SC_H, s,
-                Od));
+    PT_TRY(wg_mark(m, s));
     PT_TRY(ldx_(m, m->ds1, PT_SC_H, m->s1_w, m->dsc, x.score_in, NJo, x.score_in, PT_SC_H, EPI_STORE, nullptr, 0, s,
                 Od));
-    PT_TRY(pt_sc_in_bwd(c, m->dsc, m->sc_in, m->dq, m->dxa, m->dgd, s));
-    PT_TRY(ldw_side(m, m->dq, D, m->q1a, D, m->G(m->q2_w), m->G(m->q2_b), NJo, D, D, s, Od));
-    PT_TRY(ldx_(m, m->dq, D, m->q2_w, m->dq1, D, NJo, D, D, EPI_MUL, m->q1, D, s, Od));
-    PT_TRY(ldw_side(m, m->dq1, D, m->q_in, x.q_in, m->G(m->q1_w), m->G(m->q1_b), NJo, x.q_in, D, s, Od));
-    PT_TRY(ldx_(m, m->dq1, D, m->q1_w, m->dqin, x.q_in, NJo, x.q_in, D, EPI_STORE, nullptr, 0, s, Od));
-    const int oc0 = PT_TYPE_E + 2 * D, oa0 = oc0 + PT_OPT_E;
-    PT_TRY(ldw_side(m, m->dqin + oc0, x.q_in, m->ocard, d.d_c, m->G(m->oc_w), m->G(m->oc_b), NJo, d.d_c, PT_OPT_E, s,
+    PT_TRY(ldw_side(m, m->ds1, PT_SC_H, m->sc_in, x.score_in, m->G(m->s1_w), m->G(m->s1_b), NJo, x.score_in, PT_SC_H, s,
                 Od));
+    PT_TRY(pt_sc_in_bwd(c, m->dsc, m->sc_in, m->dq, m->dxa, m->dgd, s));
+    PT_TRY(wg_mark(m, s));
+    PT_TRY(ldx_(m, m->dq, D, m->q2_w, m->dq1, D, NJo, D, D, EPI_MUL, m->q1, D, s, Od));
+    PT_TRY(ldw_side(m, m->dq, D, m->q1a, D, m->G(m->q2_w), m->G(m->q2_b), NJo, D, D, s, Od));
+    PT_TRY(wg_mark(m, s));
+    PT_TRY(ldx_(m, m->dq1, D, m->q1_w, m->dqin, x.q_in, NJo, x.q_in, D, EPI_STORE, nullptr, 0, s, Od));
+    PT_TRY(ldw_side(m, m->dq1, D, m->q_in, x.q_in, m->G(m->q1_w), m->G(m->q1_b), NJo, x.q_in, D, s, Od));
+    const int oc0 = PT_TYPE_E + 2 * D, oa0 = oc0 + PT_OPT_E;
+    PT_TRY(wg_mark(m, s));
     PT_TRY(ldx_(m, m->dqin + oc0, x.q_in, m->oc_w, m->docard, d.d_c, NJo, d.d_c, PT_OPT_E, EPI_STORE, nullptr, 0, s,
                 Od));
-    PT_TRY(ldw_side(m, m->dqin + oa0, x.q_in, m->oatt, d.d_a, m->G(m->oa_w), m->G(m->oa_b), NJo, d.d_a, PT_OPT_E, s,
+    PT_TRY(ldw_side(m, m->dqin + oc0, x.q_in, m->ocard, d.d_c, m->G(m->oc_w), m->G(m->oc_b), NJo, d.d_c, PT_OPT_E, s,
                 Od));
+    PT_TRY(wg_mark(m, s));
     PT_TRY(ldx_(m, m->dqin + oa0, x.q_in, m->oa_w, m->doatt, d.d_a, NJo, d.d_a, PT_OPT_E, EPI_STORE, nullptr, 0, s,
+                Od));
+    PT_TRY(ldw_side(m, m->dqin + oa0, x.q_in, m->oatt, d.d_a, m->G(m->oa_w), m->G(m->oa_b), NJo, d.d_a, PT_OPT_E, s,
                 Od));
     // option-type, card and attack table rows of the option rows, then the
     // pointer gradients into the trunk rows (q_in_bwd)
@@ -1333,15 +1359,19 @@ extern "C" int ptcg_model_backward(PtcgModel* m, const float* grad, void* stream
     } else {
         PT_TRY(pt_colsum(m->dxb, (long)x.l_seq * D, N, D, m->G(m->readout), m->ws, m->ws_floats, s));
     }
-    PT_TRY(ldw_side(m, m->dtokp, D, m->tok_cat, x.tok_in, m->G(m->tp_w), m->G(m->tp_b), tok_rows, x.tok_in, D, s, Td));
+    PT_TRY(wg_mark(m, s));
     PT_TRY(ldx_(m, m->dtokp, D, m->tp_w, m->dtokcat, x.tok_in, tok_rows, x.tok_in, D, EPI_STORE, nullptr, 0, s, Td));
-    PT_TRY(ldw_side(m, m->dbc, D, m->gd, x.bcast_in, m->G(m->bc_w), m->G(m->bc_b), N, x.bcast_in, D, s));
+    PT_TRY(ldw_side(m, m->dtokp, D, m->tok_cat, x.tok_in, m->G(m->tp_w), m->G(m->tp_b), tok_rows, x.tok_in, D, s, Td));
+    PT_TRY(wg_mark(m, s));
     PT_TRY(ldx_(m, m->dbc, D, m->bc_w, m->dgd, x.bcast_in, N, x.bcast_in, D, EPI_ACCUM, nullptr, 0, s));
+    PT_TRY(ldw_side(m, m->dbc, D, m->gd, x.bcast_in, m->G(m->bc_w), m->G(m->bc_b), N, x.bcast_in, D, s));
     // decision MLP (d_dvec = dgd[:, G:])
-    PT_TRY(ldw_side(m, m->dgd + G, x.bcast_in, m->d1a, PT_DEC_H, m->G(m->d2_w), m->G(m->d2_b), N, PT_DEC_H, PT_DEC_H, s));
+    PT_TRY(wg_mark(m, s));
     PT_TRY(ldx_(m, m->dgd + G, x.bcast_in, m->d2_w, m->dd1, PT_DEC_H, N, PT_DEC_H, PT_DEC_H, EPI_MUL, m->d1, PT_DEC_H, s));
-    PT_TRY(ldw_side(m, m->dd1, PT_DEC_H, m->dec_in, x.dec_in, m->G(m->d1_w), m->G(m->d1_b), N, x.dec_in, PT_DEC_H, s));
+    PT_TRY(ldw_side(m, m->dgd + G, x.bcast_in, m->d1a, PT_DEC_H, m->G(m->d2_w), m->G(m->d2_b), N, PT_DEC_H, PT_DEC_H, s));
+    PT_TRY(wg_mark(m, s));
     PT_TRY(ldx_(m, m->dd1, PT_DEC_H, m->d1_w, m->ddec, x.dec_in, N, x.dec_in, PT_DEC_H, EPI_STORE, nullptr, 0, s));
+    PT_TRY(ldw_side(m, m->dd1, PT_DEC_H, m->dec_in, x.dec_in, m->G(m->d1_w), m->G(m->d1_b), N, x.dec_in, PT_DEC_H, s));
     // token rows (card, tool cards, zone, owner) and decision slots (select
     // type, context, card, attack) into their tables
     {
@@ -1376,8 +1406,10 @@ extern "C" int ptcg_model_backward(PtcgModel* m, const float* grad, void* stream
         PT_TRY(pt_det_finish(m->det, S, s));
     }
     // global MLP (d_g = dgd[:, :G])
-    PT_TRY(ldw_side(m, m->dgd, x.bcast_in, m->g1a, G, m->G(m->g2_w), m->G(m->g2_b), N, G, G, s));
+    PT_TRY(wg_mark(m, s));
     PT_TRY(ldx_(m, m->dgd, x.bcast_in, m->g2_w, m->dg1, G, N, G, G, EPI_MUL, m->g1, G, s));
+    PT_TRY(ldw_side(m, m->dgd, x.bcast_in, m->g1a, G, m->G(m->g2_w), m->G(m->g2_b), N, G, G, s));
+    PT_TRY(wg_mark(m, s));
     PT_TRY(ldw_side(m, m->dg1, G, m->glob_in, d.global_f, m->G(m->g1_w), m->G(m->g1_b), N, d.global_f, G, s));
     if (d.tables == 1) PT_TRY(tables_bwd(m, s));
     return wg_after(m, 5, s);   // join: the heads' and trunk input's weight gradients are done

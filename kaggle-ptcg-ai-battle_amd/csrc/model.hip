@@ -134,10 +134,12 @@ struct PtcgModel {
     // profile is open) keeps them on the main stream, so that every timed
     // launch runs alone.  The heads' and trunk input's weight gradients go to
     // the side stream too (ldw_side), wg_ev[5] marking the latest of them.
+    // In a training forward wg_ev[6] / wg_ev[7] mark the side stream's global
+    // / decision MLPs and option-row projections (forward_side).
     hipStream_t wg_s = nullptr;
     bool wg_serial = false;
-    hipEvent_t wg_ev[6] = {};
-    bool wg_rec[6] = {};
+    hipEvent_t wg_ev[8] = {};
+    bool wg_rec[8] = {};
     float* ws2 = nullptr;
     long ws2_floats = 0;
     // the trunk attention backward's dS scratch (training only)
@@ -158,9 +160,10 @@ struct PtcgModel {
 };
 
 // ------------------------------------------------------------ helpers
-static int lin(const PtcgModel* m, const float* X, long ldx, const float* W, const float* b, float* Y, long ldy,
-               int rows, int in, int out, int epi, const float* R, long ldr, float* Y2, long ldy2,
-               hipStream_t s, const int* Mdev = nullptr) {
+// Y = epi(X W^T + b) with workspace ws for split-K / tail partials
+static int lin_ws(const PtcgModel* m, float* ws, long ws_floats, const float* X, long ldx, const float* W,
+                  const float* b, float* Y, long ldy, int rows, int in, int out, int epi, const float* R, long ldr,
+                  float* Y2, long ldy2, hipStream_t s, const int* Mdev = nullptr) {
     GemmArgs g{};
     g.prec = m->prec;
     g.Mdev = Mdev;
@@ -170,7 +173,12 @@ static int lin(const PtcgModel* m, const float* X, long ldx, const float* W, con
     g.C = Y; g.ldc = ldy;
     g.bias = b; g.R = R; g.ldr = ldr; g.C2 = Y2; g.ldc2 = ldy2;
     g.epi = epi;
-    return pt_gemm(g, m->ws, m->ws_floats, s);
+    return pt_gemm(g, ws, ws_floats, s);
+}
+static int lin(const PtcgModel* m, const float* X, long ldx, const float* W, const float* b, float* Y, long ldy,
+               int rows, int in, int out, int epi, const float* R, long ldr, float* Y2, long ldy2,
+               hipStream_t s, const int* Mdev = nullptr) {
+    return lin_ws(m, m->ws, m->ws_floats, X, ldx, W, b, Y, ldy, rows, in, out, epi, R, ldr, Y2, ldy2, s, Mdev);
 }
 static int linf(const PtcgModel* m, const float* X, const float* W, const float* b, float* Y, int rows, int in,
                 int out, int epi, const float* R, float* Y2, hipStream_t s, const int* Mdev = nullptr) {
@@ -884,16 +892,44 @@ extern "C" int ptcg_model_forward(PtcgModel* m, const float* obs, const int32_t*
     const int tok_rows = m->compact ? m->rows : N * Lt;
 
     if (d.tables == 1) PT_TRY(tables_fwd(m, s));
+    // The global / decision MLPs and the option rows' card / attack
+    // projections read only the observations and the tables: in a training
+    // forward (no launch profile open) they run on the side stream beside the
+    // token path and the trunk, on the side workspace ws2, marked before the
+    // token concat and taken after it is enqueued (see wg_mark), and joined
+    // where their outputs are read (bc: the trunk input; the projections:
+    // the option rows' q_in)
+    const bool fside = m->train && m->wg_s != nullptr && !pt_prof_active();
+    hipStream_t sf = fside ? m->wg_s : s;
+    float* fws = fside ? m->ws2 : m->ws;
+    const long fwsn = fside ? m->ws2_floats : m->ws_floats;
+    const int NJ = m->orows;
+    const int* Od = m->Odev;
+    const int oc0 = PT_TYPE_E + 2 * D, oa0 = oc0 + PT_OPT_E;
+    if (fside) PT_HIP(hipEventRecord(m->wg_ev[0], s));
     PT_TRY(pt_tok_cat_fwd(c, m->card, m->zemb, m->oemb, m->tok_cat, s, tok_rows));
+    if (fside) PT_HIP(hipStreamWaitEvent(m->wg_s, m->wg_ev[0], 0));
+    PT_TRY(pt_glob_in(c, m->glob_in, sf));
+    PT_TRY(lin_ws(m, fws, fwsn, m->glob_in, d.global_f, m->g1_w, m->g1_b, m->g1, G, N, d.global_f, G,
+                  EPI_BIAS_GELU_D, nullptr, G, m->g1a, G, sf));
+    PT_TRY(lin_ws(m, fws, fwsn, m->g1a, G, m->g2_w, m->g2_b, m->gd, x.bcast_in, N, G, G, EPI_BIAS, nullptr, 0,
+                  nullptr, 0, sf));
+    PT_TRY(pt_dec_in_fwd(c, m->card, m->att, m->semb, m->cemb, m->dec_in, sf));
+    PT_TRY(lin_ws(m, fws, fwsn, m->dec_in, x.dec_in, m->d1_w, m->d1_b, m->d1, PT_DEC_H, N, x.dec_in, PT_DEC_H,
+                  EPI_BIAS_GELU_D, nullptr, PT_DEC_H, m->d1a, PT_DEC_H, sf));
+    PT_TRY(lin_ws(m, fws, fwsn, m->d1a, PT_DEC_H, m->d2_w, m->d2_b, m->gd + G, x.bcast_in, N, PT_DEC_H, PT_DEC_H,
+                  EPI_BIAS, nullptr, 0, nullptr, 0, sf));
+    PT_TRY(lin_ws(m, fws, fwsn, m->gd, x.bcast_in, m->bc_w, m->bc_b, m->bc, D, N, x.bcast_in, D, EPI_BIAS, nullptr,
+                  0, nullptr, 0, sf));
+    if (fside) PT_HIP(hipEventRecord(m->wg_ev[6], m->wg_s));
+    PT_TRY(pt_opt_gather_fwd(c, m->card, m->att, m->ocard, m->oatt, sf));
+    PT_TRY(lin_ws(m, fws, fwsn, m->ocard, d.d_c, m->oc_w, m->oc_b, m->q_in + oc0, x.q_in, NJ, d.d_c, PT_OPT_E,
+                  EPI_BIAS, nullptr, 0, nullptr, 0, sf, Od));
+    PT_TRY(lin_ws(m, fws, fwsn, m->oatt, d.d_a, m->oa_w, m->oa_b, m->q_in + oa0, x.q_in, NJ, d.d_a, PT_OPT_E,
+                  EPI_BIAS, nullptr, 0, nullptr, 0, sf, Od));
+    if (fside) PT_HIP(hipEventRecord(m->wg_ev[7], m->wg_s));
     PT_TRY(linf(m, m->tok_cat, m->tp_w, m->tp_b, m->tokp, tok_rows, x.tok_in, D, EPI_BIAS, nullptr, nullptr, s, Td));
-    PT_TRY(pt_glob_in(c, m->glob_in, s));
-    PT_TRY(linf(m, m->glob_in, m->g1_w, m->g1_b, m->g1, N, d.global_f, G, EPI_BIAS_GELU_D, nullptr, m->g1a, s));
-    PT_TRY(lin(m, m->g1a, G, m->g2_w, m->g2_b, m->gd, x.bcast_in, N, G, G, EPI_BIAS, nullptr, 0, nullptr, 0, s));
-    PT_TRY(pt_dec_in_fwd(c, m->card, m->att, m->semb, m->cemb, m->dec_in, s));
-    PT_TRY(linf(m, m->dec_in, m->d1_w, m->d1_b, m->d1, N, x.dec_in, PT_DEC_H, EPI_BIAS_GELU_D, nullptr, m->d1a, s));
-    PT_TRY(lin(m, m->d1a, PT_DEC_H, m->d2_w, m->d2_b, m->gd + G, x.bcast_in, N, PT_DEC_H, PT_DEC_H, EPI_BIAS,
-               nullptr, 0, nullptr, 0, s));
-    PT_TRY(lin(m, m->gd, x.bcast_in, m->bc_w, m->bc_b, m->bc, D, N, x.bcast_in, D, EPI_BIAS, nullptr, 0, nullptr, 0, s));
+    if (fside) PT_HIP(hipStreamWaitEvent(s, m->wg_ev[6], 0));   // bc for the trunk input
     const bool tr = m->train;
     const bool b16 = m->prec == 1;
     // at d = 256 the first block's LayerNorm 1 runs inside the trunk-input assembly
@@ -921,15 +957,9 @@ extern "C" int ptcg_model_forward(PtcgModel* m, const float* obs, const int32_t*
     }
     const int NL = N * x.l_seq;
 
-    // option scorer over the option rows (all N * n_opt, or the legal ones)
-    const int NJ = m->orows;
-    const int* Od = m->Odev;
-    const int oc0 = PT_TYPE_E + 2 * D, oa0 = oc0 + PT_OPT_E;
-    PT_TRY(pt_opt_gather_fwd(c, m->card, m->att, m->ocard, m->oatt, s));
-    PT_TRY(lin(m, m->ocard, d.d_c, m->oc_w, m->oc_b, m->q_in + oc0, x.q_in, NJ, d.d_c, PT_OPT_E, EPI_BIAS,
-               nullptr, 0, nullptr, 0, s, Od));
-    PT_TRY(lin(m, m->oatt, d.d_a, m->oa_w, m->oa_b, m->q_in + oa0, x.q_in, NJ, d.d_a, PT_OPT_E, EPI_BIAS,
-               nullptr, 0, nullptr, 0, s, Od));
+    // option scorer over the option rows (all N * n_opt, or the legal ones);
+    // their card / attack projections ran above (side stream: joined here)
+    if (fside) PT_HIP(hipStreamWaitEvent(s, m->wg_ev[7], 0));
     PT_TRY(pt_q_in_fwd(c, m->h, m->temb, m->q_in, s));
     PT_TRY(linf(m, m->q_in, m->q1_w, m->q1_b, m->q1, NJ, x.q_in, D, EPI_BIAS_GELU_D, nullptr, m->q1a, s, Od));
     PT_TRY(lin(m, m->q1a, D, m->q2_w, m->q2_b, m->sc_in, x.score_in, NJ, D, D, EPI_BIAS, nullptr, 0, nullptr, 0, s,

@@ -135,7 +135,7 @@ struct PtcgModel {
     // launch runs alone.  The heads' and trunk input's weight gradients go to
     // the side stream too (ldw_side), wg_ev[5] marking the latest of them.
     // In a training forward wg_ev[6] / wg_ev[7] mark the side stream's global
-    // / decision MLPs and option-row projections (forward_side).
+    // / decision MLPs and option-row projections (model_forward).
     hipStream_t wg_s = nullptr;
     bool wg_serial = false;
     hipEvent_t wg_ev[8] = {};

@@ -1,7 +1,8 @@
 """The drop-in boundary on the CPU: the mirror of ``_C.log`` against the key
 accesses the reference's driver makes (native/train_native.py:660-757), the
-PtcgLog struct against the C header, INTEGRATION.md's optimizer binding
-against the package's own declaration, and a product path free of torch."""
+PtcgLog struct against the C header, the integration guide's optimizer
+binding against the package's own declaration, and a product path free of
+torch."""
 import ctypes
 import math
 import os
@@ -108,12 +109,16 @@ def test_log_struct_matches_the_header(tmp_path):
 
 
 def test_integration_adam_binding_matches_the_package():
-    """INTEGRATION.md's ctypes example binds ptcg_adam_step / _lrf with the
-    argument types native.py declares (lr a device pointer, not a double)."""
+    """The integration guide's ctypes example binds ptcg_adam_step / _lrf with
+    the argument types native.py declares (lr a device pointer, not a
+    double).  The example's list expression ([ctypes.X] * k + ...) is read
+    term by term."""
     doc = open(os.path.join(ROOT, "INTEGRATION.md")).read()
     m = re.search(r"^ADAM_ARGTYPES = (.*?)\n(?=\S)", doc, flags=re.S | re.M)
-    assert m, "INTEGRATION.md has no ADAM_ARGTYPES binding"
-    argtypes = eval(m.group(1).replace("\\\n", " "), {"ctypes": ctypes})
+    assert m, "the integration guide has no ADAM_ARGTYPES binding"
+    argtypes = []
+    for name, k in re.findall(r"\[ctypes\.(\w+)\](?:\s*\*\s*(\d+))?", m.group(1)):
+        argtypes += [getattr(ctypes, name)] * int(k or 1)
     for name in ("ptcg_adam_step", "ptcg_adam_step_lrf"):
         assert argtypes == native._SIGS[name][1], name
         assert f"lib.{name}.argtypes = ADAM_ARGTYPES" in doc

@@ -171,6 +171,18 @@ int pt_tok_cat_fwd(const GatherCtx& c, const float* card, const float* zemb, con
 int pt_tok_cat_bwd(const GatherCtx& c, const float* d_cat, const DetSink& d_card, const DetSink& d_zemb,
                    const DetSink& d_oemb, hipStream_t s);
 int pt_glob_in(const GatherCtx& c, float* glob_in, hipStream_t s);
+// The global MLP, decision MLP and broadcast product of B samples in one
+// launch (mlpchain.hip): inputs glob_in (N x gf), dec_in (N x din); weights
+// (out, in) row-major; outputs g1 = gelu'(z1), g1a = gelu(z1) (N x G), d1 / d1a
+// (N x H), gd = [g | d] (N x (G + H)), bc (N x D)
+struct MlpChain {
+    int N, gf, G, din, H, D;
+    const float *glob_in, *dec_in;
+    const float *g1w, *g1b, *g2w, *g2b, *d1w, *d1b, *d2w, *d2b, *bcw, *bcb;
+    float *g1, *g1a, *d1, *d1a, *gd, *bc;
+};
+bool pt_mlp_chain_fits(const MlpChain& a);
+int pt_mlp_chain_fwd(const MlpChain& a, hipStream_t s);
 int pt_dec_in_fwd(const GatherCtx& c, const float* card, const float* att, const float* semb,
                   const float* cemb, float* dec_in, hipStream_t s);
 int pt_dec_in_bwd(const GatherCtx& c, const float* d_in, const DetSink& d_card, const DetSink& d_att,

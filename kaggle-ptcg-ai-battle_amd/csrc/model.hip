@@ -135,16 +135,14 @@ struct PtcgModel {
     // launch runs alone.  The heads' and trunk input's weight gradients go to
     // the side stream too (ldw_side), wg_ev[5] marking the latest of them.
     // In a training forward wg_ev[6] / wg_ev[7] mark the side stream's
-    // global / decision MLPs and option-row projections, the global MLP
-    // running on a second side stream (wg_s3, split-K workspace ws3) whose end
-    // wg_ev[8] marks; wg_ev[9] marks the main stream's row compaction
-    // (model_forward).
-    hipStream_t wg_s = nullptr, wg_s3 = nullptr;
+    // per-sample MLPs and option-row projections, wg_ev[8] the main stream's
+    // row compaction (model_forward).
+    hipStream_t wg_s = nullptr;
     bool wg_serial = false;
-    hipEvent_t wg_ev[10] = {};
-    bool wg_rec[10] = {};
-    float *ws2 = nullptr, *ws3 = nullptr;
-    long ws2_floats = 0, ws3_floats = 0;
+    hipEvent_t wg_ev[9] = {};
+    bool wg_rec[9] = {};
+    float* ws2 = nullptr;
+    long ws2_floats = 0;
     // the trunk attention backward's dS scratch (training only)
     void* attn_ws = nullptr;
     size_t attn_ws_bytes = 0;
@@ -711,8 +709,6 @@ static size_t carve(PtcgModel* m, char* base) {
     m->ws = c.take(m->ws_floats);
     m->ws2_floats = 16L << 20;   // the side stream's weight-gradient split-K partials
     m->ws2 = c.take(m->ws2_floats);
-    m->ws3_floats = 4L << 20;    // the forward's global MLP on the second side stream
-    m->ws3 = c.take(m->ws3_floats);
     // the trunk attention backward parks dS here (fp32 size covers both precisions)
     m->attn_ws_bytes = m->train ? pt_attn_bwd_ws_bytes(N, x.l_seq, d.heads, x.dh, 0) : 0;
     m->attn_ws = m->attn_ws_bytes ? c.take((m->attn_ws_bytes + 3) / 4) : nullptr;
@@ -731,7 +727,6 @@ static int reg(PtcgModel* m, int n, bool train) {
     m->det = DetCtx{};
     if (train && !m->wg_s) {
         PT_HIP(hipStreamCreateWithFlags(&m->wg_s, hipStreamNonBlocking));
-        PT_HIP(hipStreamCreateWithFlags(&m->wg_s3, hipStreamNonBlocking));
         for (auto& e : m->wg_ev) PT_HIP(hipEventCreateWithFlags(&e, hipEventDisableTiming));
     }
     size_t bytes = carve(m, nullptr);
@@ -769,11 +764,9 @@ extern "C" void ptcg_model_free(PtcgModel* m) {
     if (!m) return;
     if (m->wg_s) {
         (void)hipStreamSynchronize(m->wg_s);
-        if (m->wg_s3) (void)hipStreamSynchronize(m->wg_s3);
         for (auto e : m->wg_ev)
             if (e) (void)hipEventDestroy(e);
         (void)hipStreamDestroy(m->wg_s);
-        if (m->wg_s3) (void)hipStreamDestroy(m->wg_s3);
     }
     if (m->mem) (void)hipFree(m->mem);
     if (m->tmem) (void)hipFree(m->tmem);
@@ -870,23 +863,19 @@ extern "C" int ptcg_model_forward(PtcgModel* m, const float* obs, const int32_t*
     m->Odev = nullptr;
     const bool skip = m->skip_masked;
     m->skip_fwd = skip;
-    // The global / decision MLPs and the option rows' card / attack
-    // projections read only the observations and the tables: in a training
-    // forward (no launch profile open) they run beside the row compaction,
-    // the token path and the trunk on two side streams forked here (after the
-    // static-table chain, which feeds them): the global MLP on wg_s3
-    // (workspace ws3); the decision MLP on wg_s (workspace ws2), which then
-    // waits for the global MLP for the broadcast product, and for the main
-    // stream's compaction for the option rows' projections.  They join where
-    // their outputs are read (bc: the trunk input; the projections: the
+    // The global / decision MLPs, the broadcast product and the option rows'
+    // card / attack projections read only the observations and the tables:
+    // in a training forward (no launch profile open) they run on the side
+    // stream (workspace ws2) beside the row compaction, the token path and the
+    // trunk, forked here (after the static-table chain, which feeds them), the
+    // projections after the main stream's compaction (wg_ev[8]).  They join
+    // where their outputs are read (bc: the trunk input; the projections: the
     // option rows' q_in).  Each fork and join is recorded before the main
     // stream's next launch is enqueued and taken after (see wg_mark).
     const bool fside = m->train && m->wg_s != nullptr && !pt_prof_active();
-    hipStream_t sf = fside ? m->wg_s : s, sg = fside ? m->wg_s3 : s;
+    hipStream_t sf = fside ? m->wg_s : s;
     float* fws = fside ? m->ws2 : m->ws;
     const long fwsn = fside ? m->ws2_floats : m->ws_floats;
-    float* gws = fside ? m->ws3 : m->ws;
-    const long gwsn = fside ? m->ws3_floats : m->ws_floats;
     if (d.tables == 1) PT_TRY(tables_fwd(m, s));
     if (fside) PT_HIP(hipEventRecord(m->wg_ev[0], s));
     if (m->compact) {
@@ -897,10 +886,30 @@ extern "C" int ptcg_model_forward(PtcgModel* m, const float* obs, const int32_t*
         PT_TRY(pt_opt_map(c, m->o_cnt, m->o_off, m->o_row, s));
         c.orow = m->o_row; c.ooff = m->o_off; c.orows = m->o_off + N;
     }
-    if (fside) {
-        PT_HIP(hipStreamWaitEvent(m->wg_s3, m->wg_ev[0], 0));
-        PT_HIP(hipStreamWaitEvent(m->wg_s, m->wg_ev[0], 0));
+    if (fside) PT_HIP(hipStreamWaitEvent(m->wg_s, m->wg_ev[0], 0));
+    // the per-sample MLPs and the broadcast product (one launch where the
+    // widths allow: a chain of separate products is a dozen dependent
+    // launches, whose latency set when the trunk could start)
+    PT_TRY(pt_glob_in(c, m->glob_in, sf));
+    PT_TRY(pt_dec_in_fwd(c, m->card, m->att, m->semb, m->cemb, m->dec_in, sf));
+    const MlpChain mc{N, d.global_f, G, x.dec_in, PT_DEC_H, D, m->glob_in, m->dec_in,
+                      m->g1_w, m->g1_b, m->g2_w, m->g2_b, m->d1_w, m->d1_b, m->d2_w, m->d2_b, m->bc_w, m->bc_b,
+                      m->g1, m->g1a, m->d1, m->d1a, m->gd, m->bc};
+    if (pt_mlp_chain_fits(mc)) {
+        PT_TRY(pt_mlp_chain_fwd(mc, sf));
+    } else {
+        PT_TRY(lin_ws(m, fws, fwsn, m->glob_in, d.global_f, m->g1_w, m->g1_b, m->g1, G, N, d.global_f, G,
+                      EPI_BIAS_GELU_D, nullptr, G, m->g1a, G, sf));
+        PT_TRY(lin_ws(m, fws, fwsn, m->g1a, G, m->g2_w, m->g2_b, m->gd, x.bcast_in, N, G, G, EPI_BIAS, nullptr, 0,
+                      nullptr, 0, sf));
+        PT_TRY(lin_ws(m, fws, fwsn, m->dec_in, x.dec_in, m->d1_w, m->d1_b, m->d1, PT_DEC_H, N, x.dec_in, PT_DEC_H,
+                      EPI_BIAS_GELU_D, nullptr, PT_DEC_H, m->d1a, PT_DEC_H, sf));
+        PT_TRY(lin_ws(m, fws, fwsn, m->d1a, PT_DEC_H, m->d2_w, m->d2_b, m->gd + G, x.bcast_in, N, PT_DEC_H,
+                      PT_DEC_H, EPI_BIAS, nullptr, 0, nullptr, 0, sf));
+        PT_TRY(lin_ws(m, fws, fwsn, m->gd, x.bcast_in, m->bc_w, m->bc_b, m->bc, D, N, x.bcast_in, D, EPI_BIAS,
+                      nullptr, 0, nullptr, 0, sf));
     }
+    if (fside) PT_HIP(hipEventRecord(m->wg_ev[6], m->wg_s));
     if (m->compact || skip) {
         if (m->sync_free) {
             m->Tdev = m->compact ? Tr : nullptr;
@@ -924,29 +933,10 @@ extern "C" int ptcg_model_forward(PtcgModel* m, const float* obs, const int32_t*
     const int NJ = m->orows;
     const int* Od = m->Odev;
     const int oc0 = PT_TYPE_E + 2 * D, oa0 = oc0 + PT_OPT_E;
-    if (fside) PT_HIP(hipEventRecord(m->wg_ev[9], s));   // the row maps are written
+    if (fside) PT_HIP(hipEventRecord(m->wg_ev[8], s));   // the row maps are written
     PT_TRY(pt_tok_cat_fwd(c, m->card, m->zemb, m->oemb, m->tok_cat, s, tok_rows));
-    PT_TRY(pt_glob_in(c, m->glob_in, sg));
-    PT_TRY(lin_ws(m, gws, gwsn, m->glob_in, d.global_f, m->g1_w, m->g1_b, m->g1, G, N, d.global_f, G,
-                  EPI_BIAS_GELU_D, nullptr, G, m->g1a, G, sg));
-    PT_TRY(lin_ws(m, gws, gwsn, m->g1a, G, m->g2_w, m->g2_b, m->gd, x.bcast_in, N, G, G, EPI_BIAS, nullptr, 0,
-                  nullptr, 0, sg));
-    if (fside) PT_HIP(hipEventRecord(m->wg_ev[8], m->wg_s3));
-    PT_TRY(pt_dec_in_fwd(c, m->card, m->att, m->semb, m->cemb, m->dec_in, sf));
-    PT_TRY(lin_ws(m, fws, fwsn, m->dec_in, x.dec_in, m->d1_w, m->d1_b, m->d1, PT_DEC_H, N, x.dec_in, PT_DEC_H,
-                  EPI_BIAS_GELU_D, nullptr, PT_DEC_H, m->d1a, PT_DEC_H, sf));
-    PT_TRY(lin_ws(m, fws, fwsn, m->d1a, PT_DEC_H, m->d2_w, m->d2_b, m->gd + G, x.bcast_in, N, PT_DEC_H, PT_DEC_H,
-                  EPI_BIAS, nullptr, 0, nullptr, 0, sf));
-    if (fside) PT_HIP(hipStreamWaitEvent(m->wg_s, m->wg_ev[8], 0));   // the global MLP's half of gd
-    PT_TRY(lin_ws(m, fws, fwsn, m->gd, x.bcast_in, m->bc_w, m->bc_b, m->bc, D, N, x.bcast_in, D, EPI_BIAS, nullptr,
-                  0, nullptr, 0, sf));
-    if (fside) PT_HIP(hipEventRecord(m->wg_ev[6], m->wg_s));
     PT_TRY(linf(m, m->tok_cat, m->tp_w, m->tp_b, m->tokp, tok_rows, x.tok_in, D, EPI_BIAS, nullptr, nullptr, s, Td));
-    if (fside) {
-        PT_HIP(hipStreamWaitEvent(s, m->wg_ev[6], 0));   // bc for the trunk input
-        // implied by wg_ev[6]; joins the second side stream to a capture's origin
-        PT_HIP(hipStreamWaitEvent(s, m->wg_ev[8], 0));
-    }
+    if (fside) PT_HIP(hipStreamWaitEvent(s, m->wg_ev[6], 0));   // bc for the trunk input
     const bool tr = m->train;
     const bool b16 = m->prec == 1;
     // at d = 256 the first block's LayerNorm 1 runs inside the trunk-input assembly
@@ -959,7 +949,7 @@ extern "C" int ptcg_model_forward(PtcgModel* m, const float* obs, const int32_t*
         PT_TRY(pt_x0_fwd(c, m->tokp, m->bc, m->readout, m->x[0], m->keep, s));
     // the option rows' card / attack projections, captured after the trunk
     // input so that a replay's wait for bc does not wait for them as well
-    if (fside) PT_HIP(hipStreamWaitEvent(m->wg_s, m->wg_ev[9], 0));   // option row map
+    if (fside) PT_HIP(hipStreamWaitEvent(m->wg_s, m->wg_ev[8], 0));   // option row map
     PT_TRY(pt_opt_gather_fwd(c, m->card, m->att, m->ocard, m->oatt, sf));
     PT_TRY(lin_ws(m, fws, fwsn, m->ocard, d.d_c, m->oc_w, m->oc_b, m->q_in + oc0, x.q_in, NJ, d.d_c, PT_OPT_E,
                   EPI_BIAS, nullptr, 0, nullptr, 0, sf, Od));

@@ -172,3 +172,95 @@ int pt_mlp_chain_fwd(const MlpChain& a, hipStream_t s) {
     PT_LAUNCH_CHECK();
     return PTCG_OK;
 }
+
+// The backward's dX products of the same chain in one launch (reference:
+// the autograd of ptcg/rl/model.py:223-235): dgd += dbc Wb, dd1 = (dgd[:, G:]
+// W4) * gelu'(z3), ddec = dd1 W3, dg1 = (dgd[:, :G] W2) * gelu'(z1).  A
+// workgroup takes MB_R samples; per product a thread owns an output column j
+// for all MB_R rows and runs over the reduction index in order (the weight
+// row segments W[o][j..] of consecutive threads are contiguous), MB_B weights
+// in flight at once.  Deterministic; writes dgd, dd1, ddec and dg1 as the
+// separate products did.
+namespace {
+
+constexpr int MB_R = 4;      // samples per workgroup
+constexpr int MB_T = 512;    // threads per workgroup
+constexpr int MB_B = 32;     // weights per thread loaded together
+
+// Y[r][j] (+)= sum_o X[r][o] W[o][j] for the workgroup's MB_R rows: X in LDS
+// (MB_R x nin at row stride ldx), W (nin, nout) row-major; mul: Y = sum *
+// M[row][j] (M at row stride ldm); acc: Y = Yold + sum; L: the result for the
+// next product (LDS, row stride ldl)
+__device__ __forceinline__ void mb_dense(const float* X, int ldx, int nin, const float* __restrict__ W, int nout,
+                                         float* __restrict__ Y, long ldy, bool acc, const float* __restrict__ M,
+                                         long ldm, float* L, int ldl, int row0, int nrows) {
+    for (int j = threadIdx.x; j < nout; j += MB_T) {
+        float s[MB_R];
+#pragma unroll
+        for (int r = 0; r < MB_R; ++r) s[r] = 0.f;
+        for (int ob = 0; ob < nin; ob += MB_B) {
+            float wv[MB_B];
+#pragma unroll
+            for (int u = 0; u < MB_B; ++u) wv[u] = ob + u < nin ? W[(long)(ob + u) * nout + j] : 0.f;
+#pragma unroll
+            for (int u = 0; u < MB_B; ++u) {
+                if (ob + u >= nin) break;
+#pragma unroll
+                for (int r = 0; r < MB_R; ++r) s[r] = fmaf(X[r * ldx + ob + u], wv[u], s[r]);
+            }
+        }
+#pragma unroll
+        for (int r = 0; r < MB_R; ++r) {
+            float v = s[r];
+            if (r < nrows) {
+                float* y = Y + (long)(row0 + r) * ldy + j;
+                if (acc) v = *y + v;
+                if (M) v *= M[(long)(row0 + r) * ldm + j];
+                *y = v;
+            }
+            if (L) L[r * ldl + j] = v;
+        }
+    }
+}
+
+__device__ __forceinline__ void mb_load(float* dst, int ldd, const float* __restrict__ src, long lds, int w, int row0,
+                                        int nrows) {
+    for (int i = threadIdx.x; i < MB_R * w; i += MB_T) {
+        const int r = i / w, k = i - r * w;
+        dst[r * ldd + k] = r < nrows ? src[(long)(row0 + r) * lds + k] : 0.f;
+    }
+}
+
+__global__ __launch_bounds__(MB_T) void mlp_chain_bwd_kernel(const MlpChainBwd a) {
+    extern __shared__ __align__(16) float mb_smem[];
+    const int bin = a.G + a.H;
+    float* dbc = mb_smem;                 // MB_R x D
+    float* dgd = dbc + MB_R * a.D;        // MB_R x bin (after the broadcast product)
+    float* dd1 = dgd + MB_R * bin;        // MB_R x H
+    const int row0 = blockIdx.x * MB_R;
+    const int nrows = a.N - row0 < MB_R ? a.N - row0 : MB_R;
+    mb_load(dbc, a.D, a.dbc, a.D, a.D, row0, nrows);
+    __syncthreads();
+    // dgd += dbc Wb  (Wb: D x bin)
+    mb_dense(dbc, a.D, a.D, a.bcw, bin, a.dgd, bin, true, nullptr, 0, dgd, bin, row0, nrows);
+    __syncthreads();
+    // dd1 = (dgd[:, G:] W4) * d1, W4: H x H;  dg1 = (dgd[:, :G] W2) * g1, W2: G x G
+    mb_dense(dgd + a.G, bin, a.H, a.d2w, a.H, a.dd1, a.H, false, a.d1, a.H, dd1, a.H, row0, nrows);
+    mb_dense(dgd, bin, a.G, a.g2w, a.G, a.dg1, a.G, false, a.g1, a.G, nullptr, 0, row0, nrows);
+    __syncthreads();
+    // ddec = dd1 W3, W3: H x din
+    mb_dense(dd1, a.H, a.H, a.d1w, a.din, a.ddec, a.din, false, nullptr, 0, nullptr, 0, row0, nrows);
+}
+
+}  // namespace
+
+int pt_mlp_chain_bwd(const MlpChainBwd& a, hipStream_t s) {
+    PT_REQUIRE(a.N >= 1 && a.G >= 1 && a.H >= 1 && a.din >= 1 && a.D >= 1, "mlp_chain_bwd: empty widths");
+    PT_REQUIRE(a.dbc && a.bcw && a.g2w && a.d2w && a.d1w && a.g1 && a.d1 && a.dgd && a.dg1 && a.dd1 && a.ddec,
+               "mlp_chain_bwd: null pointer");
+    const long smem = 4L * MB_R * (a.D + a.G + a.H + a.H);
+    PT_REQUIRE(smem <= 64 * 1024, "mlp_chain_bwd: widths %d / %d / %d exceed LDS", a.D, a.G, a.H);
+    hipLaunchKernelGGL(mlp_chain_bwd_kernel, dim3(pt_cdiv(a.N, MB_R)), dim3(MB_T), (size_t)smem, s, a);
+    PT_LAUNCH_CHECK();
+    return PTCG_OK;
+}

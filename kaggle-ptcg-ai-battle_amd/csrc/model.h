@@ -183,6 +183,14 @@ struct MlpChain {
 };
 bool pt_mlp_chain_fits(const MlpChain& a);
 int pt_mlp_chain_fwd(const MlpChain& a, hipStream_t s);
+// the chain's dX products in one launch: dgd (N x (G + H)) += dbc (N x D) Wb,
+// dd1 = (dgd[:, G:] W4) * d1, ddec = dd1 W3 (N x din), dg1 = (dgd[:, :G] W2) * g1
+struct MlpChainBwd {
+    int N, G, H, din, D;
+    const float *dbc, *bcw, *g2w, *d2w, *d1w, *g1, *d1;
+    float *dgd, *dg1, *dd1, *ddec;
+};
+int pt_mlp_chain_bwd(const MlpChainBwd& a, hipStream_t s);
 int pt_dec_in_fwd(const GatherCtx& c, const float* card, const float* att, const float* semb,
                   const float* cemb, float* dec_in, hipStream_t s);
 int pt_dec_in_bwd(const GatherCtx& c, const float* d_in, const DetSink& d_card, const DetSink& d_att,

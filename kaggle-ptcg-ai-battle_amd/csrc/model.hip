@@ -1408,16 +1408,15 @@ extern "C" int ptcg_model_backward(PtcgModel* m, const float* grad, void* stream
     PT_TRY(wg_mark(m, s));
     PT_TRY(ldx_(m, m->dtokp, D, m->tp_w, m->dtokcat, x.tok_in, tok_rows, x.tok_in, D, EPI_STORE, nullptr, 0, s, Td));
     PT_TRY(ldw_side(m, m->dtokp, D, m->tok_cat, x.tok_in, m->G(m->tp_w), m->G(m->tp_b), tok_rows, x.tok_in, D, s, Td));
+    // the broadcast product and the decision / global MLPs: their dX products
+    // in one launch (the separate products were a chain of small dependent
+    // launches); the weight gradients on the side stream once their dY exist
+    const MlpChainBwd mb{N, G, PT_DEC_H, x.dec_in, D, m->dbc, m->bc_w, m->g2_w, m->d2_w, m->d1_w, m->g1, m->d1,
+                         m->dgd, m->dg1, m->dd1, m->ddec};
     PT_TRY(wg_mark(m, s));
-    PT_TRY(ldx_(m, m->dbc, D, m->bc_w, m->dgd, x.bcast_in, N, x.bcast_in, D, EPI_ACCUM, nullptr, 0, s));
+    PT_TRY(pt_mlp_chain_bwd(mb, s));
     PT_TRY(ldw_side(m, m->dbc, D, m->gd, x.bcast_in, m->G(m->bc_w), m->G(m->bc_b), N, x.bcast_in, D, s));
-    // decision MLP (d_dvec = dgd[:, G:])
     PT_TRY(wg_mark(m, s));
-    PT_TRY(ldx_(m, m->dgd + G, x.bcast_in, m->d2_w, m->dd1, PT_DEC_H, N, PT_DEC_H, PT_DEC_H, EPI_MUL, m->d1, PT_DEC_H, s));
-    PT_TRY(ldw_side(m, m->dgd + G, x.bcast_in, m->d1a, PT_DEC_H, m->G(m->d2_w), m->G(m->d2_b), N, PT_DEC_H, PT_DEC_H, s));
-    PT_TRY(wg_mark(m, s));
-    PT_TRY(ldx_(m, m->dd1, PT_DEC_H, m->d1_w, m->ddec, x.dec_in, N, x.dec_in, PT_DEC_H, EPI_STORE, nullptr, 0, s));
-    PT_TRY(ldw_side(m, m->dd1, PT_DEC_H, m->dec_in, x.dec_in, m->G(m->d1_w), m->G(m->d1_b), N, x.dec_in, PT_DEC_H, s));
     // token rows (card, tool cards, zone, owner) and decision slots (select
     // type, context, card, attack) into their tables
     {
@@ -1445,18 +1444,19 @@ extern "C" int ptcg_model_backward(PtcgModel* m, const float* grad, void* stream
         S.add_source(ta, m->ddec, x.dec_in, c0 + 2 * d.d_c, 2 * d.d_a, N);
         S.add_source(tc, m->ddec, x.dec_in, c0 + 2 * d.d_c + 2 * d.d_a, 2 * d.d_c, N);
         PT_TRY(pt_det_prepare(m->det, S, s));
+        // decision MLP (d_dvec = dgd[:, G:]) and global MLP (d_g = dgd[:, :G])
+        PT_TRY(ldw_side(m, m->dgd + G, x.bcast_in, m->d1a, PT_DEC_H, m->G(m->d2_w), m->G(m->d2_b), N, PT_DEC_H,
+                        PT_DEC_H, s));
+        PT_TRY(ldw_side(m, m->dd1, PT_DEC_H, m->dec_in, x.dec_in, m->G(m->d1_w), m->G(m->d1_b), N, x.dec_in,
+                        PT_DEC_H, s));
+        PT_TRY(ldw_side(m, m->dgd, x.bcast_in, m->g1a, G, m->G(m->g2_w), m->G(m->g2_b), N, G, G, s));
+        PT_TRY(ldw_side(m, m->dg1, G, m->glob_in, d.global_f, m->G(m->g1_w), m->G(m->g1_b), N, d.global_f, G, s));
         PT_TRY(pt_tok_cat_bwd(c, m->dtokcat, pt_det_sink(m->det, S, tc, d.d_c), pt_det_sink(m->det, S, tz, PT_ZONE_E),
                               pt_det_sink(m->det, S, to, PT_OWNER_E), s));
         PT_TRY(pt_dec_in_bwd(c, m->ddec, pt_det_sink(m->det, S, tc, d.d_c), pt_det_sink(m->det, S, ta, d.d_a),
                              pt_det_sink(m->det, S, tsl, PT_SEL_E), pt_det_sink(m->det, S, tcx, PT_CTX_E), s));
         PT_TRY(pt_det_finish(m->det, S, s));
     }
-    // global MLP (d_g = dgd[:, :G])
-    PT_TRY(wg_mark(m, s));
-    PT_TRY(ldx_(m, m->dgd, x.bcast_in, m->g2_w, m->dg1, G, N, G, G, EPI_MUL, m->g1, G, s));
-    PT_TRY(ldw_side(m, m->dgd, x.bcast_in, m->g1a, G, m->G(m->g2_w), m->G(m->g2_b), N, G, G, s));
-    PT_TRY(wg_mark(m, s));
-    PT_TRY(ldw_side(m, m->dg1, G, m->glob_in, d.global_f, m->G(m->g1_w), m->G(m->g1_b), N, d.global_f, G, s));
     if (d.tables == 1) PT_TRY(tables_bwd(m, s));
     return wg_after(m, 5, s);   // join: the heads' and trunk input's weight gradients are done
 }

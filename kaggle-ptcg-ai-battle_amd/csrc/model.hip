@@ -363,6 +363,19 @@ static int ldw_side(PtcgModel* m, const float* dY, long lddy, const float* X, lo
     return wg_done(m, 5);
 }
 
+// a dot head's weight gradient (pt_head_dot_dw) on the side stream, after the
+// last wg_mark, like ldw_side: grad and X are not rewritten later in the
+// backward
+static int head_dw_side(PtcgModel* m, const float* grad, int per, long ldg, int col0, const float* X, int rows,
+                        int K, float* dw, float* db, hipStream_t s, const int* rmap = nullptr,
+                        const int* rows_dev = nullptr) {
+    if (m->wg_serial)
+        return pt_head_dot_dw(grad, per, ldg, col0, X, rows, K, dw, db, m->ws, m->ws_floats, s, rmap, rows_dev);
+    PT_TRY(wg_take(m));
+    PT_TRY(pt_head_dot_dw(grad, per, ldg, col0, X, rows, K, dw, db, m->ws2, m->ws2_floats, m->wg_s, rmap, rows_dev));
+    return wg_done(m, 5);
+}
+
 // refresh the blocks' bf16 weight copies from the fp32 masters
 static int bf16_refresh(PtcgModel* m, hipStream_t s) {
     BfWeightSet ws;
@@ -1333,20 +1346,20 @@ extern "C" int ptcg_model_backward(PtcgModel* m, const float* grad, void* stream
     if (d.critic == 1) {
         PT_TRY(critic_bwd(m, c, grad, s));
     } else {
-        // blind value head: grad[:, NO]
-        PT_TRY(pt_head_dot_dw(grad, 1, NO + 1, NO, m->v1a, N, PT_VAL_H, m->G(m->v2_w), m->G(m->v2_b), m->ws,
-                              m->ws_floats, s));
+        // blind value head: grad[:, NO] (its weight gradient on the side stream)
+        PT_TRY(wg_mark(m, s));
         PT_TRY(pt_head_dot_bwd(grad, 1, NO + 1, NO, m->v2_w, m->v1, m->dv1, N, PT_VAL_H, s));
+        PT_TRY(head_dw_side(m, grad, 1, NO + 1, NO, m->v1a, N, PT_VAL_H, m->G(m->v2_w), m->G(m->v2_b), s));
         PT_TRY(wg_mark(m, s));
         PT_TRY(ldx_(m, m->dv1, PT_VAL_H, m->v1_w, m->dvin, x.val_in, N, x.val_in, PT_VAL_H, EPI_STORE, nullptr, 0, s));
         PT_TRY(ldw_side(m, m->dv1, PT_VAL_H, m->val_in, x.val_in, m->G(m->v1_w), m->G(m->v1_b), N, x.val_in, PT_VAL_H, s));
         PT_TRY(pt_val_in_bwd(c, m->dvin, m->dxa, m->dgd, s));
     }
 
-    // option scores: grad[:, :NO]
-    PT_TRY(pt_head_dot_dw(grad, NO, NO + 1, 0, m->s1a, NJo, PT_SC_H, m->G(m->s2_w), m->G(m->s2_b), m->ws,
-                          m->ws_floats, s, om, Od));
+    // option scores: grad[:, :NO] (the weight gradient on the side stream)
+    PT_TRY(wg_mark(m, s));
     PT_TRY(pt_head_dot_bwd(grad, NO, NO + 1, 0, m->s2_w, m->s1, m->ds1, NJo, PT_SC_H, s, om, Od));
+    PT_TRY(head_dw_side(m, grad, NO, NO + 1, 0, m->s1a, NJo, PT_SC_H, m->G(m->s2_w), m->G(m->s2_b), s, om, Od));
     PT_TRY(wg_mark(m, s));
     PT_TRY(ldx_(m, m->ds1, PT_SC_H, m->s1_w, m->dsc, x.score_in, NJo, x.score_in, PT_SC_H, EPI_STORE, nullptr, 0, s,
                 Od));

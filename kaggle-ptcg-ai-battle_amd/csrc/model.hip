@@ -1408,7 +1408,10 @@ extern "C" int ptcg_model_backward(PtcgModel* m, const float* grad, void* stream
     for (int i = d.layers - 1; i >= 0; --i)
         PT_TRY(block_bwd(m, m->blk[i], m->ba[i], x.l_seq, m->keep, m->x[i], m->dxb, m->dxa, s, rows, Td, coff,
                          b16 ? &m->bw[i] : nullptr));
-    PT_TRY(wg_after(m, 4, s));   // join: every block's weight gradients are done
+    // no join here: nothing after the blocks rewrites what their pending
+    // weight gradients read (dxa, dxb, dffn, dqkv, the block activations; the
+    // side stream has its own workspace), and the side stream's later work,
+    // joined at the end of the backward, runs after them
 
     // trunk input: readout / token projection / broadcast
     PT_TRY(pt_x0_bwd(c, m->dxb, m->dtokp, m->dbc, s));

@@ -145,16 +145,32 @@ __global__ __launch_bounds__(512) void attn_fwd_mfma_kernel(const T* __restrict_
         }
     };
     if (wave < ntl) load_q(wave * 16);
-    for (int idx = tid; idx < ntl * 16 * (DH / 4); idx += 512) {
-        const int l = idx / (DH / 4), c4 = (idx % (DH / 4)) * 4;
-        float4 k4 = make_float4(0.f, 0.f, 0.f, 0.f), v4 = k4;
-        if (l < L) {
-            const T* r = base + (long)l * 3 * D + c4;
-            k4 = ld4(r + D);
-            v4 = ld4(r + 2 * D);
+    // K / V staging in groups of SG row segments per thread: a group's loads
+    // are all issued before its LDS stores, so the staging waits on memory
+    // once per group instead of once per segment
+    constexpr int SG = 4;
+    const int nidx = ntl * 16 * (DH / 4);
+    for (int i0 = tid; i0 < nidx; i0 += SG * 512) {
+        float4 k4[SG], v4[SG];
+#pragma unroll
+        for (int u = 0; u < SG; ++u) {
+            const int idx = i0 + u * 512, l = idx / (DH / 4), c4 = (idx % (DH / 4)) * 4;
+            k4[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+            v4[u] = k4[u];
+            if (idx < nidx && l < L) {
+                const T* r = base + (long)l * 3 * D + c4;
+                k4[u] = ld4(r + D);
+                v4[u] = ld4(r + 2 * D);
+            }
         }
-        st_lds4(&Ks[l * SK + c4], k4);
-        st_lds4(&Vs[l * SK + c4], v4);
+#pragma unroll
+        for (int u = 0; u < SG; ++u) {
+            const int idx = i0 + u * 512, l = idx / (DH / 4), c4 = (idx % (DH / 4)) * 4;
+            if (idx < nidx) {
+                st_lds4(&Ks[l * SK + c4], k4[u]);
+                st_lds4(&Vs[l * SK + c4], v4[u]);
+            }
+        }
     }
     for (int l = tid; l < LP; l += 512) kf[l] = l < L ? (keep[rb + l] != 0.f ? 1.f : 0.f) : -1.f;
     __syncthreads();
@@ -324,24 +340,39 @@ __global__ __launch_bounds__(512) void attn_bwd_mfma_kernel(const T* __restrict_
     }
     // stage Q, dO, K and form Dv[q] = sum_d dO[q][d] O[q][d]: the DH/4 lanes
     // holding a row's 4-column partials are adjacent (512 is a multiple of
-    // DH/4), so a butterfly over them gives the row sum (padded rows 0)
-    for (int idx = tid; idx < ntl * 16 * (DH / 4); idx += 512) {
-        const int l = idx / (DH / 4), c4 = (idx % (DH / 4)) * 4;
-        float4 q4 = make_float4(0.f, 0.f, 0.f, 0.f), k4 = q4, d4 = q4, o4 = q4;
-        if (l < L) {
-            const T* r = base + (long)l * 3 * D + c4;
-            q4 = ld4(r);
-            k4 = ld4(r + D);
-            d4 = ld4(dob + (long)l * D + c4);
-            o4 = ld4(ob + (long)l * D + c4);
-        }
-        st_lds4(&Qs[l * SQ + c4], q4);
-        st_lds4(&dOs[l * SQ + c4], d4);
-        if (!GDS) st_lds4(&Ks[l * SKB + c4], k4);
-        float part = ((d4.x * o4.x + d4.y * o4.y) + d4.z * o4.z) + d4.w * o4.w;
+    // DH/4), so a butterfly over them gives the row sum (padded rows 0).
+    // Segments go in groups of SG per thread, a group's loads all issued
+    // before its stores (one wait on memory per group)
+    constexpr int SG = GDS ? 4 : 2;
+    const int nidx = ntl * 16 * (DH / 4);
+    for (int i0 = tid; i0 < nidx; i0 += SG * 512) {
+        float4 q4[SG], k4[SG], d4[SG], o4[SG];
 #pragma unroll
-        for (int o = 1; o < DH / 4; o <<= 1) part += __shfl_xor(part, o, 64);
-        if (c4 == 0) Dv[l] = part;
+        for (int u = 0; u < SG; ++u) {
+            const int idx = i0 + u * 512, l = idx / (DH / 4), c4 = (idx % (DH / 4)) * 4;
+            q4[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+            k4[u] = q4[u]; d4[u] = q4[u]; o4[u] = q4[u];
+            if (idx < nidx && l < L) {
+                const T* r = base + (long)l * 3 * D + c4;
+                q4[u] = ld4(r);
+                if (!GDS) k4[u] = ld4(r + D);
+                d4[u] = ld4(dob + (long)l * D + c4);
+                o4[u] = ld4(ob + (long)l * D + c4);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < SG; ++u) {
+            const int idx = i0 + u * 512, l = idx / (DH / 4), c4 = (idx % (DH / 4)) * 4;
+            if (idx < nidx) {
+                st_lds4(&Qs[l * SQ + c4], q4[u]);
+                st_lds4(&dOs[l * SQ + c4], d4[u]);
+                if (!GDS) st_lds4(&Ks[l * SKB + c4], k4[u]);
+                float part = ((d4[u].x * o4[u].x + d4[u].y * o4[u].y) + d4[u].z * o4[u].z) + d4[u].w * o4[u].w;
+#pragma unroll
+                for (int o = 1; o < DH / 4; o <<= 1) part += __shfl_xor(part, o, 64);
+                if (c4 == 0) Dv[l] = part;
+            }
+        }
     }
     for (int l = tid; l < LP; l += 512) {
         kf[l] = l < L ? (keep[rb + l] != 0.f ? 1.f : 0.f) : 0.f;

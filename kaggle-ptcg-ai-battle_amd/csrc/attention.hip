@@ -451,12 +451,21 @@ __global__ __launch_bounds__(512) void attn_bwd_mfma_kernel(const T* __restrict_
     __syncthreads();
     if (GDS) {
         // Q and dO are consumed: stage K into their space (its rows were just
-        // read by pass A, so they come from L2)
-        for (int idx = tid; idx < ntl * 16 * (DH / 4); idx += 512) {
-            const int l = idx / (DH / 4), c4 = (idx % (DH / 4)) * 4;
-            float4 k4 = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (l < L) k4 = ld4(base + (long)l * 3 * D + D + c4);
-            st_lds4(&Ks[l * SKB + c4], k4);
+        // read by pass A, so they come from L2), four segments' loads per
+        // thread issued before their stores
+        for (int i0 = tid; i0 < nidx; i0 += 4 * 512) {
+            float4 k4[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int idx = i0 + u * 512, l = idx / (DH / 4), c4 = (idx % (DH / 4)) * 4;
+                k4[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+                if (idx < nidx && l < L) k4[u] = ld4(base + (long)l * 3 * D + D + c4);
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int idx = i0 + u * 512, l = idx / (DH / 4), c4 = (idx % (DH / 4)) * 4;
+                if (idx < nidx) st_lds4(&Ks[l * SKB + c4], k4[u]);
+            }
         }
         __syncthreads();
     }
@@ -549,20 +558,33 @@ __global__ __launch_bounds__(512) void attn_bwd_kv_kernel(const T* __restrict__ 
     const T* ob = ctx + rb * D + h * DH;
     const T* dob = dctx + rb * D + h * DH;
     T* gb = dqkv + rb * 3 * D + h * DH;
-    for (int idx = tid; idx < ntl * 16 * (DH / 4); idx += 512) {
-        const int l = idx / (DH / 4), c4 = (idx % (DH / 4)) * 4;
-        float4 q4 = make_float4(0.f, 0.f, 0.f, 0.f), d4 = q4, o4 = q4;
-        if (l < L) {
-            q4 = ld4(base + (long)l * 3 * D + c4);
-            d4 = ld4(dob + (long)l * D + c4);
-            o4 = ld4(ob + (long)l * D + c4);
-        }
-        *reinterpret_cast<float4*>(&Qs[l * SQ + c4]) = q4;
-        *reinterpret_cast<float4*>(&dOs[l * SQ + c4]) = d4;
-        float part = ((d4.x * o4.x + d4.y * o4.y) + d4.z * o4.z) + d4.w * o4.w;
+    // staging in groups of four row segments per thread, loads before stores
+    const int nidx = ntl * 16 * (DH / 4);
+    for (int i0 = tid; i0 < nidx; i0 += 4 * 512) {
+        float4 q4[4], d4[4], o4[4];
 #pragma unroll
-        for (int o = 1; o < DH / 4; o <<= 1) part += __shfl_xor(part, o, 64);
-        if (c4 == 0) Dv[l] = part;
+        for (int u = 0; u < 4; ++u) {
+            const int idx = i0 + u * 512, l = idx / (DH / 4), c4 = (idx % (DH / 4)) * 4;
+            q4[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+            d4[u] = q4[u]; o4[u] = q4[u];
+            if (idx < nidx && l < L) {
+                q4[u] = ld4(base + (long)l * 3 * D + c4);
+                d4[u] = ld4(dob + (long)l * D + c4);
+                o4[u] = ld4(ob + (long)l * D + c4);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int idx = i0 + u * 512, l = idx / (DH / 4), c4 = (idx % (DH / 4)) * 4;
+            if (idx < nidx) {
+                *reinterpret_cast<float4*>(&Qs[l * SQ + c4]) = q4[u];
+                *reinterpret_cast<float4*>(&dOs[l * SQ + c4]) = d4[u];
+                float part = ((d4[u].x * o4[u].x + d4[u].y * o4[u].y) + d4[u].z * o4[u].z) + d4[u].w * o4[u].w;
+#pragma unroll
+                for (int o = 1; o < DH / 4; o <<= 1) part += __shfl_xor(part, o, 64);
+                if (c4 == 0) Dv[l] = part;
+            }
+        }
     }
     for (int l = tid; l < LP; l += 512) {
         kf[l] = l < L ? (keep[rb + l] != 0.f ? 1.f : 0.f) : 0.f;
@@ -659,16 +681,29 @@ __global__ __launch_bounds__(512) void attn_bwd_q_kernel(const T* __restrict__ q
     const T* ob = ctx + rb * D + h * DH;
     const T* dob = dctx + rb * D + h * DH;
     T* gb = dqkv + rb * 3 * D + h * DH;
-    for (int idx = tid; idx < ntl * 16 * (DH / 4); idx += 512) {
-        const int l = idx / (DH / 4), c4 = (idx % (DH / 4)) * 4;
-        float4 k4 = make_float4(0.f, 0.f, 0.f, 0.f), v4 = k4;
-        if (l < L) {
-            const T* r = base + (long)l * 3 * D + c4;
-            k4 = ld4(r + D);
-            v4 = ld4(r + 2 * D);
+    // staging in groups of four row segments per thread, loads before stores
+    const int nidx = ntl * 16 * (DH / 4);
+    for (int i0 = tid; i0 < nidx; i0 += 4 * 512) {
+        float4 k4[4], v4[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int idx = i0 + u * 512, l = idx / (DH / 4), c4 = (idx % (DH / 4)) * 4;
+            k4[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+            v4[u] = k4[u];
+            if (idx < nidx && l < L) {
+                const T* r = base + (long)l * 3 * D + c4;
+                k4[u] = ld4(r + D);
+                v4[u] = ld4(r + 2 * D);
+            }
         }
-        *reinterpret_cast<float4*>(&Ks[l * SQ + c4]) = k4;
-        *reinterpret_cast<float4*>(&Vs[l * SQ + c4]) = v4;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int idx = i0 + u * 512, l = idx / (DH / 4), c4 = (idx % (DH / 4)) * 4;
+            if (idx < nidx) {
+                *reinterpret_cast<float4*>(&Ks[l * SQ + c4]) = k4[u];
+                *reinterpret_cast<float4*>(&Vs[l * SQ + c4]) = v4[u];
+            }
+        }
     }
     for (int l = tid; l < LP; l += 512) kf[l] = l < L ? (keep[rb + l] != 0.f ? 1.f : 0.f) : 0.f;
     __syncthreads();

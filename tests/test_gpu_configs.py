@@ -2,7 +2,7 @@
 
 * config 2 (fp32 forward + backward + PPO loss at B = 512): forward output
   relative L2 <= 1e-5, PPO gradient <= 1e-5, every parameter-gradient
-  tensor relative L2 <= 1e-4 against the float64 oracle.
+  tensor relative L2 <= 1e-4 (the fp32 parity bar) against the float64 oracle.
 * config 4 (bf16 GEMM and attention products): forward at B = 2048 within the
   stated bf16 tolerance (legal logits |d| <= 2e-2 max(1, |ref|), value
   relative L2 <= 2e-2, mean masked-softmax KL <= 1e-3); gradients at B = 512:

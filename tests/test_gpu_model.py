@@ -1,7 +1,7 @@
 """Model / trainer parity on the GPU through the C ABI, against the CPU oracle
 on identical seeded inputs and weights.
 
-Tolerances (fp32 path; north-star bar "rel 1e-4 on fp32 logits/values/grads"):
+Tolerances (fp32 path; parity bar: relative 1e-4 on fp32 logits, values and gradients):
 * forward output (N, A+1): relative L2 <= 1e-5 and max|d| <= 1e-4 * max(1, max|ref|)
 * every parameter-gradient tensor: relative L2 <= 1e-4
 * weights after Adam steps: relative L2 <= 1e-4 on the weight blob; the
